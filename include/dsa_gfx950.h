@@ -1,0 +1,136 @@
+/*
+ * dsa_gfx950.h — C ABI of the MI355X (gfx950) DeepSeek-Sparse-Attention decode path:
+ * lightning indexer -> exact per-row top-k -> sparse MLA attention over a paged FP8 KV cache.
+ *
+ * Every pointer is a device pointer unless stated otherwise; every entry point enqueues work on `stream`
+ * (a hipStream_t passed as void*) and returns without synchronising. Return value: DSA_OK (0) or a negative
+ * DSA_E* code; dsa_strerror() names it. No entry point allocates device memory: scratch space is a
+ * caller-owned workspace sized by dsa_workspace_bytes(). Kernels never raise; every shape and argument check
+ * happens on the host before launch.
+ *
+ * Cache layout (the paged FP8 cache of trnrt/models/decoder.py:459-490 and trnrt/engine/model_runner.py:54-70,
+ * extended with per-token scales):
+ *   - a cache holds num_pages * page_size token slots; page 0 is the null page (trnrt/engine/kv_pool.py:1-15);
+ *   - token t of sequence b lives in slot page_table[b * max_pages + t / page_size] * page_size + t % page_size
+ *     (trnrt/models/decoder.py:658-667);
+ *   - indexer keys: uint8 OCP e4m3fn [slots, D] + fp32 per-token scale [slots] (key = k_fp8 * k_scale);
+ *   - latent KV: uint8 OCP e4m3fn [slots, Dqk] (Dqk = 512 latent + 64 rope) + fp32 per-token scale [slots].
+ * Page ids outside [0, num_pages) read the null page instead of faulting.
+ */
+#ifndef DSA_GFX950_H
+#define DSA_GFX950_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DSA_ABI_VERSION 1
+
+#define DSA_OK 0
+#define DSA_EINVAL (-1)      /* a null pointer or a size out of range */
+#define DSA_EUNSUPPORTED (-2) /* a shape these kernels do not implement */
+#define DSA_EWORKSPACE (-3)  /* workspace smaller than dsa_workspace_bytes() */
+#define DSA_ELAUNCH (-4)     /* the HIP runtime refused a launch */
+
+/* Workspace kinds for dsa_workspace_bytes(). */
+#define DSA_WS_TOPK 1
+#define DSA_WS_ATTENTION 2
+#define DSA_WS_LAYER 3
+
+int dsa_abi_version(void);
+const char* dsa_strerror(int status);
+
+/*
+ * Decode indexer scores (replaces trnrt/kernels/dsa_index.py:243-268 `scores`, arithmetic of
+ * dsa_index.py:44-50 `emulate` and trnrt/models/dsa_long.py:74-84 `scores`):
+ *   scores[b, t] = k_scale[slot(b,t)] * sum_h w[b, h] * relu(q[b, h, :] . k_fp8[slot(b,t), :]) + cand[b, t]
+ * for t < ctx_len[b]; NEG_INF (-1e30) for ctx_len[b] <= t < score_stride.
+ *   q        bf16 [B, Hi, D]          (D must be 128; Hi <= 64)
+ *   w        fp32 [B, Hi]             head weights with D^-0.5 already folded in (trnrt/models/mla.py:629)
+ *   k_fp8    uint8 [num_pages * page_size, D], k_scale fp32 [num_pages * page_size]
+ *   page_table int32 [B, max_pages],  ctx_len int32 [B] (values clamped to max_pages * page_size)
+ *   cand     fp32 [B, score_stride] additive (0 / NEG_INF) or NULL
+ *   scores   fp32 [B, score_stride];  page_size a multiple of 32; score_stride <= max_pages * page_size
+ */
+int dsa_indexer_decode(const void* q_bf16, const float* w, const uint8_t* k_fp8, const float* k_scale,
+                       const int32_t* page_table, const int32_t* ctx_len, const float* cand, float* scores, int B,
+                       int Hi, int D, int max_pages, int page_size, int num_pages, int score_stride, void* stream);
+
+/*
+ * Exact top-k per row (replaces trnrt/models/dsa_long.py:140-186 `select_device` and the selection of
+ * trnrt/kernels/dsa_topk.py:495-514 `select`; rule of trnrt/models/dsa_select.py:10-38): per row b over positions
+ * t < min(len[b], score_stride), the `keep` largest scores, ties at the keep-th value to the lowest positions;
+ * only scores > VISIBLE (-5e29) are selectable when vis_only != 0; -0.0 == +0.0; NaN is not allowed.
+ * Output: idx int32 [B, keep] the selected positions ascending, 0 past cnt; cnt int32 [B] = min(keep, #selectable).
+ *   len      int32 [B] or NULL (NULL: score_stride for every row)
+ *   max_len  an upper bound of the row lengths (sizes the launch; <= score_stride)
+ */
+int dsa_topk(const float* scores, const int32_t* len, int32_t* idx, int32_t* cnt, void* workspace,
+             size_t workspace_bytes, int B, int score_stride, int max_len, int keep, int vis_only, void* stream);
+
+/* 1 if dsa_topk implements rows of up to max_len scores at this keep (and vis_only), else 0. */
+int dsa_topk_supported(int max_len, int keep, int vis_only);
+
+/*
+ * Additive selection mask (the output form of trnrt/kernels/dsa_topk.py:495-514 `select` at kp = 1):
+ * mask[b, t] = 0 for the positions idx[b, 0 .. cnt[b]), NEG_INF elsewhere, t < P.
+ */
+int dsa_topk_mask(const int32_t* idx, const int32_t* cnt, float* mask, int B, int keep, int P, void* stream);
+
+/*
+ * Sparse MLA decode attention over the selected tokens (replaces trnrt/kernels/dsa_decode.py:26-43 `attend`,
+ * trnrt/kernels/dsa_slots.py:48-65 `emulate` with lse, trnrt/kernels/dsa_slots_n.py:154-203 `attend`,
+ * trnrt/models/dsa_long.py:189-223 `slots` + `attend`; split combine of trnrt/models/mla.py:853-856):
+ *   K[k] = kv_fp8[slot_k, :Dqk] * kv_scale[slot_k] (key, Dqk = 576), V[k] = K[k][:Dv] (Dv = 512)
+ *   s[h, k] = scale * q[b, h, :] . K[k] + bias_k,  p = softmax_k(s),  out[b, h, :] = sum_k p[h, k] V[k]
+ *   lse[b, h] = max_k s + log sum_k exp(s - max)
+ * Two ways to name the slots (exactly one must be given):
+ *   token form: idx int32 [B, keep] token positions + cnt int32 [B] + page_table int32 [B, max_pages];
+ *               bias_k = 0 for k < cnt[b], NEG_INF otherwise (cnt 0 attends position 0 with lse NEG_INF);
+ *   row form:   rows int32 [B, keep] cache slots + bias fp32 [B, keep] additive (0 / NEG_INF);
+ *               page_table and cnt are ignored (may be NULL).
+ *   q bf16 [B, H, Dqk] (H a multiple of 16), out bf16 [B, H, Dv] or NULL, out_f32 fp32 [B, H, Dv] or NULL,
+ *   lse fp32 [B, H] or NULL; splits >= 1 (0: chosen for the GPU) partitions the keep slots across workgroups.
+ */
+int dsa_sparse_mla_decode(const void* q_bf16, const uint8_t* kv_fp8, const float* kv_scale, const int32_t* idx,
+                          const int32_t* cnt, const int32_t* page_table, const int32_t* rows, const float* bias,
+                          void* out_bf16, float* out_f32, float* lse, void* workspace, size_t workspace_bytes, int B,
+                          int H, int Dqk, int Dv, int keep, int max_pages, int page_size, int num_pages, float scale,
+                          int splits, void* stream);
+
+/*
+ * Token positions -> cache slots (trnrt/models/dsa_long.py:189-215 `slots` at kp = 1, no tail):
+ * rows[b, k] = page_table[b, idx[b,k] / page_size] * page_size + idx[b,k] % page_size, bias[b, k] = 0 for
+ * k < cnt[b] else NEG_INF (rows 0 there).
+ */
+int dsa_token_rows(const int32_t* idx, const int32_t* cnt, const int32_t* page_table, int32_t* rows, float* bias,
+                   int B, int keep, int max_pages, int page_size, int num_pages, void* stream);
+
+/*
+ * The whole DSA decode layer step: indexer -> top-k -> sparse MLA, enqueued back to back on one stream
+ * (the order of trnrt/models/mla.py:506-528 `attention_long` at kp = 1). scores/idx/cnt are the intermediates
+ * the caller may read afterwards (scores fp32 [B, score_stride], idx int32 [B, keep], cnt int32 [B]).
+ */
+int dsa_decode_layer(const void* q_idx_bf16, const float* w, const uint8_t* k_fp8, const float* k_scale,
+                     const void* q_bf16, const uint8_t* kv_fp8, const float* kv_scale, const int32_t* page_table,
+                     const int32_t* ctx_len, float* scores, int32_t* idx, int32_t* cnt, void* out_bf16, float* lse,
+                     void* workspace, size_t workspace_bytes, int B, int Hi, int H, int max_pages, int page_size,
+                     int num_pages, int score_stride, int max_len, int keep, float scale, int splits, void* stream);
+
+/*
+ * Bytes of workspace an entry point needs. kind: DSA_WS_TOPK (B, max_len, keep), DSA_WS_ATTENTION (B, H, keep,
+ * splits; splits 0 = the GPU default), DSA_WS_LAYER (all of them). Unused arguments are ignored.
+ */
+size_t dsa_workspace_bytes(int kind, int B, int H, int keep, int max_len, int splits);
+
+/* The split count dsa_sparse_mla_decode uses for splits = 0. */
+int dsa_default_splits(int B, int H, int keep);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSA_GFX950_H */

@@ -1,0 +1,238 @@
+"""CPU oracle of the DSA decode path — TEST INFRASTRUCTURE, never the product.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this module, and only as the checker
+(or the timed CPU baseline). The product path (trnrt_amd) never calls it and has no CPU fallback.
+
+A restatement, in torch on the CPU in fp32, of the reference's arithmetic for the per-token (kpool 1) decode path with
+the BASELINE extensions (per-token FP8 scales; 576-wide KV = 512 latent + 64 rope columns, value = the latent part).
+Each function cites the reference lines it follows. How each one is pinned (tests/test_oracle_*.py):
+- indexer_ref: brute-force per-token loops, exact rational arithmetic on a tiny case, the scale-folding and
+  dequantisation invariants, planted mistakes (no relu, a transposed table) that must fail;
+- topk_ref: the tie rule as a stable sort; pinned against a second independent form (topk_radix_ref, the
+  reference's radix + tie search), a brute-force Python loop, the reference's literal known answer, its adversarial
+  score kinds, and a planted wrong tie rule that must fail;
+- two_level_ref: equal to topk_ref on the reference's own adversarial cases (trnrt/models/dsa_long.py:26-42 proves
+  it exact);
+- sparse_mla_ref: brute-force float64 loops, one selected token -> that row, all masked -> the uniform mean,
+  lse == log-sum-exp, split-K combine == unsplit, slot-order invariance;
+- splitk_combine_ref: any partition of the slots combines to the unsplit result.
+Nothing here is "parity unpinned".
+"""
+
+from __future__ import annotations
+
+import torch
+
+NEG_INF = -1e30  # trnrt/models/decoder.py NEG_INF
+VISIBLE = -5e29  # trnrt/kernels/dsa_topk.py:58
+BIG = float(2**20)  # trnrt/kernels/dsa_topk.py:59
+
+
+# -- the paged FP8 cache (trnrt/models/decoder.py:481-490, 658-667) ------------------------------------------------
+
+
+def dequant(q8: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """fp32 rows of an e4m3fn cache with per-row scales (the reference's `kv.to(dtype)` load, decoder.py:488-490,
+    times the BASELINE per-token scale)."""
+    return q8.float() * scale.float().reshape(-1, 1)
+
+
+def token_slots(table_row: torch.Tensor, positions: torch.Tensor, page_size: int) -> torch.Tensor:
+    """Cache slots of token positions through one row's page table (trnrt/models/decoder.py:658-667 `_slots`)."""
+    pos = positions.long()
+    return table_row.long()[pos // page_size] * page_size + pos % page_size
+
+
+def row_tokens(cache: torch.Tensor, scale: torch.Tensor, table_row: torch.Tensor, L: int, page_size: int):
+    """The fp32 dequantised cache rows of positions 0 .. L - 1 of one sequence, in position order."""
+    slots = token_slots(table_row, torch.arange(L), page_size)
+    return dequant(cache[slots], scale[slots])
+
+
+# -- indexer (trnrt/kernels/dsa_index.py:44-50; trnrt/models/dsa_long.py:74-84) ------------------------------------
+
+
+def indexer_ref(q_idx: torch.Tensor, w_k: torch.Tensor, k_cache: torch.Tensor, k_scale: torch.Tensor,
+                table: torch.Tensor, ctx_len, page_size: int, stride: int | None = None) -> torch.Tensor:
+    """[B, stride] fp32: score[b, t] = sum_h w_k[b, h] relu(q[b, h] . K[t]) for t < ctx_len[b], NEG_INF after
+    (the candidate mask, dsa_long.py:82-84). K = the dequantised keys; w_k carries D ** -0.5 (mla.py:629), so this is
+    dsa_long.scores' `w relu(s scale)` with the scale folded into w (relu(a x) = a relu(x), a > 0)."""
+    B = q_idx.shape[0]
+    lens = [int(x) for x in ctx_len]
+    stride = max(lens) if stride is None else stride
+    out = torch.full((B, stride), NEG_INF, dtype=torch.float32)
+    for b in range(B):
+        L = lens[b]
+        if L == 0:
+            continue
+        K = row_tokens(k_cache, k_scale, table[b], L, page_size)  # [L, D]
+        s = torch.einsum("hd,td->ht", q_idx[b].float(), K)  # dsa_long.py:79-80 (the 3-D branch, one row)
+        out[b, :L] = torch.einsum("h,ht->t", w_k[b].float(), torch.relu(s))  # dsa_long.py:81
+    return out
+
+
+# -- selection (trnrt/models/dsa_select.py:33-38; trnrt/models/dsa_long.py:94-137) ----------------------------------
+
+
+def selection_mask(scores: torch.Tensor, keep: int, vis_only: bool = True) -> torch.Tensor:
+    """bool [R, P]: the tie rule as a stable sort (dsa_select.reference_mask: descending score, then ascending
+    index, the first keep), restricted to scores > VISIBLE under vis_only (tests/test_dsa_topk.py:56-60)."""
+    s = scores.float()
+    if keep >= s.shape[-1]:
+        sel = torch.ones_like(s, dtype=torch.bool)
+    else:
+        order = torch.sort(s, dim=-1, descending=True, stable=True).indices[..., :keep]
+        sel = torch.zeros_like(s, dtype=torch.bool).scatter(-1, order, True)
+    if vis_only:
+        sel &= s > VISIBLE
+    return sel
+
+
+def ascending(sel: torch.Tensor, keep: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """(indices [R, keep] int64 ascending, 0 past the count; count [R]) of a mask with <= keep True per row
+    (dsa_long.py:94-112 `_ascending`)."""
+    R, P = sel.shape
+    idx = torch.zeros(R, keep, dtype=torch.int64)
+    cnt = sel.sum(-1).to(torch.int64)
+    for r in range(R):
+        nz = sel[r].nonzero().flatten()
+        idx[r, : nz.numel()] = nz
+    return idx, cnt
+
+
+def topk_ref(scores: torch.Tensor, keep: int, lengths=None, vis_only: bool = True):
+    """(idx [R, keep] int64 ascending, cnt [R]) of the exact selection (dsa_long.select_reference, dsa_long.py:
+    114-118); positions at or past lengths[r] are not candidates (the NEG_INF of dsa_long.scores, :82-84)."""
+    s = scores.float().clone()
+    if lengths is not None:
+        P = s.shape[1]
+        L = torch.as_tensor([int(x) for x in lengths]).view(-1, 1)
+        dead = torch.arange(P).view(1, P) >= L
+        if vis_only:
+            s[dead] = NEG_INF
+        else:
+            s[dead] = float("-inf")
+    sel = selection_mask(s, keep, vis_only)
+    if lengths is not None and not vis_only:
+        sel &= ~dead
+    return ascending(sel, keep)
+
+
+def topk_radix_ref(scores: torch.Tensor, keep: int, vis_only: bool = True) -> torch.Tensor:
+    """bool [R, P]: the reference kernel's algorithm (trnrt/kernels/dsa_topk.py:96-127 `emulate`), a second form
+    independent of the sort: the sign step, a radix search over the threshold's bit pattern (31 rounds), and the
+    lowest-index tie search over positions by binary lifting."""
+    s = scores.float()
+    R, P = s.shape
+    vis = s > VISIBLE
+    if keep >= P:
+        return vis.clone() if vis_only else torch.ones_like(vis)
+    f = (s >= 0).float().sum(-1, keepdim=True) < keep
+    sg = torch.where(f, -1.0, 1.0)
+    s2 = s * sg
+    k2 = torch.where(f, float(P + 1 - keep), float(keep))
+    pre = torch.zeros(R, 1, dtype=torch.int32)
+    for b in range(30, -1, -1):
+        cand = pre | (1 << b)
+        ok = (s2 >= cand.view(torch.float32)).float().sum(-1, keepdim=True) >= k2
+        pre = pre | (ok.to(torch.int32) << b)
+    th = pre.view(torch.float32) * sg
+    above = s > th
+    room = keep - above.float().sum(-1, keepdim=True)
+    j = torch.arange(P, dtype=torch.float32)
+    tj = torch.where(s == th, j, BIG)
+    lim = torch.zeros(R, 1)
+    for b in range(P.bit_length() - 1, -1, -1):
+        ok = (tj < lim + 2.0**b).float().sum(-1, keepdim=True) < room
+        lim = lim + ok.float() * 2.0**b
+    sel = above | (tj <= lim)
+    if vis_only:
+        sel &= vis
+    return sel
+
+
+def two_level_ref(scores: torch.Tensor, keep: int, sub: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """The two-level exact selection by sub-block maxima (trnrt/models/dsa_long.py:26-42 proof, 120-132 algorithm):
+    the top-keep sub-blocks by maximum (ties to the lowest block), then the top-keep of their elements in position
+    order."""
+    R, P = scores.shape
+    NB = -(-P // sub)
+    if NB <= keep:
+        return ascending(selection_mask(scores, keep), keep)
+    pad = NB * sub - P
+    s = torch.cat([scores.float(), torch.full((R, pad + sub), NEG_INF)], dim=1)
+    blocks = s.view(R, NB + 1, sub)
+    bm = blocks[:, :NB].amax(-1)
+    bidx, bcnt = ascending(selection_mask(bm, keep), keep)
+    bidx = torch.where(torch.arange(keep).view(1, keep) < bcnt.view(R, 1), bidx, NB)
+    cand = torch.gather(blocks, 1, bidx.unsqueeze(-1).expand(R, keep, sub)).reshape(R, keep * sub)
+    cidx, cnt = ascending(selection_mask(cand, keep), keep)
+    pools = torch.gather(bidx, 1, cidx // sub) * sub + cidx % sub
+    pools = torch.where(torch.arange(keep).view(1, keep) < cnt.view(R, 1), pools, 0)
+    return pools, cnt
+
+
+# -- sparse MLA attention (trnrt/kernels/dsa_decode.py:26-37; trnrt/kernels/dsa_slots.py:48-65) ---------------------
+
+
+def sparse_mla_rows_ref(q: torch.Tensor, K: torch.Tensor, bias: torch.Tensor, scale: float, dv: int = 512):
+    """(o [H, dv], lse [H]) of one query row over its gathered fp32 key rows K [NS, dqk] with additive bias [NS]:
+    s = scale q . K + bias, p = softmax(s), o = p K[:, :dv] (dsa_decode.emulate with the value = the first dv
+    columns), lse = max + log sum exp(s - max) (dsa_slots.emulate)."""
+    s = torch.einsum("hr,tr->ht", q.float(), K) * scale + bias.view(1, -1)
+    p = torch.softmax(s, dim=-1)
+    o = p @ K[:, :dv]
+    m = s.amax(-1)
+    return o, m + torch.log(torch.exp(s - m.unsqueeze(-1)).sum(-1))
+
+
+def sparse_mla_ref(q: torch.Tensor, kv_cache: torch.Tensor, kv_scale: torch.Tensor, idx: torch.Tensor,
+                   cnt: torch.Tensor, table: torch.Tensor, page_size: int, scale: float, dv: int = 512):
+    """(o [B, H, dv] fp32, lse [B, H]) over the selected tokens: slot k of row b is token idx[b, k] (its cache row
+    through the page table, dsa_long.slots at kp 1, dsa_long.py:189-215), bias 0 for k < cnt[b] and NEG_INF after
+    (the slots past the count read token idx[b, k], 0 in the selection's output)."""
+    B, H, _ = q.shape
+    keep = idx.shape[1]
+    o = torch.empty(B, H, dv)
+    lse = torch.empty(B, H)
+    for b in range(B):
+        slots = token_slots(table[b], idx[b].long().clamp(min=0), page_size)
+        K = dequant(kv_cache[slots], kv_scale[slots])
+        bias = torch.where(torch.arange(keep) < int(cnt[b]), 0.0, NEG_INF)
+        o[b], lse[b] = sparse_mla_rows_ref(q[b], K, bias, scale, dv)
+    return o, lse
+
+
+def sparse_mla_slots_ref(q: torch.Tensor, kv_cache: torch.Tensor, kv_scale: torch.Tensor, rows: torch.Tensor,
+                         bias: torch.Tensor, scale: float, dv: int = 512):
+    """The row form (dsa_decode.attend's `rows` + `bias`): slot k of row b is cache row rows[b, k]."""
+    B, H, _ = q.shape
+    o = torch.empty(B, H, dv)
+    lse = torch.empty(B, H)
+    for b in range(B):
+        r = rows[b].long()
+        K = dequant(kv_cache[r], kv_scale[r])
+        o[b], lse[b] = sparse_mla_rows_ref(q[b], K, bias[b].float().reshape(-1), scale, dv)
+    return o, lse
+
+
+def splitk_combine_ref(o_parts: torch.Tensor, lse_parts: torch.Tensor):
+    """(o, lse) of partial attentions over disjoint slot sets (trnrt/models/mla.py:853-856, 1152-1160):
+    LSE = logsumexp_r lse_r, o = sum_r exp(lse_r - LSE) o_r. o_parts [R, ..., dv], lse_parts [R, ...]."""
+    LSE = torch.logsumexp(lse_parts, dim=0)
+    return (o_parts * torch.exp(lse_parts - LSE).unsqueeze(-1)).sum(0), LSE
+
+
+# -- the layer (trnrt/models/mla.py:506-528 `attention_long`, kp 1) -------------------------------------------------
+
+
+def decode_layer_ref(inp, keep: int | None = None):
+    """(scores, idx, cnt, o, lse) of one decode layer step on an Inputs bundle (trnrt_amd.workloads): indexer ->
+    exact top-keep -> sparse MLA over the selected tokens."""
+    cfg = inp.cfg
+    keep = cfg.keep if keep is None else keep
+    stride = inp.max_pages * cfg.page_size
+    sc = indexer_ref(inp.q_idx, inp.w_k, inp.k_cache, inp.k_scale, inp.table, inp.ctx_len, cfg.page_size, stride)
+    idx, cnt = topk_ref(sc, keep, inp.ctx_len)
+    o, lse = sparse_mla_ref(inp.q, inp.kv_cache, inp.kv_scale, idx, cnt, inp.table, cfg.page_size, cfg.scale)
+    return sc, idx, cnt, o, lse

@@ -1,0 +1,97 @@
+"""GPU parity of the exact top-k (trnrt_amd.kernels.dsa_topk -> dsa_topk): bit-exact indices and counts against the
+oracle (oracle/dsa_oracle.py topk_ref, the rule of trnrt/models/dsa_select.py:33-38) when fed the same scores, on the
+reference's adversarial score kinds, the decode shapes (flat rows up to 32K, two-level rows to 1M), ragged lengths and
+the mask form."""
+
+import pytest
+import torch
+
+from oracle import dsa_oracle as O
+from tests._helpers import say
+from tests.test_oracle_topk import KINDS, scores_of
+from trnrt_amd.kernels import dsa_topk
+from trnrt_amd.models import dsa_long
+
+pytestmark = pytest.mark.gpu
+
+
+def _exact(s: torch.Tensor, keep: int, lengths=None, vis_only=True):
+    lg = None if lengths is None else torch.tensor(lengths, dtype=torch.int32).cuda()
+    idx, cnt = dsa_topk.select_indices(s.cuda(), keep, lengths=lg, vis_only=vis_only,
+                                       max_len=None if lengths is None else max(lengths))
+    torch.cuda.synchronize()
+    ri, rc = O.topk_ref(s, keep, lengths, vis_only)
+    assert torch.equal(cnt.cpu().long(), rc)
+    assert torch.equal(idx.cpu().long(), ri)
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("n,keep", [(3000, 2048), (4096, 2048), (8192, 2048), (32768, 2048), (5000, 17), (777, 1)])
+def test_kinds(kind, n, keep):
+    say(f"topk {kind} n={n} keep={keep}")
+    g = torch.Generator().manual_seed(KINDS.index(kind) * 100003 + n + keep)
+    _exact(scores_of(kind, 4, n, g), keep)
+
+
+@pytest.mark.parametrize("kind", ["randn", "integers", "wide", "equal"])
+def test_all_candidates_vis_only_false(kind):
+    say(f"topk vis_only=False {kind}")
+    g = torch.Generator().manual_seed(31)
+    _exact(scores_of(kind, 3, 6000, g), 2048, vis_only=False)
+
+
+def test_ragged_lengths():
+    say("topk ragged lengths")
+    g = torch.Generator().manual_seed(8)
+    s = torch.randn(6, 20000, generator=g)
+    _exact(s, 2048, lengths=[20000, 2048, 2047, 1, 0, 9999])
+
+
+@pytest.mark.parametrize("n", [65536, 131072])
+@pytest.mark.parametrize("kind", ["randn", "integers", "invisible"])
+def test_two_level_rows(n, kind):
+    say(f"topk two-level n={n} {kind}")
+    g = torch.Generator().manual_seed(n % 97)
+    _exact(scores_of(kind, 3, n, g), 2048)
+
+
+def test_one_million():
+    say("topk 1M rows")
+    g = torch.Generator().manual_seed(1)
+    s = torch.randn(2, 1 << 20, generator=g)
+    s[1, ::3] = 0.0
+    _exact(s, 2048, lengths=[1 << 20, 700000])
+
+
+def test_indexer_like_scores_config2_shape():
+    """The decode shape of BASELINE config 2 (8 rows of 32,768, keep 2048) on scores formed like the indexer's
+    (weighted relu head sums, both signs, dead keys at exactly 0; trnrt tests/test_dsa_topk.py:63-75)."""
+    say("topk config-2 shape, pooled-like scores")
+    g = torch.Generator().manual_seed(7)
+    q = torch.randn(8, 8, 16, generator=g)
+    k = torch.randn(32768, 16, generator=g)
+    w = torch.randn(8, 8, generator=g)
+    rel = torch.relu(torch.einsum("rhd,nd->rhn", q, k))
+    rel[..., ::5] = 0.0
+    _exact(torch.einsum("rh,rhn->rn", w, rel), 2048)
+
+
+def test_mask_form_and_select_device():
+    say("topk mask form + select_device")
+    g = torch.Generator().manual_seed(12)
+    s = scores_of("integers", 4, 5000, g)
+    m = dsa_topk.select(s.cuda(), 700).cpu()
+    want = O.selection_mask(s, 700, True)
+    assert torch.equal(m == 0, want) and torch.equal(m < -1e29, ~want)
+    idx, cnt = dsa_long.select_device(s.cuda(), 700)
+    ri, rc = O.topk_ref(s, 700)
+    assert idx.dtype == torch.int64 and torch.equal(idx.cpu(), ri) and torch.equal(cnt.cpu(), rc)
+
+
+def test_deterministic():
+    say("topk determinism")
+    g = torch.Generator().manual_seed(2)
+    s = scores_of("integers", 8, 32768, g).cuda()
+    a = dsa_topk.select_indices(s, 2048)
+    b = dsa_topk.select_indices(s, 2048)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])

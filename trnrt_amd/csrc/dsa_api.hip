@@ -1,0 +1,183 @@
+// C ABI entry points of libdsa_gfx950.so (declared in include/dsa_gfx950.h): host-side argument checks, launch
+// shapes, and the launches on the caller's stream. Nothing here allocates device memory or synchronises.
+#include "../../include/dsa_gfx950.h"
+
+#include "dsa_common.h"
+
+namespace dsa {
+hipError_t launch_indexer_decode(const uint16_t* q, const float* w, const uint8_t* k, const float* ks,
+                                 const int* table, const int* ctx_len, const float* cand, float* scores, int B,
+                                 int Hi, int max_pages, int page_size, int num_pages, int stride, int num_cu,
+                                 hipStream_t stream);
+hipError_t launch_topk(const float* scores, const int* len, int* idx, int* cnt, void* ws, int B, int stride,
+                       int max_len, int keep, int vis_only, hipStream_t s);
+hipError_t launch_topk_mask(const int* idx, const int* cnt, float* mask, int B, int keep, int P, hipStream_t s);
+size_t topk_workspace_bytes(int B, int max_len, int keep);
+bool topk_supported(int max_len, int keep, int vis_only);
+hipError_t launch_sparse_mla(const uint16_t* q, const uint8_t* kv, const float* kvs, const int* idx, const int* cnt,
+                             const int* table, const int* rows, const float* bias, uint16_t* out, float* out_f32,
+                             float* lse, void* ws, int B, int H, int keep, int max_pages, int page_size,
+                             int num_pages, float scale, int splits, hipStream_t s);
+hipError_t launch_token_rows(const int* idx, const int* cnt, const int* table, int* rows, float* bias, int B,
+                             int keep, int max_pages, int page_size, int num_pages, hipStream_t s);
+int attention_default_splits(int B, int H, int keep, int num_cu);
+size_t attention_workspace_bytes(int B, int H, int splits);
+}  // namespace dsa
+
+namespace {
+
+int num_cu() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 256;
+  return n;
+}
+
+int status(hipError_t e) { return e == hipSuccess ? DSA_OK : DSA_ELAUNCH; }
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+int resolve_splits(int splits, int B, int H, int keep) {
+  if (splits <= 0) splits = dsa::attention_default_splits(B, H, keep, num_cu());
+  const int max_splits = (keep + 63) / 64;
+  return splits > max_splits ? max_splits : splits;
+}
+
+// The splits the launch really uses (whole 64-slot chunks per split).
+int effective_splits(int splits, int keep) {
+  int sps = (keep + splits - 1) / splits;
+  sps = (sps + 63) / 64 * 64;
+  return (keep + sps - 1) / sps;
+}
+
+}  // namespace
+
+extern "C" {
+
+int dsa_abi_version(void) { return DSA_ABI_VERSION; }
+
+const char* dsa_strerror(int s) {
+  switch (s) {
+    case DSA_OK:
+      return "ok";
+    case DSA_EINVAL:
+      return "invalid argument (null pointer or size out of range)";
+    case DSA_EUNSUPPORTED:
+      return "unsupported shape";
+    case DSA_EWORKSPACE:
+      return "workspace too small";
+    case DSA_ELAUNCH:
+      return "kernel launch failed";
+    default:
+      return "unknown status";
+  }
+}
+
+int dsa_indexer_decode(const void* q_bf16, const float* w, const uint8_t* k_fp8, const float* k_scale,
+                       const int32_t* page_table, const int32_t* ctx_len, const float* cand, float* scores, int B,
+                       int Hi, int D, int max_pages, int page_size, int num_pages, int score_stride, void* stream) {
+  if (!q_bf16 || !w || !k_fp8 || !k_scale || !page_table || !scores) return DSA_EINVAL;
+  if (B < 0 || Hi < 1 || max_pages < 1 || page_size < 1 || num_pages < 1 || score_stride < 0) return DSA_EINVAL;
+  if (D != 128 || Hi > 64 || page_size % 32) return DSA_EUNSUPPORTED;
+  if ((long)score_stride > (long)max_pages * page_size) return DSA_EINVAL;
+  if (B == 0 || score_stride == 0) return DSA_OK;
+  return status(dsa::launch_indexer_decode(static_cast<const uint16_t*>(q_bf16), w, k_fp8, k_scale, page_table,
+                                           ctx_len, cand, scores, B, Hi, max_pages, page_size, num_pages,
+                                           score_stride, num_cu(), static_cast<hipStream_t>(stream)));
+}
+
+int dsa_topk(const float* scores, const int32_t* len, int32_t* idx, int32_t* cnt, void* workspace,
+             size_t workspace_bytes, int B, int score_stride, int max_len, int keep, int vis_only, void* stream) {
+  if (!scores || !idx || !cnt) return DSA_EINVAL;
+  if (B < 0 || score_stride < 1 || keep < 1 || max_len < 0 || max_len > score_stride) return DSA_EINVAL;
+  if (!len) max_len = score_stride;
+  if (max_len == 0) max_len = 1;
+  if (!dsa::topk_supported(max_len, keep, vis_only)) return DSA_EUNSUPPORTED;
+  const size_t need = dsa::topk_workspace_bytes(B, max_len, keep);
+  if (need && (!workspace || workspace_bytes < need)) return DSA_EWORKSPACE;
+  if (B == 0) return DSA_OK;
+  return status(dsa::launch_topk(scores, len, idx, cnt, workspace, B, score_stride, max_len, keep, vis_only ? 1 : 0,
+                                 static_cast<hipStream_t>(stream)));
+}
+
+int dsa_topk_supported(int max_len, int keep, int vis_only) {
+  if (max_len < 1 || keep < 1) return 0;
+  return dsa::topk_supported(max_len, keep, vis_only) ? 1 : 0;
+}
+
+int dsa_topk_mask(const int32_t* idx, const int32_t* cnt, float* mask, int B, int keep, int P, void* stream) {
+  if (!idx || !cnt || !mask || B < 0 || keep < 1 || P < 1) return DSA_EINVAL;
+  if (B == 0) return DSA_OK;
+  return status(dsa::launch_topk_mask(idx, cnt, mask, B, keep, P, static_cast<hipStream_t>(stream)));
+}
+
+int dsa_sparse_mla_decode(const void* q_bf16, const uint8_t* kv_fp8, const float* kv_scale, const int32_t* idx,
+                          const int32_t* cnt, const int32_t* page_table, const int32_t* rows, const float* bias,
+                          void* out_bf16, float* out_f32, float* lse, void* workspace, size_t workspace_bytes, int B,
+                          int H, int Dqk, int Dv, int keep, int max_pages, int page_size, int num_pages, float scale,
+                          int splits, void* stream) {
+  if (!q_bf16 || !kv_fp8 || !kv_scale || (!out_bf16 && !out_f32)) return DSA_EINVAL;
+  const bool token_form = idx != nullptr;
+  if (token_form == (rows != nullptr)) return DSA_EINVAL;  // exactly one slot form
+  if (token_form && (!cnt || !page_table)) return DSA_EINVAL;
+  if (!token_form && !bias) return DSA_EINVAL;
+  if (B < 0 || H < 1 || keep < 1 || page_size < 1 || num_pages < 1 || (token_form && max_pages < 1)) return DSA_EINVAL;
+  if (Dqk != 576 || Dv != 512 || H % 16) return DSA_EUNSUPPORTED;
+  if ((long)num_pages * page_size > 0x7fffffffL) return DSA_EUNSUPPORTED;
+  if (B == 0) return DSA_OK;
+  const int sp = effective_splits(resolve_splits(splits, B, H, keep), keep);
+  const size_t need = dsa::attention_workspace_bytes(B, H, sp);
+  if (need && (!workspace || workspace_bytes < need)) return DSA_EWORKSPACE;
+  return status(dsa::launch_sparse_mla(static_cast<const uint16_t*>(q_bf16), kv_fp8, kv_scale, idx, cnt, page_table,
+                                       rows, bias, static_cast<uint16_t*>(out_bf16), out_f32, lse, workspace, B, H,
+                                       keep, max_pages, page_size, num_pages, scale, sp,
+                                       static_cast<hipStream_t>(stream)));
+}
+
+int dsa_token_rows(const int32_t* idx, const int32_t* cnt, const int32_t* page_table, int32_t* rows, float* bias,
+                   int B, int keep, int max_pages, int page_size, int num_pages, void* stream) {
+  if (!idx || !cnt || !page_table || !rows) return DSA_EINVAL;
+  if (B < 0 || keep < 1 || max_pages < 1 || page_size < 1 || num_pages < 1) return DSA_EINVAL;
+  if (B == 0) return DSA_OK;
+  return status(dsa::launch_token_rows(idx, cnt, page_table, rows, bias, B, keep, max_pages, page_size, num_pages,
+                                       static_cast<hipStream_t>(stream)));
+}
+
+size_t dsa_workspace_bytes(int kind, int B, int H, int keep, int max_len, int splits) {
+  if (B < 0 || keep < 1) return 0;
+  size_t t = 0, a = 0;
+  if (kind == DSA_WS_TOPK || kind == DSA_WS_LAYER) t = dsa::topk_workspace_bytes(B, max_len, keep);
+  if (kind == DSA_WS_ATTENTION || kind == DSA_WS_LAYER) {
+    if (H < 16) return align256(t);
+    const int sp = effective_splits(resolve_splits(splits, B, H, keep), keep);
+    a = dsa::attention_workspace_bytes(B, H, sp);
+  }
+  return align256(t) + align256(a);
+}
+
+int dsa_default_splits(int B, int H, int keep) {
+  if (B < 1 || H < 16 || keep < 1) return 1;
+  return effective_splits(resolve_splits(0, B, H, keep), keep);
+}
+
+int dsa_decode_layer(const void* q_idx_bf16, const float* w, const uint8_t* k_fp8, const float* k_scale,
+                     const void* q_bf16, const uint8_t* kv_fp8, const float* kv_scale, const int32_t* page_table,
+                     const int32_t* ctx_len, float* scores, int32_t* idx, int32_t* cnt, void* out_bf16, float* lse,
+                     void* workspace, size_t workspace_bytes, int B, int Hi, int H, int max_pages, int page_size,
+                     int num_pages, int score_stride, int max_len, int keep, float scale, int splits, void* stream) {
+  if (!ctx_len) return DSA_EINVAL;
+  if (max_len < 1 || max_len > score_stride) return DSA_EINVAL;
+  const size_t t_need = align256(dsa::topk_workspace_bytes(B, max_len, keep));
+  if (workspace_bytes < dsa_workspace_bytes(DSA_WS_LAYER, B, H, keep, max_len, splits)) return DSA_EWORKSPACE;
+  int st = dsa_indexer_decode(q_idx_bf16, w, k_fp8, k_scale, page_table, ctx_len, nullptr, scores, B, Hi, 128,
+                              max_pages, page_size, num_pages, score_stride, stream);
+  if (st != DSA_OK) return st;
+  st = dsa_topk(scores, ctx_len, idx, cnt, workspace, t_need, B, score_stride, max_len, keep, 1, stream);
+  if (st != DSA_OK) return st;
+  char* aws = workspace ? static_cast<char*>(workspace) + t_need : nullptr;
+  return dsa_sparse_mla_decode(q_bf16, kv_fp8, kv_scale, idx, cnt, page_table, nullptr, nullptr, out_bf16, nullptr,
+                               lse, aws, workspace_bytes - t_need, B, H, 576, 512, keep, max_pages, page_size,
+                               num_pages, scale, splits, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,107 @@
+// Shared device helpers of the gfx950 DSA decode kernels: vector types for the MFMA operands, the OCP e4m3fn ->
+// bf16 conversion, the order-preserving integer key of an fp32 score, and wave/block reductions for wave64.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dsa {
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
+
+// A 16-byte load that bypasses the caches' retention policy for data read exactly once (streamed cache pages).
+__device__ __forceinline__ uint4 load_stream16(const void* p) {
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+constexpr float NEG_INF = -1e30f;   // trnrt/models/decoder.py NEG_INF
+constexpr float VISIBLE = -5e29f;   // trnrt/kernels/dsa_topk.py:58: scores at or below are not selectable
+constexpr int WAVE = 64;
+
+// Two OCP e4m3fn bytes (the low or high 16 bits of `w`) -> two bf16. Every e4m3fn value is exact in bf16, so the
+// conversion is exact (v_cvt_scalef32_pk_bf16_fp8 with scale 1).
+template <bool HI>
+__device__ __forceinline__ bf16x2 fp8x2_to_bf16(uint32_t w) {
+  return __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI);
+}
+
+// Eight e4m3fn bytes (two dwords, byte order = element order) -> the 8-element bf16 MFMA operand.
+__device__ __forceinline__ bf16x8 fp8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
+  bf16x2 a = fp8x2_to_bf16<false>(lo), b = fp8x2_to_bf16<true>(lo);
+  bf16x2 c = fp8x2_to_bf16<false>(hi), d = fp8x2_to_bf16<true>(hi);
+  bf16x8 r;
+  r[0] = a[0]; r[1] = a[1]; r[2] = b[0]; r[3] = b[1];
+  r[4] = c[0]; r[5] = c[1]; r[6] = d[0]; r[7] = d[1];
+  return r;
+}
+
+// Eight bf16 held as four dwords -> the MFMA operand (a bit cast).
+__device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// fp32 -> bf16 bits, round to nearest even (finite inputs).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  uint32_t r = u + 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(r >> 16);
+}
+
+// Order-preserving key of an fp32 score: a < b (IEEE) <=> key(a) < key(b), -0.0 and +0.0 share a key, and every
+// score above VISIBLE has a key > 0, so 0 can stand for "not selectable". NaN is not allowed.
+__device__ __forceinline__ uint32_t order_key(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u << 1) == 0) u = 0;  // -0.0 -> +0.0
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ float key_to_float(uint32_t k) {
+  uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+  return __uint_as_float(u);
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, WAVE);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
+  return v;
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o, WAVE));
+  return v;
+}
+
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = min(v, (uint32_t)__shfl_xor((int)v, o, WAVE));
+  return v;
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  const int lane = threadIdx.x & (WAVE - 1);
+#pragma unroll
+  for (int o = 1; o < WAVE; o <<= 1) {
+    int t = __shfl_up(v, o, WAVE);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+
+// Clamp a page id into the cache (an id outside it reads the null page 0 instead of faulting).
+__device__ __forceinline__ int safe_page(int page, int num_pages) {
+  return ((unsigned)page < (unsigned)num_pages) ? page : 0;
+}
+
+}  // namespace dsa

@@ -1,0 +1,76 @@
+"""One DSA decode layer step on gfx950 in one call: indexer -> top-k -> sparse MLA, the order of
+trnrt/models/mla.py:506-528 `attention_long` (at kpool 1, with the q_lat / W_UV projections outside, as there).
+
+DecodeLayer preallocates the intermediates (scores, indices, counts) and the workspace once for a batch shape, so a
+step allocates nothing and can be captured in a HIP graph; step() enqueues the three operators on the current stream
+through the C ABI's dsa_decode_layer.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+from . import _common as C
+
+NEG_INF = -1e30
+
+
+class DecodeLayer:
+    """Buffers and launch parameters of a decode step over B rows with up to max_pages pages each.
+
+    B, Hi (indexer heads), H (query heads), max_pages, page_size, num_pages (cache pages incl. the null page 0),
+    keep (top-k), scale (softmax scale), max_len (the longest context a step may see; default max_pages page_size),
+    splits (attention split-K; 0 = chosen for the GPU)."""
+
+    def __init__(self, B: int, Hi: int, H: int, max_pages: int, page_size: int, num_pages: int, keep: int = 2048,
+                 scale: float = 192 ** -0.5, max_len: int | None = None, splits: int = 0,
+                 device: torch.device | str = "cuda"):
+        self.B, self.Hi, self.H = B, Hi, H
+        self.max_pages, self.page_size, self.num_pages = max_pages, page_size, num_pages
+        self.keep, self.scale, self.splits = keep, float(scale), splits
+        self.stride = max_pages * page_size
+        self.max_len = self.stride if max_len is None else int(max_len)
+        dev = torch.device(device)
+        if dev.type != "cuda":
+            raise RuntimeError("trnrt_amd DSA kernels run on the GPU only (libdsa_gfx950.so)")
+        self.device = dev
+        self.scores = torch.empty(B, self.stride, dtype=torch.float32, device=dev)
+        self.idx = torch.empty(B, keep, dtype=torch.int32, device=dev)
+        self.cnt = torch.empty(B, dtype=torch.int32, device=dev)
+        self.out = torch.empty(B, H, 512, dtype=torch.bfloat16, device=dev)
+        self.lse = torch.empty(B, H, dtype=torch.float32, device=dev)
+        wsb = _lib.workspace_bytes(_lib.DSA_WS_LAYER, B, H, keep, self.max_len, splits)
+        self.workspace = torch.empty(max(wsb, 256), dtype=torch.uint8, device=dev)
+
+    def step(self, q_idx: torch.Tensor, w: torch.Tensor, k_cache: torch.Tensor, k_scale: torch.Tensor,
+             q: torch.Tensor, kv_cache: torch.Tensor, kv_scale: torch.Tensor, table: torch.Tensor,
+             ctx_len: torch.Tensor, check: bool = True) -> tuple[torch.Tensor, torch.Tensor]:
+        """(out bf16 [B, H, 512], lse fp32 [B, H]) of one layer step; self.scores / idx / cnt hold the intermediates.
+        q_idx [B, Hi, 128] bf16, w [B, Hi] fp32 (D ** -0.5 folded in), k_cache [slots, 128] e4m3fn + k_scale [slots],
+        q [B, H, 576] bf16, kv_cache [slots, 576] e4m3fn + kv_scale [slots], table [B, max_pages] int32, ctx_len [B]
+        int32 (each <= max_len). check=False skips the Python-side argument checks (the C ABI still checks sizes)."""
+        B, Hi, H = self.B, self.Hi, self.H
+        if check:
+            C.on_gpu(q_idx, w, k_cache, k_scale, q, kv_cache, kv_scale, table, ctx_len)
+            C.need(q_idx, "q_idx", torch.bfloat16, (B, Hi, 128))
+            C.need(w, "w", torch.float32, (B, Hi))
+            C.need(q, "q", torch.bfloat16, (B, H, 576))
+            C.need(table, "table", torch.int32, (B, self.max_pages))
+            C.need(ctx_len, "ctx_len", torch.int32, (B,))
+            C.fp8_bytes(k_cache, "k_cache")
+            C.fp8_bytes(kv_cache, "kv_cache")
+            slots = self.num_pages * self.page_size
+            if k_cache.numel() != slots * 128 or kv_cache.numel() != slots * 576:
+                raise ValueError(f"caches of {k_cache.numel()} / {kv_cache.numel()} bytes for {slots} slots")
+            C.need(k_scale, "k_scale", torch.float32, (slots,))
+            C.need(kv_scale, "kv_scale", torch.float32, (slots,))
+        st = _lib.lib().dsa_decode_layer(
+            q_idx.data_ptr(), w.data_ptr(), k_cache.data_ptr(), k_scale.data_ptr(), q.data_ptr(),
+            kv_cache.data_ptr(), kv_scale.data_ptr(), table.data_ptr(), ctx_len.data_ptr(), self.scores.data_ptr(),
+            self.idx.data_ptr(), self.cnt.data_ptr(), self.out.data_ptr(), self.lse.data_ptr(),
+            self.workspace.data_ptr(), self.workspace.numel(), B, Hi, H, self.max_pages, self.page_size,
+            self.num_pages, self.stride, self.max_len, self.keep, self.scale, self.splits,
+            torch.cuda.current_stream(self.device).cuda_stream)
+        _lib.check(st, "dsa_layer.step")
+        return self.out, self.lse

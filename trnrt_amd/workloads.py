@@ -1,0 +1,147 @@
+"""The decode workloads of the DSA path and their seeded synthetic inputs (shared by the tests, the smoke check and
+the benchmark; the same seed gives the same tensors on the same device type).
+
+Cache format (trnrt/models/decoder.py:459-490, 658-667; trnrt/engine/kv_pool.py:1-15), extended with per-token
+scales: pages of `page_size` token slots, page 0 the null page, token t of row b in slot
+table[b, t // page_size] * page_size + t % page_size; the page table is a seeded random permutation of pages 1..N.
+Keys and latent rows are ~N(0, 1), quantised per token to OCP e4m3fn with scale absmax / 448 (448 = the e4m3fn
+maximum, trnrt/engine/model_runner.py:62-70; the per-token scale replaces the reference's unscaled clamp,
+trnrt/models/decoder.py:481-486).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+FP8 = torch.float8_e4m3fn
+FP8_MAX = 448.0
+
+
+@dataclass(frozen=True)
+class Config:
+    name: str
+    B: int
+    L: int  # context per sequence (the longest one when ragged)
+    H: int  # query heads
+    Hi: int  # indexer heads
+    keep: int = 2048
+    page_size: int = 64
+    D: int = 128  # indexer head dim
+    dqk: int = 576  # 512 latent + 64 rope
+    dv: int = 512
+    ragged: tuple[int, int] | None = None  # lengths ~ U[lo, hi] (seeded) instead of L each
+
+    @property
+    def scale(self) -> float:
+        return 192 ** -0.5  # 1 / sqrt(128 + 64)
+
+
+CONFIGS = {
+    1: Config("b1-ctx4k-h16", B=1, L=4096, H=16, Hi=16),
+    2: Config("b8-ctx32k-h64", B=8, L=32768, H=64, Hi=64),
+    3: Config("b12-ragged8k-128k-h64", B=12, L=131072, H=64, Hi=64, ragged=(8192, 131072)),
+    4: Config("b4-ctx1m-h64", B=4, L=1048576, H=64, Hi=64),
+}
+
+
+def lengths_of(cfg: Config, seed: int = 0) -> list[int]:
+    if cfg.ragged is None:
+        return [cfg.L] * cfg.B
+    g = torch.Generator().manual_seed(1000 + seed)
+    lo, hi = cfg.ragged
+    return [int(x) for x in torch.randint(lo, hi + 1, (cfg.B,), generator=g)]
+
+
+def algorithmic_bytes(lengths: list[int], H: int, Hi: int, keep: int = 2048, page_size: int = 64) -> int:
+    """Bytes one layer-step must move at least: every input once, every output once, no intermediates
+    (FP8 key + fp32 scale per token, page table, indexer q (bf16) and weights (fp32), attention q (576 bf16), the
+    selected KV rows (576 B + fp32 scale), and the bf16 output)."""
+    tot = 0
+    for L in lengths:
+        tot += 132 * L + 4 * math.ceil(L / page_size) + 256 * Hi + 4 * Hi + 1152 * H + 580 * min(keep, L) + 1024 * H
+    return tot
+
+
+@dataclass
+class Inputs:
+    cfg: Config
+    lengths: list[int]
+    q_idx: torch.Tensor  # [B, Hi, 128] bf16
+    w: torch.Tensor  # [B, Hi] fp32 head weights (before D ** -0.5)
+    w_k: torch.Tensor  # [B, Hi] fp32 the kernel's weights: w * D ** -0.5 (trnrt/models/mla.py:629)
+    q: torch.Tensor  # [B, H, 576] bf16
+    k_cache: torch.Tensor  # [slots, 128] e4m3fn
+    k_scale: torch.Tensor  # [slots] fp32
+    kv_cache: torch.Tensor  # [slots, 576] e4m3fn
+    kv_scale: torch.Tensor  # [slots] fp32
+    table: torch.Tensor  # [B, max_pages] int32
+    ctx_len: torch.Tensor  # [B] int32
+    num_pages: int
+    max_pages: int
+
+    @property
+    def page_size(self) -> int:
+        return self.cfg.page_size
+
+    def to(self, device) -> "Inputs":
+        kw = {k: (v.to(device) if isinstance(v, torch.Tensor) else v) for k, v in self.__dict__.items()}
+        return Inputs(**kw)
+
+
+def quantize_rows(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-row e4m3fn quantisation: scale = absmax / 448, q = (x / scale) clamped to +-448 (the clamp before the cast
+    of trnrt/models/decoder.py:481-486)."""
+    s = x.abs().amax(dim=-1).clamp(min=1e-30) / FP8_MAX
+    q = (x / s.unsqueeze(-1)).clamp(-FP8_MAX, FP8_MAX).to(FP8)
+    return q, s.float()
+
+
+def _gen(device) -> torch.Generator:
+    return torch.Generator(device=device)
+
+
+def make_inputs(cfg: Config, seed: int = 0, device: str | torch.device = "cpu", lengths: list[int] | None = None,
+                chunk: int = 65536) -> Inputs:
+    """Seeded inputs of one decode layer step for cfg, generated on `device` (cache rows in chunks of `chunk`
+    slots, so a 1M-token cache never needs its fp32 form at once)."""
+    device = torch.device(device)
+    lengths = lengths_of(cfg, seed) if lengths is None else list(lengths)
+    B, ps = cfg.B, cfg.page_size
+    g = _gen(device)
+    g.manual_seed(seed)
+    npg = [math.ceil(L / ps) for L in lengths]
+    max_pages = max(max(npg), 1)
+    num_pages = 1 + sum(npg)
+    q_idx = torch.randn(B, cfg.Hi, cfg.D, generator=g, device=device).to(torch.bfloat16)
+    w = torch.randn(B, cfg.Hi, generator=g, device=device) * 0.25  # N(0, 1/16)
+    q = torch.randn(B, cfg.H, cfg.dqk, generator=g, device=device).to(torch.bfloat16)
+    perm = torch.randperm(num_pages - 1, generator=g, device=device) + 1
+    table = torch.zeros(B, max_pages, dtype=torch.int32, device=device)
+    o = 0
+    for b in range(B):
+        table[b, : npg[b]] = perm[o : o + npg[b]].to(torch.int32)
+        o += npg[b]
+    slots = num_pages * ps
+    k_cache = torch.empty(slots, cfg.D, dtype=FP8, device=device)
+    kv_cache = torch.empty(slots, cfg.dqk, dtype=FP8, device=device)
+    k_scale = torch.empty(slots, dtype=torch.float32, device=device)
+    kv_scale = torch.empty(slots, dtype=torch.float32, device=device)
+    for s0 in range(0, slots, chunk):
+        n = min(chunk, slots - s0)
+        kq, ks = quantize_rows(torch.randn(n, cfg.D, generator=g, device=device))
+        vq, vs = quantize_rows(torch.randn(n, cfg.dqk, generator=g, device=device))
+        k_cache[s0 : s0 + n] = kq
+        k_scale[s0 : s0 + n] = ks
+        kv_cache[s0 : s0 + n] = vq
+        kv_scale[s0 : s0 + n] = vs
+    # the null page holds zeros (what a padded row's write leaves; never a live token)
+    k_cache[:ps].view(torch.uint8).zero_()
+    kv_cache[:ps].view(torch.uint8).zero_()
+    k_scale[:ps] = 1.0
+    kv_scale[:ps] = 1.0
+    ctx_len = torch.tensor(lengths, dtype=torch.int32, device=device)
+    return Inputs(cfg, lengths, q_idx, w, w * cfg.D ** -0.5, q, k_cache, k_scale, kv_cache, kv_scale, table, ctx_len,
+                  num_pages, max_pages)
