@@ -5,8 +5,10 @@
  * Every pointer is a device pointer unless stated otherwise; every entry point enqueues work on `stream`
  * (a hipStream_t passed as void*) and returns without synchronising. Return value: DSA_OK (0) or a negative
  * DSA_E* code; dsa_strerror() names it. No entry point allocates device memory: scratch space is a
- * caller-owned workspace sized by dsa_workspace_bytes(). Kernels never raise; every shape and argument check
- * happens on the host before launch.
+ * caller-owned workspace sized by dsa_workspace_bytes(). A workspace must be zero-filled before its first use
+ * (dsa_workspace_clear, or any zero fill); every call leaves the parts that must be zero at zero again, so one
+ * workspace serves any number of calls (and of graph replays). Calls that share a workspace must not overlap.
+ * Kernels never raise; every shape and argument check happens on the host before launch.
  *
  * Cache layout (the paged FP8 cache of trnrt/models/decoder.py:459-490 and trnrt/engine/model_runner.py:54-70,
  * extended with per-token scales):
@@ -67,9 +69,14 @@ int dsa_indexer_decode(const void* q_bf16, const float* w, const uint8_t* k_fp8,
  * Output: idx int32 [B, keep] the selected positions ascending, 0 past cnt; cnt int32 [B] = min(keep, #selectable).
  *   len      int32 [B] or NULL (NULL: score_stride for every row)
  *   max_len  an upper bound of the row lengths (sizes the launch; <= score_stride)
+ *   workspace  dsa_workspace_bytes(DSA_WS_TOPK, B, 0, keep, max_len, 0) bytes, zero-filled before first use
  */
 int dsa_topk(const float* scores, const int32_t* len, int32_t* idx, int32_t* cnt, void* workspace,
              size_t workspace_bytes, int B, int score_stride, int max_len, int keep, int vis_only, void* stream);
+
+/* Zero-fills workspace (16-byte aligned, bytes a multiple of 16) with a kernel on `stream` (no memset node, so a
+ * captured graph may contain it). */
+int dsa_workspace_clear(void* workspace, size_t workspace_bytes, void* stream);
 
 /* 1 if dsa_topk implements rows of up to max_len scores at this keep (and vis_only), else 0. */
 int dsa_topk_supported(int max_len, int keep, int vis_only);

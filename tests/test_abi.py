@@ -21,7 +21,7 @@ def declared() -> list[str]:
 
 def test_header_and_binding_agree():
     names = declared()
-    assert len(names) >= 10
+    assert len(names) >= 11
     assert sorted(names) == sorted(_lib.SIGNATURES), "every declared entry point has a ctypes signature and back"
 
 
@@ -49,7 +49,9 @@ def test_host_side_argument_checks():
     assert lib.dsa_indexer_decode(p, p, p, p, p, p, null, p, 1, 65, 128, 1, 64, 2, 64, null) == -2  # Hi 65
     assert lib.dsa_indexer_decode(p, p, p, p, p, p, null, p, 1, 64, 128, 1, 64, 2, 128, null) == -1  # stride > cap
     assert lib.dsa_topk(p, null, p, p, null, 0, 1, 100, 100, 0, 1, null) == -1  # keep 0
-    assert lib.dsa_topk(p, p, p, p, null, 0, 2, 1 << 20, 1 << 20, 2048, 1, null) == -3  # two-level needs workspace
+    assert lib.dsa_topk(p, p, p, p, null, 0, 2, 1 << 20, 1 << 20, 2048, 1, null) == -3  # no workspace
+    assert lib.dsa_topk(p, p, p, p, p, 100, 2, 4096, 4096, 2048, 1, null) == -3  # workspace too small
+    assert lib.dsa_workspace_clear(ctypes.c_void_p(8), 64, null) == -1  # misaligned
     assert lib.dsa_topk(p, p, p, p, null, 0, 2, 1 << 20, 1 << 20, 2048, 0, null) == -2  # long rows need vis_only
     # sparse MLA: exactly one slot form, 576 / 512 widths, heads in 16s
     args = [p, p, p, p, p, p, p, p, p, null, p, null, 0, 1, 16, 576, 512, 64, 4, 64, 8, 0.1, 1, null]
@@ -69,7 +71,7 @@ def test_supported_and_workspace():
     assert lib.dsa_topk_supported(32768, 2048, 1) == 1
     assert lib.dsa_topk_supported(1 << 20, 2048, 1) == 1
     assert lib.dsa_topk_supported(1 << 20, 2048, 0) == 0
-    assert _lib.workspace_bytes(_lib.DSA_WS_TOPK, 8, 64, 2048, 32768) == 0  # one level: no workspace
+    assert _lib.workspace_bytes(_lib.DSA_WS_TOPK, 8, 64, 2048, 32768) == 8 * 4096 * 4  # one level: the histograms
     assert _lib.workspace_bytes(_lib.DSA_WS_TOPK, 4, 64, 2048, 1 << 20) > 4 * (1 << 20) // 64 * 4
     sp = lib.dsa_default_splits(8, 64, 2048)
     assert 1 <= sp <= 32

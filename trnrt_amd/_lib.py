@@ -33,6 +33,7 @@ SIGNATURES: dict[str, tuple] = {
     "dsa_indexer_decode": (c_int, [P, P, P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, P]),
     "dsa_topk": (c_int, [P, P, P, P, P, c_size_t, c_int, c_int, c_int, c_int, c_int, P]),
     "dsa_topk_supported": (c_int, [c_int, c_int, c_int]),
+    "dsa_workspace_clear": (c_int, [P, c_size_t, P]),
     "dsa_topk_mask": (c_int, [P, P, P, c_int, c_int, c_int, P]),
     "dsa_sparse_mla_decode": (
         c_int,

@@ -6,11 +6,12 @@
 
 namespace dsa {
 hipError_t launch_indexer_decode(const uint16_t* q, const float* w, const uint8_t* k, const float* ks,
-                                 const int* table, const int* ctx_len, const float* cand, float* scores, int B,
-                                 int Hi, int max_pages, int page_size, int num_pages, int stride, int num_cu,
+                                 const int* table, const int* ctx_len, const float* cand, float* scores, int* hist,
+                                 int B, int Hi, int max_pages, int page_size, int num_pages, int stride, int num_cu,
                                  hipStream_t stream);
 hipError_t launch_topk(const float* scores, const int* len, int* idx, int* cnt, void* ws, int B, int stride,
-                       int max_len, int keep, int vis_only, hipStream_t s);
+                       int max_len, int keep, int vis_only, bool hist_ready, hipStream_t s);
+hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t s);
 hipError_t launch_topk_mask(const int* idx, const int* cnt, float* mask, int B, int keep, int P, hipStream_t s);
 size_t topk_workspace_bytes(int B, int max_len, int keep);
 bool topk_supported(int max_len, int keep, int vis_only);
@@ -82,7 +83,7 @@ int dsa_indexer_decode(const void* q_bf16, const float* w, const uint8_t* k_fp8,
   if ((long)score_stride > (long)max_pages * page_size) return DSA_EINVAL;
   if (B == 0 || score_stride == 0) return DSA_OK;
   return status(dsa::launch_indexer_decode(static_cast<const uint16_t*>(q_bf16), w, k_fp8, k_scale, page_table,
-                                           ctx_len, cand, scores, B, Hi, max_pages, page_size, num_pages,
+                                           ctx_len, cand, scores, nullptr, B, Hi, max_pages, page_size, num_pages,
                                            score_stride, num_cu(), static_cast<hipStream_t>(stream)));
 }
 
@@ -94,10 +95,15 @@ int dsa_topk(const float* scores, const int32_t* len, int32_t* idx, int32_t* cnt
   if (max_len == 0) max_len = 1;
   if (!dsa::topk_supported(max_len, keep, vis_only)) return DSA_EUNSUPPORTED;
   const size_t need = dsa::topk_workspace_bytes(B, max_len, keep);
-  if (need && (!workspace || workspace_bytes < need)) return DSA_EWORKSPACE;
+  if (!workspace || workspace_bytes < need) return DSA_EWORKSPACE;
   if (B == 0) return DSA_OK;
   return status(dsa::launch_topk(scores, len, idx, cnt, workspace, B, score_stride, max_len, keep, vis_only ? 1 : 0,
-                                 static_cast<hipStream_t>(stream)));
+                                 false, static_cast<hipStream_t>(stream)));
+}
+
+int dsa_workspace_clear(void* workspace, size_t workspace_bytes, void* stream) {
+  if (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 15) || (workspace_bytes & 15)) return DSA_EINVAL;
+  return status(dsa::launch_fill_zero(workspace, workspace_bytes, static_cast<hipStream_t>(stream)));
 }
 
 int dsa_topk_supported(int max_len, int keep, int vis_only) {
@@ -165,16 +171,25 @@ int dsa_decode_layer(const void* q_idx_bf16, const float* w, const uint8_t* k_fp
                      const int32_t* ctx_len, float* scores, int32_t* idx, int32_t* cnt, void* out_bf16, float* lse,
                      void* workspace, size_t workspace_bytes, int B, int Hi, int H, int max_pages, int page_size,
                      int num_pages, int score_stride, int max_len, int keep, float scale, int splits, void* stream) {
-  if (!ctx_len) return DSA_EINVAL;
-  if (max_len < 1 || max_len > score_stride) return DSA_EINVAL;
-  const size_t t_need = align256(dsa::topk_workspace_bytes(B, max_len, keep));
+  if (!q_idx_bf16 || !w || !k_fp8 || !k_scale || !page_table || !ctx_len || !scores || !idx || !cnt || !workspace)
+    return DSA_EINVAL;
+  if (B < 0 || Hi < 1 || max_pages < 1 || page_size < 1 || num_pages < 1 || keep < 1) return DSA_EINVAL;
+  if (max_len < 1 || max_len > score_stride || (long)score_stride > (long)max_pages * page_size) return DSA_EINVAL;
+  if (Hi > 64 || page_size % 32) return DSA_EUNSUPPORTED;
+  if (!dsa::topk_supported(max_len, keep, 1)) return DSA_EUNSUPPORTED;
   if (workspace_bytes < dsa_workspace_bytes(DSA_WS_LAYER, B, H, keep, max_len, splits)) return DSA_EWORKSPACE;
-  int st = dsa_indexer_decode(q_idx_bf16, w, k_fp8, k_scale, page_table, ctx_len, nullptr, scores, B, Hi, 128,
-                              max_pages, page_size, num_pages, score_stride, stream);
-  if (st != DSA_OK) return st;
-  st = dsa_topk(scores, ctx_len, idx, cnt, workspace, t_need, B, score_stride, max_len, keep, 1, stream);
-  if (st != DSA_OK) return st;
-  char* aws = workspace ? static_cast<char*>(workspace) + t_need : nullptr;
+  if (B == 0) return DSA_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const size_t t_need = align256(dsa::topk_workspace_bytes(B, max_len, keep));
+  // flat rows: the indexer accumulates the top-k's first-level histogram (the workspace's first region)
+  const bool fused_hist = max_len <= 32 * 1024;
+  hipError_t e = dsa::launch_indexer_decode(static_cast<const uint16_t*>(q_idx_bf16), w, k_fp8, k_scale, page_table,
+                                            ctx_len, nullptr, scores, fused_hist ? static_cast<int*>(workspace) : nullptr,
+                                            B, Hi, max_pages, page_size, num_pages, score_stride, num_cu(), s);
+  if (e != hipSuccess) return DSA_ELAUNCH;
+  e = dsa::launch_topk(scores, ctx_len, idx, cnt, workspace, B, score_stride, max_len, keep, 1, fused_hist, s);
+  if (e != hipSuccess) return DSA_ELAUNCH;
+  char* aws = static_cast<char*>(workspace) + t_need;
   return dsa_sparse_mla_decode(q_bf16, kv_fp8, kv_scale, idx, cnt, page_table, nullptr, nullptr, out_bf16, nullptr,
                                lse, aws, workspace_bytes - t_need, B, H, 576, 512, keep, max_pages, page_size,
                                num_pages, scale, splits, stream);

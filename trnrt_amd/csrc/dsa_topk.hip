@@ -26,260 +26,235 @@ namespace dsa {
 
 constexpr int TK_THREADS = 1024;
 constexpr int TK_WAVES = TK_THREADS / WAVE;
-constexpr int TK_BINS = 2048;
+constexpr int TK_BINS = 2048;   // bins of a refinement pass (11 key bits)
 constexpr int TK_BITS = 11;
+constexpr int TK_HSHIFT = 20;   // first level: the top 12 bits of the order key
+constexpr int TK_HBINS = 4096;
+constexpr int TKH_THREADS = 256;  // histogram kernel: 8 scores per thread, 2048 per workgroup
+constexpr int TKH_CHUNK = TKH_THREADS * 8;
 
 struct TopkShared {
   int hist[TK_BINS];
-  int red_i[TK_WAVES];
-  uint32_t red_u[2][TK_WAVES];
-  int scan_tot[TK_WAVES];
+  uint32_t scan_tot[TK_WAVES];
   int sel_bin;
   int sel_above;
 };
 
-// Block-wide exclusive prefix sum of one int per thread (position order = thread order); returns the prefix and
-// writes the total to *total.
-__device__ __forceinline__ int block_excl_scan(int v, TopkShared& sh, int* total) {
+// The row length in elements of a selection level: len[row] for a flat row; ceil(len / len_div) for sub-block
+// maxima; len[row] * len_mul for a candidate row of len[row] sub-blocks; at most stride.
+__device__ __forceinline__ int level_len(const int* len, int row, int len_div, int len_mul, int stride) {
+  if (!len) return stride;
+  long l = len[row];
+  l = l < 0 ? 0 : l;
+  if (len_div > 1) l = (l + len_div - 1) / len_div;
+  if (len_mul > 1) l *= len_mul;
+  return (int)(l < stride ? l : stride);
+}
+
+__device__ __forceinline__ uint32_t select_key(float v, int vis_only) {
+  return (!vis_only || v > VISIBLE) ? order_key(v) : 0u;
+}
+
+// Block-wide exclusive prefix sum (thread order) of a uint32 per thread; returns it and the total.
+__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, TopkShared& sh, uint32_t* total) {
   const int wave = threadIdx.x / WAVE, lane = threadIdx.x & (WAVE - 1);
-  const int inc = wave_incl_scan(v);
+  const uint32_t inc = (uint32_t)wave_incl_scan((int)v);
   if (lane == WAVE - 1) sh.scan_tot[wave] = inc;
   __syncthreads();
-  int before = 0, tot = 0;
+  uint32_t before = 0, tot = 0;
 #pragma unroll
   for (int i = 0; i < TK_WAVES; ++i) {
-    const int t = sh.scan_tot[i];
-    before += i < wave ? t : 0;
-    tot += t;
+    const uint32_t x = sh.scan_tot[i];
+    before += i < wave ? x : 0u;
+    tot += x;
   }
   __syncthreads();
   *total = tot;
   return before + inc - v;
 }
 
-__device__ __forceinline__ int block_sum(int v, TopkShared& sh) {
-  const int wave = threadIdx.x / WAVE, lane = threadIdx.x & (WAVE - 1);
-  v = wave_sum(v);
-  if (lane == 0) sh.red_i[wave] = v;
-  __syncthreads();
-  int t = 0;
-#pragma unroll
-  for (int i = 0; i < TK_WAVES; ++i) t += sh.red_i[i];
-  __syncthreads();
-  return t;
-}
-
-__device__ __forceinline__ void block_minmax(uint32_t& mn, uint32_t& mx, TopkShared& sh) {
-  const int wave = threadIdx.x / WAVE, lane = threadIdx.x & (WAVE - 1);
-  mn = wave_min_u32(mn);
-  mx = wave_max_u32(mx);
-  if (lane == 0) {
-    sh.red_u[0][wave] = mn;
-    sh.red_u[1][wave] = mx;
-  }
-  __syncthreads();
-  mn = 0xffffffffu;
-  mx = 0;
-#pragma unroll
-  for (int i = 0; i < TK_WAVES; ++i) {
-    mn = min(mn, sh.red_u[0][i]);
-    mx = max(mx, sh.red_u[1][i]);
-  }
-  __syncthreads();
-}
-
-// Given the histogram of the keys inside the interval, finds the bin c holding the need-th largest key
-// (suffix(c) >= need > suffix(c + 1)); returns c and sets *above_in = suffix(c + 1).
-__device__ __forceinline__ int find_bin(int need, int* above_in, TopkShared& sh) {
-  const int t = threadIdx.x;
-  // thread t owns bins 2t, 2t + 1; suffix order: thread TK_THREADS - 1 first.
-  const int b0 = 2 * t, b1 = 2 * t + 1;
-  const int h0 = sh.hist[b0], h1 = sh.hist[b1];
-  // exclusive suffix sum over threads: scan over reversed thread order
-  const int rt = TK_THREADS - 1 - t;
+// Exclusive suffix sum (reverse thread order): the sum of v over the threads above this one, and the total.
+__device__ __forceinline__ int block_excl_suffix(int v, TopkShared& sh, int* total) {
+  const int rt = TK_THREADS - 1 - (int)threadIdx.x;  // reversed id: its wave is 15 - wave, its lane 63 - lane
   const int wave = rt / WAVE, lane = rt & (WAVE - 1);
-  const int v = h0 + h1;
-  // wave scan in reversed lane order: use the reversed id's lane within its wave
   int inc = v;
 #pragma unroll
   for (int o = 1; o < WAVE; o <<= 1) {
-    // lanes of the reversed order: rt's wave holds threads with the same t / 64 (reversed lanes)
-    int tt = __shfl_down(inc, o, WAVE);  // thread t + o has reversed lane - o
-    if (lane >= o) inc += tt;
+    const int x = __shfl_down(inc, o, WAVE);  // the thread o above has reversed lane - o
+    if (lane >= o) inc += x;
   }
-  __syncthreads();  // hist reads done before scan_tot is reused below
-  if (lane == WAVE - 1) sh.scan_tot[wave] = inc;
+  if (lane == WAVE - 1) sh.scan_tot[wave] = (uint32_t)inc;
   __syncthreads();
-  int before = 0;
+  int before = 0, tot = 0;
 #pragma unroll
-  for (int i = 0; i < TK_WAVES; ++i) before += i < wave ? sh.scan_tot[i] : 0;
-  const int suf_after = before + inc - v;  // keys in bins above b1
-  // bin b1 first (higher), then b0
-  if (suf_after < need && suf_after + h1 >= need) {
-    sh.sel_bin = b1;
-    sh.sel_above = suf_after;
-  } else if (suf_after + h1 < need && suf_after + h1 + h0 >= need) {
-    sh.sel_bin = b0;
-    sh.sel_above = suf_after + h1;
+  for (int i = 0; i < TK_WAVES; ++i) {
+    const int x = (int)sh.scan_tot[i];
+    before += i < wave ? x : 0;
+    tot += x;
   }
   __syncthreads();
-  const int c = sh.sel_bin;
-  *above_in = sh.sel_above;
-  __syncthreads();
-  return c;
+  *total = tot;
+  return before + inc - v;
 }
 
 __device__ __forceinline__ int bit_length(uint32_t x) { return x ? 32 - __clz(x) : 0; }
 
-// Row r's output positions: map_blocks (two-level) turns a candidate position p into map[p / sub] * sub + p % sub.
+// First level of a selection: the histogram of the top 12 bits of the selectable keys of each row, accumulated into
+// hist[row, 4096] (zero before; the select kernel zeroes it again after reading). 2048 scores per workgroup.
+__global__ __launch_bounds__(TKH_THREADS) void topk_hist_kernel(const float* __restrict__ scores, int stride,
+                                                                const int* __restrict__ len, int len_div,
+                                                                int len_mul, int vis_only, int* __restrict__ hist) {
+  __shared__ int h[TK_HBINS];
+  const int row = blockIdx.y;
+  const int L = level_len(len, row, len_div, len_mul, stride);
+  const int base = blockIdx.x * TKH_CHUNK;
+  if (base >= L) return;
+  for (int i = threadIdx.x; i < TK_HBINS; i += TKH_THREADS) h[i] = 0;
+  __syncthreads();
+  const float* srow = scores + (size_t)row * stride;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int p = base + e * TKH_THREADS + threadIdx.x;
+    if (p < L) {
+      const uint32_t k = select_key(srow[p], vis_only);
+      if (k) atomicAdd(&h[k >> TK_HSHIFT], 1);
+    }
+  }
+  __syncthreads();
+  int* hrow = hist + (size_t)row * TK_HBINS;
+  for (int i = threadIdx.x; i < TK_HBINS; i += TKH_THREADS) {
+    const int c = h[i];
+    if (c) atomicAdd(&hrow[i], c);
+  }
+}
+
+// The selection of one row (E scores per thread, positions t E .. t E + E - 1), given the row's first-level
+// histogram: the threshold's 12-bit bin from the histogram, the threshold inside it by two passes over the low key
+// bits (only keys inside the bin count), then the ordered output. Re-zeroes the histogram.
 template <int E>
-__global__ __launch_bounds__(TK_THREADS) void topk_kernel(const float* __restrict__ scores, int stride,
-                                                          const int* __restrict__ len, int len_div, int len_mul,
-                                                          int keep, int vis_only, const int* __restrict__ map_blocks,
-                                                          int map_sub, int map_stride, int* __restrict__ idx_out,
-                                                          int* __restrict__ cnt_out) {
+__global__ __launch_bounds__(TK_THREADS) void topk_select_kernel(const float* __restrict__ scores, int stride,
+                                                                 const int* __restrict__ len, int len_div,
+                                                                 int len_mul, int keep, int vis_only,
+                                                                 int* __restrict__ hist, int* __restrict__ idx_out,
+                                                                 int* __restrict__ cnt_out) {
   __shared__ TopkShared sh;
   const int row = blockIdx.x;
   const int t = threadIdx.x;
-  int L = stride;
-  if (len) {
-    // the row length in elements of this level: len[row] for a flat row; ceil(len / len_div) for block maxima;
-    // len[row] * len_mul for a candidate row of len[row] sub-blocks
-    long l = len[row];
-    l = l < 0 ? 0 : l;
-    if (len_div > 1) l = (l + len_div - 1) / len_div;
-    if (len_mul > 1) l *= len_mul;
-    L = (int)(l < stride ? l : stride);
-  }
+  const int L = level_len(len, row, len_div, len_mul, stride);
   const float* srow = scores + (size_t)row * stride;
   const int p0 = t * E;
 
+  // the row's histogram (4 bins per thread) and keys
+  int* hrow = hist + (size_t)row * TK_HBINS;
+  const int4 hv = *reinterpret_cast<const int4*>(hrow + 4 * t);
   uint32_t key[E];
-  const bool vec = ((stride & 3) == 0) && ((E & 3) == 0);
-  if (vec && p0 + E <= L) {
+  if (((stride & 3) == 0) && ((E & 3) == 0) && p0 + E <= L) {
+    float4 raw[E / 4];
 #pragma unroll
-    for (int e = 0; e < E; e += 4) {
-      const float4 v = *reinterpret_cast<const float4*>(srow + p0 + e);
-      key[e + 0] = (!vis_only || v.x > VISIBLE) ? order_key(v.x) : 0u;
-      key[e + 1] = (!vis_only || v.y > VISIBLE) ? order_key(v.y) : 0u;
-      key[e + 2] = (!vis_only || v.z > VISIBLE) ? order_key(v.z) : 0u;
-      key[e + 3] = (!vis_only || v.w > VISIBLE) ? order_key(v.w) : 0u;
+    for (int e = 0; e < E / 4; ++e) raw[e] = *reinterpret_cast<const float4*>(srow + p0 + 4 * e);
+#pragma unroll
+    for (int e = 0; e < E / 4; ++e) {
+      key[4 * e + 0] = select_key(raw[e].x, vis_only);
+      key[4 * e + 1] = select_key(raw[e].y, vis_only);
+      key[4 * e + 2] = select_key(raw[e].z, vis_only);
+      key[4 * e + 3] = select_key(raw[e].w, vis_only);
     }
   } else {
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-      const int p = p0 + e;
-      uint32_t k = 0;
-      if (p < L) {
-        const float v = srow[p];
-        k = (!vis_only || v > VISIBLE) ? order_key(v) : 0u;
-      }
-      key[e] = k;
-    }
+    for (int e = 0; e < E; ++e) key[e] = (p0 + e < L) ? select_key(srow[p0 + e], vis_only) : 0u;
   }
 
-  // selectable count and key range
-  int nv = 0;
-  uint32_t kmin = 0xffffffffu, kmax = 0;
-#pragma unroll
-  for (int e = 0; e < E; ++e) {
-    const uint32_t k = key[e];
-    nv += k != 0;
-    if (k) {
-      kmin = min(kmin, k);
-      kmax = max(kmax, k);
-    }
+  // threshold bin among this thread's 4 (bins 4t .. 4t + 3, higher bins first). The defaults keep every index in
+  // range should the histogram not match the scores (a workspace that was not zero): the selection is then wrong but
+  // every write stays inside its buffer.
+  if (t == 0) {
+    sh.sel_bin = 0;
+    sh.sel_above = 0;
   }
-  const int nvis = block_sum(nv, sh);
-  block_minmax(kmin, kmax, sh);
-
-  uint32_t T = 0;  // select key > T, plus `room` keys == T by position
+  int nvis = 0;
+  const int hsum = hv.x + hv.y + hv.z + hv.w;
+  const int above4 = block_excl_suffix(hsum, sh, &nvis);  // keys in bins above 4t + 3
+  *reinterpret_cast<int4*>(hrow + 4 * t) = make_int4(0, 0, 0, 0);  // leave the histogram zero for the next call
+  uint32_t T = 0;  // select key > T, plus the first `room` keys == T by position
   int room = 0;
   if (nvis > keep) {
-    uint32_t lo = kmin, hi = kmax;
-    int need = keep;
-    bool first = true;
+    {
+      const int hb[4] = {hv.x, hv.y, hv.z, hv.w};
+      int suf = above4;
+#pragma unroll
+      for (int i = 3; i >= 0; --i) {
+        if (suf < keep && suf + hb[i] >= keep) {
+          sh.sel_bin = 4 * t + i;
+          sh.sel_above = suf;
+        }
+        suf += hb[i];
+      }
+    }
+    __syncthreads();
+    const int c0 = sh.sel_bin & (TK_HBINS - 1);
+    int need = keep - sh.sel_above;
+    uint32_t lo = (uint32_t)c0 << TK_HSHIFT, hi = lo | ((1u << TK_HSHIFT) - 1u);
     while (lo != hi) {
       for (int i = t; i < TK_BINS; i += TK_THREADS) sh.hist[i] = 0;
       __syncthreads();
-      const float flo = key_to_float(lo), fhi = key_to_float(hi);
-      const float span = fhi - flo;
-      const bool linear = first && isfinite(flo) && isfinite(fhi) && isfinite(span) && span > 0.0f;
-      const float inv = linear ? (float)TK_BINS / span : 0.0f;
-      const int sh_bits = max(0, bit_length(hi - lo) - TK_BITS);
-      auto bin_of = [&](uint32_t k) -> int {
-        if (linear) {
-          const float f = key_to_float(k);
-          int c = (int)((f - flo) * inv);
-          return c < 0 ? 0 : (c >= TK_BINS ? TK_BINS - 1 : c);
-        }
-        return (int)((k - lo) >> sh_bits);
-      };
+      const int sb = max(0, bit_length(hi - lo) - TK_BITS);
 #pragma unroll
       for (int e = 0; e < E; ++e) {
         const uint32_t k = key[e];
-        if (k >= lo && k <= hi) atomicAdd(&sh.hist[bin_of(k)], 1);
+        if (k >= lo && k <= hi) atomicAdd(&sh.hist[(k - lo) >> sb], 1);
       }
       __syncthreads();
-      int above_in = 0;
-      const int c = find_bin(need, &above_in, sh);
-      need -= above_in;
-      if (linear) {
-        // the keys of bin c form a key interval; its bounds are the min / max key that falls into it
-        uint32_t nlo = 0xffffffffu, nhi = 0;
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-          const uint32_t k = key[e];
-          if (k >= lo && k <= hi && bin_of(k) == c) {
-            nlo = min(nlo, k);
-            nhi = max(nhi, k);
-          }
-        }
-        block_minmax(nlo, nhi, sh);
-        lo = nlo;
-        hi = nhi;
-      } else {
-        const uint32_t nlo = lo + ((uint32_t)c << sh_bits);
-        const uint32_t width = sh_bits >= 32 ? 0xffffffffu : ((1u << sh_bits) - 1u);
-        const uint32_t nhi = (hi - nlo > width) ? nlo + width : hi;
-        lo = nlo;
-        hi = nhi;
+      // the bin of the need-th largest key inside [lo, hi] (2 bins per thread)
+      const int h0 = sh.hist[2 * t], h1 = sh.hist[2 * t + 1];
+      if (t == 0) {
+        sh.sel_bin = 0;
+        sh.sel_above = 0;
       }
-      first = false;
+      int tot = 0;
+      const int suf = block_excl_suffix(h0 + h1, sh, &tot);
+      if (suf < need && suf + h1 >= need) {
+        sh.sel_bin = 2 * t + 1;
+        sh.sel_above = suf;
+      } else if (suf + h1 < need && suf + h1 + h0 >= need) {
+        sh.sel_bin = 2 * t;
+        sh.sel_above = suf + h1;
+      }
+      __syncthreads();
+      const int c = sh.sel_bin & (TK_BINS - 1);
+      need -= sh.sel_above;
+      __syncthreads();
+      const uint32_t nlo = lo + ((uint32_t)c << sb);
+      const uint32_t width = (1u << sb) - 1u;
+      hi = (hi - nlo > width) ? nlo + width : hi;
+      lo = nlo;
     }
     T = lo;
     room = need;
   }
 
-  // tied keys before this thread's positions (position order = thread order, then e)
-  int na = 0, nt = 0;
+  // ordered output: one scan of the packed (above, tied) counts; the selected before a position are the keys above
+  // T before it plus min(room, ties before it)
+  uint32_t na = 0, nt = 0;
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     na += key[e] > T;
     nt += (T != 0) && (key[e] == T);
   }
-  int tot = 0;
-  const int tie_before = block_excl_scan(nt, sh, &tot);
-  int take = room - tie_before;  // ties this thread may take
-  take = take < 0 ? 0 : (take > nt ? nt : take);
-  const int ns = na + take;
-  const int out_before = block_excl_scan(ns, sh, &tot);
-  const int cnt = nvis < keep ? nvis : keep;
+  uint32_t tot = 0;
+  const uint32_t before = block_excl_scan((na << 16) | nt, sh, &tot);
+  const int above_before = (int)(before >> 16), tie_before = (int)(before & 0xffffu);
+  int take = room - tie_before;
+  take = take < 0 ? 0 : (take > (int)nt ? (int)nt : take);
+  int o = above_before + (tie_before < room ? tie_before : room);
+  const int cnt = nvis < 0 ? 0 : (nvis < keep ? nvis : keep);
   int* orow = idx_out + (size_t)row * keep;
-  int o = out_before, taken = 0;
+  int taken = 0;
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const uint32_t k = key[e];
-    bool sel = k > T;
-    if (!sel && T != 0 && k == T && taken < take) {
-      sel = true;
-      ++taken;
-    }
-    if (sel) {
-      int p = p0 + e;
-      if (map_blocks) p = map_blocks[(size_t)row * map_stride + p / map_sub] * map_sub + p % map_sub;
-      orow[o++] = p;
-    }
+    const bool tie = T != 0 && k == T && taken < take;
+    taken += tie;
+    if ((k > T || tie) && (unsigned)o < (unsigned)keep) orow[o++] = p0 + e;  // in range whatever the counts
   }
   for (int i = cnt + t; i < keep; i += TK_THREADS) orow[i] = 0;
   if (t == 0) cnt_out[row] = cnt;
@@ -385,17 +360,21 @@ static bool topk_plan(long n, int keep, size_t* ws) {
   return true;
 }
 
-static size_t topk_ws_bytes(int B, long n, int keep) {
+// Workspace of a selection: the first-level histograms [B, 4096] int (zero between calls), then the two-level
+// buffers of rows longer than TOPK_FLAT_MAX (recursively).
+static size_t topk_level_bytes(int B, long n, int keep) {
   if (n <= TOPK_FLAT_MAX) return 0;
   const int sub = topk_sub_block(n, keep);
   const long nb = (n + sub - 1) / sub, nc = (long)keep * sub;
-  const size_t own = up256((size_t)B * nb * 4) + up256((size_t)B * keep * 4) + up256((size_t)B * 4) +
-                     up256((size_t)B * nc * 4);
-  const size_t a = topk_ws_bytes(B, nb, keep), c = topk_ws_bytes(B, nc, keep);
-  return own + (a > c ? a : c);
+  return up256((size_t)B * nb * 4) + up256((size_t)B * keep * 4) + up256((size_t)B * 4) + up256((size_t)B * nc * 4) +
+         topk_level_bytes(B, nc, keep);
 }
 
-size_t topk_workspace_bytes(int B, int max_len, int keep) { return topk_ws_bytes(B, max_len, keep); }
+size_t topk_hist_bytes(int B) { return up256((size_t)B * TK_HBINS * 4); }
+
+size_t topk_workspace_bytes(int B, int max_len, int keep) {
+  return topk_hist_bytes(B) + topk_level_bytes(B, max_len, keep);
+}
 
 bool topk_supported(int max_len, int keep, int vis_only) {
   if (keep < 1) return false;
@@ -404,12 +383,20 @@ bool topk_supported(int max_len, int keep, int vis_only) {
 }
 
 static hipError_t launch_topk_level(const float* scores, int stride, const int* len, int len_div, int len_mul,
-                                    int max_len, int keep, int vis_only, int* idx, int* cnt, int B, hipStream_t s) {
+                                    int max_len, int keep, int vis_only, int* idx, int* cnt, int* hist, bool hist_ready,
+                                    int B, hipStream_t s) {
   const int E = topk_elems(max_len);
+  if (!E) return hipErrorInvalidValue;
+  if (!hist_ready) {
+    hipLaunchKernelGGL(topk_hist_kernel, dim3((max_len + TKH_CHUNK - 1) / TKH_CHUNK, B), dim3(TKH_THREADS), 0, s,
+                       scores, stride, len, len_div, len_mul, vis_only, hist);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
 #define TK_CASE(EV)                                                                                             \
   case EV:                                                                                                      \
-    hipLaunchKernelGGL(topk_kernel<EV>, dim3(B), dim3(TK_THREADS), 0, s, scores, stride, len, len_div, len_mul, \
-                       keep, vis_only, nullptr, 1, 0, idx, cnt);                                                \
+    hipLaunchKernelGGL(topk_select_kernel<EV>, dim3(B), dim3(TK_THREADS), 0, s, scores, stride, len, len_div,   \
+                       len_mul, keep, vis_only, hist, idx, cnt);                                                \
     break;
   switch (E) {
     TK_CASE(4)
@@ -426,9 +413,11 @@ static hipError_t launch_topk_level(const float* scores, int stride, const int* 
 // Selection over rows of `stride` scores whose lengths are len[row] (len_div / len_mul as in topk_kernel), n an upper
 // bound of the lengths.
 static hipError_t topk_rows(const float* scores, int stride, const int* len, int len_div, int len_mul, long n,
-                            int keep, int vis_only, int* idx, int* cnt, char* ws, int B, hipStream_t s) {
+                            int keep, int vis_only, int* idx, int* cnt, int* hist, bool hist_ready, char* ws, int B,
+                            hipStream_t s) {
   if (n <= TOPK_FLAT_MAX)
-    return launch_topk_level(scores, stride, len, len_div, len_mul, (int)n, keep, vis_only, idx, cnt, B, s);
+    return launch_topk_level(scores, stride, len, len_div, len_mul, (int)n, keep, vis_only, idx, cnt, hist,
+                             hist_ready, B, s);
   if (len_div != 1 || len_mul != 1) return hipErrorInvalidValue;  // only flat rows are split
   const int sub = topk_sub_block(n, keep);
   const int nb = (int)((n + sub - 1) / sub), nc = keep * sub;
@@ -445,22 +434,43 @@ static hipError_t topk_rows(const float* scores, int stride, const int* len, int
   if (e != hipSuccess) return e;
   // level 1: the top-keep sub-blocks (ceil(len / sub) maxima per row)
   if (nb > TOPK_FLAT_MAX) return hipErrorInvalidValue;  // excluded by topk_plan
-  e = launch_topk_level(bm, nb, len, sub, 1, nb, keep, vis_only, bidx, bcnt, B, s);
+  e = launch_topk_level(bm, nb, len, sub, 1, nb, keep, vis_only, bidx, bcnt, hist, false, B, s);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(gather_blocks_kernel, dim3((nc + 255) / 256, B), dim3(256), 0, s, scores, stride, len, sub, bidx,
                      bcnt, keep, cand);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   // level 2: the top-keep of the selected sub-blocks' scores in position order (NEG_INF past their count)
-  e = topk_rows(cand, nc, nullptr, 1, 1, nc, keep, vis_only, idx, cnt, ws, B, s);
+  e = topk_rows(cand, nc, nullptr, 1, 1, nc, keep, vis_only, idx, cnt, hist, false, ws, B, s);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(map_blocks_kernel, dim3((keep + 255) / 256, B), dim3(256), 0, s, idx, cnt, bidx, sub, keep);
   return hipGetLastError();
 }
 
+// ws: topk_workspace_bytes(B, max_len, keep) bytes whose histogram region is zero; hist_ready: the histogram of the
+// rows is already accumulated there (by the indexer), so the first level skips its histogram kernel.
 hipError_t launch_topk(const float* scores, const int* len, int* idx, int* cnt, void* ws, int B, int stride,
-                       int max_len, int keep, int vis_only, hipStream_t s) {
-  return topk_rows(scores, stride, len, 1, 1, max_len, keep, vis_only, idx, cnt, static_cast<char*>(ws), B, s);
+                       int max_len, int keep, int vis_only, bool hist_ready, hipStream_t s) {
+  char* p = static_cast<char*>(ws);
+  int* hist = reinterpret_cast<int*>(p);
+  if (hist_ready && max_len > TOPK_FLAT_MAX) return hipErrorInvalidValue;  // the indexer histograms flat rows only
+  return topk_rows(scores, stride, len, 1, 1, max_len, keep, vis_only, idx, cnt, hist, hist_ready,
+                   p + topk_hist_bytes(B), B, s);
+}
+
+// Zero-fills a workspace (a kernel, not a memset, so that callers may capture it in a graph).
+__global__ void fill_zero_kernel(uint4* __restrict__ p, size_t n16) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n16; i += (size_t)gridDim.x * blockDim.x)
+    p[i] = make_uint4(0, 0, 0, 0);
+}
+
+hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t s) {
+  const size_t n16 = bytes / 16;
+  if (n16) {
+    const int grid = (int)((n16 + 255) / 256 < 4096 ? (n16 + 255) / 256 : 4096);
+    hipLaunchKernelGGL(fill_zero_kernel, dim3(grid), dim3(256), 0, s, static_cast<uint4*>(p), n16);
+  }
+  return hipGetLastError();
 }
 
 hipError_t launch_topk_mask(const int* idx, const int* cnt, float* mask, int B, int keep, int P, hipStream_t s) {

@@ -65,7 +65,7 @@ def _run(q: torch.Tensor, kv: torch.Tensor, kv_scale: torch.Tensor, scale: float
     ls = torch.empty(B, H, dtype=torch.float32, device=dev) if lse else None
     wsb = _lib.workspace_bytes(_lib.DSA_WS_ATTENTION, B, H, keep, 0, splits)
     if workspace is None and wsb:
-        workspace = torch.empty(wsb, dtype=torch.uint8, device=dev)
+        workspace = torch.zeros(wsb, dtype=torch.uint8, device=dev)
     ws_len = 0 if workspace is None else workspace.numel() * workspace.element_size()
     o_bf = out if out.dtype == torch.bfloat16 else None
     o_32 = out if out.dtype == torch.float32 else None

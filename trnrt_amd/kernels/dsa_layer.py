@@ -41,7 +41,8 @@ class DecodeLayer:
         self.out = torch.empty(B, H, 512, dtype=torch.bfloat16, device=dev)
         self.lse = torch.empty(B, H, dtype=torch.float32, device=dev)
         wsb = _lib.workspace_bytes(_lib.DSA_WS_LAYER, B, H, keep, self.max_len, splits)
-        self.workspace = torch.empty(max(wsb, 256), dtype=torch.uint8, device=dev)
+        # zero once: the calls keep the regions that must start at zero (the top-k histograms) at zero
+        self.workspace = torch.zeros(max(wsb, 256), dtype=torch.uint8, device=dev)
 
     def step(self, q_idx: torch.Tensor, w: torch.Tensor, k_cache: torch.Tensor, k_scale: torch.Tensor,
              q: torch.Tensor, kv_cache: torch.Tensor, kv_scale: torch.Tensor, table: torch.Tensor,

@@ -55,8 +55,8 @@ def select_indices(scores: torch.Tensor, keep: int, lengths: torch.Tensor | None
     C.need(idx, "idx", torch.int32, (R, keep))
     C.need(cnt, "cnt", torch.int32, (R,))
     wsb = _lib.workspace_bytes(_lib.DSA_WS_TOPK, R, 0, keep, max(n, 1))
-    if workspace is None and wsb:
-        workspace = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    if workspace is None:
+        workspace = torch.zeros(wsb, dtype=torch.uint8, device=dev)  # the histogram region starts (and ends) at zero
     ws_len = 0 if workspace is None else workspace.numel() * workspace.element_size()
     st = _lib.lib().dsa_topk(C.ptr(scores), C.ptr(lengths), C.ptr(idx), C.ptr(cnt), C.ptr(workspace), ws_len, R, P,
                              n, keep, int(vis_only), C.stream_ptr(dev))
