@@ -71,7 +71,8 @@ def test_supported_and_workspace():
     assert lib.dsa_topk_supported(32768, 2048, 1) == 1
     assert lib.dsa_topk_supported(1 << 20, 2048, 1) == 1
     assert lib.dsa_topk_supported(1 << 20, 2048, 0) == 0
-    assert _lib.workspace_bytes(_lib.DSA_WS_TOPK, 8, 64, 2048, 32768) == 8 * 4096 * 4  # one level: the histograms
+    # one level: the histograms, the per-row meta and the candidate lists
+    assert 8 * 4096 * 4 + 8 * 16 * 2048 * 4 <= _lib.workspace_bytes(_lib.DSA_WS_TOPK, 8, 64, 2048, 32768) < 2 << 20
     assert _lib.workspace_bytes(_lib.DSA_WS_TOPK, 4, 64, 2048, 1 << 20) > 4 * (1 << 20) // 64 * 4
     sp = lib.dsa_default_splits(8, 64, 2048)
     assert 1 <= sp <= 32

@@ -40,7 +40,8 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 int resolve_splits(int splits, int B, int H, int keep) {
   if (splits <= 0) splits = dsa::attention_default_splits(B, H, keep, num_cu());
-  const int max_splits = (keep + 63) / 64;
+  int max_splits = (keep + 63) / 64;  // whole 64-slot chunks per split, at most 32 splits (the combine's limit)
+  max_splits = max_splits > 32 ? 32 : max_splits;
   return splits > max_splits ? max_splits : splits;
 }
 

@@ -26,23 +26,37 @@ constexpr int ATT_DV = 512;
 constexpr int ATT_HPW = 16;       // heads per workgroup
 constexpr int ATT_CH = 64;        // slots per chunk
 constexpr int ATT_THREADS = 256;  // 4 waves
-constexpr int ATT_KROW = ATT_DQK + 16;  // token-major row stride (bytes)
-constexpr int ATT_VROW = ATT_CH + 4;    // dim-major row stride (bytes)
-constexpr int ATT_PROW = ATT_CH + 4;    // P row stride (bf16 elements)
+constexpr int ATT_SUPER = 256;    // slots whose ids / scales / biases are set up at once (one per thread)
+constexpr int ATT_PIECES = ATT_DQK / 16;  // 16-byte pieces of a row
+constexpr int ATT_RPT = ATT_CH * ATT_PIECES / ATT_THREADS;  // pieces per thread per chunk (9)
+// Token-major row stride: 146 dwords, so the staging writes, the score operand reads and the transposing value
+// reads of rows 0..31 spread over the banks (at most 2-way).
+constexpr int ATT_KROW = ATT_DQK + 8;   // bytes
+constexpr int ATT_PROW = ATT_CH + 8;    // P row stride (bf16 elements; 16-byte aligned rows)
+
+typedef int att_v2i __attribute__((ext_vector_type(2)));
 
 struct AttShared {
-  uint8_t kt[ATT_CH * ATT_KROW];         // token-major e4m3 rows
-  uint8_t vt[ATT_DV * ATT_VROW];         // dim-major e4m3 values
-  uint16_t p[ATT_HPW * ATT_PROW];        // bf16 P[head][token]
-  int slot[ATT_CH];
-  float kscale[ATT_CH];
-  float bias[ATT_CH];
+  uint8_t kt[ATT_CH * ATT_KROW];   // token-major e4m3 rows of the chunk
+  uint16_t p[ATT_HPW * ATT_PROW];  // bf16 P[head][token]
+  int slot[ATT_SUPER];
+  float kscale[ATT_SUPER];
+  float bias[ATT_SUPER];
   float red[4][ATT_HPW];
 };
 
-__device__ __forceinline__ uint32_t byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xffu; }
+// The value operand of v_mfma_f32_16x16x32_bf16 straight from the token-major tile: ds_read_b64_tr_b8 gives lane
+// (a = i / 8, c = i % 8) of each 16-lane block byte c of the 8-byte rows addressed by the block's lanes 2j + a,
+// j = 0..7. Lane p of block q addresses token 32 ks + 8 q + p / 2 at dims 16 n + 8 (p & 1), so lane l receives dim
+// 16 n + l % 16 of tokens 32 ks + 8 (l / 16) + j: the B operand with k-slot 8 q + j = that token.
+__device__ __forceinline__ bf16x8 value_operand(const uint8_t* kt, int ks, int n, int lane) {
+  const int q = lane >> 4, p = lane & 15;
+  const uint8_t* a = kt + (32 * ks + 8 * q + (p >> 1)) * ATT_KROW + 16 * n + 8 * (p & 1);
+  const att_v2i r = __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) att_v2i*)(a));
+  return fp8x8_to_bf16x8((uint32_t)r.x, (uint32_t)r.y);
+}
 
-__global__ __launch_bounds__(ATT_THREADS) void sparse_mla_kernel(
+__global__ __launch_bounds__(ATT_THREADS, 2) void sparse_mla_kernel(
     const uint16_t* __restrict__ q, const uint8_t* __restrict__ kv, const float* __restrict__ kvs,
     const int* __restrict__ idx, const int* __restrict__ cnt, const int* __restrict__ table,
     const int* __restrict__ rows, const float* __restrict__ bias, uint16_t* __restrict__ out,
@@ -65,9 +79,10 @@ __global__ __launch_bounds__(ATT_THREADS) void sparse_mla_kernel(
   const int l16 = lane & 15, q4 = lane >> 4;
   const bool token_form = rows == nullptr;
   int n_eff = keep;
+  int cnt_b = keep;
   if (token_form) {
-    int c = cnt[b];
-    c = c < 1 ? 1 : (c > keep ? keep : c);  // cnt 0: attend slot 0, fully masked (the reference's uniform row)
+    cnt_b = cnt[b];
+    int c = cnt_b < 1 ? 1 : (cnt_b > keep ? keep : cnt_b);  // cnt 0: attend slot 0, fully masked
     n_eff = c;
   }
   const int k_begin = sp * slots_per_split;
@@ -89,127 +104,122 @@ __global__ __launch_bounds__(ATT_THREADS) void sparse_mla_kernel(
   float l_run = 0.0f;       // this lane's share of the running sum of head l16
 
   const int* trow = table ? table + (size_t)b * max_pages : nullptr;
-  for (int k0 = k_begin; k0 < k_end; k0 += ATT_CH) {
-    // slots, scales and biases of the chunk
-    if (tid < ATT_CH) {
-      const int k = k0 + tid;
-      int slot = 0;
-      float bs = NEG_INF;
-      if (k < k_end) {
+  for (int sc0 = k_begin; sc0 < k_end; sc0 += ATT_SUPER) {
+    const int nslots = min(ATT_SUPER, k_end - sc0);
+    const int nch = (nslots + ATT_CH - 1) / ATT_CH;
+    // slots, scales and biases of the super-chunk: one per thread
+    {
+      const int k = sc0 + tid;
+      int slot = -1;
+      float bs = -INFINITY;  // past the split: weight exactly 0 (a copy of the super-chunk's first row)
+      if (tid < nslots) {
         if (token_form) {
           int pos = idx[(size_t)b * keep + k];
           pos = pos < 0 ? 0 : pos;
           int pi = pos / page_size;
           pi = pi < max_pages ? pi : max_pages - 1;
           slot = safe_page(trow[pi], num_pages) * page_size + (pos - (pos / page_size) * page_size);
-          bs = (k < cnt[b]) ? 0.0f : NEG_INF;
+          bs = (k < cnt_b) ? 0.0f : NEG_INF;
         } else {
           slot = rows[(size_t)b * keep + k];
           slot = ((unsigned)slot < (unsigned)(num_pages * page_size)) ? slot : 0;
           bs = bias[(size_t)b * keep + k];
         }
-      } else {
-        // past the split: a copy of the chunk's first row with weight exactly 0 (bias -inf), also when every real
-        // slot of the chunk is masked at NEG_INF (a fully masked row averages its real slots only)
-        slot = -1;
-        bs = -INFINITY;
       }
       sh.slot[tid] = slot;
       sh.bias[tid] = bs;
-    }
-    __syncthreads();
-    if (tid < ATT_CH) {
-      int slot = sh.slot[tid];
-      if (slot < 0) slot = sh.slot[0];
+      __syncthreads();
+      if (slot < 0) slot = sh.slot[0];  // slot 0 of a super-chunk is always real
+      __syncthreads();
       sh.slot[tid] = slot;
       sh.kscale[tid] = kvs[slot];
     }
     __syncthreads();
-    // token-major staging: 64 rows x 36 pieces of 16 bytes
-    for (int i = tid; i < ATT_CH * 36; i += ATT_THREADS) {
-      const int r = i / 36, c = i - r * 36;
-      const uint4 v = *reinterpret_cast<const uint4*>(kv + (size_t)sh.slot[r] * ATT_DQK + 16 * c);
-      *reinterpret_cast<uint4*>(&sh.kt[r * ATT_KROW + 16 * c]) = v;
-    }
-    __syncthreads();
-    // dim-major staging of the first 512 columns: 16 token quads x 128 dim quads, a 4x4 byte transpose each
-    for (int i = tid; i < 16 * 128; i += ATT_THREADS) {
-      const int g = i & 127, tq = i >> 7;
-      uint32_t w0 = *reinterpret_cast<const uint32_t*>(&sh.kt[(4 * tq + 0) * ATT_KROW + 4 * g]);
-      uint32_t w1 = *reinterpret_cast<const uint32_t*>(&sh.kt[(4 * tq + 1) * ATT_KROW + 4 * g]);
-      uint32_t w2 = *reinterpret_cast<const uint32_t*>(&sh.kt[(4 * tq + 2) * ATT_KROW + 4 * g]);
-      uint32_t w3 = *reinterpret_cast<const uint32_t*>(&sh.kt[(4 * tq + 3) * ATT_KROW + 4 * g]);
+    // the chunk's rows in registers (thread tid holds 16-byte pieces tid + 256 j), one chunk ahead of the tile
+    uint4 rv[ATT_RPT];
+    auto load_rows = [&](int c) {
 #pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        const uint32_t t = byte_of(w0, d) | (byte_of(w1, d) << 8) | (byte_of(w2, d) << 16) | (byte_of(w3, d) << 24);
-        *reinterpret_cast<uint32_t*>(&sh.vt[(4 * g + d) * ATT_VROW + 4 * tq]) = t;
+      for (int jj = 0; jj < ATT_RPT; ++jj) {
+        const int i = tid + ATT_THREADS * jj;
+        const int r = i / ATT_PIECES, pc = i - r * ATT_PIECES;
+        rv[jj] = *reinterpret_cast<const uint4*>(kv + (size_t)sh.slot[c * ATT_CH + r] * ATT_DQK + 16 * pc);
       }
-    }
+    };
+    load_rows(0);
 
-    // scores of tokens 16 wave .. 16 wave + 15, heads l16
-    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    {
-      const uint8_t* kr = &sh.kt[(16 * wave + l16) * ATT_KROW + 144 * q4];
+    for (int c = 0; c < nch; ++c) {
+      const int cb = c * ATT_CH;  // the chunk's first slot inside the super-chunk
 #pragma unroll
-      for (int st = 0; st < 18; ++st) {
-        const uint2 kb = *reinterpret_cast<const uint2*>(kr + 8 * st);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16x8(kb.x, kb.y), qb[st], acc, 0, 0, 0);
+      for (int jj = 0; jj < ATT_RPT; ++jj) {
+        const int i = tid + ATT_THREADS * jj;
+        const int r = i / ATT_PIECES, pc = i - r * ATT_PIECES;
+        uint8_t* dst = &sh.kt[r * ATT_KROW + 16 * pc];
+        *reinterpret_cast<uint2*>(dst) = make_uint2(rv[jj].x, rv[jj].y);
+        *reinterpret_cast<uint2*>(dst + 8) = make_uint2(rv[jj].z, rv[jj].w);
       }
-    }
-    // acc[r] = S^T[token 16 wave + 4 q4 + r][head l16]
-    float s[4];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int tk = 16 * wave + 4 * q4 + r;
-      s[r] = acc[r] * (sh.kscale[tk] * scale) + sh.bias[tk];
-      mx = fmaxf(mx, s[r]);
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, WAVE));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
-    if (lane < ATT_HPW) sh.red[wave][lane] = mx;
-    __syncthreads();  // chunk maxima and both staged tiles visible
-    float mc = fmaxf(fmaxf(sh.red[0][l16], sh.red[1][l16]), fmaxf(sh.red[2][l16], sh.red[3][l16]));
-    const float m_new = fmaxf(m_run, mc);
-    const float alpha = __expf(m_run - m_new);
-    m_run = m_new;
-    float psum = 0.0f;
-    uint32_t pk[2];
-#pragma unroll
-    for (int r = 0; r < 4; r += 2) {
-      const int tk = 16 * wave + 4 * q4 + r;
-      const float p0 = __expf(s[r] - m_new), p1 = __expf(s[r + 1] - m_new);
-      psum += p0 + p1;
-      pk[r / 2] = (uint32_t)f32_to_bf16_bits(p0 * sh.kscale[tk]) |
-                  ((uint32_t)f32_to_bf16_bits(p1 * sh.kscale[tk + 1]) << 16);
-    }
-    l_run = l_run * alpha + psum;
-    *reinterpret_cast<uint2*>(&sh.p[l16 * ATT_PROW + 16 * wave + 4 * q4]) = make_uint2(pk[0], pk[1]);
-    __syncthreads();  // P complete
+      __syncthreads();  // the tile is complete
+      if (c + 1 < nch) load_rows(c + 1);  // the next chunk's loads fly while this one computes
 
-    // rescale O (rows = heads 4 q4 + r) and accumulate P . V over the chunk's 64 tokens
-    float al[4];
+      // scores of tokens 16 wave .. 16 wave + 15, heads l16
+      f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+      {
+        const uint8_t* kr = &sh.kt[(16 * wave + l16) * ATT_KROW + 144 * q4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) al[r] = __shfl(alpha, 4 * q4 + r, WAVE);
-#pragma unroll
-    for (int n = 0; n < 8; ++n)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) o[n][r] *= al[r];
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const int tb = 32 * ks + 4 * q4;
-      const uint2 pa = *reinterpret_cast<const uint2*>(&sh.p[l16 * ATT_PROW + tb]);
-      const uint2 pb = *reinterpret_cast<const uint2*>(&sh.p[l16 * ATT_PROW + tb + 16]);
-      const bf16x8 pop = as_bf16x8(make_uint4(pa.x, pa.y, pb.x, pb.y));
-#pragma unroll
-      for (int n = 0; n < 8; ++n) {
-        const int dim = 128 * wave + 16 * n + l16;
-        const uint32_t va = *reinterpret_cast<const uint32_t*>(&sh.vt[dim * ATT_VROW + tb]);
-        const uint32_t vb = *reinterpret_cast<const uint32_t*>(&sh.vt[dim * ATT_VROW + tb + 16]);
-        o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pop, fp8x8_to_bf16x8(va, vb), o[n], 0, 0, 0);
+        for (int st = 0; st < 18; ++st) {
+          const uint2 kb = *reinterpret_cast<const uint2*>(kr + 8 * st);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16x8(kb.x, kb.y), qb[st], acc, 0, 0, 0);
+        }
       }
+      // acc[r] = S^T[token 16 wave + 4 q4 + r][head l16]
+      float s4[4];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int tk = cb + 16 * wave + 4 * q4 + r;
+        s4[r] = acc[r] * (sh.kscale[tk] * scale) + sh.bias[tk];
+        mx = fmaxf(mx, s4[r]);
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, WAVE));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
+      if (lane < ATT_HPW) sh.red[wave][lane] = mx;
+      __syncthreads();  // the chunk maxima
+      const float mc = fmaxf(fmaxf(sh.red[0][l16], sh.red[1][l16]), fmaxf(sh.red[2][l16], sh.red[3][l16]));
+      const float m_new = fmaxf(m_run, mc);
+      const float alpha = __expf(m_run - m_new);
+      m_run = m_new;
+      float psum = 0.0f;
+      uint32_t pk[2];
+#pragma unroll
+      for (int r = 0; r < 4; r += 2) {
+        const int tk = cb + 16 * wave + 4 * q4 + r;
+        const float p0 = __expf(s4[r] - m_new), p1 = __expf(s4[r + 1] - m_new);
+        psum += p0 + p1;
+        pk[r / 2] = (uint32_t)f32_to_bf16_bits(p0 * sh.kscale[tk]) |
+                    ((uint32_t)f32_to_bf16_bits(p1 * sh.kscale[tk + 1]) << 16);
+      }
+      l_run = l_run * alpha + psum;
+      *reinterpret_cast<uint2*>(&sh.p[l16 * ATT_PROW + 16 * wave + 4 * q4]) = make_uint2(pk[0], pk[1]);
+      __syncthreads();  // P complete
+
+      // rescale O (rows = heads 4 q4 + r) and accumulate P . V over the chunk's 64 tokens (dims 128 wave ..)
+      float al[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) al[r] = __shfl(alpha, 4 * q4 + r, WAVE);
+#pragma unroll
+      for (int n = 0; n < 8; ++n)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[n][r] *= al[r];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        // P operand: head l16, tokens 32 ks + 8 q4 .. + 7 (the value operand's k-slot order)
+        const bf16x8 pop = as_bf16x8(*reinterpret_cast<const uint4*>(&sh.p[l16 * ATT_PROW + 32 * ks + 8 * q4]));
+#pragma unroll
+        for (int n = 0; n < 8; ++n)
+          o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pop, value_operand(sh.kt, ks, 8 * wave + n, lane), o[n], 0,
+                                                         0, 0);
+      }
+      __syncthreads();  // the next chunk overwrites the tiles
     }
-    __syncthreads();  // the next chunk overwrites the tiles
   }
 
   // the row sums: lane shares -> per wave -> per workgroup
@@ -262,30 +272,42 @@ __global__ __launch_bounds__(ATT_THREADS) void sparse_mla_kernel(
 
 // o = sum_s W_s o_s / sum_s W_s with W_s = l_s exp(m_s - M), M = max_s m_s, and lse = M + log sum_s W_s, per
 // (sequence, head), from each split's normalised o_s, max m_s and sum l_s (the log-sum-exp combine of
-// trnrt/models/mla.py:853-856 with lse_s = m_s + log l_s kept in two parts); 128 threads x 4 dims.
+// trnrt/models/mla.py:853-856 with lse_s = m_s + log l_s kept in two parts); 128 threads x 4 dims. Every load is
+// issued before any is used (one memory round trip); an empty split's o_s is 0 and its weight 0.
+template <int S>
 __global__ __launch_bounds__(128) void combine_splits_kernel(const float* __restrict__ ws_o,
                                                              const float* __restrict__ ws_ml, int H, int splits,
                                                              uint16_t* __restrict__ out, float* __restrict__ out_f32,
                                                              float* __restrict__ lse_out) {
   const int bh = blockIdx.x;
   const int b = bh / H, head = bh - b * H;
+  const int d = 4 * threadIdx.x;
+  float2 ml[S];
+  float4 v[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    if (s < splits) {
+      const size_t i = ((size_t)b * splits + s) * H + head;
+      ml[s] = *reinterpret_cast<const float2*>(&ws_ml[2 * i]);
+      v[s] = *reinterpret_cast<const float4*>(&ws_o[i * ATT_DV + d]);
+    } else {
+      ml[s] = make_float2(-INFINITY, 0.0f);
+      v[s] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
   float M = -INFINITY;
-  for (int s = 0; s < splits; ++s) M = fmaxf(M, ws_ml[(((size_t)b * splits + s) * H + head) * 2]);
+#pragma unroll
+  for (int s = 0; s < S; ++s) M = fmaxf(M, ml[s].x);
   float W = 0.0f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  const int d = 4 * threadIdx.x;
-  for (int s = 0; s < splits; ++s) {
-    const size_t mi = (((size_t)b * splits + s) * H + head) * 2;
-    const float ls = ws_ml[mi + 1];
-    const float wt = ls > 0.0f ? ls * __expf(ws_ml[mi] - M) : 0.0f;
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const float wt = ml[s].y > 0.0f ? ml[s].y * __expf(ml[s].x - M) : 0.0f;
     W += wt;
-    if (wt != 0.0f) {
-      const float4 v = *reinterpret_cast<const float4*>(&ws_o[(((size_t)b * splits + s) * H + head) * ATT_DV + d]);
-      acc.x += wt * v.x;
-      acc.y += wt * v.y;
-      acc.z += wt * v.z;
-      acc.w += wt * v.w;
-    }
+    acc.x += wt * v[s].x;
+    acc.y += wt * v[s].y;
+    acc.z += wt * v[s].z;
+    acc.w += wt * v[s].w;
   }
   const float inv = 1.0f / W;
   const size_t oi = ((size_t)b * H + head) * ATT_DV + d;
@@ -317,7 +339,8 @@ __global__ void token_rows_kernel(const int* __restrict__ idx, const int* __rest
 
 int attention_default_splits(int B, int H, int keep, int num_cu) {
   const int wgs = B * (H / ATT_HPW);
-  const int max_splits = (keep + ATT_CH - 1) / ATT_CH;
+  int max_splits = (keep + ATT_CH - 1) / ATT_CH;
+  max_splits = max_splits > 32 ? 32 : max_splits;
   int s = (num_cu + wgs - 1) / (wgs > 0 ? wgs : 1);
   s = s < 1 ? 1 : s;
   return s > max_splits ? max_splits : s;
@@ -350,8 +373,15 @@ hipError_t launch_sparse_mla(const uint16_t* q, const uint8_t* kv, const float* 
                      sps);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || eff_splits == 1) return e;
-  hipLaunchKernelGGL(combine_splits_kernel, dim3(B * H), dim3(128), 0, s, ws_o, ws_ml, H, eff_splits, out, out_f32,
-                     lse);
+  if (eff_splits <= 8)
+    hipLaunchKernelGGL(combine_splits_kernel<8>, dim3(B * H), dim3(128), 0, s, ws_o, ws_ml, H, eff_splits, out,
+                       out_f32, lse);
+  else if (eff_splits <= 16)
+    hipLaunchKernelGGL(combine_splits_kernel<16>, dim3(B * H), dim3(128), 0, s, ws_o, ws_ml, H, eff_splits, out,
+                       out_f32, lse);
+  else
+    hipLaunchKernelGGL(combine_splits_kernel<32>, dim3(B * H), dim3(128), 0, s, ws_o, ws_ml, H, eff_splits, out,
+                       out_f32, lse);
   return hipGetLastError();
 }
 

@@ -128,136 +128,438 @@ __global__ __launch_bounds__(TKH_THREADS) void topk_hist_kernel(const float* __r
   }
 }
 
-// The selection of one row (E scores per thread, positions t E .. t E + E - 1), given the row's first-level
-// histogram: the threshold's 12-bit bin from the histogram, the threshold inside it by two passes over the low key
-// bits (only keys inside the bin count), then the ordered output. Re-zeroes the histogram.
-template <int E>
-__global__ __launch_bounds__(TK_THREADS) void topk_select_kernel(const float* __restrict__ scores, int stride,
-                                                                 const int* __restrict__ len, int len_div,
-                                                                 int len_mul, int keep, int vis_only,
-                                                                 int* __restrict__ hist, int* __restrict__ idx_out,
-                                                                 int* __restrict__ cnt_out) {
-  __shared__ TopkShared sh;
-  const int row = blockIdx.x;
+__device__ __forceinline__ uint64_t lanes_below() {
+  const int lane = threadIdx.x & (WAVE - 1);
+  return lane ? (~0ull >> (64 - lane)) : 0ull;
+}
+
+// The flat selection of rows of up to TS_MAXCH x 2048 scores, spread over workgroups of 2048 scores (chunks), in two
+// kernels with no waiting between workgroups:
+//   topk_chunk_kernel:  from the row's first-level histogram the threshold's 12-bit bin c0 (every chunk computes it);
+//                       per chunk the count of keys in bins above c0 and the keys of bin c0 (the candidates, a few
+//                       hundred per row for indexer scores), written in position order (so list order ranks ties);
+//   topk_output_kernel: every chunk loads the row's candidates (thread t the t-th of each chunk), two histogram
+//                       passes over their low key bits give the exact threshold T and the number of keys equal to T
+//                       to take (lowest positions first), the chunk's output base follows from the per-chunk counts,
+//                       and the chunk writes its selected positions in order.
+// Thread t holds the float4 groups e = 0, 1 at chunk positions 4 (256 e + t) .. + 3 (coalesced loads), so group e
+// of wave w is the contiguous block of 256 positions 1024 e + 256 w .. of the chunk.
+constexpr int TS_THREADS = 256;
+constexpr int TS_WAVES = TS_THREADS / WAVE;
+constexpr int TS_G = 2;
+constexpr int TS_CHUNK = TS_THREADS * 4 * TS_G;  // 2048
+constexpr int TS_MAXCH = 16;                     // rows up to 32768 scores
+
+struct RowMeta {
+  int c0;      // the threshold's 12-bit bin (-1: every selectable key is selected)
+  int above0;  // selectable keys in bins above c0
+  int nvis;    // selectable keys of the row
+  int pad;
+  int n_a[TS_MAXCH];  // per chunk: keys in bins above c0
+  int n_c[TS_MAXCH];  // per chunk: keys in bin c0
+};
+
+__device__ __forceinline__ void load_chunk_keys(const float* srow, int L, int base, bool vec, int vis_only,
+                                                uint32_t (&key)[TS_G][4]) {
   const int t = threadIdx.x;
-  const int L = level_len(len, row, len_div, len_mul, stride);
-  const float* srow = scores + (size_t)row * stride;
-  const int p0 = t * E;
-
-  // the row's histogram (4 bins per thread) and keys
-  int* hrow = hist + (size_t)row * TK_HBINS;
-  const int4 hv = *reinterpret_cast<const int4*>(hrow + 4 * t);
-  uint32_t key[E];
-  if (((stride & 3) == 0) && ((E & 3) == 0) && p0 + E <= L) {
-    float4 raw[E / 4];
 #pragma unroll
-    for (int e = 0; e < E / 4; ++e) raw[e] = *reinterpret_cast<const float4*>(srow + p0 + 4 * e);
+  for (int e = 0; e < TS_G; ++e) {
+    const int p = base + 4 * (TS_THREADS * e + t);
+    if (vec && p + 4 <= L) {
+      const float4 v = *reinterpret_cast<const float4*>(srow + p);
+      key[e][0] = select_key(v.x, vis_only);
+      key[e][1] = select_key(v.y, vis_only);
+      key[e][2] = select_key(v.z, vis_only);
+      key[e][3] = select_key(v.w, vis_only);
+    } else {
 #pragma unroll
-    for (int e = 0; e < E / 4; ++e) {
-      key[4 * e + 0] = select_key(raw[e].x, vis_only);
-      key[4 * e + 1] = select_key(raw[e].y, vis_only);
-      key[4 * e + 2] = select_key(raw[e].z, vis_only);
-      key[4 * e + 3] = select_key(raw[e].w, vis_only);
+      for (int c = 0; c < 4; ++c) key[e][c] = (p + c < L) ? select_key(srow[p + c], vis_only) : 0u;
     }
-  } else {
-#pragma unroll
-    for (int e = 0; e < E; ++e) key[e] = (p0 + e < L) ? select_key(srow[p0 + e], vis_only) : 0u;
   }
+}
 
-  // threshold bin among this thread's 4 (bins 4t .. 4t + 3, higher bins first). The defaults keep every index in
-  // range should the histogram not match the scores (a workspace that was not zero): the selection is then wrong but
-  // every write stays inside its buffer.
+// Exclusive prefix over the (e, wave) blocks of per-block counts (packed hi / lo 16 bits), in position order.
+__device__ __forceinline__ void block_bases(uint32_t (&cnt)[TS_G], uint32_t* blk, uint32_t (&base)[TS_G]) {
+  const int wave = threadIdx.x / WAVE, lane = threadIdx.x & (WAVE - 1);
+  if (lane == 0)
+#pragma unroll
+    for (int e = 0; e < TS_G; ++e) blk[e * TS_WAVES + wave] = cnt[e];
+  __syncthreads();
+#pragma unroll
+  for (int e = 0; e < TS_G; ++e) {
+    uint32_t acc = 0;
+    const int me = e * TS_WAVES + wave;
+#pragma unroll
+    for (int i = 0; i < TS_G * TS_WAVES; ++i) acc += i < me ? blk[i] : 0u;
+    base[e] = acc;
+  }
+  __syncthreads();
+}
+
+struct ChunkShared {
+  int bins[TS_THREADS];  // per thread: its 16 bins' sum, for the suffix scan
+  uint32_t blk[TS_G * TS_WAVES];
+  int c0, above0;
+};
+
+__global__ __launch_bounds__(TS_THREADS) void topk_chunk_kernel(const float* __restrict__ scores, int stride,
+                                                                const int* __restrict__ len, int len_div,
+                                                                int len_mul, int keep, int vis_only,
+                                                                const int* __restrict__ hist,
+                                                                RowMeta* __restrict__ meta,
+                                                                uint32_t* __restrict__ ckey) {
+  __shared__ ChunkShared sh;
+  const int row = blockIdx.y, chunk = blockIdx.x;
+  const int t = threadIdx.x, lane = t & (WAVE - 1);
+  const int L = level_len(len, row, len_div, len_mul, stride);
+  const int base = chunk * TS_CHUNK;
+  const int* hrow = hist + (size_t)row * TK_HBINS;
+  int4 hv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) hv[i] = *reinterpret_cast<const int4*>(hrow + 16 * t + 4 * i);
+  uint32_t key[TS_G][4];
+  load_chunk_keys(scores + (size_t)row * stride, L, base, (stride & 3) == 0, vis_only, key);
+
+  // suffix sums of the 16-bin groups (thread t: bins 16 t .. 16 t + 15), every thread its own exclusive suffix
+  int hb[16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    hb[4 * i] = hv[i].x;
+    hb[4 * i + 1] = hv[i].y;
+    hb[4 * i + 2] = hv[i].z;
+    hb[4 * i + 3] = hv[i].w;
+  }
+  int mine = 0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) mine += hb[i];
   if (t == 0) {
-    sh.sel_bin = 0;
+    sh.c0 = -1;
+    sh.above0 = 0;
+  }
+  int inc = mine;  // suffix inside the wave: lanes >= this one
+#pragma unroll
+  for (int o = 1; o < WAVE; o <<= 1) {
+    const int x = __shfl_down(inc, o, WAVE);
+    if (lane + o < WAVE) inc += x;
+  }
+  if (lane == 0) sh.bins[t / WAVE] = inc;  // the wave's total
+  __syncthreads();
+  int suf = inc - mine, nvis = 0;
+#pragma unroll
+  for (int i = 0; i < TS_WAVES; ++i) {
+    const int x = sh.bins[i];
+    suf += i > t / WAVE ? x : 0;
+    nvis += x;
+  }
+  if (nvis > keep && suf < keep && suf + mine >= keep) {
+#pragma unroll
+    for (int i = 15; i >= 0; --i) {
+      if (suf < keep && suf + hb[i] >= keep) {
+        sh.c0 = 16 * t + i;
+        sh.above0 = suf;
+      }
+      suf += hb[i];
+    }
+  }
+  __syncthreads();
+  const int c0 = sh.c0;  // -1: at most keep selectable keys, every one is selected
+  if (chunk == 0 && t == 0) {
+    meta[row].c0 = c0;
+    meta[row].above0 = sh.above0;
+    meta[row].nvis = nvis;
+  }
+  // classification: above c0, or in c0 (a candidate); the candidates in position order
+  const uint64_t below = lanes_below();
+  uint64_t cm[TS_G][4];
+  uint32_t cnt[TS_G], na = 0;
+#pragma unroll
+  for (int e = 0; e < TS_G; ++e) {
+    cnt[e] = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t k = key[e][c];
+      const int bin = (int)(k >> TK_HSHIFT);
+      na += __popcll(__ballot(k != 0 && bin > c0));
+      cm[e][c] = __ballot(k != 0 && bin == c0);
+      cnt[e] += __popcll(cm[e][c]);
+    }
+  }
+  uint32_t bb[TS_G];
+  block_bases(cnt, sh.blk, bb);
+  uint32_t* krow = ckey + ((size_t)row * TS_MAXCH + chunk) * TS_CHUNK;
+#pragma unroll
+  for (int e = 0; e < TS_G; ++e) {
+    int o = (int)bb[e];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) o += __popcll(cm[e][c] & below);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if ((cm[e][c] >> lane) & 1ull) krow[o++] = key[e][c];
+    }
+  }
+  // the chunk's counts (na was counted per wave: every lane holds its wave's total)
+  __syncthreads();
+  if (lane == 0) sh.bins[t / WAVE] = (int)na;
+  __syncthreads();
+  if (t == 0) {
+    int tot_a = 0;
+    for (int i = 0; i < TS_WAVES; ++i) tot_a += sh.bins[i];
+    int tot_c = 0;
+    for (int i = 0; i < TS_G * TS_WAVES; ++i) tot_c += (int)sh.blk[i];
+    meta[row].n_a[chunk] = tot_a;
+    meta[row].n_c[chunk] = tot_c;
+  }
+}
+
+struct OutShared {
+  int hist[TK_BINS];
+  int gt[TS_MAXCH], tie[TS_MAXCH], nc[TS_MAXCH], na[TS_MAXCH];
+  int off[TS_MAXCH + 1];
+  uint32_t blk[TS_G * TS_WAVES];
+  int c0, above0, nvis, maxc;
+  int sel_c, sel_above;
+  uint32_t T;
+  int room;
+};
+
+// One refinement pass's threshold bin, by wave 0 over the block-wide histogram of nbins bins (32 or 8 per lane):
+// the bin holding the need-th largest key and the keys above it, into sh.sel_c / sh.sel_above.
+__device__ __forceinline__ void wave0_find_bin(OutShared& sh, int nbins, int need) {
+  const int lane = threadIdx.x & (WAVE - 1);
+  constexpr int PER = TK_BINS / WAVE;
+  const int per = nbins / WAVE;
+  int hb[PER];
+  const int4* h4 = reinterpret_cast<const int4*>(sh.hist);
+#pragma unroll
+  for (int i = 0; i < PER / 4; ++i) {
+    int4 v = make_int4(0, 0, 0, 0);
+    if (4 * i < per) v = h4[(per / 4) * lane + i];
+    hb[4 * i] = v.x;
+    hb[4 * i + 1] = v.y;
+    hb[4 * i + 2] = v.z;
+    hb[4 * i + 3] = v.w;
+  }
+  int mine = 0;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) mine += hb[i];
+  int inc = mine;
+#pragma unroll
+  for (int o = 1; o < WAVE; o <<= 1) {
+    const int x = __shfl_down(inc, o, WAVE);
+    if (lane + o < WAVE) inc += x;
+  }
+  int suf = inc - mine;
+  int found = -1, above = 0;
+  if (suf < need && suf + mine >= need) {
+#pragma unroll
+    for (int i = PER - 1; i >= 0; --i) {
+      if (found < 0 && i < per) {
+        if (suf + hb[i] >= need) {
+          found = per * lane + i;
+          above = suf;
+        } else {
+          suf += hb[i];
+        }
+      }
+    }
+  }
+  const uint64_t who = __ballot(found >= 0);
+  if (who) {
+    const int src = (int)__builtin_ctzll(who);
+    if (lane == src) {
+      sh.sel_c = found;
+      sh.sel_above = above;
+    }
+  } else if (lane == 0) {  // counts that do not match (a workspace that was not zero): stay in range
+    sh.sel_c = 0;
     sh.sel_above = 0;
   }
-  int nvis = 0;
-  const int hsum = hv.x + hv.y + hv.z + hv.w;
-  const int above4 = block_excl_suffix(hsum, sh, &nvis);  // keys in bins above 4t + 3
-  *reinterpret_cast<int4*>(hrow + 4 * t) = make_int4(0, 0, 0, 0);  // leave the histogram zero for the next call
-  uint32_t T = 0;  // select key > T, plus the first `room` keys == T by position
-  int room = 0;
-  if (nvis > keep) {
-    {
-      const int hb[4] = {hv.x, hv.y, hv.z, hv.w};
-      int suf = above4;
-#pragma unroll
-      for (int i = 3; i >= 0; --i) {
-        if (suf < keep && suf + hb[i] >= keep) {
-          sh.sel_bin = 4 * t + i;
-          sh.sel_above = suf;
-        }
-        suf += hb[i];
-      }
-    }
-    __syncthreads();
-    const int c0 = sh.sel_bin & (TK_HBINS - 1);
-    int need = keep - sh.sel_above;
-    uint32_t lo = (uint32_t)c0 << TK_HSHIFT, hi = lo | ((1u << TK_HSHIFT) - 1u);
-    while (lo != hi) {
-      for (int i = t; i < TK_BINS; i += TK_THREADS) sh.hist[i] = 0;
-      __syncthreads();
-      const int sb = max(0, bit_length(hi - lo) - TK_BITS);
-#pragma unroll
-      for (int e = 0; e < E; ++e) {
-        const uint32_t k = key[e];
-        if (k >= lo && k <= hi) atomicAdd(&sh.hist[(k - lo) >> sb], 1);
-      }
-      __syncthreads();
-      // the bin of the need-th largest key inside [lo, hi] (2 bins per thread)
-      const int h0 = sh.hist[2 * t], h1 = sh.hist[2 * t + 1];
-      if (t == 0) {
-        sh.sel_bin = 0;
-        sh.sel_above = 0;
-      }
-      int tot = 0;
-      const int suf = block_excl_suffix(h0 + h1, sh, &tot);
-      if (suf < need && suf + h1 >= need) {
-        sh.sel_bin = 2 * t + 1;
-        sh.sel_above = suf;
-      } else if (suf + h1 < need && suf + h1 + h0 >= need) {
-        sh.sel_bin = 2 * t;
-        sh.sel_above = suf + h1;
-      }
-      __syncthreads();
-      const int c = sh.sel_bin & (TK_BINS - 1);
-      need -= sh.sel_above;
-      __syncthreads();
-      const uint32_t nlo = lo + ((uint32_t)c << sb);
-      const uint32_t width = (1u << sb) - 1u;
-      hi = (hi - nlo > width) ? nlo + width : hi;
-      lo = nlo;
-    }
-    T = lo;
-    room = need;
-  }
+}
 
-  // ordered output: one scan of the packed (above, tied) counts; the selected before a position are the keys above
-  // T before it plus min(room, ties before it)
-  uint32_t na = 0, nt = 0;
+__global__ __launch_bounds__(TS_THREADS) void topk_output_kernel(const float* __restrict__ scores, int stride,
+                                                                 const int* __restrict__ len, int len_div,
+                                                                 int len_mul, int keep, int vis_only, int nchunks,
+                                                                 int* __restrict__ hist,
+                                                                 const RowMeta* __restrict__ meta,
+                                                                 const uint32_t* __restrict__ ckey,
+                                                                 int* __restrict__ idx_out, int* __restrict__ cnt_out) {
+  __shared__ OutShared sh;
+  const int row = blockIdx.y, chunk = blockIdx.x;
+  const int t = threadIdx.x, wave = t / WAVE, lane = t & (WAVE - 1);
+  const int L = level_len(len, row, len_div, len_mul, stride);
+  const int base = chunk * TS_CHUNK;
+  // the row's meta in one round of loads (wave 0: lanes 0 .. 15 the chunk counts), counts clamped into range
+  if (wave == 0) {
+    int x = 0, y = 0;
+    if (lane < TS_MAXCH && lane < nchunks) {
+      x = meta[row].n_c[lane];
+      y = meta[row].n_a[lane];
+      x = x < 0 ? 0 : (x > TS_CHUNK ? TS_CHUNK : x);
+      y = y < 0 ? 0 : (y > TS_CHUNK ? TS_CHUNK : y);
+    }
+    int inc = x;  // prefix of the candidate counts (lanes 0 .. 15)
 #pragma unroll
-  for (int e = 0; e < E; ++e) {
-    na += key[e] > T;
-    nt += (T != 0) && (key[e] == T);
+    for (int o = 1; o < 32; o <<= 1) {
+      const int u = __shfl_up(inc, o, WAVE);
+      if (lane >= o) inc += u;
+    }
+    int mx = x;
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) mx = max(mx, __shfl_xor(mx, o, WAVE));
+    if (lane < TS_MAXCH) {
+      sh.nc[lane] = x;
+      sh.na[lane] = y;
+      sh.off[lane] = inc - x;
+      sh.gt[lane] = 0;
+      sh.tie[lane] = 0;
+    }
+    if (lane == TS_MAXCH) sh.off[TS_MAXCH] = __shfl(inc, TS_MAXCH - 1, WAVE);
+    if (lane == 0) {
+      sh.c0 = meta[row].c0;
+      sh.above0 = meta[row].above0;
+      sh.nvis = meta[row].nvis;
+      sh.maxc = mx;
+    }
   }
-  uint32_t tot = 0;
-  const uint32_t before = block_excl_scan((na << 16) | nt, sh, &tot);
-  const int above_before = (int)(before >> 16), tie_before = (int)(before & 0xffffu);
-  int take = room - tie_before;
-  take = take < 0 ? 0 : (take > (int)nt ? (int)nt : take);
-  int o = above_before + (tie_before < room ? tie_before : room);
-  const int cnt = nvis < 0 ? 0 : (nvis < keep ? nvis : keep);
+  uint32_t key[TS_G][4];
+  load_chunk_keys(scores + (size_t)row * stride, L, base, (stride & 3) == 0, vis_only, key);
+  // leave the row's histogram zero for the next call (each chunk clears its share; every topk_chunk_kernel
+  // workgroup has read it)
+  int* hrow = hist + (size_t)row * TK_HBINS;
+  for (int i = chunk * TS_THREADS + t; i < TK_HBINS; i += nchunks * TS_THREADS) hrow[i] = 0;
+  __syncthreads();
+  const int c0 = sh.c0, nvis = sh.nvis;
+  uint32_t T = 0;
+  int room = 0;
+  if (c0 >= 0 && nvis > keep) {
+    const uint32_t* crow = ckey + (size_t)row * TS_MAXCH * TS_CHUNK;
+    uint32_t lo = (uint32_t)c0 << TK_HSHIFT;
+    int need = keep - sh.above0;
+    if (sh.maxc <= TS_THREADS) {
+      // fast path: thread t holds the t-th candidate of every chunk (one round of 16 independent loads)
+      uint32_t v[TS_MAXCH];
+#pragma unroll
+      for (int j = 0; j < TS_MAXCH; ++j) v[j] = (j < nchunks && t < sh.nc[j]) ? crow[j * TS_CHUNK + t] : 0u;
+#pragma unroll
+      for (int pass = 0; pass < 2; ++pass) {
+        constexpr int SB = TK_HSHIFT - TK_BITS;
+        const int nb = pass == 0 ? TK_BINS : (1 << SB);
+        for (int i = t; i < nb; i += TS_THREADS) sh.hist[i] = 0;
+        __syncthreads();
+        const uint32_t width = pass == 0 ? (1u << TK_HSHIFT) : (1u << SB);
+#pragma unroll
+        for (int j = 0; j < TS_MAXCH; ++j) {
+          const uint32_t d = v[j] - lo;
+          if (v[j] != 0u && d < width) atomicAdd(&sh.hist[pass == 0 ? (d >> SB) : d], 1);
+        }
+        __syncthreads();
+        if (wave == 0) wave0_find_bin(sh, nb, need);
+        __syncthreads();
+        lo += (uint32_t)sh.sel_c << (pass == 0 ? SB : 0);
+        need -= sh.sel_above;
+        __syncthreads();
+      }
+      T = lo;
+      room = need;
+      // per chunk: candidates above T and tied at T (ballots, one add per wave and chunk)
+#pragma unroll
+      for (int j = 0; j < TS_MAXCH; ++j) {
+        const uint64_t g = __ballot(v[j] != 0u && v[j] > T);
+        const uint64_t q = __ballot(v[j] != 0u && v[j] == T);
+        if (lane == 0 && (g | q)) {
+          atomicAdd(&sh.gt[j], __popcll(g));
+          atomicAdd(&sh.tie[j], __popcll(q));
+        }
+      }
+      __syncthreads();
+    } else {
+      // many keys in one 12-bit bin (ties): the same passes over the lists in global memory
+      for (int pass = 0; pass < 2; ++pass) {
+        constexpr int SB = TK_HSHIFT - TK_BITS;
+        const int nb = pass == 0 ? TK_BINS : (1 << SB);
+        for (int i = t; i < nb; i += TS_THREADS) sh.hist[i] = 0;
+        __syncthreads();
+        const uint32_t width = pass == 0 ? (1u << TK_HSHIFT) : (1u << SB);
+        for (int j = 0; j < nchunks; ++j)
+          for (int i = t; i < sh.nc[j]; i += TS_THREADS) {
+            const uint32_t k = crow[j * TS_CHUNK + i];
+            const uint32_t d = k - lo;
+            if (d < width) atomicAdd(&sh.hist[pass == 0 ? (d >> SB) : d], 1);
+          }
+        __syncthreads();
+        if (wave == 0) wave0_find_bin(sh, nb, need);
+        __syncthreads();
+        lo += (uint32_t)sh.sel_c << (pass == 0 ? SB : 0);
+        need -= sh.sel_above;
+        __syncthreads();
+      }
+      T = lo;
+      room = need;
+      for (int j = 0; j < nchunks; ++j)
+        for (int i = t; i < sh.nc[j]; i += TS_THREADS) {
+          const uint32_t k = crow[j * TS_CHUNK + i];
+          if (k > T) atomicAdd(&sh.gt[j], 1);
+          if (k == T) atomicAdd(&sh.tie[j], 1);
+        }
+      __syncthreads();
+    }
+  }
+  // this chunk's output base and the ties it may take
+  int out_base = 0, ties_before = 0;
+  for (int j = 0; j < chunk && j < nchunks; ++j) {
+    const int na = sh.na[j];
+    int take = room - ties_before;
+    take = take < 0 ? 0 : (take > sh.tie[j] ? sh.tie[j] : take);
+    out_base += na + sh.gt[j] + take;
+    ties_before += sh.tie[j];
+  }
+  int room_here = room - ties_before;
+  room_here = room_here < 0 ? 0 : room_here;
+
+  // ordered output of the chunk: above T, and the first room_here keys equal to T
+  const uint64_t below = lanes_below();
+  uint64_t am[TS_G][4], tm[TS_G][4];
+  uint32_t cnt[TS_G];
+#pragma unroll
+  for (int e = 0; e < TS_G; ++e) {
+    uint32_t na = 0, nt = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      am[e][c] = __ballot(key[e][c] > T);
+      tm[e][c] = __ballot(T != 0 && key[e][c] == T);
+      na += __popcll(am[e][c]);
+      nt += __popcll(tm[e][c]);
+    }
+    cnt[e] = (na << 16) | nt;
+  }
+  uint32_t bb[TS_G];
+  block_bases(cnt, sh.blk, bb);
+  const int cnt_row = nvis < 0 ? 0 : (nvis < keep ? nvis : keep);
   int* orow = idx_out + (size_t)row * keep;
-  int taken = 0;
 #pragma unroll
-  for (int e = 0; e < E; ++e) {
-    const uint32_t k = key[e];
-    const bool tie = T != 0 && k == T && taken < take;
-    taken += tie;
-    if ((k > T || tie) && (unsigned)o < (unsigned)keep) orow[o++] = p0 + e;  // in range whatever the counts
+  for (int e = 0; e < TS_G; ++e) {
+    int a_before = (int)(bb[e] >> 16), t_before = (int)(bb[e] & 0xffffu);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      a_before += __popcll(am[e][c] & below);
+      t_before += __popcll(tm[e][c] & below);
+    }
+    const int p0 = base + 4 * (TS_THREADS * e + t);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const bool a = (am[e][c] >> lane) & 1ull;
+      const bool ti = (tm[e][c] >> lane) & 1ull;
+      const bool sel = a || (ti && t_before < room_here);
+      const int o = out_base + a_before + (t_before < room_here ? t_before : room_here);
+      if (sel && (unsigned)o < (unsigned)keep) orow[o] = p0 + c;  // in range whatever the counts
+      a_before += a;
+      t_before += ti;
+    }
   }
-  for (int i = cnt + t; i < keep; i += TK_THREADS) orow[i] = 0;
-  if (t == 0) cnt_out[row] = cnt;
+  if (chunk == 0) {
+    for (int i = cnt_row + t; i < keep; i += TS_THREADS) orow[i] = 0;
+    if (t == 0) cnt_out[row] = cnt_row;
+  }
 }
 
 // Sub-block maxima of each row: bm[row, j] = max of scores[row, j sub .. j sub + sub - 1] over positions < len.
@@ -324,12 +626,6 @@ __global__ void map_blocks_kernel(int* __restrict__ idx, const int* __restrict__
   }
 }
 
-static int topk_elems(int n) {
-  for (int e = 4; e <= 32; e *= 2)
-    if ((long)e * TK_THREADS >= n) return e;
-  return 0;
-}
-
 // One workgroup per row up to TOPK_FLAT_MAX scores; longer rows are selected in two levels, recursively.
 constexpr int TOPK_FLAT_MAX = 32 * TK_THREADS;
 constexpr int TOPK_LONG_KEEP_MAX = 8192;
@@ -372,8 +668,13 @@ static size_t topk_level_bytes(int B, long n, int keep) {
 
 size_t topk_hist_bytes(int B) { return up256((size_t)B * TK_HBINS * 4); }
 
+// The flat selection's meta and candidate lists (after the histograms).
+static size_t topk_flat_bytes(int B) {
+  return up256((size_t)B * sizeof(RowMeta)) + up256((size_t)B * TS_MAXCH * TS_CHUNK * 4);
+}
+
 size_t topk_workspace_bytes(int B, int max_len, int keep) {
-  return topk_hist_bytes(B) + topk_level_bytes(B, max_len, keep);
+  return topk_hist_bytes(B) + topk_flat_bytes(B) + topk_level_bytes(B, max_len, keep);
 }
 
 bool topk_supported(int max_len, int keep, int vis_only) {
@@ -382,41 +683,41 @@ bool topk_supported(int max_len, int keep, int vis_only) {
   return vis_only && topk_plan(max_len, keep, nullptr);
 }
 
+// The flat selection's buffers inside the top-k workspace: the first-level histograms [B, 4096] (zero between calls),
+// then the per-row meta and the candidate lists.
+struct TopkBuffers {
+  int* hist;
+  RowMeta* meta;
+  uint32_t* ckey;
+};
+
 static hipError_t launch_topk_level(const float* scores, int stride, const int* len, int len_div, int len_mul,
-                                    int max_len, int keep, int vis_only, int* idx, int* cnt, int* hist, bool hist_ready,
-                                    int B, hipStream_t s) {
-  const int E = topk_elems(max_len);
-  if (!E) return hipErrorInvalidValue;
+                                    int max_len, int keep, int vis_only, int* idx, int* cnt, const TopkBuffers& tb,
+                                    bool hist_ready, int B, hipStream_t s) {
+  if (max_len > TS_MAXCH * TS_CHUNK) return hipErrorInvalidValue;
+  const int nch = (max_len + TS_CHUNK - 1) / TS_CHUNK < 1 ? 1 : (max_len + TS_CHUNK - 1) / TS_CHUNK;
   if (!hist_ready) {
-    hipLaunchKernelGGL(topk_hist_kernel, dim3((max_len + TKH_CHUNK - 1) / TKH_CHUNK, B), dim3(TKH_THREADS), 0, s,
-                       scores, stride, len, len_div, len_mul, vis_only, hist);
+    hipLaunchKernelGGL(topk_hist_kernel, dim3(nch, B), dim3(TKH_THREADS), 0, s, scores, stride, len, len_div, len_mul,
+                       vis_only, tb.hist);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-#define TK_CASE(EV)                                                                                             \
-  case EV:                                                                                                      \
-    hipLaunchKernelGGL(topk_select_kernel<EV>, dim3(B), dim3(TK_THREADS), 0, s, scores, stride, len, len_div,   \
-                       len_mul, keep, vis_only, hist, idx, cnt);                                                \
-    break;
-  switch (E) {
-    TK_CASE(4)
-    TK_CASE(8)
-    TK_CASE(16)
-    TK_CASE(32)
-    default:
-      return hipErrorInvalidValue;
-  }
-#undef TK_CASE
+  hipLaunchKernelGGL(topk_chunk_kernel, dim3(nch, B), dim3(TS_THREADS), 0, s, scores, stride, len, len_div, len_mul,
+                     keep, vis_only, tb.hist, tb.meta, tb.ckey);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(topk_output_kernel, dim3(nch, B), dim3(TS_THREADS), 0, s, scores, stride, len, len_div, len_mul,
+                     keep, vis_only, nch, tb.hist, tb.meta, tb.ckey, idx, cnt);
   return hipGetLastError();
 }
 
 // Selection over rows of `stride` scores whose lengths are len[row] (len_div / len_mul as in topk_kernel), n an upper
 // bound of the lengths.
 static hipError_t topk_rows(const float* scores, int stride, const int* len, int len_div, int len_mul, long n,
-                            int keep, int vis_only, int* idx, int* cnt, int* hist, bool hist_ready, char* ws, int B,
-                            hipStream_t s) {
+                            int keep, int vis_only, int* idx, int* cnt, const TopkBuffers& tb, bool hist_ready,
+                            char* ws, int B, hipStream_t s) {
   if (n <= TOPK_FLAT_MAX)
-    return launch_topk_level(scores, stride, len, len_div, len_mul, (int)n, keep, vis_only, idx, cnt, hist,
+    return launch_topk_level(scores, stride, len, len_div, len_mul, (int)n, keep, vis_only, idx, cnt, tb,
                              hist_ready, B, s);
   if (len_div != 1 || len_mul != 1) return hipErrorInvalidValue;  // only flat rows are split
   const int sub = topk_sub_block(n, keep);
@@ -434,14 +735,14 @@ static hipError_t topk_rows(const float* scores, int stride, const int* len, int
   if (e != hipSuccess) return e;
   // level 1: the top-keep sub-blocks (ceil(len / sub) maxima per row)
   if (nb > TOPK_FLAT_MAX) return hipErrorInvalidValue;  // excluded by topk_plan
-  e = launch_topk_level(bm, nb, len, sub, 1, nb, keep, vis_only, bidx, bcnt, hist, false, B, s);
+  e = launch_topk_level(bm, nb, len, sub, 1, nb, keep, vis_only, bidx, bcnt, tb, false, B, s);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(gather_blocks_kernel, dim3((nc + 255) / 256, B), dim3(256), 0, s, scores, stride, len, sub, bidx,
                      bcnt, keep, cand);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   // level 2: the top-keep of the selected sub-blocks' scores in position order (NEG_INF past their count)
-  e = topk_rows(cand, nc, nullptr, 1, 1, nc, keep, vis_only, idx, cnt, hist, false, ws, B, s);
+  e = topk_rows(cand, nc, nullptr, 1, 1, nc, keep, vis_only, idx, cnt, tb, false, ws, B, s);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(map_blocks_kernel, dim3((keep + 255) / 256, B), dim3(256), 0, s, idx, cnt, bidx, sub, keep);
   return hipGetLastError();
@@ -452,10 +753,15 @@ static hipError_t topk_rows(const float* scores, int stride, const int* len, int
 hipError_t launch_topk(const float* scores, const int* len, int* idx, int* cnt, void* ws, int B, int stride,
                        int max_len, int keep, int vis_only, bool hist_ready, hipStream_t s) {
   char* p = static_cast<char*>(ws);
-  int* hist = reinterpret_cast<int*>(p);
   if (hist_ready && max_len > TOPK_FLAT_MAX) return hipErrorInvalidValue;  // the indexer histograms flat rows only
-  return topk_rows(scores, stride, len, 1, 1, max_len, keep, vis_only, idx, cnt, hist, hist_ready,
-                   p + topk_hist_bytes(B), B, s);
+  TopkBuffers tb;
+  tb.hist = reinterpret_cast<int*>(p);
+  p += topk_hist_bytes(B);
+  tb.meta = reinterpret_cast<RowMeta*>(p);
+  p += up256((size_t)B * sizeof(RowMeta));
+  tb.ckey = reinterpret_cast<uint32_t*>(p);
+  p += up256((size_t)B * TS_MAXCH * TS_CHUNK * 4);
+  return topk_rows(scores, stride, len, 1, 1, max_len, keep, vis_only, idx, cnt, tb, hist_ready, p, B, s);
 }
 
 // Zero-fills a workspace (a kernel, not a memset, so that callers may capture it in a graph).
