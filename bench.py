@@ -11,6 +11,11 @@ bytes per launch over its HIP-event-timed average duration) and the CPU baseline
 the reference arithmetic, timed on this host's cores on a bounded sample of the same workload).
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--config 2] [--no-cpu-baseline]
+    python bench.py --copy-probe 512    # plain device copies of 512 MiB: the calibration run for HBM counters
+
+roofline.traffic (HBM bytes per indexer launch) comes from rocprofv3 FETCH_SIZE / WRITE_SIZE counter runs of this
+script, each scaled by the same counter's reading for the --copy-probe kernels; the measured figures are kept in
+profiles/traffic.json and reported when they were taken on the same workload.
 """
 
 from __future__ import annotations
@@ -26,6 +31,37 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def copy_probe(mib: int) -> int:
+    """Device-to-device copies of known size for calibrating the HBM byte counters: torch's copy_ of mib MiB and an
+    elementwise kernel of the same size (neg, fp32), 5 launches each; each reads and writes mib MiB."""
+    import torch
+
+    n = mib * (1 << 20) // 4
+    src = torch.randn(n, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    for _ in range(5):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes_read": n * 4, "copy_probe_bytes_written": n * 4, "launches": 5}), flush=True)
+    return 0
+
+
+def measured_traffic(workload: str, kernel: str):
+    """HBM bytes per launch of `kernel` on `workload` from profiles/traffic.json (counter runs), or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            rec = json.load(f)
+    except (OSError, ValueError):
+        return None
+    ent = rec.get(kernel)
+    if not ent or ent.get("workload") != workload:
+        return None
+    return ent.get("bytes_per_launch")
 
 
 def _indexer_bytes(lengths, Hi, page_size=64):
@@ -51,7 +87,7 @@ def cpu_baseline(inp, budget_s: float = 15.0) -> dict:
         O.decode_layer_ref(cpu)
         n += 1
         dt = time.perf_counter() - t0
-        if dt >= budget_s or n >= 50:
+        if dt >= budget_s or n >= 5000:
             break
     model = ""
     try:
@@ -66,6 +102,47 @@ def cpu_baseline(inp, budget_s: float = 15.0) -> dict:
                       f"{dt:.1f} s, {cores} threads on {model or 'the host CPU'})"}
 
 
+def kernel_times(lib, step, steps: int, pairs: int = 16) -> dict:
+    """{kernel name: average device duration in us} of the kernels one call of step() launches, each timed by a
+    pair of HIP events that the runtime records at the kernel's own start and end (dsa_timing_begin)."""
+    import ctypes
+
+    import torch
+
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+    hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+    hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+    evs = []
+    for _ in range(2 * pairs * steps):
+        e = ctypes.c_void_p()
+        if hip.hipEventCreate(ctypes.byref(e)) != 0:
+            raise RuntimeError("hipEventCreate failed")
+        evs.append(e)
+    arrs = [(ctypes.c_void_p * (2 * pairs))(*[e.value for e in evs[2 * pairs * i: 2 * pairs * (i + 1)]])
+            for i in range(steps)]
+    names, n = [], 0
+    for i in range(steps):
+        lib.dsa_timing_begin(arrs[i], pairs)
+        try:
+            step()
+        finally:
+            n = lib.dsa_timing_end()
+        if i == 0:
+            names = [lib.dsa_timing_kernel_name(k).decode() for k in range(min(n, pairs))]
+    torch.cuda.synchronize()
+    tot: dict = {}
+    ms = ctypes.c_float()
+    for i in range(steps):
+        for k, name in enumerate(names):
+            if hip.hipEventElapsedTime(ctypes.byref(ms), arrs[i][2 * k], arrs[i][2 * k + 1]) != 0:
+                raise RuntimeError("hipEventElapsedTime failed")
+            tot[name] = tot.get(name, 0.0) + ms.value * 1e3
+    for e in evs:
+        hip.hipEventDestroy(e.value)
+    return {k: v / steps for k, v in tot.items()}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -74,17 +151,19 @@ def main() -> int:
     ap.add_argument("--config", type=int, default=2)
     ap.add_argument("--splits", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this path runs on one GPU; --gpus {args.gpus} is not supported (each sequence's decode is "
               f"independent, so N GPUs would run N independent batches)", file=sys.stderr)
         return 2
+    if args.copy_probe:
+        return copy_probe(args.copy_probe)
 
     import torch
 
     from trnrt_amd import _lib
     from trnrt_amd import workloads as W
-    from trnrt_amd.kernels import _common as C
     from trnrt_amd.kernels.dsa_layer import DecodeLayer
 
     cfg = W.CONFIGS[args.config]
@@ -95,8 +174,6 @@ def main() -> int:
                         max_len=max(inp.lengths), splits=args.splits, device=dev)
     g = inp
     lib = _lib.lib()
-    stream = torch.cuda.current_stream(dev)
-    sp = stream.cuda_stream
 
     def step():
         layer.step(g.q_idx, g.w_k, g.k_cache, g.k_scale, g.q, g.kv_cache, g.kv_scale, g.table, g.ctx_len,
@@ -114,42 +191,18 @@ def main() -> int:
     dt = time.perf_counter() - t0
     ms = dt * 1e3 / args.steps
 
-    # per-kernel HIP events on the launch stream over the same number of steps, the three operators called one by
-    # one (the same kernels dsa_decode_layer enqueues)
-    stride = layer.stride
-    ws = layer.workspace
-    from trnrt_amd._lib import workspace_bytes
-
-    t_need = workspace_bytes(_lib.DSA_WS_TOPK, cfg.B, cfg.H, cfg.keep, layer.max_len)
-    t_need = (t_need + 255) // 256 * 256
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
-    for i in range(args.steps):
-        e = evs[i]
-        e[0].record(stream)
-        st = lib.dsa_indexer_decode(g.q_idx.data_ptr(), g.w_k.data_ptr(), g.k_cache.data_ptr(), g.k_scale.data_ptr(),
-                                    g.table.data_ptr(), g.ctx_len.data_ptr(), None, layer.scores.data_ptr(), cfg.B,
-                                    cfg.Hi, 128, inp.max_pages, cfg.page_size, inp.num_pages, stride, sp)
-        e[1].record(stream)
-        st |= lib.dsa_topk(layer.scores.data_ptr(), g.ctx_len.data_ptr(), layer.idx.data_ptr(), layer.cnt.data_ptr(),
-                           ws.data_ptr(), t_need, cfg.B, stride, layer.max_len, cfg.keep, 1, sp)
-        e[2].record(stream)
-        st |= lib.dsa_sparse_mla_decode(g.q.data_ptr(), g.kv_cache.data_ptr(), g.kv_scale.data_ptr(),
-                                        layer.idx.data_ptr(), layer.cnt.data_ptr(), g.table.data_ptr(), None, None,
-                                        layer.out.data_ptr(), None, layer.lse.data_ptr(), ws.data_ptr() + t_need,
-                                        ws.numel() - t_need, cfg.B, cfg.H, 576, 512, cfg.keep, inp.max_pages,
-                                        cfg.page_size, inp.num_pages, cfg.scale, args.splits, sp)
-        e[3].record(stream)
-        if st:
-            raise RuntimeError(f"launch status {st}")
-    torch.cuda.synchronize()
-    k_ms = [sum(e[j].elapsed_time(e[j + 1]) for e in evs) / args.steps for j in range(3)]
+    # per-kernel device durations inside the same layer-step: HIP events recorded by the runtime at each kernel's own
+    # start and end (hipExtLaunchKernel on the launch stream), over another `steps` steps
+    k_us = kernel_times(lib, step, args.steps)
 
     lengths = inp.lengths
     idx_bytes = _indexer_bytes(lengths, cfg.Hi, cfg.page_size)
-    achieved = idx_bytes / (k_ms[0] * 1e-3) / 1e9
+    idx_us = k_us["indexer_decode_kernel"]
+    achieved = idx_bytes / (idx_us * 1e-6) / 1e9
     layer_bytes = W.algorithmic_bytes(lengths, cfg.H, cfg.Hi, cfg.keep, cfg.page_size)
     layer_gbs = layer_bytes / (ms * 1e-3) / 1e9
 
+    workload = f"config {args.config}: {cfg.name}"
     out = {
         "metric": "DSA decode layer-steps/sec at B=8, 32K ctx; achieved HBM GB/s (% of 8 TB/s)",
         "value": round(1e3 / ms, 1),
@@ -163,16 +216,17 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": f"config {args.config}: {cfg.name}", "batch": cfg.B, "context": max(lengths),
+        "config": {"workload": workload, "batch": cfg.B, "context": max(lengths),
                    "q_heads": cfg.H, "indexer_heads": cfg.Hi, "keep": cfg.keep, "page_size": cfg.page_size,
                    "kv": "fp8 e4m3 [576] + fp32 scale per token", "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "kernel": "indexer_decode_kernel", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "algorithmic_bytes": idx_bytes, "avg_ms": round(k_ms[0], 5)},
+                     "traffic": measured_traffic(workload, "indexer_decode_kernel"), "algorithmic_bytes": idx_bytes,
+                     "avg_us": round(idx_us, 3)},
         "layer": {"algorithmic_bytes": layer_bytes, "achieved_GBs": round(layer_gbs, 1),
                   "frac": round(layer_gbs / HBM_PEAK_GBS, 4),
-                  "kernel_ms": {"indexer": round(k_ms[0], 5), "topk": round(k_ms[1], 5),
-                                "attention": round(k_ms[2], 5)}},
+                  "kernel_us": {k: round(v, 3) for k, v in k_us.items()},
+                  "launch_gaps_us": round(ms * 1e3 - sum(k_us.values()), 3)},
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(inp)

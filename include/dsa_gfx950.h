@@ -136,6 +136,17 @@ size_t dsa_workspace_bytes(int kind, int B, int H, int keep, int max_len, int sp
 /* The split count dsa_sparse_mla_decode uses for splits = 0. */
 int dsa_default_splits(int B, int H, int keep);
 
+/*
+ * Kernel timing for benchmarks (no counterpart in the reference, whose kernels are timed by the Neuron profiler).
+ * Between dsa_timing_begin and dsa_timing_end on one host thread, the k-th kernel the library launches records
+ * events[2k] and events[2k+1] (hipEvent_t values created by the caller) at the kernel's own start and end, for
+ * k < pairs; dsa_timing_end returns how many kernels were launched and dsa_timing_kernel_name(k) names the k-th
+ * (valid until the next dsa_timing_begin on the thread).
+ */
+int dsa_timing_begin(void* const* events, int pairs);
+int dsa_timing_end(void);
+const char* dsa_timing_kernel_name(int k);
+
 #ifdef __cplusplus
 }
 #endif

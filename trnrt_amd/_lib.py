@@ -48,6 +48,9 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "dsa_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int]),
     "dsa_default_splits": (c_int, [c_int, c_int, c_int]),
+    "dsa_timing_begin": (c_int, [P, c_int]),
+    "dsa_timing_end": (c_int, []),
+    "dsa_timing_kernel_name": (ctypes.c_char_p, [c_int]),
 }
 
 _lib = None

@@ -23,9 +23,13 @@ hipError_t launch_token_rows(const int* idx, const int* cnt, const int* table, i
                              int keep, int max_pages, int page_size, int num_pages, hipStream_t s);
 int attention_default_splits(int B, int H, int keep, int num_cu);
 size_t attention_workspace_bytes(int B, int H, int splits);
+
+thread_local KernelTimer* g_kernel_timer = nullptr;
 }  // namespace dsa
 
 namespace {
+
+thread_local dsa::KernelTimer t_timer;
 
 int num_cu() {
   int dev = 0, n = 0;
@@ -57,6 +61,27 @@ int effective_splits(int splits, int keep) {
 extern "C" {
 
 int dsa_abi_version(void) { return DSA_ABI_VERSION; }
+
+int dsa_timing_begin(void* const* events, int pairs) {
+  if (pairs < 0 || (pairs > 0 && !events)) return DSA_EINVAL;
+  t_timer.events = reinterpret_cast<hipEvent_t*>(const_cast<void**>(events));
+  t_timer.pairs = pairs;
+  t_timer.launched = 0;
+  for (const char*& n : t_timer.names) n = nullptr;
+  dsa::g_kernel_timer = &t_timer;
+  return DSA_OK;
+}
+
+int dsa_timing_end(void) {
+  if (!dsa::g_kernel_timer) return 0;
+  dsa::g_kernel_timer = nullptr;
+  return t_timer.launched;
+}
+
+const char* dsa_timing_kernel_name(int k) {
+  if (k < 0 || k >= 32 || k >= t_timer.launched || !t_timer.names[k]) return "";
+  return t_timer.names[k];
+}
 
 const char* dsa_strerror(int s) {
   switch (s) {

@@ -368,26 +368,26 @@ hipError_t launch_sparse_mla(const uint16_t* q, const uint8_t* kv, const float* 
     ws_o = static_cast<float*>(ws);
     ws_ml = ws_o + (size_t)B * eff_splits * H * ATT_DV;  // [B, splits, H, 2]: max, sum
   }
-  hipLaunchKernelGGL(sparse_mla_kernel, dim3(grid), dim3(ATT_THREADS), 0, s, q, kv, kvs, idx, cnt, table, rows, bias,
+  launch("sparse_mla_kernel", sparse_mla_kernel, dim3(grid), dim3(ATT_THREADS), s, q, kv, kvs, idx, cnt, table, rows, bias,
                      out, out_f32, lse, ws_o, ws_ml, B, H, keep, max_pages, page_size, num_pages, scale, eff_splits,
                      sps);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || eff_splits == 1) return e;
   if (eff_splits <= 8)
-    hipLaunchKernelGGL(combine_splits_kernel<8>, dim3(B * H), dim3(128), 0, s, ws_o, ws_ml, H, eff_splits, out,
+    launch("combine_splits_kernel", combine_splits_kernel<8>, dim3(B * H), dim3(128), s, ws_o, ws_ml, H, eff_splits, out,
                        out_f32, lse);
   else if (eff_splits <= 16)
-    hipLaunchKernelGGL(combine_splits_kernel<16>, dim3(B * H), dim3(128), 0, s, ws_o, ws_ml, H, eff_splits, out,
+    launch("combine_splits_kernel", combine_splits_kernel<16>, dim3(B * H), dim3(128), s, ws_o, ws_ml, H, eff_splits, out,
                        out_f32, lse);
   else
-    hipLaunchKernelGGL(combine_splits_kernel<32>, dim3(B * H), dim3(128), 0, s, ws_o, ws_ml, H, eff_splits, out,
+    launch("combine_splits_kernel", combine_splits_kernel<32>, dim3(B * H), dim3(128), s, ws_o, ws_ml, H, eff_splits, out,
                        out_f32, lse);
   return hipGetLastError();
 }
 
 hipError_t launch_token_rows(const int* idx, const int* cnt, const int* table, int* rows, float* bias, int B,
                              int keep, int max_pages, int page_size, int num_pages, hipStream_t s) {
-  hipLaunchKernelGGL(token_rows_kernel, dim3((keep + 255) / 256, B), dim3(256), 0, s, idx, cnt, table, rows, bias,
+  launch("token_rows_kernel", token_rows_kernel, dim3((keep + 255) / 256, B), dim3(256), s, idx, cnt, table, rows, bias,
                      keep, max_pages, page_size, num_pages);
   return hipGetLastError();
 }

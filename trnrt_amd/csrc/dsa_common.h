@@ -2,10 +2,40 @@
 // bf16 conversion, the order-preserving integer key of an fp32 score, and wave/block reductions for wave64.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 namespace dsa {
+
+// Kernel timing for benchmarks: while a KernelTimer is installed on the calling host thread, every kernel this
+// library launches takes the next pair of its events, recorded by the runtime at the kernel's own start and end
+// (hipExtLaunchKernel), and its name; launches past the supplied pairs are counted but not timed.
+struct KernelTimer {
+  hipEvent_t* events;  // 2 * pairs events, created by the caller
+  int pairs;
+  int launched;
+  const char* names[32];
+};
+extern thread_local KernelTimer* g_kernel_timer;
+
+// Launches kernel<<<grid, block, 0, s>>>(args...) (through hipExtLaunchKernel, so an installed KernelTimer can
+// time it). Returns the launch status.
+template <typename F, typename... Args>
+inline hipError_t launch(const char* name, F kernel, dim3 grid, dim3 block, hipStream_t s, Args... args) {
+  KernelTimer* t = g_kernel_timer;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  if (t) {
+    if (t->launched < t->pairs) {
+      e0 = t->events[2 * t->launched];
+      e1 = t->events[2 * t->launched + 1];
+    }
+    if (t->launched < 32) t->names[t->launched] = name;
+    ++t->launched;
+  }
+  hipExtLaunchKernelGGL(kernel, grid, block, 0, s, e0, e1, 0, args...);
+  return hipGetLastError();
+}
 
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
 typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;

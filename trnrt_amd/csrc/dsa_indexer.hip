@@ -35,8 +35,9 @@ struct KeyTile {
 
 // MT: query-head tiles of 32 (Hi <= 32 MT). Each wave scores `tiles_per_wave` consecutive 32-key tiles of one row,
 // keeping IDX_PF tiles' loads in flight: a tile's buffer is refilled with the tile IDX_PF ahead as soon as its MFMAs
-// have consumed it. The row's queries and head weights are staged once per workgroup in LDS.
-template <int MT>
+// have consumed it. The row's queries and head weights are staged once per workgroup in LDS. HIST: also accumulate
+// the row's first-level top-k histogram into hist.
+template <int MT, bool HIST>
 __global__ __launch_bounds__(IDX_THREADS, 2) void indexer_decode_kernel(
     const uint16_t* __restrict__ q, const float* __restrict__ w, const uint8_t* __restrict__ kcache,
     const float* __restrict__ kscale, const int* __restrict__ table, const int* __restrict__ ctx_len,
@@ -44,7 +45,7 @@ __global__ __launch_bounds__(IDX_THREADS, 2) void indexer_decode_kernel(
     int page_size, int num_pages, int stride, int tiles_per_wave, int chunks_per_row) {
   __shared__ uint16_t qs[32 * MT * IDX_QROW];
   __shared__ float ws[32 * MT];
-  __shared__ int hs[IDX_HBINS];  // the workgroup's share of the row's top-k histogram (when hist != null)
+  __shared__ int hs[HIST ? IDX_HBINS : 1];  // the workgroup's share of the row's top-k histogram
   const int b = blockIdx.x / chunks_per_row;
   const int chunk = blockIdx.x - b * chunks_per_row;
   const int wave = threadIdx.x / WAVE;
@@ -85,7 +86,7 @@ __global__ __launch_bounds__(IDX_THREADS, 2) void indexer_decode_kernel(
     *reinterpret_cast<uint4*>(&qs[head * IDX_QROW + 8 * c]) = v;
   }
   for (int i = threadIdx.x; i < 32 * MT; i += IDX_THREADS) ws[i] = i < Hi ? w[(size_t)b * Hi + i] : 0.0f;
-  if (hist)
+  if (HIST)
     for (int i = threadIdx.x; i < IDX_HBINS; i += IDX_THREADS) hs[i] = 0;
   __syncthreads();
 
@@ -141,12 +142,12 @@ __global__ __launch_bounds__(IDX_THREADS, 2) void indexer_decode_kernel(
         }
         if (h == 0 && pos < stride) {
           srow[pos] = v;
-          if (hist && v > VISIBLE) atomicAdd(&hs[order_key(v) >> IDX_HSHIFT], 1);
+          if (HIST && v > VISIBLE) atomicAdd(&hs[order_key(v) >> IDX_HSHIFT], 1);
         }
       }
     }
   }
-  if (hist) {
+  if (HIST) {
     // the row's first-level top-k histogram (top 12 bits of the order key of the selectable scores)
     __syncthreads();
     int* hrow = hist + (size_t)b * IDX_HBINS;
@@ -165,9 +166,14 @@ static hipError_t launch_indexer_mt(const uint16_t* q, const float* w, const uin
   const int tiles_row = (stride + IDX_TILE - 1) / IDX_TILE;
   const int waves_row = (tiles_row + tiles_per_wave - 1) / tiles_per_wave;
   const int chunks_row = (waves_row + IDX_WAVES - 1) / IDX_WAVES;
-  hipLaunchKernelGGL(indexer_decode_kernel<MT>, dim3(B * chunks_row), dim3(IDX_THREADS), 0, stream, q, w, k, ks,
-                     table, ctx_len, cand, scores, hist, Hi, max_pages, page_size, num_pages, stride,
-                     tiles_per_wave, chunks_row);
+  if (hist)
+    launch("indexer_decode_kernel", (indexer_decode_kernel<MT, true>), dim3(B * chunks_row), dim3(IDX_THREADS), stream, q, w,
+                       k, ks, table, ctx_len, cand, scores, hist, Hi, max_pages, page_size, num_pages, stride,
+                       tiles_per_wave, chunks_row);
+  else
+    launch("indexer_decode_kernel", (indexer_decode_kernel<MT, false>), dim3(B * chunks_row), dim3(IDX_THREADS), stream, q, w,
+                       k, ks, table, ctx_len, cand, scores, hist, Hi, max_pages, page_size, num_pages, stride,
+                       tiles_per_wave, chunks_row);
   return hipGetLastError();
 }
 

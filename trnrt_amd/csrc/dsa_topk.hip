@@ -697,16 +697,16 @@ static hipError_t launch_topk_level(const float* scores, int stride, const int* 
   if (max_len > TS_MAXCH * TS_CHUNK) return hipErrorInvalidValue;
   const int nch = (max_len + TS_CHUNK - 1) / TS_CHUNK < 1 ? 1 : (max_len + TS_CHUNK - 1) / TS_CHUNK;
   if (!hist_ready) {
-    hipLaunchKernelGGL(topk_hist_kernel, dim3(nch, B), dim3(TKH_THREADS), 0, s, scores, stride, len, len_div, len_mul,
+    launch("topk_hist_kernel", topk_hist_kernel, dim3(nch, B), dim3(TKH_THREADS), s, scores, stride, len, len_div, len_mul,
                        vis_only, tb.hist);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(topk_chunk_kernel, dim3(nch, B), dim3(TS_THREADS), 0, s, scores, stride, len, len_div, len_mul,
+  launch("topk_chunk_kernel", topk_chunk_kernel, dim3(nch, B), dim3(TS_THREADS), s, scores, stride, len, len_div, len_mul,
                      keep, vis_only, tb.hist, tb.meta, tb.ckey);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(topk_output_kernel, dim3(nch, B), dim3(TS_THREADS), 0, s, scores, stride, len, len_div, len_mul,
+  launch("topk_output_kernel", topk_output_kernel, dim3(nch, B), dim3(TS_THREADS), s, scores, stride, len, len_div, len_mul,
                      keep, vis_only, nch, tb.hist, tb.meta, tb.ckey, idx, cnt);
   return hipGetLastError();
 }
@@ -730,21 +730,21 @@ static hipError_t topk_rows(const float* scores, int stride, const int* len, int
   ws += up256((size_t)B * 4);
   float* cand = reinterpret_cast<float*>(ws);
   ws += up256((size_t)B * nc * 4);
-  hipLaunchKernelGGL(block_max_kernel, dim3((nb + 255) / 256, B), dim3(256), 0, s, scores, stride, len, sub, nb, bm);
+  launch("block_max_kernel", block_max_kernel, dim3((nb + 255) / 256, B), dim3(256), s, scores, stride, len, sub, nb, bm);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   // level 1: the top-keep sub-blocks (ceil(len / sub) maxima per row)
   if (nb > TOPK_FLAT_MAX) return hipErrorInvalidValue;  // excluded by topk_plan
   e = launch_topk_level(bm, nb, len, sub, 1, nb, keep, vis_only, bidx, bcnt, tb, false, B, s);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(gather_blocks_kernel, dim3((nc + 255) / 256, B), dim3(256), 0, s, scores, stride, len, sub, bidx,
+  launch("gather_blocks_kernel", gather_blocks_kernel, dim3((nc + 255) / 256, B), dim3(256), s, scores, stride, len, sub, bidx,
                      bcnt, keep, cand);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   // level 2: the top-keep of the selected sub-blocks' scores in position order (NEG_INF past their count)
   e = topk_rows(cand, nc, nullptr, 1, 1, nc, keep, vis_only, idx, cnt, tb, false, ws, B, s);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(map_blocks_kernel, dim3((keep + 255) / 256, B), dim3(256), 0, s, idx, cnt, bidx, sub, keep);
+  launch("map_blocks_kernel", map_blocks_kernel, dim3((keep + 255) / 256, B), dim3(256), s, idx, cnt, bidx, sub, keep);
   return hipGetLastError();
 }
 
@@ -774,16 +774,16 @@ hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t s) {
   const size_t n16 = bytes / 16;
   if (n16) {
     const int grid = (int)((n16 + 255) / 256 < 4096 ? (n16 + 255) / 256 : 4096);
-    hipLaunchKernelGGL(fill_zero_kernel, dim3(grid), dim3(256), 0, s, static_cast<uint4*>(p), n16);
+    launch("fill_zero_kernel", fill_zero_kernel, dim3(grid), dim3(256), s, static_cast<uint4*>(p), n16);
   }
   return hipGetLastError();
 }
 
 hipError_t launch_topk_mask(const int* idx, const int* cnt, float* mask, int B, int keep, int P, hipStream_t s) {
-  hipLaunchKernelGGL(topk_mask_fill_kernel, dim3((P + 255) / 256, B), dim3(256), 0, s, mask, P);
+  launch("topk_mask_fill_kernel", topk_mask_fill_kernel, dim3((P + 255) / 256, B), dim3(256), s, mask, P);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(topk_mask_scatter_kernel, dim3((keep + 255) / 256, B), dim3(256), 0, s, idx, cnt, mask, keep,
+  launch("topk_mask_scatter_kernel", topk_mask_scatter_kernel, dim3((keep + 255) / 256, B), dim3(256), s, idx, cnt, mask, keep,
                      P);
   return hipGetLastError();
 }
