@@ -93,40 +93,83 @@ __device__ __forceinline__ float key_to_float(uint32_t k) {
   return __uint_as_float(u);
 }
 
-template <typename T>
-__device__ __forceinline__ T wave_sum(T v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, WAVE);
-  return v;
+// Cross-lane steps by DPP (data parallel primitives: a lane reads a neighbour's register in the same VALU
+// instruction), which cost a few cycles where an LDS-routed shuffle costs a round trip through the LDS pipeline.
+// Controls (GFX9): quad_perm [1,0,3,2] = 0xb1, [2,3,0,1] = 0x4e; row_shr:n = 0x110 + n; row_mirror = 0x140,
+// row_half_mirror = 0x141; row_bcast:15 = 0x142, row_bcast:31 = 0x143.
+template <int CTRL, int ROW_MASK = 0xf, bool BOUND_ZERO = true>
+__device__ __forceinline__ int dpp(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xf, BOUND_ZERO);
+}
+
+// Inclusive prefix sum over the 64 lanes (wrapping uint32 sums, so packed counters add field-wise): Hillis-Steele
+// within each row of 16 lanes, then row 0's total into row 1 and row 2's into row 3 (row_bcast:15), then rows 0-1's
+// total into rows 2-3 (row_bcast:31). Lanes a DPP step does not write add the old value 0.
+__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {
+  int x = (int)v;
+  x += dpp<0x111>(x);
+  x += dpp<0x112>(x);
+  x += dpp<0x114>(x);
+  x += dpp<0x118>(x);
+  x += dpp<0x142, 0xa, false>(x);
+  x += dpp<0x143, 0xc, false>(x);
+  return (uint32_t)x;
+}
+
+__device__ __forceinline__ int wave_incl_scan(int v) { return (int)wave_incl_scan_u32((uint32_t)v); }
+
+// Wave-wide sum, the same value in every lane (the last lane of the inclusive scan).
+__device__ __forceinline__ int wave_sum(int v) {
+  return __builtin_amdgcn_readlane((int)wave_incl_scan_u32((uint32_t)v), WAVE - 1);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  // within rows: quad swaps, half-row and row mirrors; then the four rows' sums
+  v += __int_as_float(dpp<0xb1>(__float_as_int(v)));
+  v += __int_as_float(dpp<0x4e>(__float_as_int(v)));
+  v += __int_as_float(dpp<0x141>(__float_as_int(v)));
+  v += __int_as_float(dpp<0x140>(__float_as_int(v)));
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (r0 + r1) + (r2 + r3);
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
-  return v;
+  v = fmaxf(v, __int_as_float(dpp<0xb1>(__float_as_int(v))));
+  v = fmaxf(v, __int_as_float(dpp<0x4e>(__float_as_int(v))));
+  v = fmaxf(v, __int_as_float(dpp<0x141>(__float_as_int(v))));
+  v = fmaxf(v, __int_as_float(dpp<0x140>(__float_as_int(v))));
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o, WAVE));
-  return v;
+  v = max(v, (uint32_t)dpp<0xb1>((int)v));
+  v = max(v, (uint32_t)dpp<0x4e>((int)v));
+  v = max(v, (uint32_t)dpp<0x141>((int)v));
+  v = max(v, (uint32_t)dpp<0x140>((int)v));
+  const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+  const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+  const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
+  const uint32_t r3 = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+  return max(max(r0, r1), max(r2, r3));
 }
 
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = min(v, (uint32_t)__shfl_xor((int)v, o, WAVE));
-  return v;
-}
-
-// Inclusive prefix sum over the 64 lanes of a wave.
-__device__ __forceinline__ int wave_incl_scan(int v) {
-  const int lane = threadIdx.x & (WAVE - 1);
-#pragma unroll
-  for (int o = 1; o < WAVE; o <<= 1) {
-    int t = __shfl_up(v, o, WAVE);
-    if (lane >= o) v += t;
-  }
-  return v;
+  v = min(v, (uint32_t)dpp<0xb1>((int)v));
+  v = min(v, (uint32_t)dpp<0x4e>((int)v));
+  v = min(v, (uint32_t)dpp<0x141>((int)v));
+  v = min(v, (uint32_t)dpp<0x140>((int)v));
+  const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+  const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+  const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
+  const uint32_t r3 = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+  return min(min(r0, r1), min(r2, r3));
 }
 
 // Clamp a page id into the cache (an id outside it reads the null page 0 instead of faulting).

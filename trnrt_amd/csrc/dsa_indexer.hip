@@ -23,31 +23,33 @@ constexpr int IDX_D = 128;        // index_head_dim
 constexpr int IDX_TILE = 32;      // keys per MFMA tile
 constexpr int IDX_THREADS = 256;  // 4 waves per workgroup
 constexpr int IDX_WAVES = IDX_THREADS / WAVE;
-constexpr int IDX_PF = 4;         // key tiles in flight per wave (a ring of register buffers)
+constexpr int IDX_TPW = 4;        // key tiles per wave, all loaded up front
+constexpr int IDX_TPG = IDX_TPW * IDX_WAVES;  // key tiles per workgroup
 constexpr int IDX_QROW = IDX_D + 8;  // LDS row stride of the staged queries (bf16 elements; padding spreads banks)
 constexpr int IDX_HSHIFT = 20;       // the top-k kernel's first-level bins: the top 12 bits of the order key
 constexpr int IDX_HBINS = 4096;
 
-struct KeyTile {
-  uint4 v[4];  // 64 key bytes of this lane
-  float scale;
-};
+__device__ __forceinline__ float crow_value(const float* cand, int b, int stride, int pos) {
+  return cand[(size_t)b * stride + pos];
+}
 
-// MT: query-head tiles of 32 (Hi <= 32 MT). Each wave scores `tiles_per_wave` consecutive 32-key tiles of one row,
-// keeping IDX_PF tiles' loads in flight: a tile's buffer is refilled with the tile IDX_PF ahead as soon as its MFMAs
-// have consumed it. The row's queries and head weights are staged once per workgroup in LDS. HIST: also accumulate
-// the row's first-level top-k histogram into hist.
-template <int MT, bool HIST>
+// MT: query-head tiles of 32 (Hi <= 32 MT). Each wave scores IDX_TPW consecutive 32-key tiles of one row as
+// straight-line code: it reads the tiles' page ids (one per lane), issues the loads of all its tiles' key bytes and
+// scales, then computes them in order, so each tile waits only for its own loads. Every load is unconditional (a
+// tile past the context reads the null page and its score is replaced by NEG_INF), which keeps the waits exact. The
+// row's queries and head weights are staged once per workgroup in LDS, their loads issued before the key loads.
+// HIST: also accumulate the row's first-level top-k histogram into hist. CAND: add cand to the scores.
+template <int MT, bool HIST, bool CAND>
 __global__ __launch_bounds__(IDX_THREADS, 2) void indexer_decode_kernel(
     const uint16_t* __restrict__ q, const float* __restrict__ w, const uint8_t* __restrict__ kcache,
     const float* __restrict__ kscale, const int* __restrict__ table, const int* __restrict__ ctx_len,
     const float* __restrict__ cand, float* __restrict__ scores, int* __restrict__ hist, int Hi, int max_pages,
-    int page_size, int num_pages, int stride, int tiles_per_wave, int chunks_per_row) {
+    int page_size, int num_pages, int stride, int groups_per_row) {
   __shared__ uint16_t qs[32 * MT * IDX_QROW];
   __shared__ float ws[32 * MT];
   __shared__ int hs[HIST ? IDX_HBINS : 1];  // the workgroup's share of the row's top-k histogram
-  const int b = blockIdx.x / chunks_per_row;
-  const int chunk = blockIdx.x - b * chunks_per_row;
+  const int b = blockIdx.x / groups_per_row;
+  const int grp = blockIdx.x - b * groups_per_row;
   const int wave = threadIdx.x / WAVE;
   const int lane = threadIdx.x & (WAVE - 1);
   const int j = lane & 31;  // key column of the tile / head row of the query operand
@@ -56,36 +58,52 @@ __global__ __launch_bounds__(IDX_THREADS, 2) void indexer_decode_kernel(
   const int tiles_row = (stride + IDX_TILE - 1) / IDX_TILE;
   int L = stride;
   if (ctx_len) L = min(max(ctx_len[b], 0), stride);
-  const int t_begin = (chunk * IDX_WAVES + wave) * tiles_per_wave;
-  const int t_end = min(t_begin + tiles_per_wave, tiles_row);
+  const int t_begin = grp * IDX_TPG + wave * IDX_TPW;
   const int* trow = table + (size_t)b * max_pages;
+  float* srow = scores + (size_t)b * stride;
 
-  auto load_tile = [&](int t, KeyTile& kt) {
-    const int t0 = t * IDX_TILE;
-    if (t < t_end && t0 < L) {
-      const int page = safe_page(trow[t0 / page_size], num_pages);
-      const size_t slot = (size_t)page * page_size + (t0 % page_size) + j;
-      const uint8_t* kp = kcache + slot * IDX_D + 64 * h;
-      kt.v[0] = load_stream16(kp + 0);
-      kt.v[1] = load_stream16(kp + 16);
-      kt.v[2] = load_stream16(kp + 32);
-      kt.v[3] = load_stream16(kp + 48);
-      kt.scale = kscale[slot];
-    }
-  };
-  // the first tiles' loads go out before the query staging
-  KeyTile buf[IDX_PF];
+  // the queries' loads first (each thread's 16-byte pieces, kept in registers until the LDS write)
+  constexpr int QPT = 32 * MT * (IDX_D / 8) / IDX_THREADS;  // 16-byte query pieces per thread
+  uint4 qv[QPT];
 #pragma unroll
-  for (int i = 0; i < IDX_PF; ++i) load_tile(t_begin + i, buf[i]);
+  for (int r = 0; r < QPT; ++r) {
+    const int i = threadIdx.x + r * IDX_THREADS;
+    const int head = i / (IDX_D / 8), c = i - head * (IDX_D / 8);
+    qv[r] = *reinterpret_cast<const uint4*>(q + ((size_t)b * Hi + min(head, Hi - 1)) * IDX_D + 8 * c);
+  }
+  const float wv = w[(size_t)b * Hi + min((int)threadIdx.x, Hi - 1)];
+
+  // lane i < IDX_TPW: the page of tile t_begin + i (0, the null page, past the context)
+  int pages;
+  {
+    const int t = t_begin + min(lane, IDX_TPW - 1);
+    const int pg = trow[min(t * IDX_TILE / page_size, max_pages - 1)];  // independent of L: issued with its load
+    pages = t * IDX_TILE < L ? safe_page(pg, num_pages) : 0;
+  }
+
+  // every tile's loads: 64 key bytes per lane (key j, dims 64h .. 64h + 63) and the key's scale
+  uint4 kv[IDX_TPW][4];
+  float ksc[IDX_TPW], kc[IDX_TPW];
+#pragma unroll
+  for (int i = 0; i < IDX_TPW; ++i) {
+    const int t0 = (t_begin + i) * IDX_TILE;
+    const int page = __shfl(pages, i, WAVE);
+    const size_t slot = t0 < L ? (size_t)page * page_size + (t0 % page_size) + j : (size_t)j;
+    const uint8_t* kp = kcache + slot * IDX_D + 64 * h;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) kv[i][c] = *reinterpret_cast<const uint4*>(kp + 16 * c);
+    ksc[i] = kscale[slot];
+    if (CAND) kc[i] = crow_value(cand, b, stride, t0 < L ? min(t0 + j, stride - 1) : 0);
+  }
 
   // stage the row's queries (zero rows past Hi) and head weights
-  for (int i = threadIdx.x; i < 32 * MT * (IDX_D / 8); i += IDX_THREADS) {
+#pragma unroll
+  for (int r = 0; r < QPT; ++r) {
+    const int i = threadIdx.x + r * IDX_THREADS;
     const int head = i / (IDX_D / 8), c = i - head * (IDX_D / 8);
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (head < Hi) v = *reinterpret_cast<const uint4*>(q + ((size_t)b * Hi + head) * IDX_D + 8 * c);
-    *reinterpret_cast<uint4*>(&qs[head * IDX_QROW + 8 * c]) = v;
+    *reinterpret_cast<uint4*>(&qs[head * IDX_QROW + 8 * c]) = head < Hi ? qv[r] : make_uint4(0, 0, 0, 0);
   }
-  for (int i = threadIdx.x; i < 32 * MT; i += IDX_THREADS) ws[i] = i < Hi ? w[(size_t)b * Hi + i] : 0.0f;
+  if (threadIdx.x < 32 * MT) ws[threadIdx.x] = (int)threadIdx.x < Hi ? wv : 0.0f;
   if (HIST)
     for (int i = threadIdx.x; i < IDX_HBINS; i += IDX_THREADS) hs[i] = 0;
   __syncthreads();
@@ -104,47 +122,34 @@ __global__ __launch_bounds__(IDX_THREADS, 2) void indexer_decode_kernel(
 #pragma unroll
     for (int r = 0; r < 16; ++r) wr[m][r] = ws[32 * m + 8 * (r >> 2) + 4 * h + (r & 3)];
 
-  float* srow = scores + (size_t)b * stride;
-  const float* crow = cand ? cand + (size_t)b * stride : nullptr;
-  for (int tg = t_begin; tg < t_end; tg += IDX_PF) {  // empty for a wave past the row's tiles
 #pragma unroll
-    for (int i = 0; i < IDX_PF; ++i) {
-      const int t = tg + i;
-      if (t < t_end) {
-        const int t0 = t * IDX_TILE;
-        const int pos = t0 + j;
-        float v = NEG_INF;
-        if (t0 < L) {
-          f32x16 acc[MT];
+  for (int i = 0; i < IDX_TPW; ++i) {
+    const int t = t_begin + i;
+    const int pos = t * IDX_TILE + j;
+    f32x16 acc[MT];
 #pragma unroll
-          for (int m = 0; m < MT; ++m)
+    for (int m = 0; m < MT; ++m)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[m][r] = 0.0f;
+      for (int r = 0; r < 16; ++r) acc[m][r] = 0.0f;
 #pragma unroll
-          for (int s = 0; s < 8; ++s) {
-            const uint4 kv = buf[i].v[s >> 1];
-            const bf16x8 kb = (s & 1) ? fp8x8_to_bf16x8(kv.z, kv.w) : fp8x8_to_bf16x8(kv.x, kv.y);
+    for (int s = 0; s < 8; ++s) {
+      const uint4 k4 = kv[i][s >> 1];
+      const bf16x8 kb = (s & 1) ? fp8x8_to_bf16x8(k4.z, k4.w) : fp8x8_to_bf16x8(k4.x, k4.y);
 #pragma unroll
-            for (int m = 0; m < MT; ++m)
-              acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa[m][s], kb, acc[m], 0, 0, 0);
-          }
-          const float ksc = buf[i].scale;
-          load_tile(t + IDX_PF, buf[i]);  // the buffer's operands are in the MFMA pipeline: refill it
-          float part = 0.0f;
+      for (int m = 0; m < MT; ++m)
+        acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa[m][s], kb, acc[m], 0, 0, 0);
+    }
+    float part = 0.0f;
 #pragma unroll
-          for (int m = 0; m < MT; ++m)
+    for (int m = 0; m < MT; ++m)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) part = fmaf(wr[m][r], fmaxf(acc[m][r], 0.0f), part);
-          part += __shfl_xor(part, 32, WAVE);
-          v = part * ksc;
-          if (crow && pos < stride) v += crow[pos];
-          if (pos >= L) v = NEG_INF;
-        }
-        if (h == 0 && pos < stride) {
-          srow[pos] = v;
-          if (HIST && v > VISIBLE) atomicAdd(&hs[order_key(v) >> IDX_HSHIFT], 1);
-        }
-      }
+      for (int r = 0; r < 16; ++r) part = fmaf(wr[m][r], fmaxf(acc[m][r], 0.0f), part);
+    part += __shfl_xor(part, 32, WAVE);
+    float v = CAND ? part * ksc[i] + kc[i] : part * ksc[i];
+    if (pos >= L) v = NEG_INF;
+    if (t < tiles_row && h == 0 && pos < stride) {
+      srow[pos] = v;
+      if (HIST && v > VISIBLE) atomicAdd(&hs[order_key(v) >> IDX_HSHIFT], 1);
     }
   }
   if (HIST) {
@@ -158,40 +163,46 @@ __global__ __launch_bounds__(IDX_THREADS, 2) void indexer_decode_kernel(
   }
 }
 
+template <int MT, bool HIST, bool CAND>
+static hipError_t launch_indexer_variant(const uint16_t* q, const float* w, const uint8_t* k, const float* ks,
+                                         const int* table, const int* ctx_len, const float* cand, float* scores,
+                                         int* hist, int B, int Hi, int max_pages, int page_size, int num_pages,
+                                         int stride, hipStream_t stream) {
+  const int tiles_row = (stride + IDX_TILE - 1) / IDX_TILE;
+  const int groups_row = (tiles_row + IDX_TPG - 1) / IDX_TPG;
+  return launch("indexer_decode_kernel", indexer_decode_kernel<MT, HIST, CAND>, dim3(B * groups_row),
+                dim3(IDX_THREADS), stream, q, w, k, ks, table, ctx_len, cand, scores, hist, Hi, max_pages, page_size,
+                num_pages, stride, groups_row);
+}
+
 template <int MT>
 static hipError_t launch_indexer_mt(const uint16_t* q, const float* w, const uint8_t* k, const float* ks,
                                     const int* table, const int* ctx_len, const float* cand, float* scores,
                                     int* hist, int B, int Hi, int max_pages, int page_size, int num_pages, int stride,
-                                    int tiles_per_wave, hipStream_t stream) {
-  const int tiles_row = (stride + IDX_TILE - 1) / IDX_TILE;
-  const int waves_row = (tiles_row + tiles_per_wave - 1) / tiles_per_wave;
-  const int chunks_row = (waves_row + IDX_WAVES - 1) / IDX_WAVES;
+                                    hipStream_t s) {
+  if (hist && cand)
+    return launch_indexer_variant<MT, true, true>(q, w, k, ks, table, ctx_len, cand, scores, hist, B, Hi, max_pages,
+                                                  page_size, num_pages, stride, s);
   if (hist)
-    launch("indexer_decode_kernel", (indexer_decode_kernel<MT, true>), dim3(B * chunks_row), dim3(IDX_THREADS), stream, q, w,
-                       k, ks, table, ctx_len, cand, scores, hist, Hi, max_pages, page_size, num_pages, stride,
-                       tiles_per_wave, chunks_row);
-  else
-    launch("indexer_decode_kernel", (indexer_decode_kernel<MT, false>), dim3(B * chunks_row), dim3(IDX_THREADS), stream, q, w,
-                       k, ks, table, ctx_len, cand, scores, hist, Hi, max_pages, page_size, num_pages, stride,
-                       tiles_per_wave, chunks_row);
-  return hipGetLastError();
+    return launch_indexer_variant<MT, true, false>(q, w, k, ks, table, ctx_len, cand, scores, hist, B, Hi,
+                                                   max_pages, page_size, num_pages, stride, s);
+  if (cand)
+    return launch_indexer_variant<MT, false, true>(q, w, k, ks, table, ctx_len, cand, scores, hist, B, Hi,
+                                                   max_pages, page_size, num_pages, stride, s);
+  return launch_indexer_variant<MT, false, false>(q, w, k, ks, table, ctx_len, cand, scores, hist, B, Hi, max_pages,
+                                                  page_size, num_pages, stride, s);
 }
 
 hipError_t launch_indexer_decode(const uint16_t* q, const float* w, const uint8_t* k, const float* ks,
                                  const int* table, const int* ctx_len, const float* cand, float* scores,
                                  int* hist, int B, int Hi, int max_pages, int page_size, int num_pages, int stride,
                                  int num_cu, hipStream_t stream) {
-  // Two workgroups (8 waves) per CU over the whole batch; a wave takes a multiple of the prefetch depth in tiles.
-  const long tiles = (long)B * ((stride + IDX_TILE - 1) / IDX_TILE);
-  const long waves = (long)num_cu * 2 * IDX_WAVES;
-  int tpw = (int)((tiles + waves - 1) / waves);
-  tpw = (tpw + IDX_PF - 1) / IDX_PF * IDX_PF;
-  tpw = tpw < IDX_PF ? IDX_PF : tpw;
+  (void)num_cu;  // one workgroup per IDX_TPG tiles of a row, whatever the GPU's size
   if (Hi <= 32)
     return launch_indexer_mt<1>(q, w, k, ks, table, ctx_len, cand, scores, hist, B, Hi, max_pages, page_size,
-                                num_pages, stride, tpw, stream);
+                                num_pages, stride, stream);
   return launch_indexer_mt<2>(q, w, k, ks, table, ctx_len, cand, scores, hist, B, Hi, max_pages, page_size,
-                              num_pages, stride, tpw, stream);
+                              num_pages, stride, stream);
 }
 
 }  // namespace dsa

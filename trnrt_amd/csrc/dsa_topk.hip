@@ -4,19 +4,14 @@
 // equal to the keep-th largest, the lowest positions; only scores > VISIBLE are selectable (vis_only); a row with
 // fewer selectable scores than keep selects all of them. Output: the positions in ascending order plus the count.
 //
-// One workgroup of 1024 threads owns a row of up to 1024 E scores, E consecutive positions per thread, held in
-// registers as order-preserving integer keys (dsa_common.h order_key), so every comparison is exact (the reference's
-// radix search over the threshold's bit pattern, dsa_topk.py:19-26, is exact for the same reason).
-//
-// The threshold search narrows a key interval [lo, hi] that contains the keep-th largest key, with `need` = its rank
-// from the top inside the interval, by histograms in LDS:
-//   - first pass: 2048 bins linear in VALUE over [min, max] of the row (a monotone binning, so each bin is a key
-//     interval; it spreads the bell-shaped indexer scores over many bins, where the leading key bits would put most
-//     of them into a few);
-//   - then passes over the low bits of (key - lo), 11 bits at a time, until lo == hi = the threshold T.
-// A pass counts only the keys inside the current interval, so the later passes touch a few keys.
-// Selection: key > T, plus the first `room` = keep - #(key > T) keys equal to T by position (a block-wide prefix
-// count over the tied keys in position order), written in position order by a block-wide prefix count.
+// One workgroup of 1024 threads owns a row of up to 32,768 scores, held in registers as order-preserving integer
+// keys (dsa_common.h order_key), so every comparison is exact (the reference's radix search over the threshold's bit
+// pattern, dsa_topk.py:19-26, is exact for the same reason). The threshold T (the keep-th largest key) is found
+// radix-wise from the top: a histogram of the top 12 key bits (accumulated by the indexer while it writes the
+// scores, or built here in LDS), then LDS histograms of the next 11 and the last 9 bits over the keys that share the
+// prefix found so far, each pass a block-wide suffix scan for the bin holding the need-th key. The selection is
+// every key > T plus the first `room` keys equal to T by position, written in position order by a block-wide prefix
+// count, so no list is sorted and no key moves.
 //
 // Longer rows go through the reference's two-level exact selection (trnrt/models/dsa_long.py:26-42, 114-132):
 // sub-block maxima, the top-keep sub-blocks, and the top-keep of their elements in position order.
@@ -24,21 +19,11 @@
 
 namespace dsa {
 
-constexpr int TK_THREADS = 1024;
-constexpr int TK_WAVES = TK_THREADS / WAVE;
-constexpr int TK_BINS = 2048;   // bins of a refinement pass (11 key bits)
-constexpr int TK_BITS = 11;
-constexpr int TK_HSHIFT = 20;   // first level: the top 12 bits of the order key
+constexpr int TK_HSHIFT = 20;  // first level: the top 12 bits of the order key
 constexpr int TK_HBINS = 4096;
-constexpr int TKH_THREADS = 256;  // histogram kernel: 8 scores per thread, 2048 per workgroup
-constexpr int TKH_CHUNK = TKH_THREADS * 8;
-
-struct TopkShared {
-  int hist[TK_BINS];
-  uint32_t scan_tot[TK_WAVES];
-  int sel_bin;
-  int sel_above;
-};
+constexpr int TR_THREADS = 1024;
+constexpr int TR_WAVES = TR_THREADS / WAVE;
+constexpr int TR_MAXG = 8;     // float4 groups per thread: rows of up to 4 x 8 x 1024 scores
 
 // The row length in elements of a selection level: len[row] for a flat row; ceil(len / len_div) for sub-block
 // maxima; len[row] * len_mul for a candidate row of len[row] sub-blocks; at most stride.
@@ -51,64 +36,250 @@ __device__ __forceinline__ int level_len(const int* len, int row, int len_div, i
   return (int)(l < stride ? l : stride);
 }
 
+// Branch-free (masks, not selects), so that the compiler keeps the loads feeding it unconditional.
 __device__ __forceinline__ uint32_t select_key(float v, int vis_only) {
-  return (!vis_only || v > VISIBLE) ? order_key(v) : 0u;
+  return order_key(v) & (0u - (uint32_t)(!vis_only || v > VISIBLE));
 }
 
-// Block-wide exclusive prefix sum (thread order) of a uint32 per thread; returns it and the total.
-__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, TopkShared& sh, uint32_t* total) {
-  const int wave = threadIdx.x / WAVE, lane = threadIdx.x & (WAVE - 1);
-  const uint32_t inc = (uint32_t)wave_incl_scan((int)v);
-  if (lane == WAVE - 1) sh.scan_tot[wave] = inc;
-  __syncthreads();
-  uint32_t before = 0, tot = 0;
+// Four keys of positions p .. p + 3 of a row of `stride` scores (0 past L or not selectable), loaded
+// unconditionally from in-range addresses so that the waits on the loads count exactly: VEC (stride a multiple of
+// 4, at least 4) one float4, clamped to the row's last four (a clamped p is past the row, so all four are masked);
+// otherwise four scalar loads clamped to the row.
+template <bool VEC>
+__device__ __forceinline__ void load_keys4(const float* srow, int stride, int L, int p, int vis_only, uint32_t (&k)[4]) {
+  float v[4];
+  if (VEC) {
+    const float4 f = *reinterpret_cast<const float4*>(srow + min(p, stride - 4));
+    v[0] = f.x;
+    v[1] = f.y;
+    v[2] = f.z;
+    v[3] = f.w;
+  } else {
 #pragma unroll
-  for (int i = 0; i < TK_WAVES; ++i) {
-    const uint32_t x = sh.scan_tot[i];
-    before += i < wave ? x : 0u;
+    for (int c = 0; c < 4; ++c) v[c] = srow[min(p + c, stride - 1)];
+  }
+#pragma unroll
+  for (int c = 0; c < 4; ++c) k[c] = select_key(v[c], vis_only) & (0u - (uint32_t)(p + c < L));
+}
+
+// Sum over the 16 lanes of each DPP row (quad swaps, then the half-row and row mirrors), in every lane of the row.
+__device__ __forceinline__ int row16_sum(int v) {
+  v += dpp<0xb1>(v);
+  v += dpp<0x4e>(v);
+  v += dpp<0x141>(v);
+  v += dpp<0x140>(v);
+  return v;
+}
+
+struct RowShared {
+  int bins[TK_HBINS];               // the current pass's histogram (4096, 2048 or 512 bins in key order)
+  int wtot[TR_WAVES];               // per-wave totals of a block scan
+  uint32_t blk[TR_MAXG * TR_WAVES];  // output: per (group, wave) packed counts, then their exclusive prefix
+  int sel_bin, sel_above;
+};
+
+// Block-wide, over sh.bins[0 .. nbins) (a key histogram, higher bins = larger keys): the bin holding the need-th
+// largest key (*bin) and the keys in the bins above it (*above); returns the total count. Each thread takes
+// nbins / 1024 bins (at least one; threads past nbins take none). sh.sel_bin must be -1 on entry (set before the
+// barrier that precedes the histogram's atomics); counts that cannot hold the need-th key give bin 0, above 0. The
+// caller must pass a barrier before sh.sel_bin / sh.wtot are written again.
+__device__ int row_find_bin(RowShared& sh, int nbins, int need, int* bin, int* above) {
+  const int t = threadIdx.x, wave = t / WAVE, lane = t & (WAVE - 1);
+  const int per = nbins >= TR_THREADS ? nbins / TR_THREADS : 1;
+  const int first = t * per;
+  int hb[4];
+  int mine = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    hb[i] = (i < per && first + i < nbins) ? sh.bins[first + i] : 0;
+    mine += hb[i];
+  }
+  const int pre = wave_incl_scan(mine);
+  const int inc = __builtin_amdgcn_readlane(pre, WAVE - 1) - pre + mine;  // inclusive suffix over the lanes
+  if (lane == 0) sh.wtot[wave] = inc;
+  __syncthreads();
+  int after = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < TR_WAVES; ++w) {
+    const int x = sh.wtot[w];
+    after += w > wave ? x : 0;
     tot += x;
   }
-  __syncthreads();
-  *total = tot;
-  return before + inc - v;
-}
-
-// Exclusive suffix sum (reverse thread order): the sum of v over the threads above this one, and the total.
-__device__ __forceinline__ int block_excl_suffix(int v, TopkShared& sh, int* total) {
-  const int rt = TK_THREADS - 1 - (int)threadIdx.x;  // reversed id: its wave is 15 - wave, its lane 63 - lane
-  const int wave = rt / WAVE, lane = rt & (WAVE - 1);
-  int inc = v;
+  int excl = after + inc - mine;  // keys in the bins above this thread's
+  if (excl < need && excl + mine >= need) {
 #pragma unroll
-  for (int o = 1; o < WAVE; o <<= 1) {
-    const int x = __shfl_down(inc, o, WAVE);  // the thread o above has reversed lane - o
-    if (lane >= o) inc += x;
-  }
-  if (lane == WAVE - 1) sh.scan_tot[wave] = (uint32_t)inc;
-  __syncthreads();
-  int before = 0, tot = 0;
-#pragma unroll
-  for (int i = 0; i < TK_WAVES; ++i) {
-    const int x = (int)sh.scan_tot[i];
-    before += i < wave ? x : 0;
-    tot += x;
+    for (int i = 3; i >= 0; --i) {
+      if (i < per && first + i < nbins && excl < need) {
+        if (excl + hb[i] >= need) {
+          sh.sel_bin = first + i;
+          sh.sel_above = excl;
+        }
+        excl += hb[i];
+      }
+    }
   }
   __syncthreads();
-  *total = tot;
-  return before + inc - v;
+  const int b = sh.sel_bin;
+  *bin = b < 0 ? 0 : b;
+  *above = b < 0 ? 0 : sh.sel_above;
+  return tot;
 }
 
-__device__ __forceinline__ int bit_length(uint32_t x) { return x ? 32 - __clz(x) : 0; }
+// The flat selection: one workgroup per row (blockIdx.x) of up to 4 G 1024 scores. Thread t holds the keys of
+// positions 4 (1024 e + t) + c, e < G, c < 4 (coalesced float4 loads). HIST_IN: the row's top-12-bit histogram is in
+// hist[row] (read, then zeroed for the next call); otherwise it is built here.
+template <int G, bool HIST_IN, bool VEC>
+__global__ __launch_bounds__(TR_THREADS) void topk_row_kernel(const float* __restrict__ scores, int stride,
+                                                              const int* __restrict__ len, int len_div, int len_mul,
+                                                              int keep, int vis_only, int* __restrict__ hist,
+                                                              int* __restrict__ idx_out, int* __restrict__ cnt_out) {
+  __shared__ RowShared sh;
+  const int row = blockIdx.x;
+  const int t = threadIdx.x, wave = t / WAVE, lane = t & (WAVE - 1);
+  const int L = level_len(len, row, len_div, len_mul, stride);
+  const float* srow = scores + (size_t)row * stride;
 
-// First level of a selection: the histogram of the top 12 bits of the selectable keys of each row, accumulated into
-// hist[row, 4096] (zero before; the select kernel zeroes it again after reading). 2048 scores per workgroup.
+  int4 h4 = make_int4(0, 0, 0, 0);
+  int* hrow = hist + (size_t)row * TK_HBINS;
+  if (HIST_IN) h4 = reinterpret_cast<const int4*>(hrow)[t];
+  uint32_t key[G][4];
+#pragma unroll
+  for (int e = 0; e < G; ++e) load_keys4<VEC>(srow, stride, L, 4 * (TR_THREADS * e + t), vis_only, key[e]);
+  if (t == 0) sh.sel_bin = -1;
+  if (HIST_IN) {
+    reinterpret_cast<int4*>(sh.bins)[t] = h4;
+    reinterpret_cast<int4*>(hrow)[t] = make_int4(0, 0, 0, 0);  // zero for the next call
+    __syncthreads();
+  } else {
+    reinterpret_cast<int4*>(sh.bins)[t] = make_int4(0, 0, 0, 0);
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < G; ++e)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (key[e][c]) atomicAdd(&sh.bins[key[e][c] >> TK_HSHIFT], 1);
+    __syncthreads();
+  }
+
+  // the threshold, 12 + 11 + 9 bits
+  int c0, above;
+  const int nvis = row_find_bin(sh, TK_HBINS, keep, &c0, &above);
+  uint32_t T = 0;
+  int room = 0;
+  if (nvis > keep) {
+    int need = keep - above;
+    __syncthreads();  // every thread has read the pass's result
+    reinterpret_cast<int2*>(sh.bins)[t] = make_int2(0, 0);
+    if (t == 0) sh.sel_bin = -1;
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < G; ++e)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (key[e][c] && (key[e][c] >> TK_HSHIFT) == (uint32_t)c0) atomicAdd(&sh.bins[(key[e][c] >> 9) & 2047], 1);
+    __syncthreads();
+    int c1;
+    row_find_bin(sh, 2048, need, &c1, &above);
+    need -= above;
+    const uint32_t pre = ((uint32_t)c0 << 11) | (uint32_t)c1;  // the top 23 bits of T
+    __syncthreads();
+    if (t < 512) sh.bins[t] = 0;
+    if (t == 0) sh.sel_bin = -1;
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < G; ++e)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (key[e][c] && (key[e][c] >> 9) == pre) atomicAdd(&sh.bins[key[e][c] & 511], 1);
+    __syncthreads();
+    int c2;
+    row_find_bin(sh, 512, need, &c2, &above);
+    T = (pre << 9) | (uint32_t)c2;
+    room = need - above;  // keys equal to T to take, lowest positions first
+    room = room < 0 ? 0 : room;
+  }
+
+  // per (group, wave): keys above T and keys equal to T, packed hi / lo 16 bits (each at most 32768)
+  uint32_t mine[G], incl[G];
+#pragma unroll
+  for (int e = 0; e < G; ++e) {
+    uint32_t na = 0, nt = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      na += key[e][c] > T;
+      nt += T != 0 && key[e][c] == T;
+    }
+    mine[e] = (na << 16) | nt;
+    incl[e] = wave_incl_scan_u32(mine[e]);
+    if (lane == WAVE - 1) sh.blk[e * TR_WAVES + wave] = incl[e];
+  }
+  __syncthreads();
+  if (wave == 0) {  // exclusive prefix over (group, wave) in position order: G x 16 <= 128 values, 2 per lane
+    const uint32_t x0 = 2 * lane < G * TR_WAVES ? sh.blk[2 * lane] : 0u;
+    const uint32_t x1 = 2 * lane + 1 < G * TR_WAVES ? sh.blk[2 * lane + 1] : 0u;
+    const uint32_t in2 = wave_incl_scan_u32(x0 + x1);
+    const uint32_t ex = in2 - x0 - x1;
+    if (2 * lane < G * TR_WAVES) sh.blk[2 * lane] = ex;
+    if (2 * lane + 1 < G * TR_WAVES) sh.blk[2 * lane + 1] = ex + x0;
+  }
+  __syncthreads();
+  int* orow = idx_out + (size_t)row * keep;
+#pragma unroll
+  for (int e = 0; e < G; ++e) {
+    const uint32_t before = sh.blk[e * TR_WAVES + wave] + incl[e] - mine[e];
+    int a_before = (int)(before >> 16), t_before = (int)(before & 0xffffu);
+    const int p0 = 4 * (TR_THREADS * e + t);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const bool a = key[e][c] > T;
+      const bool ti = T != 0 && key[e][c] == T;
+      const bool sel = a || (ti && t_before < room);
+      const int o = a_before + (t_before < room ? t_before : room);
+      if (sel && (unsigned)o < (unsigned)keep) orow[o] = p0 + c;  // in range whatever the counts
+      a_before += a;
+      t_before += ti;
+    }
+  }
+  const int cnt_row = nvis < keep ? nvis : keep;
+  for (int i = cnt_row + t; i < keep; i += TR_THREADS) orow[i] = 0;
+  if (t == 0) cnt_out[row] = cnt_row;
+}
+
+// The chunked selection of rows of more than 4096 scores: workgroups of 256 threads own chunks of 2048 positions
+// (thread t the positions base + 4 (256 e + t) + c, e < 2, c < 4), so the per-key work is spread over many CUs, in
+// two kernels with one round of global loads each:
+//   topk_chunk_kernel:  from the row's top-12-bit histogram the threshold's bin c0 and the keys in bins above it
+//                       (every chunk computes them); per chunk the count of its keys above c0 and its keys in bin
+//                       c0 (the candidates, a few hundred per row for indexer scores), written in position order;
+//   topk_output_kernel: every chunk loads the row's candidates and counts, finds T and the ties to take with two LDS
+//                       histogram passes (bits 19..9, then 8..0), each chunk's output base from the per-chunk counts,
+//                       and writes its own selected positions in order.
+constexpr int TC_THREADS = 256;
+constexpr int TC_WAVES = TC_THREADS / WAVE;
+constexpr int TC_CHUNK = 2048;
+constexpr int TC_MAXCH = 16;   // rows of up to 32,768 scores
+constexpr int TC_CAND = 128;   // candidates per chunk held in registers by the output kernel (more: extra rounds)
+constexpr int TKH_THREADS = 256;  // histogram kernel: 8 scores per thread, 2048 per workgroup
+
+struct RowMeta {
+  int c0;      // the threshold's 12-bit bin, -1 when the row has at most keep selectable keys
+  int above0;  // selectable keys in bins above c0
+  int nvis;    // selectable keys of the row
+  int pad;
+  int n_a[TC_MAXCH];  // per chunk: keys above c0 (all its selectable keys when c0 is -1)
+  int n_c[TC_MAXCH];  // per chunk: keys in bin c0
+};
+
+// The first level of a standalone selection: the histogram of the top 12 bits of the selectable keys of each row,
+// accumulated into hist[row, 4096] (zero before; the output kernel zeroes it again). 2048 scores per workgroup.
 __global__ __launch_bounds__(TKH_THREADS) void topk_hist_kernel(const float* __restrict__ scores, int stride,
                                                                 const int* __restrict__ len, int len_div,
                                                                 int len_mul, int vis_only, int* __restrict__ hist) {
   __shared__ int h[TK_HBINS];
   const int row = blockIdx.y;
   const int L = level_len(len, row, len_div, len_mul, stride);
-  const int base = blockIdx.x * TKH_CHUNK;
-  if (base >= L) return;
+  const int base = blockIdx.x * TC_CHUNK;
+  if (base >= L) return;  // the whole workgroup: no barrier is skipped by part of it
   for (int i = threadIdx.x; i < TK_HBINS; i += TKH_THREADS) h[i] = 0;
   __syncthreads();
   const float* srow = scores + (size_t)row * stride;
@@ -128,81 +299,44 @@ __global__ __launch_bounds__(TKH_THREADS) void topk_hist_kernel(const float* __r
   }
 }
 
-__device__ __forceinline__ uint64_t lanes_below() {
-  const int lane = threadIdx.x & (WAVE - 1);
-  return lane ? (~0ull >> (64 - lane)) : 0ull;
+// A chunk's 8 keys per thread.
+template <bool VEC>
+__device__ __forceinline__ void load_chunk_keys(const float* srow, int stride, int L, int base, int vis_only,
+                                                uint32_t (&key)[2][4]) {
+#pragma unroll
+  for (int e = 0; e < 2; ++e) load_keys4<VEC>(srow, stride, L, base + 4 * (TC_THREADS * e + (int)threadIdx.x), vis_only, key[e]);
 }
 
-// The flat selection of rows of up to TS_MAXCH x 2048 scores, spread over workgroups of 2048 scores (chunks), in two
-// kernels with no waiting between workgroups:
-//   topk_chunk_kernel:  from the row's first-level histogram the threshold's 12-bit bin c0 (every chunk computes it);
-//                       per chunk the count of keys in bins above c0 and the keys of bin c0 (the candidates, a few
-//                       hundred per row for indexer scores), written in position order (so list order ranks ties);
-//   topk_output_kernel: every chunk loads the row's candidates (thread t the t-th of each chunk), two histogram
-//                       passes over their low key bits give the exact threshold T and the number of keys equal to T
-//                       to take (lowest positions first), the chunk's output base follows from the per-chunk counts,
-//                       and the chunk writes its selected positions in order.
-// Thread t holds the float4 groups e = 0, 1 at chunk positions 4 (256 e + t) .. + 3 (coalesced loads), so group e
-// of wave w is the contiguous block of 256 positions 1024 e + 256 w .. of the chunk.
-constexpr int TS_THREADS = 256;
-constexpr int TS_WAVES = TS_THREADS / WAVE;
-constexpr int TS_G = 2;
-constexpr int TS_CHUNK = TS_THREADS * 4 * TS_G;  // 2048
-constexpr int TS_MAXCH = 16;                     // rows up to 32768 scores
-
-struct RowMeta {
-  int c0;      // the threshold's 12-bit bin (-1: every selectable key is selected)
-  int above0;  // selectable keys in bins above c0
-  int nvis;    // selectable keys of the row
-  int pad;
-  int n_a[TS_MAXCH];  // per chunk: keys in bins above c0
-  int n_c[TS_MAXCH];  // per chunk: keys in bin c0
-};
-
-__device__ __forceinline__ void load_chunk_keys(const float* srow, int L, int base, bool vec, int vis_only,
-                                                uint32_t (&key)[TS_G][4]) {
-  const int t = threadIdx.x;
-#pragma unroll
-  for (int e = 0; e < TS_G; ++e) {
-    const int p = base + 4 * (TS_THREADS * e + t);
-    if (vec && p + 4 <= L) {
-      const float4 v = *reinterpret_cast<const float4*>(srow + p);
-      key[e][0] = select_key(v.x, vis_only);
-      key[e][1] = select_key(v.y, vis_only);
-      key[e][2] = select_key(v.z, vis_only);
-      key[e][3] = select_key(v.w, vis_only);
-    } else {
-#pragma unroll
-      for (int c = 0; c < 4; ++c) key[e][c] = (p + c < L) ? select_key(srow[p + c], vis_only) : 0u;
-    }
-  }
-}
-
-// Exclusive prefix over the (e, wave) blocks of per-block counts (packed hi / lo 16 bits), in position order.
-__device__ __forceinline__ void block_bases(uint32_t (&cnt)[TS_G], uint32_t* blk, uint32_t (&base)[TS_G]) {
+// Exclusive prefix, in position order (group e, then wave, then lane), of per-thread packed counts mine[e]
+// (hi / lo 16 bits, block totals below 65536); blk: 2 x TC_WAVES words of LDS. Two barriers.
+__device__ __forceinline__ void chunk_prefix(const uint32_t (&mine)[2], uint32_t* blk, uint32_t (&before)[2]) {
   const int wave = threadIdx.x / WAVE, lane = threadIdx.x & (WAVE - 1);
-  if (lane == 0)
+  uint32_t incl[2];
 #pragma unroll
-    for (int e = 0; e < TS_G; ++e) blk[e * TS_WAVES + wave] = cnt[e];
+  for (int e = 0; e < 2; ++e) {
+    incl[e] = wave_incl_scan_u32(mine[e]);
+    if (lane == WAVE - 1) blk[e * TC_WAVES + wave] = incl[e];
+  }
   __syncthreads();
 #pragma unroll
-  for (int e = 0; e < TS_G; ++e) {
+  for (int e = 0; e < 2; ++e) {
     uint32_t acc = 0;
-    const int me = e * TS_WAVES + wave;
+    const int me = e * TC_WAVES + wave;
 #pragma unroll
-    for (int i = 0; i < TS_G * TS_WAVES; ++i) acc += i < me ? blk[i] : 0u;
-    base[e] = acc;
+    for (int i = 0; i < 2 * TC_WAVES; ++i) acc += i < me ? blk[i] : 0u;
+    before[e] = acc + incl[e] - mine[e];
   }
   __syncthreads();
 }
 
 struct ChunkShared {
-  int bins[TS_THREADS];  // per thread: its 16 bins' sum, for the suffix scan
-  uint32_t blk[TS_G * TS_WAVES];
+  int wtot[TC_WAVES];
+  uint32_t blk[2 * TC_WAVES];
   int c0, above0;
 };
 
-__global__ __launch_bounds__(TS_THREADS) void topk_chunk_kernel(const float* __restrict__ scores, int stride,
+template <bool VEC>
+__global__ __launch_bounds__(TC_THREADS) void topk_chunk_kernel(const float* __restrict__ scores, int stride,
                                                                 const int* __restrict__ len, int len_div,
                                                                 int len_mul, int keep, int vis_only,
                                                                 const int* __restrict__ hist,
@@ -210,17 +344,16 @@ __global__ __launch_bounds__(TS_THREADS) void topk_chunk_kernel(const float* __r
                                                                 uint32_t* __restrict__ ckey) {
   __shared__ ChunkShared sh;
   const int row = blockIdx.y, chunk = blockIdx.x;
-  const int t = threadIdx.x, lane = t & (WAVE - 1);
+  const int t = threadIdx.x, wave = t / WAVE, lane = t & (WAVE - 1);
   const int L = level_len(len, row, len_div, len_mul, stride);
-  const int base = chunk * TS_CHUNK;
-  const int* hrow = hist + (size_t)row * TK_HBINS;
+  const int base = chunk * TC_CHUNK;
+  // one round of loads: the thread's 16 histogram bins and its 8 keys
+  const int4* h4 = reinterpret_cast<const int4*>(hist + (size_t)row * TK_HBINS) + 4 * t;
   int4 hv[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) hv[i] = *reinterpret_cast<const int4*>(hrow + 16 * t + 4 * i);
-  uint32_t key[TS_G][4];
-  load_chunk_keys(scores + (size_t)row * stride, L, base, (stride & 3) == 0, vis_only, key);
-
-  // suffix sums of the 16-bin groups (thread t: bins 16 t .. 16 t + 15), every thread its own exclusive suffix
+  for (int i = 0; i < 4; ++i) hv[i] = h4[i];
+  uint32_t key[2][4];
+  load_chunk_keys<VEC>(scores + (size_t)row * stride, stride, L, base, vis_only, key);
   int hb[16];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -229,154 +362,139 @@ __global__ __launch_bounds__(TS_THREADS) void topk_chunk_kernel(const float* __r
     hb[4 * i + 2] = hv[i].z;
     hb[4 * i + 3] = hv[i].w;
   }
+  // c0: the bin holding the keep-th largest key (bins 16t .. 16t + 15 on thread t; suffix over threads)
   int mine = 0;
 #pragma unroll
   for (int i = 0; i < 16; ++i) mine += hb[i];
+  const int pre = wave_incl_scan(mine);
+  const int inc = __builtin_amdgcn_readlane(pre, WAVE - 1) - pre + mine;  // inclusive suffix over the lanes
+  if (lane == 0) sh.wtot[wave] = inc;
   if (t == 0) {
     sh.c0 = -1;
     sh.above0 = 0;
   }
-  int inc = mine;  // suffix inside the wave: lanes >= this one
-#pragma unroll
-  for (int o = 1; o < WAVE; o <<= 1) {
-    const int x = __shfl_down(inc, o, WAVE);
-    if (lane + o < WAVE) inc += x;
-  }
-  if (lane == 0) sh.bins[t / WAVE] = inc;  // the wave's total
   __syncthreads();
-  int suf = inc - mine, nvis = 0;
+  int after = 0, nvis = 0;
 #pragma unroll
-  for (int i = 0; i < TS_WAVES; ++i) {
-    const int x = sh.bins[i];
-    suf += i > t / WAVE ? x : 0;
+  for (int w = 0; w < TC_WAVES; ++w) {
+    const int x = sh.wtot[w];
+    after += w > wave ? x : 0;
     nvis += x;
   }
-  if (nvis > keep && suf < keep && suf + mine >= keep) {
+  int excl = after + inc - mine;
+  if (nvis > keep && excl < keep && excl + mine >= keep) {
 #pragma unroll
     for (int i = 15; i >= 0; --i) {
-      if (suf < keep && suf + hb[i] >= keep) {
-        sh.c0 = 16 * t + i;
-        sh.above0 = suf;
+      if (excl < keep) {
+        if (excl + hb[i] >= keep) {
+          sh.c0 = 16 * t + i;
+          sh.above0 = excl;
+        }
+        excl += hb[i];
       }
-      suf += hb[i];
     }
   }
   __syncthreads();
-  const int c0 = sh.c0;  // -1: at most keep selectable keys, every one is selected
-  if (chunk == 0 && t == 0) {
-    meta[row].c0 = c0;
-    meta[row].above0 = sh.above0;
-    meta[row].nvis = nvis;
-  }
-  // classification: above c0, or in c0 (a candidate); the candidates in position order
-  const uint64_t below = lanes_below();
-  uint64_t cm[TS_G][4];
-  uint32_t cnt[TS_G], na = 0;
+  const int c0 = sh.c0;
+  // classify the chunk's keys: above c0 (all selectable ones when c0 is -1) and in bin c0 (the candidates)
+  uint32_t mc[2];
+  int na = 0;
 #pragma unroll
-  for (int e = 0; e < TS_G; ++e) {
-    cnt[e] = 0;
+  for (int e = 0; e < 2; ++e) {
+    uint32_t nc = 0;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const uint32_t k = key[e][c];
       const int bin = (int)(k >> TK_HSHIFT);
-      na += __popcll(__ballot(k != 0 && bin > c0));
-      cm[e][c] = __ballot(k != 0 && bin == c0);
-      cnt[e] += __popcll(cm[e][c]);
+      na += k != 0u && bin > c0;
+      nc += k != 0u && bin == c0;
     }
+    mc[e] = nc;
   }
-  uint32_t bb[TS_G];
-  block_bases(cnt, sh.blk, bb);
-  uint32_t* krow = ckey + ((size_t)row * TS_MAXCH + chunk) * TS_CHUNK;
+  // position-ordered compaction of the candidates
+  uint32_t before[2];
+  chunk_prefix(mc, sh.blk, before);
+  uint32_t* crow = ckey + ((size_t)row * TC_MAXCH + chunk) * TC_CHUNK;
 #pragma unroll
-  for (int e = 0; e < TS_G; ++e) {
-    int o = (int)bb[e];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) o += __popcll(cm[e][c] & below);
+  for (int e = 0; e < 2; ++e) {
+    uint32_t o = before[e];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      if ((cm[e][c] >> lane) & 1ull) krow[o++] = key[e][c];
+      const uint32_t k = key[e][c];
+      if (k != 0u && (int)(k >> TK_HSHIFT) == c0) {
+        if (o < (uint32_t)TC_CHUNK) crow[o] = k;
+        ++o;
+      }
     }
   }
-  // the chunk's counts (na was counted per wave: every lane holds its wave's total)
+  // chunk totals: candidates = prefix of the last (e, wave) block + its count; above = block sum of na
+  const int na_w = wave_sum(na);
+  if (lane == 0) sh.wtot[wave] = na_w;
   __syncthreads();
-  if (lane == 0) sh.bins[t / WAVE] = (int)na;
-  __syncthreads();
-  if (t == 0) {
-    int tot_a = 0;
-    for (int i = 0; i < TS_WAVES; ++i) tot_a += sh.bins[i];
-    int tot_c = 0;
-    for (int i = 0; i < TS_G * TS_WAVES; ++i) tot_c += (int)sh.blk[i];
-    meta[row].n_a[chunk] = tot_a;
-    meta[row].n_c[chunk] = tot_c;
+  if (t == TC_THREADS - 1) {
+    int na_tot = 0;
+#pragma unroll
+    for (int w = 0; w < TC_WAVES; ++w) na_tot += sh.wtot[w];
+    const int nc_tot = (int)(before[1] + mc[1]);  // the last thread's exclusive prefix of e = 1 plus its own
+    meta[row].n_a[chunk] = na_tot;
+    meta[row].n_c[chunk] = nc_tot;
+    if (chunk == 0) {
+      meta[row].c0 = c0;
+      meta[row].above0 = sh.above0;
+      meta[row].nvis = nvis;
+    }
   }
 }
 
 struct OutShared {
-  int hist[TK_BINS];
-  int gt[TS_MAXCH], tie[TS_MAXCH], nc[TS_MAXCH], na[TS_MAXCH];
-  int off[TS_MAXCH + 1];
-  uint32_t blk[TS_G * TS_WAVES];
-  int c0, above0, nvis, maxc;
-  int sel_c, sel_above;
-  uint32_t T;
-  int room;
+  int bins[2048];
+  int wtot[TC_WAVES];
+  uint32_t blk[2 * TC_WAVES];
+  int gt[TC_MAXCH], tie[TC_MAXCH], na[TC_MAXCH];
+  int sel_bin, sel_above;
 };
 
-// One refinement pass's threshold bin, by wave 0 over the block-wide histogram of nbins bins (32 or 8 per lane):
-// the bin holding the need-th largest key and the keys above it, into sh.sel_c / sh.sel_above.
-__device__ __forceinline__ void wave0_find_bin(OutShared& sh, int nbins, int need) {
-  const int lane = threadIdx.x & (WAVE - 1);
-  constexpr int PER = TK_BINS / WAVE;
-  const int per = nbins / WAVE;
-  int hb[PER];
-  const int4* h4 = reinterpret_cast<const int4*>(sh.hist);
-#pragma unroll
-  for (int i = 0; i < PER / 4; ++i) {
-    int4 v = make_int4(0, 0, 0, 0);
-    if (4 * i < per) v = h4[(per / 4) * lane + i];
-    hb[4 * i] = v.x;
-    hb[4 * i + 1] = v.y;
-    hb[4 * i + 2] = v.z;
-    hb[4 * i + 3] = v.w;
-  }
+// Block-wide (256 threads) over sh.bins[0 .. nbins) (nbins 2048 or 512, higher bins = larger keys): the bin holding
+// the need-th largest key and the keys in the bins above it. sh.sel_bin must be -1 on entry (written before the
+// barrier preceding the histogram's atomics); inconsistent counts give bin 0, above 0. Two barriers.
+__device__ void out_find_bin(OutShared& sh, int nbins, int need, int* bin, int* above) {
+  const int t = threadIdx.x, wave = t / WAVE, lane = t & (WAVE - 1);
+  const int per = nbins / TC_THREADS;  // 8 or 2
+  int hb[8];
   int mine = 0;
 #pragma unroll
-  for (int i = 0; i < PER; ++i) mine += hb[i];
-  int inc = mine;
-#pragma unroll
-  for (int o = 1; o < WAVE; o <<= 1) {
-    const int x = __shfl_down(inc, o, WAVE);
-    if (lane + o < WAVE) inc += x;
+  for (int i = 0; i < 8; ++i) {
+    hb[i] = i < per ? sh.bins[per * t + i] : 0;
+    mine += hb[i];
   }
-  int suf = inc - mine;
-  int found = -1, above = 0;
-  if (suf < need && suf + mine >= need) {
+  const int pre = wave_incl_scan(mine);
+  const int inc = __builtin_amdgcn_readlane(pre, WAVE - 1) - pre + mine;  // inclusive suffix over the lanes
+  if (lane == 0) sh.wtot[wave] = inc;
+  __syncthreads();
+  int after = 0;
 #pragma unroll
-    for (int i = PER - 1; i >= 0; --i) {
-      if (found < 0 && i < per) {
-        if (suf + hb[i] >= need) {
-          found = per * lane + i;
-          above = suf;
-        } else {
-          suf += hb[i];
+  for (int w = 0; w < TC_WAVES; ++w) after += w > wave ? sh.wtot[w] : 0;
+  int excl = after + inc - mine;
+  if (excl < need && excl + mine >= need) {
+#pragma unroll
+    for (int i = 7; i >= 0; --i) {
+      if (i < per && excl < need) {
+        if (excl + hb[i] >= need) {
+          sh.sel_bin = per * t + i;
+          sh.sel_above = excl;
         }
+        excl += hb[i];
       }
     }
   }
-  const uint64_t who = __ballot(found >= 0);
-  if (who) {
-    const int src = (int)__builtin_ctzll(who);
-    if (lane == src) {
-      sh.sel_c = found;
-      sh.sel_above = above;
-    }
-  } else if (lane == 0) {  // counts that do not match (a workspace that was not zero): stay in range
-    sh.sel_c = 0;
-    sh.sel_above = 0;
-  }
+  __syncthreads();
+  const int b = sh.sel_bin;
+  *bin = b < 0 ? 0 : b;
+  *above = b < 0 ? 0 : sh.sel_above;
 }
 
-__global__ __launch_bounds__(TS_THREADS) void topk_output_kernel(const float* __restrict__ scores, int stride,
+template <bool VEC>
+__global__ __launch_bounds__(TC_THREADS) void topk_output_kernel(const float* __restrict__ scores, int stride,
                                                                  const int* __restrict__ len, int len_div,
                                                                  int len_mul, int keep, int vis_only, int nchunks,
                                                                  int* __restrict__ hist,
@@ -387,168 +505,133 @@ __global__ __launch_bounds__(TS_THREADS) void topk_output_kernel(const float* __
   const int row = blockIdx.y, chunk = blockIdx.x;
   const int t = threadIdx.x, wave = t / WAVE, lane = t & (WAVE - 1);
   const int L = level_len(len, row, len_div, len_mul, stride);
-  const int base = chunk * TS_CHUNK;
-  // the row's meta in one round of loads (wave 0: lanes 0 .. 15 the chunk counts), counts clamped into range
-  if (wave == 0) {
-    int x = 0, y = 0;
-    if (lane < TS_MAXCH && lane < nchunks) {
-      x = meta[row].n_c[lane];
-      y = meta[row].n_a[lane];
-      x = x < 0 ? 0 : (x > TS_CHUNK ? TS_CHUNK : x);
-      y = y < 0 ? 0 : (y > TS_CHUNK ? TS_CHUNK : y);
-    }
-    int inc = x;  // prefix of the candidate counts (lanes 0 .. 15)
+  const int base = chunk * TC_CHUNK;
+  const int g = t >> 4, sub = t & 15;  // candidate group: chunk g, entries sub + 16 k
+  // one round of loads: the row's meta, the first TC_CAND candidates of every chunk, the chunk's own keys
+  const RowMeta& rm = meta[row];
+  const int c0 = rm.c0, above0 = rm.above0, nvis = rm.nvis;
+  const int l16 = lane & 15;
+  int na_l = rm.n_a[l16], nc_l = rm.n_c[l16];
+  const int live = 0 - (int)(l16 < nchunks);  // masks, not selects: the loads stay unconditional
+  na_l = min(max(na_l, 0), TC_CHUNK) & live;
+  nc_l = min(max(nc_l, 0), TC_CHUNK) & live;
+  const uint32_t* cg = ckey + ((size_t)row * TC_MAXCH + g) * TC_CHUNK;
+  uint32_t ck[TC_CAND / 16];
 #pragma unroll
-    for (int o = 1; o < 32; o <<= 1) {
-      const int u = __shfl_up(inc, o, WAVE);
-      if (lane >= o) inc += u;
-    }
-    int mx = x;
-#pragma unroll
-    for (int o = 16; o >= 1; o >>= 1) mx = max(mx, __shfl_xor(mx, o, WAVE));
-    if (lane < TS_MAXCH) {
-      sh.nc[lane] = x;
-      sh.na[lane] = y;
-      sh.off[lane] = inc - x;
-      sh.gt[lane] = 0;
-      sh.tie[lane] = 0;
-    }
-    if (lane == TS_MAXCH) sh.off[TS_MAXCH] = __shfl(inc, TS_MAXCH - 1, WAVE);
-    if (lane == 0) {
-      sh.c0 = meta[row].c0;
-      sh.above0 = meta[row].above0;
-      sh.nvis = meta[row].nvis;
-      sh.maxc = mx;
-    }
-  }
-  uint32_t key[TS_G][4];
-  load_chunk_keys(scores + (size_t)row * stride, L, base, (stride & 3) == 0, vis_only, key);
-  // leave the row's histogram zero for the next call (each chunk clears its share; every topk_chunk_kernel
-  // workgroup has read it)
+  for (int k = 0; k < TC_CAND / 16; ++k) ck[k] = cg[sub + 16 * k];
+  uint32_t key[2][4];
+  load_chunk_keys<VEC>(scores + (size_t)row * stride, stride, L, base, vis_only, key);
+  // leave the row's histogram zero for the next call (every topk_chunk_kernel workgroup has read it)
   int* hrow = hist + (size_t)row * TK_HBINS;
-  for (int i = chunk * TS_THREADS + t; i < TK_HBINS; i += nchunks * TS_THREADS) hrow[i] = 0;
-  __syncthreads();
-  const int c0 = sh.c0, nvis = sh.nvis;
+  for (int i = chunk * TC_THREADS + t; i < TK_HBINS; i += nchunks * TC_THREADS) hrow[i] = 0;
+
+  const int ncg = __shfl(nc_l, g, WAVE);  // this thread's candidate chunk's count (lane g < 16 holds it)
+  if (t < TC_MAXCH) sh.na[t] = na_l;
+  const int maxc = (int)wave_max_u32((uint32_t)nc_l);
   uint32_t T = 0;
   int room = 0;
   if (c0 >= 0 && nvis > keep) {
-    const uint32_t* crow = ckey + (size_t)row * TS_MAXCH * TS_CHUNK;
-    uint32_t lo = (uint32_t)c0 << TK_HSHIFT;
-    int need = keep - sh.above0;
-    if (sh.maxc <= TS_THREADS) {
-      // fast path: thread t holds the t-th candidate of every chunk (one round of 16 independent loads)
-      uint32_t v[TS_MAXCH];
+    int need = keep - above0;
+    // pass A: bits 19 .. 9 of the candidates (all in bin c0)
+    for (int i = t; i < 2048; i += TC_THREADS) sh.bins[i] = 0;
+    if (t == 0) sh.sel_bin = -1;
+    __syncthreads();
 #pragma unroll
-      for (int j = 0; j < TS_MAXCH; ++j) v[j] = (j < nchunks && t < sh.nc[j]) ? crow[j * TS_CHUNK + t] : 0u;
-#pragma unroll
-      for (int pass = 0; pass < 2; ++pass) {
-        constexpr int SB = TK_HSHIFT - TK_BITS;
-        const int nb = pass == 0 ? TK_BINS : (1 << SB);
-        for (int i = t; i < nb; i += TS_THREADS) sh.hist[i] = 0;
-        __syncthreads();
-        const uint32_t width = pass == 0 ? (1u << TK_HSHIFT) : (1u << SB);
-#pragma unroll
-        for (int j = 0; j < TS_MAXCH; ++j) {
-          const uint32_t d = v[j] - lo;
-          if (v[j] != 0u && d < width) atomicAdd(&sh.hist[pass == 0 ? (d >> SB) : d], 1);
-        }
-        __syncthreads();
-        if (wave == 0) wave0_find_bin(sh, nb, need);
-        __syncthreads();
-        lo += (uint32_t)sh.sel_c << (pass == 0 ? SB : 0);
-        need -= sh.sel_above;
-        __syncthreads();
+    for (int k = 0; k < TC_CAND / 16; ++k)
+      if (g < nchunks && sub + 16 * k < ncg) atomicAdd(&sh.bins[(ck[k] >> 9) & 2047], 1);
+    for (int r = 1; r * TC_CAND < maxc; ++r)  // rare: chunks with more than TC_CAND candidates
+      for (int k = 0; k < TC_CAND / 16; ++k) {
+        const int i = r * TC_CAND + sub + 16 * k;
+        if (g < nchunks && i < ncg) atomicAdd(&sh.bins[(cg[i] >> 9) & 2047], 1);
       }
-      T = lo;
-      room = need;
-      // per chunk: candidates above T and tied at T (ballots, one add per wave and chunk)
-#pragma unroll
-      for (int j = 0; j < TS_MAXCH; ++j) {
-        const uint64_t g = __ballot(v[j] != 0u && v[j] > T);
-        const uint64_t q = __ballot(v[j] != 0u && v[j] == T);
-        if (lane == 0 && (g | q)) {
-          atomicAdd(&sh.gt[j], __popcll(g));
-          atomicAdd(&sh.tie[j], __popcll(q));
-        }
-      }
-      __syncthreads();
-    } else {
-      // many keys in one 12-bit bin (ties): the same passes over the lists in global memory
-      for (int pass = 0; pass < 2; ++pass) {
-        constexpr int SB = TK_HSHIFT - TK_BITS;
-        const int nb = pass == 0 ? TK_BINS : (1 << SB);
-        for (int i = t; i < nb; i += TS_THREADS) sh.hist[i] = 0;
-        __syncthreads();
-        const uint32_t width = pass == 0 ? (1u << TK_HSHIFT) : (1u << SB);
-        for (int j = 0; j < nchunks; ++j)
-          for (int i = t; i < sh.nc[j]; i += TS_THREADS) {
-            const uint32_t k = crow[j * TS_CHUNK + i];
-            const uint32_t d = k - lo;
-            if (d < width) atomicAdd(&sh.hist[pass == 0 ? (d >> SB) : d], 1);
-          }
-        __syncthreads();
-        if (wave == 0) wave0_find_bin(sh, nb, need);
-        __syncthreads();
-        lo += (uint32_t)sh.sel_c << (pass == 0 ? SB : 0);
-        need -= sh.sel_above;
-        __syncthreads();
-      }
-      T = lo;
-      room = need;
-      for (int j = 0; j < nchunks; ++j)
-        for (int i = t; i < sh.nc[j]; i += TS_THREADS) {
-          const uint32_t k = crow[j * TS_CHUNK + i];
-          if (k > T) atomicAdd(&sh.gt[j], 1);
-          if (k == T) atomicAdd(&sh.tie[j], 1);
-        }
-      __syncthreads();
+    __syncthreads();
+    int c1, above;
+    out_find_bin(sh, 2048, need, &c1, &above);
+    need -= above;
+    const uint32_t pre = ((uint32_t)c0 << 11) | (uint32_t)c1;
+    __syncthreads();
+    for (int i = t; i < 512; i += TC_THREADS) sh.bins[i] = 0;
+    if (t == 0) sh.sel_bin = -1;
+    if (t < TC_MAXCH) {
+      sh.gt[t] = 0;
+      sh.tie[t] = 0;
     }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < TC_CAND / 16; ++k)
+      if (g < nchunks && sub + 16 * k < ncg && (ck[k] >> 9) == pre) atomicAdd(&sh.bins[ck[k] & 511], 1);
+    for (int r = 1; r * TC_CAND < maxc; ++r)
+      for (int k = 0; k < TC_CAND / 16; ++k) {
+        const int i = r * TC_CAND + sub + 16 * k;
+        if (g < nchunks && i < ncg && (cg[i] >> 9) == pre) atomicAdd(&sh.bins[cg[i] & 511], 1);
+      }
+    __syncthreads();
+    int c2;
+    out_find_bin(sh, 512, need, &c2, &above);
+    T = (pre << 9) | (uint32_t)c2;
+    room = need - above;
+    room = room < 0 ? 0 : room;
+    // per chunk: candidates above T and equal to T (a 16-lane group per chunk)
+    int gtc = 0, tic = 0;
+#pragma unroll
+    for (int k = 0; k < TC_CAND / 16; ++k)
+      if (sub + 16 * k < ncg) {
+        gtc += ck[k] > T;
+        tic += ck[k] == T;
+      }
+    for (int r = 1; r * TC_CAND < maxc; ++r)
+      for (int k = 0; k < TC_CAND / 16; ++k) {
+        const int i = r * TC_CAND + sub + 16 * k;
+        if (i < ncg) {
+          gtc += cg[i] > T;
+          tic += cg[i] == T;
+        }
+      }
+    gtc = row16_sum(gtc);  // the 16 lanes of a candidate group are one DPP row
+    tic = row16_sum(tic);
+    if (sub == 0 && g < nchunks) {
+      sh.gt[g] = gtc;
+      sh.tie[g] = tic;
+    }
+  } else if (t < TC_MAXCH) {
+    sh.gt[t] = 0;
+    sh.tie[t] = 0;
   }
+  __syncthreads();
   // this chunk's output base and the ties it may take
   int out_base = 0, ties_before = 0;
   for (int j = 0; j < chunk && j < nchunks; ++j) {
-    const int na = sh.na[j];
+    const int tj = sh.tie[j];
     int take = room - ties_before;
-    take = take < 0 ? 0 : (take > sh.tie[j] ? sh.tie[j] : take);
-    out_base += na + sh.gt[j] + take;
-    ties_before += sh.tie[j];
+    take = take < 0 ? 0 : (take > tj ? tj : take);
+    out_base += sh.na[j] + sh.gt[j] + take;
+    ties_before += tj;
   }
   int room_here = room - ties_before;
   room_here = room_here < 0 ? 0 : room_here;
 
-  // ordered output of the chunk: above T, and the first room_here keys equal to T
-  const uint64_t below = lanes_below();
-  uint64_t am[TS_G][4], tm[TS_G][4];
-  uint32_t cnt[TS_G];
+  // ordered output of the chunk: keys above T, and the first room_here keys equal to T
+  uint32_t mine[2], before[2];
 #pragma unroll
-  for (int e = 0; e < TS_G; ++e) {
+  for (int e = 0; e < 2; ++e) {
     uint32_t na = 0, nt = 0;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      am[e][c] = __ballot(key[e][c] > T);
-      tm[e][c] = __ballot(T != 0 && key[e][c] == T);
-      na += __popcll(am[e][c]);
-      nt += __popcll(tm[e][c]);
+      na += key[e][c] > T;
+      nt += T != 0u && key[e][c] == T;
     }
-    cnt[e] = (na << 16) | nt;
+    mine[e] = (na << 16) | nt;
   }
-  uint32_t bb[TS_G];
-  block_bases(cnt, sh.blk, bb);
-  const int cnt_row = nvis < 0 ? 0 : (nvis < keep ? nvis : keep);
+  chunk_prefix(mine, sh.blk, before);
   int* orow = idx_out + (size_t)row * keep;
 #pragma unroll
-  for (int e = 0; e < TS_G; ++e) {
-    int a_before = (int)(bb[e] >> 16), t_before = (int)(bb[e] & 0xffffu);
+  for (int e = 0; e < 2; ++e) {
+    int a_before = (int)(before[e] >> 16), t_before = (int)(before[e] & 0xffffu);
+    const int p0 = base + 4 * (TC_THREADS * e + t);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      a_before += __popcll(am[e][c] & below);
-      t_before += __popcll(tm[e][c] & below);
-    }
-    const int p0 = base + 4 * (TS_THREADS * e + t);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const bool a = (am[e][c] >> lane) & 1ull;
-      const bool ti = (tm[e][c] >> lane) & 1ull;
+      const bool a = key[e][c] > T;
+      const bool ti = T != 0u && key[e][c] == T;
       const bool sel = a || (ti && t_before < room_here);
       const int o = out_base + a_before + (t_before < room_here ? t_before : room_here);
       if (sel && (unsigned)o < (unsigned)keep) orow[o] = p0 + c;  // in range whatever the counts
@@ -557,7 +640,8 @@ __global__ __launch_bounds__(TS_THREADS) void topk_output_kernel(const float* __
     }
   }
   if (chunk == 0) {
-    for (int i = cnt_row + t; i < keep; i += TS_THREADS) orow[i] = 0;
+    const int cnt_row = nvis < 0 ? 0 : (nvis < keep ? nvis : keep);
+    for (int i = cnt_row + t; i < keep; i += TC_THREADS) orow[i] = 0;
     if (t == 0) cnt_out[row] = cnt_row;
   }
 }
@@ -627,7 +711,7 @@ __global__ void map_blocks_kernel(int* __restrict__ idx, const int* __restrict__
 }
 
 // One workgroup per row up to TOPK_FLAT_MAX scores; longer rows are selected in two levels, recursively.
-constexpr int TOPK_FLAT_MAX = 32 * TK_THREADS;
+constexpr int TOPK_FLAT_MAX = 4 * TR_MAXG * TR_THREADS;
 constexpr int TOPK_LONG_KEEP_MAX = 8192;
 
 static size_t up256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -641,19 +725,14 @@ static int topk_sub_block(long n, int keep) {
 }
 
 // Recursion plan shared by the workspace size and the launch.
-static bool topk_plan(long n, int keep, size_t* ws) {
-  if (n <= TOPK_FLAT_MAX) {
-    if (ws) *ws = 0;
-    return true;
-  }
+static bool topk_plan(long n, int keep) {
+  if (n <= TOPK_FLAT_MAX) return true;
   if (keep > TOPK_LONG_KEEP_MAX) return false;
   const int sub = topk_sub_block(n, keep);
   const long nb = (n + sub - 1) / sub, nc = (long)keep * sub;
   // level 1 (the sub-block maxima) runs flat; level 2 (the candidates) may split again
   if (nb > TOPK_FLAT_MAX || nc >= n) return false;
-  if (!topk_plan(nc, keep, nullptr)) return false;
-  if (ws) *ws = 0;
-  return true;
+  return topk_plan(nc, keep);
 }
 
 // Workspace of a selection: the first-level histograms [B, 4096] int (zero between calls), then the two-level
@@ -668,57 +747,81 @@ static size_t topk_level_bytes(int B, long n, int keep) {
 
 size_t topk_hist_bytes(int B) { return up256((size_t)B * TK_HBINS * 4); }
 
-// The flat selection's meta and candidate lists (after the histograms).
-static size_t topk_flat_bytes(int B) {
-  return up256((size_t)B * sizeof(RowMeta)) + up256((size_t)B * TS_MAXCH * TS_CHUNK * 4);
-}
-
 size_t topk_workspace_bytes(int B, int max_len, int keep) {
-  return topk_hist_bytes(B) + topk_flat_bytes(B) + topk_level_bytes(B, max_len, keep);
+  return topk_hist_bytes(B) + up256((size_t)B * sizeof(RowMeta)) + up256((size_t)B * TC_MAXCH * TC_CHUNK * 4) +
+         topk_level_bytes(B, max_len, keep);
 }
 
 bool topk_supported(int max_len, int keep, int vis_only) {
   if (keep < 1) return false;
   if (max_len <= TOPK_FLAT_MAX) return true;
-  return vis_only && topk_plan(max_len, keep, nullptr);
+  return vis_only && topk_plan(max_len, keep);
 }
 
-// The flat selection's buffers inside the top-k workspace: the first-level histograms [B, 4096] (zero between calls),
-// then the per-row meta and the candidate lists.
+// The flat selection's buffers inside the top-k workspace: the first-level histograms [B, 4096] (zero between
+// calls), then the per-row meta and the candidate lists of the chunked kernels.
 struct TopkBuffers {
   int* hist;
   RowMeta* meta;
   uint32_t* ckey;
 };
 
+template <int G, bool VEC>
+static hipError_t launch_topk_row(const float* scores, int stride, const int* len, int len_div, int len_mul,
+                                  int keep, int vis_only, int* hist, bool hist_ready, int* idx, int* cnt, int B,
+                                  hipStream_t s) {
+  if (hist_ready)
+    return launch("topk_row_kernel", topk_row_kernel<G, true, VEC>, dim3(B), dim3(TR_THREADS), s, scores, stride,
+                  len, len_div, len_mul, keep, vis_only, hist, idx, cnt);
+  return launch("topk_row_kernel", topk_row_kernel<G, false, VEC>, dim3(B), dim3(TR_THREADS), s, scores, stride, len,
+                len_div, len_mul, keep, vis_only, hist, idx, cnt);
+}
+
+template <bool VEC>
+static hipError_t launch_topk_chunked(const float* scores, int stride, const int* len, int len_div, int len_mul,
+                                      int nch, int keep, int vis_only, int* idx, int* cnt, const TopkBuffers& tb,
+                                      bool hist_ready, int B, hipStream_t s) {
+  hipError_t e;
+  if (!hist_ready) {
+    e = launch("topk_hist_kernel", topk_hist_kernel, dim3(nch, B), dim3(TKH_THREADS), s, scores, stride, len, len_div,
+               len_mul, vis_only, tb.hist);
+    if (e != hipSuccess) return e;
+  }
+  e = launch("topk_chunk_kernel", topk_chunk_kernel<VEC>, dim3(nch, B), dim3(TC_THREADS), s, scores, stride, len,
+             len_div, len_mul, keep, vis_only, tb.hist, tb.meta, tb.ckey);
+  if (e != hipSuccess) return e;
+  return launch("topk_output_kernel", topk_output_kernel<VEC>, dim3(nch, B), dim3(TC_THREADS), s, scores, stride, len,
+                len_div, len_mul, keep, vis_only, nch, tb.hist, tb.meta, tb.ckey, idx, cnt);
+}
+
+
+// The flat selection of rows of at most max_len <= TOPK_FLAT_MAX scores: one workgroup per row up to 4096 scores,
+// the chunked kernels above that.
 static hipError_t launch_topk_level(const float* scores, int stride, const int* len, int len_div, int len_mul,
                                     int max_len, int keep, int vis_only, int* idx, int* cnt, const TopkBuffers& tb,
                                     bool hist_ready, int B, hipStream_t s) {
-  if (max_len > TS_MAXCH * TS_CHUNK) return hipErrorInvalidValue;
-  const int nch = (max_len + TS_CHUNK - 1) / TS_CHUNK < 1 ? 1 : (max_len + TS_CHUNK - 1) / TS_CHUNK;
-  if (!hist_ready) {
-    launch("topk_hist_kernel", topk_hist_kernel, dim3(nch, B), dim3(TKH_THREADS), s, scores, stride, len, len_div, len_mul,
-                       vis_only, tb.hist);
-    const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-  }
-  launch("topk_chunk_kernel", topk_chunk_kernel, dim3(nch, B), dim3(TS_THREADS), s, scores, stride, len, len_div, len_mul,
-                     keep, vis_only, tb.hist, tb.meta, tb.ckey);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  launch("topk_output_kernel", topk_output_kernel, dim3(nch, B), dim3(TS_THREADS), s, scores, stride, len, len_div, len_mul,
-                     keep, vis_only, nch, tb.hist, tb.meta, tb.ckey, idx, cnt);
-  return hipGetLastError();
+  const bool vec = (stride & 3) == 0 && stride >= 4;
+  if (max_len <= 4 * TR_THREADS)
+    return vec ? launch_topk_row<1, true>(scores, stride, len, len_div, len_mul, keep, vis_only, tb.hist, hist_ready,
+                                          idx, cnt, B, s)
+               : launch_topk_row<1, false>(scores, stride, len, len_div, len_mul, keep, vis_only, tb.hist, hist_ready,
+                                           idx, cnt, B, s);
+  if (max_len > TC_MAXCH * TC_CHUNK) return hipErrorInvalidValue;
+  const int nch = (max_len + TC_CHUNK - 1) / TC_CHUNK;
+  return vec ? launch_topk_chunked<true>(scores, stride, len, len_div, len_mul, nch, keep, vis_only, idx, cnt, tb,
+                                         hist_ready, B, s)
+             : launch_topk_chunked<false>(scores, stride, len, len_div, len_mul, nch, keep, vis_only, idx, cnt, tb,
+                                          hist_ready, B, s);
 }
 
-// Selection over rows of `stride` scores whose lengths are len[row] (len_div / len_mul as in topk_kernel), n an upper
+// Selection over rows of `stride` scores whose lengths are len[row] (len_div / len_mul as in level_len), n an upper
 // bound of the lengths.
 static hipError_t topk_rows(const float* scores, int stride, const int* len, int len_div, int len_mul, long n,
                             int keep, int vis_only, int* idx, int* cnt, const TopkBuffers& tb, bool hist_ready,
                             char* ws, int B, hipStream_t s) {
   if (n <= TOPK_FLAT_MAX)
-    return launch_topk_level(scores, stride, len, len_div, len_mul, (int)n, keep, vis_only, idx, cnt, tb,
-                             hist_ready, B, s);
+    return launch_topk_level(scores, stride, len, len_div, len_mul, (int)n, keep, vis_only, idx, cnt, tb, hist_ready,
+                             B, s);
   if (len_div != 1 || len_mul != 1) return hipErrorInvalidValue;  // only flat rows are split
   const int sub = topk_sub_block(n, keep);
   const int nb = (int)((n + sub - 1) / sub), nc = keep * sub;
@@ -730,26 +833,25 @@ static hipError_t topk_rows(const float* scores, int stride, const int* len, int
   ws += up256((size_t)B * 4);
   float* cand = reinterpret_cast<float*>(ws);
   ws += up256((size_t)B * nc * 4);
-  launch("block_max_kernel", block_max_kernel, dim3((nb + 255) / 256, B), dim3(256), s, scores, stride, len, sub, nb, bm);
-  hipError_t e = hipGetLastError();
+  hipError_t e = launch("block_max_kernel", block_max_kernel, dim3((nb + 255) / 256, B), dim3(256), s, scores,
+                        stride, len, sub, nb, bm);
   if (e != hipSuccess) return e;
   // level 1: the top-keep sub-blocks (ceil(len / sub) maxima per row)
   if (nb > TOPK_FLAT_MAX) return hipErrorInvalidValue;  // excluded by topk_plan
   e = launch_topk_level(bm, nb, len, sub, 1, nb, keep, vis_only, bidx, bcnt, tb, false, B, s);
   if (e != hipSuccess) return e;
-  launch("gather_blocks_kernel", gather_blocks_kernel, dim3((nc + 255) / 256, B), dim3(256), s, scores, stride, len, sub, bidx,
-                     bcnt, keep, cand);
-  e = hipGetLastError();
+  e = launch("gather_blocks_kernel", gather_blocks_kernel, dim3((nc + 255) / 256, B), dim3(256), s, scores, stride,
+             len, sub, bidx, bcnt, keep, cand);
   if (e != hipSuccess) return e;
   // level 2: the top-keep of the selected sub-blocks' scores in position order (NEG_INF past their count)
   e = topk_rows(cand, nc, nullptr, 1, 1, nc, keep, vis_only, idx, cnt, tb, false, ws, B, s);
   if (e != hipSuccess) return e;
-  launch("map_blocks_kernel", map_blocks_kernel, dim3((keep + 255) / 256, B), dim3(256), s, idx, cnt, bidx, sub, keep);
-  return hipGetLastError();
+  return launch("map_blocks_kernel", map_blocks_kernel, dim3((keep + 255) / 256, B), dim3(256), s, idx, cnt, bidx,
+                sub, keep);
 }
 
 // ws: topk_workspace_bytes(B, max_len, keep) bytes whose histogram region is zero; hist_ready: the histogram of the
-// rows is already accumulated there (by the indexer), so the first level skips its histogram kernel.
+// rows is already accumulated there (by the indexer), so the first level does not build it.
 hipError_t launch_topk(const float* scores, const int* len, int* idx, int* cnt, void* ws, int B, int stride,
                        int max_len, int keep, int vis_only, bool hist_ready, hipStream_t s) {
   char* p = static_cast<char*>(ws);
@@ -760,7 +862,7 @@ hipError_t launch_topk(const float* scores, const int* len, int* idx, int* cnt, 
   tb.meta = reinterpret_cast<RowMeta*>(p);
   p += up256((size_t)B * sizeof(RowMeta));
   tb.ckey = reinterpret_cast<uint32_t*>(p);
-  p += up256((size_t)B * TS_MAXCH * TS_CHUNK * 4);
+  p += up256((size_t)B * TC_MAXCH * TC_CHUNK * 4);
   return topk_rows(scores, stride, len, 1, 1, max_len, keep, vis_only, idx, cnt, tb, hist_ready, p, B, s);
 }
 
