@@ -10,7 +10,8 @@ hipError_t launch_indexer_decode(const uint16_t* q, const float* w, const uint8_
                                  int B, int Hi, int max_pages, int page_size, int num_pages, int stride, int num_cu,
                                  hipStream_t stream);
 hipError_t launch_topk(const float* scores, const int* len, int* idx, int* cnt, void* ws, int B, int stride,
-                       int max_len, int keep, int vis_only, bool hist_ready, hipStream_t s);
+                       int max_len, int keep, int vis_only, bool hist_ready, const int* table, int max_pages,
+                       int page_size, int num_pages, int* rows_out, hipStream_t s);
 hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t s);
 hipError_t launch_topk_mask(const int* idx, const int* cnt, float* mask, int B, int keep, int P, hipStream_t s);
 size_t topk_workspace_bytes(int B, int max_len, int keep);
@@ -41,6 +42,9 @@ int num_cu() {
 int status(hipError_t e) { return e == hipSuccess ? DSA_OK : DSA_ELAUNCH; }
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// The layer's slot-id buffer [B, keep] int32 (between the top-k and the attention workspaces).
+size_t layer_rows_bytes(int B, int keep) { return align256((size_t)B * keep * 4); }
 
 int resolve_splits(int splits, int B, int H, int keep) {
   if (splits <= 0) splits = dsa::attention_default_splits(B, H, keep, num_cu());
@@ -124,7 +128,8 @@ int dsa_topk(const float* scores, const int32_t* len, int32_t* idx, int32_t* cnt
   if (!workspace || workspace_bytes < need) return DSA_EWORKSPACE;
   if (B == 0) return DSA_OK;
   return status(dsa::launch_topk(scores, len, idx, cnt, workspace, B, score_stride, max_len, keep, vis_only ? 1 : 0,
-                                 false, static_cast<hipStream_t>(stream)));
+                                 false, nullptr, 0, 0, 0, nullptr,
+                                 static_cast<hipStream_t>(stream)));
 }
 
 int dsa_workspace_clear(void* workspace, size_t workspace_bytes, void* stream) {
@@ -179,6 +184,7 @@ size_t dsa_workspace_bytes(int kind, int B, int H, int keep, int max_len, int sp
   if (B < 0 || keep < 1) return 0;
   size_t t = 0, a = 0;
   if (kind == DSA_WS_TOPK || kind == DSA_WS_LAYER) t = dsa::topk_workspace_bytes(B, max_len, keep);
+  if (kind == DSA_WS_LAYER) t = align256(t) + layer_rows_bytes(B, keep);
   if (kind == DSA_WS_ATTENTION || kind == DSA_WS_LAYER) {
     if (H < 16) return align256(t);
     const int sp = effective_splits(resolve_splits(splits, B, H, keep), keep);
@@ -213,12 +219,25 @@ int dsa_decode_layer(const void* q_idx_bf16, const float* w, const uint8_t* k_fp
                                             ctx_len, nullptr, scores, fused_hist ? static_cast<int*>(workspace) : nullptr,
                                             B, Hi, max_pages, page_size, num_pages, score_stride, num_cu(), s);
   if (e != hipSuccess) return DSA_ELAUNCH;
-  e = dsa::launch_topk(scores, ctx_len, idx, cnt, workspace, B, score_stride, max_len, keep, 1, fused_hist, s);
+  // flat rows: the top-k also resolves the selected positions to cache slots, so the attention reads slot ids
+  // directly (one dependent load round fewer)
+  int* rows = fused_hist ? reinterpret_cast<int*>(static_cast<char*>(workspace) + t_need) : nullptr;
+  e = dsa::launch_topk(scores, ctx_len, idx, cnt, workspace, B, score_stride, max_len, keep, 1, fused_hist,
+                       page_table, max_pages, page_size, num_pages, rows, s);
   if (e != hipSuccess) return DSA_ELAUNCH;
-  char* aws = static_cast<char*>(workspace) + t_need;
-  return dsa_sparse_mla_decode(q_bf16, kv_fp8, kv_scale, idx, cnt, page_table, nullptr, nullptr, out_bf16, nullptr,
-                               lse, aws, workspace_bytes - t_need, B, H, 576, 512, keep, max_pages, page_size,
-                               num_pages, scale, splits, stream);
+  char* aws = static_cast<char*>(workspace) + t_need + layer_rows_bytes(B, keep);
+  const size_t aws_bytes = workspace_bytes - t_need - layer_rows_bytes(B, keep);
+  if (!rows)
+    return dsa_sparse_mla_decode(q_bf16, kv_fp8, kv_scale, idx, cnt, page_table, nullptr, nullptr, out_bf16, nullptr,
+                                 lse, aws, aws_bytes, B, H, 576, 512, keep, max_pages, page_size, num_pages, scale,
+                                 splits, stream);
+  if (!q_bf16 || !kv_fp8 || !kv_scale || !out_bf16) return DSA_EINVAL;
+  if (H < 1 || H % 16) return DSA_EUNSUPPORTED;
+  if ((long)num_pages * page_size > 0x7fffffffL) return DSA_EUNSUPPORTED;
+  const int sp = effective_splits(resolve_splits(splits, B, H, keep), keep);
+  return status(dsa::launch_sparse_mla(static_cast<const uint16_t*>(q_bf16), kv_fp8, kv_scale, nullptr, cnt, nullptr,
+                                       rows, nullptr, static_cast<uint16_t*>(out_bf16), nullptr, lse, aws, B, H, keep,
+                                       max_pages, page_size, num_pages, scale, sp, s));
 }
 
 }  // extern "C"

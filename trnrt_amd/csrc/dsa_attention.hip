@@ -5,16 +5,22 @@
 //   s[h, k] = scale * q[h, :] . K[k] + bias[k],  K[k] = kv_fp8[slot_k] * kv_scale[slot_k]
 //   o[h, :] = sum_k softmax_k(s)[h, k] * K[k][:512],  lse[h] = max_k s + log sum_k exp(s - max)
 //
-// Work unit: one workgroup = one sequence, 16 query heads, one split of the selected slots (split-K), in chunks of
-// 64 slots. Per chunk the 64 gathered rows are staged in LDS twice: token-major (e4m3 bytes, for the score product
-// whose contraction runs over a row) and dim-major for the first 512 columns (for the value product, whose
-// contraction runs over the tokens; an in-register 4x4 byte transpose through LDS). Both products run on
-// v_mfma_f32_16x16x32_bf16 with e4m3 -> bf16 conversions in registers (exact).
-//   - scores: S^T[token, head] = K . Q^T; wave w takes tokens 16w .. 16w + 15 of the chunk, all 16 heads, the 576
-//     dims in 18 steps (dims permuted so a lane reads 144 contiguous bytes of its row; q uses the same permutation);
-//   - online softmax in fp32 with the chunk maximum shared through LDS (every wave applies the same rescale);
+// Work unit: one workgroup = one sequence, 16 query heads, one split of the selected slots (split-K), 8 waves.
+// The split's slot ids and the queries come in one round of loads; then the rows of up to 256 slots (4 chunks of 64)
+// are gathered straight into LDS by direct-to-LDS loads (global_load_lds_dwordx4: consecutive lanes read
+// consecutive 16-byte pieces of a row, no register staging), all issued at once, so the workgroup waits for memory
+// twice: slot ids, then rows. A chunk is token-major e4m3 with a 592-byte row stride (36 pieces and one padding
+// piece, filled with a copy of piece 35), which spreads the operand reads over the LDS banks. Both products run on
+// v_mfma_f32_16x16x32_bf16 with e4m3 -> bf16 conversions in registers (exact):
+//   - scores: S^T[token, head] = K . Q^T; 16 tokens per wave, all 16 heads, the 576 dims in 18 steps of 32 (at each
+//     step the four lane groups read consecutive 8-byte pieces of a row, so lanes 0-31 and 32-63 each cover every
+//     LDS bank once; q staged once through LDS);
+//   - online softmax in fp32 with the chunk maximum shared through LDS;
 //   - value: O[head, dim] += P . V with P = exp(s - m) * kv_scale rounded to bf16 (the dequantisation of the value
-//     folded into the weight), wave w takes dims 128w .. 128w + 127.
+//     folded into the weight), its operand read transposed from the token-major rows by ds_read_b64_tr_b8.
+// The two halves of the workgroup (waves 0-3, 4-7) take alternate chunks, each with its own running max, sum and
+// output, merged at the end; within a half, wave w takes tokens 16w .. 16w + 15 for the scores and dims
+// 128w .. 128w + 127 for the value product.
 // With one split the workgroup writes bf16 o and lse; with several it writes fp32 partial o (normalised) with its
 // running max and sum, and a combine kernel merges them by log-sum-exp (trnrt/models/mla.py:853-856, 1152-1160).
 #include "dsa_common.h"
@@ -25,24 +31,27 @@ constexpr int ATT_DQK = 576;
 constexpr int ATT_DV = 512;
 constexpr int ATT_HPW = 16;       // heads per workgroup
 constexpr int ATT_CH = 64;        // slots per chunk
-constexpr int ATT_THREADS = 256;  // 4 waves
-constexpr int ATT_SUPER = 256;    // slots whose ids / scales / biases are set up at once (one per thread)
-constexpr int ATT_PIECES = ATT_DQK / 16;  // 16-byte pieces of a row
-constexpr int ATT_RPT = ATT_CH * ATT_PIECES / ATT_THREADS;  // pieces per thread per chunk (9)
-// Token-major row stride: 146 dwords, so the staging writes, the score operand reads and the transposing value
-// reads of rows 0..31 spread over the banks (at most 2-way).
-constexpr int ATT_KROW = ATT_DQK + 8;   // bytes
-constexpr int ATT_PROW = ATT_CH + 8;    // P row stride (bf16 elements; 16-byte aligned rows)
+constexpr int ATT_THREADS = 512;  // 8 waves: two halves of 4
+constexpr int ATT_NCH = 4;        // chunks staged in LDS at once
+constexpr int ATT_SUPER = ATT_NCH * ATT_CH;  // slots staged at once
+constexpr int ATT_PIECES = ATT_DQK / 16;     // 36 16-byte pieces per row
+constexpr int ATT_KPIECES = ATT_PIECES + 1;  // LDS row: the pieces and one padding piece
+constexpr int ATT_KROW = 16 * ATT_KPIECES;   // 592 bytes
+constexpr int ATT_CHUNK_BYTES = ATT_CH * ATT_KROW;  // 37,888: 37 direct-to-LDS instructions of 1 KiB
+constexpr int ATT_LOADS = ATT_NCH * ATT_KPIECES;    // 148 instructions per staged super-chunk
+constexpr int ATT_PROW = ATT_CH + 8;         // P row stride (bf16 elements; 16-byte aligned rows)
+constexpr int ATT_QROW = ATT_DQK + 8;        // staged query row stride (bf16 elements)
 
 typedef int att_v2i __attribute__((ext_vector_type(2)));
 
 struct AttShared {
-  uint8_t kt[ATT_CH * ATT_KROW];   // token-major e4m3 rows of the chunk
-  uint16_t p[ATT_HPW * ATT_PROW];  // bf16 P[head][token]
+  uint8_t kt[ATT_NCH][ATT_CHUNK_BYTES];  // token-major e4m3 rows of the staged chunks (q before them)
+  uint16_t p[2][ATT_HPW * ATT_PROW];     // per half: bf16 P[head][token]
   int slot[ATT_SUPER];
   float kscale[ATT_SUPER];
   float bias[ATT_SUPER];
-  float red[4][ATT_HPW];
+  float red[2][4][ATT_HPW];
+  float ml[2][ATT_HPW];  // the second half's final max and sum per head, for the merge
 };
 
 // The value operand of v_mfma_f32_16x16x32_bf16 straight from the token-major tile: ds_read_b64_tr_b8 gives lane
@@ -56,7 +65,9 @@ __device__ __forceinline__ bf16x8 value_operand(const uint8_t* kt, int ks, int n
   return fp8x8_to_bf16x8((uint32_t)r.x, (uint32_t)r.y);
 }
 
-__global__ __launch_bounds__(ATT_THREADS, 2) void sparse_mla_kernel(
+// Slot forms: token (idx + cnt + table: positions through the page table, bias 0 below cnt), rows + bias (cache
+// slots with an additive bias), rows + cnt (cache slots, bias 0 below cnt).
+__global__ __launch_bounds__(ATT_THREADS, 1) void sparse_mla_kernel(
     const uint16_t* __restrict__ q, const uint8_t* __restrict__ kv, const float* __restrict__ kvs,
     const int* __restrict__ idx, const int* __restrict__ cnt, const int* __restrict__ table,
     const int* __restrict__ rows, const float* __restrict__ bias, uint16_t* __restrict__ out,
@@ -76,192 +87,251 @@ __global__ __launch_bounds__(ATT_THREADS, 2) void sparse_mla_kernel(
   const int b = gi / splits, sp = gi - b * splits;
 
   const int tid = threadIdx.x, wave = tid / WAVE, lane = tid & (WAVE - 1);
+  const int half = wave >> 2, wh = wave & 3;  // the half (alternate chunks) and the wave within it
   const int l16 = lane & 15, q4 = lane >> 4;
   const bool token_form = rows == nullptr;
   int n_eff = keep;
   int cnt_b = keep;
-  if (token_form) {
+  if (cnt) {
     cnt_b = cnt[b];
-    int c = cnt_b < 1 ? 1 : (cnt_b > keep ? keep : cnt_b);  // cnt 0: attend slot 0, fully masked
-    n_eff = c;
+    if (!bias) n_eff = cnt_b < 1 ? 1 : (cnt_b > keep ? keep : cnt_b);  // cnt 0: attend slot 0, fully masked
   }
   const int k_begin = sp * slots_per_split;
   const int k_end = min(k_begin + slots_per_split, n_eff);
+  const size_t nslots_cache = (size_t)num_pages * page_size;
 
-  // query operand: head 16hg + l16, dims 144 q4 + 8 st .. + 7 at step st
-  const int head_b = ATT_HPW * hg + l16;
-  bf16x8 qb[18];
-  {
-    const uint4* qp = reinterpret_cast<const uint4*>(q + ((size_t)b * H + head_b) * ATT_DQK + 144 * q4);
+  // the queries of the 16 heads (18 KiB): 36 bytes per thread, staged through LDS below
+  const uint4* qsrc = reinterpret_cast<const uint4*>(q + ((size_t)b * H + ATT_HPW * hg) * ATT_DQK);
+  constexpr int QPIECES = ATT_HPW * ATT_DQK / 8;  // 16-byte pieces: 1152
+  uint4 qv[3];
 #pragma unroll
-    for (int st = 0; st < 18; ++st) qb[st] = as_bf16x8(qp[st]);
-  }
+  for (int i = 0; i < 3; ++i) qv[i] = qsrc[min(tid + ATT_THREADS * i, QPIECES - 1)];
 
+  bf16x8 qb[18];
   f32x4 o[8];
 #pragma unroll
   for (int n = 0; n < 8; ++n) o[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  float m_run = -INFINITY;  // running max of head l16 (the same in every wave)
-  float l_run = 0.0f;       // this lane's share of the running sum of head l16
+  float m_run = -INFINITY;  // running max of head l16 over this half's chunks (the same in its 4 waves)
+  float l_run = 0.0f;       // this lane's share of the half's running sum of head l16
 
   const int* trow = table ? table + (size_t)b * max_pages : nullptr;
   for (int sc0 = k_begin; sc0 < k_end; sc0 += ATT_SUPER) {
     const int nslots = min(ATT_SUPER, k_end - sc0);
     const int nch = (nslots + ATT_CH - 1) / ATT_CH;
-    // slots, scales and biases of the super-chunk: one per thread
-    {
-      const int k = sc0 + tid;
-      int slot = -1;
-      float bs = -INFINITY;  // past the split: weight exactly 0 (a copy of the super-chunk's first row)
-      if (tid < nslots) {
-        if (token_form) {
-          int pos = idx[(size_t)b * keep + k];
-          pos = pos < 0 ? 0 : pos;
-          int pi = pos / page_size;
-          pi = pi < max_pages ? pi : max_pages - 1;
-          slot = safe_page(trow[pi], num_pages) * page_size + (pos - (pos / page_size) * page_size);
-          bs = (k < cnt_b) ? 0.0f : NEG_INF;
-        } else {
-          slot = rows[(size_t)b * keep + k];
-          slot = ((unsigned)slot < (unsigned)(num_pages * page_size)) ? slot : 0;
-          bs = bias[(size_t)b * keep + k];
-        }
+    // slot ids and biases, one per thread of the first 256 (past the split: slot 0's row with weight exactly 0)
+    if (tid < ATT_SUPER) {
+      const int k = min(sc0 + tid, keep - 1);
+      int slot;
+      float bs;
+      if (token_form) {
+        int pos = idx[(size_t)b * keep + k];
+        pos = pos < 0 ? 0 : pos;
+        int pi = pos / page_size;
+        pi = pi < max_pages ? pi : max_pages - 1;
+        slot = safe_page(trow[pi], num_pages) * page_size + (pos - (pos / page_size) * page_size);
+        bs = (k < cnt_b) ? 0.0f : NEG_INF;
+      } else {
+        slot = rows[(size_t)b * keep + k];
+        slot = ((size_t)(unsigned)slot < nslots_cache) ? slot : 0;
+        bs = bias ? bias[(size_t)b * keep + k] : ((k < cnt_b) ? 0.0f : NEG_INF);
       }
       sh.slot[tid] = slot;
-      sh.bias[tid] = bs;
-      __syncthreads();
-      if (slot < 0) slot = sh.slot[0];  // slot 0 of a super-chunk is always real
-      __syncthreads();
-      sh.slot[tid] = slot;
-      sh.kscale[tid] = kvs[slot];
+      sh.bias[tid] = tid < nslots ? bs : -INFINITY;
     }
     __syncthreads();
-    // the chunk's rows in registers (thread tid holds 16-byte pieces tid + 256 j), one chunk ahead of the tile
-    uint4 rv[ATT_RPT];
-    auto load_rows = [&](int c) {
+    if (sc0 == k_begin) {
+      // query operand: head 16hg + l16, dims 32 st + 8 q4 .. + 7 at step st, through the rows' LDS (q rows padded
+      // to 584 elements so the operand reads spread over the banks)
+      uint16_t* qs = reinterpret_cast<uint16_t*>(sh.kt[ATT_NCH - 1]);
 #pragma unroll
-      for (int jj = 0; jj < ATT_RPT; ++jj) {
-        const int i = tid + ATT_THREADS * jj;
-        const int r = i / ATT_PIECES, pc = i - r * ATT_PIECES;
-        rv[jj] = *reinterpret_cast<const uint4*>(kv + (size_t)sh.slot[c * ATT_CH + r] * ATT_DQK + 16 * pc);
+      for (int i = 0; i < 3; ++i) {
+        const int pc = tid + ATT_THREADS * i;  // 16-byte piece: head pc / 72, elements 8 (pc % 72) ..
+        if (pc < QPIECES)
+          *reinterpret_cast<uint4*>(qs + (pc / 72) * ATT_QROW + 8 * (pc % 72)) = qv[i];
       }
-    };
-    load_rows(0);
-
-    for (int c = 0; c < nch; ++c) {
-      const int cb = c * ATT_CH;  // the chunk's first slot inside the super-chunk
+      __syncthreads();
+      const uint16_t* qh = qs + l16 * ATT_QROW + 8 * q4;
 #pragma unroll
-      for (int jj = 0; jj < ATT_RPT; ++jj) {
-        const int i = tid + ATT_THREADS * jj;
-        const int r = i / ATT_PIECES, pc = i - r * ATT_PIECES;
-        uint8_t* dst = &sh.kt[r * ATT_KROW + 16 * pc];
-        *reinterpret_cast<uint2*>(dst) = make_uint2(rv[jj].x, rv[jj].y);
-        *reinterpret_cast<uint2*>(dst + 8) = make_uint2(rv[jj].z, rv[jj].w);
+      for (int st = 0; st < 18; ++st) qb[st] = as_bf16x8(*reinterpret_cast<const uint4*>(qh + 32 * st));
+      __syncthreads();  // every wave holds its operand before the rows overwrite it
+    }
+    // every staged row straight into LDS: instruction kk (chunk kk / 37, 1-KiB block j = kk % 37 of its tile) has
+    // lane l load 16-byte unit u = 64 j + l of the tile: row u / 37, piece u % 37 (the padding piece re-reads 35);
+    // the 148 instructions are spread over the 8 waves
+    {
+      int src_slot[(ATT_LOADS + 7) / 8];
+#pragma unroll
+      for (int i = 0; i < (ATT_LOADS + 7) / 8; ++i) {
+        const int kk = min(wave + 8 * i, ATT_LOADS - 1);
+        const int c = kk / ATT_KPIECES, j = kk - c * ATT_KPIECES;
+        const int rr = c * ATT_CH + (WAVE * j + lane) / ATT_KPIECES;
+        src_slot[i] = sh.slot[rr < nslots ? rr : 0];
       }
-      __syncthreads();  // the tile is complete
-      if (c + 1 < nch) load_rows(c + 1);  // the next chunk's loads fly while this one computes
-
-      // scores of tokens 16 wave .. 16 wave + 15, heads l16
-      f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-      {
-        const uint8_t* kr = &sh.kt[(16 * wave + l16) * ATT_KROW + 144 * q4];
 #pragma unroll
-        for (int st = 0; st < 18; ++st) {
-          const uint2 kb = *reinterpret_cast<const uint2*>(kr + 8 * st);
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16x8(kb.x, kb.y), qb[st], acc, 0, 0, 0);
+      for (int i = 0; i < (ATT_LOADS + 7) / 8; ++i) {
+        const int kk = wave + 8 * i;
+        const int c = kk / ATT_KPIECES, j = kk - c * ATT_KPIECES;
+        if (kk < ATT_LOADS && c < nch) {
+          const int u = WAVE * j + lane;
+          const int pc = u - (u / ATT_KPIECES) * ATT_KPIECES;
+          const uint8_t* src = kv + (size_t)src_slot[i] * ATT_DQK + 16 * (pc < ATT_PIECES ? pc : ATT_PIECES - 1);
+          __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)&sh.kt[c][1024 * j], 16, 0,
+                                           0);
         }
       }
-      // acc[r] = S^T[token 16 wave + 4 q4 + r][head l16]
-      float s4[4];
-      float mx = -INFINITY;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int tk = cb + 16 * wave + 4 * q4 + r;
-        s4[r] = acc[r] * (sh.kscale[tk] * scale) + sh.bias[tk];
-        mx = fmaxf(mx, s4[r]);
-      }
-      mx = fmaxf(mx, __shfl_xor(mx, 16, WAVE));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
-      if (lane < ATT_HPW) sh.red[wave][lane] = mx;
-      __syncthreads();  // the chunk maxima
-      const float mc = fmaxf(fmaxf(sh.red[0][l16], sh.red[1][l16]), fmaxf(sh.red[2][l16], sh.red[3][l16]));
-      const float m_new = fmaxf(m_run, mc);
-      const float alpha = __expf(m_run - m_new);
-      m_run = m_new;
-      float psum = 0.0f;
-      uint32_t pk[2];
-#pragma unroll
-      for (int r = 0; r < 4; r += 2) {
-        const int tk = cb + 16 * wave + 4 * q4 + r;
-        const float p0 = __expf(s4[r] - m_new), p1 = __expf(s4[r + 1] - m_new);
-        psum += p0 + p1;
-        pk[r / 2] = (uint32_t)f32_to_bf16_bits(p0 * sh.kscale[tk]) |
-                    ((uint32_t)f32_to_bf16_bits(p1 * sh.kscale[tk + 1]) << 16);
-      }
-      l_run = l_run * alpha + psum;
-      *reinterpret_cast<uint2*>(&sh.p[l16 * ATT_PROW + 16 * wave + 4 * q4]) = make_uint2(pk[0], pk[1]);
-      __syncthreads();  // P complete
+    }
+    const float ksc = tid < ATT_SUPER ? kvs[sh.slot[tid < nslots ? tid : 0]] : 0.0f;
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's rows are in LDS
+    if (tid < ATT_SUPER) sh.kscale[tid] = ksc;
+    __syncthreads();  // every wave's rows are in LDS
 
-      // rescale O (rows = heads 4 q4 + r) and accumulate P . V over the chunk's 64 tokens (dims 128 wave ..)
-      float al[4];
+    for (int c0 = 0; c0 < nch; c0 += 2) {
+      const int c = c0 + half;  // this half's chunk of the pair
+      const bool live = c < nch;
+      const int cb = c * ATT_CH;
+      const uint8_t* kt = sh.kt[live ? c : 0];
+      float s4[4];
+      float alpha = 1.0f;
+      if (live) {
+        // scores of tokens 16 wh .. 16 wh + 15, heads l16 (two accumulators: independent MFMA chains)
+        f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
+        const uint8_t* kr = kt + (16 * wh + l16) * ATT_KROW + 8 * q4;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) al[r] = __shfl(alpha, 4 * q4 + r, WAVE);
+        for (int st = 0; st < 18; st += 2) {
+          const uint2 ka = *reinterpret_cast<const uint2*>(kr + 32 * st);
+          const uint2 kb = *reinterpret_cast<const uint2*>(kr + 32 * st + 32);
+          acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16x8(ka.x, ka.y), qb[st], acc0, 0, 0, 0);
+          acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16x8(kb.x, kb.y), qb[st + 1], acc1, 0, 0, 0);
+        }
+        // acc[r] = S^T[token 16 wh + 4 q4 + r][head l16]
+        float mx = -INFINITY;
 #pragma unroll
-      for (int n = 0; n < 8; ++n)
+        for (int r = 0; r < 4; ++r) {
+          const int tk = cb + 16 * wh + 4 * q4 + r;
+          s4[r] = (acc0[r] + acc1[r]) * (sh.kscale[tk] * scale) + sh.bias[tk];
+          mx = fmaxf(mx, s4[r]);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, WAVE));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
+        if (lane < ATT_HPW) sh.red[half][wh][lane] = mx;
+      }
+      __syncthreads();  // the chunk maxima
+      if (live) {
+        const float mc = fmaxf(fmaxf(sh.red[half][0][l16], sh.red[half][1][l16]),
+                               fmaxf(sh.red[half][2][l16], sh.red[half][3][l16]));
+        const float m_new = fmaxf(m_run, mc);
+        alpha = __expf(m_run - m_new);
+        m_run = m_new;
+        float psum = 0.0f;
+        uint32_t pk[2];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) o[n][r] *= al[r];
+        for (int r = 0; r < 4; r += 2) {
+          const int tk = cb + 16 * wh + 4 * q4 + r;
+          const float p0 = __expf(s4[r] - m_new), p1 = __expf(s4[r + 1] - m_new);
+          psum += p0 + p1;
+          pk[r / 2] = (uint32_t)f32_to_bf16_bits(p0 * sh.kscale[tk]) |
+                      ((uint32_t)f32_to_bf16_bits(p1 * sh.kscale[tk + 1]) << 16);
+        }
+        l_run = l_run * alpha + psum;
+        *reinterpret_cast<uint2*>(&sh.p[half][l16 * ATT_PROW + 16 * wh + 4 * q4]) = make_uint2(pk[0], pk[1]);
+      }
+      __syncthreads();  // P complete (and every wave has read the maxima)
+      if (live) {
+        // rescale O (rows = heads 4 q4 + r) and accumulate P . V over the chunk's 64 tokens (dims 128 wh ..)
+        float al[4];
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        // P operand: head l16, tokens 32 ks + 8 q4 .. + 7 (the value operand's k-slot order)
-        const bf16x8 pop = as_bf16x8(*reinterpret_cast<const uint4*>(&sh.p[l16 * ATT_PROW + 32 * ks + 8 * q4]));
+        for (int r = 0; r < 4; ++r) al[r] = __shfl(alpha, 4 * q4 + r, WAVE);
 #pragma unroll
         for (int n = 0; n < 8; ++n)
-          o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pop, value_operand(sh.kt, ks, 8 * wave + n, lane), o[n], 0,
-                                                         0, 0);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o[n][r] *= al[r];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          // P operand: head l16, tokens 32 ks + 8 q4 .. + 7 (the value operand's k-slot order)
+          const bf16x8 pop =
+              as_bf16x8(*reinterpret_cast<const uint4*>(&sh.p[half][l16 * ATT_PROW + 32 * ks + 8 * q4]));
+#pragma unroll
+          for (int n = 0; n < 8; ++n)
+            o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pop, value_operand(kt, ks, 8 * wh + n, lane), o[n], 0, 0,
+                                                           0);
+        }
       }
-      __syncthreads();  // the next chunk overwrites the tiles
+      // the next pair's maxima and P are written after its first barrier, which every wave reaches only after
+      // this pair's P . V
     }
+    __syncthreads();  // the next super-chunk overwrites the staged rows and slots
   }
 
-  // the row sums: lane shares -> per wave -> per workgroup
+  // each half's row sums: lane shares -> per wave -> per half
   float lw = l_run;
   lw += __shfl_xor(lw, 16, WAVE);
   lw += __shfl_xor(lw, 32, WAVE);
-  if (lane < ATT_HPW) sh.red[wave][lane] = lw;
+  if (lane < ATT_HPW) sh.red[half][wh][lane] = lw;
   __syncthreads();
-  const float l_tot = sh.red[0][l16] + sh.red[1][l16] + sh.red[2][l16] + sh.red[3][l16];
-  float lr[4], mr[4];
+  const float l_half = sh.red[half][0][l16] + sh.red[half][1][l16] + sh.red[half][2][l16] + sh.red[half][3][l16];
+  // merge the halves: the second half hands its max, sum and output to the first through LDS (the staged rows are
+  // no longer needed)
+  float* xo = reinterpret_cast<float*>(sh.kt[0]);  // [4 waves][32 values][64 lanes]
+  if (half == 1) {
+#pragma unroll
+    for (int n = 0; n < 8; ++n)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) xo[(wh * 32 + 4 * n + r) * WAVE + lane] = o[n][r];
+    if (wh == 0 && lane < ATT_HPW) {
+      sh.ml[0][lane] = m_run;
+      sh.ml[1][lane] = l_half;
+    }
+  }
+  __syncthreads();
+  const bool writer = half == 0;  // the first half writes the merged result
+  const float m1 = sh.ml[0][l16], l1 = sh.ml[1][l16];
+  const float m_tot = fmaxf(m_run, m1);
+  const float a0 = m_run == -INFINITY ? 0.0f : __expf(m_run - m_tot);
+  const float a1 = m1 == -INFINITY ? 0.0f : __expf(m1 - m_tot);
+  const float l_tot = a0 * l_half + a1 * l1;
+  float lr[4], mr[4], a0r[4], a1r[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     lr[r] = __shfl(l_tot, 4 * q4 + r, WAVE);
-    mr[r] = __shfl(m_run, 4 * q4 + r, WAVE);
+    mr[r] = __shfl(m_tot, 4 * q4 + r, WAVE);
+    a0r[r] = __shfl(a0, 4 * q4 + r, WAVE);
+    a1r[r] = __shfl(a1, 4 * q4 + r, WAVE);
   }
+#pragma unroll
+  for (int n = 0; n < 8; ++n)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) o[n][r] = a0r[r] * o[n][r] + a1r[r] * xo[(wh * 32 + 4 * n + r) * WAVE + lane];
   const bool empty = k_begin >= k_end;
   if (splits == 1) {
+    if (writer) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int head = ATT_HPW * hg + 4 * q4 + r;
-      const float inv = 1.0f / lr[r];
+      for (int r = 0; r < 4; ++r) {
+        const int head = ATT_HPW * hg + 4 * q4 + r;
+        const float inv = 1.0f / lr[r];
 #pragma unroll
-      for (int n = 0; n < 8; ++n) {
-        const int dim = 128 * wave + 16 * n + l16;
-        const float v = o[n][r] * inv;
-        const size_t oi = ((size_t)b * H + head) * ATT_DV + dim;
-        if (out) out[oi] = f32_to_bf16_bits(v);
-        if (out_f32) out_f32[oi] = v;
+        for (int n = 0; n < 8; ++n) {
+          const int dim = 128 * wh + 16 * n + l16;
+          const float v = o[n][r] * inv;
+          const size_t oi = ((size_t)b * H + head) * ATT_DV + dim;
+          if (out) out[oi] = f32_to_bf16_bits(v);
+          if (out_f32) out_f32[oi] = v;
+        }
+        if (lse_out && wh == 0 && l16 == 0) lse_out[(size_t)b * H + head] = mr[r] + __logf(lr[r]);
       }
-      if (lse_out && wave == 0 && l16 == 0) lse_out[(size_t)b * H + head] = mr[r] + __logf(lr[r]);
     }
-  } else {
+    return;
+  }
+  if (writer) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int head = ATT_HPW * hg + 4 * q4 + r;
       const float inv = empty ? 0.0f : 1.0f / lr[r];
       const size_t base = (((size_t)b * splits + sp) * H + head) * ATT_DV;
 #pragma unroll
-      for (int n = 0; n < 8; ++n) ws_o[base + 128 * wave + 16 * n + l16] = o[n][r] * inv;
+      for (int n = 0; n < 8; ++n) ws_o[base + 128 * wh + 16 * n + l16] = o[n][r] * inv;
       // the split's running max and sum, not its lse: at a fully masked row lse = -1e30 + log(sum) rounds to -1e30
       // in fp32 and would lose the sums that weight the splits
-      if (wave == 0 && l16 == 0) {
+      if (wh == 0 && l16 == 0) {
         const size_t mi = (((size_t)b * splits + sp) * H + head) * 2;
         ws_ml[mi] = empty ? -INFINITY : mr[r];
         ws_ml[mi + 1] = empty ? 0.0f : lr[r];
@@ -273,7 +343,8 @@ __global__ __launch_bounds__(ATT_THREADS, 2) void sparse_mla_kernel(
 // o = sum_s W_s o_s / sum_s W_s with W_s = l_s exp(m_s - M), M = max_s m_s, and lse = M + log sum_s W_s, per
 // (sequence, head), from each split's normalised o_s, max m_s and sum l_s (the log-sum-exp combine of
 // trnrt/models/mla.py:853-856 with lse_s = m_s + log l_s kept in two parts); 128 threads x 4 dims. Every load is
-// issued before any is used (one memory round trip); an empty split's o_s is 0 and its weight 0.
+// issued before any is used (one memory round trip; unconditional, so the waits count exactly); an empty split's
+// o_s is 0 and its weight 0.
 template <int S>
 __global__ __launch_bounds__(128) void combine_splits_kernel(const float* __restrict__ ws_o,
                                                              const float* __restrict__ ws_ml, int H, int splits,
@@ -286,23 +357,18 @@ __global__ __launch_bounds__(128) void combine_splits_kernel(const float* __rest
   float4 v[S];
 #pragma unroll
   for (int s = 0; s < S; ++s) {
-    if (s < splits) {
-      const size_t i = ((size_t)b * splits + s) * H + head;
-      ml[s] = *reinterpret_cast<const float2*>(&ws_ml[2 * i]);
-      v[s] = *reinterpret_cast<const float4*>(&ws_o[i * ATT_DV + d]);
-    } else {
-      ml[s] = make_float2(-INFINITY, 0.0f);
-      v[s] = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
+    const size_t i = ((size_t)b * splits + min(s, splits - 1)) * H + head;
+    ml[s] = *reinterpret_cast<const float2*>(&ws_ml[2 * i]);
+    v[s] = *reinterpret_cast<const float4*>(&ws_o[i * ATT_DV + d]);
   }
   float M = -INFINITY;
 #pragma unroll
-  for (int s = 0; s < S; ++s) M = fmaxf(M, ml[s].x);
+  for (int s = 0; s < S; ++s) M = s < splits ? fmaxf(M, ml[s].x) : M;
   float W = 0.0f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
   for (int s = 0; s < S; ++s) {
-    const float wt = ml[s].y > 0.0f ? ml[s].y * __expf(ml[s].x - M) : 0.0f;
+    const float wt = (s < splits && ml[s].y > 0.0f) ? ml[s].y * __expf(ml[s].x - M) : 0.0f;
     W += wt;
     acc.x += wt * v[s].x;
     acc.y += wt * v[s].y;
@@ -316,7 +382,8 @@ __global__ __launch_bounds__(128) void combine_splits_kernel(const float* __rest
     const uint32_t hi = f32_to_bf16_bits(acc.z * inv) | ((uint32_t)f32_to_bf16_bits(acc.w * inv) << 16);
     *reinterpret_cast<uint2*>(&out[oi]) = make_uint2(lo, hi);
   }
-  if (out_f32) *reinterpret_cast<float4*>(&out_f32[oi]) = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+  if (out_f32)
+    *reinterpret_cast<float4*>(&out_f32[oi]) = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
   if (lse_out && threadIdx.x == 0) lse_out[(size_t)b * H + head] = M + __logf(W);
 }
 
@@ -368,21 +435,18 @@ hipError_t launch_sparse_mla(const uint16_t* q, const uint8_t* kv, const float* 
     ws_o = static_cast<float*>(ws);
     ws_ml = ws_o + (size_t)B * eff_splits * H * ATT_DV;  // [B, splits, H, 2]: max, sum
   }
-  launch("sparse_mla_kernel", sparse_mla_kernel, dim3(grid), dim3(ATT_THREADS), s, q, kv, kvs, idx, cnt, table, rows, bias,
-                     out, out_f32, lse, ws_o, ws_ml, B, H, keep, max_pages, page_size, num_pages, scale, eff_splits,
-                     sps);
-  hipError_t e = hipGetLastError();
+  hipError_t e = launch("sparse_mla_kernel", sparse_mla_kernel, dim3(grid), dim3(ATT_THREADS), s, q, kv, kvs, idx,
+                        cnt, table, rows, bias, out, out_f32, lse, ws_o, ws_ml, B, H, keep, max_pages, page_size,
+                        num_pages, scale, eff_splits, sps);
   if (e != hipSuccess || eff_splits == 1) return e;
   if (eff_splits <= 8)
-    launch("combine_splits_kernel", combine_splits_kernel<8>, dim3(B * H), dim3(128), s, ws_o, ws_ml, H, eff_splits, out,
-                       out_f32, lse);
-  else if (eff_splits <= 16)
-    launch("combine_splits_kernel", combine_splits_kernel<16>, dim3(B * H), dim3(128), s, ws_o, ws_ml, H, eff_splits, out,
-                       out_f32, lse);
-  else
-    launch("combine_splits_kernel", combine_splits_kernel<32>, dim3(B * H), dim3(128), s, ws_o, ws_ml, H, eff_splits, out,
-                       out_f32, lse);
-  return hipGetLastError();
+    return launch("combine_splits_kernel", combine_splits_kernel<8>, dim3(B * H), dim3(128), s, ws_o, ws_ml, H,
+                  eff_splits, out, out_f32, lse);
+  if (eff_splits <= 16)
+    return launch("combine_splits_kernel", combine_splits_kernel<16>, dim3(B * H), dim3(128), s, ws_o, ws_ml, H,
+                  eff_splits, out, out_f32, lse);
+  return launch("combine_splits_kernel", combine_splits_kernel<32>, dim3(B * H), dim3(128), s, ws_o, ws_ml, H,
+                eff_splits, out, out_f32, lse);
 }
 
 hipError_t launch_token_rows(const int* idx, const int* cnt, const int* table, int* rows, float* bias, int B,

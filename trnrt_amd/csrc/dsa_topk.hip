@@ -71,7 +71,17 @@ __device__ __forceinline__ int row16_sum(int v) {
   return v;
 }
 
+// Optional second output of a flat selection: the cache slot of each selected position through the row's page table
+// (slot = page_table[row, p / page_size] * page_size + p % page_size, pages clamped into the cache), and for the
+// entries past the count the slot of position 0, the slot the attention reads for them.
+struct SlotOut {
+  const int* table;
+  int max_pages, page_size, num_pages;
+  int* rows;  // [B, keep], or null
+};
+
 struct RowShared {
+  int pg[128];                      // page ids of the row's first 4096 positions (slot output)
   int bins[TK_HBINS];               // the current pass's histogram (4096, 2048 or 512 bins in key order)
   int wtot[TR_WAVES];               // per-wave totals of a block scan
   uint32_t blk[TR_MAXG * TR_WAVES];  // output: per (group, wave) packed counts, then their exclusive prefix
@@ -128,11 +138,12 @@ __device__ int row_find_bin(RowShared& sh, int nbins, int need, int* bin, int* a
 // The flat selection: one workgroup per row (blockIdx.x) of up to 4 G 1024 scores. Thread t holds the keys of
 // positions 4 (1024 e + t) + c, e < G, c < 4 (coalesced float4 loads). HIST_IN: the row's top-12-bit histogram is in
 // hist[row] (read, then zeroed for the next call); otherwise it is built here.
-template <int G, bool HIST_IN, bool VEC>
+template <int G, bool HIST_IN, bool VEC, bool ROWS>
 __global__ __launch_bounds__(TR_THREADS) void topk_row_kernel(const float* __restrict__ scores, int stride,
                                                               const int* __restrict__ len, int len_div, int len_mul,
                                                               int keep, int vis_only, int* __restrict__ hist,
-                                                              int* __restrict__ idx_out, int* __restrict__ cnt_out) {
+                                                              int* __restrict__ idx_out, int* __restrict__ cnt_out,
+                                                              SlotOut so) {
   __shared__ RowShared sh;
   const int row = blockIdx.x;
   const int t = threadIdx.x, wave = t / WAVE, lane = t & (WAVE - 1);
@@ -142,9 +153,12 @@ __global__ __launch_bounds__(TR_THREADS) void topk_row_kernel(const float* __res
   int4 h4 = make_int4(0, 0, 0, 0);
   int* hrow = hist + (size_t)row * TK_HBINS;
   if (HIST_IN) h4 = reinterpret_cast<const int4*>(hrow)[t];
+  int pgv = 0;
+  if (ROWS) pgv = so.table[(size_t)row * so.max_pages + min(t, so.max_pages - 1)];
   uint32_t key[G][4];
 #pragma unroll
   for (int e = 0; e < G; ++e) load_keys4<VEC>(srow, stride, L, 4 * (TR_THREADS * e + t), vis_only, key[e]);
+  if (ROWS && t < 128) sh.pg[t] = safe_page(pgv, so.num_pages);
   if (t == 0) sh.sel_bin = -1;
   if (HIST_IN) {
     reinterpret_cast<int4*>(sh.bins)[t] = h4;
@@ -235,13 +249,22 @@ __global__ __launch_bounds__(TR_THREADS) void topk_row_kernel(const float* __res
       const bool ti = T != 0 && key[e][c] == T;
       const bool sel = a || (ti && t_before < room);
       const int o = a_before + (t_before < room ? t_before : room);
-      if (sel && (unsigned)o < (unsigned)keep) orow[o] = p0 + c;  // in range whatever the counts
+      if (sel && (unsigned)o < (unsigned)keep) {  // in range whatever the counts
+        orow[o] = p0 + c;
+        if (ROWS) {
+          const int ps = so.page_size;
+          so.rows[(size_t)row * keep + o] = sh.pg[min((p0 + c) / ps, 127)] * ps + (p0 + c) % ps;
+        }
+      }
       a_before += a;
       t_before += ti;
     }
   }
   const int cnt_row = nvis < keep ? nvis : keep;
-  for (int i = cnt_row + t; i < keep; i += TR_THREADS) orow[i] = 0;
+  for (int i = cnt_row + t; i < keep; i += TR_THREADS) {
+    orow[i] = 0;
+    if (ROWS) so.rows[(size_t)row * keep + i] = sh.pg[0] * so.page_size;
+  }
   if (t == 0) cnt_out[row] = cnt_row;
 }
 
@@ -447,6 +470,8 @@ __global__ __launch_bounds__(TC_THREADS) void topk_chunk_kernel(const float* __r
 }
 
 struct OutShared {
+  int pg[WAVE];  // page ids of the chunk's positions (slot output; pages of at least 32 positions)
+  int pg0;                    // the page of position 0
   int bins[2048];
   int wtot[TC_WAVES];
   uint32_t blk[2 * TC_WAVES];
@@ -493,14 +518,15 @@ __device__ void out_find_bin(OutShared& sh, int nbins, int need, int* bin, int* 
   *above = b < 0 ? 0 : sh.sel_above;
 }
 
-template <bool VEC>
+template <bool VEC, bool ROWS>
 __global__ __launch_bounds__(TC_THREADS) void topk_output_kernel(const float* __restrict__ scores, int stride,
                                                                  const int* __restrict__ len, int len_div,
                                                                  int len_mul, int keep, int vis_only, int nchunks,
                                                                  int* __restrict__ hist,
                                                                  const RowMeta* __restrict__ meta,
                                                                  const uint32_t* __restrict__ ckey,
-                                                                 int* __restrict__ idx_out, int* __restrict__ cnt_out) {
+                                                                 int* __restrict__ idx_out, int* __restrict__ cnt_out,
+                                                                 SlotOut so) {
   __shared__ OutShared sh;
   const int row = blockIdx.y, chunk = blockIdx.x;
   const int t = threadIdx.x, wave = t / WAVE, lane = t & (WAVE - 1);
@@ -519,8 +545,18 @@ __global__ __launch_bounds__(TC_THREADS) void topk_output_kernel(const float* __
   uint32_t ck[TC_CAND / 16];
 #pragma unroll
   for (int k = 0; k < TC_CAND / 16; ++k) ck[k] = cg[sub + 16 * k];
+  const int pg_first = ROWS ? base / so.page_size : 0;
+  int pgv = 0, pg0v = 0;
+  if (ROWS) {
+    pgv = so.table[(size_t)row * so.max_pages + min(pg_first + lane, so.max_pages - 1)];
+    pg0v = so.table[(size_t)row * so.max_pages];
+  }
   uint32_t key[2][4];
   load_chunk_keys<VEC>(scores + (size_t)row * stride, stride, L, base, vis_only, key);
+  if (ROWS && wave == 0) {
+    sh.pg[lane] = safe_page(pgv, so.num_pages);
+    if (lane == 0) sh.pg0 = safe_page(pg0v, so.num_pages);
+  }
   // leave the row's histogram zero for the next call (every topk_chunk_kernel workgroup has read it)
   int* hrow = hist + (size_t)row * TK_HBINS;
   for (int i = chunk * TC_THREADS + t; i < TK_HBINS; i += nchunks * TC_THREADS) hrow[i] = 0;
@@ -634,14 +670,23 @@ __global__ __launch_bounds__(TC_THREADS) void topk_output_kernel(const float* __
       const bool ti = T != 0u && key[e][c] == T;
       const bool sel = a || (ti && t_before < room_here);
       const int o = out_base + a_before + (t_before < room_here ? t_before : room_here);
-      if (sel && (unsigned)o < (unsigned)keep) orow[o] = p0 + c;  // in range whatever the counts
+      if (sel && (unsigned)o < (unsigned)keep) {  // in range whatever the counts
+        orow[o] = p0 + c;
+        if (ROWS) {
+          const int ps = so.page_size, p = p0 + c;
+          so.rows[(size_t)row * keep + o] = sh.pg[min(p / ps - pg_first, WAVE - 1)] * ps + p % ps;
+        }
+      }
       a_before += a;
       t_before += ti;
     }
   }
   if (chunk == 0) {
     const int cnt_row = nvis < 0 ? 0 : (nvis < keep ? nvis : keep);
-    for (int i = cnt_row + t; i < keep; i += TC_THREADS) orow[i] = 0;
+    for (int i = cnt_row + t; i < keep; i += TC_THREADS) {
+      orow[i] = 0;
+      if (ROWS) so.rows[(size_t)row * keep + i] = sh.pg0 * so.page_size;
+    }
     if (t == 0) cnt_out[row] = cnt_row;
   }
 }
@@ -768,19 +813,24 @@ struct TopkBuffers {
 
 template <int G, bool VEC>
 static hipError_t launch_topk_row(const float* scores, int stride, const int* len, int len_div, int len_mul,
-                                  int keep, int vis_only, int* hist, bool hist_ready, int* idx, int* cnt, int B,
-                                  hipStream_t s) {
-  if (hist_ready)
-    return launch("topk_row_kernel", topk_row_kernel<G, true, VEC>, dim3(B), dim3(TR_THREADS), s, scores, stride,
-                  len, len_div, len_mul, keep, vis_only, hist, idx, cnt);
-  return launch("topk_row_kernel", topk_row_kernel<G, false, VEC>, dim3(B), dim3(TR_THREADS), s, scores, stride, len,
-                len_div, len_mul, keep, vis_only, hist, idx, cnt);
+                                  int keep, int vis_only, int* hist, bool hist_ready, int* idx, int* cnt,
+                                  const SlotOut& so, int B, hipStream_t s) {
+  const dim3 grid(B), block(TR_THREADS);
+  if (so.rows)
+    return hist_ready ? launch("topk_row_kernel", topk_row_kernel<G, true, VEC, true>, grid, block, s, scores, stride,
+                               len, len_div, len_mul, keep, vis_only, hist, idx, cnt, so)
+                      : launch("topk_row_kernel", topk_row_kernel<G, false, VEC, true>, grid, block, s, scores,
+                               stride, len, len_div, len_mul, keep, vis_only, hist, idx, cnt, so);
+  return hist_ready ? launch("topk_row_kernel", topk_row_kernel<G, true, VEC, false>, grid, block, s, scores, stride,
+                             len, len_div, len_mul, keep, vis_only, hist, idx, cnt, so)
+                    : launch("topk_row_kernel", topk_row_kernel<G, false, VEC, false>, grid, block, s, scores, stride,
+                             len, len_div, len_mul, keep, vis_only, hist, idx, cnt, so);
 }
 
 template <bool VEC>
 static hipError_t launch_topk_chunked(const float* scores, int stride, const int* len, int len_div, int len_mul,
                                       int nch, int keep, int vis_only, int* idx, int* cnt, const TopkBuffers& tb,
-                                      bool hist_ready, int B, hipStream_t s) {
+                                      bool hist_ready, const SlotOut& so, int B, hipStream_t s) {
   hipError_t e;
   if (!hist_ready) {
     e = launch("topk_hist_kernel", topk_hist_kernel, dim3(nch, B), dim3(TKH_THREADS), s, scores, stride, len, len_div,
@@ -790,28 +840,30 @@ static hipError_t launch_topk_chunked(const float* scores, int stride, const int
   e = launch("topk_chunk_kernel", topk_chunk_kernel<VEC>, dim3(nch, B), dim3(TC_THREADS), s, scores, stride, len,
              len_div, len_mul, keep, vis_only, tb.hist, tb.meta, tb.ckey);
   if (e != hipSuccess) return e;
-  return launch("topk_output_kernel", topk_output_kernel<VEC>, dim3(nch, B), dim3(TC_THREADS), s, scores, stride, len,
-                len_div, len_mul, keep, vis_only, nch, tb.hist, tb.meta, tb.ckey, idx, cnt);
+  if (so.rows)
+    return launch("topk_output_kernel", topk_output_kernel<VEC, true>, dim3(nch, B), dim3(TC_THREADS), s, scores,
+                  stride, len, len_div, len_mul, keep, vis_only, nch, tb.hist, tb.meta, tb.ckey, idx, cnt, so);
+  return launch("topk_output_kernel", topk_output_kernel<VEC, false>, dim3(nch, B), dim3(TC_THREADS), s, scores,
+                stride, len, len_div, len_mul, keep, vis_only, nch, tb.hist, tb.meta, tb.ckey, idx, cnt, so);
 }
-
 
 // The flat selection of rows of at most max_len <= TOPK_FLAT_MAX scores: one workgroup per row up to 4096 scores,
 // the chunked kernels above that.
 static hipError_t launch_topk_level(const float* scores, int stride, const int* len, int len_div, int len_mul,
                                     int max_len, int keep, int vis_only, int* idx, int* cnt, const TopkBuffers& tb,
-                                    bool hist_ready, int B, hipStream_t s) {
+                                    bool hist_ready, const SlotOut& so, int B, hipStream_t s) {
   const bool vec = (stride & 3) == 0 && stride >= 4;
   if (max_len <= 4 * TR_THREADS)
     return vec ? launch_topk_row<1, true>(scores, stride, len, len_div, len_mul, keep, vis_only, tb.hist, hist_ready,
-                                          idx, cnt, B, s)
+                                          idx, cnt, so, B, s)
                : launch_topk_row<1, false>(scores, stride, len, len_div, len_mul, keep, vis_only, tb.hist, hist_ready,
-                                           idx, cnt, B, s);
+                                           idx, cnt, so, B, s);
   if (max_len > TC_MAXCH * TC_CHUNK) return hipErrorInvalidValue;
   const int nch = (max_len + TC_CHUNK - 1) / TC_CHUNK;
   return vec ? launch_topk_chunked<true>(scores, stride, len, len_div, len_mul, nch, keep, vis_only, idx, cnt, tb,
-                                         hist_ready, B, s)
+                                         hist_ready, so, B, s)
              : launch_topk_chunked<false>(scores, stride, len, len_div, len_mul, nch, keep, vis_only, idx, cnt, tb,
-                                          hist_ready, B, s);
+                                          hist_ready, so, B, s);
 }
 
 // Selection over rows of `stride` scores whose lengths are len[row] (len_div / len_mul as in level_len), n an upper
@@ -819,9 +871,10 @@ static hipError_t launch_topk_level(const float* scores, int stride, const int* 
 static hipError_t topk_rows(const float* scores, int stride, const int* len, int len_div, int len_mul, long n,
                             int keep, int vis_only, int* idx, int* cnt, const TopkBuffers& tb, bool hist_ready,
                             char* ws, int B, hipStream_t s) {
+  const SlotOut none = {nullptr, 0, 0, 0, nullptr};
   if (n <= TOPK_FLAT_MAX)
     return launch_topk_level(scores, stride, len, len_div, len_mul, (int)n, keep, vis_only, idx, cnt, tb, hist_ready,
-                             B, s);
+                             none, B, s);
   if (len_div != 1 || len_mul != 1) return hipErrorInvalidValue;  // only flat rows are split
   const int sub = topk_sub_block(n, keep);
   const int nb = (int)((n + sub - 1) / sub), nc = keep * sub;
@@ -838,7 +891,7 @@ static hipError_t topk_rows(const float* scores, int stride, const int* len, int
   if (e != hipSuccess) return e;
   // level 1: the top-keep sub-blocks (ceil(len / sub) maxima per row)
   if (nb > TOPK_FLAT_MAX) return hipErrorInvalidValue;  // excluded by topk_plan
-  e = launch_topk_level(bm, nb, len, sub, 1, nb, keep, vis_only, bidx, bcnt, tb, false, B, s);
+  e = launch_topk_level(bm, nb, len, sub, 1, nb, keep, vis_only, bidx, bcnt, tb, false, none, B, s);
   if (e != hipSuccess) return e;
   e = launch("gather_blocks_kernel", gather_blocks_kernel, dim3((nc + 255) / 256, B), dim3(256), s, scores, stride,
              len, sub, bidx, bcnt, keep, cand);
@@ -851,11 +904,14 @@ static hipError_t topk_rows(const float* scores, int stride, const int* len, int
 }
 
 // ws: topk_workspace_bytes(B, max_len, keep) bytes whose histogram region is zero; hist_ready: the histogram of the
-// rows is already accumulated there (by the indexer), so the first level does not build it.
+// rows is already accumulated there (by the indexer), so the first level does not build it. rows_out (flat rows
+// only, else null): also the cache slot of each selected position through the page table.
 hipError_t launch_topk(const float* scores, const int* len, int* idx, int* cnt, void* ws, int B, int stride,
-                       int max_len, int keep, int vis_only, bool hist_ready, hipStream_t s) {
+                       int max_len, int keep, int vis_only, bool hist_ready, const int* table, int max_pages,
+                       int page_size, int num_pages, int* rows_out, hipStream_t s) {
   char* p = static_cast<char*>(ws);
-  if (hist_ready && max_len > TOPK_FLAT_MAX) return hipErrorInvalidValue;  // the indexer histograms flat rows only
+  if ((hist_ready || rows_out) && max_len > TOPK_FLAT_MAX) return hipErrorInvalidValue;  // flat rows only
+  if (rows_out && (!table || page_size < 32 || max_pages < 1 || num_pages < 1)) return hipErrorInvalidValue;
   TopkBuffers tb;
   tb.hist = reinterpret_cast<int*>(p);
   p += topk_hist_bytes(B);
@@ -863,6 +919,10 @@ hipError_t launch_topk(const float* scores, const int* len, int* idx, int* cnt, 
   p += up256((size_t)B * sizeof(RowMeta));
   tb.ckey = reinterpret_cast<uint32_t*>(p);
   p += up256((size_t)B * TC_MAXCH * TC_CHUNK * 4);
+  if (rows_out) {
+    const SlotOut so = {table, max_pages, page_size, num_pages, rows_out};
+    return launch_topk_level(scores, stride, len, 1, 1, max_len, keep, vis_only, idx, cnt, tb, hist_ready, so, B, s);
+  }
   return topk_rows(scores, stride, len, 1, 1, max_len, keep, vis_only, idx, cnt, tb, hist_ready, p, B, s);
 }
 
