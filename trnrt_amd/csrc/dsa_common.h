@@ -50,6 +50,10 @@ __device__ __forceinline__ uint4 load_stream16(const void* p) {
 }
 
 constexpr float NEG_INF = -1e30f;   // trnrt/models/decoder.py NEG_INF
+// The top-k's first-level histogram of a row: 4096 bins (the top 12 bits of the order key), kept in HIST_REPLICAS
+// copies that the indexer's workgroups fill in turn (fewer atomics on the same address); readers sum the copies.
+constexpr int HIST_BINS = 4096;
+constexpr int HIST_REPLICAS = 1;
 constexpr float VISIBLE = -5e29f;   // trnrt/kernels/dsa_topk.py:58: scores at or below are not selectable
 constexpr int WAVE = 64;
 

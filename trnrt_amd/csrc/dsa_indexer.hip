@@ -27,7 +27,7 @@ constexpr int IDX_TPW = 4;        // key tiles per wave, all loaded up front
 constexpr int IDX_TPG = IDX_TPW * IDX_WAVES;  // key tiles per workgroup
 constexpr int IDX_QROW = IDX_D + 8;  // LDS row stride of the staged queries (bf16 elements; padding spreads banks)
 constexpr int IDX_HSHIFT = 20;       // the top-k kernel's first-level bins: the top 12 bits of the order key
-constexpr int IDX_HBINS = 4096;
+constexpr int IDX_HBINS = HIST_BINS;
 
 __device__ __forceinline__ float crow_value(const float* cand, int b, int stride, int pos) {
   return cand[(size_t)b * stride + pos];
@@ -155,7 +155,7 @@ __global__ __launch_bounds__(IDX_THREADS, 2) void indexer_decode_kernel(
   if (HIST) {
     // the row's first-level top-k histogram (top 12 bits of the order key of the selectable scores)
     __syncthreads();
-    int* hrow = hist + (size_t)b * IDX_HBINS;
+    int* hrow = hist + ((size_t)b * HIST_REPLICAS + grp % HIST_REPLICAS) * IDX_HBINS;
     for (int i = threadIdx.x; i < IDX_HBINS; i += IDX_THREADS) {
       const int c = hs[i];
       if (c) atomicAdd(&hrow[i], c);

@@ -20,7 +20,7 @@
 namespace dsa {
 
 constexpr int TK_HSHIFT = 20;  // first level: the top 12 bits of the order key
-constexpr int TK_HBINS = 4096;
+constexpr int TK_HBINS = HIST_BINS;
 constexpr int TR_THREADS = 1024;
 constexpr int TR_WAVES = TR_THREADS / WAVE;
 constexpr int TR_MAXG = 8;     // float4 groups per thread: rows of up to 4 x 8 x 1024 scores
@@ -150,9 +150,11 @@ __global__ __launch_bounds__(TR_THREADS) void topk_row_kernel(const float* __res
   const int L = level_len(len, row, len_div, len_mul, stride);
   const float* srow = scores + (size_t)row * stride;
 
-  int4 h4 = make_int4(0, 0, 0, 0);
-  int* hrow = hist + (size_t)row * TK_HBINS;
-  if (HIST_IN) h4 = reinterpret_cast<const int4*>(hrow)[t];
+  int4 h4r[HIST_REPLICAS];
+  int* hrow = hist + (size_t)row * HIST_REPLICAS * TK_HBINS;
+  if (HIST_IN)
+#pragma unroll
+    for (int r = 0; r < HIST_REPLICAS; ++r) h4r[r] = reinterpret_cast<const int4*>(hrow + r * TK_HBINS)[t];
   int pgv = 0;
   if (ROWS) pgv = so.table[(size_t)row * so.max_pages + min(t, so.max_pages - 1)];
   uint32_t key[G][4];
@@ -161,8 +163,18 @@ __global__ __launch_bounds__(TR_THREADS) void topk_row_kernel(const float* __res
   if (ROWS && t < 128) sh.pg[t] = safe_page(pgv, so.num_pages);
   if (t == 0) sh.sel_bin = -1;
   if (HIST_IN) {
+    int4 h4 = h4r[0];
+#pragma unroll
+    for (int r = 1; r < HIST_REPLICAS; ++r) {
+      h4.x += h4r[r].x;
+      h4.y += h4r[r].y;
+      h4.z += h4r[r].z;
+      h4.w += h4r[r].w;
+    }
     reinterpret_cast<int4*>(sh.bins)[t] = h4;
-    reinterpret_cast<int4*>(hrow)[t] = make_int4(0, 0, 0, 0);  // zero for the next call
+#pragma unroll
+    for (int r = 0; r < HIST_REPLICAS; ++r)
+      reinterpret_cast<int4*>(hrow + r * TK_HBINS)[t] = make_int4(0, 0, 0, 0);  // zero for the next call
     __syncthreads();
   } else {
     reinterpret_cast<int4*>(sh.bins)[t] = make_int4(0, 0, 0, 0);
@@ -315,7 +327,7 @@ __global__ __launch_bounds__(TKH_THREADS) void topk_hist_kernel(const float* __r
     }
   }
   __syncthreads();
-  int* hrow = hist + (size_t)row * TK_HBINS;
+  int* hrow = hist + ((size_t)row * HIST_REPLICAS + blockIdx.x % HIST_REPLICAS) * TK_HBINS;
   for (int i = threadIdx.x; i < TK_HBINS; i += TKH_THREADS) {
     const int c = h[i];
     if (c) atomicAdd(&hrow[i], c);
@@ -371,10 +383,10 @@ __global__ __launch_bounds__(TC_THREADS) void topk_chunk_kernel(const float* __r
   const int L = level_len(len, row, len_div, len_mul, stride);
   const int base = chunk * TC_CHUNK;
   // one round of loads: the thread's 16 histogram bins and its 8 keys
-  const int4* h4 = reinterpret_cast<const int4*>(hist + (size_t)row * TK_HBINS) + 4 * t;
-  int4 hv[4];
+  const int4* h4 = reinterpret_cast<const int4*>(hist + (size_t)row * HIST_REPLICAS * TK_HBINS) + 4 * t;
+  int4 hv[4 * HIST_REPLICAS];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) hv[i] = h4[i];
+  for (int i = 0; i < 4 * HIST_REPLICAS; ++i) hv[i] = h4[(i / 4) * (TK_HBINS / 4) + i % 4];
   uint32_t key[2][4];
   load_chunk_keys<VEC>(scores + (size_t)row * stride, stride, L, base, vis_only, key);
   int hb[16];
@@ -385,6 +397,15 @@ __global__ __launch_bounds__(TC_THREADS) void topk_chunk_kernel(const float* __r
     hb[4 * i + 2] = hv[i].z;
     hb[4 * i + 3] = hv[i].w;
   }
+#pragma unroll
+  for (int r = 1; r < HIST_REPLICAS; ++r)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      hb[4 * i] += hv[4 * r + i].x;
+      hb[4 * i + 1] += hv[4 * r + i].y;
+      hb[4 * i + 2] += hv[4 * r + i].z;
+      hb[4 * i + 3] += hv[4 * r + i].w;
+    }
   // c0: the bin holding the keep-th largest key (bins 16t .. 16t + 15 on thread t; suffix over threads)
   int mine = 0;
 #pragma unroll
@@ -558,8 +579,8 @@ __global__ __launch_bounds__(TC_THREADS) void topk_output_kernel(const float* __
     if (lane == 0) sh.pg0 = safe_page(pg0v, so.num_pages);
   }
   // leave the row's histogram zero for the next call (every topk_chunk_kernel workgroup has read it)
-  int* hrow = hist + (size_t)row * TK_HBINS;
-  for (int i = chunk * TC_THREADS + t; i < TK_HBINS; i += nchunks * TC_THREADS) hrow[i] = 0;
+  int* hrow = hist + (size_t)row * HIST_REPLICAS * TK_HBINS;
+  for (int i = chunk * TC_THREADS + t; i < HIST_REPLICAS * TK_HBINS; i += nchunks * TC_THREADS) hrow[i] = 0;
 
   const int ncg = __shfl(nc_l, g, WAVE);  // this thread's candidate chunk's count (lane g < 16 holds it)
   if (t < TC_MAXCH) sh.na[t] = na_l;
@@ -790,7 +811,7 @@ static size_t topk_level_bytes(int B, long n, int keep) {
          topk_level_bytes(B, nc, keep);
 }
 
-size_t topk_hist_bytes(int B) { return up256((size_t)B * TK_HBINS * 4); }
+size_t topk_hist_bytes(int B) { return up256((size_t)B * HIST_REPLICAS * TK_HBINS * 4); }
 
 size_t topk_workspace_bytes(int B, int max_len, int keep) {
   return topk_hist_bytes(B) + up256((size_t)B * sizeof(RowMeta)) + up256((size_t)B * TC_MAXCH * TC_CHUNK * 4) +
