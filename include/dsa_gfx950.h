@@ -62,6 +62,20 @@ int dsa_indexer_decode(const void* q_bf16, const float* w, const uint8_t* k_fp8,
                        int Hi, int D, int max_pages, int page_size, int num_pages, int score_stride, void* stream);
 
 /*
+ * Dense (prefill-chunk) indexer scores of N queries over one context's keys (replaces the score stage of
+ * trnrt/kernels/dsa_long_select.py:500-530 `select`, arithmetic of dsa_long_select.py:119-133 `emulate_scores`
+ * and trnrt/models/dsa_long.py:74-84 `scores` with a 2-D key tensor):
+ *   scores[n, p] = scale * k_scale[p] * sum_h w[n, h] * relu(q[n, h, :] . k_fp8[p, :])   for p < npool[n]
+ *   scores[n, p] = NEG_INF                                                               for npool[n] <= p < score_stride
+ *   q bf16 [N, Hi, D] (D must be 128; Hi <= 64), w fp32 [N, Hi], k_fp8 uint8 [P, D] + k_scale fp32 [P],
+ *   npool int32 [N] (each query's candidate count, clamped to [0, P]), scores fp32 [N, score_stride],
+ *   P <= score_stride.
+ */
+int dsa_indexer_prefill(const void* q_bf16, const float* w, const uint8_t* k_fp8, const float* k_scale,
+                        const int32_t* npool, float* scores, int N, int Hi, int D, int P, int score_stride,
+                        float scale, void* stream);
+
+/*
  * Exact top-k per row (replaces trnrt/models/dsa_long.py:140-186 `select_device` and the selection of
  * trnrt/kernels/dsa_topk.py:495-514 `select`; rule of trnrt/models/dsa_select.py:10-38): per row b over positions
  * t < min(len[b], score_stride), the `keep` largest scores, ties at the keep-th value to the lowest positions;

@@ -8,6 +8,9 @@ the BASELINE extensions (per-token FP8 scales; 576-wide KV = 512 latent + 64 rop
 Each function cites the reference lines it follows. How each one is pinned (tests/test_oracle_*.py):
 - indexer_ref: brute-force per-token loops, exact rational arithmetic on a tiny case, the scale-folding and
   dequantisation invariants, planted mistakes (no relu, a transposed table) that must fail;
+- prefill_scores_ref: exact rational arithmetic on a tiny case, a brute-force float64 loop, indexer_ref through an
+  identity page table, planted mistakes (an off-by-one candidate mask, no relu, one accumulator dropped) that must
+  fail;
 - topk_ref: the tie rule as a stable sort; pinned against a second independent form (topk_radix_ref, the
   reference's radix + tie search), a brute-force Python loop, the reference's literal known answer, its adversarial
   score kinds, and a planted wrong tie rule that must fail;
@@ -68,6 +71,32 @@ def indexer_ref(q_idx: torch.Tensor, w_k: torch.Tensor, k_cache: torch.Tensor, k
         K = row_tokens(k_cache, k_scale, table[b], L, page_size)  # [L, D]
         s = torch.einsum("hd,td->ht", q_idx[b].float(), K)  # dsa_long.py:79-80 (the 3-D branch, one row)
         out[b, :L] = torch.einsum("h,ht->t", w_k[b].float(), torch.relu(s))  # dsa_long.py:81
+    return out
+
+
+def prefill_scores_ref(qI: torch.Tensor, w: torch.Tensor, k8: torch.Tensor, k_scale: torch.Tensor,
+                       npool: torch.Tensor, scale: float, stride: int | None = None) -> torch.Tensor:
+    """[N, stride] fp32 index scores of N queries over one context's P keys (a prefill chunk), the arithmetic of
+    trnrt/kernels/dsa_long_select.py:119-133 `emulate_scores` with pk the dequantised FP8 keys: r_h = relu(scale
+    (qI_h . pk)) in fp32, the even heads summed in head order into A0 (which starts at the candidate term: 0 for
+    p < npool[n], NEG_INF otherwise, dsa_long_select.py:59-61), the odd heads into A1, the score A0 + A1; positions
+    P .. stride - 1 are NEG_INF."""
+    N, Hi, _ = qI.shape
+    P = k8.shape[0]
+    stride = P if stride is None else stride
+    pk = dequant(k8, k_scale)  # [P, D]
+    s = torch.einsum("nhd,pd->nhp", qI.float(), pk)
+    r = torch.relu(s * scale)
+    npool = npool.long().clamp(0, P).view(N, 1)
+    a0 = torch.where(torch.arange(P).view(1, P) < npool, 0.0, NEG_INF).float()
+    a1 = torch.zeros_like(a0)
+    for h in range(Hi):
+        if h % 2:
+            a1 = r[:, h] * w[:, h:h + 1].float() + a1
+        else:
+            a0 = r[:, h] * w[:, h:h + 1].float() + a0
+    out = torch.full((N, stride), NEG_INF, dtype=torch.float32)
+    out[:, :P] = a0 + a1
     return out
 
 

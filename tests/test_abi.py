@@ -88,3 +88,15 @@ def test_check_maps_status_to_the_reference_exceptions():
     with pytest.raises(RuntimeError):
         _lib.check(-4, "x")
     _lib.check(0, "x")
+
+
+def test_prefill_host_checks():
+    lib = _lib.lib()
+    p = ctypes.c_void_p(16)
+    null = None
+    assert lib.dsa_indexer_prefill(p, p, p, p, p, null, 4, 64, 128, 100, 100, 0.1, null) == -1  # no output
+    assert lib.dsa_indexer_prefill(p, p, p, p, p, p, 4, 64, 128, 100, 99, 0.1, null) == -1  # stride < P
+    assert lib.dsa_indexer_prefill(p, p, p, p, p, p, 4, 64, 128, 100, 100, 0.0, null) == -1  # scale 0
+    assert lib.dsa_indexer_prefill(p, p, p, p, p, p, 4, 65, 128, 100, 100, 0.1, null) == -2  # Hi 65
+    assert lib.dsa_indexer_prefill(p, p, p, p, p, p, 4, 64, 64, 100, 100, 0.1, null) == -2  # D 64
+    assert lib.dsa_indexer_prefill(p, p, p, p, p, p, 0, 64, 128, 100, 100, 0.1, null) == 0  # nothing to do

@@ -1,0 +1,134 @@
+"""GPU parity of the prefill-chunk indexer and selection (trnrt_amd.kernels.dsa_long_select -> dsa_indexer_prefill,
+dsa_topk) against the oracle (oracle/dsa_oracle.py prefill_scores_ref, after trnrt/kernels/dsa_long_select.py:
+119-133; topk_ref, after trnrt/models/dsa_long.py:114-118) on the same seeded inputs.
+
+Bounds: scores within max|diff| / max|ref| <= 1e-2 per row (the north star; the products are exact in bf16 x bf16
+-> fp32, so the real error is fp32 summation order); the selection bit-exact when fed the kernel's own scores; the
+non-candidates exactly NEG_INF."""
+
+import pytest
+import torch
+
+from oracle import dsa_oracle as O
+from tests._helpers import row_rel_err, say
+from trnrt_amd import workloads as W
+from trnrt_amd.kernels import dsa_long_select as LS
+from trnrt_amd.models import dsa_long
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-2
+
+
+def _inputs(N, Hi, P, seed, npool=None):
+    g = torch.Generator().manual_seed(seed)
+    qI = torch.randn(N, Hi, 128, generator=g).to(torch.bfloat16)
+    w = torch.randn(N, Hi, generator=g) * 0.25
+    k8, ks = W.quantize_rows(torch.randn(P, 128, generator=g))
+    if npool is None:
+        npool = torch.randint(0, P + 1, (N,), generator=g)
+    return qI, w, k8, ks, torch.as_tensor(npool, dtype=torch.int32)
+
+
+def _check_scores(qI, w, k8, ks, npool, scale, stride=None):
+    got = LS.scores(qI.cuda(), w.cuda(), k8.cuda(), npool.cuda(), scale, pk_scale=ks.cuda(), stride=stride)
+    torch.cuda.synchronize()
+    got = got.cpu()
+    ref = O.prefill_scores_ref(qI, w, k8, ks, npool, scale, stride)
+    live = ref > -1e29
+    err = row_rel_err(got, ref, live)
+    say(f"  prefill scores rel err {err:.3e}")
+    assert err <= TOL
+    assert torch.all(got[~live] == O.NEG_INF)
+    return got
+
+
+@pytest.mark.parametrize("N,Hi,P,stride", [(5, 16, 100, None), (7, 64, 1000, 1100), (4, 48, 2053, None),
+                                           (9, 33, 64, 96), (1, 1, 1, None), (13, 64, 4096, None)])
+def test_scores_vs_oracle(N, Hi, P, stride):
+    say(f"prefill scores N={N} Hi={Hi} P={P} stride={stride}")
+    qI, w, k8, ks, npool = _inputs(N, Hi, P, seed=N * 1000 + Hi)
+    npool[0] = P + 5  # clamped to P
+    if N > 1:
+        npool[1] = 0  # no candidates: a row of NEG_INF
+    _check_scores(qI, w, k8, ks, npool, 128 ** -0.5, stride)
+
+
+def test_causal_chunk_small():
+    """A small chunk of the config-5 form: 256 cached keys, 70 new queries at positions 256 .. 325."""
+    say("prefill causal chunk 256+70")
+    cfg = W.PrefillConfig("small", cached=256, chunk=70)
+    inp = W.make_prefill_inputs(cfg, seed=5)
+    _check_scores(inp.qI, inp.w, inp.k8, inp.k_scale, inp.npool, cfg.scale)
+
+
+@pytest.mark.parametrize("P,keep", [(5000, 2048), (3000, 64), (40000, 2048)])
+def test_select_exact_on_the_kernels_scores(P, keep):
+    say(f"prefill select P={P} keep={keep}")
+    N = 6
+    qI, w, k8, ks, npool = _inputs(N, 64, P, seed=P + keep)
+    npool[2] = keep - 7  # fewer candidates than keep: all of them
+    npool[3] = 0
+    args = (qI.cuda(), w.cuda(), k8.cuda(), npool.cuda())
+    sc = LS.scores(*args, 128 ** -0.5, pk_scale=ks.cuda()).cpu()
+    pools, cnt, vals = LS.select(*args, keep, 128 ** -0.5, pk_scale=ks.cuda())
+    torch.cuda.synchronize()
+    ri, rc = O.topk_ref(sc, keep, npool)
+    assert torch.equal(pools.cpu(), ri)
+    assert torch.equal(cnt.cpu(), rc)
+    assert torch.equal(cnt.cpu(), npool.long().clamp(0, P).clamp(max=keep))
+    live = torch.arange(keep).view(1, -1) < rc.view(-1, 1)
+    assert torch.equal(vals.cpu(), torch.where(live, sc.gather(1, ri), O.NEG_INF))
+    vp, vc, vv = LS.select(*args, keep, 128 ** -0.5, vorder=True, pk_scale=ks.cuda())
+    assert torch.equal(vc.cpu(), rc)
+    for n in range(N):  # the same set, by score descending then pool ascending
+        c = int(rc[n])
+        assert torch.equal(torch.sort(vp[n, :c].cpu()).values, ri[n, :c])
+        v = vv[n, :c].cpu()
+        assert torch.all(v[:-1] >= v[1:])
+        assert torch.all(vp[n, c:] == 0) and torch.all(vv[n, c:] == O.NEG_INF)
+
+
+def test_decode_batch_form_of_dsa_long_scores():
+    """dsa_long.scores with one context per row ([N, P, 128] keys) through the decode indexer."""
+    say("dsa_long.scores 3-D keys")
+    N, Hi, P = 3, 64, 320
+    g = torch.Generator().manual_seed(9)
+    qI = torch.randn(N, Hi, 128, generator=g).to(torch.bfloat16)
+    w = torch.randn(N, Hi, generator=g) * 0.25
+    k8, ks = W.quantize_rows(torch.randn(N * P, 128, generator=g))
+    npool = torch.tensor([320, 17, 0])
+    got = dsa_long.scores(qI.cuda(), w.cuda(), k8.view(N, P, 128).cuda(), npool.cuda(), 128 ** -0.5,
+                          pk_scale=ks.view(N, P).cuda())
+    torch.cuda.synchronize()
+    got = got.cpu()
+    for n in range(N):
+        ref = O.prefill_scores_ref(qI[n:n + 1], w[n:n + 1], k8[n * P:(n + 1) * P], ks[n * P:(n + 1) * P],
+                                   npool[n:n + 1], 128 ** -0.5)
+        live = ref > -1e29
+        assert row_rel_err(got[n:n + 1], ref, live) <= TOL
+        assert torch.all(got[n:n + 1][~live] < -1e29)
+
+
+def test_config5_full_size_sampled_rows():
+    """Config 5 (65,536 cached + 2,048 new queries, 64 heads): every row's candidate count and NEG_INF tail, and
+    the oracle on sampled rows; the selection of those rows bit-exact on the kernel's scores."""
+    cfg = W.PREFILL_CONFIGS[5]
+    say(f"prefill config 5 {cfg.name}")
+    inp = W.make_prefill_inputs(cfg, seed=0, device="cuda")
+    pools, cnt, vals = LS.select(inp.qI, inp.w, inp.k8, inp.npool, cfg.keep, cfg.scale, pk_scale=inp.k_scale)
+    sc = LS.scores(inp.qI, inp.w, inp.k8, inp.npool, cfg.scale, pk_scale=inp.k_scale)
+    torch.cuda.synchronize()
+    assert torch.all(cnt == cfg.keep)
+    P = cfg.P
+    live = torch.arange(P, device="cuda").view(1, P) < inp.npool.view(-1, 1).long()
+    assert torch.all((sc > -1e29) == live)
+    rows = [0, 1, 2, 3, 777, 1024, 2045, 2046, 2047]
+    c = inp.to("cpu")
+    ref = O.prefill_scores_ref(c.qI[rows], c.w[rows], c.k8, c.k_scale, c.npool[rows], cfg.scale)
+    got = sc[rows].cpu()
+    err = row_rel_err(got, ref, ref > -1e29)
+    say(f"  config 5 sampled rel err {err:.3e}")
+    assert err <= TOL
+    ri, rc = O.topk_ref(got, cfg.keep, c.npool[rows])
+    assert torch.equal(pools[rows].cpu(), ri)
+    assert torch.equal(vals[rows].cpu(), got.gather(1, ri))

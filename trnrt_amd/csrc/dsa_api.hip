@@ -9,6 +9,9 @@ hipError_t launch_indexer_decode(const uint16_t* q, const float* w, const uint8_
                                  const int* table, const int* ctx_len, const float* cand, float* scores, int* hist,
                                  int B, int Hi, int max_pages, int page_size, int num_pages, int stride, int num_cu,
                                  hipStream_t stream);
+hipError_t launch_indexer_prefill(const uint16_t* q, const float* w, const uint8_t* k, const float* ks,
+                                  const int* npool, float* scores, int N, int Hi, int P, int stride, float scale,
+                                  hipStream_t s);
 hipError_t launch_topk(const float* scores, const int* len, int* idx, int* cnt, void* ws, int B, int stride,
                        int max_len, int keep, int vis_only, bool hist_ready, const int* table, int max_pages,
                        int page_size, int num_pages, int* rows_out, hipStream_t s);
@@ -115,6 +118,17 @@ int dsa_indexer_decode(const void* q_bf16, const float* w, const uint8_t* k_fp8,
   return status(dsa::launch_indexer_decode(static_cast<const uint16_t*>(q_bf16), w, k_fp8, k_scale, page_table,
                                            ctx_len, cand, scores, nullptr, B, Hi, max_pages, page_size, num_pages,
                                            score_stride, num_cu(), static_cast<hipStream_t>(stream)));
+}
+
+int dsa_indexer_prefill(const void* q_bf16, const float* w, const uint8_t* k_fp8, const float* k_scale,
+                        const int32_t* npool, float* scores, int N, int Hi, int D, int P, int score_stride,
+                        float scale, void* stream) {
+  if (!q_bf16 || !w || !k_fp8 || !k_scale || !npool || !scores) return DSA_EINVAL;
+  if (N < 0 || Hi < 1 || P < 1 || score_stride < P || !(scale > 0.0f)) return DSA_EINVAL;
+  if (D != 128 || Hi > 64) return DSA_EUNSUPPORTED;
+  if (N == 0) return DSA_OK;
+  return status(dsa::launch_indexer_prefill(static_cast<const uint16_t*>(q_bf16), w, k_fp8, k_scale, npool, scores, N,
+                                            Hi, P, score_stride, scale, static_cast<hipStream_t>(stream)));
 }
 
 int dsa_topk(const float* scores, const int32_t* len, int32_t* idx, int32_t* cnt, void* workspace,

@@ -1,0 +1,113 @@
+"""Exact indexer selection of a prefill chunk on gfx950 (the operator surface of trnrt/kernels/dsa_long_select.py).
+
+What it computes, for N queries that share ONE context's keys (trnrt/kernels/dsa_long_select.py:5-11, 119-133):
+
+    index[n, p] = sum_h w[n, h] relu(scale (qI[n, h] . pk[p]))     for p < npool[n]  (NEG_INF otherwise)
+
+with pk the FP8 e4m3 keys times their per-token fp32 scales, then the keep largest candidates of each query, ties to
+the lowest key index, all of them when fewer, returned as key indices [N, keep] in ascending order with 0 past the
+count min(npool, keep).
+
+How: two launches. csrc/dsa_prefill.hip scores the chunk as a batched GEMM on bf16 MFMA (the e4m3 keys converted
+exactly to bf16 once per workgroup in LDS and shared by four queries; relu, the head weights and the per-token key
+scale applied to the fp32 accumulators in registers), writing the [N, P] fp32 scores once; csrc/dsa_topk.hip then
+selects each row exactly (rows above 32,768 keys by the two-level exact selection of trnrt/models/dsa_long.py:26-42).
+The reference's `sub` (its sub-block size) is accepted and ignored: the selection is exact for every shape.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+from . import _common as C
+from . import dsa_topk
+
+NEG_INF = -1e30  # trnrt/models/decoder.py NEG_INF
+VISIBLE = -5e29  # trnrt/kernels/dsa_topk.VISIBLE
+D = 128  # index_head_dim
+HI_MAX = 64  # heads per query the kernel holds (the reference's NKI kernel takes 32)
+
+
+def supported(Hi: int, D_: int, P: int, keep: int, sub: int = 0) -> bool:
+    """Shapes the kernels take (trnrt/kernels/dsa_long_select.py:136-145): 128-dim keys, 1..64 heads, and a top-k
+    of keep out of P that the selection kernel supports. sub is the reference's knob and does not restrict."""
+    del sub
+    return D_ == D and 1 <= Hi <= HI_MAX and P >= 1 and keep >= 1 and dsa_topk.supported(1, P, keep, True)
+
+
+def pick_sub(P: int, keep: int) -> int:
+    """The reference's sub-block choice (trnrt/kernels/dsa_long_select.py:475-491) has no meaning here: 0."""
+    del P, keep
+    return 0
+
+
+def scores(qI: torch.Tensor, w: torch.Tensor, pk: torch.Tensor, npool: torch.Tensor, scale: float, *,
+           pk_scale: torch.Tensor, stride: int | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """[N, stride] fp32 index scores (NEG_INF at p >= npool[n] and past P): qI [N, Hi, 128] bf16, w [N, Hi] fp32,
+    pk [P, 128] e4m3fn keys (or their uint8 bits) with pk_scale [P] fp32, npool [N] int (clamped to [0, P]),
+    scale > 0 (trnrt/kernels/dsa_long_select.py:119-133 `emulate_scores`)."""
+    dev = C.on_gpu(qI, w, pk, pk_scale, npool, out)
+    if qI.dim() != 3:
+        raise ValueError(f"dsa_long_select: qI {tuple(qI.shape)}, expected [N, Hi, {D}]")
+    N, Hi, Dq = qI.shape
+    pk = C.fp8_bytes(pk, "pk")
+    if pk.dim() != 2:
+        raise ValueError(f"dsa_long_select: pk {tuple(pk.shape)}, expected [P, {D}]")
+    P = pk.shape[0]
+    if Dq != D or pk.shape[1] != D or not 1 <= Hi <= HI_MAX:
+        raise NotImplementedError(f"dsa_long_select: Hi {Hi}, D {Dq}/{pk.shape[1]} (the kernel takes D {D}, "
+                                  f"Hi <= {HI_MAX})")
+    if not scale > 0:
+        raise ValueError(f"dsa_long_select: scale {scale} must be positive")
+    stride = P if stride is None else int(stride)
+    if stride < P:
+        raise ValueError(f"dsa_long_select: stride {stride} < {P} keys")
+    qI = C.as_bf16(qI)
+    w = C.need(C.as_f32(w), "w", torch.float32, (N, Hi))
+    pk_scale = C.need(C.as_f32(pk_scale).reshape(-1), "pk_scale", torch.float32, (P,))
+    npool = C.need(C.as_i32(npool.reshape(-1).clamp(0, P)), "npool", torch.int32, (N,))
+    if out is None:
+        out = torch.empty(N, stride, dtype=torch.float32, device=dev)
+    else:
+        C.need(out, "out", torch.float32, (N, stride))
+    st = _lib.lib().dsa_indexer_prefill(C.ptr(qI), C.ptr(w), C.ptr(pk), C.ptr(pk_scale), C.ptr(npool), C.ptr(out),
+                                        N, Hi, D, P, stride, float(scale), C.stream_ptr(dev))
+    _lib.check(st, "dsa_long_select.scores")
+    return out
+
+
+def value_order(pools: torch.Tensor, cnt: torch.Tensor, vals: torch.Tensor):
+    """A selection (pools ascending, count, scores; 0 / NEG_INF past the count) in the reference's vorder form
+    (trnrt/kernels/dsa_long_select.py:74-84): the selected pools by score descending, equal scores by pool ascending,
+    then 0 / NEG_INF."""
+    N, keep = pools.shape
+    k = torch.arange(keep, device=pools.device).view(1, keep)
+    live = k < cnt.view(N, 1)
+    key = torch.where(live, vals, torch.full_like(vals, -3.0e38))
+    order = torch.sort(key, dim=-1, descending=True, stable=True).indices
+    return (torch.where(live, pools.gather(1, order), 0), cnt, torch.where(live, vals.gather(1, order), NEG_INF))
+
+
+def select(qI: torch.Tensor, w: torch.Tensor, pk: torch.Tensor, npool: torch.Tensor, keep: int, scale: float,
+           sub: int | None = None, vorder: bool = False, *, pk_scale: torch.Tensor,
+           workspace: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(pools [N, keep] int64 ascending, 0 past the count; count [N] int64; scores [N, keep] fp32, NEG_INF past the
+    count) (trnrt/kernels/dsa_long_select.py:494-528 `select`): the scores above, then the exact top-keep per query.
+    vorder: the pools in (score descending, pool ascending) order instead. sub is accepted and ignored."""
+    del sub
+    N, Hi = qI.shape[0], qI.shape[1]
+    P = pk.shape[0]
+    if not supported(Hi, qI.shape[2], P, keep):
+        raise NotImplementedError(f"dsa_long_select: Hi {Hi}, D {qI.shape[2]}, P {P}, keep {keep}")
+    sc = scores(qI, w, pk, npool, scale, pk_scale=pk_scale)
+    lengths = npool.reshape(-1).clamp(0, P).to(torch.int32)
+    idx, cnt = dsa_topk.select_indices(sc, keep, lengths=lengths, vis_only=True, workspace=workspace)
+    pools = idx.to(torch.int64)
+    k = torch.arange(keep, device=sc.device).view(1, keep)
+    live = k < cnt.view(N, 1)
+    vals = torch.where(live, sc.gather(1, pools), NEG_INF)
+    cnt = cnt.to(torch.int64)
+    if vorder:
+        return value_order(pools, cnt, vals)
+    return pools, cnt, vals

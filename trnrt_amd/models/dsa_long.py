@@ -1,6 +1,8 @@
 """The per-token DSA decode path's selection, slots and attention (the functions of trnrt/models/dsa_long.py that
 the decode path calls, at kpool 1: each candidate is one token).
 
+- scores: the index scores of a prefill chunk (2-D keys, csrc/dsa_prefill.hip) or a decode batch (one context per
+  row, csrc/dsa_indexer.hip) (trnrt/models/dsa_long.py:74-84);
 - select_device / select: the exact top-keep of scores [N, P] as (indices [N, keep] int64 ascending, 0 past the
   count; count [N] int64) (trnrt/models/dsa_long.py:135-186), by the gfx950 top-k kernel;
 - slots: token indices -> cache rows and the 0 / NEG_INF bias (trnrt/models/dsa_long.py:189-215 at kp 1, where a
@@ -14,7 +16,7 @@ import torch
 
 from .. import _lib
 from ..kernels import _common as C
-from ..kernels import dsa_decode, dsa_topk
+from ..kernels import dsa_decode, dsa_index, dsa_long_select, dsa_topk
 
 NEG_INF = -1e30  # trnrt/models/decoder.py NEG_INF
 VISIBLE = -5e29  # trnrt/kernels/dsa_topk.VISIBLE
@@ -26,6 +28,26 @@ def npools(positions: torch.Tensor, kp: int) -> torch.Tensor:
     if kp < 1 or kp & (kp - 1):
         raise ValueError(f"kpool {kp} is not a power of two")
     return torch.div(positions.to(torch.int64) + 1, kp, rounding_mode="floor")
+
+
+def scores(qI: torch.Tensor, w: torch.Tensor, pk: torch.Tensor, npool: torch.Tensor, scale: float, *,
+           pk_scale: torch.Tensor) -> torch.Tensor:
+    """[N, P] fp32: every key's index score, NEG_INF for the non-candidates (p >= npool) (trnrt/models/dsa_long.py:
+    74-84). qI [N, Hi, 128] bf16, w [N, Hi] fp32, pk the FP8 e4m3 keys: [P, 128] (one sequence: a prefill chunk) or
+    [N, P, 128] (one context per row: a decode batch), pk_scale their per-token fp32 scales ([P] or [N, P]), npool
+    [N]. The decode form needs P a multiple of 32 (each row's keys are one page of the decode indexer)."""
+    if pk.dim() == 2:
+        return dsa_long_select.scores(qI, w, pk, npool, scale, pk_scale=pk_scale)
+    if pk.dim() != 3 or pk.shape[0] != qI.shape[0]:
+        raise ValueError(f"dsa_long.scores: pk {tuple(pk.shape)} for {qI.shape[0]} queries")
+    N, P, _ = pk.shape
+    if P % 32:
+        raise NotImplementedError(f"dsa_long.scores: {P} keys per row; the decode indexer takes multiples of 32")
+    dev = C.on_gpu(qI, w, pk, pk_scale, npool)
+    table = torch.arange(N, dtype=torch.int32, device=dev).view(N, 1)
+    lens = npool.reshape(-1).clamp(0, P).to(torch.int32)
+    return dsa_index.decode_scores(qI, w.float() * float(scale), pk.reshape(N * P, -1), pk_scale.reshape(-1), table,
+                                   lens, P, P)
 
 
 def select_device(sc: torch.Tensor, keep: int, lengths: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:

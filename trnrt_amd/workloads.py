@@ -145,3 +145,69 @@ def make_inputs(cfg: Config, seed: int = 0, device: str | torch.device = "cpu", 
     ctx_len = torch.tensor(lengths, dtype=torch.int32, device=device)
     return Inputs(cfg, lengths, q_idx, w, w * cfg.D ** -0.5, q, k_cache, k_scale, kv_cache, kv_scale, table, ctx_len,
                   num_pages, max_pages)
+
+
+# -- the chunked-prefill indexer (one sequence: cached tokens plus a chunk of new queries, causal) -----------------
+
+
+@dataclass(frozen=True)
+class PrefillConfig:
+    name: str
+    cached: int  # tokens already in the cache
+    chunk: int  # new query tokens (their keys are in the cache too)
+    Hi: int = 64
+    keep: int = 2048
+    D: int = 128
+
+    @property
+    def P(self) -> int:
+        return self.cached + self.chunk
+
+    @property
+    def scale(self) -> float:
+        return self.D ** -0.5  # the indexer's softmax-free scale (trnrt/models/mla.py:629)
+
+
+PREFILL_CONFIGS = {
+    5: PrefillConfig("prefill-65536+2048-h64", cached=65536, chunk=2048),
+}
+
+
+def prefill_flops(cfg: PrefillConfig) -> int:
+    """Algorithmic MFMA work of the chunk's scores: 2 Hi D per (query, candidate key), query i of the chunk seeing
+    cached + i + 1 keys (causal)."""
+    n = cfg.chunk * (cfg.cached + 1) + cfg.chunk * (cfg.chunk - 1) // 2
+    return 2 * cfg.Hi * cfg.D * n
+
+
+@dataclass
+class PrefillInputs:
+    cfg: PrefillConfig
+    qI: torch.Tensor  # [C, Hi, 128] bf16
+    w: torch.Tensor  # [C, Hi] fp32 ~ N(0, 1/16)
+    k8: torch.Tensor  # [P, 128] e4m3fn
+    k_scale: torch.Tensor  # [P] fp32
+    npool: torch.Tensor  # [C] int32: position + 1 (causal: key t <= the query's position)
+
+    def to(self, device) -> "PrefillInputs":
+        kw = {k: (v.to(device) if isinstance(v, torch.Tensor) else v) for k, v in self.__dict__.items()}
+        return PrefillInputs(**kw)
+
+
+def make_prefill_inputs(cfg: PrefillConfig, seed: int = 0, device: str | torch.device = "cpu",
+                        chunk: int = 65536) -> PrefillInputs:
+    """Seeded inputs of one chunk's indexer: queries ~N(0, 1) in bf16, weights ~N(0, 1/16), keys ~N(0, 1)
+    quantised per token to e4m3fn (scale absmax / 448); query i sits at position cached + i."""
+    device = torch.device(device)
+    g = _gen(device)
+    g.manual_seed(seed)
+    C, P = cfg.chunk, cfg.P
+    qI = torch.randn(C, cfg.Hi, cfg.D, generator=g, device=device).to(torch.bfloat16)
+    w = torch.randn(C, cfg.Hi, generator=g, device=device) * 0.25
+    k8 = torch.empty(P, cfg.D, dtype=FP8, device=device)
+    ks = torch.empty(P, dtype=torch.float32, device=device)
+    for s0 in range(0, P, chunk):
+        n = min(chunk, P - s0)
+        k8[s0:s0 + n], ks[s0:s0 + n] = quantize_rows(torch.randn(n, cfg.D, generator=g, device=device))
+    npool = (cfg.cached + 1 + torch.arange(C, device=device)).to(torch.int32)
+    return PrefillInputs(cfg, qI, w, k8, ks, npool)
