@@ -75,6 +75,11 @@ __device__ __forceinline__ bf16x8 fp8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
 }
 
 // Eight bf16 held as four dwords -> the MFMA operand (a bit cast).
+// relu of an fp32 value as one integer max on its bits: negative values (sign bit set) are negative integers, so
+// they become +0; non-negative values are unchanged (fmaxf would add a NaN-quieting max on every MFMA result)
+__device__ __forceinline__ float relu(float x) {
+  return __builtin_bit_cast(float, max(__builtin_bit_cast(int, x), 0));
+}
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 // fp32 -> bf16 bits, round to nearest even (finite inputs).

@@ -143,7 +143,7 @@ __global__ __launch_bounds__(IDX_THREADS, 2) void indexer_decode_kernel(
 #pragma unroll
     for (int m = 0; m < MT; ++m)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) part = fmaf(wr[m][r], fmaxf(acc[m][r], 0.0f), part);
+      for (int r = 0; r < 16; ++r) part = fmaf(wr[m][r], relu(acc[m][r]), part);
     part += __shfl_xor(part, 32, WAVE);
     float v = CAND ? part * ksc[i] + kc[i] : part * ksc[i];
     if (pos >= L) v = NEG_INF;

@@ -22,10 +22,13 @@
 namespace dsa {
 
 constexpr int PF_D = 128;
-constexpr int PF_TILE = 32;               // keys per tile
-constexpr int PF_THREADS = 256;           // 4 waves, one query each
+constexpr int PF_TILE = 32;                // keys per tile (one MFMA column block)
+constexpr int PF_THREADS = 256;            // 4 waves, one query each
 constexpr int PF_QPW = PF_THREADS / WAVE;  // queries per workgroup
-constexpr int PF_TILES = 32;              // tiles per workgroup: 1024 keys
+constexpr int PF_TILES = 64;               // tiles per workgroup: 2048 keys
+constexpr int PF_TPB = 4;                  // tiles per barrier (a "round": 128 keys)
+constexpr int PF_RING = 2 * PF_TPB;        // tiles in flight per thread: two rounds ahead
+static_assert(PF_TILES % PF_RING == 0, "a block is whole ring turns");
 
 // MT: head tiles of 32 (Hi <= 32 MT).
 template <int MT>
@@ -33,7 +36,10 @@ __global__ __launch_bounds__(PF_THREADS, 2) void indexer_prefill_kernel(
     const uint16_t* __restrict__ q, const float* __restrict__ w, const uint8_t* __restrict__ kcache,
     const float* __restrict__ kscale, const int* __restrict__ npool, float* __restrict__ scores, int N, int Hi, int P,
     int stride, float scale) {
-  __shared__ u32x4 kb[2][PF_TILE * 16];  // two bf16 tiles: key j, 16 pieces of 8 dims (swizzled)
+  // two rounds of bf16 tiles (key j of a tile: 16 pieces of 8 dims, piece p at slot 16 j + (p ^ (j & 15))), the
+  // block's per-key scales and the queries' candidate counts
+  __shared__ u32x4 kb[2][PF_TPB][PF_TILE * 16];
+  __shared__ float ksc_s[PF_TILES * PF_TILE];
   __shared__ int lmax[PF_QPW];
   const int wave = threadIdx.x / WAVE;
   const int lane = threadIdx.x & (WAVE - 1);
@@ -43,6 +49,24 @@ __global__ __launch_bounds__(PF_THREADS, 2) void indexer_prefill_kernel(
   const int nq = min(n, N - 1);  // a wave past N computes a copy of the last query and stores nothing
   const int p_begin = blockIdx.y * PF_TILES * PF_TILE;
   const int p_end = min(p_begin + PF_TILES * PF_TILE, stride);
+  const int ntiles = (p_end - p_begin + PF_TILE - 1) / PF_TILE;
+
+  // this thread's share of a tile: key t / 8, bytes 16 (t % 8) .. + 15 (coalesced), converted into two pieces.
+  // Tiles are prefetched PF_RING ahead into a ring of registers that is never copied (a copy of a register whose
+  // load is in flight waits for it): every loop turn below is unrolled, so each slot is a fixed register.
+  const int tk = threadIdx.x >> 3, tp = threadIdx.x & 7;
+  auto load_tile = [&](int it) {
+    const int key = min(p_begin + it * PF_TILE + tk, P - 1);  // in range whatever the block
+    return *reinterpret_cast<const u32x4*>(kcache + (size_t)key * PF_D + 16 * tp);
+  };
+  u32x4 ring[PF_RING];
+#pragma unroll
+  for (int u = 0; u < PF_RING; ++u) ring[u] = load_tile(u);
+#pragma unroll
+  for (int i = 0; i < PF_TILES * PF_TILE / PF_THREADS; ++i) {
+    const int k = i * PF_THREADS + threadIdx.x;
+    ksc_s[k] = kscale[min(p_begin + k, P - 1)];
+  }
 
   int L = min(max(npool[nq], 0), P);
   if (lane == 0) lmax[wave] = L;
@@ -70,54 +94,76 @@ __global__ __launch_bounds__(PF_THREADS, 2) void indexer_prefill_kernel(
       wr[m][r] = head < Hi ? x : 0.0f;
     }
   __syncthreads();
-  const int wg_L = max(max(lmax[0], lmax[1]), max(lmax[2], lmax[3]));  // keys past every query's count: no MFMA
+  const int wg_L = max(max(lmax[0], lmax[1]), max(lmax[2], lmax[3]));
 
-  // this thread's share of a tile: key t / 8, bytes 16 (t % 8) .. + 15 (coalesced), converted into two pieces
-  const int tk = threadIdx.x >> 3, tp = threadIdx.x & 7;
-  auto load_tile = [&](int p0) {
-    const int key = min(p0 + tk, P - 1);  // in range whatever the block
-    return *reinterpret_cast<const uint4*>(kcache + (size_t)key * PF_D + 16 * tp);
-  };
-  uint4 cur = load_tile(p_begin);
   float* srow = scores + (size_t)n * stride;
-  for (int p0 = p_begin, it = 0; p0 < p_end; p0 += PF_TILE, ++it) {
-    const uint4 nxt = load_tile(p0 + PF_TILE < p_end ? p0 + PF_TILE : p0);  // the next tile's loads fly meanwhile
-    const float ksc = kscale[min(p0 + j, P - 1)];
-    // convert and store: dims 16 tp .. +15 of key tk are pieces 2 tp, 2 tp + 1
-    u32x4* tile = kb[it & 1];
-    {
-      const bf16x8 lo = fp8x8_to_bf16x8(cur.x, cur.y), hi = fp8x8_to_bf16x8(cur.z, cur.w);
-      tile[16 * tk + ((2 * tp) ^ (tk & 15))] = __builtin_bit_cast(u32x4, lo);
-      tile[16 * tk + ((2 * tp + 1) ^ (tk & 15))] = __builtin_bit_cast(u32x4, hi);
-    }
-    cur = nxt;
-    __syncthreads();  // the tile is in LDS; the other buffer is free (every wave finished the previous tile)
-    const int pos = p0 + j;
-    if (p0 < wg_L) {
-      f32x16 acc[MT];
-#pragma unroll
-      for (int m = 0; m < MT; ++m)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[m][r] = 0.0f;
-#pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const int pc = 2 * s + h;
-        const bf16x8 kbv = __builtin_bit_cast(bf16x8, tile[16 * j + (pc ^ (j & 15))]);
-#pragma unroll
-        for (int m = 0; m < MT; ++m) acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa[m][s], kbv, acc[m], 0, 0, 0);
-      }
-      float part = 0.0f;
-#pragma unroll
-      for (int m = 0; m < MT; ++m)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) part = fmaf(wr[m][r], fmaxf(acc[m][r], 0.0f), part);
-      part += __shfl_xor(part, 32, WAVE);
-      const float v = pos < L ? part * (ksc * scale) : NEG_INF;
-      if (n < N && h == 0 && pos < p_end) srow[pos] = v;
-    } else if (n < N && h == 0 && pos < p_end) {
-      srow[pos] = NEG_INF;
-    }
+  if (p_begin >= wg_L) {  // no query of the workgroup has a candidate in the block: no MFMA
+    if (n < N)
+      for (int p = p_begin + lane; p < p_end; p += WAVE) srow[p] = NEG_INF;
+    return;
   }
+
+  // The relu-weighted head sum of tile t - 1 (accumulators `prev`) runs between the MFMAs of tile t (into `cur`),
+  // so the VALU work of one tile overlaps the matrix work of the next.
+  auto epilogue_part = [&](float& part, const f32x16(&prev)[MT], int s) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int e = 2 * s; e < 2 * s + 2; ++e) part = fmaf(wr[m][e], relu(prev[m][e]), part);
+  };
+  auto finish = [&](float part, int t) {  // score of tile t's key j, stored by the lanes of half 0
+    part += __shfl_xor(part, 32, WAVE);
+    const int pos = p_begin + t * PF_TILE + j;
+    const float v = pos < L ? part * (ksc_s[t * PF_TILE + j] * scale) : NEG_INF;
+    if (n < N && h == 0 && pos < p_end) srow[pos] = v;
+  };
+  auto tile_mma = [&](const u32x4* tile, int t, f32x16(&cur)[MT], const f32x16(&prev)[MT]) {
+    float part = 0.0f;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const int pc = 2 * s + h;
+      const bf16x8 kbv = __builtin_bit_cast(bf16x8, tile[16 * j + (pc ^ (j & 15))]);
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+        cur[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa[m][s], kbv, s == 0 ? f32x16{} : cur[m], 0, 0, 0);
+      epilogue_part(part, prev, s);
+    }
+    if (t > 0) finish(part, t - 1);
+  };
+  f32x16 acc_a[MT], acc_b[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) acc_b[m] = f32x16{};
+  // a round: convert the round's PF_TPB tiles from their ring slots into LDS, refill the slots PF_RING tiles ahead,
+  // one barrier, then the round's tiles on MFMA (even tiles into acc_a, odd into acc_b). Whole ring turns are run
+  // unconditionally (each slot then has the same loads in flight after it); tiles past the block's last tile load
+  // clamped keys and store nothing (their positions are at or past p_end).
+  auto round = [&](int t0, auto base) {
+    constexpr int U0 = decltype(base)::value;
+    u32x4(*tiles)[PF_TILE * 16] = kb[(t0 / PF_TPB) & 1];
+#pragma unroll
+    for (int u = 0; u < PF_TPB; ++u) {
+      const u32x4 r = ring[U0 + u];
+      const bf16x8 lo = fp8x8_to_bf16x8(r[0], r[1]), hi = fp8x8_to_bf16x8(r[2], r[3]);
+      tiles[u][16 * tk + ((2 * tp) ^ (tk & 15))] = __builtin_bit_cast(u32x4, lo);
+      tiles[u][16 * tk + ((2 * tp + 1) ^ (tk & 15))] = __builtin_bit_cast(u32x4, hi);
+      ring[U0 + u] = load_tile(t0 + u + PF_RING);
+    }
+    __syncthreads();  // the round is in LDS; the other round's buffers are free (every wave finished them)
+#pragma unroll
+    for (int u = 0; u < PF_TPB; u += 2) {
+      tile_mma(tiles[u], t0 + u, acc_a, acc_b);
+      tile_mma(tiles[u + 1], t0 + u + 1, acc_b, acc_a);
+    }
+  };
+  int t = 0;
+  for (; t < ntiles; t += PF_RING) {
+    round(t, std::integral_constant<int, 0>{});
+    round(t + PF_TPB, std::integral_constant<int, PF_TPB>{});
+  }
+  float part = 0.0f;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) epilogue_part(part, acc_b, s);
+  finish(part, t - 1);
 }
 
 template <int MT>
