@@ -11,6 +11,7 @@ bytes per launch over its HIP-event-timed average duration) and the CPU baseline
 the reference arithmetic, timed on this host's cores on a bounded sample of the same workload).
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--config 2] [--no-cpu-baseline]
+    python bench.py --config 5          # the chunked-prefill selection (65,536 cached + 2,048 new queries): its own line
     python bench.py --copy-probe 512    # plain device copies of 512 MiB: the calibration run for HBM counters
 
 roofline.traffic (HBM bytes per indexer launch) comes from rocprofv3 FETCH_SIZE / WRITE_SIZE counter runs of this
@@ -31,6 +32,8 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
+BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+FP8_PEAK_TFLOPS = 5000.0  # MI355X dense fp8 MFMA
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
 
@@ -143,6 +146,94 @@ def kernel_times(lib, step, steps: int, pairs: int = 16) -> dict:
     return {k: v / steps for k, v in tot.items()}
 
 
+def prefill_cpu_baseline(inp, cfg, budget_s: float = 15.0) -> dict:
+    """The oracle's chunk selection (prefill_scores_ref + topk_ref, torch fp32 on the host) over whole query rows of
+    the same chunk, as many rows as fit in about budget_s seconds; reported as chunks per second (rows / 2,048)."""
+    import torch
+
+    from oracle import dsa_oracle as O
+
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    torch.set_num_threads(cores)
+    cpu = inp.to("cpu")
+    rows, t0, n = 4, time.perf_counter(), 0
+    while True:
+        r0 = (n * rows) % cfg.chunk
+        sl = slice(r0, r0 + rows)
+        sc = O.prefill_scores_ref(cpu.qI[sl], cpu.w[sl], cpu.k8, cpu.k_scale, cpu.npool[sl], cfg.scale)
+        O.topk_ref(sc, cfg.keep)
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= budget_s or n * rows >= cfg.chunk:
+            break
+    done = n * rows
+    return {"value": done / cfg.chunk / dt, "unit": "chunks/s", "cores": cores, "kind": "port",
+            "sample": f"{done} of the chunk's {cfg.chunk} query rows (scores over {cfg.P} keys + top-{cfg.keep}, "
+                      f"torch fp32, {dt:.1f} s, {cores} threads)"}
+
+
+def prefill_main(args) -> int:
+    """The chunked-prefill selection (config 5): one step = the dense indexer scores of the chunk's queries over the
+    cached + new keys (bf16 MFMA) and the exact top-2048 of every query row. roofline: the indexer kernel's
+    algorithmic MFMA work (2 Hi D per causal (query, key) pair) over its HIP-event-timed duration."""
+    import torch
+
+    from trnrt_amd import _lib
+    from trnrt_amd import workloads as W
+    from trnrt_amd.kernels import dsa_long_select as LS
+
+    cfg = W.PREFILL_CONFIGS[args.config]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    inp = W.make_prefill_inputs(cfg, seed=0, device=dev)
+    wsb = _lib.workspace_bytes(_lib.DSA_WS_TOPK, cfg.chunk, 0, cfg.keep, cfg.P)
+    ws = torch.zeros(wsb, dtype=torch.uint8, device=dev)  # the top-k histograms start (and end) at zero
+    lib = _lib.lib()
+
+    def step():
+        LS.select(inp.qI, inp.w, inp.k8, inp.npool, cfg.keep, cfg.scale, pk_scale=inp.k_scale, workspace=ws)
+
+    steps = min(args.steps, 20)
+    for _ in range(min(args.warmup, 5)):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    k_us = kernel_times(lib, step, steps)
+    flops = W.prefill_flops(cfg)
+    idx_us = k_us["indexer_prefill_kernel"]
+    tflops = flops / (idx_us * 1e-6) / 1e12
+    out = {
+        "metric": "DSA chunked-prefill selection (indexer + top-2048) chunks/sec; indexer MFMA TFLOP/s",
+        "value": round(1e3 / ms, 2),
+        "unit": "chunks/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": min(args.warmup, 5),
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"config {args.config}: {cfg.name}", "cached": cfg.cached, "chunk": cfg.chunk,
+                   "indexer_heads": cfg.Hi, "keep": cfg.keep, "keys": "fp8 e4m3 [128] + fp32 scale per token",
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "kernel": "indexer_prefill_kernel", "achieved": round(tflops, 1),
+                     "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                     "fp8_peak_frac": round(tflops / FP8_PEAK_TFLOPS, 4), "traffic": None,
+                     "algorithmic_flops": flops, "avg_us": round(idx_us, 3)},
+        "kernel_us": {k: round(v, 3) for k, v in k_us.items()},
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = prefill_cpu_baseline(inp, cfg)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -159,6 +250,8 @@ def main() -> int:
         return 2
     if args.copy_probe:
         return copy_probe(args.copy_probe)
+    if args.config == 5:
+        return prefill_main(args)
 
     import torch
 
