@@ -156,11 +156,12 @@ def prefill_cpu_baseline(inp, cfg, budget_s: float = 15.0) -> dict:
     cores = min(len(os.sched_getaffinity(0)), 16)
     torch.set_num_threads(cores)
     cpu = inp.to("cpu")
+    qv = cpu.q_values()  # the queries' values (dequantised when FP8)
     rows, t0, n = 4, time.perf_counter(), 0
     while True:
         r0 = (n * rows) % cfg.chunk
         sl = slice(r0, r0 + rows)
-        sc = O.prefill_scores_ref(cpu.qI[sl], cpu.w[sl], cpu.k8, cpu.k_scale, cpu.npool[sl], cfg.scale)
+        sc = O.prefill_scores_ref(qv[sl], cpu.w[sl], cpu.k8, cpu.k_scale, cpu.npool[sl], cfg.scale)
         O.topk_ref(sc, cfg.keep)
         n += 1
         dt = time.perf_counter() - t0
@@ -191,7 +192,8 @@ def prefill_main(args) -> int:
     lib = _lib.lib()
 
     def step():
-        LS.select(inp.qI, inp.w, inp.k8, inp.npool, cfg.keep, cfg.scale, pk_scale=inp.k_scale, workspace=ws)
+        LS.select(inp.qI, inp.w, inp.k8, inp.npool, cfg.keep, cfg.scale, pk_scale=inp.k_scale, qI_scale=inp.qI_scale,
+                  workspace=ws)
 
     steps = min(args.steps, 20)
     for _ in range(min(args.warmup, 5)):
@@ -204,7 +206,8 @@ def prefill_main(args) -> int:
     ms = (time.perf_counter() - t0) * 1e3 / steps
     k_us = kernel_times(lib, step, steps)
     flops = W.prefill_flops(cfg)
-    idx_us = k_us["indexer_prefill_kernel"]
+    kname = "indexer_prefill_fp8_kernel" if cfg.q_fp8 else "indexer_prefill_kernel"
+    idx_us = k_us[kname]
     tflops = flops / (idx_us * 1e-6) / 1e12
     out = {
         "metric": "DSA chunked-prefill selection (indexer + top-2048) chunks/sec; indexer MFMA TFLOP/s",
@@ -217,14 +220,16 @@ def prefill_main(args) -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "fp8" if cfg.q_fp8 else "bf16",
         "data": "synthetic",
         "config": {"workload": f"config {args.config}: {cfg.name}", "cached": cfg.cached, "chunk": cfg.chunk,
+                   "queries": "fp8 e4m3 + fp32 scale per (query, head)" if cfg.q_fp8 else "bf16",
                    "indexer_heads": cfg.Hi, "keep": cfg.keep, "keys": "fp8 e4m3 [128] + fp32 scale per token",
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "mfma", "kernel": "indexer_prefill_kernel", "achieved": round(tflops, 1),
-                     "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
-                     "fp8_peak_frac": round(tflops / FP8_PEAK_TFLOPS, 4), "traffic": None,
+        "roofline": {"bound": "mfma", "kernel": kname, "achieved": round(tflops, 1),
+                     "peak": FP8_PEAK_TFLOPS if cfg.q_fp8 else BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / (FP8_PEAK_TFLOPS if cfg.q_fp8 else BF16_PEAK_TFLOPS), 4),
+                     "bf16_peak_frac": round(tflops / BF16_PEAK_TFLOPS, 4), "traffic": None,
                      "algorithmic_flops": flops, "avg_us": round(idx_us, 3)},
         "kernel_us": {k: round(v, 3) for k, v in k_us.items()},
     }

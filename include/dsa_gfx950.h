@@ -76,6 +76,17 @@ int dsa_indexer_prefill(const void* q_bf16, const float* w, const uint8_t* k_fp8
                         float scale, void* stream);
 
 /*
+ * The same scores with FP8 e4m3 queries and a per-(query, head) fp32 scale (the indexer's FP8 query form; the
+ * reference's arithmetic on the dequantised queries q = q_fp8 * q_scale, trnrt/kernels/dsa_long_select.py:119-133):
+ *   scores[n, p] = scale * k_scale[p] * sum_h w[n, h] q_scale[n, h] * relu(q_fp8[n, h, :] . k_fp8[p, :])
+ *   q_fp8 uint8 [N, Hi, D] (e4m3fn bits; D must be 128; Hi <= 64), q_scale fp32 [N, Hi] (positive); the rest as
+ *   dsa_indexer_prefill.
+ */
+int dsa_indexer_prefill_fp8(const uint8_t* q_fp8, const float* q_scale, const float* w, const uint8_t* k_fp8,
+                            const float* k_scale, const int32_t* npool, float* scores, int N, int Hi, int D, int P,
+                            int score_stride, float scale, void* stream);
+
+/*
  * Exact top-k per row (replaces trnrt/models/dsa_long.py:140-186 `select_device` and the selection of
  * trnrt/kernels/dsa_topk.py:495-514 `select`; rule of trnrt/models/dsa_select.py:10-38): per row b over positions
  * t < min(len[b], score_stride), the `keep` largest scores, ties at the keep-th value to the lowest positions;

@@ -100,3 +100,7 @@ def test_prefill_host_checks():
     assert lib.dsa_indexer_prefill(p, p, p, p, p, p, 4, 65, 128, 100, 100, 0.1, null) == -2  # Hi 65
     assert lib.dsa_indexer_prefill(p, p, p, p, p, p, 4, 64, 64, 100, 100, 0.1, null) == -2  # D 64
     assert lib.dsa_indexer_prefill(p, p, p, p, p, p, 0, 64, 128, 100, 100, 0.1, null) == 0  # nothing to do
+    assert lib.dsa_indexer_prefill_fp8(p, p, p, p, p, p, null, 4, 64, 128, 100, 100, 0.1, null) == -1  # no output
+    assert lib.dsa_indexer_prefill_fp8(p, null, p, p, p, p, p, 4, 64, 128, 100, 100, 0.1, null) == -1  # no q scale
+    assert lib.dsa_indexer_prefill_fp8(p, p, p, p, p, p, p, 4, 64, 96, 100, 100, 0.1, null) == -2  # D 96
+    assert lib.dsa_indexer_prefill_fp8(p, p, p, p, p, p, p, 0, 64, 128, 100, 100, 0.1, null) == 0

@@ -3,8 +3,9 @@ dsa_topk) against the oracle (oracle/dsa_oracle.py prefill_scores_ref, after trn
 119-133; topk_ref, after trnrt/models/dsa_long.py:114-118) on the same seeded inputs.
 
 Bounds: scores within max|diff| / max|ref| <= 1e-2 per row (the north star; the products are exact in bf16 x bf16
--> fp32, so the real error is fp32 summation order); the selection bit-exact when fed the kernel's own scores; the
-non-candidates exactly NEG_INF."""
+-> fp32, and in e4m3 x e4m3 -> fp32 for FP8 queries, whose oracle input is their dequantised value, so the real
+error is fp32 summation order); the selection bit-exact when fed the kernel's own scores; the non-candidates
+exactly NEG_INF."""
 
 import pytest
 import torch
@@ -29,11 +30,18 @@ def _inputs(N, Hi, P, seed, npool=None):
     return qI, w, k8, ks, torch.as_tensor(npool, dtype=torch.int32)
 
 
-def _check_scores(qI, w, k8, ks, npool, scale, stride=None):
-    got = LS.scores(qI.cuda(), w.cuda(), k8.cuda(), npool.cuda(), scale, pk_scale=ks.cuda(), stride=stride)
+def _fp8(qI):
+    """FP8 e4m3 queries with per-(query, head) scales, and the values the oracle sees (their dequantised form)."""
+    q8, qs = W.quantize_rows(qI.float())
+    return q8, qs, q8.float() * qs.unsqueeze(-1)
+
+
+def _check_scores(qI, w, k8, ks, npool, scale, stride=None, qI_scale=None, q_values=None):
+    got = LS.scores(qI.cuda(), w.cuda(), k8.cuda(), npool.cuda(), scale, pk_scale=ks.cuda(), stride=stride,
+                    qI_scale=None if qI_scale is None else qI_scale.cuda())
     torch.cuda.synchronize()
     got = got.cpu()
-    ref = O.prefill_scores_ref(qI, w, k8, ks, npool, scale, stride)
+    ref = O.prefill_scores_ref(qI if q_values is None else q_values, w, k8, ks, npool, scale, stride)
     live = ref > -1e29
     err = row_rel_err(got, ref, live)
     say(f"  prefill scores rel err {err:.3e}")
@@ -53,12 +61,35 @@ def test_scores_vs_oracle(N, Hi, P, stride):
     _check_scores(qI, w, k8, ks, npool, 128 ** -0.5, stride)
 
 
-def test_causal_chunk_small():
+@pytest.mark.parametrize("N,Hi,P,stride", [(5, 16, 100, None), (7, 64, 1000, 1100), (4, 48, 2053, None),
+                                           (9, 33, 64, 96), (1, 1, 1, None), (13, 64, 4096, None)])
+def test_scores_fp8_queries_vs_oracle(N, Hi, P, stride):
+    say(f"prefill scores fp8 q N={N} Hi={Hi} P={P} stride={stride}")
+    qI, w, k8, ks, npool = _inputs(N, Hi, P, seed=N * 1000 + Hi + 7)
+    npool[0] = P + 5
+    if N > 1:
+        npool[1] = 0
+    q8, qs, qv = _fp8(qI)
+    _check_scores(q8, w, k8, ks, npool, 128 ** -0.5, stride, qI_scale=qs, q_values=qv)
+
+
+def test_fp8_query_argument_checks():
+    qI, w, k8, ks, npool = _inputs(2, 8, 64, seed=1)
+    q8, qs, _ = _fp8(qI)
+    with pytest.raises(ValueError):
+        LS.scores(q8.cuda(), w.cuda(), k8.cuda(), npool.cuda(), 0.1, pk_scale=ks.cuda())  # no qI_scale
+    with pytest.raises(ValueError):
+        LS.scores(qI.cuda(), w.cuda(), k8.cuda(), npool.cuda(), 0.1, pk_scale=ks.cuda(), qI_scale=qs.cuda())
+
+
+@pytest.mark.parametrize("q_fp8", [False, True])
+def test_causal_chunk_small(q_fp8):
     """A small chunk of the config-5 form: 256 cached keys, 70 new queries at positions 256 .. 325."""
-    say("prefill causal chunk 256+70")
-    cfg = W.PrefillConfig("small", cached=256, chunk=70)
+    say(f"prefill causal chunk 256+70 q_fp8={q_fp8}")
+    cfg = W.PrefillConfig("small", cached=256, chunk=70, q_fp8=q_fp8)
     inp = W.make_prefill_inputs(cfg, seed=5)
-    _check_scores(inp.qI, inp.w, inp.k8, inp.k_scale, inp.npool, cfg.scale)
+    _check_scores(inp.qI, inp.w, inp.k8, inp.k_scale, inp.npool, cfg.scale, qI_scale=inp.qI_scale,
+                  q_values=inp.q_values())
 
 
 @pytest.mark.parametrize("P,keep", [(5000, 2048), (3000, 64), (40000, 2048)])
@@ -110,13 +141,14 @@ def test_decode_batch_form_of_dsa_long_scores():
 
 
 def test_config5_full_size_sampled_rows():
-    """Config 5 (65,536 cached + 2,048 new queries, 64 heads): every row's candidate count and NEG_INF tail, and
-    the oracle on sampled rows; the selection of those rows bit-exact on the kernel's scores."""
+    """Config 5 (65,536 cached + 2,048 new queries, 64 heads, FP8 queries): every row's candidate count and NEG_INF
+    tail, and the oracle on sampled rows; the selection of those rows bit-exact on the kernel's scores."""
     cfg = W.PREFILL_CONFIGS[5]
     say(f"prefill config 5 {cfg.name}")
     inp = W.make_prefill_inputs(cfg, seed=0, device="cuda")
-    pools, cnt, vals = LS.select(inp.qI, inp.w, inp.k8, inp.npool, cfg.keep, cfg.scale, pk_scale=inp.k_scale)
-    sc = LS.scores(inp.qI, inp.w, inp.k8, inp.npool, cfg.scale, pk_scale=inp.k_scale)
+    pools, cnt, vals = LS.select(inp.qI, inp.w, inp.k8, inp.npool, cfg.keep, cfg.scale, pk_scale=inp.k_scale,
+                                 qI_scale=inp.qI_scale)
+    sc = LS.scores(inp.qI, inp.w, inp.k8, inp.npool, cfg.scale, pk_scale=inp.k_scale, qI_scale=inp.qI_scale)
     torch.cuda.synchronize()
     assert torch.all(cnt == cfg.keep)
     P = cfg.P
@@ -124,7 +156,7 @@ def test_config5_full_size_sampled_rows():
     assert torch.all((sc > -1e29) == live)
     rows = [0, 1, 2, 3, 777, 1024, 2045, 2046, 2047]
     c = inp.to("cpu")
-    ref = O.prefill_scores_ref(c.qI[rows], c.w[rows], c.k8, c.k_scale, c.npool[rows], cfg.scale)
+    ref = O.prefill_scores_ref(c.q_values()[rows], c.w[rows], c.k8, c.k_scale, c.npool[rows], cfg.scale)
     got = sc[rows].cpu()
     err = row_rel_err(got, ref, ref > -1e29)
     say(f"  config 5 sampled rel err {err:.3e}")

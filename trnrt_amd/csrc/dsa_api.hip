@@ -12,6 +12,9 @@ hipError_t launch_indexer_decode(const uint16_t* q, const float* w, const uint8_
 hipError_t launch_indexer_prefill(const uint16_t* q, const float* w, const uint8_t* k, const float* ks,
                                   const int* npool, float* scores, int N, int Hi, int P, int stride, float scale,
                                   hipStream_t s);
+hipError_t launch_indexer_prefill_fp8(const uint8_t* q8, const float* qs, const float* w, const uint8_t* k,
+                                      const float* ks, const int* npool, float* scores, int N, int Hi, int P,
+                                      int stride, float scale, hipStream_t s);
 hipError_t launch_topk(const float* scores, const int* len, int* idx, int* cnt, void* ws, int B, int stride,
                        int max_len, int keep, int vis_only, bool hist_ready, const int* table, int max_pages,
                        int page_size, int num_pages, int* rows_out, hipStream_t s);
@@ -129,6 +132,17 @@ int dsa_indexer_prefill(const void* q_bf16, const float* w, const uint8_t* k_fp8
   if (N == 0) return DSA_OK;
   return status(dsa::launch_indexer_prefill(static_cast<const uint16_t*>(q_bf16), w, k_fp8, k_scale, npool, scores, N,
                                             Hi, P, score_stride, scale, static_cast<hipStream_t>(stream)));
+}
+
+int dsa_indexer_prefill_fp8(const uint8_t* q_fp8, const float* q_scale, const float* w, const uint8_t* k_fp8,
+                            const float* k_scale, const int32_t* npool, float* scores, int N, int Hi, int D, int P,
+                            int score_stride, float scale, void* stream) {
+  if (!q_fp8 || !q_scale || !w || !k_fp8 || !k_scale || !npool || !scores) return DSA_EINVAL;
+  if (N < 0 || Hi < 1 || P < 1 || score_stride < P || !(scale > 0.0f)) return DSA_EINVAL;
+  if (D != 128 || Hi > 64) return DSA_EUNSUPPORTED;
+  if (N == 0) return DSA_OK;
+  return status(dsa::launch_indexer_prefill_fp8(q_fp8, q_scale, w, k_fp8, k_scale, npool, scores, N, Hi, P,
+                                                score_stride, scale, static_cast<hipStream_t>(stream)));
 }
 
 int dsa_topk(const float* scores, const int32_t* len, int32_t* idx, int32_t* cnt, void* workspace,

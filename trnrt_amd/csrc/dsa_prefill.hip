@@ -166,6 +166,146 @@ __global__ __launch_bounds__(PF_THREADS, 2) void indexer_prefill_kernel(
   finish(part, t - 1);
 }
 
+// The FP8-query form: q is e4m3 with a per-(query, head) fp32 scale. Then every product q8 k8 is exact in the
+// fp32 accumulator of the f8f6f4 MFMA (e4m3 x e4m3), and the query scale folds into the head weight
+// (relu(a x) = a relu(x), a > 0):
+//
+//   score[n, p] = scale * k_scale[p] * sum_h (w[n, h] q_scale[n, h]) * relu(q8[n, h, :] . k8[p, :])
+//
+// Same workgroup shape and round structure as above, but the keys stay FP8 end to end: a tile is staged into LDS
+// as raw bytes (16 B per thread, no conversion) and read by each wave as the B operand of
+// v_mfma_scale_f32_32x32x64_f8f6f4 (unit scales): 64 dims per MFMA, so 2 MFMAs per 32 heads x 32 keys instead of
+// 8 bf16 ones. Lane (j, h) at step s holds dims 64 s + 32 h .. + 31 of its head (A) and of key j (B); the
+// contraction only needs A and B to use the same lane/byte -> dim map. Key j's 16-byte piece p sits at LDS slot
+// 8 j + (p ^ g(j)), g(j) = (j ^ (j >> 3)) & 7, so any 8 (or 16) consecutive lanes of a read hit different banks.
+typedef __attribute__((__vector_size__(8 * sizeof(int)))) int i32x8;
+
+__device__ __forceinline__ int pf8_slot(int key, int piece) { return 8 * key + (piece ^ ((key ^ (key >> 3)) & 7)); }
+
+template <int MT>
+__global__ __launch_bounds__(PF_THREADS, 2) void indexer_prefill_fp8_kernel(
+    const uint8_t* __restrict__ q8, const float* __restrict__ qscale, const float* __restrict__ w,
+    const uint8_t* __restrict__ kcache, const float* __restrict__ kscale, const int* __restrict__ npool,
+    float* __restrict__ scores, int N, int Hi, int P, int stride, float scale) {
+  __shared__ u32x4 kb[2][PF_TPB][PF_TILE * 8];  // two rounds of FP8 tiles (key j: 8 pieces of 16 bytes)
+  __shared__ float ksc_s[PF_TILES * PF_TILE];
+  __shared__ int lmax[PF_QPW];
+  const int wave = threadIdx.x / WAVE;
+  const int lane = threadIdx.x & (WAVE - 1);
+  const int j = lane & 31;
+  const int h = lane >> 5;
+  const int n = blockIdx.x * PF_QPW + wave;
+  const int nq = min(n, N - 1);
+  const int p_begin = blockIdx.y * PF_TILES * PF_TILE;
+  const int p_end = min(p_begin + PF_TILES * PF_TILE, stride);
+  const int ntiles = (p_end - p_begin + PF_TILE - 1) / PF_TILE;
+
+  const int tk = threadIdx.x >> 3, tp = threadIdx.x & 7;
+  auto load_tile = [&](int it) {
+    const int key = min(p_begin + it * PF_TILE + tk, P - 1);
+    return *reinterpret_cast<const u32x4*>(kcache + (size_t)key * PF_D + 16 * tp);
+  };
+  u32x4 ring[PF_RING];
+#pragma unroll
+  for (int u = 0; u < PF_RING; ++u) ring[u] = load_tile(u);
+#pragma unroll
+  for (int i = 0; i < PF_TILES * PF_TILE / PF_THREADS; ++i) {
+    const int k = i * PF_THREADS + threadIdx.x;
+    ksc_s[k] = kscale[min(p_begin + k, P - 1)];
+  }
+  int L = min(max(npool[nq], 0), P);
+  if (lane == 0) lmax[wave] = L;
+
+  // A operand: head 32 m + j, dims 64 s + 32 h .. + 31 (zero heads past Hi); head weights times the query scales in
+  // the accumulator layout (register r of head tile m: head 32 m + 8 (r / 4) + 4 h + r % 4)
+  i32x8 qa[MT][2];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    const int head = 32 * m + j;
+    const uint8_t* qp = q8 + ((size_t)nq * Hi + min(head, Hi - 1)) * PF_D + 32 * h;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const u32x4 lo = *reinterpret_cast<const u32x4*>(qp + 64 * s);
+      const u32x4 hi = *reinterpret_cast<const u32x4*>(qp + 64 * s + 16);
+      const u32x4 z = {};
+      const u32x4 a0 = head < Hi ? lo : z, a1 = head < Hi ? hi : z;
+      qa[m][s] = i32x8{(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3], (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
+    }
+  }
+  float wr[MT][16];
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int head = 32 * m + 8 * (r >> 2) + 4 * h + (r & 3);
+      const size_t o = (size_t)nq * Hi + min(head, Hi - 1);
+      wr[m][r] = head < Hi ? w[o] * qscale[o] : 0.0f;
+    }
+  __syncthreads();
+  const int wg_L = max(max(lmax[0], lmax[1]), max(lmax[2], lmax[3]));
+
+  float* srow = scores + (size_t)n * stride;
+  if (p_begin >= wg_L) {
+    if (n < N)
+      for (int p = p_begin + lane; p < p_end; p += WAVE) srow[p] = NEG_INF;
+    return;
+  }
+
+  auto epilogue_part = [&](float& part, const f32x16(&prev)[MT], int s) {  // 8 of the 16 registers per step
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int e = 8 * s; e < 8 * s + 8; ++e) part = fmaf(wr[m][e], relu(prev[m][e]), part);
+  };
+  auto finish = [&](float part, int t) {
+    part += __shfl_xor(part, 32, WAVE);
+    const int pos = p_begin + t * PF_TILE + j;
+    const float v = pos < L ? part * (ksc_s[t * PF_TILE + j] * scale) : NEG_INF;
+    if (n < N && h == 0 && pos < p_end) srow[pos] = v;
+  };
+  auto tile_mma = [&](const u32x4* tile, int t, f32x16(&cur)[MT], const f32x16(&prev)[MT]) {
+    float part = 0.0f;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const u32x4 b0 = tile[pf8_slot(j, 4 * s + 2 * h)], b1 = tile[pf8_slot(j, 4 * s + 2 * h + 1)];
+      const i32x8 kbv = {(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+        cur[m] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa[m][s], kbv, s == 0 ? f32x16{} : cur[m], 0, 0, 0,
+                                                                 127, 0, 127);
+      epilogue_part(part, prev, s);
+    }
+    if (t > 0) finish(part, t - 1);
+  };
+  f32x16 acc_a[MT], acc_b[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) acc_b[m] = f32x16{};
+  auto round = [&](int t0, auto base) {
+    constexpr int U0 = decltype(base)::value;
+    u32x4(*tiles)[PF_TILE * 8] = kb[(t0 / PF_TPB) & 1];
+#pragma unroll
+    for (int u = 0; u < PF_TPB; ++u) {
+      tiles[u][pf8_slot(tk, tp)] = ring[U0 + u];
+      ring[U0 + u] = load_tile(t0 + u + PF_RING);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < PF_TPB; u += 2) {
+      tile_mma(tiles[u], t0 + u, acc_a, acc_b);
+      tile_mma(tiles[u + 1], t0 + u + 1, acc_b, acc_a);
+    }
+  };
+  int t = 0;
+  for (; t < ntiles; t += PF_RING) {
+    round(t, std::integral_constant<int, 0>{});
+    round(t + PF_TPB, std::integral_constant<int, PF_TPB>{});
+  }
+  float part = 0.0f;
+#pragma unroll
+  for (int s = 0; s < 2; ++s) epilogue_part(part, acc_b, s);
+  finish(part, t - 1);
+}
+
 template <int MT>
 static hipError_t launch_prefill_mt(const uint16_t* q, const float* w, const uint8_t* k, const float* ks,
                                     const int* npool, float* scores, int N, int Hi, int P, int stride, float scale,
@@ -180,6 +320,26 @@ hipError_t launch_indexer_prefill(const uint16_t* q, const float* w, const uint8
                                   hipStream_t s) {
   if (Hi <= 32) return launch_prefill_mt<1>(q, w, k, ks, npool, scores, N, Hi, P, stride, scale, s);
   return launch_prefill_mt<2>(q, w, k, ks, npool, scores, N, Hi, P, stride, scale, s);
+}
+
+}  // namespace dsa
+
+namespace dsa {
+
+template <int MT>
+static hipError_t launch_prefill_fp8_mt(const uint8_t* q8, const float* qs, const float* w, const uint8_t* k,
+                                        const float* ks, const int* npool, float* scores, int N, int Hi, int P,
+                                        int stride, float scale, hipStream_t s) {
+  const dim3 grid((N + PF_QPW - 1) / PF_QPW, (stride + PF_TILES * PF_TILE - 1) / (PF_TILES * PF_TILE));
+  return launch("indexer_prefill_fp8_kernel", indexer_prefill_fp8_kernel<MT>, grid, dim3(PF_THREADS), s, q8, qs, w, k,
+                ks, npool, scores, N, Hi, P, stride, scale);
+}
+
+hipError_t launch_indexer_prefill_fp8(const uint8_t* q8, const float* qs, const float* w, const uint8_t* k,
+                                      const float* ks, const int* npool, float* scores, int N, int Hi, int P,
+                                      int stride, float scale, hipStream_t s) {
+  if (Hi <= 32) return launch_prefill_fp8_mt<1>(q8, qs, w, k, ks, npool, scores, N, Hi, P, stride, scale, s);
+  return launch_prefill_fp8_mt<2>(q8, qs, w, k, ks, npool, scores, N, Hi, P, stride, scale, s);
 }
 
 }  // namespace dsa

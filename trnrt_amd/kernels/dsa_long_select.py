@@ -8,10 +8,13 @@ with pk the FP8 e4m3 keys times their per-token fp32 scales, then the keep large
 the lowest key index, all of them when fewer, returned as key indices [N, keep] in ascending order with 0 past the
 count min(npool, keep).
 
-How: two launches. csrc/dsa_prefill.hip scores the chunk as a batched GEMM on bf16 MFMA (the e4m3 keys converted
-exactly to bf16 once per workgroup in LDS and shared by four queries; relu, the head weights and the per-token key
-scale applied to the fp32 accumulators in registers), writing the [N, P] fp32 scores once; csrc/dsa_topk.hip then
-selects each row exactly (rows above 32,768 keys by the two-level exact selection of trnrt/models/dsa_long.py:26-42).
+How: two launches. csrc/dsa_prefill.hip scores the chunk as a batched GEMM on MFMA, writing the [N, P] fp32 scores
+once: with bf16 queries (the reference's form) on bf16 MFMA, the e4m3 keys converted exactly to bf16 once per
+workgroup in LDS and shared by four queries; with FP8 e4m3 queries and per-(query, head) scales (qI_scale=) on the
+FP8 f8f6f4 MFMA, the keys staying FP8, and each query scale folded into its head weight (relu(a x) = a relu(x),
+a > 0), which is the reference's arithmetic on the dequantised queries. Either way relu, the head weights and the
+per-token key scale are applied to the fp32 accumulators in registers. csrc/dsa_topk.hip then selects each row
+exactly (rows above 32,768 keys by the two-level exact selection of trnrt/models/dsa_long.py:26-42).
 The reference's `sub` (its sub-block size) is accepted and ignored: the selection is exact for every shape.
 """
 
@@ -43,11 +46,16 @@ def pick_sub(P: int, keep: int) -> int:
 
 
 def scores(qI: torch.Tensor, w: torch.Tensor, pk: torch.Tensor, npool: torch.Tensor, scale: float, *,
-           pk_scale: torch.Tensor, stride: int | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
-    """[N, stride] fp32 index scores (NEG_INF at p >= npool[n] and past P): qI [N, Hi, 128] bf16, w [N, Hi] fp32,
-    pk [P, 128] e4m3fn keys (or their uint8 bits) with pk_scale [P] fp32, npool [N] int (clamped to [0, P]),
-    scale > 0 (trnrt/kernels/dsa_long_select.py:119-133 `emulate_scores`)."""
-    dev = C.on_gpu(qI, w, pk, pk_scale, npool, out)
+           pk_scale: torch.Tensor, qI_scale: torch.Tensor | None = None, stride: int | None = None,
+           out: torch.Tensor | None = None) -> torch.Tensor:
+    """[N, stride] fp32 index scores (NEG_INF at p >= npool[n] and past P): qI [N, Hi, 128] bf16, or e4m3fn (its
+    uint8 bits) with qI_scale [N, Hi] fp32 > 0 (the queries are qI * qI_scale), w [N, Hi] fp32, pk [P, 128] e4m3fn
+    keys (or their uint8 bits) with pk_scale [P] fp32, npool [N] int (clamped to [0, P]), scale > 0
+    (trnrt/kernels/dsa_long_select.py:119-133 `emulate_scores`)."""
+    dev = C.on_gpu(qI, w, pk, pk_scale, npool, qI_scale, out)
+    fp8_q = qI.dtype in (C.FP8, torch.uint8)
+    if fp8_q != (qI_scale is not None):
+        raise ValueError("dsa_long_select: FP8 queries need qI_scale, bf16 queries take none")
     if qI.dim() != 3:
         raise ValueError(f"dsa_long_select: qI {tuple(qI.shape)}, expected [N, Hi, {D}]")
     N, Hi, Dq = qI.shape
@@ -63,7 +71,6 @@ def scores(qI: torch.Tensor, w: torch.Tensor, pk: torch.Tensor, npool: torch.Ten
     stride = P if stride is None else int(stride)
     if stride < P:
         raise ValueError(f"dsa_long_select: stride {stride} < {P} keys")
-    qI = C.as_bf16(qI)
     w = C.need(C.as_f32(w), "w", torch.float32, (N, Hi))
     pk_scale = C.need(C.as_f32(pk_scale).reshape(-1), "pk_scale", torch.float32, (P,))
     npool = C.need(C.as_i32(npool.reshape(-1).clamp(0, P)), "npool", torch.int32, (N,))
@@ -71,8 +78,16 @@ def scores(qI: torch.Tensor, w: torch.Tensor, pk: torch.Tensor, npool: torch.Ten
         out = torch.empty(N, stride, dtype=torch.float32, device=dev)
     else:
         C.need(out, "out", torch.float32, (N, stride))
-    st = _lib.lib().dsa_indexer_prefill(C.ptr(qI), C.ptr(w), C.ptr(pk), C.ptr(pk_scale), C.ptr(npool), C.ptr(out),
-                                        N, Hi, D, P, stride, float(scale), C.stream_ptr(dev))
+    if fp8_q:
+        qI = C.fp8_bytes(qI, "qI")
+        qI_scale = C.need(C.as_f32(qI_scale), "qI_scale", torch.float32, (N, Hi))
+        st = _lib.lib().dsa_indexer_prefill_fp8(C.ptr(qI), C.ptr(qI_scale), C.ptr(w), C.ptr(pk), C.ptr(pk_scale),
+                                                C.ptr(npool), C.ptr(out), N, Hi, D, P, stride, float(scale),
+                                                C.stream_ptr(dev))
+    else:
+        qI = C.as_bf16(qI)
+        st = _lib.lib().dsa_indexer_prefill(C.ptr(qI), C.ptr(w), C.ptr(pk), C.ptr(pk_scale), C.ptr(npool),
+                                            C.ptr(out), N, Hi, D, P, stride, float(scale), C.stream_ptr(dev))
     _lib.check(st, "dsa_long_select.scores")
     return out
 
@@ -91,16 +106,18 @@ def value_order(pools: torch.Tensor, cnt: torch.Tensor, vals: torch.Tensor):
 
 def select(qI: torch.Tensor, w: torch.Tensor, pk: torch.Tensor, npool: torch.Tensor, keep: int, scale: float,
            sub: int | None = None, vorder: bool = False, *, pk_scale: torch.Tensor,
+           qI_scale: torch.Tensor | None = None,
            workspace: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """(pools [N, keep] int64 ascending, 0 past the count; count [N] int64; scores [N, keep] fp32, NEG_INF past the
-    count) (trnrt/kernels/dsa_long_select.py:494-528 `select`): the scores above, then the exact top-keep per query.
+    count) (trnrt/kernels/dsa_long_select.py:494-528 `select`): the scores above (FP8 queries with qI_scale as there),
+    then the exact top-keep per query.
     vorder: the pools in (score descending, pool ascending) order instead. sub is accepted and ignored."""
     del sub
     N, Hi = qI.shape[0], qI.shape[1]
     P = pk.shape[0]
     if not supported(Hi, qI.shape[2], P, keep):
         raise NotImplementedError(f"dsa_long_select: Hi {Hi}, D {qI.shape[2]}, P {P}, keep {keep}")
-    sc = scores(qI, w, pk, npool, scale, pk_scale=pk_scale)
+    sc = scores(qI, w, pk, npool, scale, pk_scale=pk_scale, qI_scale=qI_scale)
     lengths = npool.reshape(-1).clamp(0, P).to(torch.int32)
     idx, cnt = dsa_topk.select_indices(sc, keep, lengths=lengths, vis_only=True, workspace=workspace)
     pools = idx.to(torch.int64)

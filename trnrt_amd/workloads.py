@@ -158,6 +158,7 @@ class PrefillConfig:
     Hi: int = 64
     keep: int = 2048
     D: int = 128
+    q_fp8: bool = False  # indexer queries as e4m3 with per-(query, head) scales (the FP8-MFMA form)
 
     @property
     def P(self) -> int:
@@ -169,7 +170,7 @@ class PrefillConfig:
 
 
 PREFILL_CONFIGS = {
-    5: PrefillConfig("prefill-65536+2048-h64", cached=65536, chunk=2048),
+    5: PrefillConfig("prefill-65536+2048-h64", cached=65536, chunk=2048, q_fp8=True),
 }
 
 
@@ -183,7 +184,8 @@ def prefill_flops(cfg: PrefillConfig) -> int:
 @dataclass
 class PrefillInputs:
     cfg: PrefillConfig
-    qI: torch.Tensor  # [C, Hi, 128] bf16
+    qI: torch.Tensor  # [C, Hi, 128] bf16, or e4m3fn when cfg.q_fp8
+    qI_scale: torch.Tensor | None  # [C, Hi] fp32 per-(query, head) scales of e4m3fn queries (absmax / 448), or None
     w: torch.Tensor  # [C, Hi] fp32 ~ N(0, 1/16)
     k8: torch.Tensor  # [P, 128] e4m3fn
     k_scale: torch.Tensor  # [P] fp32
@@ -193,16 +195,26 @@ class PrefillInputs:
         kw = {k: (v.to(device) if isinstance(v, torch.Tensor) else v) for k, v in self.__dict__.items()}
         return PrefillInputs(**kw)
 
+    def q_values(self) -> torch.Tensor:
+        """The queries' values in fp32 (dequantised when FP8): what the reference's arithmetic sees."""
+        if self.qI_scale is None:
+            return self.qI.float()
+        return self.qI.float() * self.qI_scale.unsqueeze(-1)
+
 
 def make_prefill_inputs(cfg: PrefillConfig, seed: int = 0, device: str | torch.device = "cpu",
                         chunk: int = 65536) -> PrefillInputs:
-    """Seeded inputs of one chunk's indexer: queries ~N(0, 1) in bf16, weights ~N(0, 1/16), keys ~N(0, 1)
-    quantised per token to e4m3fn (scale absmax / 448); query i sits at position cached + i."""
+    """Seeded inputs of one chunk's indexer: queries ~N(0, 1) in bf16 (with cfg.q_fp8 quantised per (query, head)
+    to e4m3fn, scale absmax / 448), weights ~N(0, 1/16), keys ~N(0, 1) quantised per token to e4m3fn (scale
+    absmax / 448); query i sits at position cached + i."""
     device = torch.device(device)
     g = _gen(device)
     g.manual_seed(seed)
     C, P = cfg.chunk, cfg.P
     qI = torch.randn(C, cfg.Hi, cfg.D, generator=g, device=device).to(torch.bfloat16)
+    qI_scale = None
+    if cfg.q_fp8:
+        qI, qI_scale = quantize_rows(qI.float())
     w = torch.randn(C, cfg.Hi, generator=g, device=device) * 0.25
     k8 = torch.empty(P, cfg.D, dtype=FP8, device=device)
     ks = torch.empty(P, dtype=torch.float32, device=device)
@@ -210,4 +222,4 @@ def make_prefill_inputs(cfg: PrefillConfig, seed: int = 0, device: str | torch.d
         n = min(chunk, P - s0)
         k8[s0:s0 + n], ks[s0:s0 + n] = quantize_rows(torch.randn(n, cfg.D, generator=g, device=device))
     npool = (cfg.cached + 1 + torch.arange(C, device=device)).to(torch.int32)
-    return PrefillInputs(cfg, qI, w, k8, ks, npool)
+    return PrefillInputs(cfg, qI, qI_scale, w, k8, ks, npool)
