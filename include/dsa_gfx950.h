@@ -153,6 +153,24 @@ int dsa_decode_layer(const void* q_idx_bf16, const float* w, const uint8_t* k_fp
                      int num_pages, int score_stride, int max_len, int keep, float scale, int splits, void* stream);
 
 /*
+ * Quantise-on-write of n_rows rows into a paged FP8 cache, the cache-store step before the path (replaces
+ * trnrt/models/decoder.py:481-486 `_store`, which trnrt/models/mla.py:445-446 calls for the latent rows and the
+ * indexer-key rows at slot_mapping):
+ *   x: bf16 [n_rows, W] (x_fp32 = 0) or fp32 [n_rows, W] (x_fp32 = 1); slots int64 [n_rows] (cache slots
+ *   table[pos / page_size] * page_size + pos % page_size, trnrt/models/decoder.py:658-667); cache uint8 e4m3fn
+ *   [num_slots, W]; scale fp32 [num_slots] or null.
+ *   per_token_scale = 1 (this build's format; scale required): s = max(absmax(row), 1e-30) / 448,
+ *     cache[slot] = e4m3fn(clamp(row / s, +-fp8_max)), scale[slot] = s;
+ *   per_token_scale = 0 (the reference's form, KV scale 1.0): cache[slot] = e4m3fn(clamp(row, +-fp8_max)),
+ *     scale[slot] = 1 when a scale array is given.
+ *   fp32 arithmetic with a correctly rounded division, round-to-nearest-even into e4m3fn (torch's cast).
+ *   W a multiple of 8 in [8, 1024]; 0 < fp8_max <= 448. A row whose slot is outside [0, num_slots) is not written;
+ *   rows that share a slot leave one of them (unspecified which).
+ */
+int dsa_cache_write(const void* x, int x_fp32, const int64_t* slots, uint8_t* cache, float* scale, int n_rows, int W,
+                    long long num_slots, int per_token_scale, float fp8_max, void* stream);
+
+/*
  * Bytes of workspace an entry point needs. kind: DSA_WS_TOPK (B, max_len, keep), DSA_WS_ATTENTION (B, H, keep,
  * splits; splits 0 = the GPU default), DSA_WS_LAYER (all of them). Unused arguments are ignored.
  */

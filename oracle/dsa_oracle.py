@@ -16,6 +16,10 @@ Each function cites the reference lines it follows. How each one is pinned (test
   score kinds, and a planted wrong tie rule that must fail;
 - two_level_ref: equal to topk_ref on the reference's own adversarial cases (trnrt/models/dsa_long.py:26-42 proves
   it exact);
+- cache_write_ref: torch's float -> e4m3fn cast checked against a round-to-nearest-even encoder written from the
+  OCP e4m3fn definition over every representable value, every midpoint and its neighbours; known-answer rows; the
+  per-token round trip within half an e4m3 step; planted mistakes (no clamp, truncation instead of rounding) that
+  must fail;
 - sparse_mla_ref: brute-force float64 loops, one selected token -> that row, all masked -> the uniform mean,
   lse == log-sum-exp, split-K combine == unsplit, slot-order invariance;
 - splitk_combine_ref: any partition of the slots combines to the unsplit result.
@@ -23,6 +27,8 @@ Nothing here is "parity unpinned".
 """
 
 from __future__ import annotations
+
+import math
 
 import torch
 
@@ -98,6 +104,57 @@ def prefill_scores_ref(qI: torch.Tensor, w: torch.Tensor, k8: torch.Tensor, k_sc
     out = torch.full((N, stride), NEG_INF, dtype=torch.float32)
     out[:, :P] = a0 + a1
     return out
+
+
+# -- the cache-store step (trnrt/models/decoder.py:481-486) ----------------------------------------------------------
+
+
+def cache_write_ref(cache: torch.Tensor, scale: torch.Tensor | None, slots: torch.Tensor, x: torch.Tensor,
+                    fp8_max: float = 448.0, per_token: bool = True):
+    """(cache', scale') after writing rows x [T, W] at slots [T] (trnrt/models/decoder.py:481-486 `_store`: the row
+    clamped to +-fp8_max, then cast to float8_e4m3fn, written with index_put_). per_token: the row is first divided
+    by its scale s = max(absmax, 1e-30) / 448, and s is written to scale[slot]; otherwise the scale is 1. Rows whose
+    slot is outside the cache are skipped."""
+    W = cache.shape[-1]
+    c = cache.clone().view(torch.uint8).reshape(-1, W)
+    sc = None if scale is None else scale.clone().reshape(-1)
+    xf = x.float().reshape(-1, W)
+    if per_token:
+        s = xf.abs().amax(-1).clamp(min=1e-30) / 448.0
+        q = (xf / s.unsqueeze(-1)).clamp(-fp8_max, fp8_max).to(torch.float8_e4m3fn)
+    else:
+        s = torch.ones(xf.shape[0])
+        q = xf.clamp(-fp8_max, fp8_max).to(torch.float8_e4m3fn)
+    sl = slots.reshape(-1).long()
+    ok = (sl >= 0) & (sl < c.shape[0])
+    c[sl[ok]] = q.view(torch.uint8)[ok]
+    if sc is not None:
+        sc[sl[ok]] = s[ok]
+    return c.view(cache.dtype).reshape(cache.shape), sc
+
+
+def e4m3fn_encode(v: float) -> int:
+    """The OCP e4m3fn byte of a finite |v| <= 448 by its definition (1 sign bit, 4 exponent bits with bias 7, 3
+    mantissa bits; exponent 0 is subnormal with step 2^-9; no infinities; 0x7F is NaN), rounded to nearest with ties
+    to the even code, in exact rational arithmetic: the independent form that torch's cast is checked against."""
+    from fractions import Fraction
+
+    a = abs(Fraction(v))
+    sign = 0x80 if math.copysign(1.0, v) < 0 else 0
+    vals = []  # (value, code) of every non-negative finite code, ascending
+    for code in range(0x7F):
+        e, m = code >> 3, code & 7
+        vals.append((Fraction(m, 8) * Fraction(2) ** -6 if e == 0 else (1 + Fraction(m, 8)) * Fraction(2) ** (e - 7),
+                     code))
+    lo = max((c for c in vals if c[0] <= a), key=lambda c: c[0])
+    hi = min((c for c in vals if c[0] >= a), key=lambda c: c[0])
+    if a - lo[0] < hi[0] - a or lo[0] == a:
+        code = lo[1]
+    elif a - lo[0] > hi[0] - a:
+        code = hi[1]
+    else:  # a tie: the even code
+        code = lo[1] if lo[1] % 2 == 0 else hi[1]
+    return sign | code
 
 
 # -- selection (trnrt/models/dsa_select.py:33-38; trnrt/models/dsa_long.py:94-137) ----------------------------------

@@ -104,3 +104,14 @@ def test_prefill_host_checks():
     assert lib.dsa_indexer_prefill_fp8(p, null, p, p, p, p, p, 4, 64, 128, 100, 100, 0.1, null) == -1  # no q scale
     assert lib.dsa_indexer_prefill_fp8(p, p, p, p, p, p, p, 4, 64, 96, 100, 100, 0.1, null) == -2  # D 96
     assert lib.dsa_indexer_prefill_fp8(p, p, p, p, p, p, p, 0, 64, 128, 100, 100, 0.1, null) == 0
+
+
+def test_cache_write_host_checks():
+    lib = _lib.lib()
+    p = ctypes.c_void_p(16)
+    null = None
+    assert lib.dsa_cache_write(p, 0, p, p, null, 4, 576, 100, 1, 448.0, null) == -1  # per-token without a scale
+    assert lib.dsa_cache_write(p, 0, p, p, p, 4, 576, 100, 1, 500.0, null) == -1  # fp8_max above 448
+    assert lib.dsa_cache_write(p, 0, p, p, p, 4, 20, 100, 1, 448.0, null) == -2  # width not a multiple of 8
+    assert lib.dsa_cache_write(p, 0, p, p, p, 4, 1032, 100, 1, 448.0, null) == -2  # width above 1024
+    assert lib.dsa_cache_write(p, 0, p, p, p, 0, 576, 100, 1, 448.0, null) == 0  # nothing to do

@@ -32,6 +32,7 @@ SIGNATURES: dict[str, tuple] = {
     "dsa_strerror": (ctypes.c_char_p, [c_int]),
     "dsa_indexer_decode": (c_int, [P, P, P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, P]),
     "dsa_indexer_prefill": (c_int, [P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_float, P]),
+    "dsa_cache_write": (c_int, [P, c_int, P, P, P, c_int, c_int, ctypes.c_longlong, c_int, c_float, P]),
     "dsa_indexer_prefill_fp8": (c_int, [P, P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_float, P]),
     "dsa_topk": (c_int, [P, P, P, P, P, c_size_t, c_int, c_int, c_int, c_int, c_int, P]),
     "dsa_topk_supported": (c_int, [c_int, c_int, c_int]),

@@ -15,6 +15,9 @@ hipError_t launch_indexer_prefill(const uint16_t* q, const float* w, const uint8
 hipError_t launch_indexer_prefill_fp8(const uint8_t* q8, const float* qs, const float* w, const uint8_t* k,
                                       const float* ks, const int* npool, float* scores, int N, int Hi, int P,
                                       int stride, float scale, hipStream_t s);
+bool cache_write_width_ok(int W);
+hipError_t launch_cache_write(const void* x, int x_fp32, const int64_t* slots, uint8_t* cache, float* cscale,
+                              int n_rows, int W, long num_slots, int scaled, float fp8_max, hipStream_t s);
 hipError_t launch_topk(const float* scores, const int* len, int* idx, int* cnt, void* ws, int B, int stride,
                        int max_len, int keep, int vis_only, bool hist_ready, const int* table, int max_pages,
                        int page_size, int num_pages, int* rows_out, hipStream_t s);
@@ -143,6 +146,16 @@ int dsa_indexer_prefill_fp8(const uint8_t* q_fp8, const float* q_scale, const fl
   if (N == 0) return DSA_OK;
   return status(dsa::launch_indexer_prefill_fp8(q_fp8, q_scale, w, k_fp8, k_scale, npool, scores, N, Hi, P,
                                                 score_stride, scale, static_cast<hipStream_t>(stream)));
+}
+
+int dsa_cache_write(const void* x, int x_fp32, const int64_t* slots, uint8_t* cache, float* scale, int n_rows, int W,
+                    long long num_slots, int per_token_scale, float fp8_max, void* stream) {
+  if (!x || !slots || !cache || (per_token_scale && !scale)) return DSA_EINVAL;
+  if (n_rows < 0 || num_slots < 1 || !(fp8_max > 0.0f) || !(fp8_max <= 448.0f)) return DSA_EINVAL;
+  if (!dsa::cache_write_width_ok(W)) return DSA_EUNSUPPORTED;
+  if (n_rows == 0) return DSA_OK;
+  return status(dsa::launch_cache_write(x, x_fp32 != 0, slots, cache, scale, n_rows, W, (long)num_slots,
+                                        per_token_scale != 0, fp8_max, static_cast<hipStream_t>(stream)));
 }
 
 int dsa_topk(const float* scores, const int32_t* len, int32_t* idx, int32_t* cnt, void* workspace,

@@ -1,0 +1,105 @@
+// Quantise-on-write into the paged FP8 caches for gfx950: the cache-store step before the DSA path
+// (trnrt/models/decoder.py:481-486 `_store`, called for the latent rows and the indexer-key rows at
+// trnrt/models/mla.py:445-446), with the per-token scale of this build's cache format:
+//
+//   scaled form:    s = max(absmax(x_row), 1e-30) / 448,  cache[slot] = e4m3fn(clamp(x_row / s, +-fp8_max)),
+//                   scale[slot] = s
+//   reference form: cache[slot] = e4m3fn(clamp(x_row, +-fp8_max)),  scale[slot] = 1 (when a scale array is given)
+//
+// in fp32 with a correctly rounded division and round-to-nearest-even into e4m3fn (v_cvt_pk_fp8_f32), which is
+// torch's float -> float8_e4m3fn cast. One wave per row: each lane converts groups of 8 values (16 bytes of bf16 or
+// 32 of fp32 in, 8 bytes out), the row's absmax is a wave reduction, and lane 0 writes the scale. A row whose slot
+// is outside [0, num_slots) is not written.
+#include "dsa_common.h"
+
+namespace dsa {
+
+constexpr int CW_WAVES = 4;              // rows per workgroup
+constexpr int CW_GPL = 2;                // groups of 8 values per lane: rows up to 64 x 8 x 2 = 1024 values
+constexpr float CW_FP8_MAX = 448.0f;     // the e4m3fn maximum (the scale's target)
+
+template <typename T>
+__device__ __forceinline__ void load8(const T* p, float (&v)[8]);
+
+template <>
+__device__ __forceinline__ void load8<uint16_t>(const uint16_t* p, float (&v)[8]) {  // bf16 bits
+  const uint4 u = *reinterpret_cast<const uint4*>(p);
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = __uint_as_float(w[i] << 16);
+    v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+
+template <>
+__device__ __forceinline__ void load8<float>(const float* p, float (&v)[8]) {
+  const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
+  v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+}
+
+template <typename T, bool SCALED>
+__global__ __launch_bounds__(CW_WAVES * WAVE) void cache_write_kernel(const T* __restrict__ x,
+                                                                      const int64_t* __restrict__ slots,
+                                                                      uint8_t* __restrict__ cache,
+                                                                      float* __restrict__ cscale, int n_rows, int W,
+                                                                      long num_slots, float fp8_max) {
+  const int row = blockIdx.x * CW_WAVES + (int)(threadIdx.x / WAVE);
+  const int lane = threadIdx.x & (WAVE - 1);
+  if (row >= n_rows) return;  // wave-uniform
+  const long slot = slots[row];
+  if (slot < 0 || slot >= num_slots) return;  // wave-uniform
+  const int G = W / 8;
+  const T* xr = x + (size_t)row * W;
+  float v[CW_GPL][8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < CW_GPL; ++i) {
+    const int g = lane + WAVE * i;
+    load8<T>(xr + 8 * min(g, G - 1), v[i]);  // in range whatever the lane; lanes past the row add nothing
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax = g < G ? fmaxf(amax, fabsf(v[i][e])) : amax;
+  }
+  float s = 1.0f;
+  if (SCALED) s = fmaxf(wave_max(amax), 1e-30f) / CW_FP8_MAX;
+  uint8_t* cr = cache + (size_t)slot * W;
+#pragma unroll
+  for (int i = 0; i < CW_GPL; ++i) {
+    const int g = lane + WAVE * i;
+    if (g >= G) break;
+    float q[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) q[e] = fminf(fmaxf(SCALED ? v[i][e] / s : v[i][e], -fp8_max), fp8_max);
+    int lo = 0, hi = 0;
+    lo = __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], lo, false);
+    lo = __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], lo, true);
+    hi = __builtin_amdgcn_cvt_pk_fp8_f32(q[4], q[5], hi, false);
+    hi = __builtin_amdgcn_cvt_pk_fp8_f32(q[6], q[7], hi, true);
+    *reinterpret_cast<uint2*>(cr + 8 * g) = make_uint2((uint32_t)lo, (uint32_t)hi);
+  }
+  if (cscale && lane == 0) cscale[slot] = s;
+}
+
+template <typename T>
+static hipError_t launch_cache_write_t(const T* x, const int64_t* slots, uint8_t* cache, float* cscale, int n_rows,
+                                       int W, long num_slots, int scaled, float fp8_max, hipStream_t s) {
+  const dim3 grid((n_rows + CW_WAVES - 1) / CW_WAVES);
+  if (scaled)
+    return launch("cache_write_kernel", cache_write_kernel<T, true>, grid, dim3(CW_WAVES * WAVE), s, x, slots, cache,
+                  cscale, n_rows, W, num_slots, fp8_max);
+  return launch("cache_write_kernel", cache_write_kernel<T, false>, grid, dim3(CW_WAVES * WAVE), s, x, slots, cache,
+                cscale, n_rows, W, num_slots, fp8_max);
+}
+
+bool cache_write_width_ok(int W) { return W >= 8 && W % 8 == 0 && W <= WAVE * 8 * CW_GPL; }
+
+hipError_t launch_cache_write(const void* x, int x_fp32, const int64_t* slots, uint8_t* cache, float* cscale,
+                              int n_rows, int W, long num_slots, int scaled, float fp8_max, hipStream_t s) {
+  if (x_fp32)
+    return launch_cache_write_t(static_cast<const float*>(x), slots, cache, cscale, n_rows, W, num_slots, scaled,
+                                fp8_max, s);
+  return launch_cache_write_t(static_cast<const uint16_t*>(x), slots, cache, cscale, n_rows, W, num_slots, scaled,
+                              fp8_max, s);
+}
+
+}  // namespace dsa
