@@ -11,7 +11,7 @@ bytes per launch over its HIP-event-timed average duration) and the CPU baseline
 the reference arithmetic, timed on this host's cores on a bounded sample of the same workload).
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--config 2] [--no-cpu-baseline]
-    python bench.py --config 5          # the chunked-prefill selection (65,536 cached + 2,048 new queries): its own line
+    python bench.py --config 5          # the chunked-prefill step (65,536 cached + 2,048 new queries): its own line
     python bench.py --copy-probe 512    # plain device copies of 512 MiB: the calibration run for HBM counters
 
 roofline.traffic (HBM bytes per indexer launch) comes from rocprofv3 FETCH_SIZE / WRITE_SIZE counter runs of this
@@ -147,8 +147,9 @@ def kernel_times(lib, step, steps: int, pairs: int = 16) -> dict:
 
 
 def prefill_cpu_baseline(inp, cfg, budget_s: float = 15.0) -> dict:
-    """The oracle's chunk selection (prefill_scores_ref + topk_ref, torch fp32 on the host) over whole query rows of
-    the same chunk, as many rows as fit in about budget_s seconds; reported as chunks per second (rows / 2,048)."""
+    """The oracle's chunk step (prefill_scores_ref + topk_ref + sparse_mla_ref, torch fp32 on the host) over whole
+    query rows of the same chunk, as many rows as fit in about budget_s seconds; reported as chunks per second
+    (rows / 2,048)."""
     import torch
 
     from oracle import dsa_oracle as O
@@ -158,42 +159,54 @@ def prefill_cpu_baseline(inp, cfg, budget_s: float = 15.0) -> dict:
     cpu = inp.to("cpu")
     qv = cpu.q_values()  # the queries' values (dequantised when FP8)
     rows, t0, n = 4, time.perf_counter(), 0
+    table = cpu.table.view(1, -1).expand(rows, -1)
     while True:
         r0 = (n * rows) % cfg.chunk
         sl = slice(r0, r0 + rows)
         sc = O.prefill_scores_ref(qv[sl], cpu.w[sl], cpu.k8, cpu.k_scale, cpu.npool[sl], cfg.scale)
-        O.topk_ref(sc, cfg.keep)
+        idx, cnt = O.topk_ref(sc, cfg.keep)
+        O.sparse_mla_ref(cpu.q[sl], cpu.kv_cache, cpu.kv_scale, idx, cnt, table, cfg.page_size, cfg.softmax_scale)
         n += 1
         dt = time.perf_counter() - t0
         if dt >= budget_s or n * rows >= cfg.chunk:
             break
     done = n * rows
     return {"value": done / cfg.chunk / dt, "unit": "chunks/s", "cores": cores, "kind": "port",
-            "sample": f"{done} of the chunk's {cfg.chunk} query rows (scores over {cfg.P} keys + top-{cfg.keep}, "
-                      f"torch fp32, {dt:.1f} s, {cores} threads)"}
+            "sample": f"{done} of the chunk's {cfg.chunk} query rows (scores over {cfg.P} keys + top-{cfg.keep} + "
+                      f"sparse MLA over the selection, torch fp32, {dt:.1f} s, {cores} threads)"}
 
 
 def prefill_main(args) -> int:
-    """The chunked-prefill selection (config 5): one step = the dense indexer scores of the chunk's queries over the
-    cached + new keys (bf16 MFMA) and the exact top-2048 of every query row. roofline: the indexer kernel's
-    algorithmic MFMA work (2 Hi D per causal (query, key) pair) over its HIP-event-timed duration."""
+    """The chunked-prefill DSA step (config 5): the dense indexer scores of the chunk's queries over the cached + new
+    keys, the exact top-2048 of every query row (dsa_long_select.select), and sparse MLA of every query over its
+    selected tokens (the token form through the context's page table). roofline: the indexer kernel's algorithmic
+    MFMA work (2 Hi D per causal (query, key) pair) over its HIP-event-timed duration; `attention` gives the same for
+    sparse_mla_kernel (2 H (576 + 512) per selected token)."""
     import torch
 
     from trnrt_amd import _lib
     from trnrt_amd import workloads as W
+    from trnrt_amd.kernels import dsa_decode
     from trnrt_amd.kernels import dsa_long_select as LS
 
     cfg = W.PREFILL_CONFIGS[args.config]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    inp = W.make_prefill_inputs(cfg, seed=0, device=dev)
-    wsb = _lib.workspace_bytes(_lib.DSA_WS_TOPK, cfg.chunk, 0, cfg.keep, cfg.P)
+    inp = W.make_prefill_inputs(cfg, seed=0, device=dev, attention=True)
+    C = cfg.chunk
+    wsb = _lib.workspace_bytes(_lib.DSA_WS_TOPK, C, 0, cfg.keep, cfg.P)
     ws = torch.zeros(wsb, dtype=torch.uint8, device=dev)  # the top-k histograms start (and end) at zero
+    wsa_b = _lib.workspace_bytes(_lib.DSA_WS_ATTENTION, C, cfg.H, cfg.keep, 0, 0)
+    wsa = torch.zeros(max(wsa_b, 256), dtype=torch.uint8, device=dev)
+    table = inp.table.view(1, -1).expand(C, -1).contiguous()  # every query row reads the context's pages
+    o = torch.empty(C, cfg.H, cfg.dv, dtype=torch.bfloat16, device=dev)
     lib = _lib.lib()
 
     def step():
-        LS.select(inp.qI, inp.w, inp.k8, inp.npool, cfg.keep, cfg.scale, pk_scale=inp.k_scale, qI_scale=inp.qI_scale,
-                  workspace=ws)
+        pools, cnt, _ = LS.select(inp.qI, inp.w, inp.k8, inp.npool, cfg.keep, cfg.scale, pk_scale=inp.k_scale,
+                                  qI_scale=inp.qI_scale, workspace=ws)
+        dsa_decode.attend_tokens(inp.q, inp.kv_cache, inp.kv_scale, pools, cnt, table, cfg.page_size,
+                                 cfg.softmax_scale, out=o, workspace=wsa)
 
     steps = min(args.steps, 20)
     for _ in range(min(args.warmup, 5)):
@@ -209,8 +222,11 @@ def prefill_main(args) -> int:
     kname = "indexer_prefill_fp8_kernel" if cfg.q_fp8 else "indexer_prefill_kernel"
     idx_us = k_us[kname]
     tflops = flops / (idx_us * 1e-6) / 1e12
+    att_flops = W.prefill_attention_flops(cfg)
+    att_us = k_us["sparse_mla_kernel"] + k_us.get("combine_splits_kernel", 0.0)
+    att_tflops = att_flops / (att_us * 1e-6) / 1e12
     out = {
-        "metric": "DSA chunked-prefill selection (indexer + top-2048) chunks/sec; indexer MFMA TFLOP/s",
+        "metric": "DSA chunked-prefill step (indexer + top-2048 + sparse MLA) chunks/sec; indexer MFMA TFLOP/s",
         "value": round(1e3 / ms, 2),
         "unit": "chunks/s",
         "n_gpus": 1,
@@ -222,15 +238,19 @@ def prefill_main(args) -> int:
         "vs_baseline": None,
         "dtype": "fp8" if cfg.q_fp8 else "bf16",
         "data": "synthetic",
-        "config": {"workload": f"config {args.config}: {cfg.name}", "cached": cfg.cached, "chunk": cfg.chunk,
+        "config": {"workload": f"config {args.config}: {cfg.name}", "cached": cfg.cached, "chunk": C,
                    "queries": "fp8 e4m3 + fp32 scale per (query, head)" if cfg.q_fp8 else "bf16",
-                   "indexer_heads": cfg.Hi, "keep": cfg.keep, "keys": "fp8 e4m3 [128] + fp32 scale per token",
+                   "indexer_heads": cfg.Hi, "q_heads": cfg.H, "keep": cfg.keep, "page_size": cfg.page_size,
+                   "keys": "fp8 e4m3 [128] + fp32 scale per token", "kv": "fp8 e4m3 [576] + fp32 scale per token",
                    "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "kernel": kname, "achieved": round(tflops, 1),
                      "peak": FP8_PEAK_TFLOPS if cfg.q_fp8 else BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / (FP8_PEAK_TFLOPS if cfg.q_fp8 else BF16_PEAK_TFLOPS), 4),
                      "bf16_peak_frac": round(tflops / BF16_PEAK_TFLOPS, 4), "traffic": None,
                      "algorithmic_flops": flops, "avg_us": round(idx_us, 3)},
+        "attention": {"kernel": "sparse_mla_kernel", "avg_us": round(att_us, 3), "achieved": round(att_tflops, 1),
+                      "unit": "TFLOP/s", "peak": BF16_PEAK_TFLOPS, "frac": round(att_tflops / BF16_PEAK_TFLOPS, 4),
+                      "algorithmic_flops": att_flops},
         "kernel_us": {k: round(v, 3) for k, v in k_us.items()},
     }
     if not args.no_cpu_baseline:

@@ -11,8 +11,9 @@ import pytest
 import torch
 
 from oracle import dsa_oracle as O
-from tests._helpers import row_rel_err, say
+from tests._helpers import assert_attention_close, row_rel_err, say
 from trnrt_amd import workloads as W
+from trnrt_amd.kernels import dsa_decode
 from trnrt_amd.kernels import dsa_long_select as LS
 from trnrt_amd.models import dsa_long
 
@@ -164,3 +165,55 @@ def test_config5_full_size_sampled_rows():
     ri, rc = O.topk_ref(got, cfg.keep, c.npool[rows])
     assert torch.equal(pools[rows].cpu(), ri)
     assert torch.equal(vals[rows].cpu(), got.gather(1, ri))
+
+
+def _chunk_attention(inp, cfg, pools, cnt, rows_form):
+    """o [C, H, 512] of the chunk's queries over their selected tokens: the reference's flow (slots with the tail
+    slot, then attend; trnrt/models/mla.py:524-526) or the token form through the shared page table."""
+    C = cfg.chunk
+    if rows_form:
+        positions = torch.arange(cfg.cached, cfg.cached + C, device="cuda")
+        rows, bias = dsa_long.slots(pools, cnt, inp.npool, positions, inp.table, cfg.page_size, 1, cfg.keep + 1)
+        return dsa_long.attend(inp.q, inp.kv_cache, rows, bias, cfg.softmax_scale, kc_scale=inp.kv_scale), None
+    table = inp.table.view(1, -1).expand(C, -1).contiguous()
+    return dsa_decode.attend_tokens(inp.q, inp.kv_cache, inp.kv_scale, pools, cnt, table, cfg.page_size,
+                                    cfg.softmax_scale)
+
+
+@pytest.mark.parametrize("rows_form", [False, True])
+def test_chunk_attention_vs_oracle(rows_form):
+    """A small causal chunk end to end: FP8 indexer -> exact selection -> sparse MLA over the selected tokens, every
+    row against the oracle's attention over the same selection."""
+    cfg = W.PrefillConfig("small", cached=3000, chunk=24, keep=256, q_fp8=True)
+    say(f"prefill chunk attention rows_form={rows_form}")
+    inp = W.make_prefill_inputs(cfg, seed=8, device="cuda", attention=True)
+    pools, cnt, _ = LS.select(inp.qI, inp.w, inp.k8, inp.npool, cfg.keep, cfg.scale, pk_scale=inp.k_scale,
+                              qI_scale=inp.qI_scale)
+    o, lse = _chunk_attention(inp, cfg, pools, cnt, rows_form)
+    torch.cuda.synchronize()
+    c = inp.to("cpu")
+    table = c.table.view(1, -1).expand(cfg.chunk, -1)
+    ref_o, ref_lse = O.sparse_mla_ref(c.q, c.kv_cache, c.kv_scale, pools.cpu(), cnt.cpu(), table, cfg.page_size,
+                                      cfg.softmax_scale)
+    assert_attention_close(o, ref_o)
+    if lse is not None:
+        torch.testing.assert_close(lse.cpu(), ref_lse, atol=1e-3, rtol=1e-3)
+
+
+def test_config5_chunk_attention_sampled_rows():
+    """Config 5 end to end at full size (2,048 queries over 67,584 keys, top-2048, 64 heads): the attention of
+    sampled rows against the oracle over the kernel's own selection."""
+    cfg = W.PREFILL_CONFIGS[5]
+    say("prefill config 5 chunk attention")
+    inp = W.make_prefill_inputs(cfg, seed=1, device="cuda", attention=True)
+    pools, cnt, _ = LS.select(inp.qI, inp.w, inp.k8, inp.npool, cfg.keep, cfg.scale, pk_scale=inp.k_scale,
+                              qI_scale=inp.qI_scale)
+    o, lse = _chunk_attention(inp, cfg, pools, cnt, rows_form=False)
+    torch.cuda.synchronize()
+    rows = [0, 5, 1000, 2047]
+    c = inp.to("cpu")
+    table = c.table.view(1, -1).expand(len(rows), -1)
+    ref_o, ref_lse = O.sparse_mla_ref(c.q[rows], c.kv_cache, c.kv_scale, pools[rows].cpu(), cnt[rows].cpu(), table,
+                                      cfg.page_size, cfg.softmax_scale)
+    assert_attention_close(o[rows], ref_o)
+    torch.testing.assert_close(lse[rows].cpu(), ref_lse, atol=1e-3, rtol=1e-3)

@@ -159,6 +159,10 @@ class PrefillConfig:
     keep: int = 2048
     D: int = 128
     q_fp8: bool = False  # indexer queries as e4m3 with per-(query, head) scales (the FP8-MFMA form)
+    H: int = 64  # attention query heads
+    dqk: int = 576  # 512 latent + 64 rope
+    dv: int = 512
+    page_size: int = 64
 
     @property
     def P(self) -> int:
@@ -168,10 +172,20 @@ class PrefillConfig:
     def scale(self) -> float:
         return self.D ** -0.5  # the indexer's softmax-free scale (trnrt/models/mla.py:629)
 
+    @property
+    def softmax_scale(self) -> float:
+        return 192 ** -0.5  # 1 / sqrt(128 + 64)
+
 
 PREFILL_CONFIGS = {
     5: PrefillConfig("prefill-65536+2048-h64", cached=65536, chunk=2048, q_fp8=True),
 }
+
+
+def prefill_attention_flops(cfg: PrefillConfig) -> int:
+    """Algorithmic MFMA work of the chunk's sparse attention: per query, head and selected token, a 576-dim score
+    and a 512-dim value product (2 FLOP per multiply-add)."""
+    return 2 * cfg.chunk * cfg.H * min(cfg.keep, cfg.cached + 1) * (cfg.dqk + cfg.dv)
 
 
 def prefill_flops(cfg: PrefillConfig) -> int:
@@ -190,6 +204,11 @@ class PrefillInputs:
     k8: torch.Tensor  # [P, 128] e4m3fn
     k_scale: torch.Tensor  # [P] fp32
     npool: torch.Tensor  # [C] int32: position + 1 (causal: key t <= the query's position)
+    # the attention's inputs (make_prefill_inputs(attention=True)), else None:
+    q: torch.Tensor | None = None  # [C, H, 576] bf16 absorbed queries
+    kv_cache: torch.Tensor | None = None  # [slots, 576] e4m3fn latent rows of the context, paged
+    kv_scale: torch.Tensor | None = None  # [slots] fp32
+    table: torch.Tensor | None = None  # [P / page_size] int32: the context's pages (a seeded permutation of 1..)
 
     def to(self, device) -> "PrefillInputs":
         kw = {k: (v.to(device) if isinstance(v, torch.Tensor) else v) for k, v in self.__dict__.items()}
@@ -203,7 +222,7 @@ class PrefillInputs:
 
 
 def make_prefill_inputs(cfg: PrefillConfig, seed: int = 0, device: str | torch.device = "cpu",
-                        chunk: int = 65536) -> PrefillInputs:
+                        chunk: int = 65536, attention: bool = False) -> PrefillInputs:
     """Seeded inputs of one chunk's indexer: queries ~N(0, 1) in bf16 (with cfg.q_fp8 quantised per (query, head)
     to e4m3fn, scale absmax / 448), weights ~N(0, 1/16), keys ~N(0, 1) quantised per token to e4m3fn (scale
     absmax / 448); query i sits at position cached + i."""
@@ -222,4 +241,17 @@ def make_prefill_inputs(cfg: PrefillConfig, seed: int = 0, device: str | torch.d
         n = min(chunk, P - s0)
         k8[s0:s0 + n], ks[s0:s0 + n] = quantize_rows(torch.randn(n, cfg.D, generator=g, device=device))
     npool = (cfg.cached + 1 + torch.arange(C, device=device)).to(torch.int32)
-    return PrefillInputs(cfg, qI, qI_scale, w, k8, ks, npool)
+    inp = PrefillInputs(cfg, qI, qI_scale, w, k8, ks, npool)
+    if attention:
+        ps = cfg.page_size
+        npg = math.ceil(P / ps)
+        inp.q = torch.randn(C, cfg.H, cfg.dqk, generator=g, device=device).to(torch.bfloat16)
+        inp.table = (torch.randperm(npg, generator=g, device=device) + 1).to(torch.int32)
+        slots = (npg + 1) * ps
+        inp.kv_cache = torch.zeros(slots, cfg.dqk, dtype=FP8, device=device)
+        inp.kv_scale = torch.ones(slots, dtype=torch.float32, device=device)
+        for s0 in range(ps, slots, chunk):
+            n = min(chunk, slots - s0)
+            inp.kv_cache[s0:s0 + n], inp.kv_scale[s0:s0 + n] = quantize_rows(
+                torch.randn(n, cfg.dqk, generator=g, device=device))
+    return inp
