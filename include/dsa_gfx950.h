@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define DSA_ABI_VERSION 1
+#define DSA_ABI_VERSION 2
 
 #define DSA_OK 0
 #define DSA_EINVAL (-1)      /* a null pointer or a size out of range */
@@ -107,10 +107,13 @@ int dsa_workspace_clear(void* workspace, size_t workspace_bytes, void* stream);
 int dsa_topk_supported(int max_len, int keep, int vis_only);
 
 /*
- * Additive selection mask (the output form of trnrt/kernels/dsa_topk.py:495-514 `select` at kp = 1):
- * mask[b, t] = 0 for the positions idx[b, 0 .. cnt[b]), NEG_INF elsewhere, t < P.
+ * Additive selection mask (the output form of trnrt/kernels/dsa_topk.py:495-514 `select`, with its pooled kp and
+ * tail forms, dsa_topk.py:89-93): score p of row b (P scores per row) is taken when it is one of idx[b, 0 ..
+ * cnt[b]), or, with tail, when it is not a candidate (scores[b, p] <= VISIBLE: the reference's `sel | ~vis`);
+ * mask[b, p * kp + t] = taken ? 0 : NEG_INF for t < kp. scores (fp32 [B, P]) is read only with tail.
  */
-int dsa_topk_mask(const int32_t* idx, const int32_t* cnt, float* mask, int B, int keep, int P, void* stream);
+int dsa_topk_mask(const int32_t* idx, const int32_t* cnt, const float* scores, float* mask, int B, int keep, int P,
+                  int kp, int tail, void* stream);
 
 /*
  * Sparse MLA decode attention over the selected tokens (replaces trnrt/kernels/dsa_decode.py:26-43 `attend`,
@@ -140,6 +143,21 @@ int dsa_sparse_mla_decode(const void* q_bf16, const uint8_t* kv_fp8, const float
  */
 int dsa_token_rows(const int32_t* idx, const int32_t* cnt, const int32_t* page_table, int32_t* rows, float* bias,
                    int B, int keep, int max_pages, int page_size, int num_pages, void* stream);
+
+/*
+ * The attention's slots of N queries (replaces trnrt/models/dsa_long.py:189-215 `slots` for any kpool kp; at kp 1 a
+ * pool is a token): slot k < keep is the selected pool pools[n, k], attended when k < cnt[n]; slot keep is the
+ * query's tail pool npool[n], whose tokens kp npool .. positions[n] are attended (none when positions[n] + 1 is a
+ * multiple of kp); the slots past keep + 1 are padding (pool 0, masked).
+ *   rows[n, s] = table_n[pool / ppp] * ppp + pool % ppp: the pool's row in the latent cache viewed as
+ *   [slots / kp, kp R] (ppp = page_size / kp pools per page, a power of two); bias[n, s, t] = 0 for a token to
+ *   attend, NEG_INF otherwise. pools int32 [N, keep], cnt / npool / positions int32 [N], table int32 [N, table_pages]
+ *   or one [table_pages] shared by every query (table_shared = 1), rows int32 [N, n_slots], bias fp32
+ *   [N, n_slots, kp]; n_slots >= keep + 1.
+ */
+int dsa_pool_slots(const int32_t* pools, const int32_t* cnt, const int32_t* npool, const int32_t* positions,
+                   const int32_t* table, int table_shared, int32_t* rows, float* bias, int N, int keep, int n_slots,
+                   int table_pages, int page_size, int kp, void* stream);
 
 /*
  * The whole DSA decode layer step: indexer -> top-k -> sparse MLA, enqueued back to back on one stream

@@ -204,6 +204,18 @@ def topk_ref(scores: torch.Tensor, keep: int, lengths=None, vis_only: bool = Tru
     return ascending(sel, keep)
 
 
+def topk_mask_ref(scores: torch.Tensor, keep: int, vis_only: bool = True, kp: int = 1,
+                  tail: bool = False) -> torch.Tensor:
+    """The additive mask [R, P kp] of dsa_topk.select (trnrt/kernels/dsa_topk.py:89-93 `_out`): the selection
+    (selection_mask), with tail also every non-candidate score (<= VISIBLE), each score's value repeated for its kp
+    tokens."""
+    sel = selection_mask(scores, keep, vis_only)
+    if tail:
+        sel = sel | ~(scores.float() > VISIBLE)
+    out = torch.where(sel, 0.0, NEG_INF)
+    return out.repeat_interleave(kp, dim=-1) if kp > 1 else out
+
+
 def topk_radix_ref(scores: torch.Tensor, keep: int, vis_only: bool = True) -> torch.Tensor:
     """bool [R, P]: the reference kernel's algorithm (trnrt/kernels/dsa_topk.py:96-127 `emulate`), a second form
     independent of the sort: the sign step, a radix search over the threshold's bit pattern (31 rounds), and the
@@ -259,6 +271,34 @@ def two_level_ref(scores: torch.Tensor, keep: int, sub: int) -> tuple[torch.Tens
 
 
 # -- sparse MLA attention (trnrt/kernels/dsa_decode.py:26-37; trnrt/kernels/dsa_slots.py:48-65) ---------------------
+
+
+def pool_slots_ref(pools: torch.Tensor, cnt: torch.Tensor, npool: torch.Tensor, positions: torch.Tensor,
+                   table: torch.Tensor, page_size: int, kp: int, n_slots: int):
+    """(rows [N, n_slots] int64, bias [N, n_slots, kp]) of trnrt/models/dsa_long.py:189-215 `slots`: slot s < keep the
+    selected pool pools[n, s] (live below cnt[n]), slot keep the tail pool npool[n] (min(npool, last pool); its tokens
+    kp npool + t <= positions[n] live), the rest pool 0 (dead); rows = table[pool // ppp] ppp + pool % ppp (the latent
+    cache viewed as [slots / kp, kp R], ppp = page_size / kp); table [Pp] shared or [N, Pp] per query."""
+    N, keep = pools.shape
+    ppp = page_size // kp
+    Pp = table.shape[-1]
+    tb = table.long().view(1, Pp).expand(N, Pp) if table.dim() == 1 else table.long()
+    rows = torch.zeros(N, n_slots, dtype=torch.int64)
+    bias = torch.full((N, n_slots, kp), NEG_INF)
+    for n in range(N):
+        for s in range(n_slots):
+            if s < keep:
+                pl = int(pools[n, s])
+            elif s == keep:
+                pl = min(int(npool[n]), Pp * ppp - 1)
+            else:
+                pl = 0
+            rows[n, s] = int(tb[n, pl // ppp]) * ppp + pl % ppp
+            for t in range(kp):
+                live = (s < keep and s < int(cnt[n])) or (s == keep and int(npool[n]) * kp + t <= int(positions[n]))
+                if live:
+                    bias[n, s, t] = 0.0
+    return rows, bias
 
 
 def sparse_mla_rows_ref(q: torch.Tensor, K: torch.Tensor, bias: torch.Tensor, scale: float, dv: int = 512):

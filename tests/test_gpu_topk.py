@@ -95,3 +95,17 @@ def test_deterministic():
     a = dsa_topk.select_indices(s, 2048)
     b = dsa_topk.select_indices(s, 2048)
     assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+@pytest.mark.parametrize("kp,tail", [(4, True), (4, False), (1, True)])
+def test_pooled_mask_forms(kp, tail):
+    """dsa_topk.select(kp, tail): the pooled indexer's block mask (trnrt/models/glm5_next.py:194-208): pool scores
+    with the non-candidates (pools whose last token is not visible) at NEG_INF, keep 512."""
+    say(f"topk pooled mask kp={kp} tail={tail}")
+    g = torch.Generator().manual_seed(30 + kp)
+    R, P, keep = 6, 2048, 512
+    s = torch.randn(R, P, generator=g)
+    npool = torch.tensor([2048, 1500, 512, 100, 0, 777])
+    s[torch.arange(P).view(1, P) >= npool.view(R, 1)] = O.NEG_INF
+    m = dsa_topk.select(s.cuda(), keep, kp=kp, tail=tail).cpu()
+    assert torch.equal(m, O.topk_mask_ref(s, keep, True, kp, tail))

@@ -168,3 +168,13 @@ def test_planted_wrong_tie_rule_fails():
 
     assert not torch.equal(wrong(s, 100), brute(s, 100, True))
     assert torch.equal(O.selection_mask(s, 100, True), brute(s, 100, True))
+
+
+def test_pooled_mask_known_answer():
+    """dsa_topk._out (trnrt/kernels/dsa_topk.py:89-93): the selection, with tail every non-candidate pool, repeated
+    over each pool's kp tokens."""
+    s = torch.tensor([[3.0, 1.0, O.NEG_INF, O.NEG_INF]])
+    N = float(torch.tensor(O.NEG_INF, dtype=torch.float32))  # NEG_INF as fp32 holds it
+    assert O.topk_mask_ref(s, 1, True, 2, True).tolist() == [[0.0, 0.0, N, N, 0.0, 0.0, 0.0, 0.0]]
+    assert O.topk_mask_ref(s, 1, True, 2, False).tolist() == [[0.0, 0.0, N, N, N, N, N, N]]
+    assert O.topk_mask_ref(s, 3, True, 1, False).tolist() == [[0.0, 0.0, N, N]]  # only the visible ones

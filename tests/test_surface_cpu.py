@@ -35,8 +35,10 @@ def test_host_tensors_raise():
                           torch.zeros(1, 8, dtype=torch.int32), torch.zeros(1, 8), 0.1, kc_scale=torch.ones(64))
 
 
-def test_pooled_forms_are_not_implemented():
-    with pytest.raises(NotImplementedError):
+def test_pooled_forms_host_checks():
+    with pytest.raises(ValueError):
+        dsa_topk.select(torch.randn(2, 64), 8, vis_only=False, kp=4, tail=True)  # tail needs vis_only
+    with pytest.raises(RuntimeError, match="GPU only"):
         dsa_topk.select(torch.randn(2, 64), 8, kp=4)
     with pytest.raises(ValueError):
         dsa_long.npools(torch.tensor([3]), 3)

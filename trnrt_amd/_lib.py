@@ -23,7 +23,7 @@ DSA_WS_TOPK = 1
 DSA_WS_ATTENTION = 2
 DSA_WS_LAYER = 3
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 P = c_void_p
 # Every entry point of include/dsa_gfx950.h with its ctypes signature (restype, argtypes).
@@ -32,12 +32,13 @@ SIGNATURES: dict[str, tuple] = {
     "dsa_strerror": (ctypes.c_char_p, [c_int]),
     "dsa_indexer_decode": (c_int, [P, P, P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, P]),
     "dsa_indexer_prefill": (c_int, [P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_float, P]),
+    "dsa_pool_slots": (c_int, [P, P, P, P, P, c_int, P, P, c_int, c_int, c_int, c_int, c_int, c_int, P]),
     "dsa_cache_write": (c_int, [P, c_int, P, P, P, c_int, c_int, ctypes.c_longlong, c_int, c_float, P]),
     "dsa_indexer_prefill_fp8": (c_int, [P, P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_float, P]),
     "dsa_topk": (c_int, [P, P, P, P, P, c_size_t, c_int, c_int, c_int, c_int, c_int, P]),
     "dsa_topk_supported": (c_int, [c_int, c_int, c_int]),
     "dsa_workspace_clear": (c_int, [P, c_size_t, P]),
-    "dsa_topk_mask": (c_int, [P, P, P, c_int, c_int, c_int, P]),
+    "dsa_topk_mask": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, c_int, P]),
     "dsa_sparse_mla_decode": (
         c_int,
         [P, P, P, P, P, P, P, P, P, P, P, P, c_size_t, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,

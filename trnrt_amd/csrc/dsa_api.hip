@@ -18,11 +18,15 @@ hipError_t launch_indexer_prefill_fp8(const uint8_t* q8, const float* qs, const 
 bool cache_write_width_ok(int W);
 hipError_t launch_cache_write(const void* x, int x_fp32, const int64_t* slots, uint8_t* cache, float* cscale,
                               int n_rows, int W, long num_slots, int scaled, float fp8_max, hipStream_t s);
+hipError_t launch_pool_slots(const int* pools, const int* cnt, const int* npool, const int* positions,
+                             const int* table, int table_shared, int* rows, float* bias, int N, int keep, int n_slots,
+                             int table_pages, int page_size, int kp, hipStream_t s);
 hipError_t launch_topk(const float* scores, const int* len, int* idx, int* cnt, void* ws, int B, int stride,
                        int max_len, int keep, int vis_only, bool hist_ready, const int* table, int max_pages,
                        int page_size, int num_pages, int* rows_out, hipStream_t s);
 hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t s);
-hipError_t launch_topk_mask(const int* idx, const int* cnt, float* mask, int B, int keep, int P, hipStream_t s);
+hipError_t launch_topk_mask(const int* idx, const int* cnt, const float* scores, float* mask, int B, int keep, int P,
+                            int kp, int tail, hipStream_t s);
 size_t topk_workspace_bytes(int B, int max_len, int keep);
 bool topk_supported(int max_len, int keep, int vis_only);
 hipError_t launch_sparse_mla(const uint16_t* q, const uint8_t* kv, const float* kvs, const int* idx, const int* cnt,
@@ -183,10 +187,13 @@ int dsa_topk_supported(int max_len, int keep, int vis_only) {
   return dsa::topk_supported(max_len, keep, vis_only) ? 1 : 0;
 }
 
-int dsa_topk_mask(const int32_t* idx, const int32_t* cnt, float* mask, int B, int keep, int P, void* stream) {
-  if (!idx || !cnt || !mask || B < 0 || keep < 1 || P < 1) return DSA_EINVAL;
+int dsa_topk_mask(const int32_t* idx, const int32_t* cnt, const float* scores, float* mask, int B, int keep, int P,
+                  int kp, int tail, void* stream) {
+  if (!idx || !cnt || !mask || (tail && !scores)) return DSA_EINVAL;
+  if (B < 0 || keep < 1 || P < 1 || kp < 1 || (long)P * kp > 0x7fffffffL) return DSA_EINVAL;
   if (B == 0) return DSA_OK;
-  return status(dsa::launch_topk_mask(idx, cnt, mask, B, keep, P, static_cast<hipStream_t>(stream)));
+  return status(dsa::launch_topk_mask(idx, cnt, scores, mask, B, keep, P, kp, tail != 0,
+                                      static_cast<hipStream_t>(stream)));
 }
 
 int dsa_sparse_mla_decode(const void* q_bf16, const uint8_t* kv_fp8, const float* kv_scale, const int32_t* idx,
@@ -219,6 +226,18 @@ int dsa_token_rows(const int32_t* idx, const int32_t* cnt, const int32_t* page_t
   if (B == 0) return DSA_OK;
   return status(dsa::launch_token_rows(idx, cnt, page_table, rows, bias, B, keep, max_pages, page_size, num_pages,
                                        static_cast<hipStream_t>(stream)));
+}
+
+int dsa_pool_slots(const int32_t* pools, const int32_t* cnt, const int32_t* npool, const int32_t* positions,
+                   const int32_t* table, int table_shared, int32_t* rows, float* bias, int N, int keep, int n_slots,
+                   int table_pages, int page_size, int kp, void* stream) {
+  if (!pools || !cnt || !npool || !positions || !table || !rows || !bias) return DSA_EINVAL;
+  if (N < 0 || keep < 1 || n_slots < keep + 1 || table_pages < 1 || kp < 1) return DSA_EINVAL;
+  const int ppp = page_size / kp;
+  if (page_size % kp || ppp < 1 || (ppp & (ppp - 1))) return DSA_EINVAL;
+  if (N == 0) return DSA_OK;
+  return status(dsa::launch_pool_slots(pools, cnt, npool, positions, table, table_shared != 0, rows, bias, N, keep,
+                                       n_slots, table_pages, page_size, kp, static_cast<hipStream_t>(stream)));
 }
 
 size_t dsa_workspace_bytes(int kind, int B, int H, int keep, int max_len, int splits) {

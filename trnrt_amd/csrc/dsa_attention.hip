@@ -404,6 +404,39 @@ __global__ void token_rows_kernel(const int* __restrict__ idx, const int* __rest
   if (bias) bias[(size_t)b * keep + k] = live ? 0.0f : NEG_INF;
 }
 
+// The attention's slots of query n (the arithmetic of trnrt/models/dsa_long.py:189-215 `slots` for any kpool kp):
+// slot s < keep the selected pool pools[n, s] (taken when s < cnt[n]), slot keep the query's tail pool npool[n]
+// (its tokens kp npool .. positions[n]), the rest pool 0 (masked); rows = the pool's row of the latent cache viewed
+// as [slots / kp, kp R] through the query's table, bias 0 for every token to attend and NEG_INF otherwise.
+__global__ void pool_slots_kernel(const int* __restrict__ pools, const int* __restrict__ cnt,
+                                  const int* __restrict__ npool, const int* __restrict__ positions,
+                                  const int* __restrict__ table, int table_shared, int* __restrict__ rows,
+                                  float* __restrict__ bias, int keep, int n_slots, int table_pages, int ppp, int kp) {
+  const int n = blockIdx.y;
+  const int s = blockIdx.x * blockDim.x + threadIdx.x;
+  if (s >= n_slots) return;
+  const int last_pool = table_pages * ppp - 1;
+  const int np = npool[n];
+  int pl = s < keep ? pools[(size_t)n * keep + s] : (s == keep ? min(np, last_pool) : 0);
+  pl = min(max(pl, 0), last_pool);  // in range whatever the inputs
+  const int pg = pl / ppp;
+  const int* tab = table + (table_shared ? 0 : (size_t)n * table_pages);
+  rows[(size_t)n * n_slots + s] = tab[pg] * ppp + (pl - pg * ppp);
+  const bool sel_ok = s < keep && s < cnt[n];
+  const int pos = positions[n];
+  for (int t = 0; t < kp; ++t) {
+    const bool tail_ok = s == keep && (long)np * kp + t <= (long)pos;
+    bias[((size_t)n * n_slots + s) * kp + t] = (sel_ok || tail_ok) ? 0.0f : NEG_INF;
+  }
+}
+
+hipError_t launch_pool_slots(const int* pools, const int* cnt, const int* npool, const int* positions,
+                             const int* table, int table_shared, int* rows, float* bias, int N, int keep, int n_slots,
+                             int table_pages, int page_size, int kp, hipStream_t s) {
+  return launch("pool_slots_kernel", pool_slots_kernel, dim3((n_slots + 255) / 256, N), dim3(256), s, pools, cnt,
+                npool, positions, table, table_shared, rows, bias, keep, n_slots, table_pages, page_size / kp, kp);
+}
+
 int attention_default_splits(int B, int H, int keep, int num_cu) {
   const int wgs = B * (H / ATT_HPW);
   int max_splits = (keep + ATT_CH - 1) / ATT_CH;

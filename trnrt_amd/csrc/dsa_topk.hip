@@ -749,19 +749,27 @@ __global__ void gather_blocks_kernel(const float* __restrict__ scores, int strid
   cand[(size_t)row * keep * sub + i] = v;
 }
 
-__global__ void topk_mask_fill_kernel(float* __restrict__ mask, int P) {
+// The mask's background: NEG_INF, or with tail 0 for every token of a non-candidate score (score <= VISIBLE, the
+// reference's `sel | ~vis`, trnrt/kernels/dsa_topk.py:89-93), kp tokens per score.
+__global__ void topk_mask_fill_kernel(const float* __restrict__ scores, float* __restrict__ mask, int P, int kp,
+                                      int tail) {
   const int row = blockIdx.y;
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < P) mask[(size_t)row * P + i] = NEG_INF;
+  if (i >= P * kp) return;
+  float v = NEG_INF;
+  if (tail && !(scores[(size_t)row * P + i / kp] > VISIBLE)) v = 0.0f;
+  mask[(size_t)row * P * kp + i] = v;
 }
 
+// 0 for the kp tokens of every selected score.
 __global__ void topk_mask_scatter_kernel(const int* __restrict__ idx, const int* __restrict__ cnt,
-                                         float* __restrict__ mask, int keep, int P) {
+                                         float* __restrict__ mask, int keep, int P, int kp) {
   const int row = blockIdx.y;
   const int k = blockIdx.x * blockDim.x + threadIdx.x;
   if (k < keep && k < cnt[row]) {
     const int p = idx[(size_t)row * keep + k];
-    if ((unsigned)p < (unsigned)P) mask[(size_t)row * P + p] = 0.0f;
+    if ((unsigned)p < (unsigned)P)
+      for (int t = 0; t < kp; ++t) mask[((size_t)row * P + p) * kp + t] = 0.0f;
   }
 }
 
@@ -962,13 +970,13 @@ hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t s) {
   return hipGetLastError();
 }
 
-hipError_t launch_topk_mask(const int* idx, const int* cnt, float* mask, int B, int keep, int P, hipStream_t s) {
-  launch("topk_mask_fill_kernel", topk_mask_fill_kernel, dim3((P + 255) / 256, B), dim3(256), s, mask, P);
-  hipError_t e = hipGetLastError();
+hipError_t launch_topk_mask(const int* idx, const int* cnt, const float* scores, float* mask, int B, int keep, int P,
+                            int kp, int tail, hipStream_t s) {
+  hipError_t e = launch("topk_mask_fill_kernel", topk_mask_fill_kernel, dim3((P * kp + 255) / 256, B), dim3(256), s,
+                        scores, mask, P, kp, tail);
   if (e != hipSuccess) return e;
-  launch("topk_mask_scatter_kernel", topk_mask_scatter_kernel, dim3((keep + 255) / 256, B), dim3(256), s, idx, cnt, mask, keep,
-                     P);
-  return hipGetLastError();
+  return launch("topk_mask_scatter_kernel", topk_mask_scatter_kernel, dim3((keep + 255) / 256, B), dim3(256), s, idx,
+                cnt, mask, keep, P, kp);
 }
 
 }  // namespace dsa

@@ -77,11 +77,26 @@ def _run(q: torch.Tensor, kv: torch.Tensor, kv_scale: torch.Tensor, scale: float
     return (out, ls) if lse else out
 
 
+def pool_token_rows(rows: torch.Tensor, bias: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Slots of kp tokens each (rows [B, NS] pool rows of the cache viewed as [slots / kp, kp R], bias [B, NS, kp])
+    as token slots: rows [B, NS kp] = pool row kp + t, bias [B, NS kp] (trnrt/kernels/dsa_decode.py:26-37 reads a
+    pool row as its kp tokens)."""
+    B, NS = rows.shape
+    kp = bias.shape[-1] if bias.dim() == 3 else 1
+    if kp == 1:
+        return rows, bias.reshape(B, NS)
+    t = torch.arange(kp, device=rows.device, dtype=torch.int64)
+    tok = (rows.to(torch.int64).unsqueeze(-1) * kp + t).reshape(B, NS * kp)
+    return tok, bias.reshape(B, NS * kp)
+
+
 def attend(q_lat: torch.Tensor, kc: torch.Tensor, rows: torch.Tensor, bias: torch.Tensor, scale: float, *,
            kc_scale: torch.Tensor, lse: bool = False, splits: int = 0):
-    """o [B, H, 512] fp32 (trnrt/kernels/dsa_decode.py:40-43 `attend`): q_lat [B, H, 576], kc the FP8 cache [N, 1, 576]
-    or [N, 576] (e4m3fn), kc_scale [N] fp32 its per-token scales, rows [B, NS] int each slot's cache row (one token
-    per slot, kp = 1), bias [B, NS] or [B, NS, 1] fp32 (0 / NEG_INF). With lse also lse [B, H] fp32."""
+    """o [B, H, 512] fp32 (trnrt/kernels/dsa_decode.py:40-43 `attend`): q_lat [B, H, 576], kc the FP8 cache
+    [N, 1, 576] or [N, 576] (e4m3fn; for kp > 1 it may be the reference's pool view [N / kp, kp 576]), kc_scale [N]
+    fp32 its per-token scales, rows [B, NS] int each slot's row, bias [B, NS] or [B, NS, kp] fp32 (0 / NEG_INF): with
+    kp > 1 a slot is a pool of kp consecutive tokens. With lse also lse [B, H] fp32."""
+    rows, bias = pool_token_rows(rows, bias)
     return _run(q_lat, kc, kc_scale, scale, rows=rows, bias=bias, lse=lse, splits=splits)
 
 

@@ -16,8 +16,8 @@ NEG_INF = -1e30
 
 def attend(q_lat: torch.Tensor, kc: torch.Tensor, rows: torch.Tensor, bias: torch.Tensor, scale: float,
            n: torch.Tensor | int | None = None, lse: bool = False, fallback=False, *, kc_scale: torch.Tensor):
-    """o [N, H, 512] fp32 (and lse [N, H]) of q_lat [N, H, 576] over rows [N, NS] (kp = 1 token rows) with bias
-    [N, NS] or [N, NS, 1]; n (a 1-element int tensor or int) is the reference's live-row count and fallback its
-    Trainium kernel choice, both accepted for its signature."""
+    """o [N, H, 512] fp32 (and lse [N, H]) of q_lat [N, H, 576] over rows [N, NS] with bias [N, NS] or [N, NS, kp]
+    (kp tokens per slot, as dsa_decode.attend); n (a 1-element int tensor or int) is the reference's live-row count
+    and fallback its Trainium kernel choice, both accepted for its signature."""
     del n, fallback
     return dsa_decode.attend(q_lat, kc, rows, bias, scale, kc_scale=kc_scale, lse=lse)

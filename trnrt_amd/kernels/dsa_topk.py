@@ -66,12 +66,15 @@ def select_indices(scores: torch.Tensor, keep: int, lengths: torch.Tensor | None
 
 def select(scores: torch.Tensor, keep: int, vis_only: bool = True, group: bool = True, kp: int = 1,
            tail: bool = False) -> torch.Tensor:
-    """Additive float32 [..., P] (0 = selected, NEG_INF = not) of the selection over the last axis
-    (trnrt/kernels/dsa_topk.py:495-514 `select`). group is the reference's Trainium layout knob and is ignored; the
-    pooled forms (kp > 1, tail) are not implemented here (NotImplementedError)."""
+    """Additive float32 [..., P kp] (0 = selected, NEG_INF = not) of the selection over the last axis
+    (trnrt/kernels/dsa_topk.py:495-514 `select`): kp > 1 gives each score's kp tokens its value, tail also takes the
+    non-candidate scores' tokens (<= VISIBLE; the caller's causal mask limits them to its own incomplete pool),
+    dsa_topk.py:89-93. group is the reference's Trainium layout knob and is ignored."""
     del group
-    if kp != 1 or tail:
-        raise NotImplementedError("dsa_topk.select: the pooled forms (kp > 1, tail) are not implemented on gfx950")
+    if tail and not vis_only:
+        raise ValueError("tail needs vis_only")
+    if kp < 1:
+        raise ValueError(f"dsa_topk.select: kp {kp}")
     *lead, P = scores.shape
     R = 1
     for d in lead:
@@ -82,7 +85,8 @@ def select(scores: torch.Tensor, keep: int, vis_only: bool = True, group: bool =
         # every selectable score: the reference's short-cut (dsa_topk.py:510-511), here as a selection of P
         keep = P
     idx, cnt = select_indices(s, keep, vis_only=vis_only)
-    mask = torch.empty(R, P, dtype=torch.float32, device=dev)
-    st = _lib.lib().dsa_topk_mask(C.ptr(idx), C.ptr(cnt), C.ptr(mask), R, keep, P, C.stream_ptr(dev))
+    mask = torch.empty(R, P * kp, dtype=torch.float32, device=dev)
+    st = _lib.lib().dsa_topk_mask(C.ptr(idx), C.ptr(cnt), C.ptr(s) if tail else None, C.ptr(mask), R, keep, P, kp,
+                                  int(tail), C.stream_ptr(dev))
     _lib.check(st, "dsa_topk.select")
-    return mask.reshape(*lead, P)
+    return mask.reshape(*lead, P * kp)

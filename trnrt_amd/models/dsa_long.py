@@ -5,8 +5,8 @@ the decode path calls, at kpool 1: each candidate is one token).
   row, csrc/dsa_indexer.hip) (trnrt/models/dsa_long.py:74-84);
 - select_device / select: the exact top-keep of scores [N, P] as (indices [N, keep] int64 ascending, 0 past the
   count; count [N] int64) (trnrt/models/dsa_long.py:135-186), by the gfx950 top-k kernel;
-- slots: token indices -> cache rows and the 0 / NEG_INF bias (trnrt/models/dsa_long.py:189-215 at kp 1, where a
-  query's tail pool is always empty);
+- slots: selected pools -> cache pool rows and the 0 / NEG_INF bias with the query's tail pool
+  (trnrt/models/dsa_long.py:189-215, any kpool);
 - attend: absorbed MLA over the slots (trnrt/models/dsa_long.py:218-223).
 """
 
@@ -64,39 +64,33 @@ def select(sc: torch.Tensor, keep: int) -> tuple[torch.Tensor, torch.Tensor]:
 
 def slots(pools: torch.Tensor, cnt: torch.Tensor, npool: torch.Tensor, positions: torch.Tensor, table: torch.Tensor,
           page_size: int, kp: int, n_slots: int) -> tuple[torch.Tensor, torch.Tensor]:
-    """rows [N, n_slots] int64 (each slot's cache row) and bias [N, n_slots, 1] fp32 (0 to attend, NEG_INF not) for
-    the selected tokens pools [N, keep] (cnt [N] valid) of N decode rows with their own tables [N, Pp]: slot k < keep
-    is the k-th selected token, slot keep the query's tail (empty at kp 1), the rest padding
-    (trnrt/models/dsa_long.py:189-215 at kp = 1)."""
-    if kp != 1:
-        raise NotImplementedError("dsa_long.slots: the pooled form (kp > 1) is not implemented on gfx950")
+    """rows [N, n_slots] int64 (each slot's pool row, the latent cache viewed as [slots / kp, kp R]) and bias
+    [N, n_slots, kp] fp32 (0 for a token to attend, NEG_INF otherwise) for N queries
+    (trnrt/models/dsa_long.py:189-215): slots 0 .. keep - 1 the selected pools (pools [N, keep], cnt [N] valid),
+    slot keep the query's tail pool npool (its tokens kp npool .. pos; none when pos + 1 is a multiple of kp), the rest
+    padding. table: [Pp] one sequence's pages (a prefill chunk) or [N, Pp] one per row (a decode batch). At kp 1 a
+    pool is a token and the tail is always empty."""
     N, keep = pools.shape
-    if n_slots < keep + 1:
-        raise ValueError(f"slots: {n_slots} slots for {keep} + 1 pools")
-    dev = C.on_gpu(pools, cnt, table)
-    tb = C.as_i32(table if table.dim() == 2 else table.view(1, -1).expand(N, -1))
-    Pp = tb.shape[1]
-    idx = C.as_i32(pools)
-    cn = C.as_i32(cnt)
-    rows = torch.zeros(N, n_slots, dtype=torch.int32, device=dev)
-    bias = torch.full((N, n_slots), NEG_INF, dtype=torch.float32, device=dev)
-    sel_rows = torch.empty(N, keep, dtype=torch.int32, device=dev)
-    sel_bias = torch.empty(N, keep, dtype=torch.float32, device=dev)
-    num_pages = (2**31 - 1) // page_size  # rows are computed, not read: no page clamp is needed here
-    st = _lib.lib().dsa_token_rows(C.ptr(idx), C.ptr(cn), C.ptr(tb), C.ptr(sel_rows), C.ptr(sel_bias), N, keep, Pp,
-                                   page_size, num_pages, C.stream_ptr(dev))
+    ppp = page_size // kp if kp >= 1 else 0
+    if kp < 1 or page_size % kp or ppp & (ppp - 1) or n_slots < keep + 1:
+        raise ValueError(f"slots: page_size {page_size}, kpool {kp}, {n_slots} slots for {keep} + 1 pools")
+    dev = C.on_gpu(pools, cnt, npool, positions, table)
+    tb = C.as_i32(table)
+    if tb.dim() not in (1, 2) or (tb.dim() == 2 and tb.shape[0] != N):
+        raise ValueError(f"slots: table {tuple(table.shape)} for {N} queries")
+    # the converted inputs stay referenced until the launch: a temporary freed before it could be reused (and
+    # overwritten) by the next conversion on the same stream
+    pl = C.need(C.as_i32(pools), "pools", torch.int32, (N, keep))
+    cn = C.need(C.as_i32(cnt.reshape(-1)), "cnt", torch.int32, (N,))
+    npl = C.need(C.as_i32(npool.reshape(-1)), "npool", torch.int32, (N,))
+    pos = C.need(C.as_i32(positions.reshape(-1)), "positions", torch.int32, (N,))
+    rows = torch.empty(N, n_slots, dtype=torch.int32, device=dev)
+    bias = torch.empty(N, n_slots, kp, dtype=torch.float32, device=dev)
+    st = _lib.lib().dsa_pool_slots(C.ptr(pl), C.ptr(cn), C.ptr(npl), C.ptr(pos), C.ptr(tb), int(tb.dim() == 1),
+                                   C.ptr(rows), C.ptr(bias), N, keep, n_slots, tb.shape[-1], page_size, kp,
+                                   C.stream_ptr(dev))
     _lib.check(st, "dsa_long.slots")
-    rows[:, :keep] = sel_rows
-    bias[:, :keep] = sel_bias
-    # the tail slot reads position min(npool, last) (its tokens are none at kp 1), the padding slots position 0
-    tail = npool.to(torch.int64).clamp(max=Pp * page_size - 1).view(N, 1)
-    tpage = tb.to(torch.int64).gather(1, torch.div(tail, page_size, rounding_mode="floor"))
-    rows[:, keep:keep + 1] = (tpage * page_size + tail % page_size).to(torch.int32)
-    pad_row = tb[:, :1].to(torch.int64) * page_size
-    if n_slots > keep + 1:
-        rows[:, keep + 1:] = pad_row.to(torch.int32)
-    del positions
-    return rows.to(torch.int64), bias.view(N, n_slots, 1)
+    return rows.to(torch.int64), bias
 
 
 def attend(q_lat: torch.Tensor, kc: torch.Tensor, rows: torch.Tensor, bias: torch.Tensor, scale: float, *,
