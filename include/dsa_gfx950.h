@@ -62,6 +62,17 @@ int dsa_indexer_decode(const void* q_bf16, const float* w, const uint8_t* k_fp8,
                        int Hi, int D, int max_pages, int page_size, int num_pages, int score_stride, void* stream);
 
 /*
+ * Decode indexer scores over a bf16 key cache with no per-key scale: GLM's pooled indexer over its pool-key cache
+ * (replaces trnrt/kernels/dsa_index.py:243-268 `scores` as called at trnrt/models/mla.py:628-629, one key per pool):
+ *   scores[b, p] = sum_h w[b, h] * relu(q[b, h, :] . k_bf16[slot(b, p), :]) (+ cand[b, p]),  NEG_INF at p >= ctx_len[b]
+ *   slot(b, p) = page_table[b, p / page_size] * page_size + p % page_size (page_size keys per page, any >= 1; 16 pools
+ *   of kpool 4 in a 64-token page); k_bf16 [num_pages * page_size, D]; other arguments as dsa_indexer_decode.
+ */
+int dsa_indexer_decode_bf16(const void* q_bf16, const float* w, const void* k_bf16, const int32_t* page_table,
+                            const int32_t* ctx_len, const float* cand, float* scores, int B, int Hi, int D,
+                            int max_pages, int page_size, int num_pages, int score_stride, void* stream);
+
+/*
  * Dense (prefill-chunk) indexer scores of N queries over one context's keys (replaces the score stage of
  * trnrt/kernels/dsa_long_select.py:500-530 `select`, arithmetic of dsa_long_select.py:119-133 `emulate_scores`
  * and trnrt/models/dsa_long.py:74-84 `scores` with a 2-D key tensor):
@@ -187,6 +198,25 @@ int dsa_decode_layer(const void* q_idx_bf16, const float* w, const uint8_t* k_fp
  */
 int dsa_cache_write(const void* x, int x_fp32, const int64_t* slots, uint8_t* cache, float* scale, int n_rows, int W,
                     long long num_slots, int per_token_scale, float fp8_max, void* stream);
+
+/*
+ * GLM's pooled indexer keys, written with the cache (replaces trnrt/models/mla.py:1277-1296 `write_pool_keys`, with
+ * trnrt/models/glm5_next.py:151-160 `pool_keys` and the slots of mla.py:1262-1274 `_pool_key_slots`): for each of
+ * n_rows written tokens, the pool of kp tokens it belongs to (positions first .. first + kp - 1, first = pos - pos % kp,
+ * their slots through the token's page table) gets the key
+ *   pk[d] = bf16(sum_t bf16(bf16(softmax_t(g_t[d] + ape[t, d])) * k_t[d])),  d < 128  (softmax over the pool in fp32)
+ * from the pool's cached indexer rows [key k (128) | gate logits g (128)], written as kp pieces of 128 / kp values,
+ * piece i into the slot of the pool's i-th token. A padded row (slot_mapping < page_size: the null page) reads and
+ * writes its own slot only.
+ *   rows [num_slots, rows_width]: e4m3fn (rows_fp8 = 1; with rows_scale fp32 [num_slots] the per-token scale, or null
+ *   for the reference's unscaled cache; read as bf16 values) or bf16; ape fp32 [kp, 128]; positions int32 [n_rows];
+ *   page_table int32 [n_rows, table_pages] or one shared [table_pages] (table_shared = 1); slot_mapping int64
+ *   [n_rows]; pool_key bf16 [num_slots, 128 / kp]. kp a power of two <= 8 dividing page_size; rows_width >= 256.
+ */
+int dsa_pool_keys_write(const void* rows, int rows_fp8, const float* rows_scale, int rows_width, const float* ape,
+                        const int32_t* positions, const int32_t* page_table, int table_shared, int table_pages,
+                        const int64_t* slot_mapping, void* pool_key, int n_rows, int kp, int page_size,
+                        long long num_slots, void* stream);
 
 /*
  * Bytes of workspace an entry point needs. kind: DSA_WS_TOPK (B, max_len, keep), DSA_WS_ATTENTION (B, H, keep,

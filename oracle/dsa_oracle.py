@@ -16,6 +16,9 @@ Each function cites the reference lines it follows. How each one is pinned (test
   score kinds, and a planted wrong tie rule that must fail;
 - two_level_ref: equal to topk_ref on the reference's own adversarial cases (trnrt/models/dsa_long.py:26-42 proves
   it exact);
+- pool_keys_ref / write_pool_keys_ref: a float64 loop over the softmax-gated mean, the known answer of equal gates
+  (the plain mean of the keys), the slot layout (pieces of a pool contiguous per page) and a planted mistake (the
+  pool-position bias dropped) that must fail;
 - cache_write_ref: torch's float -> e4m3fn cast checked against a round-to-nearest-even encoder written from the
   OCP e4m3fn definition over every representable value, every midpoint and its neighbours; known-answer rows; the
   per-token round trip within half an e4m3 step; planted mistakes (no clamp, truncation instead of rounding) that
@@ -131,6 +134,48 @@ def cache_write_ref(cache: torch.Tensor, scale: torch.Tensor | None, slots: torc
     if sc is not None:
         sc[sl[ok]] = s[ok]
     return c.view(cache.dtype).reshape(cache.shape), sc
+
+
+def pool_keys_ref(rows: torch.Tensor, ape: torch.Tensor) -> torch.Tensor:
+    """Each pool's key [..., Di] from its kpool tokens' indexer rows [..., kpool, 2 Di] (bf16 values: key, then gate
+    logits): the per-channel softmax over the pool of gate + ape weighting the keys, in bf16 as
+    trnrt/models/glm5_next.py:151-160 `pool_keys` computes it (softmax in fp32, weights and products rounded to
+    bf16, the sum over the pool in fp32 rounded to bf16)."""
+    Di = ape.shape[-1]
+    k = rows[..., :Di].to(torch.bfloat16)
+    logits = rows[..., Di:2 * Di].float() + ape.float()
+    return (torch.softmax(logits, dim=-2).to(torch.bfloat16) * k).sum(dim=-2)
+
+
+def write_pool_keys_ref(pool_key: torch.Tensor, rows: torch.Tensor, rows_scale: torch.Tensor | None,
+                        positions: torch.Tensor, table: torch.Tensor, slot_mapping: torch.Tensor, ape: torch.Tensor,
+                        page_size: int, kp: int) -> torch.Tensor:
+    """pool_key' after trnrt/models/mla.py:1277-1296 `write_pool_keys`: the slots of each written token's pool
+    (mla.py:1262-1274 `_pool_key_slots`: through the table, or the row's own slot kp times for a padded row), the
+    rows there read as bf16 (an FP8 cache through its per-token scale when given), their pool key (pool_keys_ref),
+    written as kp pieces. A padded row's kp pieces all land in its own slot; the last one is kept."""
+    T = positions.shape[0]
+    Di = ape.shape[-1]
+    first = positions.long() - positions.long() % kp
+    pos = first.view(T, 1) + torch.arange(kp).view(1, kp)
+    tb = table.long()
+    pages = tb[pos // page_size] if tb.dim() == 1 else tb.gather(1, pos // page_size)
+    slots = pages * page_size + pos % page_size
+    real = (slot_mapping.long() >= page_size).view(T, 1)
+    slots = torch.where(real, slots, slot_mapping.long().view(T, 1).expand(T, kp))
+    W = rows.shape[-1]
+    r = rows.reshape(-1, W)[slots.reshape(-1)]
+    if r.dtype in (torch.float8_e4m3fn, torch.uint8):
+        r = r.view(torch.float8_e4m3fn).float()
+        if rows_scale is not None:
+            r = r * rows_scale.reshape(-1)[slots.reshape(-1)].view(-1, 1)
+    keys = pool_keys_ref(r.to(torch.bfloat16).reshape(T, kp, W)[..., :2 * Di], ape)  # [T, Di]
+    out = pool_key.clone().reshape(-1, Di // kp)
+    pieces = keys.reshape(T, kp, Di // kp)
+    for n in range(T):
+        for i in range(kp):
+            out[int(slots[n, i])] = pieces[n, i]
+    return out.reshape(pool_key.shape)
 
 
 def e4m3fn_encode(v: float) -> int:

@@ -59,3 +59,78 @@ def test_pooled_attention_vs_oracle():
     tok = (rows.cpu().unsqueeze(-1) * kp + torch.arange(kp)).reshape(cfg.B, -1)
     ref, _ = O.sparse_mla_slots_ref(inp.q, inp.kv_cache, inp.kv_scale, tok, bias.cpu().reshape(cfg.B, -1), cfg.scale)
     assert_attention_close(o, ref)
+
+
+def _pool_setup(seed, fp8_rows, B=3, L=1024, ps=64, kp=4):
+    """A GLM-like pooled cache: per token an indexer row [key 128 | gate logits 128] (bf16, or e4m3 with per-token
+    scales), B sequences of L tokens through random page tables, and an empty pool-key cache."""
+    g = torch.Generator().manual_seed(seed)
+    npg = L // ps
+    num_pages = 1 + B * npg
+    slots = num_pages * ps
+    x = torch.randn(slots, 256, generator=g) * 2
+    if fp8_rows:
+        rows, rs = W.quantize_rows(x)
+    else:
+        rows, rs = x.to(torch.bfloat16), None
+    table = (torch.randperm(num_pages - 1, generator=g)[: B * npg] + 1).view(B, npg).to(torch.int32)
+    ape = torch.randn(kp, 128, generator=g)
+    return rows, rs, table, ape, slots
+
+
+@pytest.mark.parametrize("fp8_rows", [False, True])
+def test_pool_keys_write_vs_oracle(fp8_rows):
+    say(f"pool keys write fp8_rows={fp8_rows}")
+    kp, ps, L, B = 4, 64, 1024, 3
+    rows, rs, table, ape, slots = _pool_setup(7, fp8_rows, B, L, ps, kp)
+    # every token of every sequence written (one row per token, its own table), plus two padded rows
+    positions = torch.arange(L).repeat(B)
+    tb = table.repeat_interleave(L, dim=0)
+    slot_mapping = tb.long().gather(1, (positions // ps).view(-1, 1)).view(-1) * ps + positions % ps
+    positions = torch.cat([positions, torch.zeros(2, dtype=torch.int64)])
+    tb = torch.cat([tb, table[:1].expand(2, -1)])
+    slot_mapping = torch.cat([slot_mapping, torch.tensor([3, 5])])  # padded rows: slots in the null page
+    pk0 = torch.zeros(slots, 128 // kp, dtype=torch.bfloat16)
+    want = O.write_pool_keys_ref(pk0, rows, rs, positions, tb, slot_mapping, ape, ps, kp)
+    pk = pk0.cuda()
+    from trnrt_amd.kernels import dsa_cache
+    dsa_cache.write_pool_keys(pk, rows.cuda(), positions.cuda(), tb.cuda(), slot_mapping.cuda(), ape.cuda(), ps, kp,
+                              rows_scale=None if rs is None else rs.cuda())
+    torch.cuda.synchronize()
+    got = pk.cpu()[ps:].float()  # the null page's slots take the padded rows' pieces in an unspecified order
+    ref = want[ps:].float()
+    exact = (got == ref).float().mean().item()
+    rel = ((got - ref).abs() / ref.abs().clamp(min=1e-20)).max().item()
+    say(f"  exact fraction {exact:.5f}, max rel {rel:.3e}")
+    assert exact >= 0.99 and rel <= 2 ** -6  # expf vs the host's exp may move a weight by one bf16 step
+
+
+def test_pooled_indexer_over_written_pool_keys():
+    """The pooled decode indexer (dsa_index.scores over the bf16 pool-key cache, 16 pools per 64-token page) on pool
+    keys written by the kernel, against the oracle's indexer over the same keys; candidates: complete pools."""
+    say("pooled indexer")
+    from trnrt_amd.kernels import dsa_cache, dsa_index
+    kp, ps, L, B, Hi = 4, 64, 1024, 3, 64
+    rows, rs, table, ape, slots = _pool_setup(9, False, B, L, ps, kp)
+    positions = torch.arange(L).repeat(B)
+    tb = table.repeat_interleave(L, dim=0)
+    slot_mapping = tb.long().gather(1, (positions // ps).view(-1, 1)).view(-1) * ps + positions % ps
+    pk = torch.zeros(slots, 128 // kp, dtype=torch.bfloat16, device="cuda")
+    dsa_cache.write_pool_keys(pk, rows.cuda(), positions.cuda(), tb.cuda(), slot_mapping.cuda(), ape.cuda(), ps, kp)
+    g = torch.Generator().manual_seed(10)
+    q = torch.randn(B, Hi, 128, generator=g).to(torch.bfloat16)
+    w = torch.randn(B, Hi, generator=g) * 0.25 * 128 ** -0.5
+    pos_now = torch.tensor([1023, 514, 6])
+    npool = torch.div(pos_now + 1, kp, rounding_mode="floor").to(torch.int32)
+    ppp = ps // kp
+    pkc = pk.view(-1, ppp * 128)  # the reference's page rows (trnrt/models/mla.py:629)
+    got = dsa_index.scores(q.cuda(), w.cuda(), pkc, table.cuda(), None, ctx_len=npool.cuda())
+    torch.cuda.synchronize()
+    keys = pk.cpu().view(-1, 128)  # [pool slots, 128]: pool j of page p at p * ppp + j
+    ref = O.indexer_ref(q, w, keys, torch.ones(keys.shape[0]), table, npool, ppp, stride=L // kp)
+    live = ref > -1e29
+    from tests._helpers import row_rel_err
+    err = row_rel_err(got.cpu(), ref, live)
+    say(f"  pooled indexer rel err {err:.3e}")
+    assert err <= 1e-2
+    assert torch.equal(got.cpu() < -1e29, ~live)

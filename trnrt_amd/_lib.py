@@ -31,8 +31,11 @@ SIGNATURES: dict[str, tuple] = {
     "dsa_abi_version": (c_int, []),
     "dsa_strerror": (ctypes.c_char_p, [c_int]),
     "dsa_indexer_decode": (c_int, [P, P, P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, P]),
+    "dsa_indexer_decode_bf16": (c_int, [P, P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, P]),
     "dsa_indexer_prefill": (c_int, [P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_float, P]),
     "dsa_pool_slots": (c_int, [P, P, P, P, P, c_int, P, P, c_int, c_int, c_int, c_int, c_int, c_int, P]),
+    "dsa_pool_keys_write": (c_int, [P, c_int, P, c_int, P, P, P, c_int, c_int, P, P, c_int, c_int, c_int,
+                                    ctypes.c_longlong, P]),
     "dsa_cache_write": (c_int, [P, c_int, P, P, P, c_int, c_int, ctypes.c_longlong, c_int, c_float, P]),
     "dsa_indexer_prefill_fp8": (c_int, [P, P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_float, P]),
     "dsa_topk": (c_int, [P, P, P, P, P, c_size_t, c_int, c_int, c_int, c_int, c_int, P]),

@@ -21,6 +21,13 @@ hipError_t launch_cache_write(const void* x, int x_fp32, const int64_t* slots, u
 hipError_t launch_pool_slots(const int* pools, const int* cnt, const int* npool, const int* positions,
                              const int* table, int table_shared, int* rows, float* bias, int N, int keep, int n_slots,
                              int table_pages, int page_size, int kp, hipStream_t s);
+hipError_t launch_indexer_decode_bf16(const uint16_t* q, const float* w, const uint16_t* k, const int* table,
+                                      const int* ctx_len, const float* cand, float* scores, int B, int Hi,
+                                      int max_pages, int page_size, int num_pages, int stride, hipStream_t s);
+hipError_t launch_pool_keys(const void* rows, int rows_fp8, const float* rows_scale, int rows_width, const float* ape,
+                            const int* positions, const int* table, int table_shared, int table_pages,
+                            const int64_t* slot_mapping, uint16_t* pool_key, int T, int kp, int page_size,
+                            long num_slots, hipStream_t s);
 hipError_t launch_topk(const float* scores, const int* len, int* idx, int* cnt, void* ws, int B, int stride,
                        int max_len, int keep, int vis_only, bool hist_ready, const int* table, int max_pages,
                        int page_size, int num_pages, int* rows_out, hipStream_t s);
@@ -130,6 +137,20 @@ int dsa_indexer_decode(const void* q_bf16, const float* w, const uint8_t* k_fp8,
                                            score_stride, num_cu(), static_cast<hipStream_t>(stream)));
 }
 
+int dsa_indexer_decode_bf16(const void* q_bf16, const float* w, const void* k_bf16, const int32_t* page_table,
+                            const int32_t* ctx_len, const float* cand, float* scores, int B, int Hi, int D,
+                            int max_pages, int page_size, int num_pages, int score_stride, void* stream) {
+  if (!q_bf16 || !w || !k_bf16 || !page_table || !scores) return DSA_EINVAL;
+  if (B < 0 || Hi < 1 || max_pages < 1 || page_size < 1 || num_pages < 1 || score_stride < 0) return DSA_EINVAL;
+  if (D != 128 || Hi > 64) return DSA_EUNSUPPORTED;
+  if ((long)score_stride > (long)max_pages * page_size) return DSA_EINVAL;
+  if (B == 0 || score_stride == 0) return DSA_OK;
+  return status(dsa::launch_indexer_decode_bf16(static_cast<const uint16_t*>(q_bf16), w,
+                                                static_cast<const uint16_t*>(k_bf16), page_table, ctx_len, cand,
+                                                scores, B, Hi, max_pages, page_size, num_pages, score_stride,
+                                                static_cast<hipStream_t>(stream)));
+}
+
 int dsa_indexer_prefill(const void* q_bf16, const float* w, const uint8_t* k_fp8, const float* k_scale,
                         const int32_t* npool, float* scores, int N, int Hi, int D, int P, int score_stride,
                         float scale, void* stream) {
@@ -160,6 +181,19 @@ int dsa_cache_write(const void* x, int x_fp32, const int64_t* slots, uint8_t* ca
   if (n_rows == 0) return DSA_OK;
   return status(dsa::launch_cache_write(x, x_fp32 != 0, slots, cache, scale, n_rows, W, (long)num_slots,
                                         per_token_scale != 0, fp8_max, static_cast<hipStream_t>(stream)));
+}
+
+int dsa_pool_keys_write(const void* rows, int rows_fp8, const float* rows_scale, int rows_width, const float* ape,
+                        const int32_t* positions, const int32_t* page_table, int table_shared, int table_pages,
+                        const int64_t* slot_mapping, void* pool_key, int n_rows, int kp, int page_size,
+                        long long num_slots, void* stream) {
+  if (!rows || !ape || !positions || !page_table || !slot_mapping || !pool_key) return DSA_EINVAL;
+  if (n_rows < 0 || table_pages < 1 || page_size < 1 || num_slots < 1 || rows_width < 256) return DSA_EINVAL;
+  if (kp < 1 || kp > 8 || (kp & (kp - 1)) || page_size % kp) return DSA_EUNSUPPORTED;
+  if (n_rows == 0) return DSA_OK;
+  return status(dsa::launch_pool_keys(rows, rows_fp8 != 0, rows_scale, rows_width, ape, positions, page_table,
+                                      table_shared != 0, table_pages, slot_mapping, static_cast<uint16_t*>(pool_key),
+                                      n_rows, kp, page_size, (long)num_slots, static_cast<hipStream_t>(stream)));
 }
 
 int dsa_topk(const float* scores, const int32_t* len, int32_t* idx, int32_t* cnt, void* workspace,

@@ -102,4 +102,107 @@ hipError_t launch_cache_write(const void* x, int x_fp32, const int64_t* slots, u
                               fp8_max, s);
 }
 
+// GLM's pooled indexer keys, written with the cache (trnrt/models/mla.py:1262-1296 `write_pool_keys` with
+// trnrt/models/glm5_next.py:151-160 `pool_keys`): for every written token, its pool's kp cached indexer rows
+// [key (Di) | gate logits (Di)] give the pool key
+//
+//   pk[d] = bf16( sum_t bf16( bf16(softmax_t(g_t[d] + ape[t, d])) * k_t[d] ) )    (softmax over the pool, fp32)
+//
+// written as kp pieces of Di / kp values, piece i into the slot of the pool's i-th token (a padded row, slot in the
+// null page, writes all its pieces into its own slot). One wave per written token, 2 channels per lane (Di = 128).
+constexpr int PK_MAXKP = 8;
+
+__device__ __forceinline__ float bf16_round(float x) { return __uint_as_float((uint32_t)f32_to_bf16_bits(x) << 16); }
+
+template <bool FP8>
+__global__ __launch_bounds__(CW_WAVES * WAVE) void pool_keys_kernel(
+    const void* __restrict__ rows, const float* __restrict__ rows_scale, int rows_width, const float* __restrict__ ape,
+    const int* __restrict__ positions, const int* __restrict__ table, int table_shared, int table_pages,
+    const int64_t* __restrict__ slot_mapping, uint16_t* __restrict__ pool_key, int T, int kp, int page_size,
+    long num_slots) {
+  constexpr int Di = 128;
+  const int row = blockIdx.x * CW_WAVES + (int)(threadIdx.x / WAVE);
+  const int lane = threadIdx.x & (WAVE - 1);
+  if (row >= T) return;  // wave-uniform
+  const long own = slot_mapping[row];
+  const bool real = own >= page_size;
+  const int pos = positions[row];
+  const int first = pos - pos % kp;
+  const int* tab = table + (table_shared ? 0 : (size_t)row * table_pages);
+  long slot[PK_MAXKP];
+#pragma unroll
+  for (int t = 0; t < PK_MAXKP; ++t) {
+    const int p = first + min(t, kp - 1);
+    const long sl = (long)tab[min(max(p / page_size, 0), table_pages - 1)] * page_size + p % page_size;
+    slot[t] = real ? sl : own;
+    slot[t] = min(max(slot[t], 0L), num_slots - 1);  // in range whatever the inputs
+  }
+  // this lane's two channels d = 2 lane, 2 lane + 1 of every token of the pool: key and gate logit
+  float k[PK_MAXKP][2], l[PK_MAXKP][2];
+#pragma unroll
+  for (int t = 0; t < PK_MAXKP; ++t) {
+    const size_t base = (size_t)slot[t] * rows_width;
+    if (FP8) {
+      const uint8_t* r = static_cast<const uint8_t*>(rows) + base;
+      const float sc = rows_scale ? rows_scale[slot[t]] : 1.0f;
+      const uint16_t kb = *reinterpret_cast<const uint16_t*>(r + 2 * lane);
+      const uint16_t gb = *reinterpret_cast<const uint16_t*>(r + Di + 2 * lane);
+      const auto kf = __builtin_amdgcn_cvt_pk_f32_fp8(kb, false);
+      const auto gf = __builtin_amdgcn_cvt_pk_f32_fp8(gb, false);
+      // the reference reads the FP8 rows in the model dtype (bf16), exact for e4m3 values; a per-token scale, when
+      // the cache has one, is applied in fp32 and rounded back to bf16
+      k[t][0] = bf16_round(kf[0] * sc), k[t][1] = bf16_round(kf[1] * sc);
+      l[t][0] = bf16_round(gf[0] * sc), l[t][1] = bf16_round(gf[1] * sc);
+    } else {
+      const uint16_t* r = static_cast<const uint16_t*>(rows) + base;
+      const uint32_t kw = *reinterpret_cast<const uint32_t*>(r + 2 * lane);
+      const uint32_t gw = *reinterpret_cast<const uint32_t*>(r + Di + 2 * lane);
+      k[t][0] = __uint_as_float(kw << 16), k[t][1] = __uint_as_float(kw & 0xffff0000u);
+      l[t][0] = __uint_as_float(gw << 16), l[t][1] = __uint_as_float(gw & 0xffff0000u);
+    }
+  }
+  uint16_t out[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int d = 2 * lane + c;
+    float x[PK_MAXKP], m = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < PK_MAXKP; ++t) {
+      x[t] = l[t][c] + ape[min(t, kp - 1) * Di + d];
+      if (t < kp) m = fmaxf(m, x[t]);
+    }
+    float e[PK_MAXKP], sum = 0.0f;
+#pragma unroll
+    for (int t = 0; t < PK_MAXKP; ++t) {
+      e[t] = t < kp ? expf(x[t] - m) : 0.0f;
+      sum += e[t];
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int t = 0; t < PK_MAXKP; ++t)
+      if (t < kp) acc += bf16_round(bf16_round(e[t] / sum) * k[t][c]);
+    out[c] = f32_to_bf16_bits(acc);
+  }
+  // piece i (channels i Di / kp ..) into slot i: this lane's two channels
+  const int per = Di / kp;
+  const int piece = (2 * lane) / per;
+  const long dst = slot[min(piece, PK_MAXKP - 1)];
+  *reinterpret_cast<uint32_t*>(pool_key + (size_t)dst * per + (2 * lane - piece * per)) =
+      (uint32_t)out[0] | ((uint32_t)out[1] << 16);
+}
+
+hipError_t launch_pool_keys(const void* rows, int rows_fp8, const float* rows_scale, int rows_width, const float* ape,
+                            const int* positions, const int* table, int table_shared, int table_pages,
+                            const int64_t* slot_mapping, uint16_t* pool_key, int T, int kp, int page_size,
+                            long num_slots, hipStream_t s) {
+  const dim3 grid((T + CW_WAVES - 1) / CW_WAVES);
+  if (rows_fp8)
+    return launch("pool_keys_kernel", pool_keys_kernel<true>, grid, dim3(CW_WAVES * WAVE), s, rows, rows_scale,
+                  rows_width, ape, positions, table, table_shared, table_pages, slot_mapping, pool_key, T, kp,
+                  page_size, num_slots);
+  return launch("pool_keys_kernel", pool_keys_kernel<false>, grid, dim3(CW_WAVES * WAVE), s, rows, rows_scale,
+                rows_width, ape, positions, table, table_shared, table_pages, slot_mapping, pool_key, T, kp,
+                page_size, num_slots);
+}
+
 }  // namespace dsa

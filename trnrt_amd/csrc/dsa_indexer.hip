@@ -205,4 +205,135 @@ hipError_t launch_indexer_decode(const uint16_t* q, const float* w, const uint8_
                               num_pages, stride, stream);
 }
 
+// The pooled indexer's form (trnrt/kernels/dsa_index.py:243-268 `scores` over GLM's pool-key cache,
+// trnrt/models/mla.py:628-629): bf16 keys with no per-key scale, pages of any power-of-two number of keys (a page of
+// 64 tokens holds 16 pools of kpool 4):
+//
+//   score[b, p] = sum_h w[b, h] * relu(q[b, h, :] . k_bf16[slot(b, p), :])   (+ cand[b, p]),  NEG_INF at p >= L_b
+//
+// Same wave layout as above (lane (j, h): key j of the tile, dims 64h .. 64h + 63, here 128 bytes of bf16 fed to
+// the MFMA as they are), but every lane looks up its own key's page, so a 32-key tile may span pages: one round of
+// page-id loads, then one round of key loads, as above.
+template <int MT, bool CAND>
+__global__ __launch_bounds__(IDX_THREADS, 2) void indexer_decode_bf16_kernel(
+    const uint16_t* __restrict__ q, const float* __restrict__ w, const uint16_t* __restrict__ kcache,
+    const int* __restrict__ table, const int* __restrict__ ctx_len, const float* __restrict__ cand,
+    float* __restrict__ scores, int Hi, int max_pages, int page_size, int num_pages, int stride, int groups_per_row) {
+  __shared__ uint16_t qs[32 * MT * IDX_QROW];
+  __shared__ float ws[32 * MT];
+  const int b = blockIdx.x / groups_per_row;
+  const int grp = blockIdx.x - b * groups_per_row;
+  const int wave = threadIdx.x / WAVE;
+  const int lane = threadIdx.x & (WAVE - 1);
+  const int j = lane & 31;
+  const int h = lane >> 5;
+  const int tiles_row = (stride + IDX_TILE - 1) / IDX_TILE;
+  int L = stride;
+  if (ctx_len) L = min(max(ctx_len[b], 0), stride);
+  const int t_begin = grp * IDX_TPG + wave * IDX_TPW;
+  const int* trow = table + (size_t)b * max_pages;
+  float* srow = scores + (size_t)b * stride;
+
+  constexpr int QPT = 32 * MT * (IDX_D / 8) / IDX_THREADS;
+  uint4 qv[QPT];
+#pragma unroll
+  for (int r = 0; r < QPT; ++r) {
+    const int i = threadIdx.x + r * IDX_THREADS;
+    const int head = i / (IDX_D / 8), c = i - head * (IDX_D / 8);
+    qv[r] = *reinterpret_cast<const uint4*>(q + ((size_t)b * Hi + min(head, Hi - 1)) * IDX_D + 8 * c);
+  }
+  const float wv = w[(size_t)b * Hi + min((int)threadIdx.x, Hi - 1)];
+
+  // this lane's key in each of its tiles: its page (the null page past the context), then its 128 bytes
+  int page[IDX_TPW];
+#pragma unroll
+  for (int i = 0; i < IDX_TPW; ++i) {
+    const int p = (t_begin + i) * IDX_TILE + j;
+    const int pg = trow[min(p / page_size, max_pages - 1)];
+    page[i] = p < L ? safe_page(pg, num_pages) : 0;
+  }
+  uint4 kv[IDX_TPW][8];
+  float kc[IDX_TPW];
+#pragma unroll
+  for (int i = 0; i < IDX_TPW; ++i) {
+    const int p = (t_begin + i) * IDX_TILE + j;
+    const size_t slot = (size_t)page[i] * page_size + (p < L ? p % page_size : 0);
+    const uint16_t* kp = kcache + slot * IDX_D + 64 * h;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) kv[i][c] = *reinterpret_cast<const uint4*>(kp + 8 * c);
+    if (CAND) kc[i] = crow_value(cand, b, stride, p < L ? min(p, stride - 1) : 0);
+  }
+
+#pragma unroll
+  for (int r = 0; r < QPT; ++r) {
+    const int i = threadIdx.x + r * IDX_THREADS;
+    const int head = i / (IDX_D / 8), c = i - head * (IDX_D / 8);
+    *reinterpret_cast<uint4*>(&qs[head * IDX_QROW + 8 * c]) = head < Hi ? qv[r] : make_uint4(0, 0, 0, 0);
+  }
+  if (threadIdx.x < 32 * MT) ws[threadIdx.x] = (int)threadIdx.x < Hi ? wv : 0.0f;
+  __syncthreads();
+  bf16x8 qa[MT][8];
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+      qa[m][s] = as_bf16x8(*reinterpret_cast<const uint4*>(&qs[(32 * m + j) * IDX_QROW + 64 * h + 8 * s]));
+  float wr[MT][16];
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) wr[m][r] = ws[32 * m + 8 * (r >> 2) + 4 * h + (r & 3)];
+
+#pragma unroll
+  for (int i = 0; i < IDX_TPW; ++i) {
+    const int t = t_begin + i;
+    const int pos = t * IDX_TILE + j;
+    f32x16 acc[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[m][r] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+        acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa[m][s], as_bf16x8(kv[i][s]), acc[m], 0, 0, 0);
+    float part = 0.0f;
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) part = fmaf(wr[m][r], relu(acc[m][r]), part);
+    part += __shfl_xor(part, 32, WAVE);
+    float v = CAND ? part + kc[i] : part;
+    if (pos >= L) v = NEG_INF;
+    if (t < tiles_row && h == 0 && pos < stride) srow[pos] = v;
+  }
+}
+
+template <int MT, bool CAND>
+static hipError_t launch_indexer_bf16_variant(const uint16_t* q, const float* w, const uint16_t* k, const int* table,
+                                              const int* ctx_len, const float* cand, float* scores, int B, int Hi,
+                                              int max_pages, int page_size, int num_pages, int stride,
+                                              hipStream_t stream) {
+  const int tiles_row = (stride + IDX_TILE - 1) / IDX_TILE;
+  const int groups_row = (tiles_row + IDX_TPG - 1) / IDX_TPG;
+  return launch("indexer_decode_bf16_kernel", indexer_decode_bf16_kernel<MT, CAND>, dim3(B * groups_row),
+                dim3(IDX_THREADS), stream, q, w, k, table, ctx_len, cand, scores, Hi, max_pages, page_size, num_pages,
+                stride, groups_row);
+}
+
+hipError_t launch_indexer_decode_bf16(const uint16_t* q, const float* w, const uint16_t* k, const int* table,
+                                      const int* ctx_len, const float* cand, float* scores, int B, int Hi,
+                                      int max_pages, int page_size, int num_pages, int stride, hipStream_t s) {
+  if (Hi <= 32)
+    return cand ? launch_indexer_bf16_variant<1, true>(q, w, k, table, ctx_len, cand, scores, B, Hi, max_pages,
+                                                       page_size, num_pages, stride, s)
+                : launch_indexer_bf16_variant<1, false>(q, w, k, table, ctx_len, cand, scores, B, Hi, max_pages,
+                                                        page_size, num_pages, stride, s);
+  return cand ? launch_indexer_bf16_variant<2, true>(q, w, k, table, ctx_len, cand, scores, B, Hi, max_pages,
+                                                     page_size, num_pages, stride, s)
+              : launch_indexer_bf16_variant<2, false>(q, w, k, table, ctx_len, cand, scores, B, Hi, max_pages,
+                                                      page_size, num_pages, stride, s);
+}
+
 }  // namespace dsa

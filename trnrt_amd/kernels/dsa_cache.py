@@ -8,6 +8,9 @@ indexer-key rows at the step's slot_mapping).
 
 The HIP kernel (csrc/dsa_cache.hip) converts each row in one wave: fp32 arithmetic with a correctly rounded
 division and round-to-nearest-even into e4m3fn, which is torch's float -> float8_e4m3fn cast.
+
+write_pool_keys is the pooled (GLM) indexer's key write of the same step (trnrt/models/mla.py:1277-1296): each written
+token's pool key, a softmax-gated mean of the pool's cached indexer keys, into the pool-key cache.
 """
 
 from __future__ import annotations
@@ -60,3 +63,38 @@ def store(cache: torch.Tensor, slots: torch.Tensor, x: torch.Tensor, fp8_max: fl
     st = _lib.lib().dsa_cache_write(C.ptr(x), x_fp32, C.ptr(slots), C.ptr(cache), C.ptr(scale), T, W, num_slots,
                                     int(scale is not None), float(fp8_max), C.stream_ptr(dev))
     _lib.check(st, "dsa_cache.store")
+
+
+def write_pool_keys(pool_key: torch.Tensor, rows: torch.Tensor, positions: torch.Tensor, table: torch.Tensor,
+                    slot_mapping: torch.Tensor, ape: torch.Tensor, page_size: int, kp: int, *,
+                    rows_scale: torch.Tensor | None = None) -> None:
+    """Recomputes the pool key of every written token's pool and writes it to pool_key [slots, 128 / kp] bf16 as kp
+    pieces, one per slot of the pool (trnrt/models/mla.py:1277-1296 `write_pool_keys`, glm5_next.py:151-160
+    `pool_keys`): rows the cached indexer rows [slots, W >= 256] ([key 128 | gate logits 128], e4m3fn with optional
+    per-token rows_scale, or bf16), positions [T], table [T, Pp] or one [Pp], slot_mapping [T] (a padded row, in the
+    null page, writes only its own slot), ape [kp, 128] (the pool-position bias, idx_pool_ape)."""
+    dev = C.on_gpu(pool_key, rows, positions, table, slot_mapping, ape, rows_scale)
+    if pool_key.dtype != torch.bfloat16 or not pool_key.is_contiguous():
+        raise ValueError("dsa_cache.write_pool_keys: pool_key must be a contiguous bf16 cache")
+    W = rows.shape[-1]
+    num_slots = rows.numel() // W
+    if pool_key.numel() != num_slots * (128 // kp):
+        raise ValueError(f"dsa_cache.write_pool_keys: pool_key {tuple(pool_key.shape)} for {num_slots} slots, kp {kp}")
+    fp8 = rows.dtype in (C.FP8, torch.uint8)
+    if not fp8 and rows.dtype != torch.bfloat16:
+        raise ValueError(f"dsa_cache.write_pool_keys: rows of dtype {rows.dtype}")
+    if not rows.is_contiguous():
+        raise ValueError("dsa_cache.write_pool_keys: rows must be contiguous")
+    T = positions.numel()
+    pos = C.need(C.as_i32(positions.reshape(-1)), "positions", torch.int32, (T,))
+    sm = C.need(slot_mapping.reshape(-1).to(torch.int64).contiguous(), "slot_mapping", torch.int64, (T,))
+    tb = C.as_i32(table)
+    if tb.dim() not in (1, 2) or (tb.dim() == 2 and tb.shape[0] != T):
+        raise ValueError(f"dsa_cache.write_pool_keys: table {tuple(table.shape)} for {T} rows")
+    ap = C.need(C.as_f32(ape), "ape", torch.float32, (kp, 128))
+    rs = None if rows_scale is None else C.need(C.as_f32(rows_scale).reshape(-1), "rows_scale", torch.float32,
+                                                 (num_slots,))
+    st = _lib.lib().dsa_pool_keys_write(C.ptr(rows), int(fp8), C.ptr(rs), W, C.ptr(ap), C.ptr(pos), C.ptr(tb),
+                                        int(tb.dim() == 1), tb.shape[-1], C.ptr(sm), C.ptr(pool_key), T, kp,
+                                        page_size, num_slots, C.stream_ptr(dev))
+    _lib.check(st, "dsa_cache.write_pool_keys")

@@ -45,11 +45,12 @@ def _table(ppg: torch.Tensor, B: int) -> torch.Tensor:
     return ppg
 
 
-def decode_scores(q: torch.Tensor, w: torch.Tensor, k_cache: torch.Tensor, k_scale: torch.Tensor,
+def decode_scores(q: torch.Tensor, w: torch.Tensor, k_cache: torch.Tensor, k_scale: torch.Tensor | None,
                   table: torch.Tensor, ctx_len: torch.Tensor | None, page_size: int, score_stride: int | None = None,
                   cand: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
     """[B, score_stride] fp32 scores in the cache's native layout: q [B, Hi, 128] bf16, w [B, Hi] fp32 (head weights
-    times D ** -0.5), k_cache [slots, 128] e4m3fn with slots = pages x page_size, k_scale [slots] fp32, table
+    times D ** -0.5), k_cache [slots, 128] e4m3fn with k_scale [slots] fp32 (pages of a multiple of 32 keys), or
+    bf16 with k_scale None (GLM's pool keys: pages of any number of keys), slots = pages x page_size, table
     [B, max_pages] int32, ctx_len [B] int32 (None: every row's length is score_stride), cand [B, score_stride]
     additive fp32 or None. Positions at or past a row's length score NEG_INF."""
     dev = C.on_gpu(q, w, k_cache, k_scale, table, ctx_len, cand, out)
@@ -58,13 +59,20 @@ def decode_scores(q: torch.Tensor, w: torch.Tensor, k_cache: torch.Tensor, k_sca
         raise ValueError(f"dsa_index: head dim {Dq}, the kernel implements {D}")
     q = C.as_bf16(q)
     w = C.need(C.as_f32(w), "w", torch.float32, (B, Hi))
-    k_cache = C.fp8_bytes(k_cache, "k_cache")
+    bf16_keys = k_cache.dtype == torch.bfloat16
+    if bf16_keys != (k_scale is None):
+        raise ValueError("dsa_index: FP8 keys need their k_scale, bf16 keys take none")
+    if not bf16_keys:
+        k_cache = C.fp8_bytes(k_cache, "k_cache")
+    elif not k_cache.is_contiguous():
+        raise ValueError("k_cache: must be contiguous")
     if k_cache.dim() != 2 or k_cache.shape[1] != D:
         k_cache = k_cache.reshape(-1, D)
     slots = k_cache.shape[0]
     if slots % page_size:
         raise ValueError(f"dsa_index: {slots} cache slots are not whole pages of {page_size}")
-    k_scale = C.need(C.as_f32(k_scale).reshape(-1), "k_scale", torch.float32, (slots,))
+    if not bf16_keys:
+        k_scale = C.need(C.as_f32(k_scale).reshape(-1), "k_scale", torch.float32, (slots,))
     table = C.as_i32(table)
     if table.dim() != 2 or table.shape[0] != B:
         raise ValueError(f"dsa_index: page table {tuple(table.shape)} for {B} rows")
@@ -79,20 +87,27 @@ def decode_scores(q: torch.Tensor, w: torch.Tensor, k_cache: torch.Tensor, k_sca
         out = torch.empty(B, score_stride, dtype=torch.float32, device=dev)
     else:
         C.need(out, "out", torch.float32, (B, score_stride))
-    st = _lib.lib().dsa_indexer_decode(C.ptr(q), C.ptr(w), C.ptr(k_cache), C.ptr(k_scale), C.ptr(table),
-                                       C.ptr(ctx_len), C.ptr(cand), C.ptr(out), B, Hi, D, max_pages, page_size,
-                                       slots // page_size, score_stride, C.stream_ptr(dev))
+    if bf16_keys:
+        st = _lib.lib().dsa_indexer_decode_bf16(C.ptr(q), C.ptr(w), C.ptr(k_cache), C.ptr(table), C.ptr(ctx_len),
+                                                C.ptr(cand), C.ptr(out), B, Hi, D, max_pages, page_size,
+                                                slots // page_size, score_stride, C.stream_ptr(dev))
+    else:
+        st = _lib.lib().dsa_indexer_decode(C.ptr(q), C.ptr(w), C.ptr(k_cache), C.ptr(k_scale), C.ptr(table),
+                                           C.ptr(ctx_len), C.ptr(cand), C.ptr(out), B, Hi, D, max_pages, page_size,
+                                           slots // page_size, score_stride, C.stream_ptr(dev))
     _lib.check(st, "dsa_index.decode_scores")
     return out
 
 
 def scores(q: torch.Tensor, w: torch.Tensor, pkc: torch.Tensor, ppg: torch.Tensor, cand: torch.Tensor | None,
-           dge: int | None = None, *, pkc_scale: torch.Tensor, ctx_len: torch.Tensor | None = None) -> torch.Tensor:
+           dge: int | None = None, *, pkc_scale: torch.Tensor | None = None,
+           ctx_len: torch.Tensor | None = None) -> torch.Tensor:
     """[B, P] fp32 scores (trnrt/kernels/dsa_index.py:243-268 `scores`): q [B, Hi, D], w [B, Hi] fp32 (head weights
-    times D ** -0.5), pkc [Npages, page_size D] the FP8 key cache as page rows (one key of D per token: the per-token
-    indexer, kpool 1), pkc_scale [Npages, page_size] fp32 the keys' scales, ppg page_groups(table) [128, B, NG] or a
-    table [B, NPg] int32, cand [B, P] fp32 (0 / NEG_INF) or None, ctx_len [B] int32 or None. P = NPg page_size.
-    dge is the reference's Trainium DMA knob and is ignored."""
+    times D ** -0.5), pkc [Npages, page_size D] the key cache as page rows: FP8 e4m3 with pkc_scale [Npages,
+    page_size] fp32 the keys' scales (one key per token, kpool 1), or bf16 with no scale (GLM's pool-key cache,
+    trnrt/models/mla.py:628-629: page_size pools per page); ppg page_groups(table) [128, B, NG] or a table [B, NPg]
+    int32, cand [B, P] fp32 (0 / NEG_INF) or None, ctx_len [B] int32 or None. P = NPg page_size. dge is the
+    reference's Trainium DMA knob and is ignored."""
     del dge
     B = q.shape[0]
     table = _table(ppg, B)
@@ -100,4 +115,5 @@ def scores(q: torch.Tensor, w: torch.Tensor, pkc: torch.Tensor, ppg: torch.Tenso
     if page_size is None or pkc.shape[1] != page_size * D:
         raise ValueError(f"dsa_index: pkc {tuple(pkc.shape)} is not [pages, page_size x {D}]")
     P = table.shape[1] * page_size
-    return decode_scores(q, w, pkc.reshape(-1, D), pkc_scale.reshape(-1), table, ctx_len, page_size, P, cand)
+    ks = None if pkc_scale is None else pkc_scale.reshape(-1)
+    return decode_scores(q, w, pkc.reshape(-1, D), ks, table, ctx_len, page_size, P, cand)
