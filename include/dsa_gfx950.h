@@ -130,7 +130,8 @@ int dsa_topk_mask(const int32_t* idx, const int32_t* cnt, const float* scores, f
  * Sparse MLA decode attention over the selected tokens (replaces trnrt/kernels/dsa_decode.py:26-43 `attend`,
  * trnrt/kernels/dsa_slots.py:48-65 `emulate` with lse, trnrt/kernels/dsa_slots_n.py:154-203 `attend`,
  * trnrt/models/dsa_long.py:189-223 `slots` + `attend`; split combine of trnrt/models/mla.py:853-856):
- *   K[k] = kv_fp8[slot_k, :Dqk] * kv_scale[slot_k] (key, Dqk = 576), V[k] = K[k][:Dv] (Dv = 512)
+ *   K[k] = kv_fp8[slot_k, :Dqk] * kv_scale[slot_k] (key, Dqk = 576: 512 latent + 64 rope, or 512: GLM's NoPE latent;
+ *   rows of Dqk bytes), V[k] = K[k][:Dv] (Dv = 512)
  *   s[h, k] = scale * q[b, h, :] . K[k] + bias_k,  p = softmax_k(s),  out[b, h, :] = sum_k p[h, k] V[k]
  *   lse[b, h] = max_k s + log sum_k exp(s - max)
  * Two ways to name the slots (exactly one must be given):

@@ -134,3 +134,26 @@ def test_pooled_indexer_over_written_pool_keys():
     say(f"  pooled indexer rel err {err:.3e}")
     assert err <= 1e-2
     assert torch.equal(got.cpu() < -1e29, ~live)
+
+
+@pytest.mark.parametrize("dqk", [512, 576])
+def test_pooled_attention_glm_latent_width(dqk):
+    """GLM's NoPE latent (512 wide; with rope 576) through pool slots of kpool 4: the attention kernel's two row
+    widths against the oracle."""
+    say(f"pooled attention dqk={dqk}")
+    g = torch.Generator().manual_seed(dqk)
+    B, H, L, ps, kp, keep = 4, 32, 1024, 64, 4, 48
+    npg = L // ps
+    num_pages = 1 + B * npg
+    kv, ks = W.quantize_rows(torch.randn(num_pages * ps, dqk, generator=g))
+    table = (torch.randperm(num_pages - 1, generator=g)[: B * npg] + 1).view(B, npg).to(torch.int32)
+    q = torch.randn(B, H, dqk, generator=g).to(torch.bfloat16)
+    positions = torch.tensor([1023, 700, 9, 2])
+    pools, cnt, npool = _selection(B, L, kp, keep, positions, seed=dqk + 1)
+    rows, bias = dsa_long.slots(pools.cuda(), cnt.cuda(), npool.cuda(), positions.cuda(), table.cuda(), ps, kp,
+                                keep + 1)
+    o = dsa_long.attend(q.cuda(), kv.cuda(), rows, bias, 192 ** -0.5, kc_scale=ks.cuda())
+    torch.cuda.synchronize()
+    tok = (rows.cpu().unsqueeze(-1) * kp + torch.arange(kp)).reshape(B, -1)
+    ref, _ = O.sparse_mla_slots_ref(q, kv, ks, tok, bias.cpu().reshape(B, -1), 192 ** -0.5)
+    assert_attention_close(o, ref)

@@ -38,7 +38,7 @@ size_t topk_workspace_bytes(int B, int max_len, int keep);
 bool topk_supported(int max_len, int keep, int vis_only);
 hipError_t launch_sparse_mla(const uint16_t* q, const uint8_t* kv, const float* kvs, const int* idx, const int* cnt,
                              const int* table, const int* rows, const float* bias, uint16_t* out, float* out_f32,
-                             float* lse, void* ws, int B, int H, int keep, int max_pages, int page_size,
+                             float* lse, void* ws, int B, int H, int Dqk, int keep, int max_pages, int page_size,
                              int num_pages, float scale, int splits, hipStream_t s);
 hipError_t launch_token_rows(const int* idx, const int* cnt, const int* table, int* rows, float* bias, int B,
                              int keep, int max_pages, int page_size, int num_pages, hipStream_t s);
@@ -241,7 +241,7 @@ int dsa_sparse_mla_decode(const void* q_bf16, const uint8_t* kv_fp8, const float
   if (token_form && (!cnt || !page_table)) return DSA_EINVAL;
   if (!token_form && !bias) return DSA_EINVAL;
   if (B < 0 || H < 1 || keep < 1 || page_size < 1 || num_pages < 1 || (token_form && max_pages < 1)) return DSA_EINVAL;
-  if (Dqk != 576 || Dv != 512 || H % 16) return DSA_EUNSUPPORTED;
+  if ((Dqk != 576 && Dqk != 512) || Dv != 512 || H % 16) return DSA_EUNSUPPORTED;
   if ((long)num_pages * page_size > 0x7fffffffL) return DSA_EUNSUPPORTED;
   if (B == 0) return DSA_OK;
   const int sp = effective_splits(resolve_splits(splits, B, H, keep), keep);
@@ -249,7 +249,7 @@ int dsa_sparse_mla_decode(const void* q_bf16, const uint8_t* kv_fp8, const float
   if (need && (!workspace || workspace_bytes < need)) return DSA_EWORKSPACE;
   return status(dsa::launch_sparse_mla(static_cast<const uint16_t*>(q_bf16), kv_fp8, kv_scale, idx, cnt, page_table,
                                        rows, bias, static_cast<uint16_t*>(out_bf16), out_f32, lse, workspace, B, H,
-                                       keep, max_pages, page_size, num_pages, scale, sp,
+                                       Dqk, keep, max_pages, page_size, num_pages, scale, sp,
                                        static_cast<hipStream_t>(stream)));
 }
 
@@ -330,8 +330,8 @@ int dsa_decode_layer(const void* q_idx_bf16, const float* w, const uint8_t* k_fp
   if ((long)num_pages * page_size > 0x7fffffffL) return DSA_EUNSUPPORTED;
   const int sp = effective_splits(resolve_splits(splits, B, H, keep), keep);
   return status(dsa::launch_sparse_mla(static_cast<const uint16_t*>(q_bf16), kv_fp8, kv_scale, nullptr, cnt, nullptr,
-                                       rows, nullptr, static_cast<uint16_t*>(out_bf16), nullptr, lse, aws, B, H, keep,
-                                       max_pages, page_size, num_pages, scale, sp, s));
+                                       rows, nullptr, static_cast<uint16_t*>(out_bf16), nullptr, lse, aws, B, H, 576,
+                                       keep, max_pages, page_size, num_pages, scale, sp, s));
 }
 
 }  // extern "C"

@@ -1,6 +1,7 @@
 // Sparse MLA decode attention for gfx950 over the selected tokens of a paged FP8 latent cache (the arithmetic of
 // trnrt/kernels/dsa_decode.py:26-37 and trnrt/kernels/dsa_slots.py:48-65, absorbed MLA, with a 576-wide key of
-// 512 latent + 64 rope columns and the first 512 columns as the value; per-token FP8 scales):
+// 512 latent + 64 rope columns, or GLM's 512-wide NoPE latent, and the first 512 columns as the value; per-token FP8
+// scales):
 //
 //   s[h, k] = scale * q[h, :] . K[k] + bias[k],  K[k] = kv_fp8[slot_k] * kv_scale[slot_k]
 //   o[h, :] = sum_k softmax_k(s)[h, k] * K[k][:512],  lse[h] = max_k s + log sum_k exp(s - max)
@@ -27,20 +28,20 @@
 
 namespace dsa {
 
-constexpr int ATT_DQK = 576;
-constexpr int ATT_DV = 512;
+constexpr int ATT_DV = 512;      // the value: the first 512 columns of a row (the latent)
 constexpr int ATT_HPW = 16;       // heads per workgroup
 constexpr int ATT_CH = 64;        // slots per chunk
 constexpr int ATT_THREADS = 512;  // 8 waves: two halves of 4
 constexpr int ATT_NCH = 4;        // chunks staged in LDS at once
 constexpr int ATT_SUPER = ATT_NCH * ATT_CH;  // slots staged at once
-constexpr int ATT_PIECES = ATT_DQK / 16;     // 36 16-byte pieces per row
-constexpr int ATT_KPIECES = ATT_PIECES + 1;  // LDS row: the pieces and one padding piece
+// Rows of DQK = 576 (512 latent + 64 rope, 36 16-byte pieces) or 512 (a NoPE latent, 32 pieces) columns; in LDS
+// both take 37 pieces (592 bytes: the data and one or five padding pieces), the stride that spreads the operand
+// reads over the banks.
+constexpr int ATT_KPIECES = 37;
 constexpr int ATT_KROW = 16 * ATT_KPIECES;   // 592 bytes
 constexpr int ATT_CHUNK_BYTES = ATT_CH * ATT_KROW;  // 37,888: 37 direct-to-LDS instructions of 1 KiB
 constexpr int ATT_LOADS = ATT_NCH * ATT_KPIECES;    // 148 instructions per staged super-chunk
 constexpr int ATT_PROW = ATT_CH + 8;         // P row stride (bf16 elements; 16-byte aligned rows)
-constexpr int ATT_QROW = ATT_DQK + 8;        // staged query row stride (bf16 elements)
 
 typedef int att_v2i __attribute__((ext_vector_type(2)));
 
@@ -67,6 +68,7 @@ __device__ __forceinline__ bf16x8 value_operand(const uint8_t* kt, int ks, int n
 
 // Slot forms: token (idx + cnt + table: positions through the page table, bias 0 below cnt), rows + bias (cache
 // slots with an additive bias), rows + cnt (cache slots, bias 0 below cnt).
+template <int DQK>
 __global__ __launch_bounds__(ATT_THREADS, 1) void sparse_mla_kernel(
     const uint16_t* __restrict__ q, const uint8_t* __restrict__ kv, const float* __restrict__ kvs,
     const int* __restrict__ idx, const int* __restrict__ cnt, const int* __restrict__ table,
@@ -74,6 +76,10 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void sparse_mla_kernel(
     float* __restrict__ out_f32, float* __restrict__ lse_out, float* __restrict__ ws_o, float* __restrict__ ws_ml,
     int B, int H, int keep, int max_pages, int page_size, int num_pages, float scale, int splits,
     int slots_per_split) {
+  constexpr int ATT_PIECES = DQK / 16;  // 16-byte data pieces per row
+  constexpr int ATT_QROW = DQK + 8;     // staged query row stride (bf16 elements)
+  constexpr int STEPS = DQK / 32;       // score steps of 32 dims
+  static_assert(ATT_PIECES < ATT_KPIECES && STEPS % 2 == 0, "row width");
   __shared__ AttShared sh;
   const int HG = H / ATT_HPW;
   const int groups = B * splits;
@@ -100,14 +106,14 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void sparse_mla_kernel(
   const int k_end = min(k_begin + slots_per_split, n_eff);
   const size_t nslots_cache = (size_t)num_pages * page_size;
 
-  // the queries of the 16 heads (18 KiB): 36 bytes per thread, staged through LDS below
-  const uint4* qsrc = reinterpret_cast<const uint4*>(q + ((size_t)b * H + ATT_HPW * hg) * ATT_DQK);
-  constexpr int QPIECES = ATT_HPW * ATT_DQK / 8;  // 16-byte pieces: 1152
+  // the queries of the 16 heads (16 or 18 KiB), staged through LDS below
+  const uint4* qsrc = reinterpret_cast<const uint4*>(q + ((size_t)b * H + ATT_HPW * hg) * DQK);
+  constexpr int QPIECES = ATT_HPW * DQK / 8;  // 16-byte pieces: 1024 or 1152
   uint4 qv[3];
 #pragma unroll
   for (int i = 0; i < 3; ++i) qv[i] = qsrc[min(tid + ATT_THREADS * i, QPIECES - 1)];
 
-  bf16x8 qb[18];
+  bf16x8 qb[STEPS];
   f32x4 o[8];
 #pragma unroll
   for (int n = 0; n < 8; ++n) o[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -141,22 +147,23 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void sparse_mla_kernel(
     __syncthreads();
     if (sc0 == k_begin) {
       // query operand: head 16hg + l16, dims 32 st + 8 q4 .. + 7 at step st, through the rows' LDS (q rows padded
-      // to 584 elements so the operand reads spread over the banks)
+      // by 8 elements so the operand reads spread over the banks)
       uint16_t* qs = reinterpret_cast<uint16_t*>(sh.kt[ATT_NCH - 1]);
 #pragma unroll
       for (int i = 0; i < 3; ++i) {
-        const int pc = tid + ATT_THREADS * i;  // 16-byte piece: head pc / 72, elements 8 (pc % 72) ..
+        const int pc = tid + ATT_THREADS * i;  // 16-byte piece: head pc / (DQK / 8), elements 8 (pc % (DQK / 8)) ..
         if (pc < QPIECES)
-          *reinterpret_cast<uint4*>(qs + (pc / 72) * ATT_QROW + 8 * (pc % 72)) = qv[i];
+          *reinterpret_cast<uint4*>(qs + (pc / (DQK / 8)) * ATT_QROW + 8 * (pc % (DQK / 8))) = qv[i];
       }
       __syncthreads();
       const uint16_t* qh = qs + l16 * ATT_QROW + 8 * q4;
 #pragma unroll
-      for (int st = 0; st < 18; ++st) qb[st] = as_bf16x8(*reinterpret_cast<const uint4*>(qh + 32 * st));
+      for (int st = 0; st < STEPS; ++st) qb[st] = as_bf16x8(*reinterpret_cast<const uint4*>(qh + 32 * st));
       __syncthreads();  // every wave holds its operand before the rows overwrite it
     }
     // every staged row straight into LDS: instruction kk (chunk kk / 37, 1-KiB block j = kk % 37 of its tile) has
-    // lane l load 16-byte unit u = 64 j + l of the tile: row u / 37, piece u % 37 (the padding piece re-reads 35);
+    // lane l load 16-byte unit u = 64 j + l of the tile: row u / 37, piece u % 37 (a padding piece re-reads the
+    // last data piece);
     // the 148 instructions are spread over the 8 waves
     {
       int src_slot[(ATT_LOADS + 7) / 8];
@@ -174,7 +181,7 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void sparse_mla_kernel(
         if (kk < ATT_LOADS && c < nch) {
           const int u = WAVE * j + lane;
           const int pc = u - (u / ATT_KPIECES) * ATT_KPIECES;
-          const uint8_t* src = kv + (size_t)src_slot[i] * ATT_DQK + 16 * (pc < ATT_PIECES ? pc : ATT_PIECES - 1);
+          const uint8_t* src = kv + (size_t)src_slot[i] * DQK + 16 * (pc < ATT_PIECES ? pc : ATT_PIECES - 1);
           __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)&sh.kt[c][1024 * j], 16, 0,
                                            0);
         }
@@ -197,7 +204,7 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void sparse_mla_kernel(
         f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
         const uint8_t* kr = kt + (16 * wh + l16) * ATT_KROW + 8 * q4;
 #pragma unroll
-        for (int st = 0; st < 18; st += 2) {
+        for (int st = 0; st < STEPS; st += 2) {
           const uint2 ka = *reinterpret_cast<const uint2*>(kr + 32 * st);
           const uint2 kb = *reinterpret_cast<const uint2*>(kr + 32 * st + 32);
           acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16x8(ka.x, ka.y), qb[st], acc0, 0, 0, 0);
@@ -453,7 +460,7 @@ size_t attention_workspace_bytes(int B, int H, int splits) {
 
 hipError_t launch_sparse_mla(const uint16_t* q, const uint8_t* kv, const float* kvs, const int* idx, const int* cnt,
                              const int* table, const int* rows, const float* bias, uint16_t* out, float* out_f32,
-                             float* lse, void* ws, int B, int H, int keep, int max_pages, int page_size,
+                             float* lse, void* ws, int B, int H, int Dqk, int keep, int max_pages, int page_size,
                              int num_pages, float scale, int splits, hipStream_t s) {
   const int HG = H / ATT_HPW;
   // slots per split: a whole number of chunks
@@ -468,9 +475,14 @@ hipError_t launch_sparse_mla(const uint16_t* q, const uint8_t* kv, const float* 
     ws_o = static_cast<float*>(ws);
     ws_ml = ws_o + (size_t)B * eff_splits * H * ATT_DV;  // [B, splits, H, 2]: max, sum
   }
-  hipError_t e = launch("sparse_mla_kernel", sparse_mla_kernel, dim3(grid), dim3(ATT_THREADS), s, q, kv, kvs, idx,
-                        cnt, table, rows, bias, out, out_f32, lse, ws_o, ws_ml, B, H, keep, max_pages, page_size,
-                        num_pages, scale, eff_splits, sps);
+  hipError_t e =
+      Dqk == 512
+          ? launch("sparse_mla_kernel", sparse_mla_kernel<512>, dim3(grid), dim3(ATT_THREADS), s, q, kv, kvs, idx, cnt,
+                   table, rows, bias, out, out_f32, lse, ws_o, ws_ml, B, H, keep, max_pages, page_size, num_pages,
+                   scale, eff_splits, sps)
+          : launch("sparse_mla_kernel", sparse_mla_kernel<576>, dim3(grid), dim3(ATT_THREADS), s, q, kv, kvs, idx, cnt,
+                   table, rows, bias, out, out_f32, lse, ws_o, ws_ml, B, H, keep, max_pages, page_size, num_pages,
+                   scale, eff_splits, sps);
   if (e != hipSuccess || eff_splits == 1) return e;
   if (eff_splits <= 8)
     return launch("combine_splits_kernel", combine_splits_kernel<8>, dim3(B * H), dim3(128), s, ws_o, ws_ml, H,

@@ -4,8 +4,9 @@ trnrt/kernels/dsa_decode.py, with trnrt/kernels/dsa_slots.py's log-sum-exp).
 What it computes, per row b and head h (trnrt/kernels/dsa_decode.py:26-37, absorbed MLA), over the row's slots k:
     s[k] = scale q[b, h] . K[k] + bias[b, k],  p = softmax(s),  o[b, h] = sum_k p[k] V[k]
     lse[b, h] = max_k s + log sum_k exp(s - max)                              (trnrt/kernels/dsa_slots.py:8-11)
-with K[k] the slot's 576-wide FP8 cache row times its per-token scale (512 latent + 64 rope columns) and V[k] its
-first 512 columns (the reference's NoPE latent is both; with rope the value is the latent part). A row whose slots are
+with K[k] the slot's FP8 cache row times its per-token scale, 576 wide (512 latent + 64 rope columns) or 512 wide
+(GLM's NoPE latent), and V[k] its first 512 columns (the reference's NoPE latent is both; with rope the value is the
+latent part). A row whose slots are
 all masked at NEG_INF averages them uniformly and has lse NEG_INF, as in the reference.
 
 The HIP kernel (csrc/dsa_attention.hip) gathers the rows into LDS per 64-slot chunk, runs both products on bf16 MFMA
@@ -21,7 +22,8 @@ from .. import _lib
 from . import _common as C
 
 NEG_INF = -1e30  # trnrt/models/decoder.py NEG_INF
-DQK = 576  # kv_lora_rank 512 + qk_rope_head_dim 64
+DQK = 576  # kv_lora_rank 512 + qk_rope_head_dim 64 (this build's cache format)
+DQK_WIDTHS = (576, 512)  # the row widths the kernel takes: with rope, and GLM's NoPE latent
 DV = 512  # kv_lora_rank
 
 
@@ -29,13 +31,13 @@ def _run(q: torch.Tensor, kv: torch.Tensor, kv_scale: torch.Tensor, scale: float
          page_size: int = 1, rows=None, bias=None, lse: bool = False, out_dtype=torch.float32, splits: int = 0,
          out: torch.Tensor | None = None, workspace: torch.Tensor | None = None):
     dev = C.on_gpu(q, kv, kv_scale, idx, cnt, table, rows, bias, out, workspace)
-    if q.dim() != 3 or q.shape[2] != DQK:
-        raise ValueError(f"dsa_decode: q {tuple(q.shape)}, expected [B, H, {DQK}]")
-    B, H, _ = q.shape
+    if q.dim() != 3 or q.shape[2] not in DQK_WIDTHS:
+        raise ValueError(f"dsa_decode: q {tuple(q.shape)}, expected [B, H, 576 or 512]")
+    B, H, dqk = q.shape
     if H % 16:
         raise NotImplementedError(f"dsa_decode: {H} heads (the kernel takes multiples of 16)")
     q = C.as_bf16(q)
-    kv = C.fp8_bytes(kv, "kv cache").reshape(-1, DQK)
+    kv = C.fp8_bytes(kv, "kv cache").reshape(-1, dqk)
     slots = kv.shape[0]
     kv_scale = C.need(C.as_f32(kv_scale).reshape(-1), "kv_scale", torch.float32, (slots,))
     if idx is not None:
@@ -71,7 +73,7 @@ def _run(q: torch.Tensor, kv: torch.Tensor, kv_scale: torch.Tensor, scale: float
     o_32 = out if out.dtype == torch.float32 else None
     st = _lib.lib().dsa_sparse_mla_decode(
         C.ptr(q), C.ptr(kv), C.ptr(kv_scale), C.ptr(idx), C.ptr(cnt), C.ptr(table), C.ptr(rows), C.ptr(bias),
-        C.ptr(o_bf), C.ptr(o_32), C.ptr(ls), C.ptr(workspace), ws_len, B, H, DQK, DV, keep, max_pages, page_size,
+        C.ptr(o_bf), C.ptr(o_32), C.ptr(ls), C.ptr(workspace), ws_len, B, H, dqk, DV, keep, max_pages, page_size,
         num_pages, float(scale), int(splits), C.stream_ptr(dev))
     _lib.check(st, "dsa_decode.attend")
     return (out, ls) if lse else out
