@@ -12,6 +12,7 @@ the reference arithmetic, timed on this host's cores on a bounded sample of the 
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--config 2] [--no-cpu-baseline]
     python bench.py --config 5          # the chunked-prefill step (65,536 cached + 2,048 new queries): its own line
+    python bench.py --config 6          # the pooled (GLM-5.3-Flash, kpool 4) decode step at B=8 x 32K: its own line
     python bench.py --copy-probe 512    # plain device copies of 512 MiB: the calibration run for HBM counters
 
 roofline.traffic (HBM bytes per indexer launch) comes from rocprofv3 FETCH_SIZE / WRITE_SIZE counter runs of this
@@ -259,6 +260,117 @@ def prefill_main(args) -> int:
     return 0
 
 
+def pooled_cpu_baseline(inp, cfg, npool, positions, budget_s: float = 15.0) -> dict:
+    """The oracle's pooled decode step (indexer_ref over the pool keys + topk_ref + pool_slots_ref +
+    sparse_mla_slots_ref, torch fp32 on the host) on rows of the same batch, as many as fit in about budget_s seconds;
+    reported as steps per second (rows / B)."""
+    import torch
+
+    from oracle import dsa_oracle as O
+
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    torch.set_num_threads(cores)
+    cpu = inp.to("cpu")
+    keys = cpu.pool_key.view(-1, cfg.D)
+    ones = torch.ones(keys.shape[0])
+    ppp = cfg.page_size // cfg.kp
+    n, t0 = 0, time.perf_counter()
+    while True:
+        b = n % cfg.B
+        sl = slice(b, b + 1)
+        sc = O.indexer_ref(cpu.q_idx[sl], cpu.w[sl], keys, ones, cpu.table[sl], npool[sl], ppp)
+        pools, cnt = O.topk_ref(sc, cfg.keep)
+        rows, bias = O.pool_slots_ref(pools, cnt, npool[sl], positions[sl], cpu.table[sl], cfg.page_size, cfg.kp,
+                                      cfg.keep + 1)
+        tok = (rows.unsqueeze(-1) * cfg.kp + torch.arange(cfg.kp)).reshape(1, -1)
+        O.sparse_mla_slots_ref(cpu.q[sl], cpu.kv_cache, cpu.kv_scale, tok, bias.reshape(1, -1), cfg.scale)
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= budget_s or n >= 4 * cfg.B:
+            break
+    return {"value": n / cfg.B / dt, "unit": "layer-steps/s", "cores": cores, "kind": "port",
+            "sample": f"{n} query rows of the batch's {cfg.B} (pool scores + top-{cfg.keep} pools + slots + sparse "
+                      f"MLA over {cfg.kp * (cfg.keep + 1)} token slots, torch fp32, {dt:.1f} s, {cores} threads)"}
+
+
+def pooled_main(args) -> int:
+    """The pooled (GLM-5.3-Flash) decode step (config 6): the current tokens' pool-key write (dsa_pool_keys_write),
+    then the pooled layer (dsa_pooled_decode_layer: the indexer over the bf16 pool-key cache with the top-k's
+    first-level histogram fused, the exact top-512 pools, sparse MLA over the selected pools' tokens and the tail, over
+    the 512-wide NoPE latent). roofline: the indexer kernel's algorithmic bytes over its HIP-event-timed duration."""
+    import torch
+
+    from trnrt_amd import _lib
+    from trnrt_amd import workloads as W
+    from trnrt_amd.kernels import dsa_cache
+    from trnrt_amd.kernels.dsa_layer import PooledDecodeLayer
+
+    cfg = W.POOLED_CONFIGS[args.config]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    inp = W.make_pooled_inputs(cfg, seed=0, device=dev)
+    lib = _lib.lib()
+    ps, kp = cfg.page_size, cfg.kp
+    pos = inp.positions
+    slot_mapping = dsa_cache.slots_of(pos, inp.table, ps)
+    npool_d = torch.div(pos + 1, kp, rounding_mode="floor").to(torch.int32)
+    layer = PooledDecodeLayer(cfg.B, cfg.Hi, cfg.H, cfg.dqk, inp.table.shape[1], ps, inp.pool_key.shape[0] // ps, kp,
+                              cfg.keep, cfg.scale, splits=args.splits, device=dev)
+
+    def step():
+        dsa_cache.write_pool_keys(inp.pool_key, inp.rows, pos, inp.table, slot_mapping, inp.ape, ps, kp,
+                                  rows_scale=inp.rows_scale)
+        layer.step(inp.q_idx, inp.w, inp.pool_key, inp.q, inp.kv_cache, inp.kv_scale, inp.table, npool_d, pos,
+                   check=False)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    k_us = kernel_times(lib, step, args.steps)
+    positions = pos.cpu().long()
+    npool = torch.div(positions + 1, kp, rounding_mode="floor")
+    tail = [int(p) + 1 - kp * int(n) for p, n in zip(positions, npool)]
+    tokens = [kp * min(int(n), cfg.keep) + t for n, t in zip(npool, tail)]
+    idx_bytes = W.pooled_indexer_bytes(cfg, npool.tolist())
+    idx_us = k_us["indexer_decode_bf16_kernel"]
+    achieved = idx_bytes / (idx_us * 1e-6) / 1e9
+    step_bytes = W.pooled_step_bytes(cfg, npool.tolist(), tokens)
+    step_gbs = step_bytes / (ms * 1e-3) / 1e9
+    out = {
+        "metric": "DSA pooled decode layer-steps/sec (GLM kpool 4) at B=8, 32K ctx; indexer HBM GB/s (% of 8 TB/s)",
+        "value": round(1e3 / ms, 1),
+        "unit": "layer-steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"config {args.config}: {cfg.name}", "batch": cfg.B, "context": cfg.L,
+                   "q_heads": cfg.H, "indexer_heads": cfg.Hi, "kpool": kp, "keep_pools": cfg.keep,
+                   "page_size": ps, "pool_keys": "bf16 [128] per pool (kpool pieces)",
+                   "kv": f"fp8 e4m3 [{cfg.dqk}] + fp32 scale per token", "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": "indexer_decode_bf16_kernel", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None, "algorithmic_bytes": idx_bytes, "avg_us": round(idx_us, 3)},
+        "layer": {"algorithmic_bytes": step_bytes, "achieved_GBs": round(step_gbs, 1),
+                  "frac": round(step_gbs / HBM_PEAK_GBS, 4), "kernel_us": {k: round(v, 3) for k, v in k_us.items()},
+                  "launch_gaps_us": round(ms * 1e3 - sum(k_us.values()), 3)},
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = pooled_cpu_baseline(inp, cfg, npool, positions)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -277,6 +389,8 @@ def main() -> int:
         return copy_probe(args.copy_probe)
     if args.config == 5:
         return prefill_main(args)
+    if args.config == 6:
+        return pooled_main(args)
 
     import torch
 

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define DSA_ABI_VERSION 2
+#define DSA_ABI_VERSION 3
 
 #define DSA_OK 0
 #define DSA_EINVAL (-1)      /* a null pointer or a size out of range */
@@ -183,6 +183,31 @@ int dsa_decode_layer(const void* q_idx_bf16, const float* w, const uint8_t* k_fp
                      int num_pages, int score_stride, int max_len, int keep, float scale, int splits, void* stream);
 
 /*
+ * The pooled (GLM, kpool kp > 1) DSA decode layer step, enqueued back to back on one stream (the decode batch of
+ * trnrt/models/mla.py:505-526 `attention_long`, scoring the pool-key cache's page rows in place as
+ * trnrt/models/mla.py:615-630 does): the pooled indexer over the complete pools p < npool[b] of the bf16 pool-key
+ * cache -> the exact top-keep pools -> sparse MLA over the kp tokens of each selected pool and the tail tokens
+ * kp npool .. positions[b] of the row's incomplete pool (trnrt/models/dsa_long.py:189-223).
+ *   q_idx bf16 [B, Hi, 128]; w fp32 [B, Hi] (head weights with 128 ** -0.5 folded in); pool_key bf16
+ *   [num_pages page_size, 128 / kp] (pool j of page g at page row g, pool (j mod page_size / kp)); q bf16 [B, H, Dqk];
+ *   kv e4m3fn [num_pages page_size, Dqk] with kv_scale fp32 per token; page_table int32 [B, max_pages]; npool int32
+ *   [B] = (positions + 1) / kp; positions int32 [B]. Outputs: scores fp32 [B, max_pages page_size / kp], pools int32
+ *   [B, keep] (ascending, 0 past cnt), cnt int32 [B], out bf16 [B, H, 512], lse fp32 [B, H] (or null).
+ *   workspace: dsa_pooled_workspace_bytes(B, H, keep, max_pages page_size / kp, kp, splits) bytes, zero-filled
+ *   before first use (calls leave the regions that must start at zero at zero). kp a power of two in [2, 8] dividing
+ *   page_size; Hi <= 64; H a multiple of 16; Dqk 512 or 576.
+ */
+int dsa_pooled_decode_layer(const void* q_idx_bf16, const float* w, const void* pool_key_bf16, const void* q_bf16,
+                            const uint8_t* kv_fp8, const float* kv_scale, const int32_t* page_table,
+                            const int32_t* npool, const int32_t* positions, float* scores, int32_t* pools,
+                            int32_t* cnt, void* out_bf16, float* lse, void* workspace, size_t workspace_bytes, int B,
+                            int Hi, int H, int Dqk, int max_pages, int page_size, int num_pages, int kp, int keep,
+                            float scale, int splits, void* stream);
+
+/* Bytes of workspace dsa_pooled_decode_layer needs (max_len: the most pools a row scores). */
+size_t dsa_pooled_workspace_bytes(int B, int H, int keep, int max_len, int kp, int splits);
+
+/*
  * Quantise-on-write of n_rows rows into a paged FP8 cache, the cache-store step before the path (replaces
  * trnrt/models/decoder.py:481-486 `_store`, which trnrt/models/mla.py:445-446 calls for the latent rows and the
  * indexer-key rows at slot_mapping):
@@ -203,16 +228,18 @@ int dsa_cache_write(const void* x, int x_fp32, const int64_t* slots, uint8_t* ca
 /*
  * GLM's pooled indexer keys, written with the cache (replaces trnrt/models/mla.py:1277-1296 `write_pool_keys`, with
  * trnrt/models/glm5_next.py:151-160 `pool_keys` and the slots of mla.py:1262-1274 `_pool_key_slots`): for each of
- * n_rows written tokens, the pool of kp tokens it belongs to (positions first .. first + kp - 1, first = pos - pos % kp,
- * their slots through the token's page table) gets the key
+ * n_rows written tokens, the pool of kp tokens it belongs to (positions first .. first + kp - 1, first = pos - pos % kp)
+ * gets the key
  *   pk[d] = bf16(sum_t bf16(bf16(softmax_t(g_t[d] + ape[t, d])) * k_t[d])),  d < 128  (softmax over the pool in fp32)
  * from the pool's cached indexer rows [key k (128) | gate logits g (128)], written as kp pieces of 128 / kp values,
  * piece i into the slot of the pool's i-th token. A padded row (slot_mapping < page_size: the null page) reads and
- * writes its own slot only.
+ * writes its own slot only. A pool lies inside one page (kp divides page_size), so the slots of its tokens, which the
+ * reference looks up through the page table, are slot_mapping[row] - pos % kp + t: page_table (int32 [n_rows,
+ * table_pages] or one shared [table_pages], table_shared = 1) is taken for the reference's signature, may be null,
+ * and is not read.
  *   rows [num_slots, rows_width]: e4m3fn (rows_fp8 = 1; with rows_scale fp32 [num_slots] the per-token scale, or null
  *   for the reference's unscaled cache; read as bf16 values) or bf16; ape fp32 [kp, 128]; positions int32 [n_rows];
- *   page_table int32 [n_rows, table_pages] or one shared [table_pages] (table_shared = 1); slot_mapping int64
- *   [n_rows]; pool_key bf16 [num_slots, 128 / kp]. kp a power of two <= 8 dividing page_size; rows_width >= 256.
+ *   slot_mapping int64 [n_rows]; pool_key bf16 [num_slots, 128 / kp]. kp a power of two <= 8 dividing page_size; rows_width >= 256.
  */
 int dsa_pool_keys_write(const void* rows, int rows_fp8, const float* rows_scale, int rows_width, const float* ape,
                         const int32_t* positions, const int32_t* page_table, int table_shared, int table_pages,

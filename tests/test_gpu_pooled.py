@@ -157,3 +157,96 @@ def test_pooled_attention_glm_latent_width(dqk):
     tok = (rows.cpu().unsqueeze(-1) * kp + torch.arange(kp)).reshape(B, -1)
     ref, _ = O.sparse_mla_slots_ref(q, kv, ks, tok, bias.cpu().reshape(B, -1), 192 ** -0.5)
     assert_attention_close(o, ref)
+
+
+def test_glm_pooled_decode_step_end_to_end():
+    """One GLM-5.3-Flash pooled decode batch (64 heads over the 512-wide NoPE latent, a 32-head indexer over pool keys
+    of kpool 4, top 2048 tokens = 512 pools plus the tail) through dsa_long.decode_pooled, every stage against the
+    oracle on the stage's own GPU inputs: the written pool keys, the pool scores (<= 1e-2 per row), the selection
+    (bit-exact), the slots with the tail pool (bit-exact), the attention (2e-2)."""
+    cfg = W.PooledConfig("glm-e2e", B=5, L=4096)
+    say(f"GLM pooled decode step B={cfg.B} L={cfg.L} keep={cfg.keep}")
+    inp = W.make_pooled_inputs(cfg, seed=21, device="cuda")
+    kp, ps, ppp = cfg.kp, cfg.page_size, cfg.page_size // cfg.kp
+    # a full context, a tail of one token, one of three, fewer complete pools than keep, no complete pool at all
+    positions = torch.tensor([4095, 3000, 2050, 1500, 2], dtype=torch.int32)
+    o, (sc, pools, cnt, rows, bias) = dsa_long.decode_pooled(
+        inp.q_idx, inp.w, inp.pool_key, inp.q, inp.kv_cache, inp.kv_scale, positions.cuda(), inp.table, ps, kp,
+        cfg.topk, 1.0, cfg.scale, parts=True)
+    torch.cuda.synchronize()
+    c = inp.to("cpu")
+    npool = torch.div(positions.long() + 1, kp, rounding_mode="floor")
+
+    # pool keys: every token of every sequence written by the kernel
+    pos = torch.arange(cfg.L).repeat(cfg.B)
+    tb = c.table.repeat_interleave(cfg.L, dim=0)
+    sm = tb.long().gather(1, (pos // ps).view(-1, 1)).view(-1) * ps + pos % ps
+    want_pk = O.write_pool_keys_ref(torch.zeros_like(c.pool_key), c.rows, c.rows_scale, pos, tb, sm, c.ape, ps, kp)
+    got_pk, ref_pk = c.pool_key[ps:].float(), want_pk[ps:].float()
+    exact = (got_pk == ref_pk).float().mean().item()
+    rel = ((got_pk - ref_pk).abs() / ref_pk.abs().clamp(min=1e-20)).max().item()
+    say(f"  pool keys: exact fraction {exact:.5f}, max rel {rel:.3e}")
+    assert exact >= 0.99 and rel <= 2 ** -6
+
+    # scores of the complete pools over the written pool keys
+    keys = c.pool_key.view(-1, 128)
+    ref = O.indexer_ref(c.q_idx, c.w, keys, torch.ones(keys.shape[0]), c.table, npool, ppp, stride=sc.shape[1])
+    live = ref > -1e29
+    from tests._helpers import row_rel_err
+    err = row_rel_err(sc.cpu(), ref, live)
+    say(f"  pool scores rel err {err:.3e}")
+    assert err <= 1e-2
+    assert torch.equal(sc.cpu() < -1e29, ~live)
+
+    # the exact top 512 of the GPU's scores
+    want_p, want_c = O.topk_ref(sc.cpu(), cfg.keep)
+    assert torch.equal(cnt.cpu(), want_c) and torch.equal(pools.cpu(), want_p)
+    assert cnt.cpu().tolist() == [512, 512, 512, 375, 0]
+
+    # slots: the selected pools, then the tail pool
+    want_r, want_b = O.pool_slots_ref(pools.cpu(), cnt.cpu(), npool, positions.long(), c.table, ps, kp, cfg.keep + 1)
+    assert torch.equal(rows.cpu(), want_r) and torch.equal(bias.cpu(), want_b)
+    tail_live = (bias.cpu()[:, cfg.keep] == 0).sum(-1).tolist()
+    assert tail_live == [0, 1, 3, 1, 3]
+
+    # absorbed MLA over the slots' tokens
+    tok = (rows.cpu().unsqueeze(-1) * kp + torch.arange(kp)).reshape(cfg.B, -1)
+    want_o, _ = O.sparse_mla_slots_ref(c.q, c.kv_cache, c.kv_scale, tok, bias.cpu().reshape(cfg.B, -1), cfg.scale)
+    assert_attention_close(o, want_o)
+
+
+@pytest.mark.parametrize("dqk", [512, 576])
+def test_pooled_decode_layer_matches_composition_and_oracle(dqk):
+    """The one-call pooled layer (dsa_pooled_decode_layer: the indexer with the fused first-level histogram, the
+    top-k, attention over the selected pools' tokens and the tail read straight from the pool indices) against the
+    reference-flow composition (dsa_long.decode_pooled: scores, select, slots, attend) and the oracle."""
+    from trnrt_amd.kernels.dsa_layer import PooledDecodeLayer
+    cfg = W.PooledConfig("glm-layer", B=6, L=4096, dqk=dqk)
+    say(f"pooled layer dqk={dqk} B={cfg.B} L={cfg.L}")
+    inp = W.make_pooled_inputs(cfg, seed=30 + dqk, device="cuda")
+    kp, ps = cfg.kp, cfg.page_size
+    positions = torch.tensor([4095, 4094, 3001, 2050, 700, 1], dtype=torch.int32)
+    npool = torch.div(positions + 1, kp, rounding_mode="floor").to(torch.int32)
+    layer = PooledDecodeLayer(cfg.B, cfg.Hi, cfg.H, dqk, inp.table.shape[1], ps, inp.pool_key.shape[0] // ps, kp,
+                              cfg.keep, cfg.scale)
+    out, lse = layer.step(inp.q_idx, inp.w, inp.pool_key, inp.q, inp.kv_cache, inp.kv_scale, inp.table, npool.cuda(),
+                          positions.cuda())
+    o_ref, (sc, pools, cnt, rows, bias) = dsa_long.decode_pooled(
+        inp.q_idx, inp.w, inp.pool_key, inp.q, inp.kv_cache, inp.kv_scale, positions.cuda(), inp.table, ps, kp,
+        cfg.topk, 1.0, cfg.scale, parts=True)
+    torch.cuda.synchronize()
+    assert torch.equal(layer.scores, sc)
+    assert torch.equal(layer.cnt.long(), cnt) and torch.equal(layer.pools.long(), pools)
+    c = inp.to("cpu")
+    tok = (rows.cpu().unsqueeze(-1) * kp + torch.arange(kp)).reshape(cfg.B, -1)
+    want_o, want_lse = O.sparse_mla_slots_ref(c.q, c.kv_cache, c.kv_scale, tok, bias.cpu().reshape(cfg.B, -1),
+                                              cfg.scale)
+    assert_attention_close(out.float(), want_o)
+    assert_attention_close(o_ref, want_o)
+    assert torch.allclose(lse.cpu(), want_lse, atol=2e-3, rtol=1e-4)
+    # a second step with the histogram region left at zero by the first
+    out1 = out.clone()
+    out2, _ = layer.step(inp.q_idx, inp.w, inp.pool_key, inp.q, inp.kv_cache, inp.kv_scale, inp.table, npool.cuda(),
+                         positions.cuda())
+    torch.cuda.synchronize()
+    assert torch.equal(layer.pools.long(), pools) and torch.equal(out2, out1)

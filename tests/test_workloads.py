@@ -43,3 +43,22 @@ def test_algorithmic_bytes_of_config2():
     assert W.algorithmic_bytes([32768] * 8, 64, 64) == 45_369_344
     assert W.algorithmic_bytes([4096], 16, 16) == 1_767_744
     assert W.algorithmic_bytes([1 << 20] * 4, 64, 64) == 559_285_248
+
+
+def test_pooled_config_is_glm53_flash():
+    cfg = W.POOLED_CONFIGS[6]
+    assert (cfg.B, cfg.L, cfg.H, cfg.Hi, cfg.kp, cfg.topk, cfg.dqk) == (8, 32768, 64, 32, 4, 2048, 512)
+    assert cfg.keep == 512 and cfg.scale == 1 / 16
+    small = W.PooledConfig("t", B=2, L=256)
+    inp = W.make_pooled_inputs(small, seed=3)
+    assert inp.rows.shape == (576, 256) and inp.kv_cache.shape == (576, 512) and inp.pool_key.shape == (576, 32)
+    assert inp.table.shape == (2, 4) and sorted(inp.table.view(-1).tolist()) == list(range(1, 9))
+    assert inp.positions.tolist() == [255, 255]
+
+
+def test_pooled_bytes_of_config6():
+    cfg = W.POOLED_CONFIGS[6]
+    # per row: 8,192 pool keys x 256 B + 512 table entries + 32 bf16 queries of 128 + 32 fp32 weights
+    assert W.pooled_indexer_bytes(cfg, [8192] * 8) == 8 * 2_107_520
+    # + the pool-key write, the 64 x 512 bf16 queries, 2,048 tokens x 516 B, the fp32 output
+    assert W.pooled_step_bytes(cfg, [8192] * 8, [2048] * 8) == 8 * (2_107_520 + 1_254_672)

@@ -22,7 +22,7 @@ hipError_t launch_pool_slots(const int* pools, const int* cnt, const int* npool,
                              const int* table, int table_shared, int* rows, float* bias, int N, int keep, int n_slots,
                              int table_pages, int page_size, int kp, hipStream_t s);
 hipError_t launch_indexer_decode_bf16(const uint16_t* q, const float* w, const uint16_t* k, const int* table,
-                                      const int* ctx_len, const float* cand, float* scores, int B, int Hi,
+                                      const int* ctx_len, const float* cand, float* scores, int* hist, int B, int Hi,
                                       int max_pages, int page_size, int num_pages, int stride, hipStream_t s);
 hipError_t launch_pool_keys(const void* rows, int rows_fp8, const float* rows_scale, int rows_width, const float* ape,
                             const int* positions, const int* table, int table_shared, int table_pages,
@@ -39,7 +39,7 @@ bool topk_supported(int max_len, int keep, int vis_only);
 hipError_t launch_sparse_mla(const uint16_t* q, const uint8_t* kv, const float* kvs, const int* idx, const int* cnt,
                              const int* table, const int* rows, const float* bias, uint16_t* out, float* out_f32,
                              float* lse, void* ws, int B, int H, int Dqk, int keep, int max_pages, int page_size,
-                             int num_pages, float scale, int splits, hipStream_t s);
+                             int num_pages, float scale, int splits, hipStream_t s, PoolForm pf = PoolForm{});
 hipError_t launch_token_rows(const int* idx, const int* cnt, const int* table, int* rows, float* bias, int B,
                              int keep, int max_pages, int page_size, int num_pages, hipStream_t s);
 int attention_default_splits(int B, int H, int keep, int num_cu);
@@ -147,7 +147,7 @@ int dsa_indexer_decode_bf16(const void* q_bf16, const float* w, const void* k_bf
   if (B == 0 || score_stride == 0) return DSA_OK;
   return status(dsa::launch_indexer_decode_bf16(static_cast<const uint16_t*>(q_bf16), w,
                                                 static_cast<const uint16_t*>(k_bf16), page_table, ctx_len, cand,
-                                                scores, B, Hi, max_pages, page_size, num_pages, score_stride,
+                                                scores, nullptr, B, Hi, max_pages, page_size, num_pages, score_stride,
                                                 static_cast<hipStream_t>(stream)));
 }
 
@@ -187,7 +187,7 @@ int dsa_pool_keys_write(const void* rows, int rows_fp8, const float* rows_scale,
                         const int32_t* positions, const int32_t* page_table, int table_shared, int table_pages,
                         const int64_t* slot_mapping, void* pool_key, int n_rows, int kp, int page_size,
                         long long num_slots, void* stream) {
-  if (!rows || !ape || !positions || !page_table || !slot_mapping || !pool_key) return DSA_EINVAL;
+  if (!rows || !ape || !positions || !slot_mapping || !pool_key) return DSA_EINVAL;
   if (n_rows < 0 || table_pages < 1 || page_size < 1 || num_slots < 1 || rows_width < 256) return DSA_EINVAL;
   if (kp < 1 || kp > 8 || (kp & (kp - 1)) || page_size % kp) return DSA_EUNSUPPORTED;
   if (n_rows == 0) return DSA_OK;
@@ -332,6 +332,53 @@ int dsa_decode_layer(const void* q_idx_bf16, const float* w, const uint8_t* k_fp
   return status(dsa::launch_sparse_mla(static_cast<const uint16_t*>(q_bf16), kv_fp8, kv_scale, nullptr, cnt, nullptr,
                                        rows, nullptr, static_cast<uint16_t*>(out_bf16), nullptr, lse, aws, B, H, 576,
                                        keep, max_pages, page_size, num_pages, scale, sp, s));
+}
+
+size_t dsa_pooled_workspace_bytes(int B, int H, int keep, int max_len, int kp, int splits) {
+  if (B < 0 || H < 16 || keep < 1 || max_len < 1 || kp < 2) return 0;
+  const int keep_tok = kp * (keep + 1);
+  const int sp = effective_splits(resolve_splits(splits, B, H, keep_tok), keep_tok);
+  return align256(dsa::topk_workspace_bytes(B, max_len, keep)) + align256(dsa::attention_workspace_bytes(B, H, sp));
+}
+
+int dsa_pooled_decode_layer(const void* q_idx_bf16, const float* w, const void* pool_key_bf16, const void* q_bf16,
+                            const uint8_t* kv_fp8, const float* kv_scale, const int32_t* page_table,
+                            const int32_t* npool, const int32_t* positions, float* scores, int32_t* pools,
+                            int32_t* cnt, void* out_bf16, float* lse, void* workspace, size_t workspace_bytes, int B,
+                            int Hi, int H, int Dqk, int max_pages, int page_size, int num_pages, int kp, int keep,
+                            float scale, int splits, void* stream) {
+  if (!q_idx_bf16 || !w || !pool_key_bf16 || !q_bf16 || !kv_fp8 || !kv_scale || !page_table || !npool ||
+      !positions || !scores || !pools || !cnt || !out_bf16 || !workspace)
+    return DSA_EINVAL;
+  if (B < 0 || Hi < 1 || H < 1 || max_pages < 1 || page_size < 1 || num_pages < 1 || keep < 1) return DSA_EINVAL;
+  if (kp < 2 || kp > 8 || (kp & (kp - 1)) || page_size % kp) return DSA_EUNSUPPORTED;
+  const int ppp = page_size / kp;  // pools per page
+  const long stride_l = (long)max_pages * ppp;
+  if (stride_l > 0x7fffffffL || (long)num_pages * page_size > 0x7fffffffL) return DSA_EUNSUPPORTED;
+  const int stride = (int)stride_l;
+  if (Hi > 64 || H % 16 || (Dqk != 512 && Dqk != 576)) return DSA_EUNSUPPORTED;
+  if (!dsa::topk_supported(stride, keep, 1)) return DSA_EUNSUPPORTED;
+  if (workspace_bytes < dsa_pooled_workspace_bytes(B, H, keep, stride, kp, splits)) return DSA_EWORKSPACE;
+  if (B == 0) return DSA_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const size_t t_need = align256(dsa::topk_workspace_bytes(B, stride, keep));
+  // flat rows: the indexer accumulates the top-k's first-level histogram (the workspace's first region)
+  const bool fused_hist = stride <= 32 * 1024;
+  hipError_t e = dsa::launch_indexer_decode_bf16(static_cast<const uint16_t*>(q_idx_bf16), w,
+                                                 static_cast<const uint16_t*>(pool_key_bf16), page_table, npool,
+                                                 nullptr, scores, fused_hist ? static_cast<int*>(workspace) : nullptr,
+                                                 B, Hi, max_pages, ppp, num_pages, stride, s);
+  if (e != hipSuccess) return DSA_ELAUNCH;
+  e = dsa::launch_topk(scores, npool, pools, cnt, workspace, B, stride, stride, keep, 1, fused_hist, nullptr, 0, 0, 0,
+                       nullptr, s);
+  if (e != hipSuccess) return DSA_ELAUNCH;
+  const int keep_tok = kp * (keep + 1);
+  const int sp = effective_splits(resolve_splits(splits, B, H, keep_tok), keep_tok);
+  const dsa::PoolForm pf = {__builtin_ctz((unsigned)kp), keep, npool, positions};
+  return status(dsa::launch_sparse_mla(static_cast<const uint16_t*>(q_bf16), kv_fp8, kv_scale, pools, cnt, page_table,
+                                       nullptr, nullptr, static_cast<uint16_t*>(out_bf16), nullptr, lse,
+                                       static_cast<char*>(workspace) + t_need, B, H, Dqk, keep_tok, max_pages,
+                                       page_size, num_pages, scale, sp, s, pf));
 }
 
 }  // extern "C"

@@ -67,7 +67,11 @@ __device__ __forceinline__ bf16x8 value_operand(const uint8_t* kt, int ks, int n
 }
 
 // Slot forms: token (idx + cnt + table: positions through the page table, bias 0 below cnt), rows + bias (cache
-// slots with an additive bias), rows + cnt (cache slots, bias 0 below cnt).
+// slots with an additive bias), rows + cnt (cache slots, bias 0 below cnt). The token form's pooled variant (pf.kp_shift
+// > 0, kpool = 1 << kp_shift): idx [B, pf.idx_stride] selected pools, cnt their count; the row attends the kpool
+// tokens of each selected pool and then the tail: tokens kpool npool .. pos of its incomplete pool npool (none when
+// pos + 1 is a multiple of kpool), token slot k = pool slot k >> kp_shift, token k & (kpool - 1) of that pool -- the
+// slots of trnrt/models/dsa_long.py:189-215 in the same order, with the masked ones left out.
 template <int DQK>
 __global__ __launch_bounds__(ATT_THREADS, 1) void sparse_mla_kernel(
     const uint16_t* __restrict__ q, const uint8_t* __restrict__ kv, const float* __restrict__ kvs,
@@ -75,7 +79,7 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void sparse_mla_kernel(
     const int* __restrict__ rows, const float* __restrict__ bias, uint16_t* __restrict__ out,
     float* __restrict__ out_f32, float* __restrict__ lse_out, float* __restrict__ ws_o, float* __restrict__ ws_ml,
     int B, int H, int keep, int max_pages, int page_size, int num_pages, float scale, int splits,
-    int slots_per_split) {
+    int slots_per_split, PoolForm pf) {
   constexpr int ATT_PIECES = DQK / 16;  // 16-byte data pieces per row
   constexpr int ATT_QROW = DQK + 8;     // staged query row stride (bf16 elements)
   constexpr int STEPS = DQK / 32;       // score steps of 32 dims
@@ -98,8 +102,16 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void sparse_mla_kernel(
   const bool token_form = rows == nullptr;
   int n_eff = keep;
   int cnt_b = keep;
+  int pools_b = 0, tail_pool = 0;  // pooled form: selected pools, the tail pool
   if (cnt) {
     cnt_b = cnt[b];
+    if (pf.kp_shift) {
+      // token slots: kpool per selected pool, then the tail's tokens
+      pools_b = min(max(cnt_b, 0), pf.idx_stride);
+      tail_pool = max(pf.npool[b], 0);
+      const int tail = min(max(pf.positions[b] + 1 - (tail_pool << pf.kp_shift), 0), (1 << pf.kp_shift) - 1);
+      cnt_b = (pools_b << pf.kp_shift) + tail;
+    }
     if (!bias) n_eff = cnt_b < 1 ? 1 : (cnt_b > keep ? keep : cnt_b);  // cnt 0: attend slot 0, fully masked
   }
   const int k_begin = sp * slots_per_split;
@@ -130,7 +142,14 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void sparse_mla_kernel(
       int slot;
       float bs;
       if (token_form) {
-        int pos = idx[(size_t)b * keep + k];
+        int pos;
+        if (pf.kp_shift) {
+          const int j = k >> pf.kp_shift;
+          const int pool = j < pools_b ? idx[(size_t)b * pf.idx_stride + j] : tail_pool;
+          pos = (pool << pf.kp_shift) + (k & ((1 << pf.kp_shift) - 1));
+        } else {
+          pos = idx[(size_t)b * keep + k];
+        }
         pos = pos < 0 ? 0 : pos;
         int pi = pos / page_size;
         pi = pi < max_pages ? pi : max_pages - 1;
@@ -461,7 +480,7 @@ size_t attention_workspace_bytes(int B, int H, int splits) {
 hipError_t launch_sparse_mla(const uint16_t* q, const uint8_t* kv, const float* kvs, const int* idx, const int* cnt,
                              const int* table, const int* rows, const float* bias, uint16_t* out, float* out_f32,
                              float* lse, void* ws, int B, int H, int Dqk, int keep, int max_pages, int page_size,
-                             int num_pages, float scale, int splits, hipStream_t s) {
+                             int num_pages, float scale, int splits, hipStream_t s, PoolForm pf) {
   const int HG = H / ATT_HPW;
   // slots per split: a whole number of chunks
   int sps = (keep + splits - 1) / splits;
@@ -479,10 +498,10 @@ hipError_t launch_sparse_mla(const uint16_t* q, const uint8_t* kv, const float* 
       Dqk == 512
           ? launch("sparse_mla_kernel", sparse_mla_kernel<512>, dim3(grid), dim3(ATT_THREADS), s, q, kv, kvs, idx, cnt,
                    table, rows, bias, out, out_f32, lse, ws_o, ws_ml, B, H, keep, max_pages, page_size, num_pages,
-                   scale, eff_splits, sps)
+                   scale, eff_splits, sps, pf)
           : launch("sparse_mla_kernel", sparse_mla_kernel<576>, dim3(grid), dim3(ATT_THREADS), s, q, kv, kvs, idx, cnt,
                    table, rows, bias, out, out_f32, lse, ws_o, ws_ml, B, H, keep, max_pages, page_size, num_pages,
-                   scale, eff_splits, sps);
+                   scale, eff_splits, sps, pf);
   if (e != hipSuccess || eff_splits == 1) return e;
   if (eff_splits <= 8)
     return launch("combine_splits_kernel", combine_splits_kernel<8>, dim3(B * H), dim3(128), s, ws_o, ws_ml, H,

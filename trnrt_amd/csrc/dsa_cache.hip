@@ -127,14 +127,15 @@ __global__ __launch_bounds__(CW_WAVES * WAVE) void pool_keys_kernel(
   const long own = slot_mapping[row];
   const bool real = own >= page_size;
   const int pos = positions[row];
-  const int first = pos - pos % kp;
-  const int* tab = table + (table_shared ? 0 : (size_t)row * table_pages);
+  // a pool never straddles a page (page_size % kp == 0), so its tokens' slots (table[p / page_size] page_size +
+  // p % page_size for p = pos - pos % kp + t, trnrt/models/mla.py:1262-1274) are the written row's own slot's
+  // neighbours: own - pos % kp + t. No dependent table read.
+  (void)table, (void)table_shared, (void)table_pages;
+  const int off = pos - (pos / kp) * kp;
   long slot[PK_MAXKP];
 #pragma unroll
   for (int t = 0; t < PK_MAXKP; ++t) {
-    const int p = first + min(t, kp - 1);
-    const long sl = (long)tab[min(max(p / page_size, 0), table_pages - 1)] * page_size + p % page_size;
-    slot[t] = real ? sl : own;
+    slot[t] = real ? own - off + min(t, kp - 1) : own;
     slot[t] = min(max(slot[t], 0L), num_slots - 1);  // in range whatever the inputs
   }
   // this lane's two channels d = 2 lane, 2 lane + 1 of every token of the pool: key and gate logit

@@ -53,6 +53,15 @@ constexpr float NEG_INF = -1e30f;   // trnrt/models/decoder.py NEG_INF
 // The top-k's first-level histogram of a row: 4096 bins (the top 12 bits of the order key), kept in HIST_REPLICAS
 // copies that the indexer's workgroups fill in turn (fewer atomics on the same address); readers sum the copies.
 constexpr int HIST_BINS = 4096;
+
+// The attention's pooled token form (kpool = 1 << kp_shift > 1; kp_shift 0: the per-token forms): idx holds
+// idx_stride selected pools per row, npool [B] each row's complete pools (its tail pool), positions [B] its position.
+struct PoolForm {
+  int kp_shift;
+  int idx_stride;
+  const int* npool;
+  const int* positions;
+};
 constexpr int HIST_REPLICAS = 1;
 constexpr float VISIBLE = -5e29f;   // trnrt/kernels/dsa_topk.py:58: scores at or below are not selectable
 constexpr int WAVE = 64;

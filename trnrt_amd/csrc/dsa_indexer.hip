@@ -213,14 +213,20 @@ hipError_t launch_indexer_decode(const uint16_t* q, const float* w, const uint8_
 //
 // Same wave layout as above (lane (j, h): key j of the tile, dims 64h .. 64h + 63, here 128 bytes of bf16 fed to
 // the MFMA as they are), but every lane looks up its own key's page, so a 32-key tile may span pages: one round of
-// page-id loads, then one round of key loads, as above.
-template <int MT, bool CAND>
+// page-id loads, then one round of key loads, as above. A key is 256 bytes here against 132 there, so a wave takes
+// BF_TPW tiles (half as many): the same bytes in flight per lane and twice the workgroups over a row.
+constexpr int BF_TPW = 2;
+constexpr int BF_TPG = BF_TPW * IDX_WAVES;
+
+template <int MT, bool HIST, bool CAND>
 __global__ __launch_bounds__(IDX_THREADS, 2) void indexer_decode_bf16_kernel(
     const uint16_t* __restrict__ q, const float* __restrict__ w, const uint16_t* __restrict__ kcache,
     const int* __restrict__ table, const int* __restrict__ ctx_len, const float* __restrict__ cand,
-    float* __restrict__ scores, int Hi, int max_pages, int page_size, int num_pages, int stride, int groups_per_row) {
+    float* __restrict__ scores, int* __restrict__ hist, int Hi, int max_pages, int page_size, int num_pages,
+    int stride, int groups_per_row) {
   __shared__ uint16_t qs[32 * MT * IDX_QROW];
   __shared__ float ws[32 * MT];
+  __shared__ int hs[HIST ? IDX_HBINS : 1];  // the workgroup's share of the row's top-k histogram
   const int b = blockIdx.x / groups_per_row;
   const int grp = blockIdx.x - b * groups_per_row;
   const int wave = threadIdx.x / WAVE;
@@ -230,7 +236,7 @@ __global__ __launch_bounds__(IDX_THREADS, 2) void indexer_decode_bf16_kernel(
   const int tiles_row = (stride + IDX_TILE - 1) / IDX_TILE;
   int L = stride;
   if (ctx_len) L = min(max(ctx_len[b], 0), stride);
-  const int t_begin = grp * IDX_TPG + wave * IDX_TPW;
+  const int t_begin = grp * BF_TPG + wave * BF_TPW;
   const int* trow = table + (size_t)b * max_pages;
   float* srow = scores + (size_t)b * stride;
 
@@ -245,17 +251,17 @@ __global__ __launch_bounds__(IDX_THREADS, 2) void indexer_decode_bf16_kernel(
   const float wv = w[(size_t)b * Hi + min((int)threadIdx.x, Hi - 1)];
 
   // this lane's key in each of its tiles: its page (the null page past the context), then its 128 bytes
-  int page[IDX_TPW];
+  int page[BF_TPW];
 #pragma unroll
-  for (int i = 0; i < IDX_TPW; ++i) {
+  for (int i = 0; i < BF_TPW; ++i) {
     const int p = (t_begin + i) * IDX_TILE + j;
     const int pg = trow[min(p / page_size, max_pages - 1)];
     page[i] = p < L ? safe_page(pg, num_pages) : 0;
   }
-  uint4 kv[IDX_TPW][8];
-  float kc[IDX_TPW];
+  uint4 kv[BF_TPW][8];
+  float kc[BF_TPW];
 #pragma unroll
-  for (int i = 0; i < IDX_TPW; ++i) {
+  for (int i = 0; i < BF_TPW; ++i) {
     const int p = (t_begin + i) * IDX_TILE + j;
     const size_t slot = (size_t)page[i] * page_size + (p < L ? p % page_size : 0);
     const uint16_t* kp = kcache + slot * IDX_D + 64 * h;
@@ -271,6 +277,8 @@ __global__ __launch_bounds__(IDX_THREADS, 2) void indexer_decode_bf16_kernel(
     *reinterpret_cast<uint4*>(&qs[head * IDX_QROW + 8 * c]) = head < Hi ? qv[r] : make_uint4(0, 0, 0, 0);
   }
   if (threadIdx.x < 32 * MT) ws[threadIdx.x] = (int)threadIdx.x < Hi ? wv : 0.0f;
+  if (HIST)
+    for (int i = threadIdx.x; i < IDX_HBINS; i += IDX_THREADS) hs[i] = 0;
   __syncthreads();
   bf16x8 qa[MT][8];
 #pragma unroll
@@ -285,7 +293,7 @@ __global__ __launch_bounds__(IDX_THREADS, 2) void indexer_decode_bf16_kernel(
     for (int r = 0; r < 16; ++r) wr[m][r] = ws[32 * m + 8 * (r >> 2) + 4 * h + (r & 3)];
 
 #pragma unroll
-  for (int i = 0; i < IDX_TPW; ++i) {
+  for (int i = 0; i < BF_TPW; ++i) {
     const int t = t_begin + i;
     const int pos = t * IDX_TILE + j;
     f32x16 acc[MT];
@@ -306,34 +314,61 @@ __global__ __launch_bounds__(IDX_THREADS, 2) void indexer_decode_bf16_kernel(
     part += __shfl_xor(part, 32, WAVE);
     float v = CAND ? part + kc[i] : part;
     if (pos >= L) v = NEG_INF;
-    if (t < tiles_row && h == 0 && pos < stride) srow[pos] = v;
+    if (t < tiles_row && h == 0 && pos < stride) {
+      srow[pos] = v;
+      if (HIST && v > VISIBLE) atomicAdd(&hs[order_key(v) >> IDX_HSHIFT], 1);
+    }
+  }
+  if (HIST) {
+    __syncthreads();
+    int* hrow = hist + ((size_t)b * HIST_REPLICAS + grp % HIST_REPLICAS) * IDX_HBINS;
+    for (int i = threadIdx.x; i < IDX_HBINS; i += IDX_THREADS) {
+      const int c = hs[i];
+      if (c) atomicAdd(&hrow[i], c);
+    }
   }
 }
 
-template <int MT, bool CAND>
+template <int MT, bool HIST, bool CAND>
 static hipError_t launch_indexer_bf16_variant(const uint16_t* q, const float* w, const uint16_t* k, const int* table,
-                                              const int* ctx_len, const float* cand, float* scores, int B, int Hi,
-                                              int max_pages, int page_size, int num_pages, int stride,
+                                              const int* ctx_len, const float* cand, float* scores, int* hist, int B,
+                                              int Hi, int max_pages, int page_size, int num_pages, int stride,
                                               hipStream_t stream) {
   const int tiles_row = (stride + IDX_TILE - 1) / IDX_TILE;
-  const int groups_row = (tiles_row + IDX_TPG - 1) / IDX_TPG;
-  return launch("indexer_decode_bf16_kernel", indexer_decode_bf16_kernel<MT, CAND>, dim3(B * groups_row),
-                dim3(IDX_THREADS), stream, q, w, k, table, ctx_len, cand, scores, Hi, max_pages, page_size, num_pages,
-                stride, groups_row);
+  const int groups_row = (tiles_row + BF_TPG - 1) / BF_TPG;
+  return launch("indexer_decode_bf16_kernel", indexer_decode_bf16_kernel<MT, HIST, CAND>, dim3(B * groups_row),
+                dim3(IDX_THREADS), stream, q, w, k, table, ctx_len, cand, scores, hist, Hi, max_pages, page_size,
+                num_pages, stride, groups_row);
 }
 
+template <int MT>
+static hipError_t launch_indexer_bf16_mt(const uint16_t* q, const float* w, const uint16_t* k, const int* table,
+                                         const int* ctx_len, const float* cand, float* scores, int* hist, int B,
+                                         int Hi, int max_pages, int page_size, int num_pages, int stride,
+                                         hipStream_t s) {
+  if (hist && cand)
+    return launch_indexer_bf16_variant<MT, true, true>(q, w, k, table, ctx_len, cand, scores, hist, B, Hi, max_pages,
+                                                       page_size, num_pages, stride, s);
+  if (hist)
+    return launch_indexer_bf16_variant<MT, true, false>(q, w, k, table, ctx_len, cand, scores, hist, B, Hi,
+                                                        max_pages, page_size, num_pages, stride, s);
+  if (cand)
+    return launch_indexer_bf16_variant<MT, false, true>(q, w, k, table, ctx_len, cand, scores, hist, B, Hi,
+                                                        max_pages, page_size, num_pages, stride, s);
+  return launch_indexer_bf16_variant<MT, false, false>(q, w, k, table, ctx_len, cand, scores, hist, B, Hi, max_pages,
+                                                       page_size, num_pages, stride, s);
+}
+
+// hist (or null): the rows' first-level top-k histograms, accumulated (the workspace region the top-k reads with
+// hist_ready; zero on entry).
 hipError_t launch_indexer_decode_bf16(const uint16_t* q, const float* w, const uint16_t* k, const int* table,
-                                      const int* ctx_len, const float* cand, float* scores, int B, int Hi,
+                                      const int* ctx_len, const float* cand, float* scores, int* hist, int B, int Hi,
                                       int max_pages, int page_size, int num_pages, int stride, hipStream_t s) {
   if (Hi <= 32)
-    return cand ? launch_indexer_bf16_variant<1, true>(q, w, k, table, ctx_len, cand, scores, B, Hi, max_pages,
-                                                       page_size, num_pages, stride, s)
-                : launch_indexer_bf16_variant<1, false>(q, w, k, table, ctx_len, cand, scores, B, Hi, max_pages,
-                                                        page_size, num_pages, stride, s);
-  return cand ? launch_indexer_bf16_variant<2, true>(q, w, k, table, ctx_len, cand, scores, B, Hi, max_pages,
-                                                     page_size, num_pages, stride, s)
-              : launch_indexer_bf16_variant<2, false>(q, w, k, table, ctx_len, cand, scores, B, Hi, max_pages,
-                                                      page_size, num_pages, stride, s);
+    return launch_indexer_bf16_mt<1>(q, w, k, table, ctx_len, cand, scores, hist, B, Hi, max_pages, page_size,
+                                     num_pages, stride, s);
+  return launch_indexer_bf16_mt<2>(q, w, k, table, ctx_len, cand, scores, hist, B, Hi, max_pages, page_size,
+                                   num_pages, stride, s);
 }
 
 }  // namespace dsa

@@ -3,7 +3,8 @@ trnrt/models/mla.py:506-528 `attention_long` (at kpool 1, with the q_lat / W_UV 
 
 DecodeLayer preallocates the intermediates (scores, indices, counts) and the workspace once for a batch shape, so a
 step allocates nothing and can be captured in a HIP graph; step() enqueues the three operators on the current stream
-through the C ABI's dsa_decode_layer.
+through the C ABI's dsa_decode_layer. PooledDecodeLayer is the same for GLM's pooled indexer (kpool > 1): scores of
+the bf16 pool keys, the top pools, attention over their tokens and the query's tail pool (dsa_pooled_decode_layer).
 """
 
 from __future__ import annotations
@@ -74,4 +75,71 @@ class DecodeLayer:
             self.num_pages, self.stride, self.max_len, self.keep, self.scale, self.splits,
             torch.cuda.current_stream(self.device).cuda_stream)
         _lib.check(st, "dsa_layer.step")
+        return self.out, self.lse
+
+
+class PooledDecodeLayer:
+    """Buffers and launch parameters of a pooled (GLM, kpool kp > 1) decode step over B rows with up to max_pages
+    pages each: the pooled indexer over the bf16 pool-key cache, the exact top-keep pools, sparse MLA over their
+    tokens and the tail (trnrt/models/mla.py:505-526 `attention_long` for a decode batch), enqueued by one call of the
+    C ABI's dsa_pooled_decode_layer. Nothing is allocated per step.
+
+    B, Hi (indexer heads), H (query heads), dqk (512: GLM's NoPE latent, or 576), max_pages, page_size, num_pages
+    (cache pages incl. the null page 0), kp, keep (pools: topk / kp), scale (softmax scale), splits (attention
+    split-K; 0 = chosen for the GPU)."""
+
+    def __init__(self, B: int, Hi: int, H: int, dqk: int, max_pages: int, page_size: int, num_pages: int, kp: int,
+                 keep: int, scale: float, splits: int = 0, device: torch.device | str = "cuda"):
+        self.B, self.Hi, self.H, self.dqk = B, Hi, H, dqk
+        self.max_pages, self.page_size, self.num_pages = max_pages, page_size, num_pages
+        self.kp, self.keep, self.scale, self.splits = kp, keep, float(scale), splits
+        if kp < 2 or kp & (kp - 1) or page_size % kp:
+            raise ValueError(f"PooledDecodeLayer: kpool {kp} with pages of {page_size}")
+        self.stride = max_pages * (page_size // kp)
+        dev = torch.device(device)
+        if dev.type != "cuda":
+            raise RuntimeError("trnrt_amd DSA kernels run on the GPU only (libdsa_gfx950.so)")
+        self.device = dev
+        self.scores = torch.empty(B, self.stride, dtype=torch.float32, device=dev)
+        self.pools = torch.empty(B, keep, dtype=torch.int32, device=dev)
+        self.cnt = torch.empty(B, dtype=torch.int32, device=dev)
+        self.out = torch.empty(B, H, 512, dtype=torch.bfloat16, device=dev)
+        self.lse = torch.empty(B, H, dtype=torch.float32, device=dev)
+        wsb = int(_lib.lib().dsa_pooled_workspace_bytes(B, H, keep, self.stride, kp, splits))
+        if wsb == 0:
+            raise ValueError(f"PooledDecodeLayer: no workspace size for B={B} H={H} keep={keep}")
+        # zero once: the calls keep the regions that must start at zero (the top-k histograms) at zero
+        self.workspace = torch.zeros(wsb, dtype=torch.uint8, device=dev)
+
+    def step(self, q_idx: torch.Tensor, w: torch.Tensor, pool_key: torch.Tensor, q: torch.Tensor,
+             kv_cache: torch.Tensor, kv_scale: torch.Tensor, table: torch.Tensor, npool: torch.Tensor,
+             positions: torch.Tensor, check: bool = True) -> tuple[torch.Tensor, torch.Tensor]:
+        """(out bf16 [B, H, 512], lse fp32 [B, H]); self.scores / pools / cnt hold the intermediates. q_idx
+        [B, Hi, 128] bf16, w [B, Hi] fp32 (128 ** -0.5 folded in), pool_key bf16 [slots, 128 / kp], q [B, H, dqk]
+        bf16, kv_cache [slots, dqk] e4m3fn + kv_scale [slots], table [B, max_pages] int32, npool [B] int32
+        ((positions + 1) // kp), positions [B] int32. check=False skips the Python-side checks (the C ABI still
+        checks sizes)."""
+        B, Hi, H = self.B, self.Hi, self.H
+        if check:
+            C.on_gpu(q_idx, w, pool_key, q, kv_cache, kv_scale, table, npool, positions)
+            C.need(q_idx, "q_idx", torch.bfloat16, (B, Hi, 128))
+            C.need(w, "w", torch.float32, (B, Hi))
+            C.need(q, "q", torch.bfloat16, (B, H, self.dqk))
+            C.need(table, "table", torch.int32, (B, self.max_pages))
+            C.need(npool, "npool", torch.int32, (B,))
+            C.need(positions, "positions", torch.int32, (B,))
+            C.fp8_bytes(kv_cache, "kv_cache")
+            slots = self.num_pages * self.page_size
+            C.need(pool_key, "pool_key", torch.bfloat16, (slots, 128 // self.kp))
+            if kv_cache.numel() != slots * self.dqk:
+                raise ValueError(f"kv cache of {kv_cache.numel()} bytes for {slots} slots of {self.dqk}")
+            C.need(kv_scale, "kv_scale", torch.float32, (slots,))
+        st = _lib.lib().dsa_pooled_decode_layer(
+            q_idx.data_ptr(), w.data_ptr(), pool_key.data_ptr(), q.data_ptr(), kv_cache.data_ptr(),
+            kv_scale.data_ptr(), table.data_ptr(), npool.data_ptr(), positions.data_ptr(), self.scores.data_ptr(),
+            self.pools.data_ptr(), self.cnt.data_ptr(), self.out.data_ptr(), self.lse.data_ptr(),
+            self.workspace.data_ptr(), self.workspace.numel(), B, Hi, H, self.dqk, self.max_pages, self.page_size,
+            self.num_pages, self.kp, self.keep, self.scale, self.splits,
+            torch.cuda.current_stream(self.device).cuda_stream)
+        _lib.check(st, "dsa_layer.PooledDecodeLayer.step")
         return self.out, self.lse

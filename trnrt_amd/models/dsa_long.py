@@ -1,5 +1,5 @@
-"""The per-token DSA decode path's selection, slots and attention (the functions of trnrt/models/dsa_long.py that
-the decode path calls, at kpool 1: each candidate is one token).
+"""The DSA path's scores, selection, slots and attention (the functions of trnrt/models/dsa_long.py that the decode
+and chunked-prefill paths call; a candidate is one token at kpool 1, a pool of kpool tokens above).
 
 - scores: the index scores of a prefill chunk (2-D keys, csrc/dsa_prefill.hip) or a decode batch (one context per
   row, csrc/dsa_indexer.hip) (trnrt/models/dsa_long.py:74-84);
@@ -7,7 +7,9 @@ the decode path calls, at kpool 1: each candidate is one token).
   count; count [N] int64) (trnrt/models/dsa_long.py:135-186), by the gfx950 top-k kernel;
 - slots: selected pools -> cache pool rows and the 0 / NEG_INF bias with the query's tail pool
   (trnrt/models/dsa_long.py:189-215, any kpool);
-- attend: absorbed MLA over the slots (trnrt/models/dsa_long.py:218-223).
+- attend: absorbed MLA over the slots (trnrt/models/dsa_long.py:218-223);
+- decode_pooled: a pooled (GLM) decode batch through all four over the bf16 pool-key cache
+  (trnrt/models/mla.py:505-526 `attention_long`).
 """
 
 from __future__ import annotations
@@ -97,3 +99,31 @@ def attend(q_lat: torch.Tensor, kc: torch.Tensor, rows: torch.Tensor, bias: torc
            kc_scale: torch.Tensor) -> torch.Tensor:
     """o [N, H, 512] fp32: absorbed MLA of N queries over their slots (trnrt/models/dsa_long.py:218-223)."""
     return dsa_decode.attend(q_lat, kc, rows, bias, scale, kc_scale=kc_scale)
+
+
+def decode_pooled(q_idx: torch.Tensor, w: torch.Tensor, pool_key: torch.Tensor, q_lat: torch.Tensor,
+                  kc: torch.Tensor, kc_scale: torch.Tensor, positions: torch.Tensor, table: torch.Tensor,
+                  page_size: int, kp: int, topk: int, index_scale: float, softmax_scale: float, *,
+                  parts: bool = False):
+    """One pooled decode batch's attention core after its rows and pool keys were written (trnrt/models/mla.py:505-526
+    `attention_long` for a decode batch, scoring the pool-key cache's page rows in place as trnrt/models/mla.py:
+    615-630 does): the scores of the complete pools (bf16 pool keys pool_key [slots, 128 / kp], page rows of
+    page_size / kp pools), their exact top topk / kp, the slots with the tail pool, absorbed MLA over those pools'
+    tokens. q_idx [B, Hi, 128] bf16, w [B, Hi] fp32 (the head weights, index_scale applied here), q_lat [B, H, R]
+    bf16, kc [slots, R] e4m3fn with kc_scale [slots], positions [B], table [B, pages] int32. Returns o [B, H, 512]
+    fp32, and with parts also (scores, pools, cnt, rows, bias)."""
+    B = q_idx.shape[0]
+    keep = topk // kp
+    ppp = page_size // kp
+    if kp < 2 or page_size % kp or topk % kp:
+        raise ValueError(f"decode_pooled: kpool {kp}, page_size {page_size}, topk {topk}")
+    if pool_key.dtype != torch.bfloat16 or pool_key.shape[-1] * kp != dsa_index.D:
+        raise ValueError(f"decode_pooled: pool_key {tuple(pool_key.shape)} {pool_key.dtype}, expected bf16 pieces of "
+                         f"{dsa_index.D} / {kp}")
+    npool = npools(positions, kp).to(torch.int32)
+    sc = dsa_index.scores(q_idx, w.float() * float(index_scale), pool_key.view(-1, ppp * dsa_index.D), table, None,
+                          ctx_len=npool)
+    pools, cnt = select_device(sc, keep, lengths=npool)
+    rows, bias = slots(pools, cnt, npool, positions, table, page_size, kp, keep + 1)
+    o = attend(q_lat, kc, rows, bias, softmax_scale, kc_scale=kc_scale)
+    return (o, (sc, pools, cnt, rows, bias)) if parts else o

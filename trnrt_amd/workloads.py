@@ -255,3 +255,111 @@ def make_prefill_inputs(cfg: PrefillConfig, seed: int = 0, device: str | torch.d
             inp.kv_cache[s0:s0 + n], inp.kv_scale[s0:s0 + n] = quantize_rows(
                 torch.randn(n, cfg.dqk, generator=g, device=device))
     return inp
+
+
+# -- GLM-5.3-Flash's pooled decode (the reference's own model semantics: trnrt/models/glm5_next.py) ------------------
+
+
+@dataclass(frozen=True)
+class PooledConfig:
+    """GLM-5.3-Flash's DSA decode shapes (tests/fixtures/GLM-5.3-Flash-config.json in the reference): 64 heads over a
+    512-wide NoPE latent (softmax scale qk_nope_head_dim ** -0.5 = 1/16), a 32-head indexer of dim 128 over pool keys
+    of kpool 4 tokens, top 2048 tokens = 512 pools plus the query's own incomplete pool."""
+    name: str
+    B: int
+    L: int
+    H: int = 64
+    Hi: int = 32
+    kp: int = 4
+    topk: int = 2048
+    D: int = 128
+    dqk: int = 512
+    page_size: int = 64
+
+    @property
+    def keep(self) -> int:
+        return self.topk // self.kp
+
+    @property
+    def scale(self) -> float:
+        return 256 ** -0.5  # qk_nope_head_dim ** -0.5 (GLM-5.3-Flash)
+
+
+POOLED_CONFIGS = {
+    6: PooledConfig("glm-pooled-b8-ctx32k", B=8, L=32768),
+}
+
+
+def pooled_indexer_bytes(cfg: PooledConfig, npool: list[int]) -> int:
+    """Algorithmic bytes of one pooled indexer launch: every scored pool key once (bf16, 128 x 2 B), the page-table
+    entries they span, the bf16 queries and fp32 head weights; the scores are an intermediate and are not counted."""
+    ppp = cfg.page_size // cfg.kp
+    return sum(2 * cfg.D * n + 4 * math.ceil(n / ppp) + 2 * cfg.D * cfg.Hi + 4 * cfg.Hi for n in npool)
+
+
+def pooled_step_bytes(cfg: PooledConfig, npool: list[int], tokens: list[int]) -> int:
+    """Bytes one pooled decode step must move at least: the pool-key write (the current pool's kp indexer rows of
+    256 B + scale, the kp pieces of 2 D / kp B), the indexer's inputs (pooled_indexer_bytes), the attention's bf16
+    queries, the attended tokens' latent rows (dqk B + fp32 scale) and the fp32 output."""
+    tot = pooled_indexer_bytes(cfg, npool)
+    for t in tokens:
+        tot += cfg.kp * (2 * cfg.D + 4) + 2 * cfg.D + 2 * cfg.H * cfg.dqk + (cfg.dqk + 4) * t + 4 * cfg.H * 512
+    return tot
+
+
+@dataclass
+class PooledInputs:
+    cfg: PooledConfig
+    rows: torch.Tensor  # [slots, 256] e4m3fn indexer rows: key 128 | pool gate logits 128
+    rows_scale: torch.Tensor  # [slots] fp32
+    ape: torch.Tensor  # [kp, 128] fp32 pool-position bias (idx_pool_ape)
+    pool_key: torch.Tensor  # [slots, 128 / kp] bf16: every pool's key, written from the rows
+    kv_cache: torch.Tensor  # [slots, 512] e4m3fn latent rows
+    kv_scale: torch.Tensor  # [slots] fp32
+    table: torch.Tensor  # [B, pages] int32
+    positions: torch.Tensor  # [B] int32: each row's current position (L - 1)
+    q_idx: torch.Tensor  # [B, Hi, 128] bf16
+    w: torch.Tensor  # [B, Hi] fp32 head weights times 128 ** -0.5
+    q: torch.Tensor  # [B, H, 512] bf16 absorbed queries
+
+    def to(self, device) -> "PooledInputs":
+        kw = {k: (v.to(device) if isinstance(v, torch.Tensor) else v) for k, v in self.__dict__.items()}
+        return PooledInputs(**kw)
+
+
+def make_pooled_inputs(cfg: PooledConfig, seed: int = 0, device: str | torch.device = "cpu",
+                       chunk: int = 65536) -> PooledInputs:
+    """Seeded inputs of one pooled decode step: indexer rows ~N(0, 1) and latent rows ~N(0, 1), both quantised per
+    token to e4m3fn; the pool keys are written by the library's kernel from those rows (the cache-store step), so
+    this needs the GPU library when device is a GPU."""
+    device = torch.device(device)
+    g = _gen(device)
+    g.manual_seed(seed)
+    B, ps = cfg.B, cfg.page_size
+    npg = math.ceil(cfg.L / ps)
+    num_pages = 1 + B * npg
+    slots = num_pages * ps
+    rows = torch.empty(slots, 2 * cfg.D, dtype=FP8, device=device)
+    rs = torch.empty(slots, dtype=torch.float32, device=device)
+    kv = torch.empty(slots, cfg.dqk, dtype=FP8, device=device)
+    ks = torch.empty(slots, dtype=torch.float32, device=device)
+    for s0 in range(0, slots, chunk):
+        n = min(chunk, slots - s0)
+        rows[s0:s0 + n], rs[s0:s0 + n] = quantize_rows(torch.randn(n, 2 * cfg.D, generator=g, device=device))
+        kv[s0:s0 + n], ks[s0:s0 + n] = quantize_rows(torch.randn(n, cfg.dqk, generator=g, device=device))
+    table = (torch.randperm(num_pages - 1, generator=g, device=device)[: B * npg] + 1).view(B, npg).to(torch.int32)
+    ape = torch.randn(cfg.kp, cfg.D, generator=g, device=device) * 0.5
+    q_idx = torch.randn(B, cfg.Hi, cfg.D, generator=g, device=device).to(torch.bfloat16)
+    w = torch.randn(B, cfg.Hi, generator=g, device=device) * 0.25 * cfg.D ** -0.5
+    q = torch.randn(B, cfg.H, cfg.dqk, generator=g, device=device).to(torch.bfloat16)
+    positions = torch.full((B,), cfg.L - 1, dtype=torch.int32, device=device)
+    pool_key = torch.zeros(slots, cfg.D // cfg.kp, dtype=torch.bfloat16, device=device)
+    inp = PooledInputs(cfg, rows, rs, ape, pool_key, kv, ks, table, positions, q_idx, w, q)
+    if device.type != "cpu":
+        from .kernels import dsa_cache
+
+        pos = torch.arange(cfg.L, device=device).repeat(B)
+        tb = table.repeat_interleave(cfg.L, dim=0)
+        sm = tb.long().gather(1, (pos // ps).view(-1, 1)).view(-1) * ps + pos % ps
+        dsa_cache.write_pool_keys(pool_key, rows, pos, tb, sm, ape, ps, cfg.kp, rows_scale=rs)
+    return inp
