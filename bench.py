@@ -182,7 +182,8 @@ def prefill_main(args) -> int:
     keys, the exact top-2048 of every query row (dsa_long_select.select), and sparse MLA of every query over its
     selected tokens (the token form through the context's page table). roofline: the indexer kernel's algorithmic
     MFMA work (2 Hi D per causal (query, key) pair) over its HIP-event-timed duration; `attention` gives the same for
-    sparse_mla_kernel (2 H (576 + 512) per selected token)."""
+    the attention kernel (2 H (576 + 512) per selected token; the many-row form, sparse_mla_wide_kernel, at this
+    size)."""
     import torch
 
     from trnrt_amd import _lib
@@ -224,7 +225,8 @@ def prefill_main(args) -> int:
     idx_us = k_us[kname]
     tflops = flops / (idx_us * 1e-6) / 1e12
     att_flops = W.prefill_attention_flops(cfg)
-    att_us = k_us["sparse_mla_kernel"] + k_us.get("combine_splits_kernel", 0.0)
+    att_kernel = "sparse_mla_wide_kernel" if "sparse_mla_wide_kernel" in k_us else "sparse_mla_kernel"
+    att_us = k_us[att_kernel] + k_us.get("combine_splits_kernel", 0.0)
     att_tflops = att_flops / (att_us * 1e-6) / 1e12
     out = {
         "metric": "DSA chunked-prefill step (indexer + top-2048 + sparse MLA) chunks/sec; indexer MFMA TFLOP/s",
@@ -249,7 +251,7 @@ def prefill_main(args) -> int:
                      "frac": round(tflops / (FP8_PEAK_TFLOPS if cfg.q_fp8 else BF16_PEAK_TFLOPS), 4),
                      "bf16_peak_frac": round(tflops / BF16_PEAK_TFLOPS, 4), "traffic": None,
                      "algorithmic_flops": flops, "avg_us": round(idx_us, 3)},
-        "attention": {"kernel": "sparse_mla_kernel", "avg_us": round(att_us, 3), "achieved": round(att_tflops, 1),
+        "attention": {"kernel": att_kernel, "avg_us": round(att_us, 3), "achieved": round(att_tflops, 1),
                       "unit": "TFLOP/s", "peak": BF16_PEAK_TFLOPS, "frac": round(att_tflops / BF16_PEAK_TFLOPS, 4),
                       "algorithmic_flops": att_flops},
         "kernel_us": {k: round(v, 3) for k, v in k_us.items()},

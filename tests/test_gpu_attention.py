@@ -113,3 +113,39 @@ def test_wrong_scale_is_caught():
     o, _ = _run(bad, idx, cnt, out_dtype=torch.float32)
     ro, _ = _ref(inp, idx, cnt)
     assert (o - ro).abs().max() > 2e-2 * (1 + ro.abs().max())
+
+
+@pytest.mark.parametrize("dqk", [576, 512])
+def test_many_row_form_vs_oracle(dqk):
+    """The many-row form (64-head workgroups, one per query row, pipelined gather: sparse_mla_wide_kernel), taken
+    when one split suffices and the rows fill the GPU: ragged counts (0, 1, one chunk, a chunk and one slot, every
+    slot, random), 64 heads, both row widths, against the oracle."""
+    from tests._helpers import launched_kernels
+    g = torch.Generator().manual_seed(dqk + 7)
+    B, H, L, ps, keep = 300, 64, 1024, 64, 320
+    say(f"attention many-row form dqk={dqk} B={B} keep={keep}")
+    npg = L // ps
+    num_pages = 1 + B * npg
+    kv, ks = W.quantize_rows(torch.randn(num_pages * ps, dqk, generator=g))
+    table = (torch.randperm(num_pages - 1, generator=g)[: B * npg] + 1).view(B, npg).to(torch.int32)
+    q = torch.randn(B, H, dqk, generator=g).to(torch.bfloat16)
+    cnt = torch.randint(0, keep + 1, (B,), generator=g)
+    cnt[:6] = torch.tensor([0, 1, 64, 65, keep, 63])
+    idx = torch.zeros(B, keep, dtype=torch.int64)
+    for b in range(B):
+        n = int(cnt[b])
+        idx[b, :n] = torch.randperm(L, generator=g)[:n].sort().values
+    qg, kvg, ksg, tg = q.cuda(), kv.cuda(), ks.cuda(), table.cuda()
+    res = {}
+
+    def step():
+        res["o"], res["lse"] = dsa_decode.attend_tokens(qg, kvg, ksg, idx.cuda(), cnt.cuda(), tg, ps, 192 ** -0.5,
+                                                        out_dtype=torch.float32)
+
+    names = launched_kernels(step)
+    assert names == ["sparse_mla_wide_kernel"], names
+    ro, rl = O.sparse_mla_ref(q, kv, ks, idx, cnt, table, ps, 192 ** -0.5)
+    assert_attention_close(res["o"], ro)
+    live = cnt > 0
+    torch.testing.assert_close(res["lse"].cpu()[live], rl[live], atol=1e-3, rtol=1e-4)
+    assert (res["lse"].cpu()[~live] < -1e29).all()

@@ -39,7 +39,9 @@ bool topk_supported(int max_len, int keep, int vis_only);
 hipError_t launch_sparse_mla(const uint16_t* q, const uint8_t* kv, const float* kvs, const int* idx, const int* cnt,
                              const int* table, const int* rows, const float* bias, uint16_t* out, float* out_f32,
                              float* lse, void* ws, int B, int H, int Dqk, int keep, int max_pages, int page_size,
-                             int num_pages, float scale, int splits, hipStream_t s, PoolForm pf = PoolForm{});
+                             int num_pages, float scale, int splits, hipStream_t s, PoolForm pf = PoolForm{},
+                             bool wide = false);
+bool attention_wide_ok(int B, int H, int keep, bool has_bias, int num_cu);
 hipError_t launch_token_rows(const int* idx, const int* cnt, const int* table, int* rows, float* bias, int B,
                              int keep, int max_pages, int page_size, int num_pages, hipStream_t s);
 int attention_default_splits(int B, int H, int keep, int num_cu);
@@ -247,10 +249,11 @@ int dsa_sparse_mla_decode(const void* q_bf16, const uint8_t* kv_fp8, const float
   const int sp = effective_splits(resolve_splits(splits, B, H, keep), keep);
   const size_t need = dsa::attention_workspace_bytes(B, H, sp);
   if (need && (!workspace || workspace_bytes < need)) return DSA_EWORKSPACE;
+  const bool wide = sp == 1 && dsa::attention_wide_ok(B, H, keep, bias != nullptr, num_cu()) && (token_form || cnt);
   return status(dsa::launch_sparse_mla(static_cast<const uint16_t*>(q_bf16), kv_fp8, kv_scale, idx, cnt, page_table,
                                        rows, bias, static_cast<uint16_t*>(out_bf16), out_f32, lse, workspace, B, H,
                                        Dqk, keep, max_pages, page_size, num_pages, scale, sp,
-                                       static_cast<hipStream_t>(stream)));
+                                       static_cast<hipStream_t>(stream), dsa::PoolForm{}, wide));
 }
 
 int dsa_token_rows(const int32_t* idx, const int32_t* cnt, const int32_t* page_table, int32_t* rows, float* bias,

@@ -366,6 +366,321 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void sparse_mla_kernel(
   }
 }
 
+// The many-row form (a prefill chunk's query rows, or any launch with one split and at least a workgroup per CU):
+// one workgroup = one query row x 64 heads over all its slots, so each gathered row serves 64 heads instead of 16,
+// and the gather is pipelined: chunk c + 2's rows are loaded into registers while chunk c is computed (two register
+// sets of LPT 16-byte pieces per thread, stored into two LDS tiles), so the workgroup waits for memory once at the
+// start (slot ids, scales, queries) instead of once per 256 slots. The 8 waves split the work as
+//   - scores: wave (hg = w % 4, th = w / 4) takes heads 16 hg .. + 15 and half th of the dims (9 or 8 steps of 32)
+//     over all 64 tokens of the chunk (S^T = K . Q^T on v_mfma_f32_16x16x32_bf16, four token blocks as independent
+//     chains), the query operand of its heads and dims in registers for the whole row (36 or 32 registers: the full
+//     width would not fit beside the output and the gather registers); the two halves' partial scores are
+//     exchanged through LDS, so both waves of a head group hold the chunk's full scores;
+//   - softmax: each wave takes the chunk maximum of its heads over all 64 tokens, P = exp(s - m) * kv_scale in bf16
+//     for its 32 tokens (32 th ..) into LDS [64 heads][64 tokens], the rescale factors into LDS;
+//   - value: wave w takes dims 64 w .. 64 w + 63 of all 64 heads (O in 16 accumulators, 4 head blocks x 4 dim blocks),
+//     its operand read transposed from the token-major tile by ds_read_b64_tr_b8 as in the split form.
+// The tiles are token-major with the 592-byte stride of the split form, but rows 8 .. 15 of every 16 hold each 16-byte
+// unit with its two 8-byte halves swapped: LDS serves a 64-bit read 16 lanes at a time over 32 banks, and the score's
+// 16 lanes read 16 rows at the same column, which the 592-byte stride alone maps onto 8 bank pairs (2-way conflict).
+// Slot forms: token (idx + cnt + table, with the pooled variant of PoolForm) and rows + cnt; no bias array.
+constexpr int AW_HEADS = 64;
+constexpr int AW_MAXSLOTS = 33 * ATT_CH;  // 2,112: keep 2,048 plus a pooled tail
+constexpr float AW_SLACK = 8.0f;          // lazy rescaling: p = exp(s - m) <= e^8 between moves of m
+
+struct AttWideShared {
+  uint8_t kt[2][ATT_CHUNK_BYTES];  // token-major e4m3 rows of two chunks (the queries before them)
+  uint16_t p[AW_HEADS * ATT_PROW];  // bf16 P[head][token] of the current chunk
+  int slot[AW_MAXSLOTS];
+  float kscale[AW_MAXSLOTS];  // the slots' kv scales (the P weights' dequantisation)
+  float kfac[AW_MAXSLOTS];    // kv scale x softmax scale (the scores' factor)
+  float bias[AW_MAXSLOTS];    // 0 live, NEG_INF masked (below n_eff), -inf past n_eff
+  f32x4 xs[2][4][4][WAVE];   // [th][hg][token block][lane]: partial scores over dims half th
+  float al[AW_HEADS];        // the chunk's rescale factor per head
+  int rfl[4];                // per head block: whether any of its 16 factors differs from 1
+  float lsum[2][AW_HEADS];   // [th][head]: final sums
+  float mfin[AW_HEADS];      // final maxima
+};
+
+// The many-row form's gather of one chunk into registers: LPT 16-byte pieces per thread, piece u = tid + 512 i of the
+// chunk's 64 rows (row u / PIECES, piece u % PIECES); the store of those registers into a tile.
+template <int DQK, int LPT>
+__device__ __forceinline__ void wide_gload(const uint8_t* __restrict__ kv, const int* slots, int tid, u32x4 (&r)[LPT]) {
+  constexpr int PIECES = DQK / 16, UNITS = ATT_CH * PIECES;
+#pragma unroll
+  for (int i = 0; i < LPT; ++i) {
+    const int u = min(tid + ATT_THREADS * i, UNITS - 1);
+    const int row = u / PIECES, pc = u - row * PIECES;
+    r[i] = *reinterpret_cast<const u32x4*>(kv + (size_t)slots[row] * DQK + 16 * pc);
+  }
+}
+
+template <int DQK, int LPT>
+__device__ __forceinline__ void wide_lstore(uint8_t* tile, int tid, const u32x4 (&r)[LPT]) {
+  constexpr int PIECES = DQK / 16, UNITS = ATT_CH * PIECES;
+#pragma unroll
+  for (int i = 0; i < LPT; ++i) {
+    const int u = min(tid + ATT_THREADS * i, UNITS - 1);
+    const int row = u / PIECES, pc = u - row * PIECES;
+    const u32x4 v = r[i];
+    *reinterpret_cast<u32x4*>(tile + row * ATT_KROW + 16 * pc) = (row & 8) ? u32x4{v[2], v[3], v[0], v[1]} : v;
+  }
+}
+
+// The value operand from a many-row tile (rows 8 .. 15 of every 16 hold their 16-byte units with the 8-byte halves
+// swapped): value_operand's addressing with lane p's half flipped in the rows whose bit 3 is set (row 32 ks + 8 q +
+// p / 2 has bit 3 = q & 1).
+__device__ __forceinline__ bf16x8 value_operand_sw(const uint8_t* kt, int ks, int n, int lane) {
+  const int q = lane >> 4, p = lane & 15;
+  const uint8_t* a = kt + (32 * ks + 8 * q + (p >> 1)) * ATT_KROW + 16 * n + 8 * ((p & 1) ^ (q & 1));
+  const att_v2i r = __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) att_v2i*)(a));
+  return fp8x8_to_bf16x8((uint32_t)r.x, (uint32_t)r.y);
+}
+
+template <int DQK>
+__global__ __launch_bounds__(ATT_THREADS, 1) void sparse_mla_wide_kernel(
+    const uint16_t* __restrict__ q, const uint8_t* __restrict__ kv, const float* __restrict__ kvs,
+    const int* __restrict__ idx, const int* __restrict__ cnt, const int* __restrict__ table,
+    const int* __restrict__ rows, uint16_t* __restrict__ out, float* __restrict__ out_f32,
+    float* __restrict__ lse_out, int H, int keep, int max_pages, int page_size, int num_pages, float scale,
+    PoolForm pf) {
+  constexpr int PIECES = DQK / 16;                              // 16-byte data pieces per row
+  constexpr int QROW = DQK + 8;                                 // staged query row stride (bf16 elements)
+  constexpr int STEPS = DQK / 32;                               // score steps of 32 dims
+  constexpr int UNITS = ATT_CH * PIECES;                        // 16-byte pieces per chunk
+  constexpr int LPT = (UNITS + ATT_THREADS - 1) / ATT_THREADS;  // per thread and chunk: 5 or 4
+  constexpr int QPIECES = AW_HEADS * DQK / 8;
+  constexpr int QPT = (QPIECES + ATT_THREADS - 1) / ATT_THREADS;
+  constexpr int SPT = (AW_MAXSLOTS + ATT_THREADS - 1) / ATT_THREADS;
+  static_assert(AW_HEADS * QROW * 2 <= 2 * ATT_CHUNK_BYTES && STEPS % 2 == 0, "staging");
+  __shared__ AttWideShared sh;
+  const int HB = H / AW_HEADS;
+  const int b = blockIdx.x / HB, hb64 = blockIdx.x - b * HB;
+  const int tid = threadIdx.x, wave = tid / WAVE, lane = tid & (WAVE - 1);
+  const int hg = wave & 3, th = wave >> 2;
+  const int l16 = lane & 15, q4 = lane >> 4;
+  const bool token_form = rows == nullptr;
+
+  // live slots (as in the split form): cnt_b of keep, at least one (a row with none attends slot 0 fully masked)
+  int cnt_b = cnt[b];
+  int pools_b = 0, tail_pool = 0;
+  if (pf.kp_shift) {
+    pools_b = min(max(cnt_b, 0), pf.idx_stride);
+    tail_pool = max(pf.npool[b], 0);
+    const int tail = min(max(pf.positions[b] + 1 - (tail_pool << pf.kp_shift), 0), (1 << pf.kp_shift) - 1);
+    cnt_b = (pools_b << pf.kp_shift) + tail;
+  }
+  const int n_eff = cnt_b < 1 ? 1 : (cnt_b > keep ? keep : cnt_b);
+  const int nch = (n_eff + ATT_CH - 1) / ATT_CH;
+  const int nslot = nch * ATT_CH;
+  const size_t nslots_cache = (size_t)num_pages * page_size;
+
+  // one round of loads: the 64 heads' queries, the slot ids of every chunk; then the slots' scales
+  const u32x4* qsrc = reinterpret_cast<const u32x4*>(q + ((size_t)b * H + AW_HEADS * hb64) * DQK);
+  u32x4 qv[QPT];
+#pragma unroll
+  for (int i = 0; i < QPT; ++i) qv[i] = qsrc[min(tid + ATT_THREADS * i, QPIECES - 1)];
+  const int* trow = table ? table + (size_t)b * max_pages : nullptr;
+  int slot_r[SPT];
+#pragma unroll
+  for (int i = 0; i < SPT; ++i) {
+    const int k = min(tid + ATT_THREADS * i, keep - 1);
+    int slot;
+    if (token_form) {
+      int pos;
+      if (pf.kp_shift) {
+        const int j = k >> pf.kp_shift;
+        const int pool = j < pools_b ? idx[(size_t)b * pf.idx_stride + j] : tail_pool;
+        pos = (pool << pf.kp_shift) + (k & ((1 << pf.kp_shift) - 1));
+      } else {
+        pos = idx[(size_t)b * keep + k];
+      }
+      pos = pos < 0 ? 0 : pos;
+      int pi = pos / page_size;
+      pi = pi < max_pages ? pi : max_pages - 1;
+      slot = safe_page(trow[pi], num_pages) * page_size + (pos - (pos / page_size) * page_size);
+    } else {
+      slot = rows[(size_t)b * keep + k];
+      slot = ((size_t)(unsigned)slot < nslots_cache) ? slot : 0;
+    }
+    slot_r[i] = slot;
+  }
+  float ksc_r[SPT];
+#pragma unroll
+  for (int i = 0; i < SPT; ++i) ksc_r[i] = kvs[slot_r[i]];
+  uint16_t* qs = reinterpret_cast<uint16_t*>(&sh.kt[0][0]);
+#pragma unroll
+  for (int i = 0; i < QPT; ++i) {
+    const int pc = tid + ATT_THREADS * i;
+    if (pc < QPIECES) *reinterpret_cast<u32x4*>(qs + (pc / (DQK / 8)) * QROW + 8 * (pc % (DQK / 8))) = qv[i];
+  }
+#pragma unroll
+  for (int i = 0; i < SPT; ++i) {
+    const int k = tid + ATT_THREADS * i;
+    if (k < nslot) {
+      sh.slot[k] = slot_r[i];
+      sh.kscale[k] = ksc_r[i];
+      sh.kfac[k] = ksc_r[i] * scale;
+      sh.bias[k] = k < n_eff ? (k < cnt_b ? 0.0f : NEG_INF) : -INFINITY;
+    }
+  }
+  __syncthreads();
+  constexpr int S2 = STEPS / 2;  // score steps per dims half
+  bf16x8 qb[S2];
+  {
+    const uint16_t* qh = qs + (16 * hg + l16) * QROW + 8 * q4 + 32 * S2 * th;
+#pragma unroll
+    for (int st = 0; st < S2; ++st) qb[st] = as_bf16x8(*reinterpret_cast<const uint4*>(qh + 32 * st));
+  }
+  __syncthreads();  // every wave holds its operand before the tiles overwrite the queries
+
+  f32x4 o[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int n = 0; n < 4; ++n) o[i][n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  float m_run = -INFINITY;  // running max of head 16 hg + l16 (the same in both th waves)
+  float l_run = 0.0f;       // this lane's share of the running sum of head 16 hg + l16
+
+  auto compute = [&](int c, int buf) __attribute__((always_inline)) {
+    __syncthreads();  // chunk c's tile is in LDS
+    const uint8_t* kt = sh.kt[buf];
+    const int cb = c * ATT_CH;
+    // partial scores of the 64 tokens (block k: tokens 16 k + l16 as MFMA rows) over this wave's dims half; lane
+    // (l16, q4) reads the 8-byte half q4 & 1 of unit q4 / 2 of its row's 32-dim step, the half flipped in rows whose
+    // bit 3 is set (l16 >= 8), so each 16-lane group covers the 32 banks once
+    const int kofs = l16 * ATT_KROW + 32 * S2 * th + 16 * (q4 >> 1) + 8 * ((q4 & 1) ^ (l16 >> 3));
+    f32x4 acc[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) acc[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int st = 0; st < S2; ++st)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint2 ka = *reinterpret_cast<const uint2*>(kt + kofs + 16 * k * ATT_KROW + 32 * st);
+        acc[k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16x8(ka.x, ka.y), qb[st], acc[k], 0, 0, 0);
+      }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) sh.xs[th][hg][k][lane] = acc[k];
+    __syncthreads();  // both halves' partial scores
+    // acc[k][r] + the other half's = S^T[token 16 k + 4 q4 + r][head 16 hg + l16]
+    float sv[4][4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const f32x4 o4 = sh.xs[th ^ 1][hg][k][lane];
+      const float4 kf = *reinterpret_cast<const float4*>(&sh.kfac[cb + 16 * k + 4 * q4]);
+      const float4 bs = *reinterpret_cast<const float4*>(&sh.bias[cb + 16 * k + 4 * q4]);
+      sv[k][0] = fmaf(acc[k][0] + o4[0], kf.x, bs.x);
+      sv[k][1] = fmaf(acc[k][1] + o4[1], kf.y, bs.y);
+      sv[k][2] = fmaf(acc[k][2] + o4[2], kf.z, bs.z);
+      sv[k][3] = fmaf(acc[k][3] + o4[3], kf.w, bs.w);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mx = max_nonan(mx, sv[k][r]);
+    }
+    mx = max_nonan(mx, __shfl_xor(mx, 16, WAVE));
+    mx = max_nonan(mx, __shfl_xor(mx, 32, WAVE));
+    // lazy rescaling: the running maximum moves only when the chunk's exceeds it by more than AW_SLACK, so most
+    // chunks rescale nothing; p = exp(s - m) then stays below e^AW_SLACK, and o, l and lse use the same m (exact)
+    const bool move = mx > m_run + AW_SLACK;
+    const float m_new = move ? mx : m_run;
+    const float alpha = move ? __expf(m_run - m_new) : 1.0f;
+    m_run = m_new;
+    if (th == 0) {
+      const bool any = __ballot(move) != 0;
+      if (lane == 0) sh.rfl[hg] = any;
+    }
+    float psum = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {  // this wave's tokens: blocks 2 th, 2 th + 1
+      uint32_t pk[2];
+#pragma unroll
+      for (int r = 0; r < 4; r += 2) {
+        const int tk = cb + 32 * th + 16 * k + 4 * q4 + r;
+        const float s0 = th ? sv[2 + k][r] : sv[k][r], s1 = th ? sv[2 + k][r + 1] : sv[k][r + 1];
+        const float p0 = __expf(s0 - m_new), p1 = __expf(s1 - m_new);
+        psum += p0 + p1;
+        pk[r / 2] = bf16_pack(p0 * sh.kscale[tk], p1 * sh.kscale[tk + 1]);
+      }
+      *reinterpret_cast<uint2*>(&sh.p[(16 * hg + l16) * ATT_PROW + 32 * th + 16 * k + 4 * q4]) =
+          make_uint2(pk[0], pk[1]);
+    }
+    l_run = l_run * alpha + psum;
+    if (th == 0 && lane < 16) sh.al[16 * hg + lane] = alpha;
+    __syncthreads();  // P and the rescale factors
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (sh.rfl[i]) {  // the same for every lane: a head block with no moved maximum is skipped
+        const float4 a4 = *reinterpret_cast<const float4*>(&sh.al[16 * i + 4 * q4]);
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+          o[i][n][0] *= a4.x;
+          o[i][n][1] *= a4.y;
+          o[i][n][2] *= a4.z;
+          o[i][n][3] *= a4.w;
+        }
+      }
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      bf16x8 pop[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        pop[i] = as_bf16x8(*reinterpret_cast<const uint4*>(&sh.p[(16 * i + l16) * ATT_PROW + 32 * ks + 8 * q4]));
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        const bf16x8 v = value_operand_sw(kt, ks, 4 * wave + n, lane);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pop[i], v, o[i][n], 0, 0, 0);
+      }
+    }
+    // the next chunk's partial scores, P and factors are written after its first barrier, which every wave reaches
+    // only after this chunk's P . V
+  };
+
+  // the pipeline: store chunk c (its loads were issued two steps earlier), reuse its registers for chunk c + 2,
+  // compute chunk c from tile c % 2
+  // (past the last chunk the loads re-read the last chunk, so every load is unconditional and the waits stay exact)
+  u32x4 r0[LPT], r1[LPT];
+  wide_gload<DQK, LPT>(kv, &sh.slot[0], tid, r0);
+  wide_gload<DQK, LPT>(kv, &sh.slot[min(1, nch - 1) * ATT_CH], tid, r1);
+  for (int c = 0; c < nch; c += 2) {
+    wide_lstore<DQK, LPT>(sh.kt[0], tid, r0);
+    wide_gload<DQK, LPT>(kv, &sh.slot[min(c + 2, nch - 1) * ATT_CH], tid, r0);
+    compute(c, 0);
+    wide_lstore<DQK, LPT>(sh.kt[1], tid, r1);
+    wide_gload<DQK, LPT>(kv, &sh.slot[min(c + 3, nch - 1) * ATT_CH], tid, r1);
+    if (c + 1 < nch) compute(c + 1, 1);  // workgroup-uniform
+  }
+
+  // per head: the sum over both token halves, the final max
+  float lw = l_run;
+  lw += __shfl_xor(lw, 16, WAVE);
+  lw += __shfl_xor(lw, 32, WAVE);
+  if (lane < 16) {
+    sh.lsum[th][16 * hg + lane] = lw;
+    if (th == 0) sh.mfin[16 * hg + lane] = m_run;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int head = 16 * i + 4 * q4 + r;
+      const float l = sh.lsum[0][head] + sh.lsum[1][head];
+      const float inv = 1.0f / l;
+      const size_t ob = ((size_t)b * H + AW_HEADS * hb64 + head) * ATT_DV + 64 * wave + l16;
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        const float v = o[i][n][r] * inv;
+        if (out) out[ob + 16 * n] = f32_to_bf16_bits(v);
+        if (out_f32) out_f32[ob + 16 * n] = v;
+      }
+      if (lse_out && wave == 0 && l16 == 0)
+        lse_out[(size_t)b * H + AW_HEADS * hb64 + head] = sh.mfin[head] + __logf(l);
+    }
+}
+
 // o = sum_s W_s o_s / sum_s W_s with W_s = l_s exp(m_s - M), M = max_s m_s, and lse = M + log sum_s W_s, per
 // (sequence, head), from each split's normalised o_s, max m_s and sum l_s (the log-sum-exp combine of
 // trnrt/models/mla.py:853-856 with lse_s = m_s + log l_s kept in two parts); 128 threads x 4 dims. Every load is
@@ -463,6 +778,12 @@ hipError_t launch_pool_slots(const int* pools, const int* cnt, const int* npool,
                 npool, positions, table, table_shared, rows, bias, keep, n_slots, table_pages, page_size / kp, kp);
 }
 
+// Whether a launch of one split takes the many-row form: 64-head workgroups, the token form or rows + cnt (no bias
+// array), at most AW_MAXSLOTS slots, and at least one workgroup per CU.
+bool attention_wide_ok(int B, int H, int keep, bool has_bias, int num_cu) {
+  return H % AW_HEADS == 0 && keep <= AW_MAXSLOTS && !has_bias && (long)B * (H / AW_HEADS) >= num_cu;
+}
+
 int attention_default_splits(int B, int H, int keep, int num_cu) {
   const int wgs = B * (H / ATT_HPW);
   int max_splits = (keep + ATT_CH - 1) / ATT_CH;
@@ -480,7 +801,16 @@ size_t attention_workspace_bytes(int B, int H, int splits) {
 hipError_t launch_sparse_mla(const uint16_t* q, const uint8_t* kv, const float* kvs, const int* idx, const int* cnt,
                              const int* table, const int* rows, const float* bias, uint16_t* out, float* out_f32,
                              float* lse, void* ws, int B, int H, int Dqk, int keep, int max_pages, int page_size,
-                             int num_pages, float scale, int splits, hipStream_t s, PoolForm pf) {
+                             int num_pages, float scale, int splits, hipStream_t s, PoolForm pf, bool wide) {
+  if (splits == 1 && wide) {
+    const dim3 grid(B * (H / AW_HEADS));
+    return Dqk == 512 ? launch("sparse_mla_wide_kernel", sparse_mla_wide_kernel<512>, grid, dim3(ATT_THREADS), s, q,
+                               kv, kvs, idx, cnt, table, rows, out, out_f32, lse, H, keep, max_pages, page_size,
+                               num_pages, scale, pf)
+                      : launch("sparse_mla_wide_kernel", sparse_mla_wide_kernel<576>, grid, dim3(ATT_THREADS), s, q,
+                               kv, kvs, idx, cnt, table, rows, out, out_f32, lse, H, keep, max_pages, page_size,
+                               num_pages, scale, pf);
+  }
   const int HG = H / ATT_HPW;
   // slots per split: a whole number of chunks
   int sps = (keep + splits - 1) / splits;

@@ -92,6 +92,18 @@ __device__ __forceinline__ float relu(float x) {
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 // fp32 -> bf16 bits, round to nearest even (finite inputs).
+// Two fp32 values -> two bf16 (round to nearest even, v_cvt_pk_bf16_f32), a in the low half.
+__device__ __forceinline__ uint32_t bf16_pack(float a, float b) {
+  typedef float f2v __attribute__((ext_vector_type(2)));
+  typedef __bf16 b2v __attribute__((ext_vector_type(2)));
+  const f2v v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, b2v));
+}
+
+// max of two fp32 values that are never NaN (scores, maxima) as one v_med3_f32 (the median of a, b and +inf is the
+// larger of a and b), without the NaN-quieting that fmaxf adds to each operand
+__device__ __forceinline__ float max_nonan(float a, float b) { return __builtin_amdgcn_fmed3f(a, b, INFINITY); }
+
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
   uint32_t u = __float_as_uint(f);
   uint32_t r = u + 0x7fffu + ((u >> 16) & 1u);
