@@ -362,7 +362,8 @@ def pooled_main(args) -> int:
                    "kv": f"fp8 e4m3 [{cfg.dqk}] + fp32 scale per token", "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "kernel": "indexer_decode_bf16_kernel", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "algorithmic_bytes": idx_bytes, "avg_us": round(idx_us, 3)},
+                     "traffic": measured_traffic(f"config {args.config}: {cfg.name}", "indexer_decode_bf16_kernel"),
+                     "algorithmic_bytes": idx_bytes, "avg_us": round(idx_us, 3)},
         "layer": {"algorithmic_bytes": step_bytes, "achieved_GBs": round(step_gbs, 1),
                   "frac": round(step_gbs / HBM_PEAK_GBS, 4), "kernel_us": {k: round(v, 3) for k, v in k_us.items()},
                   "launch_gaps_us": round(ms * 1e3 - sum(k_us.values()), 3)},

@@ -3,9 +3,11 @@
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this module, and only as the checker
 (or the timed CPU baseline). The product path (trnrt_amd) never calls it and has no CPU fallback.
 
-A restatement, in torch on the CPU in fp32, of the reference's arithmetic for the per-token (kpool 1) decode path with
-the BASELINE extensions (per-token FP8 scales; 576-wide KV = 512 latent + 64 rope columns, value = the latent part).
-Each function cites the reference lines it follows. How each one is pinned (tests/test_oracle_*.py):
+A restatement, in torch on the CPU in fp32, of the reference's arithmetic for the DSA path: the per-token (kpool 1)
+decode and chunked-prefill forms with per-token FP8 scales and 576-wide KV rows (512 latent + 64 rope columns, value =
+the latent part), and GLM's pooled (kpool > 1) forms (pool keys, the bucketed selection with the tail, pool slots,
+attention over 512-wide NoPE rows). Each function cites the reference lines it follows. How each one is pinned
+(tests/test_oracle_*.py):
 - indexer_ref: brute-force per-token loops, exact rational arithmetic on a tiny case, the scale-folding and
   dequantisation invariants, planted mistakes (no relu, a transposed table) that must fail;
 - prefill_scores_ref: exact rational arithmetic on a tiny case, a brute-force float64 loop, indexer_ref through an
@@ -16,6 +18,11 @@ Each function cites the reference lines it follows. How each one is pinned (test
   score kinds, and a planted wrong tie rule that must fail;
 - two_level_ref: equal to topk_ref on the reference's own adversarial cases (trnrt/models/dsa_long.py:26-42 proves
   it exact);
+- topk_mask_ref: selection_mask's pins, plus a literal known answer of the pooled form (kp 4 with the tail: each
+  score's value over its pool's tokens, every non-candidate kept);
+- pool_slots_ref: the tokens its slots attend are exactly the bucketed selection with the tail intersected with the
+  causal visibility (the reference's own check, tests/test_dsa_long.py:140-177), for one shared table and per-query
+  tables, pages of 4, 8 and 64, kpool 4 and 1; planted mistakes (the tail's last token dropped, no tail) must fail;
 - pool_keys_ref / write_pool_keys_ref: a float64 loop over the softmax-gated mean, the known answer of equal gates
   (the plain mean of the keys), the slot layout (pieces of a pool contiguous per page) and a planted mistake (the
   pool-position bias dropped) that must fail;
