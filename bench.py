@@ -196,7 +196,7 @@ def prefill_main(args) -> int:
     torch.cuda.set_device(dev)
     inp = W.make_prefill_inputs(cfg, seed=0, device=dev, attention=True)
     C = cfg.chunk
-    wsb = _lib.workspace_bytes(_lib.DSA_WS_TOPK, C, 0, cfg.keep, cfg.P)
+    wsb = int(_lib.lib().dsa_prefill_select_workspace_bytes(C, cfg.P, cfg.keep))
     ws = torch.zeros(wsb, dtype=torch.uint8, device=dev)  # the top-k histograms start (and end) at zero
     wsa_b = _lib.workspace_bytes(_lib.DSA_WS_ATTENTION, C, cfg.H, cfg.keep, 0, 0)
     wsa = torch.zeros(max(wsa_b, 256), dtype=torch.uint8, device=dev)

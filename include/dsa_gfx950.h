@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define DSA_ABI_VERSION 3
+#define DSA_ABI_VERSION 4
 
 #define DSA_OK 0
 #define DSA_EINVAL (-1)      /* a null pointer or a size out of range */
@@ -170,6 +170,21 @@ int dsa_token_rows(const int32_t* idx, const int32_t* cnt, const int32_t* page_t
 int dsa_pool_slots(const int32_t* pools, const int32_t* cnt, const int32_t* npool, const int32_t* positions,
                    const int32_t* table, int table_shared, int32_t* rows, float* bias, int N, int keep, int n_slots,
                    int table_pages, int page_size, int kp, void* stream);
+
+/*
+ * A prefill chunk's selection in one call (replaces trnrt/kernels/dsa_long_select.py:494-528 `select`, its score
+ * stage and its exact top-keep): the scores of dsa_indexer_prefill (q_scale null: bf16 queries q [N, Hi, 128]) or
+ * dsa_indexer_prefill_fp8 (q e4m3 [N, Hi, 128] with q_scale [N, Hi]) into scores [N, score_stride], then per query the
+ * exact top-keep of its npool[n] candidates (rows longer than 32,768 in two levels, the indexer writing the first
+ * level's sub-block maxima), returned as the reference returns them: pools int64 [N, keep] ascending (0 past the
+ * count), cnt int64 [N], vals fp32 [N, keep] (the selected scores, NEG_INF past the count).
+ *   workspace: dsa_prefill_select_workspace_bytes(N, P, keep) bytes, zero-filled before first use.
+ */
+int dsa_prefill_select(const void* q, const float* q_scale, const float* w, const uint8_t* k_fp8,
+                       const float* k_scale, const int32_t* npool, float* scores, int64_t* pools, int64_t* cnt,
+                       float* vals, void* workspace, size_t workspace_bytes, int N, int Hi, int D, int P,
+                       int score_stride, int keep, float scale, void* stream);
+size_t dsa_prefill_select_workspace_bytes(int N, int P, int keep);
 
 /*
  * The whole DSA decode layer step: indexer -> top-k -> sparse MLA, enqueued back to back on one stream

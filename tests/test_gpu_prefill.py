@@ -93,8 +93,11 @@ def test_causal_chunk_small(q_fp8):
                   q_values=inp.q_values())
 
 
-@pytest.mark.parametrize("P,keep", [(5000, 2048), (3000, 64), (40000, 2048)])
+@pytest.mark.parametrize("P,keep", [(5000, 2048), (3000, 64), (40000, 2048), (40001, 2048), (300000, 16)])
 def test_select_exact_on_the_kernels_scores(P, keep):
+    """dsa_prefill_select against the exact selection of the kernel's own scores: flat rows (P <= 32,768), two levels
+    with the sub-block maxima written by the indexer (sub 4; P a multiple of it or not), and two levels with sub-blocks
+    too large for that (sub 128: block_max_kernel)."""
     say(f"prefill select P={P} keep={keep}")
     N = 6
     qI, w, k8, ks, npool = _inputs(N, 64, P, seed=P + keep)

@@ -11,10 +11,15 @@ hipError_t launch_indexer_decode(const uint16_t* q, const float* w, const uint8_
                                  hipStream_t stream);
 hipError_t launch_indexer_prefill(const uint16_t* q, const float* w, const uint8_t* k, const float* ks,
                                   const int* npool, float* scores, int N, int Hi, int P, int stride, float scale,
-                                  hipStream_t s);
+                                  float* bm, int sub_log2, int nb, hipStream_t s);
 hipError_t launch_indexer_prefill_fp8(const uint8_t* q8, const float* qs, const float* w, const uint8_t* k,
                                       const float* ks, const int* npool, float* scores, int N, int Hi, int P,
-                                      int stride, float scale, hipStream_t s);
+                                      int stride, float scale, float* bm, int sub_log2, int nb, hipStream_t s);
+int topk_two_level_sub(long n, int keep);
+float* topk_bm_buffer(void* ws, int B);
+hipError_t launch_prefill_topk(const float* scores, const int* len, int* idx, int* cnt, void* ws, int B, int stride,
+                               int n, int keep, bool bm_ready, int64_t* pools, int64_t* cnt64, float* vals,
+                               hipStream_t s);
 bool cache_write_width_ok(int W);
 hipError_t launch_cache_write(const void* x, int x_fp32, const int64_t* slots, uint8_t* cache, float* cscale,
                               int n_rows, int W, long num_slots, int scaled, float fp8_max, hipStream_t s);
@@ -161,7 +166,8 @@ int dsa_indexer_prefill(const void* q_bf16, const float* w, const uint8_t* k_fp8
   if (D != 128 || Hi > 64) return DSA_EUNSUPPORTED;
   if (N == 0) return DSA_OK;
   return status(dsa::launch_indexer_prefill(static_cast<const uint16_t*>(q_bf16), w, k_fp8, k_scale, npool, scores, N,
-                                            Hi, P, score_stride, scale, static_cast<hipStream_t>(stream)));
+                                            Hi, P, score_stride, scale, nullptr, 0, 0,
+                                            static_cast<hipStream_t>(stream)));
 }
 
 int dsa_indexer_prefill_fp8(const uint8_t* q_fp8, const float* q_scale, const float* w, const uint8_t* k_fp8,
@@ -172,7 +178,43 @@ int dsa_indexer_prefill_fp8(const uint8_t* q_fp8, const float* q_scale, const fl
   if (D != 128 || Hi > 64) return DSA_EUNSUPPORTED;
   if (N == 0) return DSA_OK;
   return status(dsa::launch_indexer_prefill_fp8(q_fp8, q_scale, w, k_fp8, k_scale, npool, scores, N, Hi, P,
-                                                score_stride, scale, static_cast<hipStream_t>(stream)));
+                                                score_stride, scale, nullptr, 0, 0, static_cast<hipStream_t>(stream)));
+}
+
+size_t dsa_prefill_select_workspace_bytes(int N, int P, int keep) {
+  if (N < 0 || P < 1 || keep < 1) return 0;
+  return align256(dsa::topk_workspace_bytes(N, P, keep)) + align256((size_t)N * keep * 4) + align256((size_t)N * 4);
+}
+
+int dsa_prefill_select(const void* q, const float* q_scale, const float* w, const uint8_t* k_fp8,
+                       const float* k_scale, const int32_t* npool, float* scores, int64_t* pools, int64_t* cnt,
+                       float* vals, void* workspace, size_t workspace_bytes, int N, int Hi, int D, int P,
+                       int score_stride, int keep, float scale, void* stream) {
+  if (!q || !w || !k_fp8 || !k_scale || !npool || !scores || !pools || !cnt || !vals || !workspace) return DSA_EINVAL;
+  if (N < 0 || Hi < 1 || P < 1 || keep < 1 || score_stride < P || !(scale > 0.0f)) return DSA_EINVAL;
+  if (D != 128 || Hi > 64) return DSA_EUNSUPPORTED;
+  if (!dsa::topk_supported(P, keep, 1)) return DSA_EUNSUPPORTED;
+  if (workspace_bytes < dsa_prefill_select_workspace_bytes(N, P, keep)) return DSA_EWORKSPACE;
+  if (N == 0) return DSA_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  const size_t t_need = align256(dsa::topk_workspace_bytes(N, P, keep));
+  int* idx = reinterpret_cast<int*>(ws + t_need);
+  int* cnt32 = reinterpret_cast<int*>(ws + t_need + align256((size_t)N * keep * 4));
+  // rows selected in two levels with sub-blocks of at most 16: the indexer writes the sub-block maxima
+  const int sub = dsa::topk_two_level_sub(P, keep);
+  const bool fuse = sub >= 2 && sub <= 16;
+  float* bm = fuse ? dsa::topk_bm_buffer(workspace, N) : nullptr;
+  const int sub_log2 = fuse ? __builtin_ctz((unsigned)sub) : 0;
+  const int nb = fuse ? (P + sub - 1) / sub : 0;
+  hipError_t e = q_scale ? dsa::launch_indexer_prefill_fp8(static_cast<const uint8_t*>(q), q_scale, w, k_fp8, k_scale,
+                                                           npool, scores, N, Hi, P, score_stride, scale, bm, sub_log2,
+                                                           nb, s)
+                         : dsa::launch_indexer_prefill(static_cast<const uint16_t*>(q), w, k_fp8, k_scale, npool,
+                                                       scores, N, Hi, P, score_stride, scale, bm, sub_log2, nb, s);
+  if (e != hipSuccess) return DSA_ELAUNCH;
+  return status(dsa::launch_prefill_topk(scores, npool, idx, cnt32, workspace, N, score_stride, P, keep, fuse, pools,
+                                         cnt, vals, s));
 }
 
 int dsa_cache_write(const void* x, int x_fp32, const int64_t* slots, uint8_t* cache, float* scale, int n_rows, int W,

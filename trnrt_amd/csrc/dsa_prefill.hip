@@ -31,11 +31,36 @@ constexpr int PF_RING = 2 * PF_TPB;        // tiles in flight per thread: two ro
 static_assert(PF_TILES % PF_RING == 0, "a block is whole ring turns");
 
 // MT: head tiles of 32 (Hi <= 32 MT).
+// The two-level selection's sub-block maxima, taken by the workgroup that wrote the scores: after its last tile the
+// wave of query n reads its row's scores of the block [p_begin, p_end) back (srow[p - base]: the FP8 form
+// from its LDS copy of them, the bf16 form from the L2 after a barrier) and writes bm[n, b] = the maximum of the
+// 2^sub_log2 scores of sub-block b, for b below nb. Scores past the candidates are NEG_INF, so this is the maximum
+// over the candidates, as block_max_kernel computes it; vec: 16-byte reads (16-byte aligned rows, sub-blocks of at
+// least 4).
+__device__ __forceinline__ void block_max_rows(const float* srow, int base, float* __restrict__ bmrow, int p_begin,
+                                               int p_end, int sub_log2, int nb, bool vec, int lane) {
+  const int sub = 1 << sub_log2;
+  const int b1 = min(nb, (p_end + sub - 1) >> sub_log2);
+  for (int b = (p_begin >> sub_log2) + lane; b < b1; b += WAVE) {
+    const int p0 = b << sub_log2;
+    float m = NEG_INF;
+    if (vec && p0 + sub <= p_end) {
+      for (int e = 0; e < sub; e += 4) {
+        const float4 x = *reinterpret_cast<const float4*>(srow + (p0 + e - base));
+        m = max_nonan(max_nonan(m, x.x), max_nonan(x.y, max_nonan(x.z, x.w)));
+      }
+    } else {
+      for (int e = 0; e < sub && p0 + e < p_end; ++e) m = max_nonan(m, srow[p0 + e - base]);
+    }
+    bmrow[b] = m;
+  }
+}
+
 template <int MT>
 __global__ __launch_bounds__(PF_THREADS, 2) void indexer_prefill_kernel(
     const uint16_t* __restrict__ q, const float* __restrict__ w, const uint8_t* __restrict__ kcache,
     const float* __restrict__ kscale, const int* __restrict__ npool, float* __restrict__ scores, int N, int Hi, int P,
-    int stride, float scale) {
+    int stride, float scale, float* __restrict__ bm, int sub_log2, int nb) {
   // two rounds of bf16 tiles (key j of a tile: 16 pieces of 8 dims, piece p at slot 16 j + (p ^ (j & 15))), the
   // block's per-key scales and the queries' candidate counts
   __shared__ u32x4 kb[2][PF_TPB][PF_TILE * 16];
@@ -98,8 +123,12 @@ __global__ __launch_bounds__(PF_THREADS, 2) void indexer_prefill_kernel(
 
   float* srow = scores + (size_t)n * stride;
   if (p_begin >= wg_L) {  // no query of the workgroup has a candidate in the block: no MFMA
-    if (n < N)
+    if (n < N) {
       for (int p = p_begin + lane; p < p_end; p += WAVE) srow[p] = NEG_INF;
+      if (bm)
+        for (int b = (p_begin >> sub_log2) + lane; b < nb && (b << sub_log2) < p_end; b += WAVE)
+          bm[(size_t)n * nb + b] = NEG_INF;
+    }
     return;
   }
 
@@ -164,6 +193,10 @@ __global__ __launch_bounds__(PF_THREADS, 2) void indexer_prefill_kernel(
 #pragma unroll
   for (int s = 0; s < 8; ++s) epilogue_part(part, acc_b, s);
   finish(part, t - 1);
+  if (bm) {
+    __syncthreads();  // the workgroup's scores are written
+    if (n < N) block_max_rows(srow, 0, bm + (size_t)n * nb, p_begin, p_end, sub_log2, nb, (stride & 3) == 0, lane);
+  }
 }
 
 // The FP8-query form: q is e4m3 with a per-(query, head) fp32 scale. Then every product q8 k8 is exact in the
@@ -186,9 +219,11 @@ template <int MT>
 __global__ __launch_bounds__(PF_THREADS, 2) void indexer_prefill_fp8_kernel(
     const uint8_t* __restrict__ q8, const float* __restrict__ qscale, const float* __restrict__ w,
     const uint8_t* __restrict__ kcache, const float* __restrict__ kscale, const int* __restrict__ npool,
-    float* __restrict__ scores, int N, int Hi, int P, int stride, float scale) {
+    float* __restrict__ scores, int N, int Hi, int P, int stride, float scale, float* __restrict__ bm, int sub_log2,
+    int nb) {
   __shared__ u32x4 kb[2][PF_TPB][PF_TILE * 8];  // two rounds of FP8 tiles (key j: 8 pieces of 16 bytes)
   __shared__ float ksc_s[PF_TILES * PF_TILE];
+  __shared__ float sc_s[PF_QPW][PF_TILES * PF_TILE];  // with bm: each wave's scores of the block, for the maxima
   __shared__ int lmax[PF_QPW];
   const int wave = threadIdx.x / WAVE;
   const int lane = threadIdx.x & (WAVE - 1);
@@ -246,8 +281,12 @@ __global__ __launch_bounds__(PF_THREADS, 2) void indexer_prefill_fp8_kernel(
 
   float* srow = scores + (size_t)n * stride;
   if (p_begin >= wg_L) {
-    if (n < N)
+    if (n < N) {
       for (int p = p_begin + lane; p < p_end; p += WAVE) srow[p] = NEG_INF;
+      if (bm)
+        for (int b = (p_begin >> sub_log2) + lane; b < nb && (b << sub_log2) < p_end; b += WAVE)
+          bm[(size_t)n * nb + b] = NEG_INF;
+    }
     return;
   }
 
@@ -262,6 +301,7 @@ __global__ __launch_bounds__(PF_THREADS, 2) void indexer_prefill_fp8_kernel(
     const int pos = p_begin + t * PF_TILE + j;
     const float v = pos < L ? part * (ksc_s[t * PF_TILE + j] * scale) : NEG_INF;
     if (n < N && h == 0 && pos < p_end) srow[pos] = v;
+    if (bm && h == 0) sc_s[wave][t * PF_TILE + j] = v;
   };
   auto tile_mma = [&](const u32x4* tile, int t, f32x16(&cur)[MT], const f32x16(&prev)[MT]) {
     float part = 0.0f;
@@ -304,22 +344,25 @@ __global__ __launch_bounds__(PF_THREADS, 2) void indexer_prefill_fp8_kernel(
 #pragma unroll
   for (int s = 0; s < 2; ++s) epilogue_part(part, acc_b, s);
   finish(part, t - 1);
+  // each wave's scores are also in its LDS row (its own writes, in order): the maxima from there
+  if (bm && n < N) block_max_rows(sc_s[wave], p_begin, bm + (size_t)n * nb, p_begin, p_end, sub_log2, nb, true, lane);
 }
 
 template <int MT>
 static hipError_t launch_prefill_mt(const uint16_t* q, const float* w, const uint8_t* k, const float* ks,
                                     const int* npool, float* scores, int N, int Hi, int P, int stride, float scale,
-                                    hipStream_t s) {
+                                    float* bm, int sub_log2, int nb, hipStream_t s) {
   const dim3 grid((N + PF_QPW - 1) / PF_QPW, (stride + PF_TILES * PF_TILE - 1) / (PF_TILES * PF_TILE));
   return launch("indexer_prefill_kernel", indexer_prefill_kernel<MT>, grid, dim3(PF_THREADS), s, q, w, k, ks, npool,
-                scores, N, Hi, P, stride, scale);
+                scores, N, Hi, P, stride, scale, bm, sub_log2, nb);
 }
 
+// bm (or null): also the sub-block maxima of 2^sub_log2 scores, [N, nb].
 hipError_t launch_indexer_prefill(const uint16_t* q, const float* w, const uint8_t* k, const float* ks,
                                   const int* npool, float* scores, int N, int Hi, int P, int stride, float scale,
-                                  hipStream_t s) {
-  if (Hi <= 32) return launch_prefill_mt<1>(q, w, k, ks, npool, scores, N, Hi, P, stride, scale, s);
-  return launch_prefill_mt<2>(q, w, k, ks, npool, scores, N, Hi, P, stride, scale, s);
+                                  float* bm, int sub_log2, int nb, hipStream_t s) {
+  if (Hi <= 32) return launch_prefill_mt<1>(q, w, k, ks, npool, scores, N, Hi, P, stride, scale, bm, sub_log2, nb, s);
+  return launch_prefill_mt<2>(q, w, k, ks, npool, scores, N, Hi, P, stride, scale, bm, sub_log2, nb, s);
 }
 
 }  // namespace dsa
@@ -329,17 +372,18 @@ namespace dsa {
 template <int MT>
 static hipError_t launch_prefill_fp8_mt(const uint8_t* q8, const float* qs, const float* w, const uint8_t* k,
                                         const float* ks, const int* npool, float* scores, int N, int Hi, int P,
-                                        int stride, float scale, hipStream_t s) {
+                                        int stride, float scale, float* bm, int sub_log2, int nb, hipStream_t s) {
   const dim3 grid((N + PF_QPW - 1) / PF_QPW, (stride + PF_TILES * PF_TILE - 1) / (PF_TILES * PF_TILE));
   return launch("indexer_prefill_fp8_kernel", indexer_prefill_fp8_kernel<MT>, grid, dim3(PF_THREADS), s, q8, qs, w, k,
-                ks, npool, scores, N, Hi, P, stride, scale);
+                ks, npool, scores, N, Hi, P, stride, scale, bm, sub_log2, nb);
 }
 
 hipError_t launch_indexer_prefill_fp8(const uint8_t* q8, const float* qs, const float* w, const uint8_t* k,
                                       const float* ks, const int* npool, float* scores, int N, int Hi, int P,
-                                      int stride, float scale, hipStream_t s) {
-  if (Hi <= 32) return launch_prefill_fp8_mt<1>(q8, qs, w, k, ks, npool, scores, N, Hi, P, stride, scale, s);
-  return launch_prefill_fp8_mt<2>(q8, qs, w, k, ks, npool, scores, N, Hi, P, stride, scale, s);
+                                      int stride, float scale, float* bm, int sub_log2, int nb, hipStream_t s) {
+  if (Hi <= 32)
+    return launch_prefill_fp8_mt<1>(q8, qs, w, k, ks, npool, scores, N, Hi, P, stride, scale, bm, sub_log2, nb, s);
+  return launch_prefill_fp8_mt<2>(q8, qs, w, k, ks, npool, scores, N, Hi, P, stride, scale, bm, sub_log2, nb, s);
 }
 
 }  // namespace dsa

@@ -773,6 +773,32 @@ __global__ void topk_mask_scatter_kernel(const int* __restrict__ idx, const int*
   }
 }
 
+// gather_blocks_kernel with 16-byte loads and stores (sub a multiple of 4, rows 16-byte aligned): thread i moves
+// scores 4 i .. 4 i + 3 of the candidate row.
+__global__ void gather_blocks4_kernel(const float* __restrict__ scores, int stride, const int* __restrict__ len,
+                                      int sub, const int* __restrict__ bidx, const int* __restrict__ bcnt, int keep,
+                                      float* __restrict__ cand) {
+  const int row = blockIdx.y;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (4 * i >= keep * sub) return;
+  int L = stride;
+  if (len) L = min(max(len[row], 0), stride);
+  const int k = (4 * i) / sub, e = 4 * i - k * sub;
+  float4 v = make_float4(NEG_INF, NEG_INF, NEG_INF, NEG_INF);
+  if (k < bcnt[row]) {
+    const int p = bidx[(size_t)row * keep + k] * sub + e;
+    if (p + 3 < L) {
+      v = *reinterpret_cast<const float4*>(scores + (size_t)row * stride + p);
+    } else {
+      const float* sr = scores + (size_t)row * stride;
+      v.x = p < L ? sr[p] : NEG_INF;
+      v.y = p + 1 < L ? sr[p + 1] : NEG_INF;
+      v.z = p + 2 < L ? sr[p + 2] : NEG_INF;
+    }
+  }
+  reinterpret_cast<float4*>(cand + (size_t)row * keep * sub)[i] = v;
+}
+
 // Positions of a candidate row -> positions of the row it was gathered from (sub-blocks bidx of `sub` each).
 __global__ void map_blocks_kernel(int* __restrict__ idx, const int* __restrict__ cnt, const int* __restrict__ bidx,
                                   int sub, int keep) {
@@ -782,6 +808,31 @@ __global__ void map_blocks_kernel(int* __restrict__ idx, const int* __restrict__
     const int p = idx[(size_t)row * keep + k];
     idx[(size_t)row * keep + k] = bidx[(size_t)row * keep + p / sub] * sub + p % sub;
   }
+}
+
+// The prefill selection's outputs in the reference's form (trnrt/kernels/dsa_long_select.py:494-528 `select`): the
+// selected positions (through the selected sub-blocks bidx of `sub` each, when the rows were selected in two levels)
+// as int64, 0 past the count; their scores, NEG_INF past the count; the count as int64. idx keeps the positions.
+__global__ void select_out_kernel(int* __restrict__ idx, const int* __restrict__ cnt, const int* __restrict__ bidx,
+                                  int sub, int keep, const float* __restrict__ scores, int stride,
+                                  int64_t* __restrict__ pools, int64_t* __restrict__ cnt64, float* __restrict__ vals) {
+  const int row = blockIdx.y;
+  const int k = blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= keep) return;
+  const int c = cnt[row];
+  const size_t o = (size_t)row * keep + k;
+  int p = 0;
+  float v = NEG_INF;
+  if (k < c) {
+    p = idx[o];
+    if (bidx) p = bidx[(size_t)row * keep + p / sub] * sub + p % sub;
+    p = min(max(p, 0), stride - 1);
+    v = scores[(size_t)row * stride + p];
+    idx[o] = p;
+  }
+  pools[o] = p;
+  vals[o] = v;
+  if (k == 0) cnt64[row] = c;
 }
 
 // One workgroup per row up to TOPK_FLAT_MAX scores; longer rows are selected in two levels, recursively.
@@ -838,6 +889,13 @@ struct TopkBuffers {
   int* hist;
   RowMeta* meta;
   uint32_t* ckey;
+};
+
+// The prefill selection's outputs (select_out_kernel).
+struct SelectOut {
+  int64_t* pools;
+  int64_t* cnt;
+  float* vals;
 };
 
 template <int G, bool VEC>
@@ -899,11 +957,15 @@ static hipError_t launch_topk_level(const float* scores, int stride, const int* 
 // bound of the lengths.
 static hipError_t topk_rows(const float* scores, int stride, const int* len, int len_div, int len_mul, long n,
                             int keep, int vis_only, int* idx, int* cnt, const TopkBuffers& tb, bool hist_ready,
-                            char* ws, int B, hipStream_t s) {
+                            char* ws, int B, hipStream_t s, bool bm_ready = false, const SelectOut* out = nullptr) {
   const SlotOut none = {nullptr, 0, 0, 0, nullptr};
-  if (n <= TOPK_FLAT_MAX)
-    return launch_topk_level(scores, stride, len, len_div, len_mul, (int)n, keep, vis_only, idx, cnt, tb, hist_ready,
-                             none, B, s);
+  if (n <= TOPK_FLAT_MAX) {
+    hipError_t e = launch_topk_level(scores, stride, len, len_div, len_mul, (int)n, keep, vis_only, idx, cnt, tb,
+                                     hist_ready, none, B, s);
+    if (e != hipSuccess || !out) return e;
+    return launch("select_out_kernel", select_out_kernel, dim3((keep + 255) / 256, B), dim3(256), s, idx, cnt,
+                  nullptr, 1, keep, scores, stride, out->pools, out->cnt, out->vals);
+  }
   if (len_div != 1 || len_mul != 1) return hipErrorInvalidValue;  // only flat rows are split
   const int sub = topk_sub_block(n, keep);
   const int nb = (int)((n + sub - 1) / sub), nc = keep * sub;
@@ -915,19 +977,29 @@ static hipError_t topk_rows(const float* scores, int stride, const int* len, int
   ws += up256((size_t)B * 4);
   float* cand = reinterpret_cast<float*>(ws);
   ws += up256((size_t)B * nc * 4);
-  hipError_t e = launch("block_max_kernel", block_max_kernel, dim3((nb + 255) / 256, B), dim3(256), s, scores,
-                        stride, len, sub, nb, bm);
-  if (e != hipSuccess) return e;
+  hipError_t e = hipSuccess;
+  if (!bm_ready) {  // else the indexer wrote the maxima there (topk_bm_buffer)
+    e = launch("block_max_kernel", block_max_kernel, dim3((nb + 255) / 256, B), dim3(256), s, scores, stride, len, sub,
+               nb, bm);
+    if (e != hipSuccess) return e;
+  }
   // level 1: the top-keep sub-blocks (ceil(len / sub) maxima per row)
   if (nb > TOPK_FLAT_MAX) return hipErrorInvalidValue;  // excluded by topk_plan
   e = launch_topk_level(bm, nb, len, sub, 1, nb, keep, vis_only, bidx, bcnt, tb, false, none, B, s);
   if (e != hipSuccess) return e;
-  e = launch("gather_blocks_kernel", gather_blocks_kernel, dim3((nc + 255) / 256, B), dim3(256), s, scores, stride,
-             len, sub, bidx, bcnt, keep, cand);
+  if ((sub & 3) == 0 && (stride & 3) == 0)
+    e = launch("gather_blocks_kernel", gather_blocks4_kernel, dim3((nc / 4 + 255) / 256, B), dim3(256), s, scores,
+               stride, len, sub, bidx, bcnt, keep, cand);
+  else
+    e = launch("gather_blocks_kernel", gather_blocks_kernel, dim3((nc + 255) / 256, B), dim3(256), s, scores, stride,
+               len, sub, bidx, bcnt, keep, cand);
   if (e != hipSuccess) return e;
   // level 2: the top-keep of the selected sub-blocks' scores in position order (NEG_INF past their count)
   e = topk_rows(cand, nc, nullptr, 1, 1, nc, keep, vis_only, idx, cnt, tb, false, ws, B, s);
   if (e != hipSuccess) return e;
+  if (out)
+    return launch("select_out_kernel", select_out_kernel, dim3((keep + 255) / 256, B), dim3(256), s, idx, cnt, bidx,
+                  sub, keep, scores, stride, out->pools, out->cnt, out->vals);
   return launch("map_blocks_kernel", map_blocks_kernel, dim3((keep + 255) / 256, B), dim3(256), s, idx, cnt, bidx,
                 sub, keep);
 }
@@ -953,6 +1025,34 @@ hipError_t launch_topk(const float* scores, const int* len, int* idx, int* cnt, 
     return launch_topk_level(scores, stride, len, 1, 1, max_len, keep, vis_only, idx, cnt, tb, hist_ready, so, B, s);
   }
   return topk_rows(scores, stride, len, 1, 1, max_len, keep, vis_only, idx, cnt, tb, hist_ready, p, B, s);
+}
+
+// The sub-block size of the first level of rows of n scores (a power of two), or 0 when they are selected flat.
+int topk_two_level_sub(long n, int keep) { return n <= TOPK_FLAT_MAX ? 0 : topk_sub_block(n, keep); }
+
+// Where the first level's sub-block maxima [B, ceil(n / sub)] live in a top-k workspace: written there by a producer
+// (the prefill indexer), they let launch_prefill_topk skip block_max_kernel.
+float* topk_bm_buffer(void* ws, int B) {
+  return reinterpret_cast<float*>(static_cast<char*>(ws) + topk_hist_bytes(B) + up256((size_t)B * sizeof(RowMeta)) +
+                                  up256((size_t)B * TC_MAXCH * TC_CHUNK * 4));
+}
+
+// The prefill chunk's selection of rows of n <= stride scores (lengths len): the exact top-keep of each row, written
+// as the reference's (pools int64, cnt int64, vals) through idx / cnt (int32 [B, keep], [B]); bm_ready: the first
+// level's sub-block maxima are already in topk_bm_buffer(ws).
+hipError_t launch_prefill_topk(const float* scores, const int* len, int* idx, int* cnt, void* ws, int B, int stride,
+                               int n, int keep, bool bm_ready, int64_t* pools, int64_t* cnt64, float* vals,
+                               hipStream_t s) {
+  char* p = static_cast<char*>(ws);
+  TopkBuffers tb;
+  tb.hist = reinterpret_cast<int*>(p);
+  p += topk_hist_bytes(B);
+  tb.meta = reinterpret_cast<RowMeta*>(p);
+  p += up256((size_t)B * sizeof(RowMeta));
+  tb.ckey = reinterpret_cast<uint32_t*>(p);
+  p += up256((size_t)B * TC_MAXCH * TC_CHUNK * 4);
+  const SelectOut out = {pools, cnt64, vals};
+  return topk_rows(scores, stride, len, 1, 1, n, keep, 1, idx, cnt, tb, false, p, B, s, bm_ready, &out);
 }
 
 // Zero-fills a workspace (a kernel, not a memset, so that callers may capture it in a graph).

@@ -110,21 +110,45 @@ def select(qI: torch.Tensor, w: torch.Tensor, pk: torch.Tensor, npool: torch.Ten
            workspace: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """(pools [N, keep] int64 ascending, 0 past the count; count [N] int64; scores [N, keep] fp32, NEG_INF past the
     count) (trnrt/kernels/dsa_long_select.py:494-528 `select`): the scores above (FP8 queries with qI_scale as there),
-    then the exact top-keep per query.
-    vorder: the pools in (score descending, pool ascending) order instead. sub is accepted and ignored."""
+    then the exact top-keep per query, in one call of dsa_prefill_select (the indexer writes the two-level
+    selection's sub-block maxima, and the selection writes the reference's outputs directly).
+    vorder: the pools in (score descending, pool ascending) order instead. sub is accepted and ignored. workspace:
+    dsa_prefill_select_workspace_bytes(N, P, keep) bytes, zero-filled before its first use (calls leave it so)."""
     del sub
-    N, Hi = qI.shape[0], qI.shape[1]
+    dev = C.on_gpu(qI, w, pk, pk_scale, npool, qI_scale, workspace)
+    fp8_q = qI.dtype in (C.FP8, torch.uint8)
+    if fp8_q != (qI_scale is not None):
+        raise ValueError("dsa_long_select: FP8 queries need qI_scale, bf16 queries take none")
+    if qI.dim() != 3 or pk.dim() != 2:
+        raise ValueError(f"dsa_long_select: qI {tuple(qI.shape)}, pk {tuple(pk.shape)}")
+    N, Hi, Dq = qI.shape
     P = pk.shape[0]
-    if not supported(Hi, qI.shape[2], P, keep):
-        raise NotImplementedError(f"dsa_long_select: Hi {Hi}, D {qI.shape[2]}, P {P}, keep {keep}")
-    sc = scores(qI, w, pk, npool, scale, pk_scale=pk_scale, qI_scale=qI_scale)
-    lengths = npool.reshape(-1).clamp(0, P).to(torch.int32)
-    idx, cnt = dsa_topk.select_indices(sc, keep, lengths=lengths, vis_only=True, workspace=workspace)
-    pools = idx.to(torch.int64)
-    k = torch.arange(keep, device=sc.device).view(1, keep)
-    live = k < cnt.view(N, 1)
-    vals = torch.where(live, sc.gather(1, pools), NEG_INF)
-    cnt = cnt.to(torch.int64)
+    if not supported(Hi, Dq, P, keep) or pk.shape[1] != D:
+        raise NotImplementedError(f"dsa_long_select: Hi {Hi}, D {Dq}, P {P}, keep {keep}")
+    if not scale > 0:
+        raise ValueError(f"dsa_long_select: scale {scale} must be positive")
+    pk = C.fp8_bytes(pk, "pk")
+    w = C.need(C.as_f32(w), "w", torch.float32, (N, Hi))
+    pk_scale = C.need(C.as_f32(pk_scale).reshape(-1), "pk_scale", torch.float32, (P,))
+    npool = C.need(C.as_i32(npool.reshape(-1)), "npool", torch.int32, (N,))  # clamped to [0, P] by the kernels
+    if fp8_q:
+        qI = C.fp8_bytes(qI, "qI")
+        qI_scale = C.need(C.as_f32(qI_scale), "qI_scale", torch.float32, (N, Hi))
+    else:
+        qI = C.as_bf16(qI)
+    lib = _lib.lib()
+    wsb = int(lib.dsa_prefill_select_workspace_bytes(N, P, keep))
+    if workspace is None:
+        workspace = torch.zeros(wsb, dtype=torch.uint8, device=dev)
+    ws_len = workspace.numel() * workspace.element_size()
+    sc = torch.empty(N, P, dtype=torch.float32, device=dev)
+    pools = torch.empty(N, keep, dtype=torch.int64, device=dev)
+    cnt = torch.empty(N, dtype=torch.int64, device=dev)
+    vals = torch.empty(N, keep, dtype=torch.float32, device=dev)
+    st = lib.dsa_prefill_select(C.ptr(qI), C.ptr(qI_scale), C.ptr(w), C.ptr(pk), C.ptr(pk_scale), C.ptr(npool),
+                                C.ptr(sc), C.ptr(pools), C.ptr(cnt), C.ptr(vals), C.ptr(workspace), ws_len, N, Hi, D,
+                                P, P, keep, float(scale), C.stream_ptr(dev))
+    _lib.check(st, "dsa_long_select.select")
     if vorder:
         return value_order(pools, cnt, vals)
     return pools, cnt, vals
