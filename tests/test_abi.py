@@ -115,3 +115,41 @@ def test_cache_write_host_checks():
     assert lib.dsa_cache_write(p, 0, p, p, p, 4, 20, 100, 1, 448.0, null) == -2  # width not a multiple of 8
     assert lib.dsa_cache_write(p, 0, p, p, p, 4, 1032, 100, 1, 448.0, null) == -2  # width above 1024
     assert lib.dsa_cache_write(p, 0, p, p, p, 0, 576, 100, 1, 448.0, null) == 0  # nothing to do
+
+
+def test_prefill_select_and_pooled_layer_host_checks():
+    """Argument checks of dsa_prefill_select and dsa_pooled_decode_layer, which return before any launch."""
+    lib = _lib.lib()
+    p = ctypes.c_void_p(16)
+    null = None
+    ws = lib.dsa_prefill_select_workspace_bytes(4, 67584, 2048)
+    assert ws > 0 and lib.dsa_prefill_select_workspace_bytes(4, 0, 2048) == 0
+    big = ctypes.c_size_t(ws)
+    args = lambda **k: dict(dict(q=p, qs=p, w=p, k=p, ks=p, npool=p, sc=p, pools=p, cnt=p, vals=p, ws=p, wsb=big, N=4,
+                                 Hi=64, D=128, P=67584, stride=67584, keep=2048, scale=0.1), **k)
+
+    def call(a):
+        return lib.dsa_prefill_select(a["q"], a["qs"], a["w"], a["k"], a["ks"], a["npool"], a["sc"], a["pools"],
+                                      a["cnt"], a["vals"], a["ws"], a["wsb"], a["N"], a["Hi"], a["D"], a["P"],
+                                      a["stride"], a["keep"], a["scale"], null)
+
+    assert call(args(vals=null)) == -1  # no output
+    assert call(args(stride=67583)) == -1  # stride < P
+    assert call(args(scale=0.0)) == -1
+    assert call(args(Hi=65)) == -2
+    assert call(args(D=64)) == -2
+    assert call(args(wsb=ctypes.c_size_t(ws - 1))) == -3  # workspace too small
+    assert call(args(N=0)) == 0
+    pw = lib.dsa_pooled_workspace_bytes(8, 64, 512, 8192, 4, 0)
+    assert pw > 0 and lib.dsa_pooled_workspace_bytes(8, 64, 512, 8192, 1, 0) == 0
+    pwb = ctypes.c_size_t(pw)
+
+    def layer(kp=4, H=64, Dqk=512, page_size=64, wsb=pwb, B=8, table=p):
+        return lib.dsa_pooled_decode_layer(p, p, p, p, p, p, table, p, p, p, p, p, p, p, p, wsb, B, 32, H, Dqk, 512,
+                                           page_size, 4097, kp, 512, 0.0625, 0, null)
+
+    assert layer(table=null) == -1
+    assert layer(kp=3) == -2 and layer(kp=1) == -2 and layer(page_size=66) == -2
+    assert layer(H=40) == -2 and layer(Dqk=256) == -2
+    assert layer(wsb=ctypes.c_size_t(pw - 1)) == -3
+    assert layer(B=0) == 0
