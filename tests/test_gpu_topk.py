@@ -109,3 +109,16 @@ def test_pooled_mask_forms(kp, tail):
     s[torch.arange(P).view(1, P) >= npool.view(R, 1)] = O.NEG_INF
     m = dsa_topk.select(s.cuda(), keep, kp=kp, tail=tail).cpu()
     assert torch.equal(m, O.topk_mask_ref(s, keep, True, kp, tail))
+
+
+@pytest.mark.parametrize("n", [6000, 9000, 16384, 20000, 32768])
+@pytest.mark.parametrize("kind", ["randn", "integers", "zeros", "wide", "invisible", "equal"])
+def test_many_rows_form(kind, n):
+    """520 rows (a prefill chunk's shape): one workgroup per row holding the whole row (2 .. 8 float4 groups per
+    thread), every row bit-exact against the oracle, with ragged lengths on some rows."""
+    say(f"topk many rows {kind} n={n}")
+    g = torch.Generator().manual_seed(KINDS.index(kind) * 7919 + n)
+    s = scores_of(kind, 520, n, g)
+    lengths = [n] * 520
+    lengths[3], lengths[100], lengths[511] = 0, 2047, n - 1
+    _exact(s, 2048, lengths)

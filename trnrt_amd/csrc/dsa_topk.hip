@@ -914,6 +914,46 @@ static hipError_t launch_topk_row(const float* scores, int stride, const int* le
                              len, len_div, len_mul, keep, vis_only, hist, idx, cnt, so);
 }
 
+// Many rows (a prefill chunk's queries, the two-level selection's levels): one workgroup per row holds the whole row
+// (up to 8 float4 groups per thread, 32,768 scores) and selects it in one kernel, reading it once; the chunked form
+// spreads few long rows over many CUs instead.
+constexpr int TOPK_MANY_ROWS = 512;
+
+template <int G, bool VEC>
+static hipError_t launch_topk_row_plain(const float* scores, int stride, const int* len, int len_div, int len_mul,
+                                        int keep, int vis_only, int* hist, int* idx, int* cnt, const SlotOut& so,
+                                        int B, hipStream_t s) {
+  return launch("topk_row_kernel", topk_row_kernel<G, false, VEC, false>, dim3(B), dim3(TR_THREADS), s, scores,
+                stride, len, len_div, len_mul, keep, vis_only, hist, idx, cnt, so);
+}
+
+template <bool VEC>
+static hipError_t launch_topk_many_rows(const float* scores, int stride, const int* len, int len_div, int len_mul,
+                                        int max_len, int keep, int vis_only, int* hist, int* idx, int* cnt,
+                                        const SlotOut& so, int B, hipStream_t s) {
+  switch ((max_len + 4 * TR_THREADS - 1) / (4 * TR_THREADS)) {
+    case 1:
+      return launch_topk_row_plain<1, VEC>(scores, stride, len, len_div, len_mul, keep, vis_only, hist, idx, cnt, so,
+                                           B, s);
+    case 2:
+      return launch_topk_row_plain<2, VEC>(scores, stride, len, len_div, len_mul, keep, vis_only, hist, idx, cnt, so,
+                                           B, s);
+    case 3:
+      return launch_topk_row_plain<3, VEC>(scores, stride, len, len_div, len_mul, keep, vis_only, hist, idx, cnt, so,
+                                           B, s);
+    case 4:
+      return launch_topk_row_plain<4, VEC>(scores, stride, len, len_div, len_mul, keep, vis_only, hist, idx, cnt, so,
+                                           B, s);
+    case 5:
+    case 6:
+      return launch_topk_row_plain<6, VEC>(scores, stride, len, len_div, len_mul, keep, vis_only, hist, idx, cnt, so,
+                                           B, s);
+    default:
+      return launch_topk_row_plain<8, VEC>(scores, stride, len, len_div, len_mul, keep, vis_only, hist, idx, cnt, so,
+                                           B, s);
+  }
+}
+
 template <bool VEC>
 static hipError_t launch_topk_chunked(const float* scores, int stride, const int* len, int len_div, int len_mul,
                                       int nch, int keep, int vis_only, int* idx, int* cnt, const TopkBuffers& tb,
@@ -946,6 +986,11 @@ static hipError_t launch_topk_level(const float* scores, int stride, const int* 
                : launch_topk_row<1, false>(scores, stride, len, len_div, len_mul, keep, vis_only, tb.hist, hist_ready,
                                            idx, cnt, so, B, s);
   if (max_len > TC_MAXCH * TC_CHUNK) return hipErrorInvalidValue;
+  if (B >= TOPK_MANY_ROWS && !hist_ready && !so.rows)
+    return vec ? launch_topk_many_rows<true>(scores, stride, len, len_div, len_mul, max_len, keep, vis_only, tb.hist,
+                                             idx, cnt, so, B, s)
+               : launch_topk_many_rows<false>(scores, stride, len, len_div, len_mul, max_len, keep, vis_only, tb.hist,
+                                              idx, cnt, so, B, s);
   const int nch = (max_len + TC_CHUNK - 1) / TC_CHUNK;
   return vec ? launch_topk_chunked<true>(scores, stride, len, len_div, len_mul, nch, keep, vis_only, idx, cnt, tb,
                                          hist_ready, so, B, s)
