@@ -220,3 +220,23 @@ def test_config5_chunk_attention_sampled_rows():
                                       cfg.page_size, cfg.softmax_scale)
     assert_attention_close(o[rows], ref_o)
     torch.testing.assert_close(lse[rows].cpu(), ref_lse, atol=1e-3, rtol=1e-3)
+
+
+@pytest.mark.parametrize("P", [40000, 65540])
+def test_select_many_rows_every_row(P):
+    """520 queries (the many-row forms: one workgroup per row for both levels, the second level reading the selected
+    sub-blocks in place and writing the reference's outputs): every row bit-exact against the exact selection of the
+    kernel's own scores, with sub-blocks of 4 and of 8 (65,540 keys: the last sub-block crosses the row's end)."""
+    say(f"prefill select many rows P={P}")
+    N, keep = 520, 2048
+    qI, w, k8, ks, npool = _inputs(N, 16, P, seed=P + 1)
+    npool[:4] = torch.tensor([0, 1, keep - 1, P])
+    args = (qI.cuda(), w.cuda(), k8.cuda(), npool.cuda())
+    sc = LS.scores(*args, 128 ** -0.5, pk_scale=ks.cuda()).cpu()
+    pools, cnt, vals = LS.select(*args, keep, 128 ** -0.5, pk_scale=ks.cuda())
+    torch.cuda.synchronize()
+    ri, rc = O.topk_ref(sc, keep, npool)
+    assert torch.equal(cnt.cpu(), rc)
+    assert torch.equal(pools.cpu(), ri)
+    live = torch.arange(keep).view(1, -1) < rc.view(-1, 1)
+    assert torch.equal(vals.cpu(), torch.where(live, sc.gather(1, ri), O.NEG_INF))

@@ -80,6 +80,23 @@ struct SlotOut {
   int* rows;  // [B, keep], or null
 };
 
+// The second level of a two-level selection read in place (the row kernel's IND form): candidate position p of a
+// row is score src(p) = bidx[row, p / sub] sub + p % sub of the original row (sub a multiple of 4, so a float4 of
+// candidates is one float4 of scores), live while p / sub < bcnt[row] and src < len[row]; the selection is written
+// in the reference's form: pools int64 (the src positions) and vals (their scores), NEG_INF / 0 past the count, cnt
+// int64.
+struct IndOut {
+  const float* scores;
+  int stride;
+  const int* len;
+  const int* bidx;
+  const int* bcnt;
+  int sub;
+  int64_t* pools;
+  int64_t* cnt;
+  float* vals;
+};
+
 struct RowShared {
   int pg[128];                      // page ids of the row's first 4096 positions (slot output)
   int bins[TK_HBINS];               // the current pass's histogram (4096, 2048 or 512 bins in key order)
@@ -138,16 +155,17 @@ __device__ int row_find_bin(RowShared& sh, int nbins, int need, int* bin, int* a
 // The flat selection: one workgroup per row (blockIdx.x) of up to 4 G 1024 scores. Thread t holds the keys of
 // positions 4 (1024 e + t) + c, e < G, c < 4 (coalesced float4 loads). HIST_IN: the row's top-12-bit histogram is in
 // hist[row] (read, then zeroed for the next call); otherwise it is built here.
-template <int G, bool HIST_IN, bool VEC, bool ROWS>
+// IND: the row is the IndOut second level (scores / stride / len are unused; stride is the candidate row length).
+template <int G, bool HIST_IN, bool VEC, bool ROWS, bool IND = false>
 __global__ __launch_bounds__(TR_THREADS) void topk_row_kernel(const float* __restrict__ scores, int stride,
                                                               const int* __restrict__ len, int len_div, int len_mul,
                                                               int keep, int vis_only, int* __restrict__ hist,
                                                               int* __restrict__ idx_out, int* __restrict__ cnt_out,
-                                                              SlotOut so) {
+                                                              SlotOut so, IndOut io) {
   __shared__ RowShared sh;
   const int row = blockIdx.x;
   const int t = threadIdx.x, wave = t / WAVE, lane = t & (WAVE - 1);
-  const int L = level_len(len, row, len_div, len_mul, stride);
+  const int L = IND ? stride : level_len(len, row, len_div, len_mul, stride);
   const float* srow = scores + (size_t)row * stride;
 
   int4 h4r[HIST_REPLICAS];
@@ -158,8 +176,33 @@ __global__ __launch_bounds__(TR_THREADS) void topk_row_kernel(const float* __res
   int pgv = 0;
   if (ROWS) pgv = so.table[(size_t)row * so.max_pages + min(t, so.max_pages - 1)];
   uint32_t key[G][4];
+  int src[G];  // IND: the original position of each float4 group's first candidate
+  if (IND) {
+    const int nblk = min(io.bcnt[row], keep);
+    const int Lo = min(max(io.len[row], 0), io.stride);
+    int bsrc[G];
 #pragma unroll
-  for (int e = 0; e < G; ++e) load_keys4<VEC>(srow, stride, L, 4 * (TR_THREADS * e + t), vis_only, key[e]);
+    for (int e = 0; e < G; ++e) {
+      const int p = 4 * (TR_THREADS * e + t);
+      const int k = min(p / io.sub, keep - 1);
+      bsrc[e] = io.bidx[(size_t)row * keep + k];
+    }
+#pragma unroll
+    for (int e = 0; e < G; ++e) {
+      const int p = 4 * (TR_THREADS * e + t);
+      const int k = p / io.sub;
+      const bool blive = p < stride && k < nblk;
+      src[e] = blive ? bsrc[e] * io.sub + (p - k * io.sub) : 0;  // live positions are below Lo <= io.stride
+      const float4 f =
+          *reinterpret_cast<const float4*>(io.scores + (size_t)row * io.stride + min(max(src[e], 0), io.stride - 4));
+      const float v[4] = {f.x, f.y, f.z, f.w};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) key[e][c] = select_key(v[c], vis_only) & (0u - (uint32_t)(blive && src[e] + c < Lo));
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < G; ++e) load_keys4<VEC>(srow, stride, L, 4 * (TR_THREADS * e + t), vis_only, key[e]);
+  }
   if (ROWS && t < 128) sh.pg[t] = safe_page(pgv, so.num_pages);
   if (t == 0) sh.sel_bin = -1;
   if (HIST_IN) {
@@ -262,7 +305,12 @@ __global__ __launch_bounds__(TR_THREADS) void topk_row_kernel(const float* __res
       const bool sel = a || (ti && t_before < room);
       const int o = a_before + (t_before < room ? t_before : room);
       if (sel && (unsigned)o < (unsigned)keep) {  // in range whatever the counts
-        orow[o] = p0 + c;
+        if (IND) {
+          io.pools[(size_t)row * keep + o] = src[e] + c;
+          io.vals[(size_t)row * keep + o] = key_to_float(key[e][c]);
+        } else {
+          orow[o] = p0 + c;
+        }
         if (ROWS) {
           const int ps = so.page_size;
           so.rows[(size_t)row * keep + o] = sh.pg[min((p0 + c) / ps, 127)] * ps + (p0 + c) % ps;
@@ -274,10 +322,20 @@ __global__ __launch_bounds__(TR_THREADS) void topk_row_kernel(const float* __res
   }
   const int cnt_row = nvis < keep ? nvis : keep;
   for (int i = cnt_row + t; i < keep; i += TR_THREADS) {
-    orow[i] = 0;
+    if (IND) {
+      io.pools[(size_t)row * keep + i] = 0;
+      io.vals[(size_t)row * keep + i] = NEG_INF;
+    } else {
+      orow[i] = 0;
+    }
     if (ROWS) so.rows[(size_t)row * keep + i] = sh.pg[0] * so.page_size;
   }
-  if (t == 0) cnt_out[row] = cnt_row;
+  if (t == 0) {
+    if (IND)
+      io.cnt[row] = cnt_row;
+    else
+      cnt_out[row] = cnt_row;
+  }
 }
 
 // The chunked selection of rows of more than 4096 scores: workgroups of 256 threads own chunks of 2048 positions
@@ -905,13 +963,13 @@ static hipError_t launch_topk_row(const float* scores, int stride, const int* le
   const dim3 grid(B), block(TR_THREADS);
   if (so.rows)
     return hist_ready ? launch("topk_row_kernel", topk_row_kernel<G, true, VEC, true>, grid, block, s, scores, stride,
-                               len, len_div, len_mul, keep, vis_only, hist, idx, cnt, so)
+                               len, len_div, len_mul, keep, vis_only, hist, idx, cnt, so, IndOut{})
                       : launch("topk_row_kernel", topk_row_kernel<G, false, VEC, true>, grid, block, s, scores,
-                               stride, len, len_div, len_mul, keep, vis_only, hist, idx, cnt, so);
+                               stride, len, len_div, len_mul, keep, vis_only, hist, idx, cnt, so, IndOut{});
   return hist_ready ? launch("topk_row_kernel", topk_row_kernel<G, true, VEC, false>, grid, block, s, scores, stride,
-                             len, len_div, len_mul, keep, vis_only, hist, idx, cnt, so)
+                             len, len_div, len_mul, keep, vis_only, hist, idx, cnt, so, IndOut{})
                     : launch("topk_row_kernel", topk_row_kernel<G, false, VEC, false>, grid, block, s, scores, stride,
-                             len, len_div, len_mul, keep, vis_only, hist, idx, cnt, so);
+                             len, len_div, len_mul, keep, vis_only, hist, idx, cnt, so, IndOut{});
 }
 
 // Many rows (a prefill chunk's queries, the two-level selection's levels): one workgroup per row holds the whole row
@@ -924,7 +982,7 @@ static hipError_t launch_topk_row_plain(const float* scores, int stride, const i
                                         int keep, int vis_only, int* hist, int* idx, int* cnt, const SlotOut& so,
                                         int B, hipStream_t s) {
   return launch("topk_row_kernel", topk_row_kernel<G, false, VEC, false>, dim3(B), dim3(TR_THREADS), s, scores,
-                stride, len, len_div, len_mul, keep, vis_only, hist, idx, cnt, so);
+                stride, len, len_div, len_mul, keep, vis_only, hist, idx, cnt, so, IndOut{});
 }
 
 template <bool VEC>
@@ -951,6 +1009,28 @@ static hipError_t launch_topk_many_rows(const float* scores, int stride, const i
     default:
       return launch_topk_row_plain<8, VEC>(scores, stride, len, len_div, len_mul, keep, vis_only, hist, idx, cnt, so,
                                            B, s);
+  }
+}
+
+template <int G>
+static hipError_t launch_topk_ind_g(int nc, int keep, int vis_only, const IndOut& io, int B, hipStream_t s) {
+  const SlotOut none = {nullptr, 0, 0, 0, nullptr};
+  return launch("topk_row_kernel", topk_row_kernel<G, false, true, false, true>, dim3(B), dim3(TR_THREADS), s,
+                nullptr, nc, nullptr, 1, 1, keep, vis_only, nullptr, nullptr, nullptr, none, io);
+}
+
+// The IND second level over nc <= TOPK_FLAT_MAX candidates per row.
+static hipError_t launch_topk_ind(int nc, int keep, int vis_only, const IndOut& io, int B, hipStream_t s) {
+  switch ((nc + 4 * TR_THREADS - 1) / (4 * TR_THREADS)) {
+    case 1:
+      return launch_topk_ind_g<1>(nc, keep, vis_only, io, B, s);
+    case 2:
+      return launch_topk_ind_g<2>(nc, keep, vis_only, io, B, s);
+    case 3:
+    case 4:
+      return launch_topk_ind_g<4>(nc, keep, vis_only, io, B, s);
+    default:
+      return launch_topk_ind_g<8>(nc, keep, vis_only, io, B, s);
   }
 }
 
@@ -1032,6 +1112,12 @@ static hipError_t topk_rows(const float* scores, int stride, const int* len, int
   if (nb > TOPK_FLAT_MAX) return hipErrorInvalidValue;  // excluded by topk_plan
   e = launch_topk_level(bm, nb, len, sub, 1, nb, keep, vis_only, bidx, bcnt, tb, false, none, B, s);
   if (e != hipSuccess) return e;
+  // many rows with their outputs in the reference's form: the second level reads the selected sub-blocks in place
+  // and writes those outputs (no candidate rows, no separate mapping)
+  if (out && B >= TOPK_MANY_ROWS && nc <= TOPK_FLAT_MAX && (sub & 3) == 0 && (stride & 3) == 0 && len) {
+    const IndOut io = {scores, stride, len, bidx, bcnt, sub, out->pools, out->cnt, out->vals};
+    return launch_topk_ind(nc, keep, vis_only, io, B, s);
+  }
   if ((sub & 3) == 0 && (stride & 3) == 0)
     e = launch("gather_blocks_kernel", gather_blocks4_kernel, dim3((nc / 4 + 255) / 256, B), dim3(256), s, scores,
                stride, len, sub, bidx, bcnt, keep, cand);
