@@ -13,6 +13,7 @@ the reference arithmetic, timed on this host's cores on a bounded sample of the 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--config 2] [--no-cpu-baseline]
     python bench.py --config 5          # the chunked-prefill step (65,536 cached + 2,048 new queries): its own line
     python bench.py --config 6          # the pooled (GLM-5.3-Flash, kpool 4) decode step at B=8 x 32K: its own line
+    python bench.py --config 7          # the pooled (GLM) chunked-prefill step (65,536 cached + 2,048 new queries)
     python bench.py --copy-probe 512    # plain device copies of 512 MiB: the calibration run for HBM counters
 
 roofline.traffic (HBM bytes per indexer launch) comes from rocprofv3 FETCH_SIZE / WRITE_SIZE counter runs of this
@@ -374,6 +375,120 @@ def pooled_main(args) -> int:
     return 0
 
 
+def pooled_prefill_main(args) -> int:
+    """The GLM pooled chunked-prefill step (config 7): the prefill indexer over the context's bf16 pool keys with the
+    exact top-512 pools (dsa_long_select.select -> dsa_prefill_select), then absorbed MLA of every query over its
+    pools' tokens and its tail (dsa_long.attend_pooled -> dsa_sparse_mla_pooled). roofline: the indexer kernel's
+    algorithmic MFMA work (2 Hi D per causal (query, pool) pair) against the bf16 peak; `attention` the same for the
+    attention kernel (2 H (512 + 512) per attended token)."""
+    import torch
+
+    from trnrt_amd import _lib
+    from trnrt_amd import workloads as W
+    from trnrt_amd.kernels import dsa_long_select as LS
+    from trnrt_amd.models import dsa_long
+
+    cfg = W.POOLED_PREFILL_CONFIGS[args.config]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    inp = W.make_pooled_prefill_inputs(cfg, seed=0, device=dev)
+    C = cfg.chunk
+    lib = _lib.lib()
+    ws = torch.zeros(int(lib.dsa_prefill_select_workspace_bytes(C, cfg.P, cfg.keep)), dtype=torch.uint8, device=dev)
+    wsa = torch.zeros(max(int(lib.dsa_sparse_mla_pooled_workspace_bytes(C, cfg.H, cfg.keep, cfg.kp, 0)), 256),
+                      dtype=torch.uint8, device=dev)
+    table = inp.table.view(1, -1).expand(C, -1).contiguous()  # every query row reads the context's pages
+
+    def step():
+        pools, cnt, _ = LS.select(inp.qI, inp.w, inp.pk, inp.npool, cfg.keep, cfg.scale, workspace=ws)
+        dsa_long.attend_pooled(inp.q, inp.kv_cache, inp.kv_scale, pools, cnt, inp.npool, inp.positions, table,
+                               cfg.page_size, cfg.kp, cfg.softmax_scale, workspace=wsa)
+
+    steps = min(args.steps, 20)
+    for _ in range(min(args.warmup, 5)):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    k_us = kernel_times(lib, step, steps)
+    npool = inp.npool.long().cpu()
+    pairs = int(npool.clamp(max=cfg.P).sum())
+    flops = 2 * cfg.Hi * cfg.D * pairs
+    idx_us = k_us["indexer_prefill_kernel"]
+    tflops = flops / (idx_us * 1e-6) / 1e12
+    tail = (inp.positions.long().cpu() + 1 - cfg.kp * npool)
+    tokens = int((cfg.kp * npool.clamp(max=cfg.keep) + tail).sum())
+    att_flops = 2 * cfg.H * (cfg.dqk + 512) * tokens
+    att_kernel = "sparse_mla_wide_kernel" if "sparse_mla_wide_kernel" in k_us else "sparse_mla_kernel"
+    att_us = k_us[att_kernel] + k_us.get("combine_splits_kernel", 0.0)
+    att_tflops = att_flops / (att_us * 1e-6) / 1e12
+    out = {
+        "metric": "GLM pooled chunked-prefill step (indexer + top-512 pools + sparse MLA) chunks/sec",
+        "value": round(1e3 / ms, 2),
+        "unit": "chunks/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": min(args.warmup, 5),
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"config {args.config}: {cfg.name}", "cached": cfg.cached, "chunk": C,
+                   "indexer_heads": cfg.Hi, "q_heads": cfg.H, "kpool": cfg.kp, "keep_pools": cfg.keep,
+                   "pool_keys": "bf16 [128] per pool", "kv": f"fp8 e4m3 [{cfg.dqk}] + fp32 scale per token",
+                   "page_size": cfg.page_size, "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "kernel": "indexer_prefill_kernel", "achieved": round(tflops, 1),
+                     "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                     "traffic": None, "algorithmic_flops": flops, "avg_us": round(idx_us, 3)},
+        "attention": {"kernel": att_kernel, "avg_us": round(att_us, 3), "achieved": round(att_tflops, 1),
+                      "unit": "TFLOP/s", "peak": BF16_PEAK_TFLOPS, "frac": round(att_tflops / BF16_PEAK_TFLOPS, 4),
+                      "algorithmic_flops": att_flops},
+        "kernel_us": {k: round(v, 3) for k, v in k_us.items()},
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = pooled_prefill_cpu_baseline(inp, cfg)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def pooled_prefill_cpu_baseline(inp, cfg, budget_s: float = 15.0) -> dict:
+    """The oracle's pooled chunk step (prefill_scores_ref over the pool keys + topk_ref + pool_slots_ref +
+    sparse_mla_slots_ref, torch fp32 on the host) over whole query rows, as many as fit in about budget_s seconds;
+    reported as chunks per second."""
+    import torch
+
+    from oracle import dsa_oracle as O
+
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    torch.set_num_threads(cores)
+    c = inp.to("cpu")
+    ones = torch.ones(cfg.P)
+    rows, t0, n = 4, time.perf_counter(), 0
+    while True:
+        r0 = (n * rows) % cfg.chunk
+        sl = slice(r0, r0 + rows)
+        sc = O.prefill_scores_ref(c.qI[sl], c.w[sl], c.pk, ones, c.npool[sl], cfg.scale)
+        pools, cnt = O.topk_ref(sc, cfg.keep, c.npool[sl])
+        rw, bias = O.pool_slots_ref(pools, cnt, c.npool[sl], c.positions[sl].long(), c.table, cfg.page_size, cfg.kp,
+                                    cfg.keep + 1)
+        tok = (rw.unsqueeze(-1) * cfg.kp + torch.arange(cfg.kp)).reshape(rows, -1)
+        O.sparse_mla_slots_ref(c.q[sl], c.kv_cache, c.kv_scale, tok, bias.reshape(rows, -1), cfg.softmax_scale)
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= budget_s or n * rows >= cfg.chunk:
+            break
+    done = n * rows
+    return {"value": done / cfg.chunk / dt, "unit": "chunks/s", "cores": cores, "kind": "port",
+            "sample": f"{done} of the chunk's {cfg.chunk} query rows (scores over {cfg.P} pools + top-{cfg.keep} + "
+                      f"slots + sparse MLA over {cfg.kp * (cfg.keep + 1)} token slots, torch fp32, {dt:.1f} s, "
+                      f"{cores} threads)"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -394,6 +509,8 @@ def main() -> int:
         return prefill_main(args)
     if args.config == 6:
         return pooled_main(args)
+    if args.config == 7:
+        return pooled_prefill_main(args)
 
     import torch
 

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define DSA_ABI_VERSION 4
+#define DSA_ABI_VERSION 5
 
 #define DSA_OK 0
 #define DSA_EINVAL (-1)      /* a null pointer or a size out of range */
@@ -78,11 +78,11 @@ int dsa_indexer_decode_bf16(const void* q_bf16, const float* w, const void* k_bf
  * and trnrt/models/dsa_long.py:74-84 `scores` with a 2-D key tensor):
  *   scores[n, p] = scale * k_scale[p] * sum_h w[n, h] * relu(q[n, h, :] . k_fp8[p, :])   for p < npool[n]
  *   scores[n, p] = NEG_INF                                                               for npool[n] <= p < score_stride
- *   q bf16 [N, Hi, D] (D must be 128; Hi <= 64), w fp32 [N, Hi], k_fp8 uint8 [P, D] + k_scale fp32 [P],
- *   npool int32 [N] (each query's candidate count, clamped to [0, P]), scores fp32 [N, score_stride],
- *   P <= score_stride.
+ *   q bf16 [N, Hi, D] (D must be 128; Hi <= 64), w fp32 [N, Hi], k uint8 e4m3 [P, D] + k_scale fp32 [P], or
+ *   k bf16 [P, D] with k_scale null (GLM's pool keys, trnrt/models/mla.py:491-503; then Hi <= 32), npool int32 [N]
+ *   (each query's candidate count, clamped to [0, P]), scores fp32 [N, score_stride], P <= score_stride.
  */
-int dsa_indexer_prefill(const void* q_bf16, const float* w, const uint8_t* k_fp8, const float* k_scale,
+int dsa_indexer_prefill(const void* q_bf16, const float* w, const void* k, const float* k_scale,
                         const int32_t* npool, float* scores, int N, int Hi, int D, int P, int score_stride,
                         float scale, void* stream);
 
@@ -173,15 +173,15 @@ int dsa_pool_slots(const int32_t* pools, const int32_t* cnt, const int32_t* npoo
 
 /*
  * A prefill chunk's selection in one call (replaces trnrt/kernels/dsa_long_select.py:494-528 `select`, its score
- * stage and its exact top-keep): the scores of dsa_indexer_prefill (q_scale null: bf16 queries q [N, Hi, 128]) or
- * dsa_indexer_prefill_fp8 (q e4m3 [N, Hi, 128] with q_scale [N, Hi]) into scores [N, score_stride], then per query the
+ * stage and its exact top-keep): the scores of dsa_indexer_prefill (q_scale null: bf16 queries q [N, Hi, 128]; keys
+ * e4m3 with k_scale, or bf16 with k_scale null) or dsa_indexer_prefill_fp8 (q e4m3 [N, Hi, 128] with q_scale [N, Hi],
+ * e4m3 keys) into scores [N, score_stride], then per query the
  * exact top-keep of its npool[n] candidates (rows longer than 32,768 in two levels, the indexer writing the first
  * level's sub-block maxima), returned as the reference returns them: pools int64 [N, keep] ascending (0 past the
  * count), cnt int64 [N], vals fp32 [N, keep] (the selected scores, NEG_INF past the count).
  *   workspace: dsa_prefill_select_workspace_bytes(N, P, keep) bytes, zero-filled before first use.
  */
-int dsa_prefill_select(const void* q, const float* q_scale, const float* w, const uint8_t* k_fp8,
-                       const float* k_scale, const int32_t* npool, float* scores, int64_t* pools, int64_t* cnt,
+int dsa_prefill_select(const void* q, const float* q_scale, const float* w, const void* k, const float* k_scale, const int32_t* npool, float* scores, int64_t* pools, int64_t* cnt,
                        float* vals, void* workspace, size_t workspace_bytes, int N, int Hi, int D, int P,
                        int score_stride, int keep, float scale, void* stream);
 size_t dsa_prefill_select_workspace_bytes(int N, int P, int keep);
@@ -196,6 +196,21 @@ int dsa_decode_layer(const void* q_idx_bf16, const float* w, const uint8_t* k_fp
                      const int32_t* ctx_len, float* scores, int32_t* idx, int32_t* cnt, void* out_bf16, float* lse,
                      void* workspace, size_t workspace_bytes, int B, int Hi, int H, int max_pages, int page_size,
                      int num_pages, int score_stride, int max_len, int keep, float scale, int splits, void* stream);
+
+/*
+ * Absorbed MLA over a pooled selection (replaces trnrt/models/dsa_long.py:189-215 `slots` + :218-223 `attend`
+ * without materialising the slots): for each of B queries, the kp tokens of each selected pool (pools int32
+ * [B, keep] ascending, cnt int32 [B] valid) and the tail tokens kp npool .. positions[b] of its incomplete pool
+ * (npool int32 [B] = (positions + 1) / kp), read through page_table int32 [B, max_pages] from kv e4m3fn
+ * [num_pages page_size, Dqk] with kv_scale fp32 per token; q bf16 [B, H, Dqk] (Dqk 576 or 512), out bf16 or fp32
+ * [B, H, 512], lse fp32 [B, H] or null. workspace: dsa_sparse_mla_pooled_workspace_bytes(B, H, keep, kp, splits).
+ */
+int dsa_sparse_mla_pooled(const void* q_bf16, const uint8_t* kv_fp8, const float* kv_scale, const int32_t* pools,
+                          const int32_t* cnt, const int32_t* npool, const int32_t* positions, const int32_t* page_table,
+                          void* out_bf16, float* out_f32, float* lse, void* workspace, size_t workspace_bytes, int B,
+                          int H, int Dqk, int keep, int kp, int max_pages, int page_size, int num_pages, float scale,
+                          int splits, void* stream);
+size_t dsa_sparse_mla_pooled_workspace_bytes(int B, int H, int keep, int kp, int splits);
 
 /*
  * The pooled (GLM, kpool kp > 1) DSA decode layer step, enqueued back to back on one stream (the decode batch of

@@ -250,3 +250,40 @@ def test_pooled_decode_layer_matches_composition_and_oracle(dqk):
                          positions.cuda())
     torch.cuda.synchronize()
     assert torch.equal(layer.pools.long(), pools) and torch.equal(out2, out1)
+
+
+@pytest.mark.parametrize("cached,chunk", [(2048, 96), (3000, 70)])
+def test_glm_pooled_chunk_end_to_end(cached, chunk):
+    """A GLM chunk (trnrt/models/mla.py:505-526 with a shared table): the prefill indexer over the context's bf16 pool
+    keys, the exact top-512 pools (dsa_long_select.select), then absorbed MLA over the pools' tokens and each query's
+    tail (dsa_long.attend_pooled, and the reference flow slots + attend), every stage against the oracle."""
+    from trnrt_amd.kernels import dsa_long_select as LS
+    cfg = W.PooledPrefillConfig("glm-chunk", cached=cached, chunk=chunk)
+    say(f"GLM pooled chunk {cached}+{chunk}")
+    inp = W.make_pooled_prefill_inputs(cfg, seed=cached + chunk, device="cuda")
+    pools, cnt, vals = LS.select(inp.qI, inp.w, inp.pk, inp.npool, cfg.keep, cfg.scale)
+    sc = dsa_long.scores(inp.qI, inp.w, inp.pk, inp.npool, cfg.scale)
+    o = dsa_long.attend_pooled(inp.q, inp.kv_cache, inp.kv_scale, pools, cnt, inp.npool, inp.positions, inp.table,
+                               cfg.page_size, cfg.kp, cfg.softmax_scale)
+    rows, bias = dsa_long.slots(pools, cnt, inp.npool, inp.positions, inp.table, cfg.page_size, cfg.kp, cfg.keep + 1)
+    o_ref_flow = dsa_long.attend(inp.q, inp.kv_cache, rows, bias, cfg.softmax_scale, kc_scale=inp.kv_scale)
+    torch.cuda.synchronize()
+    c = inp.to("cpu")
+    ref = O.prefill_scores_ref(c.qI, c.w, c.pk, torch.ones(cfg.P), c.npool, cfg.scale)
+    live = ref > -1e29
+    from tests._helpers import row_rel_err
+    err = row_rel_err(sc.cpu(), ref, live)
+    say(f"  pool scores rel err {err:.3e}")
+    assert err <= 1e-2 and torch.equal(sc.cpu() < -1e29, ~live)
+    want_p, want_c = O.topk_ref(sc.cpu(), cfg.keep, c.npool)
+    assert torch.equal(pools.cpu(), want_p) and torch.equal(cnt.cpu(), want_c)
+    lv = torch.arange(cfg.keep).view(1, -1) < want_c.view(-1, 1)
+    assert torch.equal(vals.cpu(), torch.where(lv, sc.cpu().gather(1, want_p), O.NEG_INF))
+    want_r, want_b = O.pool_slots_ref(want_p, want_c, c.npool, c.positions.long(), c.table, cfg.page_size, cfg.kp,
+                                      cfg.keep + 1)
+    assert torch.equal(rows.cpu(), want_r) and torch.equal(bias.cpu(), want_b)
+    tok = (want_r.unsqueeze(-1) * cfg.kp + torch.arange(cfg.kp)).reshape(cfg.chunk, -1)
+    want_o, _ = O.sparse_mla_slots_ref(c.q, c.kv_cache, c.kv_scale, tok, want_b.reshape(cfg.chunk, -1),
+                                       cfg.softmax_scale)
+    assert_attention_close(o, want_o)
+    assert_attention_close(o_ref_flow, want_o)

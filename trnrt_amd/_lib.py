@@ -23,7 +23,7 @@ DSA_WS_TOPK = 1
 DSA_WS_ATTENTION = 2
 DSA_WS_LAYER = 3
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 P = c_void_p
 # Every entry point of include/dsa_gfx950.h with its ctypes signature (restype, argtypes).
@@ -59,6 +59,12 @@ SIGNATURES: dict[str, tuple] = {
          c_int, c_int, c_float, c_int, P],
     ),
     "dsa_pooled_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int]),
+    "dsa_sparse_mla_pooled": (
+        c_int,
+        [P, P, P, P, P, P, P, P, P, P, P, P, c_size_t, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
+         c_float, c_int, P],
+    ),
+    "dsa_sparse_mla_pooled_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
     "dsa_prefill_select": (
         c_int,
         [P, P, P, P, P, P, P, P, P, P, P, c_size_t, c_int, c_int, c_int, c_int, c_int, c_int, c_float, P],

@@ -15,6 +15,9 @@ hipError_t launch_indexer_prefill(const uint16_t* q, const float* w, const uint8
 hipError_t launch_indexer_prefill_fp8(const uint8_t* q8, const float* qs, const float* w, const uint8_t* k,
                                       const float* ks, const int* npool, float* scores, int N, int Hi, int P,
                                       int stride, float scale, float* bm, int sub_log2, int nb, hipStream_t s);
+hipError_t launch_indexer_prefill_bf16k(const uint16_t* q, const float* w, const uint16_t* k, const int* npool,
+                                        float* scores, int N, int Hi, int P, int stride, float scale, float* bm,
+                                        int sub_log2, int nb, hipStream_t s);
 int topk_two_level_sub(long n, int keep);
 float* topk_bm_buffer(void* ws, int B);
 hipError_t launch_prefill_topk(const float* scores, const int* len, int* idx, int* cnt, void* ws, int B, int stride,
@@ -158,16 +161,20 @@ int dsa_indexer_decode_bf16(const void* q_bf16, const float* w, const void* k_bf
                                                 static_cast<hipStream_t>(stream)));
 }
 
-int dsa_indexer_prefill(const void* q_bf16, const float* w, const uint8_t* k_fp8, const float* k_scale,
+int dsa_indexer_prefill(const void* q_bf16, const float* w, const void* k, const float* k_scale,
                         const int32_t* npool, float* scores, int N, int Hi, int D, int P, int score_stride,
                         float scale, void* stream) {
-  if (!q_bf16 || !w || !k_fp8 || !k_scale || !npool || !scores) return DSA_EINVAL;
+  if (!q_bf16 || !w || !k || !npool || !scores) return DSA_EINVAL;
   if (N < 0 || Hi < 1 || P < 1 || score_stride < P || !(scale > 0.0f)) return DSA_EINVAL;
-  if (D != 128 || Hi > 64) return DSA_EUNSUPPORTED;
+  if (D != 128 || Hi > (k_scale ? 64 : 32)) return DSA_EUNSUPPORTED;
   if (N == 0) return DSA_OK;
-  return status(dsa::launch_indexer_prefill(static_cast<const uint16_t*>(q_bf16), w, k_fp8, k_scale, npool, scores, N,
-                                            Hi, P, score_stride, scale, nullptr, 0, 0,
-                                            static_cast<hipStream_t>(stream)));
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (!k_scale)
+    return status(dsa::launch_indexer_prefill_bf16k(static_cast<const uint16_t*>(q_bf16), w,
+                                                    static_cast<const uint16_t*>(k), npool, scores, N, Hi, P,
+                                                    score_stride, scale, nullptr, 0, 0, s));
+  return status(dsa::launch_indexer_prefill(static_cast<const uint16_t*>(q_bf16), w, static_cast<const uint8_t*>(k),
+                                            k_scale, npool, scores, N, Hi, P, score_stride, scale, nullptr, 0, 0, s));
 }
 
 int dsa_indexer_prefill_fp8(const uint8_t* q_fp8, const float* q_scale, const float* w, const uint8_t* k_fp8,
@@ -186,13 +193,14 @@ size_t dsa_prefill_select_workspace_bytes(int N, int P, int keep) {
   return align256(dsa::topk_workspace_bytes(N, P, keep)) + align256((size_t)N * keep * 4) + align256((size_t)N * 4);
 }
 
-int dsa_prefill_select(const void* q, const float* q_scale, const float* w, const uint8_t* k_fp8,
-                       const float* k_scale, const int32_t* npool, float* scores, int64_t* pools, int64_t* cnt,
-                       float* vals, void* workspace, size_t workspace_bytes, int N, int Hi, int D, int P,
-                       int score_stride, int keep, float scale, void* stream) {
-  if (!q || !w || !k_fp8 || !k_scale || !npool || !scores || !pools || !cnt || !vals || !workspace) return DSA_EINVAL;
+int dsa_prefill_select(const void* q, const float* q_scale, const float* w, const void* k, const float* k_scale,
+                       const int32_t* npool, float* scores, int64_t* pools, int64_t* cnt, float* vals, void* workspace,
+                       size_t workspace_bytes, int N, int Hi, int D, int P, int score_stride, int keep, float scale,
+                       void* stream) {
+  if (!q || !w || !k || !npool || !scores || !pools || !cnt || !vals || !workspace) return DSA_EINVAL;
   if (N < 0 || Hi < 1 || P < 1 || keep < 1 || score_stride < P || !(scale > 0.0f)) return DSA_EINVAL;
-  if (D != 128 || Hi > 64) return DSA_EUNSUPPORTED;
+  if (q_scale && !k_scale) return DSA_EUNSUPPORTED;  // FP8 queries take FP8 keys
+  if (D != 128 || Hi > (k_scale ? 64 : 32)) return DSA_EUNSUPPORTED;
   if (!dsa::topk_supported(P, keep, 1)) return DSA_EUNSUPPORTED;
   if (workspace_bytes < dsa_prefill_select_workspace_bytes(N, P, keep)) return DSA_EWORKSPACE;
   if (N == 0) return DSA_OK;
@@ -207,11 +215,16 @@ int dsa_prefill_select(const void* q, const float* q_scale, const float* w, cons
   float* bm = fuse ? dsa::topk_bm_buffer(workspace, N) : nullptr;
   const int sub_log2 = fuse ? __builtin_ctz((unsigned)sub) : 0;
   const int nb = fuse ? (P + sub - 1) / sub : 0;
-  hipError_t e = q_scale ? dsa::launch_indexer_prefill_fp8(static_cast<const uint8_t*>(q), q_scale, w, k_fp8, k_scale,
-                                                           npool, scores, N, Hi, P, score_stride, scale, bm, sub_log2,
-                                                           nb, s)
-                         : dsa::launch_indexer_prefill(static_cast<const uint16_t*>(q), w, k_fp8, k_scale, npool,
-                                                       scores, N, Hi, P, score_stride, scale, bm, sub_log2, nb, s);
+  hipError_t e;
+  if (q_scale)
+    e = dsa::launch_indexer_prefill_fp8(static_cast<const uint8_t*>(q), q_scale, w, static_cast<const uint8_t*>(k),
+                                        k_scale, npool, scores, N, Hi, P, score_stride, scale, bm, sub_log2, nb, s);
+  else if (k_scale)
+    e = dsa::launch_indexer_prefill(static_cast<const uint16_t*>(q), w, static_cast<const uint8_t*>(k), k_scale, npool,
+                                    scores, N, Hi, P, score_stride, scale, bm, sub_log2, nb, s);
+  else
+    e = dsa::launch_indexer_prefill_bf16k(static_cast<const uint16_t*>(q), w, static_cast<const uint16_t*>(k), npool,
+                                          scores, N, Hi, P, score_stride, scale, bm, sub_log2, nb, s);
   if (e != hipSuccess) return DSA_ELAUNCH;
   return status(dsa::launch_prefill_topk(scores, npool, idx, cnt32, workspace, N, score_stride, P, keep, fuse, pools,
                                          cnt, vals, s));
@@ -377,6 +390,37 @@ int dsa_decode_layer(const void* q_idx_bf16, const float* w, const uint8_t* k_fp
   return status(dsa::launch_sparse_mla(static_cast<const uint16_t*>(q_bf16), kv_fp8, kv_scale, nullptr, cnt, nullptr,
                                        rows, nullptr, static_cast<uint16_t*>(out_bf16), nullptr, lse, aws, B, H, 576,
                                        keep, max_pages, page_size, num_pages, scale, sp, s));
+}
+
+size_t dsa_sparse_mla_pooled_workspace_bytes(int B, int H, int keep, int kp, int splits) {
+  if (B < 0 || H < 16 || keep < 1 || kp < 2) return 0;
+  const int keep_tok = kp * (keep + 1);
+  return align256(dsa::attention_workspace_bytes(B, H, effective_splits(resolve_splits(splits, B, H, keep_tok),
+                                                                          keep_tok)));
+}
+
+int dsa_sparse_mla_pooled(const void* q_bf16, const uint8_t* kv_fp8, const float* kv_scale, const int32_t* pools,
+                          const int32_t* cnt, const int32_t* npool, const int32_t* positions, const int32_t* page_table,
+                          void* out_bf16, float* out_f32, float* lse, void* workspace, size_t workspace_bytes, int B,
+                          int H, int Dqk, int keep, int kp, int max_pages, int page_size, int num_pages, float scale,
+                          int splits, void* stream) {
+  if (!q_bf16 || !kv_fp8 || !kv_scale || !pools || !cnt || !npool || !positions || !page_table) return DSA_EINVAL;
+  if (!out_bf16 && !out_f32) return DSA_EINVAL;
+  if (B < 0 || H < 1 || keep < 1 || max_pages < 1 || page_size < 1 || num_pages < 1) return DSA_EINVAL;
+  if (kp < 2 || kp > 8 || (kp & (kp - 1)) || page_size % kp) return DSA_EUNSUPPORTED;
+  if ((Dqk != 576 && Dqk != 512) || H % 16) return DSA_EUNSUPPORTED;
+  if ((long)num_pages * page_size > 0x7fffffffL) return DSA_EUNSUPPORTED;
+  if (B == 0) return DSA_OK;
+  const int keep_tok = kp * (keep + 1);
+  const int sp = effective_splits(resolve_splits(splits, B, H, keep_tok), keep_tok);
+  const size_t need = dsa::attention_workspace_bytes(B, H, sp);
+  if (need && (!workspace || workspace_bytes < need)) return DSA_EWORKSPACE;
+  const dsa::PoolForm pf = {__builtin_ctz((unsigned)kp), keep, npool, positions};
+  const bool wide = sp == 1 && dsa::attention_wide_ok(B, H, keep_tok, false, num_cu());
+  return status(dsa::launch_sparse_mla(static_cast<const uint16_t*>(q_bf16), kv_fp8, kv_scale, pools, cnt, page_table,
+                                       nullptr, nullptr, static_cast<uint16_t*>(out_bf16), out_f32, lse, workspace, B,
+                                       H, Dqk, keep_tok, max_pages, page_size, num_pages, scale, sp,
+                                       static_cast<hipStream_t>(stream), pf, wide));
 }
 
 size_t dsa_pooled_workspace_bytes(int B, int H, int keep, int max_len, int kp, int splits) {

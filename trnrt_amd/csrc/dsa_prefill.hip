@@ -56,11 +56,16 @@ __device__ __forceinline__ void block_max_rows(const float* srow, int base, floa
   }
 }
 
-template <int MT>
+// BF16K: the keys are bf16 [P, 128] with no per-key scale (GLM's pool keys, trnrt/models/dsa_long.py:74-84 over
+// trnrt/models/mla.py:491-503 `context_pool_keys`): a thread's share of a tile is 32 bytes (two loads) that go to
+// LDS as they are, so the ring holds twice the registers (taken at MT 1 only).
+template <int MT, bool BF16K>
 __global__ __launch_bounds__(PF_THREADS, 2) void indexer_prefill_kernel(
-    const uint16_t* __restrict__ q, const float* __restrict__ w, const uint8_t* __restrict__ kcache,
+    const uint16_t* __restrict__ q, const float* __restrict__ w, const void* __restrict__ kcache_v,
     const float* __restrict__ kscale, const int* __restrict__ npool, float* __restrict__ scores, int N, int Hi, int P,
     int stride, float scale, float* __restrict__ bm, int sub_log2, int nb) {
+  static_assert(!BF16K || MT == 1, "bf16 keys: up to 32 heads");
+  const uint8_t* kcache = static_cast<const uint8_t*>(kcache_v);
   // two rounds of bf16 tiles (key j of a tile: 16 pieces of 8 dims, piece p at slot 16 j + (p ^ (j & 15))), the
   // block's per-key scales and the queries' candidate counts
   __shared__ u32x4 kb[2][PF_TPB][PF_TILE * 16];
@@ -80,17 +85,21 @@ __global__ __launch_bounds__(PF_THREADS, 2) void indexer_prefill_kernel(
   // Tiles are prefetched PF_RING ahead into a ring of registers that is never copied (a copy of a register whose
   // load is in flight waits for it): every loop turn below is unrolled, so each slot is a fixed register.
   const int tk = threadIdx.x >> 3, tp = threadIdx.x & 7;
-  auto load_tile = [&](int it) {
+  constexpr int KB = BF16K ? 2 * PF_D : PF_D;  // key row bytes
+  auto load_tile = [&](int it, int half) {
     const int key = min(p_begin + it * PF_TILE + tk, P - 1);  // in range whatever the block
-    return *reinterpret_cast<const u32x4*>(kcache + (size_t)key * PF_D + 16 * tp);
+    return *reinterpret_cast<const u32x4*>(kcache + (size_t)key * KB + (BF16K ? 32 * tp + 16 * half : 16 * tp));
   };
-  u32x4 ring[PF_RING];
+  u32x4 ring[PF_RING], ring2[BF16K ? PF_RING : 1];
 #pragma unroll
-  for (int u = 0; u < PF_RING; ++u) ring[u] = load_tile(u);
+  for (int u = 0; u < PF_RING; ++u) {
+    ring[u] = load_tile(u, 0);
+    if (BF16K) ring2[u] = load_tile(u, 1);
+  }
 #pragma unroll
   for (int i = 0; i < PF_TILES * PF_TILE / PF_THREADS; ++i) {
     const int k = i * PF_THREADS + threadIdx.x;
-    ksc_s[k] = kscale[min(p_begin + k, P - 1)];
+    ksc_s[k] = BF16K ? 1.0f : kscale[min(p_begin + k, P - 1)];
   }
 
   int L = min(max(npool[nq], 0), P);
@@ -172,10 +181,16 @@ __global__ __launch_bounds__(PF_THREADS, 2) void indexer_prefill_kernel(
 #pragma unroll
     for (int u = 0; u < PF_TPB; ++u) {
       const u32x4 r = ring[U0 + u];
-      const bf16x8 lo = fp8x8_to_bf16x8(r[0], r[1]), hi = fp8x8_to_bf16x8(r[2], r[3]);
-      tiles[u][16 * tk + ((2 * tp) ^ (tk & 15))] = __builtin_bit_cast(u32x4, lo);
-      tiles[u][16 * tk + ((2 * tp + 1) ^ (tk & 15))] = __builtin_bit_cast(u32x4, hi);
-      ring[U0 + u] = load_tile(t0 + u + PF_RING);
+      if (BF16K) {
+        tiles[u][16 * tk + ((2 * tp) ^ (tk & 15))] = r;
+        tiles[u][16 * tk + ((2 * tp + 1) ^ (tk & 15))] = ring2[U0 + u];
+        ring2[U0 + u] = load_tile(t0 + u + PF_RING, 1);
+      } else {
+        const bf16x8 lo = fp8x8_to_bf16x8(r[0], r[1]), hi = fp8x8_to_bf16x8(r[2], r[3]);
+        tiles[u][16 * tk + ((2 * tp) ^ (tk & 15))] = __builtin_bit_cast(u32x4, lo);
+        tiles[u][16 * tk + ((2 * tp + 1) ^ (tk & 15))] = __builtin_bit_cast(u32x4, hi);
+      }
+      ring[U0 + u] = load_tile(t0 + u + PF_RING, 0);
     }
     __syncthreads();  // the round is in LDS; the other round's buffers are free (every wave finished them)
 #pragma unroll
@@ -348,21 +363,30 @@ __global__ __launch_bounds__(PF_THREADS, 2) void indexer_prefill_fp8_kernel(
   if (bm && n < N) block_max_rows(sc_s[wave], p_begin, bm + (size_t)n * nb, p_begin, p_end, sub_log2, nb, true, lane);
 }
 
-template <int MT>
-static hipError_t launch_prefill_mt(const uint16_t* q, const float* w, const uint8_t* k, const float* ks,
+template <int MT, bool BF16K>
+static hipError_t launch_prefill_mt(const uint16_t* q, const float* w, const void* k, const float* ks,
                                     const int* npool, float* scores, int N, int Hi, int P, int stride, float scale,
                                     float* bm, int sub_log2, int nb, hipStream_t s) {
   const dim3 grid((N + PF_QPW - 1) / PF_QPW, (stride + PF_TILES * PF_TILE - 1) / (PF_TILES * PF_TILE));
-  return launch("indexer_prefill_kernel", indexer_prefill_kernel<MT>, grid, dim3(PF_THREADS), s, q, w, k, ks, npool,
-                scores, N, Hi, P, stride, scale, bm, sub_log2, nb);
+  return launch("indexer_prefill_kernel", indexer_prefill_kernel<MT, BF16K>, grid, dim3(PF_THREADS), s, q, w, k, ks,
+                npool, scores, N, Hi, P, stride, scale, bm, sub_log2, nb);
 }
 
 // bm (or null): also the sub-block maxima of 2^sub_log2 scores, [N, nb].
 hipError_t launch_indexer_prefill(const uint16_t* q, const float* w, const uint8_t* k, const float* ks,
                                   const int* npool, float* scores, int N, int Hi, int P, int stride, float scale,
                                   float* bm, int sub_log2, int nb, hipStream_t s) {
-  if (Hi <= 32) return launch_prefill_mt<1>(q, w, k, ks, npool, scores, N, Hi, P, stride, scale, bm, sub_log2, nb, s);
-  return launch_prefill_mt<2>(q, w, k, ks, npool, scores, N, Hi, P, stride, scale, bm, sub_log2, nb, s);
+  if (Hi <= 32)
+    return launch_prefill_mt<1, false>(q, w, k, ks, npool, scores, N, Hi, P, stride, scale, bm, sub_log2, nb, s);
+  return launch_prefill_mt<2, false>(q, w, k, ks, npool, scores, N, Hi, P, stride, scale, bm, sub_log2, nb, s);
+}
+
+// bf16 keys without scales (Hi <= 32).
+hipError_t launch_indexer_prefill_bf16k(const uint16_t* q, const float* w, const uint16_t* k, const int* npool,
+                                        float* scores, int N, int Hi, int P, int stride, float scale, float* bm,
+                                        int sub_log2, int nb, hipStream_t s) {
+  if (Hi > 32) return hipErrorInvalidValue;
+  return launch_prefill_mt<1, true>(q, w, k, nullptr, npool, scores, N, Hi, P, stride, scale, bm, sub_log2, nb, s);
 }
 
 }  // namespace dsa

@@ -45,13 +45,28 @@ def pick_sub(P: int, keep: int) -> int:
     return 0
 
 
+def _keys(pk: torch.Tensor, pk_scale: torch.Tensor | None, fp8_q: bool):
+    """(key tensor for the C ABI, its scales or None): e4m3fn keys (or their uint8 bits) with pk_scale [P] fp32, or
+    bf16 keys without scales (GLM's pool keys, bf16 queries only)."""
+    if pk.dtype == torch.bfloat16:
+        if pk_scale is not None:
+            raise ValueError("dsa_long_select: bf16 keys take no pk_scale")
+        if fp8_q:
+            raise NotImplementedError("dsa_long_select: FP8 queries take FP8 keys")
+        return pk.contiguous(), None
+    if pk_scale is None:
+        raise ValueError("dsa_long_select: FP8 keys need pk_scale")
+    return C.fp8_bytes(pk, "pk"), pk_scale
+
+
 def scores(qI: torch.Tensor, w: torch.Tensor, pk: torch.Tensor, npool: torch.Tensor, scale: float, *,
-           pk_scale: torch.Tensor, qI_scale: torch.Tensor | None = None, stride: int | None = None,
+           pk_scale: torch.Tensor | None = None, qI_scale: torch.Tensor | None = None, stride: int | None = None,
            out: torch.Tensor | None = None) -> torch.Tensor:
     """[N, stride] fp32 index scores (NEG_INF at p >= npool[n] and past P): qI [N, Hi, 128] bf16, or e4m3fn (its
     uint8 bits) with qI_scale [N, Hi] fp32 > 0 (the queries are qI * qI_scale), w [N, Hi] fp32, pk [P, 128] e4m3fn
-    keys (or their uint8 bits) with pk_scale [P] fp32, npool [N] int (clamped to [0, P]), scale > 0
-    (trnrt/kernels/dsa_long_select.py:119-133 `emulate_scores`)."""
+    keys (or their uint8 bits) with pk_scale [P] fp32, or bf16 keys with no scale (GLM's pool keys; bf16 queries,
+    Hi <= 32), npool [N] int (clamped to [0, P]), scale > 0 (trnrt/kernels/dsa_long_select.py:119-133
+    `emulate_scores`)."""
     dev = C.on_gpu(qI, w, pk, pk_scale, npool, qI_scale, out)
     fp8_q = qI.dtype in (C.FP8, torch.uint8)
     if fp8_q != (qI_scale is not None):
@@ -59,7 +74,7 @@ def scores(qI: torch.Tensor, w: torch.Tensor, pk: torch.Tensor, npool: torch.Ten
     if qI.dim() != 3:
         raise ValueError(f"dsa_long_select: qI {tuple(qI.shape)}, expected [N, Hi, {D}]")
     N, Hi, Dq = qI.shape
-    pk = C.fp8_bytes(pk, "pk")
+    pk, pk_scale = _keys(pk, pk_scale, fp8_q)
     if pk.dim() != 2:
         raise ValueError(f"dsa_long_select: pk {tuple(pk.shape)}, expected [P, {D}]")
     P = pk.shape[0]
@@ -71,8 +86,11 @@ def scores(qI: torch.Tensor, w: torch.Tensor, pk: torch.Tensor, npool: torch.Ten
     stride = P if stride is None else int(stride)
     if stride < P:
         raise ValueError(f"dsa_long_select: stride {stride} < {P} keys")
+    if pk_scale is None and Hi > 32:
+        raise NotImplementedError(f"dsa_long_select: {Hi} heads over bf16 keys (the kernel takes up to 32)")
     w = C.need(C.as_f32(w), "w", torch.float32, (N, Hi))
-    pk_scale = C.need(C.as_f32(pk_scale).reshape(-1), "pk_scale", torch.float32, (P,))
+    if pk_scale is not None:
+        pk_scale = C.need(C.as_f32(pk_scale).reshape(-1), "pk_scale", torch.float32, (P,))
     npool = C.need(C.as_i32(npool.reshape(-1).clamp(0, P)), "npool", torch.int32, (N,))
     if out is None:
         out = torch.empty(N, stride, dtype=torch.float32, device=dev)
@@ -105,7 +123,7 @@ def value_order(pools: torch.Tensor, cnt: torch.Tensor, vals: torch.Tensor):
 
 
 def select(qI: torch.Tensor, w: torch.Tensor, pk: torch.Tensor, npool: torch.Tensor, keep: int, scale: float,
-           sub: int | None = None, vorder: bool = False, *, pk_scale: torch.Tensor,
+           sub: int | None = None, vorder: bool = False, *, pk_scale: torch.Tensor | None = None,
            qI_scale: torch.Tensor | None = None,
            workspace: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """(pools [N, keep] int64 ascending, 0 past the count; count [N] int64; scores [N, keep] fp32, NEG_INF past the
@@ -123,13 +141,14 @@ def select(qI: torch.Tensor, w: torch.Tensor, pk: torch.Tensor, npool: torch.Ten
         raise ValueError(f"dsa_long_select: qI {tuple(qI.shape)}, pk {tuple(pk.shape)}")
     N, Hi, Dq = qI.shape
     P = pk.shape[0]
-    if not supported(Hi, Dq, P, keep) or pk.shape[1] != D:
+    pk, pk_scale = _keys(pk, pk_scale, fp8_q)
+    if not supported(Hi, Dq, P, keep) or pk.shape[1] != D or (pk_scale is None and Hi > 32):
         raise NotImplementedError(f"dsa_long_select: Hi {Hi}, D {Dq}, P {P}, keep {keep}")
     if not scale > 0:
         raise ValueError(f"dsa_long_select: scale {scale} must be positive")
-    pk = C.fp8_bytes(pk, "pk")
     w = C.need(C.as_f32(w), "w", torch.float32, (N, Hi))
-    pk_scale = C.need(C.as_f32(pk_scale).reshape(-1), "pk_scale", torch.float32, (P,))
+    if pk_scale is not None:
+        pk_scale = C.need(C.as_f32(pk_scale).reshape(-1), "pk_scale", torch.float32, (P,))
     npool = C.need(C.as_i32(npool.reshape(-1)), "npool", torch.int32, (N,))  # clamped to [0, P] by the kernels
     if fp8_q:
         qI = C.fp8_bytes(qI, "qI")

@@ -8,6 +8,7 @@ and chunked-prefill paths call; a candidate is one token at kpool 1, a pool of k
 - slots: selected pools -> cache pool rows and the 0 / NEG_INF bias with the query's tail pool
   (trnrt/models/dsa_long.py:189-215, any kpool);
 - attend: absorbed MLA over the slots (trnrt/models/dsa_long.py:218-223);
+- attend_pooled: slots + attend of a pooled selection in one kernel (no slot rows materialised);
 - decode_pooled: a pooled (GLM) decode batch through all four over the bf16 pool-key cache
   (trnrt/models/mla.py:505-526 `attention_long`).
 """
@@ -33,11 +34,13 @@ def npools(positions: torch.Tensor, kp: int) -> torch.Tensor:
 
 
 def scores(qI: torch.Tensor, w: torch.Tensor, pk: torch.Tensor, npool: torch.Tensor, scale: float, *,
-           pk_scale: torch.Tensor) -> torch.Tensor:
+           pk_scale: torch.Tensor | None = None) -> torch.Tensor:
     """[N, P] fp32: every key's index score, NEG_INF for the non-candidates (p >= npool) (trnrt/models/dsa_long.py:
-    74-84). qI [N, Hi, 128] bf16, w [N, Hi] fp32, pk the FP8 e4m3 keys: [P, 128] (one sequence: a prefill chunk) or
-    [N, P, 128] (one context per row: a decode batch), pk_scale their per-token fp32 scales ([P] or [N, P]), npool
-    [N]. The decode form needs P a multiple of 32 (each row's keys are one page of the decode indexer)."""
+    74-84). qI [N, Hi, 128] bf16, w [N, Hi] fp32, pk the FP8 e4m3 keys with pk_scale their per-token fp32 scales, or
+    a chunk's bf16 pool keys [P, 128] (GLM's context_pool_keys, trnrt/models/mla.py:491-503) with no scale:
+    [P, 128] (one sequence: a prefill chunk) or [N, P, 128] (one context per row: a decode batch, FP8), pk_scale [P]
+    or [N, P], npool [N]. The decode form needs P a multiple of 32 (each row's keys are one page of the decode
+    indexer)."""
     if pk.dim() == 2:
         return dsa_long_select.scores(qI, w, pk, npool, scale, pk_scale=pk_scale)
     if pk.dim() != 3 or pk.shape[0] != qI.shape[0]:
@@ -48,8 +51,8 @@ def scores(qI: torch.Tensor, w: torch.Tensor, pk: torch.Tensor, npool: torch.Ten
     dev = C.on_gpu(qI, w, pk, pk_scale, npool)
     table = torch.arange(N, dtype=torch.int32, device=dev).view(N, 1)
     lens = npool.reshape(-1).clamp(0, P).to(torch.int32)
-    return dsa_index.decode_scores(qI, w.float() * float(scale), pk.reshape(N * P, -1), pk_scale.reshape(-1), table,
-                                   lens, P, P)
+    ks = None if pk_scale is None else pk_scale.reshape(-1)
+    return dsa_index.decode_scores(qI, w.float() * float(scale), pk.reshape(N * P, -1), ks, table, lens, P, P)
 
 
 def select_device(sc: torch.Tensor, keep: int, lengths: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
@@ -99,6 +102,49 @@ def attend(q_lat: torch.Tensor, kc: torch.Tensor, rows: torch.Tensor, bias: torc
            kc_scale: torch.Tensor) -> torch.Tensor:
     """o [N, H, 512] fp32: absorbed MLA of N queries over their slots (trnrt/models/dsa_long.py:218-223)."""
     return dsa_decode.attend(q_lat, kc, rows, bias, scale, kc_scale=kc_scale)
+
+
+def attend_pooled(q_lat: torch.Tensor, kc: torch.Tensor, kc_scale: torch.Tensor, pools: torch.Tensor,
+                  cnt: torch.Tensor, npool: torch.Tensor, positions: torch.Tensor, table: torch.Tensor,
+                  page_size: int, kp: int, scale: float, *, lse: bool = False,
+                  workspace: torch.Tensor | None = None):
+    """attend(slots(...)) in one kernel (trnrt/models/dsa_long.py:189-223): absorbed MLA of N queries over the kp
+    tokens of each of their selected pools (pools [N, keep] ascending, cnt [N] valid) and the tail tokens
+    kp npool .. positions[n] of their incomplete pool, read through the page table ([Pp] shared, or [N, Pp]); the
+    slot rows and biases are never materialised. q_lat [N, H, R] bf16 (R 512 or 576), kc [slots, R] e4m3fn with
+    kc_scale [slots]. Returns o [N, H, 512] fp32 (and lse [N, H] with lse). workspace: the split partials
+    (dsa_sparse_mla_pooled_workspace_bytes), allocated here when not given."""
+    N, keep = pools.shape
+    if kp < 2 or kp & (kp - 1) or page_size % kp:
+        raise ValueError(f"attend_pooled: kpool {kp} with pages of {page_size}")
+    dev = C.on_gpu(q_lat, kc, kc_scale, pools, cnt, npool, positions, table)
+    if q_lat.dim() != 3 or q_lat.shape[0] != N or q_lat.shape[2] not in dsa_decode.DQK_WIDTHS:
+        raise ValueError(f"attend_pooled: q_lat {tuple(q_lat.shape)} for {N} queries")
+    H, dqk = q_lat.shape[1], q_lat.shape[2]
+    q = C.as_bf16(q_lat)
+    kv = C.fp8_bytes(kc, "kc").reshape(-1, dqk)
+    slots_n = kv.shape[0]
+    ks = C.need(C.as_f32(kc_scale).reshape(-1), "kc_scale", torch.float32, (slots_n,))
+    pl = C.need(C.as_i32(pools), "pools", torch.int32, (N, keep))
+    cn = C.need(C.as_i32(cnt.reshape(-1)), "cnt", torch.int32, (N,))
+    npl = C.need(C.as_i32(npool.reshape(-1)), "npool", torch.int32, (N,))
+    pos = C.need(C.as_i32(positions.reshape(-1)), "positions", torch.int32, (N,))
+    tb = C.as_i32(table)
+    tb = tb.view(1, -1).expand(N, -1).contiguous() if tb.dim() == 1 else tb
+    if tb.shape[0] != N:
+        raise ValueError(f"attend_pooled: table {tuple(table.shape)} for {N} queries")
+    if slots_n % page_size:
+        raise ValueError(f"attend_pooled: {slots_n} cache slots are not whole pages of {page_size}")
+    out = torch.empty(N, H, dsa_decode.DV, dtype=torch.float32, device=dev)
+    ls = torch.empty(N, H, dtype=torch.float32, device=dev) if lse else None
+    lib = _lib.lib()
+    wsb = int(lib.dsa_sparse_mla_pooled_workspace_bytes(N, H, keep, kp, 0))
+    ws = workspace if workspace is not None else torch.empty(max(wsb, 256), dtype=torch.uint8, device=dev)
+    st = lib.dsa_sparse_mla_pooled(C.ptr(q), C.ptr(kv), C.ptr(ks), C.ptr(pl), C.ptr(cn), C.ptr(npl), C.ptr(pos),
+                                   C.ptr(tb), None, C.ptr(out), C.ptr(ls), C.ptr(ws), ws.numel(), N, H, dqk, keep, kp,
+                                   tb.shape[1], page_size, slots_n // page_size, float(scale), 0, C.stream_ptr(dev))
+    _lib.check(st, "dsa_long.attend_pooled")
+    return (out, ls) if lse else out
 
 
 def decode_pooled(q_idx: torch.Tensor, w: torch.Tensor, pool_key: torch.Tensor, q_lat: torch.Tensor,

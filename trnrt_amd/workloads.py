@@ -363,3 +363,92 @@ def make_pooled_inputs(cfg: PooledConfig, seed: int = 0, device: str | torch.dev
         sm = tb.long().gather(1, (pos // ps).view(-1, 1)).view(-1) * ps + pos % ps
         dsa_cache.write_pool_keys(pool_key, rows, pos, tb, sm, ape, ps, cfg.kp, rows_scale=rs)
     return inp
+
+
+# -- GLM-5.3-Flash's pooled chunked prefill (trnrt/models/mla.py:505-526 `attention_long` for a chunk) --------------
+
+
+@dataclass(frozen=True)
+class PooledPrefillConfig:
+    """A GLM-5.3-Flash prefill chunk over a long context: `chunk` new queries after `cached` tokens, a 32-head indexer
+    over the context's bf16 pool keys (kpool 4), the top 512 pools per query plus its tail, 64 heads of absorbed MLA
+    over the 512-wide NoPE latent."""
+    name: str
+    cached: int
+    chunk: int
+    Hi: int = 32
+    H: int = 64
+    kp: int = 4
+    topk: int = 2048
+    D: int = 128
+    dqk: int = 512
+    page_size: int = 64
+
+    @property
+    def keep(self) -> int:
+        return self.topk // self.kp
+
+    @property
+    def L(self) -> int:
+        return self.cached + self.chunk
+
+    @property
+    def P(self) -> int:  # pools of the context
+        return math.ceil(self.L / self.kp)
+
+    @property
+    def scale(self) -> float:  # index_head_dim ** -0.5
+        return self.D ** -0.5
+
+    @property
+    def softmax_scale(self) -> float:  # qk_nope_head_dim ** -0.5
+        return 256 ** -0.5
+
+
+POOLED_PREFILL_CONFIGS = {
+    7: PooledPrefillConfig("glm-prefill-65536+2048", cached=65536, chunk=2048),
+}
+
+
+@dataclass
+class PooledPrefillInputs:
+    cfg: PooledPrefillConfig
+    qI: torch.Tensor  # [C, Hi, 128] bf16
+    w: torch.Tensor  # [C, Hi] fp32 head weights
+    pk: torch.Tensor  # [P, 128] bf16: the context's pool keys in pool order (context_pool_keys)
+    positions: torch.Tensor  # [C] int32
+    npool: torch.Tensor  # [C] int32 complete pools per query
+    q: torch.Tensor  # [C, H, 512] bf16 absorbed queries
+    kv_cache: torch.Tensor  # [slots, 512] e4m3fn latent rows
+    kv_scale: torch.Tensor  # [slots] fp32
+    table: torch.Tensor  # [pages] int32 the sequence's block table
+
+    def to(self, device) -> "PooledPrefillInputs":
+        kw = {k: (v.to(device) if isinstance(v, torch.Tensor) else v) for k, v in self.__dict__.items()}
+        return PooledPrefillInputs(**kw)
+
+
+def make_pooled_prefill_inputs(cfg: PooledPrefillConfig, seed: int = 0, device: str | torch.device = "cpu",
+                               chunk: int = 65536) -> PooledPrefillInputs:
+    """Seeded inputs of one pooled chunk: pool keys ~N(0, 1) in bf16, queries ~N(0, 1) in bf16, weights ~N(0, 1/16),
+    latent rows ~N(0, 1) quantised per token to e4m3fn, the sequence's pages in a random order; query i at position
+    cached + i."""
+    device = torch.device(device)
+    g = _gen(device)
+    g.manual_seed(seed)
+    C, P, ps = cfg.chunk, cfg.P, cfg.page_size
+    qI = torch.randn(C, cfg.Hi, cfg.D, generator=g, device=device).to(torch.bfloat16)
+    w = torch.randn(C, cfg.Hi, generator=g, device=device) * 0.25
+    pk = torch.randn(P, cfg.D, generator=g, device=device).to(torch.bfloat16)
+    positions = (cfg.cached + torch.arange(C, device=device)).to(torch.int32)
+    npool = torch.div(positions + 1, cfg.kp, rounding_mode="floor").to(torch.int32)
+    q = torch.randn(C, cfg.H, cfg.dqk, generator=g, device=device).to(torch.bfloat16)
+    npg = math.ceil(cfg.L / ps)
+    table = (torch.randperm(npg, generator=g, device=device) + 1).to(torch.int32)
+    slots = (npg + 1) * ps
+    kv = torch.zeros(slots, cfg.dqk, dtype=FP8, device=device)
+    ks = torch.ones(slots, dtype=torch.float32, device=device)
+    for s0 in range(ps, slots, chunk):
+        n = min(chunk, slots - s0)
+        kv[s0:s0 + n], ks[s0:s0 + n] = quantize_rows(torch.randn(n, cfg.dqk, generator=g, device=device))
+    return PooledPrefillInputs(cfg, qI, w, pk, positions, npool, q, kv, ks, table)
