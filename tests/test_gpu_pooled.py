@@ -61,6 +61,38 @@ def test_pooled_attention_vs_oracle():
     assert_attention_close(o, ref)
 
 
+@pytest.mark.parametrize("kp,dqk", [(2, 576), (4, 512), (8, 512), (8, 576)])
+def test_attend_pooled_tails_vs_oracle(kp, dqk):
+    """dsa_long.attend_pooled (selected pools and the tail read through the page table) over rows with every tail
+    length 0 .. kp - 1, fewer selected pools than keep, and no complete pool, against the oracle over the slots of
+    the reference's own arithmetic (pool_slots_ref). The split form adds the tail in the workgroup that holds a
+    row's last slot; at kp 8 with 576-wide rows it keeps the tail among the slots instead: both are covered, with
+    several splits per row and with lse."""
+    say(f"attend_pooled tails kp={kp} dqk={dqk}")
+    g = torch.Generator().manual_seed(kp * 1000 + dqk)
+    L, ps, H = 2048, 64, 32
+    keep = 512 // kp
+    pos = [L - 1, L - 2, 1000, kp * keep + 3, 77, kp - 2, 2 * kp - 1, 1500 + kp // 2]
+    B = len(pos)
+    positions = torch.tensor(pos)
+    npg = L // ps
+    num_pages = 1 + B * npg
+    kv, ks = W.quantize_rows(torch.randn(num_pages * ps, dqk, generator=g))
+    table = (torch.randperm(num_pages - 1, generator=g)[: B * npg] + 1).view(B, npg).to(torch.int32)
+    q = torch.randn(B, H, dqk, generator=g).to(torch.bfloat16)
+    pools, cnt, npool = _selection(B, L, kp, keep, positions, seed=kp + dqk)
+    tails = (positions + 1 - npool * kp).tolist()
+    assert set(tails) == (set(range(kp)) if kp < 8 else {0, 1, 4, 6, 7})
+    o, lse = dsa_long.attend_pooled(q.cuda(), kv.cuda(), ks.cuda(), pools.cuda(), cnt.cuda(), npool.cuda(),
+                                    positions.cuda(), table.cuda(), ps, kp, 192 ** -0.5, lse=True)
+    torch.cuda.synchronize()
+    want_r, want_b = O.pool_slots_ref(pools, cnt, npool, positions, table, ps, kp, keep + 1)
+    tok = (want_r.unsqueeze(-1) * kp + torch.arange(kp)).reshape(B, -1)
+    want_o, want_lse = O.sparse_mla_slots_ref(q, kv, ks, tok, want_b.reshape(B, -1), 192 ** -0.5)
+    assert_attention_close(o, want_o)
+    assert torch.allclose(lse.cpu(), want_lse, atol=2e-3, rtol=1e-4)
+
+
 def _pool_setup(seed, fp8_rows, B=3, L=1024, ps=64, kp=4):
     """A GLM-like pooled cache: per token an indexer row [key 128 | gate logits 128] (bf16, or e4m3 with per-token
     scales), B sequences of L tokens through random page tables, and an empty pool-key cache."""

@@ -394,9 +394,9 @@ int dsa_decode_layer(const void* q_idx_bf16, const float* w, const uint8_t* k_fp
 
 size_t dsa_sparse_mla_pooled_workspace_bytes(int B, int H, int keep, int kp, int splits) {
   if (B < 0 || H < 16 || keep < 1 || kp < 2) return 0;
-  const int keep_tok = kp * (keep + 1);
-  return align256(dsa::attention_workspace_bytes(B, H, effective_splits(resolve_splits(splits, B, H, keep_tok),
-                                                                          keep_tok)));
+  const int keep_sel = kp * keep;  // the selected pools' token slots; the tail comes on top
+  return align256(dsa::attention_workspace_bytes(B, H, effective_splits(resolve_splits(splits, B, H, keep_sel),
+                                                                          keep_sel)));
 }
 
 int dsa_sparse_mla_pooled(const void* q_bf16, const uint8_t* kv_fp8, const float* kv_scale, const int32_t* pools,
@@ -411,22 +411,22 @@ int dsa_sparse_mla_pooled(const void* q_bf16, const uint8_t* kv_fp8, const float
   if ((Dqk != 576 && Dqk != 512) || H % 16) return DSA_EUNSUPPORTED;
   if ((long)num_pages * page_size > 0x7fffffffL) return DSA_EUNSUPPORTED;
   if (B == 0) return DSA_OK;
-  const int keep_tok = kp * (keep + 1);
-  const int sp = effective_splits(resolve_splits(splits, B, H, keep_tok), keep_tok);
+  const int keep_sel = kp * keep;  // the selected pools' token slots; the tail comes on top
+  const int sp = effective_splits(resolve_splits(splits, B, H, keep_sel), keep_sel);
   const size_t need = dsa::attention_workspace_bytes(B, H, sp);
   if (need && (!workspace || workspace_bytes < need)) return DSA_EWORKSPACE;
-  const dsa::PoolForm pf = {__builtin_ctz((unsigned)kp), keep, npool, positions};
-  const bool wide = sp == 1 && dsa::attention_wide_ok(B, H, keep_tok, false, num_cu());
+  const dsa::PoolForm pf = {__builtin_ctz((unsigned)kp), keep, npool, positions, 0};
+  const bool wide = sp == 1 && dsa::attention_wide_ok(B, H, keep_sel + kp, false, num_cu());
   return status(dsa::launch_sparse_mla(static_cast<const uint16_t*>(q_bf16), kv_fp8, kv_scale, pools, cnt, page_table,
                                        nullptr, nullptr, static_cast<uint16_t*>(out_bf16), out_f32, lse, workspace, B,
-                                       H, Dqk, keep_tok, max_pages, page_size, num_pages, scale, sp,
+                                       H, Dqk, keep_sel, max_pages, page_size, num_pages, scale, sp,
                                        static_cast<hipStream_t>(stream), pf, wide));
 }
 
 size_t dsa_pooled_workspace_bytes(int B, int H, int keep, int max_len, int kp, int splits) {
   if (B < 0 || H < 16 || keep < 1 || max_len < 1 || kp < 2) return 0;
-  const int keep_tok = kp * (keep + 1);
-  const int sp = effective_splits(resolve_splits(splits, B, H, keep_tok), keep_tok);
+  const int keep_sel = kp * keep;
+  const int sp = effective_splits(resolve_splits(splits, B, H, keep_sel), keep_sel);
   return align256(dsa::topk_workspace_bytes(B, max_len, keep)) + align256(dsa::attention_workspace_bytes(B, H, sp));
 }
 
@@ -461,12 +461,12 @@ int dsa_pooled_decode_layer(const void* q_idx_bf16, const float* w, const void* 
   e = dsa::launch_topk(scores, npool, pools, cnt, workspace, B, stride, stride, keep, 1, fused_hist, nullptr, 0, 0, 0,
                        nullptr, s);
   if (e != hipSuccess) return DSA_ELAUNCH;
-  const int keep_tok = kp * (keep + 1);
-  const int sp = effective_splits(resolve_splits(splits, B, H, keep_tok), keep_tok);
-  const dsa::PoolForm pf = {__builtin_ctz((unsigned)kp), keep, npool, positions};
+  const int keep_sel = kp * keep;  // the selected pools' token slots; the tail comes on top
+  const int sp = effective_splits(resolve_splits(splits, B, H, keep_sel), keep_sel);
+  const dsa::PoolForm pf = {__builtin_ctz((unsigned)kp), keep, npool, positions, 0};
   return status(dsa::launch_sparse_mla(static_cast<const uint16_t*>(q_bf16), kv_fp8, kv_scale, pools, cnt, page_table,
                                        nullptr, nullptr, static_cast<uint16_t*>(out_bf16), nullptr, lse,
-                                       static_cast<char*>(workspace) + t_need, B, H, Dqk, keep_tok, max_pages,
+                                       static_cast<char*>(workspace) + t_need, B, H, Dqk, keep_sel, max_pages,
                                        page_size, num_pages, scale, sp, s, pf));
 }
 

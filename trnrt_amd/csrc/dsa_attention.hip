@@ -42,6 +42,7 @@ constexpr int ATT_KROW = 16 * ATT_KPIECES;   // 592 bytes
 constexpr int ATT_CHUNK_BYTES = ATT_CH * ATT_KROW;  // 37,888: 37 direct-to-LDS instructions of 1 KiB
 constexpr int ATT_LOADS = ATT_NCH * ATT_KPIECES;    // 148 instructions per staged super-chunk
 constexpr int ATT_PROW = ATT_CH + 8;         // P row stride (bf16 elements; 16-byte aligned rows)
+constexpr int ATT_TAIL_BYTES = 3584;         // a pooled tail staged apart: 7 rows of 512 bytes or 6 of 576
 
 typedef int att_v2i __attribute__((ext_vector_type(2)));
 
@@ -53,6 +54,9 @@ struct AttShared {
   float bias[ATT_SUPER];
   float red[2][4][ATT_HPW];
   float ml[2][ATT_HPW];  // the second half's final max and sum per head, for the merge
+  int tslot[8];          // the pooled tail's cache slots (kpool <= 8: at most 7 tail tokens) and scales
+  float tks[8];
+  uint8_t trows[ATT_TAIL_BYTES];  // the pooled tail's rows, loaded with the first super-chunk's
 };
 
 // The value operand of v_mfma_f32_16x16x32_bf16 straight from the token-major tile: ds_read_b64_tr_b8 gives lane
@@ -103,6 +107,7 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void sparse_mla_kernel(
   int n_eff = keep;
   int cnt_b = keep;
   int pools_b = 0, tail_pool = 0;  // pooled form: selected pools, the tail pool
+  int tail_apart = 0;              // pooled form with the tail apart: the row's tail tokens
   if (cnt) {
     cnt_b = cnt[b];
     if (pf.kp_shift) {
@@ -110,12 +115,20 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void sparse_mla_kernel(
       pools_b = min(max(cnt_b, 0), pf.idx_stride);
       tail_pool = max(pf.npool[b], 0);
       const int tail = min(max(pf.positions[b] + 1 - (tail_pool << pf.kp_shift), 0), (1 << pf.kp_shift) - 1);
-      cnt_b = (pools_b << pf.kp_shift) + tail;
+      cnt_b = pools_b << pf.kp_shift;
+      if (pf.tail_apart)
+        tail_apart = tail;
+      else
+        cnt_b += tail;
     }
     if (!bias) n_eff = cnt_b < 1 ? 1 : (cnt_b > keep ? keep : cnt_b);  // cnt 0: attend slot 0, fully masked
   }
   const int k_begin = sp * slots_per_split;
   const int k_end = min(k_begin + slots_per_split, n_eff);
+  // the workgroup that holds the row's last slot (n_eff >= 1 here, so it has slots of its own) adds the tail as one
+  // more chunk: rows 0 .. tail_n - 1 of a zeroed tile, loaded into registers with its first super-chunk's rows
+  const int tail_n = (tail_apart > 0 && (n_eff - 1) / slots_per_split == sp) ? tail_apart : 0;
+  const int n_main = k_end > k_begin ? (k_end - k_begin + ATT_SUPER - 1) / ATT_SUPER : 0;
   const size_t nslots_cache = (size_t)num_pages * page_size;
 
   // the queries of the 16 heads (16 or 18 KiB), staged through LDS below
@@ -133,10 +146,93 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void sparse_mla_kernel(
   float l_run = 0.0f;       // this lane's share of the half's running sum of head l16
 
   const int* trow = table ? table + (size_t)b * max_pages : nullptr;
+  // one pair of staged chunks: half h takes chunk c0 + h of the nch staged (tile c, slots 64 c .. of the super-chunk)
+  auto chunk_pair = [&](int c0, int nch) __attribute__((always_inline)) {
+    const int c = c0 + half;  // this half's chunk of the pair
+    const bool live = c < nch;
+    const int cb = c * ATT_CH;
+    const uint8_t* kt = sh.kt[live ? c : 0];
+    float s4[4];
+    float alpha = 1.0f;
+    if (live) {
+      // scores of tokens 16 wh .. 16 wh + 15, heads l16 (two accumulators: independent MFMA chains)
+      f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
+      const uint8_t* kr = kt + (16 * wh + l16) * ATT_KROW + 8 * q4;
+#pragma unroll
+      for (int st = 0; st < STEPS; st += 2) {
+        const uint2 ka = *reinterpret_cast<const uint2*>(kr + 32 * st);
+        const uint2 kb = *reinterpret_cast<const uint2*>(kr + 32 * st + 32);
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16x8(ka.x, ka.y), qb[st], acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16x8(kb.x, kb.y), qb[st + 1], acc1, 0, 0, 0);
+      }
+      // acc[r] = S^T[token 16 wh + 4 q4 + r][head l16]
+      float mx = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int tk = cb + 16 * wh + 4 * q4 + r;
+        s4[r] = (acc0[r] + acc1[r]) * (sh.kscale[tk] * scale) + sh.bias[tk];
+        mx = fmaxf(mx, s4[r]);
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, WAVE));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
+      if (lane < ATT_HPW) sh.red[half][wh][lane] = mx;
+    }
+    __syncthreads();  // the chunk maxima
+    if (live) {
+      const float mc = fmaxf(fmaxf(sh.red[half][0][l16], sh.red[half][1][l16]),
+                             fmaxf(sh.red[half][2][l16], sh.red[half][3][l16]));
+      const float m_new = fmaxf(m_run, mc);
+      alpha = __expf(m_run - m_new);
+      m_run = m_new;
+      float psum = 0.0f;
+      uint32_t pk[2];
+#pragma unroll
+      for (int r = 0; r < 4; r += 2) {
+        const int tk = cb + 16 * wh + 4 * q4 + r;
+        const float p0 = __expf(s4[r] - m_new), p1 = __expf(s4[r + 1] - m_new);
+        psum += p0 + p1;
+        pk[r / 2] = (uint32_t)f32_to_bf16_bits(p0 * sh.kscale[tk]) |
+                    ((uint32_t)f32_to_bf16_bits(p1 * sh.kscale[tk + 1]) << 16);
+      }
+      l_run = l_run * alpha + psum;
+      *reinterpret_cast<uint2*>(&sh.p[half][l16 * ATT_PROW + 16 * wh + 4 * q4]) = make_uint2(pk[0], pk[1]);
+    }
+    __syncthreads();  // P complete (and every wave has read the maxima)
+    if (live) {
+      // rescale O (rows = heads 4 q4 + r) and accumulate P . V over the chunk's 64 tokens (dims 128 wh ..)
+      float al[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) al[r] = __shfl(alpha, 4 * q4 + r, WAVE);
+#pragma unroll
+      for (int n = 0; n < 8; ++n)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[n][r] *= al[r];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        // P operand: head l16, tokens 32 ks + 8 q4 .. + 7 (the value operand's k-slot order)
+        const bf16x8 pop =
+            as_bf16x8(*reinterpret_cast<const uint4*>(&sh.p[half][l16 * ATT_PROW + 32 * ks + 8 * q4]));
+#pragma unroll
+        for (int n = 0; n < 8; ++n)
+          o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pop, value_operand(kt, ks, 8 * wh + n, lane), o[n], 0, 0,
+                                                         0);
+      }
+    }
+    // the next pair's maxima and P are written after its first barrier, which every wave reaches only after
+    // this pair's P . V
+  };
   for (int sc0 = k_begin; sc0 < k_end; sc0 += ATT_SUPER) {
     const int nslots = min(ATT_SUPER, k_end - sc0);
     const int nch = (nslots + ATT_CH - 1) / ATT_CH;
+    const bool tail_thread = sc0 == k_begin && tid >= ATT_SUPER && tid - ATT_SUPER < tail_n;
     // slot ids and biases, one per thread of the first 256 (past the split: slot 0's row with weight exactly 0)
+    if (tail_thread) {
+      // the tail tokens' cache slots, with the first super-chunk's
+      const int pos = (tail_pool << pf.kp_shift) + (tid - ATT_SUPER);
+      int pi = pos / page_size;
+      pi = pi < max_pages ? pi : max_pages - 1;
+      sh.tslot[tid - ATT_SUPER] = safe_page(trow[pi], num_pages) * page_size + (pos - (pos / page_size) * page_size);
+    }
     if (tid < ATT_SUPER) {
       const int k = min(sc0 + tid, keep - 1);
       int slot;
@@ -206,86 +302,39 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void sparse_mla_kernel(
         }
       }
     }
-    const float ksc = tid < ATT_SUPER ? kvs[sh.slot[tid < nslots ? tid : 0]] : 0.0f;
-    __builtin_amdgcn_s_waitcnt(0);  // this thread's rows are in LDS
-    if (tid < ATT_SUPER) sh.kscale[tid] = ksc;
-    __syncthreads();  // every wave's rows are in LDS
-
-    for (int c0 = 0; c0 < nch; c0 += 2) {
-      const int c = c0 + half;  // this half's chunk of the pair
-      const bool live = c < nch;
-      const int cb = c * ATT_CH;
-      const uint8_t* kt = sh.kt[live ? c : 0];
-      float s4[4];
-      float alpha = 1.0f;
-      if (live) {
-        // scores of tokens 16 wh .. 16 wh + 15, heads l16 (two accumulators: independent MFMA chains)
-        f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
-        const uint8_t* kr = kt + (16 * wh + l16) * ATT_KROW + 8 * q4;
-#pragma unroll
-        for (int st = 0; st < STEPS; st += 2) {
-          const uint2 ka = *reinterpret_cast<const uint2*>(kr + 32 * st);
-          const uint2 kb = *reinterpret_cast<const uint2*>(kr + 32 * st + 32);
-          acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16x8(ka.x, ka.y), qb[st], acc0, 0, 0, 0);
-          acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16x8(kb.x, kb.y), qb[st + 1], acc1, 0, 0, 0);
-        }
-        // acc[r] = S^T[token 16 wh + 4 q4 + r][head l16]
-        float mx = -INFINITY;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int tk = cb + 16 * wh + 4 * q4 + r;
-          s4[r] = (acc0[r] + acc1[r]) * (sh.kscale[tk] * scale) + sh.bias[tk];
-          mx = fmaxf(mx, s4[r]);
-        }
-        mx = fmaxf(mx, __shfl_xor(mx, 16, WAVE));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
-        if (lane < ATT_HPW) sh.red[half][wh][lane] = mx;
-      }
-      __syncthreads();  // the chunk maxima
-      if (live) {
-        const float mc = fmaxf(fmaxf(sh.red[half][0][l16], sh.red[half][1][l16]),
-                               fmaxf(sh.red[half][2][l16], sh.red[half][3][l16]));
-        const float m_new = fmaxf(m_run, mc);
-        alpha = __expf(m_run - m_new);
-        m_run = m_new;
-        float psum = 0.0f;
-        uint32_t pk[2];
-#pragma unroll
-        for (int r = 0; r < 4; r += 2) {
-          const int tk = cb + 16 * wh + 4 * q4 + r;
-          const float p0 = __expf(s4[r] - m_new), p1 = __expf(s4[r + 1] - m_new);
-          psum += p0 + p1;
-          pk[r / 2] = (uint32_t)f32_to_bf16_bits(p0 * sh.kscale[tk]) |
-                      ((uint32_t)f32_to_bf16_bits(p1 * sh.kscale[tk + 1]) << 16);
-        }
-        l_run = l_run * alpha + psum;
-        *reinterpret_cast<uint2*>(&sh.p[half][l16 * ATT_PROW + 16 * wh + 4 * q4]) = make_uint2(pk[0], pk[1]);
-      }
-      __syncthreads();  // P complete (and every wave has read the maxima)
-      if (live) {
-        // rescale O (rows = heads 4 q4 + r) and accumulate P . V over the chunk's 64 tokens (dims 128 wh ..)
-        float al[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) al[r] = __shfl(alpha, 4 * q4 + r, WAVE);
-#pragma unroll
-        for (int n = 0; n < 8; ++n)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) o[n][r] *= al[r];
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          // P operand: head l16, tokens 32 ks + 8 q4 .. + 7 (the value operand's k-slot order)
-          const bf16x8 pop =
-              as_bf16x8(*reinterpret_cast<const uint4*>(&sh.p[half][l16 * ATT_PROW + 32 * ks + 8 * q4]));
-#pragma unroll
-          for (int n = 0; n < 8; ++n)
-            o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pop, value_operand(kt, ks, 8 * wh + n, lane), o[n], 0, 0,
-                                                           0);
-        }
-      }
-      // the next pair's maxima and P are written after its first barrier, which every wave reaches only after
-      // this pair's P . V
+    // the tail rows straight into their own LDS (rows of DQK bytes), beside the first super-chunk's rows: lane l of
+    // wave w < 4 loads piece 64 w + l of the tail
+    if (sc0 == k_begin && wave < 4) {
+      const int u = WAVE * wave + lane;
+      if (u < tail_n * ATT_PIECES)
+        __builtin_amdgcn_global_load_lds(kv + (size_t)sh.tslot[u / ATT_PIECES] * DQK + 16 * (u % ATT_PIECES),
+                                         (__attribute__((address_space(3))) void*)&sh.trows[1024 * wave], 16, 0, 0);
     }
+    const float ksc = tid < ATT_SUPER ? kvs[sh.slot[tid < nslots ? tid : 0]]
+                                      : (tail_thread ? kvs[sh.tslot[tid - ATT_SUPER]] : 0.0f);
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's rows are in LDS
+    if (tid < ATT_SUPER)
+      sh.kscale[tid] = ksc;
+    else if (tail_thread)
+      sh.tks[tid - ATT_SUPER] = ksc;
+    __syncthreads();  // every wave's rows are in LDS
+    for (int c0 = 0; c0 < nch; c0 += 2) chunk_pair(c0, nch);
     __syncthreads();  // the next super-chunk overwrites the staged rows and slots
+  }
+  if (tail_n > 0) {
+    // the tail chunk: its rows copied into tile 0, every other row of the tile zero (finite operands where the
+    // weight is 0), scales and biases for 64 slots
+    for (int i = tid; i < ATT_CH * ATT_KPIECES; i += ATT_THREADS)
+      if (i / ATT_KPIECES >= tail_n) *reinterpret_cast<u32x4*>(&sh.kt[0][16 * i]) = u32x4{0u, 0u, 0u, 0u};
+    if (tid < tail_n * ATT_PIECES)
+      *reinterpret_cast<u32x4*>(&sh.kt[0][(tid / ATT_PIECES) * ATT_KROW + 16 * (tid % ATT_PIECES)]) =
+          *reinterpret_cast<const u32x4*>(&sh.trows[16 * tid]);
+    if (tid < ATT_CH) {
+      sh.kscale[tid] = tid < tail_n ? sh.tks[tid] : 0.0f;
+      sh.bias[tid] = tid < tail_n ? 0.0f : -INFINITY;
+    }
+    __syncthreads();
+    chunk_pair(0, 1);
   }
 
   // each half's row sums: lane shares -> per wave -> per half
@@ -798,19 +847,28 @@ size_t attention_workspace_bytes(int B, int H, int splits) {
   return (size_t)B * splits * H * ATT_DV * 4 + (size_t)B * splits * H * 8 + 256;
 }
 
+// keep: slots per row; in the pooled form (pf.kp_shift > 0) kpool x pf.idx_stride, the selected pools' tokens, with
+// the row's tail tokens on top.
 hipError_t launch_sparse_mla(const uint16_t* q, const uint8_t* kv, const float* kvs, const int* idx, const int* cnt,
                              const int* table, const int* rows, const float* bias, uint16_t* out, float* out_f32,
                              float* lse, void* ws, int B, int H, int Dqk, int keep, int max_pages, int page_size,
                              int num_pages, float scale, int splits, hipStream_t s, PoolForm pf, bool wide) {
   if (splits == 1 && wide) {
+    // the many-row form takes the pooled tail among its slots: kpool more
+    const int keep_w = pf.kp_shift ? keep + (1 << pf.kp_shift) : keep;
+    pf.tail_apart = 0;
     const dim3 grid(B * (H / AW_HEADS));
     return Dqk == 512 ? launch("sparse_mla_wide_kernel", sparse_mla_wide_kernel<512>, grid, dim3(ATT_THREADS), s, q,
-                               kv, kvs, idx, cnt, table, rows, out, out_f32, lse, H, keep, max_pages, page_size,
+                               kv, kvs, idx, cnt, table, rows, out, out_f32, lse, H, keep_w, max_pages, page_size,
                                num_pages, scale, pf)
                       : launch("sparse_mla_wide_kernel", sparse_mla_wide_kernel<576>, grid, dim3(ATT_THREADS), s, q,
-                               kv, kvs, idx, cnt, table, rows, out, out_f32, lse, H, keep, max_pages, page_size,
+                               kv, kvs, idx, cnt, table, rows, out, out_f32, lse, H, keep_w, max_pages, page_size,
                                num_pages, scale, pf);
   }
+  // the split form adds the pooled tail apart from its keep slots when its rows fit their LDS (kpool 8 with 576-wide
+  // rows: 7 x 576 bytes do not; the tail is then among the slots, keep + kpool of them)
+  pf.tail_apart = pf.kp_shift && ((1 << pf.kp_shift) - 1) * Dqk <= ATT_TAIL_BYTES;
+  if (pf.kp_shift && !pf.tail_apart) keep += 1 << pf.kp_shift;
   const int HG = H / ATT_HPW;
   // slots per split: a whole number of chunks
   int sps = (keep + splits - 1) / splits;

@@ -56,11 +56,14 @@ constexpr int HIST_BINS = 4096;
 
 // The attention's pooled token form (kpool = 1 << kp_shift > 1; kp_shift 0: the per-token forms): idx holds
 // idx_stride selected pools per row, npool [B] each row's complete pools (its tail pool), positions [B] its position.
+// tail_apart: the row's tail tokens are not among the kernel's slots but added by the workgroup that holds the row's
+// last slot (the split form), so the kpool x idx_stride slots of the selected pools split into whole chunks.
 struct PoolForm {
   int kp_shift;
   int idx_stride;
   const int* npool;
   const int* positions;
+  int tail_apart;
 };
 constexpr int HIST_REPLICAS = 1;
 constexpr float VISIBLE = -5e29f;   // trnrt/kernels/dsa_topk.py:58: scores at or below are not selectable
