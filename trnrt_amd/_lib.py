@@ -3,6 +3,11 @@
 The library is loaded once, on first use, from the package directory. There is no fallback: if the library is not
 built the first call raises RuntimeError, the reference's behaviour when its kernel backend is missing
 (trnrt/kernels/dsa_index.py:258-259).
+
+torch is imported before the library is opened. torch ships its own HIP runtime under the soname libamdhip64.so.7,
+the soname the library links against: with torch loaded first the library binds to that runtime, while a library
+opened first would pull in ROCm's copy and the later torch import a second one, two HIP runtimes in one process
+(which crashes on the GPU).
 """
 
 from __future__ import annotations
@@ -86,6 +91,8 @@ def lib() -> ctypes.CDLL:
     if _lib is None:
         if not LIB_PATH.exists():
             raise RuntimeError(f"{LIB_PATH.name} is not built: run `python -m trnrt_amd.build` (needs hipcc, gfx950)")
+        import torch  # noqa: F401  (its HIP runtime first: one runtime per process)
+
         h = ctypes.CDLL(str(LIB_PATH))
         for name, (res, args) in SIGNATURES.items():
             f = getattr(h, name)
