@@ -32,6 +32,20 @@ def test_library_exports_every_symbol():
     assert lib.dsa_abi_version() == _lib.ABI_VERSION
 
 
+def test_one_hip_runtime_when_the_library_is_loaded_first():
+    """Opening the library before anything imported torch, then importing torch, leaves one HIP runtime in the
+    process (torch's): the loader imports torch first, so the library binds to torch's libamdhip64 instead of
+    pulling in ROCm's copy beside it. A fresh interpreter, since this one has torch loaded already."""
+    import subprocess
+    import sys
+    code = ("import re, sys; sys.path.insert(0, %r); from trnrt_amd import _lib; _lib.lib(); import torch; "
+            "print(len(set(re.findall(r'\\S*libamdhip64\\S*', open('/proc/self/maps').read()))))"
+            % os.path.dirname(HERE))
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    assert r.stdout.strip().splitlines()[-1] == "1"
+
+
 def test_status_strings():
     lib = _lib.lib()
     for s in (0, -1, -2, -3, -4, -99):
