@@ -51,6 +51,23 @@ def test_layer_full_oracle(c):
     _attention_check(inp, L)
 
 
+def test_layer_rows_of_8192_one_kernel_selection():
+    """Rows of 4,097 .. 8,192 scores: the fused indexer's first-level histogram feeds the one-workgroup-per-row
+    selection, which also writes the cache rows through the page table (128 pages a row); ragged lengths, every
+    stage against the oracle."""
+    say("layer rows of 8192")
+    cfg = W.Config("layer-8k", B=4, L=8192, H=64, Hi=64)
+    inp = W.make_inputs(cfg, seed=5, lengths=[8192, 8000, 4097, 6001])
+    g = inp.to("cuda")
+    L = _layer(g)
+    sc = L.scores.cpu()
+    ref = O.indexer_ref(inp.q_idx, inp.w_k, inp.k_cache, inp.k_scale, inp.table, inp.ctx_len, 64, sc.shape[1])
+    assert row_rel_err(sc, ref, ref > -1e29) <= 1e-2
+    ri, rc = O.topk_ref(sc, cfg.keep, inp.ctx_len)
+    assert torch.equal(L.idx.cpu().long(), ri) and torch.equal(L.cnt.cpu().long(), rc)
+    _attention_check(inp, L)
+
+
 def _sampled_indexer_check(g, sc, nsample=4096, seed=0):
     cfg = g.cfg
     gen = torch.Generator().manual_seed(seed)

@@ -247,17 +247,20 @@ def test_glm_pooled_decode_step_end_to_end():
     assert_attention_close(o, want_o)
 
 
-@pytest.mark.parametrize("dqk", [512, 576])
-def test_pooled_decode_layer_matches_composition_and_oracle(dqk):
+@pytest.mark.parametrize("dqk,L,pos", [(512, 4096, (4095, 4094, 3001, 2050, 700, 1)),
+                                       (576, 4096, (4095, 4094, 3001, 2050, 700, 1)),
+                                       (512, 32768, (32767, 30001, 9000))])
+def test_pooled_decode_layer_matches_composition_and_oracle(dqk, L, pos):
     """The one-call pooled layer (dsa_pooled_decode_layer: the indexer with the fused first-level histogram, the
     top-k, attention over the selected pools' tokens and the tail read straight from the pool indices) against the
-    reference-flow composition (dsa_long.decode_pooled: scores, select, slots, attend) and the oracle."""
+    reference-flow composition (dsa_long.decode_pooled: scores, select, slots, attend) and the oracle; at 32,768
+    tokens (8,192 pools a row) the selection is the one-workgroup-per-row kernel fed by the fused histogram."""
     from trnrt_amd.kernels.dsa_layer import PooledDecodeLayer
-    cfg = W.PooledConfig("glm-layer", B=6, L=4096, dqk=dqk)
+    cfg = W.PooledConfig("glm-layer", B=len(pos), L=L, dqk=dqk)
     say(f"pooled layer dqk={dqk} B={cfg.B} L={cfg.L}")
-    inp = W.make_pooled_inputs(cfg, seed=30 + dqk, device="cuda")
+    inp = W.make_pooled_inputs(cfg, seed=30 + dqk + L, device="cuda")
     kp, ps = cfg.kp, cfg.page_size
-    positions = torch.tensor([4095, 4094, 3001, 2050, 700, 1], dtype=torch.int32)
+    positions = torch.tensor(pos, dtype=torch.int32)
     npool = torch.div(positions + 1, kp, rounding_mode="floor").to(torch.int32)
     layer = PooledDecodeLayer(cfg.B, cfg.Hi, cfg.H, dqk, inp.table.shape[1], ps, inp.pool_key.shape[0] // ps, kp,
                               cfg.keep, cfg.scale)

@@ -98,7 +98,7 @@ struct IndOut {
 };
 
 struct RowShared {
-  int pg[128];                      // page ids of the row's first 4096 positions (slot output)
+  int pg[TR_THREADS];               // page ids of the row's first 1024 pages (slot output)
   int bins[TK_HBINS];               // the current pass's histogram (4096, 2048 or 512 bins in key order)
   int wtot[TR_WAVES];               // per-wave totals of a block scan
   uint32_t blk[TR_MAXG * TR_WAVES];  // output: per (group, wave) packed counts, then their exclusive prefix
@@ -203,7 +203,7 @@ __global__ __launch_bounds__(TR_THREADS) void topk_row_kernel(const float* __res
 #pragma unroll
     for (int e = 0; e < G; ++e) load_keys4<VEC>(srow, stride, L, 4 * (TR_THREADS * e + t), vis_only, key[e]);
   }
-  if (ROWS && t < 128) sh.pg[t] = safe_page(pgv, so.num_pages);
+  if (ROWS) sh.pg[t] = safe_page(pgv, so.num_pages);
   if (t == 0) sh.sel_bin = -1;
   if (HIST_IN) {
     int4 h4 = h4r[0];
@@ -313,7 +313,7 @@ __global__ __launch_bounds__(TR_THREADS) void topk_row_kernel(const float* __res
         }
         if (ROWS) {
           const int ps = so.page_size;
-          so.rows[(size_t)row * keep + o] = sh.pg[min((p0 + c) / ps, 127)] * ps + (p0 + c) % ps;
+          so.rows[(size_t)row * keep + o] = sh.pg[min((p0 + c) / ps, TR_THREADS - 1)] * ps + (p0 + c) % ps;
         }
       }
       a_before += a;
@@ -1066,6 +1066,15 @@ static hipError_t launch_topk_level(const float* scores, int stride, const int* 
                : launch_topk_row<1, false>(scores, stride, len, len_div, len_mul, keep, vis_only, tb.hist, hist_ready,
                                            idx, cnt, so, B, s);
   if (max_len > TC_MAXCH * TC_CHUNK) return hipErrorInvalidValue;
+  // the first-level histogram ready (the fused indexer's) and rows of at most 8192 scores: one workgroup per row,
+  // one kernel (measured at 8 rows: 7.3 us against 4.6 + 5.8 us for the chunked pair at 8192 scores, but 20.1 us
+  // against 4.3 + 7.4 us at 32768, where one CU per row is the bound)
+  if (hist_ready && max_len <= 8 * TR_THREADS &&
+      (!so.rows || (max_len + so.page_size - 1) / so.page_size <= TR_THREADS))
+    return vec ? launch_topk_row<2, true>(scores, stride, len, len_div, len_mul, keep, vis_only, tb.hist, true, idx,
+                                          cnt, so, B, s)
+               : launch_topk_row<2, false>(scores, stride, len, len_div, len_mul, keep, vis_only, tb.hist, true, idx,
+                                           cnt, so, B, s);
   if (B >= TOPK_MANY_ROWS && !hist_ready && !so.rows)
     return vec ? launch_topk_many_rows<true>(scores, stride, len, len_div, len_mul, max_len, keep, vis_only, tb.hist,
                                              idx, cnt, so, B, s)
