@@ -80,6 +80,13 @@ struct SlotOut {
   int* rows;  // [B, keep], or null
 };
 
+// p / page_size and p % page_size of a position p >= 0: shifts when the page size is a power of two (page_shift >= 0),
+// which keeps the integer division out of the per-key output loops.
+__device__ __forceinline__ int page_of(int p, int ps, int page_shift) {
+  return page_shift >= 0 ? p >> page_shift : p / ps;
+}
+__device__ __forceinline__ int page_shift_of(int ps) { return (ps & (ps - 1)) ? -1 : __builtin_ctz((unsigned)ps); }
+
 // The second level of a two-level selection read in place (the row kernel's IND form): candidate position p of a
 // row is score src(p) = bidx[row, p / sub] sub + p % sub of the original row (sub a multiple of 4, so a float4 of
 // candidates is one float4 of scores), live while p / sub < bcnt[row] and src < len[row]; the selection is written
@@ -293,6 +300,7 @@ __global__ __launch_bounds__(TR_THREADS) void topk_row_kernel(const float* __res
   }
   __syncthreads();
   int* orow = idx_out + (size_t)row * keep;
+  const int psh = ROWS ? page_shift_of(so.page_size) : 0;
 #pragma unroll
   for (int e = 0; e < G; ++e) {
     const uint32_t before = sh.blk[e * TR_WAVES + wave] + incl[e] - mine[e];
@@ -312,8 +320,8 @@ __global__ __launch_bounds__(TR_THREADS) void topk_row_kernel(const float* __res
           orow[o] = p0 + c;
         }
         if (ROWS) {
-          const int ps = so.page_size;
-          so.rows[(size_t)row * keep + o] = sh.pg[min((p0 + c) / ps, TR_THREADS - 1)] * ps + (p0 + c) % ps;
+          const int ps = so.page_size, pi = page_of(p0 + c, ps, psh);
+          so.rows[(size_t)row * keep + o] = sh.pg[min(pi, TR_THREADS - 1)] * ps + (p0 + c - pi * ps);
         }
       }
       a_before += a;
@@ -739,6 +747,7 @@ __global__ __launch_bounds__(TC_THREADS) void topk_output_kernel(const float* __
   }
   chunk_prefix(mine, sh.blk, before);
   int* orow = idx_out + (size_t)row * keep;
+  const int psh = ROWS ? page_shift_of(so.page_size) : 0;
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
     int a_before = (int)(before[e] >> 16), t_before = (int)(before[e] & 0xffffu);
@@ -752,8 +761,8 @@ __global__ __launch_bounds__(TC_THREADS) void topk_output_kernel(const float* __
       if (sel && (unsigned)o < (unsigned)keep) {  // in range whatever the counts
         orow[o] = p0 + c;
         if (ROWS) {
-          const int ps = so.page_size, p = p0 + c;
-          so.rows[(size_t)row * keep + o] = sh.pg[min(p / ps - pg_first, WAVE - 1)] * ps + p % ps;
+          const int ps = so.page_size, p = p0 + c, pi = page_of(p, ps, psh);
+          so.rows[(size_t)row * keep + o] = sh.pg[min(pi - pg_first, WAVE - 1)] * ps + (p - pi * ps);
         }
       }
       a_before += a;
