@@ -591,8 +591,9 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void sparse_mla_wide_kernel(
   float m_run = -INFINITY;  // running max of head 16 hg + l16 (the same in both th waves)
   float l_run = 0.0f;       // this lane's share of the running sum of head 16 hg + l16
 
-  auto compute = [&](int c, int buf) __attribute__((always_inline)) {
-    __syncthreads();  // chunk c's tile is in LDS
+  // chunk c from tile buf (in LDS since the previous chunk's last barrier); rn holds the next chunk's rows, stored
+  // into the other tile once every wave is past its reads of it, then reloaded with chunk c + 3
+  auto compute = [&](int c, int buf, u32x4(&rn)[LPT]) __attribute__((always_inline)) {
     const uint8_t* kt = sh.kt[buf];
     const int cb = c * ATT_CH;
     // partial scores of the 64 tokens (block k: tokens 16 k + l16 as MFMA rows) over this wave's dims half; lane
@@ -611,7 +612,9 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void sparse_mla_wide_kernel(
       }
 #pragma unroll
     for (int k = 0; k < 4; ++k) sh.xs[th][hg][k][lane] = acc[k];
-    __syncthreads();  // both halves' partial scores
+    __syncthreads();  // both halves' partial scores; every wave is past the previous chunk's value reads
+    wide_lstore<DQK, LPT>(sh.kt[buf ^ 1], tid, rn);
+    wide_gload<DQK, LPT>(kv, &sh.slot[min(c + 3, nch - 1) * ATT_CH], tid, rn);
     // acc[k][r] + the other half's = S^T[token 16 k + 4 q4 + r][head 16 hg + l16]
     float sv[4][4];
     float mx = -INFINITY;
@@ -656,7 +659,7 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void sparse_mla_wide_kernel(
     }
     l_run = l_run * alpha + psum;
     if (th == 0 && lane < 16) sh.al[16 * hg + lane] = alpha;
-    __syncthreads();  // P and the rescale factors
+    __syncthreads();  // P and the rescale factors, and the next chunk's tile
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       if (sh.rfl[i]) {  // the same for every lane: a head block with no moved maximum is skipped
@@ -687,19 +690,18 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void sparse_mla_wide_kernel(
     // only after this chunk's P . V
   };
 
-  // the pipeline: store chunk c (its loads were issued two steps earlier), reuse its registers for chunk c + 2,
-  // compute chunk c from tile c % 2
+  // the pipeline: chunk c computes from tile c % 2 and, between its two barriers, stores chunk c + 1 (loaded two
+  // chunks earlier) into the other tile and reuses those registers for chunk c + 3; two barriers per chunk
   // (past the last chunk the loads re-read the last chunk, so every load is unconditional and the waits stay exact)
   u32x4 r0[LPT], r1[LPT];
   wide_gload<DQK, LPT>(kv, &sh.slot[0], tid, r0);
   wide_gload<DQK, LPT>(kv, &sh.slot[min(1, nch - 1) * ATT_CH], tid, r1);
+  wide_lstore<DQK, LPT>(sh.kt[0], tid, r0);
+  wide_gload<DQK, LPT>(kv, &sh.slot[min(2, nch - 1) * ATT_CH], tid, r0);
+  __syncthreads();  // tile 0 in LDS
   for (int c = 0; c < nch; c += 2) {
-    wide_lstore<DQK, LPT>(sh.kt[0], tid, r0);
-    wide_gload<DQK, LPT>(kv, &sh.slot[min(c + 2, nch - 1) * ATT_CH], tid, r0);
-    compute(c, 0);
-    wide_lstore<DQK, LPT>(sh.kt[1], tid, r1);
-    wide_gload<DQK, LPT>(kv, &sh.slot[min(c + 3, nch - 1) * ATT_CH], tid, r1);
-    if (c + 1 < nch) compute(c + 1, 1);  // workgroup-uniform
+    compute(c, 0, r1);
+    if (c + 1 < nch) compute(c + 1, 1, r0);  // workgroup-uniform
   }
 
   // per head: the sum over both token halves, the final max
