@@ -429,9 +429,10 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void sparse_mla_kernel(
 //     for its 32 tokens (32 th ..) into LDS [64 heads][64 tokens], the rescale factors into LDS;
 //   - value: wave w takes dims 64 w .. 64 w + 63 of all 64 heads (O in 16 accumulators, 4 head blocks x 4 dim blocks),
 //     its operand read transposed from the token-major tile by ds_read_b64_tr_b8 as in the split form.
-// The tiles are token-major with the 592-byte stride of the split form, but rows 8 .. 15 of every 16 hold each 16-byte
-// unit with its two 8-byte halves swapped: LDS serves a 64-bit read 16 lanes at a time over 32 banks, and the score's
-// 16 lanes read 16 rows at the same column, which the 592-byte stride alone maps onto 8 bank pairs (2-way conflict).
+// The tiles are token-major with the 592-byte stride of the split form. The score reads are 128-bit, one per pair of
+// MFMA steps (lane group q4 takes dims 64 j + 16 q4 .. + 15 of its row for steps 2 j, 2 j + 1; the query operand
+// uses the same dim order): LDS serves them 8 lanes at a time, and 8 rows at one column cover the 32 banks once at
+// the 592-byte stride (148 dwords, 4 mod 8). An odd last step (576-wide rows) reads 64 bits.
 // Slot forms: token (idx + cnt + table, with the pooled variant of PoolForm) and rows + cnt; no bias array.
 constexpr int AW_HEADS = 64;
 constexpr int AW_MAXSLOTS = 33 * ATT_CH;  // 2,112: keep 2,048 plus a pooled tail
@@ -471,19 +472,8 @@ __device__ __forceinline__ void wide_lstore(uint8_t* tile, int tid, const u32x4 
   for (int i = 0; i < LPT; ++i) {
     const int u = min(tid + ATT_THREADS * i, UNITS - 1);
     const int row = u / PIECES, pc = u - row * PIECES;
-    const u32x4 v = r[i];
-    *reinterpret_cast<u32x4*>(tile + row * ATT_KROW + 16 * pc) = (row & 8) ? u32x4{v[2], v[3], v[0], v[1]} : v;
+    *reinterpret_cast<u32x4*>(tile + row * ATT_KROW + 16 * pc) = r[i];
   }
-}
-
-// The value operand from a many-row tile (rows 8 .. 15 of every 16 hold their 16-byte units with the 8-byte halves
-// swapped): value_operand's addressing with lane p's half flipped in the rows whose bit 3 is set (row 32 ks + 8 q +
-// p / 2 has bit 3 = q & 1).
-__device__ __forceinline__ bf16x8 value_operand_sw(const uint8_t* kt, int ks, int n, int lane) {
-  const int q = lane >> 4, p = lane & 15;
-  const uint8_t* a = kt + (32 * ks + 8 * q + (p >> 1)) * ATT_KROW + 16 * n + 8 * ((p & 1) ^ (q & 1));
-  const att_v2i r = __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) att_v2i*)(a));
-  return fp8x8_to_bf16x8((uint32_t)r.x, (uint32_t)r.y);
 }
 
 template <int DQK>
@@ -577,9 +567,14 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void sparse_mla_wide_kernel(
   constexpr int S2 = STEPS / 2;  // score steps per dims half
   bf16x8 qb[S2];
   {
-    const uint16_t* qh = qs + (16 * hg + l16) * QROW + 8 * q4 + 32 * S2 * th;
+    // the key operand's dim order (below): steps 2 j, 2 j + 1 give lane group q4 dims 64 j + 16 q4 + 8 (st % 2) ..
+    // + 7 of the wave's half; an odd last step dims 32 st + 8 q4 .. + 7
+    const uint16_t* qh = qs + (16 * hg + l16) * QROW + 32 * S2 * th;
 #pragma unroll
-    for (int st = 0; st < S2; ++st) qb[st] = as_bf16x8(*reinterpret_cast<const uint4*>(qh + 32 * st));
+    for (int st = 0; st < S2; ++st) {
+      const int d = st < (S2 & ~1) ? 64 * (st >> 1) + 16 * q4 + 8 * (st & 1) : 32 * st + 8 * q4;
+      qb[st] = as_bf16x8(*reinterpret_cast<const uint4*>(qh + d));
+    }
   }
   __syncthreads();  // every wave holds its operand before the tiles overwrite the queries
 
@@ -597,19 +592,34 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void sparse_mla_wide_kernel(
     const uint8_t* kt = sh.kt[buf];
     const int cb = c * ATT_CH;
     // partial scores of the 64 tokens (block k: tokens 16 k + l16 as MFMA rows) over this wave's dims half; lane
-    // (l16, q4) reads the 8-byte half q4 & 1 of unit q4 / 2 of its row's 32-dim step, the half flipped in rows whose
-    // bit 3 is set (l16 >= 8), so each 16-lane group covers the 32 banks once
-    const int kofs = l16 * ATT_KROW + 32 * S2 * th + 16 * (q4 >> 1) + 8 * ((q4 & 1) ^ (l16 >> 3));
+    // (l16, q4) reads 16 bytes of its row per pair of steps (dims 64 j + 16 q4 ..: one ds_read_b128 for two MFMAs),
+    // 8 lanes of one 16-byte column at the 592-byte row stride covering the 32 banks once
+    const uint8_t* krow = kt + l16 * ATT_KROW + 32 * S2 * th;
     f32x4 acc[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) acc[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int st = 0; st < S2; ++st)
+    for (int j = 0; j < S2 / 2; ++j) {
+      u32x4 kk[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) kk[k] = *reinterpret_cast<const u32x4*>(krow + 16 * k * ATT_KROW + 64 * j + 16 * q4);
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        acc[k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16x8(kk[k][0], kk[k][1]), qb[2 * j], acc[k], 0, 0,
+                                                         0);
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        acc[k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16x8(kk[k][2], kk[k][3]), qb[2 * j + 1], acc[k],
+                                                         0, 0, 0);
+    }
+    if (S2 & 1) {
+      constexpr int st = S2 - 1;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const uint2 ka = *reinterpret_cast<const uint2*>(kt + kofs + 16 * k * ATT_KROW + 32 * st);
+        const uint2 ka = *reinterpret_cast<const uint2*>(krow + 16 * k * ATT_KROW + 32 * st + 8 * q4);
         acc[k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16x8(ka.x, ka.y), qb[st], acc[k], 0, 0, 0);
       }
+    }
 #pragma unroll
     for (int k = 0; k < 4; ++k) sh.xs[th][hg][k][lane] = acc[k];
     __syncthreads();  // both halves' partial scores; every wave is past the previous chunk's value reads
@@ -681,7 +691,7 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void sparse_mla_wide_kernel(
         pop[i] = as_bf16x8(*reinterpret_cast<const uint4*>(&sh.p[(16 * i + l16) * ATT_PROW + 32 * ks + 8 * q4]));
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
-        const bf16x8 v = value_operand_sw(kt, ks, 4 * wave + n, lane);
+        const bf16x8 v = value_operand(kt, ks, 4 * wave + n, lane);
 #pragma unroll
         for (int i = 0; i < 4; ++i) o[i][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pop[i], v, o[i][n], 0, 0, 0);
       }
