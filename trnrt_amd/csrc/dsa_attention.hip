@@ -155,15 +155,16 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void sparse_mla_kernel(
     float s4[4];
     float alpha = 1.0f;
     if (live) {
-      // scores of tokens 16 wh .. 16 wh + 15, heads l16 (two accumulators: independent MFMA chains)
+      // scores of tokens 16 wh .. 16 wh + 15, heads l16 (two accumulators: independent MFMA chains); lane group q4
+      // reads 16 bytes of its row per pair of steps (dims 64 j + 16 q4 ..: one ds_read_b128 for two MFMAs, 8 rows
+      // at one column covering the 32 banks once at the 592-byte stride)
       f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
-      const uint8_t* kr = kt + (16 * wh + l16) * ATT_KROW + 8 * q4;
+      const uint8_t* kr = kt + (16 * wh + l16) * ATT_KROW + 16 * q4;
 #pragma unroll
       for (int st = 0; st < STEPS; st += 2) {
-        const uint2 ka = *reinterpret_cast<const uint2*>(kr + 32 * st);
-        const uint2 kb = *reinterpret_cast<const uint2*>(kr + 32 * st + 32);
-        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16x8(ka.x, ka.y), qb[st], acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16x8(kb.x, kb.y), qb[st + 1], acc1, 0, 0, 0);
+        const u32x4 kk = *reinterpret_cast<const u32x4*>(kr + 32 * st);
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16x8(kk[0], kk[1]), qb[st], acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16x8(kk[2], kk[3]), qb[st + 1], acc1, 0, 0, 0);
       }
       // acc[r] = S^T[token 16 wh + 4 q4 + r][head l16]
       float mx = -INFINITY;
@@ -271,9 +272,11 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void sparse_mla_kernel(
           *reinterpret_cast<uint4*>(qs + (pc / (DQK / 8)) * ATT_QROW + 8 * (pc % (DQK / 8))) = qv[i];
       }
       __syncthreads();
-      const uint16_t* qh = qs + l16 * ATT_QROW + 8 * q4;
+      // in the key operand's dim order: steps 2 j, 2 j + 1 give lane group q4 dims 64 j + 16 q4 + 8 (st % 2) .. + 7
+      const uint16_t* qh = qs + l16 * ATT_QROW + 16 * q4;
 #pragma unroll
-      for (int st = 0; st < STEPS; ++st) qb[st] = as_bf16x8(*reinterpret_cast<const uint4*>(qh + 32 * st));
+      for (int st = 0; st < STEPS; ++st)
+        qb[st] = as_bf16x8(*reinterpret_cast<const uint4*>(qh + 64 * (st >> 1) + 8 * (st & 1)));
       __syncthreads();  // every wave holds its operand before the rows overwrite it
     }
     // every staged row straight into LDS: instruction kk (chunk kk / 37, 1-KiB block j = kk % 37 of its tile) has
