@@ -61,14 +61,16 @@ def test_pooled_attention_vs_oracle():
     assert_attention_close(o, ref)
 
 
-@pytest.mark.parametrize("kp,dqk", [(2, 576), (4, 512), (8, 512), (8, 576)])
-def test_attend_pooled_tails_vs_oracle(kp, dqk):
+@pytest.mark.parametrize("kp,dqk,splits", [(2, 576, 0), (4, 512, 0), (8, 512, 0), (8, 576, 0), (4, 512, 1),
+                                           (4, 576, 3), (8, 512, 1)])
+def test_attend_pooled_tails_vs_oracle(kp, dqk, splits):
     """dsa_long.attend_pooled (selected pools and the tail read through the page table) over rows with every tail
     length 0 .. kp - 1, fewer selected pools than keep, and no complete pool, against the oracle over the slots of
     the reference's own arithmetic (pool_slots_ref). The split form adds the tail in the workgroup that holds a
     row's last slot; at kp 8 with 576-wide rows it keeps the tail among the slots instead: both are covered, with
-    several splits per row and with lse."""
-    say(f"attend_pooled tails kp={kp} dqk={dqk}")
+    several splits per row (splits 0: chosen for the GPU, 16 here), one split (the tail added by the only workgroup,
+    the output written directly) or 3 uneven ones, and with lse."""
+    say(f"attend_pooled tails kp={kp} dqk={dqk} splits={splits}")
     g = torch.Generator().manual_seed(kp * 1000 + dqk)
     L, ps, H = 2048, 64, 32
     keep = 512 // kp
@@ -84,7 +86,7 @@ def test_attend_pooled_tails_vs_oracle(kp, dqk):
     tails = (positions + 1 - npool * kp).tolist()
     assert set(tails) == (set(range(kp)) if kp < 8 else {0, 1, 4, 6, 7})
     o, lse = dsa_long.attend_pooled(q.cuda(), kv.cuda(), ks.cuda(), pools.cuda(), cnt.cuda(), npool.cuda(),
-                                    positions.cuda(), table.cuda(), ps, kp, 192 ** -0.5, lse=True)
+                                    positions.cuda(), table.cuda(), ps, kp, 192 ** -0.5, lse=True, splits=splits)
     torch.cuda.synchronize()
     want_r, want_b = O.pool_slots_ref(pools, cnt, npool, positions, table, ps, kp, keep + 1)
     tok = (want_r.unsqueeze(-1) * kp + torch.arange(kp)).reshape(B, -1)

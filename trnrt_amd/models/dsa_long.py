@@ -107,13 +107,14 @@ def attend(q_lat: torch.Tensor, kc: torch.Tensor, rows: torch.Tensor, bias: torc
 def attend_pooled(q_lat: torch.Tensor, kc: torch.Tensor, kc_scale: torch.Tensor, pools: torch.Tensor,
                   cnt: torch.Tensor, npool: torch.Tensor, positions: torch.Tensor, table: torch.Tensor,
                   page_size: int, kp: int, scale: float, *, lse: bool = False,
-                  workspace: torch.Tensor | None = None):
+                  workspace: torch.Tensor | None = None, splits: int = 0):
     """attend(slots(...)) in one kernel (trnrt/models/dsa_long.py:189-223): absorbed MLA of N queries over the kp
     tokens of each of their selected pools (pools [N, keep] ascending, cnt [N] valid) and the tail tokens
     kp npool .. positions[n] of their incomplete pool, read through the page table ([Pp] shared, or [N, Pp]); the
     slot rows and biases are never materialised. q_lat [N, H, R] bf16 (R 512 or 576), kc [slots, R] e4m3fn with
     kc_scale [slots]. Returns o [N, H, 512] fp32 (and lse [N, H] with lse). workspace: the split partials
-    (dsa_sparse_mla_pooled_workspace_bytes), allocated here when not given."""
+    (dsa_sparse_mla_pooled_workspace_bytes), allocated here when not given; splits: the attention's split-K (0: chosen
+    for the GPU)."""
     N, keep = pools.shape
     if kp < 2 or kp & (kp - 1) or page_size % kp:
         raise ValueError(f"attend_pooled: kpool {kp} with pages of {page_size}")
@@ -138,11 +139,12 @@ def attend_pooled(q_lat: torch.Tensor, kc: torch.Tensor, kc_scale: torch.Tensor,
     out = torch.empty(N, H, dsa_decode.DV, dtype=torch.float32, device=dev)
     ls = torch.empty(N, H, dtype=torch.float32, device=dev) if lse else None
     lib = _lib.lib()
-    wsb = int(lib.dsa_sparse_mla_pooled_workspace_bytes(N, H, keep, kp, 0))
+    wsb = int(lib.dsa_sparse_mla_pooled_workspace_bytes(N, H, keep, kp, int(splits)))
     ws = workspace if workspace is not None else torch.empty(max(wsb, 256), dtype=torch.uint8, device=dev)
     st = lib.dsa_sparse_mla_pooled(C.ptr(q), C.ptr(kv), C.ptr(ks), C.ptr(pl), C.ptr(cn), C.ptr(npl), C.ptr(pos),
                                    C.ptr(tb), None, C.ptr(out), C.ptr(ls), C.ptr(ws), ws.numel(), N, H, dqk, keep, kp,
-                                   tb.shape[1], page_size, slots_n // page_size, float(scale), 0, C.stream_ptr(dev))
+                                   tb.shape[1], page_size, slots_n // page_size, float(scale), int(splits),
+                                   C.stream_ptr(dev))
     _lib.check(st, "dsa_long.attend_pooled")
     return (out, ls) if lse else out
 
