@@ -66,6 +66,9 @@ struct PoolForm {
   int tail_apart;
 };
 constexpr int HIST_REPLICAS = 1;
+
+// s_waitcnt's immediate for "vector memory count <= n" (expcnt and lgkmcnt left at their maxima, no wait)
+__host__ __device__ constexpr int vmcnt_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 constexpr float VISIBLE = -5e29f;   // trnrt/kernels/dsa_topk.py:58: scores at or below are not selectable
 constexpr int WAVE = 64;
 

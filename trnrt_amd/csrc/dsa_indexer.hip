@@ -35,9 +35,6 @@ __device__ __forceinline__ float crow_value(const float* cand, int b, int stride
 
 constexpr int IDX_AHEAD = 1;  // key tiles a wave has in flight ahead of the one it computes (1, 2 and 3 measured)
 
-// s_waitcnt's immediate for "vector memory count <= n" (expcnt and lgkmcnt left at their maxima, no wait)
-__host__ __device__ constexpr int vmcnt_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
-
 // One 32-key tile's loads for lane (key j, half h): 64 key bytes (dims 64h .. 64h + 63) and the key's scale (a tile
 // past the context reads the null page: every load is unconditional, so the waits count exactly).
 template <bool CAND>
