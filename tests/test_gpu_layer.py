@@ -68,6 +68,24 @@ def test_layer_rows_of_8192_one_kernel_selection():
     _attention_check(inp, L)
 
 
+@pytest.mark.parametrize("ps,L", [(32, 8192), (128, 8192), (32, 20000)])
+def test_layer_other_page_sizes(ps, L):
+    """Pages of 32 and 128 tokens (a 32-key indexer tile is one page, or a quarter of one): the indexer's page reads,
+    the selection's cache rows through the table (page shift 5 and 7) and the attention's gather, against the oracle;
+    ragged lengths, rows of 8,192 (the one-workgroup selection) and 20,000 scores (the chunked one)."""
+    say(f"layer page_size={ps} L={L}")
+    cfg = W.Config(f"layer-ps{ps}", B=3, L=L, H=64, Hi=64, page_size=ps)
+    inp = W.make_inputs(cfg, seed=ps + L, lengths=[L, L - 5, L // 2 + 3])
+    g = inp.to("cuda")
+    layer = _layer(g)
+    sc = layer.scores.cpu()
+    ref = O.indexer_ref(inp.q_idx, inp.w_k, inp.k_cache, inp.k_scale, inp.table, inp.ctx_len, ps, sc.shape[1])
+    assert row_rel_err(sc, ref, ref > -1e29) <= 1e-2
+    ri, rc = O.topk_ref(sc, cfg.keep, inp.ctx_len)
+    assert torch.equal(layer.idx.cpu().long(), ri) and torch.equal(layer.cnt.cpu().long(), rc)
+    _attention_check(inp, layer)
+
+
 def _sampled_indexer_check(g, sc, nsample=4096, seed=0):
     cfg = g.cfg
     gen = torch.Generator().manual_seed(seed)
