@@ -559,24 +559,26 @@ __global__ __launch_bounds__(TC_THREADS) void topk_chunk_kernel(const float* __r
 struct OutShared {
   int pg[WAVE];  // page ids of the chunk's positions (slot output; pages of at least 32 positions)
   int pg0;                    // the page of position 0
-  int bins[2048];
+  int bins[2048];  // the 11-bit pass's histogram
+  int bins2[512];  // the 9-bit pass's, zeroed with the first so the passes need no barrier between them
   int wtot[TC_WAVES];
   uint32_t blk[2 * TC_WAVES];
   int gt[TC_MAXCH], tie[TC_MAXCH], na[TC_MAXCH];
-  int sel_bin, sel_above;
+  int sel[2], sel2[2];  // each pass's result: the bin, the keys above it
 };
 
-// Block-wide (256 threads) over sh.bins[0 .. nbins) (nbins 2048 or 512, higher bins = larger keys): the bin holding
-// the need-th largest key and the keys in the bins above it. sh.sel_bin must be -1 on entry (written before the
-// barrier preceding the histogram's atomics); inconsistent counts give bin 0, above 0. Two barriers.
-__device__ void out_find_bin(OutShared& sh, int nbins, int need, int* bin, int* above) {
+// Block-wide (256 threads) over bins[0 .. nbins) (nbins 2048 or 512, higher bins = larger keys): the bin holding the
+// need-th largest key and the keys in the bins above it, through sel[0 .. 1]. sel[0] must be -1 on entry (written
+// before the barrier preceding the histogram's atomics); inconsistent counts give bin 0, above 0. Two barriers.
+__device__ void out_find_bin(OutShared& sh, const int* bins, int* sel, int nbins, int need, int* bin,
+                             int* above) {
   const int t = threadIdx.x, wave = t / WAVE, lane = t & (WAVE - 1);
   const int per = nbins / TC_THREADS;  // 8 or 2
   int hb[8];
   int mine = 0;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    hb[i] = i < per ? sh.bins[per * t + i] : 0;
+    hb[i] = i < per ? bins[per * t + i] : 0;
     mine += hb[i];
   }
   const int pre = wave_incl_scan(mine);
@@ -592,17 +594,17 @@ __device__ void out_find_bin(OutShared& sh, int nbins, int need, int* bin, int* 
     for (int i = 7; i >= 0; --i) {
       if (i < per && excl < need) {
         if (excl + hb[i] >= need) {
-          sh.sel_bin = per * t + i;
-          sh.sel_above = excl;
+          sel[0] = per * t + i;
+          sel[1] = excl;
         }
         excl += hb[i];
       }
     }
   }
   __syncthreads();
-  const int b = sh.sel_bin;
+  const int b = sel[0];
   *bin = b < 0 ? 0 : b;
-  *above = b < 0 ? 0 : sh.sel_above;
+  *above = b < 0 ? 0 : sel[1];
 }
 
 template <bool VEC, bool ROWS>
@@ -655,9 +657,18 @@ __global__ __launch_bounds__(TC_THREADS) void topk_output_kernel(const float* __
   int room = 0;
   if (c0 >= 0 && nvis > keep) {
     int need = keep - above0;
-    // pass A: bits 19 .. 9 of the candidates (all in bin c0)
+    // pass A: bits 19 .. 9 of the candidates (all in bin c0); pass B's bins and the per-chunk counts are cleared here
+    // too
     for (int i = t; i < 2048; i += TC_THREADS) sh.bins[i] = 0;
-    if (t == 0) sh.sel_bin = -1;
+    for (int i = t; i < 512; i += TC_THREADS) sh.bins2[i] = 0;
+    if (t == 0) {
+      sh.sel[0] = -1;
+      sh.sel2[0] = -1;
+    }
+    if (t < TC_MAXCH) {
+      sh.gt[t] = 0;
+      sh.tie[t] = 0;
+    }
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < TC_CAND / 16; ++k)
@@ -669,28 +680,21 @@ __global__ __launch_bounds__(TC_THREADS) void topk_output_kernel(const float* __
       }
     __syncthreads();
     int c1, above;
-    out_find_bin(sh, 2048, need, &c1, &above);
+    out_find_bin(sh, sh.bins, sh.sel, 2048, need, &c1, &above);
     need -= above;
     const uint32_t pre = ((uint32_t)c0 << 11) | (uint32_t)c1;
-    __syncthreads();
-    for (int i = t; i < 512; i += TC_THREADS) sh.bins[i] = 0;
-    if (t == 0) sh.sel_bin = -1;
-    if (t < TC_MAXCH) {
-      sh.gt[t] = 0;
-      sh.tie[t] = 0;
-    }
-    __syncthreads();
+    // pass B: bits 8 .. 0 of the candidates under the 23-bit prefix
 #pragma unroll
     for (int k = 0; k < TC_CAND / 16; ++k)
-      if (g < nchunks && sub + 16 * k < ncg && (ck[k] >> 9) == pre) atomicAdd(&sh.bins[ck[k] & 511], 1);
+      if (g < nchunks && sub + 16 * k < ncg && (ck[k] >> 9) == pre) atomicAdd(&sh.bins2[ck[k] & 511], 1);
     for (int r = 1; r * TC_CAND < maxc; ++r)
       for (int k = 0; k < TC_CAND / 16; ++k) {
         const int i = r * TC_CAND + sub + 16 * k;
-        if (g < nchunks && i < ncg && (cg[i] >> 9) == pre) atomicAdd(&sh.bins[cg[i] & 511], 1);
+        if (g < nchunks && i < ncg && (cg[i] >> 9) == pre) atomicAdd(&sh.bins2[cg[i] & 511], 1);
       }
     __syncthreads();
     int c2;
-    out_find_bin(sh, 512, need, &c2, &above);
+    out_find_bin(sh, sh.bins2, sh.sel2, 512, need, &c2, &above);
     T = (pre << 9) | (uint32_t)c2;
     room = need - above;
     room = room < 0 ? 0 : room;
