@@ -163,7 +163,7 @@ __device__ int row_find_bin(RowShared& sh, int nbins, int need, int* bin, int* a
 // positions 4 (1024 e + t) + c, e < G, c < 4 (coalesced float4 loads). HIST_IN: the row's top-12-bit histogram is in
 // hist[row] (read, then zeroed for the next call); otherwise it is built here.
 // IND: the row is the IndOut second level (scores / stride / len are unused; stride is the candidate row length).
-template <int G, bool HIST_IN, bool VEC, bool ROWS, bool IND = false>
+template <int G, bool HIST_IN, bool VEC, bool ROWS, bool IND = false, bool OUT64 = false>
 __global__ __launch_bounds__(TR_THREADS) void topk_row_kernel(const float* __restrict__ scores, int stride,
                                                               const int* __restrict__ len, int len_div, int len_mul,
                                                               int keep, int vis_only, int* __restrict__ hist,
@@ -313,8 +313,8 @@ __global__ __launch_bounds__(TR_THREADS) void topk_row_kernel(const float* __res
       const bool sel = a || (ti && t_before < room);
       const int o = a_before + (t_before < room ? t_before : room);
       if (sel && (unsigned)o < (unsigned)keep) {  // in range whatever the counts
-        if (IND) {
-          io.pools[(size_t)row * keep + o] = src[e] + c;
+        if (IND || OUT64) {  // the reference's outputs: int64 positions, their scores
+          io.pools[(size_t)row * keep + o] = (IND ? src[e] : p0) + c;
           io.vals[(size_t)row * keep + o] = key_to_float(key[e][c]);
         } else {
           orow[o] = p0 + c;
@@ -330,7 +330,7 @@ __global__ __launch_bounds__(TR_THREADS) void topk_row_kernel(const float* __res
   }
   const int cnt_row = nvis < keep ? nvis : keep;
   for (int i = cnt_row + t; i < keep; i += TR_THREADS) {
-    if (IND) {
+    if (IND || OUT64) {
       io.pools[(size_t)row * keep + i] = 0;
       io.vals[(size_t)row * keep + i] = NEG_INF;
     } else {
@@ -339,7 +339,7 @@ __global__ __launch_bounds__(TR_THREADS) void topk_row_kernel(const float* __res
     if (ROWS) so.rows[(size_t)row * keep + i] = sh.pg[0] * so.page_size;
   }
   if (t == 0) {
-    if (IND)
+    if (IND || OUT64)
       io.cnt[row] = cnt_row;
     else
       cnt_out[row] = cnt_row;
@@ -993,7 +993,10 @@ constexpr int TOPK_MANY_ROWS = 512;
 template <int G, bool VEC>
 static hipError_t launch_topk_row_plain(const float* scores, int stride, const int* len, int len_div, int len_mul,
                                         int keep, int vis_only, int* hist, int* idx, int* cnt, const SlotOut& so,
-                                        int B, hipStream_t s) {
+                                        int B, hipStream_t s, const IndOut* out64) {
+  if (out64)  // the reference's outputs written directly (IndOut's pools, cnt, vals)
+    return launch("topk_row_kernel", topk_row_kernel<G, false, VEC, false, false, true>, dim3(B), dim3(TR_THREADS), s,
+                  scores, stride, len, len_div, len_mul, keep, vis_only, hist, idx, cnt, so, *out64);
   return launch("topk_row_kernel", topk_row_kernel<G, false, VEC, false>, dim3(B), dim3(TR_THREADS), s, scores,
                 stride, len, len_div, len_mul, keep, vis_only, hist, idx, cnt, so, IndOut{});
 }
@@ -1001,27 +1004,27 @@ static hipError_t launch_topk_row_plain(const float* scores, int stride, const i
 template <bool VEC>
 static hipError_t launch_topk_many_rows(const float* scores, int stride, const int* len, int len_div, int len_mul,
                                         int max_len, int keep, int vis_only, int* hist, int* idx, int* cnt,
-                                        const SlotOut& so, int B, hipStream_t s) {
+                                        const SlotOut& so, int B, hipStream_t s, const IndOut* out64 = nullptr) {
   switch ((max_len + 4 * TR_THREADS - 1) / (4 * TR_THREADS)) {
     case 1:
       return launch_topk_row_plain<1, VEC>(scores, stride, len, len_div, len_mul, keep, vis_only, hist, idx, cnt, so,
-                                           B, s);
+                                           B, s, out64);
     case 2:
       return launch_topk_row_plain<2, VEC>(scores, stride, len, len_div, len_mul, keep, vis_only, hist, idx, cnt, so,
-                                           B, s);
+                                           B, s, out64);
     case 3:
       return launch_topk_row_plain<3, VEC>(scores, stride, len, len_div, len_mul, keep, vis_only, hist, idx, cnt, so,
-                                           B, s);
+                                           B, s, out64);
     case 4:
       return launch_topk_row_plain<4, VEC>(scores, stride, len, len_div, len_mul, keep, vis_only, hist, idx, cnt, so,
-                                           B, s);
+                                           B, s, out64);
     case 5:
     case 6:
       return launch_topk_row_plain<6, VEC>(scores, stride, len, len_div, len_mul, keep, vis_only, hist, idx, cnt, so,
-                                           B, s);
+                                           B, s, out64);
     default:
       return launch_topk_row_plain<8, VEC>(scores, stride, len, len_div, len_mul, keep, vis_only, hist, idx, cnt, so,
-                                           B, s);
+                                           B, s, out64);
   }
 }
 
@@ -1107,6 +1110,14 @@ static hipError_t topk_rows(const float* scores, int stride, const int* len, int
                             char* ws, int B, hipStream_t s, bool bm_ready = false, const SelectOut* out = nullptr) {
   const SlotOut none = {nullptr, 0, 0, 0, nullptr};
   if (n <= TOPK_FLAT_MAX) {
+    if (out && B >= TOPK_MANY_ROWS && !hist_ready && n > 4 * TR_THREADS) {
+      // many rows: the one-workgroup-per-row kernel writes the reference's outputs itself
+      const IndOut io = {nullptr, 0, nullptr, nullptr, nullptr, 0, out->pools, out->cnt, out->vals};
+      return (stride & 3) == 0 ? launch_topk_many_rows<true>(scores, stride, len, len_div, len_mul, (int)n, keep,
+                                                             vis_only, tb.hist, idx, cnt, none, B, s, &io)
+                               : launch_topk_many_rows<false>(scores, stride, len, len_div, len_mul, (int)n, keep,
+                                                              vis_only, tb.hist, idx, cnt, none, B, s, &io);
+    }
     hipError_t e = launch_topk_level(scores, stride, len, len_div, len_mul, (int)n, keep, vis_only, idx, cnt, tb,
                                      hist_ready, none, B, s);
     if (e != hipSuccess || !out) return e;
