@@ -8,7 +8,9 @@
  * caller-owned workspace sized by dsa_workspace_bytes(). A workspace must be zero-filled before its first use
  * (dsa_workspace_clear, or any zero fill); every call leaves the parts that must be zero at zero again, so one
  * workspace serves any number of calls (and of graph replays). Calls that share a workspace must not overlap.
- * Kernels never raise; every shape and argument check happens on the host before launch.
+ * Kernels never raise; every shape and argument check happens on the host before launch, so a call that returns
+ * DSA_EINVAL, DSA_EUNSUPPORTED or DSA_EWORKSPACE has written nothing. A call that returns DSA_ELAUNCH clears the
+ * regions it had dirtied; should that clearing fail too, run dsa_workspace_clear before the workspace's next use.
  *
  * Cache layout (the paged FP8 cache of trnrt/models/decoder.py:459-490 and trnrt/engine/model_runner.py:54-70,
  * extended with per-token scales):

@@ -123,6 +123,30 @@ def test_select_exact_on_the_kernels_scores(P, keep):
         assert torch.all(vp[n, c:] == 0) and torch.all(vv[n, c:] == O.NEG_INF)
 
 
+@pytest.mark.parametrize("q_fp8", [False, True])
+def test_select_two_level_sub_blocks_of_two(q_fp8):
+    """Two-level selection with sub-blocks of 2 (P 40,000, keep 6,000): the indexer writes the sub-block maxima
+    score by score (a 16-byte read would take the next sub-block's scores into a maximum), and the selection is
+    bit-exact against the exact selection of the kernel's own scores, for bf16 and FP8 queries."""
+    P, keep, N = 40000, 6000, 6
+    say(f"prefill select sub 2 P={P} keep={keep} q_fp8={q_fp8}")
+    qI, w, k8, ks, npool = _inputs(N, 64, P, seed=77 + q_fp8)
+    npool[0], npool[1], npool[2] = P, keep - 3, 0
+    qs = None
+    if q_fp8:
+        qI, qs, _ = _fp8(qI)
+        qs = qs.cuda()
+    args = (qI.cuda(), w.cuda(), k8.cuda(), npool.cuda())
+    sc = LS.scores(*args, 128 ** -0.5, pk_scale=ks.cuda(), qI_scale=qs).cpu()
+    pools, cnt, vals = LS.select(*args, keep, 128 ** -0.5, pk_scale=ks.cuda(), qI_scale=qs)
+    torch.cuda.synchronize()
+    ri, rc = O.topk_ref(sc, keep, npool)
+    assert torch.equal(cnt.cpu(), rc)
+    assert torch.equal(pools.cpu(), ri)
+    live = torch.arange(keep).view(1, -1) < rc.view(-1, 1)
+    assert torch.equal(vals.cpu(), torch.where(live, sc.gather(1, ri), O.NEG_INF))
+
+
 def test_decode_batch_form_of_dsa_long_scores():
     """dsa_long.scores with one context per row ([N, P, 128] keys) through the decode indexer."""
     say("dsa_long.scores 3-D keys")

@@ -43,6 +43,7 @@ hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t s);
 hipError_t launch_topk_mask(const int* idx, const int* cnt, const float* scores, float* mask, int B, int keep, int P,
                             int kp, int tail, hipStream_t s);
 size_t topk_workspace_bytes(int B, int max_len, int keep);
+size_t topk_hist_bytes(int B);
 bool topk_supported(int max_len, int keep, int vis_only);
 hipError_t launch_sparse_mla(const uint16_t* q, const uint8_t* kv, const float* kvs, const int* idx, const int* cnt,
                              const int* table, const int* rows, const float* bias, uint16_t* out, float* out_f32,
@@ -355,11 +356,14 @@ int dsa_decode_layer(const void* q_idx_bf16, const float* w, const uint8_t* k_fp
                      const int32_t* ctx_len, float* scores, int32_t* idx, int32_t* cnt, void* out_bf16, float* lse,
                      void* workspace, size_t workspace_bytes, int B, int Hi, int H, int max_pages, int page_size,
                      int num_pages, int score_stride, int max_len, int keep, float scale, int splits, void* stream) {
+  // every check before the first launch: a rejected call writes nothing
   if (!q_idx_bf16 || !w || !k_fp8 || !k_scale || !page_table || !ctx_len || !scores || !idx || !cnt || !workspace)
     return DSA_EINVAL;
-  if (B < 0 || Hi < 1 || max_pages < 1 || page_size < 1 || num_pages < 1 || keep < 1) return DSA_EINVAL;
+  if (!q_bf16 || !kv_fp8 || !kv_scale || !out_bf16) return DSA_EINVAL;
+  if (B < 0 || Hi < 1 || H < 1 || max_pages < 1 || page_size < 1 || num_pages < 1 || keep < 1) return DSA_EINVAL;
   if (max_len < 1 || max_len > score_stride || (long)score_stride > (long)max_pages * page_size) return DSA_EINVAL;
-  if (Hi > 64 || page_size % 32) return DSA_EUNSUPPORTED;
+  if (Hi > 64 || page_size % 32 || H % 16) return DSA_EUNSUPPORTED;
+  if ((long)num_pages * page_size > 0x7fffffffL) return DSA_EUNSUPPORTED;
   if (!dsa::topk_supported(max_len, keep, 1)) return DSA_EUNSUPPORTED;
   if (workspace_bytes < dsa_workspace_bytes(DSA_WS_LAYER, B, H, keep, max_len, splits)) return DSA_EWORKSPACE;
   if (B == 0) return DSA_OK;
@@ -376,16 +380,18 @@ int dsa_decode_layer(const void* q_idx_bf16, const float* w, const uint8_t* k_fp
   int* rows = fused_hist ? reinterpret_cast<int*>(static_cast<char*>(workspace) + t_need) : nullptr;
   e = dsa::launch_topk(scores, ctx_len, idx, cnt, workspace, B, score_stride, max_len, keep, 1, fused_hist,
                        page_table, max_pages, page_size, num_pages, rows, s);
-  if (e != hipSuccess) return DSA_ELAUNCH;
+  if (e != hipSuccess) {
+    // the indexer has added into the histograms, which the top-k would have cleared: clear them here, so that the
+    // workspace stays usable (if this launch fails too, dsa_workspace_clear must run before the next call)
+    dsa::launch_fill_zero(workspace, dsa::topk_hist_bytes(B), s);
+    return DSA_ELAUNCH;
+  }
   char* aws = static_cast<char*>(workspace) + t_need + layer_rows_bytes(B, keep);
   const size_t aws_bytes = workspace_bytes - t_need - layer_rows_bytes(B, keep);
   if (!rows)
     return dsa_sparse_mla_decode(q_bf16, kv_fp8, kv_scale, idx, cnt, page_table, nullptr, nullptr, out_bf16, nullptr,
                                  lse, aws, aws_bytes, B, H, 576, 512, keep, max_pages, page_size, num_pages, scale,
                                  splits, stream);
-  if (!q_bf16 || !kv_fp8 || !kv_scale || !out_bf16) return DSA_EINVAL;
-  if (H < 1 || H % 16) return DSA_EUNSUPPORTED;
-  if ((long)num_pages * page_size > 0x7fffffffL) return DSA_EUNSUPPORTED;
   const int sp = effective_splits(resolve_splits(splits, B, H, keep), keep);
   return status(dsa::launch_sparse_mla(static_cast<const uint16_t*>(q_bf16), kv_fp8, kv_scale, nullptr, cnt, nullptr,
                                        rows, nullptr, static_cast<uint16_t*>(out_bf16), nullptr, lse, aws, B, H, 576,
@@ -460,7 +466,11 @@ int dsa_pooled_decode_layer(const void* q_idx_bf16, const float* w, const void* 
   if (e != hipSuccess) return DSA_ELAUNCH;
   e = dsa::launch_topk(scores, npool, pools, cnt, workspace, B, stride, stride, keep, 1, fused_hist, nullptr, 0, 0, 0,
                        nullptr, s);
-  if (e != hipSuccess) return DSA_ELAUNCH;
+  if (e != hipSuccess) {
+    // the histograms the indexer added into stay zero for the next call (as in dsa_decode_layer)
+    dsa::launch_fill_zero(workspace, dsa::topk_hist_bytes(B), s);
+    return DSA_ELAUNCH;
+  }
   const int keep_sel = kp * keep;  // the selected pools' token slots; the tail comes on top
   const int sp = effective_splits(resolve_splits(splits, B, H, keep_sel), keep_sel);
   const dsa::PoolForm pf = {__builtin_ctz((unsigned)kp), keep, npool, positions, 0};

@@ -35,12 +35,14 @@ static_assert(PF_TILES % PF_RING == 0, "a block is whole ring turns");
 // wave of query n reads its row's scores of the block [p_begin, p_end) back (srow[p - base]: the FP8 form
 // from its LDS copy of them, the bf16 form from the L2 after a barrier) and writes bm[n, b] = the maximum of the
 // 2^sub_log2 scores of sub-block b, for b below nb. Scores past the candidates are NEG_INF, so this is the maximum
-// over the candidates, as block_max_kernel computes it; vec: 16-byte reads (16-byte aligned rows, sub-blocks of at
-// least 4).
+// over the candidates, as block_max_kernel computes it; vec: 16-byte aligned rows, read 16 bytes at a time where a
+// sub-block holds a whole number of float4s (sub-blocks of 2 are read score by score: a float4 would take the next
+// sub-block's two scores into this one's maximum).
 __device__ __forceinline__ void block_max_rows(const float* srow, int base, float* __restrict__ bmrow, int p_begin,
                                                int p_end, int sub_log2, int nb, bool vec, int lane) {
   const int sub = 1 << sub_log2;
   const int b1 = min(nb, (p_end + sub - 1) >> sub_log2);
+  vec = vec && sub >= 4;
   for (int b = (p_begin >> sub_log2) + lane; b < b1; b += WAVE) {
     const int p0 = b << sub_log2;
     float m = NEG_INF;
