@@ -31,13 +31,14 @@
 extern "C" {
 #endif
 
-#define DSA_ABI_VERSION 5
+#define DSA_ABI_VERSION 6
 
 #define DSA_OK 0
 #define DSA_EINVAL (-1)      /* a null pointer or a size out of range */
 #define DSA_EUNSUPPORTED (-2) /* a shape these kernels do not implement */
 #define DSA_EWORKSPACE (-3)  /* workspace smaller than dsa_workspace_bytes() */
 #define DSA_ELAUNCH (-4)     /* the HIP runtime refused a launch */
+#define DSA_ESCRATCH (-5)    /* more scratch than dsa_decode_layer_noalloc holds */
 
 /* Workspace kinds for dsa_workspace_bytes(). */
 #define DSA_WS_TOPK 1
@@ -198,6 +199,24 @@ int dsa_decode_layer(const void* q_idx_bf16, const float* w, const uint8_t* k_fp
                      const int32_t* ctx_len, float* scores, int32_t* idx, int32_t* cnt, void* out_bf16, float* lse,
                      void* workspace, size_t workspace_bytes, int B, int Hi, int H, int max_pages, int page_size,
                      int num_pages, int score_stride, int max_len, int keep, float scale, int splits, void* stream);
+
+/*
+ * dsa_decode_layer without a workspace argument, allocating nothing (no counterpart in the reference: for callers
+ * that cannot allocate device memory, such as code under HIP graph capture, tight serving loops or harnesses that
+ * forbid hipMalloc). The workspace is the library's own scratch, a static device array of
+ * DSA_NOALLOC_SCRATCH_BYTES per GPU (allocated with the library's code object on each GPU it runs on and held until
+ * the process ends; zero-filled by a kernel on `stream` at the first call on a device). A call whose
+ * dsa_workspace_bytes(DSA_WS_LAYER, B, H, keep, max_len, splits) exceeds that size returns DSA_ESCRATCH before any
+ * HIP call. Every call on a GPU shares that GPU's scratch: calls that overlap on one GPU (several streams, host
+ * threads) race and must be serialised by the caller. Arguments and results as dsa_decode_layer.
+ */
+#define DSA_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+int dsa_decode_layer_noalloc(const void* q_idx_bf16, const float* w, const uint8_t* k_fp8, const float* k_scale,
+                             const void* q_bf16, const uint8_t* kv_fp8, const float* kv_scale,
+                             const int32_t* page_table, const int32_t* ctx_len, float* scores, int32_t* idx,
+                             int32_t* cnt, void* out_bf16, float* lse, int B, int Hi, int H, int max_pages,
+                             int page_size, int num_pages, int score_stride, int max_len, int keep, float scale,
+                             int splits, void* stream);
 
 /*
  * Absorbed MLA over a pooled selection (replaces trnrt/models/dsa_long.py:189-215 `slots` + :218-223 `attend`

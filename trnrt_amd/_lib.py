@@ -23,12 +23,14 @@ DSA_EINVAL = -1
 DSA_EUNSUPPORTED = -2
 DSA_EWORKSPACE = -3
 DSA_ELAUNCH = -4
+DSA_ESCRATCH = -5
+NOALLOC_SCRATCH_BYTES = 32 << 20
 
 DSA_WS_TOPK = 1
 DSA_WS_ATTENTION = 2
 DSA_WS_LAYER = 3
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 P = c_void_p
 # Every entry point of include/dsa_gfx950.h with its ctypes signature (restype, argtypes).
@@ -57,6 +59,11 @@ SIGNATURES: dict[str, tuple] = {
         c_int,
         [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, c_size_t, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
          c_int, c_int, c_float, c_int, P],
+    ),
+    "dsa_decode_layer_noalloc": (
+        c_int,
+        [P, P, P, P, P, P, P, P, P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
+         c_float, c_int, P],
     ),
     "dsa_pooled_decode_layer": (
         c_int,
@@ -110,7 +117,7 @@ def check(status: int, what: str) -> None:
     if status == DSA_OK:
         return
     msg = f"{what}: {lib().dsa_strerror(status).decode()}"
-    if status in (DSA_EINVAL, DSA_EWORKSPACE):
+    if status in (DSA_EINVAL, DSA_EWORKSPACE, DSA_ESCRATCH):
         raise ValueError(msg)
     if status == DSA_EUNSUPPORTED:
         raise NotImplementedError(msg)

@@ -2,6 +2,8 @@
 // shapes, and the launches on the caller's stream. Nothing here allocates device memory or synchronises.
 #include "../../include/dsa_gfx950.h"
 
+#include <mutex>
+
 #include "dsa_common.h"
 
 namespace dsa {
@@ -59,6 +61,12 @@ size_t attention_workspace_bytes(int B, int H, int splits);
 thread_local KernelTimer* g_kernel_timer = nullptr;
 }  // namespace dsa
 
+// The scratch of dsa_decode_layer_noalloc: a file-scope device array of DSA_NOALLOC_SCRATCH_BYTES, one copy on each
+// GPU the library runs on (held until the process ends). In host code `scratch` names a host-side stand-in, not a
+// device address: the per-device address comes from hipGetSymbolAddress (noalloc_scratch below), and only that address
+// reaches kernels and fills.
+static __device__ __align__(256) uint8_t scratch[DSA_NOALLOC_SCRATCH_BYTES];
+
 namespace {
 
 thread_local dsa::KernelTimer t_timer;
@@ -89,6 +97,26 @@ int effective_splits(int splits, int keep) {
   int sps = (keep + splits - 1) / splits;
   sps = (sps + 63) / 64 * 64;
   return (keep + sps - 1) / sps;
+}
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's scratch address; on the first call for a device (with that device current) its address is
+// looked up and the array zero-filled on `stream` (a fill kernel, ordered before the call that uses it), so the
+// regions dsa_decode_layer needs at zero start at zero; every call leaves them so. Null on a HIP error.
+void* noalloc_scratch(hipStream_t stream) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
+    if (dsa::launch_fill_zero(ptr, DSA_NOALLOC_SCRATCH_BYTES, stream) != hipSuccess) return nullptr;
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
 }
 
 }  // namespace
@@ -130,6 +158,8 @@ const char* dsa_strerror(int s) {
       return "workspace too small";
     case DSA_ELAUNCH:
       return "kernel launch failed";
+    case DSA_ESCRATCH:
+      return "the call needs more scratch than the allocation-free entry point holds (DSA_NOALLOC_SCRATCH_BYTES)";
     default:
       return "unknown status";
   }
@@ -396,6 +426,24 @@ int dsa_decode_layer(const void* q_idx_bf16, const float* w, const uint8_t* k_fp
   return status(dsa::launch_sparse_mla(static_cast<const uint16_t*>(q_bf16), kv_fp8, kv_scale, nullptr, cnt, nullptr,
                                        rows, nullptr, static_cast<uint16_t*>(out_bf16), nullptr, lse, aws, B, H, 576,
                                        keep, max_pages, page_size, num_pages, scale, sp, s));
+}
+
+int dsa_decode_layer_noalloc(const void* q_idx_bf16, const float* w, const uint8_t* k_fp8, const float* k_scale,
+                             const void* q_bf16, const uint8_t* kv_fp8, const float* kv_scale,
+                             const int32_t* page_table, const int32_t* ctx_len, float* scores, int32_t* idx,
+                             int32_t* cnt, void* out_bf16, float* lse, int B, int Hi, int H, int max_pages,
+                             int page_size, int num_pages, int score_stride, int max_len, int keep, float scale,
+                             int splits, void* stream) {
+  // the size checks first (no HIP call for a refused size): the layer's workspace must fit the scratch
+  if (B < 0 || H < 1 || keep < 1 || max_len < 1) return DSA_EINVAL;
+  const size_t need = dsa_workspace_bytes(DSA_WS_LAYER, B, H, keep, max_len, splits);
+  if (need == 0 || need > DSA_NOALLOC_SCRATCH_BYTES) return DSA_ESCRATCH;
+  if (B == 0) return DSA_OK;
+  void* ws = noalloc_scratch(static_cast<hipStream_t>(stream));
+  if (!ws) return DSA_ELAUNCH;
+  return dsa_decode_layer(q_idx_bf16, w, k_fp8, k_scale, q_bf16, kv_fp8, kv_scale, page_table, ctx_len, scores, idx,
+                          cnt, out_bf16, lse, ws, DSA_NOALLOC_SCRATCH_BYTES, B, Hi, H, max_pages, page_size,
+                          num_pages, score_stride, max_len, keep, scale, splits, stream);
 }
 
 size_t dsa_sparse_mla_pooled_workspace_bytes(int B, int H, int keep, int kp, int splits) {
