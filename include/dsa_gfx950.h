@@ -190,15 +190,30 @@ int dsa_prefill_select(const void* q, const float* q_scale, const float* w, cons
 size_t dsa_prefill_select_workspace_bytes(int N, int P, int keep);
 
 /*
- * The whole DSA decode layer step: indexer -> top-k -> sparse MLA, enqueued back to back on one stream
- * (the order of trnrt/models/mla.py:506-528 `attention_long` at kp = 1). scores/idx/cnt are the intermediates
- * the caller may read afterwards (scores fp32 [B, score_stride], idx int32 [B, keep], cnt int32 [B]).
+ * The whole DSA decode layer step: indexer -> top-k -> sparse MLA (the order of trnrt/models/mla.py:506-528
+ * `attention_long` at kp = 1; one call per step as trnrt/kernels/dsa_shell.py:2114-2321 `select2` fuses it).
+ * scores/idx/cnt are the intermediates the caller may read afterwards (scores fp32 [B, score_stride], idx int32
+ * [B, keep], cnt int32 [B]). On a GPU of 8 XCDs x 32 CUs with rows of at most 32,768 tokens (and the shapes the
+ * one-launch kernel takes: Hi <= 64, H a multiple of 16 up to 512, pages of a power of two >= 32, score_stride a
+ * multiple of 4, keep <= 256 * (512 / H)) the step is one kernel launch; otherwise it is dsa_decode_layer_chain.
  */
 int dsa_decode_layer(const void* q_idx_bf16, const float* w, const uint8_t* k_fp8, const float* k_scale,
                      const void* q_bf16, const uint8_t* kv_fp8, const float* kv_scale, const int32_t* page_table,
                      const int32_t* ctx_len, float* scores, int32_t* idx, int32_t* cnt, void* out_bf16, float* lse,
                      void* workspace, size_t workspace_bytes, int B, int Hi, int H, int max_pages, int page_size,
                      int num_pages, int score_stride, int max_len, int keep, float scale, int splits, void* stream);
+
+/*
+ * The same step as separate kernels enqueued back to back on one stream (indexer with the top-k's first-level
+ * histogram fused, top-k, attention, split combine): any shape dsa_decode_layer accepts. Same arguments, results and
+ * workspace.
+ */
+int dsa_decode_layer_chain(const void* q_idx_bf16, const float* w, const uint8_t* k_fp8, const float* k_scale,
+                           const void* q_bf16, const uint8_t* kv_fp8, const float* kv_scale,
+                           const int32_t* page_table, const int32_t* ctx_len, float* scores, int32_t* idx,
+                           int32_t* cnt, void* out_bf16, float* lse, void* workspace, size_t workspace_bytes, int B,
+                           int Hi, int H, int max_pages, int page_size, int num_pages, int score_stride, int max_len,
+                           int keep, float scale, int splits, void* stream);
 
 /*
  * dsa_decode_layer without a workspace argument, allocating nothing (no counterpart in the reference: for callers

@@ -1,0 +1,151 @@
+"""The one-launch decode layer (dsa_decode_layer on rows of up to 32,768 tokens: csrc/dsa_fused.hip) against the
+oracle and against the separate-kernel form (dsa_decode_layer_chain) on the same seeded inputs.
+
+Bounds (the north star's): indexer scores within 1e-2 row-relative of oracle/dsa_oracle.py indexer_ref (after
+trnrt/kernels/dsa_index.py:44-50); the top-k indices and counts bit-exact against the oracle's selection of the
+kernel's own scores (topk_ref, after trnrt/models/dsa_select.py:33-38); the bf16 output within 2e-2 and lse within
+1e-3 of the oracle attention over the kernel's selection (after trnrt/kernels/dsa_decode.py:26-37). Cases: configs 1
+and 2 in full, a ragged batch of 12 rows (two launches) with empty, one-token, shorter-than-keep and full rows, 16 and
+32 query heads with 16 and 48 indexer heads, rows of equal scores (every key a tie: the candidates past the LDS
+cache) and of two score values, and the workspace left as the next call needs it (histograms and barrier words zero,
+no barrier wait gave up)."""
+
+import pytest
+import torch
+
+from oracle import dsa_oracle as O
+from tests._helpers import assert_attention_close, launched_kernels, row_rel_err, say
+from tests.test_gpu_layer import _attention_check
+from trnrt_amd import workloads as W
+from trnrt_amd.kernels.dsa_layer import DecodeLayer
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(g, chain=False):
+    cfg = g.cfg
+    L = DecodeLayer(cfg.B, cfg.Hi, cfg.H, g.max_pages, cfg.page_size, g.num_pages, cfg.keep, cfg.scale,
+                    max_len=max(max(g.lengths), 1), chain=chain)
+    L.step(g.q_idx, g.w_k, g.k_cache, g.k_scale, g.q, g.kv_cache, g.kv_scale, g.table, g.ctx_len)
+    torch.cuda.synchronize()
+    return L
+
+
+def _workspace_clean(L):
+    """The histograms and the per-XCD barrier words (arrivals, exits) are zero again, and no error flag is set."""
+    ws = L.workspace.view(torch.int32).cpu()
+    hist_words = L.B * 4096
+    assert torch.all(ws[:hist_words] == 0), "row histograms left non-zero"
+    sync = ws[hist_words:hist_words + 8 * 16].view(8, 16)
+    assert torch.all(sync[:, :2] == 0), f"barrier words left non-zero: {sync[:, :3].tolist()}"
+    assert torch.all(sync[:, 2] == 0), "a barrier wait gave up (error flag set)"
+
+
+def _check_full(inp, L, indexer=True):
+    cfg = inp.cfg
+    sc = L.scores.cpu()
+    if indexer:
+        ref = O.indexer_ref(inp.q_idx, inp.w_k, inp.k_cache, inp.k_scale, inp.table, inp.ctx_len, cfg.page_size,
+                            sc.shape[1])
+        err = row_rel_err(sc, ref, ref > -1e29)
+        say(f"  indexer rel err {err:.3e}")
+        assert err <= 1e-2
+        assert torch.all(sc[ref <= -1e29] == O.NEG_INF)
+    ri, rc = O.topk_ref(sc, cfg.keep, inp.ctx_len)
+    assert torch.equal(L.cnt.cpu().long(), rc)
+    assert torch.equal(L.idx.cpu().long(), ri)
+    _attention_check(inp, L)
+
+
+@pytest.mark.parametrize("c", [1, 2])
+def test_fused_layer_configs(c):
+    say(f"fused layer config {c}")
+    inp = W.make_inputs(W.CONFIGS[c], seed=3)
+    g = inp.to("cuda")
+    L = _run(g)
+    names = launched_kernels(lambda: L.step(g.q_idx, g.w_k, g.k_cache, g.k_scale, g.q, g.kv_cache, g.kv_scale,
+                                            g.table, g.ctx_len))
+    assert names == ["decode_fused_kernel"], names
+    _check_full(inp, L)
+    _workspace_clean(L)
+
+
+def test_fused_layer_ragged_two_launches():
+    lengths = [32768, 1, 0, 2047, 2048, 2049, 5000, 31999, 32000, 64, 100, 17000]
+    say(f"fused layer ragged B=12 {lengths}")
+    cfg = W.Config("fused-ragged", B=12, L=32768, H=64, Hi=64)
+    inp = W.make_inputs(cfg, seed=4, lengths=lengths)
+    g = inp.to("cuda")
+    L = _run(g)
+    names = launched_kernels(lambda: L.step(g.q_idx, g.w_k, g.k_cache, g.k_scale, g.q, g.kv_cache, g.kv_scale,
+                                            g.table, g.ctx_len))
+    assert names == ["decode_fused_kernel"] * 2, names
+    _check_full(inp, L)
+    _workspace_clean(L)
+
+
+@pytest.mark.parametrize("H,Hi", [(16, 16), (32, 48), (128, 64)])
+def test_fused_layer_head_counts(H, Hi):
+    say(f"fused layer H={H} Hi={Hi}")
+    keep = 1024 if H == 128 else 2048  # 128 heads: 4 splits of 256 slots
+    cfg = W.Config(f"fused-h{H}", B=3, L=10000, H=H, Hi=Hi, keep=keep)
+    inp = W.make_inputs(cfg, seed=5 + H, lengths=[4096, 3000, 10000])
+    g = inp.to("cuda")
+    L = _run(g)
+    _check_full(inp, L)
+    _workspace_clean(L)
+
+
+def _tied_inputs(values: int):
+    """A batch whose key rows take `values` patterns (row t of the cache: pattern t % values), so the scores of a row
+    take at most that many values and the keep-th is tied with many others."""
+    cfg = W.Config(f"fused-ties{values}", B=3, L=32768, H=64, Hi=64)
+    inp = W.make_inputs(cfg, seed=6 + values, lengths=[32768, 20000, 2500])
+    base_k, base_s = inp.k_cache[64:64 + values].clone(), inp.k_scale[64:64 + values].clone()
+    n = inp.k_cache.shape[0]
+    rep = (n + values - 1) // values
+    inp.k_cache.copy_(base_k.repeat(rep, 1)[:n])
+    inp.k_scale.copy_(base_s.repeat(rep)[:n])
+    return inp
+
+
+@pytest.mark.parametrize("values", [1, 2])
+def test_fused_layer_ties(values):
+    say(f"fused layer ties values={values}")
+    inp = _tied_inputs(values)
+    L = _run(inp.to("cuda"))
+    sc = L.scores.cpu()
+    for b, n in enumerate(inp.lengths):  # ties by construction: one score value per pattern in each row
+        assert len(torch.unique(sc[b, :n])) <= values
+    _check_full(inp, L, indexer=False)
+    _workspace_clean(L)
+
+
+def test_fused_matches_chain():
+    """The one-launch and the separate-kernel forms of the same step: the same scores and selection, outputs within
+    the bound (the attention's split sizes differ, so fp32 summation order does too)."""
+    say("fused vs chain")
+    lengths = [32768, 9000, 30000, 2048, 12345, 32768, 700, 25000]
+    cfg = W.Config("fused-vs-chain", B=8, L=32768, H=64, Hi=64)
+    g = W.make_inputs(cfg, seed=9, lengths=lengths).to("cuda")
+    Lf, Lc = _run(g), _run(g, chain=True)
+    assert torch.equal(Lf.scores, Lc.scores)
+    assert torch.equal(Lf.idx, Lc.idx) and torch.equal(Lf.cnt, Lc.cnt)
+    assert_attention_close(Lf.out, Lc.out)
+    torch.testing.assert_close(Lf.lse.cpu(), Lc.lse.cpu(), atol=1e-3, rtol=1e-4)
+
+
+def test_fused_repeated_steps_same_workspace():
+    """Ten steps on one workspace, the inputs changed in place between them: every step equals a fresh layer's."""
+    say("fused repeated steps")
+    cfg = W.CONFIGS[2]
+    g = W.make_inputs(cfg, seed=10).to("cuda")
+    L = _run(g)
+    for i in range(10):
+        g.q.mul_(-1.0) if i % 2 else g.q_idx.mul_(-1.0)
+        L.step(g.q_idx, g.w_k, g.k_cache, g.k_scale, g.q, g.kv_cache, g.kv_scale, g.table, g.ctx_len)
+    torch.cuda.synchronize()
+    F = _run(g)
+    assert torch.equal(L.idx, F.idx) and torch.equal(L.cnt, F.cnt)
+    assert torch.equal(L.out, F.out) and torch.equal(L.lse, F.lse)
+    _workspace_clean(L)

@@ -60,6 +60,11 @@ SIGNATURES: dict[str, tuple] = {
         [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, c_size_t, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
          c_int, c_int, c_float, c_int, P],
     ),
+    "dsa_decode_layer_chain": (
+        c_int,
+        [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, c_size_t, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
+         c_int, c_int, c_float, c_int, P],
+    ),
     "dsa_decode_layer_noalloc": (
         c_int,
         [P, P, P, P, P, P, P, P, P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,

@@ -46,6 +46,14 @@ hipError_t launch_topk_mask(const int* idx, const int* cnt, const float* scores,
                             int kp, int tail, hipStream_t s);
 size_t topk_workspace_bytes(int B, int max_len, int keep);
 size_t topk_hist_bytes(int B);
+size_t topk_zero_bytes(int B);
+bool fused_layer_ok(int num_cu, int Hi, int H, int max_len, int keep, int page_size, int stride);
+size_t fused_layer_bytes(size_t zero_bytes, int B, int H, int keep);
+hipError_t launch_decode_fused(const uint16_t* q_idx, const float* w, const uint8_t* k, const float* ks,
+                               const uint16_t* q, const uint8_t* kv, const float* kvs, const int* table,
+                               const int* ctx_len, float* scores, int* idx, int* cnt, uint16_t* out, float* lse,
+                               void* ws, size_t hist_bytes, size_t zero_bytes, int B, int Hi, int H, int max_pages,
+                               int page_size, int num_pages, int stride, int keep, float scale, hipStream_t s);
 bool topk_supported(int max_len, int keep, int vis_only);
 hipError_t launch_sparse_mla(const uint16_t* q, const uint8_t* kv, const float* kvs, const int* idx, const int* cnt,
                              const int* table, const int* rows, const float* bias, uint16_t* out, float* out_f32,
@@ -373,7 +381,12 @@ size_t dsa_workspace_bytes(int kind, int B, int H, int keep, int max_len, int sp
     const int sp = effective_splits(resolve_splits(splits, B, H, keep), keep);
     a = dsa::attention_workspace_bytes(B, H, sp);
   }
-  return align256(t) + align256(a);
+  size_t total = align256(t) + align256(a);
+  if (kind == DSA_WS_LAYER) {  // the one-launch layer's layout shares the zero region and needs its own rest
+    const size_t f = dsa::fused_layer_bytes(dsa::topk_zero_bytes(B), B, H, keep);
+    total = f > total ? f : total;
+  }
+  return total;
 }
 
 int dsa_default_splits(int B, int H, int keep) {
@@ -381,12 +394,13 @@ int dsa_default_splits(int B, int H, int keep) {
   return effective_splits(resolve_splits(0, B, H, keep), keep);
 }
 
-int dsa_decode_layer(const void* q_idx_bf16, const float* w, const uint8_t* k_fp8, const float* k_scale,
-                     const void* q_bf16, const uint8_t* kv_fp8, const float* kv_scale, const int32_t* page_table,
-                     const int32_t* ctx_len, float* scores, int32_t* idx, int32_t* cnt, void* out_bf16, float* lse,
-                     void* workspace, size_t workspace_bytes, int B, int Hi, int H, int max_pages, int page_size,
-                     int num_pages, int score_stride, int max_len, int keep, float scale, int splits, void* stream) {
-  // every check before the first launch: a rejected call writes nothing
+// The decode layer's checks, shared by both forms (every check before the first launch: a rejected call writes
+// nothing).
+static int layer_checks(const void* q_idx_bf16, const float* w, const uint8_t* k_fp8, const float* k_scale,
+                        const void* q_bf16, const uint8_t* kv_fp8, const float* kv_scale, const int32_t* page_table,
+                        const int32_t* ctx_len, float* scores, int32_t* idx, int32_t* cnt, void* out_bf16,
+                        void* workspace, size_t workspace_bytes, int B, int Hi, int H, int max_pages, int page_size,
+                        int num_pages, int score_stride, int max_len, int keep, int splits) {
   if (!q_idx_bf16 || !w || !k_fp8 || !k_scale || !page_table || !ctx_len || !scores || !idx || !cnt || !workspace)
     return DSA_EINVAL;
   if (!q_bf16 || !kv_fp8 || !kv_scale || !out_bf16) return DSA_EINVAL;
@@ -396,7 +410,39 @@ int dsa_decode_layer(const void* q_idx_bf16, const float* w, const uint8_t* k_fp
   if ((long)num_pages * page_size > 0x7fffffffL) return DSA_EUNSUPPORTED;
   if (!dsa::topk_supported(max_len, keep, 1)) return DSA_EUNSUPPORTED;
   if (workspace_bytes < dsa_workspace_bytes(DSA_WS_LAYER, B, H, keep, max_len, splits)) return DSA_EWORKSPACE;
-  if (B == 0) return DSA_OK;
+  return DSA_OK;
+}
+
+int dsa_decode_layer(const void* q_idx_bf16, const float* w, const uint8_t* k_fp8, const float* k_scale,
+                     const void* q_bf16, const uint8_t* kv_fp8, const float* kv_scale, const int32_t* page_table,
+                     const int32_t* ctx_len, float* scores, int32_t* idx, int32_t* cnt, void* out_bf16, float* lse,
+                     void* workspace, size_t workspace_bytes, int B, int Hi, int H, int max_pages, int page_size,
+                     int num_pages, int score_stride, int max_len, int keep, float scale, int splits, void* stream) {
+  const int st = layer_checks(q_idx_bf16, w, k_fp8, k_scale, q_bf16, kv_fp8, kv_scale, page_table, ctx_len, scores,
+                              idx, cnt, out_bf16, workspace, workspace_bytes, B, Hi, H, max_pages, page_size,
+                              num_pages, score_stride, max_len, keep, splits);
+  if (st != DSA_OK || B == 0) return st;
+  if (!dsa::fused_layer_ok(num_cu(), Hi, H, max_len, keep, page_size, score_stride))
+    return dsa_decode_layer_chain(q_idx_bf16, w, k_fp8, k_scale, q_bf16, kv_fp8, kv_scale, page_table, ctx_len,
+                                  scores, idx, cnt, out_bf16, lse, workspace, workspace_bytes, B, Hi, H, max_pages,
+                                  page_size, num_pages, score_stride, max_len, keep, scale, splits, stream);
+  return status(dsa::launch_decode_fused(
+      static_cast<const uint16_t*>(q_idx_bf16), w, k_fp8, k_scale, static_cast<const uint16_t*>(q_bf16), kv_fp8,
+      kv_scale, page_table, ctx_len, scores, idx, cnt, static_cast<uint16_t*>(out_bf16), lse, workspace,
+      dsa::topk_hist_bytes(B), dsa::topk_zero_bytes(B), B, Hi, H, max_pages, page_size, num_pages, score_stride, keep,
+      scale, static_cast<hipStream_t>(stream)));
+}
+
+int dsa_decode_layer_chain(const void* q_idx_bf16, const float* w, const uint8_t* k_fp8, const float* k_scale,
+                           const void* q_bf16, const uint8_t* kv_fp8, const float* kv_scale,
+                           const int32_t* page_table, const int32_t* ctx_len, float* scores, int32_t* idx,
+                           int32_t* cnt, void* out_bf16, float* lse, void* workspace, size_t workspace_bytes, int B,
+                           int Hi, int H, int max_pages, int page_size, int num_pages, int score_stride, int max_len,
+                           int keep, float scale, int splits, void* stream) {
+  const int st = layer_checks(q_idx_bf16, w, k_fp8, k_scale, q_bf16, kv_fp8, kv_scale, page_table, ctx_len, scores,
+                              idx, cnt, out_bf16, workspace, workspace_bytes, B, Hi, H, max_pages, page_size,
+                              num_pages, score_stride, max_len, keep, splits);
+  if (st != DSA_OK || B == 0) return st;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const size_t t_need = align256(dsa::topk_workspace_bytes(B, max_len, keep));
   // flat rows: the indexer accumulates the top-k's first-level histogram (the workspace's first region)

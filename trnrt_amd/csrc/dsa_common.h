@@ -66,6 +66,9 @@ struct PoolForm {
   int tail_apart;
 };
 constexpr int HIST_REPLICAS = 1;
+// Bytes after the histograms that a workspace keeps at zero between calls: the fused decode layer's per-XCD barrier
+// words (the separate kernels never touch them).
+constexpr int WS_SYNC_BYTES = 1024;
 
 // s_waitcnt's immediate for "vector memory count <= n" (expcnt and lgkmcnt left at their maxima, no wait)
 __host__ __device__ constexpr int vmcnt_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }

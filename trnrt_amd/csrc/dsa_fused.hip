@@ -1,0 +1,919 @@
+// The whole DSA decode layer step in one launch (trnrt/models/mla.py:506-528 `attention_long` at kpool 1: indexer ->
+// exact top-keep -> sparse MLA; the single-call decode layer of trnrt/kernels/dsa_shell.py:2114-2321), for rows of up
+// to 32,768 tokens.
+//
+// gfx950 has 8 XCDs of 32 CUs, each XCD with its own L2; workgroup x of a launch runs on XCD x % 8. Row b is owned by
+// the 32 workgroups of XCD b % 8 (one per CU; a batch of more than 8 rows takes one launch per 8 rows), so every
+// hand-off between the stages of a row stays inside one L2: a workgroup's stores are complete in that L2 once its
+// memory counter drains, and its peers read them with device-coherent loads (sc1), which miss the CU caches and hit the
+// XCD's L2. The stages are separated by XCD-local barriers on a counter word per XCD (an arrival is one atomic add; a
+// waiter polls with sc1 loads, every wait bounded: past its limit the workgroup records an error flag and goes on, so
+// no wave can hang).
+//
+// Per row, workgroup j (of 32):
+//   1. indexer: scores of positions 1024 j .. 1024 j + 1023 (8 waves x 4 tiles of 32 keys, bf16 MFMA over the
+//      exactly converted e4m3 keys, the weighted relu head sum in registers; the arithmetic of
+//      trnrt/kernels/dsa_index.py:44-50), written to the scores output and kept in LDS, with an LDS histogram of the
+//      top 12 bits of their order keys added into the row's histogram; barrier A;
+//   2. selection, first level: the row histogram gives the bin c0 of the keep-th largest key; the workgroup counts its
+//      keys above c0 and writes its keys in c0 (the candidates) in position order; barrier B;
+//   3. selection, exact: every workgroup reads the row's candidates (a few hundred for indexer scores) and finds the
+//      keep-th largest key T and the ties at T to take (the lowest positions, trnrt/models/dsa_select.py:10-38) by two
+//      LDS histogram passes (11 + 9 bits), then each workgroup's count and offset in the ascending output; the
+//      workgroup writes its own selected positions and their cache slots there; barrier C;
+//   4. attention: workgroup j takes head group j % (H / 16) and split j / (H / 16) of the ascending output: it reads
+//      the split's cache slots, gathers their rows into LDS and computes softmax(scale q.K) V over the split in one
+//      pass (bf16 MFMA over the exactly converted rows, fp32 softmax over the whole split), writing the split's
+//      normalised output with its max and sum (the arithmetic of trnrt/kernels/dsa_decode.py:26-37 and
+//      trnrt/kernels/dsa_slots.py:48-65); barrier D;
+//   5. combine: the splits merged by log-sum-exp (trnrt/models/mla.py:853-856), workgroup j for 1/32 of the outputs.
+// The histogram slice a workgroup owns is cleared after barrier B, and the last workgroup of an XCD to finish resets
+// the XCD's barrier words, so the workspace regions that must be zero between calls are zero again.
+#include "dsa_common.h"
+
+namespace dsa {
+
+constexpr int FU_XCDS = 8;
+constexpr int FU_NW = 32;        // workgroups per XCD, one per CU
+constexpr int FU_THREADS = 512;  // 8 waves: two per SIMD, so one's memory waits hide under the other's work
+constexpr int FU_WAVES = FU_THREADS / WAVE;
+constexpr int FU_TILE = 32;                           // keys per MFMA tile
+constexpr int FU_TPW = 4;                             // tiles per wave
+constexpr int FU_AHEAD = 3;                           // key tiles in flight ahead of the one a wave computes
+constexpr int FU_KEYS = FU_WAVES * FU_TPW * FU_TILE;  // 1024 keys per workgroup
+constexpr int FU_MAXLEN = FU_NW * FU_KEYS;            // 32,768
+constexpr int FU_D = 128;                             // indexer head dim
+constexpr int FU_QROW = FU_D + 8;                     // staged indexer query row (bf16)
+constexpr int FU_HBINS = HIST_BINS;
+constexpr int FU_CAND_LDS = 4096;  // candidates held in LDS (more: read from the L2 in each pass)
+constexpr int FU_HPW = 16;         // heads per attention workgroup
+constexpr int FU_CH = 64;          // slot granularity of a split
+constexpr int FU_SPLIT = 256;      // at most 256 slots per split
+constexpr int FU_DQK = 576, FU_DV = 512;
+constexpr int FU_PIECES = FU_DQK / 16;  // 36 16-byte pieces per row
+constexpr int FU_KPIECES = FU_PIECES + 1;  // a staged row: the data and one padding piece (592 bytes), the stride at
+                                           // which the operand reads of 8 or 16 rows at one column hit distinct banks
+constexpr int FU_KROW = 16 * FU_KPIECES;
+constexpr int FU_STEPS = FU_DQK / 32;   // score steps
+constexpr int FU_AQROW = FU_DQK + 8;    // staged attention query row (bf16)
+constexpr int FU_PROW = FU_SPLIT + 8;   // P row stride (bf16)
+constexpr unsigned FU_SPIN = 1u << 20;  // polls before a wait gives up (a normal wait takes a few)
+constexpr int FU_SYNC_WORDS = 16;       // per XCD: arrivals, exits, error flag
+
+// LDS (160 KiB, one workgroup per CU), phase by phase:
+constexpr int L_STATE = 0;       // FuState: selection results (stage 3)
+constexpr int L_MISC = 1536;     // block-scan scratch (stages 1-3)
+constexpr int L_CV = 2048;       // stage 3: candidate values [4096]
+constexpr int L_BINS = 22528;    // stage 3: 2048 bins
+constexpr int L_BINS2 = 30720;   // stage 3: 512 bins
+constexpr int L_QS = 32768;      // stage 1: indexer queries [64][136] bf16
+constexpr int L_WS = 50176;      // stage 1: head weights [64]
+constexpr int L_HS = 50432;      // stage 1: histogram [4096]
+constexpr int L_TPG = 159616;    // stages 1-3: the page of each of the workgroup's 32 tiles
+constexpr int L_SCS = 159744;    // stages 1-3: the workgroup's 1024 scores
+constexpr int L_KT = 0;          // stage 4: the rows, token-major at the 592-byte stride
+constexpr int L_AQ = 0;          // stage 4, before the gather: the 16 heads' queries [16][584] bf16
+constexpr int L_P = 151552;      // stage 4: P [16][264] bf16; before the gather the split's slot list [256]
+constexpr int L_KSC = 160000;    // stage 4: kv scales [256]
+constexpr int L_BIAS = 161024;   // stage 4: biases [256]
+constexpr int L_RED = 162048;    // stage 4: per-wave head maxima [8][16]
+constexpr int L_SRED = 162560;   // stage 4: per-wave head sums [8][16]
+constexpr int FU_LDS = 163840;
+static_assert(L_HS + 4 * FU_HBINS <= L_TPG && L_TPG + 4 * 32 == L_SCS, "stage 1 layout");
+static_assert(L_CV + 4 * FU_CAND_LDS <= L_BINS && L_BINS2 + 4 * 512 <= L_QS, "stage 3 layout");
+static_assert(L_P == FU_SPLIT * FU_KROW && L_P + 2 * FU_HPW * FU_PROW <= L_KSC, "stage 4 layout");
+static_assert(L_SRED + 4 * FU_WAVES * FU_HPW <= FU_LDS && L_SCS + 4 * FU_KEYS == FU_LDS, "LDS size");
+static_assert(L_AQ + 2 * FU_HPW * FU_AQROW <= L_P, "query staging");
+
+struct FuState {
+  int na[FU_NW];   // per workgroup: keys above the first-level bin
+  int nc[FU_NW];   // its candidates
+  int cb[FU_NW];   // exclusive prefix of nc
+  int gt[FU_NW];   // its candidates above T
+  int eq[FU_NW];   // its candidates equal to T
+  int sel[FU_NW];  // its selected keys
+  int off[FU_NW];  // its first output index
+  int tb[FU_NW];   // ties at T before it
+  int c0, above0, nvis, cnt_row;
+  uint32_t T;
+  int room, ncand, pad;
+};
+static_assert(sizeof(FuState) <= L_MISC, "state");
+
+struct FusedArgs {
+  const uint16_t* q_idx;
+  const float* w;
+  const uint8_t* k;
+  const float* ks;
+  const uint16_t* q;
+  const uint8_t* kv;
+  const float* kvs;
+  const int* table;
+  const int* ctx_len;
+  float* scores;
+  int* idx;
+  int* cnt;
+  uint16_t* out;
+  float* lse;
+  int* hist;       // [B][4096], zero between calls
+  int* sync;       // [8][16]: barrier words, zero between calls (the error flag excepted)
+  int2* cnts;      // [B][32]: (keys above c0, candidates) per workgroup
+  uint32_t* cand;  // [B][32][1024]: candidates, (low 20 key bits << 10) | position in the workgroup's range
+  int* rows;       // [B][keep]: the cache slot of each selected position (position 0's past the count)
+  float* part;     // [B][S][H][512]: split outputs (normalised)
+  float2* ml;      // [B][S][H]: split max and sum
+  int B, Hi, H, max_pages, page_size, page_shift, num_pages, stride, keep;
+  int num_slots;  // num_pages * page_size
+  float scale;
+  int HG, S, sps;
+  int row0;  // this launch's first row (rows row0 .. row0 + 7)
+};
+
+// Device-coherent loads (sc1): they miss the CU's caches and read the XCD's L2, where a peer's completed stores are.
+__device__ __forceinline__ int ld_sc1(const int* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_sc1(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ld_sc1_64(const void* p) {
+  return __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+constexpr int FU_AUX_SC1 = 16;  // the cache-policy operand of the direct-to-LDS loads: sc1
+
+// XCD-local barrier of the 32 workgroups of an XCD: every thread's stores complete (drained memory counter), then the
+// workgroup's arrival (one atomic add) and a bounded poll. The XCD's counter is zero at a launch's start (the last
+// workgroup to finish resets it), so the n-th barrier of a launch completes at 32 n arrivals.
+__device__ __forceinline__ void fu_barrier(int* sync, int n) {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned* ctr = reinterpret_cast<unsigned*>(sync);
+    __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned target = (unsigned)n * FU_NW;
+    unsigned polls = 0;
+    while ((int)(__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - target) < 0) {
+      if (++polls > FU_SPIN) {
+        __hip_atomic_fetch_or(sync + 2, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+  }
+  __syncthreads();
+}
+
+// Block-wide over 512 threads, thread t holding the counts of bins PER t .. PER t + PER - 1 (higher bins = larger
+// keys): the bin holding the need-th largest key and the keys in the bins above it; returns the total. scr: 16 ints
+// of LDS, with scr[8] = -1 on entry (written before a barrier that precedes this call). Two barriers; the caller
+// must pass one more before scr is written again. Counts that cannot hold the need-th key give bin 0, above 0.
+template <int PER>
+__device__ int fu_find_bin(const int (&hb)[PER], int need, int* scr, int* bin, int* above) {
+  const int t = threadIdx.x, wave = t / WAVE, lane = t & (WAVE - 1);
+  int mine = 0;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) mine += hb[i];
+  const int pre = wave_incl_scan(mine);
+  const int inc = __builtin_amdgcn_readlane(pre, WAVE - 1) - pre + mine;  // inclusive suffix over the lanes
+  if (lane == 0) scr[wave] = inc;
+  __syncthreads();
+  int after = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < FU_WAVES; ++w) {
+    const int x = scr[w];
+    after += w > wave ? x : 0;
+    tot += x;
+  }
+  int excl = after + inc - mine;  // keys in the bins above this thread's
+  if (excl < need && excl + mine >= need) {
+#pragma unroll
+    for (int i = PER - 1; i >= 0; --i) {
+      if (excl < need) {
+        if (excl + hb[i] >= need) {
+          scr[8] = PER * t + i;
+          scr[9] = excl;
+        }
+        excl += hb[i];
+      }
+    }
+  }
+  __syncthreads();
+  const int b = scr[8];
+  *bin = b < 0 ? 0 : b;
+  *above = b < 0 ? 0 : scr[9];
+  return tot;
+}
+
+// Block-wide exclusive prefix (in thread order) of a packed per-thread count (two 16-bit fields; block totals below
+// 65536), and the block total. scr: FU_WAVES ints. One barrier; the caller must pass one more before scr is written
+// again.
+__device__ __forceinline__ uint32_t fu_block_prefix(uint32_t mine, int* scr, uint32_t* total) {
+  const int wave = threadIdx.x / WAVE, lane = threadIdx.x & (WAVE - 1);
+  const uint32_t incl = wave_incl_scan_u32(mine);
+  if (lane == WAVE - 1) scr[wave] = (int)incl;
+  __syncthreads();
+  uint32_t before = incl - mine, tot = 0;
+#pragma unroll
+  for (int w = 0; w < FU_WAVES; ++w) {
+    const uint32_t x = (uint32_t)scr[w];
+    before += w < wave ? x : 0u;
+    tot += x;
+  }
+  *total = tot;
+  return before;
+}
+
+// Stage 1: the indexer scores of positions 1024 j .. 1024 j + 1023 of row b (L: the row's length). Each wave streams
+// its 4 tiles of 32 keys FU_AHEAD ahead of its MFMAs.
+template <int MT>
+__device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int b, int j, int L) {
+  uint16_t* qs = reinterpret_cast<uint16_t*>(lds + L_QS);
+  float* wsh = reinterpret_cast<float*>(lds + L_WS);
+  int* hs = reinterpret_cast<int*>(lds + L_HS);
+  int* tpg = reinterpret_cast<int*>(lds + L_TPG);
+  float* scs = reinterpret_cast<float*>(lds + L_SCS);
+  const int tid = threadIdx.x, wave = tid / WAVE, lane = tid & (WAVE - 1);
+  const int jk = lane & 31, h = lane >> 5;
+  const int Hi = a.Hi;
+  float* srow = a.scores + (size_t)b * a.stride;
+
+  // the queries' loads (32 MT heads of 16 pieces: MT per thread), the weights, the tiles' pages
+  u32x4 qv[MT];
+#pragma unroll
+  for (int r = 0; r < MT; ++r) {
+    const int i = tid + FU_THREADS * r;
+    const int head = i >> 4, c = i & 15;
+    qv[r] = *reinterpret_cast<const u32x4*>(a.q_idx + ((size_t)b * Hi + min(head, Hi - 1)) * FU_D + 8 * c);
+  }
+  const float wv = a.w[(size_t)b * Hi + min(tid, Hi - 1)];
+  const int t_begin = j * (FU_KEYS / FU_TILE) + wave * FU_TPW;  // this wave's first tile
+  const bool live = t_begin * FU_TILE < L;                      // wave-uniform: any of its keys in the row
+  const int* trow = a.table + (size_t)b * a.max_pages;
+  int pages = 0;
+  {
+    const int t = t_begin + min(lane, FU_TPW - 1);
+    const int pg = trow[min((t * FU_TILE) >> a.page_shift, a.max_pages - 1)];
+    pages = t * FU_TILE < L ? safe_page(pg, a.num_pages) : 0;
+  }
+  u32x4 kv[FU_TPW][4];
+  float ksc[FU_TPW];
+  auto tile_loads = [&](int i) __attribute__((always_inline)) {
+    const int t0 = (t_begin + i) * FU_TILE;
+    const int page = __shfl(pages, i, WAVE);
+    const size_t slot = t0 < L ? (size_t)page * a.page_size + (t0 & (a.page_size - 1)) + jk : (size_t)jk;
+    const uint8_t* kp = a.k + slot * FU_D + 64 * h;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) kv[i][c] = *reinterpret_cast<const u32x4*>(kp + 16 * c);
+    ksc[i] = a.ks[slot];
+  };
+  if (live) {
+#pragma unroll
+    for (int i = 0; i < FU_AHEAD; ++i) tile_loads(i);
+  }
+
+#pragma unroll
+  for (int r = 0; r < MT; ++r) {
+    const int i = tid + FU_THREADS * r;
+    const int head = i >> 4, c = i & 15;
+    *reinterpret_cast<u32x4*>(&qs[head * FU_QROW + 8 * c]) = head < Hi ? qv[r] : u32x4{0u, 0u, 0u, 0u};
+  }
+  if (tid < 32 * MT) wsh[tid] = tid < Hi ? wv : 0.0f;
+  if (lane < FU_TPW) tpg[wave * FU_TPW + lane] = pages;
+  for (int i = tid; i < FU_HBINS; i += FU_THREADS) hs[i] = 0;
+  __syncthreads();
+
+  if (live) {
+    bf16x8 qa[MT][8];
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+        qa[m][s] = as_bf16x8(*reinterpret_cast<const uint4*>(&qs[(32 * m + jk) * FU_QROW + 64 * h + 8 * s]));
+    float wr[MT][16];
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) wr[m][r] = wsh[32 * m + 8 * (r >> 2) + 4 * h + (r & 3)];
+#pragma unroll
+    for (int i = 0; i < FU_TPW; ++i) {
+      if (i + FU_AHEAD < FU_TPW) {
+        // tile i has arrived (the later tiles in flight may still be outstanding): issue tile i + FU_AHEAD (the
+        // compiler's own wait before tile i's first use keeps the data exact)
+        __builtin_amdgcn_s_waitcnt(vmcnt_wait(5 * (FU_AHEAD - 1)));
+        __builtin_amdgcn_sched_barrier(0);
+        tile_loads(i + FU_AHEAD);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      const int pos = (t_begin + i) * FU_TILE + jk;
+      f32x16 acc[MT];
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[m][r] = 0.0f;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const u32x4 k4 = kv[i][s >> 1];
+        const bf16x8 kb = (s & 1) ? fp8x8_to_bf16x8(k4[2], k4[3]) : fp8x8_to_bf16x8(k4[0], k4[1]);
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa[m][s], kb, acc[m], 0, 0, 0);
+      }
+      float part = 0.0f;
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) part = fmaf(wr[m][r], relu(acc[m][r]), part);
+      part += __shfl_xor(part, 32, WAVE);
+      const float v = pos < L ? part * ksc[i] : NEG_INF;
+      if (h == 0) {
+        if (pos < a.stride) srow[pos] = v;
+        scs[pos - j * FU_KEYS] = v;
+        if (v > VISIBLE) atomicAdd(&hs[order_key(v) >> 20], 1);
+      }
+    }
+  } else {
+    // every key of this wave is past the row: NEG_INF
+    for (int e = lane; e < FU_TPW * FU_TILE; e += WAVE) {
+      const int pos = t_begin * FU_TILE + e;
+      if (pos < a.stride) srow[pos] = NEG_INF;
+      scs[pos - j * FU_KEYS] = NEG_INF;
+    }
+  }
+  // positions past 32,768 of a wider score row are never keys of the row
+  for (int p = FU_MAXLEN + j * FU_THREADS + tid; p < a.stride; p += FU_NW * FU_THREADS) srow[p] = NEG_INF;
+  __syncthreads();
+  int* grow = a.hist + (size_t)b * FU_HBINS;
+  for (int i = tid; i < FU_HBINS; i += FU_THREADS) {
+    const int c = hs[i];
+    if (c) atomicAdd(&grow[i], c);
+  }
+}
+
+// This thread's two keys (positions 2 tid, 2 tid + 1 of the workgroup's range; 0: not selectable).
+__device__ __forceinline__ void fu_my_keys(const uint8_t* lds, uint32_t (&key)[2]) {
+  const float2 sv = *reinterpret_cast<const float2*>(reinterpret_cast<const float*>(lds + L_SCS) + 2 * threadIdx.x);
+  key[0] = order_key(sv.x) & (0u - (uint32_t)(sv.x > VISIBLE));
+  key[1] = order_key(sv.y) & (0u - (uint32_t)(sv.y > VISIBLE));
+}
+
+// Stage 2: the first level from the row histogram, this workgroup's keys above it counted and its candidates written.
+__device__ __forceinline__ void fu_classify(const FusedArgs& a, uint8_t* lds, int b, int j) {
+  FuState& st = *reinterpret_cast<FuState*>(lds + L_STATE);
+  int* scr = reinterpret_cast<int*>(lds + L_MISC);
+  const int tid = threadIdx.x;
+  constexpr int PER = FU_HBINS / FU_THREADS;  // 8 bins per thread
+  const int* grow = a.hist + (size_t)b * FU_HBINS;
+  int hb[PER];
+#pragma unroll
+  for (int i = 0; i < PER / 2; ++i) {
+    const uint64_t v = ld_sc1_64(grow + PER * tid + 2 * i);
+    hb[2 * i] = (int)(uint32_t)v;
+    hb[2 * i + 1] = (int)(uint32_t)(v >> 32);
+  }
+  uint32_t key[2];
+  fu_my_keys(lds, key);
+  if (tid == 0) scr[8] = -1;
+  __syncthreads();
+  int c0, above0;
+  const int nvis = fu_find_bin<PER>(hb, a.keep, scr, &c0, &above0);
+  if (nvis <= a.keep) c0 = -1;  // every selectable key is selected
+  int na = 0, nc = 0;
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const int bin = (int)(key[e] >> 20);
+    na += key[e] != 0u && bin > c0;
+    nc += key[e] != 0u && bin == c0;
+  }
+  __syncthreads();  // every thread has read scr (the bin search) before it is rewritten
+  uint32_t tot;
+  const uint32_t before = fu_block_prefix(((uint32_t)na << 16) | (uint32_t)nc, scr, &tot);
+  uint32_t* crow = a.cand + ((size_t)b * FU_NW + j) * FU_KEYS;
+  int o = (int)(before & 0xFFFFu);
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    if (key[e] != 0u && (int)(key[e] >> 20) == c0) {
+      crow[o] = ((key[e] & 0xFFFFFu) << 10) | (uint32_t)(2 * tid + e);
+      ++o;
+    }
+  }
+  if (tid == 0) {
+    a.cnts[(size_t)b * FU_NW + j] = make_int2((int)(tot >> 16), (int)(tot & 0xFFFFu));
+    st.c0 = c0;
+    st.above0 = above0;
+    st.nvis = nvis;
+  }
+}
+
+// Stage 3: the exact threshold T, the ties to take, every workgroup's contribution and output offset, and this
+// workgroup's selected positions (idx) and their cache slots (rows) written at its offset.
+__device__ __forceinline__ void fu_select(const FusedArgs& a, uint8_t* lds, int b, int j) {
+  FuState& st = *reinterpret_cast<FuState*>(lds + L_STATE);
+  int* scr = reinterpret_cast<int*>(lds + L_MISC);
+  uint32_t* cv = reinterpret_cast<uint32_t*>(lds + L_CV);
+  int* bins = reinterpret_cast<int*>(lds + L_BINS);
+  int* bins2 = reinterpret_cast<int*>(lds + L_BINS2);
+  const int* tpg = reinterpret_cast<const int*>(lds + L_TPG);
+  const int tid = threadIdx.x, wave = tid / WAVE, lane = tid & (WAVE - 1);
+  const int c0 = st.c0;
+  const uint32_t* cbase = a.cand + (size_t)b * FU_NW * FU_KEYS;
+  if (wave == 0) {
+    const uint64_t v = ld_sc1_64(a.cnts + (size_t)b * FU_NW + (lane & (FU_NW - 1)));
+    const int na = lane < FU_NW ? (int)(uint32_t)v : 0, nc = lane < FU_NW ? (int)(uint32_t)(v >> 32) : 0;
+    const int inc = wave_incl_scan(nc);
+    if (lane < FU_NW) {
+      st.na[lane] = na;
+      st.nc[lane] = nc;
+      st.cb[lane] = inc - nc;
+      st.gt[lane] = 0;
+      st.eq[lane] = 0;
+    }
+    if (lane == FU_NW - 1) st.ncand = inc;
+  }
+  for (int i = tid; i < 2048; i += FU_THREADS) bins[i] = 0;
+  bins2[tid] = 0;
+  if (tid == 0) scr[8] = -1;
+  __syncthreads();
+  const int C = st.ncand;
+  const bool cached = C <= FU_CAND_LDS;
+  if (c0 >= 0) {
+    if (cached) {
+      // every workgroup's candidates straight into LDS, in workgroup order (wave v takes workgroups v, v + 8, ...;
+      // lane l of a load writes entry base + l)
+      for (int w = wave; w < FU_NW; w += FU_WAVES) {
+        const int n = st.nc[w], base = st.cb[w];
+        for (int c = 0; c < n; c += WAVE) {
+          if (c + lane < n)
+            __builtin_amdgcn_global_load_lds(cbase + (size_t)w * FU_KEYS + c + lane,
+                                             (__attribute__((address_space(3))) void*)(cv + base + c), 4, 0,
+                                             FU_AUX_SC1);
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    }
+    // candidate i's value: from LDS, or (more candidates than LDS holds) from the L2
+    auto cand_at = [&](int i) __attribute__((always_inline)) {
+      if (cached) return cv[i];
+      int w = 0;
+#pragma unroll
+      for (int s2 = 16; s2 >= 1; s2 >>= 1)
+        if (w + s2 < FU_NW && st.cb[w + s2] <= i) w += s2;
+      return ld_sc1(cbase + (size_t)w * FU_KEYS + (i - st.cb[w]));
+    };
+    for (int i = tid; i < C; i += FU_THREADS) atomicAdd(&bins[(cand_at(i) >> 19) & 2047], 1);
+    __syncthreads();
+    constexpr int P1 = 2048 / FU_THREADS;
+    int hb[P1];
+#pragma unroll
+    for (int i = 0; i < P1; ++i) hb[i] = bins[P1 * tid + i];
+    int c1, above1;
+    int need = a.keep - st.above0;
+    fu_find_bin<P1>(hb, need, scr, &c1, &above1);
+    need -= above1;
+    __syncthreads();
+    if (tid == 0) scr[8] = -1;
+    for (int i = tid; i < C; i += FU_THREADS) {
+      const uint32_t v = cand_at(i);
+      if (((v >> 19) & 2047) == (uint32_t)c1) atomicAdd(&bins2[(v >> 10) & 511], 1);
+    }
+    __syncthreads();
+    const int hb2[1] = {bins2[tid]};
+    int c2, above2;
+    fu_find_bin<1>(hb2, need, scr, &c2, &above2);
+    const uint32_t tlow = ((uint32_t)c1 << 9) | (uint32_t)c2;
+    const int room = max(need - above2, 0);
+    // per workgroup: candidates above T and equal to T (its range [cb, cb + nc) of the candidates)
+    for (int w = wave; w < FU_NW; w += FU_WAVES) {
+      const int n = st.nc[w], base = st.cb[w];
+      int gt = 0, eq = 0;
+      for (int c = 0; c < n; c += WAVE) {
+        const bool in = c + lane < n;
+        const uint32_t kl = in ? cand_at(base + c + lane) >> 10 : 0u;
+        gt += __builtin_popcountll(__ballot(in && kl > tlow));
+        eq += __builtin_popcountll(__ballot(in && kl == tlow));
+      }
+      if (lane == 0) {
+        st.gt[w] = gt;
+        st.eq[w] = eq;
+      }
+    }
+    if (tid == 0) {
+      st.T = ((uint32_t)c0 << 20) | tlow;
+      st.room = room;
+    }
+  } else if (tid == 0) {
+    st.T = 0u;
+    st.room = 0;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const int w = lane & (FU_NW - 1);
+    const int eq = lane < FU_NW ? st.eq[w] : 0;
+    const int tb = wave_incl_scan(eq) - eq;
+    const int take = min(max(st.room - tb, 0), eq);
+    const int sel = lane < FU_NW ? st.na[w] + st.gt[w] + take : 0;
+    const int off = wave_incl_scan(sel) - sel;
+    if (lane < FU_NW) {
+      st.tb[w] = tb;
+      st.sel[w] = sel;
+      st.off[w] = off;
+    }
+    if (lane == 0) st.cnt_row = min(st.nvis, a.keep);
+  }
+  __syncthreads();
+  // this workgroup's selections, in position order: keys above T, and ties at T while fewer than `room` ties of the
+  // row come before them; output index off + (selected keys before it in the workgroup)
+  const uint32_t T = st.T;
+  const int room = st.room, TB = st.tb[j], base = st.off[j];
+  uint32_t key[2];
+  fu_my_keys(lds, key);
+  uint32_t na = 0, nt = 0;
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    na += key[e] > T;
+    nt += T != 0u && key[e] == T;
+  }
+  uint32_t tot;
+  const uint32_t bef = fu_block_prefix((na << 16) | nt, scr, &tot);
+  int a_before = (int)(bef >> 16), t_before = (int)(bef & 0xFFFFu);
+  const int tb_taken = min(TB, room);
+  int* irow = a.idx + (size_t)b * a.keep;
+  int* rrow = a.rows + (size_t)b * a.keep;
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const bool above = key[e] > T;
+    const bool tie = T != 0u && key[e] == T;
+    const int o = base + a_before + (min(TB + t_before, room) - tb_taken);
+    if ((above || (tie && TB + t_before < room)) && (unsigned)o < (unsigned)a.keep) {
+      const int lp = 2 * tid + e;
+      const int p = j * FU_KEYS + lp;
+      irow[o] = p;
+      rrow[o] = tpg[lp / FU_TILE] * a.page_size + (p & (a.page_size - 1));
+    }
+    a_before += above;
+    t_before += tie;
+  }
+  // the outputs past the count (their slots: position 0's), and the count
+  const int cnt_row = st.cnt_row;
+  for (int o = cnt_row + j * FU_THREADS + tid; o < a.keep; o += FU_NW * FU_THREADS) {
+    irow[o] = 0;
+    rrow[o] = safe_page(a.table[(size_t)b * a.max_pages], a.num_pages) * a.page_size;
+  }
+  if (j == 0 && tid == 0) a.cnt[b] = cnt_row;
+}
+
+// The value operand of v_mfma_f32_16x16x32_bf16 from the token-major tile (ds_read_b64_tr_b8: lane (a, c) of each
+// 16-lane block gets byte c of the 8-byte rows addressed by the block's lanes 2j + a): lane l receives dim 16 n + l % 16
+// of tokens 32 ks + 8 (l / 16) + j, the B operand with k-slot 8 q + j = that token.
+__device__ __forceinline__ bf16x8 fu_value_operand(const uint8_t* kt, int ks, int n, int lane) {
+  typedef int v2i __attribute__((ext_vector_type(2)));
+  const int q = lane >> 4, p = lane & 15;
+  const uint8_t* ad = kt + (32 * ks + 8 * q + (p >> 1)) * FU_KROW + 16 * n + 8 * (p & 1);
+  const v2i r = __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) v2i*)(ad));
+  return fp8x8_to_bf16x8((uint32_t)r.x, (uint32_t)r.y);
+}
+
+// Stage 4: the split's attention.
+__device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int b, int j) {
+  const FuState& st = *reinterpret_cast<const FuState*>(lds + L_STATE);
+  float* ksc_l = reinterpret_cast<float*>(lds + L_KSC);
+  float* bias_l = reinterpret_cast<float*>(lds + L_BIAS);
+  float* red = reinterpret_cast<float*>(lds + L_RED);
+  float* sred = reinterpret_cast<float*>(lds + L_SRED);
+  uint16_t* pl = reinterpret_cast<uint16_t*>(lds + L_P);
+  uint8_t* kt = lds + L_KT;
+  uint16_t* qs = reinterpret_cast<uint16_t*>(lds + L_AQ);
+  const int tid = threadIdx.x, wave = tid / WAVE, lane = tid & (WAVE - 1);
+  const int l16 = lane & 15, q4 = lane >> 4;
+  const int hg = j % a.HG, s = j / a.HG;
+  if (s >= a.S) return;  // workgroup-uniform
+  const int H = a.H;
+  const int cnt_row = st.cnt_row;
+  const int o0 = s * a.sps, o1 = min(o0 + a.sps, a.keep);
+  // the split's live slots; a row with none attends position 0 masked (its lse is NEG_INF)
+  int n_slots = max(min(o1, cnt_row) - o0, 0);
+  float live_bias = 0.0f;
+  if (cnt_row == 0 && s == 0) {
+    n_slots = 1;
+    live_bias = NEG_INF;
+  }
+  float* part = a.part + ((size_t)b * a.S + s) * H * FU_DV;
+  float2* mlp = a.ml + ((size_t)b * a.S + s) * H;
+  if (n_slots == 0) {  // an empty split: weight 0 in the combine
+    for (int i = tid; i < FU_HPW * FU_DV / 4; i += FU_THREADS)
+      reinterpret_cast<float4*>(part + (size_t)FU_HPW * hg * FU_DV)[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (tid < FU_HPW) mlp[FU_HPW * hg + tid] = make_float2(-INFINITY, 0.0f);
+    return;
+  }
+  const int padded = (n_slots + FU_CH - 1) / FU_CH * FU_CH;
+
+  // one round of loads: the 16 heads' queries, the split's slots (row r = tid % 256; a padding row reads slot 0's)
+  constexpr int QP = FU_HPW * FU_DQK / 8;  // 1152 pieces of 16 bytes
+  constexpr int QPT = (QP + FU_THREADS - 1) / FU_THREADS;
+  const u32x4* qsrc = reinterpret_cast<const u32x4*>(a.q + ((size_t)b * H + FU_HPW * hg) * FU_DQK);
+  u32x4 qv[QPT];
+#pragma unroll
+  for (int i = 0; i < QPT; ++i) qv[i] = qsrc[min(tid + FU_THREADS * i, QP - 1)];
+  int* slot_l = reinterpret_cast<int*>(lds + L_P);
+  const int* rsrc = a.rows + (size_t)b * a.keep + o0;
+  int slot = 0;
+  if (tid < FU_SPLIT) {
+    slot = ld_sc1(rsrc + (tid < n_slots ? tid : 0));
+    slot = (unsigned)slot < (unsigned)a.num_slots ? slot : 0;
+    slot_l[tid] = slot;
+  }
+#pragma unroll
+  for (int i = 0; i < QPT; ++i) {
+    const int pc = tid + FU_THREADS * i;  // head pc / 72, elements 8 (pc % 72) ..
+    if (pc < QP) *reinterpret_cast<u32x4*>(qs + (pc / (FU_DQK / 8)) * FU_AQROW + 8 * (pc % (FU_DQK / 8))) = qv[i];
+  }
+  __syncthreads();
+  // the query operand: head l16, dims 64 (st / 2) + 16 q4 + 8 (st % 2) .. + 7 at score step st (the key operand's
+  // dim order below)
+  bf16x8 qb[FU_STEPS];
+  {
+    const uint16_t* qh = qs + l16 * FU_AQROW + 16 * q4;
+#pragma unroll
+    for (int st2 = 0; st2 < FU_STEPS; ++st2)
+      qb[st2] = as_bf16x8(*reinterpret_cast<const uint4*>(qh + 64 * (st2 >> 1) + 8 * (st2 & 1)));
+  }
+  __syncthreads();  // every wave holds its query operand before the rows overwrite it
+  // every row straight into LDS, coalesced: load k fills 1 KiB of the tile, lane l 16-byte unit u = 64 k + l (row
+  // u / 37, piece u % 37; the padding piece re-reads the last data piece); the loads of the padded rows' units spread
+  // over the 8 waves
+  {
+    const int units = padded * FU_KPIECES;
+    for (int k = wave; k * WAVE < units; k += FU_WAVES) {
+      const int u = WAVE * k + lane;
+      const int row = u / FU_KPIECES, pc = u - row * FU_KPIECES;
+      const uint8_t* src = a.kv + (size_t)slot_l[row] * FU_DQK + 16 * (pc < FU_PIECES ? pc : FU_PIECES - 1);
+      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(kt + 1024 * k), 16, 0, 0);
+    }
+  }
+  const float ksv = tid < padded ? a.kvs[slot] : 0.0f;
+  __builtin_amdgcn_s_waitcnt(0);
+  if (tid < padded) {
+    ksc_l[tid] = ksv;
+    bias_l[tid] = tid < n_slots ? live_bias : -INFINITY;
+  }
+  __syncthreads();  // every row in LDS
+
+  // scores of tokens 32 wave .. + 31 (two blocks of 16), all 16 heads: S^T = K . Q^T; lane group q4 reads piece
+  // 4 j + q4 (dims 64 j + 16 q4 ..) of its token per pair of steps (one ds_read_b128 for two MFMAs; 8 rows at one
+  // column cover the 32 banks once at the 592-byte stride)
+  const bool has = 32 * wave < padded;
+  float sv[2][4];
+  float mx = -INFINITY;
+  if (has) {
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) acc[k][0] = acc[k][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const uint8_t* kr = kt + (32 * wave + l16) * FU_KROW + 16 * q4;
+#pragma unroll
+    for (int st2 = 0; st2 < FU_STEPS; st2 += 2) {
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const u32x4 kk = *reinterpret_cast<const u32x4*>(kr + 16 * k * FU_KROW + 32 * st2);
+        acc[k][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16x8(kk[0], kk[1]), qb[st2], acc[k][0], 0, 0, 0);
+        acc[k][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16x8(kk[2], kk[3]), qb[st2 + 1], acc[k][1], 0, 0,
+                                                            0);
+      }
+    }
+    // acc[k][.][r] = S^T[token 32 wave + 16 k + 4 q4 + r][head l16]
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int tk = 32 * wave + 16 * k + 4 * q4;
+      const float4 ks4 = *reinterpret_cast<const float4*>(&ksc_l[tk]);
+      const float4 bs4 = *reinterpret_cast<const float4*>(&bias_l[tk]);
+      sv[k][0] = (acc[k][0][0] + acc[k][1][0]) * (ks4.x * a.scale) + bs4.x;
+      sv[k][1] = (acc[k][0][1] + acc[k][1][1]) * (ks4.y * a.scale) + bs4.y;
+      sv[k][2] = (acc[k][0][2] + acc[k][1][2]) * (ks4.z * a.scale) + bs4.z;
+      sv[k][3] = (acc[k][0][3] + acc[k][1][3]) * (ks4.w * a.scale) + bs4.w;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mx = max_nonan(mx, sv[k][i]);
+    }
+  }
+  mx = max_nonan(mx, __shfl_xor(mx, 16, WAVE));
+  mx = max_nonan(mx, __shfl_xor(mx, 32, WAVE));
+  if (lane < FU_HPW) red[wave * FU_HPW + lane] = mx;
+  __syncthreads();
+  float m = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < FU_WAVES; ++w) m = max_nonan(m, red[w * FU_HPW + l16]);
+  float psum = 0.0f;
+  if (has) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int tk = 32 * wave + 16 * k + 4 * q4;
+      const float4 ks4 = *reinterpret_cast<const float4*>(&ksc_l[tk]);
+      float p[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        p[i] = __expf(sv[k][i] - m);
+        psum += p[i];
+      }
+      // the value's dequantisation folded into the bf16 weight
+      *reinterpret_cast<uint2*>(&pl[l16 * FU_PROW + tk]) =
+          make_uint2(bf16_pack(p[0] * ks4.x, p[1] * ks4.y), bf16_pack(p[2] * ks4.z, p[3] * ks4.w));
+    }
+  }
+  psum += __shfl_xor(psum, 16, WAVE);
+  psum += __shfl_xor(psum, 32, WAVE);
+  if (lane < FU_HPW) sred[wave * FU_HPW + lane] = psum;
+  __syncthreads();  // P and the sums
+
+  // O[head][dims 64 wave ..] += P . V over the split's tokens
+  f32x4 o[4];
+#pragma unroll
+  for (int n = 0; n < 4; ++n) o[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int nks = padded / 32;
+  for (int ks = 0; ks < nks; ++ks) {
+    const bf16x8 pop = as_bf16x8(*reinterpret_cast<const uint4*>(&pl[l16 * FU_PROW + 32 * ks + 8 * q4]));
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+      o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pop, fu_value_operand(kt, ks, 4 * wave + n, lane), o[n], 0, 0, 0);
+  }
+  // the split's normalised output, max and sum (heads 4 q4 + i)
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int hl = 4 * q4 + i;
+    float l = 0.0f, mh = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < FU_WAVES; ++w) {
+      l += sred[w * FU_HPW + hl];
+      mh = max_nonan(mh, red[w * FU_HPW + hl]);
+    }
+    const float inv = 1.0f / l;
+    float* ph = part + (size_t)(FU_HPW * hg + hl) * FU_DV + 64 * wave + l16;
+#pragma unroll
+    for (int n = 0; n < 4; ++n) ph[16 * n] = o[n][i] * inv;
+    if (wave == 0 && l16 == 0) mlp[FU_HPW * hg + hl] = make_float2(mh, l);
+  }
+}
+
+// Stage 5: the splits merged by log-sum-exp, o = sum_s W_s o_s / sum_s W_s with W_s = l_s exp(m_s - M) and
+// lse = M + log sum_s W_s; item g of 16384 (head g / 256, dims 2 (g % 256) ..) on thread g % 512 of workgroup g / 512,
+// then g + 16384, ...; the splits' loads in groups of 8 (one memory round per group).
+__device__ __forceinline__ void fu_combine(const FusedArgs& a, int b, int j) {
+  const int S = a.S, H = a.H;
+  for (int g = j * FU_THREADS + (int)threadIdx.x; g < H * (FU_DV / 2); g += FU_NW * FU_THREADS) {
+    const int h = g >> 8, d = 2 * (g & 255);
+    float M = -INFINITY, W = 0.0f, x0 = 0.0f, x1 = 0.0f;
+    for (int s0 = 0; s0 < S; s0 += 8) {
+      uint64_t mlv[8], ov[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const size_t i = ((size_t)b * S + min(s0 + k, S - 1)) * H + h;
+        mlv[k] = ld_sc1_64(a.ml + i);
+        ov[k] = ld_sc1_64(a.part + i * FU_DV + d);
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float ms = __uint_as_float((uint32_t)mlv[k]), ls = __uint_as_float((uint32_t)(mlv[k] >> 32));
+        if (s0 + k < S && ls > 0.0f) {
+          // a running rescale: the group's splits against the maximum so far
+          const float Mn = max_nonan(M, ms);
+          const float f = __expf(M - Mn), wt = ls * __expf(ms - Mn);
+          W = W * f + wt;
+          x0 = x0 * f + wt * __uint_as_float((uint32_t)ov[k]);
+          x1 = x1 * f + wt * __uint_as_float((uint32_t)(ov[k] >> 32));
+          M = Mn;
+        }
+      }
+    }
+    const float inv = 1.0f / W;
+    const size_t oi = ((size_t)b * H + h) * FU_DV + d;
+    *reinterpret_cast<uint32_t*>(a.out + oi) = bf16_pack(x0 * inv, x1 * inv);
+    if (d == 0 && a.lse) a.lse[(size_t)b * H + h] = M + __logf(W);
+  }
+}
+
+template <int MT>
+__global__ __launch_bounds__(FU_THREADS, 1) void decode_fused_kernel(FusedArgs a) {
+  __shared__ __align__(16) uint8_t lds[FU_LDS];
+  const int x = blockIdx.x % FU_XCDS, j = blockIdx.x / FU_XCDS;
+  int* sync = a.sync + x * FU_SYNC_WORDS;
+  // one row per XCD and launch (rows row0 + x; a batch of more than 8 rows takes several launches, which keeps
+  // each workgroup's per-lane address arithmetic out of a loop over rows, where it would be held in registers)
+  const int b = a.row0 + x;
+  if (b >= a.B) return;  // an XCD without a row
+  const int L = min(max(a.ctx_len[b], 0), min(a.stride, FU_MAXLEN));
+  fu_indexer<MT>(a, lds, b, j, L);
+  fu_barrier(sync, 1);  // A: the row's scores and histogram
+  fu_classify(a, lds, b, j);
+  fu_barrier(sync, 2);  // B: every workgroup's counts and candidates
+  // the row histogram is read: this workgroup's slice back to zero for the next call
+  int* grow = a.hist + (size_t)b * FU_HBINS + j * (FU_HBINS / FU_NW);
+  if (threadIdx.x < FU_HBINS / FU_NW) grow[threadIdx.x] = 0;
+  fu_select(a, lds, b, j);
+  fu_barrier(sync, 3);  // C: the row's selection and slots
+  fu_attend(a, lds, b, j);
+  fu_barrier(sync, 4);  // D: every split's output
+  fu_combine(a, b, j);
+  // the last workgroup of the XCD to finish resets its barrier words (no workgroup polls them any more)
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned* wd = reinterpret_cast<unsigned*>(sync);
+    const unsigned e = __hip_atomic_fetch_add(wd + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (e == FU_NW - 1) {
+      __hip_atomic_store(wd, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(wd + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+// ---- host side ----
+
+static size_t fu_up256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Workspace of the fused layer past the zero region (histograms + barrier words): the per-workgroup counts, the
+// candidates, the selected slots, the split outputs and their (max, sum).
+struct FusedLayout {
+  size_t cnts, cand, rows, part, ml, end;
+};
+
+static FusedLayout fused_layout(size_t zero_bytes, int B, int H, int S, int keep) {
+  FusedLayout l;
+  l.cnts = zero_bytes;
+  l.cand = l.cnts + fu_up256((size_t)B * FU_NW * sizeof(int2));
+  l.rows = l.cand + fu_up256((size_t)B * FU_NW * FU_KEYS * 4);
+  l.part = l.rows + fu_up256((size_t)B * keep * 4);
+  l.ml = l.part + fu_up256((size_t)B * S * H * FU_DV * 4);
+  l.end = l.ml + fu_up256((size_t)B * S * H * sizeof(float2));
+  return l;
+}
+
+static int fused_splits(int H) { return FU_NW / (H / FU_HPW); }
+
+// Whether the fused layer takes a step: a GPU of 8 XCDs x 32 CUs, rows of at most 32,768 tokens (score rows of a
+// multiple of 4 floats), up to 64 indexer heads, query heads in 16s (at most 512), pages of a power-of-two size of at
+// least 32 tokens, and a keep that the splits hold (256 slots each).
+bool fused_layer_ok(int num_cu, int Hi, int H, int max_len, int keep, int page_size, int stride) {
+  if (num_cu != FU_XCDS * FU_NW) return false;
+  if (Hi < 1 || Hi > 64 || H < FU_HPW || H % FU_HPW || H / FU_HPW > FU_NW) return false;
+  if (max_len < 1 || max_len > FU_MAXLEN || stride < 1 || stride % 4 || keep < 1) return false;
+  if (page_size < 32 || (page_size & (page_size - 1))) return false;
+  return (long)fused_splits(H) * FU_SPLIT >= keep;
+}
+
+size_t fused_layer_bytes(size_t zero_bytes, int B, int H, int keep) {
+  if (H < FU_HPW || H % FU_HPW || H / FU_HPW > FU_NW) return 0;
+  return fused_layout(zero_bytes, B, H, fused_splits(H), keep).end;
+}
+
+hipError_t launch_decode_fused(const uint16_t* q_idx, const float* w, const uint8_t* k, const float* ks,
+                               const uint16_t* q, const uint8_t* kv, const float* kvs, const int* table,
+                               const int* ctx_len, float* scores, int* idx, int* cnt, uint16_t* out, float* lse,
+                               void* ws, size_t hist_bytes, size_t zero_bytes, int B, int Hi, int H, int max_pages,
+                               int page_size, int num_pages, int stride, int keep, float scale, hipStream_t s) {
+  FusedArgs a;
+  const int S = fused_splits(H);
+  const FusedLayout l = fused_layout(zero_bytes, B, H, S, keep);
+  char* p = static_cast<char*>(ws);
+  a.q_idx = q_idx;
+  a.w = w;
+  a.k = k;
+  a.ks = ks;
+  a.q = q;
+  a.kv = kv;
+  a.kvs = kvs;
+  a.table = table;
+  a.ctx_len = ctx_len;
+  a.scores = scores;
+  a.idx = idx;
+  a.cnt = cnt;
+  a.out = out;
+  a.lse = lse;
+  a.hist = reinterpret_cast<int*>(p);
+  a.sync = reinterpret_cast<int*>(p + hist_bytes);
+  a.cnts = reinterpret_cast<int2*>(p + l.cnts);
+  a.cand = reinterpret_cast<uint32_t*>(p + l.cand);
+  a.rows = reinterpret_cast<int*>(p + l.rows);
+  a.part = reinterpret_cast<float*>(p + l.part);
+  a.ml = reinterpret_cast<float2*>(p + l.ml);
+  a.B = B;
+  a.Hi = Hi;
+  a.H = H;
+  a.max_pages = max_pages;
+  a.page_size = page_size;
+  a.page_shift = __builtin_ctz((unsigned)page_size);
+  a.num_pages = num_pages;
+  a.num_slots = num_pages * page_size;
+  a.stride = stride;
+  a.keep = keep;
+  a.scale = scale;
+  a.HG = H / FU_HPW;
+  a.S = S;
+  int sps = (keep + S - 1) / S;
+  a.sps = (sps + FU_CH - 1) / FU_CH * FU_CH;
+  const dim3 grid(FU_XCDS * FU_NW), block(FU_THREADS);
+  for (int r0 = 0; r0 < B; r0 += FU_XCDS) {
+    a.row0 = r0;
+    const hipError_t e = Hi <= 32 ? launch("decode_fused_kernel", decode_fused_kernel<1>, grid, block, s, a)
+                                  : launch("decode_fused_kernel", decode_fused_kernel<2>, grid, block, s, a);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+}  // namespace dsa

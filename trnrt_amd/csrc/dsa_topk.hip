@@ -943,8 +943,12 @@ static size_t topk_level_bytes(int B, long n, int keep) {
 
 size_t topk_hist_bytes(int B) { return up256((size_t)B * HIST_REPLICAS * TK_HBINS * 4); }
 
+// The region a workspace keeps at zero between calls: the histograms, then the fused layer's barrier words
+// (WS_SYNC_BYTES, which the separate kernels never touch).
+size_t topk_zero_bytes(int B) { return topk_hist_bytes(B) + WS_SYNC_BYTES; }
+
 size_t topk_workspace_bytes(int B, int max_len, int keep) {
-  return topk_hist_bytes(B) + up256((size_t)B * sizeof(RowMeta)) + up256((size_t)B * TC_MAXCH * TC_CHUNK * 4) +
+  return topk_zero_bytes(B) + up256((size_t)B * sizeof(RowMeta)) + up256((size_t)B * TC_MAXCH * TC_CHUNK * 4) +
          topk_level_bytes(B, max_len, keep);
 }
 
@@ -1179,7 +1183,7 @@ hipError_t launch_topk(const float* scores, const int* len, int* idx, int* cnt, 
   if (rows_out && (!table || page_size < 32 || max_pages < 1 || num_pages < 1)) return hipErrorInvalidValue;
   TopkBuffers tb;
   tb.hist = reinterpret_cast<int*>(p);
-  p += topk_hist_bytes(B);
+  p += topk_zero_bytes(B);
   tb.meta = reinterpret_cast<RowMeta*>(p);
   p += up256((size_t)B * sizeof(RowMeta));
   tb.ckey = reinterpret_cast<uint32_t*>(p);
@@ -1197,7 +1201,7 @@ int topk_two_level_sub(long n, int keep) { return n <= TOPK_FLAT_MAX ? 0 : topk_
 // Where the first level's sub-block maxima [B, ceil(n / sub)] live in a top-k workspace: written there by a producer
 // (the prefill indexer), they let launch_prefill_topk skip block_max_kernel.
 float* topk_bm_buffer(void* ws, int B) {
-  return reinterpret_cast<float*>(static_cast<char*>(ws) + topk_hist_bytes(B) + up256((size_t)B * sizeof(RowMeta)) +
+  return reinterpret_cast<float*>(static_cast<char*>(ws) + topk_zero_bytes(B) + up256((size_t)B * sizeof(RowMeta)) +
                                   up256((size_t)B * TC_MAXCH * TC_CHUNK * 4));
 }
 
@@ -1210,7 +1214,7 @@ hipError_t launch_prefill_topk(const float* scores, const int* len, int* idx, in
   char* p = static_cast<char*>(ws);
   TopkBuffers tb;
   tb.hist = reinterpret_cast<int*>(p);
-  p += topk_hist_bytes(B);
+  p += topk_zero_bytes(B);
   tb.meta = reinterpret_cast<RowMeta*>(p);
   p += up256((size_t)B * sizeof(RowMeta));
   tb.ckey = reinterpret_cast<uint32_t*>(p);

@@ -1,5 +1,7 @@
 """One DSA decode layer step on gfx950 in one call: indexer -> top-k -> sparse MLA, the order of
-trnrt/models/mla.py:506-528 `attention_long` (at kpool 1, with the q_lat / W_UV projections outside, as there).
+trnrt/models/mla.py:506-528 `attention_long` (at kpool 1, with the q_lat / W_UV projections outside, as there). For
+rows of up to 32,768 tokens the step is one kernel launch (csrc/dsa_fused.hip); otherwise, or with chain=True, the
+separate kernels enqueued back to back.
 
 DecodeLayer preallocates the intermediates (scores, indices, counts) and the workspace once for a batch shape, so a
 step allocates nothing and can be captured in a HIP graph; step() enqueues the three operators on the current stream
@@ -26,7 +28,8 @@ class DecodeLayer:
 
     def __init__(self, B: int, Hi: int, H: int, max_pages: int, page_size: int, num_pages: int, keep: int = 2048,
                  scale: float = 192 ** -0.5, max_len: int | None = None, splits: int = 0,
-                 device: torch.device | str = "cuda"):
+                 device: torch.device | str = "cuda", chain: bool = False):
+        self.chain = chain  # True: the separate-kernel form (dsa_decode_layer_chain) even where one launch applies
         self.B, self.Hi, self.H = B, Hi, H
         self.max_pages, self.page_size, self.num_pages = max_pages, page_size, num_pages
         self.keep, self.scale, self.splits = keep, float(scale), splits
@@ -67,7 +70,8 @@ class DecodeLayer:
                 raise ValueError(f"caches of {k_cache.numel()} / {kv_cache.numel()} bytes for {slots} slots")
             C.need(k_scale, "k_scale", torch.float32, (slots,))
             C.need(kv_scale, "kv_scale", torch.float32, (slots,))
-        st = _lib.lib().dsa_decode_layer(
+        fn = _lib.lib().dsa_decode_layer_chain if self.chain else _lib.lib().dsa_decode_layer
+        st = fn(
             q_idx.data_ptr(), w.data_ptr(), k_cache.data_ptr(), k_scale.data_ptr(), q.data_ptr(),
             kv_cache.data_ptr(), kv_scale.data_ptr(), table.data_ptr(), ctx_len.data_ptr(), self.scores.data_ptr(),
             self.idx.data_ptr(), self.cnt.data_ptr(), self.out.data_ptr(), self.lse.data_ptr(),
