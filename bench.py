@@ -1,14 +1,17 @@
 """DSA decode layer-step benchmark on one MI355X (gfx950).
 
 A step is one layer of the DSA decode path over the batch: lightning indexer over every cached token -> exact
-top-2048 per row -> sparse MLA attention over the selected FP8 rows, all three as HIP kernels of libdsa_gfx950.so on
-one stream, with every input resident in HBM before the timed region. The workload is BASELINE.json's main decode
+top-2048 per row -> sparse MLA attention over the selected FP8 rows, as HIP kernels of libdsa_gfx950.so on one
+stream, with every input resident in HBM before the timed region. The workload is BASELINE.json's main decode
 shape (config 2: B=8 sequences x 32,768 tokens, 64 query heads of 512 latent + 64 rope, 64 indexer heads x 128, FP8
 e4m3 paged caches with per-token fp32 scales, pages of 64, top-2048), synthetic seeded data.
 
-Prints ONE JSON line: the layer-step rate (value), the roofline of the dominant kernel (the indexer: its algorithmic
-bytes per launch over its HIP-event-timed average duration) and the CPU baseline (the oracle's torch restatement of
-the reference arithmetic, timed on this host's cores on a bounded sample of the same workload).
+Prints ONE JSON line: the layer-step rate (value), the roofline of the dominant kernel and the CPU baseline (the
+oracle's torch restatement of the reference arithmetic, timed on this host's cores on a bounded sample of the same
+workload, each operator's median reported beside the step's). Rows of up to 32,768 tokens run as one launch per
+8 rows (decode_fused_kernel: the whole layer), so its roofline is the layer's algorithmic bytes over that kernel's
+HIP-event-timed duration; longer rows run the separate kernels, whose roofline is the indexer's. layer.step_us gives
+the median, p10 and p90 of single steps, each timed by a pair of events around it.
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--config 2] [--no-cpu-baseline]
     python bench.py --config 5          # the chunked-prefill step (65,536 cached + 2,048 new queries): its own line
@@ -16,7 +19,7 @@ the reference arithmetic, timed on this host's cores on a bounded sample of the 
     python bench.py --config 7          # the pooled (GLM) chunked-prefill step (65,536 cached + 2,048 new queries)
     python bench.py --copy-probe 512    # plain device copies of 512 MiB: the calibration run for HBM counters
 
-roofline.traffic (HBM bytes per indexer launch) comes from rocprofv3 FETCH_SIZE / WRITE_SIZE counter runs of this
+roofline.traffic (HBM bytes per launch of the roofline's kernel) comes from rocprofv3 FETCH_SIZE / WRITE_SIZE counter runs of this
 script, each scaled by the same counter's reading for the --copy-probe kernels; the measured figures are kept in
 profiles/traffic.json and reported when they were taken on the same workload.
 """
@@ -76,35 +79,65 @@ def _indexer_bytes(lengths, Hi, page_size=64):
     return sum(132 * L + 4 * -(-L // page_size) + 256 * Hi + 4 * Hi for L in lengths)
 
 
+def _host_model() -> str:
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "the host CPU"
+
+
+def _cpu_threads() -> int:
+    """The host threads a CPU baseline uses: every core of this process's affinity set, capped at 16 (a one-GPU box's
+    CPU share; its affinity set may list the whole machine's cores)."""
+    return min(len(os.sched_getaffinity(0)), 16)
+
+
 def cpu_baseline(inp, budget_s: float = 15.0) -> dict:
     """The oracle (oracle/dsa_oracle.py, torch fp32 on the host) run on whole layer-steps of the same inputs, as many
-    as fit in about budget_s seconds (at least one)."""
+    as fit in about budget_s seconds (at least three), each operator timed on its own: value = 1 / the median step;
+    ops_median_s = each operator's median."""
     import torch
 
     from oracle import dsa_oracle as O
 
-    cores = min(len(os.sched_getaffinity(0)), 16)  # the box's CPU share for one GPU
+    cores = _cpu_threads()
     torch.set_num_threads(cores)
     cpu = inp.to("cpu")
-    O.decode_layer_ref(cpu)  # warm-up
-    n, t0 = 0, time.perf_counter()
+    cfg = cpu.cfg
+    stride = cpu.max_pages * cfg.page_size
+
+    def one():
+        t = [time.perf_counter()]
+        sc = O.indexer_ref(cpu.q_idx, cpu.w_k, cpu.k_cache, cpu.k_scale, cpu.table, cpu.ctx_len, cfg.page_size, stride)
+        t.append(time.perf_counter())
+        idx, cnt = O.topk_ref(sc, cfg.keep, cpu.ctx_len)
+        t.append(time.perf_counter())
+        O.sparse_mla_ref(cpu.q, cpu.kv_cache, cpu.kv_scale, idx, cnt, cpu.table, cfg.page_size, cfg.scale)
+        t.append(time.perf_counter())
+        return [t[i + 1] - t[i] for i in range(3)]
+
+    one()  # warm-up
+    rows, t0 = [], time.perf_counter()
     while True:
-        O.decode_layer_ref(cpu)
-        n += 1
+        rows.append(one())
         dt = time.perf_counter() - t0
-        if dt >= budget_s or n >= 5000:
+        if (dt >= budget_s and len(rows) >= 3) or len(rows) >= 5000:
             break
-    model = ""
-    try:
-        for ln in open("/proc/cpuinfo"):
-            if ln.startswith("model name"):
-                model = ln.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    return {"value": n / dt, "unit": "layer-steps/s", "cores": cores, "kind": "port",
-            "sample": f"{n} full layer-steps of the same workload (indexer + top-k + attention, torch fp32, "
-                      f"{dt:.1f} s, {cores} threads on {model or 'the host CPU'})"}
+
+    def med(v):
+        v = sorted(v)
+        return v[len(v) // 2]
+
+    step = med([sum(r) for r in rows])
+    ops = {name: round(med([r[i] for r in rows]), 6) for i, name in enumerate(("indexer", "topk", "sparse_mla"))}
+    return {"value": round(1.0 / step, 3), "unit": "layer-steps/s", "cores": cores, "kind": "port",
+            "ops_median_s": ops,
+            "sample": f"{len(rows)} full layer-steps of the same workload (indexer + top-k + attention, torch fp32, "
+                      f"{dt:.1f} s, {cores} threads = this process's affinity set capped at 16 on {_host_model()}); "
+                      f"value = 1 / the median step"}
 
 
 def kernel_times(lib, step, steps: int, pairs: int = 16) -> dict:
@@ -148,6 +181,27 @@ def kernel_times(lib, step, steps: int, pairs: int = 16) -> dict:
     return {k: v / steps for k, v in tot.items()}
 
 
+def step_times(step, steps: int) -> list:
+    """Each of `steps` calls of step() timed on its own by a pair of torch CUDA events on the current stream (the
+    stream the library launches on), in us."""
+    import torch
+
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for a, b in evs:
+        a.record()
+        step()
+        b.record()
+    torch.cuda.synchronize()
+    return [a.elapsed_time(b) * 1e3 for a, b in evs]
+
+
+def percentiles(v) -> dict:
+    """median, p10 and p90 (nearest rank) of a list of durations."""
+    v = sorted(v)
+    at = lambda f: v[min(len(v) - 1, int(f * len(v)))]
+    return {"median": round(at(0.5), 3), "p10": round(at(0.1), 3), "p90": round(at(0.9), 3)}
+
+
 def prefill_cpu_baseline(inp, cfg, budget_s: float = 15.0) -> dict:
     """The oracle's chunk step (prefill_scores_ref + topk_ref + sparse_mla_ref, torch fp32 on the host) over whole
     query rows of the same chunk, as many rows as fit in about budget_s seconds; reported as chunks per second
@@ -156,7 +210,7 @@ def prefill_cpu_baseline(inp, cfg, budget_s: float = 15.0) -> dict:
 
     from oracle import dsa_oracle as O
 
-    cores = min(len(os.sched_getaffinity(0)), 16)
+    cores = _cpu_threads()
     torch.set_num_threads(cores)
     cpu = inp.to("cpu")
     qv = cpu.q_values()  # the queries' values (dequantised when FP8)
@@ -271,7 +325,7 @@ def pooled_cpu_baseline(inp, cfg, npool, positions, budget_s: float = 15.0) -> d
 
     from oracle import dsa_oracle as O
 
-    cores = min(len(os.sched_getaffinity(0)), 16)
+    cores = _cpu_threads()
     torch.set_num_threads(cores)
     cpu = inp.to("cpu")
     keys = cpu.pool_key.view(-1, cfg.D)
@@ -335,6 +389,7 @@ def pooled_main(args) -> int:
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / args.steps
     k_us = kernel_times(lib, step, args.steps)
+    spans = step_times(step, args.steps)
     positions = pos.cpu().long()
     npool = torch.div(positions + 1, kp, rounding_mode="floor")
     tail = [int(p) + 1 - kp * int(n) for p, n in zip(positions, npool)]
@@ -367,7 +422,7 @@ def pooled_main(args) -> int:
                      "algorithmic_bytes": idx_bytes, "avg_us": round(idx_us, 3)},
         "layer": {"algorithmic_bytes": step_bytes, "achieved_GBs": round(step_gbs, 1),
                   "frac": round(step_gbs / HBM_PEAK_GBS, 4), "kernel_us": {k: round(v, 3) for k, v in k_us.items()},
-                  "launch_gaps_us": round(ms * 1e3 - sum(k_us.values()), 3)},
+                  "step_us": percentiles(spans)},
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = pooled_cpu_baseline(inp, cfg, npool, positions)
@@ -464,7 +519,7 @@ def pooled_prefill_cpu_baseline(inp, cfg, budget_s: float = 15.0) -> dict:
 
     from oracle import dsa_oracle as O
 
-    cores = min(len(os.sched_getaffinity(0)), 16)
+    cores = _cpu_threads()
     torch.set_num_threads(cores)
     c = inp.to("cpu")
     ones = torch.ones(cfg.P)
@@ -544,15 +599,22 @@ def main() -> int:
     ms = dt * 1e3 / args.steps
 
     # per-kernel device durations inside the same layer-step: HIP events recorded by the runtime at each kernel's own
-    # start and end (hipExtLaunchKernel on the launch stream), over another `steps` steps
+    # start and end (hipExtLaunchKernel on the launch stream), over another `steps` steps; then each step's own device
+    # time (a pair of events around it) over another `steps`, for the median / p10 / p90
     k_us = kernel_times(lib, step, args.steps)
+    spans = step_times(step, args.steps)
 
     lengths = inp.lengths
-    idx_bytes = _indexer_bytes(lengths, cfg.Hi, cfg.page_size)
-    idx_us = k_us["indexer_decode_kernel"]
-    achieved = idx_bytes / (idx_us * 1e-6) / 1e9
     layer_bytes = W.algorithmic_bytes(lengths, cfg.H, cfg.Hi, cfg.keep, cfg.page_size)
     layer_gbs = layer_bytes / (ms * 1e-3) / 1e9
+    if "decode_fused_kernel" in k_us:
+        # the one-launch layer (rows of up to 32K tokens): its launches together move the layer's algorithmic bytes
+        kname, kbytes = "decode_fused_kernel", layer_bytes
+    else:
+        # the separate-kernel layer: the indexer, the kernel that streams the whole key cache
+        kname, kbytes = "indexer_decode_kernel", _indexer_bytes(lengths, cfg.Hi, cfg.page_size)
+    k_time = k_us[kname]
+    achieved = kbytes / (k_time * 1e-6) / 1e9
 
     workload = f"config {args.config}: {cfg.name}"
     out = {
@@ -571,14 +633,15 @@ def main() -> int:
         "config": {"workload": workload, "batch": cfg.B, "context": max(lengths),
                    "q_heads": cfg.H, "indexer_heads": cfg.Hi, "keep": cfg.keep, "page_size": cfg.page_size,
                    "kv": "fp8 e4m3 [576] + fp32 scale per token", "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "kernel": "indexer_decode_kernel", "achieved": round(achieved, 1),
+        "roofline": {"bound": "hbm", "kernel": kname, "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(workload, "indexer_decode_kernel"), "algorithmic_bytes": idx_bytes,
-                     "avg_us": round(idx_us, 3)},
+                     "traffic": measured_traffic(workload, kname), "algorithmic_bytes": kbytes,
+                     "avg_us": round(k_time, 3), "launches_per_step": -(-cfg.B // 8) if kname == "decode_fused_kernel"
+                     else 1},
         "layer": {"algorithmic_bytes": layer_bytes, "achieved_GBs": round(layer_gbs, 1),
                   "frac": round(layer_gbs / HBM_PEAK_GBS, 4),
                   "kernel_us": {k: round(v, 3) for k, v in k_us.items()},
-                  "launch_gaps_us": round(ms * 1e3 - sum(k_us.values()), 3)},
+                  "step_us": percentiles(spans)},
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(inp)
