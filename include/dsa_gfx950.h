@@ -220,7 +220,9 @@ int dsa_decode_layer_chain(const void* q_idx_bf16, const float* w, const uint8_t
  * that cannot allocate device memory, such as code under HIP graph capture, tight serving loops or harnesses that
  * forbid hipMalloc). The workspace is the library's own scratch, a static device array of
  * DSA_NOALLOC_SCRATCH_BYTES per GPU (allocated with the library's code object on each GPU it runs on and held until
- * the process ends; zero-filled by a kernel on `stream` at the first call on a device). A call whose
+ * the process ends; zero-filled by a kernel on `stream` at the first call on a device; a call whose zero region
+ * (the row histograms and barrier words of its batch size) reaches past the previous call's gets the difference
+ * zero-filled on `stream` first, so calls of any batch sizes follow each other). A call whose
  * dsa_workspace_bytes(DSA_WS_LAYER, B, H, keep, max_len, splits) exceeds that size returns DSA_ESCRATCH before any
  * HIP call. Every call on a GPU shares that GPU's scratch: calls that overlap on one GPU (several streams, host
  * threads) race and must be serialised by the caller. Arguments and results as dsa_decode_layer.

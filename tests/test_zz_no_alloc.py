@@ -1,6 +1,7 @@
 """The allocation-free decode layer entry point (dsa_decode_layer_noalloc: no workspace argument, the library's own
-static device scratch) against the workspace entry point (dsa_decode_layer) through the C ABI: two calls in a row on
-the same scratch, the second with a smaller input (fewer rows, shorter contexts, fewer heads), each checked to the
+static device scratch) against the workspace entry point (dsa_decode_layer) through the C ABI: calls in a row on
+the same scratch, the second with a smaller input (fewer rows, shorter contexts, fewer heads) and a third with more
+rows again (its zero region covers what the second call left past its own), each checked to the
 parity bar against the workspace entry point's outputs on the same inputs (indices and counts bit-exact, scores within
 1e-2 row-relative, the bf16 output within 2e-2 and lse within 1e-3), and a size beyond the scratch refused before
 any GPU work."""
@@ -54,9 +55,10 @@ def _compare(cfg, lengths, seed):
 
 
 def test_noalloc_layer_matches_workspace_layer_twice():
-    # first call: 4 rows of up to 12,000 tokens, 64 + 64 heads; second: 2 shorter rows, 16 + 16 heads
+    # first call: 4 rows of up to 12,000 tokens, 64 + 64 heads; second: 2 shorter rows, 16 + 16 heads; third: 6 rows
     _compare(W.Config("noalloc-a", B=4, L=12000, H=64, Hi=64), [12000, 9000, 2048, 700], seed=11)
     _compare(W.Config("noalloc-b", B=2, L=4096, H=16, Hi=16), [4096, 1500], seed=12)
+    _compare(W.Config("noalloc-c", B=6, L=8192, H=64, Hi=64), [8192, 5000, 300, 8000, 2049, 4096], seed=13)
 
 
 def test_noalloc_layer_refuses_more_than_its_scratch():

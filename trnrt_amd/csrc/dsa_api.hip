@@ -110,11 +110,14 @@ int effective_splits(int splits, int keep) {
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
+size_t g_scratch_zero[kMaxDevices] = {};  // bytes from the scratch's start that are zero when the next call runs
 
-// The current device's scratch address; on the first call for a device (with that device current) its address is
-// looked up and the array zero-filled on `stream` (a fill kernel, ordered before the call that uses it), so the
-// regions dsa_decode_layer needs at zero start at zero; every call leaves them so. Null on a HIP error.
-void* noalloc_scratch(hipStream_t stream) {
+// The current device's scratch address, with its first zero_bytes at zero for the call about to run. On the first
+// call for a device (with that device current) the address is looked up and the whole array zero-filled on `stream`
+// (a fill kernel, ordered before the call that uses it). A call leaves the zero region of its own batch size at zero
+// and may write anything past it, so a later call with a larger zero region gets the difference filled first. Null
+// on a HIP error.
+void* noalloc_scratch(hipStream_t stream, size_t zero_bytes) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
   std::lock_guard<std::mutex> lock(g_scratch_mu);
@@ -123,8 +126,18 @@ void* noalloc_scratch(hipStream_t stream) {
     if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
     if (dsa::launch_fill_zero(ptr, DSA_NOALLOC_SCRATCH_BYTES, stream) != hipSuccess) return nullptr;
     g_scratch_ptr[dev] = ptr;
+    g_scratch_zero[dev] = DSA_NOALLOC_SCRATCH_BYTES;
   }
-  return g_scratch_ptr[dev];
+  uint8_t* p = static_cast<uint8_t*>(g_scratch_ptr[dev]);
+  const size_t z = g_scratch_zero[dev];
+  if (zero_bytes > z) {
+    if (dsa::launch_fill_zero(p + z, zero_bytes - z, stream) != hipSuccess) {
+      g_scratch_zero[dev] = 0;
+      return nullptr;
+    }
+  }
+  g_scratch_zero[dev] = zero_bytes;
+  return p;
 }
 
 }  // namespace
@@ -485,7 +498,7 @@ int dsa_decode_layer_noalloc(const void* q_idx_bf16, const float* w, const uint8
   const size_t need = dsa_workspace_bytes(DSA_WS_LAYER, B, H, keep, max_len, splits);
   if (need == 0 || need > DSA_NOALLOC_SCRATCH_BYTES) return DSA_ESCRATCH;
   if (B == 0) return DSA_OK;
-  void* ws = noalloc_scratch(static_cast<hipStream_t>(stream));
+  void* ws = noalloc_scratch(static_cast<hipStream_t>(stream), dsa::topk_zero_bytes(B));
   if (!ws) return DSA_ELAUNCH;
   return dsa_decode_layer(q_idx_bf16, w, k_fp8, k_scale, q_bf16, kv_fp8, kv_scale, page_table, ctx_len, scores, idx,
                           cnt, out_bf16, lse, ws, DSA_NOALLOC_SCRATCH_BYTES, B, Hi, H, max_pages, page_size,
