@@ -45,7 +45,8 @@ constexpr int FU_MAXLEN = FU_NW * FU_KEYS;            // 32,768
 constexpr int FU_D = 128;                             // indexer head dim
 constexpr int FU_QROW = FU_D + 8;                     // staged indexer query row (bf16)
 constexpr int FU_HBINS = HIST_BINS;
-constexpr int FU_CAND_LDS = 4096;  // candidates held in LDS (more: read from the L2 in each pass)
+constexpr int FU_CROW = FU_KEYS + 32;  // a workgroup's candidate block: its counts word, then its candidates
+constexpr int FU_CSTAGE = 128;         // words of each block read into registers (the counts and 127 candidates)
 constexpr int FU_HPW = 16;         // heads per attention workgroup
 constexpr int FU_CH = 64;          // slot granularity of a split
 constexpr int FU_SPLIT = 256;      // at most 256 slots per split
@@ -63,9 +64,8 @@ constexpr int FU_SYNC_WORDS = 16;       // per XCD: arrivals, exits, error flag
 // LDS (160 KiB, one workgroup per CU), phase by phase:
 constexpr int L_STATE = 0;       // FuState: selection results (stage 3)
 constexpr int L_MISC = 1536;     // block-scan scratch (stages 1-3)
-constexpr int L_CV = 2048;       // stage 3: candidate values [4096]
-constexpr int L_BINS = 22528;    // stage 3: 2048 bins
-constexpr int L_BINS2 = 30720;   // stage 3: 512 bins
+constexpr int L_BINS = 2048;     // stage 3: 2048 bins
+constexpr int L_BINS2 = 10240;   // stage 3: 512 bins
 constexpr int L_QS = 32768;      // stage 1: indexer queries [64][136] bf16
 constexpr int L_WS = 50176;      // stage 1: head weights [64]
 constexpr int L_HS = 50432;      // stage 1: histogram [4096]
@@ -80,23 +80,16 @@ constexpr int L_RED = 162048;    // stage 4: per-wave head maxima [8][16]
 constexpr int L_SRED = 162560;   // stage 4: per-wave head sums [8][16]
 constexpr int FU_LDS = 163840;
 static_assert(L_HS + 4 * FU_HBINS <= L_TPG && L_TPG + 4 * 32 == L_SCS, "stage 1 layout");
-static_assert(L_CV + 4 * FU_CAND_LDS <= L_BINS && L_BINS2 + 4 * 512 <= L_QS, "stage 3 layout");
+static_assert(L_BINS + 4 * 2048 <= L_BINS2 && L_BINS2 + 4 * 512 <= L_QS, "stage 3 layout");
 static_assert(L_P == FU_SPLIT * FU_KROW && L_P + 2 * FU_HPW * FU_PROW <= L_KSC, "stage 4 layout");
 static_assert(L_SRED + 4 * FU_WAVES * FU_HPW <= FU_LDS && L_SCS + 4 * FU_KEYS == FU_LDS, "LDS size");
 static_assert(L_AQ + 2 * FU_HPW * FU_AQROW <= L_P, "query staging");
 
 struct FuState {
-  int na[FU_NW];   // per workgroup: keys above the first-level bin
-  int nc[FU_NW];   // its candidates
-  int cb[FU_NW];   // exclusive prefix of nc
-  int gt[FU_NW];   // its candidates above T
-  int eq[FU_NW];   // its candidates equal to T
-  int sel[FU_NW];  // its selected keys
-  int off[FU_NW];  // its first output index
-  int tb[FU_NW];   // ties at T before it
-  int c0, above0, nvis, cnt_row;
-  uint32_t T;
-  int room, ncand, pad;
+  int na[FU_NW];  // per workgroup: keys above the first-level bin
+  int gt[FU_NW];  // its candidates above T
+  int eq[FU_NW];  // its candidates equal to T
+  int c0, above0, nvis, pad;
 };
 static_assert(sizeof(FuState) <= L_MISC, "state");
 
@@ -117,8 +110,8 @@ struct FusedArgs {
   float* lse;
   int* hist;       // [B][4096], zero between calls
   int* sync;       // [8][16]: barrier words, zero between calls (the error flag excepted)
-  int2* cnts;      // [B][32]: (keys above c0, candidates) per workgroup
-  uint32_t* cand;  // [B][32][1024]: candidates, (low 20 key bits << 10) | position in the workgroup's range
+  uint32_t* cand;  // [B][32][1056]: per workgroup (keys above c0) << 16 | (candidates), then the candidates,
+                   // (low 20 key bits << 10) | position in the workgroup's range, in position order
   int* rows;       // [B][keep]: the cache slot of each selected position (position 0's past the count)
   float* part;     // [B][S][H][512]: split outputs (normalised)
   float2* ml;      // [B][S][H]: split max and sum
@@ -386,7 +379,7 @@ __device__ __forceinline__ void fu_classify(const FusedArgs& a, uint8_t* lds, in
   __syncthreads();  // every thread has read scr (the bin search) before it is rewritten
   uint32_t tot;
   const uint32_t before = fu_block_prefix(((uint32_t)na << 16) | (uint32_t)nc, scr, &tot);
-  uint32_t* crow = a.cand + ((size_t)b * FU_NW + j) * FU_KEYS;
+  uint32_t* crow = a.cand + ((size_t)b * FU_NW + j) * FU_CROW + 1;
   int o = (int)(before & 0xFFFFu);
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
@@ -396,7 +389,7 @@ __device__ __forceinline__ void fu_classify(const FusedArgs& a, uint8_t* lds, in
     }
   }
   if (tid == 0) {
-    a.cnts[(size_t)b * FU_NW + j] = make_int2((int)(tot >> 16), (int)(tot & 0xFFFFu));
+    crow[-1] = tot;
     st.c0 = c0;
     st.above0 = above0;
     st.nvis = nvis;
@@ -408,58 +401,44 @@ __device__ __forceinline__ void fu_classify(const FusedArgs& a, uint8_t* lds, in
 __device__ __forceinline__ void fu_select(const FusedArgs& a, uint8_t* lds, int b, int j) {
   FuState& st = *reinterpret_cast<FuState*>(lds + L_STATE);
   int* scr = reinterpret_cast<int*>(lds + L_MISC);
-  uint32_t* cv = reinterpret_cast<uint32_t*>(lds + L_CV);
   int* bins = reinterpret_cast<int*>(lds + L_BINS);
   int* bins2 = reinterpret_cast<int*>(lds + L_BINS2);
   const int* tpg = reinterpret_cast<const int*>(lds + L_TPG);
-  const int tid = threadIdx.x, wave = tid / WAVE, lane = tid & (WAVE - 1);
+  const int tid = threadIdx.x, lane = tid & (WAVE - 1);
   const int c0 = st.c0;
-  const uint32_t* cbase = a.cand + (size_t)b * FU_NW * FU_KEYS;
-  if (wave == 0) {
-    const uint64_t v = ld_sc1_64(a.cnts + (size_t)b * FU_NW + (lane & (FU_NW - 1)));
-    const int na = lane < FU_NW ? (int)(uint32_t)v : 0, nc = lane < FU_NW ? (int)(uint32_t)(v >> 32) : 0;
-    const int inc = wave_incl_scan(nc);
-    if (lane < FU_NW) {
-      st.na[lane] = na;
-      st.nc[lane] = nc;
-      st.cb[lane] = inc - nc;
-      st.gt[lane] = 0;
-      st.eq[lane] = 0;
-    }
-    if (lane == FU_NW - 1) st.ncand = inc;
+  // thread (w, q) = (tid / 16, tid % 16) holds words 8 q .. 8 q + 7 of workgroup w's candidate block (one round of
+  // L2 loads for the whole row: word 0 the counts, then up to 127 candidates; a block with more keeps the rest in
+  // the L2, read by the block's 16 threads in each pass)
+  const int w = tid >> 4, q = tid & 15;
+  const uint32_t* blk = a.cand + ((size_t)b * FU_NW + w) * FU_CROW;
+  uint32_t cw[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint64_t v = ld_sc1_64(blk + 8 * q + 2 * i);
+    cw[2 * i] = (uint32_t)v;
+    cw[2 * i + 1] = (uint32_t)(v >> 32);
   }
   for (int i = tid; i < 2048; i += FU_THREADS) bins[i] = 0;
   bins2[tid] = 0;
   if (tid == 0) scr[8] = -1;
-  __syncthreads();
-  const int C = st.ncand;
-  const bool cached = C <= FU_CAND_LDS;
-  if (c0 >= 0) {
-    if (cached) {
-      // every workgroup's candidates straight into LDS, in workgroup order (wave v takes workgroups v, v + 8, ...;
-      // lane l of a load writes entry base + l)
-      for (int w = wave; w < FU_NW; w += FU_WAVES) {
-        const int n = st.nc[w], base = st.cb[w];
-        for (int c = 0; c < n; c += WAVE) {
-          if (c + lane < n)
-            __builtin_amdgcn_global_load_lds(cbase + (size_t)w * FU_KEYS + c + lane,
-                                             (__attribute__((address_space(3))) void*)(cv + base + c), 4, 0,
-                                             FU_AUX_SC1);
-        }
-      }
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
-    }
-    // candidate i's value: from LDS, or (more candidates than LDS holds) from the L2
-    auto cand_at = [&](int i) __attribute__((always_inline)) {
-      if (cached) return cv[i];
-      int w = 0;
+  const uint32_t counts = (uint32_t)__shfl((int)cw[0], lane & ~15, WAVE);
+  const int nc = (int)(counts & 0xFFFFu);
+  if (q == 0) st.na[w] = (int)(counts >> 16);
+  // candidate e of the block (word 1 + e) is live when e < nc
+  auto each = [&](auto&& f) __attribute__((always_inline)) {
 #pragma unroll
-      for (int s2 = 16; s2 >= 1; s2 >>= 1)
-        if (w + s2 < FU_NW && st.cb[w + s2] <= i) w += s2;
-      return ld_sc1(cbase + (size_t)w * FU_KEYS + (i - st.cb[w]));
-    };
-    for (int i = tid; i < C; i += FU_THREADS) atomicAdd(&bins[(cand_at(i) >> 19) & 2047], 1);
+    for (int i = 0; i < 8; ++i) {
+      const int e = 8 * q + i - 1;
+      if (e >= 0 && e < nc) f(cw[i]);
+    }
+    for (int e = FU_CSTAGE - 1 + q; e < nc; e += 16) f(ld_sc1(blk + 1 + e));
+  };
+  __syncthreads();
+  uint32_t T = 0u;
+  int room = 0;
+  int gt = 0, eq = 0;
+  if (c0 >= 0) {
+    each([&](uint32_t v) __attribute__((always_inline)) { atomicAdd(&bins[(v >> 19) & 2047], 1); });
     __syncthreads();
     constexpr int P1 = 2048 / FU_THREADS;
     int hb[P1];
@@ -471,59 +450,43 @@ __device__ __forceinline__ void fu_select(const FusedArgs& a, uint8_t* lds, int 
     need -= above1;
     __syncthreads();
     if (tid == 0) scr[8] = -1;
-    for (int i = tid; i < C; i += FU_THREADS) {
-      const uint32_t v = cand_at(i);
+    each([&](uint32_t v) __attribute__((always_inline)) {
       if (((v >> 19) & 2047) == (uint32_t)c1) atomicAdd(&bins2[(v >> 10) & 511], 1);
-    }
+    });
     __syncthreads();
     const int hb2[1] = {bins2[tid]};
     int c2, above2;
     fu_find_bin<1>(hb2, need, scr, &c2, &above2);
     const uint32_t tlow = ((uint32_t)c1 << 9) | (uint32_t)c2;
-    const int room = max(need - above2, 0);
-    // per workgroup: candidates above T and equal to T (its range [cb, cb + nc) of the candidates)
-    for (int w = wave; w < FU_NW; w += FU_WAVES) {
-      const int n = st.nc[w], base = st.cb[w];
-      int gt = 0, eq = 0;
-      for (int c = 0; c < n; c += WAVE) {
-        const bool in = c + lane < n;
-        const uint32_t kl = in ? cand_at(base + c + lane) >> 10 : 0u;
-        gt += __builtin_popcountll(__ballot(in && kl > tlow));
-        eq += __builtin_popcountll(__ballot(in && kl == tlow));
-      }
-      if (lane == 0) {
-        st.gt[w] = gt;
-        st.eq[w] = eq;
-      }
+    room = max(need - above2, 0);
+    T = ((uint32_t)c0 << 20) | tlow;
+    // per workgroup: its candidates above T and equal to T, summed over the block's 16 threads
+    each([&](uint32_t v) __attribute__((always_inline)) {
+      gt += (v >> 10) > tlow;
+      eq += (v >> 10) == tlow;
+    });
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) {
+      gt += __shfl_xor(gt, m, WAVE);
+      eq += __shfl_xor(eq, m, WAVE);
     }
-    if (tid == 0) {
-      st.T = ((uint32_t)c0 << 20) | tlow;
-      st.room = room;
-    }
-  } else if (tid == 0) {
-    st.T = 0u;
-    st.room = 0;
+  }
+  if (q == 0) {
+    st.gt[w] = gt;
+    st.eq[w] = eq;
   }
   __syncthreads();
-  if (wave == 0) {
-    const int w = lane & (FU_NW - 1);
-    const int eq = lane < FU_NW ? st.eq[w] : 0;
-    const int tb = wave_incl_scan(eq) - eq;
-    const int take = min(max(st.room - tb, 0), eq);
-    const int sel = lane < FU_NW ? st.na[w] + st.gt[w] + take : 0;
-    const int off = wave_incl_scan(sel) - sel;
-    if (lane < FU_NW) {
-      st.tb[w] = tb;
-      st.sel[w] = sel;
-      st.off[w] = off;
-    }
-    if (lane == 0) st.cnt_row = min(st.nvis, a.keep);
-  }
-  __syncthreads();
+  // every wave: the ties at T before this workgroup and its first output index (lane w < 32 for workgroup w: ties
+  // are taken while fewer than `room` come before, so workgroup w selects na + gt + its ties taken)
+  const int ww = lane & (FU_NW - 1);
+  const int eqw = lane < FU_NW ? st.eq[ww] : 0;
+  const int tbw = wave_incl_scan(eqw) - eqw;
+  const int selw = lane < FU_NW ? st.na[ww] + st.gt[ww] + min(max(room - tbw, 0), eqw) : 0;
+  const int offw = wave_incl_scan(selw) - selw;
+  const int TB = __shfl(tbw, j, WAVE), base = __shfl(offw, j, WAVE);
+  const int cnt_row = min(st.nvis, a.keep);
   // this workgroup's selections, in position order: keys above T, and ties at T while fewer than `room` ties of the
-  // row come before them; output index off + (selected keys before it in the workgroup)
-  const uint32_t T = st.T;
-  const int room = st.room, TB = st.tb[j], base = st.off[j];
+  // row come before them; output index base + (selected keys before it in the workgroup)
   uint32_t key[2];
   fu_my_keys(lds, key);
   uint32_t na = 0, nt = 0;
@@ -533,7 +496,7 @@ __device__ __forceinline__ void fu_select(const FusedArgs& a, uint8_t* lds, int 
     nt += T != 0u && key[e] == T;
   }
   uint32_t tot;
-  const uint32_t bef = fu_block_prefix((na << 16) | nt, scr, &tot);
+  const uint32_t bef = fu_block_prefix((na << 16) | nt, scr + 16, &tot);
   int a_before = (int)(bef >> 16), t_before = (int)(bef & 0xFFFFu);
   const int tb_taken = min(TB, room);
   int* irow = a.idx + (size_t)b * a.keep;
@@ -553,7 +516,6 @@ __device__ __forceinline__ void fu_select(const FusedArgs& a, uint8_t* lds, int 
     t_before += tie;
   }
   // the outputs past the count (their slots: position 0's), and the count
-  const int cnt_row = st.cnt_row;
   for (int o = cnt_row + j * FU_THREADS + tid; o < a.keep; o += FU_NW * FU_THREADS) {
     irow[o] = 0;
     rrow[o] = safe_page(a.table[(size_t)b * a.max_pages], a.num_pages) * a.page_size;
@@ -587,7 +549,7 @@ __device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int 
   const int hg = j % a.HG, s = j / a.HG;
   if (s >= a.S) return;  // workgroup-uniform
   const int H = a.H;
-  const int cnt_row = st.cnt_row;
+  const int cnt_row = min(st.nvis, a.keep);
   const int o0 = s * a.sps, o1 = min(o0 + a.sps, a.keep);
   // the split's live slots; a row with none attends position 0 masked (its lse is NEG_INF)
   int n_slots = max(min(o1, cnt_row) - o0, 0);
@@ -826,17 +788,16 @@ __global__ __launch_bounds__(FU_THREADS, 1) void decode_fused_kernel(FusedArgs a
 
 static size_t fu_up256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// Workspace of the fused layer past the zero region (histograms + barrier words): the per-workgroup counts, the
-// candidates, the selected slots, the split outputs and their (max, sum).
+// Workspace of the fused layer past the zero region (histograms + barrier words): the per-workgroup candidate blocks,
+// the selected slots, the split outputs and their (max, sum).
 struct FusedLayout {
-  size_t cnts, cand, rows, part, ml, end;
+  size_t cand, rows, part, ml, end;
 };
 
 static FusedLayout fused_layout(size_t zero_bytes, int B, int H, int S, int keep) {
   FusedLayout l;
-  l.cnts = zero_bytes;
-  l.cand = l.cnts + fu_up256((size_t)B * FU_NW * sizeof(int2));
-  l.rows = l.cand + fu_up256((size_t)B * FU_NW * FU_KEYS * 4);
+  l.cand = zero_bytes;
+  l.rows = l.cand + fu_up256((size_t)B * FU_NW * FU_CROW * 4);
   l.part = l.rows + fu_up256((size_t)B * keep * 4);
   l.ml = l.part + fu_up256((size_t)B * S * H * FU_DV * 4);
   l.end = l.ml + fu_up256((size_t)B * S * H * sizeof(float2));
@@ -886,7 +847,6 @@ hipError_t launch_decode_fused(const uint16_t* q_idx, const float* w, const uint
   a.lse = lse;
   a.hist = reinterpret_cast<int*>(p);
   a.sync = reinterpret_cast<int*>(p + hist_bytes);
-  a.cnts = reinterpret_cast<int2*>(p + l.cnts);
   a.cand = reinterpret_cast<uint32_t*>(p + l.cand);
   a.rows = reinterpret_cast<int*>(p + l.rows);
   a.part = reinterpret_cast<float*>(p + l.part);
