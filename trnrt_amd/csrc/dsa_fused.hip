@@ -45,8 +45,16 @@ constexpr int FU_MAXLEN = FU_NW * FU_KEYS;            // 32,768
 constexpr int FU_D = 128;                             // indexer head dim
 constexpr int FU_QROW = FU_D + 8;                     // staged indexer query row (bf16)
 constexpr int FU_HBINS = HIST_BINS;
-constexpr int FU_CROW = FU_KEYS + 32;  // a workgroup's candidate block: its counts word, then its candidates
-constexpr int FU_CSTAGE = 128;         // words of each block read into registers (the counts and 127 candidates)
+constexpr int FU_BMW = FU_KEYS / 32;    // words of a workgroup's bitmap of positions
+// A workgroup's bin list: its count of nonzero histogram bins, then (bin << 16) | count for each
+constexpr int FU_HROW = 1056;
+constexpr int FU_HSTAGE = 256;  // words of each list every workgroup reads into LDS (the rest: read from the L2)
+static_assert(FU_HROW >= 1 + FU_KEYS && FU_HROW % 4 == 0, "bin list");
+// A workgroup's candidate block: its counts word, the bitmap of its keys above the first-level bin, its candidates
+constexpr int FU_CROW = 1088;
+constexpr int FU_CSTAGE = 128;                      // words of each block every workgroup reads into LDS
+constexpr int FU_CSTAGED = FU_CSTAGE - 1 - FU_BMW;  // candidates among them (the rest: read from the L2)
+static_assert(FU_CROW >= 1 + FU_BMW + FU_KEYS && FU_CROW % 4 == 0, "candidate block");
 constexpr int FU_HPW = 16;         // heads per attention workgroup
 constexpr int FU_CH = 64;          // slot granularity of a split
 constexpr int FU_SPLIT = 256;      // at most 256 slots per split
@@ -64,30 +72,38 @@ constexpr int FU_SYNC_WORDS = 16;       // per XCD: arrivals, exits, error flag
 // LDS (160 KiB, one workgroup per CU), phase by phase:
 constexpr int L_STATE = 0;       // FuState: selection results (stage 3)
 constexpr int L_MISC = 1536;     // block-scan scratch (stages 1-3)
-constexpr int L_BINS = 2048;     // stage 3: 2048 bins
-constexpr int L_BINS2 = 10240;   // stage 3: 512 bins
+constexpr int L_HLS = 2048;      // stage 2: the first 256 words of every bin list [32][256]
+constexpr int L_BINS2 = 2048;    // stage 3: 256 bins
+constexpr int L_SPG = 12288;     // stage 3: the pages of the source positions [1024]
+constexpr int L_CB = 16384;      // stage 3: the first 128 words of every candidate block [32][128]
+constexpr int L_SB = 32768;      // stage 3: per workgroup the bitmap of its selected positions [32][32]
+constexpr int L_PB = 36864;      // stage 3: their exclusive prefix popcounts [32][32]
+constexpr int L_BINS = 40960;    // stage 3: 4096 bins
+constexpr int L_QST = 57344;     // stage 3: the attention's 16 heads' queries [16][584] bf16
 constexpr int L_QS = 32768;      // stage 1: indexer queries [64][136] bf16
 constexpr int L_WS = 50176;      // stage 1: head weights [64]
 constexpr int L_HS = 50432;      // stage 1: histogram [4096]
 constexpr int L_TPG = 159616;    // stages 1-3: the page of each of the workgroup's 32 tiles
 constexpr int L_SCS = 159744;    // stages 1-3: the workgroup's 1024 scores
 constexpr int L_KT = 0;          // stage 4: the rows, token-major at the 592-byte stride
-constexpr int L_AQ = 0;          // stage 4, before the gather: the 16 heads' queries [16][584] bf16
-constexpr int L_P = 151552;      // stage 4: P [16][264] bf16; before the gather the split's slot list [256]
+constexpr int L_P = 151552;      // stage 4: P [16][264] bf16; before it (stages 3-4) the split's slot list [256]
 constexpr int L_KSC = 160000;    // stage 4: kv scales [256]
 constexpr int L_BIAS = 161024;   // stage 4: biases [256]
 constexpr int L_RED = 162048;    // stage 4: per-wave head maxima [8][16]
 constexpr int L_SRED = 162560;   // stage 4: per-wave head sums [8][16]
 constexpr int FU_LDS = 163840;
 static_assert(L_HS + 4 * FU_HBINS <= L_TPG && L_TPG + 4 * 32 == L_SCS, "stage 1 layout");
-static_assert(L_BINS + 4 * 2048 <= L_BINS2 && L_BINS2 + 4 * 512 <= L_QS, "stage 3 layout");
+static_assert(L_HLS + 4 * FU_NW * FU_HSTAGE <= L_HS, "stage 2 layout");
+static_assert(L_BINS2 + 4 * 256 <= L_SPG && L_BINS + 4 * 4096 <= L_QST, "stage 3 layout");
+static_assert(L_SPG + 4 * 1024 <= L_CB && L_CB + 4 * FU_NW * FU_CSTAGE <= L_SB && L_SB + 4 * FU_NW * FU_BMW <= L_PB &&
+                  L_PB + 4 * FU_NW * FU_BMW <= L_P,
+              "stage 3 blocks");
+static_assert(L_QST + 2 * FU_HPW * FU_AQROW <= L_P, "query staging");
 static_assert(L_P == FU_SPLIT * FU_KROW && L_P + 2 * FU_HPW * FU_PROW <= L_KSC, "stage 4 layout");
 static_assert(L_SRED + 4 * FU_WAVES * FU_HPW <= FU_LDS && L_SCS + 4 * FU_KEYS == FU_LDS, "LDS size");
-static_assert(L_AQ + 2 * FU_HPW * FU_AQROW <= L_P, "query staging");
 
 struct FuState {
-  int na[FU_NW];  // per workgroup: keys above the first-level bin
-  int gt[FU_NW];  // its candidates above T
+  int gt[FU_NW];  // per workgroup: its candidates above T
   int eq[FU_NW];  // its candidates equal to T
   int c0, above0, nvis, pad;
 };
@@ -108,11 +124,11 @@ struct FusedArgs {
   int* cnt;
   uint16_t* out;
   float* lse;
-  int* hist;       // [B][4096], zero between calls
+  uint32_t* hl;    // [B][32][1056]: per workgroup its histogram's nonzero bins (count, then (bin << 16) | count)
   int* sync;       // [8][16]: barrier words, zero between calls (the error flag excepted)
-  uint32_t* cand;  // [B][32][1056]: per workgroup (keys above c0) << 16 | (candidates), then the candidates,
-                   // (low 20 key bits << 10) | position in the workgroup's range, in position order
-  int* rows;       // [B][keep]: the cache slot of each selected position (position 0's past the count)
+  uint32_t* cand;  // [B][32][1088]: per workgroup (keys above c0) << 16 | (candidates), the bitmap of its positions
+                   // above c0 (32 words), then the candidates, (low 20 key bits << 10) | position in the workgroup's
+                   // range, in position order
   float* part;     // [B][S][H][512]: split outputs (normalised)
   float2* ml;      // [B][S][H]: split max and sum
   int B, Hi, H, max_pages, page_size, page_shift, num_pages, stride, keep;
@@ -334,18 +350,28 @@ __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int
   // positions past 32,768 of a wider score row are never keys of the row
   for (int p = FU_MAXLEN + j * FU_THREADS + tid; p < a.stride; p += FU_NW * FU_THREADS) srow[p] = NEG_INF;
   __syncthreads();
-  int* grow = a.hist + (size_t)b * FU_HBINS;
-  for (int i = tid; i < FU_HBINS; i += FU_THREADS) {
-    const int c = hs[i];
-    if (c) atomicAdd(&grow[i], c);
-  }
+  // the histogram's nonzero bins into the workgroup's bin list (thread t: bins 8 t .. 8 t + 7), in bin order
+  int hv[8];
+  *reinterpret_cast<int4*>(hv) = *reinterpret_cast<const int4*>(hs + 8 * tid);
+  *reinterpret_cast<int4*>(hv + 4) = *reinterpret_cast<const int4*>(hs + 8 * tid + 4);
+  uint32_t nz = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) nz += hv[i] != 0;
+  uint32_t tot;
+  uint32_t o = fu_block_prefix(nz, reinterpret_cast<int*>(lds + L_MISC), &tot);
+  uint32_t* hl = a.hl + ((size_t)b * FU_NW + j) * FU_HROW;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    if (hv[i]) hl[1 + o++] = ((uint32_t)(8 * tid + i) << 16) | (uint32_t)hv[i];
+  if (tid == 0) hl[0] = tot;
 }
 
-// This thread's two keys (positions 2 tid, 2 tid + 1 of the workgroup's range; 0: not selectable).
+// This thread's two keys (positions tid, tid + 512 of the workgroup's range; 0: not selectable).
 __device__ __forceinline__ void fu_my_keys(const uint8_t* lds, uint32_t (&key)[2]) {
-  const float2 sv = *reinterpret_cast<const float2*>(reinterpret_cast<const float*>(lds + L_SCS) + 2 * threadIdx.x);
-  key[0] = order_key(sv.x) & (0u - (uint32_t)(sv.x > VISIBLE));
-  key[1] = order_key(sv.y) & (0u - (uint32_t)(sv.y > VISIBLE));
+  const float* sc = reinterpret_cast<const float*>(lds + L_SCS);
+  const float v0 = sc[threadIdx.x], v1 = sc[threadIdx.x + FU_THREADS];
+  key[0] = order_key(v0) & (0u - (uint32_t)(v0 > VISIBLE));
+  key[1] = order_key(v1) & (0u - (uint32_t)(v1 > VISIBLE));
 }
 
 // Stage 2: the first level from the row histogram, this workgroup's keys above it counted and its candidates written.
@@ -354,117 +380,200 @@ __device__ __forceinline__ void fu_classify(const FusedArgs& a, uint8_t* lds, in
   int* scr = reinterpret_cast<int*>(lds + L_MISC);
   const int tid = threadIdx.x;
   constexpr int PER = FU_HBINS / FU_THREADS;  // 8 bins per thread
-  const int* grow = a.hist + (size_t)b * FU_HBINS;
-  int hb[PER];
-#pragma unroll
-  for (int i = 0; i < PER / 2; ++i) {
-    const uint64_t v = ld_sc1_64(grow + PER * tid + 2 * i);
-    hb[2 * i] = (int)(uint32_t)v;
-    hb[2 * i + 1] = (int)(uint32_t)(v >> 32);
-  }
+  const int wave = tid / WAVE, lane = tid & (WAVE - 1);
+  // the row histogram in LDS from every workgroup's bin list (the first 256 words of each straight into LDS; load
+  // i: list i, lane l words 4 l .. 4 l + 3)
+  uint32_t* hls = reinterpret_cast<uint32_t*>(lds + L_HLS);
+  int* rh = reinterpret_cast<int*>(lds + L_HS);
+  const uint32_t* hlg = a.hl + (size_t)b * FU_NW * FU_HROW;
+  for (int i = wave; i < FU_NW; i += FU_WAVES)
+    __builtin_amdgcn_global_load_lds(hlg + (size_t)i * FU_HROW + 4 * lane,
+                                     (__attribute__((address_space(3))) void*)(hls + FU_HSTAGE * i), 16, 0,
+                                     FU_AUX_SC1);
+  *reinterpret_cast<int4*>(rh + PER * tid) = int4{0, 0, 0, 0};
+  *reinterpret_cast<int4*>(rh + PER * tid + 4) = int4{0, 0, 0, 0};
   uint32_t key[2];
   fu_my_keys(lds, key);
   if (tid == 0) scr[8] = -1;
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  {
+    const int w = tid >> 4, q = tid & 15;  // list w's entries q, q + 16, ...
+    const uint32_t* lw = hls + FU_HSTAGE * w;
+    const int n = (int)lw[0];
+    uint32_t v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = lw[1 + q + 16 * i];  // within the staged 256 words
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (q + 16 * i < n) atomicAdd(&rh[v[i] >> 16], (int)(v[i] & 0xFFFFu));
+    for (int e = q + 128; e < n; e += 16) {
+      const uint32_t x = e + 1 < FU_HSTAGE ? lw[1 + e] : ld_sc1(hlg + (size_t)w * FU_HROW + 1 + e);
+      atomicAdd(&rh[x >> 16], (int)(x & 0xFFFFu));
+    }
+  }
+  __syncthreads();
+  int hb[PER];
+  *reinterpret_cast<int4*>(hb) = *reinterpret_cast<const int4*>(rh + PER * tid);
+  *reinterpret_cast<int4*>(hb + 4) = *reinterpret_cast<const int4*>(rh + PER * tid + 4);
   int c0, above0;
   const int nvis = fu_find_bin<PER>(hb, a.keep, scr, &c0, &above0);
   if (nvis <= a.keep) c0 = -1;  // every selectable key is selected
-  int na = 0, nc = 0;
+  bool sure[2], cand[2];
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
     const int bin = (int)(key[e] >> 20);
-    na += key[e] != 0u && bin > c0;
-    nc += key[e] != 0u && bin == c0;
+    sure[e] = key[e] != 0u && bin > c0;
+    cand[e] = key[e] != 0u && bin == c0;
+  }
+  // the bitmap of the positions above c0: wave v's ballots cover positions 64 v .. + 63 and 512 + 64 v .. + 63
+  uint32_t* blk = a.cand + ((size_t)b * FU_NW + j) * FU_CROW;
+  const uint64_t bm0 = __ballot(sure[0]), bm1 = __ballot(sure[1]);
+  if (lane == 0) {
+    *reinterpret_cast<uint64_t*>(blk + 1 + 2 * wave) = bm0;
+    *reinterpret_cast<uint64_t*>(blk + 1 + FU_BMW / 2 + 2 * wave) = bm1;
   }
   __syncthreads();  // every thread has read scr (the bin search) before it is rewritten
+  // (keys above c0) << 20 | (candidates in the first half) << 10 | (candidates in the second half): the candidates
+  // in position order are the first half's by thread, then the second half's
   uint32_t tot;
-  const uint32_t before = fu_block_prefix(((uint32_t)na << 16) | (uint32_t)nc, scr, &tot);
-  uint32_t* crow = a.cand + ((size_t)b * FU_NW + j) * FU_CROW + 1;
-  int o = (int)(before & 0xFFFFu);
-#pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    if (key[e] != 0u && (int)(key[e] >> 20) == c0) {
-      crow[o] = ((key[e] & 0xFFFFFu) << 10) | (uint32_t)(2 * tid + e);
-      ++o;
-    }
-  }
+  const uint32_t before = fu_block_prefix(((uint32_t)(sure[0] + sure[1]) << 20) | ((uint32_t)cand[0] << 10) |
+                                              (uint32_t)cand[1],
+                                          scr, &tot);
+  const int n0 = (int)((tot >> 10) & 1023u), n1 = (int)(tot & 1023u);
+  uint32_t* crow = blk + 1 + FU_BMW;
+  if (cand[0]) crow[(before >> 10) & 1023u] = ((key[0] & 0xFFFFFu) << 10) | (uint32_t)tid;
+  if (cand[1]) crow[n0 + (int)(before & 1023u)] = ((key[1] & 0xFFFFFu) << 10) | (uint32_t)(tid + FU_THREADS);
   if (tid == 0) {
-    crow[-1] = tot;
+    blk[0] = ((tot >> 20) << 16) | (uint32_t)(n0 + n1);
     st.c0 = c0;
     st.above0 = above0;
     st.nvis = nvis;
   }
 }
 
-// Stage 3: the exact threshold T, the ties to take, every workgroup's contribution and output offset, and this
-// workgroup's selected positions (idx) and their cache slots (rows) written at its offset.
-__device__ __forceinline__ void fu_select(const FusedArgs& a, uint8_t* lds, int b, int j) {
+// Stage 3: the exact selection and this workgroup's split of it. Every workgroup reads the first 128 words of every
+// candidate block (the counts, the bitmap of the positions above c0, the first 95 candidates) and finds T (the
+// keep-th largest key), the ties at T to take and each workgroup's output offset; the candidates taken join the
+// bitmaps, whose prefix popcounts give every selected position its output index, so the workgroup lists the slots of
+// its split's outputs [o0, o1) itself (and writes their indices): no further hand-off between workgroups. Returns the
+// split's selected count; its cache slots are in LDS at L_P.
+template <int QPT>
+__device__ __forceinline__ int fu_select(const FusedArgs& a, uint8_t* lds, int b, int j, int L, u32x4 (&qv)[QPT],
+                                         float* live_bias) {
   FuState& st = *reinterpret_cast<FuState*>(lds + L_STATE);
   int* scr = reinterpret_cast<int*>(lds + L_MISC);
   int* bins = reinterpret_cast<int*>(lds + L_BINS);
   int* bins2 = reinterpret_cast<int*>(lds + L_BINS2);
-  const int* tpg = reinterpret_cast<const int*>(lds + L_TPG);
-  const int tid = threadIdx.x, lane = tid & (WAVE - 1);
+  int* spg = reinterpret_cast<int*>(lds + L_SPG);
+  const uint32_t* cb = reinterpret_cast<const uint32_t*>(lds + L_CB);
+  uint32_t* sb = reinterpret_cast<uint32_t*>(lds + L_SB);
+  int* pb = reinterpret_cast<int*>(lds + L_PB);
+  int* slot_l = reinterpret_cast<int*>(lds + L_P);
+  const int tid = threadIdx.x, wave = tid / WAVE, lane = tid & (WAVE - 1);
   const int c0 = st.c0;
-  // thread (w, q) = (tid / 16, tid % 16) holds words 8 q .. 8 q + 7 of workgroup w's candidate block (one round of
-  // L2 loads for the whole row: word 0 the counts, then up to 127 candidates; a block with more keeps the rest in
-  // the L2, read by the block's 16 threads in each pass)
-  const int w = tid >> 4, q = tid & 15;
-  const uint32_t* blk = a.cand + ((size_t)b * FU_NW + w) * FU_CROW;
-  uint32_t cw[8];
+  const int hg = j % a.HG, s = j / a.HG;
+  const bool active = s < a.S;  // workgroup-uniform: a workgroup past the last split only helps with the barriers
+  const int o0 = active ? s * a.sps : 0, o1 = active ? min(o0 + a.sps, a.keep) : 0;
+  const uint32_t* cblk = a.cand + (size_t)b * FU_NW * FU_CROW;
+  // the staged words of every block straight into LDS (load i: blocks 2 i, 2 i + 1; lane l words 4 (l % 32) .. + 3
+  // of block 2 i + l / 32)
+  for (int i = wave; i < FU_NW / 2; i += FU_WAVES)
+    __builtin_amdgcn_global_load_lds(cblk + (size_t)(2 * i + (lane >> 5)) * FU_CROW + 4 * (lane & 31),
+                                     (__attribute__((address_space(3))) void*)(cb + 2 * FU_CSTAGE * i), 16, 0,
+                                     FU_AUX_SC1);
+  // the attention's 16 heads' queries: their QPT loads go out after the block loads (kept in that order) and are
+  // used after the selection
+  __builtin_amdgcn_sched_barrier(0);
+  if (active) {
+    const u32x4* qsrc = reinterpret_cast<const u32x4*>(a.q + ((size_t)b * a.H + FU_HPW * hg) * FU_DQK);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint64_t v = ld_sc1_64(blk + 8 * q + 2 * i);
-    cw[2 * i] = (uint32_t)v;
-    cw[2 * i + 1] = (uint32_t)(v >> 32);
+    for (int i = 0; i < QPT; ++i) qv[i] = qsrc[min(tid + FU_THREADS * i, FU_HPW * FU_DQK / 8 - 1)];
   }
-  for (int i = tid; i < 2048; i += FU_THREADS) bins[i] = 0;
-  bins2[tid] = 0;
+  for (int i = tid; i < 4096; i += FU_THREADS) bins[i] = 0;
+  if (tid < 256) bins2[tid] = 0;
+  if (tid < FU_SPLIT) slot_l[tid] = 0;  // padding rows read slot 0
   if (tid == 0) scr[8] = -1;
-  const uint32_t counts = (uint32_t)__shfl((int)cw[0], lane & ~15, WAVE);
-  const int nc = (int)(counts & 0xFFFFu);
-  if (q == 0) st.na[w] = (int)(counts >> 16);
-  // candidate e of the block (word 1 + e) is live when e < nc
-  auto each = [&](auto&& f) __attribute__((always_inline)) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int e = 8 * q + i - 1;
-      if (e >= 0 && e < nc) f(cw[i]);
-    }
-    for (int e = FU_CSTAGE - 1 + q; e < nc; e += 16) f(ld_sc1(blk + 1 + e));
-  };
+  __builtin_amdgcn_sched_barrier(0);
+  if (active)
+    __builtin_amdgcn_s_waitcnt(vmcnt_wait(QPT));  // the block loads (the queries may still be out)
+  else
+    __builtin_amdgcn_s_waitcnt(vmcnt_wait(0));
   __syncthreads();
+  // thread (w, q) = (tid / 16, tid % 16): block w's bitmap words 2 q, 2 q + 1 and its candidates q, q + 16, ...
+  const int w = tid >> 4, q = tid & 15;
+  const uint32_t* cw = cb + FU_CSTAGE * w;
+  const int nc = (int)(cw[0] & 0xFFFFu);
+  sb[FU_BMW * w + 2 * q] = cw[1 + 2 * q];
+  sb[FU_BMW * w + 2 * q + 1] = cw[2 + 2 * q];
+  auto cand_at = [&](int e) __attribute__((always_inline)) {
+    return e < FU_CSTAGED ? cw[1 + FU_BMW + e] : ld_sc1(cblk + (size_t)w * FU_CROW + 1 + FU_BMW + e);
+  };
+  const uint32_t cq = q < nc ? cw[1 + FU_BMW + q] : 0u;  // this thread's first candidate (most blocks have <= 16)
+  // lane w of every wave: block w's counts; the sources the split can draw on whatever T turns out to be (block w's
+  // outputs lie in [sum of na before it, sum of na + nc up to it)), whose pages load while T is found
+  const int ww = lane & (FU_NW - 1);
+  const uint32_t cnw = cb[FU_CSTAGE * ww];
+  const int nav = lane < FU_NW ? (int)(cnw >> 16) : 0, ncv = lane < FU_NW ? (int)(cnw & 0xFFFFu) : 0;
+  const int lo = wave_incl_scan(nav) - nav, hi = wave_incl_scan(nav + ncv);
+  const uint64_t mc = __ballot(lane < FU_NW && lo < o1 && hi > o0 && FU_KEYS * lane < L);
+  const int wa0 = mc ? (int)__builtin_ctzll(mc) : 0, nsrc0 = mc ? 64 - (int)__builtin_clzll(mc) - wa0 : 0;
+  const int pg0 = (FU_KEYS * wa0) >> a.page_shift;
+  {
+    const int npg = (FU_KEYS * nsrc0) >> a.page_shift;
+    const int* trow = a.table + (size_t)b * a.max_pages;
+    for (int c = wave; WAVE * c < npg; c += FU_WAVES) {
+      const int i = WAVE * c + lane;
+      if (i < npg)
+        __builtin_amdgcn_global_load_lds(trow + min(pg0 + i, a.max_pages - 1),
+                                         (__attribute__((address_space(3))) void*)(spg + WAVE * c), 4, 0, 0);
+    }
+  }
   uint32_t T = 0u;
   int room = 0;
   int gt = 0, eq = 0;
   if (c0 >= 0) {
-    each([&](uint32_t v) __attribute__((always_inline)) { atomicAdd(&bins[(v >> 19) & 2047], 1); });
+    // the candidates' low 20 key bits: 12 then 8
+    if (q < nc) atomicAdd(&bins[(cq >> 18) & 4095], 1);
+    for (int e = q + 16; e < nc; e += 16) atomicAdd(&bins[(cand_at(e) >> 18) & 4095], 1);
     __syncthreads();
-    constexpr int P1 = 2048 / FU_THREADS;
+    constexpr int P1 = 4096 / FU_THREADS;
     int hb[P1];
-#pragma unroll
-    for (int i = 0; i < P1; ++i) hb[i] = bins[P1 * tid + i];
+    *reinterpret_cast<int4*>(hb) = *reinterpret_cast<const int4*>(bins + P1 * tid);
+    *reinterpret_cast<int4*>(hb + 4) = *reinterpret_cast<const int4*>(bins + P1 * tid + 4);
     int c1, above1;
     int need = a.keep - st.above0;
     fu_find_bin<P1>(hb, need, scr, &c1, &above1);
     need -= above1;
-    __syncthreads();
-    if (tid == 0) scr[8] = -1;
-    each([&](uint32_t v) __attribute__((always_inline)) {
-      if (((v >> 19) & 2047) == (uint32_t)c1) atomicAdd(&bins2[(v >> 10) & 511], 1);
-    });
-    __syncthreads();
-    const int hb2[1] = {bins2[tid]};
-    int c2, above2;
-    fu_find_bin<1>(hb2, need, scr, &c2, &above2);
-    const uint32_t tlow = ((uint32_t)c1 << 9) | (uint32_t)c2;
-    room = max(need - above2, 0);
+    uint32_t tlow;
+    if (need >= bins[c1]) {
+      // every key of bin c1 is taken: T is the bin's lowest key, and all its ties
+      tlow = (uint32_t)c1 << 8;
+      room = need;
+    } else {
+      __syncthreads();
+      if (tid == 0) scr[8] = -1;
+      if (q < nc && ((cq >> 18) & 4095) == (uint32_t)c1) atomicAdd(&bins2[(cq >> 10) & 255], 1);
+      for (int e = q + 16; e < nc; e += 16) {
+        const uint32_t v = cand_at(e);
+        if (((v >> 18) & 4095) == (uint32_t)c1) atomicAdd(&bins2[(v >> 10) & 255], 1);
+      }
+      __syncthreads();
+      const int hb2[1] = {tid < 256 ? bins2[tid] : 0};
+      int c2, above2;
+      fu_find_bin<1>(hb2, need, scr, &c2, &above2);
+      tlow = ((uint32_t)c1 << 8) | (uint32_t)c2;
+      room = max(need - above2, 0);
+    }
     T = ((uint32_t)c0 << 20) | tlow;
-    // per workgroup: its candidates above T and equal to T, summed over the block's 16 threads
-    each([&](uint32_t v) __attribute__((always_inline)) {
+    // per workgroup: its candidates above T (which join its bitmap now) and equal to T, summed over the block's 16
+    // threads
+    for (int e = q; e < nc; e += 16) {
+      const uint32_t v = e == q ? cq : cand_at(e);
       gt += (v >> 10) > tlow;
       eq += (v >> 10) == tlow;
-    });
+      if ((v >> 10) > tlow) atomicOr(&sb[FU_BMW * w + ((v & 1023u) >> 5)], 1u << (v & 31u));
+    }
 #pragma unroll
     for (int m = 1; m < 16; m <<= 1) {
       gt += __shfl_xor(gt, m, WAVE);
@@ -476,51 +585,105 @@ __device__ __forceinline__ void fu_select(const FusedArgs& a, uint8_t* lds, int 
     st.eq[w] = eq;
   }
   __syncthreads();
-  // every wave: the ties at T before this workgroup and its first output index (lane w < 32 for workgroup w: ties
-  // are taken while fewer than `room` come before, so workgroup w selects na + gt + its ties taken)
-  const int ww = lane & (FU_NW - 1);
+  // every wave: per workgroup w (lane w) the ties at T before it, its selected count and first output index (ties
+  // are taken while fewer than `room` come before, so w selects na + gt + its ties taken)
   const int eqw = lane < FU_NW ? st.eq[ww] : 0;
   const int tbw = wave_incl_scan(eqw) - eqw;
-  const int selw = lane < FU_NW ? st.na[ww] + st.gt[ww] + min(max(room - tbw, 0), eqw) : 0;
+  const int selw = lane < FU_NW ? nav + st.gt[ww] + min(max(room - tbw, 0), eqw) : 0;
   const int offw = wave_incl_scan(selw) - selw;
-  const int TB = __shfl(tbw, j, WAVE), base = __shfl(offw, j, WAVE);
   const int cnt_row = min(st.nvis, a.keep);
-  // this workgroup's selections, in position order: keys above T, and ties at T while fewer than `room` ties of the
-  // row come before them; output index base + (selected keys before it in the workgroup)
-  uint32_t key[2];
-  fu_my_keys(lds, key);
-  uint32_t na = 0, nt = 0;
+  // the ties at T taken join their block's bitmap: ties are taken while fewer than `room` ties of the row come
+  // before, so a block takes all its ties, none, or (the one block where the room runs out) the first room - TB in
+  // candidate order, which is position order (counted across its 16 threads)
+  if (c0 >= 0) {
+    const uint32_t tlow = T & 0xFFFFFu;
+    const int TB = __shfl(tbw, w, WAVE), EQ = __shfl(eqw, w, WAVE);
+    if (EQ > 0 && TB < room) {  // uniform over the block's 16 threads
+      int ties = 0;  // the block's ties in the rounds before
+      for (int e0 = 0; e0 < nc; e0 += 16) {
+        const int e = e0 + q;
+        const uint32_t v = e < nc ? (e0 == 0 ? cq : cand_at(e)) : 0u;
+        const bool tie = e < nc && (v >> 10) == tlow;
+        int incl = tie;
+        if (TB + EQ > room) {  // the boundary block: its ties' ranks
 #pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    na += key[e] > T;
-    nt += T != 0u && key[e] == T;
-  }
-  uint32_t tot;
-  const uint32_t bef = fu_block_prefix((na << 16) | nt, scr + 16, &tot);
-  int a_before = (int)(bef >> 16), t_before = (int)(bef & 0xFFFFu);
-  const int tb_taken = min(TB, room);
-  int* irow = a.idx + (size_t)b * a.keep;
-  int* rrow = a.rows + (size_t)b * a.keep;
-#pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    const bool above = key[e] > T;
-    const bool tie = T != 0u && key[e] == T;
-    const int o = base + a_before + (min(TB + t_before, room) - tb_taken);
-    if ((above || (tie && TB + t_before < room)) && (unsigned)o < (unsigned)a.keep) {
-      const int lp = 2 * tid + e;
-      const int p = j * FU_KEYS + lp;
-      irow[o] = p;
-      rrow[o] = tpg[lp / FU_TILE] * a.page_size + (p & (a.page_size - 1));
+          for (int m = 1; m < 16; m <<= 1) {
+            const int y = __shfl_up(incl, m, 16);
+            incl += q >= m ? y : 0;
+          }
+        }
+        if (tie && TB + ties + incl - 1 < room) atomicOr(&sb[FU_BMW * w + ((v & 1023u) >> 5)], 1u << (v & 31u));
+        ties += __shfl(incl, (lane & ~15) + 15, WAVE);
+      }
     }
-    a_before += above;
-    t_before += tie;
   }
-  // the outputs past the count (their slots: position 0's), and the count
-  for (int o = cnt_row + j * FU_THREADS + tid; o < a.keep; o += FU_NW * FU_THREADS) {
-    irow[o] = 0;
-    rrow[o] = safe_page(a.table[(size_t)b * a.max_pages], a.num_pages) * a.page_size;
+  __syncthreads();
+  // exclusive prefix popcounts of each block's selected bitmap (thread (w, q): words 2 q, 2 q + 1)
+  {
+    const int c_a = __builtin_popcount(sb[FU_BMW * w + 2 * q]), c_b = __builtin_popcount(sb[FU_BMW * w + 2 * q + 1]);
+    int incl = c_a + c_b;
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) {
+      const int y = __shfl_up(incl, m, 16);
+      incl += q >= m ? y : 0;
+    }
+    pb[FU_BMW * w + 2 * q] = incl - c_a - c_b;
+    pb[FU_BMW * w + 2 * q + 1] = incl - c_b;
   }
+  // the queries into LDS for stage 4, head pc / 72, elements 8 (pc % 72) .. of piece pc (before the index stores
+  // below: a wait for the queries' loads there would also wait for those stores)
+  if (active) {
+    uint16_t* qs = reinterpret_cast<uint16_t*>(lds + L_QST);
+#pragma unroll
+    for (int i = 0; i < QPT; ++i) {
+      const int pc = tid + FU_THREADS * i;
+      if (pc < FU_HPW * FU_DQK / 8)
+        *reinterpret_cast<u32x4*>(qs + (pc / (FU_DQK / 8)) * FU_AQROW + 8 * (pc % (FU_DQK / 8))) = qv[i];
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's page loads have landed
+  __syncthreads();
+  // the split's sources exactly: the workgroups whose outputs meet [o0, o1); each thread takes a byte of their
+  // bitmaps (at most 8 selected positions, so a dense selection costs no more than a sparse one) and lists each
+  // selected position whose output falls in the split
+  int* irow = a.idx + (size_t)b * a.keep;
+  const uint64_t ms = __ballot(lane < FU_NW && selw > 0 && offw < o1 && offw + selw > o0);
+  if (ms) {
+    const int wa = (int)__builtin_ctzll(ms), nbytes = 4 * FU_BMW * (64 - (int)__builtin_clzll(ms) - wa);
+    for (int k = tid; k < nbytes; k += FU_THREADS) {
+      const int sw = wa + k / (4 * FU_BMW), i = (k / 4) % FU_BMW, by = 8 * (k & 3);
+      const uint32_t word = sb[FU_BMW * sw + i];
+      uint32_t bits = (word >> by) & 255u;
+      int o = __shfl(offw, sw, WAVE) + pb[FU_BMW * sw + i] + __builtin_popcount(word & ((1u << by) - 1u));
+      // the word's 32 positions lie in one page (pages of at least 32 tokens)
+      const int p0 = FU_KEYS * sw + 32 * i;
+      const int sbase =
+          safe_page(spg[(p0 >> a.page_shift) - pg0], a.num_pages) * a.page_size + (p0 & (a.page_size - 1)) + by;
+      while (bits) {
+        const int bit = __builtin_ctz(bits);
+        bits &= bits - 1u;
+        if (o >= o0 && o < o1) {
+          slot_l[o - o0] = sbase + bit;
+          if (hg == 0) irow[o] = p0 + by + bit;
+        }
+        ++o;
+      }
+    }
+  }
+  // the outputs past the count, and the count
+  if (hg == 0)
+    for (int o = max(o0, cnt_row) + tid; o < o1; o += FU_THREADS) irow[o] = 0;
   if (j == 0 && tid == 0) a.cnt[b] = cnt_row;
+  // the split's live slots; a row with none attends position 0 masked (its lse is NEG_INF)
+  int n_slots = max(min(o1, cnt_row) - o0, 0);
+  *live_bias = 0.0f;
+  if (active && cnt_row == 0 && s == 0) {
+    n_slots = 1;
+    *live_bias = NEG_INF;
+    if (tid == 0) slot_l[0] = safe_page(a.table[(size_t)b * a.max_pages], a.num_pages) * a.page_size;
+  }
+  __syncthreads();  // the slot list
+  return n_slots;
 }
 
 // The value operand of v_mfma_f32_16x16x32_bf16 from the token-major tile (ds_read_b64_tr_b8: lane (a, c) of each
@@ -534,30 +697,21 @@ __device__ __forceinline__ bf16x8 fu_value_operand(const uint8_t* kt, int ks, in
   return fp8x8_to_bf16x8((uint32_t)r.x, (uint32_t)r.y);
 }
 
-// Stage 4: the split's attention.
-__device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int b, int j) {
-  const FuState& st = *reinterpret_cast<const FuState*>(lds + L_STATE);
+// Stage 4: the split's attention over the n_slots slots of the list at L_P, with the queries staged in stage 3.
+__device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int b, int j, int n_slots,
+                                          float live_bias) {
   float* ksc_l = reinterpret_cast<float*>(lds + L_KSC);
   float* bias_l = reinterpret_cast<float*>(lds + L_BIAS);
   float* red = reinterpret_cast<float*>(lds + L_RED);
   float* sred = reinterpret_cast<float*>(lds + L_SRED);
   uint16_t* pl = reinterpret_cast<uint16_t*>(lds + L_P);
   uint8_t* kt = lds + L_KT;
-  uint16_t* qs = reinterpret_cast<uint16_t*>(lds + L_AQ);
+  const uint16_t* qs = reinterpret_cast<const uint16_t*>(lds + L_QST);
   const int tid = threadIdx.x, wave = tid / WAVE, lane = tid & (WAVE - 1);
   const int l16 = lane & 15, q4 = lane >> 4;
   const int hg = j % a.HG, s = j / a.HG;
   if (s >= a.S) return;  // workgroup-uniform
   const int H = a.H;
-  const int cnt_row = min(st.nvis, a.keep);
-  const int o0 = s * a.sps, o1 = min(o0 + a.sps, a.keep);
-  // the split's live slots; a row with none attends position 0 masked (its lse is NEG_INF)
-  int n_slots = max(min(o1, cnt_row) - o0, 0);
-  float live_bias = 0.0f;
-  if (cnt_row == 0 && s == 0) {
-    n_slots = 1;
-    live_bias = NEG_INF;
-  }
   float* part = a.part + ((size_t)b * a.S + s) * H * FU_DV;
   float2* mlp = a.ml + ((size_t)b * a.S + s) * H;
   if (n_slots == 0) {  // an empty split: weight 0 in the combine
@@ -568,27 +722,9 @@ __device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int 
   }
   const int padded = (n_slots + FU_CH - 1) / FU_CH * FU_CH;
 
-  // one round of loads: the 16 heads' queries, the split's slots (row r = tid % 256; a padding row reads slot 0's)
-  constexpr int QP = FU_HPW * FU_DQK / 8;  // 1152 pieces of 16 bytes
-  constexpr int QPT = (QP + FU_THREADS - 1) / FU_THREADS;
-  const u32x4* qsrc = reinterpret_cast<const u32x4*>(a.q + ((size_t)b * H + FU_HPW * hg) * FU_DQK);
-  u32x4 qv[QPT];
-#pragma unroll
-  for (int i = 0; i < QPT; ++i) qv[i] = qsrc[min(tid + FU_THREADS * i, QP - 1)];
-  int* slot_l = reinterpret_cast<int*>(lds + L_P);
-  const int* rsrc = a.rows + (size_t)b * a.keep + o0;
-  int slot = 0;
-  if (tid < FU_SPLIT) {
-    slot = ld_sc1(rsrc + (tid < n_slots ? tid : 0));
-    slot = (unsigned)slot < (unsigned)a.num_slots ? slot : 0;
-    slot_l[tid] = slot;
-  }
-#pragma unroll
-  for (int i = 0; i < QPT; ++i) {
-    const int pc = tid + FU_THREADS * i;  // head pc / 72, elements 8 (pc % 72) ..
-    if (pc < QP) *reinterpret_cast<u32x4*>(qs + (pc / (FU_DQK / 8)) * FU_AQROW + 8 * (pc % (FU_DQK / 8))) = qv[i];
-  }
-  __syncthreads();
+  // the slot list (a padding row reads slot 0) and the queries (staged in LDS by stage 3)
+  const int* slot_l = reinterpret_cast<const int*>(lds + L_P);
+  const int slot = tid < FU_SPLIT ? slot_l[tid] : 0;
   // the query operand: head l16, dims 64 (st / 2) + 16 q4 + 8 (st % 2) .. + 7 at score step st (the key operand's
   // dim order below)
   bf16x8 qb[FU_STEPS];
@@ -763,13 +899,12 @@ __global__ __launch_bounds__(FU_THREADS, 1) void decode_fused_kernel(FusedArgs a
   fu_barrier(sync, 1);  // A: the row's scores and histogram
   fu_classify(a, lds, b, j);
   fu_barrier(sync, 2);  // B: every workgroup's counts and candidates
-  // the row histogram is read: this workgroup's slice back to zero for the next call
-  int* grow = a.hist + (size_t)b * FU_HBINS + j * (FU_HBINS / FU_NW);
-  if (threadIdx.x < FU_HBINS / FU_NW) grow[threadIdx.x] = 0;
-  fu_select(a, lds, b, j);
-  fu_barrier(sync, 3);  // C: the row's selection and slots
-  fu_attend(a, lds, b, j);
-  fu_barrier(sync, 4);  // D: every split's output
+  constexpr int QPT = (FU_HPW * FU_DQK / 8 + FU_THREADS - 1) / FU_THREADS;
+  u32x4 qv[QPT];
+  float live_bias;
+  const int n_slots = fu_select(a, lds, b, j, L, qv, &live_bias);
+  fu_attend(a, lds, b, j, n_slots, live_bias);
+  fu_barrier(sync, 3);  // C: every split's output
   fu_combine(a, b, j);
   // the last workgroup of the XCD to finish resets its barrier words (no workgroup polls them any more)
   __builtin_amdgcn_s_waitcnt(0);
@@ -788,17 +923,17 @@ __global__ __launch_bounds__(FU_THREADS, 1) void decode_fused_kernel(FusedArgs a
 
 static size_t fu_up256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// Workspace of the fused layer past the zero region (histograms + barrier words): the per-workgroup candidate blocks,
-// the selected slots, the split outputs and their (max, sum).
+// Workspace of the fused layer past the zero region (histograms + barrier words; the fused layer uses only the barrier
+// words): the per-workgroup bin lists and candidate blocks, the split outputs and their (max, sum).
 struct FusedLayout {
-  size_t cand, rows, part, ml, end;
+  size_t hl, cand, part, ml, end;
 };
 
 static FusedLayout fused_layout(size_t zero_bytes, int B, int H, int S, int keep) {
   FusedLayout l;
-  l.cand = zero_bytes;
-  l.rows = l.cand + fu_up256((size_t)B * FU_NW * FU_CROW * 4);
-  l.part = l.rows + fu_up256((size_t)B * keep * 4);
+  l.hl = zero_bytes;
+  l.cand = l.hl + fu_up256((size_t)B * FU_NW * FU_HROW * 4);
+  l.part = l.cand + fu_up256((size_t)B * FU_NW * FU_CROW * 4);
   l.ml = l.part + fu_up256((size_t)B * S * H * FU_DV * 4);
   l.end = l.ml + fu_up256((size_t)B * S * H * sizeof(float2));
   return l;
@@ -845,10 +980,9 @@ hipError_t launch_decode_fused(const uint16_t* q_idx, const float* w, const uint
   a.cnt = cnt;
   a.out = out;
   a.lse = lse;
-  a.hist = reinterpret_cast<int*>(p);
+  a.hl = reinterpret_cast<uint32_t*>(p + l.hl);
   a.sync = reinterpret_cast<int*>(p + hist_bytes);
   a.cand = reinterpret_cast<uint32_t*>(p + l.cand);
-  a.rows = reinterpret_cast<int*>(p + l.rows);
   a.part = reinterpret_cast<float*>(p + l.part);
   a.ml = reinterpret_cast<float2*>(p + l.ml);
   a.B = B;
