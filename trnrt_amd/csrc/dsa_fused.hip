@@ -39,7 +39,7 @@ constexpr int FU_THREADS = 512;  // 8 waves: two per SIMD, so one's memory waits
 constexpr int FU_WAVES = FU_THREADS / WAVE;
 constexpr int FU_TILE = 32;                           // keys per MFMA tile
 constexpr int FU_TPW = 4;                             // tiles per wave
-constexpr int FU_AHEAD = 3;                           // key tiles in flight ahead of the one a wave computes
+constexpr int FU_AHEAD = 2;                           // key tiles in flight ahead of the one a wave computes
 constexpr int FU_KEYS = FU_WAVES * FU_TPW * FU_TILE;  // 1024 keys per workgroup
 constexpr int FU_MAXLEN = FU_NW * FU_KEYS;            // 32,768
 constexpr int FU_D = 128;                             // indexer head dim
@@ -55,9 +55,9 @@ constexpr int FU_CROW = 1088;
 constexpr int FU_CSTAGE = 128;                      // words of each block every workgroup reads into LDS
 constexpr int FU_CSTAGED = FU_CSTAGE - 1 - FU_BMW;  // candidates among them (the rest: read from the L2)
 static_assert(FU_CROW >= 1 + FU_BMW + FU_KEYS && FU_CROW % 4 == 0, "candidate block");
-constexpr int FU_HPW = 16;         // heads per attention workgroup
+constexpr int FU_HPW = 16;         // heads per MFMA block of the attention
 constexpr int FU_CH = 64;          // slot granularity of a split
-constexpr int FU_SPLIT = 256;      // at most 256 slots per split
+constexpr int FU_SPLIT = 256;      // slots per split, at most
 constexpr int FU_DQK = 576, FU_DV = 512;
 constexpr int FU_PIECES = FU_DQK / 16;  // 36 16-byte pieces per row
 constexpr int FU_KPIECES = FU_PIECES + 1;  // a staged row: the data and one padding piece (592 bytes), the stride at
@@ -65,7 +65,6 @@ constexpr int FU_KPIECES = FU_PIECES + 1;  // a staged row: the data and one pad
 constexpr int FU_KROW = 16 * FU_KPIECES;
 constexpr int FU_STEPS = FU_DQK / 32;   // score steps
 constexpr int FU_AQROW = FU_DQK + 8;    // staged attention query row (bf16)
-constexpr int FU_PROW = FU_SPLIT + 8;   // P row stride (bf16)
 constexpr unsigned FU_SPIN = 1u << 20;  // polls before a wait gives up (a normal wait takes a few)
 constexpr int FU_SYNC_WORDS = 16;       // per XCD: arrivals, exits, error flag
 
@@ -79,28 +78,43 @@ constexpr int L_CB = 16384;      // stage 3: the first 128 words of every candid
 constexpr int L_SB = 32768;      // stage 3: per workgroup the bitmap of its selected positions [32][32]
 constexpr int L_PB = 36864;      // stage 3: their exclusive prefix popcounts [32][32]
 constexpr int L_BINS = 40960;    // stage 3: 4096 bins
-constexpr int L_QST = 57344;     // stage 3: the attention's 16 heads' queries [16][584] bf16
 constexpr int L_QS = 32768;      // stage 1: indexer queries [64][136] bf16
 constexpr int L_WS = 50176;      // stage 1: head weights [64]
 constexpr int L_HS = 50432;      // stage 1: histogram [4096]
 constexpr int L_TPG = 159616;    // stages 1-3: the page of each of the workgroup's 32 tiles
 constexpr int L_SCS = 159744;    // stages 1-3: the workgroup's 1024 scores
 constexpr int L_KT = 0;          // stage 4: the rows, token-major at the 592-byte stride
-constexpr int L_P = 151552;      // stage 4: P [16][264] bf16; before it (stages 3-4) the split's slot list [256]
-constexpr int L_KSC = 160000;    // stage 4: kv scales [256]
-constexpr int L_BIAS = 161024;   // stage 4: biases [256]
-constexpr int L_RED = 162048;    // stage 4: per-wave head maxima [8][16]
-constexpr int L_SRED = 162560;   // stage 4: per-wave head sums [8][16]
 constexpr int FU_LDS = 163840;
 static_assert(L_HS + 4 * FU_HBINS <= L_TPG && L_TPG + 4 * 32 == L_SCS, "stage 1 layout");
 static_assert(L_HLS + 4 * FU_NW * FU_HSTAGE <= L_HS, "stage 2 layout");
-static_assert(L_BINS2 + 4 * 256 <= L_SPG && L_BINS + 4 * 4096 <= L_QST, "stage 3 layout");
+static_assert(L_BINS2 + 4 * 256 <= L_SPG && L_BINS + 4 * 4096 <= 57344, "stage 3 layout");
 static_assert(L_SPG + 4 * 1024 <= L_CB && L_CB + 4 * FU_NW * FU_CSTAGE <= L_SB && L_SB + 4 * FU_NW * FU_BMW <= L_PB &&
-                  L_PB + 4 * FU_NW * FU_BMW <= L_P,
+                  L_PB + 4 * FU_NW * FU_BMW <= L_BINS,
               "stage 3 blocks");
-static_assert(L_QST + 2 * FU_HPW * FU_AQROW <= L_P, "query staging");
-static_assert(L_P == FU_SPLIT * FU_KROW && L_P + 2 * FU_HPW * FU_PROW <= L_KSC, "stage 4 layout");
-static_assert(L_SRED + 4 * FU_WAVES * FU_HPW <= FU_LDS && L_SCS + 4 * FU_KEYS == FU_LDS, "LDS size");
+static_assert(L_SCS + 4 * FU_KEYS == FU_LDS, "LDS size");
+
+// The attention's shape: HPW heads per workgroup (16 or 32) over splits of up to 4096 / HPW slots, its 8 waves as
+// TG groups of 32 tokens x HB blocks of 16 heads in the scores; its LDS past the gathered rows: the split's slot list
+// (stages 3-4, later P [HPW][SPLIT + 8] bf16), kv scales and biases [SPLIT], per-wave head maxima and sums [HPW][TG],
+// and (stage 3, read before the gather) the HPW heads' queries [HPW][584] bf16.
+template <int HPW>
+struct FuAtt {
+  static constexpr int SPLIT = 4096 / HPW;
+  static constexpr int HB = HPW / 16;
+  static constexpr int TG = SPLIT / 32;
+  static constexpr int PROW = SPLIT + 8;
+  static constexpr int QPT = (HPW * FU_DQK / 8 + FU_THREADS - 1) / FU_THREADS;  // query loads per thread
+  static constexpr int L_P = SPLIT * FU_KROW;
+  static constexpr int L_KSC = L_P + 2 * HPW * PROW;
+  static constexpr int L_BIAS = L_KSC + 4 * SPLIT;
+  static constexpr int L_RED = L_BIAS + 4 * SPLIT;
+  static constexpr int L_SRED = L_RED + 4 * TG * HPW;
+  static constexpr int L_END = L_SRED + 4 * TG * HPW;
+  static constexpr int L_QST = HPW == 16 ? 57344 : L_END;  // inside the row tile (read before the gather), or past it
+};
+static_assert(FuAtt<16>::TG * FuAtt<16>::HB == FU_WAVES && FuAtt<32>::TG * FuAtt<32>::HB == FU_WAVES, "waves");
+static_assert(FuAtt<16>::L_END <= FU_LDS && FuAtt<16>::L_QST + 2 * 16 * FU_AQROW <= FuAtt<16>::L_P, "stage 4, 16");
+static_assert(FuAtt<32>::L_QST + 2 * 32 * FU_AQROW <= L_TPG && FuAtt<32>::L_P >= 57344, "stage 4, 32");
 
 struct FuState {
   int gt[FU_NW];  // per workgroup: its candidates above T
@@ -129,7 +143,7 @@ struct FusedArgs {
   uint32_t* cand;  // [B][32][1088]: per workgroup (keys above c0) << 16 | (candidates), the bitmap of its positions
                    // above c0 (32 words), then the candidates, (low 20 key bits << 10) | position in the workgroup's
                    // range, in position order
-  float* part;     // [B][S][H][512]: split outputs (normalised)
+  uint16_t* part;  // [B][S][H][512]: split outputs (normalised, bf16)
   float2* ml;      // [B][S][H]: split max and sum
   int B, Hi, H, max_pages, page_size, page_shift, num_pages, stride, keep;
   int num_slots;  // num_pages * page_size
@@ -457,10 +471,12 @@ __device__ __forceinline__ void fu_classify(const FusedArgs& a, uint8_t* lds, in
 // keep-th largest key), the ties at T to take and each workgroup's output offset; the candidates taken join the
 // bitmaps, whose prefix popcounts give every selected position its output index, so the workgroup lists the slots of
 // its split's outputs [o0, o1) itself (and writes their indices): no further hand-off between workgroups. Returns the
-// split's selected count; its cache slots are in LDS at L_P.
-template <int QPT>
-__device__ __forceinline__ int fu_select(const FusedArgs& a, uint8_t* lds, int b, int j, int L, u32x4 (&qv)[QPT],
-                                         float* live_bias) {
+// split's selected count; its cache slots are in LDS at FuAtt<HPW>::L_P.
+template <int HPW>
+__device__ __forceinline__ int fu_select(const FusedArgs& a, uint8_t* lds, int b, int j, int L,
+                                         u32x4 (&qv)[FuAtt<HPW>::QPT], float* live_bias) {
+  using AT = FuAtt<HPW>;
+  constexpr int QPT = AT::QPT;
   FuState& st = *reinterpret_cast<FuState*>(lds + L_STATE);
   int* scr = reinterpret_cast<int*>(lds + L_MISC);
   int* bins = reinterpret_cast<int*>(lds + L_BINS);
@@ -469,7 +485,7 @@ __device__ __forceinline__ int fu_select(const FusedArgs& a, uint8_t* lds, int b
   const uint32_t* cb = reinterpret_cast<const uint32_t*>(lds + L_CB);
   uint32_t* sb = reinterpret_cast<uint32_t*>(lds + L_SB);
   int* pb = reinterpret_cast<int*>(lds + L_PB);
-  int* slot_l = reinterpret_cast<int*>(lds + L_P);
+  int* slot_l = reinterpret_cast<int*>(lds + AT::L_P);
   const int tid = threadIdx.x, wave = tid / WAVE, lane = tid & (WAVE - 1);
   const int c0 = st.c0;
   const int hg = j % a.HG, s = j / a.HG;
@@ -482,17 +498,17 @@ __device__ __forceinline__ int fu_select(const FusedArgs& a, uint8_t* lds, int b
     __builtin_amdgcn_global_load_lds(cblk + (size_t)(2 * i + (lane >> 5)) * FU_CROW + 4 * (lane & 31),
                                      (__attribute__((address_space(3))) void*)(cb + 2 * FU_CSTAGE * i), 16, 0,
                                      FU_AUX_SC1);
-  // the attention's 16 heads' queries: their QPT loads go out after the block loads (kept in that order) and are
+  // the attention's HPW heads' queries: their QPT loads go out after the block loads (kept in that order) and are
   // used after the selection
   __builtin_amdgcn_sched_barrier(0);
   if (active) {
-    const u32x4* qsrc = reinterpret_cast<const u32x4*>(a.q + ((size_t)b * a.H + FU_HPW * hg) * FU_DQK);
+    const u32x4* qsrc = reinterpret_cast<const u32x4*>(a.q + ((size_t)b * a.H + HPW * hg) * FU_DQK);
 #pragma unroll
-    for (int i = 0; i < QPT; ++i) qv[i] = qsrc[min(tid + FU_THREADS * i, FU_HPW * FU_DQK / 8 - 1)];
+    for (int i = 0; i < QPT; ++i) qv[i] = qsrc[min(tid + FU_THREADS * i, HPW * FU_DQK / 8 - 1)];
   }
   for (int i = tid; i < 4096; i += FU_THREADS) bins[i] = 0;
   if (tid < 256) bins2[tid] = 0;
-  if (tid < FU_SPLIT) slot_l[tid] = 0;  // padding rows read slot 0
+  if (tid < AT::SPLIT) slot_l[tid] = 0;  // padding rows read slot 0
   if (tid == 0) scr[8] = -1;
   __builtin_amdgcn_sched_barrier(0);
   if (active)
@@ -633,11 +649,11 @@ __device__ __forceinline__ int fu_select(const FusedArgs& a, uint8_t* lds, int b
   // the queries into LDS for stage 4, head pc / 72, elements 8 (pc % 72) .. of piece pc (before the index stores
   // below: a wait for the queries' loads there would also wait for those stores)
   if (active) {
-    uint16_t* qs = reinterpret_cast<uint16_t*>(lds + L_QST);
+    uint16_t* qs = reinterpret_cast<uint16_t*>(lds + AT::L_QST);
 #pragma unroll
     for (int i = 0; i < QPT; ++i) {
       const int pc = tid + FU_THREADS * i;
-      if (pc < FU_HPW * FU_DQK / 8)
+      if (pc < HPW * FU_DQK / 8)
         *reinterpret_cast<u32x4*>(qs + (pc / (FU_DQK / 8)) * FU_AQROW + 8 * (pc % (FU_DQK / 8))) = qv[i];
     }
   }
@@ -697,39 +713,43 @@ __device__ __forceinline__ bf16x8 fu_value_operand(const uint8_t* kt, int ks, in
   return fp8x8_to_bf16x8((uint32_t)r.x, (uint32_t)r.y);
 }
 
-// Stage 4: the split's attention over the n_slots slots of the list at L_P, with the queries staged in stage 3.
+// Stage 4: the split's attention over the n_slots slots of the list at FuAtt<HPW>::L_P, with the queries staged in
+// stage 3.
+template <int HPW>
 __device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int b, int j, int n_slots,
                                           float live_bias) {
-  float* ksc_l = reinterpret_cast<float*>(lds + L_KSC);
-  float* bias_l = reinterpret_cast<float*>(lds + L_BIAS);
-  float* red = reinterpret_cast<float*>(lds + L_RED);
-  float* sred = reinterpret_cast<float*>(lds + L_SRED);
-  uint16_t* pl = reinterpret_cast<uint16_t*>(lds + L_P);
+  using AT = FuAtt<HPW>;
+  constexpr int HB = AT::HB, TG = AT::TG, PROW = AT::PROW;
+  float* ksc_l = reinterpret_cast<float*>(lds + AT::L_KSC);
+  float* bias_l = reinterpret_cast<float*>(lds + AT::L_BIAS);
+  float* red = reinterpret_cast<float*>(lds + AT::L_RED);
+  float* sred = reinterpret_cast<float*>(lds + AT::L_SRED);
+  uint16_t* pl = reinterpret_cast<uint16_t*>(lds + AT::L_P);
   uint8_t* kt = lds + L_KT;
-  const uint16_t* qs = reinterpret_cast<const uint16_t*>(lds + L_QST);
+  const uint16_t* qs = reinterpret_cast<const uint16_t*>(lds + AT::L_QST);
   const int tid = threadIdx.x, wave = tid / WAVE, lane = tid & (WAVE - 1);
   const int l16 = lane & 15, q4 = lane >> 4;
+  const int hb = wave % HB, tg = wave / HB;  // the scores: this wave's 16-head block and 32-token group
   const int hg = j % a.HG, s = j / a.HG;
   if (s >= a.S) return;  // workgroup-uniform
   const int H = a.H;
-  float* part = a.part + ((size_t)b * a.S + s) * H * FU_DV;
-  float2* mlp = a.ml + ((size_t)b * a.S + s) * H;
+  uint16_t* part = a.part + (((size_t)b * a.S + s) * H + HPW * hg) * FU_DV;
+  float2* mlp = a.ml + ((size_t)b * a.S + s) * H + HPW * hg;
   if (n_slots == 0) {  // an empty split: weight 0 in the combine
-    for (int i = tid; i < FU_HPW * FU_DV / 4; i += FU_THREADS)
-      reinterpret_cast<float4*>(part + (size_t)FU_HPW * hg * FU_DV)[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (tid < FU_HPW) mlp[FU_HPW * hg + tid] = make_float2(-INFINITY, 0.0f);
+    for (int i = tid; i < HPW * FU_DV / 8; i += FU_THREADS) reinterpret_cast<uint4*>(part)[i] = uint4{0u, 0u, 0u, 0u};
+    if (tid < HPW) mlp[tid] = make_float2(-INFINITY, 0.0f);
     return;
   }
   const int padded = (n_slots + FU_CH - 1) / FU_CH * FU_CH;
 
   // the slot list (a padding row reads slot 0) and the queries (staged in LDS by stage 3)
-  const int* slot_l = reinterpret_cast<const int*>(lds + L_P);
-  const int slot = tid < FU_SPLIT ? slot_l[tid] : 0;
-  // the query operand: head l16, dims 64 (st / 2) + 16 q4 + 8 (st % 2) .. + 7 at score step st (the key operand's
-  // dim order below)
+  const int* slot_l = reinterpret_cast<const int*>(lds + AT::L_P);
+  const int slot = tid < AT::SPLIT ? slot_l[tid] : 0;
+  // the query operand: head 16 hb + l16, dims 64 (st / 2) + 16 q4 + 8 (st % 2) .. + 7 at score step st (the key
+  // operand's dim order below)
   bf16x8 qb[FU_STEPS];
   {
-    const uint16_t* qh = qs + l16 * FU_AQROW + 16 * q4;
+    const uint16_t* qh = qs + (16 * hb + l16) * FU_AQROW + 16 * q4;
 #pragma unroll
     for (int st2 = 0; st2 < FU_STEPS; ++st2)
       qb[st2] = as_bf16x8(*reinterpret_cast<const uint4*>(qh + 64 * (st2 >> 1) + 8 * (st2 & 1)));
@@ -755,17 +775,17 @@ __device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int 
   }
   __syncthreads();  // every row in LDS
 
-  // scores of tokens 32 wave .. + 31 (two blocks of 16), all 16 heads: S^T = K . Q^T; lane group q4 reads piece
-  // 4 j + q4 (dims 64 j + 16 q4 ..) of its token per pair of steps (one ds_read_b128 for two MFMAs; 8 rows at one
-  // column cover the 32 banks once at the 592-byte stride)
-  const bool has = 32 * wave < padded;
+  // scores of tokens 32 tg .. + 31 (two blocks of 16) for heads 16 hb .. + 15: S^T = K . Q^T; lane group q4 reads
+  // piece 4 j + q4 (dims 64 j + 16 q4 ..) of its token per pair of steps (one ds_read_b128 for two MFMAs; 8 rows at
+  // one column cover the banks once at the 592-byte stride)
+  const bool has = 32 * tg < padded;
   float sv[2][4];
   float mx = -INFINITY;
   if (has) {
     f32x4 acc[2][2];
 #pragma unroll
     for (int k = 0; k < 2; ++k) acc[k][0] = acc[k][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const uint8_t* kr = kt + (32 * wave + l16) * FU_KROW + 16 * q4;
+    const uint8_t* kr = kt + (32 * tg + l16) * FU_KROW + 16 * q4;
 #pragma unroll
     for (int st2 = 0; st2 < FU_STEPS; st2 += 2) {
 #pragma unroll
@@ -776,10 +796,10 @@ __device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int 
                                                             0);
       }
     }
-    // acc[k][.][r] = S^T[token 32 wave + 16 k + 4 q4 + r][head l16]
+    // acc[k][.][r] = S^T[token 32 tg + 16 k + 4 q4 + r][head 16 hb + l16]
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
-      const int tk = 32 * wave + 16 * k + 4 * q4;
+      const int tk = 32 * tg + 16 * k + 4 * q4;
       const float4 ks4 = *reinterpret_cast<const float4*>(&ksc_l[tk]);
       const float4 bs4 = *reinterpret_cast<const float4*>(&bias_l[tk]);
       sv[k][0] = (acc[k][0][0] + acc[k][1][0]) * (ks4.x * a.scale) + bs4.x;
@@ -792,16 +812,22 @@ __device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int 
   }
   mx = max_nonan(mx, __shfl_xor(mx, 16, WAVE));
   mx = max_nonan(mx, __shfl_xor(mx, 32, WAVE));
-  if (lane < FU_HPW) red[wave * FU_HPW + lane] = mx;
+  if (lane < 16) red[(16 * hb + lane) * TG + tg] = mx;
   __syncthreads();
   float m = -INFINITY;
+  {
+    float r[TG];  // head 16 hb + l16's maxima over the token groups, in one or two vector reads
 #pragma unroll
-  for (int w = 0; w < FU_WAVES; ++w) m = max_nonan(m, red[w * FU_HPW + l16]);
+    for (int t = 0; t < TG; t += 4)
+      *reinterpret_cast<float4*>(r + t) = *reinterpret_cast<const float4*>(&red[(16 * hb + l16) * TG + t]);
+#pragma unroll
+    for (int t = 0; t < TG; ++t) m = max_nonan(m, r[t]);
+  }
   float psum = 0.0f;
   if (has) {
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
-      const int tk = 32 * wave + 16 * k + 4 * q4;
+      const int tk = 32 * tg + 16 * k + 4 * q4;
       const float4 ks4 = *reinterpret_cast<const float4*>(&ksc_l[tk]);
       float p[4];
 #pragma unroll
@@ -810,72 +836,114 @@ __device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int 
         psum += p[i];
       }
       // the value's dequantisation folded into the bf16 weight
-      *reinterpret_cast<uint2*>(&pl[l16 * FU_PROW + tk]) =
+      *reinterpret_cast<uint2*>(&pl[(16 * hb + l16) * PROW + tk]) =
           make_uint2(bf16_pack(p[0] * ks4.x, p[1] * ks4.y), bf16_pack(p[2] * ks4.z, p[3] * ks4.w));
     }
   }
   psum += __shfl_xor(psum, 16, WAVE);
   psum += __shfl_xor(psum, 32, WAVE);
-  if (lane < FU_HPW) sred[wave * FU_HPW + lane] = psum;
+  if (lane < 16) sred[(16 * hb + lane) * TG + tg] = psum;
   __syncthreads();  // P and the sums
 
-  // O[head][dims 64 wave ..] += P . V over the split's tokens
-  f32x4 o[4];
+  // O[heads][dims 64 wave ..] += P . V over the split's tokens, the value operand shared by the HB head blocks
+  f32x4 o[HB][4];
 #pragma unroll
-  for (int n = 0; n < 4; ++n) o[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int h = 0; h < HB; ++h)
+#pragma unroll
+    for (int n = 0; n < 4; ++n) o[h][n] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int nks = padded / 32;
   for (int ks = 0; ks < nks; ++ks) {
-    const bf16x8 pop = as_bf16x8(*reinterpret_cast<const uint4*>(&pl[l16 * FU_PROW + 32 * ks + 8 * q4]));
+    bf16x8 pop[HB];
 #pragma unroll
-    for (int n = 0; n < 4; ++n)
-      o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pop, fu_value_operand(kt, ks, 4 * wave + n, lane), o[n], 0, 0, 0);
-  }
-  // the split's normalised output, max and sum (heads 4 q4 + i)
+    for (int h = 0; h < HB; ++h)
+      pop[h] = as_bf16x8(*reinterpret_cast<const uint4*>(&pl[(16 * h + l16) * PROW + 32 * ks + 8 * q4]));
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int hl = 4 * q4 + i;
-    float l = 0.0f, mh = -INFINITY;
+    for (int n = 0; n < 4; ++n) {
+      const bf16x8 vop = fu_value_operand(kt, ks, 4 * wave + n, lane);
 #pragma unroll
-    for (int w = 0; w < FU_WAVES; ++w) {
-      l += sred[w * FU_HPW + hl];
-      mh = max_nonan(mh, red[w * FU_HPW + hl]);
+      for (int h = 0; h < HB; ++h) o[h][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pop[h], vop, o[h][n], 0, 0, 0);
     }
-    const float inv = 1.0f / l;
-    float* ph = part + (size_t)(FU_HPW * hg + hl) * FU_DV + 64 * wave + l16;
+  }
+  // the split's normalised output (bf16), max and sum: lane (l16, q4) holds heads 16 h + 4 q4 + i at dim
+  // 64 wave + 16 n + l16; neighbouring lanes swap halves so that an even lane stores heads i = 0, 1 and an odd lane
+  // heads i = 2, 3, each as a pair of dims
+  const bool odd = l16 & 1;
 #pragma unroll
-    for (int n = 0; n < 4; ++n) ph[16 * n] = o[n][i] * inv;
-    if (wave == 0 && l16 == 0) mlp[FU_HPW * hg + hl] = make_float2(mh, l);
+  for (int h = 0; h < HB; ++h) {
+    float inv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int hl = 16 * h + 4 * q4 + i;
+      float r[TG], mr[TG];
+#pragma unroll
+      for (int t = 0; t < TG; t += 4) {
+        *reinterpret_cast<float4*>(r + t) = *reinterpret_cast<const float4*>(&sred[hl * TG + t]);
+        *reinterpret_cast<float4*>(mr + t) = *reinterpret_cast<const float4*>(&red[hl * TG + t]);
+      }
+      float l = 0.0f, mh = -INFINITY;
+#pragma unroll
+      for (int t = 0; t < TG; ++t) {
+        l += r[t];
+        mh = max_nonan(mh, mr[t]);
+      }
+      inv[i] = 1.0f / l;
+      if (wave == 0 && l16 == 0) mlp[hl] = make_float2(mh, l);
+    }
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      float v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = o[h][n][i] * inv[i];
+      const float u0 = __shfl_xor(odd ? v[0] : v[2], 1, WAVE), u1 = __shfl_xor(odd ? v[1] : v[3], 1, WAVE);
+      const int hl = 16 * h + 4 * q4 + (odd ? 2 : 0);
+      uint16_t* ph = part + (size_t)hl * FU_DV + 64 * wave + 16 * n + (l16 & ~1);
+      *reinterpret_cast<uint32_t*>(ph) = odd ? bf16_pack(u0, v[2]) : bf16_pack(v[0], u0);
+      *reinterpret_cast<uint32_t*>(ph + FU_DV) = odd ? bf16_pack(u1, v[3]) : bf16_pack(v[1], u1);
+    }
   }
 }
 
 // Stage 5: the splits merged by log-sum-exp, o = sum_s W_s o_s / sum_s W_s with W_s = l_s exp(m_s - M) and
 // lse = M + log sum_s W_s; item g of 16384 (head g / 256, dims 2 (g % 256) ..) on thread g % 512 of workgroup g / 512,
-// then g + 16384, ...; the splits' loads in groups of 8 (one memory round per group).
+// then g + 16384, ...; the splits' loads in groups of 16 (one memory round per group).
 __device__ __forceinline__ void fu_combine(const FusedArgs& a, int b, int j) {
   const int S = a.S, H = a.H;
   for (int g = j * FU_THREADS + (int)threadIdx.x; g < H * (FU_DV / 2); g += FU_NW * FU_THREADS) {
     const int h = g >> 8, d = 2 * (g & 255);
     float M = -INFINITY, W = 0.0f, x0 = 0.0f, x1 = 0.0f;
-    for (int s0 = 0; s0 < S; s0 += 8) {
-      uint64_t mlv[8], ov[8];
+    for (int s0 = 0; s0 < S; s0 += 16) {
+      uint64_t mlv[16];
+      uint32_t ov[16];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
+      for (int k = 0; k < 16; ++k) {
         const size_t i = ((size_t)b * S + min(s0 + k, S - 1)) * H + h;
         mlv[k] = ld_sc1_64(a.ml + i);
-        ov[k] = ld_sc1_64(a.part + i * FU_DV + d);
+        ov[k] = ld_sc1(reinterpret_cast<const uint32_t*>(a.part + i * FU_DV + d));
       }
+      // the group's maximum, then its splits' weights against it (independent terms), then the group against the
+      // running maximum
+      float Mg = -INFINITY;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
+      for (int k = 0; k < 16; ++k) {
+        const float ls = __uint_as_float((uint32_t)(mlv[k] >> 32));
+        if (s0 + k < S && ls > 0.0f) Mg = max_nonan(Mg, __uint_as_float((uint32_t)mlv[k]));
+      }
+      float Wg = 0.0f, g0 = 0.0f, g1 = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
         const float ms = __uint_as_float((uint32_t)mlv[k]), ls = __uint_as_float((uint32_t)(mlv[k] >> 32));
-        if (s0 + k < S && ls > 0.0f) {
-          // a running rescale: the group's splits against the maximum so far
-          const float Mn = max_nonan(M, ms);
-          const float f = __expf(M - Mn), wt = ls * __expf(ms - Mn);
-          W = W * f + wt;
-          x0 = x0 * f + wt * __uint_as_float((uint32_t)ov[k]);
-          x1 = x1 * f + wt * __uint_as_float((uint32_t)(ov[k] >> 32));
-          M = Mn;
-        }
+        const float wt = s0 + k < S && ls > 0.0f ? ls * __expf(ms - Mg) : 0.0f;
+        Wg += wt;
+        g0 += wt * __uint_as_float(ov[k] << 16);
+        g1 += wt * __uint_as_float(ov[k] & 0xFFFF0000u);
+      }
+      if (Wg > 0.0f) {
+        const float Mn = max_nonan(M, Mg);
+        const float f = __expf(M - Mn), fg = __expf(Mg - Mn);
+        W = W * f + Wg * fg;
+        x0 = x0 * f + g0 * fg;
+        x1 = x1 * f + g1 * fg;
+        M = Mn;
       }
     }
     const float inv = 1.0f / W;
@@ -885,7 +953,7 @@ __device__ __forceinline__ void fu_combine(const FusedArgs& a, int b, int j) {
   }
 }
 
-template <int MT>
+template <int MT, int HPW>
 __global__ __launch_bounds__(FU_THREADS, 1) void decode_fused_kernel(FusedArgs a) {
   __shared__ __align__(16) uint8_t lds[FU_LDS];
   const int x = blockIdx.x % FU_XCDS, j = blockIdx.x / FU_XCDS;
@@ -899,11 +967,10 @@ __global__ __launch_bounds__(FU_THREADS, 1) void decode_fused_kernel(FusedArgs a
   fu_barrier(sync, 1);  // A: the row's scores and histogram
   fu_classify(a, lds, b, j);
   fu_barrier(sync, 2);  // B: every workgroup's counts and candidates
-  constexpr int QPT = (FU_HPW * FU_DQK / 8 + FU_THREADS - 1) / FU_THREADS;
-  u32x4 qv[QPT];
+  u32x4 qv[FuAtt<HPW>::QPT];
   float live_bias;
-  const int n_slots = fu_select(a, lds, b, j, L, qv, &live_bias);
-  fu_attend(a, lds, b, j, n_slots, live_bias);
+  const int n_slots = fu_select<HPW>(a, lds, b, j, L, qv, &live_bias);
+  fu_attend<HPW>(a, lds, b, j, n_slots, live_bias);
   fu_barrier(sync, 3);  // C: every split's output
   fu_combine(a, b, j);
   // the last workgroup of the XCD to finish resets its barrier words (no workgroup polls them any more)
@@ -934,27 +1001,35 @@ static FusedLayout fused_layout(size_t zero_bytes, int B, int H, int S, int keep
   l.hl = zero_bytes;
   l.cand = l.hl + fu_up256((size_t)B * FU_NW * FU_HROW * 4);
   l.part = l.cand + fu_up256((size_t)B * FU_NW * FU_CROW * 4);
-  l.ml = l.part + fu_up256((size_t)B * S * H * FU_DV * 4);
+  l.ml = l.part + fu_up256((size_t)B * S * H * FU_DV * 2);
   l.end = l.ml + fu_up256((size_t)B * S * H * sizeof(float2));
   return l;
 }
 
-static int fused_splits(int H) { return FU_NW / (H / FU_HPW); }
+// The attention's heads per workgroup: 32 when the splits of 128 slots hold keep, else 16 (splits of 256); 0: no
+// fused layer for these head counts.
+static int fused_hpw(int H, int keep) {
+  if (H >= 32 && H % 32 == 0 && H / 32 <= FU_NW && (long)(FU_NW / (H / 32)) * FuAtt<32>::SPLIT >= keep) return 32;
+  if (H >= 16 && H % 16 == 0 && H / 16 <= FU_NW && (long)(FU_NW / (H / 16)) * FuAtt<16>::SPLIT >= keep) return 16;
+  return 0;
+}
+
+static int fused_splits(int H, int hpw) { return FU_NW / (H / hpw); }
 
 // Whether the fused layer takes a step: a GPU of 8 XCDs x 32 CUs, rows of at most 32,768 tokens (score rows of a
 // multiple of 4 floats), up to 64 indexer heads, query heads in 16s (at most 512), pages of a power-of-two size of at
-// least 32 tokens, and a keep that the splits hold (256 slots each).
+// least 32 tokens, and a keep that the splits hold (128 slots each at 32 heads per workgroup, 256 at 16).
 bool fused_layer_ok(int num_cu, int Hi, int H, int max_len, int keep, int page_size, int stride) {
   if (num_cu != FU_XCDS * FU_NW) return false;
-  if (Hi < 1 || Hi > 64 || H < FU_HPW || H % FU_HPW || H / FU_HPW > FU_NW) return false;
-  if (max_len < 1 || max_len > FU_MAXLEN || stride < 1 || stride % 4 || keep < 1) return false;
-  if (page_size < 32 || (page_size & (page_size - 1))) return false;
-  return (long)fused_splits(H) * FU_SPLIT >= keep;
+  if (Hi < 1 || Hi > 64 || keep < 1 || !fused_hpw(H, keep)) return false;
+  if (max_len < 1 || max_len > FU_MAXLEN || stride < 1 || stride % 4) return false;
+  return page_size >= 32 && !(page_size & (page_size - 1));
 }
 
 size_t fused_layer_bytes(size_t zero_bytes, int B, int H, int keep) {
-  if (H < FU_HPW || H % FU_HPW || H / FU_HPW > FU_NW) return 0;
-  return fused_layout(zero_bytes, B, H, fused_splits(H), keep).end;
+  const int hpw = keep >= 1 ? fused_hpw(H, keep) : 0;
+  if (!hpw) return 0;
+  return fused_layout(zero_bytes, B, H, fused_splits(H, hpw), keep).end;
 }
 
 hipError_t launch_decode_fused(const uint16_t* q_idx, const float* w, const uint8_t* k, const float* ks,
@@ -963,7 +1038,9 @@ hipError_t launch_decode_fused(const uint16_t* q_idx, const float* w, const uint
                                void* ws, size_t hist_bytes, size_t zero_bytes, int B, int Hi, int H, int max_pages,
                                int page_size, int num_pages, int stride, int keep, float scale, hipStream_t s) {
   FusedArgs a;
-  const int S = fused_splits(H);
+  const int hpw = fused_hpw(H, keep);
+  if (!hpw) return hipErrorInvalidValue;
+  const int S = fused_splits(H, hpw);
   const FusedLayout l = fused_layout(zero_bytes, B, H, S, keep);
   char* p = static_cast<char*>(ws);
   a.q_idx = q_idx;
@@ -983,7 +1060,7 @@ hipError_t launch_decode_fused(const uint16_t* q_idx, const float* w, const uint
   a.hl = reinterpret_cast<uint32_t*>(p + l.hl);
   a.sync = reinterpret_cast<int*>(p + hist_bytes);
   a.cand = reinterpret_cast<uint32_t*>(p + l.cand);
-  a.part = reinterpret_cast<float*>(p + l.part);
+  a.part = reinterpret_cast<uint16_t*>(p + l.part);
   a.ml = reinterpret_cast<float2*>(p + l.ml);
   a.B = B;
   a.Hi = Hi;
@@ -996,15 +1073,18 @@ hipError_t launch_decode_fused(const uint16_t* q_idx, const float* w, const uint
   a.stride = stride;
   a.keep = keep;
   a.scale = scale;
-  a.HG = H / FU_HPW;
+  a.HG = H / hpw;
   a.S = S;
   int sps = (keep + S - 1) / S;
   a.sps = (sps + FU_CH - 1) / FU_CH * FU_CH;
   const dim3 grid(FU_XCDS * FU_NW), block(FU_THREADS);
   for (int r0 = 0; r0 < B; r0 += FU_XCDS) {
     a.row0 = r0;
-    const hipError_t e = Hi <= 32 ? launch("decode_fused_kernel", decode_fused_kernel<1>, grid, block, s, a)
-                                  : launch("decode_fused_kernel", decode_fused_kernel<2>, grid, block, s, a);
+    const hipError_t e =
+        Hi <= 32 ? (hpw == 32 ? launch("decode_fused_kernel", decode_fused_kernel<1, 32>, grid, block, s, a)
+                              : launch("decode_fused_kernel", decode_fused_kernel<1, 16>, grid, block, s, a))
+                 : (hpw == 32 ? launch("decode_fused_kernel", decode_fused_kernel<2, 32>, grid, block, s, a)
+                              : launch("decode_fused_kernel", decode_fused_kernel<2, 16>, grid, block, s, a));
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
