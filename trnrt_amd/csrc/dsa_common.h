@@ -157,6 +157,44 @@ __device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {
 
 __device__ __forceinline__ int wave_incl_scan(int v) { return (int)wave_incl_scan_u32((uint32_t)v); }
 
+// Inclusive prefix sum within each row of 16 lanes (the first four steps of the wave scan).
+__device__ __forceinline__ int row_incl_scan(int x) {
+  x += dpp<0x111>(x);
+  x += dpp<0x112>(x);
+  x += dpp<0x114>(x);
+  x += dpp<0x118>(x);
+  return x;
+}
+
+// The sum over each row of 16 lanes, in every lane of the row (quad swaps, then half-row and row mirrors).
+__device__ __forceinline__ int row_sum(int v) {
+  v += dpp<0xb1>(v);
+  v += dpp<0x4e>(v);
+  v += dpp<0x141>(v);
+  v += dpp<0x140>(v);
+  return v;
+}
+
+// The maximum over each row of 16 lanes, in every lane of the row.
+__device__ __forceinline__ float row_max(float v) {
+  v = fmaxf(v, __int_as_float(dpp<0xb1>(__float_as_int(v))));
+  v = fmaxf(v, __int_as_float(dpp<0x4e>(__float_as_int(v))));
+  v = fmaxf(v, __int_as_float(dpp<0x141>(__float_as_int(v))));
+  v = fmaxf(v, __int_as_float(dpp<0x140>(__float_as_int(v))));
+  return v;
+}
+
+__device__ __forceinline__ float row_sum(float v) {
+  v += __int_as_float(dpp<0xb1>(__float_as_int(v)));
+  v += __int_as_float(dpp<0x4e>(__float_as_int(v)));
+  v += __int_as_float(dpp<0x141>(__float_as_int(v)));
+  v += __int_as_float(dpp<0x140>(__float_as_int(v)));
+  return v;
+}
+
+// The value of the neighbouring lane (lane ^ 1), by a quad permutation.
+__device__ __forceinline__ float lane_xor1(float v) { return __int_as_float(dpp<0xb1>(__float_as_int(v))); }
+
 // Wave-wide sum, the same value in every lane (the last lane of the inclusive scan).
 __device__ __forceinline__ int wave_sum(int v) {
   return __builtin_amdgcn_readlane((int)wave_incl_scan_u32((uint32_t)v), WAVE - 1);

@@ -143,8 +143,9 @@ struct FusedArgs {
   uint32_t* cand;  // [B][32][1088]: per workgroup (keys above c0) << 16 | (candidates), the bitmap of its positions
                    // above c0 (32 words), then the candidates, (low 20 key bits << 10) | position in the workgroup's
                    // range, in position order
-  uint16_t* part;  // [B][S][H][512]: split outputs (normalised, bf16)
-  float2* ml;      // [B][S][H]: split max and sum
+  uint16_t* part;  // [B][H][S][512]: split outputs (normalised, bf16), a head's splits side by side
+
+  float2* ml;      // [B][H][S]: split max and sum
   int B, Hi, H, max_pages, page_size, page_shift, num_pages, stride, keep;
   int num_slots;  // num_pages * page_size
   float scale;
@@ -282,7 +283,7 @@ __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int
   float ksc[FU_TPW];
   auto tile_loads = [&](int i) __attribute__((always_inline)) {
     const int t0 = (t_begin + i) * FU_TILE;
-    const int page = __shfl(pages, i, WAVE);
+    const int page = __builtin_amdgcn_readlane(pages, i);
     const size_t slot = t0 < L ? (size_t)page * a.page_size + (t0 & (a.page_size - 1)) + jk : (size_t)jk;
     const uint8_t* kp = a.k + slot * FU_D + 64 * h;
 #pragma unroll
@@ -590,11 +591,8 @@ __device__ __forceinline__ int fu_select(const FusedArgs& a, uint8_t* lds, int b
       eq += (v >> 10) == tlow;
       if ((v >> 10) > tlow) atomicOr(&sb[FU_BMW * w + ((v & 1023u) >> 5)], 1u << (v & 31u));
     }
-#pragma unroll
-    for (int m = 1; m < 16; m <<= 1) {
-      gt += __shfl_xor(gt, m, WAVE);
-      eq += __shfl_xor(eq, m, WAVE);
-    }
+    gt = row_sum(gt);
+    eq = row_sum(eq);
   }
   if (q == 0) {
     st.gt[w] = gt;
@@ -620,16 +618,9 @@ __device__ __forceinline__ int fu_select(const FusedArgs& a, uint8_t* lds, int b
         const int e = e0 + q;
         const uint32_t v = e < nc ? (e0 == 0 ? cq : cand_at(e)) : 0u;
         const bool tie = e < nc && (v >> 10) == tlow;
-        int incl = tie;
-        if (TB + EQ > room) {  // the boundary block: its ties' ranks
-#pragma unroll
-          for (int m = 1; m < 16; m <<= 1) {
-            const int y = __shfl_up(incl, m, 16);
-            incl += q >= m ? y : 0;
-          }
-        }
+        const int incl = row_incl_scan(tie);  // the block's ties up to this one in the round
         if (tie && TB + ties + incl - 1 < room) atomicOr(&sb[FU_BMW * w + ((v & 1023u) >> 5)], 1u << (v & 31u));
-        ties += __shfl(incl, (lane & ~15) + 15, WAVE);
+        ties += row_sum(tie);
       }
     }
   }
@@ -637,12 +628,7 @@ __device__ __forceinline__ int fu_select(const FusedArgs& a, uint8_t* lds, int b
   // exclusive prefix popcounts of each block's selected bitmap (thread (w, q): words 2 q, 2 q + 1)
   {
     const int c_a = __builtin_popcount(sb[FU_BMW * w + 2 * q]), c_b = __builtin_popcount(sb[FU_BMW * w + 2 * q + 1]);
-    int incl = c_a + c_b;
-#pragma unroll
-    for (int m = 1; m < 16; m <<= 1) {
-      const int y = __shfl_up(incl, m, 16);
-      incl += q >= m ? y : 0;
-    }
+    const int incl = row_incl_scan(c_a + c_b);
     pb[FU_BMW * w + 2 * q] = incl - c_a - c_b;
     pb[FU_BMW * w + 2 * q + 1] = incl - c_b;
   }
@@ -733,11 +719,13 @@ __device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int 
   const int hg = j % a.HG, s = j / a.HG;
   if (s >= a.S) return;  // workgroup-uniform
   const int H = a.H;
-  uint16_t* part = a.part + (((size_t)b * a.S + s) * H + HPW * hg) * FU_DV;
-  float2* mlp = a.ml + ((size_t)b * a.S + s) * H + HPW * hg;
+  // head HPW hg + i's split output at part + i * S * 512, its (max, sum) at mlp[i * S]
+  uint16_t* part = a.part + (((size_t)b * H + HPW * hg) * a.S + s) * FU_DV;
+  float2* mlp = a.ml + ((size_t)b * H + HPW * hg) * a.S + s;
   if (n_slots == 0) {  // an empty split: weight 0 in the combine
-    for (int i = tid; i < HPW * FU_DV / 8; i += FU_THREADS) reinterpret_cast<uint4*>(part)[i] = uint4{0u, 0u, 0u, 0u};
-    if (tid < HPW) mlp[tid] = make_float2(-INFINITY, 0.0f);
+    for (int i = tid; i < HPW * FU_DV / 8; i += FU_THREADS)
+      reinterpret_cast<uint4*>(part + (size_t)(i / (FU_DV / 8)) * a.S * FU_DV)[i % (FU_DV / 8)] = uint4{0u, 0u, 0u, 0u};
+    if (tid < HPW) mlp[tid * a.S] = make_float2(-INFINITY, 0.0f);
     return;
   }
   const int padded = (n_slots + FU_CH - 1) / FU_CH * FU_CH;
@@ -887,69 +875,69 @@ __device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int 
         mh = max_nonan(mh, mr[t]);
       }
       inv[i] = 1.0f / l;
-      if (wave == 0 && l16 == 0) mlp[hl] = make_float2(mh, l);
+      if (wave == 0 && l16 == 0) mlp[hl * a.S] = make_float2(mh, l);
     }
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
       float v[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) v[i] = o[h][n][i] * inv[i];
-      const float u0 = __shfl_xor(odd ? v[0] : v[2], 1, WAVE), u1 = __shfl_xor(odd ? v[1] : v[3], 1, WAVE);
+      const float u0 = lane_xor1(odd ? v[0] : v[2]), u1 = lane_xor1(odd ? v[1] : v[3]);
       const int hl = 16 * h + 4 * q4 + (odd ? 2 : 0);
-      uint16_t* ph = part + (size_t)hl * FU_DV + 64 * wave + 16 * n + (l16 & ~1);
+      uint16_t* ph = part + (size_t)hl * a.S * FU_DV + 64 * wave + 16 * n + (l16 & ~1);
       *reinterpret_cast<uint32_t*>(ph) = odd ? bf16_pack(u0, v[2]) : bf16_pack(v[0], u0);
-      *reinterpret_cast<uint32_t*>(ph + FU_DV) = odd ? bf16_pack(u1, v[3]) : bf16_pack(v[1], u1);
+      *reinterpret_cast<uint32_t*>(ph + (size_t)a.S * FU_DV) = odd ? bf16_pack(u1, v[3]) : bf16_pack(v[1], u1);
     }
   }
 }
 
-// Stage 5: the splits merged by log-sum-exp, o = sum_s W_s o_s / sum_s W_s with W_s = l_s exp(m_s - M) and
-// lse = M + log sum_s W_s; item g of 16384 (head g / 256, dims 2 (g % 256) ..) on thread g % 512 of workgroup g / 512,
-// then g + 16384, ...; the splits' loads in groups of 16 (one memory round per group).
-__device__ __forceinline__ void fu_combine(const FusedArgs& a, int b, int j) {
-  const int S = a.S, H = a.H;
-  for (int g = j * FU_THREADS + (int)threadIdx.x; g < H * (FU_DV / 2); g += FU_NW * FU_THREADS) {
-    const int h = g >> 8, d = 2 * (g & 255);
-    float M = -INFINITY, W = 0.0f, x0 = 0.0f, x1 = 0.0f;
-    for (int s0 = 0; s0 < S; s0 += 16) {
-      uint64_t mlv[16];
-      uint32_t ov[16];
+// Stage 5: the splits merged by log-sum-exp, o = sum_s W_s o_s / sum_s W_s with W_s = l_s exp(m_s - M) over the
+// splits with l_s > 0 and lse = M + log sum_s W_s. Workgroup j takes heads 2 j, 2 j + 1 (then + 64, ...), thread t
+// head 2 j + t / 256, dims 2 (t % 256) ..: wave 0 loads the two heads' (max, sum) pairs (lane 32 h + s for head h,
+// split s), then every thread's NS split loads go out (unconditionally, a split past S re-reading the last one), wave
+// 0 turns the pairs into the weights W_s / sum W in LDS (0 past S), and each thread sums its weighted dims.
+template <int NS>
+__device__ __forceinline__ void fu_combine_heads(const FusedArgs& a, float* wts, int b, int h0) {
+  const int S = a.S, H = a.H, tid = threadIdx.x, lane = tid & (WAVE - 1);
+  const int h = h0 + (tid >> 8), d = 2 * (tid & 255);
+  const int hh = h0 + (lane >> 5), sp = lane & 31;
+  uint64_t mlv = 0;
+  if (tid < WAVE) mlv = ld_sc1_64(a.ml + ((size_t)b * H + hh) * S + min(sp, S - 1));
+  uint32_t ov[NS];
 #pragma unroll
-      for (int k = 0; k < 16; ++k) {
-        const size_t i = ((size_t)b * S + min(s0 + k, S - 1)) * H + h;
-        mlv[k] = ld_sc1_64(a.ml + i);
-        ov[k] = ld_sc1(reinterpret_cast<const uint32_t*>(a.part + i * FU_DV + d));
-      }
-      // the group's maximum, then its splits' weights against it (independent terms), then the group against the
-      // running maximum
-      float Mg = -INFINITY;
+  for (int k = 0; k < NS; ++k)
+    ov[k] = ld_sc1(reinterpret_cast<const uint32_t*>(a.part + (((size_t)b * H + h) * S + min(k, S - 1)) * FU_DV + d));
+  if (tid < WAVE) {
+    const float m = __uint_as_float((uint32_t)mlv), l = __uint_as_float((uint32_t)(mlv >> 32));
+    const bool live = sp < S && l > 0.0f;
+    float M = row_max(live ? m : -INFINITY);
+    M = fmaxf(M, __shfl_xor(M, 16, WAVE));  // the two rows of the head's 32 lanes
+    const float wt = live ? l * __expf(m - M) : 0.0f;
+    float W = row_sum(wt);
+    W += __shfl_xor(W, 16, WAVE);
+    wts[lane] = wt / W;
+    if (sp == 0 && a.lse) a.lse[(size_t)b * H + hh] = M + __logf(W);
+  }
+  __syncthreads();
+  float x0 = 0.0f, x1 = 0.0f;
+  const float* wh = wts + 32 * (tid >> 8);
 #pragma unroll
-      for (int k = 0; k < 16; ++k) {
-        const float ls = __uint_as_float((uint32_t)(mlv[k] >> 32));
-        if (s0 + k < S && ls > 0.0f) Mg = max_nonan(Mg, __uint_as_float((uint32_t)mlv[k]));
-      }
-      float Wg = 0.0f, g0 = 0.0f, g1 = 0.0f;
-#pragma unroll
-      for (int k = 0; k < 16; ++k) {
-        const float ms = __uint_as_float((uint32_t)mlv[k]), ls = __uint_as_float((uint32_t)(mlv[k] >> 32));
-        const float wt = s0 + k < S && ls > 0.0f ? ls * __expf(ms - Mg) : 0.0f;
-        Wg += wt;
-        g0 += wt * __uint_as_float(ov[k] << 16);
-        g1 += wt * __uint_as_float(ov[k] & 0xFFFF0000u);
-      }
-      if (Wg > 0.0f) {
-        const float Mn = max_nonan(M, Mg);
-        const float f = __expf(M - Mn), fg = __expf(Mg - Mn);
-        W = W * f + Wg * fg;
-        x0 = x0 * f + g0 * fg;
-        x1 = x1 * f + g1 * fg;
-        M = Mn;
-      }
-    }
-    const float inv = 1.0f / W;
-    const size_t oi = ((size_t)b * H + h) * FU_DV + d;
-    *reinterpret_cast<uint32_t*>(a.out + oi) = bf16_pack(x0 * inv, x1 * inv);
-    if (d == 0 && a.lse) a.lse[(size_t)b * H + h] = M + __logf(W);
+  for (int k = 0; k < NS; ++k) {
+    const float wk = wh[k];
+    x0 += wk * __uint_as_float(ov[k] << 16);
+    x1 += wk * __uint_as_float(ov[k] & 0xFFFF0000u);
+  }
+  *reinterpret_cast<uint32_t*>(a.out + ((size_t)b * H + h) * FU_DV + d) = bf16_pack(x0, x1);
+  __syncthreads();  // the weights are read before the next heads' overwrite them
+}
+
+__device__ __forceinline__ void fu_combine(const FusedArgs& a, uint8_t* lds, int b, int j) {
+  float* wts = reinterpret_cast<float*>(lds);  // [2][32]
+  for (int h0 = 2 * j; h0 < a.H; h0 += 2 * FU_NW) {
+    if (a.S <= 16)
+      fu_combine_heads<16>(a, wts, b, h0);
+    else
+      fu_combine_heads<32>(a, wts, b, h0);
   }
 }
 
@@ -972,7 +960,7 @@ __global__ __launch_bounds__(FU_THREADS, 1) void decode_fused_kernel(FusedArgs a
   const int n_slots = fu_select<HPW>(a, lds, b, j, L, qv, &live_bias);
   fu_attend<HPW>(a, lds, b, j, n_slots, live_bias);
   fu_barrier(sync, 3);  // C: every split's output
-  fu_combine(a, b, j);
+  fu_combine(a, lds, b, j);
   // the last workgroup of the XCD to finish resets its barrier words (no workgroup polls them any more)
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
