@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define DSA_ABI_VERSION 6
+#define DSA_ABI_VERSION 7
 
 #define DSA_OK 0
 #define DSA_EINVAL (-1)      /* a null pointer or a size out of range */
@@ -150,6 +150,30 @@ int dsa_sparse_mla_decode(const void* q_bf16, const uint8_t* kv_fp8, const float
                           void* out_bf16, float* out_f32, float* lse, void* workspace, size_t workspace_bytes, int B,
                           int H, int Dqk, int Dv, int keep, int max_pages, int page_size, int num_pages, float scale,
                           int splits, void* stream);
+
+/*
+ * Mask compaction (trnrt/models/dsa_long.py:140-166 `compact`): row n of sel fp32 [N, M] (an entry counts as a one
+ * when above 0.5) -> idx int64 [N, keep] the positions of its first keep ones, ascending, 0 past the count, and
+ * cnt int64 [N] = min(ones, keep). One workgroup per row; a row's walk stops once keep ones are placed.
+ */
+int dsa_compact_mask(const float* sel, int N, int M, int keep, int64_t* idx, int64_t* cnt, void* stream);
+
+/*
+ * Slot attention over each row's visible tokens compacted in a kernel (trnrt/kernels/dsa_slots_c.py:416-447
+ * `attend`, the arithmetic of dsa_sparse_mla_decode's row form): rows int32 [B, NS] pool rows of the cache viewed as
+ * [num_slots / kp, kp rows], bias fp32 [B, NS, kp] (0 / NEG_INF; a token is visible when its bias is above
+ * NEG_INF / 2). A compaction kernel lists each row's visible tokens (pool row kp + t, slot order); the attention then
+ * runs over that list only (its rows + count form). A row with no visible token attends pool row 0's kp tokens,
+ * all masked: their uniform mean, lse NEG_INF (the reference's compacted form fills empty entries with pool row 0).
+ * q bf16 [B, H, Dqk], kv_fp8 [num_slots, Dqk] e4m3 rows, kv_scale fp32 [num_slots], out_bf16 [B, H, 512] or NULL,
+ * out_f32 [B, H, 512] or NULL, lse fp32 [B, H] or NULL; workspace of dsa_slots_compact_workspace_bytes bytes (no
+ * zero-fill needed).
+ */
+size_t dsa_slots_compact_workspace_bytes(int B, int H, int NS, int kp, int splits);
+int dsa_sparse_mla_slots_compact(const void* q_bf16, const uint8_t* kv_fp8, const float* kv_scale,
+                                 const int32_t* rows, const float* bias, void* out_bf16, float* out_f32, float* lse,
+                                 void* workspace, size_t workspace_bytes, int B, int H, int Dqk, int NS, int kp,
+                                 long long num_slots, float scale, int splits, void* stream);
 
 /*
  * Token positions -> cache slots (trnrt/models/dsa_long.py:189-215 `slots` at kp = 1, no tail):

@@ -32,7 +32,12 @@ attention over 512-wide NoPE rows). Each function cites the reference lines it f
   must fail;
 - sparse_mla_ref: brute-force float64 loops, one selected token -> that row, all masked -> the uniform mean,
   lse == log-sum-exp, split-K combine == unsplit, slot-order invariance;
-- splitk_combine_ref: any partition of the slots combines to the unsplit result.
+- splitk_combine_ref: any partition of the slots combines to the unsplit result;
+- compact_ref: a brute-force Python loop over every position, the literal known answer of a small mask, equal to
+  ascending() when a row has at most keep ones, and a planted mistake (the count not clamped to keep) that must fail;
+- slots_compact_ref: equal to sparse_mla_slots_ref (the uncompacted form) on rows with a visible token (masked
+  tokens weigh exactly 0), the uniform mean of pool row 0's tokens on an empty row (closed form), invariant under a
+  permutation of the slots.
 Nothing here is "parity unpinned".
 """
 
@@ -238,6 +243,20 @@ def ascending(sel: torch.Tensor, keep: int) -> tuple[torch.Tensor, torch.Tensor]
     return idx, cnt
 
 
+def compact_ref(sel: torch.Tensor, keep: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """(indices [N, keep] int64 ascending, count [N] int64) of a 0 / 1 float mask [N, M] (an entry counts as a one
+    when above 0.5): the positions of each row's first keep ones, 0 past the count, count = min(ones, keep)
+    (trnrt/models/dsa_long.py:140-166 `compact`: the k-th one for k < count, the count clamped to [0, keep])."""
+    N, M = sel.shape
+    idx = torch.zeros(N, keep, dtype=torch.int64)
+    cnt = torch.zeros(N, dtype=torch.int64)
+    for n in range(N):
+        nz = (sel[n].float() > 0.5).nonzero().flatten()[:keep]
+        idx[n, : nz.numel()] = nz
+        cnt[n] = nz.numel()
+    return idx, cnt
+
+
 def topk_ref(scores: torch.Tensor, keep: int, lengths=None, vis_only: bool = True):
     """(idx [R, keep] int64 ascending, cnt [R]) of the exact selection (dsa_long.select_reference, dsa_long.py:
     114-118); positions at or past lengths[r] are not candidates (the NEG_INF of dsa_long.scores, :82-84)."""
@@ -391,6 +410,30 @@ def sparse_mla_slots_ref(q: torch.Tensor, kv_cache: torch.Tensor, kv_scale: torc
         r = rows[b].long()
         K = dequant(kv_cache[r], kv_scale[r])
         o[b], lse[b] = sparse_mla_rows_ref(q[b], K, bias[b].float().reshape(-1), scale, dv)
+    return o, lse
+
+
+def slots_compact_ref(q: torch.Tensor, kv_cache: torch.Tensor, kv_scale: torch.Tensor, rows: torch.Tensor,
+                      bias: torch.Tensor, scale: float, dv: int = 512):
+    """The compacted slot attention (trnrt/kernels/dsa_slots_c.py:92-103 `emulate`): rows [B, NS] pool rows of the
+    cache viewed as [slots / kp, kp rows], bias [B, NS, kp]. A row attends its visible tokens (bias above
+    NEG_INF / 2; pool row kp + t) with bias 0; a row with none attends pool row 0's kp tokens all at NEG_INF (the
+    compacted form's empty entries), i.e. their uniform mean."""
+    B, H, _ = q.shape
+    kp = bias.shape[-1] if bias.dim() == 3 else 1
+    o = torch.empty(B, H, dv)
+    lse = torch.empty(B, H)
+    for b in range(B):
+        bb = bias[b].float().reshape(-1)
+        vis = (bb > NEG_INF / 2).nonzero().flatten()
+        if vis.numel():
+            tok = rows[b].long()[vis // kp] * kp + vis % kp
+            bz = torch.zeros(vis.numel())
+        else:
+            tok = torch.arange(kp)
+            bz = torch.full((kp,), NEG_INF)
+        K = dequant(kv_cache[tok], kv_scale[tok])
+        o[b], lse[b] = sparse_mla_rows_ref(q[b], K, bz, scale, dv)
     return o, lse
 
 

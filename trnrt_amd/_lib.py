@@ -30,7 +30,7 @@ DSA_WS_TOPK = 1
 DSA_WS_ATTENTION = 2
 DSA_WS_LAYER = 3
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 P = c_void_p
 # Every entry point of include/dsa_gfx950.h with its ctypes signature (restype, argtypes).
@@ -55,6 +55,13 @@ SIGNATURES: dict[str, tuple] = {
          c_float, c_int, P],
     ),
     "dsa_token_rows": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, P]),
+    "dsa_compact_mask": (c_int, [P, c_int, c_int, c_int, P, P, P]),
+    "dsa_slots_compact_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
+    "dsa_sparse_mla_slots_compact": (
+        c_int,
+        [P, P, P, P, P, P, P, P, P, c_size_t, c_int, c_int, c_int, c_int, c_int, ctypes.c_longlong, c_float, c_int,
+         P],
+    ),
     "dsa_decode_layer": (
         c_int,
         [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, c_size_t, c_int, c_int, c_int, c_int, c_int, c_int, c_int,

@@ -65,6 +65,9 @@ hipError_t launch_token_rows(const int* idx, const int* cnt, const int* table, i
                              int keep, int max_pages, int page_size, int num_pages, hipStream_t s);
 int attention_default_splits(int B, int H, int keep, int num_cu);
 size_t attention_workspace_bytes(int B, int H, int splits);
+hipError_t launch_compact_mask(const float* sel, int N, int M, int keep, int64_t* idx, int64_t* cnt, hipStream_t s);
+hipError_t launch_compact_slots(const int* rows, const float* bias, int B, int NS, int kp, int pools, int* tok,
+                                int* tcnt, hipStream_t s);
 
 thread_local KernelTimer* g_kernel_timer = nullptr;
 }  // namespace dsa
@@ -361,6 +364,48 @@ int dsa_sparse_mla_decode(const void* q_bf16, const uint8_t* kv_fp8, const float
                                        rows, bias, static_cast<uint16_t*>(out_bf16), out_f32, lse, workspace, B, H,
                                        Dqk, keep, max_pages, page_size, num_pages, scale, sp,
                                        static_cast<hipStream_t>(stream), dsa::PoolForm{}, wide));
+}
+
+int dsa_compact_mask(const float* sel, int N, int M, int keep, int64_t* idx, int64_t* cnt, void* stream) {
+  if (!sel || !idx || !cnt || N < 0 || M < 1 || keep < 1) return DSA_EINVAL;
+  if (N == 0) return DSA_OK;
+  return status(dsa::launch_compact_mask(sel, N, M, keep, idx, cnt, static_cast<hipStream_t>(stream)));
+}
+
+size_t dsa_slots_compact_workspace_bytes(int B, int H, int NS, int kp, int splits) {
+  if (B < 0 || H < 16 || NS < 1 || kp < 1) return 0;
+  const int T = NS * kp;
+  return align256((size_t)B * T * 4) + align256((size_t)B * 4) +
+         align256(dsa::attention_workspace_bytes(B, H, effective_splits(resolve_splits(splits, B, H, T), T)));
+}
+
+int dsa_sparse_mla_slots_compact(const void* q_bf16, const uint8_t* kv_fp8, const float* kv_scale,
+                                 const int32_t* rows, const float* bias, void* out_bf16, float* out_f32, float* lse,
+                                 void* workspace, size_t workspace_bytes, int B, int H, int Dqk, int NS, int kp,
+                                 long long num_slots, float scale, int splits, void* stream) {
+  if (!q_bf16 || !kv_fp8 || !kv_scale || !rows || !bias || (!out_bf16 && !out_f32)) return DSA_EINVAL;
+  if (B < 0 || H < 1 || NS < 1 || kp < 1 || num_slots < kp || num_slots % kp) return DSA_EINVAL;
+  if ((Dqk != 576 && Dqk != 512) || H % 16) return DSA_EUNSUPPORTED;
+  if (num_slots > 0x7fffffffL || (long long)NS * kp > 0x7fffffffL) return DSA_EUNSUPPORTED;
+  if (B == 0) return DSA_OK;
+  const int T = NS * kp;
+  const size_t need = dsa_slots_compact_workspace_bytes(B, H, NS, kp, splits);
+  if (!workspace || workspace_bytes < need) return DSA_EWORKSPACE;
+  auto* s = static_cast<hipStream_t>(stream);
+  char* p = static_cast<char*>(workspace);
+  int* tok = reinterpret_cast<int*>(p);
+  int* tcnt = reinterpret_cast<int*>(p + align256((size_t)B * T * 4));
+  void* aws = p + align256((size_t)B * T * 4) + align256((size_t)B * 4);
+  if (dsa::launch_compact_slots(rows, bias, B, NS, kp, (int)(num_slots / kp), tok, tcnt, s) != hipSuccess)
+    return DSA_ELAUNCH;
+  // the compacted rows + count form; a row with no visible token attends its list's kp entries, all masked
+  const int sp = effective_splits(resolve_splits(splits, B, H, T), T);
+  dsa::PoolForm pf{};
+  pf.empty_n = kp;
+  const bool wide = sp == 1 && dsa::attention_wide_ok(B, H, T, false, num_cu());
+  return status(dsa::launch_sparse_mla(static_cast<const uint16_t*>(q_bf16), kv_fp8, kv_scale, nullptr, tcnt,
+                                       nullptr, tok, nullptr, static_cast<uint16_t*>(out_bf16), out_f32, lse, aws, B,
+                                       H, Dqk, T, 1, 1, (int)num_slots, scale, sp, s, pf, wide));
 }
 
 int dsa_token_rows(const int32_t* idx, const int32_t* cnt, const int32_t* page_table, int32_t* rows, float* bias,

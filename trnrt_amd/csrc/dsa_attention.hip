@@ -121,7 +121,8 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void sparse_mla_kernel(
       else
         cnt_b += tail;
     }
-    if (!bias) n_eff = cnt_b < 1 ? 1 : (cnt_b > keep ? keep : cnt_b);  // cnt 0: attend slot 0, fully masked
+    // cnt 0: attend slot 0 (or the first pf.empty_n slots), fully masked
+    if (!bias) n_eff = cnt_b < 1 ? min(max(pf.empty_n, 1), keep) : (cnt_b > keep ? keep : cnt_b);
   }
   const int k_begin = sp * slots_per_split;
   const int k_end = min(k_begin + slots_per_split, n_eff);
@@ -512,7 +513,7 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void sparse_mla_wide_kernel(
     const int tail = min(max(pf.positions[b] + 1 - (tail_pool << pf.kp_shift), 0), (1 << pf.kp_shift) - 1);
     cnt_b = (pools_b << pf.kp_shift) + tail;
   }
-  const int n_eff = cnt_b < 1 ? 1 : (cnt_b > keep ? keep : cnt_b);
+  const int n_eff = cnt_b < 1 ? min(max(pf.empty_n, 1), keep) : (cnt_b > keep ? keep : cnt_b);
   const int nch = (n_eff + ATT_CH - 1) / ATT_CH;
   const int nslot = nch * ATT_CH;
   const size_t nslots_cache = (size_t)num_pages * page_size;

@@ -64,6 +64,7 @@ struct PoolForm {
   const int* npool;
   const int* positions;
   int tail_apart;
+  int empty_n;  // rows + cnt form: the masked slots a row with cnt 0 attends (0: one)
 };
 constexpr int HIST_REPLICAS = 1;
 // Bytes after the histograms that a workspace keeps at zero between calls: the fused decode layer's per-XCD barrier

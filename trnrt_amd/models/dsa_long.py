@@ -5,6 +5,8 @@ and chunked-prefill paths call; a candidate is one token at kpool 1, a pool of k
   row, csrc/dsa_indexer.hip) (trnrt/models/dsa_long.py:74-84);
 - select_device / select: the exact top-keep of scores [N, P] as (indices [N, keep] int64 ascending, 0 past the
   count; count [N] int64) (trnrt/models/dsa_long.py:135-186), by the gfx950 top-k kernel;
+- compact: a 0 / 1 mask's ones as ascending indices and a count (trnrt/models/dsa_long.py:140-166), by a HIP
+  compaction kernel;
 - slots: selected pools -> cache pool rows and the 0 / NEG_INF bias with the query's tail pool
   (trnrt/models/dsa_long.py:189-215, any kpool);
 - attend: absorbed MLA over the slots (trnrt/models/dsa_long.py:218-223);
@@ -65,6 +67,25 @@ def select_device(sc: torch.Tensor, keep: int, lengths: torch.Tensor | None = No
 def select(sc: torch.Tensor, keep: int) -> tuple[torch.Tensor, torch.Tensor]:
     """The selection (trnrt/models/dsa_long.py:135-137): select_device."""
     return select_device(sc, keep)
+
+
+def compact(sel: torch.Tensor, keep: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """(indices [N, keep] int64 ascending, count [N] int64) of a 0 / 1 float mask sel [N, M]: the positions of each
+    row's ones, the first keep of them in a row with more, 0 past the count, count = min(ones, keep)
+    (trnrt/models/dsa_long.py:140-166). An entry counts as a one when above 0.5. One HIP kernel
+    (csrc/dsa_compact.hip): a workgroup per row, its walk stopping once keep ones are placed."""
+    dev = C.on_gpu(sel)
+    if sel.dim() != 2 or sel.shape[1] < 1:
+        raise ValueError(f"dsa_long.compact: mask {tuple(sel.shape)}, expected [N, M]")
+    if keep < 1:
+        raise ValueError(f"dsa_long.compact: keep {keep}")
+    N, M = sel.shape
+    s = C.as_f32(sel).contiguous()
+    idx = torch.empty(N, keep, dtype=torch.int64, device=dev)
+    cnt = torch.empty(N, dtype=torch.int64, device=dev)
+    st = _lib.lib().dsa_compact_mask(C.ptr(s), N, M, int(keep), C.ptr(idx), C.ptr(cnt), C.stream_ptr(dev))
+    _lib.check(st, "dsa_long.compact")
+    return idx, cnt
 
 
 def slots(pools: torch.Tensor, cnt: torch.Tensor, npool: torch.Tensor, positions: torch.Tensor, table: torch.Tensor,
