@@ -159,6 +159,15 @@ int dsa_sparse_mla_decode(const void* q_bf16, const uint8_t* kv_fp8, const float
 int dsa_compact_mask(const float* sel, int N, int M, int keep, int64_t* idx, int64_t* cnt, void* stream);
 
 /*
+ * A selection in value order (trnrt/kernels/dsa_long_select.py:74-84, the vorder output of `select`): pools int64
+ * [N, keep] ascending with cnt int64 [N] live and vals fp32 [N, keep] their scores -> out_pools / out_vals: the live
+ * entries by score descending, equal scores by pool ascending, then pool 0 / NEG_INF. keep <= 8192; the outputs must
+ * not alias the inputs.
+ */
+int dsa_value_order(const int64_t* pools, const int64_t* cnt, const float* vals, int N, int keep,
+                    int64_t* out_pools, float* out_vals, void* stream);
+
+/*
  * Slot attention over each row's visible tokens compacted in a kernel (trnrt/kernels/dsa_slots_c.py:416-447
  * `attend`, the arithmetic of dsa_sparse_mla_decode's row form): rows int32 [B, NS] pool rows of the cache viewed as
  * [num_slots / kp, kp rows], bias fp32 [B, NS, kp] (0 / NEG_INF; a token is visible when its bias is above

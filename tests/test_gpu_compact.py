@@ -69,3 +69,31 @@ def test_slots_compact_attend(kp):
     vis = (bias > O.NEG_INF / 2).reshape(B, -1).any(-1)
     assert_attention_close(o.cpu()[vis], uo.cpu()[vis])
     torch.testing.assert_close(lse.cpu()[vis], ul.cpu()[vis], atol=1e-3, rtol=1e-4)
+
+
+@pytest.mark.parametrize("keep", [1, 100, 2048, 8000])
+def test_value_order_with_ties(keep):
+    """dsa_long_select.value_order (trnrt/kernels/dsa_long_select.py:74-84) against a host sort of the same entries
+    by (score descending, pool ascending): scores drawn from 7 values so most compare equal, counts 0, keep and
+    partial, values copied bit for bit (a -0.0 stays -0.0)."""
+    from trnrt_amd.kernels import dsa_long_select as LS
+
+    say(f"value order keep={keep}")
+    N = 5
+    g = torch.Generator().manual_seed(keep)
+    pools = torch.stack([torch.sort(torch.randperm(4 * keep + 8, generator=g)[:keep]).values for _ in range(N)])
+    vals = torch.tensor([-1.5, -0.0, 0.0, 0.25, 1.0, 3.0, -2.0])[torch.randint(0, 7, (N, keep), generator=g)]
+    cnt = torch.tensor([keep, 0, keep // 2, max(keep - 1, 0), 1])[:N]
+    live = torch.arange(keep).view(1, -1) < cnt.view(-1, 1)
+    pools = torch.where(live, pools, 0)
+    vals = torch.where(live, vals, O.NEG_INF)
+    vp, vc, vv = LS.value_order(pools.cuda(), cnt.cuda(), vals.cuda())
+    torch.cuda.synchronize()
+    vp, vv = vp.cpu(), vv.cpu()
+    for n in range(N):
+        c = int(cnt[n])
+        order = sorted(range(c), key=lambda k: (-float(vals[n, k]), int(pools[n, k])))
+        assert vp[n, :c].tolist() == [int(pools[n, k]) for k in order]
+        assert torch.equal(vv[n, :c].view(torch.int32), vals[n, order].view(torch.int32))
+        assert torch.all(vp[n, c:] == 0) and torch.all(vv[n, c:] == O.NEG_INF)
+    assert torch.equal(vc.cpu(), cnt)

@@ -56,6 +56,7 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "dsa_token_rows": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, P]),
     "dsa_compact_mask": (c_int, [P, c_int, c_int, c_int, P, P, P]),
+    "dsa_value_order": (c_int, [P, P, P, c_int, c_int, P, P, P]),
     "dsa_slots_compact_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
     "dsa_sparse_mla_slots_compact": (
         c_int,

@@ -68,6 +68,8 @@ size_t attention_workspace_bytes(int B, int H, int splits);
 hipError_t launch_compact_mask(const float* sel, int N, int M, int keep, int64_t* idx, int64_t* cnt, hipStream_t s);
 hipError_t launch_compact_slots(const int* rows, const float* bias, int B, int NS, int kp, int pools, int* tok,
                                 int* tcnt, hipStream_t s);
+hipError_t launch_value_order(const int64_t* pools, const int64_t* cnt, const float* vals, int N, int keep,
+                              int64_t* out_pools, float* out_vals, hipStream_t s);
 
 thread_local KernelTimer* g_kernel_timer = nullptr;
 }  // namespace dsa
@@ -370,6 +372,15 @@ int dsa_compact_mask(const float* sel, int N, int M, int keep, int64_t* idx, int
   if (!sel || !idx || !cnt || N < 0 || M < 1 || keep < 1) return DSA_EINVAL;
   if (N == 0) return DSA_OK;
   return status(dsa::launch_compact_mask(sel, N, M, keep, idx, cnt, static_cast<hipStream_t>(stream)));
+}
+
+int dsa_value_order(const int64_t* pools, const int64_t* cnt, const float* vals, int N, int keep,
+                    int64_t* out_pools, float* out_vals, void* stream) {
+  if (!pools || !cnt || !vals || !out_pools || !out_vals || N < 0 || keep < 1) return DSA_EINVAL;
+  if (keep > 8192) return DSA_EUNSUPPORTED;
+  if (N == 0) return DSA_OK;
+  return status(dsa::launch_value_order(pools, cnt, vals, N, keep, out_pools, out_vals,
+                                        static_cast<hipStream_t>(stream)));
 }
 
 size_t dsa_slots_compact_workspace_bytes(int B, int H, int NS, int kp, int splits) {

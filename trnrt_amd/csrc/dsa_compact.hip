@@ -100,6 +100,63 @@ __global__ __launch_bounds__(CP_THREADS) void compact_slots_kernel(const int* __
   if (tid == 0) tcnt[b] = base;
 }
 
+// A selection (pools [N, keep] ascending, cnt [N], vals [N, keep]) in value order (trnrt/kernels/
+// dsa_long_select.py:74-84, the "vorder" output): a row's live entries (k < cnt) by value descending, equal values by
+// pool ascending, then pool 0 / NEG_INF. One workgroup per row sorts 64-bit keys (the value's order-preserving key,
+// then the inverted entry index, so equal values keep the input's ascending pool order; dead entries key 0, last) by
+// a bitonic network in LDS over the next power of two >= keep (at most VO_MAX), and gathers pools and values by the
+// sorted indices (the values copied, not rebuilt from their keys).
+constexpr int VO_MAX = 8192;
+constexpr int VO_THREADS = 512;
+
+__global__ __launch_bounds__(VO_THREADS) void value_order_kernel(const int64_t* __restrict__ pools,
+                                                                  const int64_t* __restrict__ cnt,
+                                                                  const float* __restrict__ vals, int keep, int np2,
+                                                                  int64_t* __restrict__ out_pools,
+                                                                  float* __restrict__ out_vals) {
+  __shared__ uint64_t key[VO_MAX];
+  const int n = blockIdx.x, tid = threadIdx.x;
+  const int64_t c = cnt[n];
+  const float* vr = vals + (size_t)n * keep;
+  for (int k = tid; k < np2; k += VO_THREADS) {
+    const bool live = k < keep && k < c;
+    key[k] = live ? ((uint64_t)order_key(vr[k]) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)k) : 0ull;
+  }
+  __syncthreads();
+  // bitonic network, descending overall: pairs (i, i ^ j) with i < i ^ j, direction by bit `size` of i
+  for (int size = 2; size <= np2; size <<= 1) {
+    for (int j = size >> 1; j > 0; j >>= 1) {
+      for (int t = tid; t < np2 / 2; t += VO_THREADS) {
+        const int i = 2 * t - (t & (j - 1));  // the lower index of the t-th pair at distance j
+        const int l = i + j;
+        const uint64_t a = key[i], b = key[l];
+        const bool desc = (i & size) == 0;
+        if (desc ? a < b : a > b) {
+          key[i] = b;
+          key[l] = a;
+        }
+      }
+      __syncthreads();
+    }
+  }
+  const int64_t* pr = pools + (size_t)n * keep;
+  for (int k = tid; k < keep; k += VO_THREADS) {
+    const uint64_t kk = key[k];
+    const bool live = kk != 0ull;
+    const int src = (int)(0xFFFFFFFFu - (uint32_t)kk);
+    out_pools[(size_t)n * keep + k] = live ? pr[src] : 0;
+    out_vals[(size_t)n * keep + k] = live ? vr[src] : NEG_INF;
+  }
+}
+
+hipError_t launch_value_order(const int64_t* pools, const int64_t* cnt, const float* vals, int N, int keep,
+                              int64_t* out_pools, float* out_vals, hipStream_t s) {
+  int np2 = 2;
+  while (np2 < keep) np2 <<= 1;
+  return launch("value_order_kernel", value_order_kernel, dim3(N), dim3(VO_THREADS), s, pools, cnt, vals, keep, np2,
+                out_pools, out_vals);
+}
+
 hipError_t launch_compact_mask(const float* sel, int N, int M, int keep, int64_t* idx, int64_t* cnt, hipStream_t s) {
   return launch("compact_mask_kernel", compact_mask_kernel, dim3(N), dim3(CP_THREADS), s, sel, M, keep, idx, cnt);
 }

@@ -111,15 +111,20 @@ def scores(qI: torch.Tensor, w: torch.Tensor, pk: torch.Tensor, npool: torch.Ten
 
 
 def value_order(pools: torch.Tensor, cnt: torch.Tensor, vals: torch.Tensor):
-    """A selection (pools ascending, count, scores; 0 / NEG_INF past the count) in the reference's vorder form
-    (trnrt/kernels/dsa_long_select.py:74-84): the selected pools by score descending, equal scores by pool ascending,
-    then 0 / NEG_INF."""
+    """A selection (pools [N, keep] ascending, count [N], scores [N, keep]; 0 / NEG_INF past the count) in the
+    reference's vorder form (trnrt/kernels/dsa_long_select.py:74-84): the selected pools by score descending, equal
+    scores by pool ascending, then 0 / NEG_INF. One HIP kernel (csrc/dsa_compact.hip: a bitonic sort of each row's
+    (score key, entry index) pairs in LDS); keep <= 8192."""
+    dev = C.on_gpu(pools, cnt, vals)
     N, keep = pools.shape
-    k = torch.arange(keep, device=pools.device).view(1, keep)
-    live = k < cnt.view(N, 1)
-    key = torch.where(live, vals, torch.full_like(vals, -3.0e38))
-    order = torch.sort(key, dim=-1, descending=True, stable=True).indices
-    return (torch.where(live, pools.gather(1, order), 0), cnt, torch.where(live, vals.gather(1, order), NEG_INF))
+    p = C.need(pools.to(torch.int64).contiguous(), "pools", torch.int64, (N, keep))
+    c = C.need(cnt.to(torch.int64).reshape(N).contiguous(), "cnt", torch.int64, (N,))
+    v = C.need(C.as_f32(vals).contiguous(), "vals", torch.float32, (N, keep))
+    op = torch.empty(N, keep, dtype=torch.int64, device=dev)
+    ov = torch.empty(N, keep, dtype=torch.float32, device=dev)
+    st = _lib.lib().dsa_value_order(C.ptr(p), C.ptr(c), C.ptr(v), N, keep, C.ptr(op), C.ptr(ov), C.stream_ptr(dev))
+    _lib.check(st, "dsa_long_select.value_order")
+    return op, cnt, ov
 
 
 def select(qI: torch.Tensor, w: torch.Tensor, pk: torch.Tensor, npool: torch.Tensor, keep: int, scale: float,
