@@ -168,9 +168,24 @@ def test_decode_batch_form_of_dsa_long_scores():
         assert torch.all(got[n:n + 1][~live] < -1e29)
 
 
+# 64 rows of a 2,048-query chunk: the first and last 16 and 32 spread between them
+ROWS64 = list(range(16)) + [16 + 63 * i for i in range(32)] + list(range(2032, 2048))
+
+
+def _prefill_ref_rows(c, rows, cfg, q_values):
+    """prefill_scores_ref of the given rows in groups of 8 (the oracle's [rows, heads, keys] intermediate stays
+    near 140 MB)."""
+    out = []
+    for i in range(0, len(rows), 8):
+        r = rows[i:i + 8]
+        out.append(O.prefill_scores_ref(q_values[r], c.w[r], c.k8, c.k_scale, c.npool[r], cfg.scale))
+    return torch.cat(out)
+
+
 def test_config5_full_size_sampled_rows():
     """Config 5 (65,536 cached + 2,048 new queries, 64 heads, FP8 queries): every row's candidate count and NEG_INF
-    tail, and the oracle on sampled rows; the selection of those rows bit-exact on the kernel's scores."""
+    tail, and the oracle on 64 rows (the first and last 16); the selection of those rows bit-exact on the kernel's
+    scores."""
     cfg = W.PREFILL_CONFIGS[5]
     say(f"prefill config 5 {cfg.name}")
     inp = W.make_prefill_inputs(cfg, seed=0, device="cuda")
@@ -182,9 +197,9 @@ def test_config5_full_size_sampled_rows():
     P = cfg.P
     live = torch.arange(P, device="cuda").view(1, P) < inp.npool.view(-1, 1).long()
     assert torch.all((sc > -1e29) == live)
-    rows = [0, 1, 2, 3, 777, 1024, 2045, 2046, 2047]
+    rows = ROWS64
     c = inp.to("cpu")
-    ref = O.prefill_scores_ref(c.q_values()[rows], c.w[rows], c.k8, c.k_scale, c.npool[rows], cfg.scale)
+    ref = _prefill_ref_rows(c, rows, cfg, c.q_values())
     got = sc[rows].cpu()
     err = row_rel_err(got, ref, ref > -1e29)
     say(f"  config 5 sampled rel err {err:.3e}")
@@ -228,8 +243,8 @@ def test_chunk_attention_vs_oracle(rows_form):
 
 
 def test_config5_chunk_attention_sampled_rows():
-    """Config 5 end to end at full size (2,048 queries over 67,584 keys, top-2048, 64 heads): the attention of
-    sampled rows against the oracle over the kernel's own selection."""
+    """Config 5 end to end at full size (2,048 queries over 67,584 keys, top-2048, 64 heads): the attention of 64
+    rows (the first and last 16) against the oracle over the kernel's own selection."""
     cfg = W.PREFILL_CONFIGS[5]
     say("prefill config 5 chunk attention")
     inp = W.make_prefill_inputs(cfg, seed=1, device="cuda", attention=True)
@@ -237,7 +252,7 @@ def test_config5_chunk_attention_sampled_rows():
                               qI_scale=inp.qI_scale)
     o, lse = _chunk_attention(inp, cfg, pools, cnt, rows_form=False)
     torch.cuda.synchronize()
-    rows = [0, 5, 1000, 2047]
+    rows = ROWS64
     c = inp.to("cpu")
     table = c.table.view(1, -1).expand(len(rows), -1)
     ref_o, ref_lse = O.sparse_mla_ref(c.q[rows], c.kv_cache, c.kv_scale, pools[rows].cpu(), cnt[rows].cpu(), table,
@@ -264,3 +279,26 @@ def test_select_many_rows_every_row(P):
     assert torch.equal(pools.cpu(), ri)
     live = torch.arange(keep).view(1, -1) < rc.view(-1, 1)
     assert torch.equal(vals.cpu(), torch.where(live, sc.gather(1, ri), O.NEG_INF))
+
+
+def test_config5_size_bf16_query_indexer():
+    """The bf16-query prefill indexer (the reference's own arithmetic, trnrt/kernels/dsa_long_select.py:119-133) at
+    config 5's size (2,048 queries over 67,584 keys, 64 heads) against the oracle on 64 rows, and every row's NEG_INF
+    tail; the selection of those rows bit-exact on the kernel's scores."""
+    cfg = W.PrefillConfig("prefill-65536+2048-bf16q", cached=65536, chunk=2048, q_fp8=False)
+    say(f"prefill {cfg.name}")
+    inp = W.make_prefill_inputs(cfg, seed=3, device="cuda")
+    sc = LS.scores(inp.qI, inp.w, inp.k8, inp.npool, cfg.scale, pk_scale=inp.k_scale)
+    pools, cnt, vals = LS.select(inp.qI, inp.w, inp.k8, inp.npool, cfg.keep, cfg.scale, pk_scale=inp.k_scale)
+    torch.cuda.synchronize()
+    P = cfg.P
+    live = torch.arange(P, device="cuda").view(1, P) < inp.npool.view(-1, 1).long()
+    assert torch.all((sc > -1e29) == live)
+    c = inp.to("cpu")
+    ref = _prefill_ref_rows(c, ROWS64, cfg, c.qI)
+    got = sc[ROWS64].cpu()
+    err = row_rel_err(got, ref, ref > -1e29)
+    say(f"  bf16-query rel err {err:.3e}")
+    assert err <= TOL
+    ri, rc = O.topk_ref(got, cfg.keep, c.npool[ROWS64])
+    assert torch.equal(pools[ROWS64].cpu(), ri) and torch.equal(cnt[ROWS64].cpu(), rc)
