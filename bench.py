@@ -14,6 +14,7 @@ HIP-event-timed duration; longer rows run the separate kernels, whose roofline i
 the median, p10 and p90 of single steps, each timed by a pair of events around it.
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--config 2] [--no-cpu-baseline]
+    python bench.py --chain             # config 2 through the separate kernels (dsa_decode_layer_chain)
     python bench.py --config 5          # the chunked-prefill step (65,536 cached + 2,048 new queries): its own line
     python bench.py --config 6          # the pooled (GLM-5.3-Flash, kpool 4) decode step at B=8 x 32K: its own line
     python bench.py --config 7          # the pooled (GLM) chunked-prefill step (65,536 cached + 2,048 new queries)
@@ -551,6 +552,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", type=int, default=2)
     ap.add_argument("--splits", type=int, default=0)
+    ap.add_argument("--chain", action="store_true",
+                    help="run the separate kernels (dsa_decode_layer_chain) even where the one-launch layer applies")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB")
     args = ap.parse_args()
@@ -578,7 +581,7 @@ def main() -> int:
     torch.cuda.set_device(dev)
     inp = W.make_inputs(cfg, seed=0, device=dev)
     layer = DecodeLayer(cfg.B, cfg.Hi, cfg.H, inp.max_pages, cfg.page_size, inp.num_pages, cfg.keep, cfg.scale,
-                        max_len=max(inp.lengths), splits=args.splits, device=dev)
+                        max_len=max(inp.lengths), splits=args.splits, device=dev, chain=args.chain)
     g = inp
     lib = _lib.lib()
 
@@ -616,7 +619,7 @@ def main() -> int:
     k_time = k_us[kname]
     achieved = kbytes / (k_time * 1e-6) / 1e9
 
-    workload = f"config {args.config}: {cfg.name}"
+    workload = f"config {args.config}: {cfg.name}" + (" (separate kernels)" if args.chain else "")
     out = {
         "metric": "DSA decode layer-steps/sec at B=8, 32K ctx; achieved HBM GB/s (% of 8 TB/s)",
         "value": round(1e3 / ms, 1),
