@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define DSA_ABI_VERSION 7
+#define DSA_ABI_VERSION 8
 
 #define DSA_OK 0
 #define DSA_EINVAL (-1)      /* a null pointer or a size out of range */
@@ -125,6 +125,8 @@ int dsa_topk_supported(int max_len, int keep, int vis_only);
  * tail forms, dsa_topk.py:89-93): score p of row b (P scores per row) is taken when it is one of idx[b, 0 ..
  * cnt[b]), or, with tail, when it is not a candidate (scores[b, p] <= VISIBLE: the reference's `sel | ~vis`);
  * mask[b, p * kp + t] = taken ? 0 : NEG_INF for t < kp. scores (fp32 [B, P]) is read only with tail.
+ * idx and cnt NULL: the form of keep >= P (dsa_topk.py:510-511, no selection run): every score that scores marks
+ * visible (scores[b, p] > VISIBLE) is taken, or every score when scores is NULL; tail as above.
  */
 int dsa_topk_mask(const int32_t* idx, const int32_t* cnt, const float* scores, float* mask, int B, int keep, int P,
                   int kp, int tail, void* stream);
@@ -211,16 +213,23 @@ int dsa_pool_slots(const int32_t* pools, const int32_t* cnt, const int32_t* npoo
  * A prefill chunk's selection in one call (replaces trnrt/kernels/dsa_long_select.py:494-528 `select`, its score
  * stage and its exact top-keep): the scores of dsa_indexer_prefill (q_scale null: bf16 queries q [N, Hi, 128]; keys
  * e4m3 with k_scale, or bf16 with k_scale null) or dsa_indexer_prefill_fp8 (q e4m3 [N, Hi, 128] with q_scale [N, Hi],
- * e4m3 keys) into scores [N, score_stride], then per query the
- * exact top-keep of its npool[n] candidates (rows longer than 32,768 in two levels, the indexer writing the first
- * level's sub-block maxima), returned as the reference returns them: pools int64 [N, keep] ascending (0 past the
- * count), cnt int64 [N], vals fp32 [N, keep] (the selected scores, NEG_INF past the count).
- *   workspace: dsa_prefill_select_workspace_bytes(N, P, keep) bytes, zero-filled before first use.
+ * e4m3 keys), then per query the exact top-keep of its npool[n] candidates (rows longer than 32,768 in two levels, the
+ * indexer writing the first level's sub-block maxima), returned as the reference returns them: pools int64 [N, keep]
+ * ascending (0 past the count), cnt int64 [N], vals fp32 [N, keep] (the selected scores, NEG_INF past the count).
+ * The queries go in tiles of tile_rows (0: tiles whose scores take at most 64 MiB), each tile scored, then selected
+ * (the reference's per-tile device form, trnrt/kernels/dsa_long_pipe.py:15-25); tiles alternate between `stream`
+ * and the library's second stream, which waits for the work enqueued on `stream` before the call and which `stream`
+ * waits for after it (events), so one tile's selection overlaps the other stream's scores. scores: fp32
+ * [N, score_stride] to receive every score, or null to keep only two tiles' scores, in the workspace (the
+ * memory-bounded form).
+ *   workspace: dsa_prefill_select_workspace_bytes(N, P, score_stride, keep, tile_rows, scores == null) bytes,
+ *   zero-filled before first use (calls leave it so). Calls on one device run their enqueues one at a time.
  */
-int dsa_prefill_select(const void* q, const float* q_scale, const float* w, const void* k, const float* k_scale, const int32_t* npool, float* scores, int64_t* pools, int64_t* cnt,
-                       float* vals, void* workspace, size_t workspace_bytes, int N, int Hi, int D, int P,
-                       int score_stride, int keep, float scale, void* stream);
-size_t dsa_prefill_select_workspace_bytes(int N, int P, int keep);
+int dsa_prefill_select(const void* q, const float* q_scale, const float* w, const void* k, const float* k_scale,
+                       const int32_t* npool, float* scores, int64_t* pools, int64_t* cnt, float* vals, void* workspace,
+                       size_t workspace_bytes, int N, int Hi, int D, int P, int score_stride, int keep, float scale,
+                       int tile_rows, void* stream);
+size_t dsa_prefill_select_workspace_bytes(int N, int P, int score_stride, int keep, int tile_rows, int own_scores);
 
 /*
  * The whole DSA decode layer step: indexer -> top-k -> sparse MLA (the order of trnrt/models/mla.py:506-528

@@ -136,23 +136,29 @@ def test_prefill_select_and_pooled_layer_host_checks():
     lib = _lib.lib()
     p = ctypes.c_void_p(16)
     null = None
-    ws = lib.dsa_prefill_select_workspace_bytes(4, 67584, 2048)
-    assert ws > 0 and lib.dsa_prefill_select_workspace_bytes(4, 0, 2048) == 0
+    ws = lib.dsa_prefill_select_workspace_bytes(4, 67584, 67584, 2048, 0, 0)
+    assert ws > 0 and lib.dsa_prefill_select_workspace_bytes(4, 0, 0, 2048, 0, 0) == 0
+    assert lib.dsa_prefill_select_workspace_bytes(4, 67584, 67583, 2048, 0, 0) == 0  # stride < P
     big = ctypes.c_size_t(ws)
     args = lambda **k: dict(dict(q=p, qs=p, w=p, k=p, ks=p, npool=p, sc=p, pools=p, cnt=p, vals=p, ws=p, wsb=big, N=4,
-                                 Hi=64, D=128, P=67584, stride=67584, keep=2048, scale=0.1), **k)
+                                 Hi=64, D=128, P=67584, stride=67584, keep=2048, scale=0.1, tile=0), **k)
 
     def call(a):
         return lib.dsa_prefill_select(a["q"], a["qs"], a["w"], a["k"], a["ks"], a["npool"], a["sc"], a["pools"],
                                       a["cnt"], a["vals"], a["ws"], a["wsb"], a["N"], a["Hi"], a["D"], a["P"],
-                                      a["stride"], a["keep"], a["scale"], null)
+                                      a["stride"], a["keep"], a["scale"], a["tile"], null)
 
     assert call(args(vals=null)) == -1  # no output
     assert call(args(stride=67583)) == -1  # stride < P
     assert call(args(scale=0.0)) == -1
+    assert call(args(tile=-1)) == -1
     assert call(args(Hi=65)) == -2
     assert call(args(D=64)) == -2
     assert call(args(wsb=ctypes.c_size_t(ws - 1))) == -3  # workspace too small
+    # the memory-bounded form (scores null) holds its score tiles in the workspace
+    own = lib.dsa_prefill_select_workspace_bytes(4, 67584, 67584, 2048, 0, 1)
+    assert own >= ws + 4 * 67584 * 4
+    assert call(args(sc=null)) == -3
     assert call(args(N=0)) == 0
     pw = lib.dsa_pooled_workspace_bytes(8, 64, 512, 8192, 4, 0)
     assert pw > 0 and lib.dsa_pooled_workspace_bytes(8, 64, 512, 8192, 1, 0) == 0

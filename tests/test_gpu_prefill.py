@@ -147,6 +147,60 @@ def test_select_two_level_sub_blocks_of_two(q_fp8):
     assert torch.equal(vals.cpu(), torch.where(live, sc.gather(1, ri), O.NEG_INF))
 
 
+@pytest.mark.parametrize("P,keep,tile", [(5000, 2048, 8), (40000, 2048, 12), (40001, 2048, 7), (300000, 16, 10),
+                                          (40000, 6000, 9)])
+@pytest.mark.parametrize("q_fp8", [False, True])
+def test_select_in_tiles(P, keep, tile, q_fp8):
+    """dsa_prefill_select over several query tiles (tile_rows below N, the last tile shorter), through every
+    selection plan: flat rows (P 5,000), two levels with the indexer's sub-block maxima (sub 4), the generic
+    two-level form (sub 128: block maxima pass; sub 2 at keep 6,000: maxima score by score), each tile's selection
+    on the second stream beside the next tile's scores where the plan allows. Bit-exact against the exact selection
+    of the kernel's own scores, for the form that keeps two score tiles in the workspace and for the form that
+    writes every score into the caller's buffer (whose scores must equal dsa_indexer_prefill's)."""
+    N = 30
+    say(f"prefill select in tiles P={P} keep={keep} tile={tile} q_fp8={q_fp8}")
+    qI, w, k8, ks, npool = _inputs(N, 64, P, seed=P + keep + tile + q_fp8)
+    npool[3], npool[4], npool[N - 1] = keep - 7, 0, P
+    qs = None
+    if q_fp8:
+        qI, qs, _ = _fp8(qI)
+        qs = qs.cuda()
+    args = (qI.cuda(), w.cuda(), k8.cuda(), npool.cuda())
+    sc = LS.scores(*args, 128 ** -0.5, pk_scale=ks.cuda(), qI_scale=qs).cpu()
+    ri, rc = O.topk_ref(sc, keep, npool)
+    live = torch.arange(keep).view(1, -1) < rc.view(-1, 1)
+    want_vals = torch.where(live, sc.gather(1, ri), O.NEG_INF)
+    ws = torch.zeros(LS.workspace_bytes(N, P, keep, tile), dtype=torch.uint8, device="cuda")
+    for _ in range(2):  # the second call on the same workspace
+        pools, cnt, vals = LS.select(*args, keep, 128 ** -0.5, pk_scale=ks.cuda(), qI_scale=qs, workspace=ws,
+                                     tile_rows=tile)
+        torch.cuda.synchronize()
+        assert torch.equal(cnt.cpu(), rc)
+        assert torch.equal(pools.cpu(), ri)
+        assert torch.equal(vals.cpu(), want_vals)
+    # the caller's-scores form through the C ABI: every score written, the same selection
+    from trnrt_amd import _lib
+    from trnrt_amd.kernels import _common as C
+    lib = _lib.lib()
+    stride = (P + 3) // 4 * 4 + 4
+    wsb = int(lib.dsa_prefill_select_workspace_bytes(N, P, stride, keep, tile, 0))
+    ws2 = torch.zeros(max(wsb, 256), dtype=torch.uint8, device="cuda")
+    full = torch.full((N, stride), 7.0, device="cuda")
+    pools2 = torch.empty(N, keep, dtype=torch.int64, device="cuda")
+    cnt2 = torch.empty(N, dtype=torch.int64, device="cuda")
+    vals2 = torch.empty(N, keep, dtype=torch.float32, device="cuda")
+    q_arg = C.fp8_bytes(args[0], "qI") if q_fp8 else args[0]
+    st = lib.dsa_prefill_select(C.ptr(q_arg), C.ptr(qs), C.ptr(args[1]), C.ptr(C.fp8_bytes(args[2], "pk")),
+                                C.ptr(ks.cuda()), C.ptr(args[3]), C.ptr(full), C.ptr(pools2), C.ptr(cnt2),
+                                C.ptr(vals2), C.ptr(ws2), wsb, N, 64, 128, P, stride, keep, 128 ** -0.5, tile,
+                                C.stream_ptr(torch.device("cuda")))
+    _lib.check(st, "dsa_prefill_select")
+    torch.cuda.synchronize()
+    assert torch.equal(full[:, :P].cpu(), sc)
+    assert torch.all(full[:, P:].cpu() == O.NEG_INF)
+    assert torch.equal(cnt2.cpu(), rc) and torch.equal(pools2.cpu(), ri) and torch.equal(vals2.cpu(), want_vals)
+
+
 def test_decode_batch_form_of_dsa_long_scores():
     """dsa_long.scores with one context per row ([N, P, 128] keys) through the decode indexer."""
     say("dsa_long.scores 3-D keys")

@@ -111,6 +111,21 @@ def test_pooled_mask_forms(kp, tail):
     assert torch.equal(m, O.topk_mask_ref(s, keep, True, kp, tail))
 
 
+@pytest.mark.parametrize("P,keep,vis_only,kp,tail", [(5000, 5000, True, 1, False), (5000, 9000, False, 1, False),
+                                                     (40000, 40000, True, 4, True), (70000, 80000, True, 2, False),
+                                                     (70000, 70000, False, 1, False)])
+def test_select_keep_at_least_p(P, keep, vis_only, kp, tail):
+    """dsa_topk.select with keep >= P (rows longer than the kernel's 32,768 included): every visible score, or every
+    score without vis_only, as the reference's short-cut (trnrt/kernels/dsa_topk.py:510-511, 103-105)."""
+    say(f"topk select keep>=P P={P} keep={keep} vis_only={vis_only} kp={kp} tail={tail}")
+    g = torch.Generator().manual_seed(P + keep)
+    s = torch.randn(3, P, generator=g)
+    s[0, P // 3:] = O.NEG_INF
+    s[2, ::7] = O.VISIBLE  # exactly VISIBLE: not visible
+    m = dsa_topk.select(s.cuda(), keep, vis_only=vis_only, kp=kp, tail=tail).cpu()
+    assert torch.equal(m, O.topk_mask_ref(s, keep, vis_only, kp, tail))
+
+
 @pytest.mark.parametrize("n", [6000, 9000, 16384, 20000, 32768])
 @pytest.mark.parametrize("kind", ["randn", "integers", "zeros", "wide", "invisible", "equal"])
 def test_many_rows_form(kind, n):

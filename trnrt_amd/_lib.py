@@ -30,7 +30,7 @@ DSA_WS_TOPK = 1
 DSA_WS_ATTENTION = 2
 DSA_WS_LAYER = 3
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 P = c_void_p
 # Every entry point of include/dsa_gfx950.h with its ctypes signature (restype, argtypes).
@@ -92,9 +92,9 @@ SIGNATURES: dict[str, tuple] = {
     "dsa_sparse_mla_pooled_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
     "dsa_prefill_select": (
         c_int,
-        [P, P, P, P, P, P, P, P, P, P, P, c_size_t, c_int, c_int, c_int, c_int, c_int, c_int, c_float, P],
+        [P, P, P, P, P, P, P, P, P, P, P, c_size_t, c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_int, P],
     ),
-    "dsa_prefill_select_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
+    "dsa_prefill_select_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int]),
     "dsa_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int]),
     "dsa_default_splits": (c_int, [c_int, c_int, c_int]),
     "dsa_timing_begin": (c_int, [P, c_int]),

@@ -1,5 +1,6 @@
 // C ABI entry points of libdsa_gfx950.so (declared in include/dsa_gfx950.h): host-side argument checks, launch
-// shapes, and the launches on the caller's stream. Nothing here allocates device memory or synchronises.
+// shapes, and the launches on the caller's stream (the prefill selection also on the library's second stream, joined
+// back to the caller's by events). Nothing here allocates device memory or synchronises the host.
 #include "../../include/dsa_gfx950.h"
 
 #include <mutex>
@@ -25,6 +26,10 @@ float* topk_bm_buffer(void* ws, int B);
 hipError_t launch_prefill_topk(const float* scores, const int* len, int* idx, int* cnt, void* ws, int B, int stride,
                                int n, int keep, bool bm_ready, int64_t* pools, int64_t* cnt64, float* vals,
                                hipStream_t s);
+int prefill_tile_plan(long n, int stride, int keep);
+hipError_t launch_prefill_tile_topk(const float* scores, int stride, const int* len, long n, int keep,
+                                    const float* bm, int* bidx, int* bcnt, int64_t* pools, int64_t* cnt64,
+                                    float* vals, int T, hipStream_t s);
 bool cache_write_width_ok(int W);
 hipError_t launch_cache_write(const void* x, int x_fp32, const int64_t* slots, uint8_t* cache, float* cscale,
                               int n_rows, int W, long num_slots, int scaled, float fp8_max, hipStream_t s);
@@ -112,7 +117,118 @@ int effective_splits(int splits, int keep) {
   return (keep + sps - 1) / sps;
 }
 
+// The prefill selection runs over tiles of T query rows: each tile's scores [T, score_stride] fp32, then its
+// selection, so that nothing of the chunk's size x the context's is held at once (the reference's device form scores
+// and selects per 128-query tile with two HBM score scratches, trnrt/kernels/dsa_long_pipe.py:15-25). By default a
+// score tile is at most kPrefillTileBytes (equal tiles, whole groups of 4 rows: the indexer's workgroup).
+constexpr size_t kPrefillTileBytes = 64ull << 20;
+
+int prefill_tile_rows(int N, int stride, int tile_rows) {
+  if (N <= 0) return 1;
+  if (tile_rows > 0) return tile_rows < N ? tile_rows : N;
+  long t = (long)(kPrefillTileBytes / ((size_t)stride * 4));
+  if (t < 64) t = 64;
+  if (t >= N) return N;
+  const long tiles = (N + t - 1) / t;
+  const long rows = ((N + tiles - 1) / tiles + 3) / 4 * 4;
+  return (int)(rows < N ? rows : N);
+}
+
+// Workspace of the prefill selection, in order: the generic selection's workspace and its int32 outputs (plan < 0
+// only; its zero region first), then `sets` score tiles (own scores only), and with plan > 0 `sets` each of the
+// sub-block maxima tiles and of the first level's outputs. plan: dsa::prefill_tile_plan. Two sets when tiles
+// alternate between two streams (plan >= 0 and more than one tile), else one.
+struct PrefillLayout {
+  int T, tiles, plan, sets;
+  size_t gidx_off, gcnt_off, sc_off, sc_bytes, bm_off, bm_bytes, bidx_off, bidx_bytes, bcnt_off, bcnt_bytes, total;
+};
+
+PrefillLayout prefill_layout(int N, int P, int stride, int keep, int tile_rows, bool own_scores) {
+  PrefillLayout L{};
+  L.T = prefill_tile_rows(N, stride, tile_rows);
+  L.tiles = N > 0 ? (N + L.T - 1) / L.T : 0;
+  L.plan = dsa::prefill_tile_plan(P, stride, keep);
+  L.sets = L.plan >= 0 && L.tiles > 1 ? 2 : 1;
+  size_t off = 0;
+  if (L.plan < 0) {
+    off = align256(dsa::topk_workspace_bytes(L.T, P, keep));
+    L.gidx_off = off;
+    off += align256((size_t)L.T * keep * 4);
+    L.gcnt_off = off;
+    off += align256((size_t)L.T * 4);
+  }
+  L.sc_off = off;
+  L.sc_bytes = own_scores ? align256((size_t)L.T * stride * 4) : 0;
+  off += L.sets * L.sc_bytes;
+  L.bm_off = off;
+  if (L.plan > 0) {
+    const long nb = (P + L.plan - 1) / L.plan;
+    L.bm_bytes = align256((size_t)L.T * nb * 4);
+    off += L.sets * L.bm_bytes;
+    L.bidx_off = off;
+    L.bidx_bytes = align256((size_t)L.T * keep * 4);
+    off += L.sets * L.bidx_bytes;
+    L.bcnt_off = off;
+    L.bcnt_bytes = align256((size_t)L.T * 4);
+    off += L.sets * L.bcnt_bytes;
+  }
+  L.total = off > 256 ? off : 256;
+  return L;
+}
+
 constexpr int kMaxDevices = 64;
+
+// The library's second stream on each device (default priority, not synchronising with the null stream), created on
+// first use and kept until the process ends, with the two events that fork it from and join it to a caller's stream.
+// One call at a time holds a device's set (the lock), so the events' records and waits of two calls never interleave.
+std::mutex g_aux_mu;
+hipStream_t g_aux_stream[kMaxDevices] = {};
+hipEvent_t g_aux_events[kMaxDevices][2] = {};
+
+struct AuxStream {
+  bool ok = false;
+  hipStream_t stream = nullptr;
+  hipEvent_t start = nullptr, end = nullptr;
+  std::unique_lock<std::mutex> lock;
+
+  explicit AuxStream(bool want) {
+    int dev = 0;
+    if (!want || hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return;
+    lock = std::unique_lock<std::mutex>(g_aux_mu);
+    if (!g_aux_stream[dev]) {
+      hipStream_t s = nullptr;
+      hipEvent_t ev[2] = {};
+      bool made = hipStreamCreateWithFlags(&s, hipStreamNonBlocking) == hipSuccess;
+      for (int i = 0; i < 2 && made; ++i) made = hipEventCreateWithFlags(&ev[i], hipEventDisableTiming) == hipSuccess;
+      if (!made) {
+        for (hipEvent_t e : ev)
+          if (e) (void)hipEventDestroy(e);
+        if (s) (void)hipStreamDestroy(s);
+        (void)hipGetLastError();  // the next launch's status must not report this failure
+        lock.unlock();
+        return;
+      }
+      g_aux_stream[dev] = s;
+      g_aux_events[dev][0] = ev[0];
+      g_aux_events[dev][1] = ev[1];
+    }
+    stream = g_aux_stream[dev];
+    start = g_aux_events[dev][0];
+    end = g_aux_events[dev][1];
+    ok = true;
+  }
+
+  // The second stream's next work waits for everything enqueued on the caller's stream so far.
+  bool fork(hipStream_t caller) {
+    return hipEventRecord(start, caller) == hipSuccess && hipStreamWaitEvent(stream, start, 0) == hipSuccess;
+  }
+
+  // The caller's stream waits for everything enqueued on the second stream so far.
+  bool join(hipStream_t caller) {
+    return hipEventRecord(end, stream) == hipSuccess && hipStreamWaitEvent(caller, end, 0) == hipSuccess;
+  }
+};
+
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
 size_t g_scratch_zero[kMaxDevices] = {};  // bytes from the scratch's start that are zero when the next call runs
@@ -245,46 +361,86 @@ int dsa_indexer_prefill_fp8(const uint8_t* q_fp8, const float* q_scale, const fl
                                                 score_stride, scale, nullptr, 0, 0, static_cast<hipStream_t>(stream)));
 }
 
-size_t dsa_prefill_select_workspace_bytes(int N, int P, int keep) {
-  if (N < 0 || P < 1 || keep < 1) return 0;
-  return align256(dsa::topk_workspace_bytes(N, P, keep)) + align256((size_t)N * keep * 4) + align256((size_t)N * 4);
+size_t dsa_prefill_select_workspace_bytes(int N, int P, int score_stride, int keep, int tile_rows, int own_scores) {
+  if (N < 0 || P < 1 || keep < 1 || score_stride < P || tile_rows < 0) return 0;
+  return prefill_layout(N, P, score_stride, keep, tile_rows, own_scores != 0).total;
 }
 
 int dsa_prefill_select(const void* q, const float* q_scale, const float* w, const void* k, const float* k_scale,
                        const int32_t* npool, float* scores, int64_t* pools, int64_t* cnt, float* vals, void* workspace,
                        size_t workspace_bytes, int N, int Hi, int D, int P, int score_stride, int keep, float scale,
-                       void* stream) {
-  if (!q || !w || !k || !npool || !scores || !pools || !cnt || !vals || !workspace) return DSA_EINVAL;
-  if (N < 0 || Hi < 1 || P < 1 || keep < 1 || score_stride < P || !(scale > 0.0f)) return DSA_EINVAL;
+                       int tile_rows, void* stream) {
+  if (!q || !w || !k || !npool || !pools || !cnt || !vals || !workspace) return DSA_EINVAL;
+  if (N < 0 || Hi < 1 || P < 1 || keep < 1 || score_stride < P || tile_rows < 0 || !(scale > 0.0f))
+    return DSA_EINVAL;
   if (q_scale && !k_scale) return DSA_EUNSUPPORTED;  // FP8 queries take FP8 keys
   if (D != 128 || Hi > (k_scale ? 64 : 32)) return DSA_EUNSUPPORTED;
   if (!dsa::topk_supported(P, keep, 1)) return DSA_EUNSUPPORTED;
-  if (workspace_bytes < dsa_prefill_select_workspace_bytes(N, P, keep)) return DSA_EWORKSPACE;
+  const PrefillLayout L = prefill_layout(N, P, score_stride, keep, tile_rows, scores == nullptr);
+  if (workspace_bytes < L.total) return DSA_EWORKSPACE;
   if (N == 0) return DSA_OK;
-  hipStream_t s = static_cast<hipStream_t>(stream);
+  const hipStream_t a = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
-  const size_t t_need = align256(dsa::topk_workspace_bytes(N, P, keep));
-  int* idx = reinterpret_cast<int*>(ws + t_need);
-  int* cnt32 = reinterpret_cast<int*>(ws + t_need + align256((size_t)N * keep * 4));
-  // rows selected in two levels with sub-blocks of at most 16: the indexer writes the sub-block maxima
-  const int sub = dsa::topk_two_level_sub(P, keep);
-  const bool fuse = sub >= 2 && sub <= 16;
-  float* bm = fuse ? dsa::topk_bm_buffer(workspace, N) : nullptr;
-  const int sub_log2 = fuse ? __builtin_ctz((unsigned)sub) : 0;
-  const int nb = fuse ? (P + sub - 1) / sub : 0;
-  hipError_t e;
-  if (q_scale)
-    e = dsa::launch_indexer_prefill_fp8(static_cast<const uint8_t*>(q), q_scale, w, static_cast<const uint8_t*>(k),
-                                        k_scale, npool, scores, N, Hi, P, score_stride, scale, bm, sub_log2, nb, s);
-  else if (k_scale)
-    e = dsa::launch_indexer_prefill(static_cast<const uint16_t*>(q), w, static_cast<const uint8_t*>(k), k_scale, npool,
-                                    scores, N, Hi, P, score_stride, scale, bm, sub_log2, nb, s);
-  else
-    e = dsa::launch_indexer_prefill_bf16k(static_cast<const uint16_t*>(q), w, static_cast<const uint16_t*>(k), npool,
-                                          scores, N, Hi, P, score_stride, scale, bm, sub_log2, nb, s);
-  if (e != hipSuccess) return DSA_ELAUNCH;
-  return status(dsa::launch_prefill_topk(scores, npool, idx, cnt32, workspace, N, score_stride, P, keep, fuse, pools,
-                                         cnt, vals, s));
+  const size_t q_row = (size_t)Hi * D * (q_scale ? 1 : 2);  // bytes of one query's heads
+  // the generic selection (plan < 0): the indexer writes its sub-block maxima when the sub-blocks are small
+  const int gsub = L.plan < 0 ? dsa::topk_two_level_sub(P, keep) : 0;
+  const bool gfuse = gsub >= 2 && gsub <= 16;
+  int* gidx = reinterpret_cast<int*>(ws + L.gidx_off);
+  int* gcnt = reinterpret_cast<int*>(ws + L.gcnt_off);
+  // tiles alternate between the caller's stream and the library's second stream, each tile's scores then its
+  // selection on one stream: a tile's selection and the boundary of its scores kernel overlap the other stream's
+  // tile, and tile t + 2 reuses tile t's buffer set on the same stream (ordered after it without events)
+  AuxStream aux(L.plan >= 0 && L.tiles > 1);
+  hipError_t e = hipSuccess;
+  if (aux.ok && !aux.fork(a)) e = hipErrorUnknown;
+  // the generic selection's histograms start at zero: a shorter last tile (here or in an earlier call on this
+  // workspace) lays its row meta over the rows a full tile's histograms take
+  if (L.plan < 0) e = dsa::launch_fill_zero(workspace, dsa::topk_zero_bytes(L.T), a);
+  for (int t = 0; t < L.tiles && e == hipSuccess; ++t) {
+    const int r0 = t * L.T, rows = N - r0 < L.T ? N - r0 : L.T, set = t % L.sets;
+    const hipStream_t st = aux.ok && set == 1 ? aux.stream : a;
+    float* sc = scores ? scores + (size_t)r0 * score_stride
+                       : reinterpret_cast<float*>(ws + L.sc_off + (size_t)set * L.sc_bytes);
+    float* bm = nullptr;
+    int sub_log2 = 0, nb = 0;
+    if (L.plan > 0 || gfuse) {
+      const int sub = L.plan > 0 ? L.plan : gsub;
+      bm = L.plan > 0 ? reinterpret_cast<float*>(ws + L.bm_off + (size_t)set * L.bm_bytes)
+                      : dsa::topk_bm_buffer(workspace, rows);
+      sub_log2 = __builtin_ctz((unsigned)sub);
+      nb = (P + sub - 1) / sub;
+    }
+    const float* qs = q_scale ? q_scale + (size_t)r0 * Hi : nullptr;
+    const char* qt = static_cast<const char*>(q) + (size_t)r0 * q_row;
+    const float* wt = w + (size_t)r0 * Hi;
+    if (q_scale)
+      e = dsa::launch_indexer_prefill_fp8(reinterpret_cast<const uint8_t*>(qt), qs, wt,
+                                          static_cast<const uint8_t*>(k), k_scale, npool + r0, sc, rows, Hi, P,
+                                          score_stride, scale, bm, sub_log2, nb, st);
+    else if (k_scale)
+      e = dsa::launch_indexer_prefill(reinterpret_cast<const uint16_t*>(qt), wt, static_cast<const uint8_t*>(k),
+                                      k_scale, npool + r0, sc, rows, Hi, P, score_stride, scale, bm, sub_log2, nb,
+                                      st);
+    else
+      e = dsa::launch_indexer_prefill_bf16k(reinterpret_cast<const uint16_t*>(qt), wt,
+                                            static_cast<const uint16_t*>(k), npool + r0, sc, rows, Hi, P,
+                                            score_stride, scale, bm, sub_log2, nb, st);
+    if (e != hipSuccess) break;
+    if (L.plan >= 0) {
+      int* bidx = reinterpret_cast<int*>(ws + L.bidx_off + (size_t)set * L.bidx_bytes);
+      int* bcnt = reinterpret_cast<int*>(ws + L.bcnt_off + (size_t)set * L.bcnt_bytes);
+      e = dsa::launch_prefill_tile_topk(sc, score_stride, npool + r0, P, keep, bm, bidx, bcnt,
+                                        pools + (size_t)r0 * keep, cnt + r0, vals + (size_t)r0 * keep, rows, st);
+    } else {
+      e = dsa::launch_prefill_topk(sc, npool + r0, gidx, gcnt, workspace, rows, score_stride, P, keep, gfuse,
+                                   pools + (size_t)r0 * keep, cnt + r0, vals + (size_t)r0 * keep, a);
+    }
+  }
+  // the caller's stream waits for everything enqueued on the second stream, whatever failed
+  if (aux.ok && !aux.join(a) && e == hipSuccess) e = hipErrorUnknown;
+  // a failed generic selection may have left its histograms non-zero: clear them for the next call
+  if (e != hipSuccess && L.plan < 0) (void)dsa::launch_fill_zero(workspace, dsa::topk_zero_bytes(L.T), a);
+  return status(e);
 }
 
 int dsa_cache_write(const void* x, int x_fp32, const int64_t* slots, uint8_t* cache, float* scale, int n_rows, int W,
@@ -337,7 +493,7 @@ int dsa_topk_supported(int max_len, int keep, int vis_only) {
 
 int dsa_topk_mask(const int32_t* idx, const int32_t* cnt, const float* scores, float* mask, int B, int keep, int P,
                   int kp, int tail, void* stream) {
-  if (!idx || !cnt || !mask || (tail && !scores)) return DSA_EINVAL;
+  if (!idx != !cnt || !mask || (tail && !scores)) return DSA_EINVAL;
   if (B < 0 || keep < 1 || P < 1 || kp < 1 || (long)P * kp > 0x7fffffffL) return DSA_EINVAL;
   if (B == 0) return DSA_OK;
   return status(dsa::launch_topk_mask(idx, cnt, scores, mask, B, keep, P, kp, tail != 0,

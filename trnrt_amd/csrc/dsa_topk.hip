@@ -821,15 +821,16 @@ __global__ void gather_blocks_kernel(const float* __restrict__ scores, int strid
 }
 
 // The mask's background: NEG_INF, or with tail 0 for every token of a non-candidate score (score <= VISIBLE, the
-// reference's `sel | ~vis`, trnrt/kernels/dsa_topk.py:89-93), kp tokens per score.
+// reference's `sel | ~vis`, trnrt/kernels/dsa_topk.py:89-93), kp tokens per score. all (keep >= P, dsa_topk.py:
+// 103-105): 0 for every visible score too (every score when scores is null), and no scatter follows.
 __global__ void topk_mask_fill_kernel(const float* __restrict__ scores, float* __restrict__ mask, int P, int kp,
-                                      int tail) {
+                                      int tail, int all) {
   const int row = blockIdx.y;
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= P * kp) return;
-  float v = NEG_INF;
-  if (tail && !(scores[(size_t)row * P + i / kp] > VISIBLE)) v = 0.0f;
-  mask[(size_t)row * P * kp + i] = v;
+  const bool vis = scores == nullptr || scores[(size_t)row * P + i / kp] > VISIBLE;
+  const bool taken = (all && vis) || (tail && !vis);
+  mask[(size_t)row * P * kp + i] = taken ? 0.0f : NEG_INF;
 }
 
 // 0 for the kp tokens of every selected score.
@@ -1223,6 +1224,48 @@ hipError_t launch_prefill_topk(const float* scores, const int* len, int* idx, in
   return topk_rows(scores, stride, len, 1, 1, n, keep, 1, idx, cnt, tb, false, p, B, s, bm_ready, &out);
 }
 
+// The prefill selection of one tile of rows through the one-workgroup-per-row kernels only (whatever the tile's row
+// count), so that it needs none of the chunked kernels' buffers (histograms, row meta, candidate keys). The plan of
+// rows of at most n scores in rows of `stride`: 0 flat (n <= TOPK_FLAT_MAX: one kernel writing the reference's
+// outputs); sub in {4, 8, 16} two levels, the first over the sub-block maxima [rows, ceil(n / sub)] that the indexer
+// wrote, the second reading the selected sub-blocks' scores in place (IND); -1 neither (launch_prefill_topk's generic
+// form over a workspace of topk_workspace_bytes).
+int prefill_tile_plan(long n, int stride, int keep) {
+  if (n <= TOPK_FLAT_MAX) return 0;
+  if (keep > TOPK_LONG_KEEP_MAX) return -1;
+  const int sub = topk_sub_block(n, keep);
+  const long nb = (n + sub - 1) / sub, nc = (long)keep * sub;
+  if (sub < 4 || sub > 16 || (stride & 3) || nb > TOPK_FLAT_MAX || nc > TOPK_FLAT_MAX || nc >= n) return -1;
+  return sub;
+}
+
+// One tile (T rows) of a plan >= 0 selection: scores [T, stride] with lengths len[T]; plan > 0: bm [T, nb] the
+// sub-block maxima (row stride nb = ceil(n / sub)), bidx [T, keep] and bcnt [T] the first level's output. Writes
+// pools / cnt64 / vals [T, ...] as launch_prefill_topk does.
+hipError_t launch_prefill_tile_topk(const float* scores, int stride, const int* len, long n, int keep,
+                                    const float* bm, int* bidx, int* bcnt, int64_t* pools, int64_t* cnt64,
+                                    float* vals, int T, hipStream_t s) {
+  const SlotOut none = {nullptr, 0, 0, 0, nullptr};
+  const int plan = prefill_tile_plan(n, stride, keep);
+  if (plan < 0) return hipErrorInvalidValue;
+  if (plan == 0) {
+    const IndOut io = {nullptr, 0, nullptr, nullptr, nullptr, 0, pools, cnt64, vals};
+    return (stride & 3) == 0 ? launch_topk_many_rows<true>(scores, stride, len, 1, 1, (int)n, keep, 1, nullptr,
+                                                           nullptr, nullptr, none, T, s, &io)
+                             : launch_topk_many_rows<false>(scores, stride, len, 1, 1, (int)n, keep, 1, nullptr,
+                                                            nullptr, nullptr, none, T, s, &io);
+  }
+  const int sub = plan, nb = (int)((n + sub - 1) / sub), nc = keep * sub;
+  // level 1: the top-keep sub-blocks of each row (ceil(len / sub) maxima)
+  hipError_t e = (nb & 3) == 0 ? launch_topk_many_rows<true>(bm, nb, len, sub, 1, nb, keep, 1, nullptr, bidx, bcnt,
+                                                             none, T, s)
+                               : launch_topk_many_rows<false>(bm, nb, len, sub, 1, nb, keep, 1, nullptr, bidx, bcnt,
+                                                              none, T, s);
+  if (e != hipSuccess) return e;
+  const IndOut io = {scores, stride, len, bidx, bcnt, sub, pools, cnt64, vals};
+  return launch_topk_ind(nc, keep, 1, io, T, s);
+}
+
 // Zero-fills a workspace (a kernel, not a memset, so that callers may capture it in a graph).
 __global__ void fill_zero_kernel(uint4* __restrict__ p, size_t n16) {
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n16; i += (size_t)gridDim.x * blockDim.x)
@@ -1240,9 +1283,10 @@ hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t s) {
 
 hipError_t launch_topk_mask(const int* idx, const int* cnt, const float* scores, float* mask, int B, int keep, int P,
                             int kp, int tail, hipStream_t s) {
+  const int all = idx == nullptr;
   hipError_t e = launch("topk_mask_fill_kernel", topk_mask_fill_kernel, dim3((P * kp + 255) / 256, B), dim3(256), s,
-                        scores, mask, P, kp, tail);
-  if (e != hipSuccess) return e;
+                        scores, mask, P, kp, tail, all);
+  if (e != hipSuccess || all) return e;
   return launch("topk_mask_scatter_kernel", topk_mask_scatter_kernel, dim3((keep + 255) / 256, B), dim3(256), s, idx,
                 cnt, mask, keep, P, kp);
 }

@@ -127,16 +127,24 @@ def value_order(pools: torch.Tensor, cnt: torch.Tensor, vals: torch.Tensor):
     return op, cnt, ov
 
 
+def workspace_bytes(N: int, P: int, keep: int, tile_rows: int = 0) -> int:
+    """Workspace bytes of select() over N queries and P keys (its score tiles included)."""
+    return int(_lib.lib().dsa_prefill_select_workspace_bytes(N, P, P, keep, tile_rows, 1))
+
+
 def select(qI: torch.Tensor, w: torch.Tensor, pk: torch.Tensor, npool: torch.Tensor, keep: int, scale: float,
            sub: int | None = None, vorder: bool = False, *, pk_scale: torch.Tensor | None = None,
-           qI_scale: torch.Tensor | None = None,
-           workspace: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+           qI_scale: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+           tile_rows: int = 0) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """(pools [N, keep] int64 ascending, 0 past the count; count [N] int64; scores [N, keep] fp32, NEG_INF past the
     count) (trnrt/kernels/dsa_long_select.py:494-528 `select`): the scores above (FP8 queries with qI_scale as there),
     then the exact top-keep per query, in one call of dsa_prefill_select (the indexer writes the two-level
-    selection's sub-block maxima, and the selection writes the reference's outputs directly).
+    selection's sub-block maxima, and the selection writes the reference's outputs directly). The queries go in
+    tiles of tile_rows (0: score tiles of at most 64 MiB), only two tiles' scores held at once (the reference's
+    per-tile form, trnrt/kernels/dsa_long_pipe.py:15-25), tiles alternating between the current stream and the
+    library's second stream so that one tile's selection overlaps the next tile's scores.
     vorder: the pools in (score descending, pool ascending) order instead. sub is accepted and ignored. workspace:
-    dsa_prefill_select_workspace_bytes(N, P, keep) bytes, zero-filled before its first use (calls leave it so)."""
+    workspace_bytes(N, P, keep, tile_rows) bytes, zero-filled before its first use (calls leave it so)."""
     del sub
     dev = C.on_gpu(qI, w, pk, pk_scale, npool, qI_scale, workspace)
     fp8_q = qI.dtype in (C.FP8, torch.uint8)
@@ -160,18 +168,18 @@ def select(qI: torch.Tensor, w: torch.Tensor, pk: torch.Tensor, npool: torch.Ten
         qI_scale = C.need(C.as_f32(qI_scale), "qI_scale", torch.float32, (N, Hi))
     else:
         qI = C.as_bf16(qI)
+    if tile_rows < 0:
+        raise ValueError(f"dsa_long_select: tile_rows {tile_rows}")
     lib = _lib.lib()
-    wsb = int(lib.dsa_prefill_select_workspace_bytes(N, P, keep))
     if workspace is None:
-        workspace = torch.zeros(wsb, dtype=torch.uint8, device=dev)
+        workspace = torch.zeros(workspace_bytes(N, P, keep, tile_rows), dtype=torch.uint8, device=dev)
     ws_len = workspace.numel() * workspace.element_size()
-    sc = torch.empty(N, P, dtype=torch.float32, device=dev)
     pools = torch.empty(N, keep, dtype=torch.int64, device=dev)
     cnt = torch.empty(N, dtype=torch.int64, device=dev)
     vals = torch.empty(N, keep, dtype=torch.float32, device=dev)
     st = lib.dsa_prefill_select(C.ptr(qI), C.ptr(qI_scale), C.ptr(w), C.ptr(pk), C.ptr(pk_scale), C.ptr(npool),
-                                C.ptr(sc), C.ptr(pools), C.ptr(cnt), C.ptr(vals), C.ptr(workspace), ws_len, N, Hi, D,
-                                P, P, keep, float(scale), C.stream_ptr(dev))
+                                None, C.ptr(pools), C.ptr(cnt), C.ptr(vals), C.ptr(workspace), ws_len, N, Hi, D,
+                                P, P, keep, float(scale), int(tile_rows), C.stream_ptr(dev))
     _lib.check(st, "dsa_long_select.select")
     if vorder:
         return value_order(pools, cnt, vals)

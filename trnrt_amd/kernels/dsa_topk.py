@@ -81,11 +81,15 @@ def select(scores: torch.Tensor, keep: int, vis_only: bool = True, group: bool =
         R *= d
     s = C.as_f32(scores).reshape(R, P)
     dev = C.on_gpu(s)
-    if keep >= P:
-        # every selectable score: the reference's short-cut (dsa_topk.py:510-511), here as a selection of P
-        keep = P
-    idx, cnt = select_indices(s, keep, vis_only=vis_only)
     mask = torch.empty(R, P * kp, dtype=torch.float32, device=dev)
+    if keep >= P:
+        # every selectable score, no selection run (the reference's short-cut, dsa_topk.py:510-511 and 103-105):
+        # the visible scores with vis_only, else every score
+        st = _lib.lib().dsa_topk_mask(None, None, C.ptr(s) if vis_only else None, C.ptr(mask), R, P, P, kp,
+                                      int(tail), C.stream_ptr(dev))
+        _lib.check(st, "dsa_topk.select")
+        return mask.reshape(*lead, P * kp)
+    idx, cnt = select_indices(s, keep, vis_only=vis_only)
     st = _lib.lib().dsa_topk_mask(C.ptr(idx), C.ptr(cnt), C.ptr(s) if tail else None, C.ptr(mask), R, keep, P, kp,
                                   int(tail), C.stream_ptr(dev))
     _lib.check(st, "dsa_topk.select")
