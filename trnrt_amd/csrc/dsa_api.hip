@@ -54,6 +54,12 @@ size_t topk_hist_bytes(int B);
 size_t topk_zero_bytes(int B);
 bool fused_layer_ok(int num_cu, int Hi, int H, int max_len, int keep, int page_size, int stride);
 size_t fused_layer_bytes(size_t zero_bytes, int B, int H, int keep);
+bool attend_xcd_ok(int num_cu, int H, int keep);
+size_t attend_xcd_bytes(int B, int H, int keep);
+hipError_t launch_decode_attend(const uint16_t* q, const uint8_t* kv, const float* kvs, const int* rows,
+                                const int* idx, const int* table, const int* cnt, uint16_t* out, float* lse, void* ws,
+                                int* sync, int B, int H, int max_pages, int page_size, int num_pages, int keep,
+                                float scale, hipStream_t s);
 hipError_t launch_decode_fused(const uint16_t* q_idx, const float* w, const uint8_t* k, const float* ks,
                                const uint16_t* q, const uint8_t* kv, const float* kvs, const int* table,
                                const int* ctx_len, float* scores, int* idx, int* cnt, uint16_t* out, float* lse,
@@ -607,9 +613,13 @@ size_t dsa_workspace_bytes(int kind, int B, int H, int keep, int max_len, int sp
     a = dsa::attention_workspace_bytes(B, H, sp);
   }
   size_t total = align256(t) + align256(a);
-  if (kind == DSA_WS_LAYER) {  // the one-launch layer's layout shares the zero region and needs its own rest
+  if (kind == DSA_WS_LAYER) {
+    // the one-launch layer's layout shares the zero region and needs its own rest; the separate kernels' XCD-local
+    // attention takes the attention's place
     const size_t f = dsa::fused_layer_bytes(dsa::topk_zero_bytes(B), B, H, keep);
+    const size_t x = align256(t) + align256(dsa::attend_xcd_bytes(B, H, keep));
     total = f > total ? f : total;
+    total = x > total ? x : total;
   }
   return total;
 }
@@ -689,6 +699,14 @@ int dsa_decode_layer_chain(const void* q_idx_bf16, const float* w, const uint8_t
   }
   char* aws = static_cast<char*>(workspace) + t_need + layer_rows_bytes(B, keep);
   const size_t aws_bytes = workspace_bytes - t_need - layer_rows_bytes(B, keep);
+  // the default split count on a GPU of 8 XCDs x 32 CUs: the one-launch layer's attention and combine as a launch of
+  // their own (XCD-local, bf16 split outputs), over the slot rows (flat rows) or the positions through the page table
+  if (splits == 0 && dsa::attend_xcd_ok(num_cu(), H, keep))
+    return status(dsa::launch_decode_attend(static_cast<const uint16_t*>(q_bf16), kv_fp8, kv_scale, rows,
+                                            rows ? nullptr : idx, page_table, cnt, static_cast<uint16_t*>(out_bf16),
+                                            lse, aws, reinterpret_cast<int*>(static_cast<char*>(workspace) +
+                                                                             dsa::topk_hist_bytes(B)),
+                                            B, H, max_pages, page_size, num_pages, keep, scale, s));
   if (!rows)
     return dsa_sparse_mla_decode(q_bf16, kv_fp8, kv_scale, idx, cnt, page_table, nullptr, nullptr, out_bf16, nullptr,
                                  lse, aws, aws_bytes, B, H, 576, 512, keep, max_pages, page_size, num_pages, scale,

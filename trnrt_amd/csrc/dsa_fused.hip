@@ -45,6 +45,7 @@ constexpr int FU_MAXLEN = FU_NW * FU_KEYS;            // 32,768
 constexpr int FU_D = 128;                             // indexer head dim
 constexpr int FU_QROW = FU_D + 8;                     // staged indexer query row (bf16)
 constexpr int FU_HBINS = HIST_BINS;
+constexpr int FU_BUF_WORD3 = 0x00020000;  // buffer descriptor word 3 of raw dword loads (gfx9)
 constexpr int FU_BMW = FU_KEYS / 32;    // words of a workgroup's bitmap of positions
 // A workgroup's bin list: its count of nonzero histogram bins, then (bin << 16) | count for each
 constexpr int FU_HROW = 1056;
@@ -747,12 +748,19 @@ __device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int 
   // u / 37, piece u % 37; the padding piece re-reads the last data piece); the loads of the padded rows' units spread
   // over the 8 waves
   {
+    // unit u = 64 k + lane's row u / 37 and piece u % 37, advanced with k (by 8: u by 512 = 13 x 37 + 31)
+    constexpr int DR = FU_WAVES * WAVE / FU_KPIECES, DP = FU_WAVES * WAVE % FU_KPIECES;
     const int units = padded * FU_KPIECES;
+    int row = (WAVE * wave + lane) / FU_KPIECES, pc = WAVE * wave + lane - row * FU_KPIECES;
     for (int k = wave; k * WAVE < units; k += FU_WAVES) {
-      const int u = WAVE * k + lane;
-      const int row = u / FU_KPIECES, pc = u - row * FU_KPIECES;
-      const uint8_t* src = a.kv + (size_t)slot_l[row] * FU_DQK + 16 * (pc < FU_PIECES ? pc : FU_PIECES - 1);
+      const uint8_t* src = a.kv + (size_t)slot_l[row] * FU_DQK + 16 * min(pc, FU_PIECES - 1);
       __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(kt + 1024 * k), 16, 0, 0);
+      row += DR;
+      pc += DP;
+      if (pc >= FU_KPIECES) {
+        pc -= FU_KPIECES;
+        ++row;
+      }
     }
   }
   const float ksv = tid < padded ? a.kvs[slot] : 0.0f;
@@ -874,7 +882,7 @@ __device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int 
         l += r[t];
         mh = max_nonan(mh, mr[t]);
       }
-      inv[i] = 1.0f / l;
+      inv[i] = __builtin_amdgcn_rcpf(l);  // l >= 1 (the split's maximum contributes exp(0))
       if (wave == 0 && l16 == 0) mlp[hl * a.S] = make_float2(mh, l);
     }
 #pragma unroll
@@ -903,10 +911,14 @@ __device__ __forceinline__ void fu_combine_heads(const FusedArgs& a, float* wts,
   const int hh = h0 + (lane >> 5), sp = lane & 31;
   uint64_t mlv = 0;
   if (tid < WAVE) mlv = ld_sc1_64(a.ml + ((size_t)b * H + hh) * S + min(sp, S - 1));
+  // the two heads' split outputs through a buffer descriptor: split k's offset is scalar, the lane's is 32-bit
+  const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.part + ((size_t)b * H + h0) * S * FU_DV), (short)0, 2 * 2 * S * FU_DV, FU_BUF_WORD3);
+  const int voff = 2 * ((tid >> 8) * S * FU_DV + d);
   uint32_t ov[NS];
 #pragma unroll
   for (int k = 0; k < NS; ++k)
-    ov[k] = ld_sc1(reinterpret_cast<const uint32_t*>(a.part + (((size_t)b * H + h) * S + min(k, S - 1)) * FU_DV + d));
+    ov[k] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(prs, voff, 2 * FU_DV * min(k, S - 1), FU_AUX_SC1);
   if (tid < WAVE) {
     const float m = __uint_as_float((uint32_t)mlv), l = __uint_as_float((uint32_t)(mlv >> 32));
     const bool live = sp < S && l > 0.0f;
@@ -915,7 +927,7 @@ __device__ __forceinline__ void fu_combine_heads(const FusedArgs& a, float* wts,
     const float wt = live ? l * __expf(m - M) : 0.0f;
     float W = row_sum(wt);
     W += __shfl_xor(W, 16, WAVE);
-    wts[lane] = wt / W;
+    wts[lane] = wt * __builtin_amdgcn_rcpf(W);  // W >= 1 (the largest split's weight is its sum)
     if (sp == 0 && a.lse) a.lse[(size_t)b * H + hh] = M + __logf(W);
   }
   __syncthreads();
@@ -941,6 +953,21 @@ __device__ __forceinline__ void fu_combine(const FusedArgs& a, uint8_t* lds, int
   }
 }
 
+// A workgroup's end: the last workgroup of the XCD to finish resets its barrier words (no workgroup polls them any
+// more).
+__device__ __forceinline__ void fu_exit(int* sync) {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned* wd = reinterpret_cast<unsigned*>(sync);
+    const unsigned e = __hip_atomic_fetch_add(wd + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (e == FU_NW - 1) {
+      __hip_atomic_store(wd, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(wd + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
 template <int MT, int HPW>
 __global__ __launch_bounds__(FU_THREADS, 1) void decode_fused_kernel(FusedArgs a) {
   __shared__ __align__(16) uint8_t lds[FU_LDS];
@@ -961,17 +988,77 @@ __global__ __launch_bounds__(FU_THREADS, 1) void decode_fused_kernel(FusedArgs a
   fu_attend<HPW>(a, lds, b, j, n_slots, live_bias);
   fu_barrier(sync, 3);  // C: every split's output
   fu_combine(a, lds, b, j);
-  // the last workgroup of the XCD to finish resets its barrier words (no workgroup polls them any more)
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    unsigned* wd = reinterpret_cast<unsigned*>(sync);
-    const unsigned e = __hip_atomic_fetch_add(wd + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (e == FU_NW - 1) {
-      __hip_atomic_store(wd, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(wd + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  fu_exit(sync);
+}
+
+// The split's slot list when the selection came from the separate kernels: output positions o0 .. o1 - 1 of row b,
+// as cache rows (rows [B, keep], the top-k's slot output) or as positions (idx [B, keep]) through the page table;
+// the attention's queries staged in LDS as stage 2 stages them. Returns the split's selected count (the empty row:
+// output 0, masked, as stage 2).
+template <int HPW>
+__device__ __forceinline__ int fu_attend_prep(const FusedArgs& a, const int* rows, uint8_t* lds, int b, int j,
+                                              float* live_bias) {
+  using AT = FuAtt<HPW>;
+  constexpr int QPT = AT::QPT;
+  int* slot_l = reinterpret_cast<int*>(lds + AT::L_P);
+  const int tid = threadIdx.x;
+  const int hg = j % a.HG, s = j / a.HG;
+  const bool active = s < a.S;
+  const int o0 = active ? s * a.sps : 0, o1 = active ? min(o0 + a.sps, a.keep) : 0;
+  const int cnt_row = min(max(a.cnt[b], 0), a.keep);
+  u32x4 qv[QPT];
+  if (active) {
+    const u32x4* qsrc = reinterpret_cast<const u32x4*>(a.q + ((size_t)b * a.H + HPW * hg) * FU_DQK);
+#pragma unroll
+    for (int i = 0; i < QPT; ++i) qv[i] = qsrc[min(tid + FU_THREADS * i, HPW * FU_DQK / 8 - 1)];
+  }
+  const int o = o0 + tid;
+  int sl = 0;
+  if (tid < AT::SPLIT && o < o1 && o < max(cnt_row, 1)) {  // the empty row lists output 0 (position 0)
+    if (rows) {
+      sl = rows[(size_t)b * a.keep + o];
+    } else {
+      const int p = max(a.idx[(size_t)b * a.keep + o], 0), pi = p / a.page_size;  // pages of any size
+      const int pg = a.table[(size_t)b * a.max_pages + min(pi, a.max_pages - 1)];
+      sl = safe_page(pg, a.num_pages) * a.page_size + (p - pi * a.page_size);
+    }
+    sl = (unsigned)sl < (unsigned)a.num_slots ? sl : 0;
+  }
+  if (active) {
+    uint16_t* qs = reinterpret_cast<uint16_t*>(lds + AT::L_QST);
+#pragma unroll
+    for (int i = 0; i < QPT; ++i) {
+      const int pc = tid + FU_THREADS * i;
+      if (pc < HPW * FU_DQK / 8)
+        *reinterpret_cast<u32x4*>(qs + (pc / (FU_DQK / 8)) * FU_AQROW + 8 * (pc % (FU_DQK / 8))) = qv[i];
     }
   }
+  if (tid < AT::SPLIT) slot_l[tid] = sl;  // padding rows read slot 0
+  int n_slots = max(min(o1, cnt_row) - o0, 0);
+  *live_bias = 0.0f;
+  if (active && cnt_row == 0 && s == 0) {
+    n_slots = 1;
+    *live_bias = NEG_INF;
+  }
+  __syncthreads();  // the slot list and the queries
+  return n_slots;
+}
+
+// The attention and combine stages of the one-launch layer as a launch of their own, after the separate kernels'
+// selection (rows of any length): row row0 + x on XCD x, the same splits, bf16 split outputs and XCD-local barrier.
+template <int HPW>
+__global__ __launch_bounds__(FU_THREADS, 1) void decode_attend_kernel(FusedArgs a, const int* rows) {
+  __shared__ __align__(16) uint8_t lds[FU_LDS];
+  const int x = blockIdx.x % FU_XCDS, j = blockIdx.x / FU_XCDS;
+  int* sync = a.sync + x * FU_SYNC_WORDS;
+  const int b = a.row0 + x;
+  if (b >= a.B) return;  // an XCD without a row
+  float live_bias;
+  const int n_slots = fu_attend_prep<HPW>(a, rows, lds, b, j, &live_bias);
+  fu_attend<HPW>(a, lds, b, j, n_slots, live_bias);
+  fu_barrier(sync, 1);  // every split's output
+  fu_combine(a, lds, b, j);
+  fu_exit(sync);
 }
 
 // ---- host side ----
@@ -1018,6 +1105,60 @@ size_t fused_layer_bytes(size_t zero_bytes, int B, int H, int keep) {
   const int hpw = keep >= 1 ? fused_hpw(H, keep) : 0;
   if (!hpw) return 0;
   return fused_layout(zero_bytes, B, H, fused_splits(H, hpw), keep).end;
+}
+
+// The separate attention launch (decode_attend_kernel): whether it takes the shape, and its workspace (the split
+// outputs and their (max, sum)).
+bool attend_xcd_ok(int num_cu, int H, int keep) { return num_cu == FU_XCDS * FU_NW && keep >= 1 && fused_hpw(H, keep); }
+
+size_t attend_xcd_bytes(int B, int H, int keep) {
+  const int hpw = keep >= 1 ? fused_hpw(H, keep) : 0;
+  if (!hpw) return 0;
+  const FusedLayout l = fused_layout(0, B, H, fused_splits(H, hpw), keep);
+  return l.end - l.part;
+}
+
+hipError_t launch_decode_attend(const uint16_t* q, const uint8_t* kv, const float* kvs, const int* rows,
+                                const int* idx, const int* table, const int* cnt, uint16_t* out, float* lse, void* ws,
+                                int* sync, int B, int H, int max_pages, int page_size, int num_pages, int keep,
+                                float scale, hipStream_t s) {
+  FusedArgs a{};
+  const int hpw = fused_hpw(H, keep);
+  if (!hpw || (!rows && (!idx || !table))) return hipErrorInvalidValue;
+  const int S = fused_splits(H, hpw);
+  const FusedLayout l = fused_layout(0, B, H, S, keep);
+  char* p = static_cast<char*>(ws) - l.part;
+  a.q = q;
+  a.kv = kv;
+  a.kvs = kvs;
+  a.table = table;
+  a.idx = const_cast<int*>(idx);
+  a.cnt = const_cast<int*>(cnt);
+  a.out = out;
+  a.lse = lse;
+  a.sync = sync;
+  a.part = reinterpret_cast<uint16_t*>(p + l.part);
+  a.ml = reinterpret_cast<float2*>(p + l.ml);
+  a.B = B;
+  a.H = H;
+  a.max_pages = max_pages;
+  a.page_size = page_size;
+  a.num_pages = num_pages;
+  a.num_slots = num_pages * page_size;
+  a.keep = keep;
+  a.scale = scale;
+  a.HG = H / hpw;
+  a.S = S;
+  int sps = (keep + S - 1) / S;
+  a.sps = (sps + FU_CH - 1) / FU_CH * FU_CH;
+  const dim3 grid(FU_XCDS * FU_NW), block(FU_THREADS);
+  for (int r0 = 0; r0 < B; r0 += FU_XCDS) {
+    a.row0 = r0;
+    const hipError_t e = hpw == 32 ? launch("decode_attend_kernel", decode_attend_kernel<32>, grid, block, s, a, rows)
+                                   : launch("decode_attend_kernel", decode_attend_kernel<16>, grid, block, s, a, rows);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 hipError_t launch_decode_fused(const uint16_t* q_idx, const float* w, const uint8_t* k, const float* ks,
