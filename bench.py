@@ -639,8 +639,10 @@ def main() -> int:
         # the one-launch layer (rows of up to 32K tokens): its launches together move the layer's algorithmic bytes
         kname, kbytes = "decode_fused_kernel", layer_bytes
     else:
-        # the separate-kernel layer: the indexer, the kernel that streams the whole key cache
-        kname, kbytes = "indexer_decode_kernel", _indexer_bytes(lengths, cfg.Hi, cfg.page_size)
+        # the separate-kernel layer: the indexer, the kernel that streams the whole key cache (its streaming form
+        # past 32K tokens)
+        kname = "indexer_decode_long_kernel" if "indexer_decode_long_kernel" in k_us else "indexer_decode_kernel"
+        kbytes = _indexer_bytes(lengths, cfg.Hi, cfg.page_size)
     k_time = k_us[kname]
     achieved = kbytes / (k_time * 1e-6) / 1e9
 

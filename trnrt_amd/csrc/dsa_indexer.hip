@@ -35,6 +35,11 @@ __device__ __forceinline__ float crow_value(const float* cand, int b, int stride
 
 constexpr int IDX_AHEAD = 1;  // key tiles a wave has in flight ahead of the one it computes (1, 2 and 3 measured)
 
+hipError_t launch_indexer_decode_long(const uint16_t* q, const float* w, const uint8_t* k, const float* ks,
+                                      const int* table, const int* ctx_len, float* scores, float* bm, int sub_log2,
+                                      int nb, int B, int Hi, int max_pages, int page_size, int num_pages, int stride,
+                                      int num_cu, hipStream_t s);
+
 // One 32-key tile's loads for lane (key j, half h): 64 key bytes (dims 64h .. 64h + 63) and the key's scale (a tile
 // past the context reads the null page: every load is unconditional, so the waits count exactly).
 template <bool CAND>
@@ -191,6 +196,168 @@ __global__ __launch_bounds__(IDX_THREADS, 2) void indexer_decode_kernel(
   }
 }
 
+// Long rows (the separate kernels' indexer past 32,768 tokens): the same wave layout and arithmetic, but each wave
+// streams TW consecutive tiles (up to 64, the launch choosing TW so that about two workgroups per CU cover the batch)
+// through a ring of IL_AHEAD + 1 register tiles, IL_AHEAD in flight ahead of the one it computes, so the row's queries
+// are staged once per workgroup for up to 8,192 keys instead of 512 and the memory stream runs without the
+// workgroups' start-up gaps. The wave's page ids are one load per lane (tile tw0 + lane). BM: also the two-level top-k's
+// first-level sub-block maxima, bm[b, p / sub] = the maximum of the scores of positions p .. p + sub - 1 (sub a power
+// of two up to 32: a tile's 32 keys hold whole sub-blocks), for p < nb sub.
+constexpr int IL_AHEAD = 2;
+constexpr int IL_RING = IL_AHEAD + 1;
+constexpr int IL_TW_MAX = 64;
+
+template <int MT, bool BM>
+__global__ __launch_bounds__(IDX_THREADS, 2) void indexer_decode_long_kernel(
+    const uint16_t* __restrict__ q, const float* __restrict__ w, const uint8_t* __restrict__ kcache,
+    const float* __restrict__ kscale, const int* __restrict__ table, const int* __restrict__ ctx_len,
+    float* __restrict__ scores, float* __restrict__ bm, int sub_log2, int nb, int Hi, int max_pages, int page_size,
+    int num_pages, int stride, int TW, int wgs_per_row) {
+  __shared__ uint16_t qs[32 * MT * IDX_QROW];
+  __shared__ float ws[32 * MT];
+  const int b = blockIdx.x / wgs_per_row;
+  const int grp = blockIdx.x - b * wgs_per_row;
+  const int wave = threadIdx.x / WAVE;
+  const int lane = threadIdx.x & (WAVE - 1);
+  const int j = lane & 31, h = lane >> 5;
+  const int tiles_row = (stride + IDX_TILE - 1) / IDX_TILE;
+  const int L = ctx_len ? min(max(ctx_len[b], 0), stride) : stride;
+  const int tw0 = (grp * IDX_WAVES + wave) * TW;  // this wave's first tile
+  const int n_t = max(min(TW, tiles_row - tw0), 0);  // its tiles in the row
+  const int n_live = max(min(n_t, (L + IDX_TILE - 1) / IDX_TILE - tw0), 0);  // those with keys of the context
+  float* srow = scores + (size_t)b * stride;
+
+  constexpr int QPT = 32 * MT * (IDX_D / 8) / IDX_THREADS;
+  uint4 qv[QPT];
+#pragma unroll
+  for (int r = 0; r < QPT; ++r) {
+    const int i = threadIdx.x + r * IDX_THREADS;
+    const int head = i / (IDX_D / 8), c = i - head * (IDX_D / 8);
+    qv[r] = *reinterpret_cast<const uint4*>(q + ((size_t)b * Hi + min(head, Hi - 1)) * IDX_D + 8 * c);
+  }
+  const float wv = w[(size_t)b * Hi + min((int)threadIdx.x, Hi - 1)];
+  int pages;  // lane i: the page of tile tw0 + i (0, the null page, past the context)
+  {
+    const int t = tw0 + lane;
+    const int pg = table[(size_t)b * max_pages + min(t * IDX_TILE / page_size, max_pages - 1)];
+    pages = t * IDX_TILE < L ? safe_page(pg, num_pages) : 0;
+  }
+  u32x4 kv[IL_RING][4];
+  float ksc[IL_RING], kc_unused;
+#pragma unroll
+  for (int r = 0; r < IL_AHEAD; ++r)
+    indexer_tile_loads<false>(kcache, kscale, nullptr, __shfl(pages, r, WAVE), (tw0 + r) * IDX_TILE, L, b, stride,
+                              page_size, j, h, kv[r], ksc[r], kc_unused);
+#pragma unroll
+  for (int r = 0; r < QPT; ++r) {
+    const int i = threadIdx.x + r * IDX_THREADS;
+    const int head = i / (IDX_D / 8), c = i - head * (IDX_D / 8);
+    *reinterpret_cast<uint4*>(&qs[head * IDX_QROW + 8 * c]) = head < Hi ? qv[r] : make_uint4(0, 0, 0, 0);
+  }
+  if (threadIdx.x < 32 * MT) ws[threadIdx.x] = (int)threadIdx.x < Hi ? wv : 0.0f;
+  __syncthreads();
+  bf16x8 qa[MT][8];
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+      qa[m][s] = as_bf16x8(*reinterpret_cast<const uint4*>(&qs[(32 * m + j) * IDX_QROW + 64 * h + 8 * s]));
+  float wr[MT][16];
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) wr[m][r] = ws[32 * m + 8 * (r >> 2) + 4 * h + (r & 3)];
+  const int sub = 1 << sub_log2;
+
+  for (int i0 = 0; i0 < n_live; i0 += IL_RING) {
+#pragma unroll
+    for (int r = 0; r < IL_RING; ++r) {
+      const int i = i0 + r;  // ring slot r
+      if (i >= n_live) break;  // wave-uniform
+      // tile i has arrived (the IL_AHEAD - 1 tiles after it and the last tiles' stores may still be out): issue tile
+      // i + IL_AHEAD into the slot tile i - 1 left (a tile past the wave's range reads its keys, unused); the
+      // compiler's own wait before tile i's first use keeps the data exact whatever this count admits
+      __builtin_amdgcn_s_waitcnt(vmcnt_wait(5 * (IL_AHEAD - 1) + (BM ? 2 : 1) * IL_AHEAD));
+      __builtin_amdgcn_sched_barrier(0);
+      {
+        const int ia = i + IL_AHEAD;
+        const int pa = ia < IL_TW_MAX ? __shfl(pages, ia, WAVE) : 0;
+        indexer_tile_loads<false>(kcache, kscale, nullptr, pa, (tw0 + ia) * IDX_TILE, L, b, stride, page_size, j,
+                                  h, kv[(r + IL_AHEAD) % IL_RING], ksc[(r + IL_AHEAD) % IL_RING], kc_unused);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      const int pos = (tw0 + i) * IDX_TILE + j;
+      f32x16 acc[MT];
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int x = 0; x < 16; ++x) acc[m][x] = 0.0f;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const u32x4 k4 = kv[r][s >> 1];
+        const bf16x8 kb = (s & 1) ? fp8x8_to_bf16x8(k4[2], k4[3]) : fp8x8_to_bf16x8(k4[0], k4[1]);
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa[m][s], kb, acc[m], 0, 0, 0);
+      }
+      float part = 0.0f;
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int x = 0; x < 16; ++x) part = fmaf(wr[m][x], relu(acc[m][x]), part);
+      part += __shfl_xor(part, 32, WAVE);
+      const float v = pos < L ? part * ksc[r] : NEG_INF;
+      if (h == 0 && pos < stride) srow[pos] = v;
+      if (BM) {
+        float mx = v;
+        for (int d = 1; d < sub; d <<= 1) mx = max_nonan(mx, __shfl_xor(mx, d, WAVE));
+        if (h == 0 && (j & (sub - 1)) == 0 && (pos >> sub_log2) < nb) bm[(size_t)b * nb + (pos >> sub_log2)] = mx;
+      }
+    }
+  }
+  // the wave's tiles past the context: NEG_INF (and their sub-block maxima)
+  for (int e = lane; e < (n_t - n_live) * IDX_TILE; e += WAVE) {
+    const int pos = (tw0 + n_live) * IDX_TILE + e;
+    if (pos < stride) srow[pos] = NEG_INF;
+    if (BM && (pos & ((1 << sub_log2) - 1)) == 0 && (pos >> sub_log2) < nb) bm[(size_t)b * nb + (pos >> sub_log2)] = NEG_INF;
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // the loads of the tiles past the range have landed before the wave ends
+}
+
+template <int MT>
+static hipError_t launch_indexer_long_mt(const uint16_t* q, const float* w, const uint8_t* k, const float* ks,
+                                         const int* table, const int* ctx_len, float* scores, float* bm, int sub_log2,
+                                         int nb, int B, int Hi, int max_pages, int page_size, int num_pages,
+                                         int stride, int num_cu, hipStream_t s) {
+  const int tiles_row = (stride + IDX_TILE - 1) / IDX_TILE;
+  // tiles per wave: about two workgroups per CU over the batch at its longest rows, 4 to 64 tiles each (four per CU,
+  // or three tiles in flight instead of two, measured slower at configs 3 and 4)
+  const long waves_target = 2L * num_cu * IDX_WAVES;
+  int TW = (int)(((long)B * tiles_row + waves_target - 1) / waves_target);
+  TW = TW < 4 ? 4 : (TW > IL_TW_MAX ? IL_TW_MAX : TW);
+  const int wgs_row = (tiles_row + IDX_WAVES * TW - 1) / (IDX_WAVES * TW);
+  if (bm)
+    return launch("indexer_decode_long_kernel", indexer_decode_long_kernel<MT, true>, dim3(B * wgs_row),
+                  dim3(IDX_THREADS), s, q, w, k, ks, table, ctx_len, scores, bm, sub_log2, nb, Hi, max_pages,
+                  page_size, num_pages, stride, TW, wgs_row);
+  return launch("indexer_decode_long_kernel", indexer_decode_long_kernel<MT, false>, dim3(B * wgs_row),
+                dim3(IDX_THREADS), s, q, w, k, ks, table, ctx_len, scores, bm, sub_log2, nb, Hi, max_pages,
+                page_size, num_pages, stride, TW, wgs_row);
+}
+
+// The long-row indexer (no histogram, no additive candidates), with the sub-block maxima when bm is given
+// (1 << sub_log2 <= 32).
+hipError_t launch_indexer_decode_long(const uint16_t* q, const float* w, const uint8_t* k, const float* ks,
+                                      const int* table, const int* ctx_len, float* scores, float* bm, int sub_log2,
+                                      int nb, int B, int Hi, int max_pages, int page_size, int num_pages, int stride,
+                                      int num_cu, hipStream_t s) {
+  if (bm && (sub_log2 < 1 || sub_log2 > 5)) return hipErrorInvalidValue;
+  if (Hi <= 32)
+    return launch_indexer_long_mt<1>(q, w, k, ks, table, ctx_len, scores, bm, sub_log2, nb, B, Hi, max_pages,
+                                     page_size, num_pages, stride, num_cu, s);
+  return launch_indexer_long_mt<2>(q, w, k, ks, table, ctx_len, scores, bm, sub_log2, nb, B, Hi, max_pages,
+                                   page_size, num_pages, stride, num_cu, s);
+}
+
 template <int MT, bool HIST, bool CAND>
 static hipError_t launch_indexer_variant(const uint16_t* q, const float* w, const uint8_t* k, const float* ks,
                                          const int* table, const int* ctx_len, const float* cand, float* scores,
@@ -225,7 +392,9 @@ hipError_t launch_indexer_decode(const uint16_t* q, const float* w, const uint8_
                                  const int* table, const int* ctx_len, const float* cand, float* scores,
                                  int* hist, int B, int Hi, int max_pages, int page_size, int num_pages, int stride,
                                  int num_cu, hipStream_t stream) {
-  (void)num_cu;  // one workgroup per IDX_TPG tiles of a row, whatever the GPU's size
+  if (!hist && !cand && stride > 32 * 1024)  // long rows: the streaming form
+    return launch_indexer_decode_long(q, w, k, ks, table, ctx_len, scores, nullptr, 0, 0, B, Hi, max_pages, page_size,
+                                      num_pages, stride, num_cu, stream);
   if (Hi <= 32)
     return launch_indexer_mt<1>(q, w, k, ks, table, ctx_len, cand, scores, hist, B, Hi, max_pages, page_size,
                                 num_pages, stride, stream);

@@ -1175,10 +1175,11 @@ static hipError_t topk_rows(const float* scores, int stride, const int* len, int
 
 // ws: topk_workspace_bytes(B, max_len, keep) bytes whose histogram region is zero; hist_ready: the histogram of the
 // rows is already accumulated there (by the indexer), so the first level does not build it. rows_out (flat rows
-// only, else null): also the cache slot of each selected position through the page table.
+// only, else null): also the cache slot of each selected position through the page table. bm_ready (rows longer than
+// TOPK_FLAT_MAX): the first level's sub-block maxima are already in topk_bm_buffer(ws, B) (the indexer wrote them).
 hipError_t launch_topk(const float* scores, const int* len, int* idx, int* cnt, void* ws, int B, int stride,
                        int max_len, int keep, int vis_only, bool hist_ready, const int* table, int max_pages,
-                       int page_size, int num_pages, int* rows_out, hipStream_t s) {
+                       int page_size, int num_pages, int* rows_out, hipStream_t s, bool bm_ready) {
   char* p = static_cast<char*>(ws);
   if ((hist_ready || rows_out) && max_len > TOPK_FLAT_MAX) return hipErrorInvalidValue;  // flat rows only
   if (rows_out && (!table || page_size < 32 || max_pages < 1 || num_pages < 1)) return hipErrorInvalidValue;
@@ -1193,7 +1194,8 @@ hipError_t launch_topk(const float* scores, const int* len, int* idx, int* cnt, 
     const SlotOut so = {table, max_pages, page_size, num_pages, rows_out};
     return launch_topk_level(scores, stride, len, 1, 1, max_len, keep, vis_only, idx, cnt, tb, hist_ready, so, B, s);
   }
-  return topk_rows(scores, stride, len, 1, 1, max_len, keep, vis_only, idx, cnt, tb, hist_ready, p, B, s);
+  return topk_rows(scores, stride, len, 1, 1, max_len, keep, vis_only, idx, cnt, tb, hist_ready, p, B, s,
+                   bm_ready && max_len > TOPK_FLAT_MAX);
 }
 
 // The sub-block size of the first level of rows of n scores (a power of two), or 0 when they are selected flat.
