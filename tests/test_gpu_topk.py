@@ -55,6 +55,17 @@ def test_two_level_rows(n, kind):
     _exact(scores_of(kind, 3, n, g), 2048)
 
 
+@pytest.mark.parametrize("kind", ["equal", "zeros", "wide", "integers"])
+def test_long_rows_ties_and_ragged(kind):
+    """Rows past 32,768 scores in a small batch (the long chunked selection): every score tied (the candidates past
+    the LDS staging, ties taken in chunk and then position order across chunks), wide-range and integer scores, with
+    ragged lengths that end inside, at and just past a 2,048-position chunk."""
+    say(f"topk long rows {kind}")
+    g = torch.Generator().manual_seed(KINDS.index(kind) + 4242)
+    s = scores_of(kind, 4, 100000, g)
+    _exact(s, 2048, lengths=[100000, 40000, 32769, 34816])
+
+
 def test_one_million():
     say("topk 1M rows")
     g = torch.Generator().manual_seed(1)

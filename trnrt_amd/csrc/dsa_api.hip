@@ -48,8 +48,9 @@ hipError_t launch_topk(const float* scores, const int* len, int* idx, int* cnt, 
                        int page_size, int num_pages, int* rows_out, hipStream_t s, bool bm_ready = false);
 hipError_t launch_indexer_decode_long(const uint16_t* q, const float* w, const uint8_t* k, const float* ks,
                                       const int* table, const int* ctx_len, float* scores, float* bm, int sub_log2,
-                                      int nb, int B, int Hi, int max_pages, int page_size, int num_pages, int stride,
-                                      int num_cu, hipStream_t s);
+                                      int nb, int* hist, int B, int Hi, int max_pages, int page_size, int num_pages,
+                                      int stride, int num_cu, hipStream_t s);
+bool topk_long_rows(int B, long n);
 hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t s);
 hipError_t launch_topk_mask(const int* idx, const int* cnt, const float* scores, float* mask, int B, int keep, int P,
                             int kp, int tail, hipStream_t s);
@@ -684,25 +685,32 @@ int dsa_decode_layer_chain(const void* q_idx_bf16, const float* w, const uint8_t
   if (st != DSA_OK || B == 0) return st;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const size_t t_need = align256(dsa::topk_workspace_bytes(B, max_len, keep));
-  // flat rows: the indexer accumulates the top-k's first-level histogram (the workspace's first region); longer rows:
-  // the long-row indexer, which writes the two-level selection's first-level sub-block maxima (sub-blocks of up to 32)
-  const bool fused_hist = max_len <= 32 * 1024;
+  // the indexer accumulates the top-k's first-level histogram (the workspace's first region): flat rows, and a few
+  // long rows (the long selection; the long-row indexer); otherwise long rows take the two-level selection, the
+  // long-row indexer writing its first-level sub-block maxima (sub-blocks of up to 32)
+  const bool flat = max_len <= 32 * 1024;
+  const bool long_sel = !flat && dsa::topk_long_rows(B, max_len);
+  const bool fused_hist = flat || long_sel;
   const int sub = fused_hist ? 0 : dsa::topk_two_level_sub(max_len, keep);
   const bool fused_bm = sub >= 2 && sub <= 32;
+  int* hist = fused_hist ? static_cast<int*>(workspace) : nullptr;
   hipError_t e;
-  if (fused_hist)
+  if (flat)
     e = dsa::launch_indexer_decode(static_cast<const uint16_t*>(q_idx_bf16), w, k_fp8, k_scale, page_table, ctx_len,
-                                   nullptr, scores, static_cast<int*>(workspace), B, Hi, max_pages, page_size,
-                                   num_pages, score_stride, num_cu(), s);
+                                   nullptr, scores, hist, B, Hi, max_pages, page_size, num_pages, score_stride,
+                                   num_cu(), s);
   else
     e = dsa::launch_indexer_decode_long(static_cast<const uint16_t*>(q_idx_bf16), w, k_fp8, k_scale, page_table,
                                         ctx_len, scores, fused_bm ? dsa::topk_bm_buffer(workspace, B) : nullptr,
                                         fused_bm ? __builtin_ctz((unsigned)sub) : 0,
-                                        fused_bm ? (max_len + sub - 1) / sub : 0, B, Hi, max_pages, page_size,
+                                        fused_bm ? (max_len + sub - 1) / sub : 0, hist, B, Hi, max_pages, page_size,
                                         num_pages, score_stride, num_cu(), s);
-  if (e != hipSuccess) return DSA_ELAUNCH;
-  // flat rows: the top-k also resolves the selected positions to cache slots, so the attention reads slot ids
-  // directly (one dependent load round fewer)
+  if (e != hipSuccess) {
+    if (hist) dsa::launch_fill_zero(workspace, dsa::topk_hist_bytes(B), s);  // a partial histogram may be in
+    return DSA_ELAUNCH;
+  }
+  // with the histogram from the indexer the top-k also resolves the selected positions to cache slots, so the
+  // attention reads slot ids directly (one dependent load round fewer)
   int* rows = fused_hist ? reinterpret_cast<int*>(static_cast<char*>(workspace) + t_need) : nullptr;
   e = dsa::launch_topk(scores, ctx_len, idx, cnt, workspace, B, score_stride, max_len, keep, 1, fused_hist,
                        page_table, max_pages, page_size, num_pages, rows, s, fused_bm);

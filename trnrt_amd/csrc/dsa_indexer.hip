@@ -37,8 +37,8 @@ constexpr int IDX_AHEAD = 1;  // key tiles a wave has in flight ahead of the one
 
 hipError_t launch_indexer_decode_long(const uint16_t* q, const float* w, const uint8_t* k, const float* ks,
                                       const int* table, const int* ctx_len, float* scores, float* bm, int sub_log2,
-                                      int nb, int B, int Hi, int max_pages, int page_size, int num_pages, int stride,
-                                      int num_cu, hipStream_t s);
+                                      int nb, int* hist, int B, int Hi, int max_pages, int page_size, int num_pages,
+                                      int stride, int num_cu, hipStream_t s);
 
 // One 32-key tile's loads for lane (key j, half h): 64 key bytes (dims 64h .. 64h + 63) and the key's scale (a tile
 // past the context reads the null page: every load is unconditional, so the waits count exactly).
@@ -200,21 +200,23 @@ __global__ __launch_bounds__(IDX_THREADS, 2) void indexer_decode_kernel(
 // streams TW consecutive tiles (up to 64, the launch choosing TW so that about two workgroups per CU cover the batch)
 // through a ring of IL_AHEAD + 1 register tiles, IL_AHEAD in flight ahead of the one it computes, so the row's queries
 // are staged once per workgroup for up to 8,192 keys instead of 512 and the memory stream runs without the
-// workgroups' start-up gaps. The wave's page ids are one load per lane (tile tw0 + lane). BM: also the two-level top-k's
+// workgroups' start-up gaps. The wave's page ids are one load per lane (tile tw0 + lane). HIST: also the row's top-k
+// first-level histogram (as the kernel above). BM: also the two-level top-k's
 // first-level sub-block maxima, bm[b, p / sub] = the maximum of the scores of positions p .. p + sub - 1 (sub a power
 // of two up to 32: a tile's 32 keys hold whole sub-blocks), for p < nb sub.
 constexpr int IL_AHEAD = 2;
 constexpr int IL_RING = IL_AHEAD + 1;
 constexpr int IL_TW_MAX = 64;
 
-template <int MT, bool BM>
+template <int MT, bool BM, bool HIST>
 __global__ __launch_bounds__(IDX_THREADS, 2) void indexer_decode_long_kernel(
     const uint16_t* __restrict__ q, const float* __restrict__ w, const uint8_t* __restrict__ kcache,
     const float* __restrict__ kscale, const int* __restrict__ table, const int* __restrict__ ctx_len,
-    float* __restrict__ scores, float* __restrict__ bm, int sub_log2, int nb, int Hi, int max_pages, int page_size,
-    int num_pages, int stride, int TW, int wgs_per_row) {
+    float* __restrict__ scores, float* __restrict__ bm, int sub_log2, int nb, int* __restrict__ hist, int Hi,
+    int max_pages, int page_size, int num_pages, int stride, int TW, int wgs_per_row) {
   __shared__ uint16_t qs[32 * MT * IDX_QROW];
   __shared__ float ws[32 * MT];
+  __shared__ int hs[HIST ? IDX_HBINS : 1];  // the workgroup's share of the row's top-k histogram
   const int b = blockIdx.x / wgs_per_row;
   const int grp = blockIdx.x - b * wgs_per_row;
   const int wave = threadIdx.x / WAVE;
@@ -255,6 +257,8 @@ __global__ __launch_bounds__(IDX_THREADS, 2) void indexer_decode_long_kernel(
     *reinterpret_cast<uint4*>(&qs[head * IDX_QROW + 8 * c]) = head < Hi ? qv[r] : make_uint4(0, 0, 0, 0);
   }
   if (threadIdx.x < 32 * MT) ws[threadIdx.x] = (int)threadIdx.x < Hi ? wv : 0.0f;
+  if (HIST)
+    for (int i = threadIdx.x; i < IDX_HBINS; i += IDX_THREADS) hs[i] = 0;
   __syncthreads();
   bf16x8 qa[MT][8];
 #pragma unroll
@@ -306,7 +310,10 @@ __global__ __launch_bounds__(IDX_THREADS, 2) void indexer_decode_long_kernel(
         for (int x = 0; x < 16; ++x) part = fmaf(wr[m][x], relu(acc[m][x]), part);
       part += __shfl_xor(part, 32, WAVE);
       const float v = pos < L ? part * ksc[r] : NEG_INF;
-      if (h == 0 && pos < stride) srow[pos] = v;
+      if (h == 0 && pos < stride) {
+        srow[pos] = v;
+        if (HIST && v > VISIBLE) atomicAdd(&hs[order_key(v) >> IDX_HSHIFT], 1);
+      }
       if (BM) {
         float mx = v;
         for (int d = 1; d < sub; d <<= 1) mx = max_nonan(mx, __shfl_xor(mx, d, WAVE));
@@ -320,14 +327,23 @@ __global__ __launch_bounds__(IDX_THREADS, 2) void indexer_decode_long_kernel(
     if (pos < stride) srow[pos] = NEG_INF;
     if (BM && (pos & ((1 << sub_log2) - 1)) == 0 && (pos >> sub_log2) < nb) bm[(size_t)b * nb + (pos >> sub_log2)] = NEG_INF;
   }
+  if (HIST) {
+    // the row's first-level top-k histogram (top 12 bits of the order key of the selectable scores)
+    __syncthreads();
+    int* hrow = hist + (size_t)b * HIST_REPLICAS * IDX_HBINS;
+    for (int i = threadIdx.x; i < IDX_HBINS; i += IDX_THREADS) {
+      const int c = hs[i];
+      if (c) atomicAdd(&hrow[i], c);
+    }
+  }
   __builtin_amdgcn_s_waitcnt(0);  // the loads of the tiles past the range have landed before the wave ends
 }
 
-template <int MT>
-static hipError_t launch_indexer_long_mt(const uint16_t* q, const float* w, const uint8_t* k, const float* ks,
-                                         const int* table, const int* ctx_len, float* scores, float* bm, int sub_log2,
-                                         int nb, int B, int Hi, int max_pages, int page_size, int num_pages,
-                                         int stride, int num_cu, hipStream_t s) {
+template <int MT, bool BM, bool HIST>
+static hipError_t launch_indexer_long_v(const uint16_t* q, const float* w, const uint8_t* k, const float* ks,
+                                        const int* table, const int* ctx_len, float* scores, float* bm, int sub_log2,
+                                        int nb, int* hist, int B, int Hi, int max_pages, int page_size, int num_pages,
+                                        int stride, int num_cu, hipStream_t s) {
   const int tiles_row = (stride + IDX_TILE - 1) / IDX_TILE;
   // tiles per wave: about two workgroups per CU over the batch at its longest rows, 4 to 64 tiles each (four per CU,
   // or three tiles in flight instead of two, measured slower at configs 3 and 4)
@@ -335,26 +351,37 @@ static hipError_t launch_indexer_long_mt(const uint16_t* q, const float* w, cons
   int TW = (int)(((long)B * tiles_row + waves_target - 1) / waves_target);
   TW = TW < 4 ? 4 : (TW > IL_TW_MAX ? IL_TW_MAX : TW);
   const int wgs_row = (tiles_row + IDX_WAVES * TW - 1) / (IDX_WAVES * TW);
-  if (bm)
-    return launch("indexer_decode_long_kernel", indexer_decode_long_kernel<MT, true>, dim3(B * wgs_row),
-                  dim3(IDX_THREADS), s, q, w, k, ks, table, ctx_len, scores, bm, sub_log2, nb, Hi, max_pages,
-                  page_size, num_pages, stride, TW, wgs_row);
-  return launch("indexer_decode_long_kernel", indexer_decode_long_kernel<MT, false>, dim3(B * wgs_row),
-                dim3(IDX_THREADS), s, q, w, k, ks, table, ctx_len, scores, bm, sub_log2, nb, Hi, max_pages,
+  return launch("indexer_decode_long_kernel", indexer_decode_long_kernel<MT, BM, HIST>, dim3(B * wgs_row),
+                dim3(IDX_THREADS), s, q, w, k, ks, table, ctx_len, scores, bm, sub_log2, nb, hist, Hi, max_pages,
                 page_size, num_pages, stride, TW, wgs_row);
 }
 
-// The long-row indexer (no histogram, no additive candidates), with the sub-block maxima when bm is given
-// (1 << sub_log2 <= 32).
+template <int MT>
+static hipError_t launch_indexer_long_mt(const uint16_t* q, const float* w, const uint8_t* k, const float* ks,
+                                         const int* table, const int* ctx_len, float* scores, float* bm, int sub_log2,
+                                         int nb, int* hist, int B, int Hi, int max_pages, int page_size,
+                                         int num_pages, int stride, int num_cu, hipStream_t s) {
+  if (hist)
+    return launch_indexer_long_v<MT, false, true>(q, w, k, ks, table, ctx_len, scores, nullptr, 0, 0, hist, B, Hi,
+                                                  max_pages, page_size, num_pages, stride, num_cu, s);
+  if (bm)
+    return launch_indexer_long_v<MT, true, false>(q, w, k, ks, table, ctx_len, scores, bm, sub_log2, nb, nullptr, B,
+                                                  Hi, max_pages, page_size, num_pages, stride, num_cu, s);
+  return launch_indexer_long_v<MT, false, false>(q, w, k, ks, table, ctx_len, scores, nullptr, 0, 0, nullptr, B, Hi,
+                                                 max_pages, page_size, num_pages, stride, num_cu, s);
+}
+
+// The long-row indexer (no additive candidates): with the top-k's first-level histogram accumulated into hist
+// [B, 4096] when given, else with the two-level selection's sub-block maxima when bm is given (1 << sub_log2 <= 32).
 hipError_t launch_indexer_decode_long(const uint16_t* q, const float* w, const uint8_t* k, const float* ks,
                                       const int* table, const int* ctx_len, float* scores, float* bm, int sub_log2,
-                                      int nb, int B, int Hi, int max_pages, int page_size, int num_pages, int stride,
-                                      int num_cu, hipStream_t s) {
-  if (bm && (sub_log2 < 1 || sub_log2 > 5)) return hipErrorInvalidValue;
+                                      int nb, int* hist, int B, int Hi, int max_pages, int page_size, int num_pages,
+                                      int stride, int num_cu, hipStream_t s) {
+  if (!hist && bm && (sub_log2 < 1 || sub_log2 > 5)) return hipErrorInvalidValue;
   if (Hi <= 32)
-    return launch_indexer_long_mt<1>(q, w, k, ks, table, ctx_len, scores, bm, sub_log2, nb, B, Hi, max_pages,
+    return launch_indexer_long_mt<1>(q, w, k, ks, table, ctx_len, scores, bm, sub_log2, nb, hist, B, Hi, max_pages,
                                      page_size, num_pages, stride, num_cu, s);
-  return launch_indexer_long_mt<2>(q, w, k, ks, table, ctx_len, scores, bm, sub_log2, nb, B, Hi, max_pages,
+  return launch_indexer_long_mt<2>(q, w, k, ks, table, ctx_len, scores, bm, sub_log2, nb, hist, B, Hi, max_pages,
                                    page_size, num_pages, stride, num_cu, s);
 }
 
@@ -393,8 +420,8 @@ hipError_t launch_indexer_decode(const uint16_t* q, const float* w, const uint8_
                                  int* hist, int B, int Hi, int max_pages, int page_size, int num_pages, int stride,
                                  int num_cu, hipStream_t stream) {
   if (!hist && !cand && stride > 32 * 1024)  // long rows: the streaming form
-    return launch_indexer_decode_long(q, w, k, ks, table, ctx_len, scores, nullptr, 0, 0, B, Hi, max_pages, page_size,
-                                      num_pages, stride, num_cu, stream);
+    return launch_indexer_decode_long(q, w, k, ks, table, ctx_len, scores, nullptr, 0, 0, nullptr, B, Hi, max_pages,
+                                      page_size, num_pages, stride, num_cu, stream);
   if (Hi <= 32)
     return launch_indexer_mt<1>(q, w, k, ks, table, ctx_len, cand, scores, hist, B, Hi, max_pages, page_size,
                                 num_pages, stride, stream);

@@ -783,6 +783,386 @@ __global__ __launch_bounds__(TC_THREADS) void topk_output_kernel(const float* __
   }
 }
 
+// Rows longer than 32,768 scores in few rows (a decode batch at long context): the chunked selection above with any
+// number of chunks, in three kernels over the row's first-level histogram (built by the indexer or topk_hist_kernel):
+//   topk_long_chunk_kernel:   per chunk of 2,048 positions, the threshold's bin c0 from the histogram, the count of
+//                             the chunk's keys above c0, and its keys in bin c0 (the candidates) in position order;
+//   topk_long_resolve_kernel: one workgroup per row reads every chunk's candidates, finds T (the keep-th largest key)
+//                             by two LDS histogram passes over their low 20 bits (11 + 9) and the ties to take, and
+//                             gives each chunk its first output index and its ties taken (ties go to the lowest
+//                             positions: chunk order, then position order inside a chunk);
+//   topk_long_output_kernel:  every chunk writes its selected positions in order (and their cache slots).
+// Candidates are held per chunk (at most its 2,048 keys), so the workspace bounds them whatever the scores.
+constexpr int TL_MAXCH = 1024;  // chunks per row: rows of up to 2,097,152 scores
+constexpr int TL_THREADS = 1024;
+constexpr int TL_WAVES = TL_THREADS / WAVE;
+
+struct LongRow {
+  int c0, above0, nvis;  // as RowMeta
+  uint32_t T;            // the threshold key (0: every selectable key is taken)
+};
+
+// Per-chunk arrays of the long selection, [B][nch] each, and the candidates [B][nch][TC_CHUNK].
+struct LongBuffers {
+  LongRow* row;
+  int *na, *nc, *base, *take;
+  uint32_t* cand;
+};
+
+template <bool VEC>
+__global__ __launch_bounds__(TC_THREADS) void topk_long_chunk_kernel(const float* __restrict__ scores, int stride,
+                                                                     const int* __restrict__ len, int keep,
+                                                                     int vis_only, const int* __restrict__ hist,
+                                                                     LongBuffers lb, int nch) {
+  __shared__ ChunkShared sh;
+  const int row = blockIdx.y, chunk = blockIdx.x;
+  const int t = threadIdx.x, wave = t / WAVE, lane = t & (WAVE - 1);
+  const int L = level_len(len, row, 1, 1, stride);
+  const int base = chunk * TC_CHUNK;
+  const int4* h4 = reinterpret_cast<const int4*>(hist + (size_t)row * HIST_REPLICAS * TK_HBINS) + 4 * t;
+  int4 hv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) hv[i] = h4[i];
+  uint32_t key[2][4];
+  load_chunk_keys<VEC>(scores + (size_t)row * stride, stride, L, base, vis_only, key);
+  int hb[16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    hb[4 * i] = hv[i].x;
+    hb[4 * i + 1] = hv[i].y;
+    hb[4 * i + 2] = hv[i].z;
+    hb[4 * i + 3] = hv[i].w;
+  }
+  // c0: the bin holding the keep-th largest key (bins 16t .. 16t + 15 on thread t; suffix over threads)
+  int mine = 0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) mine += hb[i];
+  const int pre = wave_incl_scan(mine);
+  const int inc = __builtin_amdgcn_readlane(pre, WAVE - 1) - pre + mine;
+  if (lane == 0) sh.wtot[wave] = inc;
+  if (t == 0) {
+    sh.c0 = -1;
+    sh.above0 = 0;
+  }
+  __syncthreads();
+  int after = 0, nvis = 0;
+#pragma unroll
+  for (int w = 0; w < TC_WAVES; ++w) {
+    const int x = sh.wtot[w];
+    after += w > wave ? x : 0;
+    nvis += x;
+  }
+  int excl = after + inc - mine;
+  if (nvis > keep && excl < keep && excl + mine >= keep) {
+#pragma unroll
+    for (int i = 15; i >= 0; --i) {
+      if (excl < keep) {
+        if (excl + hb[i] >= keep) {
+          sh.c0 = 16 * t + i;
+          sh.above0 = excl;
+        }
+        excl += hb[i];
+      }
+    }
+  }
+  __syncthreads();
+  const int c0 = sh.c0;
+  uint32_t mc[2];
+  int na = 0;
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    uint32_t nc = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t k = key[e][c];
+      const int bin = (int)(k >> TK_HSHIFT);
+      na += k != 0u && bin > c0;
+      nc += k != 0u && bin == c0;
+    }
+    mc[e] = nc;
+  }
+  uint32_t before[2];
+  chunk_prefix(mc, sh.blk, before);
+  const size_t ci = (size_t)row * nch + chunk;
+  uint32_t* crow = lb.cand + ci * TC_CHUNK;
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    uint32_t o = before[e];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t k = key[e][c];
+      if (k != 0u && (int)(k >> TK_HSHIFT) == c0) {
+        if (o < (uint32_t)TC_CHUNK) crow[o] = k;
+        ++o;
+      }
+    }
+  }
+  const int na_w = wave_sum(na);
+  if (lane == 0) sh.wtot[wave] = na_w;
+  __syncthreads();
+  if (t == TC_THREADS - 1) {
+    int na_tot = 0;
+#pragma unroll
+    for (int w = 0; w < TC_WAVES; ++w) na_tot += sh.wtot[w];
+    lb.na[ci] = na_tot;
+    lb.nc[ci] = (int)(before[1] + mc[1]);
+    if (chunk == 0) {
+      lb.row[row].c0 = c0;
+      lb.row[row].above0 = sh.above0;
+      lb.row[row].nvis = nvis;
+    }
+  }
+}
+
+constexpr int TL_CAP = 4096;  // candidates of a row staged in LDS (more: read from the workspace)
+
+struct LongShared {
+  int bins[2048];
+  int bins2[512];
+  int gt[TL_MAXCH], tie[TL_MAXCH];
+  int coff[TL_MAXCH];   // per chunk: its candidates' first flat index
+  uint32_t sk[TL_CAP];  // the row's candidates in flat order (chunk order, then position order)
+  uint16_t sj[TL_CAP];  // their chunks
+  int wtot[TL_WAVES];
+  int sel[2], sel2[2];
+};
+
+// Block-wide (1024 threads) over bins[0 .. nbins) (2048 or 512, higher bins = larger keys): the bin holding the
+// need-th largest key and the keys above it through sel[0 .. 1] (sel[0] -1 on entry, written before a barrier that
+// precedes this call). Two barriers; the caller passes one more before sel or wtot are written again.
+__device__ void long_find_bin(LongShared& sh, const int* bins, int* sel, int nbins, int need, int* bin, int* above) {
+  const int t = threadIdx.x, wave = t / WAVE, lane = t & (WAVE - 1);
+  const int per = nbins / TL_THREADS;  // 2, or 0 for 512 bins (thread t < 512 then takes bin t)
+  int hb[2];
+  int mine = 0;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int b = per ? per * t + i : (i == 0 ? t : nbins);
+    hb[i] = b < nbins ? bins[b] : 0;
+    mine += hb[i];
+  }
+  const int pre = wave_incl_scan(mine);
+  const int inc = __builtin_amdgcn_readlane(pre, WAVE - 1) - pre + mine;
+  if (lane == 0) sh.wtot[wave] = inc;
+  __syncthreads();
+  int after = 0;
+#pragma unroll
+  for (int w = 0; w < TL_WAVES; ++w) after += w > wave ? sh.wtot[w] : 0;
+  int excl = after + inc - mine;
+  if (excl < need && excl + mine >= need) {
+#pragma unroll
+    for (int i = 1; i >= 0; --i) {
+      const int b = per ? per * t + i : (i == 0 ? t : nbins);
+      if (b < nbins && excl < need) {
+        if (excl + hb[i] >= need) {
+          sel[0] = b;
+          sel[1] = excl;
+        }
+        excl += hb[i];
+      }
+    }
+  }
+  __syncthreads();
+  const int b = sel[0];
+  *bin = b < 0 ? 0 : b;
+  *above = b < 0 ? 0 : sel[1];
+}
+
+// Block-wide inclusive scan over the 1024 threads (thread order); the total into *tot. Two barriers.
+__device__ __forceinline__ int long_block_scan(int v, int* wtot, int* tot) {
+  const int t = threadIdx.x, wave = t / WAVE, lane = t & (WAVE - 1);
+  const int incl = wave_incl_scan(v);
+  if (lane == WAVE - 1) wtot[wave] = incl;
+  __syncthreads();
+  int before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < TL_WAVES; ++w) {
+    const int x = wtot[w];
+    before += w < wave ? x : 0;
+    all += x;
+  }
+  *tot = all;
+  __syncthreads();
+  return before + incl;
+}
+
+// The chunk of flat candidate index i (the last chunk whose first index is at most i; chunks without candidates
+// share their successor's first index, so the search lands on the one holding i).
+__device__ __forceinline__ int long_chunk_of(const int* coff, int nch, int i) {
+  int lo = 0, hi = nch - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (coff[mid] <= i) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+__global__ __launch_bounds__(TL_THREADS) void topk_long_resolve_kernel(LongBuffers lb, int nch, int keep,
+                                                                       int* __restrict__ hist,
+                                                                       int* __restrict__ cnt_out) {
+  __shared__ LongShared sh;
+  const int row = blockIdx.x;
+  const int t = threadIdx.x;
+  const LongRow lr = lb.row[row];
+  const int c0 = lr.c0, above0 = lr.above0, nvis = lr.nvis;
+  const uint32_t* cand = lb.cand + (size_t)row * nch * TC_CHUNK;
+  // one round of loads: chunk t's candidate and above counts
+  const int nc_t = t < nch ? min(max(lb.nc[(size_t)row * nch + t], 0), TC_CHUNK) : 0;
+  const int na_t = t < nch ? lb.na[(size_t)row * nch + t] : 0;
+  // leave the row's histogram zero for the next call (every chunk kernel has read it)
+  int* hrow = hist + (size_t)row * HIST_REPLICAS * TK_HBINS;
+  for (int i = t; i < HIST_REPLICAS * TK_HBINS; i += TL_THREADS) hrow[i] = 0;
+  for (int i = t; i < 2048; i += TL_THREADS) sh.bins[i] = 0;
+  if (t < 512) sh.bins2[t] = 0;
+  if (t < TL_MAXCH) {
+    sh.gt[t] = 0;
+    sh.tie[t] = 0;
+  }
+  if (t == 0) {
+    sh.sel[0] = -1;
+    sh.sel2[0] = -1;
+  }
+  const bool resolve = c0 >= 0 && nvis > keep;  // block-uniform
+  // the candidates' flat offsets, then the first TL_CAP candidates into LDS
+  int n_all;
+  const int coff_t = long_block_scan(nc_t, sh.wtot, &n_all) - nc_t;
+  if (t < nch) sh.coff[t] = coff_t;
+  __syncthreads();
+  const int n_stage = resolve ? min(n_all, TL_CAP) : 0;
+  for (int i = t; i < n_stage; i += TL_THREADS) {
+    const int j = long_chunk_of(sh.coff, nch, i);
+    sh.sk[i] = cand[(size_t)j * TC_CHUNK + (i - sh.coff[j])];
+    sh.sj[i] = (uint16_t)j;
+  }
+  __syncthreads();
+  // candidate i (flat order) and its chunk: staged, or read from the workspace past TL_CAP
+  auto cand_at = [&](int i, int* j) __attribute__((always_inline)) {
+    if (i < TL_CAP) {
+      *j = sh.sj[i];
+      return sh.sk[i];
+    }
+    *j = long_chunk_of(sh.coff, nch, i);
+    return cand[(size_t)*j * TC_CHUNK + (i - sh.coff[*j])];
+  };
+  uint32_t T = 0u;
+  int room = 0;
+  if (resolve) {
+    int need = keep - above0;
+    int j;
+    // pass A: bits 19 .. 9 of every candidate
+    for (int i = t; i < n_all; i += TL_THREADS) atomicAdd(&sh.bins[(cand_at(i, &j) >> 9) & 2047u], 1);
+    __syncthreads();
+    int c1, above;
+    long_find_bin(sh, sh.bins, sh.sel, 2048, need, &c1, &above);
+    need -= above;
+    const uint32_t pre = ((uint32_t)c0 << 11) | (uint32_t)c1;
+    // pass B: bits 8 .. 0 of the candidates under the 23-bit prefix
+    for (int i = t; i < n_all; i += TL_THREADS) {
+      const uint32_t k = cand_at(i, &j);
+      if ((k >> 9) == pre) atomicAdd(&sh.bins2[k & 511u], 1);
+    }
+    __syncthreads();
+    int c2;
+    long_find_bin(sh, sh.bins2, sh.sel2, 512, need, &c2, &above);
+    T = (pre << 9) | (uint32_t)c2;
+    room = max(need - above, 0);
+    // per chunk: its candidates above T and equal to T
+    for (int i = t; i < n_all; i += TL_THREADS) {
+      const uint32_t k = cand_at(i, &j);
+      if (k > T) atomicAdd(&sh.gt[j], 1);
+      if (k == T) atomicAdd(&sh.tie[j], 1);
+    }
+  }
+  __syncthreads();
+  // chunk t (t < nch): the ties before it, its ties taken, its first output index
+  const int tie_t = t < nch ? sh.tie[t] : 0;
+  int tot;
+  const int tie_before = long_block_scan(tie_t, sh.wtot, &tot) - tie_t;
+  const int take_t = min(max(room - tie_before, 0), tie_t);
+  const int sel_t = t < nch ? na_t + sh.gt[t] + take_t : 0;
+  const int base_t = long_block_scan(sel_t, sh.wtot, &tot) - sel_t;
+  if (t < nch) {
+    lb.base[(size_t)row * nch + t] = base_t;
+    lb.take[(size_t)row * nch + t] = take_t;
+  }
+  if (t == 0) {
+    lb.row[row].T = T;
+    cnt_out[row] = nvis < 0 ? 0 : (nvis < keep ? nvis : keep);
+  }
+}
+
+template <bool VEC, bool ROWS>
+__global__ __launch_bounds__(TC_THREADS) void topk_long_output_kernel(const float* __restrict__ scores, int stride,
+                                                                      const int* __restrict__ len, int keep,
+                                                                      int vis_only, LongBuffers lb, int nch,
+                                                                      const int* __restrict__ cnt_in,
+                                                                      int* __restrict__ idx_out, SlotOut so) {
+  __shared__ ChunkShared sh;
+  __shared__ int pg[WAVE];
+  __shared__ int pg0s;
+  const int row = blockIdx.y, chunk = blockIdx.x;
+  const int t = threadIdx.x, wave = t / WAVE, lane = t & (WAVE - 1);
+  const int L = level_len(len, row, 1, 1, stride);
+  const int base = chunk * TC_CHUNK;
+  const size_t ci = (size_t)row * nch + chunk;
+  const uint32_t T = lb.row[row].T;
+  const int out_base = lb.base[ci], room_here = lb.take[ci];
+  const int pg_first = ROWS ? base / so.page_size : 0;
+  int pgv = 0, pg0v = 0;
+  if (ROWS) {
+    pgv = so.table[(size_t)row * so.max_pages + min(pg_first + lane, so.max_pages - 1)];
+    pg0v = so.table[(size_t)row * so.max_pages];
+  }
+  uint32_t key[2][4];
+  load_chunk_keys<VEC>(scores + (size_t)row * stride, stride, L, base, vis_only, key);
+  if (ROWS && wave == 0) {
+    pg[lane] = safe_page(pgv, so.num_pages);
+    if (lane == 0) pg0s = safe_page(pg0v, so.num_pages);
+  }
+  uint32_t mine[2], before[2];
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    uint32_t na = 0, nt = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      na += key[e][c] > T;
+      nt += T != 0u && key[e][c] == T;
+    }
+    mine[e] = (na << 16) | nt;
+  }
+  chunk_prefix(mine, sh.blk, before);  // its barriers also order the page ids' LDS writes before their reads
+  int* orow = idx_out + (size_t)row * keep;
+  const int psh = ROWS ? page_shift_of(so.page_size) : 0;
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    int a_before = (int)(before[e] >> 16), t_before = (int)(before[e] & 0xffffu);
+    const int p0 = base + 4 * (TC_THREADS * e + t);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const bool a = key[e][c] > T;
+      const bool ti = T != 0u && key[e][c] == T;
+      const bool sel = a || (ti && t_before < room_here);
+      const int o = out_base + a_before + (t_before < room_here ? t_before : room_here);
+      if (sel && (unsigned)o < (unsigned)keep) {
+        orow[o] = p0 + c;
+        if (ROWS) {
+          const int ps = so.page_size, p = p0 + c, pi = page_of(p, ps, psh);
+          so.rows[(size_t)row * keep + o] = pg[min(pi - pg_first, WAVE - 1)] * ps + (p - pi * ps);
+        }
+      }
+      a_before += a;
+      t_before += ti;
+    }
+  }
+  if (chunk == 0) {
+    const int cnt_row = cnt_in[row];
+    for (int i = cnt_row + t; i < keep; i += TC_THREADS) {
+      orow[i] = 0;
+      if (ROWS) so.rows[(size_t)row * keep + i] = pg0s * so.page_size;
+    }
+  }
+}
+
 // Sub-block maxima of each row: bm[row, j] = max of scores[row, j sub .. j sub + sub - 1] over positions < len.
 __global__ void block_max_kernel(const float* __restrict__ scores, int stride, const int* __restrict__ len, int sub,
                                  int nb_stride, float* __restrict__ bm) {
@@ -948,9 +1328,16 @@ size_t topk_hist_bytes(int B) { return up256((size_t)B * HIST_REPLICAS * TK_HBIN
 // (WS_SYNC_BYTES, which the separate kernels never touch).
 size_t topk_zero_bytes(int B) { return topk_hist_bytes(B) + WS_SYNC_BYTES; }
 
+static bool topk_long_ok(int B, long n);
+static size_t topk_long_bytes(int B, long n);
+
 size_t topk_workspace_bytes(int B, int max_len, int keep) {
-  return topk_zero_bytes(B) + up256((size_t)B * sizeof(RowMeta)) + up256((size_t)B * TC_MAXCH * TC_CHUNK * 4) +
-         topk_level_bytes(B, max_len, keep);
+  size_t rest = topk_level_bytes(B, max_len, keep);
+  if (topk_long_ok(B, max_len)) {  // the long selection's buffers share the two-level selection's place
+    const size_t l = topk_long_bytes(B, max_len);
+    rest = l > rest ? l : rest;
+  }
+  return topk_zero_bytes(B) + up256((size_t)B * sizeof(RowMeta)) + up256((size_t)B * TC_MAXCH * TC_CHUNK * 4) + rest;
 }
 
 bool topk_supported(int max_len, int keep, int vis_only) {
@@ -1108,6 +1495,55 @@ static hipError_t launch_topk_level(const float* scores, int stride, const int* 
                                           hist_ready, so, B, s);
 }
 
+static size_t topk_long_bytes(int B, long n) {
+  const size_t nch = (size_t)((n + TC_CHUNK - 1) / TC_CHUNK);
+  return up256((size_t)B * sizeof(LongRow)) + 4 * up256((size_t)B * nch * 4) + up256((size_t)B * nch * TC_CHUNK * 4);
+}
+
+static LongBuffers topk_long_buffers(char* p, int B, int nch) {
+  LongBuffers lb;
+  lb.row = reinterpret_cast<LongRow*>(p);
+  p += up256((size_t)B * sizeof(LongRow));
+  int** arrs[4] = {&lb.na, &lb.nc, &lb.base, &lb.take};
+  for (int** a : arrs) {
+    *a = reinterpret_cast<int*>(p);
+    p += up256((size_t)B * nch * 4);
+  }
+  lb.cand = reinterpret_cast<uint32_t*>(p);
+  return lb;
+}
+
+// Whether the long selection takes rows of up to n scores in a batch of B rows (few rows: many rows take the
+// one-workgroup-per-row kernels).
+static bool topk_long_ok(int B, long n) {
+  return n > TOPK_FLAT_MAX && B < TOPK_MANY_ROWS && (n + TC_CHUNK - 1) / TC_CHUNK <= TL_MAXCH;
+}
+
+template <bool VEC>
+static hipError_t launch_topk_long_v(const float* scores, int stride, const int* len, long n, int keep, int vis_only,
+                                     int* hist, bool hist_ready, char* p, int* idx, int* cnt, const SlotOut& so,
+                                     int B, hipStream_t s) {
+  const int nch = (int)((n + TC_CHUNK - 1) / TC_CHUNK);
+  const LongBuffers lb = topk_long_buffers(p, B, nch);
+  hipError_t e;
+  if (!hist_ready) {
+    e = launch("topk_hist_kernel", topk_hist_kernel, dim3(nch, B), dim3(TKH_THREADS), s, scores, stride, len, 1, 1,
+               vis_only, hist);
+    if (e != hipSuccess) return e;
+  }
+  e = launch("topk_long_chunk_kernel", topk_long_chunk_kernel<VEC>, dim3(nch, B), dim3(TC_THREADS), s, scores, stride,
+             len, keep, vis_only, hist, lb, nch);
+  if (e != hipSuccess) return e;
+  e = launch("topk_long_resolve_kernel", topk_long_resolve_kernel, dim3(B), dim3(TL_THREADS), s, lb, nch, keep, hist,
+             cnt);
+  if (e != hipSuccess) return e;
+  if (so.rows)
+    return launch("topk_long_output_kernel", topk_long_output_kernel<VEC, true>, dim3(nch, B), dim3(TC_THREADS), s,
+                  scores, stride, len, keep, vis_only, lb, nch, cnt, idx, so);
+  return launch("topk_long_output_kernel", topk_long_output_kernel<VEC, false>, dim3(nch, B), dim3(TC_THREADS), s,
+                scores, stride, len, keep, vis_only, lb, nch, cnt, idx, so);
+}
+
 // Selection over rows of `stride` scores whose lengths are len[row] (len_div / len_mul as in level_len), n an upper
 // bound of the lengths.
 static hipError_t topk_rows(const float* scores, int stride, const int* len, int len_div, int len_mul, long n,
@@ -1181,7 +1617,8 @@ hipError_t launch_topk(const float* scores, const int* len, int* idx, int* cnt, 
                        int max_len, int keep, int vis_only, bool hist_ready, const int* table, int max_pages,
                        int page_size, int num_pages, int* rows_out, hipStream_t s, bool bm_ready) {
   char* p = static_cast<char*>(ws);
-  if ((hist_ready || rows_out) && max_len > TOPK_FLAT_MAX) return hipErrorInvalidValue;  // flat rows only
+  const bool long_rows = topk_long_ok(B, max_len);
+  if ((hist_ready || rows_out) && max_len > TOPK_FLAT_MAX && !long_rows) return hipErrorInvalidValue;
   if (rows_out && (!table || page_size < 32 || max_pages < 1 || num_pages < 1)) return hipErrorInvalidValue;
   TopkBuffers tb;
   tb.hist = reinterpret_cast<int*>(p);
@@ -1190,6 +1627,13 @@ hipError_t launch_topk(const float* scores, const int* len, int* idx, int* cnt, 
   p += up256((size_t)B * sizeof(RowMeta));
   tb.ckey = reinterpret_cast<uint32_t*>(p);
   p += up256((size_t)B * TC_MAXCH * TC_CHUNK * 4);
+  if (long_rows && !bm_ready) {
+    const SlotOut so = {table, max_pages, page_size, num_pages, rows_out};
+    return (stride & 3) == 0 ? launch_topk_long_v<true>(scores, stride, len, max_len, keep, vis_only, tb.hist,
+                                                        hist_ready, p, idx, cnt, so, B, s)
+                             : launch_topk_long_v<false>(scores, stride, len, max_len, keep, vis_only, tb.hist,
+                                                         hist_ready, p, idx, cnt, so, B, s);
+  }
   if (rows_out) {
     const SlotOut so = {table, max_pages, page_size, num_pages, rows_out};
     return launch_topk_level(scores, stride, len, 1, 1, max_len, keep, vis_only, idx, cnt, tb, hist_ready, so, B, s);
@@ -1197,6 +1641,10 @@ hipError_t launch_topk(const float* scores, const int* len, int* idx, int* cnt, 
   return topk_rows(scores, stride, len, 1, 1, max_len, keep, vis_only, idx, cnt, tb, hist_ready, p, B, s,
                    bm_ready && max_len > TOPK_FLAT_MAX);
 }
+
+// Whether a batch of B rows of up to n scores takes the long selection (then the first-level histogram can come from
+// the indexer, and the slot output is available).
+bool topk_long_rows(int B, long n) { return topk_long_ok(B, n); }
 
 // The sub-block size of the first level of rows of n scores (a power of two), or 0 when they are selected flat.
 int topk_two_level_sub(long n, int keep) { return n <= TOPK_FLAT_MAX ? 0 : topk_sub_block(n, keep); }
