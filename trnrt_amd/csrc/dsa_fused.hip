@@ -1045,19 +1045,25 @@ __device__ __forceinline__ int fu_attend_prep(const FusedArgs& a, const int* row
 }
 
 // The attention and combine stages of the one-launch layer as a launch of their own, after the separate kernels'
-// selection (rows of any length): row row0 + x on XCD x, the same splits, bf16 split outputs and XCD-local barrier.
+// selection (rows of any length): rows row0 + x, row0 + x + 8, ... (up to rpl of them) on XCD x, with the same
+// splits and bf16 split outputs; every workgroup takes its split of each row in turn, then one XCD-local barrier,
+// then the combines.
 template <int HPW>
-__global__ __launch_bounds__(FU_THREADS, 1) void decode_attend_kernel(FusedArgs a, const int* rows) {
+__global__ __launch_bounds__(FU_THREADS, 1) void decode_attend_kernel(FusedArgs a, const int* rows, int rpl) {
   __shared__ __align__(16) uint8_t lds[FU_LDS];
   const int x = blockIdx.x % FU_XCDS, j = blockIdx.x / FU_XCDS;
   int* sync = a.sync + x * FU_SYNC_WORDS;
-  const int b = a.row0 + x;
-  if (b >= a.B) return;  // an XCD without a row
-  float live_bias;
-  const int n_slots = fu_attend_prep<HPW>(a, rows, lds, b, j, &live_bias);
-  fu_attend<HPW>(a, lds, b, j, n_slots, live_bias);
-  fu_barrier(sync, 1);  // every split's output
-  fu_combine(a, lds, b, j);
+  if (a.row0 + x >= a.B) return;  // an XCD without a row
+  const int nr = min(rpl, (a.B - a.row0 - x + FU_XCDS - 1) / FU_XCDS);  // this XCD's rows
+  for (int r = 0; r < nr; ++r) {
+    if (r) __syncthreads();  // the previous row's attention has read its LDS before the next slot list is written
+    float live_bias;
+    const int b = a.row0 + x + FU_XCDS * r;
+    const int n_slots = fu_attend_prep<HPW>(a, rows, lds, b, j, &live_bias);
+    fu_attend<HPW>(a, lds, b, j, n_slots, live_bias);
+  }
+  fu_barrier(sync, 1);  // every split's output of the XCD's rows
+  for (int r = 0; r < nr; ++r) fu_combine(a, lds, a.row0 + x + FU_XCDS * r, j);
   fu_exit(sync);
 }
 
@@ -1152,10 +1158,14 @@ hipError_t launch_decode_attend(const uint16_t* q, const uint8_t* kv, const floa
   int sps = (keep + S - 1) / S;
   a.sps = (sps + FU_CH - 1) / FU_CH * FU_CH;
   const dim3 grid(FU_XCDS * FU_NW), block(FU_THREADS);
-  for (int r0 = 0; r0 < B; r0 += FU_XCDS) {
+  // up to 4 rows per XCD and launch: a batch of 12 rows is one launch of 2 rows per XCD (or 1), not 8 + 4
+  constexpr int RPL_MAX = 4;
+  for (int r0 = 0; r0 < B; r0 += FU_XCDS * RPL_MAX) {
     a.row0 = r0;
-    const hipError_t e = hpw == 32 ? launch("decode_attend_kernel", decode_attend_kernel<32>, grid, block, s, a, rows)
-                                   : launch("decode_attend_kernel", decode_attend_kernel<16>, grid, block, s, a, rows);
+    const int left = B - r0, rpl = (left < FU_XCDS * RPL_MAX ? left : FU_XCDS * RPL_MAX) + FU_XCDS - 1;
+    const hipError_t e =
+        hpw == 32 ? launch("decode_attend_kernel", decode_attend_kernel<32>, grid, block, s, a, rows, rpl / FU_XCDS)
+                  : launch("decode_attend_kernel", decode_attend_kernel<16>, grid, block, s, a, rows, rpl / FU_XCDS);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
