@@ -7,8 +7,10 @@ kernel's own scores (topk_ref, after trnrt/models/dsa_select.py:33-38); the bf16
 1e-3 of the oracle attention over the kernel's selection (after trnrt/kernels/dsa_decode.py:26-37). Cases: configs 1
 and 2 in full, a ragged batch of 12 rows (two launches) with empty, one-token, shorter-than-keep and full rows, 16 and
 32 query heads with 16 and 48 indexer heads, rows of equal scores (every key a tie: the candidates past the LDS
-cache) and of two score values, and the workspace left as the next call needs it (histograms and barrier words zero,
-no barrier wait gave up)."""
+cache), of two and of a hundred score values, key scales over forty octaves, a row whose selection crowds into two
+workgroups, and the workspace left as the next call needs it (histograms and barrier words zero, no barrier wait gave
+up). Each case also checks which selection form its rows took (the one-exchange form from the key lists, or the
+two-exchange form)."""
 
 import pytest
 import torch
@@ -41,6 +43,13 @@ def _workspace_clean(L):
     assert torch.all(sync[:, 2] == 0), "a barrier wait gave up (error flag set)"
 
 
+def _two_exchange_rows(L) -> int:
+    """Rows that took the two-exchange selection (stages 2 and 3) since the workspace was made: the kernel counts them
+    per XCD in the barrier words; the others took the one-exchange selection from the key lists."""
+    ws = L.workspace.view(torch.int32).cpu()
+    return int(ws[L.B * 4096:L.B * 4096 + 8 * 16].view(8, 16)[:, 3].sum())
+
+
 def _check_full(inp, L, indexer=True):
     cfg = inp.cfg
     sc = L.scores.cpu()
@@ -68,6 +77,8 @@ def test_fused_layer_configs(c):
     assert names == ["decode_fused_kernel"], names
     _check_full(inp, L)
     _workspace_clean(L)
+    # config 2's rows of 32,768 tokens select from the key lists; config 1's row of 4,096 cannot (keep 2048 of it)
+    assert _two_exchange_rows(L) == (0 if c == 2 else 2)
 
 
 def test_fused_layer_ragged_two_launches():
@@ -109,8 +120,12 @@ def _tied_inputs(values: int):
     return inp
 
 
-@pytest.mark.parametrize("values", [1, 2])
+@pytest.mark.parametrize("values", [1, 2, 100])
 def test_fused_layer_ties(values):
+    """One or two score values: every workgroup's keys fill one bin, its key list stays empty and the full row takes
+    the two-exchange selection. A hundred values: the full row selects from the key lists, with the keep-th largest
+    tied with keys that are not taken (the lowest positions of the tie are). The shorter rows take the two-exchange
+    form."""
     say(f"fused layer ties values={values}")
     inp = _tied_inputs(values)
     L = _run(inp.to("cuda"))
@@ -119,6 +134,45 @@ def test_fused_layer_ties(values):
         assert len(torch.unique(sc[b, :n])) <= values
     _check_full(inp, L, indexer=False)
     _workspace_clean(L)
+    assert _two_exchange_rows(L) == (3 if values < 100 else 2)
+    if values == 100:
+        keep = inp.cfg.keep
+        t = sc[0][L.idx[0].cpu().long()].min()
+        assert int((sc[0] == t).sum()) > int((sc[0][L.idx[0].cpu().long()] == t).sum()) > 0, "no partial tie at T"
+
+
+def test_fused_layer_wide_scales():
+    """Key scales spread over forty octaves: each workgroup's listed keys fall in more histogram bins than its list
+    header carries, so the one-exchange selection counts those lists key by key; two full rows, both selecting from
+    the lists."""
+    say("fused layer wide scales")
+    cfg = W.Config("fused-wide", B=2, L=32768, H=64, Hi=64)
+    inp = W.make_inputs(cfg, seed=13)
+    g = torch.Generator().manual_seed(13)
+    inp.k_scale.copy_(torch.exp2(torch.randint(-20, 21, inp.k_scale.shape, generator=g).float()))
+    L = _run(inp.to("cuda"))
+    _check_full(inp, L)
+    _workspace_clean(L)
+    assert _two_exchange_rows(L) == 0
+
+
+def test_fused_layer_concentrated_selection():
+    """A full row whose largest scores crowd into its first 2,048 positions (their keys' scales raised a thousandfold):
+    two workgroups hold most of the selection, more than their key lists can, so the row falls back to the
+    two-exchange selection after reading the lists; a second full row selects from its lists in the same launch."""
+    say("fused layer concentrated selection")
+    cfg = W.Config("fused-crowded", B=2, L=32768, H=64, Hi=64)
+    inp = W.make_inputs(cfg, seed=12)
+    ps = cfg.page_size
+    pos = torch.arange(2048)
+    slots = inp.table[0, pos // ps].long() * ps + pos % ps
+    inp.k_scale[slots] *= 1000.0
+    L = _run(inp.to("cuda"))
+    sel = L.idx[0].cpu().long()
+    assert int((sel < 1024).sum()) > 192 and int(((sel >= 1024) & (sel < 2048)).sum()) > 192
+    _check_full(inp, L)
+    _workspace_clean(L)
+    assert _two_exchange_rows(L) == 1
 
 
 def test_fused_matches_chain():

@@ -5,8 +5,8 @@
 // gfx950 has 8 XCDs of 32 CUs, each XCD with its own L2; workgroup x of a launch runs on XCD x % 8. Row b is owned by
 // the 32 workgroups of XCD b % 8 (one per CU; a batch of more than 8 rows takes one launch per 8 rows), so every
 // hand-off between the stages of a row stays inside one L2: a workgroup's stores are complete in that L2 once its
-// memory counter drains, and its peers read them with device-coherent loads (sc1), which miss the CU caches and hit the
-// XCD's L2. The stages are separated by XCD-local barriers on a counter word per XCD (an arrival is one atomic add; a
+// memory counter drains, and its peers read them with plain loads, which miss their CU's L1 (nothing there holds
+// those lines yet) and hit the XCD's L2. The stages are separated by XCD-local barriers on a counter word per XCD (an arrival is one atomic add; a
 // waiter polls with sc1 loads, every wait bounded: past its limit the workgroup records an error flag and goes on, so
 // no wave can hang).
 //
@@ -14,21 +14,26 @@
 //   1. indexer: scores of positions 1024 j .. 1024 j + 1023 (8 waves x 4 tiles of 32 keys, bf16 MFMA over the
 //      exactly converted e4m3 keys, the weighted relu head sum in registers; the arithmetic of
 //      trnrt/kernels/dsa_index.py:44-50), written to the scores output and kept in LDS, with an LDS histogram of the
-//      top 12 bits of their order keys added into the row's histogram; barrier A;
+//      top 12 bits of their order keys written as a list of its nonzero bins and, on rows long enough, a list of the
+//      workgroup's largest keys (whole bins, at most 192, in position order); barrier A;
+//   2+3 in one exchange (when every key at or above the row's keep-th largest is in the key lists, which the lists
+//      themselves show): every workgroup reads the 32 key lists and finds T, the ties to take and each workgroup's
+//      output offset from them alone, then lists its split's slots as stage 3 does; no barrier B. Otherwise:
 //   2. selection, first level: the row histogram gives the bin c0 of the keep-th largest key; the workgroup counts its
 //      keys above c0 and writes its keys in c0 (the candidates) in position order; barrier B;
 //   3. selection, exact: every workgroup reads the row's candidates (a few hundred for indexer scores) and finds the
 //      keep-th largest key T and the ties at T to take (the lowest positions, trnrt/models/dsa_select.py:10-38) by two
-//      LDS histogram passes (11 + 9 bits), then each workgroup's count and offset in the ascending output; the
-//      workgroup writes its own selected positions and their cache slots there; barrier C;
-//   4. attention: workgroup j takes head group j % (H / 16) and split j / (H / 16) of the ascending output: it reads
-//      the split's cache slots, gathers their rows into LDS and computes softmax(scale q.K) V over the split in one
-//      pass (bf16 MFMA over the exactly converted rows, fp32 softmax over the whole split), writing the split's
-//      normalised output with its max and sum (the arithmetic of trnrt/kernels/dsa_decode.py:26-37 and
-//      trnrt/kernels/dsa_slots.py:48-65); barrier D;
+//      LDS histogram passes (12 + 8 bits), then each workgroup's count and offset in the ascending output; from the
+//      row's bitmaps of selected positions the workgroup lists the cache slots of its own split's outputs and writes
+//      their indices (no barrier before the attention);
+//   4. attention: workgroup j takes head group j % (H / HPW) and split j / (H / HPW) of the ascending output: it
+//      gathers its split's rows into LDS and computes softmax(scale q.K) V over the split in one pass (bf16 MFMA over
+//      the exactly converted rows, fp32 softmax over the whole split), writing the split's normalised output with its
+//      max and sum (the arithmetic of trnrt/kernels/dsa_decode.py:26-37 and trnrt/kernels/dsa_slots.py:48-65);
+//      barrier C;
 //   5. combine: the splits merged by log-sum-exp (trnrt/models/mla.py:853-856), workgroup j for 1/32 of the outputs.
-// The histogram slice a workgroup owns is cleared after barrier B, and the last workgroup of an XCD to finish resets
-// the XCD's barrier words, so the workspace regions that must be zero between calls are zero again.
+// The last workgroup of an XCD to finish resets the XCD's barrier words, so the workspace region that must be zero
+// between calls is zero again.
 #include "dsa_common.h"
 
 namespace dsa {
@@ -56,6 +61,22 @@ constexpr int FU_CROW = 1088;
 constexpr int FU_CSTAGE = 128;                      // words of each block every workgroup reads into LDS
 constexpr int FU_CSTAGED = FU_CSTAGE - 1 - FU_BMW;  // candidates among them (the rest: read from the L2)
 static_assert(FU_CROW >= 1 + FU_BMW + FU_KEYS && FU_CROW % 4 == 0, "candidate block");
+// A workgroup's key list: its visible keys in the histogram bins down to the one holding its FU_LM-th largest key (all
+// of them when they number at most FU_LCAP; the bins above that one when it would hold more), in position order:
+// a 128-byte header (count, lowest bin listed (0: every visible key), 0, 0, then the workgroup's FU_LBINS highest
+// nonzero histogram bins as (bin << 16) | count in descending bin order, 0 past its nonzero bins), then (key,
+// position in the workgroup's range) pairs. Read back by 16 threads of FU_LPT entries each. Rows whose workgroups select FU_LM * 5 / 8 keys or fewer on average
+// (rows of at least 26,215 tokens at keep 2048) take the one-exchange selection from the lists; the others, and any
+// row whose lists turn out not to hold its selection, the two-exchange form (stages 2 and 3).
+constexpr int FU_LM = 128;
+constexpr int FU_LPT = 12;
+constexpr int FU_LCAP = 16 * FU_LPT;
+constexpr int FU_LHDR = 32;                 // header words
+constexpr int FU_LBINS = FU_LHDR - 4;       // bins in the header
+constexpr int FU_LROW = FU_LHDR + 2 * FU_LCAP;
+static_assert(FU_LBINS == 28, "two header bins for each of 14 of a list's 16 threads");
+static_assert(FU_LM <= FU_LCAP && FU_LPT % 2 == 0, "key list");
+static_assert(FU_HROW % 32 == 0 && FU_CROW % 32 == 0 && FU_LROW % 32 == 0, "a workgroup's rows in lines of its own");
 constexpr int FU_HPW = 16;         // heads per MFMA block of the attention
 constexpr int FU_CH = 64;          // slot granularity of a split
 constexpr int FU_SPLIT = 256;      // slots per split, at most
@@ -121,6 +142,7 @@ struct FuState {
   int gt[FU_NW];  // per workgroup: its candidates above T
   int eq[FU_NW];  // its candidates equal to T
   int c0, above0, nvis, pad;
+  int lbin[FU_NW];  // per workgroup: the lowest bin its key list holds
 };
 static_assert(sizeof(FuState) <= L_MISC, "state");
 
@@ -140,10 +162,12 @@ struct FusedArgs {
   uint16_t* out;
   float* lse;
   uint32_t* hl;    // [B][32][1056]: per workgroup its histogram's nonzero bins (count, then (bin << 16) | count)
-  int* sync;       // [8][16]: barrier words, zero between calls (the error flag excepted)
+  int* sync;       // [8][16]: per XCD the barrier arrivals and exits (zero between calls), an error flag (a wait
+                   // gave up) and the count of rows that took the two-exchange selection
   uint32_t* cand;  // [B][32][1088]: per workgroup (keys above c0) << 16 | (candidates), the bitmap of its positions
                    // above c0 (32 words), then the candidates, (low 20 key bits << 10) | position in the workgroup's
                    // range, in position order
+  uint32_t* lst;   // [B][32][FU_LROW]: per workgroup its key list
   uint16_t* part;  // [B][H][S][512]: split outputs (normalised, bf16), a head's splits side by side
 
   float2* ml;      // [B][H][S]: split max and sum
@@ -154,7 +178,12 @@ struct FusedArgs {
   int row0;  // this launch's first row (rows row0 .. row0 + 7)
 };
 
-// Device-coherent loads (sc1): they miss the CU's caches and read the XCD's L2, where a peer's completed stores are.
+// Device-scope loads (sc1) miss the CU's caches and are served past the XCD's L2 (measured: at a small fraction of
+// the L2's bandwidth). The kernel uses them only for the barrier polls and for the splits' (max, sum) pairs, which
+// peers write side by side within cache lines. Everything else a peer publishes before a barrier (bin lists,
+// candidate blocks, key lists, split outputs) is read with plain loads, which hit the XCD's L2: a CU's L1 holds no
+// stale copy of it, since the L1 is invalidated at each launch's start, no workgroup reads a peer's region before the
+// barrier that publishes it, and each workgroup's region of each kind occupies whole 128-byte lines of its own.
 __device__ __forceinline__ int ld_sc1(const int* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -164,7 +193,7 @@ __device__ __forceinline__ uint32_t ld_sc1(const uint32_t* p) {
 __device__ __forceinline__ uint64_t ld_sc1_64(const void* p) {
   return __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-constexpr int FU_AUX_SC1 = 16;  // the cache-policy operand of the direct-to-LDS loads: sc1
+constexpr int FU_AUX_PLAIN = 0;  // the cache-policy operand of the loads of a peer's published data: none
 
 // XCD-local barrier of the 32 workgroups of an XCD: every thread's stores complete (drained memory counter), then the
 // workgroup's arrival (one atomic add) and a bounded poll. The XCD's counter is zero at a launch's start (the last
@@ -248,6 +277,30 @@ __device__ __forceinline__ uint32_t fu_block_prefix(uint32_t mine, int* scr, uin
   return before;
 }
 
+// The workgroup's 1024 scores from LDS into the score output (positions 1024 j + e; none past the row's stride). They
+// are written after barrier A, behind the selection's first loads, so that their write latency overlaps the selection
+// instead of holding up the indexer's end (a wait for the memory counter there would wait for them).
+__device__ __forceinline__ void fu_store_scores(const FusedArgs& a, const uint8_t* lds, int b, int j) {
+  const float* sc = reinterpret_cast<const float*>(lds + L_SCS);
+  float* srow = a.scores + (size_t)b * a.stride;
+#pragma unroll
+  for (int e = threadIdx.x; e < FU_KEYS; e += FU_THREADS)
+    if (j * FU_KEYS + e < a.stride) srow[j * FU_KEYS + e] = sc[e];
+}
+
+// Whether a row of L tokens takes the one-exchange selection from the key lists (workgroup-uniform).
+__device__ __forceinline__ bool fu_lists_on(const FusedArgs& a, int L) {
+  return (long)a.keep * FU_KEYS * 8 <= 5L * FU_LM * L;
+}
+
+// This thread's two keys (positions tid, tid + 512 of the workgroup's range; 0: not selectable).
+__device__ __forceinline__ void fu_my_keys(const uint8_t* lds, uint32_t (&key)[2]) {
+  const float* sc = reinterpret_cast<const float*>(lds + L_SCS);
+  const float v0 = sc[threadIdx.x], v1 = sc[threadIdx.x + FU_THREADS];
+  key[0] = order_key(v0) & (0u - (uint32_t)(v0 > VISIBLE));
+  key[1] = order_key(v1) & (0u - (uint32_t)(v1 > VISIBLE));
+}
+
 // Stage 1: the indexer scores of positions 1024 j .. 1024 j + 1023 of row b (L: the row's length). Each wave streams
 // its 4 tiles of 32 keys FU_AHEAD ahead of its MFMAs.
 template <int MT>
@@ -305,6 +358,8 @@ __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int
   if (tid < 32 * MT) wsh[tid] = tid < Hi ? wv : 0.0f;
   if (lane < FU_TPW) tpg[wave * FU_TPW + lane] = pages;
   for (int i = tid; i < FU_HBINS; i += FU_THREADS) hs[i] = 0;
+  int* scr = reinterpret_cast<int*>(lds + L_MISC);
+  if (tid == 0) scr[8] = -1;  // the key list's bin search below
   __syncthreads();
 
   if (live) {
@@ -350,44 +405,72 @@ __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int
       part += __shfl_xor(part, 32, WAVE);
       const float v = pos < L ? part * ksc[i] : NEG_INF;
       if (h == 0) {
-        if (pos < a.stride) srow[pos] = v;
         scs[pos - j * FU_KEYS] = v;
         if (v > VISIBLE) atomicAdd(&hs[order_key(v) >> 20], 1);
       }
     }
   } else {
-    // every key of this wave is past the row: NEG_INF
+    // every key of this wave is past the row: NEG_INF (into the score output after barrier A, with the others)
     for (int e = lane; e < FU_TPW * FU_TILE; e += WAVE) {
       const int pos = t_begin * FU_TILE + e;
-      if (pos < a.stride) srow[pos] = NEG_INF;
       scs[pos - j * FU_KEYS] = NEG_INF;
     }
   }
   // positions past 32,768 of a wider score row are never keys of the row
   for (int p = FU_MAXLEN + j * FU_THREADS + tid; p < a.stride; p += FU_NW * FU_THREADS) srow[p] = NEG_INF;
   __syncthreads();
-  // the histogram's nonzero bins into the workgroup's bin list (thread t: bins 8 t .. 8 t + 7), in bin order
+  // the histogram's nonzero bins into the workgroup's bin list (thread t: bins 8 t .. 8 t + 7), in bin order, and
+  // the workgroup's key list: the bin of its FU_LM-th largest key, then its keys from that bin up (or from the next
+  // bin up when that would overflow the list; every key when they fit), the first half's by thread, then the second
+  // half's
   int hv[8];
   *reinterpret_cast<int4*>(hv) = *reinterpret_cast<const int4*>(hs + 8 * tid);
   *reinterpret_cast<int4*>(hv + 4) = *reinterpret_cast<const int4*>(hs + 8 * tid + 4);
+  const bool lists = fu_lists_on(a, L);
+  int lbin = FU_HBINS, lcnt = 0;  // no list
+  if (lists) {
+    int lb, labove;
+    const int nv = fu_find_bin<8>(hv, FU_LM, scr, &lb, &labove);
+    lbin = 0;
+    lcnt = nv;
+    if (nv > FU_LCAP) {
+      const int nb = labove + hs[lb];
+      lbin = nb <= FU_LCAP ? lb : lb + 1;
+      lcnt = nb <= FU_LCAP ? nb : labove;
+    }
+  }
+  uint32_t key[2];
+  fu_my_keys(lds, key);
+  const bool in0 = key[0] != 0u && (int)(key[0] >> 20) >= lbin, in1 = key[1] != 0u && (int)(key[1] >> 20) >= lbin;
   uint32_t nz = 0;
 #pragma unroll
   for (int i = 0; i < 8; ++i) nz += hv[i] != 0;
+  // (nonzero bins) << 20 | (listed keys of the first half) << 10 | (of the second half): at most 1024, 512, 512
   uint32_t tot;
-  uint32_t o = fu_block_prefix(nz, reinterpret_cast<int*>(lds + L_MISC), &tot);
+  const uint32_t before = fu_block_prefix((nz << 20) | ((uint32_t)in0 << 10) | (uint32_t)in1, scr, &tot);
   uint32_t* hl = a.hl + ((size_t)b * FU_NW + j) * FU_HROW;
+  uint32_t* lrow = a.lst + ((size_t)b * FU_NW + j) * FU_LROW;
+  const int nzt = (int)(tot >> 20);
+  uint32_t o = before >> 20;
 #pragma unroll
   for (int i = 0; i < 8; ++i)
-    if (hv[i]) hl[1 + o++] = ((uint32_t)(8 * tid + i) << 16) | (uint32_t)hv[i];
-  if (tid == 0) hl[0] = tot;
-}
-
-// This thread's two keys (positions tid, tid + 512 of the workgroup's range; 0: not selectable).
-__device__ __forceinline__ void fu_my_keys(const uint8_t* lds, uint32_t (&key)[2]) {
-  const float* sc = reinterpret_cast<const float*>(lds + L_SCS);
-  const float v0 = sc[threadIdx.x], v1 = sc[threadIdx.x + FU_THREADS];
-  key[0] = order_key(v0) & (0u - (uint32_t)(v0 > VISIBLE));
-  key[1] = order_key(v1) & (0u - (uint32_t)(v1 > VISIBLE));
+    if (hv[i]) {
+      const uint32_t e = ((uint32_t)(8 * tid + i) << 16) | (uint32_t)hv[i];
+      hl[1 + o] = e;
+      const int d = nzt - 1 - (int)o;  // this bin's place among the nonzero bins from the top
+      if (lists && d < FU_LBINS) lrow[4 + d] = e;
+      ++o;
+    }
+  if (lists) {
+    if (in0)
+      *reinterpret_cast<uint2*>(lrow + FU_LHDR + 2 * ((before >> 10) & 1023u)) = uint2{key[0], (uint32_t)tid};
+    if (in1)
+      *reinterpret_cast<uint2*>(lrow + FU_LHDR + 2 * (((tot >> 10) & 1023u) + (before & 1023u))) =
+          uint2{key[1], (uint32_t)(tid + FU_THREADS)};
+    if (tid >= nzt && tid < FU_LBINS) lrow[4 + tid] = 0u;
+    if (tid == 0) *reinterpret_cast<uint4*>(lrow) = uint4{(uint32_t)lcnt, (uint32_t)lbin, 0u, 0u};
+  }
+  if (tid == 0) hl[0] = (uint32_t)nzt;
 }
 
 // Stage 2: the first level from the row histogram, this workgroup's keys above it counted and its candidates written.
@@ -405,7 +488,7 @@ __device__ __forceinline__ void fu_classify(const FusedArgs& a, uint8_t* lds, in
   for (int i = wave; i < FU_NW; i += FU_WAVES)
     __builtin_amdgcn_global_load_lds(hlg + (size_t)i * FU_HROW + 4 * lane,
                                      (__attribute__((address_space(3))) void*)(hls + FU_HSTAGE * i), 16, 0,
-                                     FU_AUX_SC1);
+                                     FU_AUX_PLAIN);
   *reinterpret_cast<int4*>(rh + PER * tid) = int4{0, 0, 0, 0};
   *reinterpret_cast<int4*>(rh + PER * tid + 4) = int4{0, 0, 0, 0};
   uint32_t key[2];
@@ -424,7 +507,7 @@ __device__ __forceinline__ void fu_classify(const FusedArgs& a, uint8_t* lds, in
     for (int i = 0; i < 8; ++i)
       if (q + 16 * i < n) atomicAdd(&rh[v[i] >> 16], (int)(v[i] & 0xFFFFu));
     for (int e = q + 128; e < n; e += 16) {
-      const uint32_t x = e + 1 < FU_HSTAGE ? lw[1 + e] : ld_sc1(hlg + (size_t)w * FU_HROW + 1 + e);
+      const uint32_t x = e + 1 < FU_HSTAGE ? lw[1 + e] : hlg[(size_t)w * FU_HROW + 1 + e];
       atomicAdd(&rh[x >> 16], (int)(x & 0xFFFFu));
     }
   }
@@ -468,6 +551,87 @@ __device__ __forceinline__ void fu_classify(const FusedArgs& a, uint8_t* lds, in
   }
 }
 
+// The end of the selection, shared by its two forms: every workgroup's selected positions are in the bitmaps at L_SB
+// (lane w of every wave: workgroup w's selected count selw and first output index offw), the pages of the positions
+// from page pg0 on at L_SPG (this wave's loads of them may be in flight). The workgroup writes the indices of its
+// split's outputs [o0, o1), lists their cache slots at FuAtt<HPW>::L_P, stages the attention's queries and returns the
+// split's selected count.
+template <int HPW>
+__device__ __forceinline__ int fu_split_slots(const FusedArgs& a, uint8_t* lds, int b, int j, int selw, int offw,
+                                              int o0, int o1, int cnt_row, int pg0,
+                                              const u32x4 (&qv)[FuAtt<HPW>::QPT], float* live_bias) {
+  using AT = FuAtt<HPW>;
+  constexpr int QPT = AT::QPT;
+  const uint32_t* sb = reinterpret_cast<const uint32_t*>(lds + L_SB);
+  int* pb = reinterpret_cast<int*>(lds + L_PB);
+  const int* spg = reinterpret_cast<const int*>(lds + L_SPG);
+  int* slot_l = reinterpret_cast<int*>(lds + AT::L_P);
+  const int tid = threadIdx.x, lane = tid & (WAVE - 1), w = tid >> 4, q = tid & 15;
+  const int hg = j % a.HG, s = j / a.HG;
+  const bool active = s < a.S;
+  // exclusive prefix popcounts of each block's selected bitmap (thread (w, q): words 2 q, 2 q + 1)
+  {
+    const int c_a = __builtin_popcount(sb[FU_BMW * w + 2 * q]), c_b = __builtin_popcount(sb[FU_BMW * w + 2 * q + 1]);
+    const int incl = row_incl_scan(c_a + c_b);
+    pb[FU_BMW * w + 2 * q] = incl - c_a - c_b;
+    pb[FU_BMW * w + 2 * q + 1] = incl - c_b;
+  }
+  // the queries into LDS for stage 4, head pc / 72, elements 8 (pc % 72) .. of piece pc (before the index stores
+  // below: a wait for the queries' loads there would also wait for those stores)
+  if (active) {
+    uint16_t* qs = reinterpret_cast<uint16_t*>(lds + AT::L_QST);
+#pragma unroll
+    for (int i = 0; i < QPT; ++i) {
+      const int pc = tid + FU_THREADS * i;
+      if (pc < HPW * FU_DQK / 8)
+        *reinterpret_cast<u32x4*>(qs + (pc / (FU_DQK / 8)) * FU_AQROW + 8 * (pc % (FU_DQK / 8))) = qv[i];
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's page loads have landed
+  __syncthreads();
+  // the split's sources exactly: the workgroups whose outputs meet [o0, o1); each thread takes a byte of their
+  // bitmaps (at most 8 selected positions, so a dense selection costs no more than a sparse one) and lists each
+  // selected position whose output falls in the split
+  int* irow = a.idx + (size_t)b * a.keep;
+  const uint64_t ms = __ballot(lane < FU_NW && selw > 0 && offw < o1 && offw + selw > o0);
+  if (ms) {
+    const int wa = (int)__builtin_ctzll(ms), nbytes = 4 * FU_BMW * (64 - (int)__builtin_clzll(ms) - wa);
+    for (int k = tid; k < nbytes; k += FU_THREADS) {
+      const int sw = wa + k / (4 * FU_BMW), i = (k / 4) % FU_BMW, by = 8 * (k & 3);
+      const uint32_t word = sb[FU_BMW * sw + i];
+      uint32_t bits = (word >> by) & 255u;
+      int o = __shfl(offw, sw, WAVE) + pb[FU_BMW * sw + i] + __builtin_popcount(word & ((1u << by) - 1u));
+      // the word's 32 positions lie in one page (pages of at least 32 tokens)
+      const int p0 = FU_KEYS * sw + 32 * i;
+      const int sbase =
+          safe_page(spg[(p0 >> a.page_shift) - pg0], a.num_pages) * a.page_size + (p0 & (a.page_size - 1)) + by;
+      while (bits) {
+        const int bit = __builtin_ctz(bits);
+        bits &= bits - 1u;
+        if (o >= o0 && o < o1) {
+          slot_l[o - o0] = sbase + bit;
+          if (hg == 0) irow[o] = p0 + by + bit;
+        }
+        ++o;
+      }
+    }
+  }
+  // the outputs past the count, and the count
+  if (hg == 0)
+    for (int o = max(o0, cnt_row) + tid; o < o1; o += FU_THREADS) irow[o] = 0;
+  if (j == 0 && tid == 0) a.cnt[b] = cnt_row;
+  // the split's live slots; a row with none attends position 0 masked (its lse is NEG_INF)
+  int n_slots = max(min(o1, cnt_row) - o0, 0);
+  *live_bias = 0.0f;
+  if (active && cnt_row == 0 && s == 0) {
+    n_slots = 1;
+    *live_bias = NEG_INF;
+    if (tid == 0) slot_l[0] = safe_page(a.table[(size_t)b * a.max_pages], a.num_pages) * a.page_size;
+  }
+  __syncthreads();  // the slot list
+  return n_slots;
+}
+
 // Stage 3: the exact selection and this workgroup's split of it. Every workgroup reads the first 128 words of every
 // candidate block (the counts, the bitmap of the positions above c0, the first 95 candidates) and finds T (the
 // keep-th largest key), the ties at T to take and each workgroup's output offset; the candidates taken join the
@@ -499,7 +663,7 @@ __device__ __forceinline__ int fu_select(const FusedArgs& a, uint8_t* lds, int b
   for (int i = wave; i < FU_NW / 2; i += FU_WAVES)
     __builtin_amdgcn_global_load_lds(cblk + (size_t)(2 * i + (lane >> 5)) * FU_CROW + 4 * (lane & 31),
                                      (__attribute__((address_space(3))) void*)(cb + 2 * FU_CSTAGE * i), 16, 0,
-                                     FU_AUX_SC1);
+                                     FU_AUX_PLAIN);
   // the attention's HPW heads' queries: their QPT loads go out after the block loads (kept in that order) and are
   // used after the selection
   __builtin_amdgcn_sched_barrier(0);
@@ -525,7 +689,7 @@ __device__ __forceinline__ int fu_select(const FusedArgs& a, uint8_t* lds, int b
   sb[FU_BMW * w + 2 * q] = cw[1 + 2 * q];
   sb[FU_BMW * w + 2 * q + 1] = cw[2 + 2 * q];
   auto cand_at = [&](int e) __attribute__((always_inline)) {
-    return e < FU_CSTAGED ? cw[1 + FU_BMW + e] : ld_sc1(cblk + (size_t)w * FU_CROW + 1 + FU_BMW + e);
+    return e < FU_CSTAGED ? cw[1 + FU_BMW + e] : cblk[(size_t)w * FU_CROW + 1 + FU_BMW + e];
   };
   const uint32_t cq = q < nc ? cw[1 + FU_BMW + q] : 0u;  // this thread's first candidate (most blocks have <= 16)
   // lane w of every wave: block w's counts; the sources the split can draw on whatever T turns out to be (block w's
@@ -626,67 +790,195 @@ __device__ __forceinline__ int fu_select(const FusedArgs& a, uint8_t* lds, int b
     }
   }
   __syncthreads();
-  // exclusive prefix popcounts of each block's selected bitmap (thread (w, q): words 2 q, 2 q + 1)
-  {
-    const int c_a = __builtin_popcount(sb[FU_BMW * w + 2 * q]), c_b = __builtin_popcount(sb[FU_BMW * w + 2 * q + 1]);
-    const int incl = row_incl_scan(c_a + c_b);
-    pb[FU_BMW * w + 2 * q] = incl - c_a - c_b;
-    pb[FU_BMW * w + 2 * q + 1] = incl - c_b;
-  }
-  // the queries into LDS for stage 4, head pc / 72, elements 8 (pc % 72) .. of piece pc (before the index stores
-  // below: a wait for the queries' loads there would also wait for those stores)
-  if (active) {
-    uint16_t* qs = reinterpret_cast<uint16_t*>(lds + AT::L_QST);
+  return fu_split_slots<HPW>(a, lds, b, j, selw, offw, o0, o1, cnt_row, pg0, qv, live_bias);
+}
+
+// Stages 2 and 3 in one exchange, from the key lists: every workgroup reads all 32 lists of the row (thread (w, q):
+// list w's entries FU_LPT q .. + FU_LPT - 1) and the row's pages. Every key of the row at or above the lowest bin of
+// each list is in the lists, so when the bin c0 of the lists' keep-th largest key is at or above every list's lowest
+// bin, the lists hold every key at or above the row's keep-th largest, and T (the keep-th largest), the ties at T to
+// take (the lowest positions) and each workgroup's selected count follow from the lists alone (three histogram passes
+// over their keys: 12, 12 and 8 bits). Returns false when they do not (every workgroup of the row decides alike, and
+// nothing but LDS has been written): the caller then takes the two-exchange form.
+template <int HPW>
+__device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds, int b, int j, int L,
+                                                u32x4 (&qv)[FuAtt<HPW>::QPT], float* live_bias, int* n_slots) {
+  using AT = FuAtt<HPW>;
+  constexpr int QPT = AT::QPT;
+  FuState& st = *reinterpret_cast<FuState*>(lds + L_STATE);
+  int* scr = reinterpret_cast<int*>(lds + L_MISC);
+  int* bins0 = reinterpret_cast<int*>(lds + L_CB);
+  int* bins1 = reinterpret_cast<int*>(lds + L_BINS);
+  int* bins2 = reinterpret_cast<int*>(lds + L_BINS2);
+  int* spg = reinterpret_cast<int*>(lds + L_SPG);
+  uint32_t* sb = reinterpret_cast<uint32_t*>(lds + L_SB);
+  int* slot_l = reinterpret_cast<int*>(lds + AT::L_P);
+  const int tid = threadIdx.x, wave = tid / WAVE, lane = tid & (WAVE - 1);
+  const int w = tid >> 4, q = tid & 15;
+  const int hg = j % a.HG, s = j / a.HG;
+  const bool active = s < a.S;  // workgroup-uniform: a workgroup past the last split only helps with the barriers
+  const int o0 = active ? s * a.sps : 0, o1 = active ? min(o0 + a.sps, a.keep) : 0;
+  // list w's counts and this thread's entries (device-coherent buffer loads: the lists are the peers' stores)
+  constexpr int NL = FU_LPT / 2;
+  const __amdgpu_buffer_rsrc_t lrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.lst + (size_t)b * FU_NW * FU_LROW), (short)0, FU_NW * FU_LROW * 4, FU_BUF_WORD3);
+  const int lo = 4 * FU_LROW * w;
+  const uint32_t hw0 = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(lrs, lo, 0, FU_AUX_PLAIN);
+  const uint32_t hw1 = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(lrs, lo + 4, 0, FU_AUX_PLAIN);
+  // header bins 2 q, 2 q + 1 (threads q < 14)
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  const u32x2 hp = __builtin_bit_cast(
+      u32x2, __builtin_amdgcn_raw_buffer_load_b64(lrs, lo + 16 + 8 * min(q, FU_LBINS / 2 - 1), 0, FU_AUX_PLAIN));
+  u32x4 ev[NL];
 #pragma unroll
-    for (int i = 0; i < QPT; ++i) {
-      const int pc = tid + FU_THREADS * i;
-      if (pc < HPW * FU_DQK / 8)
-        *reinterpret_cast<u32x4*>(qs + (pc / (FU_DQK / 8)) * FU_AQROW + 8 * (pc % (FU_DQK / 8))) = qv[i];
-    }
+  for (int i = 0; i < NL; ++i)
+    ev[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                          lrs, lo + 4 * FU_LHDR + 8 * FU_LPT * q + 16 * i, 0, FU_AUX_PLAIN));
+  __builtin_amdgcn_sched_barrier(0);
+  // the row's pages into registers (pages tid, tid + 512, clamped: at most 1024 pages of at least 32 tokens), staged
+  // in LDS at the end (loads straight into LDS here would make every LDS access below wait for all loads, the
+  // queries' included)
+  int pgv[2];
+  {
+    const int* trow = a.table + (size_t)b * a.max_pages;
+    const int npg = (L + a.page_size - 1) >> a.page_shift;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) pgv[c] = trow[max(min(min(tid + FU_THREADS * c, npg - 1), a.max_pages - 1), 0)];
   }
-  __builtin_amdgcn_s_waitcnt(0);  // this wave's page loads have landed
+  __builtin_amdgcn_sched_barrier(0);
+  {
+    // (unconditional: a workgroup past the last split loads its head group's queries and never uses them, and no
+    // register copy of a query waits for its load at a join)
+    const u32x4* qsrc = reinterpret_cast<const u32x4*>(a.q + ((size_t)b * a.H + HPW * hg) * FU_DQK);
+#pragma unroll
+    for (int i = 0; i < QPT; ++i) qv[i] = qsrc[min(tid + FU_THREADS * i, HPW * FU_DQK / 8 - 1)];
+  }
+  fu_store_scores(a, lds, b, j);
+  __builtin_amdgcn_sched_barrier(0);
+  for (int i = tid; i < 4096; i += FU_THREADS) bins0[i] = bins1[i] = 0;
+  if (tid < 256) bins2[tid] = 0;
+  sb[tid] = sb[tid + FU_THREADS] = 0u;
+  if (tid < AT::SPLIT) slot_l[tid] = 0;  // padding rows read slot 0
+  if (tid == 0) scr[8] = scr[24] = scr[40] = -1;
+  __builtin_amdgcn_sched_barrier(0);
+  __syncthreads();  // the bins cleared (the loads above may be out; their first uses wait for them)
+  const int nw = min((int)hw0, FU_LCAP) - FU_LPT * q;  // this thread's entries: those below nw
+  uint32_t key[FU_LPT], pos[FU_LPT];
+#pragma unroll
+  for (int i = 0; i < FU_LPT; ++i) {
+    key[i] = i < nw ? ev[i / 2][2 * (i & 1)] : 0u;
+    pos[i] = ev[i / 2][2 * (i & 1) + 1] & 1023u;
+  }
+  // the keys pass through an empty asm between the passes below, so that no compare mask over them is kept across
+  // passes (twelve 64-bit masks held in scalar registers spill)
+  auto fresh = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < FU_LPT; ++i) asm volatile("" : "+v"(key[i]));
+  };
+  // the first level from the lists' header bins (their bins at or above the lowest listed are exactly the listed
+  // keys' bins); a list whose 28th header bin is listed may list more bins than its header holds: its keys one by one
+  const bool hfull = q == FU_LBINS / 2 - 1 && hp[1] != 0u && (hp[1] >> 16) >= hw1;
+  if ((__ballot(hfull) >> (16 * (w & 3))) & 0xFFFFull) {
+#pragma unroll
+    for (int i = 0; i < FU_LPT; ++i)
+      if (key[i]) atomicAdd(&bins0[key[i] >> 20], 1);
+  } else if (q < FU_LBINS / 2) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+      if (hp[k] != 0u && (hp[k] >> 16) >= hw1) atomicAdd(&bins0[hp[k] >> 16], (int)(hp[k] & 0xFFFFu));
+  }
+  fresh();
+  if (q == 0) st.lbin[w] = (int)hw1;
   __syncthreads();
-  // the split's sources exactly: the workgroups whose outputs meet [o0, o1); each thread takes a byte of their
-  // bitmaps (at most 8 selected positions, so a dense selection costs no more than a sparse one) and lists each
-  // selected position whose output falls in the split
-  int* irow = a.idx + (size_t)b * a.keep;
-  const uint64_t ms = __ballot(lane < FU_NW && selw > 0 && offw < o1 && offw + selw > o0);
-  if (ms) {
-    const int wa = (int)__builtin_ctzll(ms), nbytes = 4 * FU_BMW * (64 - (int)__builtin_clzll(ms) - wa);
-    for (int k = tid; k < nbytes; k += FU_THREADS) {
-      const int sw = wa + k / (4 * FU_BMW), i = (k / 4) % FU_BMW, by = 8 * (k & 3);
-      const uint32_t word = sb[FU_BMW * sw + i];
-      uint32_t bits = (word >> by) & 255u;
-      int o = __shfl(offw, sw, WAVE) + pb[FU_BMW * sw + i] + __builtin_popcount(word & ((1u << by) - 1u));
-      // the word's 32 positions lie in one page (pages of at least 32 tokens)
-      const int p0 = FU_KEYS * sw + 32 * i;
-      const int sbase =
-          safe_page(spg[(p0 >> a.page_shift) - pg0], a.num_pages) * a.page_size + (p0 & (a.page_size - 1)) + by;
-      while (bits) {
-        const int bit = __builtin_ctz(bits);
-        bits &= bits - 1u;
-        if (o >= o0 && o < o1) {
-          slot_l[o - o0] = sbase + bit;
-          if (hg == 0) irow[o] = p0 + by + bit;
-        }
-        ++o;
-      }
+  constexpr int P1 = 4096 / FU_THREADS;
+  int hb[P1];
+  *reinterpret_cast<int4*>(hb) = *reinterpret_cast<const int4*>(bins0 + P1 * tid);
+  *reinterpret_cast<int4*>(hb + 4) = *reinterpret_cast<const int4*>(bins0 + P1 * tid + 4);
+  int c0, above0;
+  const int nlist = fu_find_bin<P1>(hb, a.keep, scr, &c0, &above0);
+  const uint32_t lmax = wave_max_u32(lane < FU_NW ? (uint32_t)st.lbin[lane] : 0u);
+  int cnt_row;
+  if (lmax == 0u) {
+    // every list holds all its workgroup's keys
+    cnt_row = min(nlist, a.keep);
+    if (nlist <= a.keep) c0 = -1;  // every selectable key is selected
+  } else {
+    if (nlist < a.keep || c0 < (int)lmax) return false;
+    cnt_row = a.keep;
+  }
+  // T and the room for ties at T; with c0 = -1, T = 0 (below every listed key) and no ties
+  uint32_t T = 0u;
+  int room = 0;
+  if (c0 >= 0) {
+#pragma unroll
+    for (int i = 0; i < FU_LPT; ++i)
+      if (key[i] && (int)(key[i] >> 20) == c0) atomicAdd(&bins1[(key[i] >> 8) & 4095u], 1);
+    fresh();
+    __syncthreads();
+    *reinterpret_cast<int4*>(hb) = *reinterpret_cast<const int4*>(bins1 + P1 * tid);
+    *reinterpret_cast<int4*>(hb + 4) = *reinterpret_cast<const int4*>(bins1 + P1 * tid + 4);
+    int c1, above1;
+    int need = a.keep - above0;
+    fu_find_bin<P1>(hb, need, scr + 16, &c1, &above1);
+    need -= above1;
+    uint32_t tlow;
+    if (need >= bins1[c1]) {
+      // every key of bin c1 is taken: T is the bin's lowest key, and all its ties
+      tlow = (uint32_t)c1 << 8;
+      room = need;
+    } else {
+      const uint32_t hi24 = ((uint32_t)c0 << 12) | (uint32_t)c1;
+#pragma unroll
+      for (int i = 0; i < FU_LPT; ++i)
+        if (key[i] && (key[i] >> 8) == hi24) atomicAdd(&bins2[key[i] & 255u], 1);
+      fresh();
+      __syncthreads();
+      const int hb2[1] = {tid < 256 ? bins2[tid] : 0};
+      int c2, above2;
+      fu_find_bin<1>(hb2, need, scr + 32, &c2, &above2);
+      tlow = ((uint32_t)c1 << 8) | (uint32_t)c2;
+      room = max(need - above2, 0);
     }
+    T = ((uint32_t)c0 << 20) | tlow;
   }
-  // the outputs past the count, and the count
-  if (hg == 0)
-    for (int o = max(o0, cnt_row) + tid; o < o1; o += FU_THREADS) irow[o] = 0;
-  if (j == 0 && tid == 0) a.cnt[b] = cnt_row;
-  // the split's live slots; a row with none attends position 0 masked (its lse is NEG_INF)
-  int n_slots = max(min(o1, cnt_row) - o0, 0);
-  *live_bias = 0.0f;
-  if (active && cnt_row == 0 && s == 0) {
-    n_slots = 1;
-    *live_bias = NEG_INF;
-    if (tid == 0) slot_l[0] = safe_page(a.table[(size_t)b * a.max_pages], a.num_pages) * a.page_size;
+  // per list: its keys above T (into its bitmap now) and equal to T, and this thread's ties before it in the list
+  int gt = 0, eq = 0;
+#pragma unroll
+  for (int i = 0; i < FU_LPT; ++i) {
+    gt += key[i] > T;
+    eq += key[i] == T && key[i];
+    if (key[i] > T) atomicOr(&sb[FU_BMW * w + (pos[i] >> 5)], 1u << (pos[i] & 31u));
   }
-  __syncthreads();  // the slot list
-  return n_slots;
+  fresh();
+  const int eq_in = row_incl_scan(eq);
+  gt = row_sum(gt);
+  if (q == 15) {
+    st.gt[w] = gt;
+    st.eq[w] = eq_in;
+  }
+  __syncthreads();
+  // every wave: per list w (lane w) the ties at T before it, its selected count and first output index (ties are
+  // taken while fewer than `room` come before)
+  const int ww = lane & (FU_NW - 1);
+  const int eqw = lane < FU_NW ? st.eq[ww] : 0;
+  const int tbw = wave_incl_scan(eqw) - eqw;
+  const int selw = lane < FU_NW ? st.gt[ww] + min(max(room - tbw, 0), eqw) : 0;
+  const int offw = wave_incl_scan(selw) - selw;
+  const int tb_list = __shfl(tbw, w, WAVE);  // with every lane active: a lane switched off returns no value
+  if (eq > 0) {
+    int k = tb_list + eq_in - eq;  // the row's ties before this thread's first
+#pragma unroll
+    for (int i = 0; i < FU_LPT; ++i)
+      if (key[i] == T && key[i]) {
+        if (k < room) atomicOr(&sb[FU_BMW * w + (pos[i] >> 5)], 1u << (pos[i] & 31u));
+        ++k;
+      }
+  }
+  spg[tid] = pgv[0];
+  spg[tid + FU_THREADS] = pgv[1];
+  __syncthreads();
+  *n_slots = fu_split_slots<HPW>(a, lds, b, j, selw, offw, o0, o1, cnt_row, 0, qv, live_bias);
+  return true;
 }
 
 // The value operand of v_mfma_f32_16x16x32_bf16 from the token-major tile (ds_read_b64_tr_b8: lane (a, c) of each
@@ -918,7 +1210,7 @@ __device__ __forceinline__ void fu_combine_heads(const FusedArgs& a, float* wts,
   uint32_t ov[NS];
 #pragma unroll
   for (int k = 0; k < NS; ++k)
-    ov[k] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(prs, voff, 2 * FU_DV * min(k, S - 1), FU_AUX_SC1);
+    ov[k] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(prs, voff, 2 * FU_DV * min(k, S - 1), FU_AUX_PLAIN);
   if (tid < WAVE) {
     const float m = __uint_as_float((uint32_t)mlv), l = __uint_as_float((uint32_t)(mlv >> 32));
     const bool live = sp < S && l > 0.0f;
@@ -979,14 +1271,22 @@ __global__ __launch_bounds__(FU_THREADS, 1) void decode_fused_kernel(FusedArgs a
   if (b >= a.B) return;  // an XCD without a row
   const int L = min(max(a.ctx_len[b], 0), min(a.stride, FU_MAXLEN));
   fu_indexer<MT>(a, lds, b, j, L);
-  fu_barrier(sync, 1);  // A: the row's scores and histogram
-  fu_classify(a, lds, b, j);
-  fu_barrier(sync, 2);  // B: every workgroup's counts and candidates
+  fu_barrier(sync, 1);  // A: the row's scores, histogram and key lists
   u32x4 qv[FuAtt<HPW>::QPT];
   float live_bias;
-  const int n_slots = fu_select<HPW>(a, lds, b, j, L, qv, &live_bias);
+  int n_slots, nbar = 2;
+  const bool lists = fu_lists_on(a, L);
+  if (!(lists && fu_select_lists<HPW>(a, lds, b, j, L, qv, &live_bias, &n_slots))) {
+    __syncthreads();  // every thread has read the bin search's results before stage 2 reuses its words
+    if (!lists) fu_store_scores(a, lds, b, j);
+    if (j == 0 && threadIdx.x == 0) __hip_atomic_fetch_add(sync + 3, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    fu_classify(a, lds, b, j);
+    fu_barrier(sync, 2);  // B: every workgroup's counts and candidates
+    n_slots = fu_select<HPW>(a, lds, b, j, L, qv, &live_bias);
+    nbar = 3;
+  }
   fu_attend<HPW>(a, lds, b, j, n_slots, live_bias);
-  fu_barrier(sync, 3);  // C: every split's output
+  fu_barrier(sync, nbar);  // C: every split's output
   fu_combine(a, lds, b, j);
   fu_exit(sync);
 }
@@ -1074,14 +1374,15 @@ static size_t fu_up256(size_t x) { return (x + 255) & ~(size_t)255; }
 // Workspace of the fused layer past the zero region (histograms + barrier words; the fused layer uses only the barrier
 // words): the per-workgroup bin lists and candidate blocks, the split outputs and their (max, sum).
 struct FusedLayout {
-  size_t hl, cand, part, ml, end;
+  size_t hl, cand, lst, part, ml, end;
 };
 
 static FusedLayout fused_layout(size_t zero_bytes, int B, int H, int S, int keep) {
   FusedLayout l;
   l.hl = zero_bytes;
   l.cand = l.hl + fu_up256((size_t)B * FU_NW * FU_HROW * 4);
-  l.part = l.cand + fu_up256((size_t)B * FU_NW * FU_CROW * 4);
+  l.lst = l.cand + fu_up256((size_t)B * FU_NW * FU_CROW * 4);
+  l.part = l.lst + fu_up256((size_t)B * FU_NW * FU_LROW * 4);
   l.ml = l.part + fu_up256((size_t)B * S * H * FU_DV * 2);
   l.end = l.ml + fu_up256((size_t)B * S * H * sizeof(float2));
   return l;
@@ -1199,6 +1500,7 @@ hipError_t launch_decode_fused(const uint16_t* q_idx, const float* w, const uint
   a.hl = reinterpret_cast<uint32_t*>(p + l.hl);
   a.sync = reinterpret_cast<int*>(p + hist_bytes);
   a.cand = reinterpret_cast<uint32_t*>(p + l.cand);
+  a.lst = reinterpret_cast<uint32_t*>(p + l.lst);
   a.part = reinterpret_cast<uint16_t*>(p + l.part);
   a.ml = reinterpret_cast<float2*>(p + l.ml);
   a.B = B;
