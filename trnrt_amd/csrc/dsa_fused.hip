@@ -168,7 +168,7 @@ struct FusedArgs {
                    // above c0 (32 words), then the candidates, (low 20 key bits << 10) | position in the workgroup's
                    // range, in position order
   uint32_t* lst;   // [B][32][FU_LROW]: per workgroup its key list
-  uint16_t* part;  // [B][H][S][512]: split outputs (normalised, bf16), a head's splits side by side
+  uint16_t* part;  // [B][S][H][512]: split outputs (normalised, bf16), a split's heads side by side
 
   float2* ml;      // [B][H][S]: split max and sum
   int B, Hi, H, max_pages, page_size, page_shift, num_pages, stride, keep;
@@ -1012,12 +1012,12 @@ __device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int 
   const int hg = j % a.HG, s = j / a.HG;
   if (s >= a.S) return;  // workgroup-uniform
   const int H = a.H;
-  // head HPW hg + i's split output at part + i * S * 512, its (max, sum) at mlp[i * S]
-  uint16_t* part = a.part + (((size_t)b * H + HPW * hg) * a.S + s) * FU_DV;
+  // head HPW hg + i's split output at part + i * 512, its (max, sum) at mlp[i * S]
+  uint16_t* part = a.part + (((size_t)b * a.S + s) * H + HPW * hg) * FU_DV;
   float2* mlp = a.ml + ((size_t)b * H + HPW * hg) * a.S + s;
   if (n_slots == 0) {  // an empty split: weight 0 in the combine
     for (int i = tid; i < HPW * FU_DV / 8; i += FU_THREADS)
-      reinterpret_cast<uint4*>(part + (size_t)(i / (FU_DV / 8)) * a.S * FU_DV)[i % (FU_DV / 8)] = uint4{0u, 0u, 0u, 0u};
+      reinterpret_cast<uint4*>(part + (size_t)(i / (FU_DV / 8)) * FU_DV)[i % (FU_DV / 8)] = uint4{0u, 0u, 0u, 0u};
     if (tid < HPW) mlp[tid * a.S] = make_float2(-INFINITY, 0.0f);
     return;
   }
@@ -1184,9 +1184,9 @@ __device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int 
       for (int i = 0; i < 4; ++i) v[i] = o[h][n][i] * inv[i];
       const float u0 = lane_xor1(odd ? v[0] : v[2]), u1 = lane_xor1(odd ? v[1] : v[3]);
       const int hl = 16 * h + 4 * q4 + (odd ? 2 : 0);
-      uint16_t* ph = part + (size_t)hl * a.S * FU_DV + 64 * wave + 16 * n + (l16 & ~1);
+      uint16_t* ph = part + (size_t)hl * FU_DV + 64 * wave + 16 * n + (l16 & ~1);
       *reinterpret_cast<uint32_t*>(ph) = odd ? bf16_pack(u0, v[2]) : bf16_pack(v[0], u0);
-      *reinterpret_cast<uint32_t*>(ph + (size_t)a.S * FU_DV) = odd ? bf16_pack(u1, v[3]) : bf16_pack(v[1], u1);
+      *reinterpret_cast<uint32_t*>(ph + (size_t)FU_DV) = odd ? bf16_pack(u1, v[3]) : bf16_pack(v[1], u1);
     }
   }
 }
@@ -1205,12 +1205,13 @@ __device__ __forceinline__ void fu_combine_heads(const FusedArgs& a, float* wts,
   if (tid < WAVE) mlv = ld_sc1_64(a.ml + ((size_t)b * H + hh) * S + min(sp, S - 1));
   // the two heads' split outputs through a buffer descriptor: split k's offset is scalar, the lane's is 32-bit
   const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(a.part + ((size_t)b * H + h0) * S * FU_DV), (short)0, 2 * 2 * S * FU_DV, FU_BUF_WORD3);
-  const int voff = 2 * ((tid >> 8) * S * FU_DV + d);
+      (void*)(a.part + (size_t)b * S * H * FU_DV + (size_t)h0 * FU_DV), (short)0,
+      2 * ((S - 1) * H * FU_DV + 2 * FU_DV), FU_BUF_WORD3);
+  const int voff = 2 * ((tid >> 8) * FU_DV + d);
   uint32_t ov[NS];
 #pragma unroll
   for (int k = 0; k < NS; ++k)
-    ov[k] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(prs, voff, 2 * FU_DV * min(k, S - 1), FU_AUX_PLAIN);
+    ov[k] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(prs, voff, 2 * H * FU_DV * min(k, S - 1), FU_AUX_PLAIN);
   if (tid < WAVE) {
     const float m = __uint_as_float((uint32_t)mlv), l = __uint_as_float((uint32_t)(mlv >> 32));
     const bool live = sp < S && l > 0.0f;
