@@ -34,6 +34,18 @@ def _check(inp, stride=None, cand=None, tol=TOL):
     return got, ref
 
 
+@pytest.mark.parametrize("Hi", [16, 64])
+def test_long_rows_ragged_batch(Hi):
+    """Rows past 32,768 scores (the long-row streaming form): a ragged batch of empty, one-token, tile-edge and long
+    rows, so that waves' tile ranges start and end inside and past contexts; every position against the oracle,
+    NEG_INF past every context."""
+    lengths = [70016, 0, 1, 31, 32, 33, 65, 5000, 32768, 32769, 1, 1, 1, 2, 3, 64, 12345, 70000, 69999, 100, 7,
+               1024, 2048, 0]
+    say(f"indexer long rows, ragged batch, Hi={Hi}")
+    cfg = W.Config("long-ragged", B=len(lengths), L=70016, H=16, Hi=Hi)
+    _check(W.make_inputs(cfg, seed=40 + Hi, lengths=lengths))
+
+
 def test_config1():
     say("indexer config 1")
     _check(W.make_inputs(W.CONFIGS[1], seed=0))

@@ -86,6 +86,25 @@ def test_layer_other_page_sizes(ps, L):
     _attention_check(inp, layer)
 
 
+def test_layer_long_ragged_many_short_rows():
+    """A batch with one row past 32,768 tokens (the separate kernels with the long-row indexer and selection) and many
+    short rows, empty tiles and short histograms beside a long one; every stage against the oracle."""
+    lengths = [40000, 1, 2, 3, 500, 2047, 2048, 2049, 33, 7, 9000, 1, 64, 4095, 100, 31]
+    say(f"layer long ragged batch of {len(lengths)} rows")
+    cfg = W.Config("layer-long-ragged", B=len(lengths), L=40000, H=64, Hi=64)
+    inp = W.make_inputs(cfg, seed=17, lengths=lengths)
+    g = inp.to("cuda")
+    L = _layer(g)
+    sc = L.scores.cpu()
+    ref = O.indexer_ref(inp.q_idx, inp.w_k, inp.k_cache, inp.k_scale, inp.table, inp.ctx_len, cfg.page_size,
+                        sc.shape[1])
+    assert row_rel_err(sc, ref, ref > -1e29) <= 1e-2
+    assert torch.all(sc[ref <= -1e29] < -1e29)
+    ri, rc = O.topk_ref(sc, cfg.keep, inp.ctx_len)
+    assert torch.equal(L.idx.cpu().long(), ri) and torch.equal(L.cnt.cpu().long(), rc)
+    _attention_check(inp, L)
+
+
 def _sampled_indexer_check(g, sc, nsample=4096, seed=0):
     cfg = g.cfg
     gen = torch.Generator().manual_seed(seed)
