@@ -277,9 +277,10 @@ __device__ __forceinline__ uint32_t fu_block_prefix(uint32_t mine, int* scr, uin
   return before;
 }
 
-// The workgroup's 1024 scores from LDS into the score output (positions 1024 j + e; none past the row's stride). They
-// are written after barrier A, behind the selection's first loads, so that their write latency overlaps the selection
-// instead of holding up the indexer's end (a wait for the memory counter there would wait for them).
+// The workgroup's 1024 scores from LDS into the score output (positions 1024 j + e; none past the row's stride), for a
+// row that selects from the key lists: written after barrier A, behind the selection's first loads, so that their
+// write latency overlaps the selection instead of holding up the indexer's end (its bin search waits for the memory
+// counter). The two-exchange form writes each tile's scores as it is scored, as those stores drain during the tiles.
 __device__ __forceinline__ void fu_store_scores(const FusedArgs& a, const uint8_t* lds, int b, int j) {
   const float* sc = reinterpret_cast<const float*>(lds + L_SCS);
   float* srow = a.scores + (size_t)b * a.stride;
@@ -314,6 +315,8 @@ __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int
   const int jk = lane & 31, h = lane >> 5;
   const int Hi = a.Hi;
   float* srow = a.scores + (size_t)b * a.stride;
+  // a row that selects from the key lists writes its scores after barrier A; the others as each tile is scored
+  const bool lists = fu_lists_on(a, L);
 
   // the queries' loads (32 MT heads of 16 pieces: MT per thread), the weights, the tiles' pages
   u32x4 qv[MT];
@@ -405,14 +408,16 @@ __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int
       part += __shfl_xor(part, 32, WAVE);
       const float v = pos < L ? part * ksc[i] : NEG_INF;
       if (h == 0) {
+        if (!lists && pos < a.stride) srow[pos] = v;
         scs[pos - j * FU_KEYS] = v;
         if (v > VISIBLE) atomicAdd(&hs[order_key(v) >> 20], 1);
       }
     }
   } else {
-    // every key of this wave is past the row: NEG_INF (into the score output after barrier A, with the others)
+    // every key of this wave is past the row: NEG_INF
     for (int e = lane; e < FU_TPW * FU_TILE; e += WAVE) {
       const int pos = t_begin * FU_TILE + e;
+      if (!lists && pos < a.stride) srow[pos] = NEG_INF;
       scs[pos - j * FU_KEYS] = NEG_INF;
     }
   }
@@ -426,7 +431,6 @@ __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int
   int hv[8];
   *reinterpret_cast<int4*>(hv) = *reinterpret_cast<const int4*>(hs + 8 * tid);
   *reinterpret_cast<int4*>(hv + 4) = *reinterpret_cast<const int4*>(hs + 8 * tid + 4);
-  const bool lists = fu_lists_on(a, L);
   int lbin = FU_HBINS, lcnt = 0;  // no list
   if (lists) {
     int lb, labove;
@@ -439,8 +443,8 @@ __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int
       lcnt = nb <= FU_LCAP ? nb : labove;
     }
   }
-  uint32_t key[2];
-  fu_my_keys(lds, key);
+  uint32_t key[2] = {0u, 0u};
+  if (lists) fu_my_keys(lds, key);
   const bool in0 = key[0] != 0u && (int)(key[0] >> 20) >= lbin, in1 = key[1] != 0u && (int)(key[1] >> 20) >= lbin;
   uint32_t nz = 0;
 #pragma unroll
@@ -1277,10 +1281,12 @@ __global__ __launch_bounds__(FU_THREADS, 1) void decode_fused_kernel(FusedArgs a
   float live_bias;
   int n_slots, nbar = 2;
   const bool lists = fu_lists_on(a, L);
-  if (!(lists && fu_select_lists<HPW>(a, lds, b, j, L, qv, &live_bias, &n_slots))) {
-    __syncthreads();  // every thread has read the bin search's results before stage 2 reuses its words
-    if (!lists) fu_store_scores(a, lds, b, j);
-    if (j == 0 && threadIdx.x == 0) __hip_atomic_fetch_add(sync + 3, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  bool one = false;
+  if (lists) {
+    one = fu_select_lists<HPW>(a, lds, b, j, L, qv, &live_bias, &n_slots);
+    if (!one) __syncthreads();  // every thread has read the bin search's results before stage 2 reuses its words
+  }
+  if (!one) {
     fu_classify(a, lds, b, j);
     fu_barrier(sync, 2);  // B: every workgroup's counts and candidates
     n_slots = fu_select<HPW>(a, lds, b, j, L, qv, &live_bias);
@@ -1289,6 +1295,9 @@ __global__ __launch_bounds__(FU_THREADS, 1) void decode_fused_kernel(FusedArgs a
   fu_attend<HPW>(a, lds, b, j, n_slots, live_bias);
   fu_barrier(sync, nbar);  // C: every split's output
   fu_combine(a, lds, b, j);
+  // the count of rows that took the two-exchange selection (here, where no later wait is held up by its round trip)
+  if (nbar == 3 && j == 0 && threadIdx.x == 0)
+    __hip_atomic_fetch_add(sync + 3, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   fu_exit(sync);
 }
 
