@@ -105,6 +105,46 @@ def test_layer_long_ragged_many_short_rows():
     _attention_check(inp, L)
 
 
+@pytest.mark.parametrize("tied", [False, True])
+def test_layer_long_rows_mixed_forms(tied):
+    """Rows past 32,768 tokens in a small batch (the long-row indexer and the chunked long-row selection) beside rows
+    of at most keep keys (every visible key selected), a row whose selection crowds into its first 4,096 positions
+    (key scales raised a thousandfold there) and, with `tied`, rows whose scores take two values (the keep-th largest
+    tied with thousands of keys). Every stage against the oracle, then a second step on the same workspace."""
+    lengths = [100000, 40000, 1500, 33000, 2048, 70000]
+    say(f"layer long rows, mixed forms, tied={tied}")
+    cfg = W.Config("layer-long-mixed", B=len(lengths), L=100000, H=64, Hi=64)
+    inp = W.make_inputs(cfg, seed=23 + tied, lengths=lengths)
+    ps = cfg.page_size
+    pos = torch.arange(4096)
+    slots = inp.table[5, pos // ps].long() * ps + pos % ps
+    inp.k_scale[slots] *= 1000.0
+    if tied:  # rows 1 and 3: two key patterns, so two score values a row
+        for b in (1, 3):
+            n = inp.lengths[b]
+            p = torch.arange(n)
+            sl = inp.table[b, p // ps].long() * ps + p % ps
+            inp.k_cache[sl] = inp.k_cache[64 + (p % 2)]
+            inp.k_scale[sl] = inp.k_scale[64 + (p % 2)]
+    g = inp.to("cuda")
+    L = _layer(g)
+    sc = L.scores.cpu()
+    ref = O.indexer_ref(inp.q_idx, inp.w_k, inp.k_cache, inp.k_scale, inp.table, inp.ctx_len, cfg.page_size,
+                        sc.shape[1])
+    assert row_rel_err(sc, ref, ref > -1e29) <= 1e-2
+    if tied:
+        for b in (1, 3):
+            assert len(torch.unique(sc[b, :inp.lengths[b]])) <= 2
+    ri, rc = O.topk_ref(sc, cfg.keep, inp.ctx_len)
+    assert torch.equal(L.cnt.cpu().long(), rc)
+    assert torch.equal(L.idx.cpu().long(), ri)
+    _attention_check(inp, L)
+    # a second step on the same workspace (the histograms cleared by the first)
+    L.step(g.q_idx, g.w_k, g.k_cache, g.k_scale, g.q, g.kv_cache, g.kv_scale, g.table, g.ctx_len)
+    torch.cuda.synchronize()
+    assert torch.equal(L.idx.cpu().long(), ri) and torch.equal(L.cnt.cpu().long(), rc)
+
+
 def _sampled_indexer_check(g, sc, nsample=4096, seed=0):
     cfg = g.cfg
     gen = torch.Generator().manual_seed(seed)
