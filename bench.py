@@ -197,6 +197,36 @@ def step_times(step, steps: int) -> list:
     return [a.elapsed_time(b) * 1e3 for a, b in evs]
 
 
+def graph_step_us(step, steps: int, per_graph: int = 8) -> float:
+    """The same step replayed from a HIP graph (torch.cuda.CUDAGraph) that captures `per_graph` steps: us per step
+    over `steps` steps of replays, between a pair of events. The step allocates nothing and issues no memset, so its
+    capture replays the eager launches (tests/test_gpu_graph.py checks replays against eager steps)."""
+    import torch
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(per_graph):
+            step()
+    torch.cuda.synchronize()
+    reps = max(1, steps // per_graph)
+    g.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        g.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e3 / (reps * per_graph)
+
+
 def percentiles(v) -> dict:
     """median, p10 and p90 (nearest rank) of a list of durations."""
     v = sorted(v)
@@ -631,6 +661,7 @@ def main() -> int:
     # time (a pair of events around it) over another `steps`, for the median / p10 / p90
     k_us = kernel_times(lib, step, args.steps)
     spans = step_times(step, args.steps)
+    g_us = graph_step_us(step, args.steps)
 
     lengths = inp.lengths
     layer_bytes = W.algorithmic_bytes(lengths, cfg.H, cfg.Hi, cfg.keep, cfg.page_size)
@@ -671,7 +702,7 @@ def main() -> int:
         "layer": {"algorithmic_bytes": layer_bytes, "achieved_GBs": round(layer_gbs, 1),
                   "frac": round(layer_gbs / HBM_PEAK_GBS, 4),
                   "kernel_us": {k: round(v, 3) for k, v in k_us.items()},
-                  "step_us": percentiles(spans)},
+                  "step_us": percentiles(spans), "graph_step_us": round(g_us, 3)},
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(inp)
