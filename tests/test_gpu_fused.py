@@ -43,11 +43,16 @@ def _workspace_clean(L):
     assert torch.all(sync[:, 2] == 0), "a barrier wait gave up (error flag set)"
 
 
-def _two_exchange_rows(L) -> int:
-    """Rows that took the two-exchange selection (stages 2 and 3) since the workspace was made: the kernel counts them
-    per XCD in the barrier words; the others took the one-exchange selection from the key lists."""
+def _two_exchange_per_xcd(L) -> list:
+    """Per XCD, the rows that took the two-exchange selection (stages 2 and 3) since the workspace was made: the kernel
+    counts them in the XCD's barrier words (row b of a launch runs on XCD b % 8); the others took the one-exchange
+    selection from the key lists."""
     ws = L.workspace.view(torch.int32).cpu()
-    return int(ws[L.B * 4096:L.B * 4096 + 8 * 16].view(8, 16)[:, 3].sum())
+    return ws[L.B * 4096:L.B * 4096 + 8 * 16].view(8, 16)[:, 3].tolist()
+
+
+def _two_exchange_rows(L) -> int:
+    return sum(_two_exchange_per_xcd(L))
 
 
 def _check_full(inp, L, indexer=True):
@@ -77,8 +82,9 @@ def test_fused_layer_configs(c):
     assert names == ["decode_fused_kernel"], names
     _check_full(inp, L)
     _workspace_clean(L)
-    # config 2's rows of 32,768 tokens select from the key lists; config 1's row of 4,096 cannot (keep 2048 of it)
-    assert _two_exchange_rows(L) == (0 if c == 2 else 2)
+    # config 2's rows of 32,768 tokens select from the key lists, and so does config 1's row of 4,096 (blocks of 128
+    # positions: every list holds all its workgroup's keys), in both steps
+    assert _two_exchange_rows(L) == 0
 
 
 def test_fused_layer_ragged_two_launches():
@@ -110,8 +116,8 @@ def test_fused_layer_head_counts(H, Hi):
 def _tied_inputs(values: int):
     """A batch whose key rows take `values` patterns (row t of the cache: pattern t % values), so the scores of a row
     take at most that many values and the keep-th is tied with many others."""
-    cfg = W.Config(f"fused-ties{values}", B=3, L=32768, H=64, Hi=64)
-    inp = W.make_inputs(cfg, seed=6 + values, lengths=[32768, 20000, 2500])
+    cfg = W.Config(f"fused-ties{values}", B=4, L=32768, H=64, Hi=64)
+    inp = W.make_inputs(cfg, seed=6 + values, lengths=[32768, 20000, 2500, 7000])
     base_k, base_s = inp.k_cache[64:64 + values].clone(), inp.k_scale[64:64 + values].clone()
     n = inp.k_cache.shape[0]
     rep = (n + values - 1) // values
@@ -122,10 +128,14 @@ def _tied_inputs(values: int):
 
 @pytest.mark.parametrize("values", [1, 2, 100])
 def test_fused_layer_ties(values):
-    """One or two score values: every workgroup's keys fill one bin, its key list stays empty and the full row takes
-    the two-exchange selection. A hundred values: the full row selects from the key lists, with the keep-th largest
-    tied with keys that are not taken (the lowest positions of the tie are). The shorter rows take the two-exchange
-    form."""
+    """Rows of 32,768, 20,000, 2,500 and 7,000 tokens (blocks of 1024, 640, 96 and 224 positions; the last end inside
+    pages). One score value: on the rows whose blocks hold more positions than a key list, every workgroup's keys fill
+    one bin, its key list stays empty and the row takes the two-exchange selection. Two values: the same for the rows
+    of 32,768 and 20,000 (a workgroup's larger value alone overfills a list); at 7,000 each list holds its block's
+    keys of the larger value, which hold the whole selection, so the row selects from the lists, ties at T by
+    position. The row of 2,500 (every list holds all its keys) always selects from the lists. A hundred values: the
+    full row selects from the key lists, with the keep-th largest tied with keys that are not taken (the lowest
+    positions of the tie are)."""
     say(f"fused layer ties values={values}")
     inp = _tied_inputs(values)
     L = _run(inp.to("cuda"))
@@ -134,7 +144,13 @@ def test_fused_layer_ties(values):
         assert len(torch.unique(sc[b, :n])) <= values
     _check_full(inp, L, indexer=False)
     _workspace_clean(L)
-    assert _two_exchange_rows(L) == (3 if values < 100 else 2)
+    per_row = _two_exchange_per_xcd(L)[:4]
+    if values == 1:
+        assert per_row == [1, 1, 0, 1], per_row
+    elif values == 2:
+        assert per_row == [1, 1, 0, 0], per_row
+    else:
+        assert per_row[0] == 0 and per_row[2] == 0, per_row
     if values == 100:
         keep = inp.cfg.keep
         t = sc[0][L.idx[0].cpu().long()].min()

@@ -10,11 +10,13 @@
 // waiter polls with sc1 loads, every wait bounded: past its limit the workgroup records an error flag and goes on, so
 // no wave can hang).
 //
-// Per row, workgroup j (of 32):
-//   1. indexer: scores of positions 1024 j .. 1024 j + 1023 (8 waves x 4 tiles of 32 keys, bf16 MFMA over the
-//      exactly converted e4m3 keys, the weighted relu head sum in registers; the arithmetic of
+// Per row of L tokens, workgroup j (of 32) owns positions kw j .. kw j + kw - 1, kw = 32 ceil(L / 1024) (1024 at
+// most): the row's positions in 32 blocks of whole 32-key tiles, so every workgroup of a short row takes a share of
+// its keys, and position order is workgroup order.
+//   1. indexer: scores of the workgroup's positions (8 waves x up to 4 tiles of 32 keys, bf16 MFMA over the exactly
+//      converted e4m3 keys, the weighted relu head sum in registers; the arithmetic of
 //      trnrt/kernels/dsa_index.py:44-50), written to the scores output and kept in LDS, with an LDS histogram of the
-//      top 12 bits of their order keys written as a list of its nonzero bins and, on rows long enough, a list of the
+//      top 12 bits of their order keys written as a list of its nonzero bins and, on most rows, a list of the
 //      workgroup's largest keys (whole bins, at most 192, in position order); barrier A;
 //   2+3 in one exchange (when every key at or above the row's keep-th largest is in the key lists, which the lists
 //      themselves show): every workgroup reads the 32 key lists and finds T, the ties to take and each workgroup's
@@ -45,7 +47,7 @@ constexpr int FU_WAVES = FU_THREADS / WAVE;
 constexpr int FU_TILE = 32;                           // keys per MFMA tile
 constexpr int FU_TPW = 4;                             // tiles per wave
 constexpr int FU_AHEAD = 2;                           // key tiles in flight ahead of the one a wave computes
-constexpr int FU_KEYS = FU_WAVES * FU_TPW * FU_TILE;  // 1024 keys per workgroup
+constexpr int FU_KEYS = FU_WAVES * FU_TPW * FU_TILE;  // 1024: positions per workgroup at most (fu_kw)
 constexpr int FU_MAXLEN = FU_NW * FU_KEYS;            // 32,768
 constexpr int FU_D = 128;                             // indexer head dim
 constexpr int FU_QROW = FU_D + 8;                     // staged indexer query row (bf16)
@@ -65,9 +67,10 @@ static_assert(FU_CROW >= 1 + FU_BMW + FU_KEYS && FU_CROW % 4 == 0, "candidate bl
 // of them when they number at most FU_LCAP; the bins above that one when it would hold more), in position order:
 // a 128-byte header (count, lowest bin listed (0: every visible key), 0, 0, then the workgroup's FU_LBINS highest
 // nonzero histogram bins as (bin << 16) | count in descending bin order, 0 past its nonzero bins), then (key,
-// position in the workgroup's range) pairs. Read back by 16 threads of FU_LPT entries each. Rows whose workgroups select FU_LM * 5 / 8 keys or fewer on average
-// (rows of at least 26,215 tokens at keep 2048) take the one-exchange selection from the lists; the others, and any
-// row whose lists turn out not to hold its selection, the two-exchange form (stages 2 and 3).
+// position in the workgroup's block) pairs. Read back by 16 threads of FU_LPT entries each. Rows whose blocks hold at
+// most FU_LCAP positions (every list holds all its keys), or whose workgroups select FU_LM * 5 / 8 keys or fewer on
+// average (at keep 2048: every row length), take the one-exchange selection from the lists; the others, and any row
+// whose lists turn out not to hold its selection, the two-exchange form (stages 2 and 3).
 constexpr int FU_LM = 128;
 constexpr int FU_LPT = 12;
 constexpr int FU_LCAP = 16 * FU_LPT;
@@ -103,11 +106,10 @@ constexpr int L_BINS = 40960;    // stage 3: 4096 bins
 constexpr int L_QS = 32768;      // stage 1: indexer queries [64][136] bf16
 constexpr int L_WS = 50176;      // stage 1: head weights [64]
 constexpr int L_HS = 50432;      // stage 1: histogram [4096]
-constexpr int L_TPG = 159616;    // stages 1-3: the page of each of the workgroup's 32 tiles
-constexpr int L_SCS = 159744;    // stages 1-3: the workgroup's 1024 scores
+constexpr int L_SCS = 159744;    // stages 1-3: the scores of the workgroup's 1024 positions (NEG_INF past its block)
 constexpr int L_KT = 0;          // stage 4: the rows, token-major at the 592-byte stride
 constexpr int FU_LDS = 163840;
-static_assert(L_HS + 4 * FU_HBINS <= L_TPG && L_TPG + 4 * 32 == L_SCS, "stage 1 layout");
+static_assert(L_HS + 4 * FU_HBINS <= L_SCS, "stage 1 layout");
 static_assert(L_HLS + 4 * FU_NW * FU_HSTAGE <= L_HS, "stage 2 layout");
 static_assert(L_BINS2 + 4 * 256 <= L_SPG && L_BINS + 4 * 4096 <= 57344, "stage 3 layout");
 static_assert(L_SPG + 4 * 1024 <= L_CB && L_CB + 4 * FU_NW * FU_CSTAGE <= L_SB && L_SB + 4 * FU_NW * FU_BMW <= L_PB &&
@@ -136,7 +138,7 @@ struct FuAtt {
 };
 static_assert(FuAtt<16>::TG * FuAtt<16>::HB == FU_WAVES && FuAtt<32>::TG * FuAtt<32>::HB == FU_WAVES, "waves");
 static_assert(FuAtt<16>::L_END <= FU_LDS && FuAtt<16>::L_QST + 2 * 16 * FU_AQROW <= FuAtt<16>::L_P, "stage 4, 16");
-static_assert(FuAtt<32>::L_QST + 2 * 32 * FU_AQROW <= L_TPG && FuAtt<32>::L_P >= 57344, "stage 4, 32");
+static_assert(FuAtt<32>::L_QST + 2 * 32 * FU_AQROW <= L_SCS && FuAtt<32>::L_P >= 57344, "stage 4, 32");
 
 struct FuState {
   int gt[FU_NW];  // per workgroup: its candidates above T
@@ -277,24 +279,32 @@ __device__ __forceinline__ uint32_t fu_block_prefix(uint32_t mine, int* scr, uin
   return before;
 }
 
-// The workgroup's 1024 scores from LDS into the score output (positions 1024 j + e; none past the row's stride), for a
+// Positions per workgroup in a row of L tokens: 32 ceil(L / 1024), at least one tile, at most 1024.
+__device__ __forceinline__ int fu_kw(int L) {
+  return min(FU_KEYS, max(FU_TILE, (L + FU_NW * FU_TILE - 1) / (FU_NW * FU_TILE) * FU_TILE));
+}
+
+// The workgroup's kw scores from LDS into the score output (positions kw j + e; none past the row's stride), for a
 // row that selects from the key lists: written after barrier A, behind the selection's first loads, so that their
 // write latency overlaps the selection instead of holding up the indexer's end (its bin search waits for the memory
 // counter). The two-exchange form writes each tile's scores as it is scored, as those stores drain during the tiles.
-__device__ __forceinline__ void fu_store_scores(const FusedArgs& a, const uint8_t* lds, int b, int j) {
+__device__ __forceinline__ void fu_store_scores(const FusedArgs& a, const uint8_t* lds, int b, int j, int kw) {
   const float* sc = reinterpret_cast<const float*>(lds + L_SCS);
   float* srow = a.scores + (size_t)b * a.stride;
 #pragma unroll
   for (int e = threadIdx.x; e < FU_KEYS; e += FU_THREADS)
-    if (j * FU_KEYS + e < a.stride) srow[j * FU_KEYS + e] = sc[e];
+    if (e < kw && j * kw + e < a.stride) srow[j * kw + e] = sc[e];
 }
 
-// Whether a row of L tokens takes the one-exchange selection from the key lists (workgroup-uniform).
+// Whether a row of L tokens takes the one-exchange selection from the key lists (workgroup-uniform): every list holds
+// all its workgroup's keys (kw <= FU_LCAP), or the workgroups select at most 80 keys each on average.
 __device__ __forceinline__ bool fu_lists_on(const FusedArgs& a, int L) {
-  return (long)a.keep * FU_KEYS * 8 <= 5L * FU_LM * L;
+  const int kw = fu_kw(L);
+  return kw <= FU_LCAP || (long)a.keep * kw * 8 <= 5L * FU_LM * L;
 }
 
-// This thread's two keys (positions tid, tid + 512 of the workgroup's range; 0: not selectable).
+// This thread's two keys (positions tid, tid + 512 of the workgroup's block; 0: not selectable, as every position past
+// the block's kw is).
 __device__ __forceinline__ void fu_my_keys(const uint8_t* lds, uint32_t (&key)[2]) {
   const float* sc = reinterpret_cast<const float*>(lds + L_SCS);
   const float v0 = sc[threadIdx.x], v1 = sc[threadIdx.x + FU_THREADS];
@@ -302,14 +312,15 @@ __device__ __forceinline__ void fu_my_keys(const uint8_t* lds, uint32_t (&key)[2
   key[1] = order_key(v1) & (0u - (uint32_t)(v1 > VISIBLE));
 }
 
-// Stage 1: the indexer scores of positions 1024 j .. 1024 j + 1023 of row b (L: the row's length). Each wave streams
-// its 4 tiles of 32 keys FU_AHEAD ahead of its MFMAs.
+// Stage 1: the indexer scores of positions kw j .. kw j + kw - 1 of row b (L: the row's length, kw = fu_kw(L)): the
+// block's tiles (32 keys each) go to the waves in turn, wave v taking tiles v, v + 8, v + 16, v + 24 of the block (the
+// ones the block has) and streaming them FU_AHEAD ahead of its MFMAs. LDS holds the scores of all 1024 positions of
+// the workgroup's range, NEG_INF past the block.
 template <int MT>
 __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int b, int j, int L) {
   uint16_t* qs = reinterpret_cast<uint16_t*>(lds + L_QS);
   float* wsh = reinterpret_cast<float*>(lds + L_WS);
   int* hs = reinterpret_cast<int*>(lds + L_HS);
-  int* tpg = reinterpret_cast<int*>(lds + L_TPG);
   float* scs = reinterpret_cast<float*>(lds + L_SCS);
   const int tid = threadIdx.x, wave = tid / WAVE, lane = tid & (WAVE - 1);
   const int jk = lane & 31, h = lane >> 5;
@@ -327,21 +338,28 @@ __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int
     qv[r] = *reinterpret_cast<const u32x4*>(a.q_idx + ((size_t)b * Hi + min(head, Hi - 1)) * FU_D + 8 * c);
   }
   const float wv = a.w[(size_t)b * Hi + min(tid, Hi - 1)];
-  const int t_begin = j * (FU_KEYS / FU_TILE) + wave * FU_TPW;  // this wave's first tile
-  const bool live = t_begin * FU_TILE < L;                      // wave-uniform: any of its keys in the row
+  const int kw = fu_kw(L), nt = kw / FU_TILE;  // the block's positions and tiles
+  // tile i of this wave: the block's tile wave + 8 i, the row's tile t_begin + 8 i; it holds keys of the row when
+  // wave + 8 i < nt and its first position is below L
+  const int t_begin = j * nt + wave;
+  const bool live = wave < nt && t_begin * FU_TILE < L;  // wave-uniform: any of its keys in the row
+  auto in_row = [&](int i) __attribute__((always_inline)) {
+    return wave + FU_WAVES * i < nt && (t_begin + FU_WAVES * i) * FU_TILE < L;
+  };
   const int* trow = a.table + (size_t)b * a.max_pages;
   int pages = 0;
   {
-    const int t = t_begin + min(lane, FU_TPW - 1);
+    const int i = min(lane, FU_TPW - 1);
+    const int t = t_begin + FU_WAVES * i;
     const int pg = trow[min((t * FU_TILE) >> a.page_shift, a.max_pages - 1)];
-    pages = t * FU_TILE < L ? safe_page(pg, a.num_pages) : 0;
+    pages = in_row(i) ? safe_page(pg, a.num_pages) : 0;
   }
   u32x4 kv[FU_TPW][4];
   float ksc[FU_TPW];
   auto tile_loads = [&](int i) __attribute__((always_inline)) {
-    const int t0 = (t_begin + i) * FU_TILE;
+    const int t0 = (t_begin + FU_WAVES * i) * FU_TILE;
     const int page = __builtin_amdgcn_readlane(pages, i);
-    const size_t slot = t0 < L ? (size_t)page * a.page_size + (t0 & (a.page_size - 1)) + jk : (size_t)jk;
+    const size_t slot = in_row(i) ? (size_t)page * a.page_size + (t0 & (a.page_size - 1)) + jk : (size_t)jk;
     const uint8_t* kp = a.k + slot * FU_D + 64 * h;
 #pragma unroll
     for (int c = 0; c < 4; ++c) kv[i][c] = *reinterpret_cast<const u32x4*>(kp + 16 * c);
@@ -359,7 +377,6 @@ __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int
     *reinterpret_cast<u32x4*>(&qs[head * FU_QROW + 8 * c]) = head < Hi ? qv[r] : u32x4{0u, 0u, 0u, 0u};
   }
   if (tid < 32 * MT) wsh[tid] = tid < Hi ? wv : 0.0f;
-  if (lane < FU_TPW) tpg[wave * FU_TPW + lane] = pages;
   for (int i = tid; i < FU_HBINS; i += FU_THREADS) hs[i] = 0;
   int* scr = reinterpret_cast<int*>(lds + L_MISC);
   if (tid == 0) scr[8] = -1;  // the key list's bin search below
@@ -387,7 +404,8 @@ __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int
         tile_loads(i + FU_AHEAD);
         __builtin_amdgcn_sched_barrier(0);
       }
-      const int pos = (t_begin + i) * FU_TILE + jk;
+      const int pos = (t_begin + FU_WAVES * i) * FU_TILE + jk, e = (wave + FU_WAVES * i) * FU_TILE + jk;
+      const bool mine = wave + FU_WAVES * i < nt;  // a position of this workgroup's block
       f32x16 acc[MT];
 #pragma unroll
       for (int m = 0; m < MT; ++m)
@@ -406,23 +424,24 @@ __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int
 #pragma unroll
         for (int r = 0; r < 16; ++r) part = fmaf(wr[m][r], relu(acc[m][r]), part);
       part += __shfl_xor(part, 32, WAVE);
-      const float v = pos < L ? part * ksc[i] : NEG_INF;
+      const float v = mine && pos < L ? part * ksc[i] : NEG_INF;
       if (h == 0) {
-        if (!lists && pos < a.stride) srow[pos] = v;
-        scs[pos - j * FU_KEYS] = v;
+        if (!lists && mine && pos < a.stride) srow[pos] = v;
+        scs[e] = v;
         if (v > VISIBLE) atomicAdd(&hs[order_key(v) >> 20], 1);
       }
     }
   } else {
-    // every key of this wave is past the row: NEG_INF
-    for (int e = lane; e < FU_TPW * FU_TILE; e += WAVE) {
-      const int pos = t_begin * FU_TILE + e;
-      if (!lists && pos < a.stride) srow[pos] = NEG_INF;
-      scs[pos - j * FU_KEYS] = NEG_INF;
+    // every key of this wave is past the row or the block: NEG_INF
+    for (int x = lane; x < FU_TPW * FU_TILE; x += WAVE) {
+      const int lt = wave + FU_WAVES * (x / FU_TILE);  // the tile of the block
+      const int pos = (j * nt + lt) * FU_TILE + (x & (FU_TILE - 1));
+      if (!lists && lt < nt && pos < a.stride) srow[pos] = NEG_INF;
+      scs[lt * FU_TILE + (x & (FU_TILE - 1))] = NEG_INF;
     }
   }
-  // positions past 32,768 of a wider score row are never keys of the row
-  for (int p = FU_MAXLEN + j * FU_THREADS + tid; p < a.stride; p += FU_NW * FU_THREADS) srow[p] = NEG_INF;
+  // positions past the 32 blocks (32 kw) of a wider score row are never keys of the row
+  for (int p = FU_NW * kw + j * FU_THREADS + tid; p < a.stride; p += FU_NW * FU_THREADS) srow[p] = NEG_INF;
   __syncthreads();
   // the histogram's nonzero bins into the workgroup's bin list (thread t: bins 8 t .. 8 t + 7), in bin order, and
   // the workgroup's key list: the bin of its FU_LM-th largest key, then its keys from that bin up (or from the next
@@ -556,13 +575,13 @@ __device__ __forceinline__ void fu_classify(const FusedArgs& a, uint8_t* lds, in
 }
 
 // The end of the selection, shared by its two forms: every workgroup's selected positions are in the bitmaps at L_SB
-// (lane w of every wave: workgroup w's selected count selw and first output index offw), the pages of the positions
-// from page pg0 on at L_SPG (this wave's loads of them may be in flight). The workgroup writes the indices of its
-// split's outputs [o0, o1), lists their cache slots at FuAtt<HPW>::L_P, stages the attention's queries and returns the
-// split's selected count.
+// (bit e of workgroup w's: position kw w + e; lane w of every wave: workgroup w's selected count selw and first output
+// index offw), the pages of the positions from page pg0 on at L_SPG (this wave's loads of them may be in flight). The
+// workgroup writes the indices of its split's outputs [o0, o1), lists their cache slots at FuAtt<HPW>::L_P, stages the
+// attention's queries and returns the split's selected count.
 template <int HPW>
-__device__ __forceinline__ int fu_split_slots(const FusedArgs& a, uint8_t* lds, int b, int j, int selw, int offw,
-                                              int o0, int o1, int cnt_row, int pg0,
+__device__ __forceinline__ int fu_split_slots(const FusedArgs& a, uint8_t* lds, int b, int j, int kw, int selw,
+                                              int offw, int o0, int o1, int cnt_row, int pg0,
                                               const u32x4 (&qv)[FuAtt<HPW>::QPT], float* live_bias) {
   using AT = FuAtt<HPW>;
   constexpr int QPT = AT::QPT;
@@ -605,8 +624,8 @@ __device__ __forceinline__ int fu_split_slots(const FusedArgs& a, uint8_t* lds, 
       const uint32_t word = sb[FU_BMW * sw + i];
       uint32_t bits = (word >> by) & 255u;
       int o = __shfl(offw, sw, WAVE) + pb[FU_BMW * sw + i] + __builtin_popcount(word & ((1u << by) - 1u));
-      // the word's 32 positions lie in one page (pages of at least 32 tokens)
-      const int p0 = FU_KEYS * sw + 32 * i;
+      // the word's 32 positions lie in one page (kw a multiple of 32, pages of at least 32 tokens)
+      const int p0 = kw * sw + 32 * i;
       const int sbase =
           safe_page(spg[(p0 >> a.page_shift) - pg0], a.num_pages) * a.page_size + (p0 & (a.page_size - 1)) + by;
       while (bits) {
@@ -661,6 +680,7 @@ __device__ __forceinline__ int fu_select(const FusedArgs& a, uint8_t* lds, int b
   const int hg = j % a.HG, s = j / a.HG;
   const bool active = s < a.S;  // workgroup-uniform: a workgroup past the last split only helps with the barriers
   const int o0 = active ? s * a.sps : 0, o1 = active ? min(o0 + a.sps, a.keep) : 0;
+  const int kw = fu_kw(L);
   const uint32_t* cblk = a.cand + (size_t)b * FU_NW * FU_CROW;
   // the staged words of every block straight into LDS (load i: blocks 2 i, 2 i + 1; lane l words 4 (l % 32) .. + 3
   // of block 2 i + l / 32)
@@ -702,11 +722,13 @@ __device__ __forceinline__ int fu_select(const FusedArgs& a, uint8_t* lds, int b
   const uint32_t cnw = cb[FU_CSTAGE * ww];
   const int nav = lane < FU_NW ? (int)(cnw >> 16) : 0, ncv = lane < FU_NW ? (int)(cnw & 0xFFFFu) : 0;
   const int lo = wave_incl_scan(nav) - nav, hi = wave_incl_scan(nav + ncv);
-  const uint64_t mc = __ballot(lane < FU_NW && lo < o1 && hi > o0 && FU_KEYS * lane < L);
+  const uint64_t mc = __ballot(lane < FU_NW && lo < o1 && hi > o0 && kw * lane < L);
   const int wa0 = mc ? (int)__builtin_ctzll(mc) : 0, nsrc0 = mc ? 64 - (int)__builtin_clzll(mc) - wa0 : 0;
-  const int pg0 = (FU_KEYS * wa0) >> a.page_shift;
+  const int pg0 = (kw * wa0) >> a.page_shift;
   {
-    const int npg = (FU_KEYS * nsrc0) >> a.page_shift;
+    // the pages from the first source block's first position to the last one's end (at most 1024: pages of at
+    // least 32 tokens over at most 32,768 positions)
+    const int npg = nsrc0 ? ((kw * (wa0 + nsrc0) + a.page_size - 1) >> a.page_shift) - pg0 : 0;
     const int* trow = a.table + (size_t)b * a.max_pages;
     for (int c = wave; WAVE * c < npg; c += FU_WAVES) {
       const int i = WAVE * c + lane;
@@ -794,7 +816,7 @@ __device__ __forceinline__ int fu_select(const FusedArgs& a, uint8_t* lds, int b
     }
   }
   __syncthreads();
-  return fu_split_slots<HPW>(a, lds, b, j, selw, offw, o0, o1, cnt_row, pg0, qv, live_bias);
+  return fu_split_slots<HPW>(a, lds, b, j, kw, selw, offw, o0, o1, cnt_row, pg0, qv, live_bias);
 }
 
 // Stages 2 and 3 in one exchange, from the key lists: every workgroup reads all 32 lists of the row (thread (w, q):
@@ -857,7 +879,8 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
 #pragma unroll
     for (int i = 0; i < QPT; ++i) qv[i] = qsrc[min(tid + FU_THREADS * i, HPW * FU_DQK / 8 - 1)];
   }
-  fu_store_scores(a, lds, b, j);
+  const int kw = fu_kw(L);
+  fu_store_scores(a, lds, b, j, kw);
   __builtin_amdgcn_sched_barrier(0);
   for (int i = tid; i < 4096; i += FU_THREADS) bins0[i] = bins1[i] = 0;
   if (tid < 256) bins2[tid] = 0;
@@ -981,7 +1004,7 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
   spg[tid] = pgv[0];
   spg[tid + FU_THREADS] = pgv[1];
   __syncthreads();
-  *n_slots = fu_split_slots<HPW>(a, lds, b, j, selw, offw, o0, o1, cnt_row, 0, qv, live_bias);
+  *n_slots = fu_split_slots<HPW>(a, lds, b, j, kw, selw, offw, o0, o1, cnt_row, 0, qv, live_bias);
   return true;
 }
 
