@@ -305,7 +305,9 @@ size_t dsa_sparse_mla_pooled_workspace_bytes(int B, int H, int keep, int kp, int
  *   [B, keep] (ascending, 0 past cnt), cnt int32 [B], out bf16 [B, H, 512], lse fp32 [B, H] (or null).
  *   workspace: dsa_pooled_workspace_bytes(B, H, keep, max_pages page_size / kp, kp, splits) bytes, zero-filled
  *   before first use (calls leave the regions that must start at zero at zero). kp a power of two in [2, 8] dividing
- *   page_size; Hi <= 64; H a multiple of 16; Dqk 512 or 576.
+ *   page_size; Hi <= 64; H a multiple of 16; Dqk 512 or 576. With splits 0, Dqk 512, H a multiple of 32 and
+ *   keep kp <= 4096 / (H / 32) (the token slots in 128-slot splits, 32 workgroups per row) on a GPU of 8 XCDs x 32
+ *   CUs, the attention and combine are one XCD-local launch; otherwise the split attention and the combine kernel.
  */
 int dsa_pooled_decode_layer(const void* q_idx_bf16, const float* w, const void* pool_key_bf16, const void* q_bf16,
                             const uint8_t* kv_fp8, const float* kv_scale, const int32_t* page_table,

@@ -65,6 +65,12 @@ hipError_t launch_decode_attend(const uint16_t* q, const uint8_t* kv, const floa
                                 const int* idx, const int* table, const int* cnt, uint16_t* out, float* lse, void* ws,
                                 int* sync, int B, int H, int max_pages, int page_size, int num_pages, int keep,
                                 float scale, hipStream_t s);
+bool attend_xcd_pooled_ok(int num_cu, int H, int Dqk, int keep_tokens);
+hipError_t launch_decode_attend_pooled(const uint16_t* q, const uint8_t* kv, const float* kvs, const int* pools,
+                                       const int* cnt, const int* npool, const int* positions, const int* table,
+                                       uint16_t* out, float* lse, void* ws, int* sync, int B, int H, int max_pages,
+                                       int page_size, int num_pages, int keep_pools, int kp_shift, float scale,
+                                       hipStream_t s);
 hipError_t launch_decode_fused(const uint16_t* q_idx, const float* w, const uint8_t* k, const float* ks,
                                const uint16_t* q, const uint8_t* kv, const float* kvs, const int* table,
                                const int* ctx_len, float* scores, int* idx, int* cnt, uint16_t* out, float* lse,
@@ -793,7 +799,11 @@ size_t dsa_pooled_workspace_bytes(int B, int H, int keep, int max_len, int kp, i
   if (B < 0 || H < 16 || keep < 1 || max_len < 1 || kp < 2) return 0;
   const int keep_sel = kp * keep;
   const int sp = effective_splits(resolve_splits(splits, B, H, keep_sel), keep_sel);
-  return align256(dsa::topk_workspace_bytes(B, max_len, keep)) + align256(dsa::attention_workspace_bytes(B, H, sp));
+  // the split attention's workspace, or the XCD-local attention launch's (split outputs and their (max, sum))
+  const size_t t = align256(dsa::topk_workspace_bytes(B, max_len, keep));
+  const size_t a = align256(dsa::attention_workspace_bytes(B, H, sp));
+  const size_t x = align256(dsa::attend_xcd_bytes(B, H, keep_sel));
+  return t + (a > x ? a : x);
 }
 
 int dsa_pooled_decode_layer(const void* q_idx_bf16, const float* w, const void* pool_key_bf16, const void* q_bf16,
@@ -832,6 +842,15 @@ int dsa_pooled_decode_layer(const void* q_idx_bf16, const float* w, const void* 
     return DSA_ELAUNCH;
   }
   const int keep_sel = kp * keep;  // the selected pools' token slots; the tail comes on top
+  // the default split count on a GPU of 8 XCDs x 32 CUs, 512-wide rows: the attention and combine in one XCD-local
+  // launch (the separate kernels' form of the one-launch layer's last stages), the tail in the split of the last
+  // selected token; the barrier words follow the histograms in the zero region
+  if (splits == 0 && dsa::attend_xcd_pooled_ok(num_cu(), H, Dqk, keep_sel))
+    return status(dsa::launch_decode_attend_pooled(
+        static_cast<const uint16_t*>(q_bf16), kv_fp8, kv_scale, pools, cnt, npool, positions, page_table,
+        static_cast<uint16_t*>(out_bf16), lse, static_cast<char*>(workspace) + t_need,
+        reinterpret_cast<int*>(static_cast<char*>(workspace) + dsa::topk_hist_bytes(B)), B, H, max_pages, page_size,
+        num_pages, keep, __builtin_ctz((unsigned)kp), scale, s));
   const int sp = effective_splits(resolve_splits(splits, B, H, keep_sel), keep_sel);
   const dsa::PoolForm pf = {__builtin_ctz((unsigned)kp), keep, npool, positions, 0};
   return status(dsa::launch_sparse_mla(static_cast<const uint16_t*>(q_bf16), kv_fp8, kv_scale, pools, cnt, page_table,

@@ -117,21 +117,31 @@ static_assert(L_SPG + 4 * 1024 <= L_CB && L_CB + 4 * FU_NW * FU_CSTAGE <= L_SB &
               "stage 3 blocks");
 static_assert(L_SCS + 4 * FU_KEYS == FU_LDS, "LDS size");
 
-// The attention's shape: HPW heads per workgroup (16 or 32) over splits of up to 4096 / HPW slots, its 8 waves as
-// TG groups of 32 tokens x HB blocks of 16 heads in the scores; its LDS past the gathered rows: the split's slot list
-// (stages 3-4, later P [HPW][SPLIT + 8] bf16), kv scales and biases [SPLIT], per-wave head maxima and sums [HPW][TG],
-// and (stage 3, read before the gather) the HPW heads' queries [HPW][584] bf16.
-template <int HPW>
+// The attention's shape: HPW heads per workgroup (16 or 32) over splits of up to 4096 / HPW slots of DQK-byte rows
+// (576, or 512: GLM's NoPE latent), its 8 waves as TG groups of 32 tokens x HB blocks of 16 heads in the scores; with
+// XT (the pooled form) a split holds up to 64 rows more (a pooled row's tail, padded), the waves of groups 0 and 1
+// taking groups TG and TG + 1 as well. Its LDS past the gathered rows (CAP rows at the stride KROW): the split's slot
+// list (later P [HPW][CAP + 8] bf16), kv scales and biases [CAP], per-wave head maxima and sums [HPW][TG], and (read
+// before the gather) the HPW heads' queries [HPW][DQK + 8] bf16. A split's rows are padded to a multiple of FU_CH =
+// 64: the gather's loads of 64 lanes x 16 bytes then cover its padded rows' pieces exactly (no lane of the last load
+// reads a slot past the padded rows).
+template <int HPW, int DQK = FU_DQK, bool XT = false>
 struct FuAtt {
   static constexpr int SPLIT = 4096 / HPW;
+  static constexpr int CAP = SPLIT + (XT ? FU_CH : 0);
   static constexpr int HB = HPW / 16;
   static constexpr int TG = SPLIT / 32;
-  static constexpr int PROW = SPLIT + 8;
-  static constexpr int QPT = (HPW * FU_DQK / 8 + FU_THREADS - 1) / FU_THREADS;  // query loads per thread
-  static constexpr int L_P = SPLIT * FU_KROW;
+  static constexpr int PROW = CAP + 8;
+  static constexpr int PIECES = DQK / 16;        // 16-byte pieces of a row
+  static constexpr int KPIECES = PIECES + 1;     // a staged row: its pieces and one padding piece
+  static constexpr int KROW = 16 * KPIECES;      // 592 or 528 bytes: 8 rows at one column cover the banks once
+  static constexpr int STEPS = DQK / 32;         // score steps
+  static constexpr int AQROW = DQK + 8;          // staged query row (bf16)
+  static constexpr int QPT = (HPW * DQK / 8 + FU_THREADS - 1) / FU_THREADS;  // query loads per thread
+  static constexpr int L_P = CAP * KROW;
   static constexpr int L_KSC = L_P + 2 * HPW * PROW;
-  static constexpr int L_BIAS = L_KSC + 4 * SPLIT;
-  static constexpr int L_RED = L_BIAS + 4 * SPLIT;
+  static constexpr int L_BIAS = L_KSC + 4 * CAP;
+  static constexpr int L_RED = L_BIAS + 4 * CAP;
   static constexpr int L_SRED = L_RED + 4 * TG * HPW;
   static constexpr int L_END = L_SRED + 4 * TG * HPW;
   static constexpr int L_QST = HPW == 16 ? 57344 : L_END;  // inside the row tile (read before the gather), or past it
@@ -139,6 +149,10 @@ struct FuAtt {
 static_assert(FuAtt<16>::TG * FuAtt<16>::HB == FU_WAVES && FuAtt<32>::TG * FuAtt<32>::HB == FU_WAVES, "waves");
 static_assert(FuAtt<16>::L_END <= FU_LDS && FuAtt<16>::L_QST + 2 * 16 * FU_AQROW <= FuAtt<16>::L_P, "stage 4, 16");
 static_assert(FuAtt<32>::L_QST + 2 * 32 * FU_AQROW <= L_SCS && FuAtt<32>::L_P >= 57344, "stage 4, 32");
+static_assert(FuAtt<32, 512, true>::L_QST + 2 * 32 * FuAtt<32, 512, true>::AQROW <= FU_LDS &&
+                  4 * FuAtt<32, 512, true>::CAP <= 2 * 32 * FuAtt<32, 512, true>::PROW,
+              "the pooled form's attention");
+static_assert(FuAtt<32>::KROW == FU_KROW && FuAtt<32>::STEPS == FU_STEPS && FuAtt<32>::AQROW == FU_AQROW, "shape");
 
 struct FuState {
   int gt[FU_NW];  // per workgroup: its candidates above T
@@ -177,6 +191,11 @@ struct FusedArgs {
   int num_slots;  // num_pages * page_size
   float scale;
   int HG, S, sps;
+  // the pooled form of the separate attention launch (kp_shift > 0): idx holds [B][keep >> kp_shift] selected pools,
+  // cnt their count, npool and positions the rows' complete pools and positions (the tail)
+  const int* npool;
+  const int* positions;
+  int kp_shift;
   int row0;  // this launch's first row (rows row0 .. row0 + 7)
 };
 
@@ -1011,21 +1030,23 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
 // The value operand of v_mfma_f32_16x16x32_bf16 from the token-major tile (ds_read_b64_tr_b8: lane (a, c) of each
 // 16-lane block gets byte c of the 8-byte rows addressed by the block's lanes 2j + a): lane l receives dim 16 n + l % 16
 // of tokens 32 ks + 8 (l / 16) + j, the B operand with k-slot 8 q + j = that token.
+template <int KROW>
 __device__ __forceinline__ bf16x8 fu_value_operand(const uint8_t* kt, int ks, int n, int lane) {
   typedef int v2i __attribute__((ext_vector_type(2)));
   const int q = lane >> 4, p = lane & 15;
-  const uint8_t* ad = kt + (32 * ks + 8 * q + (p >> 1)) * FU_KROW + 16 * n + 8 * (p & 1);
+  const uint8_t* ad = kt + (32 * ks + 8 * q + (p >> 1)) * KROW + 16 * n + 8 * (p & 1);
   const v2i r = __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) v2i*)(ad));
   return fp8x8_to_bf16x8((uint32_t)r.x, (uint32_t)r.y);
 }
 
-// Stage 4: the split's attention over the n_slots slots of the list at FuAtt<HPW>::L_P, with the queries staged in
-// stage 3.
-template <int HPW>
+// Stage 4: the split's attention over the n_slots slots of the list at FuAtt<HPW, DQK, XT>::L_P (at most CAP), with
+// the queries staged before.
+template <int HPW, int DQK = FU_DQK, bool XT = false>
 __device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int b, int j, int n_slots,
                                           float live_bias) {
-  using AT = FuAtt<HPW>;
-  constexpr int HB = AT::HB, TG = AT::TG, PROW = AT::PROW;
+  using AT = FuAtt<HPW, DQK, XT>;
+  constexpr int HB = AT::HB, TG = AT::TG, PROW = AT::PROW, KROW = AT::KROW, KPIECES = AT::KPIECES;
+  constexpr int PIECES = AT::PIECES, STEPS = AT::STEPS, AQROW = AT::AQROW;
   float* ksc_l = reinterpret_cast<float*>(lds + AT::L_KSC);
   float* bias_l = reinterpret_cast<float*>(lds + AT::L_BIAS);
   float* red = reinterpret_cast<float*>(lds + AT::L_RED);
@@ -1048,18 +1069,19 @@ __device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int 
     if (tid < HPW) mlp[tid * a.S] = make_float2(-INFINITY, 0.0f);
     return;
   }
+  static_assert(FU_CH * KPIECES % WAVE == 0 && AT::CAP % FU_CH == 0, "a padded split's pieces fill whole loads");
   const int padded = (n_slots + FU_CH - 1) / FU_CH * FU_CH;
 
   // the slot list (a padding row reads slot 0) and the queries (staged in LDS by stage 3)
   const int* slot_l = reinterpret_cast<const int*>(lds + AT::L_P);
-  const int slot = tid < AT::SPLIT ? slot_l[tid] : 0;
+  const int slot = tid < AT::CAP ? slot_l[tid] : 0;
   // the query operand: head 16 hb + l16, dims 64 (st / 2) + 16 q4 + 8 (st % 2) .. + 7 at score step st (the key
   // operand's dim order below)
-  bf16x8 qb[FU_STEPS];
+  bf16x8 qb[STEPS];
   {
-    const uint16_t* qh = qs + (16 * hb + l16) * FU_AQROW + 16 * q4;
+    const uint16_t* qh = qs + (16 * hb + l16) * AQROW + 16 * q4;
 #pragma unroll
-    for (int st2 = 0; st2 < FU_STEPS; ++st2)
+    for (int st2 = 0; st2 < STEPS; ++st2)
       qb[st2] = as_bf16x8(*reinterpret_cast<const uint4*>(qh + 64 * (st2 >> 1) + 8 * (st2 & 1)));
   }
   __syncthreads();  // every wave holds its query operand before the rows overwrite it
@@ -1068,16 +1090,16 @@ __device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int 
   // over the 8 waves
   {
     // unit u = 64 k + lane's row u / 37 and piece u % 37, advanced with k (by 8: u by 512 = 13 x 37 + 31)
-    constexpr int DR = FU_WAVES * WAVE / FU_KPIECES, DP = FU_WAVES * WAVE % FU_KPIECES;
-    const int units = padded * FU_KPIECES;
-    int row = (WAVE * wave + lane) / FU_KPIECES, pc = WAVE * wave + lane - row * FU_KPIECES;
+    constexpr int DR = FU_WAVES * WAVE / KPIECES, DP = FU_WAVES * WAVE % KPIECES;
+    const int units = padded * KPIECES;
+    int row = (WAVE * wave + lane) / KPIECES, pc = WAVE * wave + lane - row * KPIECES;
     for (int k = wave; k * WAVE < units; k += FU_WAVES) {
-      const uint8_t* src = a.kv + (size_t)slot_l[row] * FU_DQK + 16 * min(pc, FU_PIECES - 1);
+      const uint8_t* src = a.kv + (size_t)slot_l[row] * DQK + 16 * min(pc, PIECES - 1);
       __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(kt + 1024 * k), 16, 0, 0);
       row += DR;
       pc += DP;
-      if (pc >= FU_KPIECES) {
-        pc -= FU_KPIECES;
+      if (pc >= KPIECES) {
+        pc -= KPIECES;
         ++row;
       }
     }
@@ -1090,31 +1112,29 @@ __device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int 
   }
   __syncthreads();  // every row in LDS
 
-  // scores of tokens 32 tg .. + 31 (two blocks of 16) for heads 16 hb .. + 15: S^T = K . Q^T; lane group q4 reads
-  // piece 4 j + q4 (dims 64 j + 16 q4 ..) of its token per pair of steps (one ds_read_b128 for two MFMAs; 8 rows at
-  // one column cover the banks once at the 592-byte stride)
-  const bool has = 32 * tg < padded;
-  float sv[2][4];
-  float mx = -INFINITY;
-  if (has) {
+  // scores of tokens 32 g .. + 31 (two blocks of 16) for heads 16 hb .. + 15, g = tg and (XT, tg < 2) tg + TG:
+  // S^T = K . Q^T;
+  // lane group q4 reads piece 4 j + q4 (dims 64 j + 16 q4 ..) of its token per pair of steps (one ds_read_b128 for two
+  // MFMAs; 8 rows at one column cover the banks once at the row stride)
+  auto scores_of = [&](int g, float (&sv)[2][4], float& mx) __attribute__((always_inline)) {
     f32x4 acc[2][2];
 #pragma unroll
     for (int k = 0; k < 2; ++k) acc[k][0] = acc[k][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const uint8_t* kr = kt + (32 * tg + l16) * FU_KROW + 16 * q4;
+    const uint8_t* kr = kt + (32 * g + l16) * KROW + 16 * q4;
 #pragma unroll
-    for (int st2 = 0; st2 < FU_STEPS; st2 += 2) {
+    for (int st2 = 0; st2 < STEPS; st2 += 2) {
 #pragma unroll
       for (int k = 0; k < 2; ++k) {
-        const u32x4 kk = *reinterpret_cast<const u32x4*>(kr + 16 * k * FU_KROW + 32 * st2);
+        const u32x4 kk = *reinterpret_cast<const u32x4*>(kr + 16 * k * KROW + 32 * st2);
         acc[k][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16x8(kk[0], kk[1]), qb[st2], acc[k][0], 0, 0, 0);
         acc[k][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16x8(kk[2], kk[3]), qb[st2 + 1], acc[k][1], 0, 0,
                                                             0);
       }
     }
-    // acc[k][.][r] = S^T[token 32 tg + 16 k + 4 q4 + r][head 16 hb + l16]
+    // acc[k][.][r] = S^T[token 32 g + 16 k + 4 q4 + r][head 16 hb + l16]
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
-      const int tk = 32 * tg + 16 * k + 4 * q4;
+      const int tk = 32 * g + 16 * k + 4 * q4;
       const float4 ks4 = *reinterpret_cast<const float4*>(&ksc_l[tk]);
       const float4 bs4 = *reinterpret_cast<const float4*>(&bias_l[tk]);
       sv[k][0] = (acc[k][0][0] + acc[k][1][0]) * (ks4.x * a.scale) + bs4.x;
@@ -1124,7 +1144,13 @@ __device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int 
 #pragma unroll
       for (int i = 0; i < 4; ++i) mx = max_nonan(mx, sv[k][i]);
     }
-  }
+  };
+  const bool has = 32 * tg < padded;
+  const bool has2 = XT && 32 * (tg + TG) < padded;  // the tail's rows past the split's TG groups (tg < 2: CAP)
+  float sv[2][4], sx[2][4];
+  float mx = -INFINITY;
+  if (has) scores_of(tg, sv, mx);
+  if (has2) scores_of(tg + TG, sx, mx);
   mx = max_nonan(mx, __shfl_xor(mx, 16, WAVE));
   mx = max_nonan(mx, __shfl_xor(mx, 32, WAVE));
   if (lane < 16) red[(16 * hb + lane) * TG + tg] = mx;
@@ -1139,10 +1165,11 @@ __device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int 
     for (int t = 0; t < TG; ++t) m = max_nonan(m, r[t]);
   }
   float psum = 0.0f;
-  if (has) {
+  // the weights of group g: exp(s - m), the value's dequantisation folded into the bf16 weight
+  auto weights_of = [&](int g, const float (&sv)[2][4]) __attribute__((always_inline)) {
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
-      const int tk = 32 * tg + 16 * k + 4 * q4;
+      const int tk = 32 * g + 16 * k + 4 * q4;
       const float4 ks4 = *reinterpret_cast<const float4*>(&ksc_l[tk]);
       float p[4];
 #pragma unroll
@@ -1150,11 +1177,12 @@ __device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int 
         p[i] = __expf(sv[k][i] - m);
         psum += p[i];
       }
-      // the value's dequantisation folded into the bf16 weight
       *reinterpret_cast<uint2*>(&pl[(16 * hb + l16) * PROW + tk]) =
           make_uint2(bf16_pack(p[0] * ks4.x, p[1] * ks4.y), bf16_pack(p[2] * ks4.z, p[3] * ks4.w));
     }
-  }
+  };
+  if (has) weights_of(tg, sv);
+  if (has2) weights_of(tg + TG, sx);
   psum += __shfl_xor(psum, 16, WAVE);
   psum += __shfl_xor(psum, 32, WAVE);
   if (lane < 16) sred[(16 * hb + lane) * TG + tg] = psum;
@@ -1174,7 +1202,7 @@ __device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int 
       pop[h] = as_bf16x8(*reinterpret_cast<const uint4*>(&pl[(16 * h + l16) * PROW + 32 * ks + 8 * q4]));
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
-      const bf16x8 vop = fu_value_operand(kt, ks, 4 * wave + n, lane);
+      const bf16x8 vop = fu_value_operand<KROW>(kt, ks, 4 * wave + n, lane);
 #pragma unroll
       for (int h = 0; h < HB; ++h) o[h][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pop[h], vop, o[h][n], 0, 0, 0);
     }
@@ -1327,27 +1355,55 @@ __global__ __launch_bounds__(FU_THREADS, 1) void decode_fused_kernel(FusedArgs a
 // The split's slot list when the selection came from the separate kernels: output positions o0 .. o1 - 1 of row b,
 // as cache rows (rows [B, keep], the top-k's slot output) or as positions (idx [B, keep]) through the page table;
 // the attention's queries staged in LDS as stage 2 stages them. Returns the split's selected count (the empty row:
-// output 0, masked, as stage 2).
-template <int HPW>
+// output 0, masked, as stage 2). The pooled form (XT; trnrt/models/mla.py:615-630, the kpool tokens of each selected
+// pool and then the tail): token slot k is token k & (kpool - 1) of pool idx[b][k >> kp_shift] (below the selected
+// pools' cnt kpool slots), and the tail, tokens kpool npool .. pos of the incomplete pool (none when pos + 1 is a
+// multiple of kpool), follows in the split holding the last selected token (split 0 when no pool is selected).
+template <int HPW, int DQK = FU_DQK, bool XT = false>
 __device__ __forceinline__ int fu_attend_prep(const FusedArgs& a, const int* rows, uint8_t* lds, int b, int j,
                                               float* live_bias) {
-  using AT = FuAtt<HPW>;
+  using AT = FuAtt<HPW, DQK, XT>;
   constexpr int QPT = AT::QPT;
   int* slot_l = reinterpret_cast<int*>(lds + AT::L_P);
   const int tid = threadIdx.x;
   const int hg = j % a.HG, s = j / a.HG;
   const bool active = s < a.S;
   const int o0 = active ? s * a.sps : 0, o1 = active ? min(o0 + a.sps, a.keep) : 0;
-  const int cnt_row = min(max(a.cnt[b], 0), a.keep);
+  int cnt_row = min(max(a.cnt[b], 0), a.keep);
+  int tail = 0, tail_pos0 = 0, s_last = 0;
+  const int ipr = a.keep >> a.kp_shift;  // the pooled form's selected pools a row (its idx row stride)
+  if (XT) {
+    cnt_row = min(max(a.cnt[b], 0), ipr) << a.kp_shift;
+    const int np = max(a.npool[b], 0);
+    tail_pos0 = np << a.kp_shift;
+    tail = min(max(a.positions[b] + 1 - tail_pos0, 0), (1 << a.kp_shift) - 1);
+    s_last = cnt_row > 0 ? (cnt_row - 1) / a.sps : 0;
+  }
   u32x4 qv[QPT];
   if (active) {
-    const u32x4* qsrc = reinterpret_cast<const u32x4*>(a.q + ((size_t)b * a.H + HPW * hg) * FU_DQK);
+    const u32x4* qsrc = reinterpret_cast<const u32x4*>(a.q + ((size_t)b * a.H + HPW * hg) * DQK);
 #pragma unroll
-    for (int i = 0; i < QPT; ++i) qv[i] = qsrc[min(tid + FU_THREADS * i, HPW * FU_DQK / 8 - 1)];
+    for (int i = 0; i < QPT; ++i) qv[i] = qsrc[min(tid + FU_THREADS * i, HPW * DQK / 8 - 1)];
   }
+  const int n_sel = max(min(o1, cnt_row) - o0, 0);
+  const int n_tail = XT && active && s == s_last ? tail : 0;
+  const bool empty = cnt_row == 0 && tail == 0;  // the row attends output 0 (position 0), masked
   const int o = o0 + tid;
   int sl = 0;
-  if (tid < AT::SPLIT && o < o1 && o < max(cnt_row, 1)) {  // the empty row lists output 0 (position 0)
+  if (XT) {
+    if (tid < n_sel + n_tail || (empty && tid == 0)) {
+      int pos = 0;
+      if (tid < n_sel) {
+        const int pool = max(a.idx[(size_t)b * ipr + (o >> a.kp_shift)], 0);
+        pos = (pool << a.kp_shift) + (o & ((1 << a.kp_shift) - 1));
+      } else if (!empty) {
+        pos = tail_pos0 + (tid - n_sel);
+      }
+      const int pi = pos / a.page_size;  // pages of any multiple of kpool
+      const int pg = a.table[(size_t)b * a.max_pages + min(pi, a.max_pages - 1)];
+      sl = safe_page(pg, a.num_pages) * a.page_size + (pos - pi * a.page_size);
+    }
+  } else if (tid < AT::SPLIT && o < o1 && o < max(cnt_row, 1)) {  // the empty row lists output 0 (position 0)
     if (rows) {
       sl = rows[(size_t)b * a.keep + o];
     } else {
@@ -1355,21 +1411,21 @@ __device__ __forceinline__ int fu_attend_prep(const FusedArgs& a, const int* row
       const int pg = a.table[(size_t)b * a.max_pages + min(pi, a.max_pages - 1)];
       sl = safe_page(pg, a.num_pages) * a.page_size + (p - pi * a.page_size);
     }
-    sl = (unsigned)sl < (unsigned)a.num_slots ? sl : 0;
   }
+  sl = (unsigned)sl < (unsigned)a.num_slots ? sl : 0;
   if (active) {
     uint16_t* qs = reinterpret_cast<uint16_t*>(lds + AT::L_QST);
 #pragma unroll
     for (int i = 0; i < QPT; ++i) {
       const int pc = tid + FU_THREADS * i;
-      if (pc < HPW * FU_DQK / 8)
-        *reinterpret_cast<u32x4*>(qs + (pc / (FU_DQK / 8)) * FU_AQROW + 8 * (pc % (FU_DQK / 8))) = qv[i];
+      if (pc < HPW * DQK / 8)
+        *reinterpret_cast<u32x4*>(qs + (pc / (DQK / 8)) * AT::AQROW + 8 * (pc % (DQK / 8))) = qv[i];
     }
   }
-  if (tid < AT::SPLIT) slot_l[tid] = sl;  // padding rows read slot 0
-  int n_slots = max(min(o1, cnt_row) - o0, 0);
+  if (tid < AT::CAP) slot_l[tid] = sl;  // padding rows read slot 0
+  int n_slots = n_sel + n_tail;
   *live_bias = 0.0f;
-  if (active && cnt_row == 0 && s == 0) {
+  if (active && empty && s == 0) {
     n_slots = 1;
     *live_bias = NEG_INF;
   }
@@ -1381,7 +1437,7 @@ __device__ __forceinline__ int fu_attend_prep(const FusedArgs& a, const int* row
 // selection (rows of any length): rows row0 + x, row0 + x + 8, ... (up to rpl of them) on XCD x, with the same
 // splits and bf16 split outputs; every workgroup takes its split of each row in turn, then one XCD-local barrier,
 // then the combines.
-template <int HPW>
+template <int HPW, int DQK = FU_DQK, bool XT = false>
 __global__ __launch_bounds__(FU_THREADS, 1) void decode_attend_kernel(FusedArgs a, const int* rows, int rpl) {
   __shared__ __align__(16) uint8_t lds[FU_LDS];
   const int x = blockIdx.x % FU_XCDS, j = blockIdx.x / FU_XCDS;
@@ -1392,8 +1448,8 @@ __global__ __launch_bounds__(FU_THREADS, 1) void decode_attend_kernel(FusedArgs 
     if (r) __syncthreads();  // the previous row's attention has read its LDS before the next slot list is written
     float live_bias;
     const int b = a.row0 + x + FU_XCDS * r;
-    const int n_slots = fu_attend_prep<HPW>(a, rows, lds, b, j, &live_bias);
-    fu_attend<HPW>(a, lds, b, j, n_slots, live_bias);
+    const int n_slots = fu_attend_prep<HPW, DQK, XT>(a, rows, lds, b, j, &live_bias);
+    fu_attend<HPW, DQK, XT>(a, lds, b, j, n_slots, live_bias);
   }
   fu_barrier(sync, 1);  // every split's output of the XCD's rows
   for (int r = 0; r < nr; ++r) fu_combine(a, lds, a.row0 + x + FU_XCDS * r, j);
@@ -1458,13 +1514,12 @@ size_t attend_xcd_bytes(int B, int H, int keep) {
   return l.end - l.part;
 }
 
-hipError_t launch_decode_attend(const uint16_t* q, const uint8_t* kv, const float* kvs, const int* rows,
-                                const int* idx, const int* table, const int* cnt, uint16_t* out, float* lse, void* ws,
-                                int* sync, int B, int H, int max_pages, int page_size, int num_pages, int keep,
-                                float scale, hipStream_t s) {
+// The separate attention launch's arguments past the selection's (rows, idx, cnt, npool, positions, kp_shift): the
+// split outputs in ws, the per-XCD barrier words in sync, splits of a multiple of 64 slots over `keep` slots a row.
+static FusedArgs attend_args(const uint16_t* q, const uint8_t* kv, const float* kvs, const int* table, uint16_t* out,
+                             float* lse, void* ws, int* sync, int B, int H, int max_pages, int page_size,
+                             int num_pages, int keep, float scale, int hpw) {
   FusedArgs a{};
-  const int hpw = fused_hpw(H, keep);
-  if (!hpw || (!rows && (!idx || !table))) return hipErrorInvalidValue;
   const int S = fused_splits(H, hpw);
   const FusedLayout l = fused_layout(0, B, H, S, keep);
   char* p = static_cast<char*>(ws) - l.part;
@@ -1472,8 +1527,6 @@ hipError_t launch_decode_attend(const uint16_t* q, const uint8_t* kv, const floa
   a.kv = kv;
   a.kvs = kvs;
   a.table = table;
-  a.idx = const_cast<int*>(idx);
-  a.cnt = const_cast<int*>(cnt);
   a.out = out;
   a.lse = lse;
   a.sync = sync;
@@ -1491,18 +1544,59 @@ hipError_t launch_decode_attend(const uint16_t* q, const uint8_t* kv, const floa
   a.S = S;
   int sps = (keep + S - 1) / S;
   a.sps = (sps + FU_CH - 1) / FU_CH * FU_CH;
+  return a;
+}
+
+// One launch per 4 rows per XCD at most: a batch of 12 rows is one launch of 2 rows per XCD (or 1), not 8 + 4.
+template <typename K>
+static hipError_t attend_launches(FusedArgs a, K kernel, const int* rows, hipStream_t s) {
   const dim3 grid(FU_XCDS * FU_NW), block(FU_THREADS);
-  // up to 4 rows per XCD and launch: a batch of 12 rows is one launch of 2 rows per XCD (or 1), not 8 + 4
   constexpr int RPL_MAX = 4;
-  for (int r0 = 0; r0 < B; r0 += FU_XCDS * RPL_MAX) {
+  for (int r0 = 0; r0 < a.B; r0 += FU_XCDS * RPL_MAX) {
     a.row0 = r0;
-    const int left = B - r0, rpl = (left < FU_XCDS * RPL_MAX ? left : FU_XCDS * RPL_MAX) + FU_XCDS - 1;
-    const hipError_t e =
-        hpw == 32 ? launch("decode_attend_kernel", decode_attend_kernel<32>, grid, block, s, a, rows, rpl / FU_XCDS)
-                  : launch("decode_attend_kernel", decode_attend_kernel<16>, grid, block, s, a, rows, rpl / FU_XCDS);
+    const int left = a.B - r0, rpl = (left < FU_XCDS * RPL_MAX ? left : FU_XCDS * RPL_MAX) + FU_XCDS - 1;
+    const hipError_t e = launch("decode_attend_kernel", kernel, grid, block, s, a, rows, rpl / FU_XCDS);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
+}
+
+hipError_t launch_decode_attend(const uint16_t* q, const uint8_t* kv, const float* kvs, const int* rows,
+                                const int* idx, const int* table, const int* cnt, uint16_t* out, float* lse, void* ws,
+                                int* sync, int B, int H, int max_pages, int page_size, int num_pages, int keep,
+                                float scale, hipStream_t s) {
+  const int hpw = fused_hpw(H, keep);
+  if (!hpw || (!rows && (!idx || !table))) return hipErrorInvalidValue;
+  FusedArgs a = attend_args(q, kv, kvs, table, out, lse, ws, sync, B, H, max_pages, page_size, num_pages, keep, scale,
+                            hpw);
+  a.idx = const_cast<int*>(idx);
+  a.cnt = const_cast<int*>(cnt);
+  return hpw == 32 ? attend_launches(a, decode_attend_kernel<32>, rows, s)
+                   : attend_launches(a, decode_attend_kernel<16>, rows, s);
+}
+
+// The pooled form: 512-wide rows, 32 heads per workgroup (splits of 128 token slots, the split holding a row's last
+// selected token taking its tail too).
+bool attend_xcd_pooled_ok(int num_cu, int H, int Dqk, int keep_tokens) {
+  return num_cu == FU_XCDS * FU_NW && Dqk == 512 && keep_tokens >= 1 && fused_hpw(H, keep_tokens) == 32;
+}
+
+hipError_t launch_decode_attend_pooled(const uint16_t* q, const uint8_t* kv, const float* kvs, const int* pools,
+                                       const int* cnt, const int* npool, const int* positions, const int* table,
+                                       uint16_t* out, float* lse, void* ws, int* sync, int B, int H, int max_pages,
+                                       int page_size, int num_pages, int keep_pools, int kp_shift, float scale,
+                                       hipStream_t s) {
+  const int keep = keep_pools << kp_shift;  // token slots
+  if (kp_shift < 1 || !pools || !cnt || !npool || !positions || !table || fused_hpw(H, keep) != 32)
+    return hipErrorInvalidValue;
+  FusedArgs a = attend_args(q, kv, kvs, table, out, lse, ws, sync, B, H, max_pages, page_size, num_pages, keep, scale,
+                            32);
+  a.idx = const_cast<int*>(pools);
+  a.cnt = const_cast<int*>(cnt);
+  a.npool = npool;
+  a.positions = positions;
+  a.kp_shift = kp_shift;
+  return attend_launches(a, decode_attend_kernel<32, 512, true>, nullptr, s);
 }
 
 hipError_t launch_decode_fused(const uint16_t* q_idx, const float* w, const uint8_t* k, const float* ks,
