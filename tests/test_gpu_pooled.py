@@ -249,17 +249,22 @@ def test_glm_pooled_decode_step_end_to_end():
     assert_attention_close(o, want_o)
 
 
-@pytest.mark.parametrize("dqk,L,pos", [(512, 4096, (4095, 4094, 3001, 2050, 700, 1)),
-                                       (576, 4096, (4095, 4094, 3001, 2050, 700, 1)),
-                                       (512, 32768, (32767, 30001, 9000))])
-def test_pooled_decode_layer_matches_composition_and_oracle(dqk, L, pos):
+@pytest.mark.parametrize("dqk,L,pos,H", [(512, 4096, (4095, 4094, 3001, 2050, 700, 1), 64),
+                                         (576, 4096, (4095, 4094, 3001, 2050, 700, 1), 64),
+                                         (512, 32768, (32767, 30001, 9000), 64),
+                                         (512, 4096, (4094, 2050, 700, 1), 32)])
+def test_pooled_decode_layer_matches_composition_and_oracle(dqk, L, pos, H):
     """The one-call pooled layer (dsa_pooled_decode_layer: the indexer with the fused first-level histogram, the
     top-k, attention over the selected pools' tokens and the tail read straight from the pool indices) against the
     reference-flow composition (dsa_long.decode_pooled: scores, select, slots, attend) and the oracle; at 32,768
-    tokens (8,192 pools a row) the selection is the one-workgroup-per-row kernel fed by the fused histogram."""
+    tokens (8,192 pools a row) the selection is the one-workgroup-per-row kernel fed by the fused histogram. With
+    512-wide rows the attention and combine are one XCD-local launch (64 heads: 16 splits of 128 token slots; 32
+    heads: 32 splits of 64), a row's tail in the split of its last selected token: the last split with a full
+    selection (up to 131 rows there), a middle one (175 pools), split 0 (no complete pool); 576-wide rows take the
+    split attention and the combine kernel."""
     from trnrt_amd.kernels.dsa_layer import PooledDecodeLayer
-    cfg = W.PooledConfig("glm-layer", B=len(pos), L=L, dqk=dqk)
-    say(f"pooled layer dqk={dqk} B={cfg.B} L={cfg.L}")
+    cfg = W.PooledConfig("glm-layer", B=len(pos), L=L, dqk=dqk, H=H)
+    say(f"pooled layer dqk={dqk} H={H} B={cfg.B} L={cfg.L}")
     inp = W.make_pooled_inputs(cfg, seed=30 + dqk + L, device="cuda")
     kp, ps = cfg.kp, cfg.page_size
     positions = torch.tensor(pos, dtype=torch.int32)
