@@ -101,6 +101,22 @@ def test_fused_layer_ragged_two_launches():
     _workspace_clean(L)
 
 
+def test_fused_layer_block_sizes():
+    """Rows whose lengths sit at and just past multiples of 1,024 tokens: the workgroups' blocks of positions take
+    sizes from 32 to 1,024 (32 ceil(L / 1024)), across the size past which a key list no longer holds a whole block
+    (192 -> 224 positions) and with blocks ending inside pages; 16 rows, two launches, every position of every row
+    against the oracle."""
+    lengths = [1024, 1025, 2048, 3072, 3073, 6144, 6145, 7168, 12288, 16385, 20480, 25600, 26215, 30000, 31744,
+               32767]
+    say(f"fused layer block sizes B=16 {lengths}")
+    cfg = W.Config("fused-blocks", B=16, L=32768, H=64, Hi=64)
+    inp = W.make_inputs(cfg, seed=14, lengths=lengths)
+    g = inp.to("cuda")
+    L = _run(g)
+    _check_full(inp, L)
+    _workspace_clean(L)
+
+
 @pytest.mark.parametrize("H,Hi", [(16, 16), (32, 48), (128, 64)])
 def test_fused_layer_head_counts(H, Hi):
     say(f"fused layer H={H} Hi={Hi}")
