@@ -117,6 +117,25 @@ def test_fused_layer_block_sizes():
     _workspace_clean(L)
 
 
+@pytest.mark.parametrize("seed", [101, 202, 303, 404])
+def test_fused_layer_random_batches(seed):
+    """Seeded random batches: 1 to 12 rows of random lengths (1 .. 32,768, a third of them short), query heads 16, 32
+    or 64 with 16 to 64 indexer heads; scores, selection and attention against the oracle on every position."""
+    g = torch.Generator().manual_seed(seed)
+    B = int(torch.randint(1, 13, (1,), generator=g))
+    H = [16, 32, 64][int(torch.randint(0, 3, (1,), generator=g))]
+    Hi = [16, 32, 48, 64][int(torch.randint(0, 4, (1,), generator=g))]
+    lengths = [int(torch.randint(1, 32769, (1,), generator=g)) if torch.rand(1, generator=g) > 1 / 3
+               else int(torch.randint(1, 4097, (1,), generator=g)) for _ in range(B)]
+    say(f"fused layer random seed={seed} B={B} H={H} Hi={Hi} {lengths}")
+    cfg = W.Config(f"fused-rand{seed}", B=B, L=32768, H=H, Hi=Hi)
+    inp = W.make_inputs(cfg, seed=seed, lengths=lengths)
+    gi = inp.to("cuda")
+    L = _run(gi)
+    _check_full(inp, L)
+    _workspace_clean(L)
+
+
 @pytest.mark.parametrize("H,Hi", [(16, 16), (32, 48), (128, 64)])
 def test_fused_layer_head_counts(H, Hi):
     say(f"fused layer H={H} Hi={Hi}")
