@@ -262,10 +262,26 @@ def test_pooled_decode_layer_matches_composition_and_oracle(dqk, L, pos, H):
     heads: 32 splits of 64), a row's tail in the split of its last selected token: the last split with a full
     selection (up to 131 rows there), a middle one (175 pools), split 0 (no complete pool); 576-wide rows take the
     split attention and the combine kernel."""
+    _pooled_layer_check(dqk, L, pos, H, 30 + dqk + L)
+
+
+@pytest.mark.parametrize("seed", [7, 8, 9])
+def test_pooled_decode_layer_random_positions(seed):
+    """Seeded random batches of the one-call pooled layer: 1 to 8 rows at random positions of a 4,096-token context
+    (random tails of 0 to 3 tokens, rows with fewer complete pools than keep), 32 or 64 query heads, 512-wide rows:
+    the XCD-local attention launch against the oracle."""
+    g = torch.Generator().manual_seed(seed)
+    B = int(torch.randint(1, 9, (1,), generator=g))
+    H = [32, 64][int(torch.randint(0, 2, (1,), generator=g))]
+    pos = tuple(int(x) for x in torch.randint(0, 4096, (B,), generator=g))
+    _pooled_layer_check(512, 4096, pos, H, 1000 + seed)
+
+
+def _pooled_layer_check(dqk, L, pos, H, seed):
     from trnrt_amd.kernels.dsa_layer import PooledDecodeLayer
     cfg = W.PooledConfig("glm-layer", B=len(pos), L=L, dqk=dqk, H=H)
     say(f"pooled layer dqk={dqk} H={H} B={cfg.B} L={cfg.L}")
-    inp = W.make_pooled_inputs(cfg, seed=30 + dqk + L, device="cuda")
+    inp = W.make_pooled_inputs(cfg, seed=seed, device="cuda")
     kp, ps = cfg.kp, cfg.page_size
     positions = torch.tensor(pos, dtype=torch.int32)
     npool = torch.div(positions + 1, kp, rounding_mode="floor").to(torch.int32)
