@@ -440,6 +440,8 @@ def pooled_main(args) -> int:
     ms = (time.perf_counter() - t0) * 1e3 / args.steps
     k_us = kernel_times(lib, step, args.steps)
     spans = step_times(step, args.steps)
+    if layer.status()["gave_up"]:
+        raise RuntimeError("bench.py: a barrier wait of the pooled attention launch gave up")
     positions = pos.cpu().long()
     npool = torch.div(positions + 1, kp, rounding_mode="floor")
     tail = [int(p) + 1 - kp * int(n) for p, n in zip(positions, npool)]
@@ -662,6 +664,11 @@ def main() -> int:
     k_us = kernel_times(lib, step, args.steps)
     spans = step_times(step, args.steps)
     g_us = graph_step_us(step, args.steps)
+    # no barrier wait of any step above gave up (the one-launch kernel's workgroups were all resident): the outputs
+    # the timed steps produced are the layer's
+    st = layer.status()
+    if st["gave_up"]:
+        raise RuntimeError(f"bench.py: {st['gave_up']} barrier wait(s) gave up during the benchmark")
 
     lengths = inp.lengths
     layer_bytes = W.algorithmic_bytes(lengths, cfg.H, cfg.Hi, cfg.keep, cfg.page_size)

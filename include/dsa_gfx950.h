@@ -3,14 +3,20 @@
  * lightning indexer -> exact per-row top-k -> sparse MLA attention over a paged FP8 KV cache.
  *
  * Every pointer is a device pointer unless stated otherwise; every entry point enqueues work on `stream`
- * (a hipStream_t passed as void*) and returns without synchronising. Return value: DSA_OK (0) or a negative
- * DSA_E* code; dsa_strerror() names it. No entry point allocates device memory: scratch space is a
- * caller-owned workspace sized by dsa_workspace_bytes(). A workspace must be zero-filled before its first use
- * (dsa_workspace_clear, or any zero fill); every call leaves the parts that must be zero at zero again, so one
- * workspace serves any number of calls (and of graph replays). Calls that share a workspace must not overlap.
+ * (a hipStream_t passed as void*) and returns without synchronising (dsa_layer_status excepted). Return value:
+ * DSA_OK (0) or a negative DSA_E* code; dsa_strerror() names it. No entry point allocates device memory: scratch
+ * space is a caller-owned workspace sized by dsa_workspace_bytes(). A workspace must be zero-filled before its
+ * first use (dsa_workspace_clear, or any zero fill) and written by nothing but these calls afterwards. A decode or
+ * top-k workspace starts with 1 KiB of barrier and status words at the same offset for every batch size (the status
+ * words count across calls, see dsa_layer_status), then the top-k histograms [B, 4096] int32: the zero region of a
+ * call of B rows, which the call leaves zero again; the rest is per-call scratch. The library records on the host
+ * how much of each workspace's start is zero and zero-fills the difference (a fill kernel on the call's stream)
+ * before a call whose zero region reaches further than the last call's, or before the first call it sees on a
+ * workspace: so one workspace serves any number of calls, of any batch sizes it is large enough for, and graph
+ * replays. Calls that share a workspace must not overlap.
  * Kernels never raise; every shape and argument check happens on the host before launch, so a call that returns
- * DSA_EINVAL, DSA_EUNSUPPORTED or DSA_EWORKSPACE has written nothing. A call that returns DSA_ELAUNCH clears the
- * regions it had dirtied; should that clearing fail too, run dsa_workspace_clear before the workspace's next use.
+ * DSA_EINVAL, DSA_EUNSUPPORTED or DSA_EWORKSPACE has written nothing. After a call that returns DSA_ELAUNCH the next
+ * call on its workspace zero-fills the whole zero region first.
  *
  * Cache layout (the paged FP8 cache of trnrt/models/decoder.py:459-490 and trnrt/engine/model_runner.py:54-70,
  * extended with per-token scales):
@@ -31,7 +37,7 @@
 extern "C" {
 #endif
 
-#define DSA_ABI_VERSION 8
+#define DSA_ABI_VERSION 9
 
 #define DSA_OK 0
 #define DSA_EINVAL (-1)      /* a null pointer or a size out of range */
@@ -133,10 +139,11 @@ int dsa_topk_mask(const int32_t* idx, const int32_t* cnt, const float* scores, f
 
 /*
  * Sparse MLA decode attention over the selected tokens (replaces trnrt/kernels/dsa_decode.py:26-43 `attend`,
- * trnrt/kernels/dsa_slots.py:48-65 `emulate` with lse, trnrt/kernels/dsa_slots_n.py:154-203 `attend`,
- * trnrt/models/dsa_long.py:189-223 `slots` + `attend`; split combine of trnrt/models/mla.py:853-856):
+ * trnrt/kernels/dsa_slots.py:48-65 `emulate` with lse, trnrt/models/dsa_long.py:189-223 `slots` + `attend`; split
+ * combine of trnrt/models/mla.py:853-856):
  *   K[k] = kv_fp8[slot_k, :Dqk] * kv_scale[slot_k] (key, Dqk = 576: 512 latent + 64 rope, or 512: GLM's NoPE latent;
- *   rows of Dqk bytes), V[k] = K[k][:Dv] (Dv = 512)
+ *   rows of Dqk bytes), V[k] = K[k][:Dv] (Dv = 512); kv_scale NULL: every scale 1 (the reference's unscaled FP8
+ *   cache, trnrt/models/decoder.py:481-486; so in every entry point below that takes a kv_scale)
  *   s[h, k] = scale * q[b, h, :] . K[k] + bias_k,  p = softmax_k(s),  out[b, h, :] = sum_k p[h, k] V[k]
  *   lse[b, h] = max_k s + log sum_k exp(s - max)
  * Two ways to name the slots (exactly one must be given):
@@ -152,6 +159,18 @@ int dsa_sparse_mla_decode(const void* q_bf16, const uint8_t* kv_fp8, const float
                           void* out_bf16, float* out_f32, float* lse, void* workspace, size_t workspace_bytes, int B,
                           int H, int Dqk, int Dv, int keep, int max_pages, int page_size, int num_pages, float scale,
                           int splits, void* stream);
+
+/*
+ * Slot attention over the first n rows of N, n read on the device (replaces trnrt/kernels/dsa_slots_n.py:154-203
+ * `attend`, whose n is a one-element int tensor and whose rows past n stay unwritten on the device): the row form of
+ * dsa_sparse_mla_decode (rows int32 [N, keep] cache slots of kv_fp8 [num_slots, Dqk], bias fp32 [N, keep]) over rows
+ * r < *n_live only; out / out_f32 / lse rows at or past it are not written (no work is done for them). n_live: int32
+ * [1] on the device (values past N act as N). Workspace as dsa_sparse_mla_decode's at (N, H, keep, splits).
+ */
+int dsa_sparse_mla_slots_n(const void* q_bf16, const uint8_t* kv_fp8, const float* kv_scale, const int32_t* rows,
+                           const float* bias, const int32_t* n_live, void* out_bf16, float* out_f32, float* lse,
+                           void* workspace, size_t workspace_bytes, int N, int H, int Dqk, int keep,
+                           long long num_slots, float scale, int splits, void* stream);
 
 /*
  * Mask compaction (trnrt/models/dsa_long.py:140-166 `compact`): row n of sel fp32 [N, M] (an entry counts as a one
@@ -238,6 +257,12 @@ size_t dsa_prefill_select_workspace_bytes(int N, int P, int score_stride, int ke
  * [B, keep], cnt int32 [B]). On a GPU of 8 XCDs x 32 CUs with rows of at most 32,768 tokens (and the shapes the
  * one-launch kernel takes: Hi <= 64, H a multiple of 16 up to 512, pages of a power of two >= 32, score_stride a
  * multiple of 4, keep <= 256 * (512 / H)) the step is one kernel launch; otherwise it is dsa_decode_layer_chain.
+ * The one launch, and the separate kernels' attention launch, are 256 workgroups of which the 32 on each XCD wait
+ * for each other at XCD-local barriers: they need every one of their workgroups resident at once (one per CU, 160
+ * KiB of LDS each). So these calls must not overlap one another on a GPU, whatever their workspaces and streams,
+ * and no other kernel may hold CUs throughout one of them. A barrier wait is bounded (about a second); one that
+ * gives up is counted in the workspace's status words, which dsa_layer_status reads: the call's outputs are then
+ * unreliable, though every kernel ends normally.
  */
 int dsa_decode_layer(const void* q_idx_bf16, const float* w, const uint8_t* k_fp8, const float* k_scale,
                      const void* q_bf16, const uint8_t* kv_fp8, const float* kv_scale, const int32_t* page_table,
@@ -262,9 +287,10 @@ int dsa_decode_layer_chain(const void* q_idx_bf16, const float* w, const uint8_t
  * that cannot allocate device memory, such as code under HIP graph capture, tight serving loops or harnesses that
  * forbid hipMalloc). The workspace is the library's own scratch, a static device array of
  * DSA_NOALLOC_SCRATCH_BYTES per GPU (allocated with the library's code object on each GPU it runs on and held until
- * the process ends; zero-filled by a kernel on `stream` at the first call on a device; a call whose zero region
- * (the row histograms and barrier words of its batch size) reaches past the previous call's gets the difference
- * zero-filled on `stream` first, so calls of any batch sizes follow each other). A call whose
+ * the process ends; its zero region kept as any workspace's: the first call on a device fills the zero region of
+ * its batch size, and a call whose zero region (the barrier words and its rows' histograms) reaches past the
+ * previous call's gets the difference filled on `stream` first, so calls of any batch sizes follow each other). A
+ * call whose
  * dsa_workspace_bytes(DSA_WS_LAYER, B, H, keep, max_len, splits) exceeds that size returns DSA_ESCRATCH before any
  * HIP call. Every call on a GPU shares that GPU's scratch: calls that overlap on one GPU (several streams, host
  * threads) race and must be serialised by the caller. Arguments and results as dsa_decode_layer.
@@ -366,6 +392,18 @@ size_t dsa_workspace_bytes(int kind, int B, int H, int keep, int max_len, int sp
 
 /* The split count dsa_sparse_mla_decode uses for splits = 0. */
 int dsa_default_splits(int B, int H, int keep);
+
+/*
+ * The status words of a decode workspace (no counterpart in the reference, whose device kernels never report and
+ * whose host wrappers raise, trnrt/kernels/dsa_index.py:258-259): what the calls since the last clear counted,
+ * summed over the XCDs. *gave_up: barrier waits of dsa_decode_layer (one launch), dsa_decode_layer_chain's attention
+ * launch or dsa_pooled_decode_layer's attention launch that gave up (non-zero: some of those calls' outputs may be
+ * wrong); *two_exchange: rows the one-launch layer selected in its two-exchange form (statistics). workspace: a
+ * decode workspace, or NULL for the current device's dsa_decode_layer_noalloc scratch. Synchronises `stream` (the
+ * only entry point that does), and with clear != 0 zeroes the counts (a fill kernel on `stream`, then a second
+ * synchronisation); must not overlap a call on the same workspace. Returns DSA_OK, DSA_EINVAL or DSA_ELAUNCH.
+ */
+int dsa_layer_status(void* workspace, int32_t* gave_up, int32_t* two_exchange, int clear, void* stream);
 
 /*
  * Kernel timing for benchmarks (no counterpart in the reference, whose kernels are timed by the Neuron profiler).

@@ -52,6 +52,12 @@ def test_status_strings():
         assert lib.dsa_strerror(s)
 
 
+def test_layer_status_checks_its_outputs():
+    # null output pointers are refused before any HIP call
+    lib = _lib.lib()
+    assert lib.dsa_layer_status(ctypes.c_void_p(16), None, None, 0, None) == _lib.DSA_EINVAL
+
+
 def test_host_side_argument_checks():
     lib = _lib.lib()
     null = None

@@ -33,22 +33,29 @@ def _run(g, chain=False):
     return L
 
 
+SYNC_WORDS = 256  # the workspace's first 1 KiB: per XCD 16 barrier and status words; the row histograms follow
+
+
 def _workspace_clean(L):
-    """The histograms and the per-XCD barrier words (arrivals, exits) are zero again, and no error flag is set."""
+    """The per-XCD barrier words (arrivals, exits) and the histograms are zero again, and no barrier wait gave up
+    (the status words, read through the C ABI's dsa_layer_status as well)."""
     ws = L.workspace.view(torch.int32).cpu()
-    hist_words = L.B * 4096
-    assert torch.all(ws[:hist_words] == 0), "row histograms left non-zero"
-    sync = ws[hist_words:hist_words + 8 * 16].view(8, 16)
+    sync = ws[:8 * 16].view(8, 16)
     assert torch.all(sync[:, :2] == 0), f"barrier words left non-zero: {sync[:, :3].tolist()}"
-    assert torch.all(sync[:, 2] == 0), "a barrier wait gave up (error flag set)"
+    assert torch.all(ws[8 * 16:SYNC_WORDS] == 0), "words past the 8 XCDs' barrier words"
+    assert torch.all(ws[SYNC_WORDS:SYNC_WORDS + L.B * 4096] == 0), "row histograms left non-zero"
+    assert torch.all(sync[:, 2] == 0), "a barrier wait gave up"
+    assert L.status()["gave_up"] == 0
 
 
 def _two_exchange_per_xcd(L) -> list:
     """Per XCD, the rows that took the two-exchange selection (stages 2 and 3) since the workspace was made: the kernel
-    counts them in the XCD's barrier words (row b of a launch runs on XCD b % 8); the others took the one-exchange
+    counts them in the XCD's status words (row b of a launch runs on XCD b % 8); the others took the one-exchange
     selection from the key lists."""
     ws = L.workspace.view(torch.int32).cpu()
-    return ws[L.B * 4096:L.B * 4096 + 8 * 16].view(8, 16)[:, 3].tolist()
+    per = ws[:8 * 16].view(8, 16)[:, 3].tolist()
+    assert L.status()["two_exchange"] == sum(per)
+    return per
 
 
 def _two_exchange_rows(L) -> int:

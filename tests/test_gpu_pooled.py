@@ -92,7 +92,7 @@ def test_attend_pooled_tails_vs_oracle(kp, dqk, splits):
     tok = (want_r.unsqueeze(-1) * kp + torch.arange(kp)).reshape(B, -1)
     want_o, want_lse = O.sparse_mla_slots_ref(q, kv, ks, tok, want_b.reshape(B, -1), 192 ** -0.5)
     assert_attention_close(o, want_o)
-    assert torch.allclose(lse.cpu(), want_lse, atol=2e-3, rtol=1e-4)
+    assert torch.allclose(lse.cpu(), want_lse, atol=1e-3, rtol=1e-4)
 
 
 def _pool_setup(seed, fp8_rows, B=3, L=1024, ps=64, kp=4):
@@ -301,7 +301,7 @@ def _pooled_layer_check(dqk, L, pos, H, seed):
                                               cfg.scale)
     assert_attention_close(out.float(), want_o)
     assert_attention_close(o_ref, want_o)
-    assert torch.allclose(lse.cpu(), want_lse, atol=2e-3, rtol=1e-4)
+    assert torch.allclose(lse.cpu(), want_lse, atol=1e-3, rtol=1e-4)
     # a second step with the histogram region left at zero by the first
     out1 = out.clone()
     out2, _ = layer.step(inp.q_idx, inp.w, inp.pool_key, inp.q, inp.kv_cache, inp.kv_scale, inp.table, npool.cuda(),

@@ -30,7 +30,7 @@ DSA_WS_TOPK = 1
 DSA_WS_ATTENTION = 2
 DSA_WS_LAYER = 3
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 P = c_void_p
 # Every entry point of include/dsa_gfx950.h with its ctypes signature (restype, argtypes).
@@ -53,6 +53,10 @@ SIGNATURES: dict[str, tuple] = {
         c_int,
         [P, P, P, P, P, P, P, P, P, P, P, P, c_size_t, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
          c_float, c_int, P],
+    ),
+    "dsa_sparse_mla_slots_n": (
+        c_int,
+        [P, P, P, P, P, P, P, P, P, P, c_size_t, c_int, c_int, c_int, c_int, ctypes.c_longlong, c_float, c_int, P],
     ),
     "dsa_token_rows": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, P]),
     "dsa_compact_mask": (c_int, [P, c_int, c_int, c_int, P, P, P]),
@@ -97,6 +101,7 @@ SIGNATURES: dict[str, tuple] = {
     "dsa_prefill_select_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int]),
     "dsa_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int]),
     "dsa_default_splits": (c_int, [c_int, c_int, c_int]),
+    "dsa_layer_status": (c_int, [P, P, P, c_int, P]),
     "dsa_timing_begin": (c_int, [P, c_int]),
     "dsa_timing_end": (c_int, []),
     "dsa_timing_kernel_name": (ctypes.c_char_p, [c_int]),
@@ -135,6 +140,16 @@ def check(status: int, what: str) -> None:
     if status == DSA_EUNSUPPORTED:
         raise NotImplementedError(msg)
     raise RuntimeError(msg)
+
+
+def layer_status(workspace_ptr: int | None, stream_ptr: int, clear: bool = False) -> tuple[int, int]:
+    """(barrier waits that gave up, rows selected in the two-exchange form) counted in a decode workspace since its
+    last clear (workspace_ptr None: the allocation-free entry point's scratch on the current device). Synchronises
+    the stream."""
+    gave_up, two = ctypes.c_int32(0), ctypes.c_int32(0)
+    check(lib().dsa_layer_status(workspace_ptr, ctypes.byref(gave_up), ctypes.byref(two), int(clear), stream_ptr),
+          "dsa_layer_status")
+    return int(gave_up.value), int(two.value)
 
 
 def workspace_bytes(kind: int, B: int, H: int, keep: int, max_len: int, splits: int = 0) -> int:

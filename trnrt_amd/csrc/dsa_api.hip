@@ -74,8 +74,8 @@ hipError_t launch_decode_attend_pooled(const uint16_t* q, const uint8_t* kv, con
 hipError_t launch_decode_fused(const uint16_t* q_idx, const float* w, const uint8_t* k, const float* ks,
                                const uint16_t* q, const uint8_t* kv, const float* kvs, const int* table,
                                const int* ctx_len, float* scores, int* idx, int* cnt, uint16_t* out, float* lse,
-                               void* ws, size_t hist_bytes, size_t zero_bytes, int B, int Hi, int H, int max_pages,
-                               int page_size, int num_pages, int stride, int keep, float scale, hipStream_t s);
+                               void* ws, size_t zero_bytes, int B, int Hi, int H, int max_pages, int page_size,
+                               int num_pages, int stride, int keep, float scale, hipStream_t s);
 bool topk_supported(int max_len, int keep, int vis_only);
 hipError_t launch_sparse_mla(const uint16_t* q, const uint8_t* kv, const float* kvs, const int* idx, const int* cnt,
                              const int* table, const int* rows, const float* bias, uint16_t* out, float* out_f32,
@@ -246,36 +246,86 @@ struct AuxStream {
   }
 };
 
+// How much of each workspace's start is zero for the next call on it, recorded on the host as calls are enqueued
+// (calls on one workspace are ordered: they must not overlap). A call needs the zero region of its batch size B
+// (topk_zero_bytes(B): the barrier and status words, then B rows' top-k histograms) and leaves exactly that region
+// zero, writing anything past it; so a later call whose zero region reaches further first gets the difference
+// zero-filled (a fill kernel on its stream). A workspace the record does not hold (its first call, or one dropped
+// from the bounded record) gets its whole zero region filled, which is right whatever it holds. A record never
+// claims more than is zero: a caller zero-fills a workspace before its first use (so a new workspace at a recorded
+// address holds at least the recorded zeros), dsa_workspace_clear records what it clears, and a call that fails
+// drops its workspace's record.
+struct ZeroRecord {
+  int dev;
+  const void* ws;
+  size_t zero;
+};
+constexpr int kZeroRecords = 256;
+std::mutex g_zero_mu;
+ZeroRecord g_zero[kZeroRecords] = {};
+int g_zero_next = 0;  // the record replaced next when a new workspace arrives
+
+ZeroRecord* zero_record(int dev, const void* ws) {
+  for (ZeroRecord& r : g_zero)
+    if (r.ws == ws && r.dev == dev) return &r;
+  return nullptr;
+}
+
+// The first `need` bytes of ws zero for the call about to be enqueued on s, and recorded as the call's zero region.
+hipError_t ready_zero(void* ws, size_t need, hipStream_t s) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return hipErrorUnknown;
+  std::lock_guard<std::mutex> lock(g_zero_mu);
+  ZeroRecord* r = zero_record(dev, ws);
+  const size_t have = r ? r->zero : 0;
+  if (need > have) {
+    const hipError_t e = dsa::launch_fill_zero(static_cast<char*>(ws) + have, need - have, s);
+    if (e != hipSuccess) {
+      if (r) r->ws = nullptr;
+      return e;
+    }
+  }
+  if (!r) {
+    r = &g_zero[g_zero_next];
+    g_zero_next = (g_zero_next + 1) % kZeroRecords;
+    r->dev = dev;
+    r->ws = ws;
+  }
+  r->zero = need;
+  return hipSuccess;
+}
+
+// A call on ws failed: what it left is unknown, so its next call fills its whole zero region.
+void drop_zero(const void* ws) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return;
+  std::lock_guard<std::mutex> lock(g_zero_mu);
+  if (ZeroRecord* r = zero_record(dev, ws)) r->ws = nullptr;
+}
+
+// dsa_workspace_clear zeroed the first `bytes` of ws.
+void record_cleared(const void* ws, size_t bytes) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return;
+  std::lock_guard<std::mutex> lock(g_zero_mu);
+  if (ZeroRecord* r = zero_record(dev, ws)) r->zero = bytes;
+}
+
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
-size_t g_scratch_zero[kMaxDevices] = {};  // bytes from the scratch's start that are zero when the next call runs
 
-// The current device's scratch address, with its first zero_bytes at zero for the call about to run. On the first
-// call for a device (with that device current) the address is looked up and the whole array zero-filled on `stream`
-// (a fill kernel, ordered before the call that uses it). A call leaves the zero region of its own batch size at zero
-// and may write anything past it, so a later call with a larger zero region gets the difference filled first. Null
-// on a HIP error.
-void* noalloc_scratch(hipStream_t stream, size_t zero_bytes) {
+// The current device's allocation-free scratch address, looked up on the first call for a device (with that device
+// current); its zero region is kept like any workspace's (ready_zero). Null on a HIP error.
+void* noalloc_scratch() {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch_ptr[dev]) {
     void* ptr = nullptr;
     if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
-    if (dsa::launch_fill_zero(ptr, DSA_NOALLOC_SCRATCH_BYTES, stream) != hipSuccess) return nullptr;
     g_scratch_ptr[dev] = ptr;
-    g_scratch_zero[dev] = DSA_NOALLOC_SCRATCH_BYTES;
   }
-  uint8_t* p = static_cast<uint8_t*>(g_scratch_ptr[dev]);
-  const size_t z = g_scratch_zero[dev];
-  if (zero_bytes > z) {
-    if (dsa::launch_fill_zero(p + z, zero_bytes - z, stream) != hipSuccess) {
-      g_scratch_zero[dev] = 0;
-      return nullptr;
-    }
-  }
-  g_scratch_zero[dev] = zero_bytes;
-  return p;
+  return g_scratch_ptr[dev];
 }
 
 }  // namespace
@@ -493,14 +543,49 @@ int dsa_topk(const float* scores, const int32_t* len, int32_t* idx, int32_t* cnt
   const size_t need = dsa::topk_workspace_bytes(B, max_len, keep);
   if (!workspace || workspace_bytes < need) return DSA_EWORKSPACE;
   if (B == 0) return DSA_OK;
-  return status(dsa::launch_topk(scores, len, idx, cnt, workspace, B, score_stride, max_len, keep, vis_only ? 1 : 0,
-                                 false, nullptr, 0, 0, 0, nullptr,
-                                 static_cast<hipStream_t>(stream)));
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (ready_zero(workspace, dsa::topk_zero_bytes(B), s) != hipSuccess) return DSA_ELAUNCH;
+  const int st = status(dsa::launch_topk(scores, len, idx, cnt, workspace, B, score_stride, max_len, keep,
+                                         vis_only ? 1 : 0, false, nullptr, 0, 0, 0, nullptr, s));
+  if (st != DSA_OK) drop_zero(workspace);
+  return st;
+}
+
+int dsa_layer_status(void* workspace, int32_t* gave_up, int32_t* two_exchange, int clear, void* stream) {
+  if (!gave_up || !two_exchange) return DSA_EINVAL;
+  *gave_up = 0;
+  *two_exchange = 0;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  void* ws = workspace;
+  if (!ws) {
+    // the current device's allocation-free scratch; none yet: no call has run there
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return DSA_ELAUNCH;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    ws = g_scratch_ptr[dev];
+    if (!ws) return DSA_OK;
+  }
+  int32_t words[dsa::WS_SYNC_BYTES / 4];
+  if (hipMemcpyAsync(words, ws, sizeof(words), hipMemcpyDeviceToHost, s) != hipSuccess ||
+      hipStreamSynchronize(s) != hipSuccess)
+    return DSA_ELAUNCH;
+  for (int x = 0; x < 8; ++x) {
+    *gave_up += words[x * dsa::WS_SYNC_WORDS + dsa::WS_SYNC_GAVE_UP];
+    *two_exchange += words[x * dsa::WS_SYNC_WORDS + dsa::WS_SYNC_TWO_EXCHANGE];
+  }
+  if (clear) {
+    // between calls every other word of the block is zero
+    if (dsa::launch_fill_zero(ws, dsa::WS_SYNC_BYTES, s) != hipSuccess || hipStreamSynchronize(s) != hipSuccess)
+      return DSA_ELAUNCH;
+  }
+  return DSA_OK;
 }
 
 int dsa_workspace_clear(void* workspace, size_t workspace_bytes, void* stream) {
   if (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 15) || (workspace_bytes & 15)) return DSA_EINVAL;
-  return status(dsa::launch_fill_zero(workspace, workspace_bytes, static_cast<hipStream_t>(stream)));
+  const int st = status(dsa::launch_fill_zero(workspace, workspace_bytes, static_cast<hipStream_t>(stream)));
+  if (st == DSA_OK) record_cleared(workspace, workspace_bytes);
+  return st;
 }
 
 int dsa_topk_supported(int max_len, int keep, int vis_only) {
@@ -517,12 +602,16 @@ int dsa_topk_mask(const int32_t* idx, const int32_t* cnt, const float* scores, f
                                       static_cast<hipStream_t>(stream)));
 }
 
-int dsa_sparse_mla_decode(const void* q_bf16, const uint8_t* kv_fp8, const float* kv_scale, const int32_t* idx,
-                          const int32_t* cnt, const int32_t* page_table, const int32_t* rows, const float* bias,
-                          void* out_bf16, float* out_f32, float* lse, void* workspace, size_t workspace_bytes, int B,
-                          int H, int Dqk, int Dv, int keep, int max_pages, int page_size, int num_pages, float scale,
-                          int splits, void* stream) {
-  if (!q_bf16 || !kv_fp8 || !kv_scale || (!out_bf16 && !out_f32)) return DSA_EINVAL;
+}  // extern "C"
+
+// dsa_sparse_mla_decode with an optional run-time live-row count (n_live: null, or one int on the device; the rows at
+// or past it are left unwritten): dsa_sparse_mla_decode and dsa_sparse_mla_slots_n.
+static int sparse_mla_decode(const void* q_bf16, const uint8_t* kv_fp8, const float* kv_scale, const int32_t* idx,
+                             const int32_t* cnt, const int32_t* page_table, const int32_t* rows, const float* bias,
+                             const int32_t* n_live, void* out_bf16, float* out_f32, float* lse, void* workspace,
+                             size_t workspace_bytes, int B, int H, int Dqk, int Dv, int keep, int max_pages,
+                             int page_size, int num_pages, float scale, int splits, void* stream) {
+  if (!q_bf16 || !kv_fp8 || (!out_bf16 && !out_f32)) return DSA_EINVAL;
   const bool token_form = idx != nullptr;
   if (token_form == (rows != nullptr)) return DSA_EINVAL;  // exactly one slot form
   if (token_form && (!cnt || !page_table)) return DSA_EINVAL;
@@ -535,10 +624,36 @@ int dsa_sparse_mla_decode(const void* q_bf16, const uint8_t* kv_fp8, const float
   const size_t need = dsa::attention_workspace_bytes(B, H, sp);
   if (need && (!workspace || workspace_bytes < need)) return DSA_EWORKSPACE;
   const bool wide = sp == 1 && dsa::attention_wide_ok(B, H, keep, bias != nullptr, num_cu()) && (token_form || cnt);
+  dsa::PoolForm pf{};
+  pf.n_live = n_live;
   return status(dsa::launch_sparse_mla(static_cast<const uint16_t*>(q_bf16), kv_fp8, kv_scale, idx, cnt, page_table,
                                        rows, bias, static_cast<uint16_t*>(out_bf16), out_f32, lse, workspace, B, H,
                                        Dqk, keep, max_pages, page_size, num_pages, scale, sp,
-                                       static_cast<hipStream_t>(stream), dsa::PoolForm{}, wide));
+                                       static_cast<hipStream_t>(stream), pf, wide));
+}
+
+extern "C" {
+
+int dsa_sparse_mla_decode(const void* q_bf16, const uint8_t* kv_fp8, const float* kv_scale, const int32_t* idx,
+                          const int32_t* cnt, const int32_t* page_table, const int32_t* rows, const float* bias,
+                          void* out_bf16, float* out_f32, float* lse, void* workspace, size_t workspace_bytes, int B,
+                          int H, int Dqk, int Dv, int keep, int max_pages, int page_size, int num_pages, float scale,
+                          int splits, void* stream) {
+  return sparse_mla_decode(q_bf16, kv_fp8, kv_scale, idx, cnt, page_table, rows, bias, nullptr, out_bf16, out_f32,
+                           lse, workspace, workspace_bytes, B, H, Dqk, Dv, keep, max_pages, page_size, num_pages,
+                           scale, splits, stream);
+}
+
+int dsa_sparse_mla_slots_n(const void* q_bf16, const uint8_t* kv_fp8, const float* kv_scale, const int32_t* rows,
+                           const float* bias, const int32_t* n_live, void* out_bf16, float* out_f32, float* lse,
+                           void* workspace, size_t workspace_bytes, int N, int H, int Dqk, int keep,
+                           long long num_slots, float scale, int splits, void* stream) {
+  if (!rows || !bias || !n_live) return DSA_EINVAL;
+  if (num_slots < 1) return DSA_EINVAL;
+  if (num_slots > 0x7fffffffLL) return DSA_EUNSUPPORTED;
+  return sparse_mla_decode(q_bf16, kv_fp8, kv_scale, nullptr, nullptr, nullptr, rows, bias, n_live, out_bf16, out_f32,
+                           lse, workspace, workspace_bytes, N, H, Dqk, 512, keep, 1, 1, (int)num_slots, scale, splits,
+                           stream);
 }
 
 int dsa_compact_mask(const float* sel, int N, int M, int keep, int64_t* idx, int64_t* cnt, void* stream) {
@@ -567,7 +682,7 @@ int dsa_sparse_mla_slots_compact(const void* q_bf16, const uint8_t* kv_fp8, cons
                                  const int32_t* rows, const float* bias, void* out_bf16, float* out_f32, float* lse,
                                  void* workspace, size_t workspace_bytes, int B, int H, int Dqk, int NS, int kp,
                                  long long num_slots, float scale, int splits, void* stream) {
-  if (!q_bf16 || !kv_fp8 || !kv_scale || !rows || !bias || (!out_bf16 && !out_f32)) return DSA_EINVAL;
+  if (!q_bf16 || !kv_fp8 || !rows || !bias || (!out_bf16 && !out_f32)) return DSA_EINVAL;
   if (B < 0 || H < 1 || NS < 1 || kp < 1 || num_slots < kp || num_slots % kp) return DSA_EINVAL;
   if ((Dqk != 576 && Dqk != 512) || H % 16) return DSA_EUNSUPPORTED;
   if (num_slots > 0x7fffffffL || (long long)NS * kp > 0x7fffffffL) return DSA_EUNSUPPORTED;
@@ -640,22 +755,36 @@ int dsa_default_splits(int B, int H, int keep) {
   return effective_splits(resolve_splits(0, B, H, keep), keep);
 }
 
-// The decode layer's checks, shared by both forms (every check before the first launch: a rejected call writes
-// nothing).
+static int layer_chain(const void* q_idx_bf16, const float* w, const uint8_t* k_fp8, const float* k_scale,
+                       const void* q_bf16, const uint8_t* kv_fp8, const float* kv_scale, const int32_t* page_table,
+                       const int32_t* ctx_len, float* scores, int32_t* idx, int32_t* cnt, void* out_bf16, float* lse,
+                       void* workspace, size_t workspace_bytes, int B, int Hi, int H, int max_pages, int page_size,
+                       int num_pages, int score_stride, int max_len, int keep, float scale, int splits,
+                       void* stream);
+
+static int pooled_layer(const void* q_idx_bf16, const float* w, const void* pool_key_bf16, const void* q_bf16,
+                        const uint8_t* kv_fp8, const float* kv_scale, const int32_t* page_table, const int32_t* npool,
+                        const int32_t* positions, float* scores, int32_t* pools, int32_t* cnt, void* out_bf16,
+                        float* lse, void* workspace, int B, int Hi, int H, int Dqk, int max_pages, int page_size,
+                        int num_pages, int kp, int keep, float scale, int splits, int stride, hipStream_t s);
+// The decode layer's checks, shared by its forms (every check before the first launch: a rejected call writes
+// nothing); need_ws: the caller passes a workspace (the allocation-free form checks its scratch's size itself).
 static int layer_checks(const void* q_idx_bf16, const float* w, const uint8_t* k_fp8, const float* k_scale,
                         const void* q_bf16, const uint8_t* kv_fp8, const float* kv_scale, const int32_t* page_table,
                         const int32_t* ctx_len, float* scores, int32_t* idx, int32_t* cnt, void* out_bf16,
                         void* workspace, size_t workspace_bytes, int B, int Hi, int H, int max_pages, int page_size,
-                        int num_pages, int score_stride, int max_len, int keep, int splits) {
-  if (!q_idx_bf16 || !w || !k_fp8 || !k_scale || !page_table || !ctx_len || !scores || !idx || !cnt || !workspace)
+                        int num_pages, int score_stride, int max_len, int keep, int splits, bool need_ws = true) {
+  if (!q_idx_bf16 || !w || !k_fp8 || !k_scale || !page_table || !ctx_len || !scores || !idx || !cnt)
     return DSA_EINVAL;
-  if (!q_bf16 || !kv_fp8 || !kv_scale || !out_bf16) return DSA_EINVAL;
+  if (need_ws && !workspace) return DSA_EINVAL;
+  if (!q_bf16 || !kv_fp8 || !out_bf16) return DSA_EINVAL;
   if (B < 0 || Hi < 1 || H < 1 || max_pages < 1 || page_size < 1 || num_pages < 1 || keep < 1) return DSA_EINVAL;
   if (max_len < 1 || max_len > score_stride || (long)score_stride > (long)max_pages * page_size) return DSA_EINVAL;
   if (Hi > 64 || page_size % 32 || H % 16) return DSA_EUNSUPPORTED;
   if ((long)num_pages * page_size > 0x7fffffffL) return DSA_EUNSUPPORTED;
   if (!dsa::topk_supported(max_len, keep, 1)) return DSA_EUNSUPPORTED;
-  if (workspace_bytes < dsa_workspace_bytes(DSA_WS_LAYER, B, H, keep, max_len, splits)) return DSA_EWORKSPACE;
+  if (need_ws && workspace_bytes < dsa_workspace_bytes(DSA_WS_LAYER, B, H, keep, max_len, splits))
+    return DSA_EWORKSPACE;
   return DSA_OK;
 }
 
@@ -672,11 +801,14 @@ int dsa_decode_layer(const void* q_idx_bf16, const float* w, const uint8_t* k_fp
     return dsa_decode_layer_chain(q_idx_bf16, w, k_fp8, k_scale, q_bf16, kv_fp8, kv_scale, page_table, ctx_len,
                                   scores, idx, cnt, out_bf16, lse, workspace, workspace_bytes, B, Hi, H, max_pages,
                                   page_size, num_pages, score_stride, max_len, keep, scale, splits, stream);
-  return status(dsa::launch_decode_fused(
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (ready_zero(workspace, dsa::topk_zero_bytes(B), s) != hipSuccess) return DSA_ELAUNCH;
+  const int r = status(dsa::launch_decode_fused(
       static_cast<const uint16_t*>(q_idx_bf16), w, k_fp8, k_scale, static_cast<const uint16_t*>(q_bf16), kv_fp8,
       kv_scale, page_table, ctx_len, scores, idx, cnt, static_cast<uint16_t*>(out_bf16), lse, workspace,
-      dsa::topk_hist_bytes(B), dsa::topk_zero_bytes(B), B, Hi, H, max_pages, page_size, num_pages, score_stride, keep,
-      scale, static_cast<hipStream_t>(stream)));
+      dsa::topk_zero_bytes(B), B, Hi, H, max_pages, page_size, num_pages, score_stride, keep, scale, s));
+  if (r != DSA_OK) drop_zero(workspace);
+  return r;
 }
 
 int dsa_decode_layer_chain(const void* q_idx_bf16, const float* w, const uint8_t* k_fp8, const float* k_scale,
@@ -690,6 +822,24 @@ int dsa_decode_layer_chain(const void* q_idx_bf16, const float* w, const uint8_t
                               num_pages, score_stride, max_len, keep, splits);
   if (st != DSA_OK || B == 0) return st;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (ready_zero(workspace, dsa::topk_zero_bytes(B), s) != hipSuccess) return DSA_ELAUNCH;
+  const int r = layer_chain(q_idx_bf16, w, k_fp8, k_scale, q_bf16, kv_fp8, kv_scale, page_table, ctx_len, scores, idx,
+                            cnt, out_bf16, lse, workspace, workspace_bytes, B, Hi, H, max_pages, page_size, num_pages,
+                            score_stride, max_len, keep, scale, splits, stream);
+  if (r != DSA_OK) drop_zero(workspace);
+  return r;
+}
+
+}  // extern "C"
+
+// The separate kernels of dsa_decode_layer_chain, after its checks and with the workspace's zero region ready.
+static int layer_chain(const void* q_idx_bf16, const float* w, const uint8_t* k_fp8, const float* k_scale,
+                       const void* q_bf16, const uint8_t* kv_fp8, const float* kv_scale, const int32_t* page_table,
+                       const int32_t* ctx_len, float* scores, int32_t* idx, int32_t* cnt, void* out_bf16, float* lse,
+                       void* workspace, size_t workspace_bytes, int B, int Hi, int H, int max_pages, int page_size,
+                       int num_pages, int score_stride, int max_len, int keep, float scale, int splits,
+                       void* stream) {
+  hipStream_t s = static_cast<hipStream_t>(stream);
   const size_t t_need = align256(dsa::topk_workspace_bytes(B, max_len, keep));
   // the indexer accumulates the top-k's first-level histogram (the workspace's first region): flat rows, and a few
   // long rows (the long selection; the long-row indexer); otherwise long rows take the two-level selection, the
@@ -699,7 +849,7 @@ int dsa_decode_layer_chain(const void* q_idx_bf16, const float* w, const uint8_t
   const bool fused_hist = flat || long_sel;
   const int sub = fused_hist ? 0 : dsa::topk_two_level_sub(max_len, keep);
   const bool fused_bm = sub >= 2 && sub <= 32;
-  int* hist = fused_hist ? static_cast<int*>(workspace) : nullptr;
+  int* hist = fused_hist ? dsa::ws_hist(workspace) : nullptr;
   hipError_t e;
   if (flat)
     e = dsa::launch_indexer_decode(static_cast<const uint16_t*>(q_idx_bf16), w, k_fp8, k_scale, page_table, ctx_len,
@@ -712,7 +862,7 @@ int dsa_decode_layer_chain(const void* q_idx_bf16, const float* w, const uint8_t
                                         fused_bm ? (max_len + sub - 1) / sub : 0, hist, B, Hi, max_pages, page_size,
                                         num_pages, score_stride, num_cu(), s);
   if (e != hipSuccess) {
-    if (hist) dsa::launch_fill_zero(workspace, dsa::topk_hist_bytes(B), s);  // a partial histogram may be in
+    if (hist) dsa::launch_fill_zero(hist, dsa::topk_hist_bytes(B), s);  // a partial histogram may be in
     return DSA_ELAUNCH;
   }
   // with the histogram from the indexer the top-k also resolves the selected positions to cache slots, so the
@@ -723,7 +873,7 @@ int dsa_decode_layer_chain(const void* q_idx_bf16, const float* w, const uint8_t
   if (e != hipSuccess) {
     // the indexer has added into the histograms, which the top-k would have cleared: clear them here, so that the
     // workspace stays usable (if this launch fails too, dsa_workspace_clear must run before the next call)
-    dsa::launch_fill_zero(workspace, dsa::topk_hist_bytes(B), s);
+    dsa::launch_fill_zero(dsa::ws_hist(workspace), dsa::topk_hist_bytes(B), s);
     return DSA_ELAUNCH;
   }
   char* aws = static_cast<char*>(workspace) + t_need + layer_rows_bytes(B, keep);
@@ -733,9 +883,8 @@ int dsa_decode_layer_chain(const void* q_idx_bf16, const float* w, const uint8_t
   if (splits == 0 && dsa::attend_xcd_ok(num_cu(), H, keep))
     return status(dsa::launch_decode_attend(static_cast<const uint16_t*>(q_bf16), kv_fp8, kv_scale, rows,
                                             rows ? nullptr : idx, page_table, cnt, static_cast<uint16_t*>(out_bf16),
-                                            lse, aws, reinterpret_cast<int*>(static_cast<char*>(workspace) +
-                                                                             dsa::topk_hist_bytes(B)),
-                                            B, H, max_pages, page_size, num_pages, keep, scale, s));
+                                            lse, aws, static_cast<int*>(workspace), B, H, max_pages, page_size,
+                                            num_pages, keep, scale, s));
   if (!rows)
     return dsa_sparse_mla_decode(q_bf16, kv_fp8, kv_scale, idx, cnt, page_table, nullptr, nullptr, out_bf16, nullptr,
                                  lse, aws, aws_bytes, B, H, 576, 512, keep, max_pages, page_size, num_pages, scale,
@@ -746,18 +895,24 @@ int dsa_decode_layer_chain(const void* q_idx_bf16, const float* w, const uint8_t
                                        keep, max_pages, page_size, num_pages, scale, sp, s));
 }
 
+extern "C" {
+
 int dsa_decode_layer_noalloc(const void* q_idx_bf16, const float* w, const uint8_t* k_fp8, const float* k_scale,
                              const void* q_bf16, const uint8_t* kv_fp8, const float* kv_scale,
                              const int32_t* page_table, const int32_t* ctx_len, float* scores, int32_t* idx,
                              int32_t* cnt, void* out_bf16, float* lse, int B, int Hi, int H, int max_pages,
                              int page_size, int num_pages, int score_stride, int max_len, int keep, float scale,
                              int splits, void* stream) {
-  // the size checks first (no HIP call for a refused size): the layer's workspace must fit the scratch
-  if (B < 0 || H < 1 || keep < 1 || max_len < 1) return DSA_EINVAL;
+  // every check first (no HIP call, no fill enqueued, for a refused call): the layer's own, then its workspace
+  // against the scratch
+  const int st = layer_checks(q_idx_bf16, w, k_fp8, k_scale, q_bf16, kv_fp8, kv_scale, page_table, ctx_len, scores,
+                              idx, cnt, out_bf16, nullptr, 0, B, Hi, H, max_pages, page_size, num_pages, score_stride,
+                              max_len, keep, splits, false);
+  if (st != DSA_OK) return st;
   const size_t need = dsa_workspace_bytes(DSA_WS_LAYER, B, H, keep, max_len, splits);
   if (need == 0 || need > DSA_NOALLOC_SCRATCH_BYTES) return DSA_ESCRATCH;
   if (B == 0) return DSA_OK;
-  void* ws = noalloc_scratch(static_cast<hipStream_t>(stream), dsa::topk_zero_bytes(B));
+  void* ws = noalloc_scratch();
   if (!ws) return DSA_ELAUNCH;
   return dsa_decode_layer(q_idx_bf16, w, k_fp8, k_scale, q_bf16, kv_fp8, kv_scale, page_table, ctx_len, scores, idx,
                           cnt, out_bf16, lse, ws, DSA_NOALLOC_SCRATCH_BYTES, B, Hi, H, max_pages, page_size,
@@ -776,7 +931,7 @@ int dsa_sparse_mla_pooled(const void* q_bf16, const uint8_t* kv_fp8, const float
                           void* out_bf16, float* out_f32, float* lse, void* workspace, size_t workspace_bytes, int B,
                           int H, int Dqk, int keep, int kp, int max_pages, int page_size, int num_pages, float scale,
                           int splits, void* stream) {
-  if (!q_bf16 || !kv_fp8 || !kv_scale || !pools || !cnt || !npool || !positions || !page_table) return DSA_EINVAL;
+  if (!q_bf16 || !kv_fp8 || !pools || !cnt || !npool || !positions || !page_table) return DSA_EINVAL;
   if (!out_bf16 && !out_f32) return DSA_EINVAL;
   if (B < 0 || H < 1 || keep < 1 || max_pages < 1 || page_size < 1 || num_pages < 1) return DSA_EINVAL;
   if (kp < 2 || kp > 8 || (kp & (kp - 1)) || page_size % kp) return DSA_EUNSUPPORTED;
@@ -812,7 +967,7 @@ int dsa_pooled_decode_layer(const void* q_idx_bf16, const float* w, const void* 
                             int32_t* cnt, void* out_bf16, float* lse, void* workspace, size_t workspace_bytes, int B,
                             int Hi, int H, int Dqk, int max_pages, int page_size, int num_pages, int kp, int keep,
                             float scale, int splits, void* stream) {
-  if (!q_idx_bf16 || !w || !pool_key_bf16 || !q_bf16 || !kv_fp8 || !kv_scale || !page_table || !npool ||
+  if (!q_idx_bf16 || !w || !pool_key_bf16 || !q_bf16 || !kv_fp8 || !page_table || !npool ||
       !positions || !scores || !pools || !cnt || !out_bf16 || !workspace)
     return DSA_EINVAL;
   if (B < 0 || Hi < 1 || H < 1 || max_pages < 1 || page_size < 1 || num_pages < 1 || keep < 1) return DSA_EINVAL;
@@ -826,31 +981,47 @@ int dsa_pooled_decode_layer(const void* q_idx_bf16, const float* w, const void* 
   if (workspace_bytes < dsa_pooled_workspace_bytes(B, H, keep, stride, kp, splits)) return DSA_EWORKSPACE;
   if (B == 0) return DSA_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (ready_zero(workspace, dsa::topk_zero_bytes(B), s) != hipSuccess) return DSA_ELAUNCH;
+  const int r = pooled_layer(q_idx_bf16, w, pool_key_bf16, q_bf16, kv_fp8, kv_scale, page_table, npool, positions,
+                             scores, pools, cnt, out_bf16, lse, workspace, B, Hi, H, Dqk, max_pages, page_size,
+                             num_pages, kp, keep, scale, splits, stride, s);
+  if (r != DSA_OK) drop_zero(workspace);
+  return r;
+}
+
+}  // extern "C"
+
+// The kernels of dsa_pooled_decode_layer, after its checks and with the workspace's zero region ready.
+static int pooled_layer(const void* q_idx_bf16, const float* w, const void* pool_key_bf16, const void* q_bf16,
+                        const uint8_t* kv_fp8, const float* kv_scale, const int32_t* page_table, const int32_t* npool,
+                        const int32_t* positions, float* scores, int32_t* pools, int32_t* cnt, void* out_bf16,
+                        float* lse, void* workspace, int B, int Hi, int H, int Dqk, int max_pages, int page_size,
+                        int num_pages, int kp, int keep, float scale, int splits, int stride, hipStream_t s) {
+  const int ppp = page_size / kp;  // pools per page
   const size_t t_need = align256(dsa::topk_workspace_bytes(B, stride, keep));
   // flat rows: the indexer accumulates the top-k's first-level histogram (the workspace's first region)
   const bool fused_hist = stride <= 32 * 1024;
   hipError_t e = dsa::launch_indexer_decode_bf16(static_cast<const uint16_t*>(q_idx_bf16), w,
                                                  static_cast<const uint16_t*>(pool_key_bf16), page_table, npool,
-                                                 nullptr, scores, fused_hist ? static_cast<int*>(workspace) : nullptr,
+                                                 nullptr, scores, fused_hist ? dsa::ws_hist(workspace) : nullptr,
                                                  B, Hi, max_pages, ppp, num_pages, stride, s);
   if (e != hipSuccess) return DSA_ELAUNCH;
   e = dsa::launch_topk(scores, npool, pools, cnt, workspace, B, stride, stride, keep, 1, fused_hist, nullptr, 0, 0, 0,
                        nullptr, s);
   if (e != hipSuccess) {
     // the histograms the indexer added into stay zero for the next call (as in dsa_decode_layer)
-    dsa::launch_fill_zero(workspace, dsa::topk_hist_bytes(B), s);
+    dsa::launch_fill_zero(dsa::ws_hist(workspace), dsa::topk_hist_bytes(B), s);
     return DSA_ELAUNCH;
   }
   const int keep_sel = kp * keep;  // the selected pools' token slots; the tail comes on top
   // the default split count on a GPU of 8 XCDs x 32 CUs, 512-wide rows: the attention and combine in one XCD-local
   // launch (the separate kernels' form of the one-launch layer's last stages), the tail in the split of the last
-  // selected token; the barrier words follow the histograms in the zero region
+  // selected token; the barrier words are the workspace's first bytes
   if (splits == 0 && dsa::attend_xcd_pooled_ok(num_cu(), H, Dqk, keep_sel))
     return status(dsa::launch_decode_attend_pooled(
         static_cast<const uint16_t*>(q_bf16), kv_fp8, kv_scale, pools, cnt, npool, positions, page_table,
-        static_cast<uint16_t*>(out_bf16), lse, static_cast<char*>(workspace) + t_need,
-        reinterpret_cast<int*>(static_cast<char*>(workspace) + dsa::topk_hist_bytes(B)), B, H, max_pages, page_size,
-        num_pages, keep, __builtin_ctz((unsigned)kp), scale, s));
+        static_cast<uint16_t*>(out_bf16), lse, static_cast<char*>(workspace) + t_need, static_cast<int*>(workspace), B,
+        H, max_pages, page_size, num_pages, keep, __builtin_ctz((unsigned)kp), scale, s));
   const int sp = effective_splits(resolve_splits(splits, B, H, keep_sel), keep_sel);
   const dsa::PoolForm pf = {__builtin_ctz((unsigned)kp), keep, npool, positions, 0};
   return status(dsa::launch_sparse_mla(static_cast<const uint16_t*>(q_bf16), kv_fp8, kv_scale, pools, cnt, page_table,
@@ -858,5 +1029,3 @@ int dsa_pooled_decode_layer(const void* q_idx_bf16, const float* w, const void* 
                                        static_cast<char*>(workspace) + t_need, B, H, Dqk, keep_sel, max_pages,
                                        page_size, num_pages, scale, sp, s, pf));
 }
-
-}  // extern "C"

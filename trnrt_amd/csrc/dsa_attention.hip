@@ -99,6 +99,7 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void sparse_mla_kernel(
   const int gi = blk * 8 + (rem - hg * 8);
   if (gi >= groups) return;
   const int b = gi / splits, sp = gi - b * splits;
+  if (pf.n_live && b >= *pf.n_live) return;  // a row past the run-time live count: left unwritten
 
   const int tid = threadIdx.x, wave = tid / WAVE, lane = tid & (WAVE - 1);
   const int half = wave >> 2, wh = wave & 3;  // the half (alternate chunks) and the wave within it
@@ -314,8 +315,9 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void sparse_mla_kernel(
         __builtin_amdgcn_global_load_lds(kv + (size_t)sh.tslot[u / ATT_PIECES] * DQK + 16 * (u % ATT_PIECES),
                                          (__attribute__((address_space(3))) void*)&sh.trows[1024 * wave], 16, 0, 0);
     }
-    const float ksc = tid < ATT_SUPER ? kvs[sh.slot[tid < nslots ? tid : 0]]
-                                      : (tail_thread ? kvs[sh.tslot[tid - ATT_SUPER]] : 0.0f);
+    // (kvs null: the reference's unscaled cache, scale 1)
+    const float ksc = tid < ATT_SUPER ? (kvs ? kvs[sh.slot[tid < nslots ? tid : 0]] : 1.0f)
+                                      : (tail_thread ? (kvs ? kvs[sh.tslot[tid - ATT_SUPER]] : 1.0f) : 0.0f);
     __builtin_amdgcn_s_waitcnt(0);  // this thread's rows are in LDS
     if (tid < ATT_SUPER)
       sh.kscale[tid] = ksc;
@@ -499,6 +501,7 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void sparse_mla_wide_kernel(
   __shared__ AttWideShared sh;
   const int HB = H / AW_HEADS;
   const int b = blockIdx.x / HB, hb64 = blockIdx.x - b * HB;
+  if (pf.n_live && b >= *pf.n_live) return;  // a row past the run-time live count: left unwritten
   const int tid = threadIdx.x, wave = tid / WAVE, lane = tid & (WAVE - 1);
   const int hg = wave & 3, th = wave >> 2;
   const int l16 = lane & 15, q4 = lane >> 4;
@@ -550,7 +553,7 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void sparse_mla_wide_kernel(
   }
   float ksc_r[SPT];
 #pragma unroll
-  for (int i = 0; i < SPT; ++i) ksc_r[i] = kvs[slot_r[i]];
+  for (int i = 0; i < SPT; ++i) ksc_r[i] = kvs ? kvs[slot_r[i]] : 1.0f;  // null: the unscaled cache
   uint16_t* qs = reinterpret_cast<uint16_t*>(&sh.kt[0][0]);
 #pragma unroll
   for (int i = 0; i < QPT; ++i) {
@@ -755,9 +758,11 @@ template <int S>
 __global__ __launch_bounds__(128) void combine_splits_kernel(const float* __restrict__ ws_o,
                                                              const float* __restrict__ ws_ml, int H, int splits,
                                                              uint16_t* __restrict__ out, float* __restrict__ out_f32,
-                                                             float* __restrict__ lse_out) {
+                                                             float* __restrict__ lse_out,
+                                                             const int* __restrict__ n_live) {
   const int bh = blockIdx.x;
   const int b = bh / H, head = bh - b * H;
+  if (n_live && b >= *n_live) return;  // a row past the run-time live count: left unwritten
   const int d = 4 * threadIdx.x;
   float2 ml[S];
   float4 v[S];
@@ -909,12 +914,12 @@ hipError_t launch_sparse_mla(const uint16_t* q, const uint8_t* kv, const float* 
   if (e != hipSuccess || eff_splits == 1) return e;
   if (eff_splits <= 8)
     return launch("combine_splits_kernel", combine_splits_kernel<8>, dim3(B * H), dim3(128), s, ws_o, ws_ml, H,
-                  eff_splits, out, out_f32, lse);
+                  eff_splits, out, out_f32, lse, pf.n_live);
   if (eff_splits <= 16)
     return launch("combine_splits_kernel", combine_splits_kernel<16>, dim3(B * H), dim3(128), s, ws_o, ws_ml, H,
-                  eff_splits, out, out_f32, lse);
+                  eff_splits, out, out_f32, lse, pf.n_live);
   return launch("combine_splits_kernel", combine_splits_kernel<32>, dim3(B * H), dim3(128), s, ws_o, ws_ml, H,
-                eff_splits, out, out_f32, lse);
+                eff_splits, out, out_f32, lse, pf.n_live);
 }
 
 hipError_t launch_token_rows(const int* idx, const int* cnt, const int* table, int* rows, float* bias, int B,

@@ -64,12 +64,23 @@ struct PoolForm {
   const int* npool;
   const int* positions;
   int tail_apart;
-  int empty_n;  // rows + cnt form: the masked slots a row with cnt 0 attends (0: one)
+  int empty_n;         // rows + cnt form: the masked slots a row with cnt 0 attends (0: one)
+  const int* n_live;   // null, or one int on the device: rows at or past it are neither computed nor written
 };
 constexpr int HIST_REPLICAS = 1;
-// Bytes after the histograms that a workspace keeps at zero between calls: the fused decode layer's per-XCD barrier
-// words (the separate kernels never touch them).
+// The first bytes of every decode workspace, at the same offset whatever the batch size: per XCD (8 x 16 words) the
+// XCD-local barriers' arrival and exit counters (zero between calls), then two status words that persist across
+// calls until dsa_layer_status clears them: the count of barrier waits that gave up, and the count of rows that took
+// the one-launch layer's two-exchange selection. The top-k histograms (zero between calls) follow.
 constexpr int WS_SYNC_BYTES = 1024;
+constexpr int WS_SYNC_WORDS = 16;  // per XCD
+constexpr int WS_SYNC_GAVE_UP = 2;
+constexpr int WS_SYNC_TWO_EXCHANGE = 3;
+
+// The top-k histograms of a workspace (past the barrier and status words).
+__host__ __device__ inline int* ws_hist(void* ws) {
+  return reinterpret_cast<int*>(static_cast<char*>(ws) + WS_SYNC_BYTES);
+}
 
 // s_waitcnt's immediate for "vector memory count <= n" (expcnt and lgkmcnt left at their maxima, no wait)
 __host__ __device__ constexpr int vmcnt_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }

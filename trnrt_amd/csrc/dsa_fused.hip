@@ -91,7 +91,6 @@ constexpr int FU_KROW = 16 * FU_KPIECES;
 constexpr int FU_STEPS = FU_DQK / 32;   // score steps
 constexpr int FU_AQROW = FU_DQK + 8;    // staged attention query row (bf16)
 constexpr unsigned FU_SPIN = 1u << 20;  // polls before a wait gives up (a normal wait takes a few)
-constexpr int FU_SYNC_WORDS = 16;       // per XCD: arrivals, exits, error flag
 
 // LDS (160 KiB, one workgroup per CU), phase by phase:
 constexpr int L_STATE = 0;       // FuState: selection results (stage 3)
@@ -178,8 +177,9 @@ struct FusedArgs {
   uint16_t* out;
   float* lse;
   uint32_t* hl;    // [B][32][1056]: per workgroup its histogram's nonzero bins (count, then (bin << 16) | count)
-  int* sync;       // [8][16]: per XCD the barrier arrivals and exits (zero between calls), an error flag (a wait
-                   // gave up) and the count of rows that took the two-exchange selection
+  int* sync;       // [8][16] at the workspace's start: per XCD the barrier arrivals and exits (zero between calls),
+                   // the count of waits that gave up and of rows that took the two-exchange selection (kept until
+                   // dsa_layer_status clears them)
   uint32_t* cand;  // [B][32][1088]: per workgroup (keys above c0) << 16 | (candidates), the bitmap of its positions
                    // above c0 (32 words), then the candidates, (low 20 key bits << 10) | position in the workgroup's
                    // range, in position order
@@ -218,7 +218,10 @@ constexpr int FU_AUX_PLAIN = 0;  // the cache-policy operand of the loads of a p
 
 // XCD-local barrier of the 32 workgroups of an XCD: every thread's stores complete (drained memory counter), then the
 // workgroup's arrival (one atomic add) and a bounded poll. The XCD's counter is zero at a launch's start (the last
-// workgroup to finish resets it), so the n-th barrier of a launch completes at 32 n arrivals.
+// workgroup to finish resets it), so the n-th barrier of a launch completes at 32 n arrivals. A wait that gives up
+// (all 32 workgroups must be resident at once: another kernel holding CUs for the whole poll budget, about a second,
+// breaks that) counts itself in the XCD's status word and goes on; every read of a peer's data below stays inside
+// its region whatever that data holds, so such a call ends normally, and dsa_layer_status reports it.
 __device__ __forceinline__ void fu_barrier(int* sync, int n) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -229,7 +232,7 @@ __device__ __forceinline__ void fu_barrier(int* sync, int n) {
     unsigned polls = 0;
     while ((int)(__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - target) < 0) {
       if (++polls > FU_SPIN) {
-        __hip_atomic_fetch_or(sync + 2, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(sync + WS_SYNC_GAVE_UP, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         break;
       }
       __builtin_amdgcn_s_sleep(1);
@@ -541,16 +544,16 @@ __device__ __forceinline__ void fu_classify(const FusedArgs& a, uint8_t* lds, in
   {
     const int w = tid >> 4, q = tid & 15;  // list w's entries q, q + 16, ...
     const uint32_t* lw = hls + FU_HSTAGE * w;
-    const int n = (int)lw[0];
+    const int n = min((int)lw[0], FU_KEYS);  // (bounded: a list read after a wait that gave up may be stale)
     uint32_t v[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] = lw[1 + q + 16 * i];  // within the staged 256 words
 #pragma unroll
     for (int i = 0; i < 8; ++i)
-      if (q + 16 * i < n) atomicAdd(&rh[v[i] >> 16], (int)(v[i] & 0xFFFFu));
+      if (q + 16 * i < n) atomicAdd(&rh[(v[i] >> 16) & (FU_HBINS - 1)], (int)(v[i] & 0xFFFFu));
     for (int e = q + 128; e < n; e += 16) {
       const uint32_t x = e + 1 < FU_HSTAGE ? lw[1 + e] : hlg[(size_t)w * FU_HROW + 1 + e];
-      atomicAdd(&rh[x >> 16], (int)(x & 0xFFFFu));
+      atomicAdd(&rh[(x >> 16) & (FU_HBINS - 1)], (int)(x & 0xFFFFu));
     }
   }
   __syncthreads();
@@ -728,7 +731,7 @@ __device__ __forceinline__ int fu_select(const FusedArgs& a, uint8_t* lds, int b
   // thread (w, q) = (tid / 16, tid % 16): block w's bitmap words 2 q, 2 q + 1 and its candidates q, q + 16, ...
   const int w = tid >> 4, q = tid & 15;
   const uint32_t* cw = cb + FU_CSTAGE * w;
-  const int nc = (int)(cw[0] & 0xFFFFu);
+  const int nc = min((int)(cw[0] & 0xFFFFu), FU_KEYS);  // (bounded, as the bin lists above)
   sb[FU_BMW * w + 2 * q] = cw[1 + 2 * q];
   sb[FU_BMW * w + 2 * q + 1] = cw[2 + 2 * q];
   auto cand_at = [&](int e) __attribute__((always_inline)) {
@@ -931,7 +934,7 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
   } else if (q < FU_LBINS / 2) {
 #pragma unroll
     for (int k = 0; k < 2; ++k)
-      if (hp[k] != 0u && (hp[k] >> 16) >= hw1) atomicAdd(&bins0[hp[k] >> 16], (int)(hp[k] & 0xFFFFu));
+      if (hp[k] != 0u && (hp[k] >> 16) >= hw1) atomicAdd(&bins0[(hp[k] >> 16) & 4095u], (int)(hp[k] & 0xFFFFu));
   }
   fresh();
   if (q == 0) st.lbin[w] = (int)hw1;
@@ -1104,7 +1107,7 @@ __device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int 
       }
     }
   }
-  const float ksv = tid < padded ? a.kvs[slot] : 0.0f;
+  const float ksv = tid < padded ? (a.kvs ? a.kvs[slot] : 1.0f) : 0.0f;  // kvs null: the unscaled cache
   __builtin_amdgcn_s_waitcnt(0);
   if (tid < padded) {
     ksc_l[tid] = ksv;
@@ -1320,7 +1323,7 @@ template <int MT, int HPW>
 __global__ __launch_bounds__(FU_THREADS, 1) void decode_fused_kernel(FusedArgs a) {
   __shared__ __align__(16) uint8_t lds[FU_LDS];
   const int x = blockIdx.x % FU_XCDS, j = blockIdx.x / FU_XCDS;
-  int* sync = a.sync + x * FU_SYNC_WORDS;
+  int* sync = a.sync + x * WS_SYNC_WORDS;
   // one row per XCD and launch (rows row0 + x; a batch of more than 8 rows takes several launches, which keeps
   // each workgroup's per-lane address arithmetic out of a loop over rows, where it would be held in registers)
   const int b = a.row0 + x;
@@ -1348,7 +1351,7 @@ __global__ __launch_bounds__(FU_THREADS, 1) void decode_fused_kernel(FusedArgs a
   fu_combine(a, lds, b, j);
   // the count of rows that took the two-exchange selection (here, where no later wait is held up by its round trip)
   if (nbar == 3 && j == 0 && threadIdx.x == 0)
-    __hip_atomic_fetch_add(sync + 3, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_fetch_add(sync + WS_SYNC_TWO_EXCHANGE, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   fu_exit(sync);
 }
 
@@ -1441,7 +1444,7 @@ template <int HPW, int DQK = FU_DQK, bool XT = false>
 __global__ __launch_bounds__(FU_THREADS, 1) void decode_attend_kernel(FusedArgs a, const int* rows, int rpl) {
   __shared__ __align__(16) uint8_t lds[FU_LDS];
   const int x = blockIdx.x % FU_XCDS, j = blockIdx.x / FU_XCDS;
-  int* sync = a.sync + x * FU_SYNC_WORDS;
+  int* sync = a.sync + x * WS_SYNC_WORDS;
   if (a.row0 + x >= a.B) return;  // an XCD without a row
   const int nr = min(rpl, (a.B - a.row0 - x + FU_XCDS - 1) / FU_XCDS);  // this XCD's rows
   for (int r = 0; r < nr; ++r) {
@@ -1602,8 +1605,8 @@ hipError_t launch_decode_attend_pooled(const uint16_t* q, const uint8_t* kv, con
 hipError_t launch_decode_fused(const uint16_t* q_idx, const float* w, const uint8_t* k, const float* ks,
                                const uint16_t* q, const uint8_t* kv, const float* kvs, const int* table,
                                const int* ctx_len, float* scores, int* idx, int* cnt, uint16_t* out, float* lse,
-                               void* ws, size_t hist_bytes, size_t zero_bytes, int B, int Hi, int H, int max_pages,
-                               int page_size, int num_pages, int stride, int keep, float scale, hipStream_t s) {
+                               void* ws, size_t zero_bytes, int B, int Hi, int H, int max_pages, int page_size,
+                               int num_pages, int stride, int keep, float scale, hipStream_t s) {
   FusedArgs a;
   const int hpw = fused_hpw(H, keep);
   if (!hpw) return hipErrorInvalidValue;
@@ -1625,7 +1628,7 @@ hipError_t launch_decode_fused(const uint16_t* q_idx, const float* w, const uint
   a.out = out;
   a.lse = lse;
   a.hl = reinterpret_cast<uint32_t*>(p + l.hl);
-  a.sync = reinterpret_cast<int*>(p + hist_bytes);
+  a.sync = reinterpret_cast<int*>(p);  // the workspace's first bytes
   a.cand = reinterpret_cast<uint32_t*>(p + l.cand);
   a.lst = reinterpret_cast<uint32_t*>(p + l.lst);
   a.part = reinterpret_cast<uint16_t*>(p + l.part);

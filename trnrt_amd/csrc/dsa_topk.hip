@@ -1324,9 +1324,9 @@ static size_t topk_level_bytes(int B, long n, int keep) {
 
 size_t topk_hist_bytes(int B) { return up256((size_t)B * HIST_REPLICAS * TK_HBINS * 4); }
 
-// The region a workspace keeps at zero between calls: the histograms, then the fused layer's barrier words
-// (WS_SYNC_BYTES, which the separate kernels never touch).
-size_t topk_zero_bytes(int B) { return topk_hist_bytes(B) + WS_SYNC_BYTES; }
+// The region a workspace keeps at zero between calls: the barrier and status words (WS_SYNC_BYTES, the first bytes of
+// every workspace: the status words excepted), then the histograms.
+size_t topk_zero_bytes(int B) { return WS_SYNC_BYTES + topk_hist_bytes(B); }
 
 static bool topk_long_ok(int B, long n);
 static size_t topk_long_bytes(int B, long n);
@@ -1346,8 +1346,8 @@ bool topk_supported(int max_len, int keep, int vis_only) {
   return vis_only && topk_plan(max_len, keep);
 }
 
-// The flat selection's buffers inside the top-k workspace: the first-level histograms [B, 4096] (zero between
-// calls), then the per-row meta and the candidate lists of the chunked kernels.
+// The flat selection's buffers inside the top-k workspace: past the barrier and status words, the first-level
+// histograms [B, 4096] (zero between calls), then the per-row meta and the candidate lists of the chunked kernels.
 struct TopkBuffers {
   int* hist;
   RowMeta* meta;
@@ -1621,7 +1621,7 @@ hipError_t launch_topk(const float* scores, const int* len, int* idx, int* cnt, 
   if ((hist_ready || rows_out) && max_len > TOPK_FLAT_MAX && !long_rows) return hipErrorInvalidValue;
   if (rows_out && (!table || page_size < 32 || max_pages < 1 || num_pages < 1)) return hipErrorInvalidValue;
   TopkBuffers tb;
-  tb.hist = reinterpret_cast<int*>(p);
+  tb.hist = ws_hist(p);
   p += topk_zero_bytes(B);
   tb.meta = reinterpret_cast<RowMeta*>(p);
   p += up256((size_t)B * sizeof(RowMeta));
@@ -1664,7 +1664,7 @@ hipError_t launch_prefill_topk(const float* scores, const int* len, int* idx, in
                                hipStream_t s) {
   char* p = static_cast<char*>(ws);
   TopkBuffers tb;
-  tb.hist = reinterpret_cast<int*>(p);
+  tb.hist = ws_hist(p);
   p += topk_zero_bytes(B);
   tb.meta = reinterpret_cast<RowMeta*>(p);
   p += up256((size_t)B * sizeof(RowMeta));

@@ -67,3 +67,20 @@ def fp8_bytes(t: torch.Tensor, name: str) -> torch.Tensor:
     if not t.is_contiguous():
         raise ValueError(f"{name}: must be contiguous")
     return t
+
+
+# Zero-filled workspaces kept per (device, stream, use) and reused by the functional surfaces when the caller passes
+# none: every call leaves the regions that must start at zero at zero again, so one zero fill serves every later call
+# on the same stream (calls on one stream never overlap; each stream has its own). A call needing more grows it: a
+# new zero-filled buffer on the same stream (the old one returns to torch's stream-ordered allocator).
+_WORKSPACES: dict = {}
+
+
+def cached_workspace(device: torch.device, nbytes: int, use: str) -> torch.Tensor:
+    """A zero-filled uint8 device buffer of at least nbytes for `use` on the current stream of `device`."""
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream_ptr(device), use)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = ws
+    return ws

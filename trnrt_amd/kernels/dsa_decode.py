@@ -27,10 +27,10 @@ DQK_WIDTHS = (576, 512)  # the row widths the kernel takes: with rope, and GLM's
 DV = 512  # kv_lora_rank
 
 
-def _run(q: torch.Tensor, kv: torch.Tensor, kv_scale: torch.Tensor, scale: float, *, idx=None, cnt=None, table=None,
-         page_size: int = 1, rows=None, bias=None, lse: bool = False, out_dtype=torch.float32, splits: int = 0,
-         out: torch.Tensor | None = None, workspace: torch.Tensor | None = None):
-    dev = C.on_gpu(q, kv, kv_scale, idx, cnt, table, rows, bias, out, workspace)
+def _run(q: torch.Tensor, kv: torch.Tensor, kv_scale: torch.Tensor | None, scale: float, *, idx=None, cnt=None,
+         table=None, page_size: int = 1, rows=None, bias=None, lse: bool = False, out_dtype=torch.float32,
+         splits: int = 0, out: torch.Tensor | None = None, workspace: torch.Tensor | None = None, n_live=None):
+    dev = C.on_gpu(q, kv, kv_scale, idx, cnt, table, rows, bias, out, workspace, n_live)
     if q.dim() != 3 or q.shape[2] not in DQK_WIDTHS:
         raise ValueError(f"dsa_decode: q {tuple(q.shape)}, expected [B, H, 576 or 512]")
     B, H, dqk = q.shape
@@ -39,7 +39,8 @@ def _run(q: torch.Tensor, kv: torch.Tensor, kv_scale: torch.Tensor, scale: float
     q = C.as_bf16(q)
     kv = C.fp8_bytes(kv, "kv cache").reshape(-1, dqk)
     slots = kv.shape[0]
-    kv_scale = C.need(C.as_f32(kv_scale).reshape(-1), "kv_scale", torch.float32, (slots,))
+    if kv_scale is not None:  # None: the reference's unscaled cache (every scale 1, trnrt/models/decoder.py:481-486)
+        kv_scale = C.need(C.as_f32(kv_scale).reshape(-1), "kv_scale", torch.float32, (slots,))
     if idx is not None:
         keep = idx.shape[1]
         idx = C.need(C.as_i32(idx), "idx", torch.int32, (B, keep))
@@ -64,13 +65,23 @@ def _run(q: torch.Tensor, kv: torch.Tensor, kv_scale: torch.Tensor, scale: float
     if out.dtype not in (torch.float32, torch.bfloat16):
         raise ValueError(f"dsa_decode: output dtype {out.dtype}")
     C.need(out, "out", out.dtype, (B, H, DV))
-    ls = torch.empty(B, H, dtype=torch.float32, device=dev) if lse else None
+    ls = (torch.zeros if n_live is not None else torch.empty)(B, H, dtype=torch.float32, device=dev) if lse else None
     wsb = _lib.workspace_bytes(_lib.DSA_WS_ATTENTION, B, H, keep, 0, splits)
     if workspace is None and wsb:
-        workspace = torch.zeros(wsb, dtype=torch.uint8, device=dev)
+        # the split partials (written before they are read: no zero fill), kept per stream
+        workspace = C.cached_workspace(dev, wsb, "attention")
     ws_len = 0 if workspace is None else workspace.numel() * workspace.element_size()
     o_bf = out if out.dtype == torch.bfloat16 else None
     o_32 = out if out.dtype == torch.float32 else None
+    if n_live is not None:
+        # the rows + bias form over the first n_live[0] rows (the rest left unwritten)
+        if rows is None:
+            raise ValueError("dsa_decode: a live-row count takes the rows + bias form")
+        st = _lib.lib().dsa_sparse_mla_slots_n(
+            C.ptr(q), C.ptr(kv), C.ptr(kv_scale), C.ptr(rows), C.ptr(bias), C.ptr(n_live), C.ptr(o_bf), C.ptr(o_32),
+            C.ptr(ls), C.ptr(workspace), ws_len, B, H, dqk, keep, slots, float(scale), int(splits), C.stream_ptr(dev))
+        _lib.check(st, "dsa_slots_n.attend")
+        return (out, ls) if lse else out
     st = _lib.lib().dsa_sparse_mla_decode(
         C.ptr(q), C.ptr(kv), C.ptr(kv_scale), C.ptr(idx), C.ptr(cnt), C.ptr(table), C.ptr(rows), C.ptr(bias),
         C.ptr(o_bf), C.ptr(o_32), C.ptr(ls), C.ptr(workspace), ws_len, B, H, dqk, DV, keep, max_pages, page_size,
@@ -93,21 +104,24 @@ def pool_token_rows(rows: torch.Tensor, bias: torch.Tensor) -> tuple[torch.Tenso
 
 
 def attend(q_lat: torch.Tensor, kc: torch.Tensor, rows: torch.Tensor, bias: torch.Tensor, scale: float, *,
-           kc_scale: torch.Tensor, lse: bool = False, splits: int = 0):
-    """o [B, H, 512] fp32 (trnrt/kernels/dsa_decode.py:40-43 `attend`): q_lat [B, H, 576], kc the FP8 cache
-    [N, 1, 576] or [N, 576] (e4m3fn; for kp > 1 it may be the reference's pool view [N / kp, kp 576]), kc_scale [N]
-    fp32 its per-token scales, rows [B, NS] int each slot's row, bias [B, NS] or [B, NS, kp] fp32 (0 / NEG_INF): with
-    kp > 1 a slot is a pool of kp consecutive tokens. With lse also lse [B, H] fp32."""
+           kc_scale: torch.Tensor | None = None, lse: bool = False, splits: int = 0,
+           workspace: torch.Tensor | None = None):
+    """o [B, H, 512] fp32 (trnrt/kernels/dsa_decode.py:40-43 `attend`, called as the reference calls it:
+    attend(q_lat, kc, rows, bias, scale)): q_lat [B, H, 576 or 512], kc the FP8 cache [N, 1, D] or [N, D] (e4m3fn;
+    for kp > 1 it may be the reference's pool view [N / kp, kp D]), kc_scale [N] fp32 its per-token scales or None
+    for the reference's unscaled cache (scale 1), rows [B, NS] int each slot's row, bias [B, NS] or [B, NS, kp] fp32
+    (0 / NEG_INF): with kp > 1 a slot is a pool of kp consecutive tokens. With lse also lse [B, H] fp32. workspace:
+    the split partials (dsa_workspace_bytes(DSA_WS_ATTENTION, ...)), or None for one kept per stream."""
     rows, bias = pool_token_rows(rows, bias)
-    return _run(q_lat, kc, kc_scale, scale, rows=rows, bias=bias, lse=lse, splits=splits)
+    return _run(q_lat, kc, kc_scale, scale, rows=rows, bias=bias, lse=lse, splits=splits, workspace=workspace)
 
 
-def attend_tokens(q: torch.Tensor, kv_cache: torch.Tensor, kv_scale: torch.Tensor, idx: torch.Tensor,
+def attend_tokens(q: torch.Tensor, kv_cache: torch.Tensor, kv_scale: torch.Tensor | None, idx: torch.Tensor,
                   cnt: torch.Tensor, table: torch.Tensor, page_size: int, scale: float, *, lse: bool = True,
                   out_dtype=torch.bfloat16, splits: int = 0, out: torch.Tensor | None = None,
                   workspace: torch.Tensor | None = None):
     """The decode path's form: the selected token positions idx [B, keep] (ascending, cnt [B] valid) read through the
     page table [B, max_pages] (trnrt/models/dsa_long.py:189-215 `slots` folded into the gather). Returns o
-    [B, H, 512] in out_dtype (bf16 by default) and lse [B, H] fp32."""
+    [B, H, 512] in out_dtype (bf16 by default) and lse [B, H] fp32. kv_scale None: the unscaled cache."""
     return _run(q, kv_cache, kv_scale, scale, idx=idx, cnt=cnt, table=table, page_size=page_size, lse=lse,
                 out_dtype=out_dtype, splits=splits, out=out, workspace=workspace)

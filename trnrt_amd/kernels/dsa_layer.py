@@ -19,6 +19,22 @@ from . import _common as C
 NEG_INF = -1e30
 
 
+def _status(workspace: torch.Tensor | None, device: torch.device, clear: bool) -> dict:
+    ptr = workspace.data_ptr() if workspace is not None else None
+    gave_up, two = _lib.layer_status(ptr, torch.cuda.current_stream(device).cuda_stream, clear)
+    return {"gave_up": gave_up, "two_exchange": two}
+
+
+def _verify(workspace: torch.Tensor | None, device: torch.device, what: str) -> None:
+    """RuntimeError if a barrier wait on this workspace gave up since the last check (the count is then cleared):
+    the reference raises on the host, never in a kernel (trnrt/kernels/dsa_index.py:258-259)."""
+    st = _status(workspace, device, clear=False)
+    if st["gave_up"]:
+        _status(workspace, device, clear=True)
+        raise RuntimeError(f"{what}: {st['gave_up']} barrier wait(s) gave up; the outputs of the steps since the last "
+                           "check may be wrong (another kernel held CUs the one-launch layer needs)")
+
+
 class DecodeLayer:
     """Buffers and launch parameters of a decode step over B rows with up to max_pages pages each.
 
@@ -48,13 +64,22 @@ class DecodeLayer:
         # zero once: the calls keep the regions that must start at zero (the top-k histograms) at zero
         self.workspace = torch.zeros(max(wsb, 256), dtype=torch.uint8, device=dev)
 
+    def status(self, clear: bool = False) -> dict:
+        """The workspace's status words since the last clear (synchronises the current stream): `gave_up`, barrier
+        waits that gave up (non-zero: some step's outputs may be wrong; the one-launch kernel needs all its
+        workgroups resident at once), and `two_exchange`, rows selected in the two-exchange form."""
+        return _status(self.workspace, self.device, clear)
+
     def step(self, q_idx: torch.Tensor, w: torch.Tensor, k_cache: torch.Tensor, k_scale: torch.Tensor,
-             q: torch.Tensor, kv_cache: torch.Tensor, kv_scale: torch.Tensor, table: torch.Tensor,
-             ctx_len: torch.Tensor, check: bool = True) -> tuple[torch.Tensor, torch.Tensor]:
+             q: torch.Tensor, kv_cache: torch.Tensor, kv_scale: torch.Tensor | None, table: torch.Tensor,
+             ctx_len: torch.Tensor, check: bool = True, verify: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
         """(out bf16 [B, H, 512], lse fp32 [B, H]) of one layer step; self.scores / idx / cnt hold the intermediates.
         q_idx [B, Hi, 128] bf16, w [B, Hi] fp32 (D ** -0.5 folded in), k_cache [slots, 128] e4m3fn + k_scale [slots],
-        q [B, H, 576] bf16, kv_cache [slots, 576] e4m3fn + kv_scale [slots], table [B, max_pages] int32, ctx_len [B]
-        int32 (each <= max_len). check=False skips the Python-side argument checks (the C ABI still checks sizes)."""
+        q [B, H, 576] bf16, kv_cache [slots, 576] e4m3fn + kv_scale [slots] (None: the reference's unscaled cache),
+        table [B, max_pages] int32, ctx_len [B]
+        int32 (each <= max_len). check=False skips the Python-side argument checks (the C ABI still checks sizes).
+        verify=True synchronises after the step and raises RuntimeError if a barrier wait of this or an earlier
+        unverified step gave up (clearing the count)."""
         B, Hi, H = self.B, self.Hi, self.H
         if check:
             C.on_gpu(q_idx, w, k_cache, k_scale, q, kv_cache, kv_scale, table, ctx_len)
@@ -69,16 +94,19 @@ class DecodeLayer:
             if k_cache.numel() != slots * 128 or kv_cache.numel() != slots * 576:
                 raise ValueError(f"caches of {k_cache.numel()} / {kv_cache.numel()} bytes for {slots} slots")
             C.need(k_scale, "k_scale", torch.float32, (slots,))
-            C.need(kv_scale, "kv_scale", torch.float32, (slots,))
+            if kv_scale is not None:
+                C.need(kv_scale, "kv_scale", torch.float32, (slots,))
         fn = _lib.lib().dsa_decode_layer_chain if self.chain else _lib.lib().dsa_decode_layer
         st = fn(
             q_idx.data_ptr(), w.data_ptr(), k_cache.data_ptr(), k_scale.data_ptr(), q.data_ptr(),
-            kv_cache.data_ptr(), kv_scale.data_ptr(), table.data_ptr(), ctx_len.data_ptr(), self.scores.data_ptr(),
+            kv_cache.data_ptr(), C.ptr(kv_scale), table.data_ptr(), ctx_len.data_ptr(), self.scores.data_ptr(),
             self.idx.data_ptr(), self.cnt.data_ptr(), self.out.data_ptr(), self.lse.data_ptr(),
             self.workspace.data_ptr(), self.workspace.numel(), B, Hi, H, self.max_pages, self.page_size,
             self.num_pages, self.stride, self.max_len, self.keep, self.scale, self.splits,
             torch.cuda.current_stream(self.device).cuda_stream)
         _lib.check(st, "dsa_layer.step")
+        if verify:
+            _verify(self.workspace, self.device, "dsa_layer.step")
         return self.out, self.lse
 
 
@@ -116,13 +144,13 @@ class PooledDecodeLayer:
         self.workspace = torch.zeros(wsb, dtype=torch.uint8, device=dev)
 
     def step(self, q_idx: torch.Tensor, w: torch.Tensor, pool_key: torch.Tensor, q: torch.Tensor,
-             kv_cache: torch.Tensor, kv_scale: torch.Tensor, table: torch.Tensor, npool: torch.Tensor,
-             positions: torch.Tensor, check: bool = True) -> tuple[torch.Tensor, torch.Tensor]:
+             kv_cache: torch.Tensor, kv_scale: torch.Tensor | None, table: torch.Tensor, npool: torch.Tensor,
+             positions: torch.Tensor, check: bool = True, verify: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
         """(out bf16 [B, H, 512], lse fp32 [B, H]); self.scores / pools / cnt hold the intermediates. q_idx
         [B, Hi, 128] bf16, w [B, Hi] fp32 (128 ** -0.5 folded in), pool_key bf16 [slots, 128 / kp], q [B, H, dqk]
-        bf16, kv_cache [slots, dqk] e4m3fn + kv_scale [slots], table [B, max_pages] int32, npool [B] int32
-        ((positions + 1) // kp), positions [B] int32. check=False skips the Python-side checks (the C ABI still
-        checks sizes)."""
+        bf16, kv_cache [slots, dqk] e4m3fn + kv_scale [slots] (None: unscaled), table [B, max_pages] int32, npool
+        [B] int32 ((positions + 1) // kp), positions [B] int32. check=False skips the Python-side checks (the C ABI still
+        checks sizes); verify as DecodeLayer.step."""
         B, Hi, H = self.B, self.Hi, self.H
         if check:
             C.on_gpu(q_idx, w, pool_key, q, kv_cache, kv_scale, table, npool, positions)
@@ -137,13 +165,21 @@ class PooledDecodeLayer:
             C.need(pool_key, "pool_key", torch.bfloat16, (slots, 128 // self.kp))
             if kv_cache.numel() != slots * self.dqk:
                 raise ValueError(f"kv cache of {kv_cache.numel()} bytes for {slots} slots of {self.dqk}")
-            C.need(kv_scale, "kv_scale", torch.float32, (slots,))
+            if kv_scale is not None:
+                C.need(kv_scale, "kv_scale", torch.float32, (slots,))
         st = _lib.lib().dsa_pooled_decode_layer(
             q_idx.data_ptr(), w.data_ptr(), pool_key.data_ptr(), q.data_ptr(), kv_cache.data_ptr(),
-            kv_scale.data_ptr(), table.data_ptr(), npool.data_ptr(), positions.data_ptr(), self.scores.data_ptr(),
+            C.ptr(kv_scale), table.data_ptr(), npool.data_ptr(), positions.data_ptr(), self.scores.data_ptr(),
             self.pools.data_ptr(), self.cnt.data_ptr(), self.out.data_ptr(), self.lse.data_ptr(),
             self.workspace.data_ptr(), self.workspace.numel(), B, Hi, H, self.dqk, self.max_pages, self.page_size,
             self.num_pages, self.kp, self.keep, self.scale, self.splits,
             torch.cuda.current_stream(self.device).cuda_stream)
         _lib.check(st, "dsa_layer.PooledDecodeLayer.step")
+        if verify:
+            _verify(self.workspace, self.device, "dsa_layer.PooledDecodeLayer.step")
         return self.out, self.lse
+
+    def status(self, clear: bool = False) -> dict:
+        """The workspace's status words since the last clear (as DecodeLayer.status; the attention launch's
+        barrier waits)."""
+        return _status(self.workspace, self.device, clear)

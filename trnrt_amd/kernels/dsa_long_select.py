@@ -172,7 +172,8 @@ def select(qI: torch.Tensor, w: torch.Tensor, pk: torch.Tensor, npool: torch.Ten
         raise ValueError(f"dsa_long_select: tile_rows {tile_rows}")
     lib = _lib.lib()
     if workspace is None:
-        workspace = torch.zeros(workspace_bytes(N, P, keep, tile_rows), dtype=torch.uint8, device=dev)
+        # zero-filled before its first use, left so by every call: one per stream serves every call
+        workspace = C.cached_workspace(dev, workspace_bytes(N, P, keep, tile_rows), "prefill_select")
     ws_len = workspace.numel() * workspace.element_size()
     pools = torch.empty(N, keep, dtype=torch.int64, device=dev)
     cnt = torch.empty(N, dtype=torch.int64, device=dev)

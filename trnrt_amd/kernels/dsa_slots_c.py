@@ -31,11 +31,14 @@ def live_tokens(bias: torch.Tensor) -> torch.Tensor:
 
 
 def attend(q_lat: torch.Tensor, kc: torch.Tensor, rows: torch.Tensor, bias: torch.Tensor, scale: float,
-           lse: bool = False, *, kc_scale: torch.Tensor, splits: int = 0):
+           lse: bool = False, *, kc_scale: torch.Tensor | None = None, splits: int = 0,
+           workspace: torch.Tensor | None = None):
     """o [N, H, 512] fp32 (and lse [N, H] fp32) of q_lat [N, H, 576 or 512] bf16 over the visible tokens of rows
     [N, NS] (pool rows of the FP8 cache kc viewed as [slots / kp, kp rows]; kc [slots, 1, D] or [slots, D] e4m3fn
-    with kc_scale [slots] fp32 its per-token scales) with bias [N, NS, kp] or [N, NS] fp32 (0 / NEG_INF)."""
-    dev = C.on_gpu(q_lat, kc, rows, bias, kc_scale)
+    with kc_scale [slots] fp32 its per-token scales, or None for the reference's unscaled cache) with bias
+    [N, NS, kp] or [N, NS] fp32 (0 / NEG_INF). workspace: dsa_slots_compact_workspace_bytes(N, H, NS, kp, splits)
+    bytes (no zero fill needed), or None for one kept per stream."""
+    dev = C.on_gpu(q_lat, kc, rows, bias, kc_scale, workspace)
     if q_lat.dim() != 3 or q_lat.shape[2] not in DQK_WIDTHS:
         raise ValueError(f"dsa_slots_c: q_lat {tuple(q_lat.shape)}, expected [N, H, 576 or 512]")
     N, H, dqk = q_lat.shape
@@ -53,12 +56,15 @@ def attend(q_lat: torch.Tensor, kc: torch.Tensor, rows: torch.Tensor, bias: torc
     num_slots = kv.shape[0]
     if num_slots % kp or num_slots < kp:
         raise ValueError(f"dsa_slots_c: {num_slots} cache rows are not whole pools of {kp}")
-    ks = C.need(C.as_f32(kc_scale).reshape(-1), "kc_scale", torch.float32, (num_slots,))
+    ks = None if kc_scale is None else C.need(C.as_f32(kc_scale).reshape(-1), "kc_scale", torch.float32,
+                                              (num_slots,))
     r = C.need(C.as_i32(rows), "rows", torch.int32, (N, NS))
     out = torch.empty(N, H, DV, dtype=torch.float32, device=dev)
     ls = torch.empty(N, H, dtype=torch.float32, device=dev) if lse else None
     wsb = _lib.lib().dsa_slots_compact_workspace_bytes(N, H, NS, kp, int(splits))
-    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+    ws = workspace if workspace is not None else C.cached_workspace(dev, wsb, "slots_compact")
+    if ws.numel() * ws.element_size() < wsb:
+        raise ValueError(f"dsa_slots_c.attend: workspace of {ws.numel() * ws.element_size()} bytes, needs {wsb}")
     st = _lib.lib().dsa_sparse_mla_slots_compact(
         C.ptr(q), C.ptr(kv), C.ptr(ks), C.ptr(r), C.ptr(b), None, C.ptr(out), C.ptr(ls), C.ptr(ws), wsb, N, H, dqk,
         NS, kp, num_slots, float(scale), int(splits), C.stream_ptr(dev))

@@ -33,7 +33,8 @@ def select_indices(scores: torch.Tensor, keep: int, lengths: torch.Tensor | None
                    workspace: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
     """(idx int32 [R, keep] ascending selected positions, 0 past the count; cnt int32 [R]) of scores [R, P] fp32.
     lengths [R] int32: positions at or past a row's length are not selectable (None: all P); max_len an upper bound
-    of the lengths (default P)."""
+    of the lengths (default P). workspace: the caller's (dsa_workspace_bytes(DSA_WS_TOPK, R, 0, keep, max_len),
+    zero-filled before its first use; calls leave it so), or None for one kept per stream."""
     dev = C.on_gpu(scores, lengths, idx, cnt, workspace)
     if scores.dim() != 2:
         raise ValueError(f"dsa_topk: scores {tuple(scores.shape)}, expected [rows, P]")
@@ -56,8 +57,9 @@ def select_indices(scores: torch.Tensor, keep: int, lengths: torch.Tensor | None
     C.need(cnt, "cnt", torch.int32, (R,))
     wsb = _lib.workspace_bytes(_lib.DSA_WS_TOPK, R, 0, keep, max(n, 1))
     if workspace is None:
-        workspace = torch.zeros(wsb, dtype=torch.uint8, device=dev)  # the histogram region starts (and ends) at zero
-    ws_len = 0 if workspace is None else workspace.numel() * workspace.element_size()
+        # the histogram region starts (and ends) at zero: one zero-filled buffer per stream serves every call
+        workspace = C.cached_workspace(dev, wsb, "topk")
+    ws_len = workspace.numel() * workspace.element_size()
     st = _lib.lib().dsa_topk(C.ptr(scores), C.ptr(lengths), C.ptr(idx), C.ptr(cnt), C.ptr(workspace), ws_len, R, P,
                              n, keep, int(vis_only), C.stream_ptr(dev))
     _lib.check(st, "dsa_topk.select_indices")

@@ -57,10 +57,12 @@ def scores(qI: torch.Tensor, w: torch.Tensor, pk: torch.Tensor, npool: torch.Ten
     return dsa_index.decode_scores(qI, w.float() * float(scale), pk.reshape(N * P, -1), ks, table, lens, P, P)
 
 
-def select_device(sc: torch.Tensor, keep: int, lengths: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+def select_device(sc: torch.Tensor, keep: int, lengths: torch.Tensor | None = None, *,
+                  workspace: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
     """The exact selection of scores [N, P] (non-candidates at or below VISIBLE) as (indices [N, keep] int64
-    ascending, 0 past the count; count [N] int64). lengths [N] int32 optionally bounds each row's candidates."""
-    idx, cnt = dsa_topk.select_indices(sc, keep, lengths=lengths, vis_only=True)
+    ascending, 0 past the count; count [N] int64). lengths [N] int32 optionally bounds each row's candidates.
+    workspace: the caller's top-k workspace (dsa_topk.select_indices), or None for one kept per stream."""
+    idx, cnt = dsa_topk.select_indices(sc, keep, lengths=lengths, vis_only=True, workspace=workspace)
     return idx.to(torch.int64), cnt.to(torch.int64)
 
 
@@ -120,12 +122,13 @@ def slots(pools: torch.Tensor, cnt: torch.Tensor, npool: torch.Tensor, positions
 
 
 def attend(q_lat: torch.Tensor, kc: torch.Tensor, rows: torch.Tensor, bias: torch.Tensor, scale: float, *,
-           kc_scale: torch.Tensor) -> torch.Tensor:
-    """o [N, H, 512] fp32: absorbed MLA of N queries over their slots (trnrt/models/dsa_long.py:218-223)."""
+           kc_scale: torch.Tensor | None = None) -> torch.Tensor:
+    """o [N, H, 512] fp32: absorbed MLA of N queries over their slots (trnrt/models/dsa_long.py:218-223); kc_scale
+    None: the reference's unscaled cache."""
     return dsa_decode.attend(q_lat, kc, rows, bias, scale, kc_scale=kc_scale)
 
 
-def attend_pooled(q_lat: torch.Tensor, kc: torch.Tensor, kc_scale: torch.Tensor, pools: torch.Tensor,
+def attend_pooled(q_lat: torch.Tensor, kc: torch.Tensor, kc_scale: torch.Tensor | None, pools: torch.Tensor,
                   cnt: torch.Tensor, npool: torch.Tensor, positions: torch.Tensor, table: torch.Tensor,
                   page_size: int, kp: int, scale: float, *, lse: bool = False,
                   workspace: torch.Tensor | None = None, splits: int = 0):
@@ -146,7 +149,7 @@ def attend_pooled(q_lat: torch.Tensor, kc: torch.Tensor, kc_scale: torch.Tensor,
     q = C.as_bf16(q_lat)
     kv = C.fp8_bytes(kc, "kc").reshape(-1, dqk)
     slots_n = kv.shape[0]
-    ks = C.need(C.as_f32(kc_scale).reshape(-1), "kc_scale", torch.float32, (slots_n,))
+    ks = None if kc_scale is None else C.need(C.as_f32(kc_scale).reshape(-1), "kc_scale", torch.float32, (slots_n,))
     pl = C.need(C.as_i32(pools), "pools", torch.int32, (N, keep))
     cn = C.need(C.as_i32(cnt.reshape(-1)), "cnt", torch.int32, (N,))
     npl = C.need(C.as_i32(npool.reshape(-1)), "npool", torch.int32, (N,))
@@ -161,7 +164,7 @@ def attend_pooled(q_lat: torch.Tensor, kc: torch.Tensor, kc_scale: torch.Tensor,
     ls = torch.empty(N, H, dtype=torch.float32, device=dev) if lse else None
     lib = _lib.lib()
     wsb = int(lib.dsa_sparse_mla_pooled_workspace_bytes(N, H, keep, kp, int(splits)))
-    ws = workspace if workspace is not None else torch.empty(max(wsb, 256), dtype=torch.uint8, device=dev)
+    ws = workspace if workspace is not None else C.cached_workspace(dev, wsb, "attention")
     st = lib.dsa_sparse_mla_pooled(C.ptr(q), C.ptr(kv), C.ptr(ks), C.ptr(pl), C.ptr(cn), C.ptr(npl), C.ptr(pos),
                                    C.ptr(tb), None, C.ptr(out), C.ptr(ls), C.ptr(ws), ws.numel(), N, H, dqk, keep, kp,
                                    tb.shape[1], page_size, slots_n // page_size, float(scale), int(splits),
@@ -171,7 +174,7 @@ def attend_pooled(q_lat: torch.Tensor, kc: torch.Tensor, kc_scale: torch.Tensor,
 
 
 def decode_pooled(q_idx: torch.Tensor, w: torch.Tensor, pool_key: torch.Tensor, q_lat: torch.Tensor,
-                  kc: torch.Tensor, kc_scale: torch.Tensor, positions: torch.Tensor, table: torch.Tensor,
+                  kc: torch.Tensor, kc_scale: torch.Tensor | None, positions: torch.Tensor, table: torch.Tensor,
                   page_size: int, kp: int, topk: int, index_scale: float, softmax_scale: float, *,
                   parts: bool = False):
     """One pooled decode batch's attention core after its rows and pool keys were written (trnrt/models/mla.py:505-526
