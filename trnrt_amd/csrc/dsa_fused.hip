@@ -845,9 +845,11 @@ __device__ __forceinline__ int fu_select(const FusedArgs& a, uint8_t* lds, int b
 // list w's entries FU_LPT q .. + FU_LPT - 1) and the row's pages. Every key of the row at or above the lowest bin of
 // each list is in the lists, so when the bin c0 of the lists' keep-th largest key is at or above every list's lowest
 // bin, the lists hold every key at or above the row's keep-th largest, and T (the keep-th largest), the ties at T to
-// take (the lowest positions) and each workgroup's selected count follow from the lists alone (three histogram passes
-// over their keys: 12, 12 and 8 bits). Returns false when they do not (every workgroup of the row decides alike, and
-// nothing but LDS has been written): the caller then takes the two-exchange form.
+// take (the lowest positions) and every selected key's index in the ascending output follow from the lists alone
+// (three histogram passes over their keys: 12, 12 and 8 bits; then per list its counts above and at T): the
+// workgroup writes the indices and lists the cache slots of its split's outputs [o0, o1) straight from its listed
+// keys. Returns false when the lists do not hold the selection (every workgroup of the row decides alike, and nothing
+// but LDS has been written): the caller then takes the two-exchange form.
 template <int HPW>
 __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds, int b, int j, int L,
                                                 u32x4 (&qv)[FuAtt<HPW>::QPT], float* live_bias, int* n_slots) {
@@ -859,8 +861,10 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
   int* bins1 = reinterpret_cast<int*>(lds + L_BINS);
   int* bins2 = reinterpret_cast<int*>(lds + L_BINS2);
   int* spg = reinterpret_cast<int*>(lds + L_SPG);
-  uint32_t* sb = reinterpret_cast<uint32_t*>(lds + L_SB);
   int* slot_l = reinterpret_cast<int*>(lds + AT::L_P);
+  // the split's output positions, stored to idx in one coalesced pass at the end; entry CAP of each list is a sink
+  int* pos_l = slot_l + AT::CAP + 1;
+  static_assert(4 * (2 * AT::CAP + 2) <= 2 * HPW * AT::PROW, "slot and position lists inside P's region");
   const int tid = threadIdx.x, wave = tid / WAVE, lane = tid & (WAVE - 1);
   const int w = tid >> 4, q = tid & 15;
   const int hg = j % a.HG, s = j / a.HG;
@@ -906,8 +910,7 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
   __builtin_amdgcn_sched_barrier(0);
   for (int i = tid; i < 4096; i += FU_THREADS) bins0[i] = bins1[i] = 0;
   if (tid < 256) bins2[tid] = 0;
-  sb[tid] = sb[tid + FU_THREADS] = 0u;
-  if (tid < AT::SPLIT) slot_l[tid] = 0;  // padding rows read slot 0
+  if (tid < AT::SPLIT) slot_l[tid] = pos_l[tid] = 0;  // padding rows read slot 0; outputs past the count are 0
   if (tid == 0) scr[8] = scr[24] = scr[40] = -1;
   __builtin_amdgcn_sched_barrier(0);
   __syncthreads();  // the bins cleared (the loads above may be out; their first uses wait for them)
@@ -990,43 +993,82 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
     }
     T = ((uint32_t)c0 << 20) | tlow;
   }
-  // per list: its keys above T (into its bitmap now) and equal to T, and this thread's ties before it in the list
-  int gt = 0, eq = 0;
+  // every listed key's place in the ascending output, from the lists alone: per list, its keys above T and its ties
+  // at T (packed counts, summed over its 16 threads in list order); then per list the ties of the lists before it
+  // (ties are taken in position order while fewer than `room` come before), its selected count and its first output
+  // index; a selected key's index is its list's first plus the selected keys before it in the list
+  uint32_t mine = 0;
 #pragma unroll
-  for (int i = 0; i < FU_LPT; ++i) {
-    gt += key[i] > T;
-    eq += key[i] == T && key[i];
-    if (key[i] > T) atomicOr(&sb[FU_BMW * w + (pos[i] >> 5)], 1u << (pos[i] & 31u));
-  }
+  for (int i = 0; i < FU_LPT; ++i) mine += (key[i] > T ? 1u : 0u) + (key[i] == T && key[i] ? 0x10000u : 0u);
   fresh();
-  const int eq_in = row_incl_scan(eq);
-  gt = row_sum(gt);
+  const uint32_t incl = (uint32_t)row_incl_scan((int)mine);
   if (q == 15) {
-    st.gt[w] = gt;
-    st.eq[w] = eq_in;
-  }
-  __syncthreads();
-  // every wave: per list w (lane w) the ties at T before it, its selected count and first output index (ties are
-  // taken while fewer than `room` come before)
-  const int ww = lane & (FU_NW - 1);
-  const int eqw = lane < FU_NW ? st.eq[ww] : 0;
-  const int tbw = wave_incl_scan(eqw) - eqw;
-  const int selw = lane < FU_NW ? st.gt[ww] + min(max(room - tbw, 0), eqw) : 0;
-  const int offw = wave_incl_scan(selw) - selw;
-  const int tb_list = __shfl(tbw, w, WAVE);  // with every lane active: a lane switched off returns no value
-  if (eq > 0) {
-    int k = tb_list + eq_in - eq;  // the row's ties before this thread's first
-#pragma unroll
-    for (int i = 0; i < FU_LPT; ++i)
-      if (key[i] == T && key[i]) {
-        if (k < room) atomicOr(&sb[FU_BMW * w + (pos[i] >> 5)], 1u << (pos[i] & 31u));
-        ++k;
-      }
+    st.gt[w] = (int)(incl & 0xFFFFu);
+    st.eq[w] = (int)(incl >> 16);
   }
   spg[tid] = pgv[0];
   spg[tid + FU_THREADS] = pgv[1];
   __syncthreads();
-  *n_slots = fu_split_slots<HPW>(a, lds, b, j, kw, selw, offw, o0, o1, cnt_row, 0, qv, live_bias);
+  const int ww = lane & (FU_NW - 1);
+  const int eqw = lane < FU_NW ? st.eq[ww] : 0;
+  const int tbw = wave_incl_scan(eqw) - eqw;
+  const int takew = lane < FU_NW ? min(max(room - tbw, 0), eqw) : 0;  // list w's ties taken: its first takew
+  const int selw = lane < FU_NW ? st.gt[ww] + takew : 0;
+  const int offw = wave_incl_scan(selw) - selw;
+  // (with every lane active: a lane switched off returns no value)
+  const int off_l = __shfl(offw, w, WAVE), take_l = __shfl(takew, w, WAVE);
+  // the attention's queries into LDS before the index stores below (a wait for the queries' loads there would also
+  // wait for those stores)
+  {
+    uint16_t* qs = reinterpret_cast<uint16_t*>(lds + AT::L_QST);
+#pragma unroll
+    for (int i = 0; i < QPT; ++i) {
+      const int pc = tid + FU_THREADS * i;
+      if (active && pc < HPW * FU_DQK / 8)
+        *reinterpret_cast<u32x4*>(qs + (pc / (FU_DQK / 8)) * FU_AQROW + 8 * (pc % (FU_DQK / 8))) = qv[i];
+    }
+  }
+  {
+    // this thread's selected entries take the output indices first .. first + nsel - 1; only the threads whose
+    // indices meet the split's [o0, o1) (one or two lists' worth, so most waves skip this) list their entries: each
+    // entry's index, then all their pages in one round of LDS reads, then the writes, with no branch per entry (an
+    // entry outside the split writes the sink entry past the lists)
+    int gtb = (int)((incl - mine) & 0xFFFFu), eqb = (int)((incl - mine) >> 16);  // this thread's list predecessors
+    const int first = off_l + gtb + min(eqb, take_l);
+    const int nsel = (int)(mine & 0xFFFFu) + min(max(take_l - eqb, 0), (int)(mine >> 16));
+    if (nsel > 0 && first < o1 && first + nsel > o0) {
+      int oi[FU_LPT], pg[FU_LPT];
+#pragma unroll
+      for (int i = 0; i < FU_LPT; ++i) {
+        const bool above = key[i] > T, tie = key[i] == T && key[i];
+        const int o = off_l + gtb + min(eqb, take_l) - o0;
+        oi[i] = (above || (tie && eqb < take_l)) && (unsigned)o < (unsigned)(o1 - o0) ? o : AT::CAP;
+        gtb += above;
+        eqb += tie;
+      }
+#pragma unroll
+      for (int i = 0; i < FU_LPT; ++i) pg[i] = spg[(kw * w + (int)pos[i]) >> a.page_shift];
+#pragma unroll
+      for (int i = 0; i < FU_LPT; ++i) {
+        const int p = kw * w + (int)pos[i];  // the key's position in the row
+        slot_l[oi[i]] = safe_page(pg[i], a.num_pages) * a.page_size + (p & (a.page_size - 1));
+        pos_l[oi[i]] = p;
+      }
+    }
+  }
+  if (j == 0 && tid == 0) a.cnt[b] = cnt_row;
+  // the split's live slots; a row with none attends position 0 masked (its lse is NEG_INF)
+  int ns = max(min(o1, cnt_row) - o0, 0);
+  *live_bias = 0.0f;
+  if (active && cnt_row == 0 && s == 0) {
+    ns = 1;
+    *live_bias = NEG_INF;
+    if (tid == 0) slot_l[0] = safe_page(a.table[(size_t)b * a.max_pages], a.num_pages) * a.page_size;
+  }
+  *n_slots = ns;
+  __syncthreads();  // the slot and position lists and the queries
+  // the split's outputs [o0, o1) of the ascending index output, one coalesced store (0 past the count)
+  if (hg == 0 && tid < o1 - o0) a.idx[(size_t)b * a.keep + o0 + tid] = pos_l[tid];
   return true;
 }
 
@@ -1087,7 +1129,9 @@ __device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int 
     for (int st2 = 0; st2 < STEPS; ++st2)
       qb[st2] = as_bf16x8(*reinterpret_cast<const uint4*>(qh + 64 * (st2 >> 1) + 8 * (st2 & 1)));
   }
-  __syncthreads();  // every wave holds its query operand before the rows overwrite it
+  // (16 heads: the queries are staged inside the row tile, so every wave holds its query operand before the rows
+  // overwrite it; 32: they lie past the tile, and the gather below starts while the operand reads are in flight)
+  if (AT::L_QST < AT::L_P) __syncthreads();
   // every row straight into LDS, coalesced: load k fills 1 KiB of the tile, lane l 16-byte unit u = 64 k + l (row
   // u / 37, piece u % 37; the padding piece re-reads the last data piece); the loads of the padded rows' units spread
   // over the 8 waves
