@@ -402,9 +402,10 @@ def pooled_cpu_baseline(inp, cfg, npool, positions, budget_s: float = 15.0) -> d
 
 def pooled_main(args) -> int:
     """The pooled (GLM-5.3-Flash) decode step (config 6): the current tokens' pool-key write (dsa_pool_keys_write),
-    then the pooled layer (dsa_pooled_decode_layer: the indexer over the bf16 pool-key cache with the top-k's
-    first-level histogram fused, the exact top-512 pools, sparse MLA over the selected pools' tokens and the tail, over
-    the 512-wide NoPE latent). roofline: the indexer kernel's algorithmic bytes over its HIP-event-timed duration."""
+    then the pooled layer (dsa_pooled_decode_layer: the indexer over the bf16 pool-key cache, the exact top-512 pools,
+    sparse MLA over the selected pools' tokens and the tail, over the 512-wide NoPE latent; one launch, or with
+    --chain the separate kernels). roofline: the one launch's algorithmic bytes (W.pooled_layer_bytes) over its
+    HIP-event-timed duration, or with --chain the indexer kernel's."""
     import torch
 
     from trnrt_amd import _lib
@@ -422,7 +423,7 @@ def pooled_main(args) -> int:
     slot_mapping = dsa_cache.slots_of(pos, inp.table, ps)
     npool_d = torch.div(pos + 1, kp, rounding_mode="floor").to(torch.int32)
     layer = PooledDecodeLayer(cfg.B, cfg.Hi, cfg.H, cfg.dqk, inp.table.shape[1], ps, inp.pool_key.shape[0] // ps, kp,
-                              cfg.keep, cfg.scale, splits=args.splits, device=dev)
+                              cfg.keep, cfg.scale, splits=args.splits, device=dev, chain=args.chain)
 
     def step():
         dsa_cache.write_pool_keys(inp.pool_key, inp.rows, pos, inp.table, slot_mapping, inp.ape, ps, kp,
@@ -446,13 +447,18 @@ def pooled_main(args) -> int:
     npool = torch.div(positions + 1, kp, rounding_mode="floor")
     tail = [int(p) + 1 - kp * int(n) for p, n in zip(positions, npool)]
     tokens = [kp * min(int(n), cfg.keep) + t for n, t in zip(npool, tail)]
-    idx_bytes = W.pooled_indexer_bytes(cfg, npool.tolist())
-    idx_us = k_us["indexer_decode_bf16_kernel"]
-    achieved = idx_bytes / (idx_us * 1e-6) / 1e9
+    if "decode_pooled_fused_kernel" in k_us:
+        # the one-launch layer: its launches move the layer's algorithmic bytes
+        kname, kbytes = "decode_pooled_fused_kernel", W.pooled_layer_bytes(cfg, npool.tolist(), tokens)
+    else:
+        # the separate kernels: the indexer, the kernel that streams the whole pool-key cache
+        kname, kbytes = "indexer_decode_bf16_kernel", W.pooled_indexer_bytes(cfg, npool.tolist())
+    k_time = k_us[kname]
+    achieved = kbytes / (k_time * 1e-6) / 1e9
     step_bytes = W.pooled_step_bytes(cfg, npool.tolist(), tokens)
     step_gbs = step_bytes / (ms * 1e-3) / 1e9
     out = {
-        "metric": "DSA pooled decode layer-steps/sec (GLM kpool 4) at B=8, 32K ctx; indexer HBM GB/s (% of 8 TB/s)",
+        "metric": "DSA pooled decode layer-steps/sec (GLM kpool 4) at B=8, 32K ctx; achieved HBM GB/s (% of 8 TB/s)",
         "value": round(1e3 / ms, 1),
         "unit": "layer-steps/s",
         "n_gpus": 1,
@@ -464,14 +470,16 @@ def pooled_main(args) -> int:
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": f"config {args.config}: {cfg.name}", "batch": cfg.B, "context": cfg.L,
+        "config": {"workload": f"config {args.config}: {cfg.name}" + (" (separate kernels)" if args.chain else ""),
+                   "batch": cfg.B, "context": cfg.L,
                    "q_heads": cfg.H, "indexer_heads": cfg.Hi, "kpool": kp, "keep_pools": cfg.keep,
                    "page_size": ps, "pool_keys": "bf16 [128] per pool (kpool pieces)",
                    "kv": f"fp8 e4m3 [{cfg.dqk}] + fp32 scale per token", "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "kernel": "indexer_decode_bf16_kernel", "achieved": round(achieved, 1),
+        "roofline": {"bound": "hbm", "kernel": kname, "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(f"config {args.config}: {cfg.name}", "indexer_decode_bf16_kernel"),
-                     "algorithmic_bytes": idx_bytes, "avg_us": round(idx_us, 3)},
+                     "traffic": measured_traffic(f"config {args.config}: {cfg.name}", kname),
+                     "algorithmic_bytes": kbytes, "avg_us": round(k_time, 3),
+                     "launches_per_step": -(-cfg.B // 8) if kname == "decode_pooled_fused_kernel" else 1},
         "layer": {"algorithmic_bytes": step_bytes, "achieved_GBs": round(step_gbs, 1),
                   "frac": round(step_gbs / HBM_PEAK_GBS, 4), "kernel_us": {k: round(v, 3) for k, v in k_us.items()},
                   "step_us": percentiles(spans)},

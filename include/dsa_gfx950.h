@@ -319,7 +319,7 @@ int dsa_sparse_mla_pooled(const void* q_bf16, const uint8_t* kv_fp8, const float
 size_t dsa_sparse_mla_pooled_workspace_bytes(int B, int H, int keep, int kp, int splits);
 
 /*
- * The pooled (GLM, kpool kp > 1) DSA decode layer step, enqueued back to back on one stream (the decode batch of
+ * The pooled (GLM, kpool kp > 1) DSA decode layer step (the decode batch of
  * trnrt/models/mla.py:505-526 `attention_long`, scoring the pool-key cache's page rows in place as
  * trnrt/models/mla.py:615-630 does): the pooled indexer over the complete pools p < npool[b] of the bf16 pool-key
  * cache -> the exact top-keep pools -> sparse MLA over the kp tokens of each selected pool and the tail tokens
@@ -331,9 +331,11 @@ size_t dsa_sparse_mla_pooled_workspace_bytes(int B, int H, int keep, int kp, int
  *   [B, keep] (ascending, 0 past cnt), cnt int32 [B], out bf16 [B, H, 512], lse fp32 [B, H] (or null).
  *   workspace: dsa_pooled_workspace_bytes(B, H, keep, max_pages page_size / kp, kp, splits) bytes, zero-filled
  *   before first use (calls leave the regions that must start at zero at zero). kp a power of two in [2, 8] dividing
- *   page_size; Hi <= 64; H a multiple of 16; Dqk 512 or 576. With splits 0, Dqk 512, H a multiple of 32 and
- *   keep kp <= 4096 / (H / 32) (the token slots in 128-slot splits, 32 workgroups per row) on a GPU of 8 XCDs x 32
- *   CUs, the attention and combine are one XCD-local launch; otherwise the split attention and the combine kernel.
+ *   page_size; Hi <= 64; H a multiple of 16; Dqk 512 or 576. On a GPU of 8 XCDs x 32 CUs, with splits 0, Dqk 512,
+ *   Hi <= 32, rows of at most 8,192 pools (max_pages page_size / kp, a multiple of 4), pages of at least 16 pools
+ *   and keep kp <= 4096 / (H / 32) (H a multiple of 32), the step is one kernel launch per 8 rows (the indexer,
+ *   the selection, the attention and the combine; XCD-local barriers, as dsa_decode_layer's one launch: the same
+ *   co-residency rule and status words). Otherwise it is dsa_pooled_decode_layer_chain.
  */
 int dsa_pooled_decode_layer(const void* q_idx_bf16, const float* w, const void* pool_key_bf16, const void* q_bf16,
                             const uint8_t* kv_fp8, const float* kv_scale, const int32_t* page_table,
@@ -341,6 +343,20 @@ int dsa_pooled_decode_layer(const void* q_idx_bf16, const float* w, const void* 
                             int32_t* cnt, void* out_bf16, float* lse, void* workspace, size_t workspace_bytes, int B,
                             int Hi, int H, int Dqk, int max_pages, int page_size, int num_pages, int kp, int keep,
                             float scale, int splits, void* stream);
+
+/*
+ * The same pooled step as separate kernels enqueued back to back on one stream: the pooled indexer with the top-k's
+ * first-level histogram fused, the top-keep pools, then (splits 0, Dqk 512, H a multiple of 32 and the token slots
+ * in 128-slot splits) the attention and combine as one XCD-local launch, otherwise the split attention and the
+ * combine kernel. Any shape dsa_pooled_decode_layer accepts; same arguments, results and workspace.
+ */
+int dsa_pooled_decode_layer_chain(const void* q_idx_bf16, const float* w, const void* pool_key_bf16,
+                                  const void* q_bf16, const uint8_t* kv_fp8, const float* kv_scale,
+                                  const int32_t* page_table, const int32_t* npool, const int32_t* positions,
+                                  float* scores, int32_t* pools, int32_t* cnt, void* out_bf16, float* lse,
+                                  void* workspace, size_t workspace_bytes, int B, int Hi, int H, int Dqk,
+                                  int max_pages, int page_size, int num_pages, int kp, int keep, float scale,
+                                  int splits, void* stream);
 
 /* Bytes of workspace dsa_pooled_decode_layer needs (max_len: the most pools a row scores). */
 size_t dsa_pooled_workspace_bytes(int B, int H, int keep, int max_len, int kp, int splits);

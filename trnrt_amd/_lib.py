@@ -87,6 +87,11 @@ SIGNATURES: dict[str, tuple] = {
         [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, c_size_t, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
          c_int, c_int, c_float, c_int, P],
     ),
+    "dsa_pooled_decode_layer_chain": (
+        c_int,
+        [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, c_size_t, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
+         c_int, c_int, c_float, c_int, P],
+    ),
     "dsa_pooled_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int]),
     "dsa_sparse_mla_pooled": (
         c_int,

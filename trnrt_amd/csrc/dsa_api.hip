@@ -76,6 +76,14 @@ hipError_t launch_decode_fused(const uint16_t* q_idx, const float* w, const uint
                                const int* ctx_len, float* scores, int* idx, int* cnt, uint16_t* out, float* lse,
                                void* ws, size_t zero_bytes, int B, int Hi, int H, int max_pages, int page_size,
                                int num_pages, int stride, int keep, float scale, hipStream_t s);
+bool fused_pooled_ok(int num_cu, int Hi, int H, int Dqk, int stride, int kp, int page_size, int keep_pools);
+size_t fused_pooled_bytes(size_t zero_bytes, int B, int H);
+hipError_t launch_decode_fused_pooled(const uint16_t* q_idx, const float* w, const uint16_t* pool_key,
+                                      const uint16_t* q, const uint8_t* kv, const float* kvs, const int* table,
+                                      const int* npool, const int* positions, float* scores, int* pools, int* cnt,
+                                      uint16_t* out, float* lse, void* ws, size_t zero_bytes, int B, int Hi, int H,
+                                      int max_pages, int page_size, int num_pages, int kp, int keep_pools,
+                                      float scale, hipStream_t s);
 bool topk_supported(int max_len, int keep, int vis_only);
 hipError_t launch_sparse_mla(const uint16_t* q, const uint8_t* kv, const float* kvs, const int* idx, const int* cnt,
                              const int* table, const int* rows, const float* bias, uint16_t* out, float* out_f32,
@@ -271,6 +279,15 @@ ZeroRecord* zero_record(int dev, const void* ws) {
   return nullptr;
 }
 
+// A record for a workspace the table does not hold (replacing the oldest one).
+ZeroRecord* new_zero_record(int dev, const void* ws) {
+  ZeroRecord* r = &g_zero[g_zero_next];
+  g_zero_next = (g_zero_next + 1) % kZeroRecords;
+  r->dev = dev;
+  r->ws = ws;
+  return r;
+}
+
 // The first `need` bytes of ws zero for the call about to be enqueued on s, and recorded as the call's zero region.
 hipError_t ready_zero(void* ws, size_t need, hipStream_t s) {
   int dev = 0;
@@ -285,12 +302,7 @@ hipError_t ready_zero(void* ws, size_t need, hipStream_t s) {
       return e;
     }
   }
-  if (!r) {
-    r = &g_zero[g_zero_next];
-    g_zero_next = (g_zero_next + 1) % kZeroRecords;
-    r->dev = dev;
-    r->ws = ws;
-  }
+  if (!r) r = new_zero_record(dev, ws);
   r->zero = need;
   return hipSuccess;
 }
@@ -308,7 +320,9 @@ void record_cleared(const void* ws, size_t bytes) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return;
   std::lock_guard<std::mutex> lock(g_zero_mu);
-  if (ZeroRecord* r = zero_record(dev, ws)) r->zero = bytes;
+  ZeroRecord* r = zero_record(dev, ws);
+  if (!r) r = new_zero_record(dev, ws);
+  r->zero = bytes;
 }
 
 std::mutex g_scratch_mu;
@@ -958,17 +972,20 @@ size_t dsa_pooled_workspace_bytes(int B, int H, int keep, int max_len, int kp, i
   const size_t t = align256(dsa::topk_workspace_bytes(B, max_len, keep));
   const size_t a = align256(dsa::attention_workspace_bytes(B, H, sp));
   const size_t x = align256(dsa::attend_xcd_bytes(B, H, keep_sel));
-  return t + (a > x ? a : x);
+  // the one-launch form's layout shares the zero region and needs its own rest (key lists, split outputs)
+  const size_t f = align256(dsa::fused_pooled_bytes(dsa::topk_zero_bytes(B), B, H));
+  const size_t chain = t + (a > x ? a : x);
+  return f > chain ? f : chain;
 }
 
-int dsa_pooled_decode_layer(const void* q_idx_bf16, const float* w, const void* pool_key_bf16, const void* q_bf16,
-                            const uint8_t* kv_fp8, const float* kv_scale, const int32_t* page_table,
-                            const int32_t* npool, const int32_t* positions, float* scores, int32_t* pools,
-                            int32_t* cnt, void* out_bf16, float* lse, void* workspace, size_t workspace_bytes, int B,
-                            int Hi, int H, int Dqk, int max_pages, int page_size, int num_pages, int kp, int keep,
-                            float scale, int splits, void* stream) {
-  if (!q_idx_bf16 || !w || !pool_key_bf16 || !q_bf16 || !kv_fp8 || !page_table || !npool ||
-      !positions || !scores || !pools || !cnt || !out_bf16 || !workspace)
+// The pooled layer's checks (every check before the first launch) and its pool stride; DSA_OK or a status.
+static int pooled_checks(const void* q_idx_bf16, const float* w, const void* pool_key_bf16, const void* q_bf16,
+                         const uint8_t* kv_fp8, const int32_t* page_table, const int32_t* npool,
+                         const int32_t* positions, float* scores, int32_t* pools, int32_t* cnt, void* out_bf16,
+                         void* workspace, size_t workspace_bytes, int B, int Hi, int H, int Dqk, int max_pages,
+                         int page_size, int num_pages, int kp, int keep, int splits, int* stride_out) {
+  if (!q_idx_bf16 || !w || !pool_key_bf16 || !q_bf16 || !kv_fp8 || !page_table || !npool || !positions || !scores ||
+      !pools || !cnt || !out_bf16 || !workspace)
     return DSA_EINVAL;
   if (B < 0 || Hi < 1 || H < 1 || max_pages < 1 || page_size < 1 || num_pages < 1 || keep < 1) return DSA_EINVAL;
   if (kp < 2 || kp > 8 || (kp & (kp - 1)) || page_size % kp) return DSA_EUNSUPPORTED;
@@ -979,7 +996,48 @@ int dsa_pooled_decode_layer(const void* q_idx_bf16, const float* w, const void* 
   if (Hi > 64 || H % 16 || (Dqk != 512 && Dqk != 576)) return DSA_EUNSUPPORTED;
   if (!dsa::topk_supported(stride, keep, 1)) return DSA_EUNSUPPORTED;
   if (workspace_bytes < dsa_pooled_workspace_bytes(B, H, keep, stride, kp, splits)) return DSA_EWORKSPACE;
-  if (B == 0) return DSA_OK;
+  *stride_out = stride;
+  return DSA_OK;
+}
+
+int dsa_pooled_decode_layer(const void* q_idx_bf16, const float* w, const void* pool_key_bf16, const void* q_bf16,
+                            const uint8_t* kv_fp8, const float* kv_scale, const int32_t* page_table,
+                            const int32_t* npool, const int32_t* positions, float* scores, int32_t* pools,
+                            int32_t* cnt, void* out_bf16, float* lse, void* workspace, size_t workspace_bytes, int B,
+                            int Hi, int H, int Dqk, int max_pages, int page_size, int num_pages, int kp, int keep,
+                            float scale, int splits, void* stream) {
+  int stride = 0;
+  const int st = pooled_checks(q_idx_bf16, w, pool_key_bf16, q_bf16, kv_fp8, page_table, npool, positions, scores,
+                               pools, cnt, out_bf16, workspace, workspace_bytes, B, Hi, H, Dqk, max_pages, page_size,
+                               num_pages, kp, keep, splits, &stride);
+  if (st != DSA_OK || B == 0) return st;
+  if (splits != 0 || !dsa::fused_pooled_ok(num_cu(), Hi, H, Dqk, stride, kp, page_size, keep))
+    return dsa_pooled_decode_layer_chain(q_idx_bf16, w, pool_key_bf16, q_bf16, kv_fp8, kv_scale, page_table, npool,
+                                         positions, scores, pools, cnt, out_bf16, lse, workspace, workspace_bytes, B,
+                                         Hi, H, Dqk, max_pages, page_size, num_pages, kp, keep, scale, splits, stream);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (ready_zero(workspace, dsa::topk_zero_bytes(B), s) != hipSuccess) return DSA_ELAUNCH;
+  const int r = status(dsa::launch_decode_fused_pooled(
+      static_cast<const uint16_t*>(q_idx_bf16), w, static_cast<const uint16_t*>(pool_key_bf16),
+      static_cast<const uint16_t*>(q_bf16), kv_fp8, kv_scale, page_table, npool, positions, scores, pools, cnt,
+      static_cast<uint16_t*>(out_bf16), lse, workspace, dsa::topk_zero_bytes(B), B, Hi, H, max_pages, page_size,
+      num_pages, kp, keep, scale, s));
+  if (r != DSA_OK) drop_zero(workspace);
+  return r;
+}
+
+int dsa_pooled_decode_layer_chain(const void* q_idx_bf16, const float* w, const void* pool_key_bf16,
+                                  const void* q_bf16, const uint8_t* kv_fp8, const float* kv_scale,
+                                  const int32_t* page_table, const int32_t* npool, const int32_t* positions,
+                                  float* scores, int32_t* pools, int32_t* cnt, void* out_bf16, float* lse,
+                                  void* workspace, size_t workspace_bytes, int B, int Hi, int H, int Dqk,
+                                  int max_pages, int page_size, int num_pages, int kp, int keep, float scale,
+                                  int splits, void* stream) {
+  int stride = 0;
+  const int st = pooled_checks(q_idx_bf16, w, pool_key_bf16, q_bf16, kv_fp8, page_table, npool, positions, scores,
+                               pools, cnt, out_bf16, workspace, workspace_bytes, B, Hi, H, Dqk, max_pages, page_size,
+                               num_pages, kp, keep, splits, &stride);
+  if (st != DSA_OK || B == 0) return st;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (ready_zero(workspace, dsa::topk_zero_bytes(B), s) != hipSuccess) return DSA_ELAUNCH;
   const int r = pooled_layer(q_idx_bf16, w, pool_key_bf16, q_bf16, kv_fp8, kv_scale, page_table, npool, positions,

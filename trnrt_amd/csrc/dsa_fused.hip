@@ -79,6 +79,20 @@ constexpr int FU_LBINS = FU_LHDR - 4;       // bins in the header
 constexpr int FU_LROW = FU_LHDR + 2 * FU_LCAP;
 static_assert(FU_LBINS == 28, "two header bins for each of 14 of a list's 16 threads");
 static_assert(FU_LM <= FU_LCAP && FU_LPT % 2 == 0, "key list");
+// The layer's two forms: kpool 1 (FP8 keys with per-token scales; a workgroup's key list reaches down to the bin of
+// its FU_LM-th largest key) and pooled (GLM's kpool > 1: the scores of bf16 pool keys with no scale, rows of at most
+// 8,192 pools, so blocks of at most 256, every one of which its workgroup's list holds: the one-exchange selection
+// always applies).
+template <bool POOL>
+struct FuForm {
+  static constexpr int LPT = POOL ? 16 : FU_LPT;  // list entries per reading thread
+  static constexpr int LCAP = 16 * LPT;
+  static constexpr int LROW = FU_LHDR + 2 * LCAP;
+  static constexpr int KV = POOL ? 8 : 4;       // 16-byte key loads per lane and tile (64 bf16 or 64 e4m3 dims)
+  static constexpr int TILE_LOADS = POOL ? 8 : 5;  // load instructions per lane and tile (with the scale)
+  static_assert(LROW % 32 == 0 && LPT % 2 == 0, "key list");
+};
+constexpr int FU_POOL_MAXLEN = FU_NW * FuForm<true>::LCAP;  // 8,192 pools
 static_assert(FU_HROW % 32 == 0 && FU_CROW % 32 == 0 && FU_LROW % 32 == 0, "a workgroup's rows in lines of its own");
 constexpr int FU_HPW = 16;         // heads per MFMA block of the attention
 constexpr int FU_CH = 64;          // slot granularity of a split
@@ -183,7 +197,7 @@ struct FusedArgs {
   uint32_t* cand;  // [B][32][1088]: per workgroup (keys above c0) << 16 | (candidates), the bitmap of its positions
                    // above c0 (32 words), then the candidates, (low 20 key bits << 10) | position in the workgroup's
                    // range, in position order
-  uint32_t* lst;   // [B][32][FU_LROW]: per workgroup its key list
+  uint32_t* lst;   // [B][32][FuForm::LROW]: per workgroup its key list
   uint16_t* part;  // [B][S][H][512]: split outputs (normalised, bf16), a split's heads side by side
 
   float2* ml;      // [B][H][S]: split max and sum
@@ -196,6 +210,7 @@ struct FusedArgs {
   const int* npool;
   const int* positions;
   int kp_shift;
+  int ppp_shift;  // the pooled one-launch layer: log2 of the pools per page (pool p's key: page row p >> ppp_shift)
   int row0;  // this launch's first row (rows row0 .. row0 + 7)
 };
 
@@ -319,10 +334,12 @@ __device__ __forceinline__ void fu_store_scores(const FusedArgs& a, const uint8_
 }
 
 // Whether a row of L tokens takes the one-exchange selection from the key lists (workgroup-uniform): every list holds
-// all its workgroup's keys (kw <= FU_LCAP), or the workgroups select at most 80 keys each on average.
+// all its workgroup's keys (kw <= LCAP: the pooled form always), or the workgroups select at most 80 keys each on
+// average.
+template <bool POOL = false>
 __device__ __forceinline__ bool fu_lists_on(const FusedArgs& a, int L) {
   const int kw = fu_kw(L);
-  return kw <= FU_LCAP || (long)a.keep * kw * 8 <= 5L * FU_LM * L;
+  return POOL || kw <= FU_LCAP || (long)a.keep * kw * 8 <= 5L * FU_LM * L;
 }
 
 // This thread's two keys (positions tid, tid + 512 of the workgroup's block; 0: not selectable, as every position past
@@ -337,9 +354,12 @@ __device__ __forceinline__ void fu_my_keys(const uint8_t* lds, uint32_t (&key)[2
 // Stage 1: the indexer scores of positions kw j .. kw j + kw - 1 of row b (L: the row's length, kw = fu_kw(L)): the
 // block's tiles (32 keys each) go to the waves in turn, wave v taking tiles v, v + 8, v + 16, v + 24 of the block (the
 // ones the block has) and streaming them FU_AHEAD ahead of its MFMAs. LDS holds the scores of all 1024 positions of
-// the workgroup's range, NEG_INF past the block.
-template <int MT>
+// the workgroup's range, NEG_INF past the block. The pooled form (POOL) scores pools: a position is a pool, its key
+// 128 bf16 with no scale at page row p >> ppp_shift (trnrt/models/mla.py:615-630), the arithmetic of the bf16 decode
+// indexer; its key list holds every key of the block, so it writes no bin list (no two-exchange selection reads one).
+template <int MT, bool POOL = false>
 __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int b, int j, int L) {
+  using FF = FuForm<POOL>;
   uint16_t* qs = reinterpret_cast<uint16_t*>(lds + L_QS);
   float* wsh = reinterpret_cast<float*>(lds + L_WS);
   int* hs = reinterpret_cast<int*>(lds + L_HS);
@@ -349,7 +369,7 @@ __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int
   const int Hi = a.Hi;
   float* srow = a.scores + (size_t)b * a.stride;
   // a row that selects from the key lists writes its scores after barrier A; the others as each tile is scored
-  const bool lists = fu_lists_on(a, L);
+  const bool lists = fu_lists_on<POOL>(a, L);
 
   // the queries' loads (32 MT heads of 16 pieces: MT per thread), the weights, the tiles' pages
   u32x4 qv[MT];
@@ -370,22 +390,39 @@ __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int
   };
   const int* trow = a.table + (size_t)b * a.max_pages;
   int pages = 0;
-  {
+  if (POOL) {
+    // a tile of 32 pools spans two page rows of 16 pools (or lies inside one of 32 or more): lane 2 i + u holds the
+    // page of tile i's pools 32 t + 16 u ..
+    const int i = min(lane >> 1, FU_TPW - 1), u = lane & 1;
+    const int t = t_begin + FU_WAVES * i;
+    const int pg = trow[min((t * FU_TILE + 16 * u) >> a.ppp_shift, a.max_pages - 1)];
+    pages = in_row(i) ? safe_page(pg, a.num_pages) : 0;
+  } else {
     const int i = min(lane, FU_TPW - 1);
     const int t = t_begin + FU_WAVES * i;
     const int pg = trow[min((t * FU_TILE) >> a.page_shift, a.max_pages - 1)];
     pages = in_row(i) ? safe_page(pg, a.num_pages) : 0;
   }
-  u32x4 kv[FU_TPW][4];
+  u32x4 kv[FU_TPW][FF::KV];
   float ksc[FU_TPW];
   auto tile_loads = [&](int i) __attribute__((always_inline)) {
     const int t0 = (t_begin + FU_WAVES * i) * FU_TILE;
-    const int page = __builtin_amdgcn_readlane(pages, i);
-    const size_t slot = in_row(i) ? (size_t)page * a.page_size + (t0 & (a.page_size - 1)) + jk : (size_t)jk;
-    const uint8_t* kp = a.k + slot * FU_D + 64 * h;
+    if (POOL) {
+      const int pa = __builtin_amdgcn_readlane(pages, 2 * i), pb = __builtin_amdgcn_readlane(pages, 2 * i + 1);
+      const int ppp = 1 << a.ppp_shift;
+      const size_t row = (size_t)(in_row(i) ? (jk < 16 ? pa : pb) : 0) * ppp + ((t0 + jk) & (ppp - 1));
+      const uint8_t* kp = a.k + row * (2 * FU_D) + 128 * h;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) kv[i][c] = *reinterpret_cast<const u32x4*>(kp + 16 * c);
-    ksc[i] = a.ks[slot];
+      for (int c = 0; c < FF::KV; ++c) kv[i][c] = *reinterpret_cast<const u32x4*>(kp + 16 * c);
+      ksc[i] = 1.0f;
+    } else {
+      const int page = __builtin_amdgcn_readlane(pages, i);
+      const size_t slot = in_row(i) ? (size_t)page * a.page_size + (t0 & (a.page_size - 1)) + jk : (size_t)jk;
+      const uint8_t* kp = a.k + slot * FU_D + 64 * h;
+#pragma unroll
+      for (int c = 0; c < FF::KV; ++c) kv[i][c] = *reinterpret_cast<const u32x4*>(kp + 16 * c);
+      ksc[i] = a.ks[slot];
+    }
   };
   if (live) {
 #pragma unroll
@@ -421,7 +458,7 @@ __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int
       if (i + FU_AHEAD < FU_TPW) {
         // tile i has arrived (the later tiles in flight may still be outstanding): issue tile i + FU_AHEAD (the
         // compiler's own wait before tile i's first use keeps the data exact)
-        __builtin_amdgcn_s_waitcnt(vmcnt_wait(5 * (FU_AHEAD - 1)));
+        __builtin_amdgcn_s_waitcnt(vmcnt_wait(FF::TILE_LOADS * (FU_AHEAD - 1)));
         __builtin_amdgcn_sched_barrier(0);
         tile_loads(i + FU_AHEAD);
         __builtin_amdgcn_sched_barrier(0);
@@ -435,8 +472,13 @@ __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int
         for (int r = 0; r < 16; ++r) acc[m][r] = 0.0f;
 #pragma unroll
       for (int s = 0; s < 8; ++s) {
-        const u32x4 k4 = kv[i][s >> 1];
-        const bf16x8 kb = (s & 1) ? fp8x8_to_bf16x8(k4[2], k4[3]) : fp8x8_to_bf16x8(k4[0], k4[1]);
+        bf16x8 kb;
+        if (POOL) {
+          kb = __builtin_bit_cast(bf16x8, kv[i][s]);
+        } else {
+          const u32x4 k4 = kv[i][s >> 1];
+          kb = (s & 1) ? fp8x8_to_bf16x8(k4[2], k4[3]) : fp8x8_to_bf16x8(k4[0], k4[1]);
+        }
 #pragma unroll
         for (int m = 0; m < MT; ++m) acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa[m][s], kb, acc[m], 0, 0, 0);
       }
@@ -446,7 +488,7 @@ __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int
 #pragma unroll
         for (int r = 0; r < 16; ++r) part = fmaf(wr[m][r], relu(acc[m][r]), part);
       part += __shfl_xor(part, 32, WAVE);
-      const float v = mine && pos < L ? part * ksc[i] : NEG_INF;
+      const float v = mine && pos < L ? (POOL ? part : part * ksc[i]) : NEG_INF;
       if (h == 0) {
         if (!lists && mine && pos < a.stride) srow[pos] = v;
         scs[e] = v;
@@ -473,7 +515,9 @@ __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int
   *reinterpret_cast<int4*>(hv) = *reinterpret_cast<const int4*>(hs + 8 * tid);
   *reinterpret_cast<int4*>(hv + 4) = *reinterpret_cast<const int4*>(hs + 8 * tid + 4);
   int lbin = FU_HBINS, lcnt = 0;  // no list
-  if (lists) {
+  if (POOL) {
+    lbin = 0;  // every key of the block (at most 256), whatever their bins; counted by the prefix below
+  } else if (lists) {
     int lb, labove;
     const int nv = fu_find_bin<8>(hv, FU_LM, scr, &lb, &labove);
     lbin = 0;
@@ -494,14 +538,15 @@ __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int
   uint32_t tot;
   const uint32_t before = fu_block_prefix((nz << 20) | ((uint32_t)in0 << 10) | (uint32_t)in1, scr, &tot);
   uint32_t* hl = a.hl + ((size_t)b * FU_NW + j) * FU_HROW;
-  uint32_t* lrow = a.lst + ((size_t)b * FU_NW + j) * FU_LROW;
+  uint32_t* lrow = a.lst + ((size_t)b * FU_NW + j) * FF::LROW;
   const int nzt = (int)(tot >> 20);
+  if (POOL) lcnt = (int)(((tot >> 10) & 1023u) + (tot & 1023u));
   uint32_t o = before >> 20;
 #pragma unroll
   for (int i = 0; i < 8; ++i)
     if (hv[i]) {
       const uint32_t e = ((uint32_t)(8 * tid + i) << 16) | (uint32_t)hv[i];
-      hl[1 + o] = e;
+      if (!POOL) hl[1 + o] = e;
       const int d = nzt - 1 - (int)o;  // this bin's place among the nonzero bins from the top
       if (lists && d < FU_LBINS) lrow[4 + d] = e;
       ++o;
@@ -515,7 +560,7 @@ __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int
     if (tid >= nzt && tid < FU_LBINS) lrow[4 + tid] = 0u;
     if (tid == 0) *reinterpret_cast<uint4*>(lrow) = uint4{(uint32_t)lcnt, (uint32_t)lbin, 0u, 0u};
   }
-  if (tid == 0) hl[0] = (uint32_t)nzt;
+  if (!POOL && tid == 0) hl[0] = (uint32_t)nzt;
 }
 
 // Stage 2: the first level from the row histogram, this workgroup's keys above it counted and its candidates written.
@@ -849,12 +894,18 @@ __device__ __forceinline__ int fu_select(const FusedArgs& a, uint8_t* lds, int b
 // (three histogram passes over their keys: 12, 12 and 8 bits; then per list its counts above and at T): the
 // workgroup writes the indices and lists the cache slots of its split's outputs [o0, o1) straight from its listed
 // keys. Returns false when the lists do not hold the selection (every workgroup of the row decides alike, and nothing
-// but LDS has been written): the caller then takes the two-exchange form.
-template <int HPW>
+// but LDS has been written): the caller then takes the two-exchange form. The pooled form (POOL: every list holds its
+// whole block, so this never returns false) selects pools: each selected pool in the split lists its kpool token
+// slots, and the split holding the row's last selected pool (split 0 when none is) lists the row's tail tokens
+// kpool npool .. position after them (trnrt/models/dsa_long.py:189-215, the masked slots left out).
+template <int HPW, bool POOL = false>
 __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds, int b, int j, int L,
-                                                u32x4 (&qv)[FuAtt<HPW>::QPT], float* live_bias, int* n_slots) {
-  using AT = FuAtt<HPW>;
-  constexpr int QPT = AT::QPT;
+                                                u32x4 (&qv)[FuAtt<HPW, POOL ? 512 : FU_DQK, POOL>::QPT],
+                                                float* live_bias, int* n_slots) {
+  constexpr int DQK = POOL ? 512 : FU_DQK;
+  using AT = FuAtt<HPW, DQK, POOL>;
+  using FF = FuForm<POOL>;
+  constexpr int QPT = AT::QPT, LPT = FF::LPT;
   FuState& st = *reinterpret_cast<FuState*>(lds + L_STATE);
   int* scr = reinterpret_cast<int*>(lds + L_MISC);
   int* bins0 = reinterpret_cast<int*>(lds + L_CB);
@@ -862,19 +913,21 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
   int* bins2 = reinterpret_cast<int*>(lds + L_BINS2);
   int* spg = reinterpret_cast<int*>(lds + L_SPG);
   int* slot_l = reinterpret_cast<int*>(lds + AT::L_P);
-  // the split's output positions, stored to idx in one coalesced pass at the end; entry CAP of each list is a sink
-  int* pos_l = slot_l + AT::CAP + 1;
-  static_assert(4 * (2 * AT::CAP + 2) <= 2 * HPW * AT::PROW, "slot and position lists inside P's region");
+  // the split's output positions, stored to idx in one coalesced pass at the end; the entries past CAP (slots) and
+  // past SPLIT (positions) are sinks for the writes of entries outside the split
+  constexpr int SLOT_SINK = AT::CAP, POS_SINK = AT::SPLIT;
+  int* pos_l = slot_l + AT::CAP + 8;
+  static_assert(4 * (AT::CAP + 8 + AT::SPLIT + 1) <= 2 * HPW * AT::PROW, "slot and position lists inside P's region");
   const int tid = threadIdx.x, wave = tid / WAVE, lane = tid & (WAVE - 1);
   const int w = tid >> 4, q = tid & 15;
   const int hg = j % a.HG, s = j / a.HG;
   const bool active = s < a.S;  // workgroup-uniform: a workgroup past the last split only helps with the barriers
   const int o0 = active ? s * a.sps : 0, o1 = active ? min(o0 + a.sps, a.keep) : 0;
   // list w's counts and this thread's entries (device-coherent buffer loads: the lists are the peers' stores)
-  constexpr int NL = FU_LPT / 2;
+  constexpr int NL = LPT / 2;
   const __amdgpu_buffer_rsrc_t lrs = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(a.lst + (size_t)b * FU_NW * FU_LROW), (short)0, FU_NW * FU_LROW * 4, FU_BUF_WORD3);
-  const int lo = 4 * FU_LROW * w;
+      (void*)(a.lst + (size_t)b * FU_NW * FF::LROW), (short)0, FU_NW * FF::LROW * 4, FU_BUF_WORD3);
+  const int lo = 4 * FF::LROW * w;
   const uint32_t hw0 = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(lrs, lo, 0, FU_AUX_PLAIN);
   const uint32_t hw1 = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(lrs, lo + 4, 0, FU_AUX_PLAIN);
   // header bins 2 q, 2 q + 1 (threads q < 14)
@@ -885,7 +938,7 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
 #pragma unroll
   for (int i = 0; i < NL; ++i)
     ev[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                          lrs, lo + 4 * FU_LHDR + 8 * FU_LPT * q + 16 * i, 0, FU_AUX_PLAIN));
+                                          lrs, lo + 4 * FU_LHDR + 8 * LPT * q + 16 * i, 0, FU_AUX_PLAIN));
   __builtin_amdgcn_sched_barrier(0);
   // the row's pages into registers (pages tid, tid + 512, clamped: at most 1024 pages of at least 32 tokens), staged
   // in LDS at the end (loads straight into LDS here would make every LDS access below wait for all loads, the
@@ -893,7 +946,8 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
   int pgv[2];
   {
     const int* trow = a.table + (size_t)b * a.max_pages;
-    const int npg = (L + a.page_size - 1) >> a.page_shift;
+    // (pooled: the pages of pools 0 .. L, the last the tail pool's)
+    const int npg = POOL ? (L >> a.ppp_shift) + 1 : (L + a.page_size - 1) >> a.page_shift;
 #pragma unroll
     for (int c = 0; c < 2; ++c) pgv[c] = trow[max(min(min(tid + FU_THREADS * c, npg - 1), a.max_pages - 1), 0)];
   }
@@ -901,23 +955,24 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
   {
     // (unconditional: a workgroup past the last split loads its head group's queries and never uses them, and no
     // register copy of a query waits for its load at a join)
-    const u32x4* qsrc = reinterpret_cast<const u32x4*>(a.q + ((size_t)b * a.H + HPW * hg) * FU_DQK);
+    const u32x4* qsrc = reinterpret_cast<const u32x4*>(a.q + ((size_t)b * a.H + HPW * hg) * DQK);
 #pragma unroll
-    for (int i = 0; i < QPT; ++i) qv[i] = qsrc[min(tid + FU_THREADS * i, HPW * FU_DQK / 8 - 1)];
+    for (int i = 0; i < QPT; ++i) qv[i] = qsrc[min(tid + FU_THREADS * i, HPW * DQK / 8 - 1)];
   }
   const int kw = fu_kw(L);
   fu_store_scores(a, lds, b, j, kw);
   __builtin_amdgcn_sched_barrier(0);
   for (int i = tid; i < 4096; i += FU_THREADS) bins0[i] = bins1[i] = 0;
   if (tid < 256) bins2[tid] = 0;
-  if (tid < AT::SPLIT) slot_l[tid] = pos_l[tid] = 0;  // padding rows read slot 0; outputs past the count are 0
+  if (tid < AT::CAP) slot_l[tid] = 0;  // padding rows read slot 0
+  if (tid < AT::SPLIT) pos_l[tid] = 0;  // outputs past the count are 0
   if (tid == 0) scr[8] = scr[24] = scr[40] = -1;
   __builtin_amdgcn_sched_barrier(0);
   __syncthreads();  // the bins cleared (the loads above may be out; their first uses wait for them)
-  const int nw = min((int)hw0, FU_LCAP) - FU_LPT * q;  // this thread's entries: those below nw
-  uint32_t key[FU_LPT], pos[FU_LPT];
+  const int nw = min((int)hw0, FF::LCAP) - LPT * q;  // this thread's entries: those below nw
+  uint32_t key[LPT], pos[LPT];
 #pragma unroll
-  for (int i = 0; i < FU_LPT; ++i) {
+  for (int i = 0; i < LPT; ++i) {
     key[i] = i < nw ? ev[i / 2][2 * (i & 1)] : 0u;
     pos[i] = ev[i / 2][2 * (i & 1) + 1] & 1023u;
   }
@@ -925,14 +980,14 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
   // passes (twelve 64-bit masks held in scalar registers spill)
   auto fresh = [&]() __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < FU_LPT; ++i) asm volatile("" : "+v"(key[i]));
+    for (int i = 0; i < LPT; ++i) asm volatile("" : "+v"(key[i]));
   };
   // the first level from the lists' header bins (their bins at or above the lowest listed are exactly the listed
   // keys' bins); a list whose 28th header bin is listed may list more bins than its header holds: its keys one by one
   const bool hfull = q == FU_LBINS / 2 - 1 && hp[1] != 0u && (hp[1] >> 16) >= hw1;
   if ((__ballot(hfull) >> (16 * (w & 3))) & 0xFFFFull) {
 #pragma unroll
-    for (int i = 0; i < FU_LPT; ++i)
+    for (int i = 0; i < LPT; ++i)
       if (key[i]) atomicAdd(&bins0[key[i] >> 20], 1);
   } else if (q < FU_LBINS / 2) {
 #pragma unroll
@@ -963,7 +1018,7 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
   int room = 0;
   if (c0 >= 0) {
 #pragma unroll
-    for (int i = 0; i < FU_LPT; ++i)
+    for (int i = 0; i < LPT; ++i)
       if (key[i] && (int)(key[i] >> 20) == c0) atomicAdd(&bins1[(key[i] >> 8) & 4095u], 1);
     fresh();
     __syncthreads();
@@ -981,7 +1036,7 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
     } else {
       const uint32_t hi24 = ((uint32_t)c0 << 12) | (uint32_t)c1;
 #pragma unroll
-      for (int i = 0; i < FU_LPT; ++i)
+      for (int i = 0; i < LPT; ++i)
         if (key[i] && (key[i] >> 8) == hi24) atomicAdd(&bins2[key[i] & 255u], 1);
       fresh();
       __syncthreads();
@@ -999,7 +1054,7 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
   // index; a selected key's index is its list's first plus the selected keys before it in the list
   uint32_t mine = 0;
 #pragma unroll
-  for (int i = 0; i < FU_LPT; ++i) mine += (key[i] > T ? 1u : 0u) + (key[i] == T && key[i] ? 0x10000u : 0u);
+  for (int i = 0; i < LPT; ++i) mine += (key[i] > T ? 1u : 0u) + (key[i] == T && key[i] ? 0x10000u : 0u);
   fresh();
   const uint32_t incl = (uint32_t)row_incl_scan((int)mine);
   if (q == 15) {
@@ -1024,8 +1079,8 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
 #pragma unroll
     for (int i = 0; i < QPT; ++i) {
       const int pc = tid + FU_THREADS * i;
-      if (active && pc < HPW * FU_DQK / 8)
-        *reinterpret_cast<u32x4*>(qs + (pc / (FU_DQK / 8)) * FU_AQROW + 8 * (pc % (FU_DQK / 8))) = qv[i];
+      if (active && pc < HPW * DQK / 8)
+        *reinterpret_cast<u32x4*>(qs + (pc / (DQK / 8)) * AT::AQROW + 8 * (pc % (DQK / 8))) = qv[i];
     }
   }
   {
@@ -1037,30 +1092,56 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
     const int first = off_l + gtb + min(eqb, take_l);
     const int nsel = (int)(mine & 0xFFFFu) + min(max(take_l - eqb, 0), (int)(mine >> 16));
     if (nsel > 0 && first < o1 && first + nsel > o0) {
-      int oi[FU_LPT], pg[FU_LPT];
+      int oi[LPT], pg[LPT];
 #pragma unroll
-      for (int i = 0; i < FU_LPT; ++i) {
+      for (int i = 0; i < LPT; ++i) {
         const bool above = key[i] > T, tie = key[i] == T && key[i];
         const int o = off_l + gtb + min(eqb, take_l) - o0;
-        oi[i] = (above || (tie && eqb < take_l)) && (unsigned)o < (unsigned)(o1 - o0) ? o : AT::CAP;
+        oi[i] = (above || (tie && eqb < take_l)) && (unsigned)o < (unsigned)(o1 - o0) ? o : -1;
         gtb += above;
         eqb += tie;
       }
+      const int shift = POOL ? a.ppp_shift : a.page_shift;
 #pragma unroll
-      for (int i = 0; i < FU_LPT; ++i) pg[i] = spg[(kw * w + (int)pos[i]) >> a.page_shift];
+      for (int i = 0; i < LPT; ++i) pg[i] = spg[(kw * w + (int)pos[i]) >> shift];
 #pragma unroll
-      for (int i = 0; i < FU_LPT; ++i) {
-        const int p = kw * w + (int)pos[i];  // the key's position in the row
-        slot_l[oi[i]] = safe_page(pg[i], a.num_pages) * a.page_size + (p & (a.page_size - 1));
-        pos_l[oi[i]] = p;
+      for (int i = 0; i < LPT; ++i) {
+        const int p = kw * w + (int)pos[i];  // the key's position (pooled: pool) in the row
+        const int page = safe_page(pg[i], a.num_pages);
+        if (POOL) {
+          // the pool's kpool tokens: consecutive slots of its page
+          const int kp = 1 << a.kp_shift;
+          const int base = page * a.page_size + ((p & ((1 << a.ppp_shift) - 1)) << a.kp_shift);
+          const int si = oi[i] >= 0 ? oi[i] << a.kp_shift : SLOT_SINK;
+          for (int t = 0; t < kp; ++t) slot_l[si + t] = base + t;
+        } else {
+          slot_l[oi[i] >= 0 ? oi[i] : SLOT_SINK] = page * a.page_size + (p & (a.page_size - 1));
+        }
+        pos_l[oi[i] >= 0 ? oi[i] : POS_SINK] = p;
       }
     }
   }
   if (j == 0 && tid == 0) a.cnt[b] = cnt_row;
   // the split's live slots; a row with none attends position 0 masked (its lse is NEG_INF)
   int ns = max(min(o1, cnt_row) - o0, 0);
+  bool empty = cnt_row == 0;
+  if (POOL) {
+    // the selected pools' token slots, then (in the split of the last selected pool) the tail's: tokens
+    // kpool L .. position of the incomplete pool L, in that pool's page
+    ns <<= a.kp_shift;
+    const int tail_pos0 = L << a.kp_shift;
+    const int tail = min(max(a.positions[b] + 1 - tail_pos0, 0), (1 << a.kp_shift) - 1);
+    const int s_last = cnt_row > 0 ? (cnt_row - 1) / a.sps : 0;
+    if (active && s == s_last && tail > 0) {
+      if (tid < tail)
+        slot_l[ns + tid] = safe_page(spg[L >> a.ppp_shift], a.num_pages) * a.page_size +
+                           ((tail_pos0 + tid) & (a.page_size - 1));
+      ns += tail;
+    }
+    empty = cnt_row == 0 && tail == 0;
+  }
   *live_bias = 0.0f;
-  if (active && cnt_row == 0 && s == 0) {
+  if (active && empty && s == 0) {
     ns = 1;
     *live_bias = NEG_INF;
     if (tid == 0) slot_l[0] = safe_page(a.table[(size_t)b * a.max_pages], a.num_pages) * a.page_size;
@@ -1399,6 +1480,32 @@ __global__ __launch_bounds__(FU_THREADS, 1) void decode_fused_kernel(FusedArgs a
   fu_exit(sync);
 }
 
+// The pooled (GLM, kpool > 1) decode layer step in one launch (trnrt/models/mla.py:505-526 `attention_long` for a
+// decode batch, trnrt/kernels/dsa_shell.py:2114-2321 `select2` and trnrt/kernels/dsa_satwf.py:1-20 for the served
+// form): row b of rows row0 .. row0 + 7 on XCD b % 8, its npool[b] complete pools (at most 8,192) scored from the
+// bf16 pool-key cache in blocks of at most 256 pools, the exact top-keep pools from the key lists (each holding its
+// whole block), then the attention over the selected pools' tokens and the row's tail (512-wide rows, 32 heads a
+// workgroup, splits of 128 token slots) and the combine, as the kpool-1 layer.
+template <int HPW>
+__global__ __launch_bounds__(FU_THREADS, 1) void decode_pooled_fused_kernel(FusedArgs a) {
+  __shared__ __align__(16) uint8_t lds[FU_LDS];
+  const int x = blockIdx.x % FU_XCDS, j = blockIdx.x / FU_XCDS;
+  int* sync = a.sync + x * WS_SYNC_WORDS;
+  const int b = a.row0 + x;
+  if (b >= a.B) return;  // an XCD without a row
+  const int L = min(max(a.ctx_len[b], 0), min(a.stride, FU_POOL_MAXLEN));
+  fu_indexer<1, true>(a, lds, b, j, L);
+  fu_barrier(sync, 1);  // A: the row's scores and key lists
+  u32x4 qv[FuAtt<HPW, 512, true>::QPT];
+  float live_bias;
+  int n_slots;
+  fu_select_lists<HPW, true>(a, lds, b, j, L, qv, &live_bias, &n_slots);  // (the lists hold every key)
+  fu_attend<HPW, 512, true>(a, lds, b, j, n_slots, live_bias);
+  fu_barrier(sync, 2);  // C: every split's output
+  fu_combine(a, lds, b, j);
+  fu_exit(sync);
+}
+
 // The split's slot list when the selection came from the separate kernels: output positions o0 .. o1 - 1 of row b,
 // as cache rows (rows [B, keep], the top-k's slot output) or as positions (idx [B, keep]) through the page table;
 // the attention's queries staged in LDS as stage 2 stages them. Returns the split's selected count (the empty row:
@@ -1700,6 +1807,89 @@ hipError_t launch_decode_fused(const uint16_t* q_idx, const float* w, const uint
                               : launch("decode_fused_kernel", decode_fused_kernel<1, 16>, grid, block, s, a))
                  : (hpw == 32 ? launch("decode_fused_kernel", decode_fused_kernel<2, 32>, grid, block, s, a)
                               : launch("decode_fused_kernel", decode_fused_kernel<2, 16>, grid, block, s, a));
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+
+// The pooled one-launch layer: whether it takes a step (a GPU of 8 XCDs x 32 CUs, 512-wide latent rows, at most 32
+// indexer heads, rows of at most 8,192 pools, pages of a power-of-two number of at least 16 pools, and a keep whose
+// token slots the 32-head splits of 128 hold), and its workspace past the zero region: the key lists, the split
+// outputs and their (max, sum).
+bool fused_pooled_ok(int num_cu, int Hi, int H, int Dqk, int stride, int kp, int page_size, int keep_pools) {
+  if (num_cu != FU_XCDS * FU_NW || Dqk != 512 || Hi < 1 || Hi > 32 || keep_pools < 1) return false;
+  if (kp < 2 || kp > 8 || (kp & (kp - 1)) || page_size % kp) return false;
+  const int ppp = page_size / kp;
+  if (ppp < 16 || (ppp & (ppp - 1)) || stride < 1 || stride > FU_POOL_MAXLEN || stride % 4) return false;
+  return fused_hpw(H, keep_pools * kp) == 32 && FuAtt<32>::SPLIT % kp == 0;
+}
+
+size_t fused_pooled_bytes(size_t zero_bytes, int B, int H) {
+  if (H < 32 || H % 32) return 0;
+  const int S = fused_splits(H, 32);
+  size_t off = zero_bytes;
+  off += fu_up256((size_t)B * FU_NW * FuForm<true>::LROW * 4);
+  off += fu_up256((size_t)B * S * H * FU_DV * 2);
+  off += fu_up256((size_t)B * S * H * sizeof(float2));
+  return off;
+}
+
+hipError_t launch_decode_fused_pooled(const uint16_t* q_idx, const float* w, const uint16_t* pool_key,
+                                      const uint16_t* q, const uint8_t* kv, const float* kvs, const int* table,
+                                      const int* npool, const int* positions, float* scores, int* pools, int* cnt,
+                                      uint16_t* out, float* lse, void* ws, size_t zero_bytes, int B, int Hi, int H,
+                                      int max_pages, int page_size, int num_pages, int kp, int keep_pools,
+                                      float scale, hipStream_t s) {
+  FusedArgs a{};
+  const int S = fused_splits(H, 32);
+  char* p = static_cast<char*>(ws);
+  const size_t lst = zero_bytes;
+  const size_t part = lst + fu_up256((size_t)B * FU_NW * FuForm<true>::LROW * 4);
+  const size_t ml = part + fu_up256((size_t)B * S * H * FU_DV * 2);
+  const int ppp = page_size / kp;
+  a.q_idx = q_idx;
+  a.w = w;
+  a.k = reinterpret_cast<const uint8_t*>(pool_key);
+  a.ks = nullptr;
+  a.q = q;
+  a.kv = kv;
+  a.kvs = kvs;
+  a.table = table;
+  a.ctx_len = npool;
+  a.scores = scores;
+  a.idx = pools;
+  a.cnt = cnt;
+  a.out = out;
+  a.lse = lse;
+  a.hl = nullptr;  // (no bin lists: the pooled form's key lists hold every key)
+  a.sync = reinterpret_cast<int*>(p);  // the workspace's first bytes
+  a.cand = nullptr;
+  a.lst = reinterpret_cast<uint32_t*>(p + lst);
+  a.part = reinterpret_cast<uint16_t*>(p + part);
+  a.ml = reinterpret_cast<float2*>(p + ml);
+  a.B = B;
+  a.Hi = Hi;
+  a.H = H;
+  a.max_pages = max_pages;
+  a.page_size = page_size;
+  a.page_shift = __builtin_ctz((unsigned)page_size);
+  a.num_pages = num_pages;
+  a.num_slots = num_pages * page_size;
+  a.stride = max_pages * ppp;
+  a.keep = keep_pools;
+  a.scale = scale;
+  a.HG = H / 32;
+  a.S = S;
+  a.sps = FuAtt<32>::SPLIT / kp;  // pools per split (their token slots fill one split)
+  a.npool = npool;
+  a.positions = positions;
+  a.kp_shift = __builtin_ctz((unsigned)kp);
+  a.ppp_shift = __builtin_ctz((unsigned)ppp);
+  const dim3 grid(FU_XCDS * FU_NW), block(FU_THREADS);
+  for (int r0 = 0; r0 < B; r0 += FU_XCDS) {
+    a.row0 = r0;
+    const hipError_t e = launch("decode_pooled_fused_kernel", decode_pooled_fused_kernel<32>, grid, block, s, a);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;

@@ -81,6 +81,17 @@ def cached_workspace(device: torch.device, nbytes: int, use: str) -> torch.Tenso
     key = (device.index if device.index is not None else torch.cuda.current_device(), stream_ptr(device), use)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+        ws = zeroed_workspace(max(int(nbytes), 256), device)
         _WORKSPACES[key] = ws
+    return ws
+
+
+def zeroed_workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    """A new uint8 device buffer of nbytes (a multiple of 256) zero-filled by the library's dsa_workspace_clear on the
+    current stream, which also records it as zero, so its first call does not fill it again."""
+    from .. import _lib
+
+    n = (int(nbytes) + 255) // 256 * 256
+    ws = torch.empty(n, dtype=torch.uint8, device=device)
+    _lib.check(_lib.lib().dsa_workspace_clear(ws.data_ptr(), n, stream_ptr(device)), "dsa_workspace_clear")
     return ws

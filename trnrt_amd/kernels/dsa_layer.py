@@ -62,7 +62,7 @@ class DecodeLayer:
         self.lse = torch.empty(B, H, dtype=torch.float32, device=dev)
         wsb = _lib.workspace_bytes(_lib.DSA_WS_LAYER, B, H, keep, self.max_len, splits)
         # zero once: the calls keep the regions that must start at zero (the top-k histograms) at zero
-        self.workspace = torch.zeros(max(wsb, 256), dtype=torch.uint8, device=dev)
+        self.workspace = C.zeroed_workspace(max(wsb, 256), dev)
 
     def status(self, clear: bool = False) -> dict:
         """The workspace's status words since the last clear (synchronises the current stream): `gave_up`, barrier
@@ -76,8 +76,8 @@ class DecodeLayer:
         """(out bf16 [B, H, 512], lse fp32 [B, H]) of one layer step; self.scores / idx / cnt hold the intermediates.
         q_idx [B, Hi, 128] bf16, w [B, Hi] fp32 (D ** -0.5 folded in), k_cache [slots, 128] e4m3fn + k_scale [slots],
         q [B, H, 576] bf16, kv_cache [slots, 576] e4m3fn + kv_scale [slots] (None: the reference's unscaled cache),
-        table [B, max_pages] int32, ctx_len [B]
-        int32 (each <= max_len). check=False skips the Python-side argument checks (the C ABI still checks sizes).
+        table [B, max_pages] int32, ctx_len [B] int32 (each <= max_len). check=False skips the Python-side argument
+        checks (the C ABI still checks sizes).
         verify=True synchronises after the step and raises RuntimeError if a barrier wait of this or an earlier
         unverified step gave up (clearing the count)."""
         B, Hi, H = self.B, self.Hi, self.H
@@ -114,14 +114,17 @@ class PooledDecodeLayer:
     """Buffers and launch parameters of a pooled (GLM, kpool kp > 1) decode step over B rows with up to max_pages
     pages each: the pooled indexer over the bf16 pool-key cache, the exact top-keep pools, sparse MLA over their
     tokens and the tail (trnrt/models/mla.py:505-526 `attention_long` for a decode batch), enqueued by one call of the
-    C ABI's dsa_pooled_decode_layer. Nothing is allocated per step.
+    C ABI's dsa_pooled_decode_layer: one kernel launch per 8 rows where the shapes allow (512-wide rows, at most 32
+    indexer heads, rows of at most 8,192 pools), the separate kernels otherwise or with chain=True. Nothing is
+    allocated per step.
 
     B, Hi (indexer heads), H (query heads), dqk (512: GLM's NoPE latent, or 576), max_pages, page_size, num_pages
     (cache pages incl. the null page 0), kp, keep (pools: topk / kp), scale (softmax scale), splits (attention
-    split-K; 0 = chosen for the GPU)."""
+    split-K; 0 = chosen for the GPU; any other count takes the separate kernels)."""
 
     def __init__(self, B: int, Hi: int, H: int, dqk: int, max_pages: int, page_size: int, num_pages: int, kp: int,
-                 keep: int, scale: float, splits: int = 0, device: torch.device | str = "cuda"):
+                 keep: int, scale: float, splits: int = 0, device: torch.device | str = "cuda", chain: bool = False):
+        self.chain = chain  # True: the separate kernels (dsa_pooled_decode_layer_chain) even where one launch applies
         self.B, self.Hi, self.H, self.dqk = B, Hi, H, dqk
         self.max_pages, self.page_size, self.num_pages = max_pages, page_size, num_pages
         self.kp, self.keep, self.scale, self.splits = kp, keep, float(scale), splits
@@ -141,7 +144,7 @@ class PooledDecodeLayer:
         if wsb == 0:
             raise ValueError(f"PooledDecodeLayer: no workspace size for B={B} H={H} keep={keep}")
         # zero once: the calls keep the regions that must start at zero (the top-k histograms) at zero
-        self.workspace = torch.zeros(wsb, dtype=torch.uint8, device=dev)
+        self.workspace = C.zeroed_workspace(wsb, dev)
 
     def step(self, q_idx: torch.Tensor, w: torch.Tensor, pool_key: torch.Tensor, q: torch.Tensor,
              kv_cache: torch.Tensor, kv_scale: torch.Tensor | None, table: torch.Tensor, npool: torch.Tensor,
@@ -167,7 +170,8 @@ class PooledDecodeLayer:
                 raise ValueError(f"kv cache of {kv_cache.numel()} bytes for {slots} slots of {self.dqk}")
             if kv_scale is not None:
                 C.need(kv_scale, "kv_scale", torch.float32, (slots,))
-        st = _lib.lib().dsa_pooled_decode_layer(
+        fn = _lib.lib().dsa_pooled_decode_layer_chain if self.chain else _lib.lib().dsa_pooled_decode_layer
+        st = fn(
             q_idx.data_ptr(), w.data_ptr(), pool_key.data_ptr(), q.data_ptr(), kv_cache.data_ptr(),
             C.ptr(kv_scale), table.data_ptr(), npool.data_ptr(), positions.data_ptr(), self.scores.data_ptr(),
             self.pools.data_ptr(), self.cnt.data_ptr(), self.out.data_ptr(), self.lse.data_ptr(),

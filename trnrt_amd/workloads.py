@@ -307,6 +307,16 @@ def pooled_step_bytes(cfg: PooledConfig, npool: list[int], tokens: list[int]) ->
     return tot
 
 
+def pooled_layer_bytes(cfg: PooledConfig, npool: list[int], tokens: list[int]) -> int:
+    """Algorithmic bytes of the pooled layer itself (dsa_pooled_decode_layer: every input and output once, as
+    algorithmic_bytes counts the kpool-1 layer): the indexer's inputs (pooled_indexer_bytes), then per row the bf16
+    attention queries, the attended tokens' latent rows (dqk B + fp32 scale) and the bf16 output."""
+    tot = pooled_indexer_bytes(cfg, npool)
+    for t in tokens:
+        tot += 2 * cfg.H * cfg.dqk + (cfg.dqk + 4) * t + 2 * cfg.H * 512
+    return tot
+
+
 @dataclass
 class PooledInputs:
     cfg: PooledConfig
