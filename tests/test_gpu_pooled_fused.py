@@ -150,3 +150,44 @@ def test_pooled_fused_repeated_steps():
     ws = layer.workspace.view(torch.int32).cpu()
     assert torch.all(ws[:8 * 16].view(8, 16)[:, :2] == 0), "barrier words left non-zero"
     assert layer.status()["gave_up"] == 0
+
+
+def _order_bins(sc: torch.Tensor) -> torch.Tensor:
+    """The 12-bit first-level bins (order key >> 20) of fp32 scores: the key maps floats to unsigned integers in
+    value order (negative values complemented, non-negative with the sign bit set; -0 as +0)."""
+    u = sc.contiguous().view(torch.int32).to(torch.int64) & 0xFFFFFFFF
+    u = torch.where(u == 0x80000000, torch.zeros_like(u), u)
+    key = torch.where(u >= 0x80000000, (~u) & 0xFFFFFFFF, u | 0x80000000)
+    return key >> 20
+
+
+def test_pooled_fused_header_fallback():
+    """Rows of 8,192 pools whose first block (256 pools) holds keys spread over 32 octaves, far above the rest of the
+    row: that list's header (its 64 highest nonzero bins) stops above the bin of the keep-th largest key, so the
+    first level also counts the keys below each list's header one by one. The test first shows that the row meets
+    that condition, then checks selection and outputs against the oracle."""
+    positions = [32767, 32767]
+    cfg, inp, pos, npool = _inputs(len(positions), 32768, positions, seed=66)
+    ppp = cfg.page_size // cfg.kp
+    keys = inp.pool_key.view(-1, 128)
+    keys.mul_(2.0 ** -8)
+    scale = 2.0 ** (torch.arange(256, device="cuda").float() / 8 + 8)
+    for b in range(len(positions)):
+        pages = inp.table[b, : 256 // ppp].long()
+        rows = (pages.unsqueeze(1) * ppp + torch.arange(ppp, device="cuda")).reshape(-1)
+        keys[rows] = (keys[rows].float() * scale.unsqueeze(1)).to(keys.dtype)
+    say("pooled one-launch layer, header fallback")
+    layer = _layer(cfg, inp)
+    _step(layer, inp, npool.cuda(), pos.cuda())
+    torch.cuda.synchronize()
+    sc = layer.scores.cpu()
+    for b in range(len(positions)):
+        n = int(npool[b])
+        bins = _order_bins(sc[b, :n])
+        c0 = int(torch.sort(bins, descending=True).values[cfg.keep - 1])
+        lows = []
+        for blk in bins.view(32, -1):
+            nzb = torch.unique(blk).flip(0)
+            lows.append(int(nzb[63]) if len(nzb) > 64 else 0)
+        assert c0 < max(lows), (c0, max(lows))
+    _check(cfg, inp, layer, pos, npool)

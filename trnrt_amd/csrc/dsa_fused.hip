@@ -82,12 +82,15 @@ static_assert(FU_LM <= FU_LCAP && FU_LPT % 2 == 0, "key list");
 // The layer's two forms: kpool 1 (FP8 keys with per-token scales; a workgroup's key list reaches down to the bin of
 // its FU_LM-th largest key) and pooled (GLM's kpool > 1: the scores of bf16 pool keys with no scale, rows of at most
 // 8,192 pools, so blocks of at most 256, every one of which its workgroup's list holds: the one-exchange selection
-// always applies).
+// always applies). A pooled list is the block's keys in position order, one word each (0: not selectable), then
+// the block's FU_PBINS highest nonzero histogram bins as (bin << 16) | count in descending bin order (0 past its
+// nonzero bins).
+constexpr int FU_PBINS = 64;
 template <bool POOL>
 struct FuForm {
   static constexpr int LPT = POOL ? 16 : FU_LPT;  // list entries per reading thread
   static constexpr int LCAP = 16 * LPT;
-  static constexpr int LROW = FU_LHDR + 2 * LCAP;
+  static constexpr int LROW = POOL ? LCAP + FU_PBINS : FU_LHDR + 2 * LCAP;
   static constexpr int KV = POOL ? 8 : 4;       // 16-byte key loads per lane and tile (64 bf16 or 64 e4m3 dims)
   static constexpr int TILE_LOADS = POOL ? 8 : 5;  // load instructions per lane and tile (with the scale)
   static_assert(LROW % 32 == 0 && LPT % 2 == 0, "key list");
@@ -370,6 +373,7 @@ __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int
   float* srow = a.scores + (size_t)b * a.stride;
   // a row that selects from the key lists writes its scores after barrier A; the others as each tile is scored
   const bool lists = fu_lists_on<POOL>(a, L);
+  uint32_t* plst = a.lst + ((size_t)b * FU_NW + j) * FF::LROW;  // the pooled form's key list
 
   // the queries' loads (32 MT heads of 16 pieces: MT per thread), the weights, the tiles' pages
   u32x4 qv[MT];
@@ -492,6 +496,7 @@ __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int
       if (h == 0) {
         if (!lists && mine && pos < a.stride) srow[pos] = v;
         scs[e] = v;
+        if (POOL && mine) plst[e] = order_key(v) & (0u - (uint32_t)(v > VISIBLE));
         if (v > VISIBLE) atomicAdd(&hs[order_key(v) >> 20], 1);
       }
     }
@@ -501,11 +506,34 @@ __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int
       const int lt = wave + FU_WAVES * (x / FU_TILE);  // the tile of the block
       const int pos = (j * nt + lt) * FU_TILE + (x & (FU_TILE - 1));
       if (!lists && lt < nt && pos < a.stride) srow[pos] = NEG_INF;
+      if (POOL && lt < nt) plst[lt * FU_TILE + (x & (FU_TILE - 1))] = 0u;
       scs[lt * FU_TILE + (x & (FU_TILE - 1))] = NEG_INF;
     }
   }
   // positions past the 32 blocks (32 kw) of a wider score row are never keys of the row
   for (int p = FU_NW * kw + j * FU_THREADS + tid; p < a.stride; p += FU_NW * FU_THREADS) srow[p] = NEG_INF;
+  if (POOL) {
+    // the block's highest nonzero histogram bins after its keys (thread t: bins 8 t .. 8 t + 7; its place among the
+    // nonzero bins from the top, from a block prefix of the counts)
+    __syncthreads();
+    int hv[8];
+    *reinterpret_cast<int4*>(hv) = *reinterpret_cast<const int4*>(hs + 8 * tid);
+    *reinterpret_cast<int4*>(hv + 4) = *reinterpret_cast<const int4*>(hs + 8 * tid + 4);
+    uint32_t nz = 0, tot;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) nz += hv[i] != 0;
+    uint32_t o = fu_block_prefix(nz, scr, &tot);
+    uint32_t* pb = plst + FF::LCAP;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (hv[i]) {
+        const int d = (int)tot - 1 - (int)o;
+        if (d < FU_PBINS) pb[d] = ((uint32_t)(8 * tid + i) << 16) | (uint32_t)hv[i];
+        ++o;
+      }
+    if (tid >= (int)tot && tid < FU_PBINS) pb[tid] = 0u;
+    return;
+  }
   __syncthreads();
   // the histogram's nonzero bins into the workgroup's bin list (thread t: bins 8 t .. 8 t + 7), in bin order, and
   // the workgroup's key list: the bin of its FU_LM-th largest key, then its keys from that bin up (or from the next
@@ -913,9 +941,9 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
   int* bins2 = reinterpret_cast<int*>(lds + L_BINS2);
   int* spg = reinterpret_cast<int*>(lds + L_SPG);
   int* slot_l = reinterpret_cast<int*>(lds + AT::L_P);
-  // the split's output positions, stored to idx in one coalesced pass at the end; the entries past CAP (slots) and
-  // past SPLIT (positions) are sinks for the writes of entries outside the split
-  constexpr int SLOT_SINK = AT::CAP, POS_SINK = AT::SPLIT;
+  // the split's output positions, stored to idx in one coalesced pass at the end; the entry past SPLIT is the sink
+  // for the writes of entries outside the split
+  constexpr int POS_SINK = AT::SPLIT;
   int* pos_l = slot_l + AT::CAP + 8;
   static_assert(4 * (AT::CAP + 8 + AT::SPLIT + 1) <= 2 * HPW * AT::PROW, "slot and position lists inside P's region");
   const int tid = threadIdx.x, wave = tid / WAVE, lane = tid & (WAVE - 1);
@@ -923,22 +951,34 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
   const int hg = j % a.HG, s = j / a.HG;
   const bool active = s < a.S;  // workgroup-uniform: a workgroup past the last split only helps with the barriers
   const int o0 = active ? s * a.sps : 0, o1 = active ? min(o0 + a.sps, a.keep) : 0;
-  // list w's counts and this thread's entries (device-coherent buffer loads: the lists are the peers' stores)
-  constexpr int NL = LPT / 2;
+  // list w's counts and this thread's entries (plain buffer loads: the lists are the peers' stores, in lines of their
+  // own that no workgroup read before barrier A); the pooled form: the list's keys LPT q .. LPT q + 15 and its
+  // header bins 4 q .. 4 q + 3
+  constexpr int NL = POOL ? LPT / 4 : LPT / 2;
   const __amdgpu_buffer_rsrc_t lrs = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(a.lst + (size_t)b * FU_NW * FF::LROW), (short)0, FU_NW * FF::LROW * 4, FU_BUF_WORD3);
   const int lo = 4 * FF::LROW * w;
-  const uint32_t hw0 = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(lrs, lo, 0, FU_AUX_PLAIN);
-  const uint32_t hw1 = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(lrs, lo + 4, 0, FU_AUX_PLAIN);
-  // header bins 2 q, 2 q + 1 (threads q < 14)
   typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-  const u32x2 hp = __builtin_bit_cast(
-      u32x2, __builtin_amdgcn_raw_buffer_load_b64(lrs, lo + 16 + 8 * min(q, FU_LBINS / 2 - 1), 0, FU_AUX_PLAIN));
+  uint32_t hw0 = 0u, hw1 = 0u;
+  u32x2 hp = {0u, 0u};
+  u32x4 bh = {0u, 0u, 0u, 0u};
+  if constexpr (!POOL) {
+    hw0 = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(lrs, lo, 0, FU_AUX_PLAIN);
+    hw1 = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(lrs, lo + 4, 0, FU_AUX_PLAIN);
+    // header bins 2 q, 2 q + 1 (threads q < 14)
+    hp = __builtin_bit_cast(
+        u32x2, __builtin_amdgcn_raw_buffer_load_b64(lrs, lo + 16 + 8 * min(q, FU_LBINS / 2 - 1), 0, FU_AUX_PLAIN));
+  } else {
+    // header entries 4 q .. 4 q + 3
+    bh = __builtin_bit_cast(u32x4,
+                            __builtin_amdgcn_raw_buffer_load_b128(lrs, lo + 4 * FF::LCAP + 16 * q, 0, FU_AUX_PLAIN));
+  }
   u32x4 ev[NL];
 #pragma unroll
   for (int i = 0; i < NL; ++i)
-    ev[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                          lrs, lo + 4 * FU_LHDR + 8 * LPT * q + 16 * i, 0, FU_AUX_PLAIN));
+    ev[i] = __builtin_bit_cast(
+        u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                   lrs, POOL ? lo + 4 * LPT * q + 16 * i : lo + 4 * FU_LHDR + 8 * LPT * q + 16 * i, 0, FU_AUX_PLAIN));
   __builtin_amdgcn_sched_barrier(0);
   // the row's pages into registers (pages tid, tid + 512, clamped: at most 1024 pages of at least 32 tokens), staged
   // in LDS at the end (loads straight into LDS here would make every LDS access below wait for all loads, the
@@ -966,15 +1006,24 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
   if (tid < 256) bins2[tid] = 0;
   if (tid < AT::CAP) slot_l[tid] = 0;  // padding rows read slot 0
   if (tid < AT::SPLIT) pos_l[tid] = 0;  // outputs past the count are 0
-  if (tid == 0) scr[8] = scr[24] = scr[40] = -1;
+  if (tid == 0) scr[8] = scr[24] = scr[40] = scr[56] = -1;
   __builtin_amdgcn_sched_barrier(0);
   __syncthreads();  // the bins cleared (the loads above may be out; their first uses wait for them)
-  const int nw = min((int)hw0, FF::LCAP) - LPT * q;  // this thread's entries: those below nw
   uint32_t key[LPT], pos[LPT];
+  if constexpr (POOL) {
+    // the block's keys LPT q + i (those at kw and past are not the block's)
 #pragma unroll
-  for (int i = 0; i < LPT; ++i) {
-    key[i] = i < nw ? ev[i / 2][2 * (i & 1)] : 0u;
-    pos[i] = ev[i / 2][2 * (i & 1) + 1] & 1023u;
+    for (int i = 0; i < LPT; ++i) {
+      key[i] = LPT * q + i < kw ? ev[i / 4][i & 3] : 0u;
+      pos[i] = (uint32_t)(LPT * q + i);
+    }
+  } else {
+    const int nw = min((int)hw0, FF::LCAP) - LPT * q;  // this thread's entries: those below nw
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+      key[i] = i < nw ? ev[i / 2][2 * (i & 1)] : 0u;
+      pos[i] = ev[i / 2][2 * (i & 1) + 1] & 1023u;
+    }
   }
   // the keys pass through an empty asm between the passes below, so that no compare mask over them is kept across
   // passes (twelve 64-bit masks held in scalar registers spill)
@@ -982,36 +1031,65 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
 #pragma unroll
     for (int i = 0; i < LPT; ++i) asm volatile("" : "+v"(key[i]));
   };
-  // the first level from the lists' header bins (their bins at or above the lowest listed are exactly the listed
-  // keys' bins); a list whose 28th header bin is listed may list more bins than its header holds: its keys one by one
-  const bool hfull = q == FU_LBINS / 2 - 1 && hp[1] != 0u && (hp[1] >> 16) >= hw1;
-  if ((__ballot(hfull) >> (16 * (w & 3))) & 0xFFFFull) {
-#pragma unroll
-    for (int i = 0; i < LPT; ++i)
-      if (key[i]) atomicAdd(&bins0[key[i] >> 20], 1);
-  } else if (q < FU_LBINS / 2) {
-#pragma unroll
-    for (int k = 0; k < 2; ++k)
-      if (hp[k] != 0u && (hp[k] >> 16) >= hw1) atomicAdd(&bins0[(hp[k] >> 16) & 4095u], (int)(hp[k] & 0xFFFFu));
-  }
-  fresh();
-  if (q == 0) st.lbin[w] = (int)hw1;
-  __syncthreads();
   constexpr int P1 = 4096 / FU_THREADS;
   int hb[P1];
-  *reinterpret_cast<int4*>(hb) = *reinterpret_cast<const int4*>(bins0 + P1 * tid);
-  *reinterpret_cast<int4*>(hb + 4) = *reinterpret_cast<const int4*>(bins0 + P1 * tid + 4);
-  int c0, above0;
-  const int nlist = fu_find_bin<P1>(hb, a.keep, scr, &c0, &above0);
-  const uint32_t lmax = wave_max_u32(lane < FU_NW ? (uint32_t)st.lbin[lane] : 0u);
-  int cnt_row;
-  if (lmax == 0u) {
+  int c0, above0, nlist, cnt_row;
+  if constexpr (POOL) {
+    // the first level from the lists' headers: exact for the bins at or above every list's lowest complete bin lmax
+    // (a list's 64th header bin when it has one, else every bin); when the keep-th largest key's bin c0 is below
+    // that, the keys below their list's header bins are counted one by one and the search repeated
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (bh[k]) atomicAdd(&bins0[(bh[k] >> 16) & 4095u], (int)(bh[k] & 0xFFFFu));
+    if (q == 15) st.lbin[w] = bh[3] ? (int)(bh[3] >> 16) : 0;
+    __syncthreads();
+    *reinterpret_cast<int4*>(hb) = *reinterpret_cast<const int4*>(bins0 + P1 * tid);
+    *reinterpret_cast<int4*>(hb + 4) = *reinterpret_cast<const int4*>(bins0 + P1 * tid + 4);
+    nlist = fu_find_bin<P1>(hb, a.keep, scr, &c0, &above0);
+    const int lmax = (int)wave_max_u32(lane < FU_NW ? (uint32_t)st.lbin[lane] : 0u);
+    if (lmax > 0 && (nlist <= a.keep || c0 < lmax)) {  // workgroup-uniform
+      const int low = st.lbin[w];
+#pragma unroll
+      for (int i = 0; i < LPT; ++i)
+        if (key[i] && (int)(key[i] >> 20) < low) atomicAdd(&bins0[key[i] >> 20], 1);
+      fresh();
+      __syncthreads();
+      *reinterpret_cast<int4*>(hb) = *reinterpret_cast<const int4*>(bins0 + P1 * tid);
+      *reinterpret_cast<int4*>(hb + 4) = *reinterpret_cast<const int4*>(bins0 + P1 * tid + 4);
+      nlist = fu_find_bin<P1>(hb, a.keep, scr + 48, &c0, &above0);
+    }
     // every list holds all its workgroup's keys
     cnt_row = min(nlist, a.keep);
     if (nlist <= a.keep) c0 = -1;  // every selectable key is selected
   } else {
-    if (nlist < a.keep || c0 < (int)lmax) return false;
-    cnt_row = a.keep;
+    // the first level from the lists' header bins (their bins at or above the lowest listed are exactly the listed
+    // keys' bins); a list whose 28th header bin is listed may list more bins than its header holds: its keys one by
+    // one
+    const bool hfull = q == FU_LBINS / 2 - 1 && hp[1] != 0u && (hp[1] >> 16) >= hw1;
+    if ((__ballot(hfull) >> (16 * (w & 3))) & 0xFFFFull) {
+#pragma unroll
+      for (int i = 0; i < LPT; ++i)
+        if (key[i]) atomicAdd(&bins0[key[i] >> 20], 1);
+    } else if (q < FU_LBINS / 2) {
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+        if (hp[k] != 0u && (hp[k] >> 16) >= hw1) atomicAdd(&bins0[(hp[k] >> 16) & 4095u], (int)(hp[k] & 0xFFFFu));
+    }
+    fresh();
+    if (q == 0) st.lbin[w] = (int)hw1;
+    __syncthreads();
+    *reinterpret_cast<int4*>(hb) = *reinterpret_cast<const int4*>(bins0 + P1 * tid);
+    *reinterpret_cast<int4*>(hb + 4) = *reinterpret_cast<const int4*>(bins0 + P1 * tid + 4);
+    nlist = fu_find_bin<P1>(hb, a.keep, scr, &c0, &above0);
+    const uint32_t lmax = wave_max_u32(lane < FU_NW ? (uint32_t)st.lbin[lane] : 0u);
+    if (lmax == 0u) {
+      // every list holds all its workgroup's keys
+      cnt_row = min(nlist, a.keep);
+      if (nlist <= a.keep) c0 = -1;  // every selectable key is selected
+    } else {
+      if (nlist < a.keep || c0 < (int)lmax) return false;
+      cnt_row = a.keep;
+    }
   }
   // T and the room for ties at T; with c0 = -1, T = 0 (below every listed key) and no ties
   uint32_t T = 0u;
@@ -1085,39 +1163,35 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
   }
   {
     // this thread's selected entries take the output indices first .. first + nsel - 1; only the threads whose
-    // indices meet the split's [o0, o1) (one or two lists' worth, so most waves skip this) list their entries: each
-    // entry's index, then all their pages in one round of LDS reads, then the writes, with no branch per entry (an
-    // entry outside the split writes the sink entry past the lists)
+    // indices meet the split's [o0, o1) (one or two lists' worth, so most waves skip this) store their entries'
+    // positions, with no branch per entry (an entry outside the split writes the sink entry past the list); the
+    // cache slots follow from the positions below, one thread per slot
     int gtb = (int)((incl - mine) & 0xFFFFu), eqb = (int)((incl - mine) >> 16);  // this thread's list predecessors
     const int first = off_l + gtb + min(eqb, take_l);
     const int nsel = (int)(mine & 0xFFFFu) + min(max(take_l - eqb, 0), (int)(mine >> 16));
     if (nsel > 0 && first < o1 && first + nsel > o0) {
-      int oi[LPT], pg[LPT];
+      const int nties = (int)(mine >> 16);
+      if (nties == 0 || eqb >= take_l || eqb + nties <= take_l) {
+        // none of this thread's ties is taken, or all are (every thread but at most one of the row): its selected
+        // entries are those at or above one threshold (T + 1 or T; T >= 1 when there are ties)
+        const uint32_t thr = nties > 0 && eqb < take_l ? T : T + 1u;
+        int r = first - o0;  // the next selected entry's output index in the split
 #pragma unroll
-      for (int i = 0; i < LPT; ++i) {
-        const bool above = key[i] > T, tie = key[i] == T && key[i];
-        const int o = off_l + gtb + min(eqb, take_l) - o0;
-        oi[i] = (above || (tie && eqb < take_l)) && (unsigned)o < (unsigned)(o1 - o0) ? o : -1;
-        gtb += above;
-        eqb += tie;
-      }
-      const int shift = POOL ? a.ppp_shift : a.page_shift;
-#pragma unroll
-      for (int i = 0; i < LPT; ++i) pg[i] = spg[(kw * w + (int)pos[i]) >> shift];
-#pragma unroll
-      for (int i = 0; i < LPT; ++i) {
-        const int p = kw * w + (int)pos[i];  // the key's position (pooled: pool) in the row
-        const int page = safe_page(pg[i], a.num_pages);
-        if (POOL) {
-          // the pool's kpool tokens: consecutive slots of its page
-          const int kp = 1 << a.kp_shift;
-          const int base = page * a.page_size + ((p & ((1 << a.ppp_shift) - 1)) << a.kp_shift);
-          const int si = oi[i] >= 0 ? oi[i] << a.kp_shift : SLOT_SINK;
-          for (int t = 0; t < kp; ++t) slot_l[si + t] = base + t;
-        } else {
-          slot_l[oi[i] >= 0 ? oi[i] : SLOT_SINK] = page * a.page_size + (p & (a.page_size - 1));
+        for (int i = 0; i < LPT; ++i) {
+          const bool sl = key[i] >= thr;
+          pos_l[sl && (unsigned)r < (unsigned)(o1 - o0) ? r : POS_SINK] = kw * w + (int)pos[i];
+          r += sl;
         }
-        pos_l[oi[i] >= 0 ? oi[i] : POS_SINK] = p;
+      } else {
+#pragma unroll
+        for (int i = 0; i < LPT; ++i) {
+          const bool above = key[i] > T, tie = key[i] == T && key[i];
+          const int o = off_l + gtb + min(eqb, take_l) - o0;
+          const bool in = (above || (tie && eqb < take_l)) && (unsigned)o < (unsigned)(o1 - o0);
+          pos_l[in ? o : POS_SINK] = kw * w + (int)pos[i];  // the key's position (pooled: pool) in the row
+          gtb += above;
+          eqb += tie;
+        }
       }
     }
   }
@@ -1125,10 +1199,17 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
   // the split's live slots; a row with none attends position 0 masked (its lse is NEG_INF)
   int ns = max(min(o1, cnt_row) - o0, 0);
   bool empty = cnt_row == 0;
+  __syncthreads();  // the split's positions
   if (POOL) {
-    // the selected pools' token slots, then (in the split of the last selected pool) the tail's: tokens
-    // kpool L .. position of the incomplete pool L, in that pool's page
+    // the selected pools' token slots (token t & (kpool - 1) of the split's pool t >> log2 kpool: consecutive slots
+    // of its page), then (in the split of the last selected pool) the tail's: tokens kpool L .. position of the
+    // incomplete pool L, in that pool's page
     ns <<= a.kp_shift;
+    if (tid < ns) {
+      const int p = pos_l[tid >> a.kp_shift];
+      slot_l[tid] = safe_page(spg[p >> a.ppp_shift], a.num_pages) * a.page_size +
+                    ((p & ((1 << a.ppp_shift) - 1)) << a.kp_shift) + (tid & ((1 << a.kp_shift) - 1));
+    }
     const int tail_pos0 = L << a.kp_shift;
     const int tail = min(max(a.positions[b] + 1 - tail_pos0, 0), (1 << a.kp_shift) - 1);
     const int s_last = cnt_row > 0 ? (cnt_row - 1) / a.sps : 0;
@@ -1139,6 +1220,9 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
       ns += tail;
     }
     empty = cnt_row == 0 && tail == 0;
+  } else if (tid < ns) {
+    const int p = pos_l[tid];
+    slot_l[tid] = safe_page(spg[p >> a.page_shift], a.num_pages) * a.page_size + (p & (a.page_size - 1));
   }
   *live_bias = 0.0f;
   if (active && empty && s == 0) {
