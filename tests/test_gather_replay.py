@@ -4,8 +4,8 @@ tail rows): each wave's loads k = wave, wave + 8, ... while 64 k < padded x KPIE
 of the row tile at 1024 k + 16 l from row u / KPIECES, piece u % KPIECES of unit u = 64 k + l, the row and piece
 advanced per load as the kernel advances them (by DR rows and DP pieces, with a carry). Checked: the stepped
 (row, piece) equals the division's, every lane's row is inside the split's padded rows (whose slot ids the split's
-list holds) and inside the tile's CAP rows, the piece read is inside the cache row, and the LDS bytes written stay
-inside the row tile. A load with lanes past the padded rows would read slot ids past the written list and load
+list holds) and inside the tile's CAP rows, the piece read is inside the cache row, the LDS bytes written stay
+inside the row tile, and NI loads per lane cover every load of the split. A load with lanes past the padded rows would read slot ids past the written list and load
 from outside the cache, the fault this replay once found. The constants are read from the source, so a change there
 is replayed here."""
 
@@ -39,8 +39,10 @@ def _load_consts():
     assert "static constexpr int CAP = SPLIT + (XT ? FU_CH : 0);" in text
     assert "static constexpr int KPIECES = PIECES + 1;" in text
     assert "const int padded = (n_slots + FU_CH - 1) / FU_CH * FU_CH;" in text
-    assert "for (int k = wave; k * WAVE < units; k += FU_WAVES) {" in text
-    assert "const uint8_t* src = a.kv + (size_t)slot_l[row] * DQK + 16 * min(pc, PIECES - 1);" in text
+    assert "constexpr int NI = (AT::CAP * KPIECES + FU_THREADS - 1) / FU_THREADS;" in text
+    assert "sl[i] = slot_l[min(row, AT::CAP - 1)];" in text
+    assert "const int k = wave + FU_WAVES * i;\n      if (k * WAVE < units) {" in text
+    assert "const uint8_t* src = a.kv + (size_t)sl[i] * DQK + 16 * min(pcs[i], PIECES - 1);" in text
     assert "(__attribute__((address_space(3))) void*)(kt + 1024 * k), 16, 0, 0);" in text
     return CONSTS
 
@@ -65,22 +67,27 @@ def test_gather_lanes_stay_inside_the_padded_rows(hpw, dqk, xt):
         assert padded <= cap, (n_slots, padded, cap)
         units = padded * kpieces
         assert units % WAVE == 0, f"a padded split's pieces do not fill whole loads ({n_slots} slots)"
+        ni = (cap * kpieces + WAVES * WAVE - 1) // (WAVES * WAVE)  # NI: loads per lane at most
+        loads = 0
         for wave in range(WAVES):
             for lane in range(WAVE):
                 row, pc = (WAVE * wave + lane) // kpieces, (WAVE * wave + lane) % kpieces
-                k = wave
-                while k * WAVE < units:
-                    u = WAVE * k + lane
-                    assert (row, pc) == divmod(u, kpieces), (n_slots, wave, lane, k)
-                    assert row < padded and row < cap, f"{n_slots} slots: lane {lane} of load {k} reads row {row}"
-                    assert 0 <= min(pc, pieces - 1) < pieces
-                    assert 1024 * k + 16 * lane + 16 <= tile_bytes, f"{n_slots} slots: LDS past the row tile"
+                for i in range(ni):
+                    k = wave + WAVES * i
+                    assert 0 <= min(row, cap - 1) < cap  # the slot read, taken for every i
+                    if k * WAVE < units:
+                        u = WAVE * k + lane
+                        assert (row, pc) == divmod(u, kpieces), (n_slots, wave, lane, k)
+                        assert row < padded and row < cap, f"{n_slots} slots: lane {lane} of load {k} reads row {row}"
+                        assert 0 <= min(pc, pieces - 1) < pieces
+                        assert 1024 * k + 16 * lane + 16 <= tile_bytes, f"{n_slots} slots: LDS past the row tile"
+                        loads += lane == 0
                     row += DR
                     pc += DP
                     if pc >= kpieces:
                         pc -= kpieces
                         row += 1
-                    k += WAVES
+        assert loads == units // WAVE, f"{n_slots} slots: {loads} loads for {units // WAVE} (NI too small)"
 
 
 def test_an_odd_padding_would_be_caught():

@@ -218,20 +218,11 @@ struct FusedArgs {
 };
 
 // Device-scope loads (sc1) miss the CU's caches and are served past the XCD's L2 (measured: at a small fraction of
-// the L2's bandwidth). The kernel uses them only for the barrier polls and for the splits' (max, sum) pairs, which
-// peers write side by side within cache lines. Everything else a peer publishes before a barrier (bin lists,
-// candidate blocks, key lists, split outputs) is read with plain loads, which hit the XCD's L2: a CU's L1 holds no
-// stale copy of it, since the L1 is invalidated at each launch's start, no workgroup reads a peer's region before the
-// barrier that publishes it, and each workgroup's region of each kind occupies whole 128-byte lines of its own.
-__device__ __forceinline__ int ld_sc1(const int* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint32_t ld_sc1(const uint32_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint64_t ld_sc1_64(const void* p) {
-  return __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+// the L2's bandwidth). The kernel uses them only for the barrier polls. Everything a peer publishes before a barrier
+// (bin lists, candidate blocks, key lists, split outputs and their (max, sum) pairs) is read with plain loads, which
+// hit the XCD's L2: a CU's L1 holds no stale copy of it, since the L1 is invalidated at each launch's start, no
+// workgroup reads a peer's region before the barrier that publishes it, and each workgroup's region of each kind
+// occupies whole 128-byte lines of its own.
 constexpr int FU_AUX_PLAIN = 0;  // the cache-policy operand of the loads of a peer's published data: none
 
 // XCD-local barrier of the 32 workgroups of an XCD: every thread's stores complete (drained memory counter), then the
@@ -1270,13 +1261,14 @@ __device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int 
   const int hg = j % a.HG, s = j / a.HG;
   if (s >= a.S) return;  // workgroup-uniform
   const int H = a.H;
-  // head HPW hg + i's split output at part + i * 512, its (max, sum) at mlp[i * S]
+  // head HPW hg + i's split output at part + i * 512, its (max, sum) at mlp[i] (the split's pairs [S][H]: each
+  // workgroup's in whole 128-byte lines of its own)
   uint16_t* part = a.part + (((size_t)b * a.S + s) * H + HPW * hg) * FU_DV;
-  float2* mlp = a.ml + ((size_t)b * H + HPW * hg) * a.S + s;
+  float2* mlp = a.ml + ((size_t)b * a.S + s) * H + HPW * hg;
   if (n_slots == 0) {  // an empty split: weight 0 in the combine
     for (int i = tid; i < HPW * FU_DV / 8; i += FU_THREADS)
       reinterpret_cast<uint4*>(part + (size_t)(i / (FU_DV / 8)) * FU_DV)[i % (FU_DV / 8)] = uint4{0u, 0u, 0u, 0u};
-    if (tid < HPW) mlp[tid * a.S] = make_float2(-INFINITY, 0.0f);
+    if (tid < HPW) mlp[tid] = make_float2(-INFINITY, 0.0f);
     return;
   }
   static_assert(FU_CH * KPIECES % WAVE == 0 && AT::CAP % FU_CH == 0, "a padded split's pieces fill whole loads");
@@ -1301,18 +1293,31 @@ __device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int 
   // u / 37, piece u % 37; the padding piece re-reads the last data piece); the loads of the padded rows' units spread
   // over the 8 waves
   {
-    // unit u = 64 k + lane's row u / 37 and piece u % 37, advanced with k (by 8: u by 512 = 13 x 37 + 31)
+    // unit u = 64 k + lane's row u / 37 and piece u % 37, advanced with k (by 8: u by 512 = 13 x 37 + 31); the
+    // lane's slots for its loads k = wave + 8 i in one round of LDS reads, then the loads (a slot read per load
+    // would put an LDS round trip before each)
     constexpr int DR = FU_WAVES * WAVE / KPIECES, DP = FU_WAVES * WAVE % KPIECES;
+    constexpr int NI = (AT::CAP * KPIECES + FU_THREADS - 1) / FU_THREADS;  // loads per lane at most
     const int units = padded * KPIECES;
     int row = (WAVE * wave + lane) / KPIECES, pc = WAVE * wave + lane - row * KPIECES;
-    for (int k = wave; k * WAVE < units; k += FU_WAVES) {
-      const uint8_t* src = a.kv + (size_t)slot_l[row] * DQK + 16 * min(pc, PIECES - 1);
-      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(kt + 1024 * k), 16, 0, 0);
+    int sl[NI], pcs[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      sl[i] = slot_l[min(row, AT::CAP - 1)];  // (past the units: a row of the list, never loaded)
+      pcs[i] = pc;
       row += DR;
       pc += DP;
       if (pc >= KPIECES) {
         pc -= KPIECES;
         ++row;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int k = wave + FU_WAVES * i;
+      if (k * WAVE < units) {
+        const uint8_t* src = a.kv + (size_t)sl[i] * DQK + 16 * min(pcs[i], PIECES - 1);
+        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(kt + 1024 * k), 16, 0, 0);
       }
     }
   }
@@ -1442,7 +1447,7 @@ __device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int 
         mh = max_nonan(mh, mr[t]);
       }
       inv[i] = __builtin_amdgcn_rcpf(l);  // l >= 1 (the split's maximum contributes exp(0))
-      if (wave == 0 && l16 == 0) mlp[hl * a.S] = make_float2(mh, l);
+      if (wave == 0 && l16 == 0) mlp[hl] = make_float2(mh, l);
     }
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
@@ -1469,7 +1474,7 @@ __device__ __forceinline__ void fu_combine_heads(const FusedArgs& a, float* wts,
   const int h = h0 + (tid >> 8), d = 2 * (tid & 255);
   const int hh = h0 + (lane >> 5), sp = lane & 31;
   uint64_t mlv = 0;
-  if (tid < WAVE) mlv = ld_sc1_64(a.ml + ((size_t)b * H + hh) * S + min(sp, S - 1));
+  if (tid < WAVE) mlv = *reinterpret_cast<const uint64_t*>(a.ml + ((size_t)b * S + min(sp, S - 1)) * H + hh);
   // the two heads' split outputs through a buffer descriptor: split k's offset is scalar, the lane's is 32-bit
   const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(a.part + (size_t)b * S * H * FU_DV + (size_t)h0 * FU_DV), (short)0,
