@@ -401,10 +401,10 @@ def pooled_cpu_baseline(inp, cfg, npool, positions, budget_s: float = 15.0) -> d
 
 
 def pooled_main(args) -> int:
-    """The pooled (GLM-5.3-Flash) decode step (config 6): the current tokens' pool-key write (dsa_pool_keys_write),
-    then the pooled layer (dsa_pooled_decode_layer: the indexer over the bf16 pool-key cache, the exact top-512 pools,
-    sparse MLA over the selected pools' tokens and the tail, over the 512-wide NoPE latent; one launch, or with
-    --chain the separate kernels). roofline: the one launch's algorithmic bytes (W.pooled_layer_bytes) over its
+    """The pooled (GLM-5.3-Flash) decode step (config 6): the current tokens' pool-key write, then the pooled layer
+    (the indexer over the bf16 pool-key cache, the exact top-512 pools, sparse MLA over the selected pools' tokens and
+    the tail, over the 512-wide NoPE latent): dsa_pooled_decode_step, one launch; with --chain dsa_pool_keys_write and
+    the separate kernels. roofline: the one launch's algorithmic bytes (W.pooled_step_bytes) over its
     HIP-event-timed duration, or with --chain the indexer kernel's."""
     import torch
 
@@ -425,11 +425,13 @@ def pooled_main(args) -> int:
     layer = PooledDecodeLayer(cfg.B, cfg.Hi, cfg.H, cfg.dqk, inp.table.shape[1], ps, inp.pool_key.shape[0] // ps, kp,
                               cfg.keep, cfg.scale, splits=args.splits, device=dev, chain=args.chain)
 
+    write = (inp.rows, inp.ape, slot_mapping, inp.rows_scale)
+
     def step():
-        dsa_cache.write_pool_keys(inp.pool_key, inp.rows, pos, inp.table, slot_mapping, inp.ape, ps, kp,
-                                  rows_scale=inp.rows_scale)
+        # the pool-key write of the rows' current tokens, then the layer (dsa_pooled_decode_step: one launch, or
+        # with --chain the write's kernel and the separate kernels)
         layer.step(inp.q_idx, inp.w, inp.pool_key, inp.q, inp.kv_cache, inp.kv_scale, inp.table, npool_d, pos,
-                   check=False)
+                   check=False, write=write)
 
     for _ in range(args.warmup):
         step()
@@ -448,8 +450,8 @@ def pooled_main(args) -> int:
     tail = [int(p) + 1 - kp * int(n) for p, n in zip(positions, npool)]
     tokens = [kp * min(int(n), cfg.keep) + t for n, t in zip(npool, tail)]
     if "decode_pooled_fused_kernel" in k_us:
-        # the one-launch layer: its launches move the layer's algorithmic bytes
-        kname, kbytes = "decode_pooled_fused_kernel", W.pooled_layer_bytes(cfg, npool.tolist(), tokens)
+        # the one-launch step (the pool-key write, the indexer, the selection, the attention): the step's bytes
+        kname, kbytes = "decode_pooled_fused_kernel", W.pooled_step_bytes(cfg, npool.tolist(), tokens)
     else:
         # the separate kernels: the indexer, the kernel that streams the whole pool-key cache
         kname, kbytes = "indexer_decode_bf16_kernel", W.pooled_indexer_bytes(cfg, npool.tolist())

@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define DSA_ABI_VERSION 9
+#define DSA_ABI_VERSION 10
 
 #define DSA_OK 0
 #define DSA_EINVAL (-1)      /* a null pointer or a size out of range */
@@ -357,6 +357,24 @@ int dsa_pooled_decode_layer_chain(const void* q_idx_bf16, const float* w, const 
                                   void* workspace, size_t workspace_bytes, int B, int Hi, int H, int Dqk,
                                   int max_pages, int page_size, int num_pages, int kp, int keep, float scale,
                                   int splits, void* stream);
+
+/*
+ * The pooled decode step: the pool-key write of the step's written tokens (one per row, at positions[b], cache slot
+ * slot_mapping[b]; dsa_pool_keys_write's arithmetic and arguments, with n_rows = B and the layer's page_size and
+ * num_pages page_size slots) followed by dsa_pooled_decode_layer on the written cache, as the reference's decode
+ * step runs them (trnrt/models/mla.py:448-452: write_pool_keys, then attention_long). Where dsa_pooled_decode_layer
+ * is one launch and kp is 4, so is this: the workgroup whose block holds a row's written pool computes the pool's
+ * key, stores it, and scores that pool (when it is complete) from the new key, so scores, selection and outputs equal
+ * the write followed by the layer. Otherwise it is dsa_pool_keys_write then dsa_pooled_decode_layer. pool_key is
+ * written (the written pools' slots) and read; other arguments, results and workspace as dsa_pooled_decode_layer.
+ */
+int dsa_pooled_decode_step(const void* rows, int rows_fp8, const float* rows_scale, int rows_width, const float* ape,
+                           const int64_t* slot_mapping, const void* q_idx_bf16, const float* w, void* pool_key_bf16,
+                           const void* q_bf16, const uint8_t* kv_fp8, const float* kv_scale,
+                           const int32_t* page_table, const int32_t* npool, const int32_t* positions, float* scores,
+                           int32_t* pools, int32_t* cnt, void* out_bf16, float* lse, void* workspace,
+                           size_t workspace_bytes, int B, int Hi, int H, int Dqk, int max_pages, int page_size,
+                           int num_pages, int kp, int keep, float scale, int splits, void* stream);
 
 /* Bytes of workspace dsa_pooled_decode_layer needs (max_len: the most pools a row scores). */
 size_t dsa_pooled_workspace_bytes(int B, int H, int keep, int max_len, int kp, int splits);

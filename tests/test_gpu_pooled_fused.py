@@ -59,8 +59,8 @@ def _check(cfg, inp, layer, positions, npool, scores=True):
     assert layer.status()["gave_up"] == 0
 
 
-def _inputs(B, L, positions, H=64, seed=0):
-    cfg = W.PooledConfig("glm-fused", B=B, L=L, H=H)
+def _inputs(B, L, positions, H=64, seed=0, kp=4):
+    cfg = W.PooledConfig("glm-fused", B=B, L=L, H=H, kp=kp)
     inp = W.make_pooled_inputs(cfg, seed=seed, device="cuda")
     pos = torch.tensor(positions, dtype=torch.int32)
     npool = torch.div(pos + 1, cfg.kp, rounding_mode="floor").to(torch.int32)
@@ -191,3 +191,53 @@ def test_pooled_fused_header_fallback():
             lows.append(int(nzb[63]) if len(nzb) > 64 else 0)
         assert c0 < max(lows), (c0, max(lows))
     _check(cfg, inp, layer, pos, npool)
+
+
+@pytest.mark.parametrize("H,kp", [(64, 4), (32, 4), (64, 2)])
+def test_pooled_step_writes_then_attends_in_one_launch(H, kp):
+    """dsa_pooled_decode_step (the pool-key write of each row's written token, then the layer) against the write
+    (dsa_cache.write_pool_keys) followed by the separate kernels, on the same inputs: one launch at kpool 4 (the
+    write's kernel, then the layer's one launch, at kpool 2), the written pools' keys bit-equal in the cache, scores
+    bit-equal (the completed pool scored from its new key), selection equal, outputs within the bound, and the oracle
+    on the written cache. The written tokens' indexer rows are redrawn first, so that each written pool's new key
+    differs from the one in the cache; rows: complete and incomplete written pools, a pool 0 (position kp - 1), a row
+    with no complete pool (position 0), and a padded row (null-page slot)."""
+    from trnrt_amd.kernels import dsa_cache
+
+    positions = [8191, 8190, 4095, 2050, kp - 1, 0, 6001, 0]
+    cfg, inp, pos, npool = _inputs(len(positions), 8192, positions, H=H, seed=70 + H + kp, kp=kp)
+    ps, kp = cfg.page_size, cfg.kp
+    sm = dsa_cache.slots_of(pos.cuda(), inp.table, ps)
+    sm[-1] = 7  # a padded row: its slot in the null page
+    g = torch.Generator(device="cuda").manual_seed(71)
+    new_rows, new_scale = W.quantize_rows(torch.randn(len(positions), inp.rows.shape[1], generator=g, device="cuda")
+                                          * 3.0)
+    inp.rows[sm] = new_rows
+    inp.rows_scale[sm] = new_scale
+    write = (inp.rows, inp.ape, sm, inp.rows_scale)
+    say(f"pooled one-launch step H={H} kp={kp} positions={positions}")
+    # the stale scores (the cache before the write), to show that the write changes the completed pools' scores
+    stale = _layer(cfg, inp)
+    _step(stale, inp, npool.cuda(), pos.cuda())
+    pk_ref = inp.pool_key.clone()
+    f, ch = _layer(cfg, inp), _layer(cfg, inp, chain=True)
+    names = launched_kernels(lambda: f.step(inp.q_idx, inp.w, inp.pool_key, inp.q, inp.kv_cache, inp.kv_scale,
+                                            inp.table, npool.cuda(), pos.cuda(), write=write))
+    want = ["decode_pooled_fused_kernel"] if kp == 4 else ["pool_keys_kernel", "decode_pooled_fused_kernel"]
+    assert names == want, names
+    dsa_cache.write_pool_keys(pk_ref, inp.rows, pos.cuda(), inp.table, sm, inp.ape, ps, kp,
+                              rows_scale=inp.rows_scale)
+    ch.step(inp.q_idx, inp.w, pk_ref, inp.q, inp.kv_cache, inp.kv_scale, inp.table, npool.cuda(), pos.cuda())
+    torch.cuda.synchronize()
+    assert torch.equal(inp.pool_key, pk_ref), "the written pool keys differ"
+    assert torch.equal(f.scores, ch.scores)
+    assert torch.equal(f.pools, ch.pools) and torch.equal(f.cnt, ch.cnt)
+    assert_attention_close(f.out, ch.out)
+    changed = 0
+    for b, p in enumerate(positions):
+        if (p + 1) % kp == 0 and b < len(positions) - 1:  # a completed pool, scored this step
+            P = p // kp
+            changed += int(f.scores[b, P] != stale.scores[b, P])
+    assert changed >= 3, "the written pools' scores did not change: the test does not exercise the write"
+    _check(cfg, inp, f, pos, npool)
+    assert f.status()["gave_up"] == 0

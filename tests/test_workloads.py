@@ -60,5 +60,6 @@ def test_pooled_bytes_of_config6():
     cfg = W.POOLED_CONFIGS[6]
     # per row: 8,192 pool keys x 256 B + 512 table entries + 32 bf16 queries of 128 + 32 fp32 weights
     assert W.pooled_indexer_bytes(cfg, [8192] * 8) == 8 * 2_107_520
-    # + the pool-key write, the 64 x 512 bf16 queries, 2,048 tokens x 516 B, the fp32 output
-    assert W.pooled_step_bytes(cfg, [8192] * 8, [2048] * 8) == 8 * (2_107_520 + 1_254_672)
+    # + the pool-key write (4 rows x 260 B + 256 B), the 64 x 512 bf16 queries, 2,048 tokens x 516 B, the bf16 output
+    assert W.pooled_step_bytes(cfg, [8192] * 8, [2048] * 8) == 8 * (2_107_520 + 1_040 + 256 + 65_536 + 1_056_768
+                                                                    + 65_536)

@@ -30,7 +30,7 @@ DSA_WS_TOPK = 1
 DSA_WS_ATTENTION = 2
 DSA_WS_LAYER = 3
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 P = c_void_p
 # Every entry point of include/dsa_gfx950.h with its ctypes signature (restype, argtypes).
@@ -91,6 +91,11 @@ SIGNATURES: dict[str, tuple] = {
         c_int,
         [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, c_size_t, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
          c_int, c_int, c_float, c_int, P],
+    ),
+    "dsa_pooled_decode_step": (
+        c_int,
+        [P, c_int, P, c_int, P, P] + [P] * 15 + [c_size_t, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
+                                                  c_int, c_float, c_int, P],
     ),
     "dsa_pooled_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int]),
     "dsa_sparse_mla_pooled": (

@@ -78,12 +78,13 @@ hipError_t launch_decode_fused(const uint16_t* q_idx, const float* w, const uint
                                int num_pages, int stride, int keep, float scale, hipStream_t s);
 bool fused_pooled_ok(int num_cu, int Hi, int H, int Dqk, int stride, int kp, int page_size, int keep_pools);
 size_t fused_pooled_bytes(size_t zero_bytes, int B, int H);
+bool fused_step_ok(int kp);
 hipError_t launch_decode_fused_pooled(const uint16_t* q_idx, const float* w, const uint16_t* pool_key,
                                       const uint16_t* q, const uint8_t* kv, const float* kvs, const int* table,
                                       const int* npool, const int* positions, float* scores, int* pools, int* cnt,
                                       uint16_t* out, float* lse, void* ws, size_t zero_bytes, int B, int Hi, int H,
                                       int max_pages, int page_size, int num_pages, int kp, int keep_pools,
-                                      float scale, hipStream_t s);
+                                      float scale, const PoolKeyWrite* pkw, hipStream_t s);
 bool topk_supported(int max_len, int keep, int vis_only);
 hipError_t launch_sparse_mla(const uint16_t* q, const uint8_t* kv, const float* kvs, const int* idx, const int* cnt,
                              const int* table, const int* rows, const float* bias, uint16_t* out, float* out_f32,
@@ -1000,30 +1001,74 @@ static int pooled_checks(const void* q_idx_bf16, const float* w, const void* poo
   return DSA_OK;
 }
 
-int dsa_pooled_decode_layer(const void* q_idx_bf16, const float* w, const void* pool_key_bf16, const void* q_bf16,
-                            const uint8_t* kv_fp8, const float* kv_scale, const int32_t* page_table,
-                            const int32_t* npool, const int32_t* positions, float* scores, int32_t* pools,
-                            int32_t* cnt, void* out_bf16, float* lse, void* workspace, size_t workspace_bytes, int B,
-                            int Hi, int H, int Dqk, int max_pages, int page_size, int num_pages, int kp, int keep,
-                            float scale, int splits, void* stream) {
+// The pooled layer in one launch when fused_pooled_ok holds (pkw: the step's pool-key write in the same launch),
+// otherwise the write's own kernel (pkw) and the separate kernels.
+static int pooled_layer_or_step(const void* q_idx_bf16, const float* w, const void* pool_key_bf16, const void* q_bf16,
+                                const uint8_t* kv_fp8, const float* kv_scale, const int32_t* page_table,
+                                const int32_t* npool, const int32_t* positions, float* scores, int32_t* pools,
+                                int32_t* cnt, void* out_bf16, float* lse, void* workspace, size_t workspace_bytes,
+                                int B, int Hi, int H, int Dqk, int max_pages, int page_size, int num_pages, int kp,
+                                int keep, float scale, int splits, const dsa::PoolKeyWrite* pkw, void* stream) {
   int stride = 0;
   const int st = pooled_checks(q_idx_bf16, w, pool_key_bf16, q_bf16, kv_fp8, page_table, npool, positions, scores,
                                pools, cnt, out_bf16, workspace, workspace_bytes, B, Hi, H, Dqk, max_pages, page_size,
                                num_pages, kp, keep, splits, &stride);
   if (st != DSA_OK || B == 0) return st;
-  if (splits != 0 || !dsa::fused_pooled_ok(num_cu(), Hi, H, Dqk, stride, kp, page_size, keep))
+  if (splits != 0 || !dsa::fused_pooled_ok(num_cu(), Hi, H, Dqk, stride, kp, page_size, keep)) {
+    if (pkw) {
+      const int r = dsa_pool_keys_write(pkw->rows, pkw->rows_fp8, pkw->rows_scale, pkw->rows_width, pkw->ape,
+                                        positions, page_table, 0, max_pages, pkw->slot_mapping,
+                                        const_cast<void*>(pool_key_bf16), B, kp, page_size,
+                                        (long long)num_pages * page_size, stream);
+      if (r != DSA_OK) return r;
+    }
     return dsa_pooled_decode_layer_chain(q_idx_bf16, w, pool_key_bf16, q_bf16, kv_fp8, kv_scale, page_table, npool,
                                          positions, scores, pools, cnt, out_bf16, lse, workspace, workspace_bytes, B,
                                          Hi, H, Dqk, max_pages, page_size, num_pages, kp, keep, scale, splits, stream);
+  }
+  if (pkw && !dsa::fused_step_ok(kp)) {
+    // the write's own kernel, then the layer's one launch
+    const int r = dsa_pool_keys_write(pkw->rows, pkw->rows_fp8, pkw->rows_scale, pkw->rows_width, pkw->ape, positions,
+                                      page_table, 0, max_pages, pkw->slot_mapping, const_cast<void*>(pool_key_bf16),
+                                      B, kp, page_size, (long long)num_pages * page_size, stream);
+    if (r != DSA_OK) return r;
+    pkw = nullptr;
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (ready_zero(workspace, dsa::topk_zero_bytes(B), s) != hipSuccess) return DSA_ELAUNCH;
   const int r = status(dsa::launch_decode_fused_pooled(
       static_cast<const uint16_t*>(q_idx_bf16), w, static_cast<const uint16_t*>(pool_key_bf16),
       static_cast<const uint16_t*>(q_bf16), kv_fp8, kv_scale, page_table, npool, positions, scores, pools, cnt,
       static_cast<uint16_t*>(out_bf16), lse, workspace, dsa::topk_zero_bytes(B), B, Hi, H, max_pages, page_size,
-      num_pages, kp, keep, scale, s));
+      num_pages, kp, keep, scale, pkw, s));
   if (r != DSA_OK) drop_zero(workspace);
   return r;
+}
+
+int dsa_pooled_decode_layer(const void* q_idx_bf16, const float* w, const void* pool_key_bf16, const void* q_bf16,
+                            const uint8_t* kv_fp8, const float* kv_scale, const int32_t* page_table,
+                            const int32_t* npool, const int32_t* positions, float* scores, int32_t* pools,
+                            int32_t* cnt, void* out_bf16, float* lse, void* workspace, size_t workspace_bytes, int B,
+                            int Hi, int H, int Dqk, int max_pages, int page_size, int num_pages, int kp, int keep,
+                            float scale, int splits, void* stream) {
+  return pooled_layer_or_step(q_idx_bf16, w, pool_key_bf16, q_bf16, kv_fp8, kv_scale, page_table, npool, positions,
+                              scores, pools, cnt, out_bf16, lse, workspace, workspace_bytes, B, Hi, H, Dqk, max_pages,
+                              page_size, num_pages, kp, keep, scale, splits, nullptr, stream);
+}
+
+int dsa_pooled_decode_step(const void* rows, int rows_fp8, const float* rows_scale, int rows_width, const float* ape,
+                           const int64_t* slot_mapping, const void* q_idx_bf16, const float* w, void* pool_key_bf16,
+                           const void* q_bf16, const uint8_t* kv_fp8, const float* kv_scale,
+                           const int32_t* page_table, const int32_t* npool, const int32_t* positions, float* scores,
+                           int32_t* pools, int32_t* cnt, void* out_bf16, float* lse, void* workspace,
+                           size_t workspace_bytes, int B, int Hi, int H, int Dqk, int max_pages, int page_size,
+                           int num_pages, int kp, int keep, float scale, int splits, void* stream) {
+  if (!rows || !ape || !slot_mapping) return DSA_EINVAL;
+  if (rows_width < 256) return DSA_EINVAL;
+  const dsa::PoolKeyWrite pkw{rows, rows_scale, ape, slot_mapping, rows_width, rows_fp8 != 0};
+  return pooled_layer_or_step(q_idx_bf16, w, pool_key_bf16, q_bf16, kv_fp8, kv_scale, page_table, npool, positions,
+                              scores, pools, cnt, out_bf16, lse, workspace, workspace_bytes, B, Hi, H, Dqk, max_pages,
+                              page_size, num_pages, kp, keep, scale, splits, &pkw, stream);
 }
 
 int dsa_pooled_decode_layer_chain(const void* q_idx_bf16, const float* w, const void* pool_key_bf16,

@@ -67,6 +67,17 @@ struct PoolForm {
   int empty_n;         // rows + cnt form: the masked slots a row with cnt 0 attends (0: one)
   const int* n_live;   // null, or one int on the device: rows at or past it are neither computed nor written
 };
+// The pooled decode step's pool-key write, folded into the pooled layer's launch (dsa_pooled_decode_step): the
+// indexer rows cache [slots][rows_width] (e4m3 with a per-slot fp32 scale, or bf16: rows_fp8 0), the pool-position
+// bias [kpool][128] fp32 and each row's written token's cache slot.
+struct PoolKeyWrite {
+  const void* rows;
+  const float* rows_scale;
+  const float* ape;
+  const int64_t* slot_mapping;
+  int rows_width;
+  int rows_fp8;
+};
 constexpr int HIST_REPLICAS = 1;
 // The first bytes of every decode workspace, at the same offset whatever the batch size: per XCD (8 x 16 words) the
 // XCD-local barriers' arrival and exit counters (zero between calls), then two status words that persist across

@@ -203,7 +203,7 @@ struct FusedArgs {
   uint32_t* lst;   // [B][32][FuForm::LROW]: per workgroup its key list
   uint16_t* part;  // [B][S][H][512]: split outputs (normalised, bf16), a split's heads side by side
 
-  float2* ml;      // [B][H][S]: split max and sum
+  float2* ml;      // [B][S][H]: split max and sum
   int B, Hi, H, max_pages, page_size, page_shift, num_pages, stride, keep;
   int num_slots;  // num_pages * page_size
   float scale;
@@ -214,6 +214,13 @@ struct FusedArgs {
   const int* positions;
   int kp_shift;
   int ppp_shift;  // the pooled one-launch layer: log2 of the pools per page (pool p's key: page row p >> ppp_shift)
+  // the pooled step (the pool-key write in the same launch): the indexer rows cache [slots][pk_width] (e4m3 with
+  // pk_scale per slot, or bf16), the pool-position bias [kpool][128] and each row's written token's slot
+  const void* pk_rows;
+  const float* pk_scale;
+  const float* pk_ape;
+  const int64_t* slot_mapping;
+  int pk_width, pk_fp8;
   int row0;  // this launch's first row (rows row0 .. row0 + 7)
 };
 
@@ -351,8 +358,95 @@ __device__ __forceinline__ void fu_my_keys(const uint8_t* lds, uint32_t (&key)[2
 // the workgroup's range, NEG_INF past the block. The pooled form (POOL) scores pools: a position is a pool, its key
 // 128 bf16 with no scale at page row p >> ppp_shift (trnrt/models/mla.py:615-630), the arithmetic of the bf16 decode
 // indexer; its key list holds every key of the block, so it writes no bin list (no two-exchange selection reads one).
-template <int MT, bool POOL = false>
+// The pooled step's pool-key write (WRITE; trnrt/models/mla.py:1262-1296 `write_pool_keys` with
+// trnrt/models/glm5_next.py:151-160 `pool_keys`, the arithmetic of pool_keys_kernel): the row's written token's pool
+// key, pk[d] = bf16( sum_t bf16( bf16(softmax_t(g_t[d] + ape[t, d])) * k_t[d] ) ) over its kpool cached indexer rows
+// [key 128 | gate logits 128], from one wave (2 channels a lane), stored as kpool pieces of 128 / kpool values, piece
+// i into the slot of the pool's i-th token (a padded row, slot in the null page: every piece into its own slot);
+// returns this lane's two channels as bf16 bits (the key's 128 values across the wave). Loads first (fu_pool_key_load),
+// so that they overlap the wave's key tiles.
+constexpr int PKF_MAXKP = 8;
+struct PoolKeyRows {
+  float k[PKF_MAXKP][2], g[PKF_MAXKP][2], ape[PKF_MAXKP][2];
+  long first;  // the slot of the pool's token 0 (a padded row: its own slot)
+  bool real;
+};
+template <int KP>
+__device__ __forceinline__ long fu_pool_slot(const FusedArgs& a, const PoolKeyRows& r, int t) {
+  const long sl = r.real ? r.first + min(t, KP - 1) : r.first;
+  return min(max(sl, 0L), (long)a.num_slots - 1);  // in range whatever the inputs
+}
+template <int KP>
+__device__ __forceinline__ void fu_pool_key_load_t(const FusedArgs& a, int pos, long own, PoolKeyRows& r) {
+  constexpr int Di = FU_D;
+  const int lane = threadIdx.x & (WAVE - 1);
+  r.real = own >= a.page_size;
+  r.first = r.real ? own - (pos & (KP - 1)) : own;
+#pragma unroll
+  for (int t = 0; t < KP; ++t) {
+    const long slot = fu_pool_slot<KP>(a, r, t);
+    const size_t base = (size_t)slot * a.pk_width;
+    if (a.pk_fp8) {
+      const uint8_t* row = static_cast<const uint8_t*>(a.pk_rows) + base;
+      const float sc = a.pk_scale ? a.pk_scale[slot] : 1.0f;
+      const auto kf = __builtin_amdgcn_cvt_pk_f32_fp8(*reinterpret_cast<const uint16_t*>(row + 2 * lane), false);
+      const auto gf = __builtin_amdgcn_cvt_pk_f32_fp8(*reinterpret_cast<const uint16_t*>(row + Di + 2 * lane), false);
+      // the reference reads the e4m3 rows in bf16 (exact); a per-token scale is applied in fp32, rounded to bf16
+      r.k[t][0] = __uint_as_float((uint32_t)f32_to_bf16_bits(kf[0] * sc) << 16);
+      r.k[t][1] = __uint_as_float((uint32_t)f32_to_bf16_bits(kf[1] * sc) << 16);
+      r.g[t][0] = __uint_as_float((uint32_t)f32_to_bf16_bits(gf[0] * sc) << 16);
+      r.g[t][1] = __uint_as_float((uint32_t)f32_to_bf16_bits(gf[1] * sc) << 16);
+    } else {
+      const uint16_t* row = static_cast<const uint16_t*>(a.pk_rows) + base;
+      const uint32_t kw = *reinterpret_cast<const uint32_t*>(row + 2 * lane);
+      const uint32_t gw = *reinterpret_cast<const uint32_t*>(row + Di + 2 * lane);
+      r.k[t][0] = __uint_as_float(kw << 16), r.k[t][1] = __uint_as_float(kw & 0xffff0000u);
+      r.g[t][0] = __uint_as_float(gw << 16), r.g[t][1] = __uint_as_float(gw & 0xffff0000u);
+    }
+    r.ape[t][0] = a.pk_ape[t * Di + 2 * lane];
+    r.ape[t][1] = a.pk_ape[t * Di + 2 * lane + 1];
+  }
+}
+template <int KP>
+__device__ __forceinline__ uint32_t fu_pool_key_write_t(const FusedArgs& a, const PoolKeyRows& r) {
+  constexpr int Di = FU_D;
+  const int lane = threadIdx.x & (WAVE - 1);
+  uint32_t out = 0;
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    float x[KP], m = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < KP; ++t) {
+      x[t] = r.g[t][c] + r.ape[t][c];
+      m = fmaxf(m, x[t]);
+    }
+    float e[KP], sum = 0.0f;
+#pragma unroll
+    for (int t = 0; t < KP; ++t) {
+      e[t] = expf(x[t] - m);
+      sum += e[t];
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int t = 0; t < KP; ++t) {
+      const float wt = __uint_as_float((uint32_t)f32_to_bf16_bits(e[t] / sum) << 16);
+      acc += __uint_as_float((uint32_t)f32_to_bf16_bits(wt * r.k[t][c]) << 16);
+    }
+    out |= (uint32_t)f32_to_bf16_bits(acc) << (16 * c);
+  }
+  // piece i (channels i Di / kp ..) into slot i: this lane's two channels
+  constexpr int per = Di / KP;
+  const int piece = (2 * lane) / per;
+  uint16_t* pk = reinterpret_cast<uint16_t*>(const_cast<uint8_t*>(a.k));
+  *reinterpret_cast<uint32_t*>(pk + (size_t)fu_pool_slot<KP>(a, r, piece) * per + (2 * lane - piece * per)) = out;
+  return out;
+}
+constexpr int FU_STEP_KP = 4;  // the kpool the one-launch step takes (GLM's); others write with the write's kernel
+constexpr int L_PKEY = 4096;  // stage 1 of the pooled step: the written pool's key [128] bf16
+
+template <int MT, bool POOL = false, bool WRITE = false>
 __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int b, int j, int L) {
+  static_assert(!WRITE || POOL, "the pool-key write belongs to the pooled form");
   using FF = FuForm<POOL>;
   uint16_t* qs = reinterpret_cast<uint16_t*>(lds + L_QS);
   float* wsh = reinterpret_cast<float*>(lds + L_WS);
@@ -366,6 +460,13 @@ __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int
   const bool lists = fu_lists_on<POOL>(a, L);
   uint32_t* plst = a.lst + ((size_t)b * FU_NW + j) * FF::LROW;  // the pooled form's key list
 
+  // the pooled step: the row's written position and its slot, loaded with the queries
+  int pk_pos = 0;
+  long pk_own = 0;
+  if (WRITE) {
+    pk_pos = a.positions[b];
+    pk_own = a.slot_mapping[b];
+  }
   // the queries' loads (32 MT heads of 16 pieces: MT per thread), the weights, the tiles' pages
   u32x4 qv[MT];
 #pragma unroll
@@ -398,6 +499,16 @@ __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int
     const int pg = trow[min((t * FU_TILE) >> a.page_shift, a.max_pages - 1)];
     pages = in_row(i) ? safe_page(pg, a.num_pages) : 0;
   }
+  // the pooled step: the written token's pool kP, its key written by the wave whose tile holds kP (the last block's
+  // last wave when kP is past the row's blocks) and scored from the new key when the pool is complete (kP < L)
+  int kP = 0;
+  bool kwave = false;
+  PoolKeyRows pkr;
+  if (WRITE) {
+    kP = max(pk_pos, 0) >> a.kp_shift;
+    const int jw = min(kP / kw, FU_NW - 1), tw = min(max(kP - jw * kw, 0) / FU_TILE, FU_WAVES - 1);
+    kwave = j == jw && wave == tw;  // wave-uniform
+  }
   u32x4 kv[FU_TPW][FF::KV];
   float ksc[FU_TPW];
   auto tile_loads = [&](int i) __attribute__((always_inline)) {
@@ -423,6 +534,7 @@ __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int
 #pragma unroll
     for (int i = 0; i < FU_AHEAD; ++i) tile_loads(i);
   }
+  if (WRITE && kwave) fu_pool_key_load_t<FU_STEP_KP>(a, pk_pos, pk_own, pkr);  // the written pool's rows, behind the key tiles
 
 #pragma unroll
   for (int r = 0; r < MT; ++r) {
@@ -435,6 +547,10 @@ __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int
   int* scr = reinterpret_cast<int*>(lds + L_MISC);
   if (tid == 0) scr[8] = -1;  // the key list's bin search below
   __syncthreads();
+  if (WRITE && kwave) {
+    const uint32_t key2 = fu_pool_key_write_t<FU_STEP_KP>(a, pkr);
+    if (kP < L) reinterpret_cast<uint32_t*>(lds + L_PKEY)[lane] = key2;
+  }
 
   if (live) {
     bf16x8 qa[MT][8];
@@ -457,6 +573,14 @@ __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int
         __builtin_amdgcn_sched_barrier(0);
         tile_loads(i + FU_AHEAD);
         __builtin_amdgcn_sched_barrier(0);
+      }
+      if (WRITE && i == 0 && kwave && kP < L) {
+        // the written pool's two lanes take its new key (the tile's loads read the cache before the write)
+        if (jk == (kP & (FU_TILE - 1))) {
+          const u32x4* nk = reinterpret_cast<const u32x4*>(lds + L_PKEY + 128 * h);
+#pragma unroll
+          for (int c = 0; c < FF::KV; ++c) kv[0][c] = nk[c];
+        }
       }
       const int pos = (t_begin + FU_WAVES * i) * FU_TILE + jk, e = (wave + FU_WAVES * i) * FU_TILE + jk;
       const bool mine = wave + FU_WAVES * i < nt;  // a position of this workgroup's block
@@ -1575,7 +1699,7 @@ __global__ __launch_bounds__(FU_THREADS, 1) void decode_fused_kernel(FusedArgs a
 // bf16 pool-key cache in blocks of at most 256 pools, the exact top-keep pools from the key lists (each holding its
 // whole block), then the attention over the selected pools' tokens and the row's tail (512-wide rows, 32 heads a
 // workgroup, splits of 128 token slots) and the combine, as the kpool-1 layer.
-template <int HPW>
+template <int HPW, bool WRITE>
 __global__ __launch_bounds__(FU_THREADS, 1) void decode_pooled_fused_kernel(FusedArgs a) {
   __shared__ __align__(16) uint8_t lds[FU_LDS];
   const int x = blockIdx.x % FU_XCDS, j = blockIdx.x / FU_XCDS;
@@ -1583,7 +1707,7 @@ __global__ __launch_bounds__(FU_THREADS, 1) void decode_pooled_fused_kernel(Fuse
   const int b = a.row0 + x;
   if (b >= a.B) return;  // an XCD without a row
   const int L = min(max(a.ctx_len[b], 0), min(a.stride, FU_POOL_MAXLEN));
-  fu_indexer<1, true>(a, lds, b, j, L);
+  fu_indexer<1, true, WRITE>(a, lds, b, j, L);
   fu_barrier(sync, 1);  // A: the row's scores and key lists
   u32x4 qv[FuAtt<HPW, 512, true>::QPT];
   float live_bias;
@@ -1914,6 +2038,9 @@ bool fused_pooled_ok(int num_cu, int Hi, int H, int Dqk, int stride, int kp, int
   return fused_hpw(H, keep_pools * kp) == 32 && FuAtt<32>::SPLIT % kp == 0;
 }
 
+// Whether the one-launch pooled layer also takes the step's pool-key write (kpool FU_STEP_KP).
+bool fused_step_ok(int kp) { return kp == FU_STEP_KP; }
+
 size_t fused_pooled_bytes(size_t zero_bytes, int B, int H) {
   if (H < 32 || H % 32) return 0;
   const int S = fused_splits(H, 32);
@@ -1929,7 +2056,7 @@ hipError_t launch_decode_fused_pooled(const uint16_t* q_idx, const float* w, con
                                       const int* npool, const int* positions, float* scores, int* pools, int* cnt,
                                       uint16_t* out, float* lse, void* ws, size_t zero_bytes, int B, int Hi, int H,
                                       int max_pages, int page_size, int num_pages, int kp, int keep_pools,
-                                      float scale, hipStream_t s) {
+                                      float scale, const PoolKeyWrite* pkw, hipStream_t s) {
   FusedArgs a{};
   const int S = fused_splits(H, 32);
   char* p = static_cast<char*>(ws);
@@ -1975,10 +2102,21 @@ hipError_t launch_decode_fused_pooled(const uint16_t* q_idx, const float* w, con
   a.positions = positions;
   a.kp_shift = __builtin_ctz((unsigned)kp);
   a.ppp_shift = __builtin_ctz((unsigned)ppp);
+  if (pkw) {
+    a.pk_rows = pkw->rows;
+    a.pk_scale = pkw->rows_scale;
+    a.pk_ape = pkw->ape;
+    a.slot_mapping = pkw->slot_mapping;
+    a.pk_width = pkw->rows_width;
+    a.pk_fp8 = pkw->rows_fp8;
+  }
+  if (pkw && kp != FU_STEP_KP) return hipErrorInvalidValue;  // (fused_step_ok)
   const dim3 grid(FU_XCDS * FU_NW), block(FU_THREADS);
   for (int r0 = 0; r0 < B; r0 += FU_XCDS) {
     a.row0 = r0;
-    const hipError_t e = launch("decode_pooled_fused_kernel", decode_pooled_fused_kernel<32>, grid, block, s, a);
+    const hipError_t e =
+        pkw ? launch("decode_pooled_fused_kernel", decode_pooled_fused_kernel<32, true>, grid, block, s, a)
+            : launch("decode_pooled_fused_kernel", decode_pooled_fused_kernel<32, false>, grid, block, s, a);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;

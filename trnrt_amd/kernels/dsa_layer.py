@@ -148,13 +148,38 @@ class PooledDecodeLayer:
 
     def step(self, q_idx: torch.Tensor, w: torch.Tensor, pool_key: torch.Tensor, q: torch.Tensor,
              kv_cache: torch.Tensor, kv_scale: torch.Tensor | None, table: torch.Tensor, npool: torch.Tensor,
-             positions: torch.Tensor, check: bool = True, verify: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+             positions: torch.Tensor, check: bool = True, verify: bool = False,
+             write: tuple | None = None) -> tuple[torch.Tensor, torch.Tensor]:
         """(out bf16 [B, H, 512], lse fp32 [B, H]); self.scores / pools / cnt hold the intermediates. q_idx
         [B, Hi, 128] bf16, w [B, Hi] fp32 (128 ** -0.5 folded in), pool_key bf16 [slots, 128 / kp], q [B, H, dqk]
         bf16, kv_cache [slots, dqk] e4m3fn + kv_scale [slots] (None: unscaled), table [B, max_pages] int32, npool
         [B] int32 ((positions + 1) // kp), positions [B] int32. check=False skips the Python-side checks (the C ABI still
-        checks sizes); verify as DecodeLayer.step."""
+        checks sizes); verify as DecodeLayer.step.
+
+        write = (rows, ape, slot_mapping, rows_scale): the step's pool-key write first (dsa_cache.write_pool_keys of
+        each row's written token at positions[b], slot slot_mapping[b] int64 [B]; rows the indexer rows cache [slots,
+        W >= 256] e4m3fn or bf16, ape [kp, 128] fp32, rows_scale [slots] fp32 or None), as the reference's decode step
+        writes before it attends (trnrt/models/mla.py:448-452): the C ABI's dsa_pooled_decode_step, in the same
+        launch as the layer where the layer is one launch."""
         B, Hi, H = self.B, self.Hi, self.H
+        if write is not None:
+            rows, ape, slot_mapping, rows_scale = write
+            if check:
+                C.on_gpu(rows, ape, slot_mapping, rows_scale)
+                slots = self.num_pages * self.page_size
+                if not rows.is_contiguous() or rows.dim() != 2 or rows.shape[0] != slots or rows.shape[1] < 256:
+                    raise ValueError(f"PooledDecodeLayer.step: rows {tuple(rows.shape)} for {slots} slots")
+                if rows.dtype not in (C.FP8, torch.uint8, torch.bfloat16):
+                    raise ValueError(f"PooledDecodeLayer.step: rows of dtype {rows.dtype}")
+                C.need(ape, "ape", torch.float32, (self.kp, 128))
+                C.need(slot_mapping, "slot_mapping", torch.int64, (B,))
+                if rows_scale is not None:
+                    C.need(rows_scale, "rows_scale", torch.float32, (slots,))
+            if self.chain:
+                from . import dsa_cache
+                dsa_cache.write_pool_keys(pool_key, rows, positions, table, slot_mapping, ape, self.page_size,
+                                          self.kp, rows_scale=rows_scale)
+                write = None
         if check:
             C.on_gpu(q_idx, w, pool_key, q, kv_cache, kv_scale, table, npool, positions)
             C.need(q_idx, "q_idx", torch.bfloat16, (B, Hi, 128))
@@ -170,7 +195,13 @@ class PooledDecodeLayer:
                 raise ValueError(f"kv cache of {kv_cache.numel()} bytes for {slots} slots of {self.dqk}")
             if kv_scale is not None:
                 C.need(kv_scale, "kv_scale", torch.float32, (slots,))
-        fn = _lib.lib().dsa_pooled_decode_layer_chain if self.chain else _lib.lib().dsa_pooled_decode_layer
+        if write is not None:
+            rows, ape, slot_mapping, rows_scale = write
+            pre = (rows.data_ptr(), int(rows.dtype != torch.bfloat16), C.ptr(rows_scale), rows.shape[1],
+                   ape.data_ptr(), slot_mapping.data_ptr())
+            fn = lambda *args: _lib.lib().dsa_pooled_decode_step(*pre, *args)  # noqa: E731
+        else:
+            fn = _lib.lib().dsa_pooled_decode_layer_chain if self.chain else _lib.lib().dsa_pooled_decode_layer
         st = fn(
             q_idx.data_ptr(), w.data_ptr(), pool_key.data_ptr(), q.data_ptr(), kv_cache.data_ptr(),
             C.ptr(kv_scale), table.data_ptr(), npool.data_ptr(), positions.data_ptr(), self.scores.data_ptr(),

@@ -300,10 +300,10 @@ def pooled_indexer_bytes(cfg: PooledConfig, npool: list[int]) -> int:
 def pooled_step_bytes(cfg: PooledConfig, npool: list[int], tokens: list[int]) -> int:
     """Bytes one pooled decode step must move at least: the pool-key write (the current pool's kp indexer rows of
     256 B + scale, the kp pieces of 2 D / kp B), the indexer's inputs (pooled_indexer_bytes), the attention's bf16
-    queries, the attended tokens' latent rows (dqk B + fp32 scale) and the fp32 output."""
+    queries, the attended tokens' latent rows (dqk B + fp32 scale) and the bf16 output."""
     tot = pooled_indexer_bytes(cfg, npool)
     for t in tokens:
-        tot += cfg.kp * (2 * cfg.D + 4) + 2 * cfg.D + 2 * cfg.H * cfg.dqk + (cfg.dqk + 4) * t + 4 * cfg.H * 512
+        tot += cfg.kp * (2 * cfg.D + 4) + 2 * cfg.D + 2 * cfg.H * cfg.dqk + (cfg.dqk + 4) * t + 2 * cfg.H * 512
     return tot
 
 
