@@ -28,6 +28,7 @@ profiles/traffic.json and reported when they were taken on the same workload.
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import os
 import sys
@@ -292,6 +293,9 @@ def prefill_main(args) -> int:
     from trnrt_amd.kernels import dsa_long_select as LS
 
     cfg = W.PREFILL_CONFIGS[args.config]
+    if args.bf16_queries:
+        # the reference's own query precision: bf16 indexer queries (the bf16-query indexer kernel)
+        cfg = dataclasses.replace(cfg, q_fp8=False)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     inp = W.make_prefill_inputs(cfg, seed=0, device=dev, attention=True)
@@ -344,7 +348,8 @@ def prefill_main(args) -> int:
         "vs_baseline": None,
         "dtype": "fp8" if cfg.q_fp8 else "bf16",
         "data": "synthetic",
-        "config": {"workload": f"config {args.config}: {cfg.name}", "cached": cfg.cached, "chunk": C,
+        "config": {"workload": f"config {args.config}: {cfg.name}" + (" (bf16 queries)" if args.bf16_queries else ""),
+                   "cached": cfg.cached, "chunk": C,
                    "queries": "fp8 e4m3 + fp32 scale per (query, head)" if cfg.q_fp8 else "bf16",
                    "indexer_heads": cfg.Hi, "q_heads": cfg.H, "keep": cfg.keep, "page_size": cfg.page_size,
                    "keys": "fp8 e4m3 [128] + fp32 scale per token", "kv": "fp8 e4m3 [576] + fp32 scale per token",
@@ -622,6 +627,8 @@ def main() -> int:
     ap.add_argument("--chain", action="store_true",
                     help="run the separate kernels (dsa_decode_layer_chain) even where the one-launch layer applies")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--bf16-queries", action="store_true",
+                    help="config 5: bf16 indexer queries (the reference's precision) instead of e4m3 with scales")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB")
     args = ap.parse_args()
     if args.gpus != 1:
