@@ -42,7 +42,9 @@ def _load_consts():
     assert "constexpr int NI = (AT::CAP * KPIECES + FU_THREADS - 1) / FU_THREADS;" in text
     assert "sl[i] = slot_l[min(row, AT::CAP - 1)];" in text
     assert "const int k = wave + FU_WAVES * i;\n      if (k * WAVE < units) {" in text
-    assert "const uint8_t* src = a.kv + (size_t)sl[i] * DQK + 16 * min(pcs[i], PIECES - 1);" in text
+    assert "const uint8_t* src = a.kv + (size_t)sl[i] * DQK + 16 * min(pc, PIECES - 1);" in text
+    # the issue loop steps the piece alone (pc += DP, less KPIECES on a carry), as the slot loop steps it
+    assert "      pc += DP;\n      if (pc >= KPIECES) pc -= KPIECES;\n" in text
     assert "(__attribute__((address_space(3))) void*)(kt + 1024 * k), 16, 0, 0);" in text
     return CONSTS
 
@@ -72,6 +74,7 @@ def test_gather_lanes_stay_inside_the_padded_rows(hpw, dqk, xt):
         for wave in range(WAVES):
             for lane in range(WAVE):
                 row, pc = (WAVE * wave + lane) // kpieces, (WAVE * wave + lane) % kpieces
+                pc0 = pc
                 for i in range(ni):
                     k = wave + WAVES * i
                     assert 0 <= min(row, cap - 1) < cap  # the slot read, taken for every i
@@ -82,6 +85,8 @@ def test_gather_lanes_stay_inside_the_padded_rows(hpw, dqk, xt):
                         assert 0 <= min(pc, pieces - 1) < pieces
                         assert 1024 * k + 16 * lane + 16 <= tile_bytes, f"{n_slots} slots: LDS past the row tile"
                         loads += lane == 0
+                    # the issue loop's piece, stepped without the row: the same sequence
+                    assert pc == (pc0 + DP * i) % kpieces
                     row += DR
                     pc += DP
                     if pc >= kpieces:

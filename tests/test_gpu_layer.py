@@ -182,3 +182,34 @@ def test_layer_full_size(c):
     ri, rc = O.topk_ref(sc, g.cfg.keep, g.lengths)
     assert torch.equal(L.idx.cpu().long(), ri) and torch.equal(L.cnt.cpu().long(), rc)
     _attention_check(g, L, rows=range(g.cfg.B))
+
+
+def test_layer_long_rows_two_launches():
+    """A batch with rows past 32,768 tokens is two launches: the long-row indexer (scores and each row's first-level
+    histogram), then the selection, attention and combine in one XCD-local launch (decode_long_attend_kernel);
+    12 rows (two rows on four XCDs) of ragged lengths, every stage against the oracle, the workspace's histograms
+    left zero (a second step gives the same results)."""
+    from tests._helpers import launched_kernels
+
+    lengths = [40000, 131072, 8192, 65536, 33000, 100000, 50000, 9000, 120000, 32769, 70000, 16384]
+    say("layer long rows, two launches")
+    cfg = W.Config("layer-long-2", B=len(lengths), L=131072, H=64, Hi=64)
+    inp = W.make_inputs(cfg, seed=31, lengths=lengths)
+    g = inp.to("cuda")
+    L = DecodeLayer(cfg.B, cfg.Hi, cfg.H, g.max_pages, cfg.page_size, g.num_pages, cfg.keep, cfg.scale,
+                    max_len=max(g.lengths))
+    step = lambda: L.step(g.q_idx, g.w_k, g.k_cache, g.k_scale, g.q, g.kv_cache, g.kv_scale, g.table,  # noqa: E731
+                          g.ctx_len)
+    names = launched_kernels(step)
+    assert names == ["indexer_decode_long_kernel", "decode_long_attend_kernel"], names
+    torch.cuda.synchronize()
+    sc = L.scores.cpu()
+    ri, rc = O.topk_ref(sc, cfg.keep, inp.ctx_len)
+    assert torch.equal(L.cnt.cpu().long(), rc)
+    assert torch.equal(L.idx.cpu().long(), ri)
+    _attention_check(inp, L)
+    out0 = L.out.clone()
+    step()
+    torch.cuda.synchronize()
+    assert torch.equal(L.idx.cpu().long(), ri) and torch.equal(L.out, out0)
+    assert L.status()["gave_up"] == 0

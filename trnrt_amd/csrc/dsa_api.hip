@@ -65,6 +65,13 @@ hipError_t launch_decode_attend(const uint16_t* q, const uint8_t* kv, const floa
                                 const int* idx, const int* table, const int* cnt, uint16_t* out, float* lse, void* ws,
                                 int* sync, int B, int H, int max_pages, int page_size, int num_pages, int keep,
                                 float scale, hipStream_t s);
+bool long_attend_ok(int num_cu, int H, int keep, long max_len, int stride);
+size_t long_attend_bytes(int B, int H, int keep, long max_len);
+hipError_t launch_decode_long_attend(const uint16_t* q, const uint8_t* kv, const float* kvs, const int* table,
+                                     const int* ctx_len, const float* scores, int stride, int* hist, int* idx,
+                                     int* cnt, uint16_t* out, float* lse, void* ws, int* sync, int B, int H,
+                                     int max_pages, int page_size, int num_pages, int keep, float scale, long max_len,
+                                     hipStream_t s);
 bool attend_xcd_pooled_ok(int num_cu, int H, int Dqk, int keep_tokens);
 hipError_t launch_decode_attend_pooled(const uint16_t* q, const uint8_t* kv, const float* kvs, const int* pools,
                                        const int* cnt, const int* npool, const int* positions, const int* table,
@@ -759,8 +766,11 @@ size_t dsa_workspace_bytes(int kind, int B, int H, int keep, int max_len, int sp
     // attention takes the attention's place
     const size_t f = dsa::fused_layer_bytes(dsa::topk_zero_bytes(B), B, H, keep);
     const size_t x = align256(t) + align256(dsa::attend_xcd_bytes(B, H, keep));
+    // rows past 32,768 tokens: the selection, attention and combine in one launch, its lists past the attention's
+    const size_t lg = align256(t) + align256(dsa::long_attend_bytes(B, H, keep, max_len));
     total = f > total ? f : total;
     total = x > total ? x : total;
+    total = lg > total ? lg : total;
   }
   return total;
 }
@@ -879,6 +889,19 @@ static int layer_chain(const void* q_idx_bf16, const float* w, const uint8_t* k_
   if (e != hipSuccess) {
     if (hist) dsa::launch_fill_zero(hist, dsa::topk_hist_bytes(B), s);  // a partial histogram may be in
     return DSA_ELAUNCH;
+  }
+  if (long_sel && splits == 0 && dsa::long_attend_ok(num_cu(), H, keep, max_len, score_stride)) {
+    // the long rows' selection, attention and combine in one launch over the indexer's scores and histograms
+    char* lws = static_cast<char*>(workspace) + t_need + layer_rows_bytes(B, keep);
+    e = dsa::launch_decode_long_attend(static_cast<const uint16_t*>(q_bf16), kv_fp8, kv_scale, page_table, ctx_len,
+                                       scores, score_stride, hist, idx, cnt, static_cast<uint16_t*>(out_bf16), lse,
+                                       lws, static_cast<int*>(workspace), B, H, max_pages, page_size, num_pages, keep,
+                                       scale, max_len, s);
+    if (e != hipSuccess) {
+      dsa::launch_fill_zero(dsa::ws_hist(workspace), dsa::topk_hist_bytes(B), s);  // (as below)
+      return DSA_ELAUNCH;
+    }
+    return DSA_OK;
   }
   // with the histogram from the indexer the top-k also resolves the selected positions to cache slots, so the
   // attention reads slot ids directly (one dependent load round fewer)

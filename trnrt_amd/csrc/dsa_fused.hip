@@ -1423,12 +1423,12 @@ __device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int 
     constexpr int DR = FU_WAVES * WAVE / KPIECES, DP = FU_WAVES * WAVE % KPIECES;
     constexpr int NI = (AT::CAP * KPIECES + FU_THREADS - 1) / FU_THREADS;  // loads per lane at most
     const int units = padded * KPIECES;
-    int row = (WAVE * wave + lane) / KPIECES, pc = WAVE * wave + lane - row * KPIECES;
-    int sl[NI], pcs[NI];
+    const int row0 = (WAVE * wave + lane) / KPIECES, pc0 = WAVE * wave + lane - row0 * KPIECES;
+    int row = row0, pc = pc0;
+    int sl[NI];
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       sl[i] = slot_l[min(row, AT::CAP - 1)];  // (past the units: a row of the list, never loaded)
-      pcs[i] = pc;
       row += DR;
       pc += DP;
       if (pc >= KPIECES) {
@@ -1436,13 +1436,16 @@ __device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int 
         ++row;
       }
     }
+    pc = pc0;  // (the pieces again, stepped as above)
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const int k = wave + FU_WAVES * i;
       if (k * WAVE < units) {
-        const uint8_t* src = a.kv + (size_t)sl[i] * DQK + 16 * min(pcs[i], PIECES - 1);
+        const uint8_t* src = a.kv + (size_t)sl[i] * DQK + 16 * min(pc, PIECES - 1);
         __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(kt + 1024 * k), 16, 0, 0);
       }
+      pc += DP;
+      if (pc >= KPIECES) pc -= KPIECES;
     }
   }
   const float ksv = tid < padded ? (a.kvs ? a.kvs[slot] : 1.0f) : 0.0f;  // kvs null: the unscaled cache
@@ -1823,6 +1826,406 @@ __global__ __launch_bounds__(FU_THREADS, 1) void decode_attend_kernel(FusedArgs 
   fu_exit(sync);
 }
 
+// ---- Rows longer than 32,768 tokens: the selection, the attention and the combine in one launch ----
+// After the long-row indexer (indexer_decode_long_kernel: the rows' scores [B, stride] and each row's first-level
+// histogram of the top 12 key bits), the rows of a launch (row0 + x + 8 r on XCD x, r < rpl) are selected and
+// attended by their XCD's 32 workgroups, replacing the long top-k's three launches (chunk counts, one resolving
+// workgroup per row, ordered output) and the separate attention launch:
+//   1. every workgroup finds the bin c0 of the row's keep-th largest key in the row's histogram (c0 = -1, every
+//      visible key, when the row has at most keep), then lists its block of the row (positions [j bw, (j + 1) bw))
+//      as the (key, position) of its keys at or above c0, in position order; barrier (then the histogram is cleared);
+//   2. every workgroup reads the 32 lists: T (the keep-th largest key) from the next 12 and 8 bits of the keys in c0,
+//      each list's keys above and at T, the ties taken (the lowest positions: list order, then position order) and
+//      each list's first output index;
+//   3. the split's outputs [o0, o1): each list holding some of them is passed once with a block prefix of its keys
+//      above and at T (a selected key's output index follows), into the idx output and the split's slot list; then
+//      stage 4 of the one-launch layer (fu_attend). After the XCD's rows: barrier, the combine (stage 5).
+// The selection is exact (the reference's arithmetic of trnrt/kernels/dsa_topk.py, ties to the lowest positions),
+// as the long top-k's: same T, same outputs in the same order.
+struct LongAttArgs {
+  int* hist;        // [B][4096]: the rows' first-level histograms, zero again after the launch
+  uint32_t* lst;    // [B][32][LA_HDR + 2 bw]: per workgroup its block's list
+  int bw;           // positions per block, a multiple of LA_PASS x 512
+  int rpl;          // rows per XCD
+};
+constexpr int LA_HDR = 32;   // list header words (the count)
+constexpr int LA_PASS = 8;   // positions per thread and pass of stage 1 (two 16-byte score loads)
+constexpr int LA_MAXLEN = FU_NW * 65536;  // 2,097,152 tokens a row
+constexpr int L_LA = 0;      // stage 2's per-list words [6][32] (L_STATE's place)
+constexpr int LA_BATCH = 4;  // stage 1's passes a round of loads
+constexpr int L_LA_STAGE = 81920;  // stage 1's scores [LA_BATCH][4096] (past the split's positions, dead by stage 3)
+static_assert(L_LA_STAGE + LA_BATCH * FU_THREADS * LA_PASS * 4 <= FU_LDS, "stage 1's scores in LDS");
+static_assert(L_LA_STAGE >= FuAtt<32>::L_P + 4 * (FuAtt<32>::CAP + 8 + FuAtt<32>::SPLIT + 1) &&
+                  L_LA_STAGE + LA_BATCH * FU_THREADS * LA_PASS * 4 <= FuAtt<16>::L_P,
+              "stage 1's scores clear of the split's slot and position lists");
+static_assert(L_BINS + 4 * 4096 <= L_LA_STAGE, "stage 1's scores clear of the bins");
+
+// The split's queries (loaded before the selection, so that their load overlaps it).
+template <int HPW>
+__device__ __forceinline__ void la_queries(const FusedArgs& a, int b, int j, u32x4 (&qv)[FuAtt<HPW>::QPT]) {
+  const int tid = threadIdx.x, hg = j % a.HG;
+  // (unconditional: a workgroup past the last split loads its head group's queries and never uses them)
+  const u32x4* qsrc = reinterpret_cast<const u32x4*>(a.q + ((size_t)b * a.H + HPW * hg) * FU_DQK);
+#pragma unroll
+  for (int i = 0; i < FuAtt<HPW>::QPT; ++i) qv[i] = qsrc[min(tid + FU_THREADS * i, HPW * FU_DQK / 8 - 1)];
+}
+
+template <int HPW>
+__device__ __forceinline__ int la_prep(const FusedArgs& a, uint8_t* lds, const int* pos_l, int b, int j, int cnt_row,
+                                       const u32x4 (&qv)[FuAtt<HPW>::QPT], float* live_bias) {
+  // fu_attend_prep's token form, the split's positions taken from pos_l (the output order) instead of idx
+  using AT = FuAtt<HPW>;
+  constexpr int QPT = AT::QPT;
+  int* slot_l = reinterpret_cast<int*>(lds + AT::L_P);
+  const int tid = threadIdx.x;
+  const int s = j / a.HG;
+  const bool active = s < a.S;
+  const int o0 = active ? s * a.sps : 0, o1 = active ? min(o0 + a.sps, a.keep) : 0;
+  const int o = o0 + tid;
+  int sl = 0;
+  if (tid < AT::SPLIT && o < o1 && o < max(cnt_row, 1)) {  // the empty row lists output 0 (position 0)
+    const int p = max(pos_l[tid], 0), pi = p / a.page_size;
+    const int pg = a.table[(size_t)b * a.max_pages + min(pi, a.max_pages - 1)];
+    sl = safe_page(pg, a.num_pages) * a.page_size + (p - pi * a.page_size);
+  }
+  sl = (unsigned)sl < (unsigned)a.num_slots ? sl : 0;
+  if (active) {
+    uint16_t* qs = reinterpret_cast<uint16_t*>(lds + AT::L_QST);
+#pragma unroll
+    for (int i = 0; i < QPT; ++i) {
+      const int pc = tid + FU_THREADS * i;
+      if (pc < HPW * FU_DQK / 8)
+        *reinterpret_cast<u32x4*>(qs + (pc / (FU_DQK / 8)) * AT::AQROW + 8 * (pc % (FU_DQK / 8))) = qv[i];
+    }
+  }
+  if (tid < AT::CAP) slot_l[tid] = sl;  // padding rows read slot 0 (the slot list lies before the positions)
+  int n_slots = max(min(o1, cnt_row) - o0, 0);
+  *live_bias = 0.0f;
+  if (active && cnt_row == 0 && s == 0) {
+    n_slots = 1;
+    *live_bias = NEG_INF;
+  }
+  __syncthreads();  // the slot list and the queries
+  return n_slots;
+}
+
+// Stage 2 and the split's positions (stage 3) over the row's 32 lists, their counts in LDS (lcnt). The T search of
+// the one-exchange selection: the next 12 and 8 bits from the keys in c0 (c0 = -1: T = 0, every listed key taken),
+// each list's keys above and at T, the ties taken (room: the lowest positions, list order then position order) and
+// each list's first output index; then every selected key's output index, the split's [o0, o1) into pos_l.
+// la_select_regs: every list of at most LA_LCAP entries, held in registers (thread (w, q): list w's entries
+// 16 q .. 16 q + 15, one round of loads); la_select_loop: any lists, passed from the L2 (a list at a time).
+constexpr int LA_LPT = 16, LA_LCAP = 16 * LA_LPT;
+__device__ __forceinline__ void la_t_search(const FusedArgs& a, uint8_t* lds, int c0, int above0, uint32_t* T,
+                                            int* room) {
+  int* scr = reinterpret_cast<int*>(lds + L_MISC);
+  int* bins1 = reinterpret_cast<int*>(lds + L_BINS);
+  const int tid = threadIdx.x;
+  int hb[8];
+  *reinterpret_cast<int4*>(hb) = *reinterpret_cast<const int4*>(bins1 + 8 * tid);
+  *reinterpret_cast<int4*>(hb + 4) = *reinterpret_cast<const int4*>(bins1 + 8 * tid + 4);
+  int c1, above1;
+  int need = a.keep - above0;
+  fu_find_bin<8>(hb, need, scr + 16, &c1, &above1);
+  need -= above1;
+  *T = ((uint32_t)c0 << 20) | ((uint32_t)c1 << 8);
+  *room = need;  // (need >= bins1[c1]: every key of bin c1 is taken, T its lowest key with all its ties)
+  (void)tid;
+}
+
+__device__ __forceinline__ void la_select_regs(const FusedArgs& a, uint8_t* lds, const uint32_t* lst_b,
+                                               size_t lrow_words, int c0, int above0, int o0, int o1, int* pos_l) {
+  int* scr = reinterpret_cast<int*>(lds + L_MISC);
+  int* bins1 = reinterpret_cast<int*>(lds + L_BINS);
+  int* bins2 = reinterpret_cast<int*>(lds + L_BINS2);
+  int* lcnt = reinterpret_cast<int*>(lds + L_LA);
+  int *lgt = lcnt + FU_NW, *leq = lcnt + 2 * FU_NW, *ltake = lcnt + 3 * FU_NW, *loff = lcnt + 4 * FU_NW;
+  const int tid = threadIdx.x, lane = tid & (WAVE - 1);
+  const int w = tid >> 4, q = tid & 15;
+  const int nw = lcnt[w] - LA_LPT * q;  // this thread's entries: those below nw
+  const uint32_t* src = lst_b + (size_t)w * lrow_words + LA_HDR + 2 * LA_LPT * q;
+  u32x4 ev[LA_LPT / 2];
+#pragma unroll
+  for (int i = 0; i < LA_LPT / 2; ++i)
+    ev[i] = i * 2 < nw ? reinterpret_cast<const u32x4*>(src)[i] : u32x4{0u, 0u, 0u, 0u};
+  uint32_t key[LA_LPT], pos[LA_LPT];
+#pragma unroll
+  for (int i = 0; i < LA_LPT; ++i) {
+    key[i] = i < nw ? ev[i / 2][2 * (i & 1)] : 0u;
+    pos[i] = ev[i / 2][2 * (i & 1) + 1];
+  }
+  uint32_t T = 0u;
+  int room = 0;
+  if (c0 >= 0) {
+#pragma unroll
+    for (int i = 0; i < LA_LPT; ++i)
+      if (key[i] && (int)(key[i] >> 20) == c0) atomicAdd(&bins1[(key[i] >> 8) & 4095u], 1);
+    __syncthreads();
+    la_t_search(a, lds, c0, above0, &T, &room);
+    const int c1 = (int)((T >> 8) & 4095u);
+    if (room < bins1[c1]) {
+      const uint32_t hi24 = T >> 8;
+#pragma unroll
+      for (int i = 0; i < LA_LPT; ++i)
+        if (key[i] && (key[i] >> 8) == hi24) atomicAdd(&bins2[key[i] & 255u], 1);
+      __syncthreads();
+      const int hb2[1] = {tid < 256 ? bins2[tid] : 0};
+      int c2, above2;
+      fu_find_bin<1>(hb2, room, scr + 32, &c2, &above2);
+      T |= (uint32_t)c2;
+      room = max(room - above2, 0);
+    }
+  }
+  // per list: its keys above and at T (packed counts, summed over its 16 threads in list order)
+  uint32_t mine = 0;
+#pragma unroll
+  for (int i = 0; i < LA_LPT; ++i) mine += (key[i] > T ? 1u : 0u) + (key[i] == T && key[i] ? 0x10000u : 0u);
+  const uint32_t incl = (uint32_t)row_incl_scan((int)mine);
+  if (q == 15) {
+    lgt[w] = (int)(incl & 0xFFFFu);
+    leq[w] = (int)(incl >> 16);
+  }
+  __syncthreads();
+  const int ww = lane & (FU_NW - 1);
+  const int eqw = lane < FU_NW ? leq[ww] : 0;
+  const int tbw = wave_incl_scan(eqw) - eqw;
+  const int takew = lane < FU_NW ? min(max(room - tbw, 0), eqw) : 0;
+  const int selw = lane < FU_NW ? lgt[ww] + takew : 0;
+  const int offw = wave_incl_scan(selw) - selw;
+  const int off_l = __shfl(offw, w, WAVE), take_l = __shfl(takew, w, WAVE);
+  // the selected entries meeting the split: each entry's output index from its list's first, the list's keys above
+  // T before it and its ties taken before it (as the one-launch layer's one-exchange selection)
+  int gtb = (int)((incl - mine) & 0xFFFFu), eqb = (int)((incl - mine) >> 16);
+  const int first = off_l + gtb + min(eqb, take_l);
+  const int nsel = (int)(mine & 0xFFFFu) + min(max(take_l - eqb, 0), (int)(mine >> 16));
+  if (nsel > 0 && first < o1 && first + nsel > o0) {
+    const int nties = (int)(mine >> 16);
+    if (nties == 0 || eqb >= take_l || eqb + nties <= take_l) {
+      const uint32_t thr = nties > 0 && eqb < take_l ? T : T + 1u;
+      int r = first - o0;
+#pragma unroll
+      for (int i = 0; i < LA_LPT; ++i) {
+        const bool sl = key[i] >= thr;
+        if (sl && (unsigned)r < (unsigned)(o1 - o0)) pos_l[r] = (int)pos[i];
+        r += sl;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < LA_LPT; ++i) {
+        const bool above = key[i] > T, tie = key[i] == T && key[i];
+        const int o = off_l + gtb + min(eqb, take_l) - o0;
+        if ((above || (tie && eqb < take_l)) && (unsigned)o < (unsigned)(o1 - o0)) pos_l[o] = (int)pos[i];
+        gtb += above;
+        eqb += tie;
+      }
+    }
+  }
+  (void)ltake, (void)loff;
+}
+
+__device__ __forceinline__ void la_select_loop(const FusedArgs& a, uint8_t* lds, const uint32_t* lst_b,
+                                               size_t lrow_words, int c0, int above0, int o0, int o1, int* pos_l) {
+  int* scr = reinterpret_cast<int*>(lds + L_MISC);
+  int* bins1 = reinterpret_cast<int*>(lds + L_BINS);
+  int* bins2 = reinterpret_cast<int*>(lds + L_BINS2);
+  int* lcnt = reinterpret_cast<int*>(lds + L_LA);
+  int *lgt = lcnt + FU_NW, *leq = lcnt + 2 * FU_NW, *ltake = lcnt + 3 * FU_NW, *loff = lcnt + 4 * FU_NW;
+  const int tid = threadIdx.x, lane = tid & (WAVE - 1);
+  uint32_t T = 0u;
+  int room = 0;
+  if (c0 >= 0) {
+    for (int w = 0; w < FU_NW; ++w) {
+      const uint2* e = reinterpret_cast<const uint2*>(lst_b + (size_t)w * lrow_words + LA_HDR);
+      for (int i = tid; i < lcnt[w]; i += FU_THREADS) {
+        const uint32_t k = e[i].x;
+        if ((int)(k >> 20) == c0) atomicAdd(&bins1[(k >> 8) & 4095u], 1);
+      }
+    }
+    __syncthreads();
+    la_t_search(a, lds, c0, above0, &T, &room);
+    const int c1 = (int)((T >> 8) & 4095u);
+    if (room < bins1[c1]) {
+      const uint32_t hi24 = T >> 8;
+      for (int w = 0; w < FU_NW; ++w) {
+        const uint2* e = reinterpret_cast<const uint2*>(lst_b + (size_t)w * lrow_words + LA_HDR);
+        for (int i = tid; i < lcnt[w]; i += FU_THREADS) {
+          const uint32_t k = e[i].x;
+          if ((k >> 8) == hi24) atomicAdd(&bins2[k & 255u], 1);
+        }
+      }
+      __syncthreads();
+      const int hb2[1] = {tid < 256 ? bins2[tid] : 0};
+      int c2, above2;
+      fu_find_bin<1>(hb2, room, scr + 32, &c2, &above2);
+      T |= (uint32_t)c2;
+      room = max(room - above2, 0);
+    }
+  }
+  // per list: its keys above T and at T
+  for (int w = 0; w < FU_NW; ++w) {
+    const uint2* e = reinterpret_cast<const uint2*>(lst_b + (size_t)w * lrow_words + LA_HDR);
+    int g = 0, q = 0;
+    for (int i = tid; i < lcnt[w]; i += FU_THREADS) {
+      const uint32_t k = e[i].x;
+      g += k > T;
+      q += k == T;
+    }
+    if (g) atomicAdd(&lgt[w], g);
+    if (q) atomicAdd(&leq[w], q);
+  }
+  __syncthreads();
+  if (tid < WAVE) {  // wave 0: the ties taken (while fewer than room come before) and each list's first output
+    const int eqw = lane < FU_NW ? leq[lane] : 0;
+    const int tbw = wave_incl_scan(eqw) - eqw;
+    const int takew = lane < FU_NW ? min(max(room - tbw, 0), eqw) : 0;
+    const int selw = lane < FU_NW ? lgt[lane] + takew : 0;
+    const int offw = wave_incl_scan(selw) - selw;
+    if (lane < FU_NW) {
+      ltake[lane] = takew;
+      loff[lane] = offw;
+    }
+  }
+  __syncthreads();
+  // the split's positions, from the lists holding its outputs (a block prefix per pass of 512 entries)
+  for (int w = 0; w < FU_NW; ++w) {  // workgroup-uniform
+    const int ow = loff[w], sw = lgt[w] + ltake[w], n = lcnt[w], take = ltake[w];
+    if (sw == 0 || ow >= o1 || ow + sw <= o0) continue;
+    const uint2* e = reinterpret_cast<const uint2*>(lst_b + (size_t)w * lrow_words + LA_HDR);
+    int gtc = 0, eqc = 0;  // the list's keys above and at T in the passes before
+    for (int c = 0; c < n; c += FU_THREADS) {
+      const int i = c + tid;
+      const uint2 en = i < n ? e[i] : make_uint2(0u, 0u);
+      const bool ab = en.x > T, tie = en.x == T && en.x;
+      uint32_t tot;
+      const uint32_t before = fu_block_prefix((ab ? 1u : 0u) | (tie ? 0x10000u : 0u), scr, &tot);
+      const int gb = gtc + (int)(before & 0xFFFFu), eb = eqc + (int)(before >> 16);
+      const int o = ow + gb + min(eb, take);
+      if ((ab || (tie && eb < take)) && o >= o0 && o < o1) pos_l[o - o0] = (int)en.y;
+      gtc += (int)(tot & 0xFFFFu);
+      eqc += (int)(tot >> 16);
+      __syncthreads();  // scr is written again by the next pass's prefix
+    }
+  }
+}
+
+template <int HPW>
+__global__ __launch_bounds__(FU_THREADS, 1) void decode_long_attend_kernel(FusedArgs a, LongAttArgs la) {
+  __shared__ __align__(16) uint8_t lds[FU_LDS];
+  using AT = FuAtt<HPW>;
+  const int x = blockIdx.x % FU_XCDS, j = blockIdx.x / FU_XCDS;
+  int* sync = a.sync + x * WS_SYNC_WORDS;
+  if (a.row0 + x >= a.B) return;  // an XCD without a row
+  const int nr = min(la.rpl, (a.B - a.row0 - x + FU_XCDS - 1) / FU_XCDS);  // this XCD's rows
+  const int tid = threadIdx.x, lane = tid & (WAVE - 1);
+  int* scr = reinterpret_cast<int*>(lds + L_MISC);
+  int* bins1 = reinterpret_cast<int*>(lds + L_BINS);
+  int* bins2 = reinterpret_cast<int*>(lds + L_BINS2);
+  int* lcnt = reinterpret_cast<int*>(lds + L_LA);  // per list: its entries, above T, at T, ties taken, first output
+  int *lgt = lcnt + FU_NW, *leq = lcnt + 2 * FU_NW;
+  int* pos_l = reinterpret_cast<int*>(lds + AT::L_P) + AT::CAP + 8;  // the split's positions (P's region)
+  const int hg = j % a.HG, s = j / a.HG;
+  const bool active = s < a.S;
+  const int o0 = active ? s * a.sps : 0, o1 = active ? min(o0 + a.sps, a.keep) : 0;
+  const size_t lrow_words = LA_HDR + 2 * (size_t)la.bw;
+  for (int r = 0; r < nr; ++r) {
+    const int b = a.row0 + x + FU_XCDS * r;
+    const int L = min(max(a.ctx_len[b], 0), a.stride);
+    if (r) __syncthreads();  // the previous row's attention is done with the LDS
+    // the block's keys at or above c0 (every visible key when c0 = -1) into its list, in position order: the row in
+    // 32 blocks of bwb positions (a multiple of 8, at most the launch's bw), thread t taking positions 8 t .. 8 t + 7
+    // of each pass of 4096
+    uint32_t* lrow = la.lst + ((size_t)b * FU_NW + j) * lrow_words;
+    uint2* lent = reinterpret_cast<uint2*>(lrow + LA_HDR);
+    const float* srow = a.scores + (size_t)b * a.stride;
+    const int bwb = min((L + FU_NW * LA_PASS - 1) / (FU_NW * LA_PASS) * LA_PASS, la.bw);
+    const int pb = j * bwb, pe = min(pb + bwb, L);
+    const int npass = (bwb + FU_THREADS * LA_PASS - 1) / (FU_THREADS * LA_PASS);
+    int listed = 0;
+    int c0 = 0, above0 = 0;  // (stage 1's boundary bin, found below)
+    // pass k's scores straight into LDS (slot k % LA_BATCH: lane l of wave v's 8 floats at 2048 v + 16 l and
+    // 2048 v + 1024 + 16 l, read back by the same lane), LA_BATCH passes a round of loads
+    auto pass_issue = [&](int k) __attribute__((always_inline)) {
+      const int pt = pb + FU_THREADS * LA_PASS * k + LA_PASS * tid;
+      uint8_t* dst = lds + L_LA_STAGE + (FU_THREADS * LA_PASS * 4) * (k % LA_BATCH) + 2048 * (tid / WAVE);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const float* src = srow + (pt + 4 * h < pe ? pt + 4 * h : 0);  // (past the block: a score never used)
+        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(dst + 1024 * h), 16, 0, 0);
+      }
+    };
+    auto pass_list = [&](int k) __attribute__((always_inline)) {
+      const int pt = pb + FU_THREADS * LA_PASS * k + LA_PASS * tid;
+      const uint8_t* src = lds + L_LA_STAGE + (FU_THREADS * LA_PASS * 4) * (k % LA_BATCH) + 2048 * (tid / WAVE) +
+                           16 * lane;
+      const float4 f0 = *reinterpret_cast<const float4*>(src), f1 = *reinterpret_cast<const float4*>(src + 1024);
+      const float v[LA_PASS] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+      uint32_t key[LA_PASS], mine = 0;
+#pragma unroll
+      for (int i = 0; i < LA_PASS; ++i) {
+        const float x2 = pt + i < pe ? v[i] : NEG_INF;
+        key[i] = order_key(x2) & (0u - (uint32_t)(x2 > VISIBLE));
+        if (key[i] && (int)(key[i] >> 20) < c0) key[i] = 0u;  // below the boundary bin: not listed
+        mine += key[i] != 0u;
+      }
+      uint32_t tot;
+      uint32_t at = (uint32_t)listed + fu_block_prefix(mine, scr, &tot);
+#pragma unroll
+      for (int i = 0; i < LA_PASS; ++i)
+        if (key[i]) lent[at++] = make_uint2(key[i], (uint32_t)(pt + i));
+      listed += (int)tot;
+      __syncthreads();  // scr is written again by the next pass's prefix, the slots by the next round's loads
+    };
+    for (int k = 0; k < LA_BATCH && k < npass; ++k) pass_issue(k);  // (before the histogram: the loads overlap)
+    // stage 1: the bin c0 of the row's keep-th largest key (the histogram's bins 8 tid .. 8 tid + 7)
+    int hv[8];
+    {
+      const int4* h4 = reinterpret_cast<const int4*>(la.hist + (size_t)b * FU_HBINS) + 2 * tid;
+      *reinterpret_cast<int4*>(hv) = h4[0];
+      *reinterpret_cast<int4*>(hv + 4) = h4[1];
+    }
+    for (int i = tid; i < 4096; i += FU_THREADS) bins1[i] = 0;
+    if (tid < 256) bins2[tid] = 0;
+    if (tid < FU_NW) lgt[tid] = leq[tid] = 0;
+    if (tid < AT::SPLIT) pos_l[tid] = 0;  // outputs past the count are 0
+    if (tid == 0) scr[8] = scr[24] = scr[40] = -1;
+    __syncthreads();
+    const int nvis = fu_find_bin<8>(hv, a.keep, scr, &c0, &above0);
+    if (nvis <= a.keep) c0 = -1;  // every visible key is selected
+    for (int k0 = 0; k0 < npass; k0 += LA_BATCH) {  // workgroup-uniform (the first round issued above)
+      if (k0) for (int k = k0; k < k0 + LA_BATCH && k < npass; ++k) pass_issue(k);
+      __builtin_amdgcn_s_waitcnt(0);  // (the lane's own loads: no barrier)
+      for (int k = k0; k < k0 + LA_BATCH && k < npass; ++k) pass_list(k);
+    }
+    if (tid == 0) lrow[0] = (uint32_t)listed;
+    fu_barrier(sync, r + 1);  // every block's list of the row (and every workgroup past its histogram read)
+    if (tid < FU_HBINS / FU_NW / 4)  // the row's histogram back to zero, 1/32 by each workgroup
+      reinterpret_cast<uint4*>(la.hist + (size_t)b * FU_HBINS + (FU_HBINS / FU_NW) * j)[tid] =
+          uint4{0u, 0u, 0u, 0u};
+    // stage 2: the lists' counts, then T and the ties to take (the split's queries loading meanwhile)
+    u32x4 qv[AT::QPT];
+    la_queries<HPW>(a, b, j, qv);
+    const uint32_t* lst_b = la.lst + (size_t)b * FU_NW * lrow_words;
+    if (tid < FU_NW) lcnt[tid] = min((int)lst_b[(size_t)tid * lrow_words], la.bw);
+    __syncthreads();
+    const int cnt_row = min(nvis, a.keep);
+    const int lmax = (int)wave_max_u32(lane < FU_NW ? (uint32_t)lcnt[lane] : 0u);
+    if (lmax <= LA_LCAP) {
+      la_select_regs(a, lds, lst_b, lrow_words, c0, above0, o0, o1, pos_l);
+    } else {
+      la_select_loop(a, lds, lst_b, lrow_words, c0, above0, o0, o1, pos_l);
+    }
+    if (j == 0 && tid == 0) a.cnt[b] = cnt_row;
+    __syncthreads();  // the split's positions
+    if (hg == 0 && tid < o1 - o0) a.idx[(size_t)b * a.keep + o0 + tid] = pos_l[tid];
+    float live_bias;
+    const int n_slots = la_prep<HPW>(a, lds, pos_l, b, j, cnt_row, qv, &live_bias);
+    fu_attend<HPW>(a, lds, b, j, n_slots, live_bias);
+  }
+  fu_barrier(sync, nr + 1);  // every split's output of the XCD's rows
+  for (int r = 0; r < nr; ++r) fu_combine(a, lds, a.row0 + x + FU_XCDS * r, j);
+  fu_exit(sync);
+}
+
 // ---- host side ----
 
 static size_t fu_up256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -1940,6 +2343,58 @@ hipError_t launch_decode_attend(const uint16_t* q, const uint8_t* kv, const floa
   a.cnt = const_cast<int*>(cnt);
   return hpw == 32 ? attend_launches(a, decode_attend_kernel<32>, rows, s)
                    : attend_launches(a, decode_attend_kernel<16>, rows, s);
+}
+
+// The long rows' selection, attention and combine in one launch (decode_long_attend_kernel): rows past 32,768
+// tokens (at most LA_MAXLEN), the attention's head shapes, score rows of a multiple of 4 floats.
+static int la_block(long max_len) {
+  const long per = (max_len + FU_NW - 1) / FU_NW, q = (long)LA_PASS * FU_THREADS;
+  return (int)((per + q - 1) / q * q);
+}
+
+bool long_attend_ok(int num_cu, int H, int keep, long max_len, int stride) {
+  return num_cu == FU_XCDS * FU_NW && keep >= 1 && fused_hpw(H, keep) && max_len > FU_MAXLEN &&
+         max_len <= LA_MAXLEN && stride >= max_len && stride % 4 == 0;
+}
+
+// Its workspace past the top-k's: the split outputs and their (max, sum), then the blocks' lists.
+size_t long_attend_bytes(int B, int H, int keep, long max_len) {
+  if (keep < 1 || !fused_hpw(H, keep) || max_len <= FU_MAXLEN || max_len > LA_MAXLEN) return 0;
+  return fu_up256(attend_xcd_bytes(B, H, keep)) +
+         fu_up256((size_t)B * FU_NW * (LA_HDR + 2 * (size_t)la_block(max_len)) * 4);
+}
+
+hipError_t launch_decode_long_attend(const uint16_t* q, const uint8_t* kv, const float* kvs, const int* table,
+                                     const int* ctx_len, const float* scores, int stride, int* hist, int* idx,
+                                     int* cnt, uint16_t* out, float* lse, void* ws, int* sync, int B, int H,
+                                     int max_pages, int page_size, int num_pages, int keep, float scale, long max_len,
+                                     hipStream_t s) {
+  const int hpw = fused_hpw(H, keep);
+  if (!hpw || max_len <= FU_MAXLEN || max_len > LA_MAXLEN || stride % 4) return hipErrorInvalidValue;
+  FusedArgs a = attend_args(q, kv, kvs, table, out, lse, ws, sync, B, H, max_pages, page_size, num_pages, keep, scale,
+                            hpw);
+  a.scores = const_cast<float*>(scores);
+  a.stride = stride;
+  a.ctx_len = ctx_len;
+  a.idx = idx;
+  a.cnt = cnt;
+  LongAttArgs la;
+  la.hist = hist;
+  la.bw = la_block(max_len);
+  la.lst = reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + fu_up256(attend_xcd_bytes(B, H, keep)));
+  const dim3 grid(FU_XCDS * FU_NW), block(FU_THREADS);
+  constexpr int RPL_MAX = 4;
+  for (int r0 = 0; r0 < B; r0 += FU_XCDS * RPL_MAX) {
+    a.row0 = r0;
+    const int left = B - r0;
+    la.rpl = ((left < FU_XCDS * RPL_MAX ? left : FU_XCDS * RPL_MAX) + FU_XCDS - 1) / FU_XCDS;
+    const hipError_t e = hpw == 32 ? launch("decode_long_attend_kernel", decode_long_attend_kernel<32>, grid, block,
+                                            s, a, la)
+                                   : launch("decode_long_attend_kernel", decode_long_attend_kernel<16>, grid, block,
+                                            s, a, la);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 // The pooled form: 512-wide rows, 32 heads per workgroup (splits of 128 token slots, the split holding a row's last
