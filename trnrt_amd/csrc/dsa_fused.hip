@@ -111,6 +111,8 @@ constexpr unsigned FU_SPIN = 1u << 20;  // polls before a wait gives up (a norma
 
 // LDS (160 KiB, one workgroup per CU), phase by phase:
 constexpr int L_STATE = 0;       // FuState: selection results (stage 3)
+constexpr int L_CO0 = 512;       // the one-exchange selection: coarse bins of its first level [64]
+constexpr int L_CO1 = 768;       // and of its second [64]
 constexpr int L_MISC = 1536;     // block-scan scratch (stages 1-3)
 constexpr int L_HLS = 2048;      // stage 2: the first 256 words of every bin list [32][256]
 constexpr int L_BINS2 = 2048;    // stage 3: 256 bins
@@ -122,10 +124,11 @@ constexpr int L_BINS = 40960;    // stage 3: 4096 bins
 constexpr int L_QS = 32768;      // stage 1: indexer queries [64][136] bf16
 constexpr int L_WS = 50176;      // stage 1: head weights [64]
 constexpr int L_HS = 50432;      // stage 1: histogram [4096]
+constexpr int L_HSC = 66816;     // stage 1: its coarse bins [64] (bins 64 c .. 64 c + 63)
 constexpr int L_SCS = 159744;    // stages 1-3: the scores of the workgroup's 1024 positions (NEG_INF past its block)
 constexpr int L_KT = 0;          // stage 4: the rows, token-major at the 592-byte stride
 constexpr int FU_LDS = 163840;
-static_assert(L_HS + 4 * FU_HBINS <= L_SCS, "stage 1 layout");
+static_assert(L_HS + 4 * FU_HBINS <= L_HSC && L_HSC + 4 * 64 <= L_SCS && FU_HBINS == 4096, "stage 1 layout");
 static_assert(L_HLS + 4 * FU_NW * FU_HSTAGE <= L_HS, "stage 2 layout");
 static_assert(L_BINS2 + 4 * 256 <= L_SPG && L_BINS + 4 * 4096 <= 57344, "stage 3 layout");
 static_assert(L_SPG + 4 * 1024 <= L_CB && L_CB + 4 * FU_NW * FU_CSTAGE <= L_SB && L_SB + 4 * FU_NW * FU_BMW <= L_PB &&
@@ -176,7 +179,7 @@ struct FuState {
   int c0, above0, nvis, pad;
   int lbin[FU_NW];  // per workgroup: the lowest bin its key list holds
 };
-static_assert(sizeof(FuState) <= L_MISC, "state");
+static_assert(sizeof(FuState) <= L_CO0 && L_CO1 + 4 * 64 <= L_MISC, "state");
 
 struct FusedArgs {
   const uint16_t* q_idx;
@@ -295,6 +298,62 @@ __device__ int fu_find_bin(const int (&hb)[PER], int need, int* scr, int* bin, i
   const int b = scr[8];
   *bin = b < 0 ? 0 : b;
   *above = b < 0 ? 0 : scr[9];
+  return tot;
+}
+
+// Wave-level (every wave alike, no barrier) over a 4096-bin histogram in LDS, fine[64 c + f], with its coarse bins
+// coarse[c] = fine[64 c] + .. + fine[64 c + 63] (higher bins = larger keys): the bin holding the need-th largest key
+// and the keys in the bins above it; returns the total. Lane l takes coarse bin l, then fine bin 64 k + l of the
+// coarse bin k found (suffix sums over the lanes do not increase with the lane, so the lanes whose sum reaches need
+// are lanes 0 .. k). Counts that cannot hold the need-th key (or need <= 0) give bin 0, above 0.
+__device__ __forceinline__ int fu_wave_find(const int* fine, const int* coarse, int need, int* bin, int* above) {
+  const int lane = threadIdx.x & (WAVE - 1);
+  const int cc = coarse[lane];
+  const int pc = wave_incl_scan(cc);
+  const int tot = __builtin_amdgcn_readlane(pc, WAVE - 1);
+  const int sc = tot - pc + cc;  // coarse bins lane .. 63
+  if (need <= 0 || tot < need) {  // wave-uniform
+    *bin = 0;
+    *above = 0;
+    return tot;
+  }
+  const int k = __popcll(__ballot(sc >= need)) - 1;
+  const int abv = __builtin_amdgcn_readlane(sc - cc, k);  // keys above coarse bin k
+  const int cf = fine[64 * k + lane];
+  const int pf = wave_incl_scan(cf);
+  const int sf = abv + __builtin_amdgcn_readlane(pf, WAVE - 1) - pf + cf;
+  const int f = __popcll(__ballot(sf >= need)) - 1;
+  *bin = 64 * k + f;
+  *above = __builtin_amdgcn_readlane(sf - cf, f);
+  return tot;
+}
+
+// The same over 256 bins (lane l: bins 4 l .. 4 l + 3).
+__device__ __forceinline__ int fu_wave_find256(const int* bins, int need, int* bin, int* above) {
+  const int lane = threadIdx.x & (WAVE - 1);
+  int v[4];
+  *reinterpret_cast<int4*>(v) = *reinterpret_cast<const int4*>(bins + 4 * lane);
+  const int m = v[0] + v[1] + v[2] + v[3];
+  const int p = wave_incl_scan(m);
+  const int tot = __builtin_amdgcn_readlane(p, WAVE - 1);
+  const int sc = tot - p + m;
+  if (need <= 0 || tot < need) {
+    *bin = 0;
+    *above = 0;
+    return tot;
+  }
+  const int k = __popcll(__ballot(sc >= need)) - 1;
+  int e = sc - m, bl = 4 * lane, al = 0;
+#pragma unroll
+  for (int i = 3; i >= 0; --i) {
+    if (e < need && e + v[i] >= need) {
+      bl = 4 * lane + i;
+      al = e;
+    }
+    e += v[i];
+  }
+  *bin = __builtin_amdgcn_readlane(bl, k);
+  *above = __builtin_amdgcn_readlane(al, k);
   return tot;
 }
 
@@ -451,6 +510,7 @@ __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int
   uint16_t* qs = reinterpret_cast<uint16_t*>(lds + L_QS);
   float* wsh = reinterpret_cast<float*>(lds + L_WS);
   int* hs = reinterpret_cast<int*>(lds + L_HS);
+  int* hsc = reinterpret_cast<int*>(lds + L_HSC);
   float* scs = reinterpret_cast<float*>(lds + L_SCS);
   const int tid = threadIdx.x, wave = tid / WAVE, lane = tid & (WAVE - 1);
   const int jk = lane & 31, h = lane >> 5;
@@ -544,8 +604,8 @@ __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int
   }
   if (tid < 32 * MT) wsh[tid] = tid < Hi ? wv : 0.0f;
   for (int i = tid; i < FU_HBINS; i += FU_THREADS) hs[i] = 0;
+  if (tid < 64) hsc[tid] = 0;
   int* scr = reinterpret_cast<int*>(lds + L_MISC);
-  if (tid == 0) scr[8] = -1;  // the key list's bin search below
   __syncthreads();
   if (WRITE && kwave) {
     const uint32_t key2 = fu_pool_key_write_t<FU_STEP_KP>(a, pkr);
@@ -612,7 +672,10 @@ __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int
         if (!lists && mine && pos < a.stride) srow[pos] = v;
         scs[e] = v;
         if (POOL && mine) plst[e] = order_key(v) & (0u - (uint32_t)(v > VISIBLE));
-        if (v > VISIBLE) atomicAdd(&hs[order_key(v) >> 20], 1);
+        if (v > VISIBLE) {
+          atomicAdd(&hs[order_key(v) >> 20], 1);
+          if (!POOL && lists) atomicAdd(&hsc[order_key(v) >> 26], 1);  // the key list's bin search
+        }
       }
     }
   } else {
@@ -662,7 +725,7 @@ __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int
     lbin = 0;  // every key of the block (at most 256), whatever their bins; counted by the prefix below
   } else if (lists) {
     int lb, labove;
-    const int nv = fu_find_bin<8>(hv, FU_LM, scr, &lb, &labove);
+    const int nv = fu_wave_find(hs, hsc, FU_LM, &lb, &labove);
     lbin = 0;
     lcnt = nv;
     if (nv > FU_LCAP) {
@@ -1050,10 +1113,11 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
   using FF = FuForm<POOL>;
   constexpr int QPT = AT::QPT, LPT = FF::LPT;
   FuState& st = *reinterpret_cast<FuState*>(lds + L_STATE);
-  int* scr = reinterpret_cast<int*>(lds + L_MISC);
   int* bins0 = reinterpret_cast<int*>(lds + L_CB);
   int* bins1 = reinterpret_cast<int*>(lds + L_BINS);
   int* bins2 = reinterpret_cast<int*>(lds + L_BINS2);
+  int* co0 = reinterpret_cast<int*>(lds + L_CO0);
+  int* co1 = reinterpret_cast<int*>(lds + L_CO1);
   int* spg = reinterpret_cast<int*>(lds + L_SPG);
   int* slot_l = reinterpret_cast<int*>(lds + AT::L_P);
   // the split's output positions, stored to idx in one coalesced pass at the end; the entry past SPLIT is the sink
@@ -1119,9 +1183,9 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
   __builtin_amdgcn_sched_barrier(0);
   for (int i = tid; i < 4096; i += FU_THREADS) bins0[i] = bins1[i] = 0;
   if (tid < 256) bins2[tid] = 0;
+  if (tid < 64) co0[tid] = co1[tid] = 0;
   if (tid < AT::CAP) slot_l[tid] = 0;  // padding rows read slot 0
   if (tid < AT::SPLIT) pos_l[tid] = 0;  // outputs past the count are 0
-  if (tid == 0) scr[8] = scr[24] = scr[40] = scr[56] = -1;
   __builtin_amdgcn_sched_barrier(0);
   __syncthreads();  // the bins cleared (the loads above may be out; their first uses wait for them)
   uint32_t key[LPT], pos[LPT];
@@ -1146,8 +1210,12 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
 #pragma unroll
     for (int i = 0; i < LPT; ++i) asm volatile("" : "+v"(key[i]));
   };
-  constexpr int P1 = 4096 / FU_THREADS;
-  int hb[P1];
+  // a histogram level's counts go to its 4096 bins and their 64 coarse bins (the wave-level bin searches below read
+  // both after one barrier)
+  auto add0 = [&](uint32_t bin, int n) __attribute__((always_inline)) {
+    atomicAdd(&bins0[bin], n);
+    atomicAdd(&co0[bin >> 6], n);
+  };
   int c0, above0, nlist, cnt_row;
   if constexpr (POOL) {
     // the first level from the lists' headers: exact for the bins at or above every list's lowest complete bin lmax
@@ -1155,23 +1223,20 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
     // that, the keys below their list's header bins are counted one by one and the search repeated
 #pragma unroll
     for (int k = 0; k < 4; ++k)
-      if (bh[k]) atomicAdd(&bins0[(bh[k] >> 16) & 4095u], (int)(bh[k] & 0xFFFFu));
+      if (bh[k]) add0((bh[k] >> 16) & 4095u, (int)(bh[k] & 0xFFFFu));
     if (q == 15) st.lbin[w] = bh[3] ? (int)(bh[3] >> 16) : 0;
     __syncthreads();
-    *reinterpret_cast<int4*>(hb) = *reinterpret_cast<const int4*>(bins0 + P1 * tid);
-    *reinterpret_cast<int4*>(hb + 4) = *reinterpret_cast<const int4*>(bins0 + P1 * tid + 4);
-    nlist = fu_find_bin<P1>(hb, a.keep, scr, &c0, &above0);
+    nlist = fu_wave_find(bins0, co0, a.keep, &c0, &above0);
     const int lmax = (int)wave_max_u32(lane < FU_NW ? (uint32_t)st.lbin[lane] : 0u);
     if (lmax > 0 && (nlist <= a.keep || c0 < lmax)) {  // workgroup-uniform
       const int low = st.lbin[w];
+      __syncthreads();  // every wave's search above has read the bins
 #pragma unroll
       for (int i = 0; i < LPT; ++i)
-        if (key[i] && (int)(key[i] >> 20) < low) atomicAdd(&bins0[key[i] >> 20], 1);
+        if (key[i] && (int)(key[i] >> 20) < low) add0(key[i] >> 20, 1);
       fresh();
       __syncthreads();
-      *reinterpret_cast<int4*>(hb) = *reinterpret_cast<const int4*>(bins0 + P1 * tid);
-      *reinterpret_cast<int4*>(hb + 4) = *reinterpret_cast<const int4*>(bins0 + P1 * tid + 4);
-      nlist = fu_find_bin<P1>(hb, a.keep, scr + 48, &c0, &above0);
+      nlist = fu_wave_find(bins0, co0, a.keep, &c0, &above0);
     }
     // every list holds all its workgroup's keys
     cnt_row = min(nlist, a.keep);
@@ -1184,18 +1249,16 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
     if ((__ballot(hfull) >> (16 * (w & 3))) & 0xFFFFull) {
 #pragma unroll
       for (int i = 0; i < LPT; ++i)
-        if (key[i]) atomicAdd(&bins0[key[i] >> 20], 1);
+        if (key[i]) add0(key[i] >> 20, 1);
     } else if (q < FU_LBINS / 2) {
 #pragma unroll
       for (int k = 0; k < 2; ++k)
-        if (hp[k] != 0u && (hp[k] >> 16) >= hw1) atomicAdd(&bins0[(hp[k] >> 16) & 4095u], (int)(hp[k] & 0xFFFFu));
+        if (hp[k] != 0u && (hp[k] >> 16) >= hw1) add0((hp[k] >> 16) & 4095u, (int)(hp[k] & 0xFFFFu));
     }
     fresh();
     if (q == 0) st.lbin[w] = (int)hw1;
     __syncthreads();
-    *reinterpret_cast<int4*>(hb) = *reinterpret_cast<const int4*>(bins0 + P1 * tid);
-    *reinterpret_cast<int4*>(hb + 4) = *reinterpret_cast<const int4*>(bins0 + P1 * tid + 4);
-    nlist = fu_find_bin<P1>(hb, a.keep, scr, &c0, &above0);
+    nlist = fu_wave_find(bins0, co0, a.keep, &c0, &above0);
     const uint32_t lmax = wave_max_u32(lane < FU_NW ? (uint32_t)st.lbin[lane] : 0u);
     if (lmax == 0u) {
       // every list holds all its workgroup's keys
@@ -1212,14 +1275,15 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
   if (c0 >= 0) {
 #pragma unroll
     for (int i = 0; i < LPT; ++i)
-      if (key[i] && (int)(key[i] >> 20) == c0) atomicAdd(&bins1[(key[i] >> 8) & 4095u], 1);
+      if (key[i] && (int)(key[i] >> 20) == c0) {
+        atomicAdd(&bins1[(key[i] >> 8) & 4095u], 1);
+        atomicAdd(&co1[(key[i] >> 14) & 63u], 1);
+      }
     fresh();
     __syncthreads();
-    *reinterpret_cast<int4*>(hb) = *reinterpret_cast<const int4*>(bins1 + P1 * tid);
-    *reinterpret_cast<int4*>(hb + 4) = *reinterpret_cast<const int4*>(bins1 + P1 * tid + 4);
     int c1, above1;
     int need = a.keep - above0;
-    fu_find_bin<P1>(hb, need, scr + 16, &c1, &above1);
+    fu_wave_find(bins1, co1, need, &c1, &above1);
     need -= above1;
     uint32_t tlow;
     if (need >= bins1[c1]) {
@@ -1233,9 +1297,8 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
         if (key[i] && (key[i] >> 8) == hi24) atomicAdd(&bins2[key[i] & 255u], 1);
       fresh();
       __syncthreads();
-      const int hb2[1] = {tid < 256 ? bins2[tid] : 0};
       int c2, above2;
-      fu_find_bin<1>(hb2, need, scr + 32, &c2, &above2);
+      fu_wave_find256(bins2, need, &c2, &above2);
       tlow = ((uint32_t)c1 << 8) | (uint32_t)c2;
       room = max(need - above2, 0);
     }
