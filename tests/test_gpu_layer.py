@@ -145,6 +145,31 @@ def test_layer_long_rows_mixed_forms(tied):
     assert torch.equal(L.idx.cpu().long(), ri) and torch.equal(L.cnt.cpu().long(), rc)
 
 
+def test_layer_long_tied_row_every_tile_read():
+    """A row of 300,000 tokens whose scores take two values: every 32-key tile's maximum is the row's largest score,
+    so the one-launch long-row selection reads every tile of every block (296 a block: more than one round of 256
+    tile loads) and lists every key; beside it a row of 50,000 with distinct scores. The selection bit-exact on the
+    kernel's scores (ties to the lowest positions), the attention against the oracle."""
+    lengths = [300000, 50000]
+    say("layer long tied row, every tile read")
+    cfg = W.Config("layer-long-tied", B=len(lengths), L=300000, H=64, Hi=64)
+    inp = W.make_inputs(cfg, seed=41, lengths=lengths)
+    ps = cfg.page_size
+    n = lengths[0]
+    p = torch.arange(n)
+    sl = inp.table[0, p // ps].long() * ps + p % ps
+    inp.k_cache[sl] = inp.k_cache[64 + (p % 2)]
+    inp.k_scale[sl] = inp.k_scale[64 + (p % 2)]
+    g = inp.to("cuda")
+    L = _layer(g)
+    sc = L.scores.cpu()
+    assert len(torch.unique(sc[0, :n])) <= 2
+    ri, rc = O.topk_ref(sc, cfg.keep, inp.ctx_len)
+    assert torch.equal(L.cnt.cpu().long(), rc)
+    assert torch.equal(L.idx.cpu().long(), ri)
+    _attention_check(inp, L)
+
+
 def _sampled_indexer_check(g, sc, nsample=4096, seed=0):
     cfg = g.cfg
     gen = torch.Generator().manual_seed(seed)

@@ -67,6 +67,9 @@ hipError_t launch_decode_attend(const uint16_t* q, const uint8_t* kv, const floa
                                 float scale, hipStream_t s);
 bool long_attend_ok(int num_cu, int H, int keep, long max_len, int stride);
 size_t long_attend_bytes(int B, int H, int keep, long max_len);
+float* long_attend_tmax(void* ws, int B, int H, int keep, long max_len);
+int long_attend_ntile(long max_len);
+bool long_attend_tiles(long max_len);
 hipError_t launch_decode_long_attend(const uint16_t* q, const uint8_t* kv, const float* kvs, const int* table,
                                      const int* ctx_len, const float* scores, int stride, int* hist, int* idx,
                                      int* cnt, uint16_t* out, float* lse, void* ws, int* sync, int B, int H,
@@ -875,6 +878,11 @@ static int layer_chain(const void* q_idx_bf16, const float* w, const uint8_t* k_
   const int sub = fused_hist ? 0 : dsa::topk_two_level_sub(max_len, keep);
   const bool fused_bm = sub >= 2 && sub <= 32;
   int* hist = fused_hist ? dsa::ws_hist(workspace) : nullptr;
+  // long rows through the one-launch selection and attention: for rows past 524,288 tokens the indexer also writes
+  // the maxima of the rows' 32-key tiles into that launch's workspace
+  const bool la = long_sel && splits == 0 && dsa::long_attend_ok(num_cu(), H, keep, max_len, score_stride);
+  char* lws = static_cast<char*>(workspace) + t_need + layer_rows_bytes(B, keep);
+  float* tmax = la && dsa::long_attend_tiles(max_len) ? dsa::long_attend_tmax(lws, B, H, keep, max_len) : nullptr;
   hipError_t e;
   if (flat)
     e = dsa::launch_indexer_decode(static_cast<const uint16_t*>(q_idx_bf16), w, k_fp8, k_scale, page_table, ctx_len,
@@ -882,17 +890,18 @@ static int layer_chain(const void* q_idx_bf16, const float* w, const uint8_t* k_
                                    num_cu(), s);
   else
     e = dsa::launch_indexer_decode_long(static_cast<const uint16_t*>(q_idx_bf16), w, k_fp8, k_scale, page_table,
-                                        ctx_len, scores, fused_bm ? dsa::topk_bm_buffer(workspace, B) : nullptr,
-                                        fused_bm ? __builtin_ctz((unsigned)sub) : 0,
-                                        fused_bm ? (max_len + sub - 1) / sub : 0, hist, B, Hi, max_pages, page_size,
-                                        num_pages, score_stride, num_cu(), s);
+                                        ctx_len, scores,
+                                        tmax ? tmax : fused_bm ? dsa::topk_bm_buffer(workspace, B) : nullptr,
+                                        tmax ? 5 : fused_bm ? __builtin_ctz((unsigned)sub) : 0,
+                                        tmax ? dsa::long_attend_ntile(max_len) : fused_bm ? (max_len + sub - 1) / sub : 0,
+                                        hist, B, Hi, max_pages, page_size, num_pages, score_stride, num_cu(), s);
   if (e != hipSuccess) {
     if (hist) dsa::launch_fill_zero(hist, dsa::topk_hist_bytes(B), s);  // a partial histogram may be in
     return DSA_ELAUNCH;
   }
-  if (long_sel && splits == 0 && dsa::long_attend_ok(num_cu(), H, keep, max_len, score_stride)) {
-    // the long rows' selection, attention and combine in one launch over the indexer's scores and histograms
-    char* lws = static_cast<char*>(workspace) + t_need + layer_rows_bytes(B, keep);
+  if (la) {
+    // the long rows' selection, attention and combine in one launch over the indexer's scores, histograms and tile
+    // maxima
     e = dsa::launch_decode_long_attend(static_cast<const uint16_t*>(q_bf16), kv_fp8, kv_scale, page_table, ctx_len,
                                        scores, score_stride, hist, idx, cnt, static_cast<uint16_t*>(out_bf16), lse,
                                        lws, static_cast<int*>(workspace), B, H, max_pages, page_size, num_pages, keep,

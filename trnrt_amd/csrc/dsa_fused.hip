@@ -1500,6 +1500,9 @@ __device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int 
       }
     }
     pc = pc0;  // (the pieces again, stepped as above)
+    // (opaque here: in a kernel that attends several rows in turn, the loads' per-lane offsets would otherwise be
+    // computed once before the rows and held in registers throughout, which spills)
+    asm volatile("" : "+v"(pc));
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const int k = wave + FU_WAVES * i;
@@ -1896,7 +1899,10 @@ __global__ __launch_bounds__(FU_THREADS, 1) void decode_attend_kernel(FusedArgs 
 // workgroup per row, ordered output) and the separate attention launch:
 //   1. every workgroup finds the bin c0 of the row's keep-th largest key in the row's histogram (c0 = -1, every
 //      visible key, when the row has at most keep), then lists its block of the row (positions [j bw, (j + 1) bw))
-//      as the (key, position) of its keys at or above c0, in position order; barrier (then the histogram is cleared);
+//      as the (key, position) of its keys at or above c0, in position order: a block of at most 16,384 positions
+//      from its scores (one round of loads), a longer one from the indexer's maxima of its 32-key tiles (the tiles
+//      whose maximum is at or above c0, which alone can hold such keys, and then their scores alone); barrier (then
+//      the histogram is cleared);
 //   2. every workgroup reads the 32 lists: T (the keep-th largest key) from the next 12 and 8 bits of the keys in c0,
 //      each list's keys above and at T, the ties taken (the lowest positions: list order, then position order) and
 //      each list's first output index;
@@ -1906,22 +1912,33 @@ __global__ __launch_bounds__(FU_THREADS, 1) void decode_attend_kernel(FusedArgs 
 // The selection is exact (the reference's arithmetic of trnrt/kernels/dsa_topk.py, ties to the lowest positions),
 // as the long top-k's: same T, same outputs in the same order.
 struct LongAttArgs {
-  int* hist;        // [B][4096]: the rows' first-level histograms, zero again after the launch
-  uint32_t* lst;    // [B][32][LA_HDR + 2 bw]: per workgroup its block's list
-  int bw;           // positions per block, a multiple of LA_PASS x 512
-  int rpl;          // rows per XCD
+  int* hist;          // [B][4096]: the rows' first-level histograms, zero again after the launch
+  const float* tmax;  // [B][ntile]: the maxima of the rows' 32-key tiles (tile t: positions 32 t .. 32 t + 31), or
+                      // null: stage 1 over the scores
+  uint32_t* lst;      // [B][32][LA_HDR + 2 bw]: per workgroup its block's list
+  int bw;             // positions per block, a multiple of 4,096 (at most LA_SCAN_MAX without tmax)
+  int ntile;          // tiles per row of tmax, a multiple of 4
+  int rpl;            // rows per XCD
 };
 constexpr int LA_HDR = 32;   // list header words (the count)
-constexpr int LA_PASS = 8;   // positions per thread and pass of stage 1 (two 16-byte score loads)
 constexpr int LA_MAXLEN = FU_NW * 65536;  // 2,097,152 tokens a row
 constexpr int L_LA = 0;      // stage 2's per-list words [6][32] (L_STATE's place)
-constexpr int LA_BATCH = 4;  // stage 1's passes a round of loads
-constexpr int L_LA_STAGE = 81920;  // stage 1's scores [LA_BATCH][4096] (past the split's positions, dead by stage 3)
+// stage 1 over the scores (blocks of at most LA_SCAN_MAX positions: at most one round of loads)
+constexpr int LA_PASS = 8;   // positions per thread and pass (two 16-byte score loads)
+constexpr int LA_BATCH = 4;  // passes a round of loads
+constexpr int LA_SCAN_MAX = LA_BATCH * FU_THREADS * LA_PASS;
+constexpr int L_LA_STAGE = 81920;  // the scores [LA_BATCH][4096] (past the split's positions, dead by stage 3)
 static_assert(L_LA_STAGE + LA_BATCH * FU_THREADS * LA_PASS * 4 <= FU_LDS, "stage 1's scores in LDS");
 static_assert(L_LA_STAGE >= FuAtt<32>::L_P + 4 * (FuAtt<32>::CAP + 8 + FuAtt<32>::SPLIT + 1) &&
                   L_LA_STAGE + LA_BATCH * FU_THREADS * LA_PASS * 4 <= FuAtt<16>::L_P,
               "stage 1's scores clear of the split's slot and position lists");
 static_assert(L_BINS + 4 * 4096 <= L_LA_STAGE, "stage 1's scores clear of the bins");
+// stage 1 over the tile maxima (longer blocks)
+constexpr int LA_TPT = 4;    // tiles per thread (a block of at most 2,048 tiles)
+constexpr int LA_GR = 4;     // rounds of 64 tiles whose scores are loaded at once
+constexpr int L_LA_HOT = L_LA_STAGE;  // the tiles to read [2048]
+static_assert(FU_THREADS * LA_TPT * 32 == 65536 && 4 * FU_THREADS * LA_TPT <= LA_SCAN_MAX * 4,
+              "a block of at most 2,048 tiles, their list inside the scores' place");
 
 // The split's queries (loaded before the selection, so that their load overlaps it).
 template <int HPW>
@@ -2194,52 +2211,41 @@ __global__ __launch_bounds__(FU_THREADS, 1) void decode_long_attend_kernel(Fused
     const int b = a.row0 + x + FU_XCDS * r;
     const int L = min(max(a.ctx_len[b], 0), a.stride);
     if (r) __syncthreads();  // the previous row's attention is done with the LDS
-    // the block's keys at or above c0 (every visible key when c0 = -1) into its list, in position order: the row in
-    // 32 blocks of bwb positions (a multiple of 8, at most the launch's bw), thread t taking positions 8 t .. 8 t + 7
-    // of each pass of 4096
+    // stage 1: the block's keys at or above c0 (every visible key when c0 = -1) into its list, in position order
     uint32_t* lrow = la.lst + ((size_t)b * FU_NW + j) * lrow_words;
     uint2* lent = reinterpret_cast<uint2*>(lrow + LA_HDR);
     const float* srow = a.scores + (size_t)b * a.stride;
-    const int bwb = min((L + FU_NW * LA_PASS - 1) / (FU_NW * LA_PASS) * LA_PASS, la.bw);
-    const int pb = j * bwb, pe = min(pb + bwb, L);
-    const int npass = (bwb + FU_THREADS * LA_PASS - 1) / (FU_THREADS * LA_PASS);
     int listed = 0;
-    int c0 = 0, above0 = 0;  // (stage 1's boundary bin, found below)
-    // pass k's scores straight into LDS (slot k % LA_BATCH: lane l of wave v's 8 floats at 2048 v + 16 l and
-    // 2048 v + 1024 + 16 l, read back by the same lane), LA_BATCH passes a round of loads
-    auto pass_issue = [&](int k) __attribute__((always_inline)) {
-      const int pt = pb + FU_THREADS * LA_PASS * k + LA_PASS * tid;
-      uint8_t* dst = lds + L_LA_STAGE + (FU_THREADS * LA_PASS * 4) * (k % LA_BATCH) + 2048 * (tid / WAVE);
+    int c0 = 0, above0 = 0;
+    // the row in 32 blocks of bwb positions (at most the launch's bw), positions [pb, pe) of this workgroup's; with the
+    // tile maxima a multiple of 128, thread t holding those of tiles tb + 4 t .. tb + 4 t + 3 (tiles [tb, te) of 32);
+    // over the scores a multiple of 8, thread t taking positions 8 t .. 8 t + 7 of each pass of 4,096
+    const bool tiles = la.tmax != nullptr;  // (launch-uniform)
+    const int bq = tiles ? 128 : LA_PASS;
+    const int bwb = min((L + FU_NW * bq - 1) / (FU_NW * bq) * bq, la.bw);
+    const int pb = j * bwb, pe = min(pb + bwb, L);
+    const int tb = pb / 32, te = tiles ? min((pe + 31) / 32, la.ntile) : 0;  // (a row longer than max_len: not past)
+    const int npass = tiles ? 0 : (bwb + FU_THREADS * LA_PASS - 1) / (FU_THREADS * LA_PASS);
+    float tm[LA_TPT];
+    if (tiles) {
+      const int t0 = tb + LA_TPT * tid;
+      const float4 m4 = t0 < te ? *reinterpret_cast<const float4*>(la.tmax + (size_t)b * la.ntile + t0)
+                                : make_float4(NEG_INF, NEG_INF, NEG_INF, NEG_INF);
+      tm[0] = m4.x, tm[1] = m4.y, tm[2] = m4.z, tm[3] = m4.w;
+    } else {
+      // the block's scores straight into LDS (pass k in slot k: lane l of wave v's 8 floats at 2048 v + 16 l and
+      // 2048 v + 1024 + 16 l, read back by the same lane), one round of loads
+      for (int k = 0; k < npass; ++k) {
+        const int pt = pb + FU_THREADS * LA_PASS * k + LA_PASS * tid;
+        uint8_t* dst = lds + L_LA_STAGE + (FU_THREADS * LA_PASS * 4) * k + 2048 * (tid / WAVE);
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const float* src = srow + (pt + 4 * h < pe ? pt + 4 * h : 0);  // (past the block: a score never used)
-        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(dst + 1024 * h), 16, 0, 0);
+        for (int h = 0; h < 2; ++h) {
+          const float* src = srow + (pt + 4 * h < pe ? pt + 4 * h : 0);  // (past the block: a score never used)
+          __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(dst + 1024 * h), 16, 0, 0);
+        }
       }
-    };
-    auto pass_list = [&](int k) __attribute__((always_inline)) {
-      const int pt = pb + FU_THREADS * LA_PASS * k + LA_PASS * tid;
-      const uint8_t* src = lds + L_LA_STAGE + (FU_THREADS * LA_PASS * 4) * (k % LA_BATCH) + 2048 * (tid / WAVE) +
-                           16 * lane;
-      const float4 f0 = *reinterpret_cast<const float4*>(src), f1 = *reinterpret_cast<const float4*>(src + 1024);
-      const float v[LA_PASS] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
-      uint32_t key[LA_PASS], mine = 0;
-#pragma unroll
-      for (int i = 0; i < LA_PASS; ++i) {
-        const float x2 = pt + i < pe ? v[i] : NEG_INF;
-        key[i] = order_key(x2) & (0u - (uint32_t)(x2 > VISIBLE));
-        if (key[i] && (int)(key[i] >> 20) < c0) key[i] = 0u;  // below the boundary bin: not listed
-        mine += key[i] != 0u;
-      }
-      uint32_t tot;
-      uint32_t at = (uint32_t)listed + fu_block_prefix(mine, scr, &tot);
-#pragma unroll
-      for (int i = 0; i < LA_PASS; ++i)
-        if (key[i]) lent[at++] = make_uint2(key[i], (uint32_t)(pt + i));
-      listed += (int)tot;
-      __syncthreads();  // scr is written again by the next pass's prefix, the slots by the next round's loads
-    };
-    for (int k = 0; k < LA_BATCH && k < npass; ++k) pass_issue(k);  // (before the histogram: the loads overlap)
-    // stage 1: the bin c0 of the row's keep-th largest key (the histogram's bins 8 tid .. 8 tid + 7)
+    }
+    // the bin c0 of the row's keep-th largest key (the histogram's bins 8 tid .. 8 tid + 7)
     int hv[8];
     {
       const int4* h4 = reinterpret_cast<const int4*>(la.hist + (size_t)b * FU_HBINS) + 2 * tid;
@@ -2254,10 +2260,78 @@ __global__ __launch_bounds__(FU_THREADS, 1) void decode_long_attend_kernel(Fused
     __syncthreads();
     const int nvis = fu_find_bin<8>(hv, a.keep, scr, &c0, &above0);
     if (nvis <= a.keep) c0 = -1;  // every visible key is selected
-    for (int k0 = 0; k0 < npass; k0 += LA_BATCH) {  // workgroup-uniform (the first round issued above)
-      if (k0) for (int k = k0; k < k0 + LA_BATCH && k < npass; ++k) pass_issue(k);
+    // the keys of N consecutive positions from p0 (v: their scores; live: whether they are the block's) that are at
+    // or above c0 (0: not listed), and their count
+    auto keys_of = [&](const float* v, int N, int p0, bool live, uint32_t* key) __attribute__((always_inline)) {
+      uint32_t n = 0;
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        const float x2 = live && p0 + i < pe ? v[i] : NEG_INF;
+        key[i] = order_key(x2) & (0u - (uint32_t)(x2 > VISIBLE));
+        if (key[i] && (int)(key[i] >> 20) < c0) key[i] = 0u;  // below the boundary bin: not listed
+        n += key[i] != 0u;
+      }
+      return n;
+    };
+    if (tiles) {
+      // the block's tiles that can hold a key at or above c0, in tile order
+      int* hot = reinterpret_cast<int*>(lds + L_LA_HOT);
+      uint32_t nh = 0;
+      bool ht[LA_TPT];
+#pragma unroll
+      for (int i = 0; i < LA_TPT; ++i) {
+        const uint32_t mk = order_key(tm[i]);
+        ht[i] = tb + LA_TPT * tid + i < te && tm[i] > VISIBLE && (int)(mk >> 20) >= c0;
+        nh += ht[i];
+      }
+      uint32_t nhot;
+      uint32_t at = fu_block_prefix(nh, scr, &nhot);
+#pragma unroll
+      for (int i = 0; i < LA_TPT; ++i)
+        if (ht[i]) hot[at++] = tb + LA_TPT * tid + i;
+      __syncthreads();  // the tile list (and scr, written again below)
+      // their scores, LA_GR rounds of 64 tiles a round of loads (thread t: 4 scores of tile t / 8 of the round)
+      for (int g0 = 0; g0 < (int)nhot; g0 += 64 * LA_GR) {  // workgroup-uniform
+        float4 sv[LA_GR];
+#pragma unroll
+        for (int r = 0; r < LA_GR; ++r) {
+          const int hi = g0 + 64 * r + (tid >> 3);
+          const int p0 = 32 * (hi < (int)nhot ? hot[hi] : tb) + 4 * (tid & 7);
+          sv[r] = p0 < a.stride ? *reinterpret_cast<const float4*>(srow + p0)
+                                : make_float4(NEG_INF, NEG_INF, NEG_INF, NEG_INF);
+        }
+#pragma unroll
+        for (int r = 0; r < LA_GR; ++r) {
+          if (g0 + 64 * r >= (int)nhot) break;  // workgroup-uniform
+          const int hi = g0 + 64 * r + (tid >> 3);
+          const int p0 = 32 * (hi < (int)nhot ? hot[hi] : tb) + 4 * (tid & 7);
+          const float v[4] = {sv[r].x, sv[r].y, sv[r].z, sv[r].w};
+          uint32_t key[4], tot;
+          const uint32_t mine = keys_of(v, 4, p0, hi < (int)nhot, key);
+          uint32_t e = (uint32_t)listed + fu_block_prefix(mine, scr, &tot);
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (key[i]) lent[e++] = make_uint2(key[i], (uint32_t)(p0 + i));
+          listed += (int)tot;
+          __syncthreads();  // scr is written again by the next round's prefix
+        }
+      }
+    } else {
       __builtin_amdgcn_s_waitcnt(0);  // (the lane's own loads: no barrier)
-      for (int k = k0; k < k0 + LA_BATCH && k < npass; ++k) pass_list(k);
+      for (int k = 0; k < npass; ++k) {
+        const int pt = pb + FU_THREADS * LA_PASS * k + LA_PASS * tid;
+        const uint8_t* src = lds + L_LA_STAGE + (FU_THREADS * LA_PASS * 4) * k + 2048 * (tid / WAVE) + 16 * lane;
+        const float4 f0 = *reinterpret_cast<const float4*>(src), f1 = *reinterpret_cast<const float4*>(src + 1024);
+        const float v[LA_PASS] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+        uint32_t key[LA_PASS], tot;
+        const uint32_t mine = keys_of(v, LA_PASS, pt, true, key);
+        uint32_t e = (uint32_t)listed + fu_block_prefix(mine, scr, &tot);
+#pragma unroll
+        for (int i = 0; i < LA_PASS; ++i)
+          if (key[i]) lent[e++] = make_uint2(key[i], (uint32_t)(pt + i));
+        listed += (int)tot;
+        __syncthreads();  // scr is written again by the next pass's prefix
+      }
     }
     if (tid == 0) lrow[0] = (uint32_t)listed;
     fu_barrier(sync, r + 1);  // every block's list of the row (and every workgroup past its histogram read)
@@ -2411,21 +2485,36 @@ hipError_t launch_decode_attend(const uint16_t* q, const uint8_t* kv, const floa
 // The long rows' selection, attention and combine in one launch (decode_long_attend_kernel): rows past 32,768
 // tokens (at most LA_MAXLEN), the attention's head shapes, score rows of a multiple of 4 floats.
 static int la_block(long max_len) {
-  const long per = (max_len + FU_NW - 1) / FU_NW, q = (long)LA_PASS * FU_THREADS;
+  const long per = (max_len + FU_NW - 1) / FU_NW, q = 4096;  // (a multiple of 4 tiles a thread)
   return (int)((per + q - 1) / q * q);
 }
+
+// The tiles per row of the tile maxima (a multiple of 4: each thread reads 4 with one 16-byte load).
+static int la_ntile(long max_len) { return (int)((max_len + 127) / 128 * 4); }
+
+// Whether stage 1 reads the tile maxima (blocks longer than one round of score loads).
+bool long_attend_tiles(long max_len) { return la_block(max_len) > LA_SCAN_MAX; }
 
 bool long_attend_ok(int num_cu, int H, int keep, long max_len, int stride) {
   return num_cu == FU_XCDS * FU_NW && keep >= 1 && fused_hpw(H, keep) && max_len > FU_MAXLEN &&
          max_len <= LA_MAXLEN && stride >= max_len && stride % 4 == 0;
 }
 
-// Its workspace past the top-k's: the split outputs and their (max, sum), then the blocks' lists.
+// Its workspace past the top-k's: the split outputs and their (max, sum), the blocks' lists, then the rows' tile
+// maxima (written by the long-row indexer before the launch).
 size_t long_attend_bytes(int B, int H, int keep, long max_len) {
   if (keep < 1 || !fused_hpw(H, keep) || max_len <= FU_MAXLEN || max_len > LA_MAXLEN) return 0;
   return fu_up256(attend_xcd_bytes(B, H, keep)) +
-         fu_up256((size_t)B * FU_NW * (LA_HDR + 2 * (size_t)la_block(max_len)) * 4);
+         fu_up256((size_t)B * FU_NW * (LA_HDR + 2 * (size_t)la_block(max_len)) * 4) +
+         fu_up256((size_t)B * la_ntile(max_len) * 4);
 }
+
+// The tile maxima's place in that workspace and their tiles per row (the long-row indexer's bm and nb, tiles of 32).
+float* long_attend_tmax(void* ws, int B, int H, int keep, long max_len) {
+  return reinterpret_cast<float*>(static_cast<char*>(ws) + fu_up256(attend_xcd_bytes(B, H, keep)) +
+                                  fu_up256((size_t)B * FU_NW * (LA_HDR + 2 * (size_t)la_block(max_len)) * 4));
+}
+int long_attend_ntile(long max_len) { return la_ntile(max_len); }
 
 hipError_t launch_decode_long_attend(const uint16_t* q, const uint8_t* kv, const float* kvs, const int* table,
                                      const int* ctx_len, const float* scores, int stride, int* hist, int* idx,
@@ -2444,7 +2533,9 @@ hipError_t launch_decode_long_attend(const uint16_t* q, const uint8_t* kv, const
   LongAttArgs la;
   la.hist = hist;
   la.bw = la_block(max_len);
+  la.ntile = la_ntile(max_len);
   la.lst = reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + fu_up256(attend_xcd_bytes(B, H, keep)));
+  la.tmax = long_attend_tiles(max_len) ? long_attend_tmax(ws, B, H, keep, max_len) : nullptr;
   const dim3 grid(FU_XCDS * FU_NW), block(FU_THREADS);
   constexpr int RPL_MAX = 4;
   for (int r0 = 0; r0 < B; r0 += FU_XCDS * RPL_MAX) {

@@ -272,6 +272,7 @@ __global__ __launch_bounds__(IDX_THREADS, 2) void indexer_decode_long_kernel(
 #pragma unroll
     for (int r = 0; r < 16; ++r) wr[m][r] = ws[32 * m + 8 * (r >> 2) + 4 * h + (r & 3)];
   const int sub = 1 << sub_log2;
+  int tmr = __float_as_int(NEG_INF);  // tiles of 32 (sub_log2 = 5): lane i holds the maximum of the wave's tile i
 
   for (int i0 = 0; i0 < n_live; i0 += IL_RING) {
 #pragma unroll
@@ -281,7 +282,11 @@ __global__ __launch_bounds__(IDX_THREADS, 2) void indexer_decode_long_kernel(
       // tile i has arrived (the IL_AHEAD - 1 tiles after it and the last tiles' stores may still be out): issue tile
       // i + IL_AHEAD into the slot tile i - 1 left (a tile past the wave's range reads its keys, unused); the
       // compiler's own wait before tile i's first use keeps the data exact whatever this count admits
-      __builtin_amdgcn_s_waitcnt(vmcnt_wait(5 * (IL_AHEAD - 1) + (BM ? 2 : 1) * IL_AHEAD));
+      // (stores a tile: the score, and with sub-blocks below 32 their maxima)
+      if (BM && sub_log2 < 5)
+        __builtin_amdgcn_s_waitcnt(vmcnt_wait(5 * (IL_AHEAD - 1) + 2 * IL_AHEAD));
+      else
+        __builtin_amdgcn_s_waitcnt(vmcnt_wait(5 * (IL_AHEAD - 1) + IL_AHEAD));
       __builtin_amdgcn_sched_barrier(0);
       {
         const int ia = i + IL_AHEAD;
@@ -315,9 +320,17 @@ __global__ __launch_bounds__(IDX_THREADS, 2) void indexer_decode_long_kernel(
         if (HIST && v > VISIBLE) atomicAdd(&hs[order_key(v) >> IDX_HSHIFT], 1);
       }
       if (BM) {
-        float mx = v;
-        for (int d = 1; d < sub; d <<= 1) mx = max_nonan(mx, __shfl_xor(mx, d, WAVE));
-        if (h == 0 && (j & (sub - 1)) == 0 && (pos >> sub_log2) < nb) bm[(size_t)b * nb + (pos >> sub_log2)] = mx;
+        if (sub_log2 == 5) {
+          // (uniform) the tile's maximum by DPP (each row of 16 lanes, then row 0's into row 1) into lane i of tmr
+          float mx = row_max(v);
+          mx = fmaxf(mx, __int_as_float(dpp<0x142, 0xa, false>(__float_as_int(mx))));
+          const int m16 = __builtin_amdgcn_readlane(__float_as_int(mx), 16);
+          tmr = lane == i ? m16 : tmr;
+        } else {
+          float mx = v;
+          for (int d = 1; d < sub; d <<= 1) mx = max_nonan(mx, __shfl_xor(mx, d, WAVE));
+          if (h == 0 && (j & (sub - 1)) == 0 && (pos >> sub_log2) < nb) bm[(size_t)b * nb + (pos >> sub_log2)] = mx;
+        }
       }
     }
   }
@@ -325,8 +338,11 @@ __global__ __launch_bounds__(IDX_THREADS, 2) void indexer_decode_long_kernel(
   for (int e = lane; e < (n_t - n_live) * IDX_TILE; e += WAVE) {
     const int pos = (tw0 + n_live) * IDX_TILE + e;
     if (pos < stride) srow[pos] = NEG_INF;
-    if (BM && (pos & ((1 << sub_log2) - 1)) == 0 && (pos >> sub_log2) < nb) bm[(size_t)b * nb + (pos >> sub_log2)] = NEG_INF;
+    if (BM && sub_log2 < 5 && (pos & ((1 << sub_log2) - 1)) == 0 && (pos >> sub_log2) < nb)
+      bm[(size_t)b * nb + (pos >> sub_log2)] = NEG_INF;
   }
+  // tiles of 32: the wave's tile maxima in one store (NEG_INF past the context)
+  if (BM && sub_log2 == 5 && lane < n_t && tw0 + lane < nb) bm[(size_t)b * nb + tw0 + lane] = __int_as_float(tmr);
   if (HIST) {
     // the row's first-level top-k histogram (top 12 bits of the order key of the selectable scores)
     __syncthreads();
@@ -361,6 +377,9 @@ static hipError_t launch_indexer_long_mt(const uint16_t* q, const float* w, cons
                                          const int* table, const int* ctx_len, float* scores, float* bm, int sub_log2,
                                          int nb, int* hist, int B, int Hi, int max_pages, int page_size,
                                          int num_pages, int stride, int num_cu, hipStream_t s) {
+  if (hist && bm)
+    return launch_indexer_long_v<MT, true, true>(q, w, k, ks, table, ctx_len, scores, bm, sub_log2, nb, hist, B, Hi,
+                                                 max_pages, page_size, num_pages, stride, num_cu, s);
   if (hist)
     return launch_indexer_long_v<MT, false, true>(q, w, k, ks, table, ctx_len, scores, nullptr, 0, 0, hist, B, Hi,
                                                   max_pages, page_size, num_pages, stride, num_cu, s);
@@ -372,12 +391,14 @@ static hipError_t launch_indexer_long_mt(const uint16_t* q, const float* w, cons
 }
 
 // The long-row indexer (no additive candidates): with the top-k's first-level histogram accumulated into hist
-// [B, 4096] when given, else with the two-level selection's sub-block maxima when bm is given (1 << sub_log2 <= 32).
+// [B, 4096] when given, and with sub-block maxima bm [B, nb] when bm is given (1 << sub_log2 <= 32): the two-level
+// selection's first level, or (with the histogram) the maxima of the 32-key tiles that the long rows' one-launch
+// selection reads instead of the scores.
 hipError_t launch_indexer_decode_long(const uint16_t* q, const float* w, const uint8_t* k, const float* ks,
                                       const int* table, const int* ctx_len, float* scores, float* bm, int sub_log2,
                                       int nb, int* hist, int B, int Hi, int max_pages, int page_size, int num_pages,
                                       int stride, int num_cu, hipStream_t s) {
-  if (!hist && bm && (sub_log2 < 1 || sub_log2 > 5)) return hipErrorInvalidValue;
+  if (bm && (sub_log2 < 1 || sub_log2 > 5)) return hipErrorInvalidValue;
   if (Hi <= 32)
     return launch_indexer_long_mt<1>(q, w, k, ks, table, ctx_len, scores, bm, sub_log2, nb, hist, B, Hi, max_pages,
                                      page_size, num_pages, stride, num_cu, s);
