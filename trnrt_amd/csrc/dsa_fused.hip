@@ -1922,7 +1922,8 @@ struct LongAttArgs {
 };
 constexpr int LA_HDR = 32;   // list header words (the count)
 constexpr int LA_MAXLEN = FU_NW * 65536;  // 2,097,152 tokens a row
-constexpr int L_LA = 0;      // stage 2's per-list words [6][32] (L_STATE's place)
+constexpr int L_LA = 0;      // stage 2's per-list words [6][32] (L_STATE's place, before L_CO1)
+static_assert(L_LA + 4 * 6 * FU_NW <= L_CO1, "the per-list words clear of the coarse bins");
 // stage 1 over the scores (blocks of at most LA_SCAN_MAX positions: at most one round of loads)
 constexpr int LA_PASS = 8;   // positions per thread and pass (two 16-byte score loads)
 constexpr int LA_BATCH = 4;  // passes a round of loads
@@ -1996,21 +1997,23 @@ __device__ __forceinline__ int la_prep(const FusedArgs& a, uint8_t* lds, const i
 // la_select_regs: every list of at most LA_LCAP entries, held in registers (thread (w, q): list w's entries
 // 16 q .. 16 q + 15, one round of loads); la_select_loop: any lists, passed from the L2 (a list at a time).
 constexpr int LA_LPT = 16, LA_LCAP = 16 * LA_LPT;
+// (the second level's counts in bins1 and their coarse bins in co1, by every wave alike)
 __device__ __forceinline__ void la_t_search(const FusedArgs& a, uint8_t* lds, int c0, int above0, uint32_t* T,
                                             int* room) {
-  int* scr = reinterpret_cast<int*>(lds + L_MISC);
-  int* bins1 = reinterpret_cast<int*>(lds + L_BINS);
-  const int tid = threadIdx.x;
-  int hb[8];
-  *reinterpret_cast<int4*>(hb) = *reinterpret_cast<const int4*>(bins1 + 8 * tid);
-  *reinterpret_cast<int4*>(hb + 4) = *reinterpret_cast<const int4*>(bins1 + 8 * tid + 4);
+  const int* bins1 = reinterpret_cast<const int*>(lds + L_BINS);
+  const int* co1 = reinterpret_cast<const int*>(lds + L_CO1);
   int c1, above1;
   int need = a.keep - above0;
-  fu_find_bin<8>(hb, need, scr + 16, &c1, &above1);
+  fu_wave_find(bins1, co1, need, &c1, &above1);
   need -= above1;
   *T = ((uint32_t)c0 << 20) | ((uint32_t)c1 << 8);
   *room = need;  // (need >= bins1[c1]: every key of bin c1 is taken, T its lowest key with all its ties)
-  (void)tid;
+}
+
+// A key of bin c0 into the second level's counts.
+__device__ __forceinline__ void la_add1(uint8_t* lds, uint32_t k) {
+  atomicAdd(reinterpret_cast<int*>(lds + L_BINS) + ((k >> 8) & 4095u), 1);
+  atomicAdd(reinterpret_cast<int*>(lds + L_CO1) + ((k >> 14) & 63u), 1);
 }
 
 __device__ __forceinline__ void la_select_regs(const FusedArgs& a, uint8_t* lds, const uint32_t* lst_b,
@@ -2039,7 +2042,7 @@ __device__ __forceinline__ void la_select_regs(const FusedArgs& a, uint8_t* lds,
   if (c0 >= 0) {
 #pragma unroll
     for (int i = 0; i < LA_LPT; ++i)
-      if (key[i] && (int)(key[i] >> 20) == c0) atomicAdd(&bins1[(key[i] >> 8) & 4095u], 1);
+      if (key[i] && (int)(key[i] >> 20) == c0) la_add1(lds, key[i]);
     __syncthreads();
     la_t_search(a, lds, c0, above0, &T, &room);
     const int c1 = (int)((T >> 8) & 4095u);
@@ -2049,9 +2052,8 @@ __device__ __forceinline__ void la_select_regs(const FusedArgs& a, uint8_t* lds,
       for (int i = 0; i < LA_LPT; ++i)
         if (key[i] && (key[i] >> 8) == hi24) atomicAdd(&bins2[key[i] & 255u], 1);
       __syncthreads();
-      const int hb2[1] = {tid < 256 ? bins2[tid] : 0};
       int c2, above2;
-      fu_find_bin<1>(hb2, room, scr + 32, &c2, &above2);
+      fu_wave_find256(bins2, room, &c2, &above2);
       T |= (uint32_t)c2;
       room = max(room - above2, 0);
     }
@@ -2118,7 +2120,7 @@ __device__ __forceinline__ void la_select_loop(const FusedArgs& a, uint8_t* lds,
       const uint2* e = reinterpret_cast<const uint2*>(lst_b + (size_t)w * lrow_words + LA_HDR);
       for (int i = tid; i < lcnt[w]; i += FU_THREADS) {
         const uint32_t k = e[i].x;
-        if ((int)(k >> 20) == c0) atomicAdd(&bins1[(k >> 8) & 4095u], 1);
+        if ((int)(k >> 20) == c0) la_add1(lds, k);
       }
     }
     __syncthreads();
@@ -2134,9 +2136,8 @@ __device__ __forceinline__ void la_select_loop(const FusedArgs& a, uint8_t* lds,
         }
       }
       __syncthreads();
-      const int hb2[1] = {tid < 256 ? bins2[tid] : 0};
       int c2, above2;
-      fu_find_bin<1>(hb2, room, scr + 32, &c2, &above2);
+      fu_wave_find256(bins2, room, &c2, &above2);
       T |= (uint32_t)c2;
       room = max(room - above2, 0);
     }
@@ -2254,6 +2255,7 @@ __global__ __launch_bounds__(FU_THREADS, 1) void decode_long_attend_kernel(Fused
     }
     for (int i = tid; i < 4096; i += FU_THREADS) bins1[i] = 0;
     if (tid < 256) bins2[tid] = 0;
+    if (tid < 64) reinterpret_cast<int*>(lds + L_CO1)[tid] = 0;
     if (tid < FU_NW) lgt[tid] = leq[tid] = 0;
     if (tid < AT::SPLIT) pos_l[tid] = 0;  // outputs past the count are 0
     if (tid == 0) scr[8] = scr[24] = scr[40] = -1;
