@@ -7,9 +7,11 @@
  * DSA_OK (0) or a negative DSA_E* code; dsa_strerror() names it. No entry point allocates device memory: scratch
  * space is a caller-owned workspace sized by dsa_workspace_bytes(). A workspace must be zero-filled before its
  * first use (dsa_workspace_clear, or any zero fill) and written by nothing but these calls afterwards. A decode or
- * top-k workspace starts with 1 KiB of barrier and status words at the same offset for every batch size (the status
- * words count across calls, see dsa_layer_status), then the top-k histograms [B, 4096] int32: the zero region of a
- * call of B rows, which the call leaves zero again; the rest is per-call scratch. The library records on the host
+ * top-k workspace starts with 1 KiB of barrier and status words at the same offset for every batch size (a barrier
+ * counter only grows, by 256 per launch that uses it, so it always holds a multiple of 256 between calls, zero
+ * included; the status words count across calls, see dsa_layer_status), then the top-k histograms [B, 4096] int32:
+ * with the barrier words, the zero region of a call of B rows, which the call leaves as it found it (histograms zero,
+ * counters multiples of 256); the rest is per-call scratch. The library records on the host
  * how much of each workspace's start is zero and zero-fills the difference (a fill kernel on the call's stream)
  * before a call whose zero region reaches further than the last call's, or before the first call it sees on a
  * workspace: so one workspace serves any number of calls, of any batch sizes it is large enough for, and graph

@@ -37,11 +37,12 @@ SYNC_WORDS = 256  # the workspace's first 1 KiB: per XCD 16 barrier and status w
 
 
 def _workspace_clean(L):
-    """The per-XCD barrier words (arrivals, exits) and the histograms are zero again, and no barrier wait gave up
-    (the status words, read through the C ABI's dsa_layer_status as well)."""
+    """The per-XCD barrier counters hold a multiple of 256 (each launch adds 256 on the XCDs it uses), the word after
+    each is zero, the histograms are zero again, and no barrier wait gave up (the status words, read through the C
+    ABI's dsa_layer_status as well)."""
     ws = L.workspace.view(torch.int32).cpu()
     sync = ws[:8 * 16].view(8, 16)
-    assert torch.all(sync[:, :2] == 0), f"barrier words left non-zero: {sync[:, :3].tolist()}"
+    assert torch.all(sync[:, 0] % 256 == 0) and torch.all(sync[:, 1] == 0), f"barrier words: {sync[:, :3].tolist()}"
     assert torch.all(ws[8 * 16:SYNC_WORDS] == 0), "words past the 8 XCDs' barrier words"
     assert torch.all(ws[SYNC_WORDS:SYNC_WORDS + L.B * 4096] == 0), "row histograms left non-zero"
     assert torch.all(sync[:, 2] == 0), "a barrier wait gave up"

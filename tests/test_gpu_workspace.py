@@ -66,7 +66,8 @@ def test_workspace_reused_from_one_launch_to_separate_kernels():
     assert int(Lb.cnt[4]) == 2044
     _check_full(b, Lb)
     ws = Lb.workspace.view(torch.int32).cpu()
-    assert torch.all(ws[:8 * 16].view(8, 16)[:, :2] == 0)
+    sync = ws[:8 * 16].view(8, 16)
+    assert torch.all(sync[:, 0] % 256 == 0) and torch.all(sync[:, 1] == 0)
     assert torch.all(ws[SYNC_WORDS:SYNC_WORDS + 8 * 4096] == 0), "row histograms left non-zero"
     assert Lb.status(clear=True) == {"gave_up": 0, "two_exchange": 1}
     assert Lb.status() == {"gave_up": 0, "two_exchange": 0}

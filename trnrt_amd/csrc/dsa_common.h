@@ -80,7 +80,8 @@ struct PoolKeyWrite {
 };
 constexpr int HIST_REPLICAS = 1;
 // The first bytes of every decode workspace, at the same offset whatever the batch size: per XCD (8 x 16 words) the
-// XCD-local barriers' arrival and exit counters (zero between calls), then two status words that persist across
+// XCD-local barriers' arrival counter (a multiple of 256 between calls: each launch adds 256) and an unused word
+// (zero), then two status words that persist across
 // calls until dsa_layer_status clears them: the count of barrier waits that gave up, and the count of rows that took
 // the one-launch layer's two-exchange selection. The top-k histograms (zero between calls) follow.
 constexpr int WS_SYNC_BYTES = 1024;

@@ -236,28 +236,52 @@ struct FusedArgs {
 constexpr int FU_AUX_PLAIN = 0;  // the cache-policy operand of the loads of a peer's published data: none
 
 // XCD-local barrier of the 32 workgroups of an XCD: every thread's stores complete (drained memory counter), then the
-// workgroup's arrival (one atomic add) and a bounded poll. The XCD's counter is zero at a launch's start (the last
-// workgroup to finish resets it), so the n-th barrier of a launch completes at 32 n arrivals. A wait that gives up
-// (all 32 workgroups must be resident at once: another kernel holding CUs for the whole poll budget, about a second,
-// breaks that) counts itself in the XCD's status word and goes on; every read of a peer's data below stays inside
-// its region whatever that data holds, so such a call ends normally, and dsa_layer_status reports it.
-__device__ __forceinline__ void fu_barrier(int* sync, int n) {
+// workgroup's arrival (one atomic add) and a bounded poll. The XCD's counter only grows: every launch adds exactly
+// FU_SPAN = 8 x 32 to it (each workgroup one arrival per barrier, and the rest of its 8 at its exit, with no wait), so
+// at a launch's start it holds a multiple of FU_SPAN plus the arrivals at this launch's first barrier (fewer than 32:
+// that barrier needs every workgroup's); the base read then, rounded down to FU_SPAN, places the n-th barrier at
+// base + 32 n arrivals (unsigned, so the counter may wrap). Every kernel using these barriers takes at most 8. A wait
+// that gives up (all 32 workgroups must be resident at once: another kernel holding CUs for the whole poll budget,
+// about a second, breaks that) counts itself in the XCD's status word and goes on; every read of a peer's data below
+// stays inside its region whatever that data holds, so such a call ends normally, and dsa_layer_status reports it.
+constexpr unsigned FU_SPAN = 8 * FU_NW;
+struct FuSync {
+  int* w;         // the XCD's words: the counter, then the status words
+  unsigned base;  // the counter's value at this launch's start (thread 0's)
+};
+
+__device__ __forceinline__ FuSync fu_sync_begin(int* w) {
+  FuSync sy{w, 0u};
+  if (threadIdx.x == 0)
+    sy.base = __hip_atomic_load(reinterpret_cast<unsigned*>(w), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) &
+              ~(FU_SPAN - 1u);
+  return sy;
+}
+
+__device__ __forceinline__ void fu_barrier(const FuSync& sy, int n) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) {
-    unsigned* ctr = reinterpret_cast<unsigned*>(sync);
+    unsigned* ctr = reinterpret_cast<unsigned*>(sy.w);
     __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const unsigned target = (unsigned)n * FU_NW;
+    const unsigned target = sy.base + (unsigned)n * FU_NW;
     unsigned polls = 0;
     while ((int)(__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - target) < 0) {
       if (++polls > FU_SPIN) {
-        __hip_atomic_fetch_add(sync + WS_SYNC_GAVE_UP, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(sy.w + WS_SYNC_GAVE_UP, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         break;
       }
       __builtin_amdgcn_s_sleep(1);
     }
   }
   __syncthreads();
+}
+
+// The workgroup's exit after nbar barriers: its remaining arrivals of the launch's FU_SPAN (one add, not waited for).
+__device__ __forceinline__ void fu_exit(const FuSync& sy, int nbar) {
+  if (threadIdx.x == 0)
+    __hip_atomic_fetch_add(reinterpret_cast<unsigned*>(sy.w), FU_SPAN / FU_NW - (unsigned)nbar, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Block-wide over 512 threads, thread t holding the counts of bins PER t .. PER t + PER - 1 (higher bins = larger
@@ -1711,26 +1735,11 @@ __device__ __forceinline__ void fu_combine(const FusedArgs& a, uint8_t* lds, int
   }
 }
 
-// A workgroup's end: the last workgroup of the XCD to finish resets its barrier words (no workgroup polls them any
-// more).
-__device__ __forceinline__ void fu_exit(int* sync) {
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    unsigned* wd = reinterpret_cast<unsigned*>(sync);
-    const unsigned e = __hip_atomic_fetch_add(wd + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (e == FU_NW - 1) {
-      __hip_atomic_store(wd, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(wd + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
-}
-
 template <int MT, int HPW>
 __global__ __launch_bounds__(FU_THREADS, 1) void decode_fused_kernel(FusedArgs a) {
   __shared__ __align__(16) uint8_t lds[FU_LDS];
   const int x = blockIdx.x % FU_XCDS, j = blockIdx.x / FU_XCDS;
-  int* sync = a.sync + x * WS_SYNC_WORDS;
+  const FuSync sync = fu_sync_begin(a.sync + x * WS_SYNC_WORDS);
   // one row per XCD and launch (rows row0 + x; a batch of more than 8 rows takes several launches, which keeps
   // each workgroup's per-lane address arithmetic out of a loop over rows, where it would be held in registers)
   const int b = a.row0 + x;
@@ -1758,8 +1767,8 @@ __global__ __launch_bounds__(FU_THREADS, 1) void decode_fused_kernel(FusedArgs a
   fu_combine(a, lds, b, j);
   // the count of rows that took the two-exchange selection (here, where no later wait is held up by its round trip)
   if (nbar == 3 && j == 0 && threadIdx.x == 0)
-    __hip_atomic_fetch_add(sync + WS_SYNC_TWO_EXCHANGE, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  fu_exit(sync);
+    __hip_atomic_fetch_add(sync.w + WS_SYNC_TWO_EXCHANGE, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  fu_exit(sync, nbar);
 }
 
 // The pooled (GLM, kpool > 1) decode layer step in one launch (trnrt/models/mla.py:505-526 `attention_long` for a
@@ -1772,7 +1781,7 @@ template <int HPW, bool WRITE>
 __global__ __launch_bounds__(FU_THREADS, 1) void decode_pooled_fused_kernel(FusedArgs a) {
   __shared__ __align__(16) uint8_t lds[FU_LDS];
   const int x = blockIdx.x % FU_XCDS, j = blockIdx.x / FU_XCDS;
-  int* sync = a.sync + x * WS_SYNC_WORDS;
+  const FuSync sync = fu_sync_begin(a.sync + x * WS_SYNC_WORDS);
   const int b = a.row0 + x;
   if (b >= a.B) return;  // an XCD without a row
   const int L = min(max(a.ctx_len[b], 0), min(a.stride, FU_POOL_MAXLEN));
@@ -1785,7 +1794,7 @@ __global__ __launch_bounds__(FU_THREADS, 1) void decode_pooled_fused_kernel(Fuse
   fu_attend<HPW, 512, true>(a, lds, b, j, n_slots, live_bias);
   fu_barrier(sync, 2);  // C: every split's output
   fu_combine(a, lds, b, j);
-  fu_exit(sync);
+  fu_exit(sync, 2);
 }
 
 // The split's slot list when the selection came from the separate kernels: output positions o0 .. o1 - 1 of row b,
@@ -1877,7 +1886,7 @@ template <int HPW, int DQK = FU_DQK, bool XT = false>
 __global__ __launch_bounds__(FU_THREADS, 1) void decode_attend_kernel(FusedArgs a, const int* rows, int rpl) {
   __shared__ __align__(16) uint8_t lds[FU_LDS];
   const int x = blockIdx.x % FU_XCDS, j = blockIdx.x / FU_XCDS;
-  int* sync = a.sync + x * WS_SYNC_WORDS;
+  const FuSync sync = fu_sync_begin(a.sync + x * WS_SYNC_WORDS);
   if (a.row0 + x >= a.B) return;  // an XCD without a row
   const int nr = min(rpl, (a.B - a.row0 - x + FU_XCDS - 1) / FU_XCDS);  // this XCD's rows
   for (int r = 0; r < nr; ++r) {
@@ -1889,7 +1898,7 @@ __global__ __launch_bounds__(FU_THREADS, 1) void decode_attend_kernel(FusedArgs 
   }
   fu_barrier(sync, 1);  // every split's output of the XCD's rows
   for (int r = 0; r < nr; ++r) fu_combine(a, lds, a.row0 + x + FU_XCDS * r, j);
-  fu_exit(sync);
+  fu_exit(sync, 1);
 }
 
 // ---- Rows longer than 32,768 tokens: the selection, the attention and the combine in one launch ----
@@ -2194,7 +2203,7 @@ __global__ __launch_bounds__(FU_THREADS, 1) void decode_long_attend_kernel(Fused
   __shared__ __align__(16) uint8_t lds[FU_LDS];
   using AT = FuAtt<HPW>;
   const int x = blockIdx.x % FU_XCDS, j = blockIdx.x / FU_XCDS;
-  int* sync = a.sync + x * WS_SYNC_WORDS;
+  const FuSync sync = fu_sync_begin(a.sync + x * WS_SYNC_WORDS);
   if (a.row0 + x >= a.B) return;  // an XCD without a row
   const int nr = min(la.rpl, (a.B - a.row0 - x + FU_XCDS - 1) / FU_XCDS);  // this XCD's rows
   const int tid = threadIdx.x, lane = tid & (WAVE - 1);
@@ -2362,7 +2371,7 @@ __global__ __launch_bounds__(FU_THREADS, 1) void decode_long_attend_kernel(Fused
   }
   fu_barrier(sync, nr + 1);  // every split's output of the XCD's rows
   for (int r = 0; r < nr; ++r) fu_combine(a, lds, a.row0 + x + FU_XCDS * r, j);
-  fu_exit(sync);
+  fu_exit(sync, nr + 1);
 }
 
 // ---- host side ----
@@ -2540,6 +2549,7 @@ hipError_t launch_decode_long_attend(const uint16_t* q, const uint8_t* kv, const
   la.tmax = long_attend_tiles(max_len) ? long_attend_tmax(ws, B, H, keep, max_len) : nullptr;
   const dim3 grid(FU_XCDS * FU_NW), block(FU_THREADS);
   constexpr int RPL_MAX = 4;
+  static_assert(RPL_MAX + 1 <= (int)(FU_SPAN / FU_NW), "a launch's barriers within its span");
   for (int r0 = 0; r0 < B; r0 += FU_XCDS * RPL_MAX) {
     a.row0 = r0;
     const int left = B - r0;
