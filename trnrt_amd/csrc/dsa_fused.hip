@@ -30,8 +30,9 @@
 //      their indices (no barrier before the attention);
 //   4. attention: workgroup j takes head group j % (H / HPW) and split j / (H / HPW) of the ascending output: it
 //      gathers its split's rows into LDS and computes softmax(scale q.K) V over the split in one pass (bf16 MFMA over
-//      the exactly converted rows, fp32 softmax over the whole split), writing the split's normalised output with its
-//      max and sum (the arithmetic of trnrt/kernels/dsa_decode.py:26-37 and trnrt/kernels/dsa_slots.py:48-65);
+//      the exactly converted rows, fp32 softmax over the whole split), writing the split's output (the sum of
+//      exp(score - max) v, divided in the combine) with its max and sum (the arithmetic of
+//      trnrt/kernels/dsa_decode.py:26-37 and trnrt/kernels/dsa_slots.py:48-65);
 //      barrier C;
 //   5. combine: the splits merged by log-sum-exp (trnrt/models/mla.py:853-856), workgroup j for 1/32 of the outputs.
 // The last workgroup of an XCD to finish resets the XCD's barrier words, so the workspace region that must be zero
@@ -204,7 +205,7 @@ struct FusedArgs {
                    // above c0 (32 words), then the candidates, (low 20 key bits << 10) | position in the workgroup's
                    // range, in position order
   uint32_t* lst;   // [B][32][FuForm::LROW]: per workgroup its key list
-  uint16_t* part;  // [B][S][H][512]: split outputs (normalised, bf16), a split's heads side by side
+  uint16_t* part;  // [B][S][H][512]: split outputs (bf16, sums of exp(score - split max) v), heads side by side
 
   float2* ml;      // [B][S][H]: split max and sum
   int B, Hi, H, max_pages, page_size, page_shift, num_pages, stride, keep;
@@ -1641,36 +1642,39 @@ __device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int 
       for (int h = 0; h < HB; ++h) o[h][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pop[h], vop, o[h][n], 0, 0, 0);
     }
   }
-  // the split's normalised output (bf16), max and sum: lane (l16, q4) holds heads 16 h + 4 q4 + i at dim
-  // 64 wave + 16 n + l16; neighbouring lanes swap halves so that an even lane stores heads i = 0, 1 and an odd lane
-  // heads i = 2, 3, each as a pair of dims
+  // the split's output (bf16, not normalised: the combine divides by the splits' total), max and sum: lane (l16, q4)
+  // holds heads 16 h + 4 q4 + i at dim 64 wave + 16 n + l16; neighbouring lanes swap halves so that an even lane
+  // stores heads i = 0, 1 and an odd lane heads i = 2, 3, each as a pair of dims; wave 0's lanes l16 = 0 store the
+  // (max, sum) pairs
   const bool odd = l16 & 1;
+  if (wave == 0 && l16 == 0) {
+#pragma unroll
+    for (int h = 0; h < HB; ++h)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int hl = 16 * h + 4 * q4 + i;
+        float r[TG], mr[TG];
+#pragma unroll
+        for (int t = 0; t < TG; t += 4) {
+          *reinterpret_cast<float4*>(r + t) = *reinterpret_cast<const float4*>(&sred[hl * TG + t]);
+          *reinterpret_cast<float4*>(mr + t) = *reinterpret_cast<const float4*>(&red[hl * TG + t]);
+        }
+        float l = 0.0f, mh = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < TG; ++t) {
+          l += r[t];
+          mh = max_nonan(mh, mr[t]);
+        }
+        mlp[hl] = make_float2(mh, l);
+      }
+  }
 #pragma unroll
   for (int h = 0; h < HB; ++h) {
-    float inv[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int hl = 16 * h + 4 * q4 + i;
-      float r[TG], mr[TG];
-#pragma unroll
-      for (int t = 0; t < TG; t += 4) {
-        *reinterpret_cast<float4*>(r + t) = *reinterpret_cast<const float4*>(&sred[hl * TG + t]);
-        *reinterpret_cast<float4*>(mr + t) = *reinterpret_cast<const float4*>(&red[hl * TG + t]);
-      }
-      float l = 0.0f, mh = -INFINITY;
-#pragma unroll
-      for (int t = 0; t < TG; ++t) {
-        l += r[t];
-        mh = max_nonan(mh, mr[t]);
-      }
-      inv[i] = __builtin_amdgcn_rcpf(l);  // l >= 1 (the split's maximum contributes exp(0))
-      if (wave == 0 && l16 == 0) mlp[hl] = make_float2(mh, l);
-    }
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
       float v[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = o[h][n][i] * inv[i];
+      for (int i = 0; i < 4; ++i) v[i] = o[h][n][i];
       const float u0 = lane_xor1(odd ? v[0] : v[2]), u1 = lane_xor1(odd ? v[1] : v[3]);
       const int hl = 16 * h + 4 * q4 + (odd ? 2 : 0);
       uint16_t* ph = part + (size_t)hl * FU_DV + 64 * wave + 16 * n + (l16 & ~1);
@@ -1706,10 +1710,12 @@ __device__ __forceinline__ void fu_combine_heads(const FusedArgs& a, float* wts,
     const bool live = sp < S && l > 0.0f;
     float M = row_max(live ? m : -INFINITY);
     M = fmaxf(M, __shfl_xor(M, 16, WAVE));  // the two rows of the head's 32 lanes
-    const float wt = live ? l * __expf(m - M) : 0.0f;
-    float W = row_sum(wt);
+    // split s's output is its unnormalised sum of exp(score - m_s) v: weighted by exp(m_s - M) / W, W the splits'
+    // total sum at the common maximum M
+    const float e = live ? __expf(m - M) : 0.0f;
+    float W = row_sum(e * l);
     W += __shfl_xor(W, 16, WAVE);
-    wts[lane] = wt * __builtin_amdgcn_rcpf(W);  // W >= 1 (the largest split's weight is its sum)
+    wts[lane] = e * __builtin_amdgcn_rcpf(W);  // W >= 1 (the largest split's weight is its sum)
     if (sp == 0 && a.lse) a.lse[(size_t)b * H + hh] = M + __logf(W);
   }
   __syncthreads();
