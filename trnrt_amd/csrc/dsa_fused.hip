@@ -237,7 +237,7 @@ struct FusedArgs {
 constexpr int FU_AUX_PLAIN = 0;  // the cache-policy operand of the loads of a peer's published data: none
 
 // XCD-local barrier of the 32 workgroups of an XCD: every thread's stores complete (drained memory counter), then the
-// workgroup's arrival (one atomic add) and a bounded poll. The XCD's counter only grows: every launch adds exactly
+// workgroup's arrival (one atomic add) and a bounded poll (atomic adds of 0). The XCD's counter only grows: every launch adds exactly
 // FU_SPAN = 8 x 32 to it (each workgroup one arrival per barrier, and the rest of its 8 at its exit, with no wait), so
 // at a launch's start it holds a multiple of FU_SPAN plus the arrivals at this launch's first barrier (fewer than 32:
 // that barrier needs every workgroup's); the base read then, rounded down to FU_SPAN, places the n-th barrier at
@@ -267,7 +267,11 @@ __device__ __forceinline__ void fu_barrier(const FuSync& sy, int n) {
     __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const unsigned target = sy.base + (unsigned)n * FU_NW;
     unsigned polls = 0;
-    while ((int)(__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - target) < 0) {
+    // (each poll an atomic add of 0 with return, read where the arrivals are added: 0.57 us a launch faster than
+    // device-scope loads; a literal 0 would be folded into such a load)
+    unsigned z;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+    while ((int)(__hip_atomic_fetch_add(ctr, z, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - target) < 0) {
       if (++polls > FU_SPIN) {
         __hip_atomic_fetch_add(sy.w + WS_SYNC_GAVE_UP, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         break;
