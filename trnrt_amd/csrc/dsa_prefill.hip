@@ -28,6 +28,9 @@ constexpr int PF_QPW = PF_THREADS / WAVE;  // queries per workgroup
 constexpr int PF_TILES = 64;               // tiles per workgroup: 2048 keys
 constexpr int PF_TPB = 4;                  // tiles per barrier (a "round": 128 keys)
 constexpr int PF_RING = 2 * PF_TPB;        // tiles in flight per thread: two rounds ahead
+constexpr int PF8_TPB = 2;                 // the FP8 kernel's: rounds of 64 keys (fewer registers, 3 workgroups a CU)
+constexpr int PF8_RING = 2 * PF8_TPB;
+static_assert(PF_TILES % PF8_RING == 0, "a block is whole ring turns");
 static_assert(PF_TILES % PF_RING == 0, "a block is whole ring turns");
 
 // MT: head tiles of 32 (Hi <= 32 MT).
@@ -233,14 +236,13 @@ typedef __attribute__((__vector_size__(8 * sizeof(int)))) int i32x8;
 __device__ __forceinline__ int pf8_slot(int key, int piece) { return 8 * key + (piece ^ ((key ^ (key >> 3)) & 7)); }
 
 template <int MT>
-__global__ __launch_bounds__(PF_THREADS, 2) void indexer_prefill_fp8_kernel(
+__global__ __launch_bounds__(PF_THREADS, 3) void indexer_prefill_fp8_kernel(
     const uint8_t* __restrict__ q8, const float* __restrict__ qscale, const float* __restrict__ w,
     const uint8_t* __restrict__ kcache, const float* __restrict__ kscale, const int* __restrict__ npool,
     float* __restrict__ scores, int N, int Hi, int P, int stride, float scale, float* __restrict__ bm, int sub_log2,
     int nb) {
-  __shared__ u32x4 kb[2][PF_TPB][PF_TILE * 8];  // two rounds of FP8 tiles (key j: 8 pieces of 16 bytes)
+  __shared__ u32x4 kb[2][PF8_TPB][PF_TILE * 8];  // two rounds of FP8 tiles (key j: 8 pieces of 16 bytes)
   __shared__ float ksc_s[PF_TILES * PF_TILE];
-  __shared__ float sc_s[PF_QPW][PF_TILES * PF_TILE];  // with bm: each wave's scores of the block, for the maxima
   __shared__ int lmax[PF_QPW];
   const int wave = threadIdx.x / WAVE;
   const int lane = threadIdx.x & (WAVE - 1);
@@ -257,9 +259,9 @@ __global__ __launch_bounds__(PF_THREADS, 2) void indexer_prefill_fp8_kernel(
     const int key = min(p_begin + it * PF_TILE + tk, P - 1);
     return *reinterpret_cast<const u32x4*>(kcache + (size_t)key * PF_D + 16 * tp);
   };
-  u32x4 ring[PF_RING];
+  u32x4 ring[PF8_RING];
 #pragma unroll
-  for (int u = 0; u < PF_RING; ++u) ring[u] = load_tile(u);
+  for (int u = 0; u < PF8_RING; ++u) ring[u] = load_tile(u);
 #pragma unroll
   for (int i = 0; i < PF_TILES * PF_TILE / PF_THREADS; ++i) {
     const int k = i * PF_THREADS + threadIdx.x;
@@ -318,7 +320,6 @@ __global__ __launch_bounds__(PF_THREADS, 2) void indexer_prefill_fp8_kernel(
     const int pos = p_begin + t * PF_TILE + j;
     const float v = pos < L ? part * (ksc_s[t * PF_TILE + j] * scale) : NEG_INF;
     if (n < N && h == 0 && pos < p_end) srow[pos] = v;
-    if (bm && h == 0) sc_s[wave][t * PF_TILE + j] = v;
   };
   auto tile_mma = [&](const u32x4* tile, int t, f32x16(&cur)[MT], const f32x16(&prev)[MT]) {
     float part = 0.0f;
@@ -339,30 +340,32 @@ __global__ __launch_bounds__(PF_THREADS, 2) void indexer_prefill_fp8_kernel(
   for (int m = 0; m < MT; ++m) acc_b[m] = f32x16{};
   auto round = [&](int t0, auto base) {
     constexpr int U0 = decltype(base)::value;
-    u32x4(*tiles)[PF_TILE * 8] = kb[(t0 / PF_TPB) & 1];
+    u32x4(*tiles)[PF_TILE * 8] = kb[(t0 / PF8_TPB) & 1];
 #pragma unroll
-    for (int u = 0; u < PF_TPB; ++u) {
+    for (int u = 0; u < PF8_TPB; ++u) {
       tiles[u][pf8_slot(tk, tp)] = ring[U0 + u];
-      ring[U0 + u] = load_tile(t0 + u + PF_RING);
+      ring[U0 + u] = load_tile(t0 + u + PF8_RING);
     }
     __syncthreads();
 #pragma unroll
-    for (int u = 0; u < PF_TPB; u += 2) {
+    for (int u = 0; u < PF8_TPB; u += 2) {
       tile_mma(tiles[u], t0 + u, acc_a, acc_b);
       tile_mma(tiles[u + 1], t0 + u + 1, acc_b, acc_a);
     }
   };
   int t = 0;
-  for (; t < ntiles; t += PF_RING) {
+  for (; t < ntiles; t += PF8_RING) {
     round(t, std::integral_constant<int, 0>{});
-    round(t + PF_TPB, std::integral_constant<int, PF_TPB>{});
+    round(t + PF8_TPB, std::integral_constant<int, PF8_TPB>{});
   }
   float part = 0.0f;
 #pragma unroll
   for (int s = 0; s < 2; ++s) epilogue_part(part, acc_b, s);
   finish(part, t - 1);
-  // each wave's scores are also in its LDS row (its own writes, in order): the maxima from there
-  if (bm && n < N) block_max_rows(sc_s[wave], p_begin, bm + (size_t)n * nb, p_begin, p_end, sub_log2, nb, true, lane);
+  if (bm) {
+    __syncthreads();  // the workgroup's scores are written
+    if (n < N) block_max_rows(srow, 0, bm + (size_t)n * nb, p_begin, p_end, sub_log2, nb, (stride & 3) == 0, lane);
+  }
 }
 
 template <int MT, bool BF16K>
