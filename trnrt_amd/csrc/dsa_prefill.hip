@@ -28,7 +28,7 @@ constexpr int PF_QPW = PF_THREADS / WAVE;  // queries per workgroup
 constexpr int PF_TILES = 64;               // tiles per workgroup: 2048 keys
 constexpr int PF_TPB = 4;                  // tiles per barrier (a "round": 128 keys)
 constexpr int PF_RING = 2 * PF_TPB;        // tiles in flight per thread: two rounds ahead
-constexpr int PF8_TPB = 2;                 // the FP8 kernel's: rounds of 64 keys (fewer registers, 3 workgroups a CU)
+constexpr int PF8_TPB = 2;                 // rounds of 64 keys (fewer registers and LDS: 3 workgroups a CU)
 constexpr int PF8_RING = 2 * PF8_TPB;
 static_assert(PF_TILES % PF8_RING == 0, "a block is whole ring turns");
 static_assert(PF_TILES % PF_RING == 0, "a block is whole ring turns");
@@ -65,15 +65,19 @@ __device__ __forceinline__ void block_max_rows(const float* srow, int base, floa
 // trnrt/models/mla.py:491-503 `context_pool_keys`): a thread's share of a tile is 32 bytes (two loads) that go to
 // LDS as they are, so the ring holds twice the registers (taken at MT 1 only).
 template <int MT, bool BF16K>
-__global__ __launch_bounds__(PF_THREADS, 2) void indexer_prefill_kernel(
+__global__ __launch_bounds__(PF_THREADS, MT == 1 ? 3 : 2) void indexer_prefill_kernel(
     const uint16_t* __restrict__ q, const float* __restrict__ w, const void* __restrict__ kcache_v,
     const float* __restrict__ kscale, const int* __restrict__ npool, float* __restrict__ scores, int N, int Hi, int P,
     int stride, float scale, float* __restrict__ bm, int sub_log2, int nb) {
   static_assert(!BF16K || MT == 1, "bf16 keys: up to 32 heads");
+  // rounds of TPB tiles, RING in flight: at 32 heads rounds of 2 (fewer registers and LDS: 3 workgroups a CU), at 64
+  // rounds of 4 (2 workgroups a CU; rounds of 2 there spill)
+  constexpr int TPB = MT == 1 ? PF8_TPB : PF_TPB, RING = 2 * TPB;
+  static_assert(PF_TILES % RING == 0, "a block is whole ring turns");
   const uint8_t* kcache = static_cast<const uint8_t*>(kcache_v);
   // two rounds of bf16 tiles (key j of a tile: 16 pieces of 8 dims, piece p at slot 16 j + (p ^ (j & 15))), the
   // block's per-key scales and the queries' candidate counts
-  __shared__ u32x4 kb[2][PF_TPB][PF_TILE * 16];
+  __shared__ u32x4 kb[2][TPB][PF_TILE * 16];
   __shared__ float ksc_s[PF_TILES * PF_TILE];
   __shared__ int lmax[PF_QPW];
   const int wave = threadIdx.x / WAVE;
@@ -87,7 +91,7 @@ __global__ __launch_bounds__(PF_THREADS, 2) void indexer_prefill_kernel(
   const int ntiles = (p_end - p_begin + PF_TILE - 1) / PF_TILE;
 
   // this thread's share of a tile: key t / 8, bytes 16 (t % 8) .. + 15 (coalesced), converted into two pieces.
-  // Tiles are prefetched PF_RING ahead into a ring of registers that is never copied (a copy of a register whose
+  // Tiles are prefetched RING ahead into a ring of registers that is never copied (a copy of a register whose
   // load is in flight waits for it): every loop turn below is unrolled, so each slot is a fixed register.
   const int tk = threadIdx.x >> 3, tp = threadIdx.x & 7;
   constexpr int KB = BF16K ? 2 * PF_D : PF_D;  // key row bytes
@@ -95,9 +99,9 @@ __global__ __launch_bounds__(PF_THREADS, 2) void indexer_prefill_kernel(
     const int key = min(p_begin + it * PF_TILE + tk, P - 1);  // in range whatever the block
     return *reinterpret_cast<const u32x4*>(kcache + (size_t)key * KB + (BF16K ? 32 * tp + 16 * half : 16 * tp));
   };
-  u32x4 ring[PF_RING], ring2[BF16K ? PF_RING : 1];
+  u32x4 ring[RING], ring2[BF16K ? RING : 1];
 #pragma unroll
-  for (int u = 0; u < PF_RING; ++u) {
+  for (int u = 0; u < RING; ++u) {
     ring[u] = load_tile(u, 0);
     if (BF16K) ring2[u] = load_tile(u, 1);
   }
@@ -176,38 +180,38 @@ __global__ __launch_bounds__(PF_THREADS, 2) void indexer_prefill_kernel(
   f32x16 acc_a[MT], acc_b[MT];
 #pragma unroll
   for (int m = 0; m < MT; ++m) acc_b[m] = f32x16{};
-  // a round: convert the round's PF_TPB tiles from their ring slots into LDS, refill the slots PF_RING tiles ahead,
+  // a round: convert the round's TPB tiles from their ring slots into LDS, refill the slots RING tiles ahead,
   // one barrier, then the round's tiles on MFMA (even tiles into acc_a, odd into acc_b). Whole ring turns are run
   // unconditionally (each slot then has the same loads in flight after it); tiles past the block's last tile load
   // clamped keys and store nothing (their positions are at or past p_end).
   auto round = [&](int t0, auto base) {
     constexpr int U0 = decltype(base)::value;
-    u32x4(*tiles)[PF_TILE * 16] = kb[(t0 / PF_TPB) & 1];
+    u32x4(*tiles)[PF_TILE * 16] = kb[(t0 / TPB) & 1];
 #pragma unroll
-    for (int u = 0; u < PF_TPB; ++u) {
+    for (int u = 0; u < TPB; ++u) {
       const u32x4 r = ring[U0 + u];
       if (BF16K) {
         tiles[u][16 * tk + ((2 * tp) ^ (tk & 15))] = r;
         tiles[u][16 * tk + ((2 * tp + 1) ^ (tk & 15))] = ring2[U0 + u];
-        ring2[U0 + u] = load_tile(t0 + u + PF_RING, 1);
+        ring2[U0 + u] = load_tile(t0 + u + RING, 1);
       } else {
         const bf16x8 lo = fp8x8_to_bf16x8(r[0], r[1]), hi = fp8x8_to_bf16x8(r[2], r[3]);
         tiles[u][16 * tk + ((2 * tp) ^ (tk & 15))] = __builtin_bit_cast(u32x4, lo);
         tiles[u][16 * tk + ((2 * tp + 1) ^ (tk & 15))] = __builtin_bit_cast(u32x4, hi);
       }
-      ring[U0 + u] = load_tile(t0 + u + PF_RING, 0);
+      ring[U0 + u] = load_tile(t0 + u + RING, 0);
     }
     __syncthreads();  // the round is in LDS; the other round's buffers are free (every wave finished them)
 #pragma unroll
-    for (int u = 0; u < PF_TPB; u += 2) {
+    for (int u = 0; u < TPB; u += 2) {
       tile_mma(tiles[u], t0 + u, acc_a, acc_b);
       tile_mma(tiles[u + 1], t0 + u + 1, acc_b, acc_a);
     }
   };
   int t = 0;
-  for (; t < ntiles; t += PF_RING) {
+  for (; t < ntiles; t += RING) {
     round(t, std::integral_constant<int, 0>{});
-    round(t + PF_TPB, std::integral_constant<int, PF_TPB>{});
+    round(t + TPB, std::integral_constant<int, TPB>{});
   }
   float part = 0.0f;
 #pragma unroll
