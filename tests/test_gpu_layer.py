@@ -105,6 +105,34 @@ def test_layer_long_ragged_many_short_rows():
     _attention_check(inp, L)
 
 
+@pytest.mark.parametrize("H, lengths", [
+    # 21 rows: XCDs 0-4 hold three (two rows at once, then one row by all 32 workgroups), XCDs 5-7 two at once
+    (64, [40000, 1, 33000, 2048, 2049, 7, 36000, 100, 4095, 34000, 0, 50, 39000, 2000, 17, 3000, 33, 38000, 1024, 9,
+          35000]),
+    # one head group of 32 heads: the rows of an XCD one at a time
+    (32, [40000, 3, 33000, 2048, 5000, 37000, 1, 64, 39000, 2047]),
+])
+def test_layer_long_rows_paired(H, lengths):
+    """The long-row launch with two or three rows an XCD: two rows take 16 workgroups each (each workgroup's row's
+    selection once, then both head groups of one split), a third row all 32; with one head group the rows go one at a
+    time. Short, empty and tied-free ragged rows; every stage against the oracle."""
+    say(f"layer long rows paired: H={H}, {len(lengths)} rows")
+    cfg = W.Config("layer-long-paired", B=len(lengths), L=max(lengths), H=H, Hi=64)
+    inp = W.make_inputs(cfg, seed=53 + H, lengths=lengths)
+    g = inp.to("cuda")
+    L = _layer(g)
+    sc = L.scores.cpu()
+    ref = O.indexer_ref(inp.q_idx, inp.w_k, inp.k_cache, inp.k_scale, inp.table, inp.ctx_len, cfg.page_size,
+                        sc.shape[1])
+    assert row_rel_err(sc, ref, ref > -1e29) <= 1e-2
+    assert torch.all(sc[ref <= -1e29] < -1e29)
+    ri, rc = O.topk_ref(sc, cfg.keep, inp.ctx_len)
+    assert torch.equal(L.cnt.cpu().long(), rc)
+    assert torch.equal(L.idx.cpu().long(), ri)
+    _attention_check(inp, L)
+    assert L.status()["gave_up"] == 0
+
+
 @pytest.mark.parametrize("tied", [False, True])
 def test_layer_long_rows_mixed_forms(tied):
     """Rows past 32,768 tokens in a small batch (the long-row indexer and the chunked long-row selection) beside rows

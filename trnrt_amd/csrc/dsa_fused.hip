@@ -1939,7 +1939,7 @@ struct LongAttArgs {
   int ntile;          // tiles per row of tmax, a multiple of 4
   int rpl;            // rows per XCD
 };
-constexpr int LA_HDR = 32;   // list header words (the count)
+constexpr int LA_HDR = 32;   // list header words (the count; the row's boundary bin, keys above it, visible keys)
 constexpr int LA_MAXLEN = FU_NW * 65536;  // 2,097,152 tokens a row
 constexpr int L_LA = 0;      // stage 2's per-list words [6][32] (L_STATE's place, before L_CO1)
 static_assert(L_LA + 4 * 6 * FU_NW <= L_CO1, "the per-list words clear of the coarse bins");
@@ -1970,25 +1970,33 @@ __device__ __forceinline__ void la_queries(const FusedArgs& a, int b, int j, u32
   for (int i = 0; i < FuAtt<HPW>::QPT; ++i) qv[i] = qsrc[min(tid + FU_THREADS * i, HPW * FU_DQK / 8 - 1)];
 }
 
+// fu_attend_prep's token form in two steps, the split's positions taken from pos_l (the output order) instead of idx:
+// la_slot, thread t's slot of the split's output t (0 past the split), then la_stage, the slot list and the unit's
+// queries into LDS
 template <int HPW>
-__device__ __forceinline__ int la_prep(const FusedArgs& a, uint8_t* lds, const int* pos_l, int b, int j, int cnt_row,
-                                       const u32x4 (&qv)[FuAtt<HPW>::QPT], float* live_bias) {
-  // fu_attend_prep's token form, the split's positions taken from pos_l (the output order) instead of idx
-  using AT = FuAtt<HPW>;
-  constexpr int QPT = AT::QPT;
-  int* slot_l = reinterpret_cast<int*>(lds + AT::L_P);
+__device__ __forceinline__ int la_slot(const FusedArgs& a, const int* pos_l, int b, int s, int cnt_row) {
   const int tid = threadIdx.x;
-  const int s = j / a.HG;
   const bool active = s < a.S;
   const int o0 = active ? s * a.sps : 0, o1 = active ? min(o0 + a.sps, a.keep) : 0;
   const int o = o0 + tid;
   int sl = 0;
-  if (tid < AT::SPLIT && o < o1 && o < max(cnt_row, 1)) {  // the empty row lists output 0 (position 0)
+  if (tid < FuAtt<HPW>::SPLIT && o < o1 && o < max(cnt_row, 1)) {  // the empty row lists output 0 (position 0)
     const int p = max(pos_l[tid], 0), pi = p / a.page_size;
     const int pg = a.table[(size_t)b * a.max_pages + min(pi, a.max_pages - 1)];
     sl = safe_page(pg, a.num_pages) * a.page_size + (p - pi * a.page_size);
   }
-  sl = (unsigned)sl < (unsigned)a.num_slots ? sl : 0;
+  return (unsigned)sl < (unsigned)a.num_slots ? sl : 0;
+}
+
+template <int HPW>
+__device__ __forceinline__ int la_stage(const FusedArgs& a, uint8_t* lds, int sl, int s, int cnt_row,
+                                        const u32x4 (&qv)[FuAtt<HPW>::QPT], float* live_bias) {
+  using AT = FuAtt<HPW>;
+  constexpr int QPT = AT::QPT;
+  int* slot_l = reinterpret_cast<int*>(lds + AT::L_P);
+  const int tid = threadIdx.x;
+  const bool active = s < a.S;
+  const int o0 = active ? s * a.sps : 0, o1 = active ? min(o0 + a.sps, a.keep) : 0;
   if (active) {
     uint16_t* qs = reinterpret_cast<uint16_t*>(lds + AT::L_QST);
 #pragma unroll
@@ -2208,6 +2216,8 @@ __device__ __forceinline__ void la_select_loop(const FusedArgs& a, uint8_t* lds,
   }
 }
 
+constexpr int LA_RPL = 4;  // rows an XCD a launch at most
+
 template <int HPW>
 __global__ __launch_bounds__(FU_THREADS, 1) void decode_long_attend_kernel(FusedArgs a, LongAttArgs la) {
   __shared__ __align__(16) uint8_t lds[FU_LDS];
@@ -2223,14 +2233,11 @@ __global__ __launch_bounds__(FU_THREADS, 1) void decode_long_attend_kernel(Fused
   int* lcnt = reinterpret_cast<int*>(lds + L_LA);  // per list: its entries, above T, at T, ties taken, first output
   int *lgt = lcnt + FU_NW, *leq = lcnt + 2 * FU_NW;
   int* pos_l = reinterpret_cast<int*>(lds + AT::L_P) + AT::CAP + 8;  // the split's positions (P's region)
-  const int hg = j % a.HG, s = j / a.HG;
-  const bool active = s < a.S;
-  const int o0 = active ? s * a.sps : 0, o1 = active ? min(o0 + a.sps, a.keep) : 0;
   const size_t lrow_words = LA_HDR + 2 * (size_t)la.bw;
   for (int r = 0; r < nr; ++r) {
     const int b = a.row0 + x + FU_XCDS * r;
     const int L = min(max(a.ctx_len[b], 0), a.stride);
-    if (r) __syncthreads();  // the previous row's attention is done with the LDS
+    if (r) __syncthreads();  // the previous row's stage 1 is done with the LDS
     // stage 1: the block's keys at or above c0 (every visible key when c0 = -1) into its list, in position order
     uint32_t* lrow = la.lst + ((size_t)b * FU_NW + j) * lrow_words;
     uint2* lent = reinterpret_cast<uint2*>(lrow + LA_HDR);
@@ -2272,12 +2279,7 @@ __global__ __launch_bounds__(FU_THREADS, 1) void decode_long_attend_kernel(Fused
       *reinterpret_cast<int4*>(hv) = h4[0];
       *reinterpret_cast<int4*>(hv + 4) = h4[1];
     }
-    for (int i = tid; i < 4096; i += FU_THREADS) bins1[i] = 0;
-    if (tid < 256) bins2[tid] = 0;
-    if (tid < 64) reinterpret_cast<int*>(lds + L_CO1)[tid] = 0;
-    if (tid < FU_NW) lgt[tid] = leq[tid] = 0;
-    if (tid < AT::SPLIT) pos_l[tid] = 0;  // outputs past the count are 0
-    if (tid == 0) scr[8] = scr[24] = scr[40] = -1;
+    if (tid == 0) scr[8] = -1;
     __syncthreads();
     const int nvis = fu_find_bin<8>(hv, a.keep, scr, &c0, &above0);
     if (nvis <= a.keep) c0 = -1;  // every visible key is selected
@@ -2354,15 +2356,37 @@ __global__ __launch_bounds__(FU_THREADS, 1) void decode_long_attend_kernel(Fused
         __syncthreads();  // scr is written again by the next pass's prefix
       }
     }
-    if (tid == 0) lrow[0] = (uint32_t)listed;
-    fu_barrier(sync, r + 1);  // every block's list of the row (and every workgroup past its histogram read)
+    // the list's count, and for stage 2 the row's boundary bin, the keys above it and its visible keys
+    if (tid == 0) *reinterpret_cast<uint4*>(lrow) = uint4{(uint32_t)listed, (uint32_t)c0, (uint32_t)above0, (uint32_t)nvis};
+  }
+  fu_barrier(sync, 1);  // every block's list of the XCD's rows (and every workgroup past their histograms' reads)
+  for (int r = 0; r < nr; ++r)
     if (tid < FU_HBINS / FU_NW / 4)  // the row's histogram back to zero, 1/32 by each workgroup
-      reinterpret_cast<uint4*>(la.hist + (size_t)b * FU_HBINS + (FU_HBINS / FU_NW) * j)[tid] =
+      reinterpret_cast<uint4*>(la.hist + (size_t)(a.row0 + x + FU_XCDS * r) * FU_HBINS + (FU_HBINS / FU_NW) * j)[tid] =
           uint4{0u, 0u, 0u, 0u};
+  // stages 2-4 a row at a time, or two rows at once: with an even number of head groups, workgroups 0-15 take row r
+  // and 16-31 row r + 1, each its row's selection once and then the two head groups of one split (units 2 u and
+  // 2 u + 1, u = j mod 16, of the row's 32), where taking the rows in turn costs each workgroup two selections
+  for (int r = 0; r < nr;) {
+    const bool paired = a.HG % 2 == 0 && r + 1 < nr;  // (launch-uniform)
+    const int b = a.row0 + x + FU_XCDS * (paired ? r + j / (FU_NW / 2) : r);
+    const int u0 = paired ? 2 * (j % (FU_NW / 2)) : j;  // the first unit (split u0 / HG, head group u0 mod HG)
+    const int hg = u0 % a.HG, s = u0 / a.HG;
+    const bool active = s < a.S;
+    const int o0 = active ? s * a.sps : 0, o1 = active ? min(o0 + a.sps, a.keep) : 0;
+    if (r) __syncthreads();  // the previous rows' attention is done with the LDS
     // stage 2: the lists' counts, then T and the ties to take (the split's queries loading meanwhile)
     u32x4 qv[AT::QPT];
-    la_queries<HPW>(a, b, j, qv);
+    la_queries<HPW>(a, b, u0, qv);
     const uint32_t* lst_b = la.lst + (size_t)b * FU_NW * lrow_words;
+    const uint4 hdr = *reinterpret_cast<const uint4*>(lst_b + (size_t)j * lrow_words);  // this workgroup's own words
+    const int c0 = (int)hdr.y, above0 = (int)hdr.z, nvis = (int)hdr.w;
+    for (int i = tid; i < 4096; i += FU_THREADS) bins1[i] = 0;
+    if (tid < 256) bins2[tid] = 0;
+    if (tid < 64) reinterpret_cast<int*>(lds + L_CO1)[tid] = 0;
+    if (tid < FU_NW) lgt[tid] = leq[tid] = 0;
+    if (tid < AT::SPLIT) pos_l[tid] = 0;  // outputs past the count are 0
+    if (tid == 0) scr[24] = scr[40] = -1;
     if (tid < FU_NW) lcnt[tid] = min((int)lst_b[(size_t)tid * lrow_words], la.bw);
     __syncthreads();
     const int cnt_row = min(nvis, a.keep);
@@ -2372,16 +2396,24 @@ __global__ __launch_bounds__(FU_THREADS, 1) void decode_long_attend_kernel(Fused
     } else {
       la_select_loop(a, lds, lst_b, lrow_words, c0, above0, o0, o1, pos_l);
     }
-    if (j == 0 && tid == 0) a.cnt[b] = cnt_row;
+    if (u0 == 0 && tid == 0) a.cnt[b] = cnt_row;
     __syncthreads();  // the split's positions
     if (hg == 0 && tid < o1 - o0) a.idx[(size_t)b * a.keep + o0 + tid] = pos_l[tid];
-    float live_bias;
-    const int n_slots = la_prep<HPW>(a, lds, pos_l, b, j, cnt_row, qv, &live_bias);
-    fu_attend<HPW>(a, lds, b, j, n_slots, live_bias);
+    const int sl = la_slot<HPW>(a, pos_l, b, s, cnt_row);
+    for (int e = 0; e < (paired ? 2 : 1); ++e) {
+      if (e) {
+        __syncthreads();  // the first unit's attention is done with the LDS
+        la_queries<HPW>(a, b, u0 + 1, qv);
+      }
+      float live_bias;
+      const int n_slots = la_stage<HPW>(a, lds, sl, s, cnt_row, qv, &live_bias);
+      fu_attend<HPW>(a, lds, b, u0 + e, n_slots, live_bias);
+    }
+    r += paired ? 2 : 1;
   }
-  fu_barrier(sync, nr + 1);  // every split's output of the XCD's rows
+  fu_barrier(sync, 2);  // every split's output of the XCD's rows
   for (int r = 0; r < nr; ++r) fu_combine(a, lds, a.row0 + x + FU_XCDS * r, j);
-  fu_exit(sync, nr + 1);
+  fu_exit(sync, 2);
 }
 
 // ---- host side ----
@@ -2558,12 +2590,11 @@ hipError_t launch_decode_long_attend(const uint16_t* q, const uint8_t* kv, const
   la.lst = reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + fu_up256(attend_xcd_bytes(B, H, keep)));
   la.tmax = long_attend_tiles(max_len) ? long_attend_tmax(ws, B, H, keep, max_len) : nullptr;
   const dim3 grid(FU_XCDS * FU_NW), block(FU_THREADS);
-  constexpr int RPL_MAX = 4;
-  static_assert(RPL_MAX + 1 <= (int)(FU_SPAN / FU_NW), "a launch's barriers within its span");
-  for (int r0 = 0; r0 < B; r0 += FU_XCDS * RPL_MAX) {
+  static_assert(2 <= (int)(FU_SPAN / FU_NW), "a launch's barriers within its span");
+  for (int r0 = 0; r0 < B; r0 += FU_XCDS * LA_RPL) {
     a.row0 = r0;
     const int left = B - r0;
-    la.rpl = ((left < FU_XCDS * RPL_MAX ? left : FU_XCDS * RPL_MAX) + FU_XCDS - 1) / FU_XCDS;
+    la.rpl = ((left < FU_XCDS * LA_RPL ? left : FU_XCDS * LA_RPL) + FU_XCDS - 1) / FU_XCDS;
     const hipError_t e = hpw == 32 ? launch("decode_long_attend_kernel", decode_long_attend_kernel<32>, grid, block,
                                             s, a, la)
                                    : launch("decode_long_attend_kernel", decode_long_attend_kernel<16>, grid, block,

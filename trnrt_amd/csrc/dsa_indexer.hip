@@ -197,36 +197,116 @@ __global__ __launch_bounds__(IDX_THREADS, 2) void indexer_decode_kernel(
 }
 
 // Long rows (the separate kernels' indexer past 32,768 tokens): the same wave layout and arithmetic, but each wave
-// streams TW consecutive tiles (up to 64, the launch choosing TW so that about two workgroups per CU cover the batch)
-// through a ring of IL_AHEAD + 1 register tiles, IL_AHEAD in flight ahead of the one it computes, so the row's queries
-// are staged once per workgroup for up to 8,192 keys instead of 512 and the memory stream runs without the
-// workgroups' start-up gaps. The wave's page ids are one load per lane (tile tw0 + lane). HIST: also the row's top-k
-// first-level histogram (as the kernel above). BM: also the two-level top-k's
+// streams up to 64 consecutive tiles of one row through a ring of IL_AHEAD + 1 register tiles, IL_AHEAD in flight
+// ahead of the one it computes, so the row's queries are staged once per workgroup for up to 8,192 keys instead of 512
+// and the memory stream runs without the workgroups' start-up gaps. The wave's page ids are one load per lane (tile
+// tw0 + lane). HIST: also the row's top-k first-level histogram (as the kernel above). BM: also the two-level top-k's
 // first-level sub-block maxima, bm[b, p / sub] = the maximum of the scores of positions p .. p + sub - 1 (sub a power
 // of two up to 32: a tile's 32 keys hold whole sub-blocks), for p < nb sub.
+//
+// Work split (TW = 0, rows' lengths given, B <= 256): the grid's workgroups share the batch's live tiles (those
+// holding a position below the row's length) evenly, whatever the rows' lengths: every workgroup reads the B
+// lengths, and with T live tiles in all and G workgroups, each wave takes cw = ceil(T / (4 (G - B))) consecutive
+// tiles of one row, row b taking ceil(T_b / 4 cw) workgroups (at most G in all); the tiles past each row's length
+// (NEG_INF scores and maxima) are shared out the same way, ceil(Q / G) of the Q of them a workgroup. (A fixed TW
+// tiles a wave: row b takes wgs_per_row workgroups whatever its length, those past it writing NEG_INF.)
 constexpr int IL_AHEAD = 2;
 constexpr int IL_RING = IL_AHEAD + 1;
 constexpr int IL_TW_MAX = 64;
+constexpr int IL_BAL_MAXB = IDX_THREADS;  // rows of a batch the even split takes (one a thread)
+
+// Exclusive prefix sum over the workgroup's IDX_THREADS threads (one value each) and the total; sc holds
+// IDX_WAVES + 1 ints (written, then read after a barrier; the caller's next use of sc waits for a barrier of its own).
+__device__ __forceinline__ int il_block_excl(int v, int* sc, int* total) {
+  const int wave = threadIdx.x / WAVE, lane = threadIdx.x & (WAVE - 1);
+  const int inc = wave_incl_scan(v);
+  if (lane == WAVE - 1) sc[wave] = inc;
+  __syncthreads();
+  int before = 0, all = 0;
+#pragma unroll
+  for (int w2 = 0; w2 < IDX_WAVES; ++w2) {
+    const int t = sc[w2];
+    before += w2 < wave ? t : 0;
+    all += t;
+  }
+  *total = all;
+  return before + inc - v;
+}
 
 template <int MT, bool BM, bool HIST>
 __global__ __launch_bounds__(IDX_THREADS, 2) void indexer_decode_long_kernel(
     const uint16_t* __restrict__ q, const float* __restrict__ w, const uint8_t* __restrict__ kcache,
     const float* __restrict__ kscale, const int* __restrict__ table, const int* __restrict__ ctx_len,
     float* __restrict__ scores, float* __restrict__ bm, int sub_log2, int nb, int* __restrict__ hist, int Hi,
-    int max_pages, int page_size, int num_pages, int stride, int TW, int wgs_per_row) {
+    int max_pages, int page_size, int num_pages, int stride, int TW, int wgs_per_row, int B) {
   __shared__ uint16_t qs[32 * MT * IDX_QROW];
   __shared__ float ws[32 * MT];
   __shared__ int hs[HIST ? IDX_HBINS : 1];  // the workgroup's share of the row's top-k histogram
-  const int b = blockIdx.x / wgs_per_row;
-  const int grp = blockIdx.x - b * wgs_per_row;
+  // the even split: each row's first tail tile in the batch's tail order, its live tiles; the scan's scratch; the
+  // workgroup's row (-1: none) and its first tile
+  __shared__ int bal[2 * IL_BAL_MAXB + IDX_WAVES + 2];
   const int wave = threadIdx.x / WAVE;
   const int lane = threadIdx.x & (WAVE - 1);
   const int j = lane & 31, h = lane >> 5;
   const int tiles_row = (stride + IDX_TILE - 1) / IDX_TILE;
-  const int L = ctx_len ? min(max(ctx_len[b], 0), stride) : stride;
-  const int tw0 = (grp * IDX_WAVES + wave) * TW;  // this wave's first tile
-  const int n_t = max(min(TW, tiles_row - tw0), 0);  // its tiles in the row
-  const int n_live = max(min(n_t, (L + IDX_TILE - 1) / IDX_TILE - tw0), 0);  // those with keys of the context
+  int b, L, tw0, n_t, n_live;
+  if (TW == 0) {  // (launch-uniform) the even split of the live tiles
+    const int t = threadIdx.x, G = gridDim.x, g = blockIdx.x;
+    int* sc = bal + 2 * IL_BAL_MAXB;
+    int* wrow = sc + IDX_WAVES;
+    if (t == 0) wrow[0] = -1;
+    const int Lt = t < B ? min(max(ctx_len[t], 0), stride) : 0;
+    const int Tt = min((Lt + IDX_TILE - 1) / IDX_TILE, tiles_row);  // row t's live tiles
+    int T, Q, wgs;
+    il_block_excl(Tt, sc, &T);
+    const int cw = max((T + 4 * (G - B) - 1) / (4 * (G - B)), 1);  // tiles a wave (at most 64: the launch's G)
+    const int mt = (Tt + 4 * cw - 1) / (4 * cw);                   // row t's workgroups
+    __syncthreads();  // sc read by every thread
+    const int Mt = il_block_excl(mt, sc, &wgs);
+    if (t < B && g >= Mt && g < Mt + mt) {
+      wrow[0] = t;
+      wrow[1] = (g - Mt) * 4 * cw;  // the workgroup's first tile of the row
+    }
+    const int Pt = t < B ? tiles_row - Tt : 0;  // row t's tiles past its length
+    __syncthreads();  // sc read by every thread
+    const int Ut = il_block_excl(Pt, sc, &Q);
+    if (t < B) {
+      bal[t] = Ut;
+      bal[IL_BAL_MAXB + t] = Tt;
+    }
+    __syncthreads();
+    // the tiles past the rows' lengths, tail tile u of ceil(Q / G) a workgroup: 8 tiles a pass, 32 lanes a tile
+    const int qg = (Q + G - 1) / G, u0 = g * qg, u1 = min(u0 + qg, Q);
+    for (int u = u0 + t / IDX_TILE; u < u1; u += IDX_THREADS / IDX_TILE) {
+      int lo = 0, hi = B - 1;  // the last row whose tail starts at or before u
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (bal[mid] <= u) lo = mid; else hi = mid - 1;
+      }
+      const int tile = bal[IL_BAL_MAXB + lo] + (u - bal[lo]);
+      const int pos = tile * IDX_TILE + (t & (IDX_TILE - 1));
+      if (pos < stride) scores[(size_t)lo * stride + pos] = NEG_INF;
+      if (BM) {
+        if (sub_log2 == 5) {
+          if ((t & (IDX_TILE - 1)) == 0 && tile < nb) bm[(size_t)lo * nb + tile] = NEG_INF;
+        } else if ((pos & ((1 << sub_log2) - 1)) == 0 && (pos >> sub_log2) < nb) {
+          bm[(size_t)lo * nb + (pos >> sub_log2)] = NEG_INF;
+        }
+      }
+    }
+    b = wrow[0];
+    if (b < 0) return;  // (workgroup-uniform) a workgroup past the rows' shares
+    L = min(max(ctx_len[b], 0), stride);
+    tw0 = wrow[1] + wave * cw;
+    n_live = n_t = max(min(cw, bal[IL_BAL_MAXB + b] - tw0), 0);
+  } else {
+    b = blockIdx.x / wgs_per_row;
+    const int grp = blockIdx.x - b * wgs_per_row;
+    L = ctx_len ? min(max(ctx_len[b], 0), stride) : stride;
+    tw0 = (grp * IDX_WAVES + wave) * TW;                                // this wave's first tile
+    n_t = max(min(TW, tiles_row - tw0), 0);                             // its tiles in the row
+    n_live = max(min(n_t, (L + IDX_TILE - 1) / IDX_TILE - tw0), 0);  // those with keys of the context
+  }
   float* srow = scores + (size_t)b * stride;
 
   constexpr int QPT = 32 * MT * (IDX_D / 8) / IDX_THREADS;
@@ -361,15 +441,23 @@ static hipError_t launch_indexer_long_v(const uint16_t* q, const float* w, const
                                         int nb, int* hist, int B, int Hi, int max_pages, int page_size, int num_pages,
                                         int stride, int num_cu, hipStream_t s) {
   const int tiles_row = (stride + IDX_TILE - 1) / IDX_TILE;
-  // tiles per wave: about two workgroups per CU over the batch at its longest rows, 4 to 64 tiles each (four per CU,
-  // or three tiles in flight instead of two, measured slower at configs 3 and 4)
+  if (ctx_len && B <= IL_BAL_MAXB) {
+    // the even split: two workgroups per CU (four per CU, or three tiles in flight instead of two, measured slower at
+    // configs 3 and 4), more when the batch's tiles need them at 64 a wave
+    const long need = B + ((long)B * tiles_row + IDX_WAVES * IL_TW_MAX - 1) / (IDX_WAVES * IL_TW_MAX);
+    const long G = need > 2L * num_cu ? need : 2L * num_cu;
+    return launch("indexer_decode_long_kernel", indexer_decode_long_kernel<MT, BM, HIST>, dim3((unsigned)G),
+                  dim3(IDX_THREADS), s, q, w, k, ks, table, ctx_len, scores, bm, sub_log2, nb, hist, Hi, max_pages,
+                  page_size, num_pages, stride, 0, 0, B);
+  }
+  // tiles per wave: about two workgroups per CU over the batch at its longest rows, 4 to 64 tiles each
   const long waves_target = 2L * num_cu * IDX_WAVES;
   int TW = (int)(((long)B * tiles_row + waves_target - 1) / waves_target);
   TW = TW < 4 ? 4 : (TW > IL_TW_MAX ? IL_TW_MAX : TW);
   const int wgs_row = (tiles_row + IDX_WAVES * TW - 1) / (IDX_WAVES * TW);
   return launch("indexer_decode_long_kernel", indexer_decode_long_kernel<MT, BM, HIST>, dim3(B * wgs_row),
                 dim3(IDX_THREADS), s, q, w, k, ks, table, ctx_len, scores, bm, sub_log2, nb, hist, Hi, max_pages,
-                page_size, num_pages, stride, TW, wgs_row);
+                page_size, num_pages, stride, TW, wgs_row, B);
 }
 
 template <int MT>
