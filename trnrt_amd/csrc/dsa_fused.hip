@@ -1457,10 +1457,11 @@ __device__ __forceinline__ bf16x8 fu_value_operand(const uint8_t* kt, int ks, in
 }
 
 // Stage 4: the split's attention over the n_slots slots of the list at FuAtt<HPW, DQK, XT>::L_P (at most CAP), with
-// the queries staged before.
+// the queries staged before at qoff. gather = false: the rows, their scales and biases are still in LDS from the
+// previous call over the same slots (queries past the row tile only), and the slot list is not read.
 template <int HPW, int DQK = FU_DQK, bool XT = false>
 __device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int b, int j, int n_slots,
-                                          float live_bias) {
+                                          float live_bias, bool gather = true, int qoff = FuAtt<HPW, DQK, XT>::L_QST) {
   using AT = FuAtt<HPW, DQK, XT>;
   constexpr int HB = AT::HB, TG = AT::TG, PROW = AT::PROW, KROW = AT::KROW, KPIECES = AT::KPIECES;
   constexpr int PIECES = AT::PIECES, STEPS = AT::STEPS, AQROW = AT::AQROW;
@@ -1470,7 +1471,7 @@ __device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int 
   float* sred = reinterpret_cast<float*>(lds + AT::L_SRED);
   uint16_t* pl = reinterpret_cast<uint16_t*>(lds + AT::L_P);
   uint8_t* kt = lds + L_KT;
-  const uint16_t* qs = reinterpret_cast<const uint16_t*>(lds + AT::L_QST);
+  const uint16_t* qs = reinterpret_cast<const uint16_t*>(lds + qoff);
   const int tid = threadIdx.x, wave = tid / WAVE, lane = tid & (WAVE - 1);
   const int l16 = lane & 15, q4 = lane >> 4;
   const int hb = wave % HB, tg = wave / HB;  // the scores: this wave's 16-head block and 32-token group
@@ -1508,7 +1509,7 @@ __device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int 
   // every row straight into LDS, coalesced: load k fills 1 KiB of the tile, lane l 16-byte unit u = 64 k + l (row
   // u / 37, piece u % 37; the padding piece re-reads the last data piece); the loads of the padded rows' units spread
   // over the 8 waves
-  {
+  if (gather) {
     // unit u = 64 k + lane's row u / 37 and piece u % 37, advanced with k (by 8: u by 512 = 13 x 37 + 31); the
     // lane's slots for its loads k = wave + 8 i in one round of LDS reads, then the loads (a slot read per load
     // would put an LDS round trip before each)
@@ -1543,11 +1544,13 @@ __device__ __forceinline__ void fu_attend(const FusedArgs& a, uint8_t* lds, int 
       if (pc >= KPIECES) pc -= KPIECES;
     }
   }
-  const float ksv = tid < padded ? (a.kvs ? a.kvs[slot] : 1.0f) : 0.0f;  // kvs null: the unscaled cache
-  __builtin_amdgcn_s_waitcnt(0);
-  if (tid < padded) {
-    ksc_l[tid] = ksv;
-    bias_l[tid] = tid < n_slots ? live_bias : -INFINITY;
+  if (gather) {
+    const float ksv = tid < padded ? (a.kvs ? a.kvs[slot] : 1.0f) : 0.0f;  // kvs null: the unscaled cache
+    __builtin_amdgcn_s_waitcnt(0);
+    if (tid < padded) {
+      ksc_l[tid] = ksv;
+      bias_l[tid] = tid < n_slots ? live_bias : -INFINITY;
+    }
   }
   __syncthreads();  // every row in LDS
 
@@ -1988,24 +1991,32 @@ __device__ __forceinline__ int la_slot(const FusedArgs& a, const int* pos_l, int
   return (unsigned)sl < (unsigned)a.num_slots ? sl : 0;
 }
 
+// The unit's queries into LDS at qs, [HPW][AQROW] bf16.
+template <int HPW>
+__device__ __forceinline__ void la_put_queries(uint16_t* qs, const u32x4 (&qv)[FuAtt<HPW>::QPT]) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < FuAtt<HPW>::QPT; ++i) {
+    const int pc = tid + FU_THREADS * i;
+    if (pc < HPW * FU_DQK / 8)
+      *reinterpret_cast<u32x4*>(qs + (pc / (FU_DQK / 8)) * FuAtt<HPW>::AQROW + 8 * (pc % (FU_DQK / 8))) = qv[i];
+  }
+}
+
+// A second unit's queries, staged while the first unit attends: past the 32-head attention's LDS.
+constexpr int L_LA_Q2 = FuAtt<32>::L_QST + 2 * 32 * FU_AQROW;
+static_assert(L_LA_Q2 + 2 * 32 * FU_AQROW <= FU_LDS && FuAtt<32>::L_QST >= FuAtt<32>::L_END,
+              "the second unit's queries clear of the first's attention");
+
 template <int HPW>
 __device__ __forceinline__ int la_stage(const FusedArgs& a, uint8_t* lds, int sl, int s, int cnt_row,
                                         const u32x4 (&qv)[FuAtt<HPW>::QPT], float* live_bias) {
   using AT = FuAtt<HPW>;
-  constexpr int QPT = AT::QPT;
   int* slot_l = reinterpret_cast<int*>(lds + AT::L_P);
   const int tid = threadIdx.x;
   const bool active = s < a.S;
   const int o0 = active ? s * a.sps : 0, o1 = active ? min(o0 + a.sps, a.keep) : 0;
-  if (active) {
-    uint16_t* qs = reinterpret_cast<uint16_t*>(lds + AT::L_QST);
-#pragma unroll
-    for (int i = 0; i < QPT; ++i) {
-      const int pc = tid + FU_THREADS * i;
-      if (pc < HPW * FU_DQK / 8)
-        *reinterpret_cast<u32x4*>(qs + (pc / (FU_DQK / 8)) * AT::AQROW + 8 * (pc % (FU_DQK / 8))) = qv[i];
-    }
-  }
+  if (active) la_put_queries<HPW>(reinterpret_cast<uint16_t*>(lds + AT::L_QST), qv);
   if (tid < AT::CAP) slot_l[tid] = sl;  // padding rows read slot 0 (the slot list lies before the positions)
   int n_slots = max(min(o1, cnt_row) - o0, 0);
   *live_bias = 0.0f;
@@ -2375,11 +2386,13 @@ __global__ __launch_bounds__(FU_THREADS, 1) void decode_long_attend_kernel(Fused
     const bool active = s < a.S;
     const int o0 = active ? s * a.sps : 0, o1 = active ? min(o0 + a.sps, a.keep) : 0;
     if (r) __syncthreads();  // the previous rows' attention is done with the LDS
-    // stage 2: the lists' counts, then T and the ties to take (the split's queries loading meanwhile)
-    u32x4 qv[AT::QPT];
-    la_queries<HPW>(a, b, u0, qv);
+    // stage 2: the lists' counts, then T and the ties to take (the split's queries loading meanwhile, issued after
+    // the counts: the loads complete in order, so the counts' wait does not include the queries')
     const uint32_t* lst_b = la.lst + (size_t)b * FU_NW * lrow_words;
     const uint4 hdr = *reinterpret_cast<const uint4*>(lst_b + (size_t)j * lrow_words);  // this workgroup's own words
+    const int lc = tid < FU_NW ? (int)lst_b[(size_t)tid * lrow_words] : 0;
+    u32x4 qv[AT::QPT];
+    la_queries<HPW>(a, b, u0, qv);
     const int c0 = (int)hdr.y, above0 = (int)hdr.z, nvis = (int)hdr.w;
     for (int i = tid; i < 4096; i += FU_THREADS) bins1[i] = 0;
     if (tid < 256) bins2[tid] = 0;
@@ -2387,7 +2400,7 @@ __global__ __launch_bounds__(FU_THREADS, 1) void decode_long_attend_kernel(Fused
     if (tid < FU_NW) lgt[tid] = leq[tid] = 0;
     if (tid < AT::SPLIT) pos_l[tid] = 0;  // outputs past the count are 0
     if (tid == 0) scr[24] = scr[40] = -1;
-    if (tid < FU_NW) lcnt[tid] = min((int)lst_b[(size_t)tid * lrow_words], la.bw);
+    if (tid < FU_NW) lcnt[tid] = min(lc, la.bw);
     __syncthreads();
     const int cnt_row = min(nvis, a.keep);
     const int lmax = (int)wave_max_u32(lane < FU_NW ? (uint32_t)lcnt[lane] : 0u);
@@ -2400,14 +2413,24 @@ __global__ __launch_bounds__(FU_THREADS, 1) void decode_long_attend_kernel(Fused
     __syncthreads();  // the split's positions
     if (hg == 0 && tid < o1 - o0) a.idx[(size_t)b * a.keep + o0 + tid] = pos_l[tid];
     const int sl = la_slot<HPW>(a, pos_l, b, s, cnt_row);
-    for (int e = 0; e < (paired ? 2 : 1); ++e) {
-      if (e) {
-        __syncthreads();  // the first unit's attention is done with the LDS
+    // 32 heads: the second unit attends the rows the first gathered (its queries lie past the row tile), and its
+    // queries load while the first unit's stage
+    constexpr bool REUSE = HPW == 32;
+    u32x4 qv1[AT::QPT];
+    if (REUSE && paired) la_queries<HPW>(a, b, u0 + 1, qv1);
+    float live_bias;
+    const int n_slots = la_stage<HPW>(a, lds, sl, s, cnt_row, qv, &live_bias);
+    if (REUSE && paired) la_put_queries<HPW>(reinterpret_cast<uint16_t*>(lds + L_LA_Q2), qv1);  // (read after a barrier)
+    fu_attend<HPW>(a, lds, b, u0, n_slots, live_bias);
+    if (paired) {
+      __syncthreads();  // the first unit's attention is done with the LDS
+      if (REUSE) {
+        fu_attend<HPW>(a, lds, b, u0 + 1, n_slots, live_bias, false, L_LA_Q2);
+      } else {
         la_queries<HPW>(a, b, u0 + 1, qv);
+        const int n1 = la_stage<HPW>(a, lds, sl, s, cnt_row, qv, &live_bias);
+        fu_attend<HPW>(a, lds, b, u0 + 1, n1, live_bias);
       }
-      float live_bias;
-      const int n_slots = la_stage<HPW>(a, lds, sl, s, cnt_row, qv, &live_bias);
-      fu_attend<HPW>(a, lds, b, u0 + e, n_slots, live_bias);
     }
     r += paired ? 2 : 1;
   }
