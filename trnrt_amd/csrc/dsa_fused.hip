@@ -357,6 +357,20 @@ __device__ __forceinline__ int fu_wave_find(const int* fine, const int* coarse, 
   return tot;
 }
 
+// The 64 coarse sums of 4096 fine bins (coarse c: bins 64 c .. 64 c + 63), by the whole workgroup: thread t sums bins
+// 8 t .. 8 t + 7, then its 8 lanes' sums add up by DPP (quad swaps and the half-row mirror). The fine bins are complete
+// (a barrier before); a barrier after, before the coarse bins are read.
+__device__ __forceinline__ void fu_coarse_sums(const int* fine, int* coarse) {
+  const int t = threadIdx.x;
+  const int4 a = reinterpret_cast<const int4*>(fine)[2 * t], b = reinterpret_cast<const int4*>(fine)[2 * t + 1];
+  int v = a.x + a.y + a.z + a.w + b.x + b.y + b.z + b.w;
+  v += dpp<0xb1>(v);
+  v += dpp<0x4e>(v);
+  v += dpp<0x141>(v);
+  if ((t & 7) == 0) coarse[t >> 3] = v;
+}
+static_assert(FU_THREADS * 8 == 4096, "a thread's 8 fine bins");
+
 // The same over 256 bins (lane l: bins 4 l .. 4 l + 3).
 __device__ __forceinline__ int fu_wave_find256(const int* bins, int need, int* bin, int* above) {
   const int lane = threadIdx.x & (WAVE - 1);
@@ -701,10 +715,7 @@ __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int
         if (!lists && mine && pos < a.stride) srow[pos] = v;
         scs[e] = v;
         if (POOL && mine) plst[e] = order_key(v) & (0u - (uint32_t)(v > VISIBLE));
-        if (v > VISIBLE) {
-          atomicAdd(&hs[order_key(v) >> 20], 1);
-          if (!POOL && lists) atomicAdd(&hsc[order_key(v) >> 26], 1);  // the key list's bin search
-        }
+        if (v > VISIBLE) atomicAdd(&hs[order_key(v) >> 20], 1);
       }
     }
   } else {
@@ -753,6 +764,16 @@ __device__ __forceinline__ void fu_indexer(const FusedArgs& a, uint8_t* lds, int
   if (POOL) {
     lbin = 0;  // every key of the block (at most 256), whatever their bins; counted by the prefix below
   } else if (lists) {
+    // the key list's bin search over the histogram and its coarse sums (summed here: a row's keys fall in few
+    // coarse bins, and adding each key to its coarse bin queued the tiles' atomics on a few words)
+    {
+      int v = hv[0] + hv[1] + hv[2] + hv[3] + hv[4] + hv[5] + hv[6] + hv[7];
+      v += dpp<0xb1>(v);
+      v += dpp<0x4e>(v);
+      v += dpp<0x141>(v);
+      if ((tid & 7) == 0) hsc[tid >> 3] = v;
+    }
+    __syncthreads();
     int lb, labove;
     const int nv = fu_wave_find(hs, hsc, FU_LM, &lb, &labove);
     lbin = 0;
@@ -1241,10 +1262,9 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
   };
   // a histogram level's counts go to its 4096 bins and their 64 coarse bins (the wave-level bin searches below read
   // both after one barrier)
-  auto add0 = [&](uint32_t bin, int n) __attribute__((always_inline)) {
-    atomicAdd(&bins0[bin], n);
-    atomicAdd(&co0[bin >> 6], n);
-  };
+  // (the first level's coarse bins are summed from the fine ones after the adds: the lists' header bins are the
+  // highest, so their coarse bins are few, and adding to them directly queued thousands of atomics on a few words)
+  auto add0 = [&](uint32_t bin, int n) __attribute__((always_inline)) { atomicAdd(&bins0[bin], n); };
   int c0, above0, nlist, cnt_row;
   if constexpr (POOL) {
     // the first level from the lists' headers: exact for the bins at or above every list's lowest complete bin lmax
@@ -1255,6 +1275,8 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
       if (bh[k]) add0((bh[k] >> 16) & 4095u, (int)(bh[k] & 0xFFFFu));
     if (q == 15) st.lbin[w] = bh[3] ? (int)(bh[3] >> 16) : 0;
     __syncthreads();
+    fu_coarse_sums(bins0, co0);
+    __syncthreads();
     nlist = fu_wave_find(bins0, co0, a.keep, &c0, &above0);
     const int lmax = (int)wave_max_u32(lane < FU_NW ? (uint32_t)st.lbin[lane] : 0u);
     if (lmax > 0 && (nlist <= a.keep || c0 < lmax)) {  // workgroup-uniform
@@ -1264,6 +1286,8 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
       for (int i = 0; i < LPT; ++i)
         if (key[i] && (int)(key[i] >> 20) < low) add0(key[i] >> 20, 1);
       fresh();
+      __syncthreads();
+      fu_coarse_sums(bins0, co0);
       __syncthreads();
       nlist = fu_wave_find(bins0, co0, a.keep, &c0, &above0);
     }
@@ -1286,6 +1310,8 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
     }
     fresh();
     if (q == 0) st.lbin[w] = (int)hw1;
+    __syncthreads();
+    fu_coarse_sums(bins0, co0);
     __syncthreads();
     nlist = fu_wave_find(bins0, co0, a.keep, &c0, &above0);
     const uint32_t lmax = wave_max_u32(lane < FU_NW ? (uint32_t)st.lbin[lane] : 0u);
