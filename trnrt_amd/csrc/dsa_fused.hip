@@ -1330,11 +1330,10 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
   if (c0 >= 0) {
 #pragma unroll
     for (int i = 0; i < LPT; ++i)
-      if (key[i] && (int)(key[i] >> 20) == c0) {
-        atomicAdd(&bins1[(key[i] >> 8) & 4095u], 1);
-        atomicAdd(&co1[(key[i] >> 14) & 63u], 1);
-      }
+      if (key[i] && (int)(key[i] >> 20) == c0) atomicAdd(&bins1[(key[i] >> 8) & 4095u], 1);
     fresh();
+    __syncthreads();
+    fu_coarse_sums(bins1, co1);  // (as the first level's: a pooled row's bin c0 can hold hundreds of keys)
     __syncthreads();
     int c1, above1;
     int need = a.keep - above0;
