@@ -989,7 +989,7 @@ int dsa_sparse_mla_pooled(const void* q_bf16, const uint8_t* kv_fp8, const float
   const int sp = effective_splits(resolve_splits(splits, B, H, keep_sel), keep_sel);
   const size_t need = dsa::attention_workspace_bytes(B, H, sp);
   if (need && (!workspace || workspace_bytes < need)) return DSA_EWORKSPACE;
-  const dsa::PoolForm pf = {__builtin_ctz((unsigned)kp), keep, npool, positions, 0};
+  const dsa::PoolForm pf = {__builtin_ctz((unsigned)kp), keep, npool, positions, 0, 0, nullptr};
   const bool wide = sp == 1 && dsa::attention_wide_ok(B, H, keep_sel + kp, false, num_cu());
   return status(dsa::launch_sparse_mla(static_cast<const uint16_t*>(q_bf16), kv_fp8, kv_scale, pools, cnt, page_table,
                                        nullptr, nullptr, static_cast<uint16_t*>(out_bf16), out_f32, lse, workspace, B,
@@ -1158,7 +1158,7 @@ static int pooled_layer(const void* q_idx_bf16, const float* w, const void* pool
         static_cast<uint16_t*>(out_bf16), lse, static_cast<char*>(workspace) + t_need, static_cast<int*>(workspace), B,
         H, max_pages, page_size, num_pages, keep, __builtin_ctz((unsigned)kp), scale, s));
   const int sp = effective_splits(resolve_splits(splits, B, H, keep_sel), keep_sel);
-  const dsa::PoolForm pf = {__builtin_ctz((unsigned)kp), keep, npool, positions, 0};
+  const dsa::PoolForm pf = {__builtin_ctz((unsigned)kp), keep, npool, positions, 0, 0, nullptr};
   return status(dsa::launch_sparse_mla(static_cast<const uint16_t*>(q_bf16), kv_fp8, kv_scale, pools, cnt, page_table,
                                        nullptr, nullptr, static_cast<uint16_t*>(out_bf16), nullptr, lse,
                                        static_cast<char*>(workspace) + t_need, B, H, Dqk, keep_sel, max_pages,

@@ -130,7 +130,6 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void sparse_mla_kernel(
   // the workgroup that holds the row's last slot (n_eff >= 1 here, so it has slots of its own) adds the tail as one
   // more chunk: rows 0 .. tail_n - 1 of a zeroed tile, loaded into registers with its first super-chunk's rows
   const int tail_n = (tail_apart > 0 && (n_eff - 1) / slots_per_split == sp) ? tail_apart : 0;
-  const int n_main = k_end > k_begin ? (k_end - k_begin + ATT_SUPER - 1) / ATT_SUPER : 0;
   const size_t nslots_cache = (size_t)num_pages * page_size;
 
   // the queries of the 16 heads (16 or 18 KiB), staged through LDS below

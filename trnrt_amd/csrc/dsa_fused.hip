@@ -98,9 +98,7 @@ struct FuForm {
 };
 constexpr int FU_POOL_MAXLEN = FU_NW * FuForm<true>::LCAP;  // 8,192 pools
 static_assert(FU_HROW % 32 == 0 && FU_CROW % 32 == 0 && FU_LROW % 32 == 0, "a workgroup's rows in lines of its own");
-constexpr int FU_HPW = 16;         // heads per MFMA block of the attention
 constexpr int FU_CH = 64;          // slot granularity of a split
-constexpr int FU_SPLIT = 256;      // slots per split, at most
 constexpr int FU_DQK = 576, FU_DV = 512;
 constexpr int FU_PIECES = FU_DQK / 16;  // 36 16-byte pieces per row
 constexpr int FU_KPIECES = FU_PIECES + 1;  // a staged row: the data and one padding piece (592 bytes), the stride at
@@ -996,7 +994,6 @@ __device__ __forceinline__ int fu_select(const FusedArgs& a, uint8_t* lds, int b
   int* spg = reinterpret_cast<int*>(lds + L_SPG);
   const uint32_t* cb = reinterpret_cast<const uint32_t*>(lds + L_CB);
   uint32_t* sb = reinterpret_cast<uint32_t*>(lds + L_SB);
-  int* pb = reinterpret_cast<int*>(lds + L_PB);
   int* slot_l = reinterpret_cast<int*>(lds + AT::L_P);
   const int tid = threadIdx.x, wave = tid / WAVE, lane = tid & (WAVE - 1);
   const int c0 = st.c0;
@@ -1175,7 +1172,7 @@ __device__ __forceinline__ bool fu_select_lists(const FusedArgs& a, uint8_t* lds
   constexpr int POS_SINK = AT::SPLIT;
   int* pos_l = slot_l + AT::CAP + 8;
   static_assert(4 * (AT::CAP + 8 + AT::SPLIT + 1) <= 2 * HPW * AT::PROW, "slot and position lists inside P's region");
-  const int tid = threadIdx.x, wave = tid / WAVE, lane = tid & (WAVE - 1);
+  const int tid = threadIdx.x, lane = tid & (WAVE - 1);
   const int w = tid >> 4, q = tid & 15;
   const int hg = j % a.HG, s = j / a.HG;
   const bool active = s < a.S;  // workgroup-uniform: a workgroup past the last split only helps with the barriers
@@ -2081,7 +2078,6 @@ __device__ __forceinline__ void la_add1(uint8_t* lds, uint32_t k) {
 
 __device__ __forceinline__ void la_select_regs(const FusedArgs& a, uint8_t* lds, const uint32_t* lst_b,
                                                size_t lrow_words, int c0, int above0, int o0, int o1, int* pos_l) {
-  int* scr = reinterpret_cast<int*>(lds + L_MISC);
   int* bins1 = reinterpret_cast<int*>(lds + L_BINS);
   int* bins2 = reinterpret_cast<int*>(lds + L_BINS2);
   int* lcnt = reinterpret_cast<int*>(lds + L_LA);
@@ -2474,7 +2470,7 @@ struct FusedLayout {
   size_t hl, cand, lst, part, ml, end;
 };
 
-static FusedLayout fused_layout(size_t zero_bytes, int B, int H, int S, int keep) {
+static FusedLayout fused_layout(size_t zero_bytes, int B, int H, int S) {
   FusedLayout l;
   l.hl = zero_bytes;
   l.cand = l.hl + fu_up256((size_t)B * FU_NW * FU_HROW * 4);
@@ -2508,7 +2504,7 @@ bool fused_layer_ok(int num_cu, int Hi, int H, int max_len, int keep, int page_s
 size_t fused_layer_bytes(size_t zero_bytes, int B, int H, int keep) {
   const int hpw = keep >= 1 ? fused_hpw(H, keep) : 0;
   if (!hpw) return 0;
-  return fused_layout(zero_bytes, B, H, fused_splits(H, hpw), keep).end;
+  return fused_layout(zero_bytes, B, H, fused_splits(H, hpw)).end;
 }
 
 // The separate attention launch (decode_attend_kernel): whether it takes the shape, and its workspace (the split
@@ -2518,7 +2514,7 @@ bool attend_xcd_ok(int num_cu, int H, int keep) { return num_cu == FU_XCDS * FU_
 size_t attend_xcd_bytes(int B, int H, int keep) {
   const int hpw = keep >= 1 ? fused_hpw(H, keep) : 0;
   if (!hpw) return 0;
-  const FusedLayout l = fused_layout(0, B, H, fused_splits(H, hpw), keep);
+  const FusedLayout l = fused_layout(0, B, H, fused_splits(H, hpw));
   return l.end - l.part;
 }
 
@@ -2529,7 +2525,7 @@ static FusedArgs attend_args(const uint16_t* q, const uint8_t* kv, const float* 
                              int num_pages, int keep, float scale, int hpw) {
   FusedArgs a{};
   const int S = fused_splits(H, hpw);
-  const FusedLayout l = fused_layout(0, B, H, S, keep);
+  const FusedLayout l = fused_layout(0, B, H, S);
   char* p = static_cast<char*>(ws) - l.part;
   a.q = q;
   a.kv = kv;
@@ -2685,7 +2681,7 @@ hipError_t launch_decode_fused(const uint16_t* q_idx, const float* w, const uint
   const int hpw = fused_hpw(H, keep);
   if (!hpw) return hipErrorInvalidValue;
   const int S = fused_splits(H, hpw);
-  const FusedLayout l = fused_layout(zero_bytes, B, H, S, keep);
+  const FusedLayout l = fused_layout(zero_bytes, B, H, S);
   char* p = static_cast<char*>(ws);
   a.q_idx = q_idx;
   a.w = w;
