@@ -2396,11 +2396,13 @@ __global__ __launch_bounds__(FU_THREADS, 1) void decode_long_attend_kernel(Fused
     if (tid < FU_HBINS / FU_NW / 4)  // the row's histogram back to zero, 1/32 by each workgroup
       reinterpret_cast<uint4*>(la.hist + (size_t)(a.row0 + x + FU_XCDS * r) * FU_HBINS + (FU_HBINS / FU_NW) * j)[tid] =
           uint4{0u, 0u, 0u, 0u};
-  // stages 2-4 a row at a time, or two rows at once: with an even number of head groups, workgroups 0-15 take row r
-  // and 16-31 row r + 1, each its row's selection once and then the two head groups of one split (units 2 u and
-  // 2 u + 1, u = j mod 16, of the row's 32), where taking the rows in turn costs each workgroup two selections
+  // stages 2-4 a row at a time, or two rows at once: with 32 heads a workgroup and an even number of head groups,
+  // workgroups 0-15 take row r and 16-31 row r + 1, each its row's selection once and then the two head groups of one
+  // split (units 2 u and 2 u + 1, u = j mod 16, of the row's 32; the second attends the rows the first gathered, its
+  // queries staged past the row tile), where taking the rows in turn costs each workgroup two selections
+  static_assert(FuAtt<32>::L_QST >= FuAtt<32>::L_P, "the 32-head queries past the row tile");
   for (int r = 0; r < nr;) {
-    const bool paired = a.HG % 2 == 0 && r + 1 < nr;  // (launch-uniform)
+    const bool paired = HPW == 32 && a.HG % 2 == 0 && r + 1 < nr;  // (launch-uniform)
     const int b = a.row0 + x + FU_XCDS * (paired ? r + j / (FU_NW / 2) : r);
     const int u0 = paired ? 2 * (j % (FU_NW / 2)) : j;  // the first unit (split u0 / HG, head group u0 mod HG)
     const int hg = u0 % a.HG, s = u0 / a.HG;
@@ -2434,24 +2436,16 @@ __global__ __launch_bounds__(FU_THREADS, 1) void decode_long_attend_kernel(Fused
     __syncthreads();  // the split's positions
     if (hg == 0 && tid < o1 - o0) a.idx[(size_t)b * a.keep + o0 + tid] = pos_l[tid];
     const int sl = la_slot<HPW>(a, pos_l, b, s, cnt_row);
-    // 32 heads: the second unit attends the rows the first gathered (its queries lie past the row tile), and its
-    // queries load while the first unit's stage
-    constexpr bool REUSE = HPW == 32;
+    // paired: the second unit's queries load while the first unit's stage
     u32x4 qv1[AT::QPT];
-    if (REUSE && paired) la_queries<HPW>(a, b, u0 + 1, qv1);
+    if (paired) la_queries<HPW>(a, b, u0 + 1, qv1);
     float live_bias;
     const int n_slots = la_stage<HPW>(a, lds, sl, s, cnt_row, qv, &live_bias);
-    if (REUSE && paired) la_put_queries<HPW>(reinterpret_cast<uint16_t*>(lds + L_LA_Q2), qv1);  // (read after a barrier)
+    if (paired) la_put_queries<HPW>(reinterpret_cast<uint16_t*>(lds + L_LA_Q2), qv1);  // (read after a barrier)
     fu_attend<HPW>(a, lds, b, u0, n_slots, live_bias);
     if (paired) {
       __syncthreads();  // the first unit's attention is done with the LDS
-      if (REUSE) {
-        fu_attend<HPW>(a, lds, b, u0 + 1, n_slots, live_bias, false, L_LA_Q2);
-      } else {
-        la_queries<HPW>(a, b, u0 + 1, qv);
-        const int n1 = la_stage<HPW>(a, lds, sl, s, cnt_row, qv, &live_bias);
-        fu_attend<HPW>(a, lds, b, u0 + 1, n1, live_bias);
-      }
+      fu_attend<HPW>(a, lds, b, u0 + 1, n_slots, live_bias, false, L_LA_Q2);
     }
     r += paired ? 2 : 1;
   }
