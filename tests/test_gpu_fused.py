@@ -33,7 +33,8 @@ def _run(g, chain=False):
     return L
 
 
-SYNC_WORDS = 256  # the workspace's first 1 KiB: per XCD 16 barrier and status words; the row histograms follow
+SYNC_WORDS = 256  # the workspace's first 1 KiB: per XCD 32 barrier and status words; the row histograms follow
+XCD_WORDS = 32
 
 
 def _workspace_clean(L):
@@ -41,9 +42,9 @@ def _workspace_clean(L):
     each is zero, the histograms are zero again, and no barrier wait gave up (the status words, read through the C
     ABI's dsa_layer_status as well)."""
     ws = L.workspace.view(torch.int32).cpu()
-    sync = ws[:8 * 16].view(8, 16)
+    sync = ws[:SYNC_WORDS].view(8, XCD_WORDS)
     assert torch.all(sync[:, 0] % 256 == 0) and torch.all(sync[:, 1] == 0), f"barrier words: {sync[:, :3].tolist()}"
-    assert torch.all(ws[8 * 16:SYNC_WORDS] == 0), "words past the 8 XCDs' barrier words"
+    assert torch.all(sync[:, 4:] == 0), "words past each XCD's barrier and status words"
     assert torch.all(ws[SYNC_WORDS:SYNC_WORDS + L.B * 4096] == 0), "row histograms left non-zero"
     assert torch.all(sync[:, 2] == 0), "a barrier wait gave up"
     assert L.status()["gave_up"] == 0
@@ -54,7 +55,7 @@ def _two_exchange_per_xcd(L) -> list:
     counts them in the XCD's status words (row b of a launch runs on XCD b % 8); the others took the one-exchange
     selection from the key lists."""
     ws = L.workspace.view(torch.int32).cpu()
-    per = ws[:8 * 16].view(8, 16)[:, 3].tolist()
+    per = ws[:SYNC_WORDS].view(8, XCD_WORDS)[:, 3].tolist()
     assert L.status()["two_exchange"] == sum(per)
     return per
 

@@ -13,7 +13,7 @@ import pytest
 import torch
 
 from tests._helpers import say
-from tests.test_gpu_fused import SYNC_WORDS, _check_full
+from tests.test_gpu_fused import SYNC_WORDS, XCD_WORDS, _check_full
 from trnrt_amd import _lib
 from trnrt_amd import workloads as W
 from trnrt_amd.kernels.dsa_layer import DecodeLayer
@@ -66,7 +66,7 @@ def test_workspace_reused_from_one_launch_to_separate_kernels():
     assert int(Lb.cnt[4]) == 2044
     _check_full(b, Lb)
     ws = Lb.workspace.view(torch.int32).cpu()
-    sync = ws[:8 * 16].view(8, 16)
+    sync = ws[:SYNC_WORDS].view(8, XCD_WORDS)
     assert torch.all(sync[:, 0] % 256 == 0) and torch.all(sync[:, 1] == 0)
     assert torch.all(ws[SYNC_WORDS:SYNC_WORDS + 8 * 4096] == 0), "row histograms left non-zero"
     assert Lb.status(clear=True) == {"gave_up": 0, "two_exchange": 1}
@@ -119,7 +119,7 @@ def test_gave_up_count_is_reported_and_cleared():
     say("status: a give-up set from the host")
     L.step(g.q_idx, g.w_k, g.k_cache, g.k_scale, g.q, g.kv_cache, g.kv_scale, g.table, g.ctx_len, verify=True)
     out0 = L.out.clone()
-    L.workspace.view(torch.int32)[3 * 16 + 2] = 5
+    L.workspace.view(torch.int32)[3 * XCD_WORDS + 2] = 5
     assert L.status()["gave_up"] == 5
     with pytest.raises(RuntimeError, match="gave up"):
         L.step(g.q_idx, g.w_k, g.k_cache, g.k_scale, g.q, g.kv_cache, g.kv_scale, g.table, g.ctx_len, verify=True)
