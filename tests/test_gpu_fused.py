@@ -33,8 +33,21 @@ def _run(g, chain=False):
     return L
 
 
-SYNC_WORDS = 256  # the workspace's first 1 KiB: per XCD 32 barrier and status words; the row histograms follow
-XCD_WORDS = 32
+# The workspace's first 4 KiB: per XCD four 128-byte lines, word 0 of each a copy of the barrier counter, the first
+# line's words 2 and 3 the status words; the row histograms follow.
+SYNC_LINES, LINE_WORDS = 4, 32
+XCD_WORDS = SYNC_LINES * LINE_WORDS
+SYNC_WORDS = 8 * XCD_WORDS
+
+
+def sync_block(ws: torch.Tensor):
+    """The barrier block of an int32 workspace: (the counter copies [8, 4], the first lines [8, 32]); asserts that
+    every other word of it is zero and that every XCD's copies agree."""
+    s = ws[:SYNC_WORDS].view(8, SYNC_LINES, LINE_WORDS)
+    ctr = s[:, :, 0]
+    assert torch.all(ctr == ctr[:, :1]), f"counter copies differ: {ctr.tolist()}"
+    assert torch.all(s[:, 0, 4:] == 0) and torch.all(s[:, 1:, 1:] == 0), "words past the barrier and status words"
+    return ctr, s[:, 0]
 
 
 def _workspace_clean(L):
@@ -42,9 +55,8 @@ def _workspace_clean(L):
     each is zero, the histograms are zero again, and no barrier wait gave up (the status words, read through the C
     ABI's dsa_layer_status as well)."""
     ws = L.workspace.view(torch.int32).cpu()
-    sync = ws[:SYNC_WORDS].view(8, XCD_WORDS)
-    assert torch.all(sync[:, 0] % 256 == 0) and torch.all(sync[:, 1] == 0), f"barrier words: {sync[:, :3].tolist()}"
-    assert torch.all(sync[:, 4:] == 0), "words past each XCD's barrier and status words"
+    ctr, sync = sync_block(ws)
+    assert torch.all(ctr % 256 == 0) and torch.all(sync[:, 1] == 0), f"barrier words: {sync[:, :3].tolist()}"
     assert torch.all(ws[SYNC_WORDS:SYNC_WORDS + L.B * 4096] == 0), "row histograms left non-zero"
     assert torch.all(sync[:, 2] == 0), "a barrier wait gave up"
     assert L.status()["gave_up"] == 0
@@ -55,7 +67,7 @@ def _two_exchange_per_xcd(L) -> list:
     counts them in the XCD's status words (row b of a launch runs on XCD b % 8); the others took the one-exchange
     selection from the key lists."""
     ws = L.workspace.view(torch.int32).cpu()
-    per = ws[:SYNC_WORDS].view(8, XCD_WORDS)[:, 3].tolist()
+    per = sync_block(ws)[1][:, 3].tolist()
     assert L.status()["two_exchange"] == sum(per)
     return per
 

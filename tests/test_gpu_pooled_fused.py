@@ -16,6 +16,7 @@ import torch
 
 from oracle import dsa_oracle as O
 from tests._helpers import assert_attention_close, launched_kernels, row_rel_err, say
+from tests.test_gpu_fused import sync_block
 from trnrt_amd import workloads as W
 from trnrt_amd.kernels.dsa_layer import PooledDecodeLayer
 
@@ -148,8 +149,8 @@ def test_pooled_fused_repeated_steps():
     assert torch.equal(layer.pools, fresh.pools) and torch.equal(layer.cnt, fresh.cnt)
     assert torch.equal(layer.out, fresh.out) and torch.equal(layer.lse, fresh.lse)
     ws = layer.workspace.view(torch.int32).cpu()
-    sync = ws[:256].view(8, 32)  # per XCD 32 barrier and status words
-    assert torch.all(sync[:, 0] % 256 == 0) and torch.all(sync[:, 1] == 0), "barrier words not at a launch boundary"
+    ctr, sync = sync_block(ws)
+    assert torch.all(ctr % 256 == 0) and torch.all(sync[:, 1] == 0), "barrier words not at a launch boundary"
     assert layer.status()["gave_up"] == 0
 
 

@@ -13,7 +13,7 @@ import pytest
 import torch
 
 from tests._helpers import say
-from tests.test_gpu_fused import SYNC_WORDS, XCD_WORDS, _check_full
+from tests.test_gpu_fused import SYNC_WORDS, XCD_WORDS, _check_full, sync_block
 from trnrt_amd import _lib
 from trnrt_amd import workloads as W
 from trnrt_amd.kernels.dsa_layer import DecodeLayer
@@ -66,8 +66,8 @@ def test_workspace_reused_from_one_launch_to_separate_kernels():
     assert int(Lb.cnt[4]) == 2044
     _check_full(b, Lb)
     ws = Lb.workspace.view(torch.int32).cpu()
-    sync = ws[:SYNC_WORDS].view(8, XCD_WORDS)
-    assert torch.all(sync[:, 0] % 256 == 0) and torch.all(sync[:, 1] == 0)
+    ctr, sync = sync_block(ws)
+    assert torch.all(ctr % 256 == 0) and torch.all(sync[:, 1] == 0)
     assert torch.all(ws[SYNC_WORDS:SYNC_WORDS + 8 * 4096] == 0), "row histograms left non-zero"
     assert Lb.status(clear=True) == {"gave_up": 0, "two_exchange": 1}
     assert Lb.status() == {"gave_up": 0, "two_exchange": 0}

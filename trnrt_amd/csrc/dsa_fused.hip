@@ -235,7 +235,8 @@ struct FusedArgs {
 constexpr int FU_AUX_PLAIN = 0;  // the cache-policy operand of the loads of a peer's published data: none
 
 // XCD-local barrier of the 32 workgroups of an XCD: every thread's stores complete (drained memory counter), then the
-// workgroup's arrival (one atomic add) and a bounded poll (atomic adds of 0). The XCD's counter only grows: every launch adds exactly
+// workgroup's arrival (one atomic add to each of the counter's WS_SYNC_LINES copies, a line each) and a bounded poll
+// (atomic adds of 0) of copy j mod WS_SYNC_LINES. Each copy of the XCD's counter only grows: every launch adds exactly
 // FU_SPAN = 8 x 32 to it (each workgroup one arrival per barrier, and the rest of its 8 at its exit, with no wait), so
 // at a launch's start it holds a multiple of FU_SPAN plus the arrivals at this launch's first barrier (fewer than 32:
 // that barrier needs every workgroup's); the base read then, rounded down to FU_SPAN, places the n-th barrier at
@@ -246,23 +247,25 @@ constexpr int FU_AUX_PLAIN = 0;  // the cache-policy operand of the loads of a p
 constexpr unsigned FU_SPAN = 8 * FU_NW;
 struct FuSync {
   int* w;         // the XCD's words: the counter, then the status words
+  unsigned* rep;  // the copy of the counter this workgroup polls
   unsigned base;  // the counter's value at this launch's start (thread 0's)
 };
 
-__device__ __forceinline__ FuSync fu_sync_begin(int* w) {
-  FuSync sy{w, 0u};
+__device__ __forceinline__ FuSync fu_sync_begin(int* w, int j) {
+  FuSync sy{w, reinterpret_cast<unsigned*>(w + WS_SYNC_LINE_WORDS * (j % WS_SYNC_LINES)), 0u};
   if (threadIdx.x == 0)
-    sy.base = __hip_atomic_load(reinterpret_cast<unsigned*>(w), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) &
-              ~(FU_SPAN - 1u);
+    sy.base = __hip_atomic_load(sy.rep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & ~(FU_SPAN - 1u);
   return sy;
 }
 
 __device__ __forceinline__ void fu_barrier(const FuSync& sy, int n) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  if (threadIdx.x < WS_SYNC_LINES)  // the arrival, on every copy of the counter
+    __hip_atomic_fetch_add(reinterpret_cast<unsigned*>(sy.w + WS_SYNC_LINE_WORDS * threadIdx.x), 1u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
   if (threadIdx.x == 0) {
-    unsigned* ctr = reinterpret_cast<unsigned*>(sy.w);
-    __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    unsigned* ctr = sy.rep;
     const unsigned target = sy.base + (unsigned)n * FU_NW;
     unsigned polls = 0;
     // (each poll an atomic add of 0 with return, read where the arrivals are added: 0.57 us a launch faster than
@@ -282,9 +285,9 @@ __device__ __forceinline__ void fu_barrier(const FuSync& sy, int n) {
 
 // The workgroup's exit after nbar barriers: its remaining arrivals of the launch's FU_SPAN (one add, not waited for).
 __device__ __forceinline__ void fu_exit(const FuSync& sy, int nbar) {
-  if (threadIdx.x == 0)
-    __hip_atomic_fetch_add(reinterpret_cast<unsigned*>(sy.w), FU_SPAN / FU_NW - (unsigned)nbar, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x < WS_SYNC_LINES)
+    __hip_atomic_fetch_add(reinterpret_cast<unsigned*>(sy.w + WS_SYNC_LINE_WORDS * threadIdx.x),
+                           FU_SPAN / FU_NW - (unsigned)nbar, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Block-wide over 512 threads, thread t holding the counts of bins PER t .. PER t + PER - 1 (higher bins = larger
@@ -1774,7 +1777,7 @@ template <int MT, int HPW>
 __global__ __launch_bounds__(FU_THREADS, 1) void decode_fused_kernel(FusedArgs a) {
   __shared__ __align__(16) uint8_t lds[FU_LDS];
   const int x = blockIdx.x % FU_XCDS, j = blockIdx.x / FU_XCDS;
-  const FuSync sync = fu_sync_begin(a.sync + x * WS_SYNC_WORDS);
+  const FuSync sync = fu_sync_begin(a.sync + x * WS_SYNC_WORDS, j);
   // one row per XCD and launch (rows row0 + x; a batch of more than 8 rows takes several launches, which keeps
   // each workgroup's per-lane address arithmetic out of a loop over rows, where it would be held in registers)
   const int b = a.row0 + x;
@@ -1816,7 +1819,7 @@ template <int HPW, bool WRITE>
 __global__ __launch_bounds__(FU_THREADS, 1) void decode_pooled_fused_kernel(FusedArgs a) {
   __shared__ __align__(16) uint8_t lds[FU_LDS];
   const int x = blockIdx.x % FU_XCDS, j = blockIdx.x / FU_XCDS;
-  const FuSync sync = fu_sync_begin(a.sync + x * WS_SYNC_WORDS);
+  const FuSync sync = fu_sync_begin(a.sync + x * WS_SYNC_WORDS, j);
   const int b = a.row0 + x;
   if (b >= a.B) return;  // an XCD without a row
   const int L = min(max(a.ctx_len[b], 0), min(a.stride, FU_POOL_MAXLEN));
@@ -1921,7 +1924,7 @@ template <int HPW, int DQK = FU_DQK, bool XT = false>
 __global__ __launch_bounds__(FU_THREADS, 1) void decode_attend_kernel(FusedArgs a, const int* rows, int rpl) {
   __shared__ __align__(16) uint8_t lds[FU_LDS];
   const int x = blockIdx.x % FU_XCDS, j = blockIdx.x / FU_XCDS;
-  const FuSync sync = fu_sync_begin(a.sync + x * WS_SYNC_WORDS);
+  const FuSync sync = fu_sync_begin(a.sync + x * WS_SYNC_WORDS, j);
   if (a.row0 + x >= a.B) return;  // an XCD without a row
   const int nr = min(rpl, (a.B - a.row0 - x + FU_XCDS - 1) / FU_XCDS);  // this XCD's rows
   for (int r = 0; r < nr; ++r) {
@@ -2255,7 +2258,7 @@ __global__ __launch_bounds__(FU_THREADS, 1) void decode_long_attend_kernel(Fused
   __shared__ __align__(16) uint8_t lds[FU_LDS];
   using AT = FuAtt<HPW>;
   const int x = blockIdx.x % FU_XCDS, j = blockIdx.x / FU_XCDS;
-  const FuSync sync = fu_sync_begin(a.sync + x * WS_SYNC_WORDS);
+  const FuSync sync = fu_sync_begin(a.sync + x * WS_SYNC_WORDS, j);
   if (a.row0 + x >= a.B) return;  // an XCD without a row
   const int nr = min(la.rpl, (a.B - a.row0 - x + FU_XCDS - 1) / FU_XCDS);  // this XCD's rows
   const int tid = threadIdx.x, lane = tid & (WAVE - 1);
