@@ -7,7 +7,7 @@
  * DSA_OK (0) or a negative DSA_E* code; dsa_strerror() names it. No entry point allocates device memory: scratch
  * space is a caller-owned workspace sized by dsa_workspace_bytes(). A workspace must be zero-filled before its
  * first use (dsa_workspace_clear, or any zero fill) and written by nothing but these calls afterwards. A decode or
- * top-k workspace starts with 4 KiB of barrier and status words at the same offset for every batch size (a barrier
+ * top-k workspace starts with 8 KiB of barrier and status words at the same offset for every batch size (a barrier
  * counter only grows, by 256 per launch that uses it, so it always holds a multiple of 256 between calls, zero
  * included; the status words count across calls, see dsa_layer_status), then the top-k histograms [B, 4096] int32:
  * with the barrier words, the zero region of a call of B rows, which the call leaves as it found it (histograms zero,

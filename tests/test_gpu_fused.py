@@ -33,15 +33,15 @@ def _run(g, chain=False):
     return L
 
 
-# The workspace's first 4 KiB: per XCD four 128-byte lines, word 0 of each a copy of the barrier counter, the first
+# The workspace's first 8 KiB: per XCD eight 128-byte lines, word 0 of each a copy of the barrier counter, the first
 # line's words 2 and 3 the status words; the row histograms follow.
-SYNC_LINES, LINE_WORDS = 4, 32
+SYNC_LINES, LINE_WORDS = 8, 32
 XCD_WORDS = SYNC_LINES * LINE_WORDS
 SYNC_WORDS = 8 * XCD_WORDS
 
 
 def sync_block(ws: torch.Tensor):
-    """The barrier block of an int32 workspace: (the counter copies [8, 4], the first lines [8, 32]); asserts that
+    """The barrier block of an int32 workspace: (the counter copies [8, 8], the first lines [8, 32]); asserts that
     every other word of it is zero and that every XCD's copies agree."""
     s = ws[:SYNC_WORDS].view(8, SYNC_LINES, LINE_WORDS)
     ctr = s[:, :, 0]

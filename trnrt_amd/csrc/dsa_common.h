@@ -79,16 +79,16 @@ struct PoolKeyWrite {
   int rows_fp8;
 };
 constexpr int HIST_REPLICAS = 1;
-// The first bytes of every decode workspace, at the same offset whatever the batch size: per XCD (8 x 128 words) four
+// The first bytes of every decode workspace, at the same offset whatever the batch size: per XCD (8 x 256 words) eight
 // 128-byte lines. Word 0 of each line is a copy of the XCD-local barriers' arrival counter (a multiple of 256 between
 // calls: each launch adds 256 to every copy); the first line then holds an unused word (zero) and two status words
 // that persist across calls until dsa_layer_status clears them: the count of barrier waits that gave up, and the
 // count of rows that took the one-launch layer's two-exchange selection. Every other word is zero. The top-k
 // histograms (zero between calls) follow. Each arrival adds to every copy and each workgroup polls one, so a copy's
-// line takes the atomics of 8 of the XCD's 32 workgroups' polls; with two XCDs' counters in one line their polls and
-// arrivals queued on each other (measured: 0.6-0.9 us a launch of the one-launch layers), and four copies a line of
-// their own took 0.2-0.3 us more off.
-constexpr int WS_SYNC_LINES = 4;
+// line takes the polls of 4 of the XCD's 32 workgroups; with two XCDs' counters in one line their polls and
+// arrivals queued on each other (measured: 0.6-0.9 us a launch of the one-launch layers), and four or eight copies a
+// line of their own took 0.2-0.3 us more off.
+constexpr int WS_SYNC_LINES = 8;
 constexpr int WS_SYNC_LINE_WORDS = 32;
 constexpr int WS_SYNC_WORDS = WS_SYNC_LINE_WORDS * WS_SYNC_LINES;  // per XCD
 constexpr int WS_SYNC_BYTES = 8 * 4 * WS_SYNC_WORDS;

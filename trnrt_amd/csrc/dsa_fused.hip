@@ -269,15 +269,23 @@ __device__ __forceinline__ void fu_barrier(const FuSync& sy, int n) {
     const unsigned target = sy.base + (unsigned)n * FU_NW;
     unsigned polls = 0;
     // (each poll an atomic add of 0 with return, read where the arrivals are added: 0.57 us a launch faster than
-    // device-scope loads; a literal 0 would be folded into such a load)
+    // device-scope loads; a literal 0 would be folded into such a load). Two polls are in flight, 512 clocks apart at
+    // first, each reissued as soon as it returns short of the target; the address is passed through a VGPR, so the
+    // compiler keeps each poll one atomic instruction and waits only for the older one (vmcnt(1)).
     unsigned z;
     asm volatile("v_mov_b32 %0, 0" : "=v"(z));
-    while ((int)(__hip_atomic_fetch_add(ctr, z, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - target) < 0) {
+    __attribute__((address_space(1))) unsigned* pc = (__attribute__((address_space(1))) unsigned*)ctr;
+    asm volatile("" : "+v"(pc));
+    unsigned p = __hip_atomic_fetch_add(pc, z, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_sleep(8);
+    unsigned q = __hip_atomic_fetch_add(pc, z, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    while ((int)(p - target) < 0) {
       if (++polls > FU_SPIN) {
         __hip_atomic_fetch_add(sy.w + WS_SYNC_GAVE_UP, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         break;
       }
-      __builtin_amdgcn_s_sleep(1);
+      p = q;
+      q = __hip_atomic_fetch_add(pc, z, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
   __syncthreads();
