@@ -262,7 +262,7 @@ size_t dsa_prefill_select_workspace_bytes(int N, int P, int score_stride, int ke
  * The one launch, and the separate kernels' attention launch, are 256 workgroups of which the 32 on each XCD wait
  * for each other at XCD-local barriers: they need every one of their workgroups resident at once (one per CU, 160
  * KiB of LDS each). So these calls must not overlap one another on a GPU, whatever their workspaces and streams,
- * and no other kernel may hold CUs throughout one of them. A barrier wait is bounded (about a second); one that
+ * and no other kernel may hold CUs throughout one of them. A barrier wait is bounded (under a second); one that
  * gives up is counted in the workspace's status words, which dsa_layer_status reads: the call's outputs are then
  * unreliable, though every kernel ends normally.
  */

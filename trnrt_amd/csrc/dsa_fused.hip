@@ -242,7 +242,7 @@ constexpr int FU_AUX_PLAIN = 0;  // the cache-policy operand of the loads of a p
 // that barrier needs every workgroup's); the base read then, rounded down to FU_SPAN, places the n-th barrier at
 // base + 32 n arrivals (unsigned, so the counter may wrap). Every kernel using these barriers takes at most 8. A wait
 // that gives up (all 32 workgroups must be resident at once: another kernel holding CUs for the whole poll budget,
-// about a second, breaks that) counts itself in the XCD's status word and goes on; every read of a peer's data below
+// a fraction of a second, breaks that) counts itself in the XCD's status word and goes on; every read of a peer's data below
 // stays inside its region whatever that data holds, so such a call ends normally, and dsa_layer_status reports it.
 constexpr unsigned FU_SPAN = 8 * FU_NW;
 struct FuSync {
